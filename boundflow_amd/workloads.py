@@ -1,0 +1,281 @@
+"""Seeded synthetic workloads for the five benchmark configurations.
+
+Everything is generated on the CPU from one ``torch.Generator`` so that the
+HIP path and the CPU baseline see bit-identical inputs.  Networks are built
+directly as ``BFTaskModule`` programs with the op vocabulary the reference's
+planner emits (``linear``/``conv2d``/``relu``/``flatten``), one task, one
+buffer per value.
+
+Configurations (shapes, distributions and optimiser settings):
+
+* C1  IBP+CROWN, MLP 784-256-256-10, B=64, box eps=2/255 clamped to [0,1]
+* C2  CROWN with all intermediate bounds by CROWN, MLP 784-500x6-10, B=256, Linf 0.015
+* C3  CROWN, CNN 3x32x32 conv(16,4,s2,p1)-conv(32,4,s2,p1)-fc100-fc10, B=128, Linf 2/255
+* C4  alpha-CROWN on the C3 CNN, B=32, Linf 8/255, 20 Adam steps, lr 0.1, alpha from CROWN
+* C5  beta-CROWN BaB domain batch, MLP 784-256x4-10, 4096 domains from one input,
+      Linf 0.03, 1-12 random unstable-neuron splits per domain, 10 steps
+
+Weights are Kaiming (uniform for C1/C3/C4/C5, normal for C2, relu gain);
+biases are 0 except C2 (N(0, 0.01^2)).  Specs are the 9 margin rows
+``e_y - e_j`` of a random true label ``y``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from .ir import BFTaskModule, BoundTask, TaskKind, TaskOp, default_storage_plan
+from .spec import InputSpec
+
+
+@dataclass
+class Workload:
+    name: str
+    module: BFTaskModule
+    spec: InputSpec
+    C: torch.Tensor
+    labels: torch.Tensor
+    extra: Dict[str, object] = field(default_factory=dict)
+
+    @property
+    def batch(self) -> int:
+        return int(self.spec.center.shape[0])
+
+    @property
+    def num_specs(self) -> int:
+        return int(self.C.shape[1])
+
+
+def _kaiming(shape, *, fan_in: int, gen: torch.Generator, kind: str) -> torch.Tensor:
+    gain = math.sqrt(2.0)
+    std = gain / math.sqrt(fan_in)
+    if kind == "uniform":
+        bound = math.sqrt(3.0) * std
+        return (torch.rand(shape, generator=gen, dtype=torch.float64) * 2.0 - 1.0).mul_(bound).to(torch.float32)
+    return (torch.randn(shape, generator=gen, dtype=torch.float64) * std).to(torch.float32)
+
+
+def build_mlp(dims: Sequence[int], *, gen: torch.Generator, init: str = "uniform",
+              bias_std: float = 0.0) -> BFTaskModule:
+    """Chain MLP ``dims[0] -> ... -> dims[-1]`` with ReLU between linear layers."""
+    ops: List[TaskOp] = []
+    params: Dict[str, torch.Tensor] = {}
+    prev = "input"
+    values = ["input"]
+    n = len(dims) - 1
+    for i in range(n):
+        W = _kaiming((dims[i + 1], dims[i]), fan_in=dims[i], gen=gen, kind=init)
+        if bias_std > 0:
+            b = (torch.randn(dims[i + 1], generator=gen, dtype=torch.float64) * bias_std).to(torch.float32)
+        else:
+            b = torch.zeros(dims[i + 1], dtype=torch.float32)
+        params[f"W{i}"] = W
+        params[f"b{i}"] = b
+        out = "out" if i == n - 1 else f"h{i}"
+        ops.append(TaskOp(op_type="linear", name=f"linear{i}", inputs=[prev, f"W{i}", f"b{i}"], outputs=[out]))
+        values.append(out)
+        if i < n - 1:
+            r = f"r{i}"
+            ops.append(TaskOp(op_type="relu", name=f"relu{i}", inputs=[out], outputs=[r]))
+            values.append(r)
+            prev = r
+    return _module(ops, params, values)
+
+
+def build_cnn(*, gen: torch.Generator) -> BFTaskModule:
+    """3x32x32 -> conv(16,4,s2,p1) -> relu -> conv(32,4,s2,p1) -> relu -> flatten -> fc100 -> relu -> fc10."""
+    ops: List[TaskOp] = []
+    params: Dict[str, torch.Tensor] = {}
+    params["W0"] = _kaiming((16, 3, 4, 4), fan_in=3 * 16, gen=gen, kind="uniform")
+    params["b0"] = torch.zeros(16)
+    params["W1"] = _kaiming((32, 16, 4, 4), fan_in=16 * 16, gen=gen, kind="uniform")
+    params["b1"] = torch.zeros(32)
+    params["W2"] = _kaiming((100, 2048), fan_in=2048, gen=gen, kind="uniform")
+    params["b2"] = torch.zeros(100)
+    params["W3"] = _kaiming((10, 100), fan_in=100, gen=gen, kind="uniform")
+    params["b3"] = torch.zeros(10)
+    conv = {"stride": 2, "padding": 1, "dilation": 1, "groups": 1}
+    ops.append(TaskOp("conv2d", "conv0", ["input", "W0", "b0"], ["h0"], dict(conv)))
+    ops.append(TaskOp("relu", "relu0", ["h0"], ["r0"]))
+    ops.append(TaskOp("conv2d", "conv1", ["r0", "W1", "b1"], ["h1"], dict(conv)))
+    ops.append(TaskOp("relu", "relu1", ["h1"], ["r1"]))
+    ops.append(TaskOp("flatten", "flatten", ["r1"], ["f1"], {"start_dim": 1, "end_dim": -1}))
+    ops.append(TaskOp("linear", "linear2", ["f1", "W2", "b2"], ["h2"]))
+    ops.append(TaskOp("relu", "relu2", ["h2"], ["r2"]))
+    ops.append(TaskOp("linear", "linear3", ["r2", "W3", "b3"], ["out"]))
+    values = ["input", "h0", "r0", "h1", "r1", "f1", "h2", "r2", "out"]
+    return _module(ops, params, values)
+
+
+def _module(ops: List[TaskOp], params: Dict[str, torch.Tensor], values: List[str]) -> BFTaskModule:
+    task = BoundTask(task_id="t0", kind=TaskKind.INTERVAL_IBP, ops=ops, input_values=["input"],
+                     output_values=["out"], params=list(params.keys()))
+    return BFTaskModule(tasks=[task], entry_task_id="t0", bindings={"params": params},
+                        storage_plan=default_storage_plan(values))
+
+
+def margin_spec(labels: torch.Tensor, num_classes: int = 10) -> torch.Tensor:
+    """C[b] rows are e_y - e_j for every j != y, ordered by j."""
+    B = int(labels.shape[0])
+    C = torch.zeros(B, num_classes - 1, num_classes)
+    for b in range(B):
+        y = int(labels[b])
+        r = 0
+        for j in range(num_classes):
+            if j == y:
+                continue
+            C[b, r, y] = 1.0
+            C[b, r, j] = -1.0
+            r += 1
+    return C
+
+
+def predicted_labels(module: BFTaskModule, x: torch.Tensor) -> torch.Tensor:
+    """Arg-max class of the clean network output at ``x`` (fp64 forward)."""
+    params = module.params
+    h = x.double()
+    for op in module.get_entry_task().ops:
+        if op.op_type == "linear":
+            h = h.reshape(h.shape[0], -1) @ params[op.inputs[1]].double().t() + params[op.inputs[2]].double()
+        elif op.op_type == "conv2d":
+            h = torch.nn.functional.conv2d(h, params[op.inputs[1]].double(), params[op.inputs[2]].double(),
+                                           stride=op.attrs.get("stride", 1), padding=op.attrs.get("padding", 0))
+        elif op.op_type == "relu":
+            h = h.clamp_min(0)
+        elif op.op_type == "flatten":
+            h = h.reshape(h.shape[0], -1)
+    return h.argmax(dim=1)
+
+
+def make_c1(seed: int = 0, batch: int = 64, eps: float = 2.0 / 255.0, label_mode: str = "random") -> Workload:
+    """``label_mode="predicted"`` labels each input with the network's own
+    prediction, which gives a mix of certified and uncertified inputs at small eps."""
+    g = torch.Generator().manual_seed(seed)
+    module = build_mlp([784, 256, 256, 10], gen=g)
+    x = torch.rand(batch, 784, generator=g)
+    labels = torch.randint(0, 10, (batch,), generator=g)
+    if label_mode == "predicted":
+        labels = predicted_labels(module, x)
+    lo = torch.clamp(x - eps, 0.0, 1.0)
+    hi = torch.clamp(x + eps, 0.0, 1.0)
+    spec = InputSpec.box(value_name="input", lower=lo, upper=hi)
+    return Workload("C1", module, spec, margin_spec(labels), labels)
+
+
+def make_c2(seed: int = 0, batch: int = 256, width: int = 500, depth: int = 6) -> Workload:
+    g = torch.Generator().manual_seed(seed)
+    module = build_mlp([784] + [width] * depth + [10], gen=g, init="normal", bias_std=0.01)
+    x = torch.rand(batch, 784, generator=g)
+    labels = torch.randint(0, 10, (batch,), generator=g)
+    spec = InputSpec.linf(value_name="input", center=x, eps=0.015)
+    return Workload("C2", module, spec, margin_spec(labels), labels)
+
+
+def make_c3(seed: int = 0, batch: int = 128, eps: float = 2.0 / 255.0, name: str = "C3") -> Workload:
+    g = torch.Generator().manual_seed(seed)
+    module = build_cnn(gen=g)
+    x = torch.rand(batch, 3, 32, 32, generator=g)
+    labels = torch.randint(0, 10, (batch,), generator=g)
+    spec = InputSpec.linf(value_name="input", center=x, eps=eps)
+    return Workload(name, module, spec, margin_spec(labels), labels)
+
+
+def make_c4(seed: int = 0, batch: int = 32) -> Workload:
+    w = make_c3(seed=seed, batch=batch, eps=8.0 / 255.0, name="C4")
+    w.extra.update({"steps": 20, "lr": 0.1, "alpha_init": "crown"})
+    return w
+
+
+def _ibp_relu_bounds_f64(module: BFTaskModule, x: torch.Tensor, eps: float) -> List[Tuple[torch.Tensor, torch.Tensor]]:
+    """Root pre-activation boxes of an MLP, fp64, used only to pick split candidates."""
+    params = module.params
+    ops = module.get_entry_task().ops
+    l = (x - eps).double()
+    u = (x + eps).double()
+    out = []
+    for op in ops:
+        if op.op_type == "linear":
+            W = params[op.inputs[1]].double()
+            b = params[op.inputs[2]].double()
+            c = (l + u) / 2
+            r = (u - l) / 2
+            mid = c @ W.t() + b
+            rad = r @ W.abs().t()
+            l, u = mid - rad, mid + rad
+        elif op.op_type == "relu":
+            out.append((l.clone(), u.clone()))
+            l, u = l.clamp_min(0), u.clamp_min(0)
+    return out
+
+
+def make_c5(seed: int = 0, domains: int = 4096, eps: float = 0.03, max_splits: int = 12,
+            width: int = 256, depth: int = 4, label_mode: str = "random") -> Workload:
+    g = torch.Generator().manual_seed(seed)
+    module = build_mlp([784] + [width] * depth + [10], gen=g)
+    x0 = torch.rand(1, 784, generator=g)
+    label = torch.randint(0, 10, (1,), generator=g)
+    if label_mode == "predicted":
+        label = predicted_labels(module, x0)
+    relu_names = [op.inputs[0] for op in module.get_entry_task().ops if op.op_type == "relu"]
+    root = _ibp_relu_bounds_f64(module, x0, eps)
+    cand: List[Tuple[int, int]] = []
+    for li, (l, u) in enumerate(root):
+        amb = ((l[0] < 0) & (u[0] > 0)).nonzero(as_tuple=False).flatten().tolist()
+        cand.extend((li, j) for j in amb)
+    splits = {name: torch.zeros(domains, width, dtype=torch.int8) for name in relu_names}
+    ncand = len(cand)
+    for d in range(domains):
+        k = int(torch.randint(1, max_splits + 1, (1,), generator=g))
+        k = min(k, ncand)
+        pick = torch.randperm(ncand, generator=g)[:k].tolist()
+        signs = torch.randint(0, 2, (k,), generator=g) * 2 - 1
+        for p, s in zip(pick, signs.tolist()):
+            li, j = cand[p]
+            splits[relu_names[li]][d, j] = int(s)
+    x = x0.expand(domains, 784).contiguous()
+    labels = label.expand(domains).contiguous()
+    spec = InputSpec.linf(value_name="input", center=x, eps=eps)
+    w = Workload("C5", module, spec, margin_spec(labels), labels)
+    w.extra.update({"splits": splits, "steps": 10, "lr": 0.2, "alpha_init": 0.5, "beta_init": 0.0,
+                    "num_candidates": ncand})
+    return w
+
+
+MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5}
+
+
+def make(name: str, **kw) -> Workload:
+    return MAKERS[name](**kw)
+
+
+def relu_input_names(module: BFTaskModule) -> List[str]:
+    return [op.inputs[0] for op in module.get_entry_task().ops if op.op_type == "relu"]
+
+
+def to_device(w: Workload, device) -> Workload:
+    """Copy a workload (params, spec, C, splits) to ``device``."""
+    params = {k: v.to(device) for k, v in w.module.params.items()}
+    mod = BFTaskModule(tasks=w.module.tasks, entry_task_id=w.module.entry_task_id,
+                       bindings={"params": params}, storage_plan=w.module.storage_plan)
+    extra = dict(w.extra)
+    if "splits" in extra:
+        extra["splits"] = {k: v.to(device) for k, v in extra["splits"].items()}
+    return Workload(w.name, mod, w.spec.to(device), w.C.to(device), w.labels.to(device), extra)
+
+
+def subset(w: Workload, n: int) -> Workload:
+    """First ``n`` inputs/domains of a workload (same network)."""
+    spec = w.spec
+    if hasattr(spec.perturbation, "lower"):
+        spec = InputSpec.box(value_name=spec.value_name, lower=spec.perturbation.lower[:n],
+                             upper=spec.perturbation.upper[:n])
+    else:
+        spec = InputSpec(value_name=spec.value_name, center=spec.center[:n], perturbation=spec.perturbation)
+    extra = dict(w.extra)
+    if "splits" in extra:
+        extra["splits"] = {k: v[:n] for k, v in extra["splits"].items()}
+    return Workload(w.name, w.module, spec, w.C[:n], w.labels[:n], extra)
