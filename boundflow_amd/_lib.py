@@ -1,0 +1,113 @@
+"""ctypes binding of the in-tree HIP library ``libboundflow_hip.so``.
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already mapped (both carry the SONAME ``libamdhip64.so.7``); one
+runtime per process.  There is no CPU fallback: if the library is missing or a
+call fails, the error is raised to the caller.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libboundflow_hip.so"
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32 = ctypes.c_int
+F32 = ctypes.c_float
+F64 = ctypes.c_double
+
+# name -> (restype, argtypes); every entry point listed in include/boundflow_hip.h
+SIGNATURES = {
+    "bf_abi_version": (I32, []),
+    "bf_last_error": (ctypes.c_char_p, []),
+    "bf_gemm": (I32, [P, I64, P, I64, I32, I32, P, I64, I64, I64, I64, P]),
+    "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, P, I64, P, P, P, P, P, P, P,
+                                       P]),
+    "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, P, I64, P, P, P, F32,
+                                              P, P, P, P, P, P]),
+    "bf_crown_relu_linear_concretize_workspace": (I64, [I64, I64, I64]),
+    "bf_crown_relu_relax": (I32, [P, P, I64, I64, I64, P, P, P, I64, P, I64, P, P, P, P, P, P, P, P]),
+    "bf_concretize_dense": (I32, [P, I64, I64, I64, P, P, F32, P, I32, P, P]),
+    "bf_ibp_linear": (I32, [P, P, I64, I64, I32, F32, I32, P, P, I64, P, I64, P, P, P, P, P, P]),
+    "bf_ibp_linear_workspace": (I64, [I64, I64, I64]),
+    "bf_interval_clip": (I32, [P, P, P, P, P, I64, I64, I64, P, P]),
+    "bf_branch_update": (I32, [P, P, I64, I64, I32, P, P, P, P]),
+    "bf_adam_clamp_step": (I32, [P, P, P, P, I64, F64, F64, F64, F32, I32, F32, F32, I32, P]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise HipError(
+            f"{LIB_PATH} is missing: build it with `python -m boundflow_amd.build` "
+            "(the HIP backend has no CPU fallback)")
+    lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.bf_abi_version() != 1:
+        raise HipError("libboundflow_hip ABI version mismatch")
+    _lib = lib
+    return lib
+
+
+def ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(stream: Optional[torch.cuda.Stream] = None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def call(name: str, *args) -> int:
+    """Invoke an entry point and raise HipError with bf_last_error() on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if SIGNATURES[name][0] is I32 and name not in ("bf_abi_version",) and rc != 0:
+        msg = lib.bf_last_error().decode(errors="replace")
+        raise HipError(f"{name} failed (status {rc}): {msg}")
+    return rc
+
+
+def require_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise HipError(f"{name} must be a HIP device tensor (the backend has no CPU path)")
+    if t.dtype != torch.float32 and t.dtype not in (torch.int8, torch.int32):
+        raise HipError(f"{name} must be float32, got {t.dtype}")
+    if not t.is_contiguous():
+        raise HipError(f"{name} must be contiguous")
+
+
+def loaded_path() -> str:
+    return str(LIB_PATH)
+
+
+def library_exports(path: Optional[str] = None):
+    """Names of SIGNATURES that the shared object exports (no device call)."""
+    lib = ctypes.CDLL(str(path or LIB_PATH))
+    return [n for n in SIGNATURES if hasattr(lib, n)]
+
+
+def env_flag(name: str) -> bool:
+    return os.environ.get(name, "") not in ("", "0", "false", "False")

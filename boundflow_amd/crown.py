@@ -1,0 +1,483 @@
+"""HIP-native CROWN-IBP for chain-structured BoundTask programs.
+
+Host driver mirroring the reference entry points
+
+* ``forward_ibp_trace``        -- boundflow/runtime/crown_ibp.py:101-342 (_forward_ibp_trace_mlp)
+* ``run_crown_ibp_mlp``        -- boundflow/runtime/crown_ibp.py:2054-2133
+* ``run_crown_ibp_mlp_from_forward_trace`` -- boundflow/runtime/crown_ibp.py:2136-2199
+* ``run_crown_all_intermediate`` -- layer-by-layer composition of
+  boundflow/runtime/native_intermediate_refinement.py:923-988
+
+with the same argument meaning and error behaviour (ValueError on an
+infeasible split or constraint, NotImplementedError for an unsupported graph),
+but every numeric step runs in the HIP library on the caller's stream:
+
+* IBP per affine layer in center/radius form (``bf_ibp_linear``), with the
+  consumer ReLU's split and constraint intersection fused into the epilogue;
+* the CROWN backward as one fused kernel per Affine->ReLU region
+  (``bf_crown_relu_linear_fwd``: ReLU relaxation in the A-tile prologue, fp32
+  MFMA contraction, bias reductions), and the input layer fused with the
+  Linf/box concretization (``bf_crown_relu_linear_concretize``).
+
+Tensors live on the HIP device; nothing is copied to the host except the
+feasibility flags when the caller asked for the reference's raise-on-infeasible
+behaviour.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, List, Mapping, Optional, Tuple
+
+import torch
+
+from . import _lib
+from .profiling import launch as _timed
+from .conv import conv_backward_step, ibp_conv2d
+from .ir import BFTaskModule, TaskKind
+from .spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation, normalize_input_spec
+
+
+# ---------------------------------------------------------------------------
+# Graph parsing
+
+
+@dataclass
+class AffineLayer:
+    kind: str                     # "linear" | "conv2d"
+    op_index: int
+    in_name: str
+    out_name: str
+    weight: torch.Tensor
+    bias: Optional[torch.Tensor]
+    in_shape: Tuple[int, ...]     # per-sample input shape
+    out_shape: Tuple[int, ...]    # per-sample output shape
+    attrs: Dict[str, object] = field(default_factory=dict)
+    relu_input_of_consumer: bool = False   # output feeds a ReLU
+    input_is_relu_of: Optional[str] = None  # name of the pre-activation whose ReLU is this layer's input
+
+
+@dataclass
+class Chain:
+    layers: List[AffineLayer]
+    relu_names: List[str]
+    output_value: str
+
+
+def _pair(v) -> Tuple[int, int]:
+    if isinstance(v, int):
+        return (v, v)
+    v = tuple(int(x) for x in v)
+    return (v[0], v[0]) if len(v) == 1 else (v[0], v[1])
+
+
+def parse_chain(module: BFTaskModule, spec: InputSpec, output_value: Optional[str] = None) -> Chain:
+    """Validate that the entry task is a chain of affine/ReLU/flatten ops and
+    collect per-layer shapes.  Raises NotImplementedError otherwise."""
+    module.validate()
+    task = module.get_entry_task()
+    if task.kind != TaskKind.INTERVAL_IBP:
+        raise NotImplementedError(f"HIP CROWN only supports INTERVAL_IBP, got {task.kind}")
+    if module.task_graph is not None or len(module.tasks) != 1:
+        raise NotImplementedError("HIP CROWN supports single-task modules only")
+    params = module.params
+    if output_value is None:
+        if len(task.output_values) != 1:
+            raise ValueError(f"task has {len(task.output_values)} outputs; specify output_value explicitly")
+        output_value = task.output_values[0]
+    shapes: Dict[str, Tuple[int, ...]] = {spec.value_name: tuple(int(d) for d in spec.center.shape[1:])}
+    relu_of: Dict[str, str] = {}     # relu output -> relu input
+    layers: List[AffineLayer] = []
+    relu_names: List[str] = []
+    current = spec.value_name
+    for idx, op in enumerate(task.ops):
+        if len(op.outputs) != 1:
+            raise NotImplementedError(f"multi-output op {op.name}")
+        x = op.inputs[0]
+        if x != current:
+            raise NotImplementedError(f"HIP CROWN supports chain graphs only (op {op.name} reads {x})")
+        t = op.op_type
+        if t == "linear":
+            W = params[op.inputs[1]]
+            b = params[op.inputs[2]] if len(op.inputs) == 3 else None
+            if W.dim() != 2:
+                raise NotImplementedError("batched linear weights are not supported")
+            in_shape = shapes[x]
+            if len(in_shape) != 1 or in_shape[0] != int(W.shape[1]):
+                raise ValueError(f"linear {op.name}: input shape {in_shape} vs weight {tuple(W.shape)}")
+            out_shape = (int(W.shape[0]),)
+            layers.append(AffineLayer("linear", idx, x, op.outputs[0], W, b, in_shape, out_shape,
+                                      input_is_relu_of=relu_of.get(x)))
+        elif t == "conv2d":
+            W = params[op.inputs[1]]
+            b = params[op.inputs[2]] if len(op.inputs) == 3 else None
+            in_shape = shapes[x]
+            stride = _pair(op.attrs.get("stride", 1))
+            padding = _pair(op.attrs.get("padding", 0))
+            dilation = _pair(op.attrs.get("dilation", 1))
+            groups = int(op.attrs.get("groups", 1))
+            if groups != 1 or dilation != (1, 1):
+                raise NotImplementedError("HIP conv2d supports groups=1, dilation=1")
+            if len(in_shape) != 3 or in_shape[0] != int(W.shape[1]):
+                raise ValueError(f"conv2d {op.name}: input shape {in_shape} vs weight {tuple(W.shape)}")
+            kh, kw = int(W.shape[2]), int(W.shape[3])
+            ho = (in_shape[1] + 2 * padding[0] - kh) // stride[0] + 1
+            wo = (in_shape[2] + 2 * padding[1] - kw) // stride[1] + 1
+            out_shape = (int(W.shape[0]), ho, wo)
+            layers.append(AffineLayer("conv2d", idx, x, op.outputs[0], W, b, in_shape, out_shape,
+                                      attrs={"stride": stride, "padding": padding},
+                                      input_is_relu_of=relu_of.get(x)))
+        elif t == "relu":
+            if not layers or layers[-1].out_name != x:
+                raise NotImplementedError("HIP CROWN expects every ReLU to follow an affine layer")
+            layers[-1].relu_input_of_consumer = True
+            relu_of[op.outputs[0]] = x
+            relu_names.append(x)
+            out_shape = shapes[x]
+        elif t in ("flatten", "reshape"):
+            if t == "flatten" and (int(op.attrs.get("start_dim", 1)) != 1 or int(op.attrs.get("end_dim", -1)) != -1):
+                raise NotImplementedError("flatten(start_dim=1, end_dim=-1) only")
+            n = 1
+            for d in shapes[x]:
+                n *= d
+            out_shape = (n,) if t == "flatten" else tuple(int(d) for d in op.attrs["shape"][1:])
+            if x in relu_of:
+                relu_of[op.outputs[0]] = relu_of[x]
+        else:
+            raise NotImplementedError(f"HIP CROWN: unsupported op_type {t}")
+        if t in ("linear", "conv2d"):
+            out_shape = layers[-1].out_shape
+        shapes[op.outputs[0]] = out_shape
+        current = op.outputs[0]
+        if op.outputs[0] == output_value:
+            break
+    if current != output_value:
+        raise ValueError(f"output_value {output_value} not produced by the chain")
+    if not layers or layers[-1].out_name != output_value:
+        raise NotImplementedError("the output value must be produced by an affine layer")
+    return Chain(layers=layers, relu_names=[r for r in relu_names if r != output_value], output_value=output_value)
+
+
+def _numel(shape) -> int:
+    n = 1
+    for d in shape:
+        n *= int(d)
+    return n
+
+
+# ---------------------------------------------------------------------------
+# Forward IBP trace
+
+
+@dataclass
+class ForwardTrace:
+    interval_env: Dict[str, IntervalState]
+    relu_pre: Dict[str, IntervalState]
+    infeasible: Optional[torch.Tensor]       # int32 [B] (1 = the split/constraint emptied a box)
+    input_center_proj: Dict[str, torch.Tensor] = field(default_factory=dict)  # first-layer x0 W^T (no bias)
+
+
+def _broadcast_split(split: torch.Tensor, batch: int, numel: int) -> Tuple[torch.Tensor, int]:
+    s = split.to(dtype=torch.int8)
+    if s.numel() == numel:
+        return s.reshape(numel).contiguous(), 0
+    if s.numel() == batch * numel and int(s.shape[0]) == batch:
+        return s.reshape(batch, numel).contiguous(), numel
+    raise ValueError(f"relu split of shape {tuple(split.shape)} cannot broadcast to ({batch}, {numel})")
+
+
+def forward_ibp_trace(
+    module: BFTaskModule,
+    input_spec,
+    *,
+    relu_split_state: Optional[Dict[str, torch.Tensor]] = None,
+    relu_pre_constraints: Optional[Mapping[str, IntervalState]] = None,
+    raise_on_infeasible: bool = True,
+    chain: Optional[Chain] = None,
+) -> ForwardTrace:
+    spec = normalize_input_spec(input_spec)
+    if chain is None:
+        chain = parse_chain(module, spec)
+    center = spec.center
+    _lib.require_device(center, "input center")
+    B = int(center.shape[0])
+    dev = center.device
+    stream = _lib.stream_handle()
+    relu_set = set(chain.relu_names)
+    infeasible = torch.zeros(B, dtype=torch.int32, device=dev)
+    interval_env: Dict[str, IntervalState] = {}
+    relu_pre: Dict[str, IntervalState] = {}
+    proj: Dict[str, torch.Tensor] = {}
+    pert = spec.perturbation
+    if isinstance(pert, LpBallPerturbation) and pert.normalized_p() != "inf":
+        raise NotImplementedError("HIP backend supports Linf balls and boxes")
+    prev_lo = prev_hi = None
+    for li, layer in enumerate(chain.layers):
+        split = None
+        split_ld = 0
+        out_numel = _numel(layer.out_shape)
+        consumer_relu = layer.out_name in relu_set
+        if consumer_relu and relu_split_state is not None and layer.out_name in relu_split_state:
+            split, split_ld = _broadcast_split(relu_split_state[layer.out_name].to(dev), B, out_numel)
+        has_constraint = consumer_relu and relu_pre_constraints is not None
+        lo = torch.empty((B,) + layer.out_shape, device=dev, dtype=torch.float32)
+        hi = torch.empty_like(lo)
+        first = li == 0
+        if layer.kind == "linear":
+            K = _numel(layer.in_shape)
+            N = out_numel
+            ws = torch.empty(int(_lib.load().bf_ibp_linear_workspace(B, K, N)), device=dev, dtype=torch.float32)
+            W = layer.weight.contiguous()
+            b = None if layer.bias is None else layer.bias.contiguous()
+            cproj = None
+            if first:
+                cproj = torch.empty(B, N, device=dev, dtype=torch.float32)
+                if isinstance(pert, BoxPerturbation):
+                    in_lo, in_hi, kind, eps, relu_in = (pert.lower.reshape(B, K).contiguous(),
+                                                        pert.upper.reshape(B, K).contiguous(), 0, 0.0, 0)
+                else:
+                    in_lo, in_hi, kind, eps, relu_in = center.reshape(B, K).contiguous(), None, 1, float(pert.eps), 0
+            else:
+                in_lo, in_hi, kind, eps = prev_lo.reshape(B, K), prev_hi.reshape(B, K), 0, 0.0
+                relu_in = 1 if layer.input_is_relu_of is not None else 0
+            _lib.call("bf_ibp_linear", _lib.ptr(in_lo), _lib.ptr(in_hi), B, K, kind, eps, relu_in, _lib.ptr(W),
+                      _lib.ptr(b), N, _lib.ptr(None if has_constraint else split), split_ld, _lib.ptr(ws),
+                      _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(cproj), _lib.ptr(infeasible), stream)
+            if cproj is not None:
+                proj[layer.out_name] = cproj
+        else:
+            if first:
+                blo, bhi = pert.bounding_box(center)
+                in_lo, in_hi, relu_in = blo.contiguous(), bhi.contiguous(), 0
+            else:
+                in_lo, in_hi = prev_lo, prev_hi
+                relu_in = 1 if layer.input_is_relu_of is not None else 0
+            ibp_conv2d(in_lo, in_hi, relu_in, layer, None if has_constraint else split, split_ld, lo, hi,
+                       infeasible)
+        if has_constraint:
+            c = relu_pre_constraints[layer.out_name]
+            _lib.call("bf_interval_clip", _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(c.lower.contiguous()),
+                      _lib.ptr(c.upper.contiguous()), _lib.ptr(split), split_ld, B, out_numel,
+                      _lib.ptr(infeasible), stream)
+        st = IntervalState(lo, hi)
+        interval_env[layer.out_name] = st
+        if consumer_relu:
+            relu_pre[layer.out_name] = st
+        prev_lo, prev_hi = lo, hi
+    if raise_on_infeasible and (relu_split_state or relu_pre_constraints):
+        if bool(infeasible.any().item()):
+            raise ValueError("infeasible relu split or constraint: lower>upper after applying split")
+    return ForwardTrace(interval_env=interval_env, relu_pre=relu_pre, infeasible=infeasible,
+                        input_center_proj=proj)
+
+
+# ---------------------------------------------------------------------------
+# CROWN backward
+
+
+def _flat_param(v: torch.Tensor, batch: int, numel: int, label: str) -> Tuple[torch.Tensor, int]:
+    """[*shape] / [numel] / [1, numel] -> shared (stride 0); [B, *shape] -> per-domain (stride numel)."""
+    v = v.to(torch.float32)
+    if v.numel() == numel:
+        return v.reshape(numel).contiguous(), 0
+    if v.numel() == batch * numel and int(v.shape[0]) == batch:
+        return v.reshape(batch, numel).contiguous(), numel
+    raise ValueError(f"{label} of shape {tuple(v.shape)} cannot broadcast to ({batch}, {numel})")
+
+
+@dataclass
+class BackwardSaved:
+    """Per-layer tensors kept for the gradient pass (lower bound only)."""
+    A_in: List[Optional[torch.Tensor]]      # coefficient entering each layer's relaxation ([M, n_k]) or None
+    b_rows: torch.Tensor
+
+
+def _init_spec(C: Optional[torch.Tensor], batch: int, out_dim: int, dev) -> Tuple[torch.Tensor, int, int]:
+    """Return (A0, S, a_dstride) for the initial coefficient (crown_ibp.py:672-719)."""
+    if C is None:
+        eye = torch.eye(out_dim, device=dev, dtype=torch.float32)
+        return eye, out_dim, 0
+    C = C.to(device=dev, dtype=torch.float32)
+    if C.dim() == 2:
+        if int(C.shape[1]) != out_dim:
+            raise ValueError(f"linear_spec_C shape mismatch: C={tuple(C.shape)} out=({batch}, {out_dim})")
+        return C.contiguous(), int(C.shape[0]), 0
+    if C.dim() != 3 or int(C.shape[0]) != batch or int(C.shape[2]) != out_dim:
+        raise ValueError(f"linear_spec_C shape mismatch: C={tuple(C.shape)} out=({batch}, {out_dim})")
+    S = int(C.shape[1])
+    return C.contiguous(), S, S * out_dim
+
+
+def crown_backward(
+    module: BFTaskModule,
+    spec: InputSpec,
+    trace: ForwardTrace,
+    *,
+    chain: Chain,
+    linear_spec_C: Optional[torch.Tensor] = None,
+    relu_alpha: Optional[Dict[str, torch.Tensor]] = None,
+    relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
+    need_upper: bool = True,
+    need_lower: bool = True,
+    save: Optional[dict] = None,
+) -> IntervalState:
+    dev = spec.center.device
+    B = int(spec.center.shape[0])
+    stream = _lib.stream_handle()
+    layers = chain.layers
+    out_dim = _numel(layers[-1].out_shape)
+    A0, S, a_dstride = _init_spec(linear_spec_C, B, out_dim, dev)
+    M = B * S
+    pert = spec.perturbation
+    A_u: Optional[torch.Tensor] = A0 if need_upper else None
+    A_l: Optional[torch.Tensor] = A0 if need_lower else None
+    b_u = b_l = None
+    stride = a_dstride
+    for k in range(len(layers) - 1, -1, -1):
+        layer = layers[k]
+        relax_name = layer.out_name if k < len(layers) - 1 else None
+        pre = trace.relu_pre[relax_name] if relax_name is not None else None
+        N = _numel(layer.out_shape)
+        alpha = add = None
+        alpha_ld = add_ld = 0
+        if relax_name is not None:
+            if relu_alpha is not None and relax_name in relu_alpha:
+                alpha, alpha_ld = _flat_param(relu_alpha[relax_name], B, N, f"relu_alpha[{relax_name}]")
+            if relu_pre_add_coeff_l is not None and relax_name in relu_pre_add_coeff_l:
+                add, add_ld = _flat_param(relu_pre_add_coeff_l[relax_name], B, N,
+                                          f"relu_pre_add_coeff_l[{relax_name}]")
+        pre_lo = None if pre is None else pre.lower.reshape(B, N)
+        pre_hi = None if pre is None else pre.upper.reshape(B, N)
+        if save is not None and A_l is not None:
+            save.setdefault("A_in", {})[k] = (A_l, stride)
+            save.setdefault("b_in", {})[k] = b_l
+        if layer.kind == "conv2d":
+            A_u, A_l, b_u, b_l, stride, done = conv_backward_step(
+                layer, k == 0, A_u, A_l, stride, b_u, b_l, B, S, pre_lo, pre_hi, alpha, alpha_ld, add, add_ld,
+                spec, trace)
+            if done is not None:
+                return done
+            continue
+        W = layer.weight.contiguous()
+        bias = None if layer.bias is None else layer.bias.contiguous()
+        P = _numel(layer.in_shape)
+        if k > 0 and linear_spec_C is None and k == len(layers) - 1:
+            # C = I: I @ W is W itself, shared by every domain (no contraction needed)
+            A_u = W if A_u is not None else None
+            A_l = W if A_l is not None else None
+            brow = (bias if bias is not None else torch.zeros(N, device=dev)).repeat(B).contiguous()
+            b_u = brow if A_u is not None else None
+            b_l = brow if A_l is not None else None
+            stride = 0
+            continue
+        if k == 0:
+            # input layer: relaxation + contraction fused with the concretization
+            if isinstance(pert, BoxPerturbation):
+                lo = pert.lower.reshape(B, P)
+                hi = pert.upper.reshape(B, P)
+                rad = ((hi - lo) / 2.0).contiguous()
+                cvec = trace.input_center_proj.get(layer.out_name)
+                # center term A' (mid W^T): the trace holds mid W^T when the input is a box
+                eps = 1.0
+            else:
+                rad = None
+                cvec = trace.input_center_proj.get(layer.out_name)
+                eps = float(pert.eps)
+            if cvec is None:
+                raise RuntimeError("forward trace lacks the input-layer projection")
+            ws = torch.empty(int(_lib.load().bf_crown_relu_linear_concretize_workspace(B, S, P)), device=dev,
+                             dtype=torch.float32)
+            lb = torch.empty(B, S, device=dev, dtype=torch.float32) if A_l is not None else None
+            ub = torch.empty(B, S, device=dev, dtype=torch.float32) if A_u is not None else None
+            nz = int(A_u is not None) + int(A_l is not None)
+            with _timed("crown_relu_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
+                _lib.call("bf_crown_relu_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
+                          _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld,
+                          _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(cvec), _lib.ptr(rad), eps, _lib.ptr(b_u),
+                          _lib.ptr(b_l), _lib.ptr(ws), _lib.ptr(lb), _lib.ptr(ub), stream)
+            if save is not None:
+                save["final_ws"] = ws
+            return IntervalState(lower=lb, upper=ub)
+        nA_u = torch.empty(M, P, device=dev, dtype=torch.float32) if A_u is not None else None
+        nA_l = torch.empty(M, P, device=dev, dtype=torch.float32) if A_l is not None else None
+        nb_u = torch.empty(M, device=dev, dtype=torch.float32) if A_u is not None else None
+        nb_l = torch.empty(M, device=dev, dtype=torch.float32) if A_l is not None else None
+        nz = int(A_u is not None) + int(A_l is not None)
+        a_rows = M if stride != 0 else S
+        with _timed("crown_relu_linear_fwd", 2.0 * nz * M * N * P, 4.0 * nz * (a_rows * N + N * P + M * P)):
+            _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
+                      _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld,
+                      _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(nA_u),
+                      _lib.ptr(nA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), stream)
+        A_u, A_l, b_u, b_l = nA_u, nA_l, nb_u, nb_l
+        stride = S * P
+    raise RuntimeError("backward did not reach the input layer")
+
+
+def _check_alpha_beta_args(relu_pre_add_coeff_u):
+    if relu_pre_add_coeff_u:
+        raise NotImplementedError("relu_pre_add_coeff_u is not used by the alpha-beta objective and unsupported")
+
+
+def run_crown_ibp_mlp(
+    module: BFTaskModule,
+    input_spec,
+    *,
+    linear_spec_C: Optional[torch.Tensor] = None,
+    output_value: Optional[str] = None,
+    relu_alpha: Optional[Dict[str, torch.Tensor]] = None,
+    relu_pre_add_coeff_u: Optional[Dict[str, torch.Tensor]] = None,
+    relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
+    relu_split_state: Optional[Dict[str, torch.Tensor]] = None,
+) -> IntervalState:
+    """HIP counterpart of run_crown_ibp_mlp (crown_ibp.py:2054-2133)."""
+    _check_alpha_beta_args(relu_pre_add_coeff_u)
+    spec = normalize_input_spec(input_spec)
+    chain_full = parse_chain(module, spec)
+    trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain_full)
+    chain = parse_chain(module, spec, output_value) if output_value is not None else chain_full
+    return crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=relu_alpha,
+                          relu_pre_add_coeff_l=relu_pre_add_coeff_l)
+
+
+def run_crown_ibp_mlp_from_forward_trace(
+    module: BFTaskModule,
+    input_spec,
+    *,
+    trace: ForwardTrace,
+    linear_spec_C: Optional[torch.Tensor] = None,
+    output_value: Optional[str] = None,
+    relu_alpha: Optional[Dict[str, torch.Tensor]] = None,
+    relu_pre_add_coeff_u: Optional[Dict[str, torch.Tensor]] = None,
+    relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
+) -> IntervalState:
+    """HIP counterpart of run_crown_ibp_mlp_from_forward_trace (crown_ibp.py:2136-2199)."""
+    _check_alpha_beta_args(relu_pre_add_coeff_u)
+    spec = normalize_input_spec(input_spec)
+    chain = parse_chain(module, spec, output_value)
+    return crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=relu_alpha,
+                          relu_pre_add_coeff_l=relu_pre_add_coeff_l)
+
+
+def run_crown_all_intermediate(module: BFTaskModule, input_spec, *, linear_spec_C: torch.Tensor):
+    """Every intermediate pre-activation bound by CROWN (C = I per layer),
+    intersected with the IBP bound, then the final spec bound; the composition of
+    native_intermediate_refinement.py:923-988 applied to every ReLU after the first."""
+    spec = normalize_input_spec(input_spec)
+    chain_full = parse_chain(module, spec)
+    trace = forward_ibp_trace(module, spec, chain=chain_full)
+    names = list(trace.relu_pre.keys())
+    stream = _lib.stream_handle()
+    B = int(spec.center.shape[0])
+    for name in names[1:]:
+        chain = parse_chain(module, spec, name)
+        b = crown_backward(module, spec, trace, chain=chain, linear_spec_C=None)
+        cur = trace.relu_pre[name]
+        n = int(cur.lower[0].numel())
+        lo = cur.lower.reshape(B, n)
+        hi = cur.upper.reshape(B, n)
+        flag = torch.zeros(B, dtype=torch.int32, device=spec.center.device)
+        _lib.call("bf_interval_clip", _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(b.lower.contiguous()),
+                  _lib.ptr(b.upper.contiguous()), None, 0, B, n, _lib.ptr(flag), stream)
+    final = crown_backward(module, spec, trace, chain=chain_full, linear_spec_C=linear_spec_C)
+    return final, trace.relu_pre

@@ -1,0 +1,47 @@
+// Argument block of the fp32 MFMA contraction kernel (see bf_gemm.hip).
+#pragma once
+
+#include "bf_common.h"
+
+namespace bf {
+
+enum : int { PRO_PLAIN = 0, PRO_RELAX = 1 };
+enum : int { EPI_STORE = 0, EPI_ABSSUM = 1 };
+
+struct GemmArgs {
+  // Operand pair selected by blockIdx.z (z = 0 "upper", z = 1 "lower").
+  const float* A[2];
+  float* C[2];
+  int64_t lda, ldc;
+  int64_t lda_d;    // A row m = d*S + s lives at A + d*lda_d + s*lda (lda_d = S*lda when contiguous,
+                    // 0 when every domain shares the same S rows)
+  const float* B;   // [K, N] row-major (ldb) or, with trans_b, [N, K] row-major (ldb)
+  int64_t ldb;
+  int trans_b;
+  int abs_b;        // use |B| (interval radius products)
+  int64_t M, N, K;
+  int z_lower_first;  // when 1, blockIdx.z = 0 uses lower semantics (single lower pass)
+
+  // --- ReLU relaxation prologue (PRO_RELAX) ---
+  int64_t S;                 // rows per domain
+  const float* pre_lo;       // [D, K] (row stride ld_pre); null = identity (no relaxation, row sums only)
+  const float* pre_hi;
+  int64_t ld_pre;
+  const float* alpha;        // optional lower-slope override, [D, K] with row stride alpha_ld (0 = shared)
+  int64_t alpha_ld;
+  const float* add_l;        // optional coefficient added to the lower A' (beta split term), row stride add_ld
+  int64_t add_ld;
+  const float* kbias;        // optional [K] bias of the affine layer: sum_k A'[m,k] * kbias[k]
+  const float* cvec;         // optional [D, K] center vector: sum_k A'[m,k] * cvec[d,k]
+  int64_t cvec_ld;
+  const float* b_in[2];      // optional running bias [M]
+  float* b_out[2];           // [M] = (b_in + sum A*beta_sel) + sum A'*kbias   (written by blockIdx.y == 0)
+  float* c_out[2];           // [M] center sums (written by blockIdx.y == 0)
+
+  // --- |C| row-reduction epilogue (EPI_ABSSUM) ---
+  const float* wvec;         // optional [D, N] weights (box radius), row stride w_ld
+  int64_t w_ld;
+  float* partial[2];         // [gridDim.y, M] partial row sums
+};
+
+}  // namespace bf

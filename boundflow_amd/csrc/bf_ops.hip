@@ -1,0 +1,539 @@
+// Bandwidth-bound kernels and the C-ABI of the boundflow HIP library.
+//
+// Every extern "C" entry point takes device pointers, int64 sizes, scalar
+// parameters and a hipStream_t; it launches asynchronously on that stream,
+// never allocates or synchronizes, and returns 0 on success or a nonzero
+// status with a message retrievable through bf_last_error().
+
+#include "bf_common.h"
+
+#include <cstring>
+
+namespace bf {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+}  // namespace bf
+
+#include "bf_gemm_args.h"
+
+namespace bf {
+
+int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream);
+int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
+                        const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream);
+int gemm_partial_count(int64_t N);
+
+// ---------------------------------------------------------------------------
+// IBP helpers (center/radius form)
+
+// mid = (relu?(l) + relu?(u)) / 2, rad = (relu?(u) - relu?(l)) / 2
+__global__ void ibp_center_radius_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int64_t n,
+                                         int apply_relu, float* __restrict__ mid, float* __restrict__ rad) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float l = lo[i], u = hi[i];
+  if (apply_relu) {
+    l = fmaxf(l, 0.f);
+    u = fmaxf(u, 0.f);
+  }
+  mid[i] = (l + u) / 2.0f;
+  rad[i] = (u - l) / 2.0f;
+}
+
+// row_norm[o] = sum_i |W[o, i]|   (Linf input layer, perturbation.py:133)
+__global__ void row_abs_sum_kernel(const float* __restrict__ W, int64_t O, int64_t I, float* __restrict__ out) {
+  int64_t o = (int64_t)blockIdx.x;
+  if (o >= O) return;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < I; i += blockDim.x) s += fabsf(W[o * I + i]);
+  __shared__ float sh[256];
+  sh[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[o] = sh[0];
+}
+
+// lo = (c - dev) + b, hi = (c + dev) + b, then the ReLU split of the consumer
+// (crown_ibp.py:70-98): active -> lo = max(lo, 0); inactive -> hi = min(hi, 0);
+// a domain with lo > hi anywhere is flagged infeasible.
+__global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __restrict__ r,
+                                    const float* __restrict__ rownorm, float eps, const float* __restrict__ bias,
+                                    const int8_t* __restrict__ split, int64_t split_ld, int64_t B, int64_t N,
+                                    float* __restrict__ lo, float* __restrict__ hi, int* __restrict__ infeasible) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * N) return;
+  int64_t b = i / N, n = i % N;
+  float dev = rownorm ? eps * rownorm[n] : r[i];
+  float l = c[i] - dev;
+  float u = c[i] + dev;
+  if (bias) {
+    l = l + bias[n];
+    u = u + bias[n];
+  }
+  if (split) {
+    int8_t s = split[b * split_ld + n];
+    if (s > 0) l = fmaxf(l, 0.f);
+    if (s < 0) u = fminf(u, 0.f);
+    if (l > u && infeasible) infeasible[b] = 1;
+  }
+  lo[i] = l;
+  hi[i] = u;
+}
+
+// Intersect with external constraints (crown_ibp.py:186-209) and apply a split.
+__global__ void interval_clip_kernel(float* __restrict__ lo, float* __restrict__ hi, const float* __restrict__ clo,
+                                     const float* __restrict__ chi, const int8_t* __restrict__ split,
+                                     int64_t split_ld, int64_t B, int64_t N, int* __restrict__ infeasible) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * N) return;
+  int64_t b = i / N, n = i % N;
+  float l = lo[i], u = hi[i];
+  if (clo) {
+    l = fmaxf(l, clo[i]);
+    u = fminf(u, chi[i]);
+  }
+  if (split) {
+    int8_t s = split[b * split_ld + n];
+    if (s > 0) l = fmaxf(l, 0.f);
+    if (s < 0) u = fminf(u, 0.f);
+  }
+  if (l > u && infeasible) infeasible[b] = 1;
+  lo[i] = l;
+  hi[i] = u;
+}
+
+// ---------------------------------------------------------------------------
+// Standalone ReLU relaxation pass (north-star kernel #3 in its unfused form):
+// one wave64 per coefficient row, float loads strided by 64 lanes, wave
+// reduction of the bias terms.  Writes A' for both bounds and
+//   b_out = (b_in + sum_k A * beta_sel)  [+ sum_k A' * kbias if kbias].
+__global__ void __launch_bounds__(256)
+relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t M, int64_t S, int64_t K,
+                       const float* __restrict__ lo, const float* __restrict__ hi, const float* __restrict__ alpha,
+                       int64_t alpha_ld, const float* __restrict__ add_l, int64_t add_ld,
+                       const float* __restrict__ kbias, const float* __restrict__ bu_in,
+                       const float* __restrict__ bl_in, float* __restrict__ Au_out, float* __restrict__ Al_out,
+                       float* __restrict__ bu_out, float* __restrict__ bl_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const int64_t d = m / S;
+  float su = 0.f, sl = 0.f, ku = 0.f, kl = 0.f;
+  for (int64_t k = lane; k < K; k += 64) {
+    const float l = lo[d * K + k], u = hi[d * K + k];
+    const bool has_alpha = alpha != nullptr;
+    const float a = has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f;
+    Relax r = relu_relax(l, u, has_alpha, a);
+    if (Au) {
+      float v = Au[m * K + k];
+      bool nn = v >= 0.f;
+      float o = v * (nn ? r.au : r.al);
+      su += v * (nn ? r.bu : r.bl);
+      if (kbias) ku += o * kbias[k];
+      Au_out[m * K + k] = o;
+    }
+    if (Al) {
+      float v = Al[m * K + k];
+      bool nn = v >= 0.f;
+      float o = v * (nn ? r.al : r.au);
+      sl += v * (nn ? r.bl : r.bu);
+      if (add_l) o = o + add_l[d * add_ld + k];
+      if (kbias) kl += o * kbias[k];
+      Al_out[m * K + k] = o;
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    su += __shfl_xor(su, off, 64);
+    sl += __shfl_xor(sl, off, 64);
+    ku += __shfl_xor(ku, off, 64);
+    kl += __shfl_xor(kl, off, 64);
+  }
+  if (lane == 0) {
+    if (bu_out) bu_out[m] = ((bu_in ? bu_in[m] : 0.f) + su) + ku;
+    if (bl_out) bl_out[m] = ((bl_in ? bl_in[m] : 0.f) + sl) + kl;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dense concretization (north-star kernel #4): one wave64 per row
+//   center = sum_i A[m,i] * c[d,i];  norm = sum_i |A[m,i]| (* rad[d,i])
+//   Linf: lb = (center - eps*norm) + b ; box: eps = 1 with radius weights.
+__global__ void __launch_bounds__(256)
+concretize_rows_kernel(const float* __restrict__ A, int64_t M, int64_t S, int64_t I, const float* __restrict__ cen,
+                       const float* __restrict__ rad, float eps, const float* __restrict__ b, int is_lower,
+                       float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const int64_t d = m / S;
+  float c = 0.f, nrm = 0.f;
+  const float* __restrict__ row = A + m * I;
+  const float* __restrict__ cr = cen + d * I;
+  if ((I & 3) == 0) {
+    const float4* row4 = reinterpret_cast<const float4*>(row);
+    const float4* c4 = reinterpret_cast<const float4*>(cr);
+    const float4* r4 = rad ? reinterpret_cast<const float4*>(rad + d * I) : nullptr;
+    for (int64_t q = lane; q < I / 4; q += 64) {
+      float4 a = row4[q], x = c4[q];
+      c += a.x * x.x + a.y * x.y + a.z * x.z + a.w * x.w;
+      if (r4) {
+        float4 w = r4[q];
+        nrm += fabsf(a.x) * w.x + fabsf(a.y) * w.y + fabsf(a.z) * w.z + fabsf(a.w) * w.w;
+      } else {
+        nrm += fabsf(a.x) + fabsf(a.y) + fabsf(a.z) + fabsf(a.w);
+      }
+    }
+  } else {
+    for (int64_t i = lane; i < I; i += 64) {
+      float a = row[i];
+      c += a * cr[i];
+      nrm += rad ? fabsf(a) * rad[d * I + i] : fabsf(a);
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    c += __shfl_xor(c, off, 64);
+    nrm += __shfl_xor(nrm, off, 64);
+  }
+  if (lane == 0) {
+    float dev = eps * nrm;
+    float v = is_lower ? c - dev : c + dev;
+    out[m] = b ? v + b[m] : v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Branching heuristic update for one ReLU layer (alpha_beta_crown.py:145-182):
+// per domain, widest ambiguous neuron (first index on ties); replaces the
+// running best only when strictly wider (earlier layers win ties).
+__global__ void branch_update_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int64_t D,
+                                     int64_t N, int layer, float* __restrict__ best_gap, int* __restrict__ best_layer,
+                                     int* __restrict__ best_idx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t d = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (d >= D) return;
+  float g = -INFINITY;
+  int idx = 0;
+  bool any = false;
+  for (int64_t n = lane; n < N; n += 64) {
+    float l = lo[d * N + n], u = hi[d * N + n];
+    bool amb = (l < 0.f) && (u > 0.f);
+    if (amb) {
+      any = true;
+      float gap = fmaxf(u - l, 0.f);
+      if (gap > g) {
+        g = gap;
+        idx = (int)n;
+      }
+    }
+  }
+  // reduce (max gap, then min index)
+  for (int off = 32; off >= 1; off >>= 1) {
+    float og = __shfl_xor(g, off, 64);
+    int oi = __shfl_xor(idx, off, 64);
+    int oa = __shfl_xor((int)any, off, 64);
+    if (oa) {
+      if (!any || og > g || (og == g && oi < idx)) {
+        g = og;
+        idx = oi;
+      }
+      any = true;
+    }
+  }
+  if (lane == 0 && any) {
+    if (g > best_gap[d]) {
+      best_gap[d] = g;
+      best_layer[d] = layer;
+      best_idx[d] = idx;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// torch.optim.Adam step (defaults: no weight decay, no amsgrad) followed by
+// clamp_(lo, hi), applied in place.  Matches the single-tensor update order:
+//   m = lerp(m, g, 1 - b1); v = v * b2 + (1 - b2) * g * g;
+//   p -= (lr / (1 - b1^t)) * m / (sqrt(v) / sqrt(1 - b2^t) + eps)
+__global__ void adam_clamp_kernel(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
+                                  const float* __restrict__ g, int64_t n, float w1, float b2, float w2, float eps,
+                                  float neg_step, float bc2_sqrt, float lo, float hi, int clamp_hi) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float gi = g[i];
+  float mi = m[i];
+  // exp_avg.lerp_(grad, 1 - beta1): torch's vectorized CPU lerp is fma(w, g - m, m) for w < 0.5
+  mi = (w1 < 0.5f) ? fmaf(w1, gi - mi, mi) : fmaf(w1 - 1.0f, gi - mi, gi);
+  float vi = v[i] * b2;                                                       // exp_avg_sq.mul_(beta2)
+  vi = vi + w2 * gi * gi;                                                     //   .addcmul_(g, g, 1 - beta2)
+  m[i] = mi;
+  v[i] = vi;
+  const float denom = sqrtf(vi) / bc2_sqrt + eps;                             // (sqrt(v) / bc2_sqrt).add_(eps)
+  float pi = p[i] + neg_step * mi / denom;                                    // addcdiv_(m, denom, -step_size)
+  pi = fmaxf(pi, lo);
+  if (clamp_hi) pi = fminf(pi, hi);
+  p[i] = pi;
+}
+
+}  // namespace bf
+
+using namespace bf;
+
+extern "C" {
+
+int bf_abi_version(void) { return 1; }
+
+const char* bf_last_error(void) { return g_err; }
+
+int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, int abs_b, float* C, int64_t ldc,
+            int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  BF_REQUIRE(M >= 0 && N >= 0 && K >= 0, "bf_gemm: negative size");
+  if (M == 0 || N == 0) return BF_OK;
+  BF_REQUIRE(A && B && C, "bf_gemm: null pointer");
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A[0] = A;
+  a.C[0] = C;
+  a.lda = lda;
+  a.lda_d = lda;
+  a.ldc = ldc;
+  a.B = B;
+  a.ldb = ldb;
+  a.trans_b = trans_b;
+  a.abs_b = abs_b;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.S = 1;
+  return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, 1, stream);
+}
+
+int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
+                             const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
+                             const float* add_l, int64_t add_ld, const float* W, int64_t P, const float* bias,
+                             const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
+                             float* b_u_out, float* b_l_out, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && P > 0, "bf_crown_relu_linear_fwd: bad sizes");
+  const int64_t M = D * S;
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(W && ((pre_lo == nullptr) == (pre_hi == nullptr)), "bf_crown_relu_linear_fwd: null weight or half a pre-bound");
+  BF_REQUIRE((A_u != nullptr) == (A_prev_u != nullptr) && (A_l != nullptr) == (A_prev_l != nullptr),
+             "bf_crown_relu_linear_fwd: input/output pointer mismatch");
+  BF_REQUIRE(A_u || A_l, "bf_crown_relu_linear_fwd: no coefficient");
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  int nz = 0;
+  // z order: upper first when present
+  if (A_u) {
+    a.A[nz] = A_u; a.C[nz] = A_prev_u; a.b_in[nz] = b_u_in; a.b_out[nz] = b_u_out; ++nz;
+  }
+  if (A_l) {
+    a.A[nz] = A_l; a.C[nz] = A_prev_l; a.b_in[nz] = b_l_in; a.b_out[nz] = b_l_out; ++nz;
+  }
+  a.z_lower_first = (A_u == nullptr) ? 1 : 0;
+  a.lda = N;
+  a.lda_d = a_dstride;
+  a.ldc = P;
+  a.B = W;
+  a.ldb = P;
+  a.trans_b = 0;
+  a.M = M;
+  a.N = P;
+  a.K = N;
+  a.S = S;
+  a.pre_lo = pre_lo;
+  a.pre_hi = pre_hi;
+  a.ld_pre = N;
+  a.alpha = alpha;
+  a.alpha_ld = alpha_ld;
+  a.add_l = add_l;
+  a.add_ld = add_ld;
+  a.kbias = bias;
+  return gemm_dispatch(a, PRO_RELAX, EPI_STORE, nz, stream);
+}
+
+int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
+                                    const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
+                                    const float* add_l, int64_t add_ld, const float* W, int64_t I,
+                                    const float* bias, const float* cvec, const float* rad, float eps,
+                                    const float* b_u_in, const float* b_l_in, float* workspace, float* lb,
+                                    float* ub, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize: bad sizes");
+  const int64_t M = D * S;
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(W && cvec && workspace && ((pre_lo == nullptr) == (pre_hi == nullptr)),
+             "bf_crown_relu_linear_concretize: null pointer");
+  BF_REQUIRE((A_u != nullptr) == (ub != nullptr) && (A_l != nullptr) == (lb != nullptr),
+             "bf_crown_relu_linear_concretize: input/output pointer mismatch");
+  const int nparts = gemm_partial_count(I);
+  // workspace layout: partial_u [nparts*M], partial_l [nparts*M], cen_u [M], cen_l [M], bout_u [M], bout_l [M]
+  float* pu = workspace;
+  float* pl = pu + (int64_t)nparts * M;
+  float* cu = pl + (int64_t)nparts * M;
+  float* cl = cu + M;
+  float* bu = cl + M;
+  float* bl = bu + M;
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  int nz = 0;
+  if (A_u) {
+    a.A[nz] = A_u; a.b_in[nz] = b_u_in; a.b_out[nz] = bu; a.c_out[nz] = cu; a.partial[nz] = pu; ++nz;
+  }
+  if (A_l) {
+    a.A[nz] = A_l; a.b_in[nz] = b_l_in; a.b_out[nz] = bl; a.c_out[nz] = cl; a.partial[nz] = pl; ++nz;
+  }
+  a.z_lower_first = (A_u == nullptr) ? 1 : 0;
+  a.lda = N;
+  a.lda_d = a_dstride;
+  a.B = W;
+  a.ldb = I;
+  a.M = M;
+  a.N = I;
+  a.K = N;
+  a.S = S;
+  a.pre_lo = pre_lo;
+  a.pre_hi = pre_hi;
+  a.ld_pre = N;
+  a.alpha = alpha;
+  a.alpha_ld = alpha_ld;
+  a.add_l = add_l;
+  a.add_ld = add_ld;
+  a.kbias = bias;
+  a.cvec = cvec;
+  a.cvec_ld = N;
+  a.wvec = rad;
+  a.w_ld = I;
+  int rc = gemm_dispatch(a, PRO_RELAX, EPI_ABSSUM, nz, stream);
+  if (rc) return rc;
+  return concretize_finalize(pu, pl, nparts, M, cu, cl, bu, bl, rad ? 1.0f : eps, lb, ub, stream);
+}
+
+int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
+  const int64_t M = D * S;
+  return (2 * (int64_t)gemm_partial_count(I) + 4) * M;
+}
+
+int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* pre_lo,
+                        const float* pre_hi, const float* alpha, int64_t alpha_ld, const float* add_l,
+                        int64_t add_ld, const float* kbias, const float* b_u_in, const float* b_l_in,
+                        float* A_u_out, float* A_l_out, float* b_u_out, float* b_l_out, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S >= 0 && K > 0, "bf_crown_relu_relax: bad sizes");
+  const int64_t M = D * S;
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(pre_lo && pre_hi, "bf_crown_relu_relax: null pre-bounds");
+  BF_REQUIRE((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr),
+             "bf_crown_relu_relax: input/output mismatch");
+  hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l, M, S,
+                     K, pre_lo, pre_hi, alpha, alpha_ld, add_l, add_ld, kbias, b_u_in, b_l_in, A_u_out, A_l_out,
+                     b_u_out, b_l_out);
+  BF_LAUNCH_CHECK("relu_relax_rows_kernel");
+  return BF_OK;
+}
+
+int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
+                        float eps, const float* b, int is_lower, float* out, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S >= 0 && I > 0, "bf_concretize_dense: bad sizes");
+  const int64_t M = D * S;
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(A && center && out, "bf_concretize_dense: null pointer");
+  BF_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)center % 16) == 0, "bf_concretize_dense: unaligned");
+  hipLaunchKernelGGL(concretize_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A, M, S, I,
+                     center, rad, rad ? 1.0f : eps, b, is_lower, out);
+  BF_LAUNCH_CHECK("concretize_rows_kernel");
+  return BF_OK;
+}
+
+int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, int input_kind, float eps,
+                  int apply_relu, const float* W, const float* bias, int64_t N, const int8_t* split, int64_t split_ld,
+                  float* workspace, float* out_lo, float* out_hi, float* center_out, int* infeasible,
+                  hipStream_t stream) {
+  // input_kind 0: interval [in_lo, in_hi] (optionally through ReLU) or box; 1: Linf ball around in_lo
+  BF_REQUIRE(B >= 0 && K > 0 && N > 0, "bf_ibp_linear: bad sizes");
+  if (B == 0) return BF_OK;
+  BF_REQUIRE(in_lo && W && out_lo && out_hi && workspace, "bf_ibp_linear: null pointer");
+  // workspace: mid [B*K], rad [B*K], c [B*N], r [B*N], rownorm [N]
+  float* mid = workspace;
+  float* rad = mid + B * K;
+  float* c = rad + B * K;
+  float* r = c + B * N;
+  float* rownorm = r + B * N;
+  int rc;
+  if (input_kind == 1) {
+    float* cdst = center_out ? center_out : c;
+    rc = bf_gemm(in_lo, K, W, K, 1, 0, cdst, N, B, N, K, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(row_abs_sum_kernel, dim3((unsigned)N), dim3(256), 0, stream, W, N, K, rownorm);
+    BF_LAUNCH_CHECK("row_abs_sum_kernel");
+    hipLaunchKernelGGL(ibp_finalize_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, cdst,
+                       (const float*)nullptr, rownorm, eps, bias, split, split_ld, B, N, out_lo, out_hi, infeasible);
+    BF_LAUNCH_CHECK("ibp_finalize_kernel");
+    return BF_OK;
+  }
+  BF_REQUIRE(in_hi, "bf_ibp_linear: interval input needs in_hi");
+  hipLaunchKernelGGL(ibp_center_radius_kernel, dim3((unsigned)ceil_div(B * K, 256)), dim3(256), 0, stream, in_lo,
+                     in_hi, B * K, apply_relu, mid, rad);
+  BF_LAUNCH_CHECK("ibp_center_radius_kernel");
+  float* cdst = center_out ? center_out : c;
+  rc = bf_gemm(mid, K, W, K, 1, 0, cdst, N, B, N, K, stream);
+  if (rc) return rc;
+  rc = bf_gemm(rad, K, W, K, 1, 1, r, N, B, N, K, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(ibp_finalize_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, cdst, r,
+                     (const float*)nullptr, 0.f, bias, split, split_ld, B, N, out_lo, out_hi, infeasible);
+  BF_LAUNCH_CHECK("ibp_finalize_kernel");
+  return BF_OK;
+}
+
+int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) { return 2 * B * K + 2 * B * N + N; }
+
+int bf_interval_clip(float* lo, float* hi, const float* clo, const float* chi, const int8_t* split, int64_t split_ld,
+                     int64_t B, int64_t N, int* infeasible, hipStream_t stream) {
+  BF_REQUIRE(B >= 0 && N >= 0, "bf_interval_clip: bad sizes");
+  if (B * N == 0) return BF_OK;
+  BF_REQUIRE(lo && hi && ((clo == nullptr) == (chi == nullptr)), "bf_interval_clip: null pointer");
+  hipLaunchKernelGGL(interval_clip_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, lo, hi, clo,
+                     chi, split, split_ld, B, N, infeasible);
+  BF_LAUNCH_CHECK("interval_clip_kernel");
+  return BF_OK;
+}
+
+int bf_branch_update(const float* lo, const float* hi, int64_t D, int64_t N, int layer, float* best_gap,
+                     int* best_layer, int* best_idx, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && N >= 0, "bf_branch_update: bad sizes");
+  if (D == 0 || N == 0) return BF_OK;
+  BF_REQUIRE(lo && hi && best_gap && best_layer && best_idx, "bf_branch_update: null pointer");
+  hipLaunchKernelGGL(branch_update_kernel, dim3((unsigned)ceil_div(D, 4)), dim3(256), 0, stream, lo, hi, D, N, layer,
+                     best_gap, best_layer, best_idx);
+  BF_LAUNCH_CHECK("branch_update_kernel");
+  return BF_OK;
+}
+
+int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, double lr, double beta1,
+                       double beta2, float eps, int step, float clamp_lo, float clamp_hi, int has_clamp_hi,
+                       hipStream_t stream) {
+  BF_REQUIRE(n >= 0 && step >= 1, "bf_adam_clamp_step: bad arguments");
+  if (n == 0) return BF_OK;
+  BF_REQUIRE(p && m && v && g, "bf_adam_clamp_step: null pointer");
+  // bias corrections in double then rounded, as torch computes them from Python floats
+  const double bc1 = 1.0 - __builtin_pow((double)beta1, (double)step);
+  const double bc2 = 1.0 - __builtin_pow((double)beta2, (double)step);
+  const float neg_step = (float)(-((double)lr / bc1));
+  const float bc2_sqrt = (float)__builtin_sqrt(bc2);
+  const float w1 = (float)(1.0 - (double)beta1);
+  const float w2 = (float)(1.0 - (double)beta2);
+  hipLaunchKernelGGL(adam_clamp_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, p, m, v, g, n, w1,
+                     beta2, w2, eps, neg_step, bc2_sqrt, clamp_lo, clamp_hi, has_clamp_hi);
+  BF_LAUNCH_CHECK("adam_clamp_kernel");
+  return BF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,67 @@
+"""Optional per-launch timing of the library's kernels with HIP events.
+
+When a ``LaunchTimer`` is active, the host driver brackets each launch of the
+named kernel families with ``torch.cuda.Event`` records on the stream the
+kernel is launched on (the caller's current stream), together with the
+algorithmic flop and byte counts of that launch.  Nothing is synchronized
+until ``summary()`` is called.
+"""
+
+from __future__ import annotations
+
+from collections import defaultdict
+from contextlib import contextmanager
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+_active: Optional["LaunchTimer"] = None
+
+
+class LaunchTimer:
+    def __init__(self) -> None:
+        self.records: List[Tuple[str, float, float, torch.cuda.Event, torch.cuda.Event]] = []
+
+    def summary(self) -> Dict[str, Dict[str, float]]:
+        torch.cuda.synchronize()
+        agg: Dict[str, Dict[str, float]] = defaultdict(lambda: {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+        for name, flops, nbytes, s, e in self.records:
+            a = agg[name]
+            a["launches"] += 1
+            a["ms"] += s.elapsed_time(e)
+            a["flops"] += flops
+            a["bytes"] += nbytes
+        out = {}
+        for name, a in agg.items():
+            sec = a["ms"] / 1e3
+            out[name] = dict(a)
+            out[name]["avg_ms"] = a["ms"] / max(1, a["launches"])
+            out[name]["tflops"] = a["flops"] / sec / 1e12 if sec > 0 else 0.0
+            out[name]["gbps"] = a["bytes"] / sec / 1e9 if sec > 0 else 0.0
+        return out
+
+
+@contextmanager
+def timing(timer: LaunchTimer):
+    global _active
+    prev = _active
+    _active = timer
+    try:
+        yield timer
+    finally:
+        _active = prev
+
+
+@contextmanager
+def launch(name: str, flops: float, nbytes: float):
+    """Bracket one launch (no-op unless a LaunchTimer is active)."""
+    t = _active
+    if t is None:
+        yield
+        return
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    yield
+    e.record()
+    t.records.append((name, float(flops), float(nbytes), s, e))

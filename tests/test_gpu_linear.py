@@ -1,0 +1,235 @@
+"""HIP parity tests for the linear (MLP) CROWN path, checked against the CPU
+oracle and the reference-generated golden vectors."""
+
+import pytest
+import torch
+
+from boundflow_amd import _lib
+from boundflow_amd import crown as hc
+from boundflow_amd import workloads as wl
+from oracle import alpha_beta_ref as ab
+from oracle import crown_ref as cr
+from tests.golden_util import load, t
+from tests.gpu_util import announce, assert_bounds_close, contraction_tol, device
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,N,K,trans_b,abs_b", [
+    (37, 19, 5, 0, 0), (128, 128, 16, 0, 0), (300, 257, 130, 1, 0), (576, 784, 256, 0, 0),
+    (1000, 500, 500, 1, 1), (9, 10, 10, 0, 0),
+])
+def test_gemm_matches_fp64(M, N, K, trans_b, abs_b):
+    dev = device()
+    announce(f"gemm M={M} N={N} K={K} trans_b={trans_b} abs_b={abs_b}")
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(N, K, generator=g) if trans_b else torch.randn(K, N, generator=g)
+    Bm = B.t() if trans_b else B
+    if abs_b:
+        Bm = Bm.abs()
+    ref = A.double() @ Bm.double()
+    C = torch.empty(M, N, device=dev)
+    Ad, Bd = A.to(dev), B.to(dev)
+    _lib.call("bf_gemm", _lib.ptr(Ad), K, _lib.ptr(Bd), (K if trans_b else N), trans_b, abs_b, _lib.ptr(C), N,
+              M, N, K, _lib.stream_handle())
+    torch.cuda.synchronize()
+    tol = contraction_tol(A, Bm, K) + 1e-30
+    err = (C.cpu().double() - ref).abs()
+    assert bool((err <= tol).all()), float((err / tol).max())
+
+
+def test_fused_relu_linear_region_golden():
+    dev = device()
+    announce("fused relu+linear region vs reference fixture")
+    gz = load("fused_linear")
+    A_u, A_l = t(gz["A_u"]), t(gz["A_l"])
+    D, S, N = A_u.shape
+    W = t(gz["weight"])
+    P = int(W.shape[1])
+    outs = [torch.empty(D * S, P, device=dev), torch.empty(D * S, P, device=dev),
+            torch.empty(D * S, device=dev), torch.empty(D * S, device=dev)]
+    args = [x.to(dev).contiguous() for x in (A_u, A_l, t(gz["l"]), t(gz["u"]), W, t(gz["bias"]))]
+    _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(args[0]), _lib.ptr(args[1]), S * N, D, S, N, _lib.ptr(args[2]),
+              _lib.ptr(args[3]), None, 0, None, 0, _lib.ptr(args[4]), P, _lib.ptr(args[5]), None, None,
+              _lib.ptr(outs[0]), _lib.ptr(outs[1]), _lib.ptr(outs[2]), _lib.ptr(outs[3]), _lib.stream_handle())
+    torch.cuda.synchronize()
+    assert_bounds_close(outs[0].reshape(D, S, P), t(gz["A_prev_u"]), "A_prev_u", rtol=1e-5, atol=1e-5)
+    assert_bounds_close(outs[1].reshape(D, S, P), t(gz["A_prev_l"]), "A_prev_l", rtol=1e-5, atol=1e-5)
+    assert_bounds_close(outs[2].reshape(D, S), t(gz["bias_delta_u"]), "bias_delta_u", rtol=1e-5, atol=1e-5)
+    assert_bounds_close(outs[3].reshape(D, S), t(gz["bias_delta_l"]), "bias_delta_l", rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("tag,maker", [
+    ("crown_c1", lambda: wl.make_c1()),
+    ("crown_c1_mixed", lambda: wl.make_c1(eps=0.001, label_mode="predicted")),
+])
+def test_crown_mlp_matches_reference(tag, maker):
+    dev = device()
+    announce(f"run_crown_ibp_mlp {tag}")
+    gz = load(tag)
+    w = maker()
+    wd = wl.to_device(w, dev)
+    trace = hc.forward_ibp_trace(wd.module, wd.spec)
+    # Intermediate IBP boxes: the reference sums l.W+ and u.W- separately (cancellation near 0),
+    # the HIP path uses the center/radius form; both carry fp32 rounding of the summed terms, so
+    # near-zero entries are compared with an absolute floor of 1e-5.
+    for i, st in enumerate(trace.relu_pre.values()):
+        n = gz[f"pre{i}_lower"].shape[0]
+        assert_bounds_close(st.lower[:n], t(gz[f"pre{i}_lower"]), f"{tag} relu_pre[{i}].lower", atol=1e-5)
+        assert_bounds_close(st.upper[:n], t(gz[f"pre{i}_upper"]), f"{tag} relu_pre[{i}].upper", atol=1e-5)
+    b = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+    torch.cuda.synchronize()
+    assert_bounds_close(b.lower, t(gz["lower"]), f"{tag} lower")
+    assert_bounds_close(b.upper, t(gz["upper"]), f"{tag} upper")
+    v_gpu = (b.lower.cpu().min(1).values >= 0)
+    v_ref = (t(gz["lower"]).min(1).values >= 0)
+    announce(f"{tag}: certified gpu={int(v_gpu.sum())} ref={int(v_ref.sum())}")
+    assert torch.equal(v_gpu, v_ref)
+
+
+def test_crown_mlp_with_splits_matches_oracle():
+    dev = device()
+    announce("run_crown_ibp_mlp with per-domain splits (C5 network, 64 domains)")
+    w = wl.subset(wl.make_c5(eps=0.004, depth=2, label_mode="predicted"), 64)
+    feas = ab.domain_feasible(w.module, w.spec, w.extra["splits"])
+    idx = feas.nonzero().flatten()
+    w = wl.Workload(w.name, w.module,
+                    type(w.spec)(value_name="input", center=w.spec.center[idx], perturbation=w.spec.perturbation),
+                    w.C[idx], w.labels[idx], {"splits": {k: v[idx] for k, v in w.extra["splits"].items()}})
+    ref = cr.run_crown_ibp(w.module, w.spec, linear_spec_C=w.C, relu_split_state=w.extra["splits"])
+    wd = wl.to_device(w, dev)
+    b = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state=wd.extra["splits"])
+    assert_bounds_close(b.lower, ref.lower, "split lower")
+    assert_bounds_close(b.upper, ref.upper, "split upper")
+
+
+def test_infeasible_split_raises_and_flags():
+    dev = device()
+    announce("infeasible split -> ValueError / per-domain flag")
+    w = wl.subset(wl.make_c5(), 8)
+    wd = wl.to_device(w, dev)
+    names = wl.relu_input_names(w.module)
+    trace = hc.forward_ibp_trace(wd.module, wd.spec, raise_on_infeasible=False)
+    # force domain 3 to split a stably-inactive neuron active
+    u = trace.relu_pre[names[0]].upper[3].cpu()
+    j = int(torch.argmin(u))
+    assert float(u[j]) < 0
+    split = {k: v.clone() for k, v in wd.extra["splits"].items()}
+    split[names[0]][3, j] = 1
+    tr = hc.forward_ibp_trace(wd.module, wd.spec, relu_split_state=split, raise_on_infeasible=False)
+    flags = tr.infeasible.cpu()
+    assert int(flags[3]) == 1
+    with pytest.raises(ValueError):
+        hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state=split)
+
+
+def test_all_intermediate_c2_matches_reference():
+    dev = device()
+    announce("C2 all-intermediate CROWN, B=4")
+    gz = load("crown_c2_allint_b4")
+    w = wl.subset(wl.make_c2(), 4)
+    wd = wl.to_device(w, dev)
+    final, pre = hc.run_crown_all_intermediate(wd.module, wd.spec, linear_spec_C=wd.C)
+    for i, st in enumerate(pre.values()):
+        assert_bounds_close(st.lower, t(gz[f"pre{i}_lower"]), f"C2 pre{i} lower", rtol=1e-5, atol=1e-5)
+        assert_bounds_close(st.upper, t(gz[f"pre{i}_upper"]), f"C2 pre{i} upper", rtol=1e-5, atol=1e-5)
+    assert_bounds_close(final.lower, t(gz["lower"]), "C2 lower")
+    assert_bounds_close(final.upper, t(gz["upper"]), "C2 upper")
+
+
+def test_relax_pass_and_dense_concretize_match_oracle():
+    dev = device()
+    announce("standalone relax pass + dense concretize")
+    g = torch.Generator().manual_seed(11)
+    D, S, K = 5, 7, 133
+    A_u = torch.randn(D, S, K, generator=g)
+    A_l = torch.randn(D, S, K, generator=g)
+    A_u[0, 0, :4] = torch.tensor([0.0, -0.0, 1.0, -1.0])
+    l = torch.randn(D, K, generator=g)
+    u = l + torch.rand(D, K, generator=g)
+    l[0, :3] = torch.tensor([0.0, -1.0, 0.0])
+    u[0, :3] = torch.tensor([0.0, 0.0, 1.0])
+    alpha = torch.rand(D, K, generator=g) * 1.4 - 0.2
+    add = torch.randn(D, K, generator=g)
+    bu, bl = torch.randn(D, S, generator=g), torch.randn(D, S, generator=g)
+    pre = cr.IntervalState(l, u)
+    ref = cr.relu_backward_dense(A_u, A_l, bu, bl, pre=pre, name="h", relu_alpha={"h": alpha},
+                                 add_l={"h": add})
+    d = [x.to(dev).contiguous() for x in (A_u, A_l, l, u, alpha, add, bu, bl)]
+    out = [torch.empty(D * S, K, device=dev), torch.empty(D * S, K, device=dev), torch.empty(D * S, device=dev),
+           torch.empty(D * S, device=dev)]
+    _lib.call("bf_crown_relu_relax", _lib.ptr(d[0]), _lib.ptr(d[1]), D, S, K, _lib.ptr(d[2]), _lib.ptr(d[3]),
+              _lib.ptr(d[4]), K, _lib.ptr(d[5]), K, None, _lib.ptr(d[6]), _lib.ptr(d[7]), _lib.ptr(out[0]),
+              _lib.ptr(out[1]), _lib.ptr(out[2]), _lib.ptr(out[3]), _lib.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(out[0].cpu().reshape(D, S, K), ref[0])
+    assert torch.equal(out[1].cpu().reshape(D, S, K), ref[1])
+    assert_bounds_close(out[2].reshape(D, S), ref[2], "relax b_u")
+    assert_bounds_close(out[3].reshape(D, S), ref[3], "relax b_l")
+    # dense Linf concretize of A_l
+    x0 = torch.rand(D, K, generator=g)
+    spec = cr.InputSpec.linf(value_name="input", center=x0, eps=0.05)
+    lb_ref, ub_ref = cr.concretize_affine(spec, x0, cr.DenseOp(ref[1], (K,)), ref[3])
+    lb = torch.empty(D * S, device=dev)
+    xd = x0.to(dev).contiguous()
+    Al = ref[1].to(dev).contiguous()
+    bld = ref[3].to(dev).contiguous()
+    _lib.call("bf_concretize_dense", _lib.ptr(Al), D, S, K, _lib.ptr(xd), None, 0.05, _lib.ptr(bld), 1,
+              _lib.ptr(lb), _lib.stream_handle())
+    torch.cuda.synchronize()
+    assert_bounds_close(lb.reshape(D, S), lb_ref, "concretize lb")
+
+
+def test_branch_update_matches_oracle():
+    dev = device()
+    announce("branch argmax update")
+    g = torch.Generator().manual_seed(4)
+    pre = {}
+    for name, n in (("a", 70), ("b", 130)):
+        l = torch.randn(33, n, generator=g)
+        u = l + torch.rand(33, n, generator=g) * 2
+        pre[name] = cr.IntervalState(l, u)
+    # exact ties: row 0 -> two equal gaps inside "a", row 1 -> equal best gap in "a" and "b"
+    pre["a"].lower[0, 5], pre["a"].upper[0, 5] = -3.0, 3.0
+    pre["a"].lower[0, 9], pre["a"].upper[0, 9] = -2.0, 4.0
+    pre["a"].lower[1, 2], pre["a"].upper[1, 2] = -4.0, 4.0
+    pre["b"].lower[1, 1], pre["b"].upper[1, 1] = -5.0, 3.0
+    pre["b"].lower[2] = 1.0  # no ambiguous neuron in layer b for row 2
+    ref = ab.branch_choices(pre)
+    gap = torch.full((33,), float("-inf"), device=dev)
+    lay = torch.full((33,), -1, dtype=torch.int32, device=dev)
+    idx = torch.zeros(33, dtype=torch.int32, device=dev)
+    for li, (name, st) in enumerate(pre.items()):
+        lo, hi = st.lower.to(dev).contiguous(), st.upper.to(dev).contiguous()
+        _lib.call("bf_branch_update", _lib.ptr(lo), _lib.ptr(hi), 33, int(lo.shape[1]), li, _lib.ptr(gap),
+                  _lib.ptr(lay), _lib.ptr(idx), _lib.stream_handle())
+    names = list(pre.keys())
+    got = [None if int(a) < 0 else (names[int(a)], int(b)) for a, b in zip(lay.cpu(), idx.cpu())]
+    assert got == ref
+
+
+def test_adam_clamp_matches_torch():
+    dev = device()
+    announce("adam + clamp step")
+    g = torch.Generator().manual_seed(9)
+    p0 = torch.rand(1000, generator=g)
+    p = p0.clone().requires_grad_(True)
+    opt = torch.optim.Adam([p], lr=0.2)
+    pd = p0.to(dev).contiguous()
+    m = torch.zeros_like(pd)
+    v = torch.zeros_like(pd)
+    for step in range(1, 6):
+        grad = torch.randn(1000, generator=g) * (10.0 ** (step - 3))
+        grad[:5] = 0.0
+        opt.zero_grad()
+        p.grad = grad.clone()
+        opt.step()
+        with torch.no_grad():
+            p.clamp_(0.0, 1.0)
+        gd = grad.to(dev).contiguous()
+        _lib.call("bf_adam_clamp_step", _lib.ptr(pd), _lib.ptr(m), _lib.ptr(v), _lib.ptr(gd), 1000, 0.2, 0.9, 0.999,
+                  1e-8, step, 0.0, 1.0, 1, _lib.stream_handle())
+        torch.cuda.synchronize()
+        # torch's CPU kernels mix fused and unfused multiply-adds; agree to a few ulps
+        assert torch.allclose(pd.cpu(), p.detach(), rtol=1e-6, atol=1e-7), float((pd.cpu() - p.detach()).abs().max())
