@@ -65,3 +65,27 @@ def launch(name: str, flops: float, nbytes: float):
     yield
     e.record()
     t.records.append((name, float(flops), float(nbytes), s, e))
+
+
+def summarize_rocpd(db_path: str, top: int = 12) -> str:
+    """Per-kernel dispatch count / average / total duration from a rocprofv3
+    ``*_results.db`` (kernel-trace run), as a Markdown table."""
+    import sqlite3
+
+    con = sqlite3.connect(db_path)
+    q = ("select s.kernel_name, count(*), avg(d.end - d.start), sum(d.end - d.start) "
+         "from rocpd_kernel_dispatch d join rocpd_info_kernel_symbol s on d.kernel_id = s.id "
+         "group by s.kernel_name order by 4 desc")
+    rows = list(con.execute(q))
+    total = sum(r[3] for r in rows) or 1
+    out = ["| kernel | calls | avg (us) | total (ms) | share |", "|---|---:|---:|---:|---:|"]
+    for name, n, avg, tot in rows[:top]:
+        out.append(f"| `{name.removesuffix('.kd')}` | {n} | {avg / 1e3:.2f} | {tot / 1e6:.3f} | "
+                   f"{100.0 * tot / total:.1f}% |")
+    return "\n".join(out)
+
+
+if __name__ == "__main__":
+    import sys
+
+    print(summarize_rocpd(sys.argv[1]))

@@ -45,3 +45,20 @@ def assert_bounds_close(got: torch.Tensor, ref: torch.Tensor, what: str, rtol: f
 def contraction_tol(a: torch.Tensor, b: torch.Tensor, k: int) -> torch.Tensor:
     """fp32 accumulation error bound for C = a @ b: k * 2^-23 * (|a| @ |b|)."""
     return k * (2.0 ** -23) * (a.abs().double() @ b.abs().double())
+
+
+def assert_parity(got, ref32, ref64, what: str):
+    """Contract tolerance, with fp32-cancellation mismatches accepted only when
+    the fp64 oracle shows the HIP value is as close to exact as the reference."""
+    from oracle import parity
+    rep = parity.compare(got, ref32, ref64)
+    announce(rep.line(what))
+    assert rep.ok, rep.line(what)
+    return rep
+
+
+def assert_verdicts(got_lower, ref32_lower, ref64_lower, what: str):
+    from oracle import parity
+    mism, ties_flipped, ties = parity.verdict_parity(got_lower, ref32_lower, ref64_lower)
+    announce(f"{what}: verdict mismatches={mism} near-tie flips={ties_flipped} near-ties={ties}")
+    assert mism == 0, f"{what}: {mism} verdict mismatches"

@@ -10,7 +10,8 @@ from boundflow_amd import workloads as wl
 from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
 from tests.golden_util import load, t
-from tests.gpu_util import announce, assert_bounds_close, contraction_tol, device
+from oracle import parity
+from tests.gpu_util import announce, assert_bounds_close, assert_parity, assert_verdicts, contraction_tol, device
 
 pytestmark = pytest.mark.gpu
 
@@ -80,12 +81,11 @@ def test_crown_mlp_matches_reference(tag, maker):
         assert_bounds_close(st.upper[:n], t(gz[f"pre{i}_upper"]), f"{tag} relu_pre[{i}].upper", atol=1e-5)
     b = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
     torch.cuda.synchronize()
-    assert_bounds_close(b.lower, t(gz["lower"]), f"{tag} lower")
-    assert_bounds_close(b.upper, t(gz["upper"]), f"{tag} upper")
-    v_gpu = (b.lower.cpu().min(1).values >= 0)
-    v_ref = (t(gz["lower"]).min(1).values >= 0)
-    announce(f"{tag}: certified gpu={int(v_gpu.sum())} ref={int(v_ref.sum())}")
-    assert torch.equal(v_gpu, v_ref)
+    w64 = parity.to_float64(w)
+    ref64 = cr.run_crown_ibp(w64.module, w64.spec, linear_spec_C=w64.C)
+    assert_parity(b.lower, t(gz["lower"]), ref64.lower, f"{tag} lower")
+    assert_parity(b.upper, t(gz["upper"]), ref64.upper, f"{tag} upper")
+    assert_verdicts(b.lower, t(gz["lower"]), ref64.lower, tag)
 
 
 def test_crown_mlp_with_splits_matches_oracle():
@@ -98,10 +98,13 @@ def test_crown_mlp_with_splits_matches_oracle():
                     type(w.spec)(value_name="input", center=w.spec.center[idx], perturbation=w.spec.perturbation),
                     w.C[idx], w.labels[idx], {"splits": {k: v[idx] for k, v in w.extra["splits"].items()}})
     ref = cr.run_crown_ibp(w.module, w.spec, linear_spec_C=w.C, relu_split_state=w.extra["splits"])
+    w64 = parity.to_float64(w)
+    ref64 = cr.run_crown_ibp(w64.module, w64.spec, linear_spec_C=w64.C, relu_split_state=w64.extra["splits"])
     wd = wl.to_device(w, dev)
     b = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state=wd.extra["splits"])
-    assert_bounds_close(b.lower, ref.lower, "split lower")
-    assert_bounds_close(b.upper, ref.upper, "split upper")
+    assert_parity(b.lower, ref.lower, ref64.lower, "split lower")
+    assert_parity(b.upper, ref.upper, ref64.upper, "split upper")
+    assert_verdicts(b.lower, ref.lower, ref64.lower, "split")
 
 
 def test_infeasible_split_raises_and_flags():
@@ -134,8 +137,10 @@ def test_all_intermediate_c2_matches_reference():
     for i, st in enumerate(pre.values()):
         assert_bounds_close(st.lower, t(gz[f"pre{i}_lower"]), f"C2 pre{i} lower", rtol=1e-5, atol=1e-5)
         assert_bounds_close(st.upper, t(gz[f"pre{i}_upper"]), f"C2 pre{i} upper", rtol=1e-5, atol=1e-5)
-    assert_bounds_close(final.lower, t(gz["lower"]), "C2 lower")
-    assert_bounds_close(final.upper, t(gz["upper"]), "C2 upper")
+    w64 = parity.to_float64(w)
+    ref64, _ = cr.run_crown_all_intermediate(w64.module, w64.spec, linear_spec_C=w64.C)
+    assert_parity(final.lower, t(gz["lower"]), ref64.lower, "C2 lower")
+    assert_parity(final.upper, t(gz["upper"]), ref64.upper, "C2 upper")
 
 
 def test_relax_pass_and_dense_concretize_match_oracle():
