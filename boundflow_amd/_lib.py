@@ -28,18 +28,34 @@ SIGNATURES = {
     "bf_abi_version": (I32, []),
     "bf_last_error": (ctypes.c_char_p, []),
     "bf_gemm": (I32, [P, I64, P, I64, I32, I32, P, I64, I64, I64, I64, P]),
+    "bf_gemm_rank1": (I32, [P, I64, P, I64, I32, P, I64, I64, I64, I64, I64, P, P, I64, P]),
     "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, P, I64, P, P, P, P, P, P, P,
                                        P]),
     "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, P, I64, P, P, P, F32,
-                                              P, P, P, P, P, P]),
+                                              P, P, P, P, P, P, P, P]),
     "bf_crown_relu_linear_concretize_workspace": (I64, [I64, I64, I64]),
-    "bf_crown_relu_relax": (I32, [P, P, I64, I64, I64, P, P, P, I64, P, I64, P, P, P, P, P, P, P, P]),
+    "bf_crown_relu_relax": (I32, [P, P, I64, I64, I64, P, P, P, I64, P, I64, P, P, P, P, P, P, P, P, P, P, P]),
     "bf_concretize_dense": (I32, [P, I64, I64, I64, P, P, F32, P, I32, P, P]),
     "bf_ibp_linear": (I32, [P, P, I64, I64, I32, F32, I32, P, P, I64, P, I64, P, P, P, P, P, P]),
     "bf_ibp_linear_workspace": (I64, [I64, I64, I64]),
     "bf_interval_clip": (I32, [P, P, P, P, P, I64, I64, I64, P, P]),
     "bf_branch_update": (I32, [P, P, I64, I64, I32, P, P, P, P]),
     "bf_adam_clamp_step": (I32, [P, P, P, P, I64, F64, F64, F64, F32, I32, F32, F32, I32, P]),
+    "bf_conv2d_rows": (I32, [P, I64, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P, P,
+                             I64, I64, P]),
+    "bf_conv_transpose_rows": (I32, [P, P, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P,
+                                     I64, P, I64, P, P, P, P, P]),
+    "bf_ibp_conv2d": (I32, [P, P, I64, I32, I32, I32, I32, F32, I32, P, P, I32, I32, I32, I32, I32, I32, I32, I32, I32,
+                            P, I64, P, P, P, P, P, P]),
+    "bf_ibp_conv2d_workspace": (I64, [I64, I64, I64]),
+    "bf_relu_grad": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, P, I64, P, P, P, P]),
+    "bf_beta_coeff": (I32, [P, I64, P, I64, I64, I64, P, P]),
+    "bf_best_update": (I32, [P, P, I64, I64, P, P, P, P, I32, P]),
+    "bf_masked_copy_rows": (I32, [P, P, I64, I64, P, P]),
+    "bf_sum_rows": (I32, [P, I64, I64, P, P]),
+    "bf_concretize_finalize": (I32, [P, P, I32, I64, P, P, P, P, F32, P, P, P]),
+    "bf_alpha_from_crown": (I32, [P, P, I64, P, P]),
+    "bf_domain_status": (I32, [P, I64, I64, P, F32, F32, P, P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -84,7 +100,7 @@ def call(name: str, *args) -> int:
     """Invoke an entry point and raise HipError with bf_last_error() on failure."""
     lib = load()
     rc = getattr(lib, name)(*args)
-    if SIGNATURES[name][0] is I32 and name not in ("bf_abi_version",) and rc != 0:
+    if SIGNATURES[name][0] is I32 and name != "bf_abi_version" and rc != 0:
         msg = lib.bf_last_error().decode(errors="replace")
         raise HipError(f"{name} failed (status {rc}): {msg}")
     return rc

@@ -1,0 +1,363 @@
+"""HIP alpha-CROWN / alpha-beta-CROWN optimisation loop.
+
+Mirrors ``run_alpha_beta_crown_mlp`` (boundflow/runtime/alpha_beta_crown.py:643-941)
+and ``run_alpha_crown_mlp`` (boundflow/runtime/alpha_crown.py:137-261) for the
+"lower" objective with the "mean" spec reduction, the configuration the BaB
+solver uses (boundflow/runtime/bab.py:134-153):
+
+* one forward IBP trace (split-aware), branch choices from it
+  (alpha_beta_crown.py:145-182);
+* ``steps + 1`` bound evaluations; each runs the fused CROWN backward for both
+  bounds and keeps the lower-bound coefficients needed by the gradient;
+* best-of tracking per domain (per_batch_params) or globally;
+* between evaluations, the analytic reverse pass of the lower bound (the
+  gradient autograd computes in the reference): fused concretization seed ->
+  transposed contractions with rank-1 bias terms -> per-ReLU gradient kernels
+  that reduce dL/dalpha and dL/dbeta over the specs;
+* torch.optim.Adam's update (lr, betas 0.9/0.999, eps 1e-8) and the clamps
+  alpha in [0, 1], beta >= 0, applied in place on the device.
+
+The loss is -sum_d mean_s lb (per-domain parameters) or -mean lb (shared), so
+the gradient of every lower bound row is -1/S or -1/(D*S).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+from .crown import (
+    Chain,
+    ForwardTrace,
+    _broadcast_split,
+    _numel,
+    crown_backward,
+    forward_ibp_trace,
+    parse_chain,
+)
+from .profiling import launch as _timed
+from .spec import InputSpec, IntervalState, normalize_input_spec
+
+
+@dataclass
+class AlphaBetaStats:
+    feasibility: str = "unknown"
+    reason: str = "ok"
+    branch_choices: Optional[List[Optional[Tuple[str, int]]]] = None
+    infeasible: Optional[torch.Tensor] = None
+    steps: int = 0
+    lr: float = 0.0
+
+
+class _Adam:
+    """Device-resident Adam state for one parameter tensor."""
+
+    def __init__(self, p: torch.Tensor):
+        self.p = p
+        self.m = torch.zeros_like(p)
+        self.v = torch.zeros_like(p)
+        self.t = 0
+
+    def step(self, grad: torch.Tensor, lr: float, lo: float, hi: Optional[float], stream) -> None:
+        self.t += 1
+        _lib.call("bf_adam_clamp_step", _lib.ptr(self.p), _lib.ptr(self.m), _lib.ptr(self.v), _lib.ptr(grad),
+                  self.p.numel(), float(lr), 0.9, 0.999, 1e-8, self.t, float(lo), float(hi or 0.0),
+                  1 if hi is not None else 0, stream)
+
+
+def branch_choices(trace: ForwardTrace, batch: int) -> List[Optional[Tuple[str, int]]]:
+    """Widest ambiguous neuron per domain (alpha_beta_crown.py:145-182), on the device."""
+    dev = next(iter(trace.relu_pre.values())).lower.device if trace.relu_pre else torch.device("cuda")
+    gap = torch.full((batch,), float("-inf"), device=dev)
+    layer = torch.full((batch,), -1, dtype=torch.int32, device=dev)
+    idx = torch.zeros(batch, dtype=torch.int32, device=dev)
+    names = list(trace.relu_pre.keys())
+    stream = _lib.stream_handle()
+    for li, name in enumerate(names):
+        pre = trace.relu_pre[name]
+        n = int(pre.lower[0].numel())
+        _lib.call("bf_branch_update", _lib.ptr(pre.lower.reshape(batch, n)), _lib.ptr(pre.upper.reshape(batch, n)),
+                  batch, n, li, _lib.ptr(gap), _lib.ptr(layer), _lib.ptr(idx), stream)
+    lay = layer.cpu().tolist()
+    ids = idx.cpu().tolist()
+    return [None if lay[i] < 0 else (names[lay[i]], int(ids[i])) for i in range(batch)]
+
+
+def branch_tensors(trace: ForwardTrace, batch: int):
+    """Device tensors (layer index, neuron index, gap) of the branching rule."""
+    dev = next(iter(trace.relu_pre.values())).lower.device
+    gap = torch.full((batch,), float("-inf"), device=dev)
+    layer = torch.full((batch,), -1, dtype=torch.int32, device=dev)
+    idx = torch.zeros(batch, dtype=torch.int32, device=dev)
+    stream = _lib.stream_handle()
+    for li, (name, pre) in enumerate(trace.relu_pre.items()):
+        n = int(pre.lower[0].numel())
+        _lib.call("bf_branch_update", _lib.ptr(pre.lower.reshape(batch, n)), _lib.ptr(pre.upper.reshape(batch, n)),
+                  batch, n, li, _lib.ptr(gap), _lib.ptr(layer), _lib.ptr(idx), stream)
+    return layer, idx, gap
+
+
+def alpha_from_crown(trace: ForwardTrace) -> Dict[str, torch.Tensor]:
+    """Adaptive lower-slope init (native_alpha_beta_optimizer_schedule.py:635-653)."""
+    out = {}
+    stream = _lib.stream_handle()
+    for name, pre in trace.relu_pre.items():
+        a = torch.empty_like(pre.lower)
+        _lib.call("bf_alpha_from_crown", _lib.ptr(pre.lower), _lib.ptr(pre.upper), pre.lower.numel(), _lib.ptr(a),
+                  stream)
+        out[name] = a
+    return out
+
+
+def _grad_pass(spec: InputSpec, chain: Chain, trace: ForwardTrace, saved: dict, B: int, S: int,
+               alpha: Dict[str, Tuple[torch.Tensor, int]], splits: Dict[str, Tuple[torch.Tensor, int]],
+               G: torch.Tensor) -> Tuple[Dict[str, torch.Tensor], Dict[str, torch.Tensor]]:
+    """Reverse pass of the lower bound; returns dL/dalpha and dL/dbeta per ReLU ([B, n])."""
+    dev = spec.center.device
+    stream = _lib.stream_handle()
+    layers = chain.layers
+    M = B * S
+    g = saved["h"]                       # dL/d(input coefficient)  [M, n_in0]
+    cvec = saved["cvec"]                 # first-layer center projection [B, n_out0]
+    g_alpha: Dict[str, torch.Tensor] = {}
+    g_beta: Dict[str, torch.Tensor] = {}
+    for k in range(0, len(layers) - 1):
+        layer = layers[k]
+        n_out = _numel(layer.out_shape)
+        n_in = _numel(layer.in_shape)
+        # rank-1 term: every row's bias contribution b += A~ . bias_k (and the center term on the input layer)
+        if k == 0:
+            vec = cvec if layer.bias is None else (cvec + _bias_map(layer))
+            vec_ld = n_out
+        else:
+            vec = _bias_map(layer) if layer.bias is not None else None
+            vec_ld = 0
+        gt = torch.empty(M, n_out, device=dev)
+        if layer.kind == "linear":
+            with _timed("grad_gemm", 2.0 * M * n_in * n_out, 4.0 * (M * n_in + M * n_out + n_in * n_out)):
+                _lib.call("bf_gemm_rank1", _lib.ptr(g), n_in, _lib.ptr(layer.weight.contiguous()), n_in, 1,
+                          _lib.ptr(gt), n_out, M, n_out, n_in, S, _lib.ptr(G if vec is not None else None),
+                          _lib.ptr(vec), vec_ld, stream)
+        else:
+            Ci, Hi, Wi = layer.in_shape
+            Co, Ho, Wo = layer.out_shape
+            KH, KW = int(layer.weight.shape[2]), int(layer.weight.shape[3])
+            sh, sw = layer.attrs["stride"]
+            ph, pw = layer.attrs["padding"]
+            with _timed("grad_conv", 2.0 * M * n_out * Ci * KH * KW, 4.0 * (M * n_in + M * n_out)):
+                _lib.call("bf_conv2d_rows", _lib.ptr(g), 1, M, Ci, Hi, Wi, _lib.ptr(layer.weight.contiguous()), 0,
+                          Co, KH, KW, sh, sw, ph, pw, Ho, Wo, _lib.ptr(gt), _lib.ptr(G if vec is not None else None),
+                          _lib.ptr(vec), S if vec_ld else 1, vec_ld, stream)
+        # through the ReLU relaxation of layer k's output
+        name = layer.out_name
+        pre = trace.relu_pre[name]
+        A_in, a_stride = saved["A_in"][k]
+        ga = torch.empty(B, n_out, device=dev)
+        gb = torch.empty(B, n_out, device=dev)
+        a_t, a_ld = alpha.get(name, (None, 0))
+        sp, sp_ld = splits.get(name, (None, 0))
+        g_in = torch.empty(M, n_out, device=dev)
+        with _timed("relu_grad", 0.0, 4.0 * (3 * M * n_out + 4 * B * n_out)):
+            _lib.call("bf_relu_grad", _lib.ptr(gt), _lib.ptr(A_in), a_stride, B, S, n_out,
+                      _lib.ptr(pre.lower.reshape(B, n_out)), _lib.ptr(pre.upper.reshape(B, n_out)), _lib.ptr(a_t),
+                      a_ld, _lib.ptr(G), _lib.ptr(sp), sp_ld, _lib.ptr(g_in), _lib.ptr(ga), _lib.ptr(gb), stream)
+        g_alpha[name] = ga
+        g_beta[name] = gb
+        g = g_in
+    return g_alpha, g_beta
+
+
+def _bias_map(layer) -> torch.Tensor:
+    if layer.kind == "linear":
+        return layer.bias.contiguous()
+    Co, Ho, Wo = layer.out_shape
+    return layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous()
+
+
+def run_alpha_beta_crown_mlp(
+    module,
+    input_spec,
+    *,
+    linear_spec_C: Optional[torch.Tensor] = None,
+    relu_split_state: Optional[Dict[str, torch.Tensor]] = None,
+    steps: int = 20,
+    lr: float = 0.2,
+    alpha_init: float = 0.5,
+    beta_init: float = 0.0,
+    warm_start_alpha: Optional[Dict[str, torch.Tensor]] = None,
+    warm_start_beta: Optional[Dict[str, torch.Tensor]] = None,
+    objective: str = "lower",
+    spec_reduce: str = "mean",
+    per_batch_params: bool = False,
+    trace: Optional[ForwardTrace] = None,
+    raise_on_infeasible: bool = True,
+):
+    """HIP counterpart of run_alpha_beta_crown_mlp (alpha_beta_crown.py:643-941).
+
+    Returns (best_bounds, best_alpha, best_beta, stats)."""
+    if objective != "lower" or spec_reduce != "mean":
+        raise NotImplementedError("HIP alpha-beta CROWN implements objective='lower', spec_reduce='mean'")
+    spec = normalize_input_spec(input_spec)
+    chain = parse_chain(module, spec)
+    if trace is None:
+        trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
+                                  raise_on_infeasible=raise_on_infeasible)
+    dev = spec.center.device
+    B = int(spec.center.shape[0])
+    stream = _lib.stream_handle()
+    names = list(trace.relu_pre.keys())
+    shapes = {n: tuple(int(d) for d in trace.relu_pre[n].lower.shape[1:]) for n in names}
+    numel = {n: _numel(shapes[n]) for n in names}
+
+    def init_param(warm, value):
+        out = {}
+        for n in names:
+            target = (B, numel[n]) if per_batch_params else (numel[n],)
+            if warm is not None and n in warm:
+                t = warm[n].to(device=dev, dtype=torch.float32)
+                if t.numel() == numel[n] and per_batch_params:
+                    t = t.reshape(1, numel[n]).expand(B, numel[n])
+                out[n] = t.reshape(target).contiguous().clone()
+            else:
+                out[n] = torch.full(target, float(value), device=dev, dtype=torch.float32)
+        return out
+
+    alpha = init_param(warm_start_alpha, alpha_init)
+    beta = init_param(warm_start_beta, beta_init)
+    p_ld = {n: (numel[n] if per_batch_params else 0) for n in names}
+    splits: Dict[str, Tuple[torch.Tensor, int]] = {}
+    if relu_split_state:
+        for n in names:
+            if n in relu_split_state:
+                s, ld = _broadcast_split(relu_split_state[n].to(dev), B, numel[n])
+                splits[n] = (s, ld)
+    # names whose split has a nonzero entry get the beta coefficient (alpha_beta_crown.py:630-633)
+    beta_names = [n for n, (s, _ld) in splits.items() if bool((s != 0).any().item())]
+    choices = branch_choices(trace, B)
+    S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else _numel(chain.layers[-1].out_shape)
+    M = B * S
+    # d(-sum_d mean_s lb)/dlb = -1/S ; d(-mean_d mean_s lb)/dlb = (-1/B)/S   (fp32, as autograd divides)
+    g_row = np.float32(-1.0) / np.float32(S) if per_batch_params else (np.float32(-1.0) / np.float32(B)) / np.float32(S)
+    G = torch.full((M,), float(g_row), device=dev, dtype=torch.float32)
+    adam_a = {n: _Adam(alpha[n]) for n in names}
+    adam_b = {n: _Adam(beta[n]) for n in names}
+    best_metric = torch.empty(B, device=dev)
+    best_lb = torch.empty(B, S, device=dev)
+    best_ub = torch.empty(B, S, device=dev)
+    improved = torch.empty(B, dtype=torch.int32, device=dev)
+    best_alpha = {n: alpha[n].clone() for n in names}
+    best_beta = {n: beta[n].clone() for n in names}
+    best_scalar = None
+    add = {n: torch.empty(B, numel[n], device=dev) for n in beta_names}
+    for step in range(int(steps) + 1):
+        for n in beta_names:
+            s, sld = splits[n]
+            _lib.call("bf_beta_coeff", _lib.ptr(beta[n]), p_ld[n], _lib.ptr(s), sld, B, numel[n], _lib.ptr(add[n]),
+                      stream)
+        saved = {"grad_rows": G} if step < int(steps) else None
+        bounds = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C,
+                                relu_alpha={n: alpha[n] for n in names},
+                                relu_pre_add_coeff_l={n: add[n] for n in beta_names}, save=saved)
+        if per_batch_params:
+            _lib.call("bf_best_update", _lib.ptr(bounds.lower), _lib.ptr(bounds.upper), B, S, _lib.ptr(best_metric),
+                      _lib.ptr(best_lb), _lib.ptr(best_ub), _lib.ptr(improved), 1 if step == 0 else 0, stream)
+            for n in names:
+                _lib.call("bf_masked_copy_rows", _lib.ptr(best_alpha[n]), _lib.ptr(alpha[n]), B, numel[n],
+                          _lib.ptr(improved), stream)
+                _lib.call("bf_masked_copy_rows", _lib.ptr(best_beta[n]), _lib.ptr(beta[n]), B, numel[n],
+                          _lib.ptr(improved), stream)
+        else:
+            metric = float(bounds.lower.mean().item())
+            if best_scalar is None or metric > best_scalar:
+                best_scalar = metric
+                best_lb.copy_(bounds.lower)
+                best_ub.copy_(bounds.upper)
+                for n in names:
+                    best_alpha[n].copy_(alpha[n])
+                    best_beta[n].copy_(beta[n])
+        if step == int(steps):
+            break
+        a_arg = {n: (alpha[n], p_ld[n]) for n in names}
+        g_alpha, g_beta = _grad_pass(spec, chain, trace, saved, B, S, a_arg, splits, G)
+        for n in names:
+            ga, gb = g_alpha[n], g_beta[n]
+            if not per_batch_params:
+                ra = torch.empty(numel[n], device=dev)
+                rb = torch.empty(numel[n], device=dev)
+                _lib.call("bf_sum_rows", _lib.ptr(ga), B, numel[n], _lib.ptr(ra), stream)
+                _lib.call("bf_sum_rows", _lib.ptr(gb), B, numel[n], _lib.ptr(rb), stream)
+                ga, gb = ra, rb
+            adam_a[n].step(ga, lr, 0.0, 1.0, stream)
+            adam_b[n].step(gb, lr, 0.0, None, stream)
+    out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
+    out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
+    stats = AlphaBetaStats(branch_choices=choices, infeasible=trace.infeasible, steps=int(steps), lr=float(lr))
+    return IntervalState(lower=best_lb, upper=best_ub), out_alpha, out_beta, stats
+
+
+def run_alpha_crown_mlp(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.2,
+                        alpha_init: float = 0.5, relu_split_state=None):
+    """HIP counterpart of run_alpha_crown_mlp (alpha_crown.py:137-261): alpha shared
+    by all domains, loss -mean(lb)."""
+    bounds, alpha, _beta, stats = run_alpha_beta_crown_mlp(
+        module, input_spec, linear_spec_C=linear_spec_C, relu_split_state=relu_split_state, steps=steps, lr=lr,
+        alpha_init=alpha_init, per_batch_params=False)
+    return bounds, alpha, stats
+
+
+def run_alpha_crown_from_crown_init(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.1):
+    """Config C4: per-domain alpha initialised from the CROWN relaxation
+    (alpha_from_crown), then ``steps`` Adam steps on the lower bound."""
+    spec = normalize_input_spec(input_spec)
+    chain = parse_chain(module, spec)
+    trace = forward_ibp_trace(module, spec, chain=chain)
+    init = alpha_from_crown(trace)
+    return run_alpha_beta_crown_mlp(module, spec, linear_spec_C=linear_spec_C, steps=steps, lr=lr,
+                                    warm_start_alpha=init, per_batch_params=True, trace=trace)
+
+
+def lower_bound_gradients(module, input_spec, *, linear_spec_C, relu_alpha: Dict[str, torch.Tensor],
+                          relu_beta: Optional[Dict[str, torch.Tensor]] = None,
+                          relu_split_state: Optional[Dict[str, torch.Tensor]] = None, per_batch_params: bool = True):
+    """One evaluation plus one reverse pass: returns (bounds, dL/dalpha, dL/dbeta)
+    for L = -sum_d mean_s lb (per-domain parameters) or -mean lb (shared)."""
+    spec = normalize_input_spec(input_spec)
+    chain = parse_chain(module, spec)
+    trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain)
+    dev = spec.center.device
+    B = int(spec.center.shape[0])
+    names = list(trace.relu_pre.keys())
+    numel = {n: int(trace.relu_pre[n].lower[0].numel()) for n in names}
+    S = int(linear_spec_C.shape[-2])
+    g_row = np.float32(-1.0) / np.float32(S) if per_batch_params else (np.float32(-1.0) / np.float32(B)) / np.float32(S)
+    G = torch.full((B * S,), float(g_row), device=dev, dtype=torch.float32)
+    stream = _lib.stream_handle()
+    alpha = {n: relu_alpha[n].reshape((B, numel[n]) if per_batch_params else (numel[n],)).contiguous()
+             for n in names}
+    p_ld = {n: (numel[n] if per_batch_params else 0) for n in names}
+    splits: Dict[str, Tuple[torch.Tensor, int]] = {}
+    add = {}
+    if relu_split_state:
+        for n in names:
+            if n in relu_split_state:
+                splits[n] = _broadcast_split(relu_split_state[n].to(dev), B, numel[n])
+                if relu_beta is not None and bool((splits[n][0] != 0).any().item()):
+                    b = relu_beta[n].reshape((B, numel[n]) if per_batch_params else (numel[n],)).contiguous()
+                    add[n] = torch.empty(B, numel[n], device=dev)
+                    _lib.call("bf_beta_coeff", _lib.ptr(b), p_ld[n], _lib.ptr(splits[n][0]), splits[n][1], B,
+                              numel[n], _lib.ptr(add[n]), stream)
+    saved = {"grad_rows": G}
+    bounds = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=alpha,
+                            relu_pre_add_coeff_l=add, save=saved)
+    g_alpha, g_beta = _grad_pass(spec, chain, trace, saved, B, S, {n: (alpha[n], p_ld[n]) for n in names}, splits, G)
+    if not per_batch_params:
+        for d in (g_alpha, g_beta):
+            for n in list(d.keys()):
+                r = torch.empty(numel[n], device=dev)
+                _lib.call("bf_sum_rows", _lib.ptr(d[n]), B, numel[n], _lib.ptr(r), stream)
+                d[n] = r
+    return bounds, g_alpha, g_beta

@@ -1,12 +1,132 @@
-"""Conv2d pieces of the HIP CROWN path (IBP conv and the conv backward step)."""
+"""Conv2d pieces of the HIP CROWN path.
+
+* ``ibp_conv2d`` -- interval conv in center/radius form (``bf_ibp_conv2d``),
+  the counterpart of the reference's W+/W- conv transformer
+  (boundflow/domains/interval.py:57-74) after ``bounding_box`` for the input
+  layer (boundflow/runtime/crown_ibp.py:167-181).
+* ``conv_backward_step`` -- one ReLU -> Conv2d region of the CROWN backward:
+  the relaxation pass (``bf_crown_relu_relax``, with the conv bias map and, on
+  the input layer, the center projection reduced in the same pass), then the
+  transposed convolution (``bf_conv_transpose_rows``,
+  boundflow/runtime/linear_operator.py:1067-1092), fused with the Linf / box
+  concretization on the input layer.
+"""
 
 from __future__ import annotations
 
+from typing import Optional
 
-def ibp_conv2d(in_lo, in_hi, relu_in, layer, split, split_ld, lo, hi, infeasible):
-    raise NotImplementedError("HIP conv2d IBP is not built yet")
+import torch
+
+from . import _lib
+from .profiling import launch as _timed
+from .spec import BoxPerturbation, IntervalState
+
+
+def _numel(shape) -> int:
+    n = 1
+    for d in shape:
+        n *= int(d)
+    return n
+
+
+def ibp_conv2d(in_lo, in_hi, relu_in, layer, split, split_ld, lo, hi, infeasible, *, linf_eps=None,
+               center_out=None):
+    Ci, Hi, Wi = layer.in_shape
+    Co, Ho, Wo = layer.out_shape
+    KH, KW = int(layer.weight.shape[2]), int(layer.weight.shape[3])
+    sh, sw = layer.attrs["stride"]
+    ph, pw = layer.attrs["padding"]
+    B = int(in_lo.shape[0])
+    ws = torch.empty(int(_lib.load().bf_ibp_conv2d_workspace(B, Ci * Hi * Wi, Co * Ho * Wo)), device=in_lo.device,
+                     dtype=torch.float32)
+    kind = 1 if linf_eps is not None else 0
+    _lib.call("bf_ibp_conv2d", _lib.ptr(in_lo.contiguous()), _lib.ptr(None if in_hi is None else in_hi.contiguous()),
+              B, Ci, Hi, Wi, kind, float(linf_eps or 0.0), int(relu_in), _lib.ptr(layer.weight.contiguous()),
+              _lib.ptr(None if layer.bias is None else layer.bias.contiguous()), Co, KH, KW, sh, sw, ph, pw, Ho, Wo,
+              _lib.ptr(split), split_ld, _lib.ptr(ws), _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(center_out),
+              _lib.ptr(infeasible), _lib.stream_handle())
 
 
 def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo, pre_hi, alpha, alpha_ld, add,
-                       add_ld, spec, trace):
-    raise NotImplementedError("HIP conv2d CROWN backward is not built yet")
+                       add_ld, spec, trace, save=None):
+    """Returns (A_u, A_l, b_u, b_l, stride, done) where ``done`` is the final
+    IntervalState on the input layer and None otherwise."""
+    dev = spec.center.device
+    stream = _lib.stream_handle()
+    M = B * S
+    Co, Ho, Wo = layer.out_shape
+    Ci, Hi, Wi = layer.in_shape
+    n_out = Co * Ho * Wo
+    n_in = Ci * Hi * Wi
+    KH, KW = int(layer.weight.shape[2]), int(layer.weight.shape[3])
+    sh, sw = layer.attrs["stride"]
+    ph, pw = layer.attrs["padding"]
+    W = layer.weight.contiguous()
+
+    def materialize(A):
+        if A is None:
+            return None
+        if stride == S * n_out:
+            return A.reshape(M, n_out)
+        return A.reshape(-1, n_out)[: S].unsqueeze(0).expand(B, S, n_out).reshape(M, n_out).contiguous()
+
+    A_u = materialize(A_u)
+    A_l = materialize(A_l)
+    kbias = None
+    if layer.bias is not None:
+        kbias = layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(n_out).contiguous()
+    cvec = trace.input_center_proj.get(layer.out_name) if is_first else None
+    rA_u = torch.empty_like(A_u) if A_u is not None else None
+    rA_l = torch.empty_like(A_l) if A_l is not None else None
+    nb_u = torch.empty(M, device=dev) if A_u is not None else None
+    nb_l = torch.empty(M, device=dev) if A_l is not None else None
+    c_u = torch.empty(M, device=dev) if (A_u is not None and cvec is not None) else None
+    c_l = torch.empty(M, device=dev) if (A_l is not None and cvec is not None) else None
+    nz = int(A_u is not None) + int(A_l is not None)
+    with _timed("crown_relu_relax", 0.0, 4.0 * nz * 2 * M * n_out):
+        _lib.call("bf_crown_relu_relax", _lib.ptr(A_u), _lib.ptr(A_l), B, S, n_out, _lib.ptr(pre_lo),
+                  _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld, _lib.ptr(kbias),
+                  _lib.ptr(cvec), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u), _lib.ptr(rA_l), _lib.ptr(nb_u),
+                  _lib.ptr(nb_l), _lib.ptr(c_u), _lib.ptr(c_l), stream)
+    taps = KH * KW / float(sh * sw)
+    flops = 2.0 * nz * M * n_in * Co * taps
+    if not is_first:
+        y_u = torch.empty(M, n_in, device=dev) if A_u is not None else None
+        y_l = torch.empty(M, n_in, device=dev) if A_l is not None else None
+        with _timed("conv_transpose", flops, 4.0 * nz * (M * n_out + M * n_in)):
+            _lib.call("bf_conv_transpose_rows", _lib.ptr(rA_u), _lib.ptr(rA_l), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH,
+                      KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(y_l), S, None, 0, None, None, None, None,
+                      stream)
+        if save is not None:
+            save.setdefault("relaxed", {})[layer.op_index] = rA_l
+        return y_u, y_l, nb_u, nb_l, S * n_in, None
+    # input layer: transposed conv fused with the concretization
+    pert = spec.perturbation
+    if cvec is None:
+        raise RuntimeError("forward trace lacks the input-layer projection")
+    if isinstance(pert, BoxPerturbation):
+        rad = ((pert.upper - pert.lower) / 2.0).reshape(B, n_in).contiguous()
+        eps = 1.0
+    else:
+        rad = None
+        eps = float(pert.eps)
+    norm_u = torch.empty(M, device=dev) if A_u is not None else None
+    norm_l = torch.empty(M, device=dev) if A_l is not None else None
+    h_scale = h_out = None
+    if save is not None and save.get("grad_rows") is not None:
+        h_scale = (save["grad_rows"] * (-eps)).contiguous()
+        h_out = torch.empty(M, n_in, device=dev)
+        save["h"] = h_out
+        save["cvec"] = cvec
+    with _timed("conv_transpose_concretize", flops, 4.0 * nz * M * n_out):
+        _lib.call("bf_conv_transpose_rows", _lib.ptr(rA_u), _lib.ptr(rA_l), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW,
+                  sh, sw, ph, pw, Hi, Wi, None, None, S, _lib.ptr(rad), n_in, _lib.ptr(norm_u), _lib.ptr(norm_l),
+                  _lib.ptr(h_scale), _lib.ptr(h_out), stream)
+    if save is not None:
+        save.setdefault("relaxed", {})[layer.op_index] = rA_l
+    lb = torch.empty(B, S, device=dev) if A_l is not None else None
+    ub = torch.empty(B, S, device=dev) if A_u is not None else None
+    _lib.call("bf_concretize_finalize", _lib.ptr(norm_u), _lib.ptr(norm_l), 1, M, _lib.ptr(c_u), _lib.ptr(c_l),
+              _lib.ptr(nb_u), _lib.ptr(nb_l), eps, _lib.ptr(lb), _lib.ptr(ub), stream)
+    return None, None, None, None, 0, IntervalState(lower=lb, upper=ub)

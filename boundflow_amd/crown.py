@@ -246,14 +246,21 @@ def forward_ibp_trace(
             if cproj is not None:
                 proj[layer.out_name] = cproj
         else:
+            linf = None
+            cproj = None
             if first:
-                blo, bhi = pert.bounding_box(center)
-                in_lo, in_hi, relu_in = blo.contiguous(), bhi.contiguous(), 0
+                cproj = torch.empty((B,) + layer.out_shape, device=dev, dtype=torch.float32)
+                if isinstance(pert, BoxPerturbation):
+                    in_lo, in_hi, relu_in = pert.lower.contiguous(), pert.upper.contiguous(), 0
+                else:
+                    in_lo, in_hi, relu_in, linf = center.contiguous(), None, 0, float(pert.eps)
             else:
                 in_lo, in_hi = prev_lo, prev_hi
                 relu_in = 1 if layer.input_is_relu_of is not None else 0
             ibp_conv2d(in_lo, in_hi, relu_in, layer, None if has_constraint else split, split_ld, lo, hi,
-                       infeasible)
+                       infeasible, linf_eps=linf, center_out=cproj)
+            if cproj is not None:
+                proj[layer.out_name] = cproj.reshape(B, out_numel)
         if has_constraint:
             c = relu_pre_constraints[layer.out_name]
             _lib.call("bf_interval_clip", _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(c.lower.contiguous()),
@@ -354,7 +361,7 @@ def crown_backward(
         if layer.kind == "conv2d":
             A_u, A_l, b_u, b_l, stride, done = conv_backward_step(
                 layer, k == 0, A_u, A_l, stride, b_u, b_l, B, S, pre_lo, pre_hi, alpha, alpha_ld, add, add_ld,
-                spec, trace)
+                spec, trace, save=save)
             if done is not None:
                 return done
             continue
@@ -389,12 +396,20 @@ def crown_backward(
                              dtype=torch.float32)
             lb = torch.empty(B, S, device=dev, dtype=torch.float32) if A_l is not None else None
             ub = torch.empty(B, S, device=dev, dtype=torch.float32) if A_u is not None else None
+            h_scale = h_out = None
+            if save is not None and save.get("grad_rows") is not None:
+                # gradient seed of the concretization: h = -eps * G * sign(A W) (* radius for a box)
+                h_scale = (save["grad_rows"] * (-eps)).contiguous()
+                h_out = torch.empty(M, P, device=dev, dtype=torch.float32)
+                save["h"] = h_out
+                save["cvec"] = cvec
             nz = int(A_u is not None) + int(A_l is not None)
             with _timed("crown_relu_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
                 _lib.call("bf_crown_relu_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
                           _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld,
                           _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(cvec), _lib.ptr(rad), eps, _lib.ptr(b_u),
-                          _lib.ptr(b_l), _lib.ptr(ws), _lib.ptr(lb), _lib.ptr(ub), stream)
+                          _lib.ptr(b_l), _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(ws), _lib.ptr(lb),
+                          _lib.ptr(ub), stream)
             if save is not None:
                 save["final_ws"] = ws
             return IntervalState(lower=lb, upper=ub)

@@ -232,7 +232,11 @@ gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-          if (row < M && col < N) C[row * p.ldc + col] = acc[i][j][r];
+          if (row < M && col < N) {
+            float v = acc[i][j][r];
+            if (p.r1_row) v = v + p.r1_row[row] * p.r1_col[(row / p.S) * p.r1_ld + col];
+            C[row * p.ldc + col] = v;
+          }
         }
       }
   } else {
@@ -247,12 +251,20 @@ gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int64_t col = n0 + wn * 64 + j * 32 + lrow;
-          float v = fabsf(acc[i][j][r]);
+          const float a = acc[i][j][r];
+          float v = fabsf(a);
+          float wgt = 1.f;
           if (p.wvec) {
             int64_t d = (row < M) ? row / p.S : 0;
-            v = (row < M && col < N) ? v * p.wvec[d * p.w_ld + col] : 0.f;
+            wgt = (row < M && col < N) ? p.wvec[d * p.w_ld + col] : 0.f;
+            v = v * wgt;
           }
           s += v;
+          if (lower && p.h_out && row < M && col < N) {
+            const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
+            const float hs = p.h_scale[row];
+            p.h_out[row * N + col] = p.wvec ? hs * sg * wgt : hs * sg;
+          }
         }
         rs[i][r] = s;
       }

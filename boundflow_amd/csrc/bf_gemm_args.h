@@ -42,6 +42,13 @@ struct GemmArgs {
   const float* wvec;         // optional [D, N] weights (box radius), row stride w_ld
   int64_t w_ld;
   float* partial[2];         // [gridDim.y, M] partial row sums
+  const float* h_scale;      // optional [M]: lower pass also writes h = h_scale[m] * sign(C) * w  (gradient seed)
+  float* h_out;              // [M, N] row-major (ldh = N)
+
+  // --- rank-1 term of the store epilogue: C[m, n] = acc + r1_row[m] * r1_col[(m / S) * r1_ld + n] ---
+  const float* r1_row;
+  const float* r1_col;
+  int64_t r1_ld;
 };
 
 }  // namespace bf

@@ -1,0 +1,219 @@
+// Gradient kernels of alpha / alpha-beta CROWN (north-star kernel #5) and the
+// optimiser bookkeeping that stays on the device.
+//
+// The objective is the lower bound; with G = dL/dlb (one value per
+// coefficient row m = d*S + s) the reverse pass through one ReLU relaxation
+// (boundflow/runtime/crown_ibp.py:1211-1298, lower half) is, per element,
+//
+//   A' = A * sel(A >= 0, alpha_l, alpha_u) + add;   b += A * sel(A >= 0, beta_l, beta_u)
+//   dL/dA      = dL/dA' * sel(A >= 0, alpha_l, alpha_u) + G * sel(A >= 0, beta_l, beta_u)
+//   dL/dalpha  = sum_s dL/dA' * A * 1(A >= 0)   on ambiguous neurons, where 0 <= alpha <= 1
+//   dL/dbeta   = -s * 1(s != 0) * sum_s dL/dA'   (add = -beta * s * 1(s != 0),
+//                boundflow/runtime/alpha_beta_crown.py:615-640)
+//
+// The selection itself is not differentiated (torch.where), the clamp passes
+// the gradient on [0, 1] inclusive, as autograd does.
+
+#include "bf_common.h"
+
+namespace bf {
+
+// One thread per (domain, neuron); the S rows of the domain are walked in
+// order, so the reductions over specs are deterministic and reads of row m are
+// coalesced across neurons.
+__global__ void relu_grad_kernel(const float* __restrict__ g_out, const float* __restrict__ A, int64_t a_dstride,
+                                 int64_t D, int64_t S, int64_t N, const float* __restrict__ lo,
+                                 const float* __restrict__ hi, const float* __restrict__ alpha, int64_t alpha_ld,
+                                 const float* __restrict__ G, const int8_t* __restrict__ split, int64_t split_ld,
+                                 float* __restrict__ g_in, float* __restrict__ g_alpha, float* __restrict__ g_beta) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D * N) return;
+  const int64_t d = i / N, n = i % N;
+  const float l = lo[d * N + n], u = hi[d * N + n];
+  const bool has_alpha = alpha != nullptr;
+  const float araw = has_alpha ? alpha[d * alpha_ld + n] : 0.f;
+  const Relax r = relu_relax(l, u, has_alpha, clamp01(araw));
+  const bool amb = (l < 0.f) && (u > 0.f);
+  const bool pass = has_alpha && amb && (araw >= 0.f) && (araw <= 1.f);
+  float ga = 0.f, gs = 0.f;
+  for (int64_t s = 0; s < S; ++s) {
+    const int64_t m = d * S + s;
+    const float a = A[d * a_dstride + s * N + n];
+    const float go = g_out[m * N + n];
+    const bool nn = a >= 0.f;
+    const float sa = nn ? r.al : r.au;
+    const float sb = nn ? r.bl : r.bu;
+    g_in[m * N + n] = go * sa + G[m] * sb;
+    if (nn) ga += go * a;
+    gs += go;
+  }
+  if (g_alpha) g_alpha[d * N + n] = pass ? ga : 0.f;
+  if (g_beta) {
+    const int8_t sp = split ? split[d * split_ld + n] : 0;
+    g_beta[d * N + n] = sp ? -(float)sp * gs : 0.f;
+  }
+}
+
+// add[d, n] = -beta[d, n] * s[d, n] * 1(s != 0)
+__global__ void beta_coeff_kernel(const float* __restrict__ beta, int64_t beta_ld, const int8_t* __restrict__ split,
+                                  int64_t split_ld, int64_t D, int64_t N, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D * N) return;
+  const int64_t d = i / N, n = i % N;
+  const int8_t s = split[d * split_ld + n];
+  const float sf = (float)s;
+  out[i] = (-beta[d * beta_ld + n] * sf) * (s != 0 ? 1.f : 0.f);
+}
+
+// Per-domain best-of tracking (boundflow/runtime/alpha_beta_crown.py:840-876):
+// metric = mean over specs of the lower bound; on the first call or when the
+// metric strictly improves, keep the bounds and flag the domain.
+__global__ void best_update_kernel(const float* __restrict__ lb, const float* __restrict__ ub, int64_t D, int64_t S,
+                                   float* __restrict__ best_metric, float* __restrict__ best_lb,
+                                   float* __restrict__ best_ub, int* __restrict__ improved, int first) {
+  const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= D) return;
+  float sum = 0.f;
+  for (int64_t s = 0; s < S; ++s) sum += lb[d * S + s];
+  const float metric = sum / (float)S;
+  const bool take = first || (metric > best_metric[d]);
+  improved[d] = take ? 1 : 0;
+  if (take) {
+    best_metric[d] = metric;
+    for (int64_t s = 0; s < S; ++s) {
+      best_lb[d * S + s] = lb[d * S + s];
+      best_ub[d * S + s] = ub[d * S + s];
+    }
+  }
+}
+
+__global__ void masked_copy_rows_kernel(float* __restrict__ dst, const float* __restrict__ src, int64_t D, int64_t N,
+                                        const int* __restrict__ mask) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D * N) return;
+  if (mask[i / N]) dst[i] = src[i];
+}
+
+// out[n] = sum_d x[d, n] in domain order (gradient of a parameter shared by all domains)
+__global__ void sum_rows_kernel(const float* __restrict__ x, int64_t D, int64_t N, float* __restrict__ out) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float s = 0.f;
+  for (int64_t d = 0; d < D; ++d) s += x[d * N + n];
+  out[n] = s;
+}
+
+// "alpha from CROWN" initialisation
+// (boundflow/runtime/native_alpha_beta_optimizer_schedule.py:635-653):
+// 1 on stable-active neurons, 1(u > -l) on ambiguous ones, 0 otherwise.
+__global__ void alpha_from_crown_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int64_t n,
+                                        float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float l = lo[i], u = hi[i];
+  const bool pos = l >= 0.f;
+  const bool neg = u <= 0.f;
+  float a = 0.f;
+  if (pos) a = 1.f;
+  if (!pos && !neg) a = (u > -l) ? 1.f : 0.f;
+  out[i] = a;
+}
+
+// BaB node verdict (boundflow/runtime/bab.py:870-895): a domain is closed when
+// min_s lb >= threshold - tol; a domain whose split emptied a box is closed as
+// infeasible.  status: 0 = open (to branch), 1 = certified, 2 = infeasible.
+__global__ void domain_status_kernel(const float* __restrict__ lb, int64_t D, int64_t S,
+                                     const int* __restrict__ infeasible, float threshold, float tol,
+                                     int* __restrict__ status) {
+  const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= D) return;
+  if (infeasible && infeasible[d]) {
+    status[d] = 2;
+    return;
+  }
+  float mn = lb[d * S];
+  for (int64_t s = 1; s < S; ++s) mn = fminf(mn, lb[d * S + s]);
+  status[d] = (mn >= threshold - tol) ? 1 : 0;
+}
+
+}  // namespace bf
+
+using namespace bf;
+
+extern "C" {
+
+int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
+                 const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, const float* G,
+                 const int8_t* split, int64_t split_ld, float* g_in, float* g_alpha, float* g_beta,
+                 hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && N > 0, "bf_relu_grad: bad sizes");
+  if (D == 0) return BF_OK;
+  BF_REQUIRE(g_out && A && pre_lo && pre_hi && G && g_in, "bf_relu_grad: null pointer");
+  hipLaunchKernelGGL(relu_grad_kernel, dim3((unsigned)ceil_div(D * N, 256)), dim3(256), 0, stream, g_out, A,
+                     a_dstride, D, S, N, pre_lo, pre_hi, alpha, alpha_ld, G, split, split_ld, g_in, g_alpha, g_beta);
+  BF_LAUNCH_CHECK("relu_grad_kernel");
+  return BF_OK;
+}
+
+int bf_beta_coeff(const float* beta, int64_t beta_ld, const int8_t* split, int64_t split_ld, int64_t D, int64_t N,
+                  float* out, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && N >= 0, "bf_beta_coeff: bad sizes");
+  if (D * N == 0) return BF_OK;
+  BF_REQUIRE(beta && split && out, "bf_beta_coeff: null pointer");
+  hipLaunchKernelGGL(beta_coeff_kernel, dim3((unsigned)ceil_div(D * N, 256)), dim3(256), 0, stream, beta, beta_ld,
+                     split, split_ld, D, N, out);
+  BF_LAUNCH_CHECK("beta_coeff_kernel");
+  return BF_OK;
+}
+
+int bf_best_update(const float* lb, const float* ub, int64_t D, int64_t S, float* best_metric, float* best_lb,
+                   float* best_ub, int* improved, int first, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0, "bf_best_update: bad sizes");
+  if (D == 0) return BF_OK;
+  BF_REQUIRE(lb && ub && best_metric && best_lb && best_ub && improved, "bf_best_update: null pointer");
+  hipLaunchKernelGGL(best_update_kernel, dim3((unsigned)ceil_div(D, 256)), dim3(256), 0, stream, lb, ub, D, S,
+                     best_metric, best_lb, best_ub, improved, first);
+  BF_LAUNCH_CHECK("best_update_kernel");
+  return BF_OK;
+}
+
+int bf_masked_copy_rows(float* dst, const float* src, int64_t D, int64_t N, const int* mask, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && N >= 0, "bf_masked_copy_rows: bad sizes");
+  if (D * N == 0) return BF_OK;
+  BF_REQUIRE(dst && src && mask, "bf_masked_copy_rows: null pointer");
+  hipLaunchKernelGGL(masked_copy_rows_kernel, dim3((unsigned)ceil_div(D * N, 256)), dim3(256), 0, stream, dst, src,
+                     D, N, mask);
+  BF_LAUNCH_CHECK("masked_copy_rows_kernel");
+  return BF_OK;
+}
+
+int bf_sum_rows(const float* x, int64_t D, int64_t N, float* out, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && N >= 0, "bf_sum_rows: bad sizes");
+  if (N == 0) return BF_OK;
+  BF_REQUIRE(x && out, "bf_sum_rows: null pointer");
+  hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)ceil_div(N, 256)), dim3(256), 0, stream, x, D, N, out);
+  BF_LAUNCH_CHECK("sum_rows_kernel");
+  return BF_OK;
+}
+
+int bf_domain_status(const float* lb, int64_t D, int64_t S, const int* infeasible, float threshold, float tol,
+                     int* status, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0, "bf_domain_status: bad sizes");
+  if (D == 0) return BF_OK;
+  BF_REQUIRE(lb && status, "bf_domain_status: null pointer");
+  hipLaunchKernelGGL(domain_status_kernel, dim3((unsigned)ceil_div(D, 256)), dim3(256), 0, stream, lb, D, S,
+                     infeasible, threshold, tol, status);
+  BF_LAUNCH_CHECK("domain_status_kernel");
+  return BF_OK;
+}
+
+int bf_alpha_from_crown(const float* lo, const float* hi, int64_t n, float* out, hipStream_t stream) {
+  BF_REQUIRE(n >= 0, "bf_alpha_from_crown: bad size");
+  if (n == 0) return BF_OK;
+  BF_REQUIRE(lo && hi && out, "bf_alpha_from_crown: null pointer");
+  hipLaunchKernelGGL(alpha_from_crown_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, lo, hi, n, out);
+  BF_LAUNCH_CHECK("alpha_from_crown_kernel");
+  return BF_OK;
+}
+
+}  // extern "C"

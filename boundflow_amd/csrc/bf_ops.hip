@@ -48,6 +48,15 @@ __global__ void ibp_center_radius_kernel(const float* __restrict__ lo, const flo
   rad[i] = (u - l) / 2.0f;
 }
 
+int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
+                      hipStream_t stream) {
+  if (n == 0) return BF_OK;
+  hipLaunchKernelGGL(ibp_center_radius_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, lo, hi, n,
+                     apply_relu, mid, rad);
+  BF_LAUNCH_CHECK("ibp_center_radius_kernel");
+  return BF_OK;
+}
+
 // row_norm[o] = sum_i |W[o, i]|   (Linf input layer, perturbation.py:133)
 __global__ void row_abs_sum_kernel(const float* __restrict__ W, int64_t O, int64_t I, float* __restrict__ out) {
   int64_t o = (int64_t)blockIdx.x;
@@ -69,8 +78,9 @@ __global__ void row_abs_sum_kernel(const float* __restrict__ W, int64_t O, int64
 // a domain with lo > hi anywhere is flagged infeasible.
 __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __restrict__ r,
                                     const float* __restrict__ rownorm, float eps, const float* __restrict__ bias,
-                                    const int8_t* __restrict__ split, int64_t split_ld, int64_t B, int64_t N,
-                                    float* __restrict__ lo, float* __restrict__ hi, int* __restrict__ infeasible) {
+                                    int64_t bias_div, const int8_t* __restrict__ split, int64_t split_ld, int64_t B,
+                                    int64_t N, float* __restrict__ lo, float* __restrict__ hi,
+                                    int* __restrict__ infeasible) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= B * N) return;
   int64_t b = i / N, n = i % N;
@@ -78,8 +88,8 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
   float l = c[i] - dev;
   float u = c[i] + dev;
   if (bias) {
-    l = l + bias[n];
-    u = u + bias[n];
+    l = l + bias[n / bias_div];
+    u = u + bias[n / bias_div];
   }
   if (split) {
     int8_t s = split[b * split_ld + n];
@@ -89,6 +99,31 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
   }
   lo[i] = l;
   hi[i] = u;
+}
+
+__global__ void fill_kernel(float* __restrict__ p, int64_t n, float v) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+int fill_value(float* p, int64_t n, float v, hipStream_t stream) {
+  if (n == 0) return BF_OK;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, p, n, v);
+  BF_LAUNCH_CHECK("fill_kernel");
+  return BF_OK;
+}
+
+int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
+                      hipStream_t stream);
+
+int ibp_finalize(const float* c, const float* r, const float* rownorm, float eps, const float* bias,
+                 int64_t bias_div, const int8_t* split, int64_t split_ld, int64_t B, int64_t N, float* lo, float* hi,
+                 int* infeasible, hipStream_t stream) {
+  if (B * N == 0) return BF_OK;
+  hipLaunchKernelGGL(ibp_finalize_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, c, r, rownorm,
+                     eps, bias, bias_div, split, split_ld, B, N, lo, hi, infeasible);
+  BF_LAUNCH_CHECK("ibp_finalize_kernel");
+  return BF_OK;
 }
 
 // Intersect with external constraints (crown_ibp.py:186-209) and apply a split.
@@ -122,25 +157,32 @@ __global__ void __launch_bounds__(256)
 relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t M, int64_t S, int64_t K,
                        const float* __restrict__ lo, const float* __restrict__ hi, const float* __restrict__ alpha,
                        int64_t alpha_ld, const float* __restrict__ add_l, int64_t add_ld,
-                       const float* __restrict__ kbias, const float* __restrict__ bu_in,
-                       const float* __restrict__ bl_in, float* __restrict__ Au_out, float* __restrict__ Al_out,
-                       float* __restrict__ bu_out, float* __restrict__ bl_out) {
+                       const float* __restrict__ kbias, const float* __restrict__ cvec,
+                       const float* __restrict__ bu_in, const float* __restrict__ bl_in, float* __restrict__ Au_out,
+                       float* __restrict__ Al_out, float* __restrict__ bu_out, float* __restrict__ bl_out,
+                       float* __restrict__ cu_out, float* __restrict__ cl_out) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= M) return;
   const int64_t d = m / S;
-  float su = 0.f, sl = 0.f, ku = 0.f, kl = 0.f;
+  float su = 0.f, sl = 0.f, ku = 0.f, kl = 0.f, cu = 0.f, cl = 0.f;
   for (int64_t k = lane; k < K; k += 64) {
-    const float l = lo[d * K + k], u = hi[d * K + k];
-    const bool has_alpha = alpha != nullptr;
-    const float a = has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f;
-    Relax r = relu_relax(l, u, has_alpha, a);
+    Relax r;
+    if (lo) {
+      const float l = lo[d * K + k], u = hi[d * K + k];
+      const bool has_alpha = alpha != nullptr;
+      const float a = has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f;
+      r = relu_relax(l, u, has_alpha, a);
+    } else {
+      r.au = 1.f; r.bu = 0.f; r.al = 1.f; r.bl = 0.f;  // no ReLU: identity
+    }
     if (Au) {
       float v = Au[m * K + k];
       bool nn = v >= 0.f;
       float o = v * (nn ? r.au : r.al);
       su += v * (nn ? r.bu : r.bl);
       if (kbias) ku += o * kbias[k];
+      if (cvec) cu += o * cvec[d * K + k];
       Au_out[m * K + k] = o;
     }
     if (Al) {
@@ -150,6 +192,7 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
       sl += v * (nn ? r.bl : r.bu);
       if (add_l) o = o + add_l[d * add_ld + k];
       if (kbias) kl += o * kbias[k];
+      if (cvec) cl += o * cvec[d * K + k];
       Al_out[m * K + k] = o;
     }
   }
@@ -158,10 +201,14 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
     sl += __shfl_xor(sl, off, 64);
     ku += __shfl_xor(ku, off, 64);
     kl += __shfl_xor(kl, off, 64);
+    cu += __shfl_xor(cu, off, 64);
+    cl += __shfl_xor(cl, off, 64);
   }
   if (lane == 0) {
     if (bu_out) bu_out[m] = ((bu_in ? bu_in[m] : 0.f) + su) + ku;
     if (bl_out) bl_out[m] = ((bl_in ? bl_in[m] : 0.f) + sl) + kl;
+    if (cu_out) cu_out[m] = cu;
+    if (cl_out) cl_out[m] = cl;
   }
 }
 
@@ -317,6 +364,41 @@ int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_
   return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, 1, stream);
 }
 
+int bf_gemm_rank1(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, float* C, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, int64_t S, const float* r_row, const float* v_col, int64_t v_ld,
+                  hipStream_t stream) {
+  BF_REQUIRE(M >= 0 && N >= 0 && K >= 0 && S > 0, "bf_gemm_rank1: bad sizes");
+  if (M == 0 || N == 0) return BF_OK;
+  BF_REQUIRE(A && B && C && ((r_row == nullptr) == (v_col == nullptr)), "bf_gemm_rank1: null pointer");
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A[0] = A;
+  a.C[0] = C;
+  a.lda = lda;
+  a.lda_d = lda * S;
+  a.ldc = ldc;
+  a.B = B;
+  a.ldb = ldb;
+  a.trans_b = trans_b;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.S = S;
+  a.r1_row = r_row;
+  a.r1_col = v_col;
+  a.r1_ld = v_ld;
+  return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, 1, stream);
+}
+
+int bf_concretize_finalize(const float* partial_u, const float* partial_l, int nparts, int64_t M,
+                           const float* cen_u, const float* cen_l, const float* b_u, const float* b_l, float eps,
+                           float* lb, float* ub, hipStream_t stream) {
+  BF_REQUIRE(M >= 0 && nparts >= 1, "bf_concretize_finalize: bad sizes");
+  BF_REQUIRE((lb == nullptr || (partial_l && cen_l && b_l)) && (ub == nullptr || (partial_u && cen_u && b_u)),
+             "bf_concretize_finalize: null pointer");
+  return concretize_finalize(partial_u, partial_l, nparts, M, cen_u, cen_l, b_u, b_l, eps, lb, ub, stream);
+}
+
 int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
                              const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
                              const float* add_l, int64_t add_ld, const float* W, int64_t P, const float* bias,
@@ -365,8 +447,8 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
                                     const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
                                     const float* add_l, int64_t add_ld, const float* W, int64_t I,
                                     const float* bias, const float* cvec, const float* rad, float eps,
-                                    const float* b_u_in, const float* b_l_in, float* workspace, float* lb,
-                                    float* ub, hipStream_t stream) {
+                                    const float* b_u_in, const float* b_l_in, const float* h_scale,
+                                    float* h_out, float* workspace, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
@@ -412,6 +494,10 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
   a.cvec_ld = N;
   a.wvec = rad;
   a.w_ld = I;
+  BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || A_l != nullptr),
+             "bf_crown_relu_linear_concretize: h_out needs h_scale and the lower coefficient");
+  a.h_scale = h_scale;
+  a.h_out = h_out;
   int rc = gemm_dispatch(a, PRO_RELAX, EPI_ABSSUM, nz, stream);
   if (rc) return rc;
   return concretize_finalize(pu, pl, nparts, M, cu, cl, bu, bl, rad ? 1.0f : eps, lb, ub, stream);
@@ -424,17 +510,18 @@ int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t 
 
 int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* pre_lo,
                         const float* pre_hi, const float* alpha, int64_t alpha_ld, const float* add_l,
-                        int64_t add_ld, const float* kbias, const float* b_u_in, const float* b_l_in,
-                        float* A_u_out, float* A_l_out, float* b_u_out, float* b_l_out, hipStream_t stream) {
+                        int64_t add_ld, const float* kbias, const float* cvec, const float* b_u_in,
+                        const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out, float* b_l_out,
+                        float* c_u_out, float* c_l_out, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && K > 0, "bf_crown_relu_relax: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
-  BF_REQUIRE(pre_lo && pre_hi, "bf_crown_relu_relax: null pre-bounds");
+  BF_REQUIRE((pre_lo == nullptr) == (pre_hi == nullptr), "bf_crown_relu_relax: half a pre-bound");
   BF_REQUIRE((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr),
              "bf_crown_relu_relax: input/output mismatch");
   hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l, M, S,
-                     K, pre_lo, pre_hi, alpha, alpha_ld, add_l, add_ld, kbias, b_u_in, b_l_in, A_u_out, A_l_out,
-                     b_u_out, b_l_out);
+                     K, pre_lo, pre_hi, alpha, alpha_ld, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
+                     A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
   BF_LAUNCH_CHECK("relu_relax_rows_kernel");
   return BF_OK;
 }
@@ -473,24 +560,18 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
     if (rc) return rc;
     hipLaunchKernelGGL(row_abs_sum_kernel, dim3((unsigned)N), dim3(256), 0, stream, W, N, K, rownorm);
     BF_LAUNCH_CHECK("row_abs_sum_kernel");
-    hipLaunchKernelGGL(ibp_finalize_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, cdst,
-                       (const float*)nullptr, rownorm, eps, bias, split, split_ld, B, N, out_lo, out_hi, infeasible);
-    BF_LAUNCH_CHECK("ibp_finalize_kernel");
-    return BF_OK;
+    return ibp_finalize(cdst, nullptr, rownorm, eps, bias, 1, split, split_ld, B, N, out_lo, out_hi, infeasible,
+                        stream);
   }
   BF_REQUIRE(in_hi, "bf_ibp_linear: interval input needs in_hi");
-  hipLaunchKernelGGL(ibp_center_radius_kernel, dim3((unsigned)ceil_div(B * K, 256)), dim3(256), 0, stream, in_lo,
-                     in_hi, B * K, apply_relu, mid, rad);
-  BF_LAUNCH_CHECK("ibp_center_radius_kernel");
+  rc = ibp_center_radius(in_lo, in_hi, B * K, apply_relu, mid, rad, stream);
+  if (rc) return rc;
   float* cdst = center_out ? center_out : c;
   rc = bf_gemm(mid, K, W, K, 1, 0, cdst, N, B, N, K, stream);
   if (rc) return rc;
   rc = bf_gemm(rad, K, W, K, 1, 1, r, N, B, N, K, stream);
   if (rc) return rc;
-  hipLaunchKernelGGL(ibp_finalize_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, cdst, r,
-                     (const float*)nullptr, 0.f, bias, split, split_ld, B, N, out_lo, out_hi, infeasible);
-  BF_LAUNCH_CHECK("ibp_finalize_kernel");
-  return BF_OK;
+  return ibp_finalize(cdst, r, nullptr, 0.f, bias, 1, split, split_ld, B, N, out_lo, out_hi, infeasible, stream);
 }
 
 int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) { return 2 * B * K + 2 * B * N + N; }

@@ -1,0 +1,206 @@
+/* boundflow_hip.h -- C ABI of libboundflow_hip.so, the MI355X (gfx950) HIP
+ * backend of the bound-propagation hot path.
+ *
+ * Conventions (all entry points):
+ *  - pointers are device pointers (fp32 unless stated; int8 split masks,
+ *    int32 flags); tensors are dense row-major;
+ *  - "rows" are coefficient rows m = d * S + s (domain d, spec s), M = D * S;
+ *    a per-domain vector of length n is addressed vec[d * ld + j] where
+ *    ld = n (one per domain) or 0 (shared by all domains);
+ *  - work is enqueued on `stream` (torch's current stream by default); no call
+ *    synchronizes, allocates or frees -- callers pass outputs and workspaces;
+ *  - every int-returning entry returns 0 on success and a nonzero status
+ *    (1 invalid argument, 2 launch failure, 3 size limit) with a message from
+ *    bf_last_error() (thread-local).  No C++ exception crosses the boundary.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (paths relative to the reference checkout's boundflow/ package).
+ */
+#ifndef BOUNDFLOW_HIP_H
+#define BOUNDFLOW_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+int bf_abi_version(void);
+const char* bf_last_error(void);
+
+/* ---- kernel #1: IBP ---------------------------------------------------- */
+
+/* Interval linear layer in center/radius form, with the consumer ReLU's split
+ * applied and per-domain infeasibility flagged.
+ * Replaces LpBallPerturbation/BoxPerturbation.concretize_matmul
+ * (runtime/perturbation.py:102-173, 282-325) for the input layer and
+ * IntervalDomain.affine_transformer (domains/interval.py:79-86) for hidden
+ * layers, and _apply_relu_split (runtime/crown_ibp.py:70-98).
+ * input_kind 0: [in_lo, in_hi] box (ReLU applied first when apply_relu);
+ * input_kind 1: Linf ball of radius eps around in_lo.
+ * workspace: bf_ibp_linear_workspace(B, K, N) floats.  center_out (optional,
+ * [B, N]) receives mid @ W^T without bias. */
+int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, int input_kind, float eps,
+                  int apply_relu, const float* W, const float* bias, int64_t N, const int8_t* split,
+                  int64_t split_ld, float* workspace, float* out_lo, float* out_hi, float* center_out,
+                  int* infeasible, hipStream_t stream);
+int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N);
+
+/* Interval conv2d (NCHW, groups 1, dilation 1) in center/radius form.
+ * Replaces IntervalDomain.affine_transformer conv branch (domains/interval.py:57-74)
+ * and the input bounding box of runtime/crown_ibp.py:167-181.
+ * workspace: bf_ibp_conv2d_workspace(B, Ci*Hi*Wi, Co*Ho*Wo) floats. */
+int bf_ibp_conv2d(const float* in_lo, const float* in_hi, int64_t B, int Ci, int Hi, int Wi, int input_kind,
+                  float eps, int apply_relu, const float* W, const float* bias, int Co, int KH, int KW, int sh,
+                  int sw, int ph, int pw, int Ho, int Wo, const int8_t* split, int64_t split_ld, float* workspace,
+                  float* out_lo, float* out_hi, float* center_out, int* infeasible, hipStream_t stream);
+int64_t bf_ibp_conv2d_workspace(int64_t B, int64_t nin, int64_t nout);
+
+/* Intersection with external pre-activation constraints and a split
+ * (runtime/crown_ibp.py:186-209), in place; flags infeasible domains. */
+int bf_interval_clip(float* lo, float* hi, const float* clo, const float* chi, const int8_t* split,
+                     int64_t split_ld, int64_t B, int64_t N, int* infeasible, hipStream_t stream);
+
+/* ---- kernels #2 + #3: CROWN backward, fused ReLU relaxation + contraction -- */
+
+/* One ReLU -> Linear region: A' = relax(A) (upper: sel(A>=0, alpha_u, alpha_l),
+ * lower mirrored, plus the optional beta split coefficient add_l on the lower
+ * bound), A_prev = A' @ W on fp32 MFMA, and
+ * b_out = (b_in + sum_k A * beta_sel) + sum_k A' * bias.
+ * Replaces FusedCrownExecutor.run for "fused_relu_linear"
+ * (runtime/fused_crown.py:97-123, reference equations :330-400) and the dense
+ * ReLU step + linear step of runtime/crown_ibp.py:1073-1090, 1211-1298.
+ * A rows: A + d*a_dstride + s*N (a_dstride = S*N, or 0 when every domain
+ * shares the same S rows).  pre_lo/pre_hi NULL = no relaxation (identity).
+ * alpha: lower-slope override [D,N] (alpha_ld N) or shared (alpha_ld 0),
+ * clamped to [0,1] and used on ambiguous neurons only (crown_ibp.py:1176-1208).
+ * Either bound may be NULL (input and output together). */
+int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
+                             const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
+                             const float* add_l, int64_t add_ld, const float* W, int64_t P, const float* bias,
+                             const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
+                             float* b_u_out, float* b_l_out, hipStream_t stream);
+
+/* The input-layer region fused with the concretization (kernel #4):
+ * lb = (A' . cvec - eps * sum_i |(A' W)_i| * rad_i) + b, ub mirrored;
+ * rad NULL = Linf (weights 1, eps used), else box radius [D, I] (eps ignored).
+ * cvec = center @ W^T per domain [D, N].  Replaces concretize_affine
+ * (runtime/perturbation.py:175-222, 327-359) on RightMatmulLinearOperator
+ * (runtime/linear_operator.py:503-586) as called at runtime/crown_ibp.py:2044-2051.
+ * h_scale/h_out (optional, lower bound only): h = h_scale[m] * sign(A'W) * rad,
+ * the gradient seed of the concretization.
+ * workspace: bf_crown_relu_linear_concretize_workspace(D, S, I) floats. */
+int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
+                                    int64_t N, const float* pre_lo, const float* pre_hi, const float* alpha,
+                                    int64_t alpha_ld, const float* add_l, int64_t add_ld, const float* W, int64_t I,
+                                    const float* bias, const float* cvec, const float* rad, float eps,
+                                    const float* b_u_in, const float* b_l_in, const float* h_scale, float* h_out,
+                                    float* workspace, float* lb, float* ub, hipStream_t stream);
+int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I);
+
+/* Standalone relaxation pass (bandwidth-bound form of kernel #3): writes A'
+ * and the bias/center row sums.  Replaces _backprop_relu_step_dense_reference
+ * (runtime/crown_ibp.py:1211-1298); used ahead of the conv transposed
+ * contraction.  kbias: per-element bias of the affine layer [K]; cvec: center
+ * projection [D, K] (optional). */
+int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* pre_lo,
+                        const float* pre_hi, const float* alpha, int64_t alpha_ld, const float* add_l,
+                        int64_t add_ld, const float* kbias, const float* cvec, const float* b_u_in,
+                        const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out, float* b_l_out,
+                        float* c_u_out, float* c_l_out, hipStream_t stream);
+
+/* Transposed convolution of coefficient rows (Conv2dLinearOperator.to_dense,
+ * runtime/linear_operator.py:1067-1092; FusedCrownExecutor "fused_relu_conv2d"
+ * after bf_crown_relu_relax).  With norm_u/norm_l instead of y_u/y_l the
+ * output rows are reduced to sum |y| (* wvec[d, e]) -- the concretization norm
+ * of the input layer (linear_operator.py:1378-1452 + perturbation.py:175-222). */
+int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co, int Ho, int Wo, const float* W,
+                           int Ci, int KH, int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
+                           float* y_l, int64_t S, const float* wvec, int64_t w_ld, float* norm_u, float* norm_l,
+                           const float* h_scale, float* h_out, hipStream_t stream);
+
+/* Convolution of rows (IBP center/radius, center projection x0 conv W, and the
+ * gradient of a transposed convolution), plus optional rank-1 term
+ * y[r] += row_scale[r] * vec[(r / vec_div) * vec_ld + e]. */
+int bf_conv2d_rows(const float* x, int64_t in_div, int64_t R, int Ci, int Hi, int Wi, const float* W, int abs_w,
+                   int Co, int KH, int KW, int sh, int sw, int ph, int pw, int Ho, int Wo, float* y,
+                   const float* row_scale, const float* vec, int64_t vec_div, int64_t vec_ld, hipStream_t stream);
+
+/* Plain fp32 MFMA contraction C = A @ op(B) (op = transpose when trans_b,
+ * |.| when abs_b): the lazy A @ W of RightMatmulLinearOperator.to_dense
+ * (runtime/linear_operator.py:585-586). */
+int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, int abs_b, float* C, int64_t ldc,
+            int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* Contraction with a rank-1 epilogue C[m,n] = (A @ op(B))[m,n] + r_row[m] * v_col[(m/S)*v_ld + n]:
+ * the transposed contraction of the gradient pass with the bias terms. */
+int bf_gemm_rank1(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, float* C, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, int64_t S, const float* r_row, const float* v_col, int64_t v_ld,
+                  hipStream_t stream);
+
+/* ---- kernel #4: concretization -------------------------------------------- */
+
+/* Dense coefficient rows A [M, I] against the input set:
+ * out = A . center[d] -/+ eps * sum |A| (Linf, rad NULL) or -/+ sum |A| * rad[d] (box), + b.
+ * Replaces LpBallPerturbation/BoxPerturbation.concretize_affine on a
+ * DenseLinearOperator (runtime/perturbation.py:175-222, 327-359;
+ * runtime/linear_operator.py:354-372).  is_lower selects the sign. */
+int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
+                        float eps, const float* b, int is_lower, float* out, hipStream_t stream);
+
+/* lb = (cen_l - eps * sum_q partial_l[q]) + b_l (ub mirrored), fixed-order sum over nparts. */
+int bf_concretize_finalize(const float* partial_u, const float* partial_l, int nparts, int64_t M,
+                           const float* cen_u, const float* cen_l, const float* b_u, const float* b_l, float eps,
+                           float* lb, float* ub, hipStream_t stream);
+
+/* ---- kernel #5: alpha / beta gradients and the optimiser ------------------ */
+
+/* Reverse pass through one ReLU relaxation of the lower bound: g_in = dL/dA,
+ * g_alpha = dL/dalpha [D,N], g_beta = dL/dbeta [D,N] (see bf_grad.hip).
+ * Replaces the autograd backward of runtime/crown_ibp.py:1211-1298 driven by
+ * runtime/alpha_beta_crown.py:913-923 / runtime/alpha_crown.py:236-246. */
+int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
+                 const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, const float* G,
+                 const int8_t* split, int64_t split_ld, float* g_in, float* g_alpha, float* g_beta,
+                 hipStream_t stream);
+
+/* beta split coefficient add = -beta * s * 1(s != 0) (runtime/alpha_beta_crown.py:615-640). */
+int bf_beta_coeff(const float* beta, int64_t beta_ld, const int8_t* split, int64_t split_ld, int64_t D, int64_t N,
+                  float* out, hipStream_t stream);
+
+/* torch.optim.Adam step (no weight decay / amsgrad) then clamp to [lo, hi]
+ * (hi only when has_clamp_hi), in place (runtime/alpha_beta_crown.py:747, 918-923). */
+int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, double lr, double beta1,
+                       double beta2, float eps, int step, float clamp_lo, float clamp_hi, int has_clamp_hi,
+                       hipStream_t stream);
+
+/* Per-domain best-of tracking on mean_s lb (runtime/alpha_beta_crown.py:840-876). */
+int bf_best_update(const float* lb, const float* ub, int64_t D, int64_t S, float* best_metric, float* best_lb,
+                   float* best_ub, int* improved, int first, hipStream_t stream);
+int bf_masked_copy_rows(float* dst, const float* src, int64_t D, int64_t N, const int* mask, hipStream_t stream);
+
+/* out[n] = sum_d x[d, n] (gradient of a parameter shared by all domains). */
+int bf_sum_rows(const float* x, int64_t D, int64_t N, float* out, hipStream_t stream);
+
+/* "alpha from CROWN" init (runtime/native_alpha_beta_optimizer_schedule.py:635-653). */
+int bf_alpha_from_crown(const float* lo, const float* hi, int64_t n, float* out, hipStream_t stream);
+
+/* ---- BaB decisions ----------------------------------------------------------- */
+
+/* Branching rule update for one ReLU layer (runtime/alpha_beta_crown.py:145-182):
+ * widest ambiguous neuron, first index on ties, strictly wider to replace. */
+int bf_branch_update(const float* lo, const float* hi, int64_t D, int64_t N, int layer, float* best_gap,
+                     int* best_layer, int* best_idx, hipStream_t stream);
+
+/* Node verdict (runtime/bab.py:870-895): 1 certified (min_s lb >= threshold - tol),
+ * 2 infeasible split, 0 open. */
+int bf_domain_status(const float* lb, int64_t D, int64_t S, const int* infeasible, float threshold, float tol,
+                     int* status, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BOUNDFLOW_HIP_H */

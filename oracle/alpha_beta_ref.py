@@ -284,8 +284,8 @@ def evaluate_domain_batch(
     idx = feasible.nonzero(as_tuple=False).flatten()
     D = int(spec.center.shape[0])
     S = int(linear_spec_C.shape[1])
-    lower = torch.full((D, S), float("nan"))
-    upper = torch.full((D, S), float("nan"))
+    lower = torch.full((D, S), float("nan"), dtype=spec.center.dtype)
+    upper = torch.full((D, S), float("nan"), dtype=spec.center.dtype)
     branch: List[Optional[Tuple[str, int]]] = [None] * D
     if idx.numel() > 0:
         sub_spec = InputSpec(value_name=spec.value_name, center=spec.center[idx], perturbation=spec.perturbation)

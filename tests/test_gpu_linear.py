@@ -165,8 +165,8 @@ def test_relax_pass_and_dense_concretize_match_oracle():
     out = [torch.empty(D * S, K, device=dev), torch.empty(D * S, K, device=dev), torch.empty(D * S, device=dev),
            torch.empty(D * S, device=dev)]
     _lib.call("bf_crown_relu_relax", _lib.ptr(d[0]), _lib.ptr(d[1]), D, S, K, _lib.ptr(d[2]), _lib.ptr(d[3]),
-              _lib.ptr(d[4]), K, _lib.ptr(d[5]), K, None, _lib.ptr(d[6]), _lib.ptr(d[7]), _lib.ptr(out[0]),
-              _lib.ptr(out[1]), _lib.ptr(out[2]), _lib.ptr(out[3]), _lib.stream_handle())
+              _lib.ptr(d[4]), K, _lib.ptr(d[5]), K, None, None, _lib.ptr(d[6]), _lib.ptr(d[7]), _lib.ptr(out[0]),
+              _lib.ptr(out[1]), _lib.ptr(out[2]), _lib.ptr(out[3]), None, None, _lib.stream_handle())
     torch.cuda.synchronize()
     assert torch.equal(out[0].cpu().reshape(D, S, K), ref[0])
     assert torch.equal(out[1].cpu().reshape(D, S, K), ref[1])
