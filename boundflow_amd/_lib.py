@@ -27,18 +27,23 @@ F64 = ctypes.c_double
 SIGNATURES = {
     "bf_abi_version": (I32, []),
     "bf_last_error": (ctypes.c_char_p, []),
+    "bf_tuning_set_gemm_tile": (I32, [I32]),
     "bf_gemm": (I32, [P, I64, P, I64, I32, I32, P, I64, I64, I64, I64, P]),
     "bf_gemm_rank1": (I32, [P, I64, P, I64, I32, P, I64, I64, I64, I64, I64, P, P, I64, P]),
-    "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, P, I64, P, P, P, P, P, P, P,
-                                       P]),
-    "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, P, I64, P, P, P, F32,
-                                              P, P, P, P, P, P, P, P]),
+    "bf_relu_relax_table": (I32, [P, P, P, I64, I64, I64, P, P]),
+    "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, P, P, P, P, P, P, P, P]),
+    "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, P, P, P, F32, P, P, P, P,
+                                              P, P, P, P]),
     "bf_crown_relu_linear_concretize_workspace": (I64, [I64, I64, I64]),
-    "bf_crown_relu_relax": (I32, [P, P, I64, I64, I64, P, P, P, I64, P, I64, P, P, P, P, P, P, P, P, P, P, P]),
+    "bf_crown_relu_relax": (I32, [P, P, I64, I64, I64, P, P, I64, P, P, P, P, P, P, P, P, P, P, P]),
     "bf_concretize_dense": (I32, [P, I64, I64, I64, P, P, F32, P, I32, P, P]),
     "bf_ibp_linear": (I32, [P, P, I64, I64, I32, F32, I32, P, P, I64, P, I64, P, P, P, P, P, P]),
     "bf_ibp_linear_workspace": (I64, [I64, I64, I64]),
     "bf_interval_clip": (I32, [P, P, P, P, P, I64, I64, I64, P, P]),
+    "bf_interval_relu": (I32, [P, P, I64, P, P, P]),
+    "bf_interval_add": (I32, [P, P, P, P, I64, P, P, P]),
+    "bf_spec_linear": (I32, [P, P, P, I64, I64, I64, P, P, P]),
+    "bf_ibp_batched_linear": (I32, [P, P, I64, I64, P, P, I64, P, P, P]),
     "bf_branch_update": (I32, [P, P, I64, I64, I32, P, P, P, P]),
     "bf_adam_clamp_step": (I32, [P, P, P, P, I64, F64, F64, F64, F32, I32, F32, F32, I32, P]),
     "bf_conv2d_rows": (I32, [P, I64, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P, P,

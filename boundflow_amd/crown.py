@@ -355,6 +355,12 @@ def crown_backward(
                                           f"relu_pre_add_coeff_l[{relax_name}]")
         pre_lo = None if pre is None else pre.lower.reshape(B, N)
         pre_hi = None if pre is None else pre.upper.reshape(B, N)
+        relax = None
+        if pre is not None and layer.kind == "linear":
+            # slopes/intercepts once per (domain, neuron), shared by both bounds
+            relax = torch.empty(B, N, 4, device=dev, dtype=torch.float32)
+            _lib.call("bf_relu_relax_table", _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, B, N,
+                      _lib.ptr(relax), stream)
         if save is not None and A_l is not None:
             save.setdefault("A_in", {})[k] = (A_l, stride)
             save.setdefault("b_in", {})[k] = b_l
@@ -406,8 +412,7 @@ def crown_backward(
             nz = int(A_u is not None) + int(A_l is not None)
             with _timed("crown_relu_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
                 _lib.call("bf_crown_relu_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
-                          _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld,
-                          _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(cvec), _lib.ptr(rad), eps, _lib.ptr(b_u),
+                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(cvec), _lib.ptr(rad), eps, _lib.ptr(b_u),
                           _lib.ptr(b_l), _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(ws), _lib.ptr(lb),
                           _lib.ptr(ub), stream)
             if save is not None:
@@ -421,8 +426,7 @@ def crown_backward(
         a_rows = M if stride != 0 else S
         with _timed("crown_relu_linear_fwd", 2.0 * nz * M * N * P, 4.0 * nz * (a_rows * N + N * P + M * P)):
             _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
-                      _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld,
-                      _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(nA_u),
+                      _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(nA_u),
                       _lib.ptr(nA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), stream)
         A_u, A_l, b_u, b_l = nA_u, nA_l, nb_u, nb_l
         stride = S * P

@@ -5,18 +5,24 @@
 // M = domains x specs (the coefficient rows), K = current-layer neurons,
 // N = previous-layer neurons.  A' is either A itself or A after the ReLU
 // relaxation of the layer (boundflow/runtime/crown_ibp.py:1211-1298), applied
-// while the A tile is staged into LDS; the row reductions the relaxation needs
-// (the bias terms sum_k A * beta_sel and sum_k A' * bias_k, and optionally a
-// center term sum_k A' * c_k) are produced in the same pass.  The epilogue
-// either stores C or reduces |C| (optionally weighted) along each row, which is
-// the Linf / box concretization norm (boundflow/runtime/perturbation.py:175-222,
-// 327-359) fused so that the final [M, input] coefficient never reaches HBM.
+// while the A tile is staged into LDS from a per-(domain, neuron) table of
+// slopes/intercepts; the row reductions the relaxation needs (the bias terms
+// sum_k A * beta_sel and sum_k A' * bias_k, and optionally a center term
+// sum_k A' * c_k) are produced in the same pass.  The epilogue either stores C
+// (optionally plus a rank-1 term) or reduces |C| (optionally weighted) along
+// each row -- the Linf / box concretization norm
+// (boundflow/runtime/perturbation.py:175-222, 327-359) fused so that the final
+// [M, input] coefficient never reaches HBM.
 //
-// Tiling: 256 threads = 4 wave64s, block tile 128 x 128, K tile 16, each wave
-// owns a 64 x 64 sub-tile computed with 2 x 2 v_mfma_f32_32x32x2f32 ops per
-// k-pair.  A and B tiles are stored k-major in LDS (pitch +4 floats) and
-// double-buffered; global loads of tile k+1 are in flight while tile k feeds
-// the matrix cores.
+// Tiling (template Tile<BM, BN, BK, NWM, NWN, OCC>): NWM x NWN wave64s per
+// workgroup, each owning a (BM/NWM) x (BN/NWN) sub-tile of 32 x 32
+// v_mfma_f32_32x32x2f32 blocks.  The two lane halves of a wave take the two
+// halves of the K tile (a fixed permutation of the reduction order), so a
+// lane's A (and transposed B) operands for four consecutive k-steps are one
+// 128-bit LDS read.  Global tiles are read as float4 and double-buffered in LDS
+// with one barrier per K tile.  Workgroups are mapped to tiles XCD-aware: each
+// of the 8 XCDs receives a contiguous run of tiles, so the column tiles that
+// share an A row-block share that XCD's L2.
 
 #include "bf_common.h"
 #include "bf_gemm_args.h"
@@ -25,151 +31,197 @@ namespace bf {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int GBM = 128;
-constexpr int GBN = 128;
-constexpr int GBK = 16;
-constexpr int GNT = 256;
-constexpr int APITCH = GBM + 4;
-constexpr int BPITCH = GBN + 4;
-constexpr int A_PER_T = GBM * GBK / GNT;  // 8
-constexpr int B_PER_T = GBN * GBK / GNT;  // 8
+// Partial-norm granularity of the |C| epilogue (columns per partial sum); every
+// tile configuration used with EPI_ABSSUM has BN == NORM_BN.
+constexpr int NORM_BN = 128;
 
-__device__ __forceinline__ float select_scale(float a, const Relax& r, bool lower, float* beta_sel) {
+template <int BM_, int BN_, int BK_, int NWM_, int NWN_, int OCC_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, NWM = NWM_, NWN = NWN_, OCC = OCC_;
+  static constexpr int NT = 64 * NWM * NWN;          // threads
+  static constexpr int WTM = BM / NWM;               // wave tile rows
+  static constexpr int WTN = BN / NWN;               // wave tile cols
+  static constexpr int FM = WTM / 32;                // 32x32 MFMA blocks per wave (rows)
+  static constexpr int FN = WTN / 32;                // (cols)
+  static constexpr int AP = BK + 4;                  // As row pitch (row-major along k)
+  static constexpr int BPT = BK + 4;                 // Bs row pitch (n-major [n][k], for either B layout)
+  static constexpr int KQ = BK / 4;                  // float4 per A row per K tile
+  static constexpr int A_SLOTS = BM * BK / 4 / NT;
+  static constexpr int B_SLOTS = BN * BK / 4 / NT;
+  static constexpr int RPP = NT / KQ;                // A rows covered per slot index
+  static constexpr int BS_FLOATS = BN * BPT;
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert((BM * BK) % (4 * NT) == 0 && (BN * BK) % (4 * NT) == 0, "tile/thread mismatch");
+  static_assert((BK & (BK - 1)) == 0 && BK >= 8, "BK must be a power of two >= 8");
+};
+
+__device__ __forceinline__ float fsel(const float4& r, bool lower, bool nonneg, float* beta) {
   // upper: A >= 0 -> (alpha_u, beta_u) else (alpha_l, beta_l); lower: mirrored
-  const bool nonneg = a >= 0.f;
-  float al, be;
-  if (lower) {
-    al = nonneg ? r.al : r.au;
-    be = nonneg ? r.bl : r.bu;
-  } else {
-    al = nonneg ? r.au : r.al;
-    be = nonneg ? r.bu : r.bl;
-  }
-  *beta_sel = be;
-  return al;
+  const bool use_u = lower ? !nonneg : nonneg;
+  *beta = use_u ? r.y : r.w;
+  return use_u ? r.x : r.z;
 }
 
-template <int PRO, int EPI, bool TRANS_B>
-__global__ void __launch_bounds__(GNT)
+template <int PRO, int EPI, bool TRANS_B, class T>
+__global__ void __launch_bounds__(T::NT, T::OCC)
 gemm_kernel(GemmArgs p) {
-  __shared__ float As[2][GBK][APITCH];
-  __shared__ float Bs[2][GBK][BPITCH];
-  __shared__ float red[2][GBM];
+  constexpr int GBM = T::BM, GBN = T::BN, GBK = T::BK, GNT = T::NT;
+  constexpr int AP = T::AP, BPT = T::BPT, A_SLOTS = T::A_SLOTS, B_SLOTS = T::B_SLOTS;
+  constexpr int KQ = T::KQ, RPP = T::RPP, FM = T::FM, FN = T::FN;
+  __shared__ __attribute__((aligned(16))) float As[2][GBM * AP];
+  __shared__ __attribute__((aligned(16))) float Bs[2][T::BS_FLOATS];
+  __shared__ float red[T::NWN][GBM];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
-  const int z = blockIdx.z;
+  const int wm = wave / T::NWN;
+  const int wn = wave % T::NWN;
+  const int z = blockIdx.y;
   const bool lower = p.z_lower_first ? (z == 0) : (z == 1);
   const float* __restrict__ A = p.A[z];
-  const int64_t m0 = (int64_t)blockIdx.x * GBM;
-  const int64_t n0 = (int64_t)blockIdx.y * GBN;
   const int64_t M = p.M, N = p.N, K = p.K;
-  const bool row_reduce = (PRO == PRO_RELAX) && (blockIdx.y == 0);
+  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs, so
+  // give each XCD a contiguous run of tiles in row-major (n fastest) order.
+  const int64_t ntn = ceil_div(N, GBN);
+  const int64_t ntiles = ceil_div(M, GBM) * ntn;
+  const int64_t per_xcd = ceil_div(ntiles, 8);
+  const int64_t tile = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (tile >= ntiles) return;
+  const int64_t tile_n = tile % ntn;
+  const int64_t m0 = (tile / ntn) * GBM;
+  const int64_t n0 = tile_n * GBN;
+  const bool row_reduce = (PRO == PRO_RELAX) && (tile_n == 0);
+  const bool vec_a = ((K & 3) == 0) && ((p.lda & 3) == 0) && ((p.lda_d & 3) == 0) && (((uintptr_t)A & 15) == 0);
+  const bool vec_b = TRANS_B ? (((K & 3) == 0) && ((p.ldb & 3) == 0) && (((uintptr_t)p.B & 15) == 0))
+                             : (((N & 3) == 0) && ((p.ldb & 3) == 0) && (((uintptr_t)p.B & 15) == 0));
 
-  // A-tile element ownership: e = t + GNT*j -> row = e / GBK, kk = e % GBK
-  const int a_kk = t % GBK;
-  const int a_r0 = t / GBK;  // rows a_r0 + 16*j
-  int64_t a_dom[A_PER_T];
-  float s_beta[A_PER_T], s_bias[A_PER_T], s_cen[A_PER_T];
+  // A-tile ownership: float4 slot q = t + GNT*j -> row (t / KQ) + RPP*j, k quad (t % KQ)
+  const int a_kq = t % KQ;
+  const int a_r0 = t / KQ;
+  int64_t a_base[A_SLOTS];
+  int64_t a_dom[A_SLOTS];
+  float s_beta[A_SLOTS], s_bias[A_SLOTS], s_cen[A_SLOTS];
 #pragma unroll
-  for (int j = 0; j < A_PER_T; ++j) {
-    int64_t m = m0 + a_r0 + 16 * j;
-    a_dom[j] = (PRO == PRO_RELAX) ? (m < M ? m / p.S : 0) : 0;
-    s_beta[j] = 0.f; s_bias[j] = 0.f; s_cen[j] = 0.f;
+  for (int j = 0; j < A_SLOTS; ++j) {
+    const int64_t m = m0 + a_r0 + RPP * j;
+    const int64_t mm = m < M ? m : 0;
+    a_dom[j] = mm / p.S;
+    a_base[j] = a_dom[j] * p.lda_d + (mm - a_dom[j] * p.S) * p.lda;
+    s_beta[j] = 0.f;
+    s_bias[j] = 0.f;
+    s_cen[j] = 0.f;
   }
 
-  float a_reg[A_PER_T];
-  float b_reg[B_PER_T];
-
-  // A row base offsets (rows are d*S + s; see GemmArgs::lda_d)
-  int64_t a_base[A_PER_T];
-#pragma unroll
-  for (int j = 0; j < A_PER_T; ++j) {
-    int64_t m = m0 + a_r0 + 16 * j;
-    int64_t mm = m < M ? m : 0;
-    a_base[j] = (mm / p.S) * p.lda_d + (mm % p.S) * p.lda;
-  }
+  float4 a_reg[A_SLOTS];
+  float4 b_reg[B_SLOTS];
 
   auto load_tiles = [&](int64_t k0) {
 #pragma unroll
-    for (int j = 0; j < A_PER_T; ++j) {
-      int64_t m = m0 + a_r0 + 16 * j;
-      int64_t k = k0 + a_kk;
-      a_reg[j] = (m < M && k < K) ? A[a_base[j] + k] : 0.f;
+    for (int j = 0; j < A_SLOTS; ++j) {
+      const int64_t m = m0 + a_r0 + RPP * j;
+      const int64_t k = k0 + 4 * a_kq;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (m < M) {
+        const float* src = A + a_base[j] + k;
+        if (vec_a) {
+          if (k < K) v = *reinterpret_cast<const float4*>(src);
+        } else {
+          if (k + 0 < K) v.x = src[0];
+          if (k + 1 < K) v.y = src[1];
+          if (k + 2 < K) v.z = src[2];
+          if (k + 3 < K) v.w = src[3];
+        }
+      }
+      a_reg[j] = v;
     }
 #pragma unroll
-    for (int j = 0; j < B_PER_T; ++j) {
-      int e = t + GNT * j;
-      float v;
+    for (int j = 0; j < B_SLOTS; ++j) {
+      const int q = t + GNT * j;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (TRANS_B) {
-        int n = e / GBK, kk = e % GBK;
-        int64_t gn = n0 + n, gk = k0 + kk;
-        v = (gn < N && gk < K) ? p.B[gn * p.ldb + gk] : 0.f;
+        const int n = q / KQ, kq = q % KQ;
+        const int64_t gn = n0 + n, gk = k0 + 4 * kq;
+        if (gn < N) {
+          const float* src = p.B + gn * p.ldb + gk;
+          if (vec_b) {
+            if (gk < K) v = *reinterpret_cast<const float4*>(src);
+          } else {
+            if (gk + 0 < K) v.x = src[0];
+            if (gk + 1 < K) v.y = src[1];
+            if (gk + 2 < K) v.z = src[2];
+            if (gk + 3 < K) v.w = src[3];
+          }
+        }
       } else {
-        int kk = e / GBN, n = e % GBN;
-        int64_t gn = n0 + n, gk = k0 + kk;
-        v = (gn < N && gk < K) ? p.B[gk * p.ldb + gn] : 0.f;
+        // B given as [K, N]: thread reads 4 consecutive k of one column n (each of
+        // the 4 loads is coalesced across the wave), stored as one n-major float4.
+        const int n = q % GBN, kq = q / GBN;
+        const int64_t gn = n0 + n, gk = k0 + 4 * kq;
+        if (gn < N) {
+          const float* src = p.B + gk * p.ldb + gn;
+          if (gk + 0 < K) v.x = src[0];
+          if (gk + 1 < K) v.y = src[p.ldb];
+          if (gk + 2 < K) v.z = src[2 * p.ldb];
+          if (gk + 3 < K) v.w = src[3 * p.ldb];
+        }
       }
-      b_reg[j] = p.abs_b ? fabsf(v) : v;
+      if (p.abs_b) {
+        v.x = fabsf(v.x); v.y = fabsf(v.y); v.z = fabsf(v.z); v.w = fabsf(v.w);
+      }
+      b_reg[j] = v;
     }
+  };
+
+  const bool use_add = (PRO == PRO_RELAX) && lower && (p.add_l != nullptr);
+
+  // ReLU relaxation of one coefficient (crown_ibp.py:1261-1296), applied as the
+  // A tile is written to LDS; padding elements (outside M or K) stay zero.
+  // The table entries are read here rather than with the A tile: holding them
+  // across the MFMA loop costs more occupancy than their latency does.
+  auto relax_one = [&](float a, int j, int64_t k) -> float {
+    if (k >= K) return a;
+    const int64_t d = a_dom[j];
+    const float4 r = p.relax ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
+    float be;
+    float out = a * fsel(r, lower, a >= 0.f, &be);
+    if (use_add) out = out + p.add_l[d * p.add_ld + k];
+    if (row_reduce) {
+      s_beta[j] += a * be;
+      if (p.kbias) s_bias[j] += out * p.kbias[k];
+      if (p.cvec) s_cen[j] += out * p.cvec[d * p.cvec_ld + k];
+    }
+    return out;
   };
 
   auto store_tiles = [&](int buf, int64_t k0) {
 #pragma unroll
-    for (int j = 0; j < A_PER_T; ++j) {
-      int r = a_r0 + 16 * j;
-      float v = a_reg[j];
-      if (PRO == PRO_RELAX) {
-        int64_t m = m0 + r;
-        int64_t k = k0 + a_kk;
-        if (m < M && k < K) {
-          const int64_t d = a_dom[j];
-          float be = 0.f;
-          float out = v;
-          if (p.pre_lo) {
-            const float l = p.pre_lo[d * p.ld_pre + k];
-            const float u = p.pre_hi[d * p.ld_pre + k];
-            float alpha = 0.f;
-            const bool has_alpha = p.alpha != nullptr;
-            if (has_alpha) alpha = clamp01(p.alpha[d * p.alpha_ld + k]);
-            Relax rx = relu_relax(l, u, has_alpha, alpha);
-            float sc = select_scale(v, rx, lower, &be);
-            out = v * sc;
-            if (lower && p.add_l) out = out + p.add_l[d * p.add_ld + k];
-          }
-          if (row_reduce) {
-            s_beta[j] += v * be;
-            if (p.kbias) s_bias[j] += out * p.kbias[k];
-            if (p.cvec) s_cen[j] += out * p.cvec[d * p.cvec_ld + k];
-          }
-          v = out;
-        } else {
-          v = 0.f;
-        }
+    for (int j = 0; j < A_SLOTS; ++j) {
+      const int r = a_r0 + RPP * j;
+      float4 v = a_reg[j];
+      if (PRO == PRO_RELAX && m0 + r < M) {
+        const int64_t k = k0 + 4 * a_kq;
+        v.x = relax_one(v.x, j, k + 0);
+        v.y = relax_one(v.y, j, k + 1);
+        v.z = relax_one(v.z, j, k + 2);
+        v.w = relax_one(v.w, j, k + 3);
       }
-      As[buf][a_kk][r] = v;
+      *reinterpret_cast<float4*>(&As[buf][r * AP + 4 * a_kq]) = v;
     }
 #pragma unroll
-    for (int j = 0; j < B_PER_T; ++j) {
-      int e = t + GNT * j;
-      if (TRANS_B) {
-        int n = e / GBK, kk = e % GBK;
-        Bs[buf][kk][n] = b_reg[j];
-      } else {
-        int kk = e / GBN, n = e % GBN;
-        Bs[buf][kk][n] = b_reg[j];
-      }
+    for (int j = 0; j < B_SLOTS; ++j) {
+      const int q = t + GNT * j;
+      const int n = TRANS_B ? q / KQ : q % GBN;
+      const int kq = TRANS_B ? q % KQ : q / GBN;
+      *reinterpret_cast<float4*>(&Bs[buf][n * BPT + 4 * kq]) = b_reg[j];
     }
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -179,43 +231,56 @@ gemm_kernel(GemmArgs p) {
   __syncthreads();
   int buf = 0;
   const int lrow = lane & 31;
-  const int lk = lane >> 5;
+  const int h = lane >> 5;   // lane half -> k half of the tile
   for (int64_t kt = 0; kt < nk; ++kt) {
     const bool more = kt + 1 < nk;
     if (more) load_tiles((kt + 1) * GBK);
+    const float* __restrict__ as = As[buf];
+    const float* __restrict__ bs = Bs[buf];
 #pragma unroll
-    for (int kk = 0; kk < GBK; kk += 2) {
-      float af[2], bfr[2];
+    for (int jb = 0; jb < GBK / 2; jb += 4) {
+      float av[FM][4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = As[buf][kk + lk][wm * 64 + i * 32 + lrow];
+      for (int i = 0; i < FM; ++i) {
+        const float4 a4 = *reinterpret_cast<const float4*>(
+            &as[(wm * T::WTM + i * 32 + lrow) * AP + h * (GBK / 2) + jb]);
+        av[i][0] = a4.x; av[i][1] = a4.y; av[i][2] = a4.z; av[i][3] = a4.w;
+      }
+      float bv[FN][4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bfr[j] = Bs[buf][kk + lk][wn * 64 + j * 32 + lrow];
+      for (int jj = 0; jj < FN; ++jj) {
+        const float4 b4 = *reinterpret_cast<const float4*>(
+            &bs[(wn * T::WTN + jj * 32 + lrow) * BPT + h * (GBK / 2) + jb]);
+        bv[jj][0] = b4.x; bv[jj][1] = b4.y; bv[jj][2] = b4.z; bv[jj][3] = b4.w;
+      }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int jj = 0; jj < FN; ++jj)
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
     }
     if (more) store_tiles(buf ^ 1, (kt + 1) * GBK);
     __syncthreads();
     buf ^= 1;
   }
 
-  // Row reductions of the relaxation prologue: the 16 threads holding one row
-  // are 16 consecutive lanes; reduce with xor shuffles in a fixed order.
+  // Row reductions of the relaxation prologue: the KQ threads holding one row
+  // are KQ consecutive lanes; reduce with xor shuffles in a fixed order.
   if (row_reduce) {
 #pragma unroll
-    for (int j = 0; j < A_PER_T; ++j) {
+    for (int j = 0; j < A_SLOTS; ++j) {
       float sb = s_beta[j], sk = s_bias[j], sc = s_cen[j];
 #pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) {
+      for (int off = KQ / 2; off >= 1; off >>= 1) {
         sb += __shfl_xor(sb, off, 64);
         sk += __shfl_xor(sk, off, 64);
         sc += __shfl_xor(sc, off, 64);
       }
-      int64_t m = m0 + a_r0 + 16 * j;
-      if (a_kk == 0 && m < M) {
-        float b0 = p.b_in[z] ? p.b_in[z][m] : 0.f;
+      const int64_t m = m0 + a_r0 + RPP * j;
+      if (a_kq == 0 && m < M) {
+        const float b0 = p.b_in[z] ? p.b_in[z][m] : 0.f;
         if (p.b_out[z]) p.b_out[z][m] = (b0 + sb) + sk;
         if (p.c_out[z]) p.c_out[z][m] = sc;
       }
@@ -225,13 +290,13 @@ gemm_kernel(GemmArgs p) {
   if (EPI == EPI_STORE) {
     float* __restrict__ C = p.C[z];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t col = n0 + wn * 64 + j * 32 + lrow;
+      for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           if (row < M && col < N) {
             float v = acc[i][j][r];
             if (p.r1_row) v = v + p.r1_row[row] * p.r1_col[(row / p.S) * p.r1_ld + col];
@@ -240,22 +305,23 @@ gemm_kernel(GemmArgs p) {
         }
       }
   } else {
-    // sum_n |C[m, n]| * w[d, n] over this block's 128 columns, fixed order.
-    float rs[2][16];
+    static_assert(EPI != EPI_ABSSUM || GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
+    // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order.
+    float rs[FM][16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int64_t d = (row < M) ? row / p.S : 0;
         float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int64_t col = n0 + wn * 64 + j * 32 + lrow;
+        for (int j = 0; j < FN; ++j) {
+          const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
           const float a = acc[i][j][r];
           float v = fabsf(a);
           float wgt = 1.f;
           if (p.wvec) {
-            int64_t d = (row < M) ? row / p.S : 0;
             wgt = (row < M && col < N) ? p.wvec[d * p.w_ld + col] : 0.f;
             v = v * wgt;
           }
@@ -268,9 +334,8 @@ gemm_kernel(GemmArgs p) {
         }
         rs[i][r] = s;
       }
-    // reduce across the 32 lanes that share a row set (lanes differ in column)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float s = rs[i][r];
@@ -280,17 +345,22 @@ gemm_kernel(GemmArgs p) {
       }
     if (lrow == 0) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int rloc = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+          const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           red[wn][rloc] = rs[i][r];
         }
     }
     __syncthreads();
-    if (t < GBM) {
-      int64_t row = m0 + t;
-      if (row < M) p.partial[z][(int64_t)blockIdx.y * M + row] = red[0][t] + red[1][t];
+    for (int rr = t; rr < GBM; rr += GNT) {
+      const int64_t row = m0 + rr;
+      if (row < M) {
+        float s = 0.f;
+#pragma unroll
+        for (int q = 0; q < T::NWN; ++q) s += red[q][rr];
+        p.partial[z][tile_n * M + row] = s;
+      }
     }
   }
 }
@@ -317,17 +387,60 @@ __global__ void concretize_finalize_kernel(const float* __restrict__ partial_u, 
   }
 }
 
-template <int PRO, int EPI>
-static int launch_gemm(const GemmArgs& a, int nz, hipStream_t stream) {
-  dim3 grid((unsigned)ceil_div(a.M, GBM), (unsigned)ceil_div(a.N, GBN), (unsigned)nz);
-  BF_REQUIRE(grid.x < (1u << 31) && grid.y <= 65535, "gemm grid too large (M=%lld N=%lld)", (long long)a.M,
-             (long long)a.N);
+// Slopes/intercepts of the ReLU relaxation per (domain, neuron)
+// (crown_ibp.py:722-758, 1176-1208): {alpha_u, beta_u, alpha_l, beta_l}, with the
+// optional lower-slope override clamp(alpha, 0, 1) on ambiguous neurons.
+__global__ void relax_table_kernel(const float* __restrict__ lo, const float* __restrict__ hi,
+                                   const float* __restrict__ alpha, int64_t alpha_ld, int64_t D, int64_t K,
+                                   float4* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D * K) return;
+  const int64_t d = i / K, k = i - (i / K) * K;
+  const bool has_alpha = alpha != nullptr;
+  const float a = has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f;
+  const Relax r = relu_relax(lo[i], hi[i], has_alpha, a);
+  out[i] = make_float4(r.au, r.bu, r.al, r.bl);
+}
+
+// Tile configurations (selected at run time by launch_gemm; a fixed one can be
+// forced through bf_tuning_set_gemm_tile).
+using TileA = Tile<128, 128, 16, 2, 2, 3>;   // 4 waves of 64x64, 3 workgroups per CU
+using TileB = Tile<128, 128, 32, 2, 2, 2>;   // deeper K tile, 2 workgroups per CU
+using TileC = Tile<256, 128, 16, 4, 2, 1>;   // 8 waves of 64x64
+using TileD = Tile<128, 256, 16, 2, 2, 2>;   // 4 waves of 64x128 (store epilogue only)
+using TileE = Tile<64, 128, 16, 1, 2, 4>;    // 2 waves of 64x64: more workgroups for short M
+using TileF = Tile<128, 128, 16, 2, 2, 2>;   // TileA at 2 workgroups per CU
+
+template <int PRO, int EPI, class T>
+static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
+  const int64_t ntiles = ceil_div(a.M, T::BM) * ceil_div(a.N, T::BN);
+  BF_REQUIRE(ntiles + 8 < (1LL << 31), "gemm grid too large (M=%lld N=%lld)", (long long)a.M, (long long)a.N);
+  dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), (unsigned)nz);
   if (a.trans_b)
-    hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true>), grid, dim3(GNT), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T>), grid, dim3(T::NT), 0, stream, a);
   else
-    hipLaunchKernelGGL((gemm_kernel<PRO, EPI, false>), grid, dim3(GNT), 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<PRO, EPI, false, T>), grid, dim3(T::NT), 0, stream, a);
   BF_LAUNCH_CHECK("gemm_kernel");
   return BF_OK;
+}
+
+static int g_force_config = -1;   // tuning hook: -1 = automatic
+
+template <int PRO, int EPI>
+static int launch_gemm(const GemmArgs& a, int nz, hipStream_t stream) {
+  int cfg = g_force_config;
+  if (cfg < 0) cfg = 0;
+  switch (cfg) {
+    case 1: return launch_gemm_t<PRO, EPI, TileB>(a, nz, stream);
+    case 2: return launch_gemm_t<PRO, EPI, TileC>(a, nz, stream);
+    case 3:
+      // the |C| epilogue needs BN == NORM_BN; TileD is a store-only configuration
+      if (EPI == EPI_STORE) return launch_gemm_t<PRO, EPI_STORE, TileD>(a, nz, stream);
+      return launch_gemm_t<PRO, EPI, TileA>(a, nz, stream);
+    case 4: return launch_gemm_t<PRO, EPI, TileE>(a, nz, stream);
+    case 5: return launch_gemm_t<PRO, EPI, TileF>(a, nz, stream);
+    default: return launch_gemm_t<PRO, EPI, TileA>(a, nz, stream);
+  }
 }
 
 int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {
@@ -339,6 +452,8 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
   return BF_EINVAL;
 }
 
+void gemm_force_config(int cfg) { g_force_config = cfg; }
+
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
                         const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream) {
   if (M == 0) return BF_OK;
@@ -348,6 +463,15 @@ int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M,
   return BF_OK;
 }
 
-int gemm_partial_count(int64_t N) { return (int)ceil_div(N, GBN); }
+int relax_table(const float* lo, const float* hi, const float* alpha, int64_t alpha_ld, int64_t D, int64_t K,
+                float4* out, hipStream_t stream) {
+  if (D * K == 0) return BF_OK;
+  hipLaunchKernelGGL(relax_table_kernel, dim3((unsigned)ceil_div(D * K, 256)), dim3(256), 0, stream, lo, hi, alpha,
+                     alpha_ld, D, K, out);
+  BF_LAUNCH_CHECK("relax_table_kernel");
+  return BF_OK;
+}
+
+int gemm_partial_count(int64_t N) { return (int)ceil_div(N, NORM_BN); }
 
 }  // namespace bf

@@ -24,11 +24,7 @@ struct GemmArgs {
 
   // --- ReLU relaxation prologue (PRO_RELAX) ---
   int64_t S;                 // rows per domain
-  const float* pre_lo;       // [D, K] (row stride ld_pre); null = identity (no relaxation, row sums only)
-  const float* pre_hi;
-  int64_t ld_pre;
-  const float* alpha;        // optional lower-slope override, [D, K] with row stride alpha_ld (0 = shared)
-  int64_t alpha_ld;
+  const float4* relax;       // [D, K] {alpha_u, beta_u, alpha_l, beta_l}; null = identity (row sums only)
   const float* add_l;        // optional coefficient added to the lower A' (beta split term), row stride add_ld
   int64_t add_ld;
   const float* kbias;        // optional [K] bias of the affine layer: sum_k A'[m,k] * kbias[k]

@@ -30,6 +30,9 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
                         const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream);
 int gemm_partial_count(int64_t N);
+void gemm_force_config(int cfg);
+int relax_table(const float* lo, const float* hi, const float* alpha, int64_t alpha_ld, int64_t D, int64_t K,
+                float4* out, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // IBP helpers (center/radius form)
@@ -149,14 +152,85 @@ __global__ void interval_clip_kernel(float* __restrict__ lo, float* __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// Op-by-op interval kernels of the IBP task executor
+// (boundflow/runtime/task_executor.py:360-563).
+
+// relu(l), relu(u)  (domains/interval.py:88-91)
+__global__ void interval_relu_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int64_t n,
+                                     float* __restrict__ olo, float* __restrict__ ohi) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  olo[i] = fmaxf(lo[i], 0.f);
+  ohi[i] = fmaxf(hi[i], 0.f);
+}
+
+// [a_l + b_l, a_u + b_u]  (task_executor.py:476-490)
+__global__ void interval_add_kernel(const float* __restrict__ alo, const float* __restrict__ ahi,
+                                    const float* __restrict__ blo, const float* __restrict__ bhi, int64_t n,
+                                    float* __restrict__ olo, float* __restrict__ ohi) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  olo[i] = alo[i] + blo[i];
+  ohi[i] = ahi[i] + bhi[i];
+}
+
+// spec_linear (task_executor.py:423-439): lb = sum_o C+ l + C- u, ub = sum_o C+ u + C- l; one thread per (b, s)
+__global__ void spec_linear_kernel(const float* __restrict__ C, const float* __restrict__ lo,
+                                   const float* __restrict__ hi, int64_t B, int64_t S, int64_t O,
+                                   float* __restrict__ olo, float* __restrict__ ohi) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * S) return;
+  const int64_t b = i / S;
+  float sl = 0.f, su = 0.f;
+  for (int64_t o = 0; o < O; ++o) {
+    const float c = C[i * O + o];
+    const float cp = fmaxf(c, 0.f), cn = fminf(c, 0.f);
+    const float l = lo[b * O + o], u = hi[b * O + o];
+    sl += cp * l + cn * u;
+    su += cp * u + cn * l;
+  }
+  olo[i] = sl;
+  ohi[i] = su;
+}
+
+// Batched linear with per-sample weights W[b] [O, I] (the spec-fused last layer of
+// planner/interval_v1.py:85-164), center/radius form (task_executor.py:445-458):
+// lb = mid . W[b, o] - rad . |W[b, o]| + bias[b, o].  One wave64 per (b, o).
+__global__ void __launch_bounds__(256)
+ibp_batched_linear_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int64_t B, int64_t I,
+                          const float* __restrict__ W, const float* __restrict__ bias, int64_t O,
+                          float* __restrict__ olo, float* __restrict__ ohi) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= B * O) return;
+  const int64_t b = r / O;
+  float c = 0.f, d = 0.f;
+  for (int64_t i = lane; i < I; i += 64) {
+    const float l = lo[b * I + i], u = hi[b * I + i];
+    const float mid = (l + u) / 2.0f, rad = (u - l) / 2.0f;
+    const float w = W[r * I + i];
+    c += mid * w;
+    d += rad * fabsf(w);
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    c += __shfl_xor(c, off, 64);
+    d += __shfl_xor(d, off, 64);
+  }
+  if (lane == 0) {
+    const float bb = bias ? bias[r] : 0.f;
+    olo[r] = (c - d) + bb;
+    ohi[r] = (c + d) + bb;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Standalone ReLU relaxation pass (north-star kernel #3 in its unfused form):
 // one wave64 per coefficient row, float loads strided by 64 lanes, wave
 // reduction of the bias terms.  Writes A' for both bounds and
 //   b_out = (b_in + sum_k A * beta_sel)  [+ sum_k A' * kbias if kbias].
 __global__ void __launch_bounds__(256)
 relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t M, int64_t S, int64_t K,
-                       const float* __restrict__ lo, const float* __restrict__ hi, const float* __restrict__ alpha,
-                       int64_t alpha_ld, const float* __restrict__ add_l, int64_t add_ld,
+                       const float4* __restrict__ relax, const float* __restrict__ add_l, int64_t add_ld,
                        const float* __restrict__ kbias, const float* __restrict__ cvec,
                        const float* __restrict__ bu_in, const float* __restrict__ bl_in, float* __restrict__ Au_out,
                        float* __restrict__ Al_out, float* __restrict__ bu_out, float* __restrict__ bl_out,
@@ -167,20 +241,13 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
   const int64_t d = m / S;
   float su = 0.f, sl = 0.f, ku = 0.f, kl = 0.f, cu = 0.f, cl = 0.f;
   for (int64_t k = lane; k < K; k += 64) {
-    Relax r;
-    if (lo) {
-      const float l = lo[d * K + k], u = hi[d * K + k];
-      const bool has_alpha = alpha != nullptr;
-      const float a = has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f;
-      r = relu_relax(l, u, has_alpha, a);
-    } else {
-      r.au = 1.f; r.bu = 0.f; r.al = 1.f; r.bl = 0.f;  // no ReLU: identity
-    }
+    // {alpha_u, beta_u, alpha_l, beta_l}; no table = no ReLU (identity)
+    const float4 r = relax ? relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
     if (Au) {
       float v = Au[m * K + k];
       bool nn = v >= 0.f;
-      float o = v * (nn ? r.au : r.al);
-      su += v * (nn ? r.bu : r.bl);
+      float o = v * (nn ? r.x : r.z);
+      su += v * (nn ? r.y : r.w);
       if (kbias) ku += o * kbias[k];
       if (cvec) cu += o * cvec[d * K + k];
       Au_out[m * K + k] = o;
@@ -188,8 +255,8 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
     if (Al) {
       float v = Al[m * K + k];
       bool nn = v >= 0.f;
-      float o = v * (nn ? r.al : r.au);
-      sl += v * (nn ? r.bl : r.bu);
+      float o = v * (nn ? r.z : r.x);
+      sl += v * (nn ? r.w : r.y);
       if (add_l) o = o + add_l[d * add_ld + k];
       if (kbias) kl += o * kbias[k];
       if (cvec) cl += o * cvec[d * K + k];
@@ -339,6 +406,12 @@ extern "C" {
 
 int bf_abi_version(void) { return 1; }
 
+int bf_tuning_set_gemm_tile(int config) {
+  BF_REQUIRE(config >= -1 && config <= 5, "bf_tuning_set_gemm_tile: config must be -1 (automatic) or 0..5");
+  gemm_force_config(config);
+  return BF_OK;
+}
+
 const char* bf_last_error(void) { return g_err; }
 
 int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, int abs_b, float* C, int64_t ldc,
@@ -399,15 +472,24 @@ int bf_concretize_finalize(const float* partial_u, const float* partial_l, int n
   return concretize_finalize(partial_u, partial_l, nparts, M, cen_u, cen_l, b_u, b_l, eps, lb, ub, stream);
 }
 
+int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, int64_t D,
+                        int64_t K, float* table, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && K >= 0, "bf_relu_relax_table: bad sizes");
+  if (D * K == 0) return BF_OK;
+  BF_REQUIRE(pre_lo && pre_hi && table, "bf_relu_relax_table: null pointer");
+  BF_REQUIRE(((uintptr_t)table & 15) == 0, "bf_relu_relax_table: table must be 16-byte aligned");
+  return relax_table(pre_lo, pre_hi, alpha, alpha_ld, D, K, reinterpret_cast<float4*>(table), stream);
+}
+
 int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
-                             const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
-                             const float* add_l, int64_t add_ld, const float* W, int64_t P, const float* bias,
-                             const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
-                             float* b_u_out, float* b_l_out, hipStream_t stream) {
+                             const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
+                             const float* bias, const float* b_u_in, const float* b_l_in, float* A_prev_u,
+                             float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && P > 0, "bf_crown_relu_linear_fwd: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
-  BF_REQUIRE(W && ((pre_lo == nullptr) == (pre_hi == nullptr)), "bf_crown_relu_linear_fwd: null weight or half a pre-bound");
+  BF_REQUIRE(W != nullptr, "bf_crown_relu_linear_fwd: null weight");
+  BF_REQUIRE(((uintptr_t)relax & 15) == 0, "bf_crown_relu_linear_fwd: relax table must be 16-byte aligned");
   BF_REQUIRE((A_u != nullptr) == (A_prev_u != nullptr) && (A_l != nullptr) == (A_prev_l != nullptr),
              "bf_crown_relu_linear_fwd: input/output pointer mismatch");
   BF_REQUIRE(A_u || A_l, "bf_crown_relu_linear_fwd: no coefficient");
@@ -432,11 +514,7 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
   a.N = P;
   a.K = N;
   a.S = S;
-  a.pre_lo = pre_lo;
-  a.pre_hi = pre_hi;
-  a.ld_pre = N;
-  a.alpha = alpha;
-  a.alpha_ld = alpha_ld;
+  a.relax = reinterpret_cast<const float4*>(relax);
   a.add_l = add_l;
   a.add_ld = add_ld;
   a.kbias = bias;
@@ -444,16 +522,15 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
 }
 
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
-                                    const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
-                                    const float* add_l, int64_t add_ld, const float* W, int64_t I,
+                                    const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t I,
                                     const float* bias, const float* cvec, const float* rad, float eps,
                                     const float* b_u_in, const float* b_l_in, const float* h_scale,
                                     float* h_out, float* workspace, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
-  BF_REQUIRE(W && cvec && workspace && ((pre_lo == nullptr) == (pre_hi == nullptr)),
-             "bf_crown_relu_linear_concretize: null pointer");
+  BF_REQUIRE(W && cvec && workspace, "bf_crown_relu_linear_concretize: null pointer");
+  BF_REQUIRE(((uintptr_t)relax & 15) == 0, "bf_crown_relu_linear_concretize: relax table must be 16-byte aligned");
   BF_REQUIRE((A_u != nullptr) == (ub != nullptr) && (A_l != nullptr) == (lb != nullptr),
              "bf_crown_relu_linear_concretize: input/output pointer mismatch");
   const int nparts = gemm_partial_count(I);
@@ -482,11 +559,7 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
   a.N = I;
   a.K = N;
   a.S = S;
-  a.pre_lo = pre_lo;
-  a.pre_hi = pre_hi;
-  a.ld_pre = N;
-  a.alpha = alpha;
-  a.alpha_ld = alpha_ld;
+  a.relax = reinterpret_cast<const float4*>(relax);
   a.add_l = add_l;
   a.add_ld = add_ld;
   a.kbias = bias;
@@ -508,19 +581,18 @@ int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t 
   return (2 * (int64_t)gemm_partial_count(I) + 4) * M;
 }
 
-int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* pre_lo,
-                        const float* pre_hi, const float* alpha, int64_t alpha_ld, const float* add_l,
-                        int64_t add_ld, const float* kbias, const float* cvec, const float* b_u_in,
-                        const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out, float* b_l_out,
-                        float* c_u_out, float* c_l_out, hipStream_t stream) {
+int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* relax,
+                        const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+                        const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
+                        float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && K > 0, "bf_crown_relu_relax: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
-  BF_REQUIRE((pre_lo == nullptr) == (pre_hi == nullptr), "bf_crown_relu_relax: half a pre-bound");
+  BF_REQUIRE(((uintptr_t)relax & 15) == 0, "bf_crown_relu_relax: relax table must be 16-byte aligned");
   BF_REQUIRE((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr),
              "bf_crown_relu_relax: input/output mismatch");
   hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l, M, S,
-                     K, pre_lo, pre_hi, alpha, alpha_ld, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
+                     K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
                      A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
   BF_LAUNCH_CHECK("relu_relax_rows_kernel");
   return BF_OK;
@@ -575,6 +647,49 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
 }
 
 int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) { return 2 * B * K + 2 * B * N + N; }
+
+int bf_interval_relu(const float* lo, const float* hi, int64_t n, float* out_lo, float* out_hi, hipStream_t stream) {
+  BF_REQUIRE(n >= 0, "bf_interval_relu: bad size");
+  if (n == 0) return BF_OK;
+  BF_REQUIRE(lo && hi && out_lo && out_hi, "bf_interval_relu: null pointer");
+  hipLaunchKernelGGL(interval_relu_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, lo, hi, n, out_lo,
+                     out_hi);
+  BF_LAUNCH_CHECK("interval_relu_kernel");
+  return BF_OK;
+}
+
+int bf_interval_add(const float* a_lo, const float* a_hi, const float* b_lo, const float* b_hi, int64_t n,
+                    float* out_lo, float* out_hi, hipStream_t stream) {
+  BF_REQUIRE(n >= 0, "bf_interval_add: bad size");
+  if (n == 0) return BF_OK;
+  BF_REQUIRE(a_lo && a_hi && b_lo && b_hi && out_lo && out_hi, "bf_interval_add: null pointer");
+  hipLaunchKernelGGL(interval_add_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, a_lo, a_hi, b_lo,
+                     b_hi, n, out_lo, out_hi);
+  BF_LAUNCH_CHECK("interval_add_kernel");
+  return BF_OK;
+}
+
+int bf_spec_linear(const float* C, const float* lo, const float* hi, int64_t B, int64_t S, int64_t O, float* out_lo,
+                   float* out_hi, hipStream_t stream) {
+  BF_REQUIRE(B >= 0 && S >= 0 && O > 0, "bf_spec_linear: bad sizes");
+  if (B * S == 0) return BF_OK;
+  BF_REQUIRE(C && lo && hi && out_lo && out_hi, "bf_spec_linear: null pointer");
+  hipLaunchKernelGGL(spec_linear_kernel, dim3((unsigned)ceil_div(B * S, 256)), dim3(256), 0, stream, C, lo, hi, B, S,
+                     O, out_lo, out_hi);
+  BF_LAUNCH_CHECK("spec_linear_kernel");
+  return BF_OK;
+}
+
+int bf_ibp_batched_linear(const float* lo, const float* hi, int64_t B, int64_t I, const float* W, const float* bias,
+                          int64_t O, float* out_lo, float* out_hi, hipStream_t stream) {
+  BF_REQUIRE(B >= 0 && I > 0 && O > 0, "bf_ibp_batched_linear: bad sizes");
+  if (B == 0) return BF_OK;
+  BF_REQUIRE(lo && hi && W && out_lo && out_hi, "bf_ibp_batched_linear: null pointer");
+  hipLaunchKernelGGL(ibp_batched_linear_kernel, dim3((unsigned)ceil_div(B * O, 4)), dim3(256), 0, stream, lo, hi, B,
+                     I, W, bias, O, out_lo, out_hi);
+  BF_LAUNCH_CHECK("ibp_batched_linear_kernel");
+  return BF_OK;
+}
 
 int bf_interval_clip(float* lo, float* hi, const float* clo, const float* chi, const int8_t* split, int64_t split_ld,
                      int64_t B, int64_t N, int* infeasible, hipStream_t stream) {

@@ -30,6 +30,13 @@ typedef struct ihipStream_t* hipStream_t;
 int bf_abi_version(void);
 const char* bf_last_error(void);
 
+/* Tuning knob (no reference counterpart): force the contraction tile
+ * configuration, -1 = automatic choice, 0..5 = fixed configuration
+ * (0: 128x128x16 4 waves, 3 workgroups/CU; 1: 128x128x32; 2: 256x128x16 8 waves;
+ * 3: 128x256x16, store epilogue only; 4: 64x128x16 2 waves; 5: 128x128x16 4 waves,
+ * 2 workgroups/CU).  Process-wide. */
+int bf_tuning_set_gemm_tile(int config);
+
 /* ---- kernel #1: IBP ---------------------------------------------------- */
 
 /* Interval linear layer in center/radius form, with the consumer ReLU's split
@@ -63,7 +70,28 @@ int64_t bf_ibp_conv2d_workspace(int64_t B, int64_t nin, int64_t nout);
 int bf_interval_clip(float* lo, float* hi, const float* clo, const float* chi, const int8_t* split,
                      int64_t split_ld, int64_t B, int64_t N, int* infeasible, hipStream_t stream);
 
+/* Op-by-op interval kernels of the IBP task executor (runtime/task_executor.py:360-563):
+ * relu (domains/interval.py:88-91), add, spec_linear (C+ l + C- u, :423-439) and the
+ * batched per-sample linear W [B, O, I] in center/radius form (:445-458). */
+int bf_interval_relu(const float* lo, const float* hi, int64_t n, float* out_lo, float* out_hi, hipStream_t stream);
+int bf_interval_add(const float* a_lo, const float* a_hi, const float* b_lo, const float* b_hi, int64_t n,
+                    float* out_lo, float* out_hi, hipStream_t stream);
+int bf_spec_linear(const float* C, const float* lo, const float* hi, int64_t B, int64_t S, int64_t O, float* out_lo,
+                   float* out_hi, hipStream_t stream);
+int bf_ibp_batched_linear(const float* lo, const float* hi, int64_t B, int64_t I, const float* W, const float* bias,
+                          int64_t O, float* out_lo, float* out_hi, hipStream_t stream);
+
 /* ---- kernels #2 + #3: CROWN backward, fused ReLU relaxation + contraction -- */
+
+/* Slopes/intercepts of the ReLU relaxation per (domain, neuron), as the
+ * interleaved table {alpha_u, beta_u, alpha_l, beta_l} [D, K, 4] (16-byte
+ * aligned) -- the four tensors of FusedReluAffineRequest
+ * (runtime/fused_crown.py:33-48) computed by _relu_backward_relaxation
+ * (runtime/crown_ibp.py:722-758, 1176-1208).  alpha: optional lower-slope
+ * override [D,K] (alpha_ld K) or shared (alpha_ld 0), clamped to [0,1] and used
+ * on ambiguous neurons only. */
+int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, int64_t D,
+                        int64_t K, float* table, hipStream_t stream);
 
 /* One ReLU -> Linear region: A' = relax(A) (upper: sel(A>=0, alpha_u, alpha_l),
  * lower mirrored, plus the optional beta split coefficient add_l on the lower
@@ -73,15 +101,12 @@ int bf_interval_clip(float* lo, float* hi, const float* clo, const float* chi, c
  * (runtime/fused_crown.py:97-123, reference equations :330-400) and the dense
  * ReLU step + linear step of runtime/crown_ibp.py:1073-1090, 1211-1298.
  * A rows: A + d*a_dstride + s*N (a_dstride = S*N, or 0 when every domain
- * shares the same S rows).  pre_lo/pre_hi NULL = no relaxation (identity).
- * alpha: lower-slope override [D,N] (alpha_ld N) or shared (alpha_ld 0),
- * clamped to [0,1] and used on ambiguous neurons only (crown_ibp.py:1176-1208).
- * Either bound may be NULL (input and output together). */
+ * shares the same S rows).  relax: table of bf_relu_relax_table, NULL = no
+ * relaxation (identity).  Either bound may be NULL (input and output together). */
 int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
-                             const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
-                             const float* add_l, int64_t add_ld, const float* W, int64_t P, const float* bias,
-                             const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
-                             float* b_u_out, float* b_l_out, hipStream_t stream);
+                             const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
+                             const float* bias, const float* b_u_in, const float* b_l_in, float* A_prev_u,
+                             float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream);
 
 /* The input-layer region fused with the concretization (kernel #4):
  * lb = (A' . cvec - eps * sum_i |(A' W)_i| * rad_i) + b, ub mirrored;
@@ -93,23 +118,23 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
  * the gradient seed of the concretization.
  * workspace: bf_crown_relu_linear_concretize_workspace(D, S, I) floats. */
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
-                                    int64_t N, const float* pre_lo, const float* pre_hi, const float* alpha,
-                                    int64_t alpha_ld, const float* add_l, int64_t add_ld, const float* W, int64_t I,
+                                    int64_t N, const float* relax, const float* add_l, int64_t add_ld, const float* W,
+                                    int64_t I,
                                     const float* bias, const float* cvec, const float* rad, float eps,
                                     const float* b_u_in, const float* b_l_in, const float* h_scale, float* h_out,
                                     float* workspace, float* lb, float* ub, hipStream_t stream);
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I);
 
 /* Standalone relaxation pass (bandwidth-bound form of kernel #3): writes A'
- * and the bias/center row sums.  Replaces _backprop_relu_step_dense_reference
- * (runtime/crown_ibp.py:1211-1298); used ahead of the conv transposed
- * contraction.  kbias: per-element bias of the affine layer [K]; cvec: center
- * projection [D, K] (optional). */
-int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* pre_lo,
-                        const float* pre_hi, const float* alpha, int64_t alpha_ld, const float* add_l,
-                        int64_t add_ld, const float* kbias, const float* cvec, const float* b_u_in,
-                        const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out, float* b_l_out,
-                        float* c_u_out, float* c_l_out, hipStream_t stream);
+ * and the bias/center row sums, one wave64 per row.  Replaces
+ * _backprop_relu_step_dense_reference (runtime/crown_ibp.py:1211-1298); used
+ * ahead of the conv transposed contraction.  relax: table of
+ * bf_relu_relax_table (NULL = identity); kbias: per-element bias of the affine
+ * layer [K]; cvec: center projection [D, K] (optional). */
+int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* relax,
+                        const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+                        const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
+                        float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream);
 
 /* Transposed convolution of coefficient rows (Conv2dLinearOperator.to_dense,
  * runtime/linear_operator.py:1067-1092; FusedCrownExecutor "fused_relu_conv2d"

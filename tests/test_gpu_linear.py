@@ -51,8 +51,14 @@ def test_fused_relu_linear_region_golden():
     outs = [torch.empty(D * S, P, device=dev), torch.empty(D * S, P, device=dev),
             torch.empty(D * S, device=dev), torch.empty(D * S, device=dev)]
     args = [x.to(dev).contiguous() for x in (A_u, A_l, t(gz["l"]), t(gz["u"]), W, t(gz["bias"]))]
-    _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(args[0]), _lib.ptr(args[1]), S * N, D, S, N, _lib.ptr(args[2]),
-              _lib.ptr(args[3]), None, 0, None, 0, _lib.ptr(args[4]), P, _lib.ptr(args[5]), None, None,
+    table = torch.empty(D, N, 4, device=dev)
+    _lib.call("bf_relu_relax_table", _lib.ptr(args[2]), _lib.ptr(args[3]), None, 0, D, N, _lib.ptr(table),
+              _lib.stream_handle())
+    # the table holds exactly the executor request's alpha_u, beta_u, alpha_l, beta_l
+    for i, k in enumerate(("alpha_u", "beta_u", "alpha_l", "beta_l")):
+        assert torch.equal(table[..., i].cpu(), t(gz[k])), k
+    _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(args[0]), _lib.ptr(args[1]), S * N, D, S, N, _lib.ptr(table),
+              None, 0, _lib.ptr(args[4]), P, _lib.ptr(args[5]), None, None,
               _lib.ptr(outs[0]), _lib.ptr(outs[1]), _lib.ptr(outs[2]), _lib.ptr(outs[3]), _lib.stream_handle())
     torch.cuda.synchronize()
     assert_bounds_close(outs[0].reshape(D, S, P), t(gz["A_prev_u"]), "A_prev_u", rtol=1e-5, atol=1e-5)
@@ -164,9 +170,12 @@ def test_relax_pass_and_dense_concretize_match_oracle():
     d = [x.to(dev).contiguous() for x in (A_u, A_l, l, u, alpha, add, bu, bl)]
     out = [torch.empty(D * S, K, device=dev), torch.empty(D * S, K, device=dev), torch.empty(D * S, device=dev),
            torch.empty(D * S, device=dev)]
-    _lib.call("bf_crown_relu_relax", _lib.ptr(d[0]), _lib.ptr(d[1]), D, S, K, _lib.ptr(d[2]), _lib.ptr(d[3]),
-              _lib.ptr(d[4]), K, _lib.ptr(d[5]), K, None, None, _lib.ptr(d[6]), _lib.ptr(d[7]), _lib.ptr(out[0]),
-              _lib.ptr(out[1]), _lib.ptr(out[2]), _lib.ptr(out[3]), None, None, _lib.stream_handle())
+    table = torch.empty(D, K, 4, device=dev)
+    _lib.call("bf_relu_relax_table", _lib.ptr(d[2]), _lib.ptr(d[3]), _lib.ptr(d[4]), K, D, K, _lib.ptr(table),
+              _lib.stream_handle())
+    _lib.call("bf_crown_relu_relax", _lib.ptr(d[0]), _lib.ptr(d[1]), D, S, K, _lib.ptr(table), _lib.ptr(d[5]), K,
+              None, None, _lib.ptr(d[6]), _lib.ptr(d[7]), _lib.ptr(out[0]), _lib.ptr(out[1]), _lib.ptr(out[2]),
+              _lib.ptr(out[3]), None, None, _lib.stream_handle())
     torch.cuda.synchronize()
     assert torch.equal(out[0].cpu().reshape(D, S, K), ref[0])
     assert torch.equal(out[1].cpu().reshape(D, S, K), ref[1])
