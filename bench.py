@@ -14,6 +14,8 @@ region) and a CPU baseline (the PyTorch CPU restatement of the reference path
 timed on a bounded sample on this host).
 
     python bench.py [--steps K] [--warmup W] [--config C2|C1|C3|C4|C5] [--cpu-seconds S]
+    python bench.py --calibrate-copy MIB   # one plain device copy of MIB MiB, the
+                                           # reference kernel for HBM byte counters
 """
 
 from __future__ import annotations
@@ -27,6 +29,14 @@ import time
 
 PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak
 PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E
+
+# HBM bytes per launch of a dominant kernel, measured with rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE over one query (each scaled by what the counter
+# reads for a 1 GiB device copy: x2.0 and x1.0), averaged over the launch mix
+# of that query.  Keyed by (config, kernel family); other pairs report null.
+MEASURED_TRAFFIC = {
+    ("C2", "crown_relu_linear_fwd"): (6.404e8, "profiles/c2_fused_relax_gemm_hbm_traffic.md"),
+}
 
 
 def cpu_model() -> str:
@@ -132,11 +142,12 @@ def main() -> int:
     ap.add_argument("--config", default="C2")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU only; the path shards by domain with no "
-                                   "collective during bound computation (see DESIGN.md), run with --gpus 1"}))
+                                   "collective during bound computation, run with --gpus 1"}))
         return 2
 
     import torch
@@ -145,6 +156,16 @@ def main() -> int:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no HIP device"}))
         return 1
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}), flush=True)
+        return 0
     w, step, units, unit, desc = build_case(args.config)
     for _ in range(args.warmup):
         step()
@@ -162,16 +183,17 @@ def main() -> int:
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms"]) if kernels else (None, None)
     roofline = None
     if dom is not None:
+        traffic, source = MEASURED_TRAFFIC.get((args.config, dom_name), (None, None))
+        common = {"kernel": dom_name, "traffic": traffic, "traffic_source": source,
+                  "algorithmic_bytes_per_launch": round(dom["bytes"] / max(1, dom["launches"])),
+                  "avg_launch_ms": round(dom["avg_ms"], 4), "launches": int(dom["launches"]),
+                  "share_of_step": round(dom["ms"] / 1e3 / sec, 4)}
         if dom["flops"] > 0:
-            roofline = {"bound": "mfma", "kernel": dom_name, "achieved": round(dom["tflops"], 3),
-                        "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(dom["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
-                        "avg_launch_ms": round(dom["avg_ms"], 4), "launches": int(dom["launches"]),
-                        "share_of_step": round(dom["ms"] / 1e3 / sec, 4)}
+            roofline = {"bound": "mfma", "achieved": round(dom["tflops"], 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4), **common}
         else:
-            roofline = {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["gbps"], 1),
-                        "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4),
-                        "traffic": None, "avg_launch_ms": round(dom["avg_ms"], 4)}
+            roofline = {"bound": "hbm", "achieved": round(dom["gbps"], 1), "peak": PEAK_HBM_GBPS,
+                        "unit": "GB/s", "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), **common}
     line = {
         "metric": "CROWN bounds/sec & BaB domains/sec on 1 GPU; % of HBM / fp32-MFMA roofline",
         "value": round(units * args.steps / sec, 2),

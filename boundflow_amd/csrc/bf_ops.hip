@@ -174,6 +174,22 @@ __global__ void interval_add_kernel(const float* __restrict__ alo, const float* 
   ohi[i] = ahi[i] + bhi[i];
 }
 
+// Interval product (domains/interval.py:102-112): min / max over the four endpoint
+// products; a NaN among them propagates, as in torch.min / torch.max over a stack.
+__device__ __forceinline__ float nan_min(float m, float c) { return (c < m || c != c) ? c : m; }
+__device__ __forceinline__ float nan_max(float m, float c) { return (c > m || c != c) ? c : m; }
+
+__global__ void interval_mul_kernel(const float* __restrict__ alo, const float* __restrict__ ahi,
+                                    const float* __restrict__ blo, const float* __restrict__ bhi, int64_t n,
+                                    float* __restrict__ olo, float* __restrict__ ohi) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float al = alo[i], au = ahi[i], bl = blo[i], bu = bhi[i];
+  const float c0 = al * bl, c1 = al * bu, c2 = au * bl, c3 = au * bu;
+  olo[i] = nan_min(nan_min(nan_min(c0, c1), c2), c3);
+  ohi[i] = nan_max(nan_max(nan_max(c0, c1), c2), c3);
+}
+
 // spec_linear (task_executor.py:423-439): lb = sum_o C+ l + C- u, ub = sum_o C+ u + C- l; one thread per (b, s)
 __global__ void spec_linear_kernel(const float* __restrict__ C, const float* __restrict__ lo,
                                    const float* __restrict__ hi, int64_t B, int64_t S, int64_t O,
@@ -666,6 +682,17 @@ int bf_interval_add(const float* a_lo, const float* a_hi, const float* b_lo, con
   hipLaunchKernelGGL(interval_add_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, a_lo, a_hi, b_lo,
                      b_hi, n, out_lo, out_hi);
   BF_LAUNCH_CHECK("interval_add_kernel");
+  return BF_OK;
+}
+
+int bf_interval_mul(const float* a_lo, const float* a_hi, const float* b_lo, const float* b_hi, int64_t n,
+                    float* out_lo, float* out_hi, hipStream_t stream) {
+  BF_REQUIRE(n >= 0, "bf_interval_mul: bad size");
+  if (n == 0) return BF_OK;
+  BF_REQUIRE(a_lo && a_hi && b_lo && b_hi && out_lo && out_hi, "bf_interval_mul: null pointer");
+  hipLaunchKernelGGL(interval_mul_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, a_lo, a_hi, b_lo,
+                     b_hi, n, out_lo, out_hi);
+  BF_LAUNCH_CHECK("interval_mul_kernel");
   return BF_OK;
 }
 

@@ -1,0 +1,306 @@
+"""Fused ReLU->Affine CROWN region contract and its HIP executor.
+
+The dataclasses and planning helpers carry the reference's backend-neutral
+contract unchanged (boundflow/runtime/fused_crown.py):
+
+* ``FusedReluAffineRequest`` / ``FusedReluAffineResult``      -- :33-58
+* ``FusedCrownExecutionContext``                              -- :61-69
+* ``FusedCrownExecutionStep``, ``FusedCrownRuntimeSelection`` -- :72-94
+* ``FusedCrownExecutor`` protocol                             -- :97-123
+* ``FusedReluAffineDescriptor``                               -- :137-149
+* ``fused_crown_graph_fingerprint``                           -- :152-168
+* ``plan_fused_crown_regions`` / ``validate_fused_crown_execution_steps`` -- :178-276
+* ``build_fused_crown_runtime_selection``                     -- :826-847
+
+with one addition: the backend id ``"hip_fused"`` in the step whitelist and the
+runtime selection, mapped to ``HipFusedCrownExecutor``.  That executor accepts
+every plain-CROWN fp32 linear region and conv2d regions with groups 1 /
+dilation 1 (any kernel size, stride and padding -- the reference's TVM kernel
+rejects the 4x4 kernels of the benchmark CNN) and runs them on the caller's
+stream through the C ABI; it allocates the four outputs with the torch
+allocator, as the reference executors do (fused_crown.py:704-718).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+from dataclasses import dataclass
+from enum import Enum
+from typing import Any, Literal, Mapping, Optional, Protocol, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+
+class BoundaryRepresentation(Enum):
+    DENSE = "dense"
+    STRUCTURED = "structured"
+
+
+class InternalMaterializationPolicy(Enum):
+    EAGER = "eager"
+    ELIDE_RELU_SCALED_A = "elide_relu_scaled_a"
+
+
+@dataclass(frozen=True)
+class FusedReluAffineRequest:
+    kind: Literal["linear", "conv2d"]
+    A_u: torch.Tensor
+    A_l: torch.Tensor
+    alpha_u: torch.Tensor
+    alpha_l: torch.Tensor
+    beta_u: torch.Tensor
+    beta_l: torch.Tensor
+    weight: torch.Tensor
+    bias: Optional[torch.Tensor]
+    input_shape: Tuple[int, ...]
+    output_shape: Tuple[int, ...]
+    attrs: Mapping[str, object]
+
+
+@dataclass(frozen=True)
+class FusedReluAffineResult:
+    A_prev_u: torch.Tensor
+    A_prev_l: torch.Tensor
+    bias_delta_u: torch.Tensor
+    bias_delta_l: torch.Tensor
+
+
+@dataclass(frozen=True)
+class FusedCrownExecutionContext:
+    plain_crown: bool = True
+    requires_grad: bool = False
+    alpha_enabled: bool = False
+    beta_enabled: bool = False
+    split_state_present: bool = False
+
+
+@dataclass(frozen=True)
+class FusedCrownExecutionStep:
+    kind: Literal["fused_relu_linear", "fused_relu_conv2d"]
+    relu_op_index: int
+    affine_op_index: int
+    consumed_outputs: Tuple[str, str]
+    graph_fingerprint: str
+    boundary_representation: BoundaryRepresentation = BoundaryRepresentation.DENSE
+    internal_materialization: InternalMaterializationPolicy = InternalMaterializationPolicy.ELIDE_RELU_SCALED_A
+    backend: str = "tvm_fused_tir"
+
+
+@dataclass(frozen=True)
+class FusedCrownRuntimeSelection:
+    backend: str
+    executor: Optional["FusedCrownExecutor"]
+    steps: Tuple[FusedCrownExecutionStep, ...]
+
+
+@dataclass(frozen=True)
+class FusedReluAffineDescriptor:
+    kind: Literal["linear", "conv2d"]
+    coefficient_shape: Tuple[int, int, int]
+    weight: torch.Tensor
+    bias: Optional[torch.Tensor]
+    input_shape: Tuple[int, ...]
+    output_shape: Tuple[int, ...]
+    attrs: Mapping[str, object]
+    device: torch.device
+    dtype: torch.dtype
+
+
+class FusedCrownExecutor(Protocol):
+    def supports_descriptor(self, descriptor: FusedReluAffineDescriptor,
+                            context: FusedCrownExecutionContext) -> bool: ...
+
+    def supports(self, request: FusedReluAffineRequest, context: FusedCrownExecutionContext) -> bool: ...
+
+    def run(self, request: FusedReluAffineRequest, *,
+            stream: Optional[torch.cuda.Stream] = None) -> FusedReluAffineResult: ...
+
+
+_BACKENDS = {"tvm_fused_tir", "tvm_tir_unfused", "pytorch_chunked", "hip_fused"}
+
+
+def fused_crown_graph_fingerprint(ops: Sequence[Any]) -> str:
+    payload = [
+        {
+            "index": index,
+            "op_type": op.op_type,
+            "name": op.name,
+            "inputs": list(op.inputs),
+            "outputs": list(op.outputs),
+            "attrs": sorted((str(key), repr(value)) for key, value in op.attrs.items()),
+        }
+        for index, op in enumerate(ops)
+    ]
+    encoded = json.dumps(payload, sort_keys=True, separators=(",", ":")).encode()
+    return hashlib.sha256(encoded).hexdigest()
+
+
+def _consumers(ops: Sequence[Any]):
+    out: dict = {}
+    for index, op in enumerate(ops):
+        for name in op.inputs:
+            out.setdefault(name, []).append(index)
+    return {k: tuple(v) for k, v in out.items()}
+
+
+def plan_fused_crown_regions(ops: Sequence[Any], *, backend: str = "hip_fused") -> Tuple[FusedCrownExecutionStep, ...]:
+    """Match forward Affine->ReLU pairs whose affine output feeds only the ReLU."""
+    if backend not in _BACKENDS:
+        raise ValueError(f"unsupported fused CROWN backend: {backend}")
+    steps = []
+    consumers = _consumers(ops)
+    fp = fused_crown_graph_fingerprint(ops)
+    for relu_index, relu_op in enumerate(ops):
+        if relu_op.op_type != "relu" or relu_index == 0:
+            continue
+        affine = ops[relu_index - 1]
+        if affine.op_type not in {"linear", "conv2d"}:
+            continue
+        if len(affine.outputs) != 1 or tuple(relu_op.inputs) != tuple(affine.outputs):
+            continue
+        if consumers.get(affine.outputs[0], ()) != (relu_index,):
+            continue
+        kind = "fused_relu_linear" if affine.op_type == "linear" else "fused_relu_conv2d"
+        steps.append(FusedCrownExecutionStep(kind=kind, relu_op_index=relu_index, affine_op_index=relu_index - 1,
+                                             consumed_outputs=(relu_op.outputs[0], affine.outputs[0]),
+                                             graph_fingerprint=fp, backend=backend))
+    return tuple(steps)
+
+
+def validate_fused_crown_execution_steps(ops: Sequence[Any],
+                                         steps: Sequence[FusedCrownExecutionStep]) -> Tuple[FusedCrownExecutionStep, ...]:
+    """Keep only graph-current, single-consumer, supported steps."""
+    fp = fused_crown_graph_fingerprint(ops)
+    consumers = _consumers(ops)
+    valid = []
+    seen_relu: set = set()
+    seen_affine: set = set()
+    for step in steps:
+        if step.graph_fingerprint != fp:
+            continue
+        if step.relu_op_index in seen_relu or step.affine_op_index in seen_affine:
+            continue
+        if not 0 <= step.affine_op_index < step.relu_op_index < len(ops):
+            continue
+        if step.relu_op_index != step.affine_op_index + 1:
+            continue
+        affine = ops[step.affine_op_index]
+        relu = ops[step.relu_op_index]
+        expected = "fused_relu_linear" if affine.op_type == "linear" else "fused_relu_conv2d"
+        if affine.op_type not in {"linear", "conv2d"} or step.kind != expected:
+            continue
+        if relu.op_type != "relu" or tuple(relu.inputs) != tuple(affine.outputs):
+            continue
+        if len(affine.outputs) != 1 or len(relu.outputs) != 1:
+            continue
+        if step.consumed_outputs != (relu.outputs[0], affine.outputs[0]):
+            continue
+        if consumers.get(affine.outputs[0], ()) != (step.relu_op_index,):
+            continue
+        if step.boundary_representation != BoundaryRepresentation.DENSE:
+            continue
+        if step.internal_materialization != InternalMaterializationPolicy.ELIDE_RELU_SCALED_A:
+            continue
+        if step.backend not in _BACKENDS:
+            continue
+        valid.append(step)
+        seen_relu.add(step.relu_op_index)
+        seen_affine.add(step.affine_op_index)
+    return tuple(valid)
+
+
+def _pair(attrs: Mapping[str, object], name: str, default: Tuple[int, int]) -> Tuple[int, int]:
+    v = attrs.get(name, default)
+    if isinstance(v, int):
+        return (v, v)
+    if isinstance(v, (list, tuple)) and len(v) == 2:
+        return (int(v[0]), int(v[1]))
+    raise ValueError(f"{name} expects an integer pair, got {v!r}")
+
+
+class HipFusedCrownExecutor:
+    """FusedCrownExecutor backed by libboundflow_hip (backend id "hip_fused")."""
+
+    def supports_descriptor(self, descriptor: FusedReluAffineDescriptor,
+                            context: FusedCrownExecutionContext) -> bool:
+        if not (context.plain_crown and not context.requires_grad and not context.alpha_enabled
+                and not context.beta_enabled and not context.split_state_present):
+            return False
+        if descriptor.dtype != torch.float32 or descriptor.device.type != "cuda":
+            return False
+        if descriptor.kind == "linear":
+            return descriptor.weight.dim() == 2
+        if descriptor.kind == "conv2d":
+            a = descriptor.attrs
+            if int(a.get("groups", 1)) != 1 or _pair(a, "dilation", (1, 1)) != (1, 1):
+                return False
+            Co, Ho, Wo = (int(d) for d in descriptor.output_shape)
+            Ci, Hi, Wi = (int(d) for d in descriptor.input_shape)
+            return Co * Ho * Wo * 4 <= 64 * 1024 and descriptor.weight.dim() == 4
+        return False
+
+    def supports(self, request: FusedReluAffineRequest, context: FusedCrownExecutionContext) -> bool:
+        tensors = [request.A_u, request.A_l, request.alpha_u, request.alpha_l, request.beta_u, request.beta_l,
+                   request.weight] + ([request.bias] if request.bias is not None else [])
+        return bool(context.plain_crown and not context.requires_grad and not context.alpha_enabled
+                    and not context.beta_enabled and not context.split_state_present
+                    and request.kind in ("linear", "conv2d")
+                    and all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and not t.requires_grad
+                            for t in tensors))
+
+    def run(self, request: FusedReluAffineRequest, *,
+            stream: Optional[torch.cuda.Stream] = None) -> FusedReluAffineResult:
+        st = _lib.stream_handle(stream)
+        dev = request.A_u.device
+        D, S = int(request.A_u.shape[0]), int(request.A_u.shape[1])
+        M = D * S
+        N = int(request.alpha_u.reshape(D, -1).shape[1])
+        # the four relaxation tensors, interleaved as the kernels' table
+        table = torch.stack([request.alpha_u.reshape(D, N), request.beta_u.reshape(D, N),
+                             request.alpha_l.reshape(D, N), request.beta_l.reshape(D, N)], dim=-1).contiguous()
+        bias = None if request.bias is None else request.bias.contiguous()
+        du = torch.empty(D, S, device=dev, dtype=torch.float32)
+        dl = torch.empty(D, S, device=dev, dtype=torch.float32)
+        if request.kind == "linear":
+            W = request.weight.contiguous()
+            P = int(W.shape[1])
+            pu = torch.empty(D, S, P, device=dev, dtype=torch.float32)
+            pl = torch.empty(D, S, P, device=dev, dtype=torch.float32)
+            _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
+                      _lib.ptr(table), None, 0, _lib.ptr(W), P, _lib.ptr(bias), None, None, _lib.ptr(pu),
+                      _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
+            return FusedReluAffineResult(pu, pl, du, dl)
+        Co, Ho, Wo = (int(d) for d in request.output_shape)
+        Ci, Hi, Wi = (int(d) for d in request.input_shape)
+        W = request.weight.contiguous()
+        KH, KW = int(W.shape[2]), int(W.shape[3])
+        sh, sw = _pair(request.attrs, "stride", (1, 1))
+        ph, pw = _pair(request.attrs, "padding", (0, 0))
+        kbias = None if bias is None else bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous()
+        ru = torch.empty(M, N, device=dev)
+        rl = torch.empty(M, N, device=dev)
+        _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), D, S, N, _lib.ptr(table), None,
+                  0, _lib.ptr(kbias), None, None, None, _lib.ptr(ru), _lib.ptr(rl), _lib.ptr(du), _lib.ptr(dl), None,
+                  None, st)
+        pu = torch.empty(D, S, Ci, Hi, Wi, device=dev)
+        pl = torch.empty(D, S, Ci, Hi, Wi, device=dev)
+        _lib.call("bf_conv_transpose_rows", _lib.ptr(ru), _lib.ptr(rl), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW, sh, sw,
+                  ph, pw, Hi, Wi, _lib.ptr(pu), _lib.ptr(pl), S, None, 0, None, None, None, None, st)
+        return FusedReluAffineResult(pu, pl, du, dl)
+
+
+def build_fused_crown_runtime_selection(ops: Sequence[Any], *, backend: str,
+                                        chunk_rows: int = 512) -> FusedCrownRuntimeSelection:
+    """Map a planner backend decision to an executable runtime plan; "hip_fused"
+    selects HipFusedCrownExecutor (the reference's TVM/PyTorch backends are not
+    part of this package)."""
+    del chunk_rows
+    if backend in {"pytorch_eager", "pytorch_structured"}:
+        return FusedCrownRuntimeSelection(backend=backend, executor=None, steps=())
+    if backend != "hip_fused":
+        raise ValueError(f"unsupported fused CROWN runtime backend in the HIP package: {backend}")
+    return FusedCrownRuntimeSelection(backend=backend, executor=HipFusedCrownExecutor(),
+                                      steps=plan_fused_crown_regions(ops, backend=backend))

@@ -10,6 +10,7 @@ this backend unchanged:
 * ``TaskOp`` -- boundflow/ir/task.py:119-132
 * ``BoundTask`` -- boundflow/ir/task.py:135-173
 * ``BFTaskModule`` -- boundflow/ir/task.py:176-240
+* ``TaskBufferDep``/``TaskDepEdge``/``TaskGraph`` -- boundflow/ir/task_graph.py:11-168
 
 Only the planner-visible contract lives here; nothing in this module touches
 the device.
@@ -17,9 +18,10 @@ the device.
 
 from __future__ import annotations
 
+import heapq
 from dataclasses import dataclass, field
 from enum import Enum
-from typing import Any, Dict, List, Optional
+from typing import Any, Dict, List, Optional, Set
 
 
 class TaskKind(Enum):
@@ -196,11 +198,122 @@ class BFTaskModule:
                     b = self.storage_plan.value_to_buffer.get(v)
                     if b is None or b not in task.output_buffers:
                         raise ValueError(f"task '{task.task_id}' output_buffers missing buffer for value '{v}'")
+            self.task_graph.validate(tasks_by_id={t.task_id: t for t in self.tasks},
+                                     entry_task_id=self.entry_task_id, storage_plan=self.storage_plan)
 
     @property
     def params(self) -> Dict[str, Any]:
         raw = self.bindings.get("params", {})
         return dict(raw) if isinstance(raw, dict) else {}
+
+
+@dataclass(frozen=True)
+class TaskBufferDep:
+    """One value handed from a producer task to a consumer task, with the
+    buffers both sides bind it to (task_graph.py:11-20)."""
+
+    src_value: str
+    src_buffer_id: str
+    dst_value: str
+    dst_buffer_id: str
+
+
+@dataclass(frozen=True)
+class TaskDepEdge:
+    """Producer -> consumer task edge at buffer granularity (task_graph.py:23-34)."""
+
+    src_task_id: str
+    dst_task_id: str
+    deps: List[TaskBufferDep]
+
+
+@dataclass
+class TaskGraph:
+    """DAG of BoundTasks scheduled in topological order (task_graph.py:37-168)."""
+
+    task_ids: List[str]
+    edges: List[TaskDepEdge] = field(default_factory=list)
+
+    def validate(self, *, tasks_by_id: Dict[str, BoundTask], entry_task_id: str, storage_plan: StoragePlan) -> None:
+        if entry_task_id not in tasks_by_id:
+            raise KeyError(f"entry_task_id not found in tasks: {entry_task_id}")
+        if not self.task_ids:
+            raise ValueError("TaskGraph.task_ids must be non-empty")
+        if len(set(self.task_ids)) != len(self.task_ids):
+            raise ValueError("TaskGraph.task_ids contains duplicates")
+        missing = [t for t in self.task_ids if t not in tasks_by_id]
+        if missing:
+            raise KeyError(f"TaskGraph references missing task_id: {missing[0]}")
+        for edge in self.edges:
+            for end in (edge.src_task_id, edge.dst_task_id):
+                if end not in tasks_by_id:
+                    raise KeyError(f"edge task_id missing: {end}")
+            src, dst = tasks_by_id[edge.src_task_id], tasks_by_id[edge.dst_task_id]
+            for dep in edge.deps:
+                if dep.src_value not in src.output_values:
+                    raise ValueError(f"edge src_value '{dep.src_value}' not in src task outputs: {src.task_id}")
+                if dep.dst_value not in dst.input_values:
+                    raise ValueError(f"edge dst_value '{dep.dst_value}' not in dst task inputs: {dst.task_id}")
+                for value, bid, task, side in ((dep.src_value, dep.src_buffer_id, src, "output"),
+                                               (dep.dst_value, dep.dst_buffer_id, dst, "input")):
+                    if bid not in storage_plan.buffers:
+                        raise ValueError(f"edge buffer missing in storage_plan: {bid}")
+                    bound = task.output_buffers if side == "output" else task.input_buffers
+                    if bound and bid not in bound:
+                        raise ValueError(f"edge buffer '{bid}' not in task {side}_buffers: {task.task_id}")
+                    if storage_plan.value_to_buffer.get(value) != bid:
+                        raise ValueError(f"edge value->buffer mismatch: {value} -> "
+                                         f"{storage_plan.value_to_buffer.get(value)} (edge expects {bid})")
+        self.topo_sort(tasks_by_id=tasks_by_id, entry_task_id=entry_task_id)
+
+    def reachable_from(self, entry_task_id: str) -> Set[str]:
+        succ: Dict[str, List[str]] = {}
+        for e in self.edges:
+            succ.setdefault(e.src_task_id, []).append(e.dst_task_id)
+        seen: Set[str] = set()
+        todo = [entry_task_id]
+        while todo:
+            t = todo.pop()
+            if t not in seen:
+                seen.add(t)
+                todo.extend(n for n in succ.get(t, []) if n not in seen)
+        return seen
+
+    def topo_sort(self, *, tasks_by_id: Dict[str, BoundTask], entry_task_id: str) -> List[str]:
+        """Kahn's algorithm over the subgraph reachable from the entry task; ready
+        tasks leave in lexicographic order, so the order is deterministic."""
+        reachable = self.reachable_from(entry_task_id)
+        indeg = {t: 0 for t in reachable}
+        succ: Dict[str, List[str]] = {t: [] for t in reachable}
+        for e in self.edges:
+            if e.src_task_id in reachable and e.dst_task_id in reachable:
+                succ[e.src_task_id].append(e.dst_task_id)
+                indeg[e.dst_task_id] += 1
+        ready = sorted(t for t, d in indeg.items() if d == 0)
+        heapq.heapify(ready)
+        order: List[str] = []
+        while ready:
+            t = heapq.heappop(ready)
+            order.append(t)
+            for n in succ[t]:
+                indeg[n] -= 1
+                if indeg[n] == 0:
+                    heapq.heappush(ready, n)
+        if len(order) != len(reachable):
+            raise ValueError(f"TaskGraph contains a cycle in reachable subgraph: {sorted(reachable)}")
+        for t in order:
+            if t not in tasks_by_id:
+                raise KeyError(f"topo_sort referenced missing task_id: {t}")
+        return order
+
+    @staticmethod
+    def chain(*task_ids: str, deps: Optional[List[TaskBufferDep]] = None) -> "TaskGraph":
+        """t0 -> t1 -> ... -> tn, every edge carrying ``deps``."""
+        if not task_ids:
+            raise ValueError("TaskGraph.chain expects at least one task_id")
+        edges = [TaskDepEdge(src_task_id=a, dst_task_id=b, deps=list(deps or []))
+                 for a, b in zip(task_ids[:-1], task_ids[1:])]
+        return TaskGraph(task_ids=list(task_ids), edges=edges)
 
 
 def default_storage_plan(values: List[str], *, dtype: str = "float32") -> StoragePlan:

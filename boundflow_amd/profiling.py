@@ -72,7 +72,11 @@ def summarize_rocpd(db_path: str, top: int = 12) -> str:
     ``*_results.db`` (kernel-trace run), as a Markdown table."""
     import sqlite3
 
-    con = sqlite3.connect(db_path)
+    import os
+
+    if not os.path.isfile(db_path):
+        raise FileNotFoundError(f"no rocprofv3 database at {db_path}")
+    con = sqlite3.connect(f"file:{db_path}?mode=ro", uri=True)
     q = ("select s.kernel_name, count(*), avg(d.end - d.start), sum(d.end - d.start) "
          "from rocpd_kernel_dispatch d join rocpd_info_kernel_symbol s on d.kernel_id = s.id "
          "group by s.kernel_name order by 4 desc")
@@ -88,4 +92,6 @@ def summarize_rocpd(db_path: str, top: int = 12) -> str:
 if __name__ == "__main__":
     import sys
 
+    if len(sys.argv) != 2 or sys.argv[1].startswith("-"):
+        raise SystemExit("usage: python -m boundflow_amd.profiling <rocprofv3 *_results.db>")
     print(summarize_rocpd(sys.argv[1]))

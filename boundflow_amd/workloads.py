@@ -28,7 +28,8 @@ from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 
-from .ir import BFTaskModule, BoundTask, TaskKind, TaskOp, default_storage_plan
+from .ir import (BFTaskModule, BoundTask, BufferSpec, StoragePlan, TaskBufferDep, TaskDepEdge, TaskGraph, TaskKind,
+                 TaskOp, default_storage_plan)
 from .spec import InputSpec
 
 
@@ -245,6 +246,100 @@ def make_c5(seed: int = 0, domains: int = 4096, eps: float = 0.03, max_splits: i
     return w
 
 
+def make_ibp_dag(seed: int = 0, batch: int = 8, eps: float = 0.05, box: bool = False) -> Workload:
+    """One-task IBP program that uses every op of the task executors: linear on
+    the input set with a shared [O, I] and a per-sample [B, O, I] weight, relu,
+    add, mul (by a mixed-sign gate), reshape, permute, flatten, concat and
+    spec_linear.  Output value ``margins`` [B, 9]."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    B = batch
+    p: Dict[str, torch.Tensor] = {}
+    p["W0"] = _kaiming((32, 24), fan_in=24, gen=g, kind="uniform")
+    p["b0"] = torch.randn(32, generator=g) * 0.1
+    p["W1"] = _kaiming((16, 32), fan_in=32, gen=g, kind="uniform")
+    p["b1"] = torch.randn(16, generator=g) * 0.1
+    p["W2"] = _kaiming((16, 32), fan_in=32, gen=g, kind="uniform")
+    p["gate"] = torch.randn(16, generator=g)
+    p["Wi"] = torch.randn(B, 8, 24, generator=g) * 0.2
+    p["bi"] = torch.randn(B, 8, generator=g) * 0.1
+    p["W3"] = _kaiming((10, 56), fan_in=56, gen=g, kind="uniform")
+    p["b3"] = torch.randn(10, generator=g) * 0.1
+    x = torch.rand(B, 24, generator=g)
+    labels = torch.randint(0, 10, (B,), generator=g)
+    p["C"] = margin_spec(labels)
+    ops = [
+        TaskOp("linear", "linear0", ["input", "W0", "b0"], ["h0"]),
+        TaskOp("relu", "relu0", ["h0"], ["r0"]),
+        TaskOp("linear", "linear1", ["r0", "W1", "b1"], ["a"]),
+        TaskOp("linear", "linear2", ["r0", "W2"], ["c"]),
+        TaskOp("add", "add", ["a", "c"], ["s"]),
+        TaskOp("mul", "mul", ["s", "gate"], ["m"]),
+        TaskOp("reshape", "reshape", ["r0"], ["rr"], {"shape": [B, 2, 16]}),
+        TaskOp("permute", "permute", ["rr"], ["rp"], {"dims": [0, 2, 1]}),
+        TaskOp("flatten", "flatten", ["rp"], ["rf"], {"start_dim": 1, "end_dim": -1}),
+        TaskOp("linear", "linear_in", ["input", "Wi", "bi"], ["hi"]),
+        TaskOp("concat", "concat", ["m", "rf", "hi"], ["cat"], {"axis": 1}),
+        TaskOp("relu", "relu1", ["cat"], ["rc"]),
+        TaskOp("linear", "linear3", ["rc", "W3", "b3"], ["out"]),
+        TaskOp("spec_linear", "spec", ["out", "C"], ["margins"]),
+    ]
+    values = ["input", "h0", "r0", "a", "c", "s", "m", "rr", "rp", "rf", "hi", "cat", "rc", "out", "margins"]
+    task = BoundTask(task_id="t0", kind=TaskKind.INTERVAL_IBP, ops=ops, input_values=["input"],
+                     output_values=["margins"], params=list(p.keys()))
+    module = BFTaskModule(tasks=[task], entry_task_id="t0", bindings={"params": p},
+                          storage_plan=default_storage_plan(values))
+    if box:
+        spec = InputSpec.box(value_name="input", lower=torch.clamp(x - eps, 0.0, 1.0),
+                             upper=torch.clamp(x + eps, 0.0, 1.0))
+    else:
+        spec = InputSpec.linf(value_name="input", center=x, eps=eps)
+    return Workload("ibp_dag", module, spec, p["C"], labels)
+
+
+def split_ibp_dag(w: Workload) -> BFTaskModule:
+    """The ``make_ibp_dag`` program as three tasks joined by a TaskGraph, with a
+    storage plan that reuses physical buffers (``h0``/``a`` and ``c``/``rr``
+    share one each: the first of each pair is dead before the second is
+    written)."""
+    ops = {op.name: op for op in w.module.get_entry_task().ops}
+    groups = {
+        "t0": (["linear0", "relu0"], ["input"], ["r0"]),
+        "t1": (["linear1", "linear2", "add", "mul", "reshape", "permute", "flatten", "linear_in"],
+               ["r0", "input"], ["m", "rf", "hi"]),
+        "t2": (["concat", "relu1", "linear3", "spec"], ["m", "rf", "hi"], ["margins"]),
+    }
+    # ``gate`` is a parameter read as an interval operand (mul); run_ibp_task
+    # resolves such operands through the storage plan as well
+    values = ["input", "h0", "r0", "a", "c", "s", "gate", "m", "rr", "rp", "rf", "hi", "cat", "rc", "out",
+              "margins"]
+    plan = StoragePlan()
+    for v in values:
+        plan.buffers[f"buf_{v}"] = BufferSpec(buffer_id=f"buf_{v}", dtype="float32", shape=[None])
+        plan.value_to_buffer[v] = f"buf_{v}"
+    alias = {"buf_a": "phys_h0_a", "buf_h0": "phys_h0_a", "buf_c": "phys_c_rr", "buf_rr": "phys_c_rr"}
+    for lb in plan.buffers:
+        pb = alias.get(lb, "phys_" + lb[4:])
+        plan.logical_to_physical[lb] = pb
+        plan.physical_buffers[pb] = BufferSpec(buffer_id=pb, dtype="float32", shape=[None])
+    tasks = []
+    for tid, (names, ins, outs) in groups.items():
+        tasks.append(BoundTask(task_id=tid, kind=TaskKind.INTERVAL_IBP, ops=[ops[n] for n in names],
+                               input_values=ins, output_values=outs,
+                               input_buffers=[plan.value_to_buffer[v] for v in ins],
+                               output_buffers=[plan.value_to_buffer[v] for v in outs]))
+
+    def dep(v):
+        return TaskBufferDep(src_value=v, src_buffer_id=plan.value_to_buffer[v], dst_value=v,
+                             dst_buffer_id=plan.value_to_buffer[v])
+
+    graph = TaskGraph(task_ids=["t0", "t1", "t2"], edges=[
+        TaskDepEdge(src_task_id="t0", dst_task_id="t1", deps=[dep("r0")]),
+        TaskDepEdge(src_task_id="t1", dst_task_id="t2", deps=[dep("m"), dep("rf"), dep("hi")]),
+    ])
+    return BFTaskModule(tasks=tasks, entry_task_id="t0", bindings={"params": w.module.params}, storage_plan=plan,
+                        task_graph=graph)
+
+
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5}
 
 
@@ -260,7 +355,8 @@ def to_device(w: Workload, device) -> Workload:
     """Copy a workload (params, spec, C, splits) to ``device``."""
     params = {k: v.to(device) for k, v in w.module.params.items()}
     mod = BFTaskModule(tasks=w.module.tasks, entry_task_id=w.module.entry_task_id,
-                       bindings={"params": params}, storage_plan=w.module.storage_plan)
+                       bindings={"params": params}, storage_plan=w.module.storage_plan,
+                       task_graph=w.module.task_graph)
     extra = dict(w.extra)
     if "splits" in extra:
         extra["splits"] = {k: v.to(device) for k, v in extra["splits"].items()}

@@ -71,10 +71,13 @@ int bf_interval_clip(float* lo, float* hi, const float* clo, const float* chi, c
                      int64_t split_ld, int64_t B, int64_t N, int* infeasible, hipStream_t stream);
 
 /* Op-by-op interval kernels of the IBP task executor (runtime/task_executor.py:360-563):
- * relu (domains/interval.py:88-91), add, spec_linear (C+ l + C- u, :423-439) and the
- * batched per-sample linear W [B, O, I] in center/radius form (:445-458). */
+ * relu (domains/interval.py:88-91), add, mul (four endpoint products, interval.py:102-112),
+ * spec_linear (C+ l + C- u, :423-439) and the batched per-sample linear W [B, O, I] in
+ * center/radius form (:445-458).  mul expects both operands already broadcast to n elements. */
 int bf_interval_relu(const float* lo, const float* hi, int64_t n, float* out_lo, float* out_hi, hipStream_t stream);
 int bf_interval_add(const float* a_lo, const float* a_hi, const float* b_lo, const float* b_hi, int64_t n,
+                    float* out_lo, float* out_hi, hipStream_t stream);
+int bf_interval_mul(const float* a_lo, const float* a_hi, const float* b_lo, const float* b_hi, int64_t n,
                     float* out_lo, float* out_hi, hipStream_t stream);
 int bf_spec_linear(const float* C, const float* lo, const float* hi, int64_t B, int64_t S, int64_t O, float* out_lo,
                    float* out_hi, hipStream_t stream);
