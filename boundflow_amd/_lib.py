@@ -31,9 +31,9 @@ SIGNATURES = {
     "bf_gemm": (I32, [P, I64, P, I64, I32, I32, P, I64, I64, I64, I64, P]),
     "bf_gemm_rank1": (I32, [P, I64, P, I64, I32, P, I64, I64, I64, I64, I64, P, P, I64, P]),
     "bf_relu_relax_table": (I32, [P, P, P, I64, I64, I64, P, P]),
-    "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, P, P, P, P, P, P, P, P]),
-    "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, P, P, P, F32, P, P, P, P,
-                                              P, P, P, P]),
+    "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, P, P, P, P, P]),
+    "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, F32, P, P,
+                                              P, P, P, P, P, P]),
     "bf_crown_relu_linear_concretize_workspace": (I64, [I64, I64, I64]),
     "bf_crown_relu_relax": (I32, [P, P, I64, I64, I64, P, P, I64, P, P, P, P, P, P, P, P, P, P, P]),
     "bf_concretize_dense": (I32, [P, I64, I64, I64, P, P, F32, P, I32, P, P]),

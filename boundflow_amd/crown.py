@@ -372,6 +372,8 @@ def crown_backward(
                 return done
             continue
         W = layer.weight.contiguous()
+        # the contraction reads W^T [P, N] row-major: 128-bit operand loads along N
+        Wt = W.t().contiguous()
         bias = None if layer.bias is None else layer.bias.contiguous()
         P = _numel(layer.in_shape)
         if k > 0 and linear_spec_C is None and k == len(layers) - 1:
@@ -412,7 +414,8 @@ def crown_backward(
             nz = int(A_u is not None) + int(A_l is not None)
             with _timed("crown_relu_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
                 _lib.call("bf_crown_relu_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
-                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(cvec), _lib.ptr(rad), eps, _lib.ptr(b_u),
+                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(cvec),
+                          _lib.ptr(rad), eps, _lib.ptr(b_u),
                           _lib.ptr(b_l), _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(ws), _lib.ptr(lb),
                           _lib.ptr(ub), stream)
             if save is not None:
@@ -426,7 +429,8 @@ def crown_backward(
         a_rows = M if stride != 0 else S
         with _timed("crown_relu_linear_fwd", 2.0 * nz * M * N * P, 4.0 * nz * (a_rows * N + N * P + M * P)):
             _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
-                      _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(W), P, _lib.ptr(bias), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(nA_u),
+                      _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(b_u),
+                      _lib.ptr(b_l), _lib.ptr(nA_u),
                       _lib.ptr(nA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), stream)
         A_u, A_l, b_u, b_l = nA_u, nA_l, nb_u, nb_l
         stride = S * P

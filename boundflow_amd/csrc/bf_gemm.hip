@@ -50,6 +50,10 @@ struct Tile {
   static constexpr int B_SLOTS = BN * BK / 4 / NT;
   static constexpr int RPP = NT / KQ;                // A rows covered per slot index
   static constexpr int BS_FLOATS = BN * BPT;
+  // Relaxation operands staged in LDS per K tile: one (domain, k) entry per
+  // thread, so a tile whose rows span at most TAB_DOMS domains reads them there.
+  static constexpr int TAB_ENTRIES = NT;
+  static constexpr int TAB_DOMS = NT / BK;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert((BM * BK) % (4 * NT) == 0 && (BN * BK) % (4 * NT) == 0, "tile/thread mismatch");
   static_assert((BK & (BK - 1)) == 0 && BK >= 8, "BK must be a power of two >= 8");
@@ -71,6 +75,11 @@ gemm_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(16))) float As[2][GBM * AP];
   __shared__ __attribute__((aligned(16))) float Bs[2][T::BS_FLOATS];
   __shared__ float red[T::NWN][GBM];
+  constexpr int TE = (PRO == PRO_RELAX) ? T::TAB_ENTRIES : 1;
+  constexpr int TK = (PRO == PRO_RELAX) ? GBK : 1;
+  __shared__ float4 Ts[2][TE];   // relaxation table slice of a K tile, double-buffered
+  __shared__ float As_add[2][TE];  // beta split coefficient slice (lower bound)
+  __shared__ float Kb[2][TK];    // affine bias slice
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -100,14 +109,15 @@ gemm_kernel(GemmArgs p) {
   const int a_kq = t % KQ;
   const int a_r0 = t / KQ;
   int64_t a_base[A_SLOTS];
-  int64_t a_dom[A_SLOTS];
+  int a_dom[A_SLOTS];   // domain of the row (D < 2^31)
   float s_beta[A_SLOTS], s_bias[A_SLOTS], s_cen[A_SLOTS];
 #pragma unroll
   for (int j = 0; j < A_SLOTS; ++j) {
     const int64_t m = m0 + a_r0 + RPP * j;
     const int64_t mm = m < M ? m : 0;
-    a_dom[j] = mm / p.S;
-    a_base[j] = a_dom[j] * p.lda_d + (mm - a_dom[j] * p.S) * p.lda;
+    const int64_t d = mm / p.S;
+    a_dom[j] = (int)d;
+    a_base[j] = d * p.lda_d + (mm - d * p.S) * p.lda;
     s_beta[j] = 0.f;
     s_bias[j] = 0.f;
     s_cen[j] = 0.f;
@@ -143,7 +153,8 @@ gemm_kernel(GemmArgs p) {
         const int n = q / KQ, kq = q % KQ;
         const int64_t gn = n0 + n, gk = k0 + 4 * kq;
         if (gn < N) {
-          const float* src = p.B + gn * p.ldb + gk;
+          // B offsets fit in 32 bits (checked at launch): uniform base + 32-bit offset
+          const float* src = p.B + (uint32_t)(gn * p.ldb + gk);
           if (vec_b) {
             if (gk < K) v = *reinterpret_cast<const float4*>(src);
           } else {
@@ -159,11 +170,11 @@ gemm_kernel(GemmArgs p) {
         const int n = q % GBN, kq = q / GBN;
         const int64_t gn = n0 + n, gk = k0 + 4 * kq;
         if (gn < N) {
-          const float* src = p.B + gk * p.ldb + gn;
-          if (gk + 0 < K) v.x = src[0];
-          if (gk + 1 < K) v.y = src[p.ldb];
-          if (gk + 2 < K) v.z = src[2 * p.ldb];
-          if (gk + 3 < K) v.w = src[3 * p.ldb];
+          const uint32_t o = (uint32_t)(gk * p.ldb + gn), ld = (uint32_t)p.ldb;
+          if (gk + 0 < K) v.x = p.B[o];
+          if (gk + 1 < K) v.y = p.B[o + ld];
+          if (gk + 2 < K) v.z = p.B[o + 2 * ld];
+          if (gk + 3 < K) v.w = p.B[o + 3 * ld];
         }
       }
       if (p.abs_b) {
@@ -175,36 +186,80 @@ gemm_kernel(GemmArgs p) {
 
   const bool use_add = (PRO == PRO_RELAX) && lower && (p.add_l != nullptr);
 
+  // The rows of this tile span domains d_first .. d_first + ndom - 1.  When that
+  // fits TAB_DOMS, the relaxation operands of a K tile are loaded once per
+  // (domain, k) -- one entry per thread, coalesced -- and staged in LDS one K
+  // tile ahead (slot (kt & 1)), so every coefficient reads them from LDS.
+  int d_first = 0;
+  int ndom = 0;
+  bool tab_lds = false;
+  if (PRO == PRO_RELAX && p.relax) {
+    const int64_t m_last = (m0 + GBM < M ? m0 + GBM : M) - 1;
+    d_first = (int)(m0 / p.S);
+    const int64_t nd = m_last / p.S - d_first + 1;
+    tab_lds = nd <= T::TAB_DOMS;
+    ndom = tab_lds ? (int)nd : 0;
+  }
+  const int e_dom = t / GBK, e_k = t % GBK;   // this thread's table entry
+  float4 tab_reg = make_float4(1.f, 0.f, 1.f, 0.f);
+  float add_reg = 0.f, kb_reg = 0.f;
+  auto load_tab = [&](int64_t k0) {
+    if (PRO != PRO_RELAX) return;
+    const int64_t k = k0 + e_k;
+    const bool ok = tab_lds && e_dom < ndom && k < K;
+    const int64_t d = (int64_t)d_first + e_dom;
+    tab_reg = ok ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
+    if (use_add) add_reg = ok ? p.add_l[d * p.add_ld + k] : 0.f;
+    if (t < GBK) kb_reg = (tab_lds && p.kbias && k0 + t < K) ? p.kbias[k0 + t] : 0.f;
+  };
+  auto store_tab = [&](int slot) {
+    if (PRO != PRO_RELAX) return;
+    Ts[slot][t] = tab_reg;
+    if (use_add) As_add[slot][t] = add_reg;
+    if (t < GBK) Kb[slot][t] = kb_reg;
+  };
+
   // ReLU relaxation of one coefficient (crown_ibp.py:1261-1296), applied as the
   // A tile is written to LDS; padding elements (outside M or K) stay zero.
-  // The table entries are read here rather than with the A tile: holding them
-  // across the MFMA loop costs more occupancy than their latency does.
-  auto relax_one = [&](float a, int j, int64_t k) -> float {
+  auto relax_one = [&](float a, int j, int64_t k, int64_t k0, int slot) -> float {
     if (k >= K) return a;
     const int64_t d = a_dom[j];
-    const float4 r = p.relax ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
+    float4 r;
+    float add = 0.f, kb = 0.f;
+    if (tab_lds) {
+      const int e = (a_dom[j] - d_first) * GBK + (int)(k - k0);
+      r = Ts[slot][e];
+      if (use_add) add = As_add[slot][e];
+      kb = Kb[slot][k - k0];
+    } else {
+      r = p.relax ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
+      if (use_add) add = p.add_l[d * p.add_ld + k];
+      if (p.kbias) kb = p.kbias[k];
+    }
     float be;
     float out = a * fsel(r, lower, a >= 0.f, &be);
-    if (use_add) out = out + p.add_l[d * p.add_ld + k];
+    if (use_add) out = out + add;
     if (row_reduce) {
       s_beta[j] += a * be;
-      if (p.kbias) s_bias[j] += out * p.kbias[k];
+      if (p.kbias) s_bias[j] += out * kb;
       if (p.cvec) s_cen[j] += out * p.cvec[d * p.cvec_ld + k];
     }
     return out;
   };
 
-  auto store_tiles = [&](int buf, int64_t k0) {
+  // kt: index of the K tile being stored (its relaxation slice is in slot kt & 1)
+  auto store_tiles = [&](int buf, int64_t k0, int64_t kt) {
+    const int slot = (int)(kt & 1);
 #pragma unroll
     for (int j = 0; j < A_SLOTS; ++j) {
       const int r = a_r0 + RPP * j;
       float4 v = a_reg[j];
       if (PRO == PRO_RELAX && m0 + r < M) {
         const int64_t k = k0 + 4 * a_kq;
-        v.x = relax_one(v.x, j, k + 0);
-        v.y = relax_one(v.y, j, k + 1);
-        v.z = relax_one(v.z, j, k + 2);
-        v.w = relax_one(v.w, j, k + 3);
+        v.x = relax_one(v.x, j, k + 0, k0, slot);
+        v.y = relax_one(v.y, j, k + 1, k0, slot);
+        v.z = relax_one(v.z, j, k + 2, k0, slot);
+        v.w = relax_one(v.w, j, k + 3, k0, slot);
       }
       *reinterpret_cast<float4*>(&As[buf][r * AP + 4 * a_kq]) = v;
     }
@@ -226,15 +281,25 @@ gemm_kernel(GemmArgs p) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int64_t nk = ceil_div(K, GBK);
+  // Prologue: relaxation slices of K tiles 0 and 1, then tile 0 itself.
+  load_tab(0);
+  store_tab(0);
+  if (nk > 1) {
+    load_tab(GBK);
+    store_tab(1);
+  }
   load_tiles(0);
-  store_tiles(0, 0);
+  __syncthreads();
+  store_tiles(0, 0, 0);
   __syncthreads();
   int buf = 0;
   const int lrow = lane & 31;
   const int h = lane >> 5;   // lane half -> k half of the tile
   for (int64_t kt = 0; kt < nk; ++kt) {
     const bool more = kt + 1 < nk;
+    const bool more2 = kt + 2 < nk;
     if (more) load_tiles((kt + 1) * GBK);
+    if (more2) load_tab((kt + 2) * GBK);
     const float* __restrict__ as = As[buf];
     const float* __restrict__ bs = Bs[buf];
 #pragma unroll
@@ -261,7 +326,9 @@ gemm_kernel(GemmArgs p) {
           for (int jj = 0; jj < FN; ++jj)
             acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
     }
-    if (more) store_tiles(buf ^ 1, (kt + 1) * GBK);
+    if (more) store_tiles(buf ^ 1, (kt + 1) * GBK, kt + 1);
+    // slot kt & 1 held tile kt's slice, consumed one iteration ago
+    if (more2) store_tab((int)(kt & 1));
     __syncthreads();
     buf ^= 1;
   }
@@ -413,6 +480,9 @@ using TileF = Tile<128, 128, 16, 2, 2, 2>;   // TileA at 2 workgroups per CU
 
 template <int PRO, int EPI, class T>
 static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
+  const int64_t b_extent = a.trans_b ? (a.N - 1) * a.ldb + a.K : (a.K - 1) * a.ldb + a.N;
+  BF_REQUIRE(b_extent < (1LL << 31), "gemm: B operand too large for 32-bit offsets (%lld elements)",
+             (long long)b_extent);
   const int64_t ntiles = ceil_div(a.M, T::BM) * ceil_div(a.N, T::BN);
   BF_REQUIRE(ntiles + 8 < (1LL << 31), "gemm grid too large (M=%lld N=%lld)", (long long)a.M, (long long)a.N);
   dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), (unsigned)nz);

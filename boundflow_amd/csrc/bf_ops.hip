@@ -499,8 +499,8 @@ int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* a
 
 int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
                              const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
-                             const float* bias, const float* b_u_in, const float* b_l_in, float* A_prev_u,
-                             float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream) {
+                             int w_trans, const float* bias, const float* b_u_in, const float* b_l_in,
+                             float* A_prev_u, float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && P > 0, "bf_crown_relu_linear_fwd: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
@@ -524,8 +524,8 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
   a.lda_d = a_dstride;
   a.ldc = P;
   a.B = W;
-  a.ldb = P;
-  a.trans_b = 0;
+  a.trans_b = w_trans ? 1 : 0;
+  a.ldb = w_trans ? N : P;
   a.M = M;
   a.N = P;
   a.K = N;
@@ -539,7 +539,7 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
 
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
                                     const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t I,
-                                    const float* bias, const float* cvec, const float* rad, float eps,
+                                    int w_trans, const float* bias, const float* cvec, const float* rad, float eps,
                                     const float* b_u_in, const float* b_l_in, const float* h_scale,
                                     float* h_out, float* workspace, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize: bad sizes");
@@ -570,7 +570,8 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
   a.lda = N;
   a.lda_d = a_dstride;
   a.B = W;
-  a.ldb = I;
+  a.trans_b = w_trans ? 1 : 0;
+  a.ldb = w_trans ? N : I;
   a.M = M;
   a.N = I;
   a.K = N;

@@ -265,12 +265,12 @@ class HipFusedCrownExecutor:
         du = torch.empty(D, S, device=dev, dtype=torch.float32)
         dl = torch.empty(D, S, device=dev, dtype=torch.float32)
         if request.kind == "linear":
-            W = request.weight.contiguous()
-            P = int(W.shape[1])
+            P = int(request.weight.shape[1])
+            Wt = request.weight.t().contiguous()   # [P, N]: the kernel's faster operand layout
             pu = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             pl = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
-                      _lib.ptr(table), None, 0, _lib.ptr(W), P, _lib.ptr(bias), None, None, _lib.ptr(pu),
+                      _lib.ptr(table), None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None, _lib.ptr(pu),
                       _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
             return FusedReluAffineResult(pu, pl, du, dl)
         Co, Ho, Wo = (int(d) for d in request.output_shape)

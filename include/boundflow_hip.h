@@ -105,11 +105,14 @@ int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* a
  * ReLU step + linear step of runtime/crown_ibp.py:1073-1090, 1211-1298.
  * A rows: A + d*a_dstride + s*N (a_dstride = S*N, or 0 when every domain
  * shares the same S rows).  relax: table of bf_relu_relax_table, NULL = no
- * relaxation (identity).  Either bound may be NULL (input and output together). */
+ * relaxation (identity).  Either bound may be NULL (input and output together).
+ * W: the layer weight [N, P] row-major (the reference's [out, in]) when
+ * w_trans = 0, or its transpose [P, N] row-major when w_trans = 1 (the faster
+ * operand layout: 128-bit loads along the contraction). */
 int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
                              const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
-                             const float* bias, const float* b_u_in, const float* b_l_in, float* A_prev_u,
-                             float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream);
+                             int w_trans, const float* bias, const float* b_u_in, const float* b_l_in,
+                             float* A_prev_u, float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream);
 
 /* The input-layer region fused with the concretization (kernel #4):
  * lb = (A' . cvec - eps * sum_i |(A' W)_i| * rad_i) + b, ub mirrored;
@@ -118,11 +121,11 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
  * (runtime/perturbation.py:175-222, 327-359) on RightMatmulLinearOperator
  * (runtime/linear_operator.py:503-586) as called at runtime/crown_ibp.py:2044-2051.
  * h_scale/h_out (optional, lower bound only): h = h_scale[m] * sign(A'W) * rad,
- * the gradient seed of the concretization.
+ * the gradient seed of the concretization.  W / w_trans as for bf_crown_relu_linear_fwd.
  * workspace: bf_crown_relu_linear_concretize_workspace(D, S, I) floats. */
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
                                     int64_t N, const float* relax, const float* add_l, int64_t add_ld, const float* W,
-                                    int64_t I,
+                                    int64_t I, int w_trans,
                                     const float* bias, const float* cvec, const float* rad, float eps,
                                     const float* b_u_in, const float* b_l_in, const float* h_scale, float* h_out,
                                     float* workspace, float* lb, float* ub, hipStream_t stream);

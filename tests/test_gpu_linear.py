@@ -40,9 +40,10 @@ def test_gemm_matches_fp64(M, N, K, trans_b, abs_b):
     assert bool((err <= tol).all()), float((err / tol).max())
 
 
-def test_fused_relu_linear_region_golden():
+@pytest.mark.parametrize("w_trans", [0, 1])
+def test_fused_relu_linear_region_golden(w_trans):
     dev = device()
-    announce("fused relu+linear region vs reference fixture")
+    announce(f"fused relu+linear region vs reference fixture (w_trans={w_trans})")
     gz = load("fused_linear")
     A_u, A_l = t(gz["A_u"]), t(gz["A_l"])
     D, S, N = A_u.shape
@@ -57,8 +58,9 @@ def test_fused_relu_linear_region_golden():
     # the table holds exactly the executor request's alpha_u, beta_u, alpha_l, beta_l
     for i, k in enumerate(("alpha_u", "beta_u", "alpha_l", "beta_l")):
         assert torch.equal(table[..., i].cpu(), t(gz[k])), k
+    Wop = args[4].t().contiguous() if w_trans else args[4]
     _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(args[0]), _lib.ptr(args[1]), S * N, D, S, N, _lib.ptr(table),
-              None, 0, _lib.ptr(args[4]), P, _lib.ptr(args[5]), None, None,
+              None, 0, _lib.ptr(Wop), P, w_trans, _lib.ptr(args[5]), None, None,
               _lib.ptr(outs[0]), _lib.ptr(outs[1]), _lib.ptr(outs[2]), _lib.ptr(outs[3]), _lib.stream_handle())
     torch.cuda.synchronize()
     assert_bounds_close(outs[0].reshape(D, S, P), t(gz["A_prev_u"]), "A_prev_u", rtol=1e-5, atol=1e-5)
