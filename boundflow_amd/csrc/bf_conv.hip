@@ -14,6 +14,8 @@
 //   an optional fused concretization epilogue: the weighted |y| row sum (the
 //   Linf / box norm) and, for the gradient pass, h = h_scale[r] * sign(y) * w.
 
+#include <cstring>
+
 #include "bf_common.h"
 
 namespace bf {
@@ -125,6 +127,213 @@ conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// conv_transpose2d of coefficient rows on fp32 MFMA (v_mfma_f32_16x16x4f32).
+//
+// With KH % sh == 0 and KW % sw == 0, the output pixels split into sh*sw
+// parity classes (alpha, beta) = ((hi + ph) % sh, (wi + pw) % sw).  Within a
+// class, y[ci, u, v] = sum_{co, a, b} A[co, u - a, v - b] * W[co, ci, alpha + sh*a,
+// beta + sw*b] -- a dense gather-GEMM with K = Co * (KH/sh) * (KW/sw).  A row's
+// coefficient map is staged in LDS with a zero halo (no bounds checks in the
+// gather), the per-class weights once per workgroup; each wave computes
+// 16 (channel) x 16 (pixel) output tiles, D = W_class . A_gather.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int GT = 256;
+constexpr int GMAX_CLASSES = 16;
+
+struct GatherClass {
+  int np;              // pixels of the class
+  int n2;              // pixels per class row: p -> (q1, q2) = (p / n2, p % n2)
+  int poff0, s1, s2;   // padded-map offset of a pixel: poff0 + q1*s1 + q2*s2
+  int out0, o1, o2;    // output-map offset of a pixel: out0 + q1*o1 + q2*o2
+  int tbase;           // first task index of the class
+};
+
+struct GatherArgs {
+  const float* A[2];
+  float* y[2];
+  float* nrm[2];
+  const float* W;
+  const float* wv;
+  const float* h_scale;
+  float* h_out;
+  int64_t R, S, w_ld;
+  int rows_per_wg, z_lower_first;
+  int Co, Ho, Wo, Hp, Wp, pad_h, pad_w;
+  int Ci, Hi, Wi, KH, KW, sh, sw;
+  int nA, nB, T, Kc4, npad, nblk, nclasses, ntasks;
+  GatherClass cls[GMAX_CLASSES];
+};
+
+__global__ void __launch_bounds__(GT)
+conv_t_mfma_kernel(GatherArgs g) {
+  extern __shared__ float smem[];
+  float* Ws = smem;                                              // [nclasses][Kc4][npad]
+  int* koff = reinterpret_cast<int*>(Ws + (size_t)g.nclasses * g.Kc4 * g.npad);   // [Kc4]
+  float* As = reinterpret_cast<float*>(koff + g.Kc4);            // [Co][Hp][Wp]
+  __shared__ float red[GT / 64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int z = blockIdx.y;
+  const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
+  const float* __restrict__ A = g.A[z];
+  float* __restrict__ y = g.y[z];
+  float* __restrict__ nrm = g.nrm[z];
+  const int Kc = g.Co * g.T;
+  const int kstride = g.Kc4 * g.npad;
+
+  // weights of every class, zero-padded in k (to Kc4) and in channels (to npad)
+  for (int idx = tid; idx < g.nclasses * kstride; idx += GT) {
+    const int c = idx / kstride, rem = idx - c * kstride;
+    const int k = rem / g.npad, n = rem - k * g.npad;
+    float w = 0.f;
+    if (k < Kc && n < g.Ci) {
+      const int co = k / g.T, t = k - co * g.T;
+      const int a = t / g.nB, b = t - a * g.nB;
+      const int kh = c / g.sw + g.sh * a, kw = c % g.sw + g.sw * b;
+      w = g.W[(((int64_t)co * g.Ci + n) * g.KH + kh) * g.KW + kw];
+    }
+    Ws[idx] = w;
+  }
+  for (int k = tid; k < g.Kc4; k += GT) {
+    int off = 0;
+    if (k < Kc) {
+      const int co = k / g.T, t = k - co * g.T;
+      const int a = t / g.nB, b = t - a * g.nB;
+      off = co * g.Hp * g.Wp - a * g.Wp - b;
+    }
+    koff[k] = off;
+  }
+
+  const int nin = g.Co * g.Ho * g.Wo;
+  const int64_t nout = (int64_t)g.Ci * g.Hi * g.Wi;
+  const int HWi = g.Hi * g.Wi;
+  const int map = g.Co * g.Hp * g.Wp;
+  const int j = lane >> 4;     // k sub-index of the MFMA operands; output row group
+  const int col = lane & 15;   // pixel column (B operand / D column); channel row (A operand)
+
+  for (int i = 0; i < g.rows_per_wg; ++i) {
+    const int64_t r = (int64_t)blockIdx.x * g.rows_per_wg + i;
+    if (r >= g.R) break;   // uniform
+    __syncthreads();       // weights staged / previous row's map and partial sums consumed
+    const float* __restrict__ ar = A + r * nin;
+    for (int idx = tid; idx < map; idx += GT) {
+      const int co = idx / (g.Hp * g.Wp), rem = idx - co * g.Hp * g.Wp;
+      const int ho = rem / g.Wp - g.pad_h, wo = rem % g.Wp - g.pad_w;
+      As[idx] = (ho >= 0 && ho < g.Ho && wo >= 0 && wo < g.Wo) ? ar[(co * g.Ho + ho) * g.Wo + wo] : 0.f;
+    }
+    __syncthreads();
+    const int64_t d = r / g.S;
+    const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
+    float s = 0.f;
+    for (int task = wave; task < g.ntasks; task += GT / 64) {
+      int c = 0;
+      while (c + 1 < g.nclasses && task >= g.cls[c + 1].tbase) ++c;
+      const GatherClass& C = g.cls[c];
+      const int tl = task - C.tbase;
+      const int pt = tl / g.nblk, cb = tl - pt * g.nblk;
+      const int p = pt * 16 + col;
+      const bool pok = p < C.np;
+      const int pc = pok ? p : C.np - 1;
+      const int q1 = pc / C.n2, q2 = pc - q1 * C.n2;
+      const float* __restrict__ as = As + C.poff0 + q1 * C.s1 + q2 * C.s2;
+      const float* __restrict__ ws = Ws + (size_t)c * kstride + cb * 16 + col;
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int k = j; k < g.Kc4; k += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[k * g.npad], as[koff[k]], acc, 0, 0, 0);
+      const int opix = C.out0 + q1 * C.o1 + q2 * C.o2;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int n = cb * 16 + 4 * j + rr;
+        if (n < g.Ci && pok) {
+          const float v = acc[rr];
+          const int64_t oidx = (int64_t)n * HWi + opix;
+          if (y) y[r * nout + oidx] = v;
+          if (nrm) {
+            const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
+            s += g.wv ? fabsf(v) * wgt : fabsf(v);
+            if (lower && g.h_out) {
+              const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
+              g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
+            }
+          }
+        }
+      }
+    }
+    if (nrm) {
+      for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+      if (lane == 0) red[wave] = s;
+      __syncthreads();
+      if (tid == 0) {
+        float t = 0.f;
+        for (int q = 0; q < GT / 64; ++q) t += red[q];
+        nrm[r] = t;
+      }
+    }
+  }
+}
+
+// floor / ceil of x / y for y > 0 and any sign of x
+static inline int fdiv(int x, int y) { return x >= 0 ? x / y : -((-x + y - 1) / y); }
+static inline int cdiv(int x, int y) { return x >= 0 ? (x + y - 1) / y : -((-x) / y); }
+
+// Build the class decomposition; returns false when the MFMA path does not apply.
+static bool conv_t_mfma_plan(GatherArgs& g, int64_t R, int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh,
+                             int sw, int ph, int pw, int Hi, int Wi, size_t* lds_bytes) {
+  if (KH % sh || KW % sw || sh * sw > GMAX_CLASSES) return false;
+  g.Co = Co; g.Ho = Ho; g.Wo = Wo; g.Ci = Ci; g.Hi = Hi; g.Wi = Wi;
+  g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw;
+  g.nA = KH / sh; g.nB = KW / sw; g.T = g.nA * g.nB;
+  g.Kc4 = (Co * g.T + 3) / 4 * 4;
+  g.npad = (Ci + 15) / 16 * 16;
+  g.nblk = g.npad / 16;
+  g.nclasses = sh * sw;
+  int umin_all = 1 << 30, umax_all = -(1 << 30), vmin_all = 1 << 30, vmax_all = -(1 << 30);
+  int umin[GMAX_CLASSES], vmin[GMAX_CLASSES], nu[GMAX_CLASSES], nv[GMAX_CLASSES];
+  for (int c = 0; c < g.nclasses; ++c) {
+    const int al = c / sw, be = c % sw;
+    umin[c] = cdiv(ph - al, sh);
+    vmin[c] = cdiv(pw - be, sw);
+    const int umax = fdiv(Hi - 1 + ph - al, sh), vmax = fdiv(Wi - 1 + pw - be, sw);
+    nu[c] = umax >= umin[c] ? umax - umin[c] + 1 : 0;
+    nv[c] = vmax >= vmin[c] ? vmax - vmin[c] + 1 : 0;
+    if (nu[c] && nv[c]) {
+      umin_all = umin[c] < umin_all ? umin[c] : umin_all;
+      vmin_all = vmin[c] < vmin_all ? vmin[c] : vmin_all;
+      umax_all = umax > umax_all ? umax : umax_all;
+      vmax_all = vmax > vmax_all ? vmax : vmax_all;
+    }
+  }
+  if (umax_all < 0) return false;
+  // halo so that u - a and v - b (a < nA, b < nB) always index inside the padded map
+  g.pad_h = (g.nA - 1) - umin_all > 0 ? (g.nA - 1) - umin_all : 0;
+  g.pad_w = (g.nB - 1) - vmin_all > 0 ? (g.nB - 1) - vmin_all : 0;
+  g.Hp = (Ho > umax_all + 1 ? Ho : umax_all + 1) + g.pad_h;
+  g.Wp = (Wo > vmax_all + 1 ? Wo : vmax_all + 1) + g.pad_w;
+  int ntasks = 0;
+  for (int c = 0; c < g.nclasses; ++c) {
+    GatherClass& C = g.cls[c];
+    const int al = c / sw, be = c % sw;
+    C.np = nu[c] * nv[c];
+    C.n2 = nv[c] > 0 ? nv[c] : 1;
+    C.poff0 = (umin[c] + g.pad_h) * g.Wp + vmin[c] + g.pad_w;
+    C.s1 = g.Wp;
+    C.s2 = 1;
+    C.out0 = (sh * umin[c] + al - ph) * Wi + sw * vmin[c] + be - pw;
+    C.o1 = sh * Wi;
+    C.o2 = sw;
+    C.tbase = ntasks;
+    ntasks += (C.np + 15) / 16 * g.nblk;
+  }
+  g.ntasks = ntasks;
+  const size_t lds = sizeof(float) * ((size_t)g.nclasses * g.Kc4 * g.npad + g.Kc4 + (size_t)Co * g.Hp * g.Wp);
+  if (lds > 64 * 1024) return false;
+  *lds_bytes = lds;
+  g.R = R;
+  return true;
+}
+
 int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
                       hipStream_t stream);
 int ibp_finalize(const float* c, const float* r, const float* rownorm, float eps, const float* bias,
@@ -175,9 +384,35 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
              "bf_conv_transpose_rows: each given coefficient needs an output or a norm");
   BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || norm_l != nullptr),
              "bf_conv_transpose_rows: h_out needs h_scale and the lower norm");
+  const unsigned nz = (A_u && A_l) ? 2u : 1u;
+  {
+    GatherArgs g;
+    memset(&g, 0, sizeof(g));
+    size_t glds = 0;
+    if (conv_t_mfma_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
+      int nzi = 0;
+      if (A_u) { g.A[nzi] = A_u; g.y[nzi] = y_u; g.nrm[nzi] = norm_u; ++nzi; }
+      if (A_l) { g.A[nzi] = A_l; g.y[nzi] = y_l; g.nrm[nzi] = norm_l; ++nzi; }
+      g.z_lower_first = A_u ? 0 : 1;
+      g.W = W;
+      g.wv = wvec;
+      g.w_ld = w_ld;
+      g.h_scale = h_scale;
+      g.h_out = h_out;
+      g.S = S;
+      // rows per workgroup: amortize the weight stage, keep >= ~3 workgroups per CU
+      const int64_t work = R * nz;
+      int rpw = (int)(work / 768);
+      rpw = rpw < 1 ? 1 : (rpw > 8 ? 8 : rpw);
+      g.rows_per_wg = rpw;
+      BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
+      hipLaunchKernelGGL(conv_t_mfma_kernel, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GT), glds, stream, g);
+      BF_LAUNCH_CHECK("conv_t_mfma_kernel");
+      return BF_OK;
+    }
+  }
   const size_t lds = sizeof(float) * (size_t)Co * Ho * Wo;
   BF_REQUIRE(lds <= 64 * 1024, "bf_conv_transpose_rows: coefficient map exceeds the 64 KB LDS row stage");
-  const unsigned nz = (A_u && A_l) ? 2u : 1u;
   hipLaunchKernelGGL(conv_transpose_rows_kernel, dim3((unsigned)R, nz), dim3(CT), lds, stream, A_u, A_l, Co, Ho, Wo,
                      W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S, wvec, w_ld, norm_u, norm_l, h_scale, h_out);
   BF_LAUNCH_CHECK("conv_transpose_rows_kernel");

@@ -24,6 +24,8 @@
 // of the 8 XCDs receives a contiguous run of tiles, so the column tiles that
 // share an A row-block share that XCD's L2.
 
+#include <type_traits>
+
 #include "bf_common.h"
 #include "bf_gemm_args.h"
 
@@ -79,6 +81,8 @@ gemm_kernel(GemmArgs p) {
   constexpr int TK = (PRO == PRO_RELAX) ? GBK : 1;
   __shared__ float4 Ts[2][TE];   // relaxation table slice of a K tile, double-buffered
   __shared__ float As_add[2][TE];  // beta split coefficient slice (lower bound)
+  constexpr int TC = (PRO == PRO_RELAX && EPI == EPI_ABSSUM) ? T::TAB_ENTRIES : 1;
+  __shared__ float Cs[2][TC];      // center-vector slice (concretization)
   __shared__ float Kb[2][TK];    // affine bias slice
 
   const int t = threadIdx.x;
@@ -193,7 +197,7 @@ gemm_kernel(GemmArgs p) {
   int d_first = 0;
   int ndom = 0;
   bool tab_lds = false;
-  if (PRO == PRO_RELAX && p.relax) {
+  if (PRO == PRO_RELAX && p.relax && (EPI != EPI_ABSSUM || p.cvec)) {
     const int64_t m_last = (m0 + GBM < M ? m0 + GBM : M) - 1;
     d_first = (int)(m0 / p.S);
     const int64_t nd = m_last / p.S - d_first + 1;
@@ -201,76 +205,12 @@ gemm_kernel(GemmArgs p) {
     ndom = tab_lds ? (int)nd : 0;
   }
   const int e_dom = t / GBK, e_k = t % GBK;   // this thread's table entry
-  float4 tab_reg = make_float4(1.f, 0.f, 1.f, 0.f);
-  float add_reg = 0.f, kb_reg = 0.f;
-  auto load_tab = [&](int64_t k0) {
-    if (PRO != PRO_RELAX) return;
-    const int64_t k = k0 + e_k;
-    const bool ok = tab_lds && e_dom < ndom && k < K;
-    const int64_t d = (int64_t)d_first + e_dom;
-    tab_reg = ok ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
-    if (use_add) add_reg = ok ? p.add_l[d * p.add_ld + k] : 0.f;
-    if (t < GBK) kb_reg = (tab_lds && p.kbias && k0 + t < K) ? p.kbias[k0 + t] : 0.f;
-  };
-  auto store_tab = [&](int slot) {
-    if (PRO != PRO_RELAX) return;
-    Ts[slot][t] = tab_reg;
-    if (use_add) As_add[slot][t] = add_reg;
-    if (t < GBK) Kb[slot][t] = kb_reg;
-  };
-
-  // ReLU relaxation of one coefficient (crown_ibp.py:1261-1296), applied as the
-  // A tile is written to LDS; padding elements (outside M or K) stay zero.
-  auto relax_one = [&](float a, int j, int64_t k, int64_t k0, int slot) -> float {
-    if (k >= K) return a;
-    const int64_t d = a_dom[j];
-    float4 r;
-    float add = 0.f, kb = 0.f;
-    if (tab_lds) {
-      const int e = (a_dom[j] - d_first) * GBK + (int)(k - k0);
-      r = Ts[slot][e];
-      if (use_add) add = As_add[slot][e];
-      kb = Kb[slot][k - k0];
-    } else {
-      r = p.relax ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
-      if (use_add) add = p.add_l[d * p.add_ld + k];
-      if (p.kbias) kb = p.kbias[k];
-    }
-    float be;
-    float out = a * fsel(r, lower, a >= 0.f, &be);
-    if (use_add) out = out + add;
-    if (row_reduce) {
-      s_beta[j] += a * be;
-      if (p.kbias) s_bias[j] += out * kb;
-      if (p.cvec) s_cen[j] += out * p.cvec[d * p.cvec_ld + k];
-    }
-    return out;
-  };
-
-  // kt: index of the K tile being stored (its relaxation slice is in slot kt & 1)
-  auto store_tiles = [&](int buf, int64_t k0, int64_t kt) {
-    const int slot = (int)(kt & 1);
+  // LDS entry of this thread's first coefficient of slot j (loop invariant);
+  // rows past M read their first domain's entries, their results are discarded
+  int e_base[A_SLOTS];
 #pragma unroll
-    for (int j = 0; j < A_SLOTS; ++j) {
-      const int r = a_r0 + RPP * j;
-      float4 v = a_reg[j];
-      if (PRO == PRO_RELAX && m0 + r < M) {
-        const int64_t k = k0 + 4 * a_kq;
-        v.x = relax_one(v.x, j, k + 0, k0, slot);
-        v.y = relax_one(v.y, j, k + 1, k0, slot);
-        v.z = relax_one(v.z, j, k + 2, k0, slot);
-        v.w = relax_one(v.w, j, k + 3, k0, slot);
-      }
-      *reinterpret_cast<float4*>(&As[buf][r * AP + 4 * a_kq]) = v;
-    }
-#pragma unroll
-    for (int j = 0; j < B_SLOTS; ++j) {
-      const int q = t + GNT * j;
-      const int n = TRANS_B ? q / KQ : q % GBN;
-      const int kq = TRANS_B ? q % KQ : q / GBN;
-      *reinterpret_cast<float4*>(&Bs[buf][n * BPT + 4 * kq]) = b_reg[j];
-    }
-  };
+  for (int j = 0; j < A_SLOTS; ++j)
+    e_base[j] = ((m0 + a_r0 + RPP * j < M ? a_dom[j] : d_first) - d_first) * GBK + 4 * a_kq;
 
   floatx16 acc[FM][FN];
 #pragma unroll
@@ -281,56 +221,175 @@ gemm_kernel(GemmArgs p) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int64_t nk = ceil_div(K, GBK);
-  // Prologue: relaxation slices of K tiles 0 and 1, then tile 0 itself.
-  load_tab(0);
-  store_tab(0);
-  if (nk > 1) {
-    load_tab(GBK);
-    store_tab(1);
-  }
-  load_tiles(0);
-  __syncthreads();
-  store_tiles(0, 0, 0);
-  __syncthreads();
-  int buf = 0;
   const int lrow = lane & 31;
   const int h = lane >> 5;   // lane half -> k half of the tile
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    const bool more2 = kt + 2 < nk;
-    if (more) load_tiles((kt + 1) * GBK);
-    if (more2) load_tab((kt + 2) * GBK);
-    const float* __restrict__ as = As[buf];
-    const float* __restrict__ bs = Bs[buf];
-#pragma unroll
-    for (int jb = 0; jb < GBK / 2; jb += 4) {
-      float av[FM][4];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const float4 a4 = *reinterpret_cast<const float4*>(
-            &as[(wm * T::WTM + i * 32 + lrow) * AP + h * (GBK / 2) + jb]);
-        av[i][0] = a4.x; av[i][1] = a4.y; av[i][2] = a4.z; av[i][3] = a4.w;
+
+  // The main loop, instantiated per combination of the uniform relaxation
+  // options so that the loop body carries no branches on them.  FAST: operands
+  // from the LDS slices; ADD: beta split term; KB: affine bias; RR: row sums
+  // (first column tile only); the center sums follow EPI == EPI_ABSSUM.
+  auto main_loop = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c) {
+    constexpr bool FAST = decltype(fast_c)::value;
+    constexpr bool ADD = decltype(add_c)::value;
+    constexpr bool KB = decltype(kb_c)::value;
+    constexpr bool RR = decltype(rr_c)::value;
+    constexpr bool CV = (EPI == EPI_ABSSUM);
+    float4 tab_reg = make_float4(1.f, 0.f, 1.f, 0.f);
+    float add_reg = 0.f, kb_reg = 0.f, cv_reg = 0.f;
+
+    auto load_tab = [&](int64_t k0) {
+      if constexpr (PRO == PRO_RELAX && FAST) {
+        const int64_t k = k0 + e_k;
+        const bool ok = e_dom < ndom && k < K;
+        const int64_t d = (int64_t)d_first + e_dom;
+        tab_reg = ok ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
+        if constexpr (ADD) add_reg = ok ? p.add_l[d * p.add_ld + k] : 0.f;
+        if constexpr (CV && RR) cv_reg = ok ? p.cvec[d * p.cvec_ld + k] : 0.f;
+        if constexpr (KB && RR)
+          if (t < GBK) kb_reg = (k0 + t < K) ? p.kbias[k0 + t] : 0.f;
       }
-      float bv[FN][4];
+    };
+    auto store_tab = [&](int slot) {
+      if constexpr (PRO == PRO_RELAX && FAST) {
+        Ts[slot][t] = tab_reg;
+        if constexpr (ADD) As_add[slot][t] = add_reg;
+        if constexpr (CV && RR) Cs[slot][t] = cv_reg;
+        if constexpr (KB && RR)
+          if (t < GBK) Kb[slot][t] = kb_reg;
+      }
+    };
+
+    // ReLU relaxation of one coefficient (crown_ibp.py:1261-1296), applied as
+    // the A tile is written to LDS.  Fast path: padding coefficients (k >= K)
+    // are zero and meet identity / zero entries, so they contribute nothing.
+    auto relax_one = [&](float a, int j, int e, int64_t k, int slot) -> float {
+      float4 r;
+      float add = 0.f, kb = 0.f, cv = 0.f;
+      if constexpr (FAST) {
+        r = Ts[slot][e_base[j] + e];
+        if constexpr (ADD) add = As_add[slot][e_base[j] + e];
+        if constexpr (KB && RR) kb = Kb[slot][4 * a_kq + e];
+        if constexpr (CV && RR) cv = Cs[slot][e_base[j] + e];
+      } else {
+        if (k >= K) return a;
+        const int64_t d = a_dom[j];
+        r = p.relax ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
+        if (use_add) add = p.add_l[d * p.add_ld + k];
+        if (p.kbias) kb = p.kbias[k];
+        if (p.cvec) cv = p.cvec[d * p.cvec_ld + k];
+      }
+      float be;
+      float out = a * fsel(r, lower, a >= 0.f, &be);
+      if constexpr (FAST) {
+        if constexpr (ADD) out = out + add;
+        if constexpr (RR) {
+          s_beta[j] += a * be;
+          if constexpr (KB) s_bias[j] += out * kb;
+          if constexpr (CV) s_cen[j] += out * cv;
+        }
+      } else {
+        if (use_add) out = out + add;
+        if (row_reduce) {
+          s_beta[j] += a * be;
+          if (p.kbias) s_bias[j] += out * kb;
+          if (p.cvec) s_cen[j] += out * cv;
+        }
+      }
+      return out;
+    };
+
+    // kt: index of the K tile being stored (its relaxation slice is in slot kt & 1)
+    auto store_tiles = [&](int buf, int64_t k0, int64_t kt) {
+      const int slot = (int)(kt & 1);
 #pragma unroll
-      for (int jj = 0; jj < FN; ++jj) {
-        const float4 b4 = *reinterpret_cast<const float4*>(
-            &bs[(wn * T::WTN + jj * 32 + lrow) * BPT + h * (GBK / 2) + jb]);
-        bv[jj][0] = b4.x; bv[jj][1] = b4.y; bv[jj][2] = b4.z; bv[jj][3] = b4.w;
+      for (int j = 0; j < A_SLOTS; ++j) {
+        const int r = a_r0 + RPP * j;
+        float4 v = a_reg[j];
+        if constexpr (PRO == PRO_RELAX) {
+          if (FAST || m0 + r < M) {
+            const int64_t k = k0 + 4 * a_kq;
+            v.x = relax_one(v.x, j, 0, k + 0, slot);
+            v.y = relax_one(v.y, j, 1, k + 1, slot);
+            v.z = relax_one(v.z, j, 2, k + 2, slot);
+            v.w = relax_one(v.w, j, 3, k + 3, slot);
+          }
+        }
+        *reinterpret_cast<float4*>(&As[buf][r * AP + 4 * a_kq]) = v;
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int jj = 0; jj < FN; ++jj)
-            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
+      for (int j = 0; j < B_SLOTS; ++j) {
+        const int q = t + GNT * j;
+        const int n = TRANS_B ? q / KQ : q % GBN;
+        const int kq = TRANS_B ? q % KQ : q / GBN;
+        *reinterpret_cast<float4*>(&Bs[buf][n * BPT + 4 * kq]) = b_reg[j];
+      }
+    };
+
+    // Prologue: relaxation slices of K tiles 0 and 1, then tile 0 itself.
+    load_tab(0);
+    store_tab(0);
+    if (nk > 1) {
+      load_tab(GBK);
+      store_tab(1);
     }
-    if (more) store_tiles(buf ^ 1, (kt + 1) * GBK, kt + 1);
-    // slot kt & 1 held tile kt's slice, consumed one iteration ago
-    if (more2) store_tab((int)(kt & 1));
+    load_tiles(0);
     __syncthreads();
-    buf ^= 1;
+    store_tiles(0, 0, 0);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const bool more = kt + 1 < nk;
+      const bool more2 = kt + 2 < nk;
+      if (more) load_tiles((kt + 1) * GBK);
+      if (more2) load_tab((kt + 2) * GBK);
+      const float* __restrict__ as = As[buf];
+      const float* __restrict__ bs = Bs[buf];
+#pragma unroll
+      for (int jb = 0; jb < GBK / 2; jb += 4) {
+        float av[FM][4];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const float4 a4 = *reinterpret_cast<const float4*>(
+              &as[(wm * T::WTM + i * 32 + lrow) * AP + h * (GBK / 2) + jb]);
+          av[i][0] = a4.x; av[i][1] = a4.y; av[i][2] = a4.z; av[i][3] = a4.w;
+        }
+        float bv[FN][4];
+#pragma unroll
+        for (int jj = 0; jj < FN; ++jj) {
+          const float4 b4 = *reinterpret_cast<const float4*>(
+              &bs[(wn * T::WTN + jj * 32 + lrow) * BPT + h * (GBK / 2) + jb]);
+          bv[jj][0] = b4.x; bv[jj][1] = b4.y; bv[jj][2] = b4.z; bv[jj][3] = b4.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int jj = 0; jj < FN; ++jj)
+              acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
+      }
+      if (more) store_tiles(buf ^ 1, (kt + 1) * GBK, kt + 1);
+      // slot kt & 1 held tile kt's slice, consumed one iteration ago
+      if (more2) store_tab((int)(kt & 1));
+      __syncthreads();
+      buf ^= 1;
+    }
+  };
+
+  using TT = std::true_type;
+  using FF = std::false_type;
+  if constexpr (PRO == PRO_PLAIN) {
+    main_loop(FF{}, FF{}, FF{}, FF{});
+  } else {
+    const bool kb = p.kbias != nullptr;
+    if (!tab_lds) main_loop(FF{}, FF{}, FF{}, FF{});
+    else if (row_reduce) {
+      if (use_add) { if (kb) main_loop(TT{}, TT{}, TT{}, TT{}); else main_loop(TT{}, TT{}, FF{}, TT{}); }
+      else { if (kb) main_loop(TT{}, FF{}, TT{}, TT{}); else main_loop(TT{}, FF{}, FF{}, TT{}); }
+    } else {
+      if (use_add) main_loop(TT{}, TT{}, FF{}, FF{});
+      else main_loop(TT{}, FF{}, FF{}, FF{});
+    }
   }
 
   // Row reductions of the relaxation prologue: the KQ threads holding one row

@@ -78,15 +78,73 @@ def _oracle_grads(w, alpha, beta=None, splits=None, per_batch=True, dtype=torch.
     return b, ga, gb
 
 
-def _grad_close(got, ref32, ref64, what):
+def _abs_op(op):
+    """The same lazy input-layer operator over |coefficients| and |weights|: its
+    dense form is sum_k |A_k| |W_k,i|, the magnitude bound of each coefficient's sum."""
+    if isinstance(op, cr.DenseOp):
+        return cr.DenseOp(op.coeffs.abs(), op.input_shape)
+    if isinstance(op, cr.RightMatmulOp):
+        return cr.RightMatmulOp(_abs_op(op.base), op.rhs.abs())
+    if isinstance(op, cr.ReshapeOp):
+        return cr.ReshapeOp(_abs_op(op.base), op.input_shape)
+    if isinstance(op, cr.Conv2dOp):
+        return cr.Conv2dOp(_abs_op(op.base), op.weight.abs(), op.stride, op.padding, op.dilation, op.groups,
+                           op.input_shape)
+    raise TypeError(type(op))
+
+
+def _sign_tie_allowance(w64, alpha64, per_batch, tau=1e-5):
+    """Float64 bound of how far dL/dalpha may move when the sign of an input-layer
+    coefficient y_i (the concretization's |y_i| term, whose derivative is
+    sign(y_i)) is decided the other way.  Only coefficients with
+    |y_i| <= tau * sum_k |terms| -- inside fp32 rounding of their sum -- count;
+    flipping one changes the lower bound's gradient by 2 * eps * dy_i/dalpha,
+    scaled by the loss's mean over specs (and batch when shared)."""
+    captured = {}
+    orig = cr.concretize_affine
+
+    def capture(spec, center, op, b):
+        captured["dense"] = op.to_dense()
+        captured["bound"] = _abs_op(op).to_dense().detach()
+        return orig(spec, center, op, b)
+
+    a = {k: v.clone().requires_grad_(True) for k, v in alpha64.items()}
+    cr.concretize_affine = capture
+    try:
+        env, pre = cr.forward_ibp_trace(w64.module, w64.spec)
+        cr.crown_backward_from_trace(w64.module, w64.spec, interval_env=env, relu_pre=pre, linear_spec_C=w64.C,
+                                     relu_alpha=a)
+    finally:
+        cr.concretize_affine = orig
+    dense, bound = captured["dense"], captured["bound"]
+    B, S = int(dense.shape[0]), int(dense.shape[1])
+    eps = float(w64.spec.perturbation.eps)
+    scale = 1.0 / S if per_batch else 1.0 / (S * B)
+    flat = dense.reshape(-1)
+    tie = (flat.detach().abs() <= tau * bound.reshape(-1)).nonzero().flatten().tolist()
+    allow = {k: torch.zeros_like(v) for k, v in alpha64.items()}
+    for i in tie:
+        grads = torch.autograd.grad(flat[i], list(a.values()), retain_graph=True, allow_unused=True)
+        for (k, _), gr in zip(a.items(), grads):
+            if gr is not None:
+                allow[k] += 2.0 * eps * scale * gr.abs()
+    return allow, len(tie)
+
+
+def _grad_close(got, ref32, ref64, what, allowance=None):
+    """|hip - fp64| within 4x the CPU fp32 reference's own error or 1e-5 of the
+    gradient's scale, plus (elementwise) the sign-tie allowance when given."""
     g = got.detach().cpu().double().reshape(ref32.shape)
     r = ref32.double()
     e = ref64.double()
     scale = float(e.abs().max()) + 1e-30
-    err = float((g - e).abs().max())
+    err = (g - e).abs()
     ref_err = float((r - e).abs().max())
-    announce(f"{what}: max|hip-fp64|={err:.3e} max|cpu32-fp64|={ref_err:.3e} scale={scale:.3e}")
-    assert err <= max(4.0 * ref_err, 1e-5 * scale), what
+    base = max(4.0 * ref_err, 1e-5 * scale)
+    extra = torch.zeros_like(err) if allowance is None else allowance.double().reshape(err.shape)
+    announce(f"{what}: max|hip-fp64|={float(err.max()):.3e} max|cpu32-fp64|={ref_err:.3e} scale={scale:.3e} "
+             f"max allowance={float(extra.max()):.3e}")
+    assert bool((err <= base + extra).all()), what
 
 
 @pytest.mark.parametrize("case", ["mlp_beta", "cnn_alpha"])
@@ -116,8 +174,14 @@ def test_lower_bound_gradients_match_autograd(case):
         wd.module, wd.spec, linear_spec_C=wd.C, relu_alpha={k: v.to(dev) for k, v in alpha.items()},
         relu_beta=None if beta is None else {k: v.to(dev) for k, v in beta.items()}, relu_split_state=sd)
     assert_parity(bounds.lower, ref32.lower, ref64.lower, f"{case} lower")
+    allow = None
+    if beta is None:
+        # the gradient jumps where an input-layer coefficient's sign is within fp32 rounding of 0
+        allow, nties = _sign_tie_allowance(parity.to_float64(w), {k: v.double() for k, v in alpha.items()},
+                                           per_batch=True)
+        announce(f"{case}: {nties} input-layer coefficients within fp32 rounding of zero")
     for k in ga32:
-        _grad_close(ga[k], ga32[k], ga64[k], f"{case} dL/dalpha[{k}]")
+        _grad_close(ga[k], ga32[k], ga64[k], f"{case} dL/dalpha[{k}]", None if allow is None else allow[k])
     if gb32 is not None:
         for k in gb32:
             _grad_close(gb[k], gb32[k], gb64[k], f"{case} dL/dbeta[{k}]")
