@@ -15,6 +15,8 @@ from typing import Optional
 
 import torch
 
+from . import profiling
+
 LIB_PATH = Path(__file__).resolve().parent / "libboundflow_hip.so"
 
 P = ctypes.c_void_p
@@ -29,7 +31,8 @@ SIGNATURES = {
     "bf_last_error": (ctypes.c_char_p, []),
     "bf_tuning_set_gemm_tile": (I32, [I32]),
     "bf_gemm": (I32, [P, I64, P, I64, I32, I32, P, I64, I64, I64, I64, P]),
-    "bf_gemm_rank1": (I32, [P, I64, P, I64, I32, P, I64, I64, I64, I64, I64, P, P, I64, P]),
+    "bf_gemm_rank1": (I32, [P, I64, P, I64, I32, P, I64, I64, I64, I64, I64, P, P, I64, P, I64, P]),
+    "bf_gemm_rank1_workspace": (I64, [I64, I64, I64]),
     "bf_relu_relax_table": (I32, [P, P, P, I64, I64, I64, P, P]),
     "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, P, P, P, P, P]),
     "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, F32, P, P,
@@ -91,10 +94,22 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+class DevicePtr(ctypes.c_void_p):
+    """A tensor's address that keeps the tensor alive.  Arguments such as
+    ``ptr(x.contiguous())`` may be temporaries; held here, they survive until
+    the call that receives them has enqueued its kernels, so the caching
+    allocator cannot hand their memory to a later argument of the same call
+    (later reuse is ordered after the launch on the stream)."""
+
+    def __init__(self, t: torch.Tensor):
+        super().__init__(t.data_ptr())
+        self.tensor = t
+
+
 def ptr(t: Optional[torch.Tensor]):
     if t is None:
         return None
-    return ctypes.c_void_p(t.data_ptr())
+    return DevicePtr(t)
 
 
 def stream_handle(stream: Optional[torch.cuda.Stream] = None):
@@ -105,7 +120,10 @@ def stream_handle(stream: Optional[torch.cuda.Stream] = None):
 def call(name: str, *args) -> int:
     """Invoke an entry point and raise HipError with bf_last_error() on failure."""
     lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = getattr(lib, name)
+    profiling.begin_call()
+    rc = fn(*args)
+    profiling.end_call()
     if SIGNATURES[name][0] is I32 and name != "bf_abi_version" and rc != 0:
         msg = lib.bf_last_error().decode(errors="replace")
         raise HipError(f"{name} failed (status {rc}): {msg}")

@@ -45,12 +45,28 @@ from .spec import InputSpec, IntervalState, normalize_input_spec
 
 @dataclass
 class AlphaBetaStats:
+    """Run statistics.  The branching decision stays on the device
+    (``branch_layer`` / ``branch_neuron``, layer -1 = no ambiguous neuron);
+    ``branch_choices`` converts it to the reference's list of
+    ``(relu_input, index)`` on first access, so a run issues no host
+    synchronization unless the caller asks for it."""
+
     feasibility: str = "unknown"
     reason: str = "ok"
-    branch_choices: Optional[List[Optional[Tuple[str, int]]]] = None
     infeasible: Optional[torch.Tensor] = None
     steps: int = 0
     lr: float = 0.0
+    branch_layer: Optional[torch.Tensor] = None
+    branch_neuron: Optional[torch.Tensor] = None
+    relu_names: Tuple[str, ...] = ()
+
+    @property
+    def branch_choices(self) -> Optional[List[Optional[Tuple[str, int]]]]:
+        if self.branch_layer is None:
+            return None
+        lay = self.branch_layer.cpu().tolist()
+        ids = self.branch_neuron.cpu().tolist()
+        return [None if lay[i] < 0 else (self.relu_names[lay[i]], int(ids[i])) for i in range(len(lay))]
 
 
 class _Adam:
@@ -138,10 +154,12 @@ def _grad_pass(spec: InputSpec, chain: Chain, trace: ForwardTrace, saved: dict, 
             vec_ld = 0
         gt = torch.empty(M, n_out, device=dev)
         if layer.kind == "linear":
+            wsz = int(_lib.load().bf_gemm_rank1_workspace(M, n_out, n_in))
+            ws = torch.empty(wsz, device=dev) if wsz else None
             with _timed("grad_gemm", 2.0 * M * n_in * n_out, 4.0 * (M * n_in + M * n_out + n_in * n_out)):
                 _lib.call("bf_gemm_rank1", _lib.ptr(g), n_in, _lib.ptr(layer.weight.contiguous()), n_in, 1,
                           _lib.ptr(gt), n_out, M, n_out, n_in, S, _lib.ptr(G if vec is not None else None),
-                          _lib.ptr(vec), vec_ld, stream)
+                          _lib.ptr(vec), vec_ld, _lib.ptr(ws), wsz, stream)
         else:
             Ci, Hi, Wi = layer.in_shape
             Co, Ho, Wo = layer.out_shape
@@ -237,7 +255,7 @@ def run_alpha_beta_crown_mlp(
                 splits[n] = (s, ld)
     # names whose split has a nonzero entry get the beta coefficient (alpha_beta_crown.py:630-633)
     beta_names = [n for n, (s, _ld) in splits.items() if bool((s != 0).any().item())]
-    choices = branch_choices(trace, B)
+    b_layer, b_neuron, _gap = branch_tensors(trace, B) if trace.relu_pre else (None, None, None)
     S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else _numel(chain.layers[-1].out_shape)
     M = B * S
     # d(-sum_d mean_s lb)/dlb = -1/S ; d(-mean_d mean_s lb)/dlb = (-1/B)/S   (fp32, as autograd divides)
@@ -295,7 +313,8 @@ def run_alpha_beta_crown_mlp(
             adam_b[n].step(gb, lr, 0.0, None, stream)
     out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
     out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
-    stats = AlphaBetaStats(branch_choices=choices, infeasible=trace.infeasible, steps=int(steps), lr=float(lr))
+    stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,
+                           branch_neuron=b_neuron, relu_names=tuple(trace.relu_pre.keys()))
     return IntervalState(lower=best_lb, upper=best_ub), out_alpha, out_beta, stats
 
 

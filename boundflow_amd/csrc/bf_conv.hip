@@ -128,19 +128,27 @@ conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restric
 }
 
 // ---------------------------------------------------------------------------
-// conv_transpose2d of coefficient rows on fp32 MFMA (v_mfma_f32_16x16x4f32).
+// Convolutions of rows on fp32 MFMA (v_mfma_f32_16x16x4f32) as gather-GEMMs.
 //
-// With KH % sh == 0 and KW % sw == 0, the output pixels split into sh*sw
-// parity classes (alpha, beta) = ((hi + ph) % sh, (wi + pw) % sw).  Within a
-// class, y[ci, u, v] = sum_{co, a, b} A[co, u - a, v - b] * W[co, ci, alpha + sh*a,
-// beta + sw*b] -- a dense gather-GEMM with K = Co * (KH/sh) * (KW/sw).  A row's
-// coefficient map is staged in LDS with a zero halo (no bounds checks in the
-// gather), the per-class weights once per workgroup; each wave computes
-// 16 (channel) x 16 (pixel) output tiles, D = W_class . A_gather.
+// One row's input map is staged in LDS with a zero halo, so every operand
+// gather is in bounds without checks, and the weights once per workgroup.
+// Output pixels are grouped in classes; within a class,
+//   out[n, pixel] = sum_k Wc[n, k] * map[koff[k] + poff(pixel)],
+// computed as 16 (channel) x 16 (pixel) tiles per wave, D = Wc . gather.
+//
+// * MODE_T (conv_transpose2d of coefficient rows, KH % sh == 0, KW % sw == 0):
+//   sh*sw parity classes (alpha, beta) = ((hi + ph) % sh, (wi + pw) % sw); in a
+//   class y[ci, u, v] = sum_{co, a, b} A[co, u - a, v - b] W[co, ci, alpha + sh*a,
+//   beta + sw*b], k = (co, a, b).  Epilogue: store, or the concretization norm
+//   sum |y| * w and the gradient seed h = h_scale * sign(y) * w.
+// * MODE_F (conv2d): one class, k = (ci, kh, kw),
+//   y[co, ho, wo] = sum_k W[co, ci, kh, kw] x[ci, ho*sh - ph + kh, wo*sw - pw + kw]
+//   (optionally |W|), plus the rank-1 term row_scale[r] * vec[(r / vec_div) * vec_ld + e].
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int GT = 256;
 constexpr int GMAX_CLASSES = 16;
+enum : int { MODE_T = 0, MODE_F = 1 };
 
 struct GatherClass {
   int np;              // pixels of the class
@@ -151,36 +159,42 @@ struct GatherClass {
 };
 
 struct GatherArgs {
-  const float* A[2];
+  const float* X[2];   // input rows per blockIdx.y
   float* y[2];
   float* nrm[2];
   const float* W;
-  const float* wv;
+  int abs_w;
+  const float* wv;     // MODE_T norm weights [D, nout] (w_ld)
   const float* h_scale;
   float* h_out;
-  int64_t R, S, w_ld;
+  const float* rs;     // MODE_F rank-1 term
+  const float* v;
+  int64_t v_div, v_ld;
+  int64_t R, S, w_ld, in_div;
   int rows_per_wg, z_lower_first;
-  int Co, Ho, Wo, Hp, Wp, pad_h, pad_w;
-  int Ci, Hi, Wi, KH, KW, sh, sw;
-  int nA, nB, T, Kc4, npad, nblk, nclasses, ntasks;
+  int Cm, Hm, Wm, Hp, Wp, pad_h, pad_w;   // input map and its padded LDS copy
+  int Cin, KH, KW, sh, sw;                // W is [Co, Ci, KH, KW]; Cin = Ci
+  int nch, HWout;                         // output channels and pixels per channel
+  int nA, nB, T;                          // MODE_T taps per class
+  int Kc, Kc4, npad, nblk, nclasses, ntasks;
   GatherClass cls[GMAX_CLASSES];
 };
 
+template <int MODE>
 __global__ void __launch_bounds__(GT)
-conv_t_mfma_kernel(GatherArgs g) {
+conv_mfma_kernel(GatherArgs g) {
   extern __shared__ float smem[];
   float* Ws = smem;                                              // [nclasses][Kc4][npad]
   int* koff = reinterpret_cast<int*>(Ws + (size_t)g.nclasses * g.Kc4 * g.npad);   // [Kc4]
-  float* As = reinterpret_cast<float*>(koff + g.Kc4);            // [Co][Hp][Wp]
+  float* As = reinterpret_cast<float*>(koff + g.Kc4);            // [Cm][Hp][Wp]
   __shared__ float red[GT / 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int z = blockIdx.y;
   const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
-  const float* __restrict__ A = g.A[z];
+  const float* __restrict__ X = g.X[z];
   float* __restrict__ y = g.y[z];
   float* __restrict__ nrm = g.nrm[z];
-  const int Kc = g.Co * g.T;
   const int kstride = g.Kc4 * g.npad;
 
   // weights of every class, zero-padded in k (to Kc4) and in channels (to npad)
@@ -188,28 +202,38 @@ conv_t_mfma_kernel(GatherArgs g) {
     const int c = idx / kstride, rem = idx - c * kstride;
     const int k = rem / g.npad, n = rem - k * g.npad;
     float w = 0.f;
-    if (k < Kc && n < g.Ci) {
-      const int co = k / g.T, t = k - co * g.T;
-      const int a = t / g.nB, b = t - a * g.nB;
-      const int kh = c / g.sw + g.sh * a, kw = c % g.sw + g.sw * b;
-      w = g.W[(((int64_t)co * g.Ci + n) * g.KH + kh) * g.KW + kw];
+    if (k < g.Kc && n < g.nch) {
+      if (MODE == MODE_T) {
+        const int co = k / g.T, t = k - co * g.T;
+        const int a = t / g.nB, b = t - a * g.nB;
+        const int kh = c / g.sw + g.sh * a, kw = c % g.sw + g.sw * b;
+        w = g.W[(((int64_t)co * g.Cin + n) * g.KH + kh) * g.KW + kw];
+      } else {
+        w = g.W[(int64_t)n * g.Kc + k];   // k = (ci * KH + kh) * KW + kw
+        if (g.abs_w) w = fabsf(w);
+      }
     }
     Ws[idx] = w;
   }
   for (int k = tid; k < g.Kc4; k += GT) {
     int off = 0;
-    if (k < Kc) {
-      const int co = k / g.T, t = k - co * g.T;
-      const int a = t / g.nB, b = t - a * g.nB;
-      off = co * g.Hp * g.Wp - a * g.Wp - b;
+    if (k < g.Kc) {
+      if (MODE == MODE_T) {
+        const int co = k / g.T, t = k - co * g.T;
+        const int a = t / g.nB, b = t - a * g.nB;
+        off = co * g.Hp * g.Wp - a * g.Wp - b;
+      } else {
+        const int ci = k / (g.KH * g.KW), t = k - ci * g.KH * g.KW;
+        const int kh = t / g.KW, kw = t - kh * g.KW;
+        off = (ci * g.Hp + kh) * g.Wp + kw;
+      }
     }
     koff[k] = off;
   }
 
-  const int nin = g.Co * g.Ho * g.Wo;
-  const int64_t nout = (int64_t)g.Ci * g.Hi * g.Wi;
-  const int HWi = g.Hi * g.Wi;
-  const int map = g.Co * g.Hp * g.Wp;
+  const int nin = g.Cm * g.Hm * g.Wm;
+  const int64_t nout = (int64_t)g.nch * g.HWout;
+  const int map = g.Cm * g.Hp * g.Wp;
   const int j = lane >> 4;     // k sub-index of the MFMA operands; output row group
   const int col = lane & 15;   // pixel column (B operand / D column); channel row (A operand)
 
@@ -217,15 +241,17 @@ conv_t_mfma_kernel(GatherArgs g) {
     const int64_t r = (int64_t)blockIdx.x * g.rows_per_wg + i;
     if (r >= g.R) break;   // uniform
     __syncthreads();       // weights staged / previous row's map and partial sums consumed
-    const float* __restrict__ ar = A + r * nin;
+    const float* __restrict__ xr = X + (r / g.in_div) * nin;
     for (int idx = tid; idx < map; idx += GT) {
-      const int co = idx / (g.Hp * g.Wp), rem = idx - co * g.Hp * g.Wp;
-      const int ho = rem / g.Wp - g.pad_h, wo = rem % g.Wp - g.pad_w;
-      As[idx] = (ho >= 0 && ho < g.Ho && wo >= 0 && wo < g.Wo) ? ar[(co * g.Ho + ho) * g.Wo + wo] : 0.f;
+      const int c = idx / (g.Hp * g.Wp), rem = idx - c * g.Hp * g.Wp;
+      const int hm = rem / g.Wp - g.pad_h, wm = rem % g.Wp - g.pad_w;
+      As[idx] = (hm >= 0 && hm < g.Hm && wm >= 0 && wm < g.Wm) ? xr[(c * g.Hm + hm) * g.Wm + wm] : 0.f;
     }
     __syncthreads();
     const int64_t d = r / g.S;
-    const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
+    const float hs = (MODE == MODE_T && lower && g.h_out) ? g.h_scale[r] : 0.f;
+    const float rsv = (MODE == MODE_F && g.rs) ? g.rs[r] : 0.f;
+    const float* __restrict__ vr = (MODE == MODE_F && g.rs) ? g.v + (r / g.v_div) * g.v_ld : nullptr;
     float s = 0.f;
     for (int task = wave; task < g.ntasks; task += GT / 64) {
       int c = 0;
@@ -246,11 +272,12 @@ conv_t_mfma_kernel(GatherArgs g) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int n = cb * 16 + 4 * j + rr;
-        if (n < g.Ci && pok) {
-          const float v = acc[rr];
-          const int64_t oidx = (int64_t)n * HWi + opix;
+        if (n < g.nch && pok) {
+          float v = acc[rr];
+          const int64_t oidx = (int64_t)n * g.HWout + opix;
+          if (MODE == MODE_F && vr) v = v + rsv * vr[oidx];
           if (y) y[r * nout + oidx] = v;
-          if (nrm) {
+          if (MODE == MODE_T && nrm) {
             const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
             s += g.wv ? fabsf(v) * wgt : fabsf(v);
             if (lower && g.h_out) {
@@ -261,7 +288,7 @@ conv_t_mfma_kernel(GatherArgs g) {
         }
       }
     }
-    if (nrm) {
+    if (MODE == MODE_T && nrm) {
       for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
       if (lane == 0) red[wave] = s;
       __syncthreads();
@@ -282,10 +309,11 @@ static inline int cdiv(int x, int y) { return x >= 0 ? (x + y - 1) / y : -((-x) 
 static bool conv_t_mfma_plan(GatherArgs& g, int64_t R, int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh,
                              int sw, int ph, int pw, int Hi, int Wi, size_t* lds_bytes) {
   if (KH % sh || KW % sw || sh * sw > GMAX_CLASSES) return false;
-  g.Co = Co; g.Ho = Ho; g.Wo = Wo; g.Ci = Ci; g.Hi = Hi; g.Wi = Wi;
+  g.Cm = Co; g.Hm = Ho; g.Wm = Wo; g.Cin = Ci; g.nch = Ci; g.HWout = Hi * Wi;
   g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw;
   g.nA = KH / sh; g.nB = KW / sw; g.T = g.nA * g.nB;
-  g.Kc4 = (Co * g.T + 3) / 4 * 4;
+  g.Kc = Co * g.T;
+  g.Kc4 = (g.Kc + 3) / 4 * 4;
   g.npad = (Ci + 15) / 16 * 16;
   g.nblk = g.npad / 16;
   g.nclasses = sh * sw;
@@ -331,7 +359,48 @@ static bool conv_t_mfma_plan(GatherArgs& g, int64_t R, int Co, int Ho, int Wo, i
   if (lds > 64 * 1024) return false;
   *lds_bytes = lds;
   g.R = R;
+  g.in_div = 1;
   return true;
+}
+
+// conv2d as one gather class; returns false when the LDS stage does not fit.
+static bool conv_f_mfma_plan(GatherArgs& g, int64_t R, int Ci, int Hi, int Wi, int Co, int KH, int KW, int sh,
+                             int sw, int ph, int pw, int Ho, int Wo, size_t* lds_bytes) {
+  g.Cm = Ci; g.Hm = Hi; g.Wm = Wi; g.Cin = Ci; g.nch = Co; g.HWout = Ho * Wo;
+  g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw;
+  g.Kc = Ci * KH * KW;
+  g.Kc4 = (g.Kc + 3) / 4 * 4;
+  g.npad = (Co + 15) / 16 * 16;
+  g.nblk = g.npad / 16;
+  g.nclasses = 1;
+  // padded map coordinate hp = hi + ph = ho*sh + kh
+  g.pad_h = ph;
+  g.pad_w = pw;
+  const int need_h = (Ho - 1) * sh + KH, need_w = (Wo - 1) * sw + KW;
+  g.Hp = Hi + ph > need_h ? Hi + ph : need_h;
+  g.Wp = Wi + pw > need_w ? Wi + pw : need_w;
+  GatherClass& C = g.cls[0];
+  C.np = Ho * Wo;
+  C.n2 = Wo;
+  C.poff0 = 0;
+  C.s1 = sh * g.Wp;
+  C.s2 = sw;
+  C.out0 = 0;
+  C.o1 = Wo;
+  C.o2 = 1;
+  C.tbase = 0;
+  g.ntasks = (C.np + 15) / 16 * g.nblk;
+  const size_t lds = sizeof(float) * ((size_t)g.Kc4 * g.npad + g.Kc4 + (size_t)Ci * g.Hp * g.Wp);
+  if (lds > 64 * 1024) return false;
+  *lds_bytes = lds;
+  g.R = R;
+  return true;
+}
+
+// rows per workgroup: amortize the weight stage, keep >= ~3 workgroups per CU
+static int gather_rows_per_wg(int64_t work) {
+  int64_t rpw = work / 768;
+  return rpw < 1 ? 1 : (rpw > 8 ? 8 : (int)rpw);
 }
 
 int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
@@ -344,6 +413,30 @@ int fill_value(float* p, int64_t n, float v, hipStream_t stream);
 static int conv2d_launch(const float* x, int64_t in_div, int64_t R, int Ci, int Hi, int Wi, const float* W, int abs_w,
                          int Co, int KH, int KW, int sh, int sw, int ph, int pw, int Ho, int Wo, float* y,
                          const float* rs, const float* v, int64_t v_div, int64_t v_ld, hipStream_t stream) {
+  {
+    GatherArgs g;
+    memset(&g, 0, sizeof(g));
+    size_t glds = 0;
+    if (conv_f_mfma_plan(g, R, Ci, Hi, Wi, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, &glds)) {
+      g.X[0] = x;
+      g.y[0] = y;
+      g.W = W;
+      g.abs_w = abs_w;
+      g.in_div = in_div;
+      g.rs = rs;
+      g.v = v;
+      g.v_div = v_div;
+      g.v_ld = v_ld;
+      g.S = 1;
+      g.rows_per_wg = gather_rows_per_wg(R);
+      const int rpw = g.rows_per_wg;
+      BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "conv2d: too many rows");
+      hipLaunchKernelGGL(conv_mfma_kernel<MODE_F>, dim3((unsigned)((R + rpw - 1) / rpw), 1), dim3(GT), glds, stream,
+                         g);
+      BF_LAUNCH_CHECK("conv_mfma_kernel<conv2d>");
+      return BF_OK;
+    }
+  }
   const size_t lds = sizeof(float) * (size_t)Ci * Hi * Wi;
   BF_REQUIRE(lds <= 64 * 1024, "conv2d: input map of %d x %d x %d exceeds the 64 KB LDS row stage", Ci, Hi, Wi);
   BF_REQUIRE(R < (1LL << 31), "conv2d: too many rows");
@@ -391,8 +484,8 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
     size_t glds = 0;
     if (conv_t_mfma_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
       int nzi = 0;
-      if (A_u) { g.A[nzi] = A_u; g.y[nzi] = y_u; g.nrm[nzi] = norm_u; ++nzi; }
-      if (A_l) { g.A[nzi] = A_l; g.y[nzi] = y_l; g.nrm[nzi] = norm_l; ++nzi; }
+      if (A_u) { g.X[nzi] = A_u; g.y[nzi] = y_u; g.nrm[nzi] = norm_u; ++nzi; }
+      if (A_l) { g.X[nzi] = A_l; g.y[nzi] = y_l; g.nrm[nzi] = norm_l; ++nzi; }
       g.z_lower_first = A_u ? 0 : 1;
       g.W = W;
       g.wv = wvec;
@@ -400,14 +493,12 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
       g.h_scale = h_scale;
       g.h_out = h_out;
       g.S = S;
-      // rows per workgroup: amortize the weight stage, keep >= ~3 workgroups per CU
-      const int64_t work = R * nz;
-      int rpw = (int)(work / 768);
-      rpw = rpw < 1 ? 1 : (rpw > 8 ? 8 : rpw);
+      const int rpw = gather_rows_per_wg(R * nz);
       g.rows_per_wg = rpw;
       BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
-      hipLaunchKernelGGL(conv_t_mfma_kernel, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GT), glds, stream, g);
-      BF_LAUNCH_CHECK("conv_t_mfma_kernel");
+      hipLaunchKernelGGL(conv_mfma_kernel<MODE_T>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GT), glds, stream,
+                         g);
+      BF_LAUNCH_CHECK("conv_mfma_kernel<conv_transpose2d>");
       return BF_OK;
     }
   }

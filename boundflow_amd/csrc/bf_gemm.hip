@@ -90,10 +90,14 @@ gemm_kernel(GemmArgs p) {
   const int wave = t >> 6;
   const int wm = wave / T::NWN;
   const int wn = wave % T::NWN;
-  const int z = blockIdx.y;
+  const bool split = (PRO == PRO_PLAIN && EPI == EPI_STORE) && p.ksplit > 1;   // uniform
+  const int z = split ? 0 : blockIdx.y;
   const bool lower = p.z_lower_first ? (z == 0) : (z == 1);
   const float* __restrict__ A = p.A[z];
-  const int64_t M = p.M, N = p.N, K = p.K;
+  // K range of this workgroup: [kbase, K) (the whole contraction unless split)
+  const int64_t kbase = split ? (int64_t)blockIdx.y * p.kchunk : 0;
+  const int64_t M = p.M, N = p.N;
+  const int64_t K = split ? (kbase + p.kchunk < p.K ? kbase + p.kchunk : p.K) : p.K;
   // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs, so
   // give each XCD a contiguous run of tiles in row-major (n fastest) order.
   const int64_t ntn = ceil_div(N, GBN);
@@ -220,7 +224,7 @@ gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int64_t nk = ceil_div(K, GBK);
+  const int64_t nk = ceil_div(K - kbase, GBK);
   const int lrow = lane & 31;
   const int h = lane >> 5;   // lane half -> k half of the tile
 
@@ -332,15 +336,15 @@ gemm_kernel(GemmArgs p) {
       load_tab(GBK);
       store_tab(1);
     }
-    load_tiles(0);
+    load_tiles(kbase);
     __syncthreads();
-    store_tiles(0, 0, 0);
+    store_tiles(0, kbase, 0);
     __syncthreads();
     int buf = 0;
     for (int64_t kt = 0; kt < nk; ++kt) {
       const bool more = kt + 1 < nk;
       const bool more2 = kt + 2 < nk;
-      if (more) load_tiles((kt + 1) * GBK);
+      if (more) load_tiles(kbase + (kt + 1) * GBK);
       if (more2) load_tab((kt + 2) * GBK);
       const float* __restrict__ as = As[buf];
       const float* __restrict__ bs = Bs[buf];
@@ -368,7 +372,7 @@ gemm_kernel(GemmArgs p) {
             for (int jj = 0; jj < FN; ++jj)
               acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
       }
-      if (more) store_tiles(buf ^ 1, (kt + 1) * GBK, kt + 1);
+      if (more) store_tiles(buf ^ 1, kbase + (kt + 1) * GBK, kt + 1);
       // slot kt & 1 held tile kt's slice, consumed one iteration ago
       if (more2) store_tab((int)(kt & 1));
       __syncthreads();
@@ -414,7 +418,9 @@ gemm_kernel(GemmArgs p) {
   }
 
   if (EPI == EPI_STORE) {
-    float* __restrict__ C = p.C[z];
+    float* __restrict__ C = split ? p.part + (int64_t)blockIdx.y * M * N : p.C[z];
+    const int64_t ldc = split ? N : p.ldc;
+    const bool r1 = !split && p.r1_row;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -425,8 +431,8 @@ gemm_kernel(GemmArgs p) {
           const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           if (row < M && col < N) {
             float v = acc[i][j][r];
-            if (p.r1_row) v = v + p.r1_row[row] * p.r1_col[(row / p.S) * p.r1_ld + col];
-            C[row * p.ldc + col] = v;
+            if (r1) v = v + p.r1_row[row] * p.r1_col[(row / p.S) * p.r1_ld + col];
+            C[row * ldc + col] = v;
           }
         }
       }
@@ -544,7 +550,8 @@ static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
              (long long)b_extent);
   const int64_t ntiles = ceil_div(a.M, T::BM) * ceil_div(a.N, T::BN);
   BF_REQUIRE(ntiles + 8 < (1LL << 31), "gemm grid too large (M=%lld N=%lld)", (long long)a.M, (long long)a.N);
-  dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), (unsigned)nz);
+  const unsigned gy = (PRO == PRO_PLAIN && EPI == EPI_STORE && a.ksplit > 1) ? (unsigned)a.ksplit : (unsigned)nz;
+  dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), gy);
   if (a.trans_b)
     hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T>), grid, dim3(T::NT), 0, stream, a);
   else
@@ -602,5 +609,40 @@ int relax_table(const float* lo, const float* hi, const float* alpha, int64_t al
 }
 
 int gemm_partial_count(int64_t N) { return (int)ceil_div(N, NORM_BN); }
+
+// Sum of the split-K partial products in chunk order, plus the rank-1 term.
+__global__ void splitk_reduce_kernel(const float* __restrict__ part, int ks, int64_t M, int64_t N,
+                                     float* __restrict__ C, int64_t ldc, const float* __restrict__ r_row,
+                                     const float* __restrict__ v_col, int64_t v_ld, int64_t S) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float v = part[i];
+  for (int s = 1; s < ks; ++s) v += part[(int64_t)s * M * N + i];
+  if (r_row) v = v + r_row[m] * v_col[(m / S) * v_ld + n];
+  C[m * ldc + n] = v;
+}
+
+// Split-K plan of a plain contraction: chunks of a multiple of 32 in k, used
+// when the output has too few 128 x 128 tiles to fill the device.
+int gemm_ksplit(int64_t M, int64_t N, int64_t K, int64_t* kchunk) {
+  const int64_t tiles = ceil_div(M, 128) * ceil_div(N, 128);
+  *kchunk = K;
+  if (tiles >= 128 || K < 256) return 1;
+  int64_t ks = ceil_div(512, tiles);
+  if (ks > K / 64) ks = K / 64;
+  if (ks > 64) ks = 64;
+  if (ks < 2) return 1;
+  *kchunk = ceil_div(ceil_div(K, ks), 32) * 32;
+  return (int)ceil_div(K, *kchunk);
+}
+
+int splitk_reduce(const float* part, int ks, int64_t M, int64_t N, float* C, int64_t ldc, const float* r_row,
+                  const float* v_col, int64_t v_ld, int64_t S, hipStream_t stream) {
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0, stream, part, ks, M, N,
+                     C, ldc, r_row, v_col, v_ld, S);
+  BF_LAUNCH_CHECK("splitk_reduce_kernel");
+  return BF_OK;
+}
 
 }  // namespace bf

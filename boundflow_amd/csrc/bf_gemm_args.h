@@ -45,6 +45,13 @@ struct GemmArgs {
   const float* r1_row;
   const float* r1_col;
   int64_t r1_ld;
+
+  // --- split K (PRO_PLAIN, EPI_STORE, one operand pair): blockIdx.y = chunk index;
+  // chunk s covers k in [s * kchunk, min(K, (s + 1) * kchunk)) and stores its
+  // partial product to part + s * M * N (row-major, ld = N, no rank-1 term) ---
+  int ksplit;
+  int64_t kchunk;
+  float* part;
 };
 
 }  // namespace bf

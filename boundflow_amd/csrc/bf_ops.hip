@@ -30,6 +30,9 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
                         const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream);
 int gemm_partial_count(int64_t N);
+int gemm_ksplit(int64_t M, int64_t N, int64_t K, int64_t* kchunk);
+int splitk_reduce(const float* part, int ks, int64_t M, int64_t N, float* C, int64_t ldc, const float* r_row,
+                  const float* v_col, int64_t v_ld, int64_t S, hipStream_t stream);
 void gemm_force_config(int cfg);
 int relax_table(const float* lo, const float* hi, const float* alpha, int64_t alpha_ld, int64_t D, int64_t K,
                 float4* out, hipStream_t stream);
@@ -453,12 +456,21 @@ int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_
   return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, 1, stream);
 }
 
+int64_t bf_gemm_rank1_workspace(int64_t M, int64_t N, int64_t K) {
+  int64_t kchunk;
+  const int ks = gemm_ksplit(M, N, K, &kchunk);
+  return ks > 1 ? (int64_t)ks * M * N : 0;
+}
+
 int bf_gemm_rank1(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, float* C, int64_t ldc,
                   int64_t M, int64_t N, int64_t K, int64_t S, const float* r_row, const float* v_col, int64_t v_ld,
-                  hipStream_t stream) {
+                  float* workspace, int64_t workspace_floats, hipStream_t stream) {
   BF_REQUIRE(M >= 0 && N >= 0 && K >= 0 && S > 0, "bf_gemm_rank1: bad sizes");
   if (M == 0 || N == 0) return BF_OK;
   BF_REQUIRE(A && B && C && ((r_row == nullptr) == (v_col == nullptr)), "bf_gemm_rank1: null pointer");
+  int64_t kchunk = K;
+  int ks = gemm_ksplit(M, N, K, &kchunk);
+  if (ks > 1 && (workspace == nullptr || workspace_floats < (int64_t)ks * M * N)) ks = 1;   // no split without room
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.A[0] = A;
@@ -476,7 +488,13 @@ int bf_gemm_rank1(const float* A, int64_t lda, const float* B, int64_t ldb, int 
   a.r1_row = r_row;
   a.r1_col = v_col;
   a.r1_ld = v_ld;
-  return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, 1, stream);
+  if (ks == 1) return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, 1, stream);
+  a.ksplit = ks;
+  a.kchunk = kchunk;
+  a.part = workspace;
+  const int rc = gemm_dispatch(a, PRO_PLAIN, EPI_STORE, 1, stream);
+  if (rc) return rc;
+  return splitk_reduce(workspace, ks, M, N, C, ldc, r_row, v_col, v_ld, S, stream);
 }
 
 int bf_concretize_finalize(const float* partial_u, const float* partial_l, int nparts, int64_t M,

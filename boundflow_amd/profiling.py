@@ -1,9 +1,9 @@
 """Optional per-launch timing of the library's kernels with HIP events.
 
-When a ``LaunchTimer`` is active, the host driver brackets each launch of the
-named kernel families with ``torch.cuda.Event`` records on the stream the
-kernel is launched on (the caller's current stream), together with the
-algorithmic flop and byte counts of that launch.  Nothing is synchronized
+When a ``LaunchTimer`` is active, each launch of the named kernel families is
+bracketed by ``torch.cuda.Event`` records on the stream the kernel is launched
+on (the caller's current stream), taken right around the library call, with
+the algorithmic flop and byte counts of that launch.  Nothing is synchronized
 until ``summary()`` is called.
 """
 
@@ -52,19 +52,41 @@ def timing(timer: LaunchTimer):
         _active = prev
 
 
+_pending: Optional[list] = None   # [name, flops, bytes, start event, end event] of the bracketed launch
+
+
 @contextmanager
 def launch(name: str, flops: float, nbytes: float):
-    """Bracket one launch (no-op unless a LaunchTimer is active)."""
+    """Time the first library call inside the block (no-op unless a
+    LaunchTimer is active).  The events are recorded by the call itself,
+    immediately around the foreign function, so host work that prepares the
+    arguments -- during which a launch-bound device idles -- is not counted."""
+    global _pending
     t = _active
     if t is None:
         yield
         return
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    s.record()
-    yield
-    e.record()
-    t.records.append((name, float(flops), float(nbytes), s, e))
+    _pending = [name, float(flops), float(nbytes), None, None]
+    try:
+        yield
+    finally:
+        rec, _pending = _pending, None
+        if rec is not None and rec[3] is not None and rec[4] is not None:
+            t.records.append(tuple(rec))
+
+
+def begin_call() -> None:
+    if _pending is not None and _pending[3] is None:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        _pending[3] = ev
+
+
+def end_call() -> None:
+    if _pending is not None and _pending[3] is not None and _pending[4] is None:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        _pending[4] = ev
 
 
 def summarize_rocpd(db_path: str, top: int = 12) -> str:

@@ -166,10 +166,15 @@ int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_
             int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /* Contraction with a rank-1 epilogue C[m,n] = (A @ op(B))[m,n] + r_row[m] * v_col[(m/S)*v_ld + n]:
- * the transposed contraction of the gradient pass with the bias terms. */
+ * the transposed contraction of the gradient pass with the bias terms.  When
+ * the output is too small to fill the device, K is split into chunks whose
+ * partial products go to the workspace (bf_gemm_rank1_workspace floats; 0 =
+ * no split for this shape) and are summed in chunk order; with a NULL or too
+ * small workspace the contraction runs unsplit. */
 int bf_gemm_rank1(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, float* C, int64_t ldc,
                   int64_t M, int64_t N, int64_t K, int64_t S, const float* r_row, const float* v_col, int64_t v_ld,
-                  hipStream_t stream);
+                  float* workspace, int64_t workspace_floats, hipStream_t stream);
+int64_t bf_gemm_rank1_workspace(int64_t M, int64_t N, int64_t K);
 
 /* ---- kernel #4: concretization -------------------------------------------- */
 

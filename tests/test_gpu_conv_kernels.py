@@ -5,8 +5,11 @@ bf_conv_transpose_rows replaces Conv2dLinearOperator.to_dense
 coefficient row, optionally fused with the concretization norm
 sum |y| * w and the gradient seed h = h_scale * sign(y) * w.  Shapes with
 KH % sh == 0 and KW % sw == 0 run the parity-class MFMA kernel, the others the
-row kernel; both are covered.  Tolerance: the fp32 accumulation bound
-K * 2^-23 * sum |A| |W| of each output (K = contributing taps).
+row kernel; both are covered.  bf_conv2d_rows (conv2d of rows with W or |W| and
+a rank-1 term: the IBP conv step, the input-center projection and the gradient
+of a transposed convolution) runs the same gather-GEMM kernel in its forward
+mode.  Tolerance: the fp32 accumulation bound K * 2^-23 * sum |terms| of each
+output (K = contributing taps).
 """
 
 import pytest
@@ -92,3 +95,50 @@ def test_conv_transpose_rows_matches_fp64(shape):
     expect = hsc.double()[:, None] * torch.sign(ref["l"].flatten(1)) * wrow.flatten(1)
     got = h.cpu().double()
     assert torch.allclose(got[sure], expect[sure], rtol=1e-6, atol=0), "gradient seed"
+
+
+# (R, in_div, Ci, Hi, Wi, Co, KH, KW, sh, sw, ph, pw, abs_w, rank1)
+CONV_SHAPES = [
+    (40, 1, 16, 16, 16, 32, 4, 4, 2, 2, 1, 1, 0, True),    # C3 conv1 (gradient conv with the rank-1 term)
+    (24, 1, 3, 32, 32, 16, 4, 4, 2, 2, 1, 1, 1, False),    # C3 conv0 radius (|W|)
+    (18, 9, 3, 32, 32, 16, 4, 4, 2, 2, 1, 1, 0, False),    # center projection shared by 9 rows
+    (7, 1, 20, 9, 7, 18, 3, 3, 1, 1, 1, 1, 0, True),       # 3x3 stride 1, Co > 16
+]
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=[f"R{s[0]}_div{s[1]}_Ci{s[2]}_{s[3]}x{s[4]}_Co{s[5]}_k{s[6]}s{s[8]}"
+                                                      f"_abs{s[12]}_r1{int(s[13])}" for s in CONV_SHAPES])
+def test_conv2d_rows_matches_fp64(shape):
+    dev = device()
+    R, in_div, Ci, Hi, Wi, Co, KH, KW, sh, sw, ph, pw, abs_w, rank1 = shape
+    Ho = (Hi + 2 * ph - KH) // sh + 1
+    Wo = (Wi + 2 * pw - KW) // sw + 1
+    announce(f"bf_conv2d_rows {shape} -> {Co}x{Ho}x{Wo}")
+    g = torch.Generator().manual_seed(R * 7 + Ci)
+    nrows_in = (R + in_div - 1) // in_div
+    x = torch.randn(nrows_in, Ci, Hi, Wi, generator=g)
+    W = torch.randn(Co, Ci, KH, KW, generator=g)
+    Wm = W.abs() if abs_w else W
+    nout = Co * Ho * Wo
+    rs = torch.randn(R, generator=g) if rank1 else None
+    vdiv = 3
+    vec = torch.randn((R + vdiv - 1) // vdiv, nout, generator=g) if rank1 else None
+    xin = x.double()[torch.arange(R) // in_div]
+    ref = F.conv2d(xin, Wm.double(), stride=(sh, sw), padding=(ph, pw)).reshape(R, nout)
+    bound = F.conv2d(xin.abs(), W.double().abs(), stride=(sh, sw), padding=(ph, pw)).reshape(R, nout)
+    if rank1:
+        extra = rs.double()[:, None] * vec.double()[torch.arange(R) // vdiv]
+        ref = ref + extra
+        bound = bound + extra.abs()
+    y = torch.empty(R, nout, device=dev)
+    # device copies held by name until the kernel has run
+    xd, Wd = x.to(dev), W.to(dev)
+    rsd = None if rs is None else rs.to(dev)
+    vd = None if vec is None else vec.to(dev)
+    _lib.call("bf_conv2d_rows", _lib.ptr(xd), in_div, R, Ci, Hi, Wi, _lib.ptr(Wd), abs_w, Co, KH, KW,
+              sh, sw, ph, pw, Ho, Wo, _lib.ptr(y), _lib.ptr(rsd), _lib.ptr(vd), vdiv if rank1 else 1,
+              nout if rank1 else 0, _lib.stream_handle())
+    torch.cuda.synchronize()
+    tol = (Ci * KH * KW + 2) * 2.0 ** -23 * bound + 1e-30
+    err = (y.cpu().double() - ref).abs()
+    assert bool((err <= tol).all()), f"{float((err / tol).max()):.3g} x tolerance"

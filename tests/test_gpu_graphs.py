@@ -1,0 +1,62 @@
+"""HIP graph replay of launch-bound queries (boundflow_amd.graphs).
+
+Every replay must reproduce the eager result exactly: the same kernels run on
+the same buffers.  Replays are interleaved with unrelated eager work and host
+synchronizations, and each one is checked, as graph replays after the first
+are where recorded memset nodes have gone wrong on this hardware.
+"""
+
+import pytest
+import torch
+
+from boundflow_amd import alpha_beta as hab
+from boundflow_amd import crown as hc
+from boundflow_amd import graphs
+from boundflow_amd import workloads as wl
+from tests.gpu_util import announce, device
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("name,n", [("C1", 64), ("C3", 16)])
+def test_captured_query_replays_match_eager(name, n):
+    dev = device()
+    announce(f"graph replay of run_crown_ibp_mlp {name} (batch {n})")
+    wd = wl.to_device(wl.subset(wl.make(name), n), dev)
+    eager = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+    torch.cuda.synchronize()
+    ref_lo, ref_hi = eager.lower.clone(), eager.upper.clone()
+    cap = graphs.CapturedQuery(lambda: hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C))
+    for rep in range(4):
+        # unrelated eager work between replays
+        junk = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+        junk.lower.add_(1.0)
+        torch.cuda.synchronize()
+        out = cap()
+        torch.cuda.synchronize()
+        assert torch.equal(out.lower, ref_lo), f"replay {rep} lower"
+        assert torch.equal(out.upper, ref_hi), f"replay {rep} upper"
+
+
+def test_captured_alpha_crown_replays_match_eager():
+    """The whole C4 query: forward trace, alpha from CROWN, 20 Adam steps with
+    best-of tracking -- no host synchronization, so one graph."""
+    dev = device()
+    announce("graph replay of run_alpha_crown_from_crown_init (C4, batch 4)")
+    wd = wl.to_device(wl.subset(wl.make_c4(), 4), dev)
+
+    def query():
+        return hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C, steps=20, lr=0.1)[0]
+
+    eager = query()
+    torch.cuda.synchronize()
+    ref_lo, ref_hi = eager.lower.clone(), eager.upper.clone()
+    cap = graphs.CapturedQuery(query)
+    for rep in range(3):
+        junk = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+        junk.lower.add_(1.0)
+        torch.cuda.synchronize()
+        out = cap()
+        torch.cuda.synchronize()
+        assert torch.equal(out.lower, ref_lo), f"replay {rep} lower"
+        assert torch.equal(out.upper, ref_hi), f"replay {rep} upper"

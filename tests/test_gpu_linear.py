@@ -40,6 +40,38 @@ def test_gemm_matches_fp64(M, N, K, trans_b, abs_b):
     assert bool((err <= tol).all()), float((err / tol).max())
 
 
+@pytest.mark.parametrize("M,N,K,S", [(288, 100, 2048, 9), (2304, 784, 256, 9), (36, 10, 100, 9), (500, 40, 4000, 5)])
+def test_gemm_rank1_split_k_matches_fp64(M, N, K, S):
+    """bf_gemm_rank1 (gradient contraction g . W^T + r_row x v_col): the split-K
+    path (skinny outputs) and the unsplit path against float64, and the split
+    result is identical on a second run (chunks are summed in a fixed order)."""
+    dev = device()
+    announce(f"gemm_rank1 M={M} N={N} K={K} S={S}")
+    g = torch.Generator().manual_seed(M + K)
+    A = torch.randn(M, K, generator=g)
+    W = torch.randn(N, K, generator=g)
+    r = torch.randn(M, generator=g)
+    D = (M + S - 1) // S
+    v = torch.randn(D, N, generator=g)
+    ref = A.double() @ W.double().t() + r.double()[:, None] * v.double()[torch.arange(M) // S]
+    tol = contraction_tol(A, W.t(), K) + (r.double()[:, None] * v.double()[torch.arange(M) // S]).abs() * 2.0 ** -22
+    Ad, Wd, rd, vd = A.to(dev), W.to(dev), r.to(dev), v.to(dev)
+    wsz = int(_lib.load().bf_gemm_rank1_workspace(M, N, K))
+    ws = torch.empty(max(wsz, 1), device=dev)
+    outs = []
+    for use_ws in (True, True, False):
+        C = torch.empty(M, N, device=dev)
+        _lib.call("bf_gemm_rank1", _lib.ptr(Ad), K, _lib.ptr(Wd), K, 1, _lib.ptr(C), N, M, N, K, S, _lib.ptr(rd),
+                  _lib.ptr(vd), N, _lib.ptr(ws) if use_ws else None, wsz if use_ws else 0, _lib.stream_handle())
+        outs.append(C)
+    torch.cuda.synchronize()
+    announce(f"  split workspace floats {wsz}")
+    for C in outs:
+        err = (C.cpu().double() - ref).abs()
+        assert bool((err <= tol).all()), float((err / tol).max())
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("w_trans", [0, 1])
 def test_fused_relu_linear_region_golden(w_trans):
     dev = device()
