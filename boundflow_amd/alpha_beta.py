@@ -213,10 +213,13 @@ def run_alpha_beta_crown_mlp(
     per_batch_params: bool = False,
     trace: Optional[ForwardTrace] = None,
     raise_on_infeasible: bool = True,
+    use_beta: bool = True,
 ):
     """HIP counterpart of run_alpha_beta_crown_mlp (alpha_beta_crown.py:643-941).
 
-    Returns (best_bounds, best_alpha, best_beta, stats)."""
+    ``use_beta=False`` drops the split multipliers (alpha-CROWN with splits
+    applied only to the pre-activation boxes and relaxations,
+    alpha_crown.py:137-261).  Returns (best_bounds, best_alpha, best_beta, stats)."""
     if objective != "lower" or spec_reduce != "mean":
         raise NotImplementedError("HIP alpha-beta CROWN implements objective='lower', spec_reduce='mean'")
     spec = normalize_input_spec(input_spec)
@@ -254,7 +257,7 @@ def run_alpha_beta_crown_mlp(
                 s, ld = _broadcast_split(relu_split_state[n].to(dev), B, numel[n])
                 splits[n] = (s, ld)
     # names whose split has a nonzero entry get the beta coefficient (alpha_beta_crown.py:630-633)
-    beta_names = [n for n, (s, _ld) in splits.items() if bool((s != 0).any().item())]
+    beta_names = [n for n, (s, _ld) in splits.items() if bool((s != 0).any().item())] if use_beta else []
     b_layer, b_neuron, _gap = branch_tensors(trace, B) if trace.relu_pre else (None, None, None)
     S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else _numel(chain.layers[-1].out_shape)
     M = B * S
@@ -310,7 +313,8 @@ def run_alpha_beta_crown_mlp(
                 _lib.call("bf_sum_rows", _lib.ptr(gb), B, numel[n], _lib.ptr(rb), stream)
                 ga, gb = ra, rb
             adam_a[n].step(ga, lr, 0.0, 1.0, stream)
-            adam_b[n].step(gb, lr, 0.0, None, stream)
+            if n in beta_names:
+                adam_b[n].step(gb, lr, 0.0, None, stream)
     out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
     out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
     stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,
@@ -319,12 +323,14 @@ def run_alpha_beta_crown_mlp(
 
 
 def run_alpha_crown_mlp(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.2,
-                        alpha_init: float = 0.5, relu_split_state=None):
+                        alpha_init: float = 0.5, warm_start: Optional[Dict[str, torch.Tensor]] = None,
+                        relu_split_state=None, trace: Optional[ForwardTrace] = None):
     """HIP counterpart of run_alpha_crown_mlp (alpha_crown.py:137-261): alpha shared
-    by all domains, loss -mean(lb)."""
+    by all domains, loss -mean(lb), no split multipliers.  ``warm_start`` maps
+    ReLU input names to alpha tensors of the ReLU's logical shape."""
     bounds, alpha, _beta, stats = run_alpha_beta_crown_mlp(
         module, input_spec, linear_spec_C=linear_spec_C, relu_split_state=relu_split_state, steps=steps, lr=lr,
-        alpha_init=alpha_init, per_batch_params=False)
+        alpha_init=alpha_init, warm_start_alpha=warm_start, per_batch_params=False, use_beta=False, trace=trace)
     return bounds, alpha, stats
 
 

@@ -15,14 +15,16 @@ does not disturb the others.
 
 from __future__ import annotations
 
-from typing import Dict, Optional
+import heapq
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
 from . import _lib
-from .alpha_beta import branch_tensors, run_alpha_beta_crown_mlp
+from .alpha_beta import branch_tensors, run_alpha_beta_crown_mlp, run_alpha_crown_mlp
 from .crown import forward_ibp_trace, parse_chain
-from .spec import normalize_input_spec
+from .spec import BoxPerturbation, InputSpec, normalize_input_spec
 
 
 def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
@@ -51,3 +53,303 @@ def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
     return {"status": status, "lower": bounds.lower, "upper": bounds.upper, "branch_layer": layer,
             "branch_neuron": neuron, "alpha": alpha, "beta": beta, "infeasible": trace.infeasible,
             "relu_names": list(trace.relu_pre.keys())}
+
+
+# ---------------------------------------------------------------------------
+# Branch and bound over a device-resident frontier
+
+
+@dataclass(frozen=True)
+class BabConfig:
+    """Search options, field for field as the reference's BabConfig (bab.py:134-153)."""
+
+    max_nodes: int = 10_000
+    oracle: str = "alpha"
+    use_1d_linf_input_restriction_patch: bool = False
+    node_batch_size: int = 1
+    use_branch_hint: bool = True
+    enable_node_eval_cache: bool = True
+    enable_batch_infeasible_prune: bool = False
+    alpha_steps: int = 20
+    alpha_lr: float = 0.2
+    alpha_init: float = 0.5
+    beta_init: float = 0.0
+    objective: str = "lower"
+    spec_reduce: str = "mean"
+    soft_tau: float = 1.0
+    lb_weight: float = 1.0
+    ub_weight: float = 1.0
+    threshold: float = 0.0
+    tol: float = 1e-6
+
+
+@dataclass(frozen=True)
+class BabPerExampleResult:
+    example_idx: int
+    status: str
+    nodes_visited: int
+    nodes_evaluated: int
+    nodes_expanded: int
+    best_lower: float
+    best_upper: float
+
+
+@dataclass(frozen=True)
+class BabResult:
+    status: str
+    nodes_visited: int
+    nodes_evaluated: int
+    nodes_expanded: int
+    max_queue: int
+    batch_rounds: int
+    avg_batch_fill_rate: float
+    best_lower: float
+    best_upper: float
+    per_example: Tuple[BabPerExampleResult, ...] = ()
+
+
+def _aggregate_status(statuses: List[str]) -> str:
+    if any(s == "unsafe" for s in statuses):
+        return "unsafe"
+    if all(s == "proven" for s in statuses):
+        return "proven"
+    return "unknown"
+
+
+class _Frontier:
+    """Split vectors and warm-start alpha/beta of the open nodes, one device row
+    per node slot (int8 splits, fp32 parameters), grown by doubling; freed slots
+    are reused."""
+
+    def __init__(self, sizes: Dict[str, int], dev, capacity: int = 64):
+        self.sizes = sizes
+        self.dev = dev
+        self.cap = capacity
+        self.split = {n: torch.zeros(capacity, k, dtype=torch.int8, device=dev) for n, k in sizes.items()}
+        self.alpha = {n: torch.zeros(capacity, k, device=dev) for n, k in sizes.items()}
+        self.beta = {n: torch.zeros(capacity, k, device=dev) for n, k in sizes.items()}
+        self.free: List[int] = list(range(capacity - 1, -1, -1))
+
+    def alloc(self, count: int) -> List[int]:
+        while len(self.free) < count:
+            old = self.cap
+            self.cap *= 2
+            for d in (self.split, self.alpha, self.beta):
+                for n, t in d.items():
+                    grown = torch.zeros((self.cap,) + tuple(t.shape[1:]), dtype=t.dtype, device=self.dev)
+                    grown[:old] = t
+                    d[n] = grown
+            self.free.extend(range(self.cap - 1, old - 1, -1))
+        return [self.free.pop() for _ in range(count)]
+
+    def release(self, slots: List[int]) -> None:
+        self.free.extend(slots)
+
+
+def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] = None,
+                  config: Optional[BabConfig] = None) -> BabResult:
+    """HIP counterpart of solve_bab_mlp (boundflow/runtime/bab.py:631-1528).
+
+    One search tree per input example; nodes are popped in the reference's
+    heap order (parent lower bound, then creation order), up to
+    ``node_batch_size`` per round for the alpha-beta oracle, and evaluated
+    together.  Split vectors and warm-start parameters of every open node stay
+    on the device; a round gathers them, runs one ``run_alpha_beta_crown_mlp``
+    (per-node parameters) or, for the alpha oracle, one ``run_alpha_crown_mlp``,
+    reads back the node lower/upper bounds, infeasibility and branching
+    decisions in a single transfer, and writes the children's split vectors and
+    warm starts (the parent's best alpha/beta) into free rows.  A node is
+    closed when min_s lb >= threshold - tol, dropped when its splits are
+    infeasible, and split on the widest ambiguous neuron otherwise; an example
+    is "unsafe" when an open node has no ambiguous neuron left, "unknown" when
+    its node budget runs out, "proven" when its tree empties.
+
+    Results do not depend on node evaluations being cached, so the reference's
+    node-evaluation cache has no counterpart.  Supported: objective "lower",
+    spec_reduce "mean", no 1-D input restriction, no first-layer infeasibility
+    pre-pruning.
+    """
+    cfg = config or BabConfig()
+    if int(cfg.max_nodes) < 1:
+        raise ValueError(f"max_nodes must be >=1, got {cfg.max_nodes}")
+    if int(cfg.node_batch_size) < 1:
+        raise ValueError(f"node_batch_size must be >=1, got {cfg.node_batch_size}")
+    if cfg.objective != "lower" or cfg.spec_reduce != "mean":
+        raise NotImplementedError("HIP BaB implements objective='lower', spec_reduce='mean'")
+    if cfg.use_1d_linf_input_restriction_patch or cfg.enable_batch_infeasible_prune:
+        raise NotImplementedError("HIP BaB does not implement the 1-D input restriction or batch pre-pruning")
+    if cfg.oracle not in ("alpha", "alpha_beta"):
+        raise ValueError(f"unknown BaB oracle: {cfg.oracle}")
+    spec = normalize_input_spec(input_spec)
+    module.validate()
+    chain = parse_chain(module, spec)
+    has_conv = any(layer.kind == "conv2d" for layer in chain.layers)
+    if has_conv and cfg.oracle != "alpha_beta":
+        raise NotImplementedError("alpha-only BaB does not yet support conv graphs")
+    dev = spec.center.device
+    E = int(spec.center.shape[0])
+    sizes = {name: int(torch.tensor(chain.relu_shapes[name]).prod()) for name in chain.relu_names}
+    names = list(sizes)
+    front = _Frontier(sizes, dev)
+    threshold, tol = float(cfg.threshold), float(cfg.tol)
+
+    heap: List[Tuple[float, int, int, int]] = []   # (priority, node_id, example, slot)
+    live = [0] * E
+    visited = [0] * E
+    evaluated = [0] * E
+    expanded = [0] * E
+    best_lower = [float("-inf")] * E
+    best_upper = [float("inf")] * E
+    status: List[Optional[str]] = [None] * E
+    node_id = 0
+    roots = front.alloc(E)
+    for e in range(E):
+        slot = roots[e]
+        for n in names:
+            front.split[n][slot].zero_()
+            front.alpha[n][slot].fill_(float(cfg.alpha_init))
+            front.beta[n][slot].fill_(float(cfg.beta_init))
+        heapq.heappush(heap, (float("-inf"), node_id, e, slot))
+        node_id += 1
+        live[e] = 1
+    batch_rounds = 0
+    popped_total = 0
+    max_q = len(heap)
+    do_batch = cfg.oracle == "alpha_beta" and int(cfg.node_batch_size) > 1
+
+    def finish_if_empty(e: int) -> None:
+        if status[e] is None and live[e] == 0:
+            status[e] = "proven"
+
+    while heap and any(s is None for s in status):
+        want = int(cfg.node_batch_size) if do_batch else 1
+        items: List[Tuple[float, int, int, int]] = []
+        while len(items) < want and heap:
+            item = heapq.heappop(heap)
+            e = item[2]
+            if status[e] is not None:
+                front.release([item[3]])
+                continue
+            if visited[e] >= int(cfg.max_nodes):
+                status[e] = "unknown"
+                live[e] = 0
+                front.release([item[3]])
+                continue
+            visited[e] += 1
+            items.append(item)
+        if not items:
+            break
+        if do_batch:
+            batch_rounds += 1
+            popped_total += len(items)
+        out = _evaluate_nodes(module, spec, chain, linear_spec_C, items, front, names, cfg)
+        expansions: List[Tuple[int, int, int]] = []   # (row in this round, layer, neuron)
+        child_meta: List[Tuple[int, float]] = []      # (example, priority) per expansion
+        for row, item in enumerate(items):
+            e = item[2]
+            if out["infeasible"][row]:
+                live[e] = max(0, live[e] - 1)
+                finish_if_empty(e)
+                continue
+            evaluated[e] += 1
+            node_lower = out["node_lower"][row]
+            node_upper = out["node_upper"][row]
+            best_lower[e] = max(best_lower[e], node_lower)
+            best_upper[e] = min(best_upper[e], node_upper)
+            live[e] = max(0, live[e] - 1)
+            if status[e] is not None:
+                continue
+            if node_lower >= threshold - tol:
+                finish_if_empty(e)
+                continue
+            layer = out["branch_layer"][row]
+            if layer < 0:
+                status[e] = "unsafe"
+                continue
+            if visited[e] >= int(cfg.max_nodes):
+                status[e] = "unknown"
+                continue
+            expansions.append((row, layer, out["branch_neuron"][row]))
+            child_meta.append((e, node_lower))
+            live[e] += 2
+            expanded[e] += 1
+        if expansions:
+            slots = front.alloc(2 * len(expansions))
+            rows = torch.tensor([r for r, _l, _n in expansions for _ in (0, 1)], device=dev, dtype=torch.long)
+            dst = torch.tensor(slots, device=dev, dtype=torch.long)
+            for li, n in enumerate(names):
+                front.split[n][dst] = out["split"][n][rows]
+                front.alpha[n][dst] = out["alpha"][n][rows].to(torch.float32)
+                front.beta[n][dst] = out["beta"][n][rows].to(torch.float32)
+                sel = [(2 * i + side, nn, val) for i, (_r, lay, nn) in enumerate(expansions) if lay == li
+                       for side, val in ((0, -1), (1, 1))]
+                if sel:
+                    si = torch.tensor([slots[k] for k, _nn, _v in sel], device=dev, dtype=torch.long)
+                    ni = torch.tensor([nn for _k, nn, _v in sel], device=dev, dtype=torch.long)
+                    vv = torch.tensor([v for _k, _nn, v in sel], device=dev, dtype=torch.int8)
+                    front.split[n][si, ni] = vv
+            for i, (e, prio) in enumerate(child_meta):
+                heapq.heappush(heap, (prio, node_id, e, slots[2 * i]))       # left: inactive (-1)
+                node_id += 1
+                heapq.heappush(heap, (prio, node_id, e, slots[2 * i + 1]))   # right: active (+1)
+                node_id += 1
+            max_q = max(max_q, len(heap))
+        front.release([item[3] for item in items])
+
+    for e in range(E):
+        if status[e] is None:
+            status[e] = "proven" if live[e] == 0 else "unknown"
+    per = tuple(BabPerExampleResult(example_idx=e, status=status[e] or "unknown", nodes_visited=visited[e],
+                                    nodes_evaluated=evaluated[e], nodes_expanded=expanded[e],
+                                    best_lower=best_lower[e], best_upper=best_upper[e]) for e in range(E))
+    fill = 0.0 if int(cfg.node_batch_size) <= 1 or batch_rounds == 0 else \
+        float(popped_total) / float(batch_rounds * int(cfg.node_batch_size))
+    return BabResult(status=_aggregate_status([r.status for r in per]), nodes_visited=sum(visited),
+                     nodes_evaluated=sum(evaluated), nodes_expanded=sum(expanded), max_queue=max_q,
+                     batch_rounds=batch_rounds, avg_batch_fill_rate=fill,
+                     best_lower=min(r.best_lower for r in per), best_upper=max(r.best_upper for r in per),
+                     per_example=per)
+
+
+def _evaluate_nodes(module, spec, chain, linear_spec_C, items, front: _Frontier, names, cfg: BabConfig):
+    """One round: gather the popped nodes' inputs, splits and warm starts from
+    the frontier, run the oracle on all of them, and return the node
+    lower/upper bounds, infeasibility and branch decisions on the host (one
+    transfer) plus the gathered splits and the best alpha/beta on the device."""
+    dev = spec.center.device
+    ex = torch.tensor([it[2] for it in items], device=dev, dtype=torch.long)
+    sl = torch.tensor([it[3] for it in items], device=dev, dtype=torch.long)
+    b = len(items)
+    pert = spec.perturbation
+    if isinstance(pert, BoxPerturbation):
+        sub = InputSpec.box(value_name=spec.value_name, lower=pert.lower[ex], upper=pert.upper[ex])
+    else:
+        sub = InputSpec(value_name=spec.value_name, center=spec.center[ex], perturbation=pert)
+    C = None if linear_spec_C is None else linear_spec_C[ex]
+    shapes = chain.relu_shapes
+    split = {n: front.split[n][sl] for n in names}
+    split_by = {n: split[n].reshape((b,) + tuple(shapes[n])) for n in names}
+    warm_a = {n: front.alpha[n][sl].reshape((b,) + tuple(shapes[n])) for n in names}
+    warm_b = {n: front.beta[n][sl].reshape((b,) + tuple(shapes[n])) for n in names}
+    trace = forward_ibp_trace(module, sub, relu_split_state=split_by, chain=chain, raise_on_infeasible=False)
+    layer, neuron, _gap = branch_tensors(trace, b)
+    if cfg.oracle == "alpha_beta":
+        bounds, alpha, beta, _stats = run_alpha_beta_crown_mlp(
+            module, sub, linear_spec_C=C, relu_split_state=split_by, steps=int(cfg.alpha_steps),
+            lr=float(cfg.alpha_lr), alpha_init=float(cfg.alpha_init), beta_init=float(cfg.beta_init),
+            warm_start_alpha=warm_a, warm_start_beta=warm_b, per_batch_params=True, trace=trace)
+    else:
+        # alpha oracle: one node per round, shared alpha of that node, no split multipliers
+        bounds, alpha, _stats = run_alpha_crown_mlp(
+            module, sub, linear_spec_C=C, steps=int(cfg.alpha_steps), lr=float(cfg.alpha_lr),
+            alpha_init=float(cfg.alpha_init), warm_start={n: v[0] for n, v in warm_a.items()},
+            relu_split_state=split_by, trace=trace)
+        alpha = {n: v.reshape((1,) + tuple(v.shape)) for n, v in alpha.items()}
+        beta = warm_b
+    summary = torch.stack([bounds.lower.min(dim=1).values.double(), bounds.upper.max(dim=1).values.double(),
+                           trace.infeasible.double(), layer.double(), neuron.double()]).cpu()
+    lo, up, inf, lay, neu = summary.tolist()
+    return {"node_lower": lo, "node_upper": up, "infeasible": [v != 0 for v in inf],
+            "branch_layer": [int(v) for v in lay], "branch_neuron": [int(v) for v in neu],
+            "split": split, "alpha": {n: v.reshape(b, -1) for n, v in alpha.items()},
+            "beta": {n: v.reshape(b, -1) for n, v in beta.items()}}

@@ -63,6 +63,12 @@ class Chain:
     relu_names: List[str]
     output_value: str
 
+    @property
+    def relu_shapes(self) -> Dict[str, Tuple[int, ...]]:
+        """Logical (per-example) shape of every ReLU input, in op order."""
+        out = {layer.out_name: tuple(layer.out_shape) for layer in self.layers}
+        return {name: out[name] for name in self.relu_names}
+
 
 def _pair(v) -> Tuple[int, int]:
     if isinstance(v, int):

@@ -296,6 +296,18 @@ def make_ibp_dag(seed: int = 0, batch: int = 8, eps: float = 0.05, box: bool = F
     return Workload("ibp_dag", module, spec, p["C"], labels)
 
 
+def make_bab_toy(seed: int = 0, batch: int = 6, eps: float = 0.08, dims: Sequence[int] = (12, 16, 16, 4)) -> Workload:
+    """Small MLP for whole branch-and-bound searches: inputs in [0, 1]^12, Linf
+    eps, margin specs of the network's own prediction (so some examples are
+    provable, some are not)."""
+    g = torch.Generator().manual_seed(2000 + seed)
+    module = build_mlp(list(dims), gen=g, bias_std=0.1)
+    x = torch.rand(batch, dims[0], generator=g)
+    labels = predicted_labels(module, x)
+    spec = InputSpec.linf(value_name="input", center=x, eps=eps)
+    return Workload("bab_toy", module, spec, margin_spec(labels, dims[-1]), labels)
+
+
 def split_ibp_dag(w: Workload) -> BFTaskModule:
     """The ``make_ibp_dag`` program as three tasks joined by a TaskGraph, with a
     storage plan that reuses physical buffers (``h0``/``a`` and ``c``/``rr``

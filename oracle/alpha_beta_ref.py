@@ -213,13 +213,20 @@ def run_alpha_crown(
     lr: float = 0.2,
     alpha_init: float = 0.5,
     relu_split_state=None,
+    warm_start: Optional[Dict[str, torch.Tensor]] = None,
 ):
-    """alpha_crown.py:137-261 (shared alpha per ReLU, objective lower, mean over specs)."""
+    """alpha_crown.py:137-261 (shared alpha per ReLU, objective lower, mean over
+    specs); ``warm_start`` seeds alpha per ReLU input (alpha_crown.py:42-60)."""
     spec = normalize_input_spec(input_spec)
     interval_env, relu_pre = forward_ibp_trace(module, spec, relu_split_state=relu_split_state)
-    alpha = {k: torch.full(tuple(int(d) for d in p.lower.shape[1:]), float(alpha_init),
-                           dtype=spec.center.dtype).requires_grad_(True)
-             for k, p in relu_pre.items()}
+    alpha = {}
+    for k, p in relu_pre.items():
+        shape = tuple(int(d) for d in p.lower.shape[1:])
+        if warm_start is not None and k in warm_start:
+            a = warm_start[k].to(dtype=spec.center.dtype).reshape(shape).detach().clone()
+        else:
+            a = torch.full(shape, float(alpha_init), dtype=spec.center.dtype)
+        alpha[k] = a.requires_grad_(True)
     opt = torch.optim.Adam(list(alpha.values()), lr=float(lr))
     best_metric = None
     best_bounds = None
@@ -236,6 +243,8 @@ def run_alpha_crown(
         if step == int(steps):
             break
         loss = -bounds.lower.mean()
+        if not loss.requires_grad:   # no ambiguous ReLU left (alpha_crown.py:240-241)
+            break
         opt.zero_grad(set_to_none=True)
         loss.backward()
         opt.step()

@@ -250,6 +250,34 @@ def golden_task_ibp_scheduled(w, tag):
     save(tag, lower=out.lower, upper=out.upper, checksum=workload_checksum(w))
 
 
+BAB_SOLVE_CASES = {
+    "bab_solve_ab_e003": (0.03, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "bab_solve_ab_e005": (0.05, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "bab_solve_alpha_e005": (0.05, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
+}
+
+
+def golden_bab_solve(tag):
+    """solve_bab_mlp (bab.py:631-1528) on the small BaB workload."""
+    from boundflow.runtime.bab import BabConfig as RBabConfig
+    from boundflow.runtime.bab import solve_bab_mlp as r_solve
+    eps, kw = BAB_SOLVE_CASES[tag]
+    w = wl.make_bab_toy(eps=eps)
+    res = r_solve(to_ref_module(w.module), to_ref_spec(w.spec), linear_spec_C=w.C, config=RBabConfig(**kw))
+    per = res.per_example
+    status_code = {"proven": 0, "unsafe": 1, "unknown": 2}
+    save(tag, status=status_code[res.status], nodes_visited=res.nodes_visited, nodes_evaluated=res.nodes_evaluated,
+         nodes_expanded=res.nodes_expanded, max_queue=res.max_queue, batch_rounds=res.batch_rounds,
+         avg_batch_fill_rate=res.avg_batch_fill_rate, best_lower=res.best_lower, best_upper=res.best_upper,
+         per_status=np.array([status_code[r.status] for r in per]),
+         per_visited=np.array([r.nodes_visited for r in per]),
+         per_evaluated=np.array([r.nodes_evaluated for r in per]),
+         per_expanded=np.array([r.nodes_expanded for r in per]),
+         per_best_lower=np.array([r.best_lower for r in per]),
+         per_best_upper=np.array([r.best_upper for r in per]),
+         checksum=workload_checksum(w))
+
+
 def golden_shared_alpha(tag):
     g = torch.Generator().manual_seed(5)
     m = wl.build_mlp([20, 16, 16, 5], gen=g, bias_std=0.1)
@@ -284,6 +312,9 @@ GOLDENS = [
     ("task_ibp_dag", lambda t: golden_task_ibp(wl.make_ibp_dag(), t)),
     ("task_ibp_dag_box", lambda t: golden_task_ibp(wl.make_ibp_dag(box=True), t)),
     ("task_ibp_dag_sched", lambda t: golden_task_ibp_scheduled(wl.make_ibp_dag(), t)),
+    ("bab_solve_ab_e003", golden_bab_solve),
+    ("bab_solve_ab_e005", golden_bab_solve),
+    ("bab_solve_alpha_e005", golden_bab_solve),
 ]
 
 

@@ -1,0 +1,59 @@
+"""HIP branch and bound (boundflow_amd.bab.solve_bab_mlp) against whole
+searches of the reference's solve_bab_mlp (tests/golden) on the small BaB
+workload: identical statuses, node counts, rounds and queue size (every
+certification and branching decision matches), best bounds within rtol 1e-4
+(10-step Adam trajectories, as the domain-batch tests)."""
+
+import numpy as np
+import pytest
+import torch
+
+from boundflow_amd import bab as hbab
+from boundflow_amd import workloads as wl
+from tests.golden_util import load
+from tests.gpu_util import announce, device
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "bab_solve_ab_e003": (0.03, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "bab_solve_ab_e005": (0.05, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "bab_solve_alpha_e005": (0.05, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
+}
+CODE = {"proven": 0, "unsafe": 1, "unknown": 2}
+
+
+@pytest.mark.parametrize("tag", list(CASES))
+def test_hip_bab_search_matches_reference(tag):
+    dev = device()
+    eps, kw = CASES[tag]
+    announce(f"solve_bab_mlp {tag}")
+    g = load(tag)
+    wd = wl.to_device(wl.make_bab_toy(eps=eps), dev)
+    r = hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C, config=hbab.BabConfig(**kw))
+    per = r.per_example
+    announce(f"  statuses {[p.status for p in per]} visited {[p.nodes_visited for p in per]} "
+             f"rounds {r.batch_rounds}")
+    assert CODE[r.status] == int(g["status"])
+    assert [CODE[p.status] for p in per] == g["per_status"].tolist()
+    assert [p.nodes_visited for p in per] == g["per_visited"].tolist()
+    assert [p.nodes_evaluated for p in per] == g["per_evaluated"].tolist()
+    assert [p.nodes_expanded for p in per] == g["per_expanded"].tolist()
+    assert (r.max_queue, r.batch_rounds) == (int(g["max_queue"]), int(g["batch_rounds"]))
+    assert abs(r.avg_batch_fill_rate - float(g["avg_batch_fill_rate"])) < 1e-12
+    np.testing.assert_allclose([p.best_lower for p in per], g["per_best_lower"], rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose([p.best_upper for p in per], g["per_best_upper"], rtol=1e-4, atol=1e-5)
+
+
+def test_hip_bab_frontier_growth_and_budget():
+    """A budget far below the tree size: the frontier grows past its initial
+    capacity and every example ends "unknown" or decided, never open."""
+    dev = device()
+    announce("solve_bab_mlp frontier growth")
+    wd = wl.to_device(wl.make_bab_toy(eps=0.12, batch=6), dev)
+    r = hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C,
+                           config=hbab.BabConfig(max_nodes=60, oracle="alpha_beta", node_batch_size=16,
+                                                 alpha_steps=4))
+    assert all(p.status in ("proven", "unsafe", "unknown") for p in r.per_example)
+    assert all(p.nodes_visited <= 60 for p in r.per_example)
+    assert r.max_queue >= 1 and r.batch_rounds >= 1

@@ -1,0 +1,91 @@
+"""Pin the branch-and-bound oracle (oracle/bab_ref.py).
+
+* against whole searches of the reference's solve_bab_mlp (tests/golden,
+  written by tests/golden/make_golden.py): statuses, node counts, rounds, queue
+  size, fill rate and best bounds;
+* by what a verdict means: a "proven" example has no sampled point of its input
+  ball with a negative margin; an "unsafe" one has a point that violates
+  (found by projected gradient descent on the margin, or by sampling).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from boundflow_amd import workloads as wl
+from oracle import bab_ref
+from tests.golden_util import load, workload_checksum
+
+CASES = {
+    "bab_solve_ab_e003": (0.03, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "bab_solve_ab_e005": (0.05, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "bab_solve_alpha_e005": (0.05, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
+}
+DEFAULTS = dict(use_branch_hint=True, alpha_lr=0.2, alpha_init=0.5, beta_init=0.0, threshold=0.0, tol=1e-6)
+CODE = {"proven": 0, "unsafe": 1, "unknown": 2}
+
+
+def config(tag):
+    eps, kw = CASES[tag]
+    return eps, {**DEFAULTS, **kw}
+
+
+@pytest.mark.parametrize("tag", list(CASES))
+def test_bab_search_matches_reference(tag):
+    g = load(tag)
+    eps, cfg = config(tag)
+    w = wl.make_bab_toy(eps=eps)
+    assert workload_checksum(w) == str(g["checksum"])
+    r = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
+    assert CODE[r["status"]] == int(g["status"])
+    assert [CODE[s] for s in r["per_status"]] == g["per_status"].tolist()
+    for k in ("nodes_visited", "nodes_evaluated", "nodes_expanded", "max_queue", "batch_rounds"):
+        assert r[k] == int(g[k]), k
+    assert r["per_visited"] == g["per_visited"].tolist()
+    assert r["per_evaluated"] == g["per_evaluated"].tolist()
+    assert r["per_expanded"] == g["per_expanded"].tolist()
+    assert abs(r["avg_batch_fill_rate"] - float(g["avg_batch_fill_rate"])) < 1e-12
+    np.testing.assert_allclose(r["per_best_lower"], g["per_best_lower"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(r["per_best_upper"], g["per_best_upper"], rtol=1e-5, atol=1e-6)
+
+
+def _margins(w, x):
+    p = {k: v.double() for k, v in w.module.params.items()}
+    h = x.double()
+    ops = [op for op in w.module.get_entry_task().ops]
+    for op in ops:
+        if op.op_type == "linear":
+            h = h @ p[op.inputs[1]].t() + p[op.inputs[2]]
+        elif op.op_type == "relu":
+            h = h.clamp_min(0)
+    return torch.einsum("bso,bo->bs", w.C.double(), h)
+
+
+@pytest.mark.parametrize("tag", ["bab_solve_ab_e003", "bab_solve_ab_e005"])
+def test_bab_verdicts_are_sound(tag):
+    eps, cfg = config(tag)
+    w = wl.make_bab_toy(eps=eps)
+    r = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
+    x0 = w.spec.center.double()
+    g = torch.Generator().manual_seed(9)
+    for e, st in enumerate(r["per_status"]):
+        if st == "proven":
+            pts = x0[e] + eps * (2 * torch.rand(4000, x0.shape[1], generator=g, dtype=torch.float64) - 1)
+            corners = x0[e] + eps * torch.sign(torch.randn(4000, x0.shape[1], generator=g, dtype=torch.float64))
+            xs = torch.cat([pts, corners])
+            C = w.C[e:e + 1].double().expand(xs.shape[0], -1, -1)
+            ww = type(w)(w.name, w.module, w.spec, C, w.labels)
+            assert float(_margins(ww, xs).min()) >= -1e-9, f"example {e} proven but a sampled point violates"
+        if st == "unsafe":
+            # projected gradient descent on the smallest margin from many starts
+            xs = (x0[e] + eps * (2 * torch.rand(256, x0.shape[1], generator=g, dtype=torch.float64) - 1))
+            xs.requires_grad_(True)
+            C = w.C[e:e + 1].double().expand(xs.shape[0], -1, -1)
+            ww = type(w)(w.name, w.module, w.spec, C, w.labels)
+            for _ in range(200):
+                m = _margins(ww, xs).min(dim=1).values
+                (gx,) = torch.autograd.grad(m.sum(), xs)
+                with torch.no_grad():
+                    xs -= eps * 0.05 * gx.sign()
+                    xs.copy_(torch.maximum(torch.minimum(xs, x0[e] + eps), x0[e] - eps))
+            assert float(_margins(ww, xs.detach()).min()) < 0, f"example {e} unsafe but no violating point found"
