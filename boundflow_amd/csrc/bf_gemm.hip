@@ -1,501 +1,10 @@
-// fp32 MFMA contraction for the CROWN backward pass (gfx950).
-//
-//   C[M, N] = A'[M, K] x B[K, N]
-//
-// M = domains x specs (the coefficient rows), K = current-layer neurons,
-// N = previous-layer neurons.  A' is either A itself or A after the ReLU
-// relaxation of the layer (boundflow/runtime/crown_ibp.py:1211-1298), applied
-// while the A tile is staged into LDS from a per-(domain, neuron) table of
-// slopes/intercepts; the row reductions the relaxation needs (the bias terms
-// sum_k A * beta_sel and sum_k A' * bias_k, and optionally a center term
-// sum_k A' * c_k) are produced in the same pass.  The epilogue either stores C
-// (optionally plus a rank-1 term) or reduces |C| (optionally weighted) along
-// each row -- the Linf / box concretization norm
-// (boundflow/runtime/perturbation.py:175-222, 327-359) fused so that the final
-// [M, input] coefficient never reaches HBM.
-//
-// Tiling (template Tile<BM, BN, BK, NWM, NWN, OCC>): NWM x NWN wave64s per
-// workgroup, each owning a (BM/NWM) x (BN/NWN) sub-tile of 32 x 32
-// v_mfma_f32_32x32x2f32 blocks.  The two lane halves of a wave take the two
-// halves of the K tile (a fixed permutation of the reduction order), so a
-// lane's A (and transposed B) operands for four consecutive k-steps are one
-// 128-bit LDS read.  Global tiles are read as float4 and double-buffered in LDS
-// with one barrier per K tile.  Workgroups are mapped to tiles XCD-aware: each
-// of the 8 XCDs receives a contiguous run of tiles, so the column tiles that
-// share an A row-block share that XCD's L2.
+// Dispatch of the fp32 MFMA contraction (bf_gemm_kernel.h) over its tile
+// configurations, and the small kernels around it: the relaxation table, the
+// concretization finalize and the split-K reduction.
 
-#include <type_traits>
-
-#include "bf_common.h"
-#include "bf_gemm_args.h"
+#include "bf_gemm_kernel.h"
 
 namespace bf {
-
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-// Partial-norm granularity of the |C| epilogue (columns per partial sum); every
-// tile configuration used with EPI_ABSSUM has BN == NORM_BN.
-constexpr int NORM_BN = 128;
-
-template <int BM_, int BN_, int BK_, int NWM_, int NWN_, int OCC_>
-struct Tile {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, NWM = NWM_, NWN = NWN_, OCC = OCC_;
-  static constexpr int NT = 64 * NWM * NWN;          // threads
-  static constexpr int WTM = BM / NWM;               // wave tile rows
-  static constexpr int WTN = BN / NWN;               // wave tile cols
-  static constexpr int FM = WTM / 32;                // 32x32 MFMA blocks per wave (rows)
-  static constexpr int FN = WTN / 32;                // (cols)
-  static constexpr int AP = BK + 4;                  // As row pitch (row-major along k)
-  static constexpr int BPT = BK + 4;                 // Bs row pitch (n-major [n][k], for either B layout)
-  static constexpr int KQ = BK / 4;                  // float4 per A row per K tile
-  static constexpr int A_SLOTS = BM * BK / 4 / NT;
-  static constexpr int B_SLOTS = BN * BK / 4 / NT;
-  static constexpr int RPP = NT / KQ;                // A rows covered per slot index
-  static constexpr int BS_FLOATS = BN * BPT;
-  // Relaxation operands staged in LDS per K tile: one (domain, k) entry per
-  // thread, so a tile whose rows span at most TAB_DOMS domains reads them there.
-  static constexpr int TAB_ENTRIES = NT;
-  static constexpr int TAB_DOMS = NT / BK;
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert((BM * BK) % (4 * NT) == 0 && (BN * BK) % (4 * NT) == 0, "tile/thread mismatch");
-  static_assert((BK & (BK - 1)) == 0 && BK >= 8, "BK must be a power of two >= 8");
-};
-
-__device__ __forceinline__ float fsel(const float4& r, bool lower, bool nonneg, float* beta) {
-  // upper: A >= 0 -> (alpha_u, beta_u) else (alpha_l, beta_l); lower: mirrored
-  const bool use_u = lower ? !nonneg : nonneg;
-  *beta = use_u ? r.y : r.w;
-  return use_u ? r.x : r.z;
-}
-
-template <int PRO, int EPI, bool TRANS_B, class T>
-__global__ void __launch_bounds__(T::NT, T::OCC)
-gemm_kernel(GemmArgs p) {
-  constexpr int GBM = T::BM, GBN = T::BN, GBK = T::BK, GNT = T::NT;
-  constexpr int AP = T::AP, BPT = T::BPT, A_SLOTS = T::A_SLOTS, B_SLOTS = T::B_SLOTS;
-  constexpr int KQ = T::KQ, RPP = T::RPP, FM = T::FM, FN = T::FN;
-  __shared__ __attribute__((aligned(16))) float As[2][GBM * AP];
-  __shared__ __attribute__((aligned(16))) float Bs[2][T::BS_FLOATS];
-  __shared__ float red[T::NWN][GBM];
-  constexpr int TE = (PRO == PRO_RELAX) ? T::TAB_ENTRIES : 1;
-  constexpr int TK = (PRO == PRO_RELAX) ? GBK : 1;
-  __shared__ float4 Ts[2][TE];   // relaxation table slice of a K tile, double-buffered
-  __shared__ float As_add[2][TE];  // beta split coefficient slice (lower bound)
-  constexpr int TC = (PRO == PRO_RELAX && EPI == EPI_ABSSUM) ? T::TAB_ENTRIES : 1;
-  __shared__ float Cs[2][TC];      // center-vector slice (concretization)
-  __shared__ float Kb[2][TK];    // affine bias slice
-
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wave = t >> 6;
-  const int wm = wave / T::NWN;
-  const int wn = wave % T::NWN;
-  const bool split = (PRO == PRO_PLAIN && EPI == EPI_STORE) && p.ksplit > 1;   // uniform
-  const int z = split ? 0 : blockIdx.y;
-  const bool lower = p.z_lower_first ? (z == 0) : (z == 1);
-  const float* __restrict__ A = p.A[z];
-  // K range of this workgroup: [kbase, K) (the whole contraction unless split)
-  const int64_t kbase = split ? (int64_t)blockIdx.y * p.kchunk : 0;
-  const int64_t M = p.M, N = p.N;
-  const int64_t K = split ? (kbase + p.kchunk < p.K ? kbase + p.kchunk : p.K) : p.K;
-  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs, so
-  // give each XCD a contiguous run of tiles in row-major (n fastest) order.
-  const int64_t ntn = ceil_div(N, GBN);
-  const int64_t ntiles = ceil_div(M, GBM) * ntn;
-  const int64_t per_xcd = ceil_div(ntiles, 8);
-  const int64_t tile = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (tile >= ntiles) return;
-  const int64_t tile_n = tile % ntn;
-  const int64_t m0 = (tile / ntn) * GBM;
-  const int64_t n0 = tile_n * GBN;
-  const bool row_reduce = (PRO == PRO_RELAX) && (tile_n == 0);
-  const bool vec_a = ((K & 3) == 0) && ((p.lda & 3) == 0) && ((p.lda_d & 3) == 0) && (((uintptr_t)A & 15) == 0);
-  const bool vec_b = TRANS_B ? (((K & 3) == 0) && ((p.ldb & 3) == 0) && (((uintptr_t)p.B & 15) == 0))
-                             : (((N & 3) == 0) && ((p.ldb & 3) == 0) && (((uintptr_t)p.B & 15) == 0));
-
-  // A-tile ownership: float4 slot q = t + GNT*j -> row (t / KQ) + RPP*j, k quad (t % KQ)
-  const int a_kq = t % KQ;
-  const int a_r0 = t / KQ;
-  int64_t a_base[A_SLOTS];
-  int a_dom[A_SLOTS];   // domain of the row (D < 2^31)
-  float s_beta[A_SLOTS], s_bias[A_SLOTS], s_cen[A_SLOTS];
-#pragma unroll
-  for (int j = 0; j < A_SLOTS; ++j) {
-    const int64_t m = m0 + a_r0 + RPP * j;
-    const int64_t mm = m < M ? m : 0;
-    const int64_t d = mm / p.S;
-    a_dom[j] = (int)d;
-    a_base[j] = d * p.lda_d + (mm - d * p.S) * p.lda;
-    s_beta[j] = 0.f;
-    s_bias[j] = 0.f;
-    s_cen[j] = 0.f;
-  }
-
-  float4 a_reg[A_SLOTS];
-  float4 b_reg[B_SLOTS];
-
-  auto load_tiles = [&](int64_t k0) {
-#pragma unroll
-    for (int j = 0; j < A_SLOTS; ++j) {
-      const int64_t m = m0 + a_r0 + RPP * j;
-      const int64_t k = k0 + 4 * a_kq;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (m < M) {
-        const float* src = A + a_base[j] + k;
-        if (vec_a) {
-          if (k < K) v = *reinterpret_cast<const float4*>(src);
-        } else {
-          if (k + 0 < K) v.x = src[0];
-          if (k + 1 < K) v.y = src[1];
-          if (k + 2 < K) v.z = src[2];
-          if (k + 3 < K) v.w = src[3];
-        }
-      }
-      a_reg[j] = v;
-    }
-#pragma unroll
-    for (int j = 0; j < B_SLOTS; ++j) {
-      const int q = t + GNT * j;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (TRANS_B) {
-        const int n = q / KQ, kq = q % KQ;
-        const int64_t gn = n0 + n, gk = k0 + 4 * kq;
-        if (gn < N) {
-          // B offsets fit in 32 bits (checked at launch): uniform base + 32-bit offset
-          const float* src = p.B + (uint32_t)(gn * p.ldb + gk);
-          if (vec_b) {
-            if (gk < K) v = *reinterpret_cast<const float4*>(src);
-          } else {
-            if (gk + 0 < K) v.x = src[0];
-            if (gk + 1 < K) v.y = src[1];
-            if (gk + 2 < K) v.z = src[2];
-            if (gk + 3 < K) v.w = src[3];
-          }
-        }
-      } else {
-        // B given as [K, N]: thread reads 4 consecutive k of one column n (each of
-        // the 4 loads is coalesced across the wave), stored as one n-major float4.
-        const int n = q % GBN, kq = q / GBN;
-        const int64_t gn = n0 + n, gk = k0 + 4 * kq;
-        if (gn < N) {
-          const uint32_t o = (uint32_t)(gk * p.ldb + gn), ld = (uint32_t)p.ldb;
-          if (gk + 0 < K) v.x = p.B[o];
-          if (gk + 1 < K) v.y = p.B[o + ld];
-          if (gk + 2 < K) v.z = p.B[o + 2 * ld];
-          if (gk + 3 < K) v.w = p.B[o + 3 * ld];
-        }
-      }
-      if (p.abs_b) {
-        v.x = fabsf(v.x); v.y = fabsf(v.y); v.z = fabsf(v.z); v.w = fabsf(v.w);
-      }
-      b_reg[j] = v;
-    }
-  };
-
-  const bool use_add = (PRO == PRO_RELAX) && lower && (p.add_l != nullptr);
-
-  // The rows of this tile span domains d_first .. d_first + ndom - 1.  When that
-  // fits TAB_DOMS, the relaxation operands of a K tile are loaded once per
-  // (domain, k) -- one entry per thread, coalesced -- and staged in LDS one K
-  // tile ahead (slot (kt & 1)), so every coefficient reads them from LDS.
-  int d_first = 0;
-  int ndom = 0;
-  bool tab_lds = false;
-  if (PRO == PRO_RELAX && p.relax && (EPI != EPI_ABSSUM || p.cvec)) {
-    const int64_t m_last = (m0 + GBM < M ? m0 + GBM : M) - 1;
-    d_first = (int)(m0 / p.S);
-    const int64_t nd = m_last / p.S - d_first + 1;
-    tab_lds = nd <= T::TAB_DOMS;
-    ndom = tab_lds ? (int)nd : 0;
-  }
-  const int e_dom = t / GBK, e_k = t % GBK;   // this thread's table entry
-  // LDS entry of this thread's first coefficient of slot j (loop invariant);
-  // rows past M read their first domain's entries, their results are discarded
-  int e_base[A_SLOTS];
-#pragma unroll
-  for (int j = 0; j < A_SLOTS; ++j)
-    e_base[j] = ((m0 + a_r0 + RPP * j < M ? a_dom[j] : d_first) - d_first) * GBK + 4 * a_kq;
-
-  floatx16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  const int64_t nk = ceil_div(K - kbase, GBK);
-  const int lrow = lane & 31;
-  const int h = lane >> 5;   // lane half -> k half of the tile
-
-  // The main loop, instantiated per combination of the uniform relaxation
-  // options so that the loop body carries no branches on them.  FAST: operands
-  // from the LDS slices; ADD: beta split term; KB: affine bias; RR: row sums
-  // (first column tile only); the center sums follow EPI == EPI_ABSSUM.
-  auto main_loop = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c) {
-    constexpr bool FAST = decltype(fast_c)::value;
-    constexpr bool ADD = decltype(add_c)::value;
-    constexpr bool KB = decltype(kb_c)::value;
-    constexpr bool RR = decltype(rr_c)::value;
-    constexpr bool CV = (EPI == EPI_ABSSUM);
-    float4 tab_reg = make_float4(1.f, 0.f, 1.f, 0.f);
-    float add_reg = 0.f, kb_reg = 0.f, cv_reg = 0.f;
-
-    auto load_tab = [&](int64_t k0) {
-      if constexpr (PRO == PRO_RELAX && FAST) {
-        const int64_t k = k0 + e_k;
-        const bool ok = e_dom < ndom && k < K;
-        const int64_t d = (int64_t)d_first + e_dom;
-        tab_reg = ok ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
-        if constexpr (ADD) add_reg = ok ? p.add_l[d * p.add_ld + k] : 0.f;
-        if constexpr (CV && RR) cv_reg = ok ? p.cvec[d * p.cvec_ld + k] : 0.f;
-        if constexpr (KB && RR)
-          if (t < GBK) kb_reg = (k0 + t < K) ? p.kbias[k0 + t] : 0.f;
-      }
-    };
-    auto store_tab = [&](int slot) {
-      if constexpr (PRO == PRO_RELAX && FAST) {
-        Ts[slot][t] = tab_reg;
-        if constexpr (ADD) As_add[slot][t] = add_reg;
-        if constexpr (CV && RR) Cs[slot][t] = cv_reg;
-        if constexpr (KB && RR)
-          if (t < GBK) Kb[slot][t] = kb_reg;
-      }
-    };
-
-    // ReLU relaxation of one coefficient (crown_ibp.py:1261-1296), applied as
-    // the A tile is written to LDS.  Fast path: padding coefficients (k >= K)
-    // are zero and meet identity / zero entries, so they contribute nothing.
-    auto relax_one = [&](float a, int j, int e, int64_t k, int slot) -> float {
-      float4 r;
-      float add = 0.f, kb = 0.f, cv = 0.f;
-      if constexpr (FAST) {
-        r = Ts[slot][e_base[j] + e];
-        if constexpr (ADD) add = As_add[slot][e_base[j] + e];
-        if constexpr (KB && RR) kb = Kb[slot][4 * a_kq + e];
-        if constexpr (CV && RR) cv = Cs[slot][e_base[j] + e];
-      } else {
-        if (k >= K) return a;
-        const int64_t d = a_dom[j];
-        r = p.relax ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
-        if (use_add) add = p.add_l[d * p.add_ld + k];
-        if (p.kbias) kb = p.kbias[k];
-        if (p.cvec) cv = p.cvec[d * p.cvec_ld + k];
-      }
-      float be;
-      float out = a * fsel(r, lower, a >= 0.f, &be);
-      if constexpr (FAST) {
-        if constexpr (ADD) out = out + add;
-        if constexpr (RR) {
-          s_beta[j] += a * be;
-          if constexpr (KB) s_bias[j] += out * kb;
-          if constexpr (CV) s_cen[j] += out * cv;
-        }
-      } else {
-        if (use_add) out = out + add;
-        if (row_reduce) {
-          s_beta[j] += a * be;
-          if (p.kbias) s_bias[j] += out * kb;
-          if (p.cvec) s_cen[j] += out * cv;
-        }
-      }
-      return out;
-    };
-
-    // kt: index of the K tile being stored (its relaxation slice is in slot kt & 1)
-    auto store_tiles = [&](int buf, int64_t k0, int64_t kt) {
-      const int slot = (int)(kt & 1);
-#pragma unroll
-      for (int j = 0; j < A_SLOTS; ++j) {
-        const int r = a_r0 + RPP * j;
-        float4 v = a_reg[j];
-        if constexpr (PRO == PRO_RELAX) {
-          if (FAST || m0 + r < M) {
-            const int64_t k = k0 + 4 * a_kq;
-            v.x = relax_one(v.x, j, 0, k + 0, slot);
-            v.y = relax_one(v.y, j, 1, k + 1, slot);
-            v.z = relax_one(v.z, j, 2, k + 2, slot);
-            v.w = relax_one(v.w, j, 3, k + 3, slot);
-          }
-        }
-        *reinterpret_cast<float4*>(&As[buf][r * AP + 4 * a_kq]) = v;
-      }
-#pragma unroll
-      for (int j = 0; j < B_SLOTS; ++j) {
-        const int q = t + GNT * j;
-        const int n = TRANS_B ? q / KQ : q % GBN;
-        const int kq = TRANS_B ? q % KQ : q / GBN;
-        *reinterpret_cast<float4*>(&Bs[buf][n * BPT + 4 * kq]) = b_reg[j];
-      }
-    };
-
-    // Prologue: relaxation slices of K tiles 0 and 1, then tile 0 itself.
-    load_tab(0);
-    store_tab(0);
-    if (nk > 1) {
-      load_tab(GBK);
-      store_tab(1);
-    }
-    load_tiles(kbase);
-    __syncthreads();
-    store_tiles(0, kbase, 0);
-    __syncthreads();
-    int buf = 0;
-    for (int64_t kt = 0; kt < nk; ++kt) {
-      const bool more = kt + 1 < nk;
-      const bool more2 = kt + 2 < nk;
-      if (more) load_tiles(kbase + (kt + 1) * GBK);
-      if (more2) load_tab((kt + 2) * GBK);
-      const float* __restrict__ as = As[buf];
-      const float* __restrict__ bs = Bs[buf];
-#pragma unroll
-      for (int jb = 0; jb < GBK / 2; jb += 4) {
-        float av[FM][4];
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          const float4 a4 = *reinterpret_cast<const float4*>(
-              &as[(wm * T::WTM + i * 32 + lrow) * AP + h * (GBK / 2) + jb]);
-          av[i][0] = a4.x; av[i][1] = a4.y; av[i][2] = a4.z; av[i][3] = a4.w;
-        }
-        float bv[FN][4];
-#pragma unroll
-        for (int jj = 0; jj < FN; ++jj) {
-          const float4 b4 = *reinterpret_cast<const float4*>(
-              &bs[(wn * T::WTN + jj * 32 + lrow) * BPT + h * (GBK / 2) + jb]);
-          bv[jj][0] = b4.x; bv[jj][1] = b4.y; bv[jj][2] = b4.z; bv[jj][3] = b4.w;
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int jj = 0; jj < FN; ++jj)
-              acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
-      }
-      if (more) store_tiles(buf ^ 1, kbase + (kt + 1) * GBK, kt + 1);
-      // slot kt & 1 held tile kt's slice, consumed one iteration ago
-      if (more2) store_tab((int)(kt & 1));
-      __syncthreads();
-      buf ^= 1;
-    }
-  };
-
-  using TT = std::true_type;
-  using FF = std::false_type;
-  if constexpr (PRO == PRO_PLAIN) {
-    main_loop(FF{}, FF{}, FF{}, FF{});
-  } else {
-    const bool kb = p.kbias != nullptr;
-    if (!tab_lds) main_loop(FF{}, FF{}, FF{}, FF{});
-    else if (row_reduce) {
-      if (use_add) { if (kb) main_loop(TT{}, TT{}, TT{}, TT{}); else main_loop(TT{}, TT{}, FF{}, TT{}); }
-      else { if (kb) main_loop(TT{}, FF{}, TT{}, TT{}); else main_loop(TT{}, FF{}, FF{}, TT{}); }
-    } else {
-      if (use_add) main_loop(TT{}, TT{}, FF{}, FF{});
-      else main_loop(TT{}, FF{}, FF{}, FF{});
-    }
-  }
-
-  // Row reductions of the relaxation prologue: the KQ threads holding one row
-  // are KQ consecutive lanes; reduce with xor shuffles in a fixed order.
-  if (row_reduce) {
-#pragma unroll
-    for (int j = 0; j < A_SLOTS; ++j) {
-      float sb = s_beta[j], sk = s_bias[j], sc = s_cen[j];
-#pragma unroll
-      for (int off = KQ / 2; off >= 1; off >>= 1) {
-        sb += __shfl_xor(sb, off, 64);
-        sk += __shfl_xor(sk, off, 64);
-        sc += __shfl_xor(sc, off, 64);
-      }
-      const int64_t m = m0 + a_r0 + RPP * j;
-      if (a_kq == 0 && m < M) {
-        const float b0 = p.b_in[z] ? p.b_in[z][m] : 0.f;
-        if (p.b_out[z]) p.b_out[z][m] = (b0 + sb) + sk;
-        if (p.c_out[z]) p.c_out[z][m] = sc;
-      }
-    }
-  }
-
-  if (EPI == EPI_STORE) {
-    float* __restrict__ C = split ? p.part + (int64_t)blockIdx.y * M * N : p.C[z];
-    const int64_t ldc = split ? N : p.ldc;
-    const bool r1 = !split && p.r1_row;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (row < M && col < N) {
-            float v = acc[i][j][r];
-            if (r1) v = v + p.r1_row[row] * p.r1_col[(row / p.S) * p.r1_ld + col];
-            C[row * ldc + col] = v;
-          }
-        }
-      }
-  } else {
-    static_assert(EPI != EPI_ABSSUM || GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
-    // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order.
-    float rs[FM][16];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int64_t d = (row < M) ? row / p.S : 0;
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
-          const float a = acc[i][j][r];
-          float v = fabsf(a);
-          float wgt = 1.f;
-          if (p.wvec) {
-            wgt = (row < M && col < N) ? p.wvec[d * p.w_ld + col] : 0.f;
-            v = v * wgt;
-          }
-          s += v;
-          if (lower && p.h_out && row < M && col < N) {
-            const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
-            const float hs = p.h_scale[row];
-            p.h_out[row * N + col] = p.wvec ? hs * sg * wgt : hs * sg;
-          }
-        }
-        rs[i][r] = s;
-      }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float s = rs[i][r];
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-        rs[i][r] = s;
-      }
-    if (lrow == 0) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          red[wn][rloc] = rs[i][r];
-        }
-    }
-    __syncthreads();
-    for (int rr = t; rr < GBM; rr += GNT) {
-      const int64_t row = m0 + rr;
-      if (row < M) {
-        float s = 0.f;
-#pragma unroll
-        for (int q = 0; q < T::NWN; ++q) s += red[q][rr];
-        p.partial[z][tile_n * M + row] = s;
-      }
-    }
-  }
-}
 
 // Fixed-order sum of the per-column-block partial norms, then
 //   lb = (center - eps * norm) + b,   ub = (center + eps * norm) + b
@@ -534,58 +43,24 @@ __global__ void relax_table_kernel(const float* __restrict__ lo, const float* __
   out[i] = make_float4(r.au, r.bu, r.al, r.bl);
 }
 
-// Tile configurations (selected at run time by launch_gemm; a fixed one can be
-// forced through bf_tuning_set_gemm_tile).
-using TileA = Tile<128, 128, 16, 2, 2, 3>;   // 4 waves of 64x64, 3 workgroups per CU
-using TileB = Tile<128, 128, 32, 2, 2, 2>;   // deeper K tile, 2 workgroups per CU
-using TileC = Tile<256, 128, 16, 4, 2, 1>;   // 8 waves of 64x64
-using TileD = Tile<128, 256, 16, 2, 2, 2>;   // 4 waves of 64x128 (store epilogue only)
-using TileE = Tile<64, 128, 16, 1, 2, 4>;    // 2 waves of 64x64: more workgroups for short M
-using TileF = Tile<128, 128, 16, 2, 2, 2>;   // TileA at 2 workgroups per CU
-
-template <int PRO, int EPI, class T>
-static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
-  const int64_t b_extent = a.trans_b ? (a.N - 1) * a.ldb + a.K : (a.K - 1) * a.ldb + a.N;
-  BF_REQUIRE(b_extent < (1LL << 31), "gemm: B operand too large for 32-bit offsets (%lld elements)",
-             (long long)b_extent);
-  const int64_t ntiles = ceil_div(a.M, T::BM) * ceil_div(a.N, T::BN);
-  BF_REQUIRE(ntiles + 8 < (1LL << 31), "gemm grid too large (M=%lld N=%lld)", (long long)a.M, (long long)a.N);
-  const unsigned gy = (PRO == PRO_PLAIN && EPI == EPI_STORE && a.ksplit > 1) ? (unsigned)a.ksplit : (unsigned)nz;
-  dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), gy);
-  if (a.trans_b)
-    hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T>), grid, dim3(T::NT), 0, stream, a);
-  else
-    hipLaunchKernelGGL((gemm_kernel<PRO, EPI, false, T>), grid, dim3(T::NT), 0, stream, a);
-  BF_LAUNCH_CHECK("gemm_kernel");
-  return BF_OK;
-}
-
 static int g_force_config = -1;   // tuning hook: -1 = automatic
 
-template <int PRO, int EPI>
-static int launch_gemm(const GemmArgs& a, int nz, hipStream_t stream) {
-  int cfg = g_force_config;
-  if (cfg < 0) cfg = 0;
-  switch (cfg) {
-    case 1: return launch_gemm_t<PRO, EPI, TileB>(a, nz, stream);
-    case 2: return launch_gemm_t<PRO, EPI, TileC>(a, nz, stream);
+int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {
+  if ((pro != PRO_PLAIN && pro != PRO_RELAX) || (epi != EPI_STORE && epi != EPI_ABSSUM)) {
+    set_error("gemm_dispatch: bad mode pro=%d epi=%d", pro, epi);
+    return BF_EINVAL;
+  }
+  switch (g_force_config) {
+    case 1: return launch_tile<TileB>(a, pro, epi, nz, stream);
+    case 2: return launch_tile<TileC>(a, pro, epi, nz, stream);
     case 3:
       // the |C| epilogue needs BN == NORM_BN; TileD is a store-only configuration
-      if (EPI == EPI_STORE) return launch_gemm_t<PRO, EPI_STORE, TileD>(a, nz, stream);
-      return launch_gemm_t<PRO, EPI, TileA>(a, nz, stream);
-    case 4: return launch_gemm_t<PRO, EPI, TileE>(a, nz, stream);
-    case 5: return launch_gemm_t<PRO, EPI, TileF>(a, nz, stream);
-    default: return launch_gemm_t<PRO, EPI, TileA>(a, nz, stream);
+      if (epi == EPI_STORE) return launch_tile<TileD>(a, pro, epi, nz, stream);
+      return launch_tile<TileA>(a, pro, epi, nz, stream);
+    case 4: return launch_tile<TileE>(a, pro, epi, nz, stream);
+    case 5: return launch_tile<TileF>(a, pro, epi, nz, stream);
+    default: return launch_tile<TileA>(a, pro, epi, nz, stream);
   }
-}
-
-int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {
-  if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_gemm<PRO_PLAIN, EPI_STORE>(a, nz, stream);
-  if (pro == PRO_RELAX && epi == EPI_STORE) return launch_gemm<PRO_RELAX, EPI_STORE>(a, nz, stream);
-  if (pro == PRO_PLAIN && epi == EPI_ABSSUM) return launch_gemm<PRO_PLAIN, EPI_ABSSUM>(a, nz, stream);
-  if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_gemm<PRO_RELAX, EPI_ABSSUM>(a, nz, stream);
-  set_error("gemm_dispatch: bad mode pro=%d epi=%d", pro, epi);
-  return BF_EINVAL;
 }
 
 void gemm_force_config(int cfg) { g_force_config = cfg; }

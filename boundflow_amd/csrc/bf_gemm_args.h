@@ -18,7 +18,7 @@ struct GemmArgs {
   const float* B;   // [K, N] row-major (ldb) or, with trans_b, [N, K] row-major (ldb)
   int64_t ldb;
   int trans_b;
-  int abs_b;        // use |B| (interval radius products)
+  int abs_b;        // bit z set: product z uses |B| (interval radius products)
   int64_t M, N, K;
   int z_lower_first;  // when 1, blockIdx.z = 0 uses lower semantics (single lower pass)
 

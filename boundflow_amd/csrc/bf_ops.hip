@@ -298,6 +298,96 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
   }
 }
 
+// The same pass, vectorized: TPR threads per row (256 / TPR rows per
+// workgroup), each thread handling 4 consecutive k per step, so a row of K
+// coefficients is covered in ceil(K / (4 TPR)) steps with two 16-byte loads per
+// bound and four table entries in flight per thread.  Needs K % 4 == 0 and
+// 16-byte aligned rows.  Row sums: per-thread partials in k order, then a fixed
+// tree (wave shuffles, then the workgroup's waves through LDS when TPR > 64).
+template <int TPR>
+__global__ void __launch_bounds__(256)
+relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t M, int64_t S, int64_t K,
+                        const float4* __restrict__ relax, const float* __restrict__ add_l, int64_t add_ld,
+                        const float* __restrict__ kbias, const float* __restrict__ cvec,
+                        const float* __restrict__ bu_in, const float* __restrict__ bl_in, float* __restrict__ Au_out,
+                        float* __restrict__ Al_out, float* __restrict__ bu_out, float* __restrict__ bl_out,
+                        float* __restrict__ cu_out, float* __restrict__ cl_out) {
+  constexpr int RPB = 256 / TPR;   // rows per workgroup
+  constexpr int WPR = TPR / 64;    // waves per row
+  __shared__ float red[6][256 / 64];
+  const int t = threadIdx.x % TPR;
+  const int64_t m = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const bool live = m < M;   // uniform per wave (TPR >= 64)
+  float s[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // su, sl, ku, kl, cu, cl
+  if (live) {
+    const int64_t d = m / S;
+    for (int64_t k = 4 * (int64_t)t; k < K; k += 4 * TPR) {
+      float4 r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = relax ? relax[d * K + k + e] : make_float4(1.f, 0.f, 1.f, 0.f);
+      const float4 kb = kbias ? *reinterpret_cast<const float4*>(kbias + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 cv = cvec ? *reinterpret_cast<const float4*>(cvec + d * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float kbv[4] = {kb.x, kb.y, kb.z, kb.w};
+      const float cvv[4] = {cv.x, cv.y, cv.z, cv.w};
+      if (Au) {
+        const float4 v4 = *reinterpret_cast<const float4*>(Au + m * K + k);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool nn = v[e] >= 0.f;
+          o[e] = v[e] * (nn ? r[e].x : r[e].z);
+          s[0] += v[e] * (nn ? r[e].y : r[e].w);
+          if (kbias) s[2] += o[e] * kbv[e];
+          if (cvec) s[4] += o[e] * cvv[e];
+        }
+        *reinterpret_cast<float4*>(Au_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+      if (Al) {
+        const float4 v4 = *reinterpret_cast<const float4*>(Al + m * K + k);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        const float4 ad =
+            add_l ? *reinterpret_cast<const float4*>(add_l + d * add_ld + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float adv[4] = {ad.x, ad.y, ad.z, ad.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool nn = v[e] >= 0.f;
+          o[e] = v[e] * (nn ? r[e].z : r[e].x);
+          s[1] += v[e] * (nn ? r[e].w : r[e].y);
+          if (add_l) o[e] = o[e] + adv[e];
+          if (kbias) s[3] += o[e] * kbv[e];
+          if (cvec) s[5] += o[e] * cvv[e];
+        }
+        *reinterpret_cast<float4*>(Al_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 6; ++q)
+    for (int off = 32; off >= 1; off >>= 1) s[q] += __shfl_xor(s[q], off, 64);
+  if (WPR > 1) {
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+      for (int q = 0; q < 6; ++q) red[q][w] = s[q];
+    __syncthreads();
+    if (t == 0)
+#pragma unroll
+      for (int q = 0; q < 6; ++q) {
+        float v = red[q][w];
+        for (int i = 1; i < WPR; ++i) v += red[q][w + i];
+        s[q] = v;
+      }
+  }
+  if (live && t == 0) {
+    if (bu_out) bu_out[m] = ((bu_in ? bu_in[m] : 0.f) + s[0]) + s[2];
+    if (bl_out) bl_out[m] = ((bl_in ? bl_in[m] : 0.f) + s[1]) + s[3];
+    if (cu_out) cu_out[m] = s[4];
+    if (cl_out) cl_out[m] = s[5];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Dense concretization (north-star kernel #4): one wave64 per row
 //   center = sum_i A[m,i] * c[d,i];  norm = sum_i |A[m,i]| (* rad[d,i])
@@ -448,7 +538,7 @@ int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_
   a.B = B;
   a.ldb = ldb;
   a.trans_b = trans_b;
-  a.abs_b = abs_b;
+  a.abs_b = abs_b ? 1 : 0;
   a.M = M;
   a.N = N;
   a.K = K;
@@ -626,10 +716,25 @@ int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S
   BF_REQUIRE(((uintptr_t)relax & 15) == 0, "bf_crown_relu_relax: relax table must be 16-byte aligned");
   BF_REQUIRE((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr),
              "bf_crown_relu_relax: input/output mismatch");
-  hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l, M, S,
-                     K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
-                     A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
-  BF_LAUNCH_CHECK("relu_relax_rows_kernel");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool vec = (K % 4 == 0) && al16(A_u) && al16(A_l) && al16(A_u_out) && al16(A_l_out) && al16(kbias) &&
+                   al16(cvec) && al16(add_l) && (add_l == nullptr || add_ld % 4 == 0);
+  if (vec && K >= 1024) {
+    hipLaunchKernelGGL(relu_relax_rows4_kernel<256>, dim3((unsigned)M), dim3(256), 0, stream, A_u, A_l, M, S, K,
+                       reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
+                       A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+    BF_LAUNCH_CHECK("relu_relax_rows4_kernel<256>");
+  } else if (vec) {
+    hipLaunchKernelGGL(relu_relax_rows4_kernel<64>, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l,
+                       M, S, K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in,
+                       A_u_out, A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+    BF_LAUNCH_CHECK("relu_relax_rows4_kernel<64>");
+  } else {
+    hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l, M, S,
+                       K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
+                       A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+    BF_LAUNCH_CHECK("relu_relax_rows_kernel");
+  }
   return BF_OK;
 }
 
@@ -646,6 +751,46 @@ int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const f
   return BF_OK;
 }
 
+// c = Xc . W^T and, when Xr is given, r = Xr . |W|^T, as one launch of the
+// contraction kernel (product z = blockIdx.y).  An output of few tiles (a small
+// batch) is split along K into the partial buffer `part`, whose chunks are added
+// in chunk order.
+static int ibp_products(const float* xc, const float* xr, const float* W, int64_t B, int64_t K, int64_t N, float* c,
+                        float* r, float* part, hipStream_t stream) {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  const int nz = xr ? 2 : 1;
+  a.A[0] = xc;
+  a.C[0] = c;
+  a.A[1] = xr;
+  a.C[1] = r;
+  a.lda = K;
+  a.lda_d = K;
+  a.ldc = N;
+  a.B = W;
+  a.ldb = K;
+  a.trans_b = 1;
+  a.abs_b = 2;   // product 1 takes |W|
+  a.M = B;
+  a.N = N;
+  a.K = K;
+  a.S = 1;
+  int64_t kchunk = K;
+  const int ks = gemm_ksplit(B, N, K, &kchunk);
+  if (ks > 1) {
+    a.ksplit = ks;
+    a.kchunk = kchunk;
+    a.part = part;
+  }
+  int rc = gemm_dispatch(a, PRO_PLAIN, EPI_STORE, nz, stream);
+  if (rc || ks == 1) return rc;
+  for (int z = 0; z < nz; ++z) {
+    rc = splitk_reduce(part + (int64_t)z * ks * B * N, ks, B, N, z ? r : c, N, nullptr, nullptr, 0, 1, stream);
+    if (rc) return rc;
+  }
+  return BF_OK;
+}
+
 int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, int input_kind, float eps,
                   int apply_relu, const float* W, const float* bias, int64_t N, const int8_t* split, int64_t split_ld,
                   float* workspace, float* out_lo, float* out_hi, float* center_out, int* infeasible,
@@ -654,16 +799,17 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   BF_REQUIRE(B >= 0 && K > 0 && N > 0, "bf_ibp_linear: bad sizes");
   if (B == 0) return BF_OK;
   BF_REQUIRE(in_lo && W && out_lo && out_hi && workspace, "bf_ibp_linear: null pointer");
-  // workspace: mid [B*K], rad [B*K], c [B*N], r [B*N], rownorm [N]
+  // workspace: mid [B*K], rad [B*K], c [B*N], r [B*N], rownorm [N], split-K partials
   float* mid = workspace;
   float* rad = mid + B * K;
   float* c = rad + B * K;
   float* r = c + B * N;
   float* rownorm = r + B * N;
+  float* part = rownorm + N;
+  float* cdst = center_out ? center_out : c;
   int rc;
   if (input_kind == 1) {
-    float* cdst = center_out ? center_out : c;
-    rc = bf_gemm(in_lo, K, W, K, 1, 0, cdst, N, B, N, K, stream);
+    rc = ibp_products(in_lo, nullptr, W, B, K, N, cdst, nullptr, part, stream);
     if (rc) return rc;
     hipLaunchKernelGGL(row_abs_sum_kernel, dim3((unsigned)N), dim3(256), 0, stream, W, N, K, rownorm);
     BF_LAUNCH_CHECK("row_abs_sum_kernel");
@@ -673,15 +819,16 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   BF_REQUIRE(in_hi, "bf_ibp_linear: interval input needs in_hi");
   rc = ibp_center_radius(in_lo, in_hi, B * K, apply_relu, mid, rad, stream);
   if (rc) return rc;
-  float* cdst = center_out ? center_out : c;
-  rc = bf_gemm(mid, K, W, K, 1, 0, cdst, N, B, N, K, stream);
-  if (rc) return rc;
-  rc = bf_gemm(rad, K, W, K, 1, 1, r, N, B, N, K, stream);
+  rc = ibp_products(mid, rad, W, B, K, N, cdst, r, part, stream);
   if (rc) return rc;
   return ibp_finalize(cdst, r, nullptr, 0.f, bias, 1, split, split_ld, B, N, out_lo, out_hi, infeasible, stream);
 }
 
-int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) { return 2 * B * K + 2 * B * N + N; }
+int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) {
+  int64_t kchunk;
+  const int ks = gemm_ksplit(B, N, K, &kchunk);
+  return 2 * B * K + 2 * B * N + N + (ks > 1 ? 2 * (int64_t)ks * B * N : 0);
+}
 
 int bf_interval_relu(const float* lo, const float* hi, int64_t n, float* out_lo, float* out_hi, hipStream_t stream) {
   BF_REQUIRE(n >= 0, "bf_interval_relu: bad size");

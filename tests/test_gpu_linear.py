@@ -183,11 +183,13 @@ def test_all_intermediate_c2_matches_reference():
     assert_parity(final.upper, t(gz["upper"]), ref64.upper, "C2 upper")
 
 
-def test_relax_pass_and_dense_concretize_match_oracle():
+# K = 133: scalar kernel (K % 4 != 0); 132: float4 kernel, a wave per row; 2048: float4, a workgroup per row
+@pytest.mark.parametrize("K", [133, 132, 2048])
+def test_relax_pass_and_dense_concretize_match_oracle(K):
     dev = device()
-    announce("standalone relax pass + dense concretize")
+    announce(f"standalone relax pass + dense concretize K={K}")
     g = torch.Generator().manual_seed(11)
-    D, S, K = 5, 7, 133
+    D, S = 5, 7
     A_u = torch.randn(D, S, K, generator=g)
     A_l = torch.randn(D, S, K, generator=g)
     A_u[0, 0, :4] = torch.tensor([0.0, -0.0, 1.0, -1.0])
