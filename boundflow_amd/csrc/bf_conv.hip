@@ -150,6 +150,21 @@ constexpr int GT = 256;
 constexpr int GMAX_CLASSES = 16;
 enum : int { MODE_T = 0, MODE_F = 1 };
 
+// q = n / d for n, d < 2^16 as a multiply-high by m = ceil(2^32 / d): with
+// m d = 2^32 + e (0 <= e < d), n m / 2^32 = n / d + n e / (d 2^32) and n e < 2^32,
+// so the error never reaches the next integer.  d == 1 is kept apart (m would
+// need 33 bits).  Every numerator below indexes an LDS array of at most 64 KB.
+struct FastDiv {
+  uint32_t m, d;
+};
+static FastDiv make_fdiv(int d) {
+  FastDiv f;
+  f.d = (uint32_t)d;
+  f.m = d > 1 ? (uint32_t)((0x100000000ull + (uint64_t)d - 1) / (uint64_t)d) : 0u;
+  return f;
+}
+__device__ __forceinline__ int fdivq(int n, FastDiv f) { return f.d == 1 ? n : (int)__umulhi((uint32_t)n, f.m); }
+
 struct GatherClass {
   int np;              // pixels of the class
   int n2;              // pixels per class row: p -> (q1, q2) = (p / n2, p % n2)
@@ -177,8 +192,21 @@ struct GatherArgs {
   int nch, HWout;                         // output channels and pixels per channel
   int nA, nB, T;                          // MODE_T taps per class
   int Kc, Kc4, npad, nblk, nclasses, ntasks;
+  FastDiv f_kstride, f_npad, f_T, f_nB, f_sw, f_KHKW, f_KW, f_HpWp, f_Wp;   // staging index divisions
   GatherClass cls[GMAX_CLASSES];
 };
+
+static void gather_fdivs(GatherArgs& g) {
+  g.f_kstride = make_fdiv(g.Kc4 * g.npad);
+  g.f_npad = make_fdiv(g.npad);
+  g.f_T = make_fdiv(g.T > 0 ? g.T : 1);
+  g.f_nB = make_fdiv(g.nB > 0 ? g.nB : 1);
+  g.f_sw = make_fdiv(g.sw);
+  g.f_KHKW = make_fdiv(g.KH * g.KW);
+  g.f_KW = make_fdiv(g.KW);
+  g.f_HpWp = make_fdiv(g.Hp * g.Wp);
+  g.f_Wp = make_fdiv(g.Wp);
+}
 
 template <int MODE>
 __global__ void __launch_bounds__(GT)
@@ -197,34 +225,47 @@ conv_mfma_kernel(GatherArgs g) {
   float* __restrict__ nrm = g.nrm[z];
   const int kstride = g.Kc4 * g.npad;
 
-  // weights of every class, zero-padded in k (to Kc4) and in channels (to npad)
-  for (int idx = tid; idx < g.nclasses * kstride; idx += GT) {
-    const int c = idx / kstride, rem = idx - c * kstride;
-    const int k = rem / g.npad, n = rem - k * g.npad;
-    float w = 0.f;
-    if (k < g.Kc && n < g.nch) {
+  // weights of every class, zero-padded in k (to Kc4) and in channels (to npad);
+  // eight loads per thread in flight, from clamped addresses, before the stores
+  const int wtotal = g.nclasses * kstride;
+  for (int base = 0; base < wtotal; base += 8 * GT) {
+    float wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * GT + tid;
+      const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
+      const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
+      const bool ok = idx < wtotal && k < g.Kc && n < g.nch;
+      int64_t src;
       if (MODE == MODE_T) {
-        const int co = k / g.T, t = k - co * g.T;
-        const int a = t / g.nB, b = t - a * g.nB;
-        const int kh = c / g.sw + g.sh * a, kw = c % g.sw + g.sw * b;
-        w = g.W[(((int64_t)co * g.Cin + n) * g.KH + kh) * g.KW + kw];
+        const int co = fdivq(k, g.f_T), t = k - co * g.T;
+        const int a = fdivq(t, g.f_nB), b = t - a * g.nB;
+        const int cr = fdivq(c, g.f_sw);
+        const int kh = cr + g.sh * a, kw = (c - cr * g.sw) + g.sw * b;
+        src = (((int64_t)co * g.Cin + n) * g.KH + kh) * g.KW + kw;
       } else {
-        w = g.W[(int64_t)n * g.Kc + k];   // k = (ci * KH + kh) * KW + kw
-        if (g.abs_w) w = fabsf(w);
+        src = (int64_t)n * g.Kc + k;   // k = (ci * KH + kh) * KW + kw
       }
+      float w = g.W[ok ? src : 0];
+      if (MODE == MODE_F && g.abs_w) w = fabsf(w);
+      wv[u] = ok ? w : 0.f;
     }
-    Ws[idx] = w;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * GT + tid;
+      if (idx < wtotal) Ws[idx] = wv[u];
+    }
   }
   for (int k = tid; k < g.Kc4; k += GT) {
     int off = 0;
     if (k < g.Kc) {
       if (MODE == MODE_T) {
-        const int co = k / g.T, t = k - co * g.T;
-        const int a = t / g.nB, b = t - a * g.nB;
+        const int co = fdivq(k, g.f_T), t = k - co * g.T;
+        const int a = fdivq(t, g.f_nB), b = t - a * g.nB;
         off = co * g.Hp * g.Wp - a * g.Wp - b;
       } else {
-        const int ci = k / (g.KH * g.KW), t = k - ci * g.KH * g.KW;
-        const int kh = t / g.KW, kw = t - kh * g.KW;
+        const int ci = fdivq(k, g.f_KHKW), t = k - ci * g.KH * g.KW;
+        const int kh = fdivq(t, g.f_KW), kw = t - kh * g.KW;
         off = (ci * g.Hp + kh) * g.Wp + kw;
       }
     }
@@ -242,10 +283,23 @@ conv_mfma_kernel(GatherArgs g) {
     if (r >= g.R) break;   // uniform
     __syncthreads();       // weights staged / previous row's map and partial sums consumed
     const float* __restrict__ xr = X + (r / g.in_div) * nin;
-    for (int idx = tid; idx < map; idx += GT) {
-      const int c = idx / (g.Hp * g.Wp), rem = idx - c * g.Hp * g.Wp;
-      const int hm = rem / g.Wp - g.pad_h, wm = rem % g.Wp - g.pad_w;
-      As[idx] = (hm >= 0 && hm < g.Hm && wm >= 0 && wm < g.Wm) ? xr[(c * g.Hm + hm) * g.Wm + wm] : 0.f;
+    for (int base = 0; base < map; base += 8 * GT) {
+      float xv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int idx = base + u * GT + tid;
+        const int c = fdivq(idx, g.f_HpWp), rem = idx - c * g.Hp * g.Wp;
+        const int hr = fdivq(rem, g.f_Wp);
+        const int hm = hr - g.pad_h, wm = (rem - hr * g.Wp) - g.pad_w;
+        const bool ok = idx < map && hm >= 0 && hm < g.Hm && wm >= 0 && wm < g.Wm;
+        const float x = xr[ok ? (c * g.Hm + hm) * g.Wm + wm : 0];
+        xv[u] = ok ? x : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int idx = base + u * GT + tid;
+        if (idx < map) As[idx] = xv[u];
+      }
     }
     __syncthreads();
     const int64_t d = r / g.S;
@@ -266,6 +320,7 @@ conv_mfma_kernel(GatherArgs g) {
       const float* __restrict__ as = As + C.poff0 + q1 * C.s1 + q2 * C.s2;
       const float* __restrict__ ws = Ws + (size_t)c * kstride + cb * 16 + col;
       floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
       for (int k = j; k < g.Kc4; k += 4)
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[k * g.npad], as[koff[k]], acc, 0, 0, 0);
       const int opix = C.out0 + q1 * C.o1 + q2 * C.o2;
@@ -360,6 +415,7 @@ static bool conv_t_mfma_plan(GatherArgs& g, int64_t R, int Co, int Ho, int Wo, i
   *lds_bytes = lds;
   g.R = R;
   g.in_div = 1;
+  gather_fdivs(g);
   return true;
 }
 
@@ -394,6 +450,7 @@ static bool conv_f_mfma_plan(GatherArgs& g, int64_t R, int Ci, int Hi, int Wi, i
   if (lds > 64 * 1024) return false;
   *lds_bytes = lds;
   g.R = R;
+  gather_fdivs(g);
   return true;
 }
 
