@@ -345,28 +345,51 @@ def crown_backward(
     A_u: Optional[torch.Tensor] = A0 if need_upper else None
     A_l: Optional[torch.Tensor] = A0 if need_lower else None
     b_u = b_l = None
+    c_u = c_l = None
     stride = a_dstride
-    for k in range(len(layers) - 1, -1, -1):
+    tables: Dict[int, torch.Tensor] = {}
+
+    def relax_params(k: int):
+        """(alpha, alpha_ld, add, add_ld, pre_lo, pre_hi, N) of the ReLU after layer k."""
         layer = layers[k]
         relax_name = layer.out_name if k < len(layers) - 1 else None
         pre = trace.relu_pre[relax_name] if relax_name is not None else None
-        N = _numel(layer.out_shape)
+        n = _numel(layer.out_shape)
         alpha = add = None
         alpha_ld = add_ld = 0
         if relax_name is not None:
             if relu_alpha is not None and relax_name in relu_alpha:
-                alpha, alpha_ld = _flat_param(relu_alpha[relax_name], B, N, f"relu_alpha[{relax_name}]")
+                alpha, alpha_ld = _flat_param(relu_alpha[relax_name], B, n, f"relu_alpha[{relax_name}]")
             if relu_pre_add_coeff_l is not None and relax_name in relu_pre_add_coeff_l:
-                add, add_ld = _flat_param(relu_pre_add_coeff_l[relax_name], B, N,
+                add, add_ld = _flat_param(relu_pre_add_coeff_l[relax_name], B, n,
                                           f"relu_pre_add_coeff_l[{relax_name}]")
-        pre_lo = None if pre is None else pre.lower.reshape(B, N)
-        pre_hi = None if pre is None else pre.upper.reshape(B, N)
-        relax = None
-        if pre is not None and layer.kind == "linear":
-            # slopes/intercepts once per (domain, neuron), shared by both bounds
-            relax = torch.empty(B, N, 4, device=dev, dtype=torch.float32)
-            _lib.call("bf_relu_relax_table", _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, B, N,
-                      _lib.ptr(relax), stream)
+        pre_lo = None if pre is None else pre.lower.reshape(B, n)
+        pre_hi = None if pre is None else pre.upper.reshape(B, n)
+        return alpha, alpha_ld, add, add_ld, pre_lo, pre_hi, n
+
+    def relax_table(k: int) -> Optional[torch.Tensor]:
+        """Slopes/intercepts of the ReLU after linear layer k, once per (domain, neuron), shared by both bounds."""
+        if k in tables:
+            return tables[k]
+        alpha, alpha_ld, _, _, pre_lo, pre_hi, n = relax_params(k)
+        table = None
+        if pre_lo is not None and layers[k].kind == "linear":
+            table = torch.empty(B, n, 4, device=dev, dtype=torch.float32)
+            _lib.call("bf_relu_relax_table", _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, B, n,
+                      _lib.ptr(table), stream)
+        tables[k] = table
+        return table
+
+    # A coefficient produced by bf_crown_relu_linear_relu_fwd already carries the
+    # relaxation (and bias) of the ReLU it enters: the next region skips its prologue.
+    pre_relaxed = False
+    for k in range(len(layers) - 1, -1, -1):
+        layer = layers[k]
+        alpha, alpha_ld, add, add_ld, pre_lo, pre_hi, N = relax_params(k)
+        relax = relax_table(k)
+        if pre_relaxed:
+            relax = add = None
+            add_ld = 0
         if save is not None and A_l is not None:
             save.setdefault("A_in", {})[k] = (A_l, stride)
             save.setdefault("b_in", {})[k] = b_l
@@ -380,7 +403,7 @@ def crown_backward(
         W = layer.weight.contiguous()
         # the contraction reads W^T [P, N] row-major: 128-bit operand loads along N
         Wt = W.t().contiguous()
-        bias = None if layer.bias is None else layer.bias.contiguous()
+        bias = None if layer.bias is None or pre_relaxed else layer.bias.contiguous()
         P = _numel(layer.in_shape)
         if k > 0 and linear_spec_C is None and k == len(layers) - 1:
             # C = I: I @ W is W itself, shared by every domain (no contraction needed)
@@ -391,6 +414,19 @@ def crown_backward(
             b_l = brow if A_l is not None else None
             stride = 0
             continue
+        if k == 0 and pre_relaxed:
+            # input layer of an already relaxed coefficient: contraction fused with the concretization
+            rad, eps = _input_radius(pert, B, P)
+            ws = torch.empty(int(_lib.load().bf_crown_linear_concretize_workspace(B, S, P)), device=dev,
+                             dtype=torch.float32)
+            lb = torch.empty(B, S, device=dev, dtype=torch.float32) if A_l is not None else None
+            ub = torch.empty(B, S, device=dev, dtype=torch.float32) if A_u is not None else None
+            nz = int(A_u is not None) + int(A_l is not None)
+            with _timed("crown_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
+                _lib.call("bf_crown_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N, _lib.ptr(Wt),
+                          P, _lib.ptr(rad), eps, _lib.ptr(c_u), _lib.ptr(c_l), _lib.ptr(b_u), _lib.ptr(b_l),
+                          _lib.ptr(ws), _lib.ptr(lb), _lib.ptr(ub), stream)
+            return IntervalState(lower=lb, upper=ub)
         if k == 0:
             # input layer: relaxation + contraction fused with the concretization
             if isinstance(pert, BoxPerturbation):
@@ -433,14 +469,65 @@ def crown_backward(
         nb_l = torch.empty(M, device=dev, dtype=torch.float32) if A_l is not None else None
         nz = int(A_u is not None) + int(A_l is not None)
         a_rows = M if stride != 0 else S
-        with _timed("crown_relu_linear_fwd", 2.0 * nz * M * N * P, 4.0 * nz * (a_rows * N + N * P + M * P)):
-            _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
-                      _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(b_u),
-                      _lib.ptr(b_l), _lib.ptr(nA_u),
-                      _lib.ptr(nA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), stream)
+        flops, nbytes = 2.0 * nz * M * N * P, 4.0 * nz * (a_rows * N + N * P + M * P)
+        if save is None and layers[k - 1].kind == "linear" and S >= EPILOGUE_MIN_ROWS:
+            # the next region's relaxation in this contraction's epilogue
+            n_alpha, n_alpha_ld, n_add, n_add_ld, _, _, _ = relax_params(k - 1)
+            n_table = relax_table(k - 1)
+            prev = layers[k - 1]
+            n_bias = None if prev.bias is None else prev.bias.contiguous()
+            cvec = None
+            if k - 1 == 0:
+                cvec = trace.input_center_proj.get(prev.out_name)
+                if cvec is None:
+                    raise RuntimeError("forward trace lacks the input-layer projection")
+            if n_table is None:
+                n_table = _identity_table(B, P, dev)
+            ws = torch.empty(int(_lib.load().bf_crown_relu_linear_relu_fwd_workspace(B, S, P)), device=dev,
+                             dtype=torch.float32)
+            nc_u = torch.empty(M, device=dev, dtype=torch.float32) if (cvec is not None and A_u is not None) else None
+            nc_l = torch.empty(M, device=dev, dtype=torch.float32) if (cvec is not None and A_l is not None) else None
+            with _timed("crown_relu_linear_relu_fwd", flops, nbytes):
+                _lib.call("bf_crown_relu_linear_relu_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
+                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, _lib.ptr(bias), _lib.ptr(b_u),
+                          _lib.ptr(b_l), _lib.ptr(n_table), _lib.ptr(n_add), n_add_ld, _lib.ptr(n_bias),
+                          _lib.ptr(cvec), P, _lib.ptr(ws), _lib.ptr(nA_u), _lib.ptr(nA_l), _lib.ptr(nb_u),
+                          _lib.ptr(nb_l), _lib.ptr(nc_u), _lib.ptr(nc_l), stream)
+            c_u, c_l = nc_u, nc_l
+            pre_relaxed = True
+        else:
+            with _timed("crown_relu_linear_fwd", flops, nbytes):
+                _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
+                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(b_u),
+                          _lib.ptr(b_l), _lib.ptr(nA_u),
+                          _lib.ptr(nA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), stream)
+            pre_relaxed = False
         A_u, A_l, b_u, b_l = nA_u, nA_l, nb_u, nb_l
         stride = S * P
     raise RuntimeError("backward did not reach the input layer")
+
+
+# Rows per domain from which the backward relaxes each coefficient in the epilogue
+# of the contraction that produces it: a 128-row tile then spans at most 10 domains,
+# whose relaxation entries fit the kernel's LDS stage.
+EPILOGUE_MIN_ROWS = 15
+
+
+def _identity_table(B: int, n: int, dev) -> torch.Tensor:
+    """Relaxation table of a linear (no ReLU) boundary: slopes 1, intercepts 0."""
+    t = torch.zeros(B, n, 4, device=dev, dtype=torch.float32)
+    t[:, :, 0] = 1.0
+    t[:, :, 2] = 1.0
+    return t
+
+
+def _input_radius(pert, B: int, P: int):
+    """(rad, eps) of the input concretization: box radius with eps 1, or Linf eps without weights."""
+    if isinstance(pert, BoxPerturbation):
+        lo = pert.lower.reshape(B, P)
+        hi = pert.upper.reshape(B, P)
+        return ((hi - lo) / 2.0).contiguous(), 1.0
+    return None, float(pert.eps)
 
 
 def _check_alpha_beta_args(relu_pre_add_coeff_u):

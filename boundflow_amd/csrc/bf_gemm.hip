@@ -46,10 +46,11 @@ __global__ void relax_table_kernel(const float* __restrict__ lo, const float* __
 static int g_force_config = -1;   // tuning hook: -1 = automatic
 
 int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {
-  if ((pro != PRO_PLAIN && pro != PRO_RELAX) || (epi != EPI_STORE && epi != EPI_ABSSUM)) {
+  if ((pro != PRO_PLAIN && pro != PRO_RELAX) || (epi != EPI_STORE && epi != EPI_ABSSUM && epi != EPI_RELAX)) {
     set_error("gemm_dispatch: bad mode pro=%d epi=%d", pro, epi);
     return BF_EINVAL;
   }
+  if (epi == EPI_RELAX) return launch_tile<TileA>(a, pro, epi, nz, stream);   // its one configuration
   switch (g_force_config) {
     case 1: return launch_tile<TileB>(a, pro, epi, nz, stream);
     case 2: return launch_tile<TileC>(a, pro, epi, nz, stream);
@@ -84,6 +85,32 @@ int relax_table(const float* lo, const float* hi, const float* alpha, int64_t al
 }
 
 int gemm_partial_count(int64_t N) { return (int)ceil_div(N, NORM_BN); }
+
+// Sums of the relaxation epilogue over the column tiles, in tile order:
+//   b_out[m] = b_src[m] + sum_t pb[t][m]   (b_src NULL = 0; b_src may alias b_out)
+//   c_out[m] = sum_t pc[t][m]              (when c_out)
+__global__ void rows_finalize_kernel(const float* b_src, const float* __restrict__ pb, const float* __restrict__ pc,
+                                     int nparts, int64_t M, float* b_out, float* __restrict__ c_out) {
+  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  float v = b_src ? b_src[m] : 0.f;
+  for (int q = 0; q < nparts; ++q) v += pb[(int64_t)q * M + m];
+  b_out[m] = v;
+  if (c_out) {
+    float c = 0.f;
+    for (int q = 0; q < nparts; ++q) c += pc[(int64_t)q * M + m];
+    c_out[m] = c;
+  }
+}
+
+int rows_finalize(const float* b_src, const float* pb, const float* pc, int nparts, int64_t M, float* b_out,
+                  float* c_out, hipStream_t stream) {
+  if (M == 0) return BF_OK;
+  hipLaunchKernelGGL(rows_finalize_kernel, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, stream, b_src, pb, pc,
+                     nparts, M, b_out, c_out);
+  BF_LAUNCH_CHECK("rows_finalize_kernel");
+  return BF_OK;
+}
 
 // Sum of the split-K partial products in chunk order, plus the rank-1 term.
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, int ks, int64_t M, int64_t N,

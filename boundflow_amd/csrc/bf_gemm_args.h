@@ -6,7 +6,7 @@
 namespace bf {
 
 enum : int { PRO_PLAIN = 0, PRO_RELAX = 1 };
-enum : int { EPI_STORE = 0, EPI_ABSSUM = 1 };
+enum : int { EPI_STORE = 0, EPI_ABSSUM = 1, EPI_RELAX = 2 };
 
 struct GemmArgs {
   // Operand pair selected by blockIdx.z (z = 0 "upper", z = 1 "lower").
@@ -40,6 +40,19 @@ struct GemmArgs {
   float* partial[2];         // [gridDim.y, M] partial row sums
   const float* h_scale;      // optional [M]: lower pass also writes h = h_scale[m] * sign(C) * w  (gradient seed)
   float* h_out;              // [M, N] row-major (ldh = N)
+
+  // --- relaxation epilogue (EPI_RELAX): the ReLU relaxation of the NEXT layer,
+  // indexed by the output columns, applied to C before it is stored:
+  //   C'[m, n] = C * slope_sel(d, n) (+ e_add[d, n] on the lower pass)
+  //   partial[tile_n][m]   = sum over the tile's columns of (C * beta_sel + C' * e_kbias[n])
+  //   partial_c[tile_n][m] = sum over the tile's columns of C' * e_cvec[d, n]   (optional)
+  const float4* e_relax;     // [D, N] {alpha_u, beta_u, alpha_l, beta_l}
+  const float* e_add;        // optional, lower pass only, row stride e_add_ld
+  int64_t e_add_ld;
+  const float* e_kbias;      // optional [N]
+  const float* e_cvec;       // optional [D, N], row stride e_cvec_ld
+  int64_t e_cvec_ld;
+  float* partial_c[2];
 
   // --- rank-1 term of the store epilogue: C[m, n] = acc + r1_row[m] * r1_col[(m / S) * r1_ld + n] ---
   const float* r1_row;

@@ -426,7 +426,7 @@ gemm_kernel(GemmArgs p) {
     }
   }
 
-  if (EPI == EPI_STORE) {
+  if constexpr (EPI == EPI_STORE) {
     float* __restrict__ C = split ? p.part + (int64_t)blockIdx.y * M * N : p.C[z];   // partial (z, kc)
     const int64_t ldc = split ? N : p.ldc;
     const bool r1 = !split && p.r1_row;
@@ -445,8 +445,8 @@ gemm_kernel(GemmArgs p) {
           }
         }
       }
-  } else {
-    static_assert(EPI != EPI_ABSSUM || GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
+  } else if constexpr (EPI == EPI_ABSSUM) {
+    static_assert(GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
     // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order.
     float rs[FM][16];
 #pragma unroll
@@ -503,6 +503,122 @@ gemm_kernel(GemmArgs p) {
         p.partial[z][tile_n * M + row] = s;
       }
     }
+  } else {
+    // Relaxation of the next ReLU (crown_ibp.py:1261-1296) applied to C before
+    // it is stored, so the next contraction reads A' directly; every coefficient
+    // is relaxed once here instead of once per column tile of its consumer.
+    static_assert(GBN == NORM_BN, "the relaxation epilogue needs BN == NORM_BN");
+    // As / Bs are free once every wave has left the main loop: As holds the
+    // relaxation entries of the tile's domains x columns, Bs the split term,
+    // the center vector, the bias and the domain of each row.
+    constexpr int E_DOMS = (2 * GBM * AP) / (4 * GBN);
+    static_assert(2 * E_DOMS * GBN + GBN + GBM <= 2 * T::BS_FLOATS, "epilogue slices exceed the B stage");
+    __syncthreads();
+    float4* Te = reinterpret_cast<float4*>(&As[0][0]);
+    float* Ae = &Bs[0][0];
+    float* Ce = Ae + E_DOMS * GBN;
+    float* Ke = Ce + E_DOMS * GBN;
+    int* Re = reinterpret_cast<int*>(Ke + GBN);
+    const int64_t m_last = (m0 + GBM < M ? m0 + GBM : M) - 1;
+    const int e_first = (int)(m0 / p.S);
+    const int endom = (int)(m_last / p.S) - e_first + 1;
+    const bool staged = endom <= E_DOMS;   // uniform; otherwise entries are read from global memory
+    const bool add_e = lower && (p.e_add != nullptr);
+    const bool kb_e = p.e_kbias != nullptr;
+    const bool cv_e = p.e_cvec != nullptr;
+    if (staged) {
+      for (int q = t; q < endom * GBN; q += GNT) {
+        const int dd = q / GBN, c = q % GBN;
+        const int64_t n = n0 + c, d = (int64_t)e_first + dd;
+        const bool ok = n < N;
+        Te[q] = ok ? p.e_relax[d * N + n] : make_float4(1.f, 0.f, 1.f, 0.f);
+        if (add_e) Ae[q] = ok ? p.e_add[d * p.e_add_ld + n] : 0.f;
+        if (cv_e) Ce[q] = ok ? p.e_cvec[d * p.e_cvec_ld + n] : 0.f;
+      }
+      for (int c = t; c < GBN; c += GNT) Ke[c] = (kb_e && n0 + c < N) ? p.e_kbias[n0 + c] : 0.f;
+      for (int rl = t; rl < GBM; rl += GNT) {
+        const int64_t m = m0 + rl;
+        Re[rl] = (m < M ? (int)(m / p.S) : e_first) - e_first;
+      }
+    }
+    __syncthreads();
+    float* __restrict__ C = p.C[z];
+    float pb[FM][16], pc[FM][16];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int64_t row = m0 + rloc;
+        float sb = 0.f, sc = 0.f;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int cloc = wn * T::WTN + j * 32 + lrow;
+          const int64_t col = n0 + cloc;
+          if (row < M && col < N) {
+            const float a = acc[i][j][r];
+            float4 e;
+            float add = 0.f, cv = 0.f, kb = 0.f;
+            if (staged) {
+              const int q = Re[rloc] * GBN + cloc;
+              e = Te[q];
+              if (add_e) add = Ae[q];
+              if (cv_e) cv = Ce[q];
+              kb = Ke[cloc];
+            } else {
+              const int64_t d = row / p.S;
+              e = p.e_relax[d * N + col];
+              if (add_e) add = p.e_add[d * p.e_add_ld + col];
+              if (cv_e) cv = p.e_cvec[d * p.e_cvec_ld + col];
+              if (kb_e) kb = p.e_kbias[col];
+            }
+            float be;
+            float out = a * fsel(e, lower, a >= 0.f, &be);
+            if (add_e) out = out + add;
+            sb += a * be;
+            if (kb_e) sb += out * kb;
+            if (cv_e) sc += out * cv;
+            C[row * p.ldc + col] = out;
+          }
+        }
+        pb[i][r] = sb;
+        pc[i][r] = sc;
+      }
+    // fixed-order reduction over the tile's columns: 32 lanes, then the NWN waves
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) {
+          pb[i][r] += __shfl_xor(pb[i][r], off, 64);
+          if (cv_e) pc[i][r] += __shfl_xor(pc[i][r], off, 64);
+        }
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      if (pass == 1 && !cv_e) break;   // uniform
+      if (lrow == 0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            red[wn][rloc] = pass == 0 ? pb[i][r] : pc[i][r];
+          }
+      }
+      __syncthreads();
+      float* __restrict__ dst = pass == 0 ? p.partial[z] : p.partial_c[z];
+      for (int rr = t; rr < GBM; rr += GNT) {
+        const int64_t row = m0 + rr;
+        if (row < M) {
+          float v = 0.f;
+#pragma unroll
+          for (int q = 0; q < T::NWN; ++q) v += red[q][rr];
+          dst[tile_n * M + row] = v;
+        }
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -524,10 +640,16 @@ static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
   BF_REQUIRE(ntiles + 8 < (1LL << 31), "gemm grid too large (M=%lld N=%lld)", (long long)a.M, (long long)a.N);
   const unsigned gy = (PRO == PRO_PLAIN && EPI == EPI_STORE && a.ksplit > 1) ? (unsigned)(a.ksplit * nz) : (unsigned)nz;
   dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), gy);
-  if (a.trans_b)
+  if (a.trans_b) {
     hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T>), grid, dim3(T::NT), 0, stream, a);
-  else
-    hipLaunchKernelGGL((gemm_kernel<PRO, EPI, false, T>), grid, dim3(T::NT), 0, stream, a);
+  } else {
+    if constexpr (EPI == EPI_RELAX) {
+      set_error("gemm: the relaxation epilogue takes the transposed weight");
+      return BF_EINVAL;
+    } else {
+      hipLaunchKernelGGL((gemm_kernel<PRO, EPI, false, T>), grid, dim3(T::NT), 0, stream, a);
+    }
+  }
   BF_LAUNCH_CHECK("gemm_kernel");
   return BF_OK;
 }
@@ -545,6 +667,10 @@ int launch_tile(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream)
     if constexpr (T::BN == NORM_BN) {                                                        \
       if (pro == PRO_PLAIN && epi == EPI_ABSSUM) return launch_gemm_t<PRO_PLAIN, EPI_ABSSUM, T>(a, nz, stream); \
       if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_gemm_t<PRO_RELAX, EPI_ABSSUM, T>(a, nz, stream); \
+    }                                                                                        \
+    if constexpr (std::is_same<T, TileA>::value) {                                           \
+      if (pro == PRO_PLAIN && epi == EPI_RELAX) return launch_gemm_t<PRO_PLAIN, EPI_RELAX, T>(a, nz, stream);   \
+      if (pro == PRO_RELAX && epi == EPI_RELAX) return launch_gemm_t<PRO_RELAX, EPI_RELAX, T>(a, nz, stream);   \
     }                                                                                        \
     set_error("gemm: tile configuration does not support pro=%d epi=%d", pro, epi);          \
     return BF_EINVAL;                                                                        \

@@ -30,6 +30,8 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
                         const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream);
 int gemm_partial_count(int64_t N);
+int rows_finalize(const float* b_src, const float* pb, const float* pc, int nparts, int64_t M, float* b_out,
+                  float* c_out, hipStream_t stream);
 int gemm_ksplit(int64_t M, int64_t N, int64_t K, int64_t* kchunk);
 int splitk_reduce(const float* part, int ks, int64_t M, int64_t N, float* C, int64_t ldc, const float* r_row,
                   const float* v_col, int64_t v_ld, int64_t S, hipStream_t stream);
@@ -642,7 +644,16 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
   a.add_l = add_l;
   a.add_ld = add_ld;
   a.kbias = bias;
-  return gemm_dispatch(a, PRO_RELAX, EPI_STORE, nz, stream);
+  if (relax || add_l || bias) return gemm_dispatch(a, PRO_RELAX, EPI_STORE, nz, stream);
+  // nothing to relax (A already relaxed): the plain contraction, b_out = b_in
+  const int rc = gemm_dispatch(a, PRO_PLAIN, EPI_STORE, nz, stream);
+  for (int z = 0; z < nz && rc == 0; ++z) {
+    if (a.b_out[z]) {
+      const int r2 = rows_finalize(a.b_in[z], nullptr, nullptr, 0, M, a.b_out[z], nullptr, stream);
+      if (r2) return r2;
+    }
+  }
+  return rc;
 }
 
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
@@ -704,6 +715,130 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
   const int64_t M = D * S;
   return (2 * (int64_t)gemm_partial_count(I) + 4) * M;
+}
+
+int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
+                                  int64_t N, const float* relax, const float* add_l, int64_t add_ld,
+                                  const float* W_t, int64_t P, const float* bias, const float* b_u_in,
+                                  const float* b_l_in, const float* relax_next, const float* add_next,
+                                  int64_t add_next_ld, const float* bias_next, const float* cvec_next,
+                                  int64_t cvec_next_ld, float* workspace, float* A_next_u, float* A_next_l,
+                                  float* b_u_out, float* b_l_out, float* c_u_out, float* c_l_out,
+                                  hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && N > 0 && P > 0, "bf_crown_relu_linear_relu_fwd: bad sizes");
+  const int64_t M = D * S;
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(W_t && relax_next && workspace, "bf_crown_relu_linear_relu_fwd: null weight, table or workspace");
+  BF_REQUIRE(((uintptr_t)relax & 15) == 0 && ((uintptr_t)relax_next & 15) == 0,
+             "bf_crown_relu_linear_relu_fwd: relaxation tables must be 16-byte aligned");
+  BF_REQUIRE((A_u != nullptr) == (A_next_u != nullptr) && (A_u != nullptr) == (b_u_out != nullptr) &&
+                 (A_l != nullptr) == (A_next_l != nullptr) && (A_l != nullptr) == (b_l_out != nullptr),
+             "bf_crown_relu_linear_relu_fwd: input/output pointer mismatch");
+  BF_REQUIRE(A_u || A_l, "bf_crown_relu_linear_relu_fwd: no coefficient");
+  BF_REQUIRE(cvec_next == nullptr || ((A_u == nullptr || c_u_out) && (A_l == nullptr || c_l_out)),
+             "bf_crown_relu_linear_relu_fwd: center sums need c_out");
+  const int nparts = gemm_partial_count(P);
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  int nz = 0;
+  float* pb[2] = {nullptr, nullptr};
+  float* pc[2] = {nullptr, nullptr};
+  float* cdst[2] = {nullptr, nullptr};
+  const float* bsrc[2] = {nullptr, nullptr};
+  float* bdst[2] = {nullptr, nullptr};
+  const bool relax_in = relax || add_l || bias;   // prologue relaxation (else A is already relaxed)
+  for (int side = 0; side < 2; ++side) {
+    const float* Ain = side == 0 ? A_u : A_l;
+    if (!Ain) continue;
+    a.A[nz] = Ain;
+    a.C[nz] = side == 0 ? A_next_u : A_next_l;
+    a.b_in[nz] = side == 0 ? b_u_in : b_l_in;
+    bdst[nz] = side == 0 ? b_u_out : b_l_out;
+    a.b_out[nz] = relax_in ? bdst[nz] : nullptr;
+    bsrc[nz] = relax_in ? bdst[nz] : a.b_in[nz];
+    pb[nz] = workspace + (int64_t)(2 * nz) * nparts * M;
+    pc[nz] = workspace + (int64_t)(2 * nz + 1) * nparts * M;
+    cdst[nz] = cvec_next ? (side == 0 ? c_u_out : c_l_out) : nullptr;
+    a.partial[nz] = pb[nz];
+    a.partial_c[nz] = pc[nz];
+    ++nz;
+  }
+  a.z_lower_first = (A_u == nullptr) ? 1 : 0;
+  a.lda = N;
+  a.lda_d = a_dstride;
+  a.ldc = P;
+  a.B = W_t;
+  a.trans_b = 1;
+  a.ldb = N;
+  a.M = M;
+  a.N = P;
+  a.K = N;
+  a.S = S;
+  a.relax = reinterpret_cast<const float4*>(relax);
+  a.add_l = add_l;
+  a.add_ld = add_ld;
+  a.kbias = bias;
+  a.e_relax = reinterpret_cast<const float4*>(relax_next);
+  a.e_add = add_next;
+  a.e_add_ld = add_next_ld;
+  a.e_kbias = bias_next;
+  a.e_cvec = cvec_next;
+  a.e_cvec_ld = cvec_next_ld;
+  int rc = gemm_dispatch(a, relax_in ? PRO_RELAX : PRO_PLAIN, EPI_RELAX, nz, stream);
+  if (rc) return rc;
+  for (int z = 0; z < nz; ++z) {
+    rc = rows_finalize(bsrc[z], pb[z], pc[z], nparts, M, bdst[z], cdst[z], stream);
+    if (rc) return rc;
+  }
+  return BF_OK;
+}
+
+int64_t bf_crown_relu_linear_relu_fwd_workspace(int64_t D, int64_t S, int64_t P) {
+  return 4 * (int64_t)gemm_partial_count(P) * D * S;
+}
+
+int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
+                               int64_t N, const float* W_t, int64_t I, const float* rad, float eps,
+                               const float* cen_u, const float* cen_l, const float* b_u, const float* b_l,
+                               float* workspace, float* lb, float* ub, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && N > 0 && I > 0, "bf_crown_linear_concretize: bad sizes");
+  const int64_t M = D * S;
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(W_t && workspace, "bf_crown_linear_concretize: null weight or workspace");
+  BF_REQUIRE((A_u == nullptr || (ub && cen_u && b_u)) && (A_l == nullptr || (lb && cen_l && b_l)) && (A_u || A_l),
+             "bf_crown_linear_concretize: missing coefficient, center, bias or output");
+  const int nparts = gemm_partial_count(I);
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  int nz = 0;
+  float* pu = workspace;
+  float* pl = workspace + (int64_t)nparts * M;
+  if (A_u) {
+    a.A[nz] = A_u; a.partial[nz] = pu; ++nz;
+  }
+  if (A_l) {
+    a.A[nz] = A_l; a.partial[nz] = pl; ++nz;
+  }
+  a.z_lower_first = (A_u == nullptr) ? 1 : 0;
+  a.lda = N;
+  a.lda_d = a_dstride;
+  a.B = W_t;
+  a.trans_b = 1;
+  a.ldb = N;
+  a.M = M;
+  a.N = I;
+  a.K = N;
+  a.S = S;
+  a.wvec = rad;
+  a.w_ld = I;
+  int rc = gemm_dispatch(a, PRO_PLAIN, EPI_ABSSUM, nz, stream);
+  if (rc) return rc;
+  return concretize_finalize(A_u ? pu : nullptr, A_l ? pl : nullptr, nparts, M, cen_u, cen_l, b_u, b_l,
+                             rad ? 1.0f : eps, A_l ? lb : nullptr, A_u ? ub : nullptr, stream);
+}
+
+int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
+  return 2 * (int64_t)gemm_partial_count(I) * D * S;
 }
 
 int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* relax,

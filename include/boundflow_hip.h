@@ -131,6 +131,44 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
                                     float* workspace, float* lb, float* ub, hipStream_t stream);
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I);
 
+/* Two consecutive regions of the CROWN backward of an MLP in one launch: the
+ * ReLU -> Linear region of bf_crown_relu_linear_fwd (prologue relaxation with
+ * relax / add_l / bias; when all three are NULL, A is taken as already relaxed)
+ * and the relaxation of the NEXT ReLU applied to the product before it is
+ * stored:
+ *   A_next = relax_next(A'' W^T) (+ add_next on the lower bound),
+ *   b_out  = b_in [+ prologue sums] + sum_n (C * beta_sel + A_next * bias_next),
+ *   c_out  = sum_n A_next * cvec_next   (only when cvec_next; row stride cvec_next_ld),
+ * so the next region reads A_next as it is (relax, add_l and bias NULL) and the
+ * input region can be concretized with bf_crown_linear_concretize.  The same
+ * steps as runtime/crown_ibp.py:1073-1090, 1211-1298 applied to two
+ * consecutive layers (the reference's dense backward loop, crown_ibp.py:1371-1700).
+ * W_t: the layer weight transposed, [P, N] row-major.  relax_next: table of
+ * bf_relu_relax_table over the P columns ([D, P]).  Rows of one 128-row tile
+ * spanning more than 10 domains (S < 15) read the tables from global memory.
+ * workspace: bf_crown_relu_linear_relu_fwd_workspace(D, S, P) floats. */
+int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
+                                  int64_t N, const float* relax, const float* add_l, int64_t add_ld,
+                                  const float* W_t, int64_t P, const float* bias, const float* b_u_in,
+                                  const float* b_l_in, const float* relax_next, const float* add_next,
+                                  int64_t add_next_ld, const float* bias_next, const float* cvec_next,
+                                  int64_t cvec_next_ld, float* workspace, float* A_next_u, float* A_next_l,
+                                  float* b_u_out, float* b_l_out, float* c_u_out, float* c_l_out,
+                                  hipStream_t stream);
+int64_t bf_crown_relu_linear_relu_fwd_workspace(int64_t D, int64_t S, int64_t P);
+
+/* Linf / box concretization of an input layer whose coefficient is already
+ * relaxed (the output of bf_crown_relu_linear_relu_fwd):
+ *   lb = (cen_l - eps * sum_i |(A_l W^T)_i| * rad_i) + b_l, ub mirrored,
+ * with the center and bias sums given per row.  concretize_affine
+ * (runtime/perturbation.py:175-222, 327-359) as called at crown_ibp.py:2044-2051.
+ * workspace: bf_crown_linear_concretize_workspace(D, S, I) floats. */
+int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
+                               int64_t N, const float* W_t, int64_t I, const float* rad, float eps,
+                               const float* cen_u, const float* cen_l, const float* b_u, const float* b_l,
+                               float* workspace, float* lb, float* ub, hipStream_t stream);
+int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I);
+
 /* Standalone relaxation pass (bandwidth-bound form of kernel #3): writes A'
  * and the bias/center row sums, one wave64 per row.  Replaces
  * _backprop_relu_step_dense_reference (runtime/crown_ibp.py:1211-1298); used
