@@ -50,17 +50,24 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
     set_error("gemm_dispatch: bad mode pro=%d epi=%d", pro, epi);
     return BF_EINVAL;
   }
-  if (epi == EPI_RELAX) return launch_tile<TileA>(a, pro, epi, nz, stream);   // its one configuration
   switch (g_force_config) {
-    case 1: return launch_tile<TileB>(a, pro, epi, nz, stream);
-    case 2: return launch_tile<TileC>(a, pro, epi, nz, stream);
+    case 0: return launch_tile<TileA>(a, pro, epi, nz, stream);
+    // the relaxation epilogue exists for the 128 x 128 configurations (TileA, TileG)
+    case 1: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileB>(a, pro, epi, nz, stream);
+    case 2: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileC>(a, pro, epi, nz, stream);
     case 3:
-      // the |C| epilogue needs BN == NORM_BN; TileD is a store-only configuration
+      // the |C| epilogues need BN == NORM_BN; TileD is a store-only configuration
       if (epi == EPI_STORE) return launch_tile<TileD>(a, pro, epi, nz, stream);
       return launch_tile<TileA>(a, pro, epi, nz, stream);
-    case 4: return launch_tile<TileE>(a, pro, epi, nz, stream);
-    case 5: return launch_tile<TileF>(a, pro, epi, nz, stream);
-    default: return launch_tile<TileA>(a, pro, epi, nz, stream);
+    case 4: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileE>(a, pro, epi, nz, stream);
+    case 5: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileF>(a, pro, epi, nz, stream);
+    case 6: return launch_tile<TileG>(a, pro, epi, nz, stream);
+    default:
+      // automatic: 8 waves per workgroup (TileG) for every form but the fused
+      // relaxation + concretization, whose LDS stage of the relaxation, center and
+      // split slices keeps TileG at 2 workgroups per CU
+      if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_tile<TileA>(a, pro, epi, nz, stream);
+      return launch_tile<TileG>(a, pro, epi, nz, stream);
   }
 }
 

@@ -59,9 +59,10 @@ struct Tile {
   static constexpr int RPP = NT / KQ;                // A rows covered per slot index
   static constexpr int BS_FLOATS = BN * BPT;
   // Relaxation operands staged in LDS per K tile: one (domain, k) entry per
-  // thread, so a tile whose rows span at most TAB_DOMS domains reads them there.
-  static constexpr int TAB_ENTRIES = NT;
-  static constexpr int TAB_DOMS = NT / BK;
+  // thread of the first TAB_ENTRIES, so a tile whose rows span at most TAB_DOMS
+  // domains reads them there (16 domains: every tile when S >= 9).
+  static constexpr int TAB_ENTRIES = NT < 256 ? NT : 256;
+  static constexpr int TAB_DOMS = TAB_ENTRIES / BK;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert((BM * BK) % (4 * NT) == 0 && (BN * BK) % (4 * NT) == 0, "tile/thread mismatch");
   static_assert((BK & (BK - 1)) == 0 && BK >= 8, "BK must be a power of two >= 8");
@@ -264,9 +265,11 @@ gemm_kernel(GemmArgs p) {
     };
     auto store_tab = [&](int slot) {
       if constexpr (PRO == PRO_RELAX && FAST) {
-        Ts[slot][t] = tab_reg;
-        if constexpr (ADD) As_add[slot][t] = add_reg;
-        if constexpr (CV && RR) Cs[slot][t] = cv_reg;
+        if (t < T::TAB_ENTRIES) {
+          Ts[slot][t] = tab_reg;
+          if constexpr (ADD) As_add[slot][t] = add_reg;
+          if constexpr (CV && RR) Cs[slot][t] = cv_reg;
+        }
         if constexpr (KB && RR)
           if (t < GBK) Kb[slot][t] = kb_reg;
       }
@@ -338,23 +341,8 @@ gemm_kernel(GemmArgs p) {
       }
     };
 
-    // Prologue: relaxation slices of K tiles 0 and 1, then tile 0 itself.
-    load_tab(0);
-    store_tab(0);
-    if (nk > 1) {
-      load_tab(GBK);
-      store_tab(1);
-    }
-    load_tiles(kbase);
-    __syncthreads();
-    store_tiles(0, kbase, 0);
-    __syncthreads();
-    int buf = 0;
-    for (int64_t kt = 0; kt < nk; ++kt) {
-      const bool more = kt + 1 < nk;
-      const bool more2 = kt + 2 < nk;
-      if (more) load_tiles(kbase + (kt + 1) * GBK);
-      if (more2) load_tab((kt + 2) * GBK);
+    // The 32 MFMAs of one K tile of this wave, operands from LDS buffer buf.
+    auto mfma_tile = [&](int buf) {
       const float* __restrict__ as = As[buf];
       const float* __restrict__ bs = Bs[buf];
 #pragma unroll
@@ -381,6 +369,26 @@ gemm_kernel(GemmArgs p) {
             for (int jj = 0; jj < FN; ++jj)
               acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
       }
+    };
+
+    // Prologue: relaxation slices of K tiles 0 and 1, then tile 0 itself.
+    load_tab(0);
+    store_tab(0);
+    if (nk > 1) {
+      load_tab(GBK);
+      store_tab(1);
+    }
+    load_tiles(kbase);
+    __syncthreads();
+    store_tiles(0, kbase, 0);
+    __syncthreads();
+    int buf = 0;
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const bool more = kt + 1 < nk;
+      const bool more2 = kt + 2 < nk;
+      if (more) load_tiles(kbase + (kt + 1) * GBK);
+      if (more2) load_tab((kt + 2) * GBK);
+      mfma_tile(buf);
       if (more) store_tiles(buf ^ 1, kbase + (kt + 1) * GBK, kt + 1);
       // slot kt & 1 held tile kt's slice, consumed one iteration ago
       if (more2) store_tab((int)(kt & 1));
@@ -630,6 +638,7 @@ using TileC = Tile<256, 128, 16, 4, 2, 1>;   // 8 waves of 64x64
 using TileD = Tile<128, 256, 16, 2, 2, 2>;   // 4 waves of 64x128 (store epilogue only)
 using TileE = Tile<64, 128, 16, 1, 2, 4>;    // 2 waves of 64x64: more workgroups for short M
 using TileF = Tile<128, 128, 16, 2, 2, 2>;   // TileA at 2 workgroups per CU
+using TileG = Tile<128, 128, 16, 4, 2, 3>;   // 8 waves of 32x64: twice the waves per CU of TileA
 
 template <int PRO, int EPI, class T>
 static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
@@ -668,7 +677,7 @@ int launch_tile(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream)
       if (pro == PRO_PLAIN && epi == EPI_ABSSUM) return launch_gemm_t<PRO_PLAIN, EPI_ABSSUM, T>(a, nz, stream); \
       if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_gemm_t<PRO_RELAX, EPI_ABSSUM, T>(a, nz, stream); \
     }                                                                                        \
-    if constexpr (std::is_same<T, TileA>::value) {                                           \
+    if constexpr (T::BN == NORM_BN && T::BM == 128) {                                        \
       if (pro == PRO_PLAIN && epi == EPI_RELAX) return launch_gemm_t<PRO_PLAIN, EPI_RELAX, T>(a, nz, stream);   \
       if (pro == PRO_RELAX && epi == EPI_RELAX) return launch_gemm_t<PRO_RELAX, EPI_RELAX, T>(a, nz, stream);   \
     }                                                                                        \
@@ -682,5 +691,6 @@ template <> int launch_tile<TileC>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileD>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileE>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileF>(const GemmArgs&, int, int, int, hipStream_t);
+template <> int launch_tile<TileG>(const GemmArgs&, int, int, int, hipStream_t);
 
 }  // namespace bf
