@@ -50,43 +50,132 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def hip_runner(name: str):
+    """The HIP path of a configuration as a function of a device workload."""
+    from boundflow_amd import crown as hc
+
+    if name == "C2":
+        return lambda wd: hc.run_crown_all_intermediate(wd.module, wd.spec, linear_spec_C=wd.C)[0]
+    if name in ("C1", "C3"):
+        return lambda wd: hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+    if name == "C4":
+        from boundflow_amd import alpha_beta as hab
+        return lambda wd: hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C, steps=20,
+                                                              lr=0.1)[0]
+    if name == "C5":
+        from boundflow_amd import bab as hbab
+        return lambda wd: hbab.evaluate_domain_batch(wd.module, wd.spec, linear_spec_C=wd.C,
+                                                     relu_split_state=wd.extra["splits"], steps=10, lr=0.2)
+    raise SystemExit(f"unknown config {name}")
+
+
 def build_case(name: str):
     import torch
-    from boundflow_amd import crown as hc
     from boundflow_amd import workloads as wl
 
     dev = torch.device("cuda:0")
     w = wl.make(name)
     wd = wl.to_device(w, dev)
-    if name == "C2":
-        def step():
-            return hc.run_crown_all_intermediate(wd.module, wd.spec, linear_spec_C=wd.C)[0]
-        units, unit = w.batch * w.num_specs, "bounds/s"
-        desc = "C2: CROWN, all intermediate bounds by CROWN, MLP 784-500x6-10, B=256, Linf 0.015, 9 margin specs"
-    elif name in ("C1", "C3"):
-        def step():
-            return hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
-        units, unit = w.batch * w.num_specs, "bounds/s"
-        desc = {"C1": "C1: IBP+CROWN, MLP 784-256-256-10, B=64, box eps 2/255 clamped, 9 margin specs",
-                "C3": "C3: CROWN, CNN 3x32x32 conv16-conv32-fc100-fc10, B=128, Linf 2/255, 9 margin specs"}[name]
-    elif name == "C4":
-        from boundflow_amd import alpha_beta as hab
+    run = hip_runner(name)
 
-        def step():
-            return hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C, steps=20, lr=0.1)[0]
-        units, unit = w.batch * w.num_specs, "bounds/s"
-        desc = "C4: alpha-CROWN, CNN of C3, B=32, Linf 8/255, 20 Adam steps lr 0.1, alpha from CROWN"
-    elif name == "C5":
-        from boundflow_amd import bab as hbab
+    def step():
+        return run(wd)
 
-        def step():
-            return hbab.evaluate_domain_batch(wd.module, wd.spec, linear_spec_C=wd.C,
-                                              relu_split_state=wd.extra["splits"], steps=10, lr=0.2)
+    if name == "C5":
         units, unit = w.batch, "domains/s"
-        desc = "C5: beta-CROWN BaB batch, MLP 784-256x4-10, 4096 domains, Linf 0.03, 1-12 splits, 10 steps"
     else:
-        raise SystemExit(f"unknown config {name}")
+        units, unit = w.batch * w.num_specs, "bounds/s"
+    desc = {"C1": "C1: IBP+CROWN, MLP 784-256-256-10, B=64, box eps 2/255 clamped, 9 margin specs",
+            "C2": "C2: CROWN, all intermediate bounds by CROWN, MLP 784-500x6-10, B=256, Linf 0.015, 9 margin specs",
+            "C3": "C3: CROWN, CNN 3x32x32 conv16-conv32-fc100-fc10, B=128, Linf 2/255, 9 margin specs",
+            "C4": "C4: alpha-CROWN, CNN of C3, B=32, Linf 8/255, 20 Adam steps lr 0.1, alpha from CROWN",
+            "C5": "C5: beta-CROWN BaB batch, MLP 784-256x4-10, 4096 domains, Linf 0.03, 1-12 splits, 10 steps"}[name]
     return w, step, units, unit, desc
+
+
+def intermediate_bounds(w) -> int:
+    """Pre-activation bounds refined by CROWN per C2 step: every ReLU input after the first, per input."""
+    from boundflow_amd import crown as hc
+
+    shapes = hc.parse_chain(w.module, w.spec).relu_shapes
+    widths = [int(torch_numel(s)) for s in shapes.values()]
+    return w.batch * sum(widths[1:])
+
+
+def torch_numel(shape) -> int:
+    n = 1
+    for d in shape:
+        n *= int(d)
+    return n
+
+
+def _oracle_run(name: str, sub):
+    """The oracle's result for a workload (the computation the CPU baseline times)."""
+    import torch
+    from oracle import alpha_beta_ref as ab
+    from oracle import crown_ref as cr
+
+    if name == "C2":
+        with torch.inference_mode():
+            return cr.run_crown_all_intermediate(sub.module, sub.spec, linear_spec_C=sub.C)
+    if name in ("C1", "C3"):
+        with torch.inference_mode():
+            return cr.run_crown_ibp(sub.module, sub.spec, linear_spec_C=sub.C)
+    if name == "C4":
+        _e, pre = cr.forward_ibp_trace(sub.module, sub.spec)
+        init = ab.adaptive_alpha_init(pre)
+        return ab.run_alpha_beta_crown(sub.module, sub.spec, linear_spec_C=sub.C, steps=20, lr=0.1,
+                                       warm_start_alpha=init, per_batch_params=True)
+    return ab.evaluate_domain_batch(sub.module, sub.spec, linear_spec_C=sub.C,
+                                    relu_split_state=sub.extra["splits"], steps=10, lr=0.2)
+
+
+def _bounds(name: str, res):
+    if name == "C5":
+        return res["lower"], res["upper"]
+    r = res[0] if isinstance(res, tuple) else res
+    return r.lower, r.upper
+
+
+def parity_summary(name: str, sub, ref) -> dict:
+    """HIP result on the CPU-baseline sample against the oracle's result on it.
+    The contract: rtol 1e-5 / atol 1e-6 on both bounds (C1-C3); rtol 1e-4 /
+    atol 1e-4 on the optimised lower bound (C4, C5: Adam trajectories amplify fp32
+    rounding).  Rows outside it count as explained when the fp64 oracle run is
+    as far from the fp32 oracle as the HIP value is.  Also: verdict mismatches,
+    near ties (|min_s lb| < 1e-4) and, for the BaB batch, statuses and branching."""
+    import torch
+    from boundflow_amd import workloads as wl
+    from oracle import parity
+
+    got = hip_runner(name)(wl.to_device(sub, torch.device("cuda:0")))
+    torch.cuda.synchronize()
+    g_lo, g_hi = (t.cpu() for t in _bounds(name, got))
+    r_lo, r_hi = _bounds(name, ref)
+    optimised = name in ("C4", "C5")
+    rtol, atol = (1e-4, 1e-4) if optimised else (1e-5, 1e-6)
+    keep = torch.isfinite(r_lo).all(dim=1)
+    pick = (lambda lo, hi: lo[keep]) if optimised else (lambda lo, hi: torch.cat([lo[keep], hi[keep]]))
+    rep = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None, rtol=rtol, atol=atol)
+    if rep.strict_violations:
+        ref64 = _oracle_run(name, parity.to_float64(sub))
+        e_lo, e_hi = _bounds(name, ref64)
+        rep = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), pick(e_lo, e_hi), rtol=rtol, atol=atol)
+    g_min = g_lo[keep].min(dim=1).values
+    r_min = r_lo[keep].min(dim=1).values
+    out = {"contract": f"rtol {rtol:g} atol {atol:g} on " + ("the optimised lower bound" if optimised else "both bounds"),
+           "values": rep.n, "max_abs_err": rep.max_abs, "max_rel_err": rep.max_rel,
+           "outside_contract": rep.strict_violations, "explained_by_fp64": rep.explained_by_fp32,
+           "unexplained": rep.unexplained, "verdict_mismatches": int(((g_min >= 0) != (r_min >= 0)).sum()),
+           "near_ties": int((r_min.abs() < 1e-4).sum())}
+    if name == "C5":
+        out["status_mismatches"] = int(((got["status"].cpu() == 1) != ref["certified"]).sum())
+        names = got["relu_names"]
+        layer, neuron = got["branch_layer"].cpu().tolist(), got["branch_neuron"].cpu().tolist()
+        hip_branch = [None if l < 0 else (names[l], n) for l, n in zip(layer, neuron)]
+        out["branch_mismatches"] = sum(bool(ref["feasible"][i]) and hip_branch[i] != ref["branch"][i]
+                                       for i in range(len(hip_branch)))
+    return out
 
 
 def cpu_baseline(name: str, w, seconds: float):
@@ -94,43 +183,29 @@ def cpu_baseline(name: str, w, seconds: float):
     bounded sample of the same workload; returns throughput in the metric unit."""
     import torch
     from boundflow_amd import workloads as wl
-    from oracle import alpha_beta_ref as ab
-    from oracle import crown_ref as cr
 
     threads = torch.get_num_threads()
     done_units = 0
     elapsed = 0.0
     rounds = 0
     sample_b = {"C1": 16, "C2": 4, "C3": 16, "C4": 2, "C5": 64}[name]
+    first = None
     while elapsed < seconds and rounds < 64:
         sub = wl.subset(w, sample_b)
         t0 = time.perf_counter()
-        if name == "C2":
-            with torch.inference_mode():
-                cr.run_crown_all_intermediate(sub.module, sub.spec, linear_spec_C=sub.C)
-            done_units += sub.batch * sub.num_specs
-        elif name in ("C1", "C3"):
-            with torch.inference_mode():
-                cr.run_crown_ibp(sub.module, sub.spec, linear_spec_C=sub.C)
-            done_units += sub.batch * sub.num_specs
-        elif name == "C4":
-            _e, pre = cr.forward_ibp_trace(sub.module, sub.spec)
-            init = ab.adaptive_alpha_init(pre)
-            ab.run_alpha_beta_crown(sub.module, sub.spec, linear_spec_C=sub.C, steps=20, lr=0.1,
-                                    warm_start_alpha=init, per_batch_params=True)
-            done_units += sub.batch * sub.num_specs
-        else:
-            ab.evaluate_domain_batch(sub.module, sub.spec, linear_spec_C=sub.C,
-                                     relu_split_state=sub.extra["splits"], steps=10, lr=0.2)
-            done_units += sub.batch
+        res = _oracle_run(name, sub)
+        done_units += sub.batch if name == "C5" else sub.batch * sub.num_specs
         elapsed += time.perf_counter() - t0
         rounds += 1
+        if first is None:
+            first = (sub, res)
     return {
         "value": done_units / elapsed,
         "cores": threads,
         "kind": "port",
         "sample": f"{rounds} x {sample_b}-input subsets of {name} ({done_units} units, {elapsed:.1f} s), "
                   f"PyTorch CPU fp32 restatement of the reference path, {threads} threads on {cpu_model()}",
+        "parity": parity_summary(name, *first),
     }
 
 
@@ -229,7 +304,8 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded Kaiming weights, uniform inputs)",
         "config": {"workload": desc, "units_per_step": units, "parallelism": "single GPU",
-                   "launch": "hip_graph replay" if use_graph else "eager"},
+                   "launch": "hip_graph replay" if use_graph else "eager",
+                   **({"intermediate_bounds_per_step": intermediate_bounds(w)} if args.config == "C2" else {})},
         "roofline": roofline,
         "kernels": {k: {"launches": int(v["launches"]), "avg_ms": round(v["avg_ms"], 4),
                         "tflops": round(v["tflops"], 3), "gbps": round(v["gbps"], 1)} for k, v in kernels.items()},
