@@ -356,6 +356,148 @@ conv_mfma_kernel(GatherArgs g) {
   }
 }
 
+// conv_transpose2d of rows with few output channels (Ci <= 4, KH * KW <= 16),
+// where the gather-GEMM above leaves most of its 16 MFMA channel rows idle.
+// Per row and per output channel n, the taps are computed as one dense product
+//   Z_n[(kh, kw), p] = sum_co W[co, n, kh, kw] * X[co, p]      (p: pixel of the Ho x Wo map)
+// on v_mfma_f32_16x16x4f32 (16 tap rows, 16 pixels, 4 channels per step), kept
+// in LDS, and each output pixel then gathers its taps (col2im):
+//   y[n, oh, ow] = sum over (kh, kw) with ih = (oh + ph - kh) / sh, iw = (ow + pw - kw) / sw
+//   integral and inside the map of Z_n[(kh, kw), (ih, iw)],
+// followed by the store / weighted-norm / gradient-seed epilogue of conv_mfma_kernel.
+struct SmallTArgs {
+  const float* X[2];
+  float* y[2];
+  float* nrm[2];
+  const float* W;          // [Co, Ci, KH, KW]
+  const float* wv;         // norm weights [D, Ci*Hi*Wi] (w_ld) or NULL
+  const float* h_scale;
+  float* h_out;
+  int64_t R, S, w_ld;
+  int rows_per_wg, z_lower_first;
+  int Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi;
+  int Co4, npix, nblk;     // channels padded to 4, pixels Ho*Wo, 16-pixel blocks
+  int vec;                 // rows copied as float4 (npix % 16 == 0 and 16-byte aligned row starts)
+  FastDiv f_Wi, f_sh, f_sw, f_pitch;   // index divisions of the col2im and the map copy
+};
+
+__global__ void __launch_bounds__(GT)
+conv_t_small_kernel(SmallTArgs g) {
+  extern __shared__ float smem[];
+  float* Wsm = smem;                                   // [Ci][Co4][16]: tap-fastest MFMA A operand
+  float* Xs = Wsm + (size_t)g.Ci * g.Co4 * 16;          // [Co4][nblk * 16]
+  float* Zs = Xs + (size_t)g.Co4 * g.nblk * 16;         // [16][nblk * 16]
+  __shared__ float red[GT / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int z = blockIdx.y;
+  const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
+  const float* __restrict__ X = g.X[z];
+  float* __restrict__ y = g.y[z];
+  float* __restrict__ nrm = g.nrm[z];
+  const int taps = g.KH * g.KW;
+  const int pitch = g.nblk * 16;
+  const int nin = g.Co * g.npix;
+  const int64_t nout = (int64_t)g.Ci * g.Hi * g.Wi;
+
+  for (int idx = tid; idx < g.Ci * g.Co4 * 16; idx += GT) {
+    const int n = idx / (g.Co4 * 16), rem = idx - n * g.Co4 * 16;
+    const int co = rem / 16, t = rem - co * 16;
+    float w = 0.f;
+    if (co < g.Co && t < taps) w = g.W[((int64_t)co * g.Ci + n) * taps + t];   // t = kh * KW + kw
+    Wsm[idx] = w;
+  }
+
+  const int k4 = lane >> 4;    // k sub-index of the operands; row group of the result
+  const int col = lane & 15;
+  for (int i = 0; i < g.rows_per_wg; ++i) {
+    const int64_t r = (int64_t)blockIdx.x * g.rows_per_wg + i;
+    if (r >= g.R) break;   // uniform
+    __syncthreads();       // weights staged / the previous row's maps consumed
+    const float* __restrict__ xr = X + r * nin;
+    if (g.vec) {
+      // unpadded map (npix % 16 == 0, 16-byte aligned rows): a float4 copy, then the zero channels
+      const float4* __restrict__ x4 = reinterpret_cast<const float4*>(xr);
+      float4* xs4 = reinterpret_cast<float4*>(Xs);
+      for (int q = tid; q < nin / 4; q += GT) xs4[q] = x4[q];
+      for (int idx = nin + tid; idx < g.Co4 * pitch; idx += GT) Xs[idx] = 0.f;
+    } else {
+      for (int idx = tid; idx < g.Co4 * pitch; idx += GT) {
+        const int co = fdivq(idx, g.f_pitch), p = idx - co * pitch;
+        Xs[idx] = (co < g.Co && p < g.npix) ? xr[co * g.npix + p] : 0.f;
+      }
+    }
+    const int64_t d = r / g.S;
+    const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
+    float s = 0.f;
+    for (int n = 0; n < g.Ci; ++n) {
+      __syncthreads();   // Xs staged / the previous channel's taps consumed
+      const float* __restrict__ wn = Wsm + (size_t)n * g.Co4 * 16;
+      for (int jb = wave; jb < g.nblk; jb += GT / 64) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int k = k4; k < g.Co4; k += 4)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wn[k * 16 + col], Xs[k * pitch + jb * 16 + col], acc, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) Zs[(4 * k4 + q) * pitch + jb * 16 + col] = acc[q];
+      }
+      __syncthreads();
+      for (int o = tid; o < g.Hi * g.Wi; o += GT) {
+        const int oh = fdivq(o, g.f_Wi), ow = o - oh * g.Wi;
+        // taps kh = kh0 + sh*a reach map row ih0 - a (kh0 = (oh + ph) mod sh), likewise for columns
+        const int qh = fdivq(oh + g.ph, g.f_sh), qw = fdivq(ow + g.pw, g.f_sw);
+        const int kh0 = oh + g.ph - qh * g.sh, kw0 = ow + g.pw - qw * g.sw;
+        float v = 0.f;
+        for (int kh = kh0, ih = qh; kh < g.KH; kh += g.sh, --ih) {
+          if (ih < 0 || ih >= g.Ho) continue;
+          for (int kw = kw0, iw = qw; kw < g.KW; kw += g.sw, --iw) {
+            if (iw < 0 || iw >= g.Wo) continue;
+            v += Zs[(kh * g.KW + kw) * pitch + ih * g.Wo + iw];
+          }
+        }
+        const int64_t oidx = (int64_t)n * g.Hi * g.Wi + o;
+        if (y) y[r * nout + oidx] = v;
+        if (nrm) {
+          const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
+          s += g.wv ? fabsf(v) * wgt : fabsf(v);
+          if (lower && g.h_out) {
+            const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
+            g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
+          }
+        }
+      }
+    }
+    if (nrm) {
+      for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+      if (lane == 0) red[wave] = s;
+      __syncthreads();
+      if (tid == 0) {
+        float tsum = 0.f;
+        for (int q = 0; q < GT / 64; ++q) tsum += red[q];
+        nrm[r] = tsum;
+      }
+    }
+  }
+}
+
+// Plan of conv_t_small_kernel; false when it does not apply.
+static bool conv_t_small_plan(SmallTArgs& g, int64_t R, int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh,
+                              int sw, int ph, int pw, int Hi, int Wi, size_t* lds_bytes) {
+  if (Ci > 4 || KH * KW > 16 || ph < 0 || pw < 0) return false;
+  g.R = R;
+  g.Co = Co; g.Ho = Ho; g.Wo = Wo; g.Ci = Ci; g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw; g.ph = ph; g.pw = pw;
+  g.Hi = Hi; g.Wi = Wi;
+  g.Co4 = (Co + 3) / 4 * 4;
+  g.npix = Ho * Wo;
+  g.nblk = (g.npix + 15) / 16;
+  const size_t lds = sizeof(float) * ((size_t)Ci * g.Co4 * 16 + (size_t)g.Co4 * g.nblk * 16 + (size_t)16 * g.nblk * 16);
+  if (lds > 64 * 1024 || Hi * Wi >= 65536 || Hi + ph >= 65536 || Wi + pw >= 65536) return false;
+  *lds_bytes = lds;
+  g.f_Wi = make_fdiv(Wi);
+  g.f_sh = make_fdiv(sh);
+  g.f_sw = make_fdiv(sw);
+  g.f_pitch = make_fdiv(g.nblk * 16);
+  return true;
+}
+
 // floor / ceil of x / y for y > 0 and any sign of x
 static inline int fdiv(int x, int y) { return x >= 0 ? x / y : -((-x + y - 1) / y); }
 static inline int cdiv(int x, int y) { return x >= 0 ? (x + y - 1) / y : -((-x) / y); }
@@ -535,6 +677,31 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
   BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || norm_l != nullptr),
              "bf_conv_transpose_rows: h_out needs h_scale and the lower norm");
   const unsigned nz = (A_u && A_l) ? 2u : 1u;
+  {
+    SmallTArgs g;
+    memset(&g, 0, sizeof(g));
+    size_t glds = 0;
+    if (conv_t_small_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
+      int nzi = 0;
+      if (A_u) { g.X[nzi] = A_u; g.y[nzi] = y_u; g.nrm[nzi] = norm_u; ++nzi; }
+      if (A_l) { g.X[nzi] = A_l; g.y[nzi] = y_l; g.nrm[nzi] = norm_l; ++nzi; }
+      g.z_lower_first = A_u ? 0 : 1;
+      g.W = W;
+      g.wv = wvec;
+      g.w_ld = w_ld;
+      g.h_scale = h_scale;
+      g.h_out = h_out;
+      g.S = S;
+      g.vec = (g.npix % 16 == 0) && (((uintptr_t)(A_u ? A_u : A_l) & 15) == 0) &&
+              (A_u == nullptr || A_l == nullptr || ((uintptr_t)A_l & 15) == 0) ? 1 : 0;
+      const int rpw = gather_rows_per_wg(R * nz);
+      g.rows_per_wg = rpw;
+      BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
+      hipLaunchKernelGGL(conv_t_small_kernel, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GT), glds, stream, g);
+      BF_LAUNCH_CHECK("conv_t_small_kernel");
+      return BF_OK;
+    }
+  }
   {
     GatherArgs g;
     memset(&g, 0, sizeof(g));

@@ -62,11 +62,16 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
     case 4: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileE>(a, pro, epi, nz, stream);
     case 5: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileF>(a, pro, epi, nz, stream);
     case 6: return launch_tile<TileG>(a, pro, epi, nz, stream);
+    case 7: return launch_tile<TileH>(a, pro, epi, nz, stream);
     default:
-      // automatic: 8 waves per workgroup (TileG) for every form but the fused
-      // relaxation + concretization, whose LDS stage of the relaxation, center and
-      // split slices keeps TileG at 2 workgroups per CU
+      // automatic (measured per form on the C2 and C5 shapes): the fused relaxation
+      // + concretization on TileA (its LDS slices keep the 8- and 16-wave tiles at
+      // fewer workgroups per CU); the plain prologue with the relaxation epilogue,
+      // and the plain concretization over a long contraction, on the 16-wave TileH;
+      // every other form on the 8-wave TileG.
       if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_tile<TileA>(a, pro, epi, nz, stream);
+      if (pro == PRO_PLAIN && (epi == EPI_RELAX || (epi == EPI_ABSSUM && a.K >= 384)))
+        return launch_tile<TileH>(a, pro, epi, nz, stream);
       return launch_tile<TileG>(a, pro, epi, nz, stream);
   }
 }

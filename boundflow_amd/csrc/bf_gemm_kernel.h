@@ -639,6 +639,7 @@ using TileD = Tile<128, 256, 16, 2, 2, 2>;   // 4 waves of 64x128 (store epilogu
 using TileE = Tile<64, 128, 16, 1, 2, 4>;    // 2 waves of 64x64: more workgroups for short M
 using TileF = Tile<128, 128, 16, 2, 2, 2>;   // TileA at 2 workgroups per CU
 using TileG = Tile<128, 128, 16, 4, 2, 3>;   // 8 waves of 32x64: twice the waves per CU of TileA
+using TileH = Tile<128, 128, 32, 4, 4, 1>;   // 16 waves of 32x32, BK 32
 
 template <int PRO, int EPI, class T>
 static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
@@ -692,5 +693,6 @@ template <> int launch_tile<TileD>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileE>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileF>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileG>(const GemmArgs&, int, int, int, hipStream_t);
+template <> int launch_tile<TileH>(const GemmArgs&, int, int, int, hipStream_t);
 
 }  // namespace bf

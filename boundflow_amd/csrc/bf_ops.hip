@@ -518,7 +518,7 @@ extern "C" {
 int bf_abi_version(void) { return 1; }
 
 int bf_tuning_set_gemm_tile(int config) {
-  BF_REQUIRE(config >= -1 && config <= 6, "bf_tuning_set_gemm_tile: config must be -1 (automatic) or 0..6");
+  BF_REQUIRE(config >= -1 && config <= 7, "bf_tuning_set_gemm_tile: config must be -1 (automatic) or 0..7");
   gemm_force_config(config);
   return BF_OK;
 }

@@ -3,9 +3,10 @@
 bf_conv_transpose_rows replaces Conv2dLinearOperator.to_dense
 (boundflow/runtime/linear_operator.py:1067-1092), i.e. conv_transpose2d of every
 coefficient row, optionally fused with the concretization norm
-sum |y| * w and the gradient seed h = h_scale * sign(y) * w.  Shapes with
-KH % sh == 0 and KW % sw == 0 run the parity-class MFMA kernel, the others the
-row kernel; both are covered.  bf_conv2d_rows (conv2d of rows with W or |W| and
+sum |y| * w and the gradient seed h = h_scale * sign(y) * w.  Shapes with at
+most 4 output channels and 16 taps run the tap-product MFMA kernel, other
+shapes with KH % sh == 0 and KW % sw == 0 the parity-class MFMA kernel, the
+rest the row kernel; all three are covered.  bf_conv2d_rows (conv2d of rows with W or |W| and
 a rank-1 term: the IBP conv step, the input-center projection and the gradient
 of a transposed convolution) runs the same gather-GEMM kernel in its forward
 mode.  Tolerance: the fp32 accumulation bound K * 2^-23 * sum |terms| of each
@@ -23,11 +24,13 @@ pytestmark = pytest.mark.gpu
 
 # (R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, S)
 SHAPES = [
-    (37, 32, 8, 8, 16, 4, 4, 2, 2, 1, 1, 9),     # C3 conv1 backward (MFMA path)
-    (20, 16, 16, 16, 3, 4, 4, 2, 2, 1, 1, 4),    # C3 conv0 backward (MFMA path, Ci < 16)
-    (9, 8, 7, 5, 20, 3, 3, 1, 1, 1, 1, 3),       # stride 1, 3x3, Ci > 16 (MFMA path, 9 taps)
-    (6, 5, 6, 6, 4, 2, 2, 2, 2, 0, 0, 2),        # 2x2 stride 2, no padding (MFMA path)
-    (7, 6, 5, 5, 3, 3, 3, 2, 2, 1, 1, 7),        # KH % sh != 0 (row kernel)
+    (37, 32, 8, 8, 16, 4, 4, 2, 2, 1, 1, 9),     # C3 conv1 backward (parity-class MFMA kernel)
+    (20, 16, 16, 16, 3, 4, 4, 2, 2, 1, 1, 4),    # C3 conv0 backward (tap-product kernel, float4 map copy)
+    (9, 8, 7, 5, 20, 3, 3, 1, 1, 1, 1, 3),       # stride 1, 3x3, Ci > 16 (parity-class kernel, 9 taps)
+    (6, 5, 6, 6, 4, 2, 2, 2, 2, 0, 0, 2),        # 2x2 stride 2, no padding, 36 pixels (tap-product kernel)
+    (7, 6, 5, 5, 3, 3, 3, 2, 2, 1, 1, 7),        # KH % sh != 0, 3 channels (tap-product kernel)
+    (11, 7, 9, 9, 1, 3, 3, 1, 1, 0, 0, 4),       # one channel, stride 1, no padding (tap-product kernel)
+    (5, 6, 5, 5, 8, 3, 3, 2, 2, 1, 1, 5),        # KH % sh != 0, 8 channels (row kernel)
 ]
 
 
