@@ -90,8 +90,8 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
         _lib.call("bf_relu_relax_table", _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, B, n_out,
                   _lib.ptr(relax), stream)
     with _timed("crown_relu_relax", 0.0, 4.0 * nz * 2 * M * n_out):
-        _lib.call("bf_crown_relu_relax", _lib.ptr(A_u), _lib.ptr(A_l), B, S, n_out, _lib.ptr(relax), _lib.ptr(add),
-                  add_ld, _lib.ptr(kbias), _lib.ptr(cvec), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u),
+        _lib.call("bf_crown_relu_relax", _lib.ptr(A_u), _lib.ptr(A_l), S * n_out, B, S, n_out, _lib.ptr(relax),
+                  _lib.ptr(add), add_ld, _lib.ptr(kbias), _lib.ptr(cvec), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u),
                   _lib.ptr(rA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), _lib.ptr(c_u), _lib.ptr(c_l), stream)
     taps = KH * KW / float(sh * sw)
     flops = 2.0 * nz * M * n_in * Co * taps

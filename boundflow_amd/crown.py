@@ -390,7 +390,8 @@ def crown_backward(
         if pre_relaxed:
             relax = add = None
             add_ld = 0
-        if save is not None and A_l is not None:
+        if save is not None and A_l is not None and not pre_relaxed:
+            # (a coefficient relaxed by the producing epilogue had its unrelaxed form recorded there)
             save.setdefault("A_in", {})[k] = (A_l, stride)
             save.setdefault("b_in", {})[k] = b_l
         if layer.kind == "conv2d":
@@ -414,6 +415,30 @@ def crown_backward(
             b_l = brow if A_l is not None else None
             stride = 0
             continue
+        if (stride == 0 and relax is not None and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M
+                and (k == 0 or layers[k - 1].kind == "linear")):
+            # A coefficient shared by every domain (the first region of a C = I query):
+            # its relaxation differs per domain, so one bandwidth-bound pass writes it
+            # per domain (with the bias terms and, at the input layer, the center sums)
+            # and the contraction below runs with the plain prologue.
+            cvec0 = trace.input_center_proj.get(layer.out_name) if k == 0 else None
+            rA_u = torch.empty(M, N, device=dev, dtype=torch.float32) if A_u is not None else None
+            rA_l = torch.empty(M, N, device=dev, dtype=torch.float32) if A_l is not None else None
+            rb_u = torch.empty(M, device=dev, dtype=torch.float32) if A_u is not None else None
+            rb_l = torch.empty(M, device=dev, dtype=torch.float32) if A_l is not None else None
+            c_u = torch.empty(M, device=dev, dtype=torch.float32) if (cvec0 is not None and A_u is not None) else None
+            c_l = torch.empty(M, device=dev, dtype=torch.float32) if (cvec0 is not None and A_l is not None) else None
+            nz = int(A_u is not None) + int(A_l is not None)
+            with _timed("crown_relu_relax", 0.0, 4.0 * nz * (S * N + M * N)):
+                _lib.call("bf_crown_relu_relax", _lib.ptr(A_u), _lib.ptr(A_l), 0, B, S, N, _lib.ptr(relax),
+                          _lib.ptr(add), add_ld, _lib.ptr(bias), _lib.ptr(cvec0), _lib.ptr(b_u), _lib.ptr(b_l),
+                          _lib.ptr(rA_u), _lib.ptr(rA_l), _lib.ptr(rb_u), _lib.ptr(rb_l), _lib.ptr(c_u), _lib.ptr(c_l),
+                          stream)
+            A_u, A_l, b_u, b_l = rA_u, rA_l, rb_u, rb_l
+            stride = S * N
+            relax = add = bias = None
+            add_ld = 0
+            pre_relaxed = True
         if k == 0 and pre_relaxed:
             # input layer of an already relaxed coefficient: contraction fused with the concretization
             rad, eps = _input_radius(pert, B, P)
@@ -421,11 +446,20 @@ def crown_backward(
                              dtype=torch.float32)
             lb = torch.empty(B, S, device=dev, dtype=torch.float32) if A_l is not None else None
             ub = torch.empty(B, S, device=dev, dtype=torch.float32) if A_u is not None else None
+            h_scale = h_out = None
+            if save is not None and save.get("grad_rows") is not None:
+                # gradient seed of the concretization: h = -eps * G * sign(A W) (* radius for a box)
+                h_scale = (save["grad_rows"] * (-eps)).contiguous()
+                h_out = torch.empty(M, P, device=dev, dtype=torch.float32)
+                save["h"] = h_out
+                save["cvec"] = trace.input_center_proj.get(layer.out_name)
             nz = int(A_u is not None) + int(A_l is not None)
             with _timed("crown_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
                 _lib.call("bf_crown_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N, _lib.ptr(Wt),
                           P, _lib.ptr(rad), eps, _lib.ptr(c_u), _lib.ptr(c_l), _lib.ptr(b_u), _lib.ptr(b_l),
-                          _lib.ptr(ws), _lib.ptr(lb), _lib.ptr(ub), stream)
+                          _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(ws), _lib.ptr(lb), _lib.ptr(ub), stream)
+            if save is not None:
+                save["final_ws"] = ws
             return IntervalState(lower=lb, upper=ub)
         if k == 0:
             # input layer: relaxation + contraction fused with the concretization
@@ -470,7 +504,7 @@ def crown_backward(
         nz = int(A_u is not None) + int(A_l is not None)
         a_rows = M if stride != 0 else S
         flops, nbytes = 2.0 * nz * M * N * P, 4.0 * nz * (a_rows * N + N * P + M * P)
-        if save is None and layers[k - 1].kind == "linear" and S >= EPILOGUE_MIN_ROWS:
+        if layers[k - 1].kind == "linear" and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M:
             # the next region's relaxation in this contraction's epilogue
             n_alpha, n_alpha_ld, n_add, n_add_ld, _, _, _ = relax_params(k - 1)
             n_table = relax_table(k - 1)
@@ -487,12 +521,17 @@ def crown_backward(
                              dtype=torch.float32)
             nc_u = torch.empty(M, device=dev, dtype=torch.float32) if (cvec is not None and A_u is not None) else None
             nc_l = torch.empty(M, device=dev, dtype=torch.float32) if (cvec is not None and A_l is not None) else None
+            # the gradient pass reads the lower coefficient before the next relaxation
+            pre_l = torch.empty(M, P, device=dev, dtype=torch.float32) if (save is not None and A_l is not None) else None
             with _timed("crown_relu_linear_relu_fwd", flops, nbytes):
                 _lib.call("bf_crown_relu_linear_relu_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
                           _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, _lib.ptr(bias), _lib.ptr(b_u),
                           _lib.ptr(b_l), _lib.ptr(n_table), _lib.ptr(n_add), n_add_ld, _lib.ptr(n_bias),
-                          _lib.ptr(cvec), P, _lib.ptr(ws), _lib.ptr(nA_u), _lib.ptr(nA_l), _lib.ptr(nb_u),
-                          _lib.ptr(nb_l), _lib.ptr(nc_u), _lib.ptr(nc_l), stream)
+                          _lib.ptr(cvec), P, _lib.ptr(ws), _lib.ptr(nA_u), _lib.ptr(nA_l), None, _lib.ptr(pre_l),
+                          _lib.ptr(nb_u), _lib.ptr(nb_l), _lib.ptr(nc_u), _lib.ptr(nc_l), stream)
+            if pre_l is not None:
+                save.setdefault("A_in", {})[k - 1] = (pre_l, S * P)
+                save.setdefault("b_in", {})[k - 1] = nb_l
             c_u, c_l = nc_u, nc_l
             pre_relaxed = True
         else:
@@ -507,10 +546,14 @@ def crown_backward(
     raise RuntimeError("backward did not reach the input layer")
 
 
-# Rows per domain from which the backward relaxes each coefficient in the epilogue
-# of the contraction that produces it: a 128-row tile then spans at most 10 domains,
-# whose relaxation entries fit the kernel's LDS stage.
-EPILOGUE_MIN_ROWS = 15
+# The backward relaxes each coefficient in the epilogue of the contraction that
+# produces it when a domain has at least EPILOGUE_MIN_ROWS rows (a 128-row tile then
+# spans at most 17 domains, whose relaxation entries fit the LDS stage of the
+# library's choice of tile) and the query has at least EPILOGUE_MIN_M rows (below
+# that, the launch-bound query is better served by the fewer launches of the fused
+# prologue).
+EPILOGUE_MIN_ROWS = 8
+EPILOGUE_MIN_M = 8192
 
 
 def _identity_table(B: int, n: int, dev) -> torch.Tensor:

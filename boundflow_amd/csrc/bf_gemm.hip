@@ -70,8 +70,10 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
       // and the plain concretization over a long contraction, on the 16-wave TileH;
       // every other form on the 8-wave TileG.
       if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_tile<TileA>(a, pro, epi, nz, stream);
-      if (pro == PRO_PLAIN && (epi == EPI_RELAX || (epi == EPI_ABSSUM && a.K >= 384)))
-        return launch_tile<TileH>(a, pro, epi, nz, stream);
+      // the relaxation epilogue stages the domains of a 128-row tile in the A stage: up
+      // to 10 on TileG (S >= 15), 18 on TileH (S >= 8)
+      if (epi == EPI_RELAX && (pro == PRO_PLAIN || a.S < 15)) return launch_tile<TileH>(a, pro, epi, nz, stream);
+      if (pro == PRO_PLAIN && epi == EPI_ABSSUM && a.K >= 384) return launch_tile<TileH>(a, pro, epi, nz, stream);
       return launch_tile<TileG>(a, pro, epi, nz, stream);
   }
 }

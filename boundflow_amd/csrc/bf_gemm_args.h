@@ -53,6 +53,7 @@ struct GemmArgs {
   const float* e_cvec;       // optional [D, N], row stride e_cvec_ld
   int64_t e_cvec_ld;
   float* partial_c[2];
+  float* C_pre[2];           // optional: C before the relaxation (same layout as C)
 
   // --- rank-1 term of the store epilogue: C[m, n] = acc + r1_row[m] * r1_col[(m / S) * r1_ld + n] ---
   const float* r1_row;

@@ -46,7 +46,7 @@ constexpr int NORM_BN = 128;
 template <int BM_, int BN_, int BK_, int NWM_, int NWN_, int OCC_>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, NWM = NWM_, NWN = NWN_, OCC = OCC_;
-  static constexpr int NT = 64 * NWM * NWN;          // threads
+  static constexpr int NT = 64 * NWM * NWN;          // threads (OCC: workgroups per CU, see gemm_waves_per_simd)
   static constexpr int WTM = BM / NWM;               // wave tile rows
   static constexpr int WTN = BN / NWN;               // wave tile cols
   static constexpr int FM = WTM / 32;                // 32x32 MFMA blocks per wave (rows)
@@ -75,8 +75,17 @@ __device__ __forceinline__ float fsel(const float4& r, bool lower, bool nonneg, 
   return use_u ? r.x : r.z;
 }
 
+// Occupancy target of an instantiation, in waves per SIMD (the second argument
+// of __launch_bounds__): OCC workgroups per CU for the plain prologue; the
+// relaxation prologue keeps OCC waves per SIMD (a register budget of 512 / OCC),
+// since binding its larger state to the plain kernel's budget spills.
+template <int PRO, class T>
+constexpr int gemm_waves_per_simd() {
+  return (PRO == PRO_PLAIN && T::OCC * T::NT / 256 > T::OCC) ? T::OCC * T::NT / 256 : T::OCC;
+}
+
 template <int PRO, int EPI, bool TRANS_B, class T>
-__global__ void __launch_bounds__(T::NT, T::OCC)
+__global__ void __launch_bounds__(T::NT, (gemm_waves_per_simd<PRO, T>()))
 gemm_kernel(GemmArgs p) {
   constexpr int GBM = T::BM, GBN = T::BN, GBK = T::BK, GNT = T::NT;
   constexpr int AP = T::AP, BPT = T::BPT, A_SLOTS = T::A_SLOTS, B_SLOTS = T::B_SLOTS;
@@ -551,6 +560,7 @@ gemm_kernel(GemmArgs p) {
     }
     __syncthreads();
     float* __restrict__ C = p.C[z];
+    float* __restrict__ Cpre = p.C_pre[z];
     float pb[FM][16], pc[FM][16];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -580,6 +590,7 @@ gemm_kernel(GemmArgs p) {
               if (cv_e) cv = p.e_cvec[d * p.e_cvec_ld + col];
               if (kb_e) kb = p.e_kbias[col];
             }
+            if (Cpre) Cpre[row * p.ldc + col] = a;
             float be;
             float out = a * fsel(e, lower, a >= 0.f, &be);
             if (add_e) out = out + add;
@@ -639,7 +650,7 @@ using TileD = Tile<128, 256, 16, 2, 2, 2>;   // 4 waves of 64x128 (store epilogu
 using TileE = Tile<64, 128, 16, 1, 2, 4>;    // 2 waves of 64x64: more workgroups for short M
 using TileF = Tile<128, 128, 16, 2, 2, 2>;   // TileA at 2 workgroups per CU
 using TileG = Tile<128, 128, 16, 4, 2, 3>;   // 8 waves of 32x64: twice the waves per CU of TileA
-using TileH = Tile<128, 128, 32, 4, 4, 1>;   // 16 waves of 32x32, BK 32
+using TileH = Tile<128, 128, 32, 4, 4, 2>;   // 16 waves of 32x32, BK 32, 2 workgroups per CU (64 VGPRs)
 
 template <int PRO, int EPI, class T>
 static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {

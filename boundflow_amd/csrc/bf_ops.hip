@@ -250,7 +250,8 @@ ibp_batched_linear_kernel(const float* __restrict__ lo, const float* __restrict_
 // reduction of the bias terms.  Writes A' for both bounds and
 //   b_out = (b_in + sum_k A * beta_sel)  [+ sum_k A' * kbias if kbias].
 __global__ void __launch_bounds__(256)
-relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t M, int64_t S, int64_t K,
+relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t a_dstride, int64_t M,
+                       int64_t S, int64_t K,
                        const float4* __restrict__ relax, const float* __restrict__ add_l, int64_t add_ld,
                        const float* __restrict__ kbias, const float* __restrict__ cvec,
                        const float* __restrict__ bu_in, const float* __restrict__ bl_in, float* __restrict__ Au_out,
@@ -260,12 +261,13 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= M) return;
   const int64_t d = m / S;
+  const int64_t a_row = d * a_dstride + (m - d * S) * K;   // input row (shared by all domains when a_dstride = 0)
   float su = 0.f, sl = 0.f, ku = 0.f, kl = 0.f, cu = 0.f, cl = 0.f;
   for (int64_t k = lane; k < K; k += 64) {
     // {alpha_u, beta_u, alpha_l, beta_l}; no table = no ReLU (identity)
     const float4 r = relax ? relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
     if (Au) {
-      float v = Au[m * K + k];
+      float v = Au[a_row + k];
       bool nn = v >= 0.f;
       float o = v * (nn ? r.x : r.z);
       su += v * (nn ? r.y : r.w);
@@ -274,7 +276,7 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
       Au_out[m * K + k] = o;
     }
     if (Al) {
-      float v = Al[m * K + k];
+      float v = Al[a_row + k];
       bool nn = v >= 0.f;
       float o = v * (nn ? r.z : r.x);
       sl += v * (nn ? r.w : r.y);
@@ -308,7 +310,8 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
 // tree (wave shuffles, then the workgroup's waves through LDS when TPR > 64).
 template <int TPR>
 __global__ void __launch_bounds__(256)
-relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t M, int64_t S, int64_t K,
+relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t a_dstride, int64_t M,
+                        int64_t S, int64_t K,
                         const float4* __restrict__ relax, const float* __restrict__ add_l, int64_t add_ld,
                         const float* __restrict__ kbias, const float* __restrict__ cvec,
                         const float* __restrict__ bu_in, const float* __restrict__ bl_in, float* __restrict__ Au_out,
@@ -323,6 +326,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
   float s[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // su, sl, ku, kl, cu, cl
   if (live) {
     const int64_t d = m / S;
+    const int64_t a_row = d * a_dstride + (m - d * S) * K;   // input row (shared by all domains when a_dstride = 0)
     for (int64_t k = 4 * (int64_t)t; k < K; k += 4 * TPR) {
       float4 r[4];
 #pragma unroll
@@ -332,7 +336,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
       const float kbv[4] = {kb.x, kb.y, kb.z, kb.w};
       const float cvv[4] = {cv.x, cv.y, cv.z, cv.w};
       if (Au) {
-        const float4 v4 = *reinterpret_cast<const float4*>(Au + m * K + k);
+        const float4 v4 = *reinterpret_cast<const float4*>(Au + a_row + k);
         const float v[4] = {v4.x, v4.y, v4.z, v4.w};
         float o[4];
 #pragma unroll
@@ -346,7 +350,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
         *reinterpret_cast<float4*>(Au_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
       }
       if (Al) {
-        const float4 v4 = *reinterpret_cast<const float4*>(Al + m * K + k);
+        const float4 v4 = *reinterpret_cast<const float4*>(Al + a_row + k);
         const float v[4] = {v4.x, v4.y, v4.z, v4.w};
         const float4 ad =
             add_l ? *reinterpret_cast<const float4*>(add_l + d * add_ld + k) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -723,8 +727,8 @@ int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_
                                   const float* b_l_in, const float* relax_next, const float* add_next,
                                   int64_t add_next_ld, const float* bias_next, const float* cvec_next,
                                   int64_t cvec_next_ld, float* workspace, float* A_next_u, float* A_next_l,
-                                  float* b_u_out, float* b_l_out, float* c_u_out, float* c_l_out,
-                                  hipStream_t stream) {
+                                  float* A_pre_u, float* A_pre_l, float* b_u_out, float* b_l_out, float* c_u_out,
+                                  float* c_l_out, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0 && N > 0 && P > 0, "bf_crown_relu_linear_relu_fwd: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
@@ -752,6 +756,7 @@ int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_
     if (!Ain) continue;
     a.A[nz] = Ain;
     a.C[nz] = side == 0 ? A_next_u : A_next_l;
+    a.C_pre[nz] = side == 0 ? A_pre_u : A_pre_l;
     a.b_in[nz] = side == 0 ? b_u_in : b_l_in;
     bdst[nz] = side == 0 ? b_u_out : b_l_out;
     a.b_out[nz] = relax_in ? bdst[nz] : nullptr;
@@ -800,7 +805,8 @@ int64_t bf_crown_relu_linear_relu_fwd_workspace(int64_t D, int64_t S, int64_t P)
 int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
                                int64_t N, const float* W_t, int64_t I, const float* rad, float eps,
                                const float* cen_u, const float* cen_l, const float* b_u, const float* b_l,
-                               float* workspace, float* lb, float* ub, hipStream_t stream) {
+                               const float* h_scale, float* h_out, float* workspace, float* lb, float* ub,
+                               hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0 && N > 0 && I > 0, "bf_crown_linear_concretize: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
@@ -831,6 +837,10 @@ int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dst
   a.S = S;
   a.wvec = rad;
   a.w_ld = I;
+  BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || A_l != nullptr),
+             "bf_crown_linear_concretize: h_out needs h_scale and the lower coefficient");
+  a.h_scale = h_scale;
+  a.h_out = h_out;
   int rc = gemm_dispatch(a, PRO_PLAIN, EPI_ABSSUM, nz, stream);
   if (rc) return rc;
   return concretize_finalize(A_u ? pu : nullptr, A_l ? pl : nullptr, nparts, M, cen_u, cen_l, b_u, b_l,
@@ -841,7 +851,8 @@ int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
   return 2 * (int64_t)gemm_partial_count(I) * D * S;
 }
 
-int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* relax,
+int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
+                        const float* relax,
                         const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
                         const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
                         float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
@@ -852,22 +863,23 @@ int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S
   BF_REQUIRE((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr),
              "bf_crown_relu_relax: input/output mismatch");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  const bool vec = (K % 4 == 0) && al16(A_u) && al16(A_l) && al16(A_u_out) && al16(A_l_out) && al16(kbias) &&
+  const bool vec = (K % 4 == 0) && (a_dstride % 4 == 0) && al16(A_u) && al16(A_l) && al16(A_u_out) &&
+                   al16(A_l_out) && al16(kbias) &&
                    al16(cvec) && al16(add_l) && (add_l == nullptr || add_ld % 4 == 0);
   if (vec && K >= 1024) {
-    hipLaunchKernelGGL(relu_relax_rows4_kernel<256>, dim3((unsigned)M), dim3(256), 0, stream, A_u, A_l, M, S, K,
-                       reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
+    hipLaunchKernelGGL(relu_relax_rows4_kernel<256>, dim3((unsigned)M), dim3(256), 0, stream, A_u, A_l, a_dstride, M, S,
+                       K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
                        A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
     BF_LAUNCH_CHECK("relu_relax_rows4_kernel<256>");
   } else if (vec) {
     hipLaunchKernelGGL(relu_relax_rows4_kernel<64>, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l,
-                       M, S, K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in,
-                       A_u_out, A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+                       a_dstride, M, S, K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec,
+                       b_u_in, b_l_in, A_u_out, A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
     BF_LAUNCH_CHECK("relu_relax_rows4_kernel<64>");
   } else {
-    hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l, M, S,
-                       K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
-                       A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+    hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l,
+                       a_dstride, M, S, K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec,
+                       b_u_in, b_l_in, A_u_out, A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
     BF_LAUNCH_CHECK("relu_relax_rows_kernel");
   }
   return BF_OK;

@@ -282,9 +282,9 @@ class HipFusedCrownExecutor:
         kbias = None if bias is None else bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous()
         ru = torch.empty(M, N, device=dev)
         rl = torch.empty(M, N, device=dev)
-        _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), D, S, N, _lib.ptr(table), None,
-                  0, _lib.ptr(kbias), None, None, None, _lib.ptr(ru), _lib.ptr(rl), _lib.ptr(du), _lib.ptr(dl), None,
-                  None, st)
+        _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
+                  _lib.ptr(table), None, 0, _lib.ptr(kbias), None, None, None, _lib.ptr(ru), _lib.ptr(rl), _lib.ptr(du),
+                  _lib.ptr(dl), None, None, st)
         pu = torch.empty(D, S, Ci, Hi, Wi, device=dev)
         pl = torch.empty(D, S, Ci, Hi, Wi, device=dev)
         _lib.call("bf_conv_transpose_rows", _lib.ptr(ru), _lib.ptr(rl), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW, sh, sw,

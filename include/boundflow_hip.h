@@ -144,12 +144,15 @@ int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t 
  *   b_out  = b_in [+ prologue sums] + sum_n (C * beta_sel + A_next * bias_next),
  *   c_out  = sum_n A_next * cvec_next   (only when cvec_next; row stride cvec_next_ld),
  * so the next region reads A_next as it is (relax, add_l and bias NULL) and the
- * input region can be concretized with bf_crown_linear_concretize.  The same
+ * input region can be concretized with bf_crown_linear_concretize.  A_pre_u /
+ * A_pre_l (optional) receive the product before that relaxation (the
+ * coefficient the alpha/beta gradient pass reads).  The same
  * steps as runtime/crown_ibp.py:1073-1090, 1211-1298 applied to two
  * consecutive layers (the reference's dense backward loop, crown_ibp.py:1371-1700).
  * W_t: the layer weight transposed, [P, N] row-major.  relax_next: table of
  * bf_relu_relax_table over the P columns ([D, P]).  Rows of one 128-row tile
- * spanning more than 10 domains (S < 15) read the tables from global memory.
+ * spanning more than its LDS stage holds (10 domains with a relaxation prologue
+ * and S >= 15, else 18) read the tables from global memory.
  * workspace: bf_crown_relu_linear_relu_fwd_workspace(D, S, P) floats. */
 int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
                                   int64_t N, const float* relax, const float* add_l, int64_t add_ld,
@@ -157,8 +160,8 @@ int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_
                                   const float* b_l_in, const float* relax_next, const float* add_next,
                                   int64_t add_next_ld, const float* bias_next, const float* cvec_next,
                                   int64_t cvec_next_ld, float* workspace, float* A_next_u, float* A_next_l,
-                                  float* b_u_out, float* b_l_out, float* c_u_out, float* c_l_out,
-                                  hipStream_t stream);
+                                  float* A_pre_u, float* A_pre_l, float* b_u_out, float* b_l_out, float* c_u_out,
+                                  float* c_l_out, hipStream_t stream);
 int64_t bf_crown_relu_linear_relu_fwd_workspace(int64_t D, int64_t S, int64_t P);
 
 /* Linf / box concretization of an input layer whose coefficient is already
@@ -166,21 +169,26 @@ int64_t bf_crown_relu_linear_relu_fwd_workspace(int64_t D, int64_t S, int64_t P)
  *   lb = (cen_l - eps * sum_i |(A_l W^T)_i| * rad_i) + b_l, ub mirrored,
  * with the center and bias sums given per row.  concretize_affine
  * (runtime/perturbation.py:175-222, 327-359) as called at crown_ibp.py:2044-2051.
+ * h_scale/h_out (optional, lower bound only): the gradient seed
+ * h = h_scale[m] * sign(A_l W^T) * rad, as in bf_crown_relu_linear_concretize.
  * workspace: bf_crown_linear_concretize_workspace(D, S, I) floats. */
 int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
                                int64_t N, const float* W_t, int64_t I, const float* rad, float eps,
                                const float* cen_u, const float* cen_l, const float* b_u, const float* b_l,
-                               float* workspace, float* lb, float* ub, hipStream_t stream);
+                               const float* h_scale, float* h_out, float* workspace, float* lb, float* ub,
+                               hipStream_t stream);
 int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I);
 
 /* Standalone relaxation pass (bandwidth-bound form of kernel #3): writes A'
- * and the bias/center row sums, one wave64 per row.  Replaces
+ * [D*S, K] and the bias/center row sums.  Replaces
  * _backprop_relu_step_dense_reference (runtime/crown_ibp.py:1211-1298); used
- * ahead of the conv transposed contraction.  relax: table of
- * bf_relu_relax_table (NULL = identity); kbias: per-element bias of the affine
- * layer [K]; cvec: center projection [D, K] (optional). */
-int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t K, const float* relax,
-                        const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+ * ahead of the conv transposed contraction, and to materialize per domain the
+ * relaxation of a coefficient shared by all domains.  A rows: A + d*a_dstride +
+ * s*K (a_dstride = S*K, or 0 when every domain shares the same S rows).  relax:
+ * table of bf_relu_relax_table (NULL = identity); kbias: per-element bias of the
+ * affine layer [K]; cvec: center projection [D, K] (optional). */
+int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
+                        const float* relax, const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
                         const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
                         float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream);
 

@@ -147,10 +147,15 @@ def _grad_close(got, ref32, ref64, what, allowance=None):
     assert bool((err <= base + extra).all()), what
 
 
-@pytest.mark.parametrize("case", ["mlp_beta", "cnn_alpha"])
-def test_lower_bound_gradients_match_autograd(case):
+# mlp_beta_epilogue: the MLP regions relaxed in the producing contraction's epilogue (the path
+# large queries take), which also stores the unrelaxed coefficient the gradient pass reads
+@pytest.mark.parametrize("case", ["mlp_beta", "mlp_beta_epilogue", "cnn_alpha"])
+def test_lower_bound_gradients_match_autograd(case, monkeypatch):
     dev = device()
     announce(f"alpha/beta gradient pass vs autograd: {case}")
+    if case == "mlp_beta_epilogue":
+        monkeypatch.setattr(hc, "EPILOGUE_MIN_M", 0)
+        case = "mlp_beta"
     g = torch.Generator().manual_seed(21)
     if case == "mlp_beta":
         w = wl.subset(wl.make_c5(eps=0.004, depth=2, label_mode="predicted"), 12)
@@ -220,13 +225,18 @@ def test_shared_alpha_crown_matches_reference():
     assert_bounds_close(bounds.upper, t(gz["upper"]), "shared upper", rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("epilogue", [False, True])
 @pytest.mark.parametrize("tag,maker", [
     ("bab_c5_d256", lambda: wl.subset(wl.make_c5(), 256)),
     ("bab_c5d2_mixed", lambda: wl.subset(wl.make_c5(eps=0.004, depth=2, label_mode="predicted"), 256)),
 ])
-def test_bab_domain_batch_matches_reference(tag, maker):
+def test_bab_domain_batch_matches_reference(tag, maker, epilogue, monkeypatch):
+    """epilogue: every MLP region relaxed in the producing contraction's epilogue (the
+    path of batches of at least EPILOGUE_MIN_M rows), at this fixture's size."""
     dev = device()
-    announce(f"BaB domain batch {tag}")
+    if epilogue:
+        monkeypatch.setattr(hc, "EPILOGUE_MIN_M", 0)
+    announce(f"BaB domain batch {tag} epilogue={epilogue}")
     gz = load(tag)
     w = maker()
     wd = wl.to_device(w, dev)

@@ -98,11 +98,14 @@ def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec):
     bo_u, bo_l = torch.empty(M, device=dev), torch.empty(M, device=dev)
     co_u = torch.empty(M, device=dev) if cvec else None
     co_l = torch.empty(M, device=dev) if cvec else None
+    Pre_u = torch.empty(M, P, device=dev) if alpha else None   # the product before the relaxation (optional)
+    Pre_l = torch.empty(M, P, device=dev) if alpha else None
     _lib.call("bf_crown_relu_linear_relu_fwd", _lib.ptr(Au_d), _lib.ptr(Al_d), S * N, D, S, N, _lib.ptr(t1),
               _lib.ptr(add1_d if prologue else None), N, _lib.ptr(Wt_d), P,
               _lib.ptr(bias1_d if prologue else None), _lib.ptr(bu_d), _lib.ptr(bl_d), _lib.ptr(t2),
               _lib.ptr(add2_d), P, _lib.ptr(bias2_d), _lib.ptr(cv_d), P, _lib.ptr(ws), _lib.ptr(An_u),
-              _lib.ptr(An_l), _lib.ptr(bo_u), _lib.ptr(bo_l), _lib.ptr(co_u), _lib.ptr(co_l), _lib.stream_handle())
+              _lib.ptr(An_l), _lib.ptr(Pre_u), _lib.ptr(Pre_l), _lib.ptr(bo_u), _lib.ptr(bo_l), _lib.ptr(co_u),
+              _lib.ptr(co_l), _lib.stream_handle())
     torch.cuda.synchronize()
 
     # fp32 accumulation bounds: contraction over N (and the prologue's sums), then the row sums over P
@@ -121,6 +124,10 @@ def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec):
         tol = (N + P) * 2.0 ** -22 * sc
         announce(f"  {what}: max abs err {float(err.max()):.3e}")
         assert bool((err <= tol).all()), f"{what}: {float((err / tol).max()):.3f} x tolerance"
+    if alpha:
+        for got, ref, what in ((Pre_u, Cu, "pre-relaxation upper"), (Pre_l, Cl, "pre-relaxation lower")):
+            err = (got.cpu().double().reshape(D, S, P) - ref).abs()
+            assert bool((err <= tolC).all()), f"{what}: {float((err / tolC).max()):.3f} x tolerance"
     if cvec:
         for got, C2, what in ((co_u, Cu2, "center upper"), (co_l, Cl2, "center lower")):
             ref = (C2 * f(cv)[:, None, :]).sum(-1)
@@ -156,16 +163,19 @@ def _with_spec(w, spec, C):
     return wl.Workload(w.name, w.module, spec, C, w.labels, {})
 
 
-@pytest.mark.parametrize("box", [False, True])
-def test_crown_query_on_epilogue_path_matches_oracle(box):
+@pytest.mark.parametrize("box,shared", [(False, False), (True, False), (False, True)])
+def test_crown_query_on_epilogue_path_matches_oracle(box, shared, monkeypatch):
     """A CROWN query with 20 spec rows per domain (the epilogue path at every hidden
-    layer), alpha slopes and beta split coefficients on every ReLU."""
+    layer), alpha slopes and beta split coefficients on every ReLU.  shared: one
+    [20, 10] spec matrix for every domain, whose first relaxation is materialized
+    per domain by the relaxation pass before the plain contraction."""
     dev = device()
-    announce(f"CROWN query on the relaxation-epilogue path, box={box}")
+    monkeypatch.setattr(hc, "EPILOGUE_MIN_M", 0)   # the epilogue path at this small size
+    announce(f"CROWN query on the relaxation-epilogue path, box={box} shared={shared}")
     B, S = 12, 20
     w = wl.make_c2(batch=B, width=200, depth=4)
     g = torch.Generator().manual_seed(17)
-    C = torch.randn(B, S, 10, generator=g)
+    C = torch.randn(S, 10, generator=g) if shared else torch.randn(B, S, 10, generator=g)
     x = w.spec.center
     if box:
         spec = InputSpec.box(value_name="input", lower=(x - 0.02).clamp(0, 1), upper=(x + 0.02).clamp(0, 1))

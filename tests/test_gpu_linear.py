@@ -167,9 +167,14 @@ def test_infeasible_split_raises_and_flags():
         hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state=split)
 
 
-def test_all_intermediate_c2_matches_reference():
+# epilogue: the regions relaxed in the producing contraction's epilogue, the path of C2
+# at full size (at least EPILOGUE_MIN_M rows), taken here at the fixture's size
+@pytest.mark.parametrize("epilogue", [False, True])
+def test_all_intermediate_c2_matches_reference(epilogue, monkeypatch):
     dev = device()
-    announce("C2 all-intermediate CROWN, B=4")
+    if epilogue:
+        monkeypatch.setattr(hc, "EPILOGUE_MIN_M", 0)
+    announce(f"C2 all-intermediate CROWN, B=4, epilogue={epilogue}")
     gz = load("crown_c2_allint_b4")
     w = wl.subset(wl.make_c2(), 4)
     wd = wl.to_device(w, dev)
@@ -181,6 +186,49 @@ def test_all_intermediate_c2_matches_reference():
     ref64, _ = cr.run_crown_all_intermediate(w64.module, w64.spec, linear_spec_C=w64.C)
     assert_parity(final.lower, t(gz["lower"]), ref64.lower, "C2 lower")
     assert_parity(final.upper, t(gz["upper"]), ref64.upper, "C2 upper")
+
+
+@pytest.mark.parametrize("K", [132, 133])
+def test_relax_pass_of_shared_coefficient(K):
+    """bf_crown_relu_relax with a_dstride = 0: one [S, K] coefficient shared by every
+    domain, relaxed per domain into [D*S, K] (the first region of a C = I query)."""
+    dev = device()
+    announce(f"relax pass of a shared coefficient K={K}")
+    g = torch.Generator().manual_seed(K)
+    D, S = 6, 17
+    A = torch.randn(S, K, generator=g)
+    l = torch.randn(D, K, generator=g)
+    u = l + torch.rand(D, K, generator=g)
+    alpha = torch.rand(D, K, generator=g)
+    kb = torch.randn(K, generator=g)
+    b = torch.randn(D, S, generator=g)
+    Ab = A.expand(D, S, K)
+    ref = cr.relu_backward_dense(Ab, Ab, b, b, pre=cr.IntervalState(l, u), name="h", relu_alpha={"h": alpha})
+    # bias sums in float64, with the fp32 summation bound K * 2^-22 * sum |terms| as tolerance
+    f = lambda x: x.double()
+    r64 = cr.relu_backward_dense(f(Ab), f(Ab), f(b), f(b), pre=cr.IntervalState(f(l), f(u)), name="h",
+                                 relu_alpha={"h": f(alpha)})
+    ref_bu, ref_bl = r64[2] + r64[0] @ f(kb), r64[3] + r64[1] @ f(kb)
+    # |beta_sel| <= max(|l|, |u|): bound of the summed terms A * beta_sel and A' * kbias, plus the input bias
+    scale = ((f(Ab).abs() * torch.maximum(f(l).abs(), f(u).abs())[:, None, :]).sum(-1)
+             + torch.maximum(r64[0].abs(), r64[1].abs()) @ f(kb).abs() + f(b).abs())
+    d = [x.to(dev).contiguous() for x in (A, l, u, alpha, kb, b)]
+    table = torch.empty(D, K, 4, device=dev)
+    _lib.call("bf_relu_relax_table", _lib.ptr(d[1]), _lib.ptr(d[2]), _lib.ptr(d[3]), K, D, K, _lib.ptr(table),
+              _lib.stream_handle())
+    out = [torch.empty(D * S, K, device=dev), torch.empty(D * S, K, device=dev), torch.empty(D * S, device=dev),
+           torch.empty(D * S, device=dev)]
+    _lib.call("bf_crown_relu_relax", _lib.ptr(d[0]), _lib.ptr(d[0]), 0, D, S, K, _lib.ptr(table), None, 0,
+              _lib.ptr(d[4]), None, _lib.ptr(d[5]), _lib.ptr(d[5]), _lib.ptr(out[0]), _lib.ptr(out[1]),
+              _lib.ptr(out[2]), _lib.ptr(out[3]), None, None, _lib.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(out[0].cpu().reshape(D, S, K), ref[0])
+    assert torch.equal(out[1].cpu().reshape(D, S, K), ref[1])
+    for got, ref_b, what in ((out[2], ref_bu, "b_u"), (out[3], ref_bl, "b_l")):
+        err = (got.cpu().double().reshape(D, S) - ref_b).abs()
+        tol = 2 * K * 2.0 ** -23 * scale
+        announce(f"  shared relax {what}: max abs err {float(err.max()):.3e}")
+        assert bool((err <= tol).all()), f"{what}: {float((err / tol).max()):.3f} x tolerance"
 
 
 # K = 133: scalar kernel (K % 4 != 0); 132: float4 kernel, a wave per row; 2048: float4, a workgroup per row
@@ -209,7 +257,7 @@ def test_relax_pass_and_dense_concretize_match_oracle(K):
     table = torch.empty(D, K, 4, device=dev)
     _lib.call("bf_relu_relax_table", _lib.ptr(d[2]), _lib.ptr(d[3]), _lib.ptr(d[4]), K, D, K, _lib.ptr(table),
               _lib.stream_handle())
-    _lib.call("bf_crown_relu_relax", _lib.ptr(d[0]), _lib.ptr(d[1]), D, S, K, _lib.ptr(table), _lib.ptr(d[5]), K,
+    _lib.call("bf_crown_relu_relax", _lib.ptr(d[0]), _lib.ptr(d[1]), S * K, D, S, K, _lib.ptr(table), _lib.ptr(d[5]), K,
               None, None, _lib.ptr(d[6]), _lib.ptr(d[7]), _lib.ptr(out[0]), _lib.ptr(out[1]), _lib.ptr(out[2]),
               _lib.ptr(out[3]), None, None, _lib.stream_handle())
     torch.cuda.synchronize()
