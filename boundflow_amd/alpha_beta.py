@@ -7,9 +7,10 @@ solver uses (boundflow/runtime/bab.py:134-153):
 
 * one forward IBP trace (split-aware), branch choices from it
   (alpha_beta_crown.py:145-182);
-* ``steps + 1`` bound evaluations; each runs the fused CROWN backward for both
-  bounds and keeps the lower-bound coefficients needed by the gradient;
-* best-of tracking per domain (per_batch_params) or globally;
+* ``steps + 1`` evaluations of the lower bound (the fused CROWN backward keeps
+  the coefficients the gradient needs);
+* best-of tracking per domain (per_batch_params) or globally, then one upper
+  bound evaluation with the best parameters;
 * between evaluations, the analytic reverse pass of the lower bound (the
   gradient autograd computes in the reference): fused concretization seed ->
   transposed contractions with rank-1 bias terms -> per-ReLU gradient kernels
@@ -268,7 +269,6 @@ def run_alpha_beta_crown_mlp(
     adam_b = {n: _Adam(beta[n]) for n in names}
     best_metric = torch.empty(B, device=dev)
     best_lb = torch.empty(B, S, device=dev)
-    best_ub = torch.empty(B, S, device=dev)
     improved = torch.empty(B, dtype=torch.int32, device=dev)
     best_alpha = {n: alpha[n].clone() for n in names}
     best_beta = {n: beta[n].clone() for n in names}
@@ -280,12 +280,13 @@ def run_alpha_beta_crown_mlp(
             _lib.call("bf_beta_coeff", _lib.ptr(beta[n]), p_ld[n], _lib.ptr(s), sld, B, numel[n], _lib.ptr(add[n]),
                       stream)
         saved = {"grad_rows": G} if step < int(steps) else None
+        # lower bound only: the objective and the best-of rule read nothing else
         bounds = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C,
                                 relu_alpha={n: alpha[n] for n in names},
-                                relu_pre_add_coeff_l={n: add[n] for n in beta_names}, save=saved)
+                                relu_pre_add_coeff_l={n: add[n] for n in beta_names}, need_upper=False, save=saved)
         if per_batch_params:
-            _lib.call("bf_best_update", _lib.ptr(bounds.lower), _lib.ptr(bounds.upper), B, S, _lib.ptr(best_metric),
-                      _lib.ptr(best_lb), _lib.ptr(best_ub), _lib.ptr(improved), 1 if step == 0 else 0, stream)
+            _lib.call("bf_best_update", _lib.ptr(bounds.lower), None, B, S, _lib.ptr(best_metric),
+                      _lib.ptr(best_lb), None, _lib.ptr(improved), 1 if step == 0 else 0, stream)
             for n in names:
                 _lib.call("bf_masked_copy_rows", _lib.ptr(best_alpha[n]), _lib.ptr(alpha[n]), B, numel[n],
                           _lib.ptr(improved), stream)
@@ -296,7 +297,6 @@ def run_alpha_beta_crown_mlp(
             if best_scalar is None or metric > best_scalar:
                 best_scalar = metric
                 best_lb.copy_(bounds.lower)
-                best_ub.copy_(bounds.upper)
                 for n in names:
                     best_alpha[n].copy_(alpha[n])
                     best_beta[n].copy_(beta[n])
@@ -315,6 +315,12 @@ def run_alpha_beta_crown_mlp(
             adam_a[n].step(ga, lr, 0.0, 1.0, stream)
             if n in beta_names:
                 adam_b[n].step(gb, lr, 0.0, None, stream)
+    # The reference keeps the upper bound of the evaluation that gave the best lower
+    # bound.  The upper bound depends on alpha alone (beta enters the lower bound
+    # only) and every domain's rows on that domain's parameters alone, so one upper
+    # pass with the best parameters reproduces it.
+    best_ub = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C,
+                             relu_alpha={n: best_alpha[n] for n in names}, need_lower=False).upper
     out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
     out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
     stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,

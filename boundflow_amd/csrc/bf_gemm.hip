@@ -63,18 +63,16 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
     case 5: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileF>(a, pro, epi, nz, stream);
     case 6: return launch_tile<TileG>(a, pro, epi, nz, stream);
     case 7: return launch_tile<TileH>(a, pro, epi, nz, stream);
-    default:
-      // automatic (measured per form on the C2 and C5 shapes): the fused relaxation
-      // + concretization on TileA (its LDS slices keep the 8- and 16-wave tiles at
-      // fewer workgroups per CU); the plain prologue with the relaxation epilogue,
-      // and the plain concretization over a long contraction, on the 16-wave TileH;
-      // every other form on the 8-wave TileG.
-      if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_tile<TileA>(a, pro, epi, nz, stream);
-      // the relaxation epilogue stages the domains of a 128-row tile in the A stage: up
-      // to 10 on TileG (S >= 15), 18 on TileH (S >= 8)
-      if (epi == EPI_RELAX && (pro == PRO_PLAIN || a.S < 15)) return launch_tile<TileH>(a, pro, epi, nz, stream);
-      if (pro == PRO_PLAIN && epi == EPI_ABSSUM && a.K >= 384) return launch_tile<TileH>(a, pro, epi, nz, stream);
+    default: {
+      // automatic (measured on the five benchmark shapes): the 8-wave TileG at 3
+      // workgroups per CU for every form; a grid with fewer 128 x 128 tiles than the
+      // device has CUs takes the 16-wave TileH instead, which spreads each tile's
+      // contraction over twice the waves.
+      const int64_t ks = (pro == PRO_PLAIN && epi == EPI_STORE && a.ksplit > 1) ? a.ksplit : 1;
+      const int64_t wgs = ceil_div(a.M, 128) * ceil_div(a.N, 128) * nz * ks;
+      if (wgs < 256) return launch_tile<TileH>(a, pro, epi, nz, stream);
       return launch_tile<TileG>(a, pro, epi, nz, stream);
+    }
   }
 }
 

@@ -80,10 +80,9 @@ __global__ void best_update_kernel(const float* __restrict__ lb, const float* __
   improved[d] = take ? 1 : 0;
   if (take) {
     best_metric[d] = metric;
-    for (int64_t s = 0; s < S; ++s) {
-      best_lb[d * S + s] = lb[d * S + s];
-      best_ub[d * S + s] = ub[d * S + s];
-    }
+    for (int64_t s = 0; s < S; ++s) best_lb[d * S + s] = lb[d * S + s];
+    if (ub)
+      for (int64_t s = 0; s < S; ++s) best_ub[d * S + s] = ub[d * S + s];
   }
 }
 
@@ -170,7 +169,8 @@ int bf_best_update(const float* lb, const float* ub, int64_t D, int64_t S, float
                    float* best_ub, int* improved, int first, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0, "bf_best_update: bad sizes");
   if (D == 0) return BF_OK;
-  BF_REQUIRE(lb && ub && best_metric && best_lb && best_ub && improved, "bf_best_update: null pointer");
+  BF_REQUIRE(lb && best_metric && best_lb && improved, "bf_best_update: null pointer");
+  BF_REQUIRE((ub == nullptr) == (best_ub == nullptr), "bf_best_update: ub and best_ub must both be given or both be null");
   hipLaunchKernelGGL(best_update_kernel, dim3((unsigned)ceil_div(D, 256)), dim3(256), 0, stream, lb, ub, D, S,
                      best_metric, best_lb, best_ub, improved, first);
   BF_LAUNCH_CHECK("best_update_kernel");

@@ -19,8 +19,17 @@ _active: Optional["LaunchTimer"] = None
 
 
 class LaunchTimer:
-    def __init__(self) -> None:
+    """``spin_cycles`` > 0 queues a bounded spin kernel (``torch.cuda._sleep``)
+    ahead of each timed launch.  A launch-bound sequence issued from Python
+    leaves the device idle between launches, and a start event recorded on an
+    idle stream completes before its kernel is even submitted; the spin holds
+    the device while the host records the start event and submits the kernel,
+    so the two events bracket the kernel's execution.  Only for timing runs
+    whose wall time is not measured."""
+
+    def __init__(self, spin_cycles: int = 0) -> None:
         self.records: List[Tuple[str, float, float, torch.cuda.Event, torch.cuda.Event]] = []
+        self.spin_cycles = int(spin_cycles)
 
     def summary(self) -> Dict[str, Dict[str, float]]:
         torch.cuda.synchronize()
@@ -77,6 +86,8 @@ def launch(name: str, flops: float, nbytes: float):
 
 def begin_call() -> None:
     if _pending is not None and _pending[3] is None:
+        if _active is not None and _active.spin_cycles > 0:
+            torch.cuda._sleep(_active.spin_cycles)
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
         _pending[3] = ev
@@ -87,6 +98,19 @@ def end_call() -> None:
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
         _pending[4] = ev
+
+
+def spin_cycles(ms: float) -> int:
+    """Cycle count of a ``torch.cuda._sleep`` spin of about ``ms`` milliseconds on
+    the current device (calibrated with events)."""
+    probe = 1 << 20
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    torch.cuda._sleep(probe)
+    e.record()
+    e.synchronize()
+    return max(1, int(probe / max(s.elapsed_time(e), 1e-3) * ms))
 
 
 def summarize_rocpd(db_path: str, top: int = 12) -> str:

@@ -262,7 +262,9 @@ int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, 
                        double beta2, float eps, int step, float clamp_lo, float clamp_hi, int has_clamp_hi,
                        hipStream_t stream);
 
-/* Per-domain best-of tracking on mean_s lb (runtime/alpha_beta_crown.py:840-876). */
+/* Per-domain best-of tracking on mean_s lb (runtime/alpha_beta_crown.py:840-876).  ub and best_ub may
+ * both be NULL: the lower bounds alone are tracked (the caller then evaluates the upper bound once, with
+ * the best parameters). */
 int bf_best_update(const float* lb, const float* ub, int64_t D, int64_t S, float* best_metric, float* best_lb,
                    float* best_ub, int* improved, int first, hipStream_t stream);
 int bf_masked_copy_rows(float* dst, const float* src, int64_t D, int64_t N, const int* mask, hipStream_t stream);
