@@ -251,11 +251,17 @@ gemm_kernel(GemmArgs p) {
   // options so that the loop body carries no branches on them.  FAST: operands
   // from the LDS slices; ADD: beta split term; KB: affine bias; RR: row sums
   // (first column tile only); the center sums follow EPI == EPI_ABSSUM.
-  auto main_loop = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c) {
+  // FULL: every 32-column MFMA block of this wave lies inside N; otherwise the
+  // blocks past N (the last column tile of a ragged N) skip their MFMAs.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int64_t wcol0 = n0 + (int64_t)(wave_u % T::NWN) * T::WTN;
+  const int fn_act = wcol0 >= N ? 0 : (int)(ceil_div(N - wcol0, 32) < FN ? ceil_div(N - wcol0, 32) : FN);
+  auto main_loop = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c, auto full_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     constexpr bool ADD = decltype(add_c)::value;
     constexpr bool KB = decltype(kb_c)::value;
     constexpr bool RR = decltype(rr_c)::value;
+    constexpr bool FULL = decltype(full_c)::value;
     constexpr bool CV = (EPI == EPI_ABSSUM);
     float4 tab_reg = make_float4(1.f, 0.f, 1.f, 0.f);
     float add_reg = 0.f, kb_reg = 0.f, cv_reg = 0.f;
@@ -376,7 +382,8 @@ gemm_kernel(GemmArgs p) {
           for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int jj = 0; jj < FN; ++jj)
-              acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
+              if (FULL || jj < fn_act)
+                acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
       }
     };
 
@@ -408,17 +415,22 @@ gemm_kernel(GemmArgs p) {
 
   using TT = std::true_type;
   using FF = std::false_type;
+  const bool full = fn_act == FN;   // wave-uniform
+  auto run = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c) {
+    if (full) main_loop(fast_c, add_c, kb_c, rr_c, TT{});
+    else main_loop(fast_c, add_c, kb_c, rr_c, FF{});
+  };
   if constexpr (PRO == PRO_PLAIN) {
-    main_loop(FF{}, FF{}, FF{}, FF{});
+    run(FF{}, FF{}, FF{}, FF{});
   } else {
     const bool kb = p.kbias != nullptr;
-    if (!tab_lds) main_loop(FF{}, FF{}, FF{}, FF{});
+    if (!tab_lds) run(FF{}, FF{}, FF{}, FF{});
     else if (row_reduce) {
-      if (use_add) { if (kb) main_loop(TT{}, TT{}, TT{}, TT{}); else main_loop(TT{}, TT{}, FF{}, TT{}); }
-      else { if (kb) main_loop(TT{}, FF{}, TT{}, TT{}); else main_loop(TT{}, FF{}, FF{}, TT{}); }
+      if (use_add) { if (kb) run(TT{}, TT{}, TT{}, TT{}); else run(TT{}, TT{}, FF{}, TT{}); }
+      else { if (kb) run(TT{}, FF{}, TT{}, TT{}); else run(TT{}, FF{}, FF{}, TT{}); }
     } else {
-      if (use_add) main_loop(TT{}, TT{}, FF{}, FF{});
-      else main_loop(TT{}, FF{}, FF{}, FF{});
+      if (use_add) run(TT{}, TT{}, FF{}, FF{});
+      else run(TT{}, FF{}, FF{}, FF{});
     }
   }
 
