@@ -5,7 +5,7 @@
   (boundflow/domains/interval.py:57-74) after ``bounding_box`` for the input
   layer (boundflow/runtime/crown_ibp.py:167-181).
 * ``conv_backward_step`` -- one ReLU -> Conv2d region of the CROWN backward:
-  the relaxation pass (``bf_crown_relu_relax``, with the conv bias map and, on
+  the relaxation pass (``bf_crown_relu_relax_lu``, with the conv bias map and, on
   the input layer, the center projection reduced in the same pass), then the
   transposed convolution (``bf_conv_transpose_rows``,
   boundflow/runtime/linear_operator.py:1067-1092), fused with the Linf / box
@@ -84,15 +84,11 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
     c_u = torch.empty(M, device=dev) if (A_u is not None and cvec is not None) else None
     c_l = torch.empty(M, device=dev) if (A_l is not None and cvec is not None) else None
     nz = int(A_u is not None) + int(A_l is not None)
-    relax = None
-    if pre_lo is not None:
-        relax = torch.empty(B, n_out, 4, device=dev, dtype=torch.float32)
-        _lib.call("bf_relu_relax_table", _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, B, n_out,
-                  _lib.ptr(relax), stream)
     with _timed("crown_relu_relax", 0.0, 4.0 * nz * 2 * M * n_out):
-        _lib.call("bf_crown_relu_relax", _lib.ptr(A_u), _lib.ptr(A_l), S * n_out, B, S, n_out, _lib.ptr(relax),
-                  _lib.ptr(add), add_ld, _lib.ptr(kbias), _lib.ptr(cvec), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u),
-                  _lib.ptr(rA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), _lib.ptr(c_u), _lib.ptr(c_l), stream)
+        _lib.call("bf_crown_relu_relax_lu", _lib.ptr(A_u), _lib.ptr(A_l), S * n_out, B, S, n_out, _lib.ptr(pre_lo),
+                  _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld, _lib.ptr(kbias), _lib.ptr(cvec),
+                  _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u), _lib.ptr(rA_l), _lib.ptr(nb_u), _lib.ptr(nb_l),
+                  _lib.ptr(c_u), _lib.ptr(c_l), stream)
     taps = KH * KW / float(sh * sw)
     flops = 2.0 * nz * M * n_in * Co * taps
     if not is_first:

@@ -386,9 +386,10 @@ def crown_backward(
     for k in range(len(layers) - 1, -1, -1):
         layer = layers[k]
         alpha, alpha_ld, add, add_ld, pre_lo, pre_hi, N = relax_params(k)
-        relax = relax_table(k)
+        # the relaxation of this region is still to apply (its table is built on first use)
+        relaxes = pre_lo is not None and layer.kind == "linear" and not pre_relaxed
         if pre_relaxed:
-            relax = add = None
+            add = None
             add_ld = 0
         if save is not None and A_l is not None and not pre_relaxed:
             # (a coefficient relaxed by the producing epilogue had its unrelaxed form recorded there)
@@ -415,7 +416,7 @@ def crown_backward(
             b_l = brow if A_l is not None else None
             stride = 0
             continue
-        if (stride == 0 and relax is not None and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M
+        if (stride == 0 and relaxes and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M
                 and (k == 0 or layers[k - 1].kind == "linear")):
             # A coefficient shared by every domain (the first region of a C = I query):
             # its relaxation differs per domain, so one bandwidth-bound pass writes it
@@ -430,15 +431,17 @@ def crown_backward(
             c_l = torch.empty(M, device=dev, dtype=torch.float32) if (cvec0 is not None and A_l is not None) else None
             nz = int(A_u is not None) + int(A_l is not None)
             with _timed("crown_relu_relax", 0.0, 4.0 * nz * (S * N + M * N)):
-                _lib.call("bf_crown_relu_relax", _lib.ptr(A_u), _lib.ptr(A_l), 0, B, S, N, _lib.ptr(relax),
-                          _lib.ptr(add), add_ld, _lib.ptr(bias), _lib.ptr(cvec0), _lib.ptr(b_u), _lib.ptr(b_l),
-                          _lib.ptr(rA_u), _lib.ptr(rA_l), _lib.ptr(rb_u), _lib.ptr(rb_l), _lib.ptr(c_u), _lib.ptr(c_l),
-                          stream)
+                _lib.call("bf_crown_relu_relax_lu", _lib.ptr(A_u), _lib.ptr(A_l), 0, B, S, N, _lib.ptr(pre_lo),
+                          _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld, _lib.ptr(bias),
+                          _lib.ptr(cvec0), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u), _lib.ptr(rA_l),
+                          _lib.ptr(rb_u), _lib.ptr(rb_l), _lib.ptr(c_u), _lib.ptr(c_l), stream)
             A_u, A_l, b_u, b_l = rA_u, rA_l, rb_u, rb_l
             stride = S * N
-            relax = add = bias = None
+            add = bias = None
             add_ld = 0
+            relaxes = False
             pre_relaxed = True
+        relax = relax_table(k) if relaxes else None
         if k == 0 and pre_relaxed:
             # input layer of an already relaxed coefficient: contraction fused with the concretization
             rad, eps = _input_radius(pert, B, P)

@@ -245,6 +245,53 @@ ibp_batched_linear_kernel(const float* __restrict__ lo, const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Where a relaxation pass reads the slopes/intercepts {alpha_u, beta_u, alpha_l,
+// beta_l} of (domain d, neuron k): a table of bf_relu_relax_table, or computed in
+// place from the pre-activation box [lo, hi] and the optional lower-slope
+// override with the table kernel's own arithmetic (relu_relax), which reads 8-12
+// contiguous bytes per neuron instead of a 16-byte entry.  Neither: identity.
+struct RelaxSrc {
+  const float4* table;   // [D, K]
+  const float* lo;       // [D, K]
+  const float* hi;
+  const float* alpha;    // [D, K] (alpha_ld K) or shared (alpha_ld 0)
+  int64_t alpha_ld;
+
+  __device__ __forceinline__ float4 at(int64_t d, int64_t K, int64_t k) const {
+    if (table) return table[d * K + k];
+    if (!lo) return make_float4(1.f, 0.f, 1.f, 0.f);
+    const bool has_alpha = alpha != nullptr;
+    const Relax r = relu_relax(lo[d * K + k], hi[d * K + k], has_alpha,
+                               has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f);
+    return make_float4(r.au, r.bu, r.al, r.bl);
+  }
+
+  // entries of k .. k + 3 (16-byte aligned operands)
+  __device__ __forceinline__ void quad(int64_t d, int64_t K, int64_t k, float4 (&e)[4]) const {
+    if (table) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) e[q] = table[d * K + k + q];
+      return;
+    }
+    if (!lo) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) e[q] = make_float4(1.f, 0.f, 1.f, 0.f);
+      return;
+    }
+    const float4 l4 = *reinterpret_cast<const float4*>(lo + d * K + k);
+    const float4 u4 = *reinterpret_cast<const float4*>(hi + d * K + k);
+    const bool has_alpha = alpha != nullptr;
+    const float4 a4 = has_alpha ? *reinterpret_cast<const float4*>(alpha + d * alpha_ld + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, uv[4] = {u4.x, u4.y, u4.z, u4.w}, av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const Relax r = relu_relax(lv[q], uv[q], has_alpha, has_alpha ? clamp01(av[q]) : 0.f);
+      e[q] = make_float4(r.au, r.bu, r.al, r.bl);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Standalone ReLU relaxation pass (north-star kernel #3 in its unfused form):
 // one wave64 per coefficient row, float loads strided by 64 lanes, wave
 // reduction of the bias terms.  Writes A' for both bounds and
@@ -252,7 +299,7 @@ ibp_batched_linear_kernel(const float* __restrict__ lo, const float* __restrict_
 __global__ void __launch_bounds__(256)
 relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t a_dstride, int64_t M,
                        int64_t S, int64_t K,
-                       const float4* __restrict__ relax, const float* __restrict__ add_l, int64_t add_ld,
+                       RelaxSrc relax, const float* __restrict__ add_l, int64_t add_ld,
                        const float* __restrict__ kbias, const float* __restrict__ cvec,
                        const float* __restrict__ bu_in, const float* __restrict__ bl_in, float* __restrict__ Au_out,
                        float* __restrict__ Al_out, float* __restrict__ bu_out, float* __restrict__ bl_out,
@@ -264,8 +311,8 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
   const int64_t a_row = d * a_dstride + (m - d * S) * K;   // input row (shared by all domains when a_dstride = 0)
   float su = 0.f, sl = 0.f, ku = 0.f, kl = 0.f, cu = 0.f, cl = 0.f;
   for (int64_t k = lane; k < K; k += 64) {
-    // {alpha_u, beta_u, alpha_l, beta_l}; no table = no ReLU (identity)
-    const float4 r = relax ? relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
+    // {alpha_u, beta_u, alpha_l, beta_l}; no source = no ReLU (identity)
+    const float4 r = relax.at(d, K, k);
     if (Au) {
       float v = Au[a_row + k];
       bool nn = v >= 0.f;
@@ -312,7 +359,7 @@ template <int TPR>
 __global__ void __launch_bounds__(256)
 relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t a_dstride, int64_t M,
                         int64_t S, int64_t K,
-                        const float4* __restrict__ relax, const float* __restrict__ add_l, int64_t add_ld,
+                        RelaxSrc relax, const float* __restrict__ add_l, int64_t add_ld,
                         const float* __restrict__ kbias, const float* __restrict__ cvec,
                         const float* __restrict__ bu_in, const float* __restrict__ bl_in, float* __restrict__ Au_out,
                         float* __restrict__ Al_out, float* __restrict__ bu_out, float* __restrict__ bl_out,
@@ -329,8 +376,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
     const int64_t a_row = d * a_dstride + (m - d * S) * K;   // input row (shared by all domains when a_dstride = 0)
     for (int64_t k = 4 * (int64_t)t; k < K; k += 4 * TPR) {
       float4 r[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = relax ? relax[d * K + k + e] : make_float4(1.f, 0.f, 1.f, 0.f);
+      relax.quad(d, K, k, r);
       const float4 kb = kbias ? *reinterpret_cast<const float4*>(kbias + k) : make_float4(0.f, 0.f, 0.f, 0.f);
       const float4 cv = cvec ? *reinterpret_cast<const float4*>(cvec + d * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
       const float kbv[4] = {kb.x, kb.y, kb.z, kb.w};
@@ -851,38 +897,60 @@ int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
   return 2 * (int64_t)gemm_partial_count(I) * D * S;
 }
 
-int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
-                        const float* relax,
-                        const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
-                        const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
-                        float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
+static int relax_pass(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
+                      const RelaxSrc& src, const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+                      const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
+                      float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && K > 0, "bf_crown_relu_relax: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
-  BF_REQUIRE(((uintptr_t)relax & 15) == 0, "bf_crown_relu_relax: relax table must be 16-byte aligned");
+  BF_REQUIRE(((uintptr_t)src.table & 15) == 0, "bf_crown_relu_relax: relax table must be 16-byte aligned");
+  BF_REQUIRE((src.lo == nullptr) == (src.hi == nullptr), "bf_crown_relu_relax: give both pre_lo and pre_hi");
   BF_REQUIRE((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr),
              "bf_crown_relu_relax: input/output mismatch");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   const bool vec = (K % 4 == 0) && (a_dstride % 4 == 0) && al16(A_u) && al16(A_l) && al16(A_u_out) &&
                    al16(A_l_out) && al16(kbias) &&
-                   al16(cvec) && al16(add_l) && (add_l == nullptr || add_ld % 4 == 0);
+                   al16(cvec) && al16(add_l) && (add_l == nullptr || add_ld % 4 == 0) && al16(src.lo) &&
+                   al16(src.hi) && al16(src.alpha) && (src.alpha_ld % 4 == 0);
   if (vec && K >= 1024) {
     hipLaunchKernelGGL(relu_relax_rows4_kernel<256>, dim3((unsigned)M), dim3(256), 0, stream, A_u, A_l, a_dstride, M, S,
-                       K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out,
-                       A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+                       K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out, b_l_out, c_u_out,
+                       c_l_out);
     BF_LAUNCH_CHECK("relu_relax_rows4_kernel<256>");
   } else if (vec) {
     hipLaunchKernelGGL(relu_relax_rows4_kernel<64>, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l,
-                       a_dstride, M, S, K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec,
-                       b_u_in, b_l_in, A_u_out, A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+                       a_dstride, M, S, K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out,
+                       b_l_out, c_u_out, c_l_out);
     BF_LAUNCH_CHECK("relu_relax_rows4_kernel<64>");
   } else {
     hipLaunchKernelGGL(relu_relax_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A_u, A_l,
-                       a_dstride, M, S, K, reinterpret_cast<const float4*>(relax), add_l, add_ld, kbias, cvec,
-                       b_u_in, b_l_in, A_u_out, A_l_out, b_u_out, b_l_out, c_u_out, c_l_out);
+                       a_dstride, M, S, K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out,
+                       b_l_out, c_u_out, c_l_out);
     BF_LAUNCH_CHECK("relu_relax_rows_kernel");
   }
   return BF_OK;
+}
+
+int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
+                        const float* relax,
+                        const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+                        const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
+                        float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
+  const RelaxSrc src{reinterpret_cast<const float4*>(relax), nullptr, nullptr, nullptr, 0};
+  return relax_pass(A_u, A_l, a_dstride, D, S, K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out,
+                    b_u_out, b_l_out, c_u_out, c_l_out, stream);
+}
+
+int bf_crown_relu_relax_lu(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
+                           const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
+                           const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+                           const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
+                           float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
+  BF_REQUIRE(alpha == nullptr || alpha_ld == 0 || alpha_ld >= K, "bf_crown_relu_relax_lu: bad alpha_ld");
+  const RelaxSrc src{nullptr, pre_lo, pre_hi, alpha, alpha_ld};
+  return relax_pass(A_u, A_l, a_dstride, D, S, K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out,
+                    b_u_out, b_l_out, c_u_out, c_l_out, stream);
 }
 
 int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,

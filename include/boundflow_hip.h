@@ -192,6 +192,17 @@ int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t a_dstride, i
                         const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
                         float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream);
 
+/* The same pass with the slopes and intercepts computed in place from the
+ * pre-activation box (pre_lo, pre_hi [D,K]; both NULL = identity) and the
+ * optional lower-slope override alpha ([D,K] with alpha_ld K, or shared with
+ * alpha_ld 0), by the arithmetic of bf_relu_relax_table
+ * (runtime/crown_ibp.py:722-758, 1176-1298): no table is built or read. */
+int bf_crown_relu_relax_lu(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
+                           const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
+                           const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+                           const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
+                           float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream);
+
 /* Transposed convolution of coefficient rows (Conv2dLinearOperator.to_dense,
  * runtime/linear_operator.py:1067-1092; FusedCrownExecutor "fused_relu_conv2d"
  * after bf_crown_relu_relax).  With norm_u/norm_l instead of y_u/y_l the

@@ -188,7 +188,7 @@ def test_all_intermediate_c2_matches_reference(epilogue, monkeypatch):
     assert_parity(final.upper, t(gz["upper"]), ref64.upper, "C2 upper")
 
 
-@pytest.mark.parametrize("K", [132, 133])
+@pytest.mark.parametrize("K", [132, 133, 500])
 def test_relax_pass_of_shared_coefficient(K):
     """bf_crown_relu_relax with a_dstride = 0: one [S, K] coefficient shared by every
     domain, relaxed per domain into [D*S, K] (the first region of a C = I query)."""
@@ -231,13 +231,15 @@ def test_relax_pass_of_shared_coefficient(K):
         assert bool((err <= tol).all()), f"{what}: {float((err / tol).max()):.3f} x tolerance"
 
 
-# K = 133: scalar kernel (K % 4 != 0); 132: float4 kernel, a wave per row; 2048: float4, a workgroup per row
-@pytest.mark.parametrize("K", [133, 132, 2048])
-def test_relax_pass_and_dense_concretize_match_oracle(K):
+# K = 133: scalar kernel (K % 4 != 0); 132, 256, 500: float4 kernel, a wave per row (500:
+# two quad steps, the second partial); 2048, 4100: float4, a workgroup per row (4100: a
+# partial last step); S = 19, 9, 3 vary the rows per domain
+@pytest.mark.parametrize("K,S", [(133, 7), (132, 7), (2048, 7), (500, 19), (256, 9), (4100, 3)])
+def test_relax_pass_and_dense_concretize_match_oracle(K, S):
     dev = device()
-    announce(f"standalone relax pass + dense concretize K={K}")
+    announce(f"standalone relax pass + dense concretize K={K} S={S}")
     g = torch.Generator().manual_seed(11)
-    D, S = 5, 7
+    D = 5
     A_u = torch.randn(D, S, K, generator=g)
     A_l = torch.randn(D, S, K, generator=g)
     A_u[0, 0, :4] = torch.tensor([0.0, -0.0, 1.0, -1.0])
@@ -276,7 +278,59 @@ def test_relax_pass_and_dense_concretize_match_oracle(K):
     _lib.call("bf_concretize_dense", _lib.ptr(Al), D, S, K, _lib.ptr(xd), None, 0.05, _lib.ptr(bld), 1,
               _lib.ptr(lb), _lib.stream_handle())
     torch.cuda.synchronize()
-    assert_bounds_close(lb.reshape(D, S), lb_ref, "concretize lb")
+    # fp32 cancellation in center - eps * norm + b: judged against the fp64 oracle where the fp32 one differs
+    f = lambda x: x.double()
+    spec64 = cr.InputSpec.linf(value_name="input", center=f(x0), eps=0.05)
+    lb64, _ub64 = cr.concretize_affine(spec64, f(x0), cr.DenseOp(f(ref[1]), (K,)), f(ref[3]))
+    assert_parity(lb.reshape(D, S), lb_ref, lb64, "concretize lb")
+
+
+# (K, S, shared coefficient, alpha): float4 / scalar kernels, a wave or a workgroup per row,
+# per-domain / shared / no lower-slope override, and no ReLU at all (identity)
+@pytest.mark.parametrize("K,S,stride0,alpha_mode", [(132, 7, False, "domain"), (133, 7, False, "shared"),
+                                                    (500, 19, True, "domain"), (2048, 3, False, "none"),
+                                                    (256, 9, False, "identity")])
+def test_relax_pass_from_box_equals_table_pass(K, S, stride0, alpha_mode):
+    """bf_crown_relu_relax_lu computes the slopes from the pre-activation box with the
+    arithmetic of bf_relu_relax_table: every output is bit-identical to the table pass."""
+    dev = device()
+    announce(f"relax pass from the box K={K} S={S} stride0={stride0} alpha={alpha_mode}")
+    g = torch.Generator().manual_seed(K + S)
+    D = 6
+    A_u = torch.randn(S if stride0 else D * S, K, generator=g)
+    A_l = A_u if stride0 else torch.randn(D * S, K, generator=g)
+    l = torch.randn(D, K, generator=g)
+    u = l + torch.rand(D, K, generator=g)
+    l[0, :3] = torch.tensor([0.0, -1.0, 0.0])
+    u[0, :3] = torch.tensor([0.0, 0.0, 1.0])
+    alpha = {"domain": torch.rand(D, K, generator=g) * 1.4 - 0.2, "shared": torch.rand(K, generator=g)}.get(alpha_mode)
+    alpha_ld = K if alpha_mode == "domain" else 0
+    add = torch.randn(D, K, generator=g)
+    kb = torch.randn(K, generator=g)
+    cv = torch.randn(D, K, generator=g)
+    b_in = torch.randn(D * S, generator=g)
+    dd = lambda x: None if x is None else x.to(dev).contiguous()
+    Au, Al, ld, ud, ad, addd, kbd, cvd, bd = (dd(x) for x in (A_u, A_l, l, u, alpha, add, kb, cv, b_in))
+    if alpha_mode == "identity":
+        ld = ud = ad = None
+    stride = 0 if stride0 else S * K
+    st = _lib.stream_handle()
+    table = None
+    if ld is not None:
+        table = torch.empty(D, K, 4, device=dev)
+        _lib.call("bf_relu_relax_table", _lib.ptr(ld), _lib.ptr(ud), _lib.ptr(ad), alpha_ld, D, K, _lib.ptr(table), st)
+    outs = []
+    for use_box in (False, True):
+        o = [torch.empty(D * S, K, device=dev), torch.empty(D * S, K, device=dev)] + \
+            [torch.empty(D * S, device=dev) for _ in range(4)]
+        src = (_lib.ptr(ld), _lib.ptr(ud), _lib.ptr(ad), alpha_ld) if use_box else (_lib.ptr(table),)
+        _lib.call("bf_crown_relu_relax_lu" if use_box else "bf_crown_relu_relax", _lib.ptr(Au), _lib.ptr(Al), stride,
+                  D, S, K, *src, _lib.ptr(addd), K, _lib.ptr(kbd), _lib.ptr(cvd), _lib.ptr(bd), _lib.ptr(bd),
+                  *(_lib.ptr(x) for x in o), st)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for i, (x, y) in enumerate(zip(*outs)):
+        assert torch.equal(x.cpu(), y.cpu()), f"output {i} differs between the box and the table source"
 
 
 def test_branch_update_matches_oracle():
