@@ -526,7 +526,8 @@ def crown_backward(
             nc_l = torch.empty(M, device=dev, dtype=torch.float32) if (cvec is not None and A_l is not None) else None
             # the gradient pass reads the lower coefficient before the next relaxation
             pre_l = torch.empty(M, P, device=dev, dtype=torch.float32) if (save is not None and A_l is not None) else None
-            with _timed("crown_relu_linear_relu_fwd", flops, nbytes):
+            # bytes: the unrelaxed lower coefficient kept for the gradient is a second output
+            with _timed("crown_relu_linear_relu_fwd", flops, nbytes + (4.0 * M * P if pre_l is not None else 0.0)):
                 _lib.call("bf_crown_relu_linear_relu_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
                           _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, _lib.ptr(bias), _lib.ptr(b_u),
                           _lib.ptr(b_l), _lib.ptr(n_table), _lib.ptr(n_add), n_add_ld, _lib.ptr(n_bias),

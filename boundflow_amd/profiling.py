@@ -135,9 +135,40 @@ def summarize_rocpd(db_path: str, top: int = 12) -> str:
     return "\n".join(out)
 
 
+def summarize_pmc(csv_path: str, top: int = 12) -> str:
+    """Per-kernel dispatch count and average counter value per dispatch from a
+    rocprofv3 ``--pmc ... --output-format csv`` run (``*_counter_collection.csv``),
+    as a Markdown table; counters summed over the device for each dispatch."""
+    import csv
+    import os
+    from collections import OrderedDict
+
+    if not os.path.isfile(csv_path):
+        raise FileNotFoundError(f"no rocprofv3 counter file at {csv_path}")
+    per_dispatch: "OrderedDict[tuple, float]" = OrderedDict()
+    names = {}
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            key = (row["Dispatch_Id"], row["Counter_Name"])
+            per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
+            names[row["Dispatch_Id"]] = (row["Kernel_Name"], row.get("Grid_Size", ""))
+    agg: Dict[Tuple[str, str], List[float]] = defaultdict(list)
+    for (disp, ctr), v in per_dispatch.items():
+        agg[(names[disp][0], ctr)].append(v)
+    rows = sorted(agg.items(), key=lambda kv: -sum(kv[1]))
+    out = ["| kernel | counter | dispatches | average per dispatch | total |", "|---|---|---:|---:|---:|"]
+    for (name, ctr), vals in rows[:top]:
+        out.append(f"| `{name[:100]}` | {ctr} | {len(vals)} | {sum(vals) / len(vals):.1f} | {sum(vals):.1f} |")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
     import sys
 
-    if len(sys.argv) != 2 or sys.argv[1].startswith("-"):
-        raise SystemExit("usage: python -m boundflow_amd.profiling <rocprofv3 *_results.db>")
-    print(summarize_rocpd(sys.argv[1]))
+    if len(sys.argv) == 3 and sys.argv[1] == "--pmc":
+        print(summarize_pmc(sys.argv[2]))
+    elif len(sys.argv) == 2 and not sys.argv[1].startswith("-"):
+        print(summarize_rocpd(sys.argv[1]))
+    else:
+        raise SystemExit("usage: python -m boundflow_amd.profiling <rocprofv3 *_results.db>\n"
+                         "       python -m boundflow_amd.profiling --pmc <rocprofv3 *_counter_collection.csv>")
