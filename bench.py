@@ -21,6 +21,7 @@ timed on a bounded sample on this host).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import platform
@@ -264,13 +265,20 @@ def main() -> int:
         t1 = time.perf_counter()
         # Per-kernel durations (the same in eager launches) for the roofline, in a
         # separate pass after one untimed eager query (the first eager query after
-        # the graph replays runs slow): each timed launch is preceded by a 0.2 ms
-        # spin so that its events bracket execution, not the host's launch latency.
+        # the graph replays runs slow), with the garbage collector off: each timed
+        # launch is preceded by a 0.2 ms spin so that its events bracket execution,
+        # not the host's launch latency.
         step()
         timer = profiling.LaunchTimer(spin_cycles=profiling.spin_cycles(0.2))
-        with profiling.timing(timer):
-            for _ in range(args.steps):
-                step()
+        # a garbage-collection pause between a start event and its launch would outlast the spin
+        gc.disable()
+        try:
+            with profiling.timing(timer):
+                for _ in range(args.steps):
+                    step()
+            torch.cuda.synchronize()
+        finally:
+            gc.enable()
     else:
         with profiling.timing(timer):
             torch.cuda.synchronize()

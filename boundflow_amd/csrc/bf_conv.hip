@@ -147,6 +147,8 @@ conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restric
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int GT = 256;
+// threads of a gather-GEMM or tap-product workgroup: its waves share one LDS copy of the weights
+constexpr int GTM = 512;
 constexpr int GMAX_CLASSES = 16;
 enum : int { MODE_T = 0, MODE_F = 1 };
 
@@ -208,14 +210,31 @@ static void gather_fdivs(GatherArgs& g) {
   g.f_Wp = make_fdiv(g.Wp);
 }
 
+// LDS layout of the gather-GEMM operands.  The weights of class c, output channel n
+// (block cb = n / 16, column col = n % 16) and reduction index k = j + 4 s
+// (j = k % 4, the MFMA k lane group; s = 4 sq + e) live at
+//   ((((c nblk + cb) 4 + j) (Kc4 / 16) + sq) 16 + col) 4 + e,
+// so the four weights of steps 4 sq .. 4 sq + 3 of one lane are one 16-byte chunk and
+// the 16 columns of a lane group read consecutive chunks; the map offsets of k are at
+// (j (Kc4 / 16) + sq) 4 + e (the same for all 16 columns: a broadcast).  Kc4 is a
+// multiple of 16.
+__device__ __forceinline__ int ws_index(const GatherArgs& g, int c, int n, int k) {
+  const int cb = n >> 4, col = n & 15, j = k & 3, s = k >> 2, sq = s >> 2, e = s & 3;
+  return ((((c * g.nblk + cb) * 4 + j) * (g.Kc4 >> 4) + sq) * 16 + col) * 4 + e;
+}
+__device__ __forceinline__ int koff_index(const GatherArgs& g, int k) {
+  const int j = k & 3, s = k >> 2;
+  return (j * (g.Kc4 >> 4) + (s >> 2)) * 4 + (s & 3);
+}
+
 template <int MODE>
-__global__ void __launch_bounds__(GT)
+__global__ void __launch_bounds__(GTM)
 conv_mfma_kernel(GatherArgs g) {
-  extern __shared__ float smem[];
+  extern __shared__ __attribute__((aligned(16))) float smem[];
   float* Ws = smem;                                              // [nclasses][Kc4][npad]
   int* koff = reinterpret_cast<int*>(Ws + (size_t)g.nclasses * g.Kc4 * g.npad);   // [Kc4]
   float* As = reinterpret_cast<float*>(koff + g.Kc4);            // [Cm][Hp][Wp]
-  __shared__ float red[GT / 64];
+  __shared__ float red[GTM / 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int z = blockIdx.y;
@@ -228,11 +247,11 @@ conv_mfma_kernel(GatherArgs g) {
   // weights of every class, zero-padded in k (to Kc4) and in channels (to npad);
   // eight loads per thread in flight, from clamped addresses, before the stores
   const int wtotal = g.nclasses * kstride;
-  for (int base = 0; base < wtotal; base += 8 * GT) {
+  for (int base = 0; base < wtotal; base += 8 * GTM) {
     float wv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int idx = base + u * GT + tid;
+      const int idx = base + u * GTM + tid;
       const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
       const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
       const bool ok = idx < wtotal && k < g.Kc && n < g.nch;
@@ -252,11 +271,15 @@ conv_mfma_kernel(GatherArgs g) {
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int idx = base + u * GT + tid;
-      if (idx < wtotal) Ws[idx] = wv[u];
+      const int idx = base + u * GTM + tid;
+      if (idx < wtotal) {
+        const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
+        const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
+        Ws[ws_index(g, c, n, k)] = wv[u];
+      }
     }
   }
-  for (int k = tid; k < g.Kc4; k += GT) {
+  for (int k = tid; k < g.Kc4; k += GTM) {
     int off = 0;
     if (k < g.Kc) {
       if (MODE == MODE_T) {
@@ -269,7 +292,7 @@ conv_mfma_kernel(GatherArgs g) {
         off = (ci * g.Hp + kh) * g.Wp + kw;
       }
     }
-    koff[k] = off;
+    koff[koff_index(g, k)] = off;
   }
 
   const int nin = g.Cm * g.Hm * g.Wm;
@@ -283,11 +306,11 @@ conv_mfma_kernel(GatherArgs g) {
     if (r >= g.R) break;   // uniform
     __syncthreads();       // weights staged / previous row's map and partial sums consumed
     const float* __restrict__ xr = X + (r / g.in_div) * nin;
-    for (int base = 0; base < map; base += 8 * GT) {
+    for (int base = 0; base < map; base += 8 * GTM) {
       float xv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int idx = base + u * GT + tid;
+        const int idx = base + u * GTM + tid;
         const int c = fdivq(idx, g.f_HpWp), rem = idx - c * g.Hp * g.Wp;
         const int hr = fdivq(rem, g.f_Wp);
         const int hm = hr - g.pad_h, wm = (rem - hr * g.Wp) - g.pad_w;
@@ -297,7 +320,7 @@ conv_mfma_kernel(GatherArgs g) {
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int idx = base + u * GT + tid;
+        const int idx = base + u * GTM + tid;
         if (idx < map) As[idx] = xv[u];
       }
     }
@@ -307,7 +330,7 @@ conv_mfma_kernel(GatherArgs g) {
     const float rsv = (MODE == MODE_F && g.rs) ? g.rs[r] : 0.f;
     const float* __restrict__ vr = (MODE == MODE_F && g.rs) ? g.v + (r / g.v_div) * g.v_ld : nullptr;
     float s = 0.f;
-    for (int task = wave; task < g.ntasks; task += GT / 64) {
+    for (int task = wave; task < g.ntasks; task += GTM / 64) {
       int c = 0;
       while (c + 1 < g.nclasses && task >= g.cls[c + 1].tbase) ++c;
       const GatherClass& C = g.cls[c];
@@ -318,11 +341,21 @@ conv_mfma_kernel(GatherArgs g) {
       const int pc = pok ? p : C.np - 1;
       const int q1 = pc / C.n2, q2 = pc - q1 * C.n2;
       const float* __restrict__ as = As + C.poff0 + q1 * C.s1 + q2 * C.s2;
-      const float* __restrict__ ws = Ws + (size_t)c * kstride + cb * 16 + col;
+      // k = j + 4 s, s = 4 sq + e: one 128-bit LDS read gives this lane's weights of four
+      // consecutive k steps, one broadcast read their map offsets
+      const float* __restrict__ wl = Ws + ws_index(g, c, cb * 16 + col, j);
+      const int* __restrict__ kl = koff + koff_index(g, j);
       floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int k = j; k < g.Kc4; k += 4)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ws[k * g.npad], as[koff[k]], acc, 0, 0, 0);
+      const int nq = g.Kc4 / 16;
+#pragma unroll 2
+      for (int sq = 0; sq < nq; ++sq) {
+        const float4 w4 = *reinterpret_cast<const float4*>(wl + sq * 64);
+        const int4 o4 = *reinterpret_cast<const int4*>(kl + sq * 4);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.x, as[o4.x], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.y, as[o4.y], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.z, as[o4.z], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.w, as[o4.w], acc, 0, 0, 0);
+      }
       const int opix = C.out0 + q1 * C.o1 + q2 * C.o2;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -349,7 +382,7 @@ conv_mfma_kernel(GatherArgs g) {
       __syncthreads();
       if (tid == 0) {
         float t = 0.f;
-        for (int q = 0; q < GT / 64; ++q) t += red[q];
+        for (int q = 0; q < GTM / 64; ++q) t += red[q];
         nrm[r] = t;
       }
     }
@@ -381,13 +414,13 @@ struct SmallTArgs {
   FastDiv f_Wi, f_sh, f_sw, f_pitch;   // index divisions of the col2im and the map copy
 };
 
-__global__ void __launch_bounds__(GT)
+__global__ void __launch_bounds__(GTM)
 conv_t_small_kernel(SmallTArgs g) {
   extern __shared__ float smem[];
   float* Wsm = smem;                                   // [Ci][Co4][16]: tap-fastest MFMA A operand
   float* Xs = Wsm + (size_t)g.Ci * g.Co4 * 16;          // [Co4][nblk * 16]
   float* Zs = Xs + (size_t)g.Co4 * g.nblk * 16;         // [16][nblk * 16]
-  __shared__ float red[GT / 64];
+  __shared__ float red[GTM / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int z = blockIdx.y;
   const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
@@ -399,7 +432,7 @@ conv_t_small_kernel(SmallTArgs g) {
   const int nin = g.Co * g.npix;
   const int64_t nout = (int64_t)g.Ci * g.Hi * g.Wi;
 
-  for (int idx = tid; idx < g.Ci * g.Co4 * 16; idx += GT) {
+  for (int idx = tid; idx < g.Ci * g.Co4 * 16; idx += GTM) {
     const int n = idx / (g.Co4 * 16), rem = idx - n * g.Co4 * 16;
     const int co = rem / 16, t = rem - co * 16;
     float w = 0.f;
@@ -418,10 +451,10 @@ conv_t_small_kernel(SmallTArgs g) {
       // unpadded map (npix % 16 == 0, 16-byte aligned rows): a float4 copy, then the zero channels
       const float4* __restrict__ x4 = reinterpret_cast<const float4*>(xr);
       float4* xs4 = reinterpret_cast<float4*>(Xs);
-      for (int q = tid; q < nin / 4; q += GT) xs4[q] = x4[q];
-      for (int idx = nin + tid; idx < g.Co4 * pitch; idx += GT) Xs[idx] = 0.f;
+      for (int q = tid; q < nin / 4; q += GTM) xs4[q] = x4[q];
+      for (int idx = nin + tid; idx < g.Co4 * pitch; idx += GTM) Xs[idx] = 0.f;
     } else {
-      for (int idx = tid; idx < g.Co4 * pitch; idx += GT) {
+      for (int idx = tid; idx < g.Co4 * pitch; idx += GTM) {
         const int co = fdivq(idx, g.f_pitch), p = idx - co * pitch;
         Xs[idx] = (co < g.Co && p < g.npix) ? xr[co * g.npix + p] : 0.f;
       }
@@ -432,7 +465,7 @@ conv_t_small_kernel(SmallTArgs g) {
     for (int n = 0; n < g.Ci; ++n) {
       __syncthreads();   // Xs staged / the previous channel's taps consumed
       const float* __restrict__ wn = Wsm + (size_t)n * g.Co4 * 16;
-      for (int jb = wave; jb < g.nblk; jb += GT / 64) {
+      for (int jb = wave; jb < g.nblk; jb += GTM / 64) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int k = k4; k < g.Co4; k += 4)
           acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wn[k * 16 + col], Xs[k * pitch + jb * 16 + col], acc, 0, 0, 0);
@@ -440,7 +473,7 @@ conv_t_small_kernel(SmallTArgs g) {
         for (int q = 0; q < 4; ++q) Zs[(4 * k4 + q) * pitch + jb * 16 + col] = acc[q];
       }
       __syncthreads();
-      for (int o = tid; o < g.Hi * g.Wi; o += GT) {
+      for (int o = tid; o < g.Hi * g.Wi; o += GTM) {
         const int oh = fdivq(o, g.f_Wi), ow = o - oh * g.Wi;
         // taps kh = kh0 + sh*a reach map row ih0 - a (kh0 = (oh + ph) mod sh), likewise for columns
         const int qh = fdivq(oh + g.ph, g.f_sh), qw = fdivq(ow + g.pw, g.f_sw);
@@ -471,7 +504,7 @@ conv_t_small_kernel(SmallTArgs g) {
       __syncthreads();
       if (tid == 0) {
         float tsum = 0.f;
-        for (int q = 0; q < GT / 64; ++q) tsum += red[q];
+        for (int q = 0; q < GTM / 64; ++q) tsum += red[q];
         nrm[r] = tsum;
       }
     }
@@ -510,7 +543,7 @@ static bool conv_t_mfma_plan(GatherArgs& g, int64_t R, int Co, int Ho, int Wo, i
   g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw;
   g.nA = KH / sh; g.nB = KW / sw; g.T = g.nA * g.nB;
   g.Kc = Co * g.T;
-  g.Kc4 = (g.Kc + 3) / 4 * 4;
+  g.Kc4 = (g.Kc + 15) / 16 * 16;
   g.npad = (Ci + 15) / 16 * 16;
   g.nblk = g.npad / 16;
   g.nclasses = sh * sw;
@@ -567,7 +600,7 @@ static bool conv_f_mfma_plan(GatherArgs& g, int64_t R, int Ci, int Hi, int Wi, i
   g.Cm = Ci; g.Hm = Hi; g.Wm = Wi; g.Cin = Ci; g.nch = Co; g.HWout = Ho * Wo;
   g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw;
   g.Kc = Ci * KH * KW;
-  g.Kc4 = (g.Kc + 3) / 4 * 4;
+  g.Kc4 = (g.Kc + 15) / 16 * 16;
   g.npad = (Co + 15) / 16 * 16;
   g.nblk = g.npad / 16;
   g.nclasses = 1;
@@ -630,7 +663,7 @@ static int conv2d_launch(const float* x, int64_t in_div, int64_t R, int Ci, int 
       g.rows_per_wg = gather_rows_per_wg(R);
       const int rpw = g.rows_per_wg;
       BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "conv2d: too many rows");
-      hipLaunchKernelGGL(conv_mfma_kernel<MODE_F>, dim3((unsigned)((R + rpw - 1) / rpw), 1), dim3(GT), glds, stream,
+      hipLaunchKernelGGL(conv_mfma_kernel<MODE_F>, dim3((unsigned)((R + rpw - 1) / rpw), 1), dim3(GTM), glds, stream,
                          g);
       BF_LAUNCH_CHECK("conv_mfma_kernel<conv2d>");
       return BF_OK;
@@ -697,7 +730,7 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
       const int rpw = gather_rows_per_wg(R * nz);
       g.rows_per_wg = rpw;
       BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
-      hipLaunchKernelGGL(conv_t_small_kernel, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GT), glds, stream, g);
+      hipLaunchKernelGGL(conv_t_small_kernel, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g);
       BF_LAUNCH_CHECK("conv_t_small_kernel");
       return BF_OK;
     }
@@ -720,7 +753,7 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
       const int rpw = gather_rows_per_wg(R * nz);
       g.rows_per_wg = rpw;
       BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
-      hipLaunchKernelGGL(conv_mfma_kernel<MODE_T>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GT), glds, stream,
+      hipLaunchKernelGGL(conv_mfma_kernel<MODE_T>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream,
                          g);
       BF_LAUNCH_CHECK("conv_mfma_kernel<conv_transpose2d>");
       return BF_OK;
