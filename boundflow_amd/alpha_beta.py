@@ -257,8 +257,11 @@ def run_alpha_beta_crown_mlp(
             if n in relu_split_state:
                 s, ld = _broadcast_split(relu_split_state[n].to(dev), B, numel[n])
                 splits[n] = (s, ld)
-    # names whose split has a nonzero entry get the beta coefficient (alpha_beta_crown.py:630-633)
-    beta_names = [n for n, (s, _ld) in splits.items() if bool((s != 0).any().item())] if use_beta else []
+    # Every ReLU with a split state gets the split term.  The reference keeps those with a
+    # nonzero entry (alpha_beta_crown.py:630-633); an all-zero split adds exact zeros and
+    # receives a zero beta gradient (Adam then leaves beta unchanged), so the results are
+    # the same, and no host synchronization is needed: the batch can be captured as a graph.
+    beta_names = list(splits.keys()) if use_beta else []
     b_layer, b_neuron, _gap = branch_tensors(trace, B) if trace.relu_pre else (None, None, None)
     S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else _numel(chain.layers[-1].out_shape)
     M = B * S

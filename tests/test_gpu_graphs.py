@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from boundflow_amd import alpha_beta as hab
+from boundflow_amd import bab as hbab
 from boundflow_amd import crown as hc
 from boundflow_amd import graphs
 from boundflow_amd import workloads as wl
@@ -60,3 +61,30 @@ def test_captured_alpha_crown_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(out.lower, ref_lo), f"replay {rep} lower"
         assert torch.equal(out.upper, ref_hi), f"replay {rep} upper"
+
+
+def test_captured_domain_batch_replays_match_eager():
+    """A C5 domain batch (splits, 10 alpha-beta steps, certification) has no host
+    synchronization either: every replay gives the eager statuses, bounds and
+    branching decisions."""
+    dev = device()
+    announce("graph replay of evaluate_domain_batch (C5, 256 domains)")
+    wd = wl.to_device(wl.subset(wl.make_c5(), 256), dev)
+
+    def batch():
+        return hbab.evaluate_domain_batch(wd.module, wd.spec, linear_spec_C=wd.C,
+                                          relu_split_state=wd.extra["splits"], steps=10, lr=0.2)
+
+    eager = batch()
+    torch.cuda.synchronize()
+    keys = ("status", "lower", "upper", "branch_layer", "branch_neuron")
+    ref = {k: eager[k].clone() for k in keys}
+    cap = graphs.CapturedQuery(batch)
+    for rep in range(3):
+        junk = batch()
+        junk["lower"].add_(1.0)
+        torch.cuda.synchronize()
+        out = cap()
+        torch.cuda.synchronize()
+        for k in keys:
+            assert torch.equal(out[k], ref[k]), f"replay {rep} {k}"
