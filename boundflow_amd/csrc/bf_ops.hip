@@ -559,6 +559,126 @@ __global__ void adam_clamp_kernel(float* __restrict__ p, float* __restrict__ m, 
   p[i] = pi;
 }
 
+// ---------------------------------------------------------------------------
+// The two-region step of bf_crown_relu_linear_relu_fwd when the contraction is
+// short (N <= SMALLK_MAX: the first region C x W of the output layer) and A needs
+// no prologue relaxation.  The tiled contraction would run one wave of workgroups
+// whose fixed latencies never overlap; here a wave takes the S rows of one domain
+// over 256 output columns (4 per lane), keeps the weight columns and the next
+// ReLU's relaxation entries of its columns in registers, reads each coefficient
+// row with scalar loads, and stores A_next (and A_pre) as 16-byte vectors.  The
+// four waves of a workgroup take four domains of one column chunk and stage that
+// chunk's weights in LDS once, with coalesced loads.  Row
+// sums per 256-column chunk go to the workspace, summed in chunk order by
+// rows_finalize like the tiled path's per-tile partials.
+constexpr int SMALLK_MAX = 16;
+constexpr int SMALLK_ROWS = 256;
+
+__global__ void __launch_bounds__(256)
+small_k_relax_epi_kernel(const float* __restrict__ A0, const float* __restrict__ A1, int64_t a_dstride, int64_t D,
+                         int64_t S, int N, const float* __restrict__ Wt, int64_t P, const float* __restrict__ bias,
+                         const float* __restrict__ b_in0, const float* __restrict__ b_in1,
+                         const float4* __restrict__ relax_next, const float* __restrict__ add_next,
+                         int64_t add_next_ld, const float* __restrict__ bias_next, const float* __restrict__ cvec_next,
+                         int64_t cvec_next_ld, float* __restrict__ An0, float* __restrict__ An1,
+                         float* __restrict__ Ap0, float* __restrict__ Ap1, float* __restrict__ bo0,
+                         float* __restrict__ bo1, float* __restrict__ pb0, float* __restrict__ pb1,
+                         float* __restrict__ pc0, float* __restrict__ pc1, int z_lower_first, int nchunks) {
+  const int z = blockIdx.y;
+  const bool lower = z_lower_first ? (z == 0) : (z == 1);
+  const float* __restrict__ A = z == 0 ? A0 : A1;
+  const float* __restrict__ b_in = z == 0 ? b_in0 : b_in1;
+  float* __restrict__ An = z == 0 ? An0 : An1;
+  float* __restrict__ Ap = z == 0 ? Ap0 : Ap1;
+  float* __restrict__ bo = z == 0 ? bo0 : bo1;
+  float* __restrict__ pb = z == 0 ? pb0 : pb1;
+  float* __restrict__ pc = z == 0 ? pc0 : pc1;
+  __shared__ float Ws[256 * SMALLK_MAX];   // the chunk's weight rows [256 columns][N]
+  __shared__ float Asm[4][SMALLK_ROWS];    // each wave's domain block of A [S][N] when S N <= SMALLK_ROWS
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int chunk = (int)(blockIdx.x % nchunks);
+  const int64_t d = (int64_t)(blockIdx.x / nchunks) * 4 + wave;
+  const int64_t cols = P - (int64_t)chunk * 256 < 256 ? P - (int64_t)chunk * 256 : 256;
+  for (int64_t i = threadIdx.x; i < cols * N; i += 256) Ws[i] = Wt[(int64_t)chunk * 256 * N + i];
+  const bool a_lds = S * N <= SMALLK_ROWS;   // uniform
+  if (a_lds && d < D)
+    for (int64_t i = lane; i < S * N; i += 64) Asm[wave][i] = A[d * a_dstride + i];
+  __syncthreads();
+  if (d >= D) return;   // whole wave
+  const int64_t M = D * S;
+  const int64_t p0 = (int64_t)chunk * 256 + 4 * lane;
+  const bool act = p0 < P;   // P % 4 == 0: the whole quad is inside
+  float wv[4][SMALLK_MAX];
+  float4 e[4];
+  float ad[4] = {0.f, 0.f, 0.f, 0.f}, kb[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int n = 0; n < SMALLK_MAX; ++n) wv[q][n] = (act && n < N) ? Ws[(4 * lane + q) * N + n] : 0.f;
+    e[q] = act ? relax_next[d * P + p0 + q] : make_float4(1.f, 0.f, 1.f, 0.f);
+    if (act && lower && add_next) ad[q] = add_next[d * add_next_ld + p0 + q];
+    if (act && bias_next) kb[q] = bias_next[p0 + q];
+    if (act && cvec_next) cv[q] = cvec_next[d * cvec_next_ld + p0 + q];
+  }
+  float bv[SMALLK_MAX];
+#pragma unroll
+  for (int n = 0; n < SMALLK_MAX; ++n) bv[n] = (bo && n < N) ? bias[n] : 0.f;
+  for (int64_t s_ = 0; s_ < S; ++s_) {
+    const int64_t m = d * S + s_;
+    // the row from LDS (a broadcast read) or, for a large domain block, from global memory
+    float a[SMALLK_MAX];
+    if (a_lds) {
+      const float* ar = &Asm[wave][s_ * N];
+#pragma unroll
+      for (int n = 0; n < SMALLK_MAX; ++n) a[n] = n < N ? ar[n] : 0.f;
+    } else {
+      const float* __restrict__ ar = A + d * a_dstride + s_ * N;
+#pragma unroll
+      for (int n = 0; n < SMALLK_MAX; ++n) a[n] = n < N ? ar[n] : 0.f;
+    }
+    float acc[4], out[4];
+    float sb = 0.f, sc = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float v = 0.f;
+#pragma unroll
+      for (int n = 0; n < SMALLK_MAX; ++n) v += a[n] * wv[q][n];
+      acc[q] = v;
+      // upper: C >= 0 -> (alpha_u, beta_u) else (alpha_l, beta_l); lower mirrored
+      const bool use_u = lower ? !(v >= 0.f) : (v >= 0.f);
+      float o = v * (use_u ? e[q].x : e[q].z);
+      const float be = use_u ? e[q].y : e[q].w;
+      if (lower && add_next) o = o + ad[q];
+      sb += v * be;
+      if (bias_next) sb += o * kb[q];
+      if (cvec_next) sc += o * cv[q];
+      out[q] = o;
+    }
+    if (act) {
+      if (Ap) *reinterpret_cast<float4*>(Ap + m * P + p0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *reinterpret_cast<float4*>(An + m * P + p0) = make_float4(out[0], out[1], out[2], out[3]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      sb += __shfl_xor(sb, off, 64);
+      if (cvec_next) sc += __shfl_xor(sc, off, 64);
+    }
+    if (lane == 0) {
+      pb[(int64_t)chunk * M + m] = sb;
+      if (cvec_next) pc[(int64_t)chunk * M + m] = sc;
+      if (bo && chunk == 0) {
+        // the affine bias of this region: b += A . bias
+        float sk = 0.f;
+#pragma unroll
+        for (int n = 0; n < SMALLK_MAX; ++n)
+          if (n < N) sk += a[n] * bv[n];
+        bo[m] = ((b_in ? b_in[m] : 0.f) + 0.f) + sk;
+      }
+    }
+  }
+}
+
 }  // namespace bf
 
 using namespace bf;
@@ -787,6 +907,38 @@ int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_
   BF_REQUIRE(A_u || A_l, "bf_crown_relu_linear_relu_fwd: no coefficient");
   BF_REQUIRE(cvec_next == nullptr || ((A_u == nullptr || c_u_out) && (A_l == nullptr || c_l_out)),
              "bf_crown_relu_linear_relu_fwd: center sums need c_out");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (N <= SMALLK_MAX && relax == nullptr && add_l == nullptr && P % 4 == 0 && al16(A_next_u) && al16(A_next_l) &&
+      al16(A_pre_u) && al16(A_pre_l)) {
+    const int nchunks = (int)ceil_div(P, 256);
+    const int nz = (A_u ? 1 : 0) + (A_l ? 1 : 0);
+    const float* As[2] = {A_u ? A_u : A_l, A_l};
+    const float* bi[2] = {A_u ? b_u_in : b_l_in, b_l_in};
+    float* an[2] = {A_u ? A_next_u : A_next_l, A_next_l};
+    float* ap[2] = {A_u ? A_pre_u : A_pre_l, A_pre_l};
+    float* bo[2] = {A_u ? b_u_out : b_l_out, b_l_out};
+    float* co[2] = {A_u ? c_u_out : c_l_out, c_l_out};
+    float* pbz[2], *pcz[2];
+    for (int z = 0; z < 2; ++z) {
+      pbz[z] = workspace + (int64_t)(2 * z) * nchunks * M;
+      pcz[z] = workspace + (int64_t)(2 * z + 1) * nchunks * M;
+    }
+    const bool bias_in = bias != nullptr;
+    const int64_t wgs = ceil_div(D, 4) * nchunks;
+    BF_REQUIRE(wgs < (1LL << 31), "bf_crown_relu_linear_relu_fwd: too many domains");
+    hipLaunchKernelGGL(small_k_relax_epi_kernel, dim3((unsigned)wgs, (unsigned)nz), dim3(256), 0,
+                       stream, As[0], As[1], a_dstride, D, S, (int)N, W_t, P, bias, bi[0], bi[1],
+                       reinterpret_cast<const float4*>(relax_next), add_next, add_next_ld, bias_next, cvec_next,
+                       cvec_next_ld, an[0], an[1], ap[0], ap[1], bias_in ? bo[0] : nullptr, bias_in ? bo[1] : nullptr,
+                       pbz[0], pbz[1], pcz[0], pcz[1], A_u == nullptr ? 1 : 0, nchunks);
+    BF_LAUNCH_CHECK("small_k_relax_epi_kernel");
+    for (int z = 0; z < nz; ++z) {
+      const int rc = rows_finalize(bias_in ? bo[z] : bi[z], pbz[z], cvec_next ? pcz[z] : nullptr, nchunks, M, bo[z],
+                                   cvec_next ? co[z] : nullptr, stream);
+      if (rc) return rc;
+    }
+    return BF_OK;
+  }
   const int nparts = gemm_partial_count(P);
   GemmArgs a;
   memset(&a, 0, sizeof(a));

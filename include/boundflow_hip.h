@@ -152,7 +152,10 @@ int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t 
  * W_t: the layer weight transposed, [P, N] row-major.  relax_next: table of
  * bf_relu_relax_table over the P columns ([D, P]).  Rows of one 128-row tile
  * spanning more than its LDS stage holds (10 domains with a relaxation prologue
- * and S >= 15, else 18) read the tables from global memory.
+ * and S >= 15, else 18) read the tables from global memory.  A short contraction
+ * (N <= 16, e.g. the spec rows times the output layer) with no prologue table or
+ * split term runs on the VALU instead of the tiled MFMA kernel (P % 4 == 0,
+ * 16-byte aligned outputs).
  * workspace: bf_crown_relu_linear_relu_fwd_workspace(D, S, P) floats. */
 int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
                                   int64_t N, const float* relax, const float* add_l, int64_t add_ld,

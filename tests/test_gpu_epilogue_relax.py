@@ -42,18 +42,24 @@ def _table(lo, hi, alpha, dev):
 
 
 # S = 20 and 40: a 128-row tile spans <= 10 domains (entries staged in LDS);
-# S = 9: up to 16 domains per tile (entries read from global memory).
-@pytest.mark.parametrize("S,prologue,alpha,add,cvec", [
-    (20, True, True, True, True),
-    (20, False, False, False, False),
-    (9, True, False, True, True),
-    (40, False, True, True, False),
+# S = 9: up to 16 domains per tile (entries read from global memory).  N <= 16 with no
+# prologue relaxation: the short-contraction kernel (a wave per domain and 256 columns;
+# P = 300 gives two column chunks, the second partial), with or without the region's bias.
+@pytest.mark.parametrize("S,prologue,alpha,add,cvec,N,bias_only", [
+    (20, True, True, True, True, 150, False),
+    (20, False, False, False, False, 150, False),
+    (9, True, False, True, True, 150, False),
+    (40, False, True, True, False, 150, False),
+    (9, False, True, True, True, 10, True),
+    (20, False, False, False, False, 16, False),
+    (3, False, True, False, True, 7, True),
 ])
-def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec):
+def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec, N, bias_only):
     dev = device()
-    announce(f"relax epilogue step S={S} prologue={prologue} alpha={alpha} add={add} cvec={cvec}")
-    g = torch.Generator().manual_seed(S * 3 + prologue)
-    D, N, P = 13, 150, 300
+    announce(f"relax epilogue step S={S} N={N} prologue={prologue} bias_only={bias_only} alpha={alpha} add={add} "
+             f"cvec={cvec}")
+    g = torch.Generator().manual_seed(S * 3 + prologue + N)
+    D, P = 13, 300
     A_u = torch.randn(D, S, N, generator=g)
     A_l = torch.randn(D, S, N, generator=g)
     l1, u1 = _pre(D, N, g)
@@ -76,6 +82,9 @@ def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec):
         Au, Al, bu, bl = cr.relu_backward_dense(
             Au, Al, bu, bl, pre=cr.IntervalState(f(l1), f(u1)), name="h1",
             relu_alpha=None if a1 is None else {"h1": f(a1)}, add_l=None if add1 is None else {"h1": f(add1)})
+        bu = bu + Au @ f(bias1)
+        bl = bl + Al @ f(bias1)
+    elif bias_only:
         bu = bu + Au @ f(bias1)
         bl = bl + Al @ f(bias1)
     Cu, Cl = Au @ f(W), Al @ f(W)
@@ -102,7 +111,7 @@ def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec):
     Pre_l = torch.empty(M, P, device=dev) if alpha else None
     _lib.call("bf_crown_relu_linear_relu_fwd", _lib.ptr(Au_d), _lib.ptr(Al_d), S * N, D, S, N, _lib.ptr(t1),
               _lib.ptr(add1_d if prologue else None), N, _lib.ptr(Wt_d), P,
-              _lib.ptr(bias1_d if prologue else None), _lib.ptr(bu_d), _lib.ptr(bl_d), _lib.ptr(t2),
+              _lib.ptr(bias1_d if prologue or bias_only else None), _lib.ptr(bu_d), _lib.ptr(bl_d), _lib.ptr(t2),
               _lib.ptr(add2_d), P, _lib.ptr(bias2_d), _lib.ptr(cv_d), P, _lib.ptr(ws), _lib.ptr(An_u),
               _lib.ptr(An_l), _lib.ptr(Pre_u), _lib.ptr(Pre_l), _lib.ptr(bo_u), _lib.ptr(bo_l), _lib.ptr(co_u),
               _lib.ptr(co_l), _lib.stream_handle())
@@ -116,9 +125,9 @@ def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec):
         announce(f"  {what}: max abs err {float(err.max()):.3e}")
         assert bool((err <= tolC).all()), f"{what}: {float((err / tolC).max()):.3f} x tolerance"
     scale_u = (Cu.abs() @ torch.ones(P, dtype=torch.float64) * 2 + Cu2.abs() @ f(bias2).abs() + bu.abs()
-               + (absA @ f(bias1).abs() if prologue else 0) + 1.0)
+               + (absA @ f(bias1).abs() if prologue or bias_only else 0) + 1.0)
     scale_l = (Cl.abs() @ torch.ones(P, dtype=torch.float64) * 2 + Cl2.abs() @ f(bias2).abs() + bl.abs()
-               + (absA @ f(bias1).abs() if prologue else 0) + 1.0)
+               + (absA @ f(bias1).abs() if prologue or bias_only else 0) + 1.0)
     for got, ref, sc, what in ((bo_u, bu2, scale_u, "b upper"), (bo_l, bl2, scale_l, "b lower")):
         err = (got.cpu().double().reshape(D, S) - ref).abs()
         tol = (N + P) * 2.0 ** -22 * sc
