@@ -71,4 +71,23 @@ __device__ __forceinline__ Relax relu_relax(float l, float u, bool has_alpha, fl
 
 __device__ __forceinline__ float clamp01(float x) { return fminf(fmaxf(x, 0.f), 1.f); }
 
+// Sum over the 64 lanes of a wave in a fixed order (pairs, quads, half rows and
+// rows of 16 by DPP, then the row broadcasts that gather the total in lane 63),
+// returned to every lane.  Cheaper than a butterfly of ds_bpermute shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0xb1, 0xf, 0xf, false);    // quad_perm [1, 0, 3, 2]
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x4e, 0xf, 0xf, false);    // quad_perm [2, 3, 0, 1]
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x141, 0xf, 0xf, false);   // row_half_mirror
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x140, 0xf, 0xf, false);   // row_mirror
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x142, 0xa, 0xf, false);   // row_bcast:15 into rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x143, 0xc, 0xf, false);   // row_bcast:31 into rows 2 and 3
+  // readlane moves 32-bit integers: the float travels as its bit pattern
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// m / d for 0 <= m, d > 0, in 32-bit arithmetic when both fit (uniform over a launch)
+__device__ __forceinline__ int64_t div_rows(int64_t m, int64_t d, bool fits32) {
+  return fits32 ? (int64_t)((uint32_t)m / (uint32_t)d) : m / d;
+}
+
 }  // namespace bf

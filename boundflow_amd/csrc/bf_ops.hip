@@ -372,7 +372,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
   const bool live = m < M;   // uniform per wave (TPR >= 64)
   float s[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // su, sl, ku, kl, cu, cl
   if (live) {
-    const int64_t d = m / S;
+    const int64_t d = div_rows(m, S, M < (1LL << 31));
     const int64_t a_row = d * a_dstride + (m - d * S) * K;   // input row (shared by all domains when a_dstride = 0)
     for (int64_t k = 4 * (int64_t)t; k < K; k += 4 * TPR) {
       float4 r[4];
@@ -415,9 +415,11 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
       }
     }
   }
+  // the sums this call needs (conditions uniform over the launch)
+  const bool need[6] = {Au != nullptr, Al != nullptr, Au && kbias, Al && kbias, Au && cvec, Al && cvec};
 #pragma unroll
   for (int q = 0; q < 6; ++q)
-    for (int off = 32; off >= 1; off >>= 1) s[q] += __shfl_xor(s[q], off, 64);
+    if (need[q]) s[q] = wave_sum(s[q]);
   if (WPR > 1) {
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0)
