@@ -57,6 +57,7 @@ SIGNATURES = {
     "bf_ibp_batched_linear": (I32, [P, P, I64, I64, P, P, I64, P, P, P]),
     "bf_branch_update": (I32, [P, P, I64, I64, I32, P, P, P, P]),
     "bf_adam_clamp_step": (I32, [P, P, P, P, I64, F64, F64, F64, F32, I32, F32, F32, I32, P]),
+    "bf_adam_clamp_multi": (I32, [I32, P, P, P, P, P, P, P, P, F64, F64, F64, F32, I32, P]),
     "bf_conv2d_rows": (I32, [P, I64, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P, P,
                              I64, I64, P]),
     "bf_conv_transpose_rows": (I32, [P, P, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P,
@@ -66,8 +67,10 @@ SIGNATURES = {
     "bf_ibp_conv2d_workspace": (I64, [I64, I64, I64]),
     "bf_relu_grad": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, P, I64, P, P, P, P]),
     "bf_beta_coeff": (I32, [P, I64, P, I64, I64, I64, P, P]),
+    "bf_beta_coeff_multi": (I32, [I32, P, P, P, P, P, I64, P, P]),
     "bf_best_update": (I32, [P, P, I64, I64, P, P, P, P, I32, P]),
     "bf_masked_copy_rows": (I32, [P, P, I64, I64, P, P]),
+    "bf_masked_copy_rows_multi": (I32, [I32, P, P, P, I64, P, P]),
     "bf_sum_rows": (I32, [P, I64, I64, P, P]),
     "bf_concretize_finalize": (I32, [P, P, I32, I64, P, P, P, P, F32, P, P, P]),
     "bf_alpha_from_crown": (I32, [P, P, I64, P, P]),
@@ -117,6 +120,37 @@ def ptr(t: Optional[torch.Tensor]):
     if t is None:
         return None
     return DevicePtr(t)
+
+
+class HostArray:
+    """A host array argument of a multi-tensor entry point (device pointers or
+    sizes); keeps the tensors whose addresses it holds alive."""
+
+    def __init__(self, ctype, values, keep=()):
+        self.buf = (ctype * max(1, len(values)))(*values)
+        self.keep = tuple(keep)
+
+    @property
+    def _as_parameter_(self):
+        return ctypes.cast(self.buf, ctypes.c_void_p)
+
+
+def ptr_array(tensors) -> HostArray:
+    """Host array of the device addresses of ``tensors`` (None -> NULL)."""
+    return HostArray(ctypes.c_void_p, [None if t is None else t.data_ptr() for t in tensors],
+                     keep=[t for t in tensors if t is not None])
+
+
+def i64_array(values) -> HostArray:
+    return HostArray(ctypes.c_int64, [int(v) for v in values])
+
+
+def i32_array(values) -> HostArray:
+    return HostArray(ctypes.c_int32, [int(v) for v in values])
+
+
+def f32_array(values) -> HostArray:
+    return HostArray(ctypes.c_float, [float(v) for v in values])
 
 
 def stream_handle(stream: Optional[torch.cuda.Stream] = None):

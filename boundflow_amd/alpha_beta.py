@@ -70,20 +70,26 @@ class AlphaBetaStats:
         return [None if lay[i] < 0 else (self.relu_names[lay[i]], int(ids[i])) for i in range(len(lay))]
 
 
-class _Adam:
-    """Device-resident Adam state for one parameter tensor."""
+class _AdamGroup:
+    """Device-resident Adam state of several parameter tensors, stepped together in
+    one launch (the reference runs one torch.optim.Adam over every alpha and beta,
+    alpha_beta_crown.py:747); each tensor has its own clamp after the step."""
 
-    def __init__(self, p: torch.Tensor):
-        self.p = p
-        self.m = torch.zeros_like(p)
-        self.v = torch.zeros_like(p)
+    def __init__(self, params: List[torch.Tensor], clamps: List[Tuple[float, Optional[float]]]):
+        self.p = params
+        self.m = [torch.zeros_like(t) for t in params]
+        self.v = [torch.zeros_like(t) for t in params]
         self.t = 0
+        self.args = (_lib.ptr_array(self.p), _lib.ptr_array(self.m), _lib.ptr_array(self.v))
+        self.n = _lib.i64_array([t.numel() for t in params])
+        self.lo = _lib.f32_array([lo for lo, _hi in clamps])
+        self.hi = _lib.f32_array([0.0 if hi is None else hi for _lo, hi in clamps])
+        self.has_hi = _lib.i32_array([0 if hi is None else 1 for _lo, hi in clamps])
 
-    def step(self, grad: torch.Tensor, lr: float, lo: float, hi: Optional[float], stream) -> None:
+    def step(self, grads: List[torch.Tensor], lr: float, stream) -> None:
         self.t += 1
-        _lib.call("bf_adam_clamp_step", _lib.ptr(self.p), _lib.ptr(self.m), _lib.ptr(self.v), _lib.ptr(grad),
-                  self.p.numel(), float(lr), 0.9, 0.999, 1e-8, self.t, float(lo), float(hi or 0.0),
-                  1 if hi is not None else 0, stream)
+        _lib.call("bf_adam_clamp_multi", len(self.p), *self.args, _lib.ptr_array(grads), self.n, self.lo, self.hi,
+                  self.has_hi, float(lr), 0.9, 0.999, 1e-8, self.t, stream)
 
 
 def branch_choices(trace: ForwardTrace, batch: int) -> List[Optional[Tuple[str, int]]]:
@@ -268,8 +274,9 @@ def run_alpha_beta_crown_mlp(
     # d(-sum_d mean_s lb)/dlb = -1/S ; d(-mean_d mean_s lb)/dlb = (-1/B)/S   (fp32, as autograd divides)
     g_row = np.float32(-1.0) / np.float32(S) if per_batch_params else (np.float32(-1.0) / np.float32(B)) / np.float32(S)
     G = torch.full((M,), float(g_row), device=dev, dtype=torch.float32)
-    adam_a = {n: _Adam(alpha[n]) for n in names}
-    adam_b = {n: _Adam(beta[n]) for n in names}
+    # one optimizer over every alpha (clamped to [0, 1]) and every split multiplier (>= 0)
+    adam = _AdamGroup([alpha[n] for n in names] + [beta[n] for n in beta_names],
+                      [(0.0, 1.0)] * len(names) + [(0.0, None)] * len(beta_names))
     best_metric = torch.empty(B, device=dev)
     best_lb = torch.empty(B, S, device=dev)
     improved = torch.empty(B, dtype=torch.int32, device=dev)
@@ -277,11 +284,16 @@ def run_alpha_beta_crown_mlp(
     best_beta = {n: beta[n].clone() for n in names}
     best_scalar = None
     add = {n: torch.empty(B, numel[n], device=dev) for n in beta_names}
+    beta_args = (_lib.ptr_array([beta[n] for n in beta_names]), _lib.i64_array([p_ld[n] for n in beta_names]),
+                 _lib.ptr_array([splits[n][0] for n in beta_names]), _lib.i64_array([splits[n][1] for n in beta_names]),
+                 _lib.i64_array([numel[n] for n in beta_names]), B, _lib.ptr_array([add[n] for n in beta_names]))
+    # the best-of copy: alpha of every ReLU, beta of those that move (the others keep their initial value)
+    copy_dst = [best_alpha[n] for n in names] + [best_beta[n] for n in beta_names]
+    copy_args = (_lib.ptr_array(copy_dst), _lib.ptr_array([alpha[n] for n in names] + [beta[n] for n in beta_names]),
+                 _lib.i64_array([numel[n] for n in names] + [numel[n] for n in beta_names]), B, _lib.ptr(improved))
     for step in range(int(steps) + 1):
-        for n in beta_names:
-            s, sld = splits[n]
-            _lib.call("bf_beta_coeff", _lib.ptr(beta[n]), p_ld[n], _lib.ptr(s), sld, B, numel[n], _lib.ptr(add[n]),
-                      stream)
+        if beta_names:
+            _lib.call("bf_beta_coeff_multi", len(beta_names), *beta_args, stream)
         saved = {"grad_rows": G} if step < int(steps) else None
         # lower bound only: the objective and the best-of rule read nothing else
         bounds = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C,
@@ -290,11 +302,7 @@ def run_alpha_beta_crown_mlp(
         if per_batch_params:
             _lib.call("bf_best_update", _lib.ptr(bounds.lower), None, B, S, _lib.ptr(best_metric),
                       _lib.ptr(best_lb), None, _lib.ptr(improved), 1 if step == 0 else 0, stream)
-            for n in names:
-                _lib.call("bf_masked_copy_rows", _lib.ptr(best_alpha[n]), _lib.ptr(alpha[n]), B, numel[n],
-                          _lib.ptr(improved), stream)
-                _lib.call("bf_masked_copy_rows", _lib.ptr(best_beta[n]), _lib.ptr(beta[n]), B, numel[n],
-                          _lib.ptr(improved), stream)
+            _lib.call("bf_masked_copy_rows_multi", len(copy_dst), *copy_args, stream)
         else:
             metric = float(bounds.lower.mean().item())
             if best_scalar is None or metric > best_scalar:
@@ -307,17 +315,13 @@ def run_alpha_beta_crown_mlp(
             break
         a_arg = {n: (alpha[n], p_ld[n]) for n in names}
         g_alpha, g_beta = _grad_pass(spec, chain, trace, saved, B, S, a_arg, splits, G)
-        for n in names:
-            ga, gb = g_alpha[n], g_beta[n]
-            if not per_batch_params:
-                ra = torch.empty(numel[n], device=dev)
-                rb = torch.empty(numel[n], device=dev)
-                _lib.call("bf_sum_rows", _lib.ptr(ga), B, numel[n], _lib.ptr(ra), stream)
-                _lib.call("bf_sum_rows", _lib.ptr(gb), B, numel[n], _lib.ptr(rb), stream)
-                ga, gb = ra, rb
-            adam_a[n].step(ga, lr, 0.0, 1.0, stream)
-            if n in beta_names:
-                adam_b[n].step(gb, lr, 0.0, None, stream)
+        if not per_batch_params:
+            for d in (g_alpha, g_beta):
+                for n in names:
+                    r = torch.empty(numel[n], device=dev)
+                    _lib.call("bf_sum_rows", _lib.ptr(d[n]), B, numel[n], _lib.ptr(r), stream)
+                    d[n] = r
+        adam.step([g_alpha[n] for n in names] + [g_beta[n] for n in beta_names], lr, stream)
     # The reference keeps the upper bound of the evaluation that gave the best lower
     # bound.  The upper bound depends on alpha alone (beta enters the lower bound
     # only) and every domain's rows on that domain's parameters alone, so one upper

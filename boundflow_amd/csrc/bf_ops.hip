@@ -541,11 +541,10 @@ __global__ void branch_update_kernel(const float* __restrict__ lo, const float* 
 // clamp_(lo, hi), applied in place.  Matches the single-tensor update order:
 //   m = lerp(m, g, 1 - b1); v = v * b2 + (1 - b2) * g * g;
 //   p -= (lr / (1 - b1^t)) * m / (sqrt(v) / sqrt(1 - b2^t) + eps)
-__global__ void adam_clamp_kernel(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
-                                  const float* __restrict__ g, int64_t n, float w1, float b2, float w2, float eps,
-                                  float neg_step, float bc2_sqrt, float lo, float hi, int clamp_hi) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+__device__ __forceinline__ void adam_clamp_one(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
+                                               const float* __restrict__ g, int64_t i, float w1, float b2, float w2,
+                                               float eps, float neg_step, float bc2_sqrt, float lo, float hi,
+                                               int clamp_hi) {
   const float gi = g[i];
   float mi = m[i];
   // exp_avg.lerp_(grad, 1 - beta1): torch's vectorized CPU lerp is fma(w, g - m, m) for w < 0.5
@@ -559,6 +558,86 @@ __global__ void adam_clamp_kernel(float* __restrict__ p, float* __restrict__ m, 
   pi = fmaxf(pi, lo);
   if (clamp_hi) pi = fminf(pi, hi);
   p[i] = pi;
+}
+
+__global__ void adam_clamp_kernel(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
+                                  const float* __restrict__ g, int64_t n, float w1, float b2, float w2, float eps,
+                                  float neg_step, float bc2_sqrt, float lo, float hi, int clamp_hi) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  adam_clamp_one(p, m, v, g, i, w1, b2, w2, eps, neg_step, bc2_sqrt, lo, hi, clamp_hi);
+}
+
+// Several tensors in one launch.  Workgroups are dealt to the tensors in order
+// (tensor s owns blocks bstart[s] .. bstart[s + 1] - 1), so a workgroup's tensor
+// is uniform and its pointers are scalar loads.
+constexpr int BF_SEG_MAX = 16;
+
+struct AdamSegs {
+  float* p[BF_SEG_MAX];
+  float* m[BF_SEG_MAX];
+  float* v[BF_SEG_MAX];
+  const float* g[BF_SEG_MAX];
+  int64_t n[BF_SEG_MAX];
+  float lo[BF_SEG_MAX], hi[BF_SEG_MAX];
+  int clamp_hi[BF_SEG_MAX];
+  int64_t bstart[BF_SEG_MAX + 1];
+  int count;
+};
+
+__device__ __forceinline__ int seg_of_block(const int64_t* bstart, int count) {
+  int s = 0;
+  while (s + 1 < count && (int64_t)blockIdx.x >= bstart[s + 1]) ++s;
+  return s;
+}
+
+__global__ void adam_clamp_multi_kernel(AdamSegs a, float w1, float b2, float w2, float eps, float neg_step,
+                                        float bc2_sqrt) {
+  const int s = seg_of_block(a.bstart, a.count);
+  const int64_t i = ((int64_t)blockIdx.x - a.bstart[s]) * 256 + threadIdx.x;
+  if (i >= a.n[s]) return;
+  adam_clamp_one(a.p[s], a.m[s], a.v[s], a.g[s], i, w1, b2, w2, eps, neg_step, bc2_sqrt, a.lo[s], a.hi[s],
+                 a.clamp_hi[s]);
+}
+
+// dst[s][d, j] = src[s][d, j] where mask[d] (the best-of copy of several parameters)
+struct CopySegs {
+  float* dst[BF_SEG_MAX];
+  const float* src[BF_SEG_MAX];
+  int64_t ncol[BF_SEG_MAX];
+  int64_t bstart[BF_SEG_MAX + 1];
+  int count;
+};
+
+__global__ void masked_copy_rows_multi_kernel(CopySegs c, int64_t D, const int* __restrict__ mask) {
+  const int s = seg_of_block(c.bstart, c.count);
+  const int64_t i = ((int64_t)blockIdx.x - c.bstart[s]) * 256 + threadIdx.x;
+  const int64_t N = c.ncol[s];
+  if (i >= D * N) return;
+  if (mask[i / N]) c.dst[s][i] = c.src[s][i];
+}
+
+// out[s][d, j] = -beta[s][d, j] * split[s][d, j] * 1(split != 0) for several ReLUs
+struct BetaSegs {
+  const float* beta[BF_SEG_MAX];
+  int64_t beta_ld[BF_SEG_MAX];
+  const int8_t* split[BF_SEG_MAX];
+  int64_t split_ld[BF_SEG_MAX];
+  int64_t ncol[BF_SEG_MAX];
+  float* out[BF_SEG_MAX];
+  int64_t bstart[BF_SEG_MAX + 1];
+  int count;
+};
+
+__global__ void beta_coeff_multi_kernel(BetaSegs b, int64_t D) {
+  const int s = seg_of_block(b.bstart, b.count);
+  const int64_t i = ((int64_t)blockIdx.x - b.bstart[s]) * 256 + threadIdx.x;
+  const int64_t N = b.ncol[s];
+  if (i >= D * N) return;
+  const int64_t d = i / N, n = i - d * N;
+  const int8_t sp = b.split[s][d * b.split_ld[s] + n];
+  const float sf = (float)sp;
+  b.out[s][i] = (-b.beta[s][d * b.beta_ld[s] + n] * sf) * (sp != 0 ? 1.f : 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1291,6 +1370,101 @@ int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, 
   hipLaunchKernelGGL(adam_clamp_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, p, m, v, g, n, w1,
                      beta2, w2, eps, neg_step, bc2_sqrt, clamp_lo, clamp_hi, has_clamp_hi);
   BF_LAUNCH_CHECK("adam_clamp_kernel");
+  return BF_OK;
+}
+
+static void adam_consts(double lr, double beta1, double beta2, int step, float* w1, float* w2, float* neg_step,
+                        float* bc2_sqrt) {
+  // bias corrections in double then rounded, as torch computes them from Python floats
+  const double bc1 = 1.0 - __builtin_pow((double)beta1, (double)step);
+  const double bc2 = 1.0 - __builtin_pow((double)beta2, (double)step);
+  *neg_step = (float)(-((double)lr / bc1));
+  *bc2_sqrt = (float)__builtin_sqrt(bc2);
+  *w1 = (float)(1.0 - (double)beta1);
+  *w2 = (float)(1.0 - (double)beta2);
+}
+
+int bf_adam_clamp_multi(int count, float* const* p, float* const* m, float* const* v, const float* const* g,
+                        const int64_t* n, const float* clamp_lo, const float* clamp_hi, const int* has_clamp_hi,
+                        double lr, double beta1, double beta2, float eps, int step, hipStream_t stream) {
+  BF_REQUIRE(count >= 0 && step >= 1, "bf_adam_clamp_multi: bad arguments");
+  BF_REQUIRE(count == 0 || (p && m && v && g && n && clamp_lo && clamp_hi && has_clamp_hi),
+             "bf_adam_clamp_multi: null array");
+  float w1, w2, neg_step, bc2_sqrt;
+  adam_consts(lr, beta1, beta2, step, &w1, &w2, &neg_step, &bc2_sqrt);
+  for (int base = 0; base < count; base += BF_SEG_MAX) {
+    AdamSegs a;
+    memset(&a, 0, sizeof(a));
+    a.count = count - base < BF_SEG_MAX ? count - base : BF_SEG_MAX;
+    int64_t blocks = 0;
+    for (int t = 0; t < a.count; ++t) {
+      const int k = base + t;
+      BF_REQUIRE(n[k] >= 0 && (n[k] == 0 || (p[k] && m[k] && v[k] && g[k])), "bf_adam_clamp_multi: tensor %d", k);
+      a.p[t] = p[k]; a.m[t] = m[k]; a.v[t] = v[k]; a.g[t] = g[k]; a.n[t] = n[k];
+      a.lo[t] = clamp_lo[k]; a.hi[t] = clamp_hi[k]; a.clamp_hi[t] = has_clamp_hi[k];
+      a.bstart[t] = blocks;
+      blocks += ceil_div(n[k], 256);
+    }
+    a.bstart[a.count] = blocks;
+    if (blocks == 0) continue;
+    BF_REQUIRE(blocks < (1LL << 31), "bf_adam_clamp_multi: too many elements");
+    hipLaunchKernelGGL(adam_clamp_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a, w1, (float)beta2,
+                       w2, eps, neg_step, bc2_sqrt);
+    BF_LAUNCH_CHECK("adam_clamp_multi_kernel");
+  }
+  return BF_OK;
+}
+
+int bf_masked_copy_rows_multi(int count, float* const* dst, const float* const* src, const int64_t* ncol, int64_t D,
+                              const int* mask, hipStream_t stream) {
+  BF_REQUIRE(count >= 0 && D >= 0, "bf_masked_copy_rows_multi: bad arguments");
+  BF_REQUIRE(count == 0 || D == 0 || (dst && src && ncol && mask), "bf_masked_copy_rows_multi: null array");
+  for (int base = 0; base < count; base += BF_SEG_MAX) {
+    CopySegs c;
+    memset(&c, 0, sizeof(c));
+    c.count = count - base < BF_SEG_MAX ? count - base : BF_SEG_MAX;
+    int64_t blocks = 0;
+    for (int t = 0; t < c.count; ++t) {
+      const int k = base + t;
+      BF_REQUIRE(ncol[k] > 0 && dst[k] && src[k], "bf_masked_copy_rows_multi: tensor %d", k);
+      c.dst[t] = dst[k]; c.src[t] = src[k]; c.ncol[t] = ncol[k];
+      c.bstart[t] = blocks;
+      blocks += ceil_div(D * ncol[k], 256);
+    }
+    c.bstart[c.count] = blocks;
+    if (blocks == 0) continue;
+    BF_REQUIRE(blocks < (1LL << 31), "bf_masked_copy_rows_multi: too many elements");
+    hipLaunchKernelGGL(masked_copy_rows_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, c, D, mask);
+    BF_LAUNCH_CHECK("masked_copy_rows_multi_kernel");
+  }
+  return BF_OK;
+}
+
+int bf_beta_coeff_multi(int count, const float* const* beta, const int64_t* beta_ld, const int8_t* const* split,
+                        const int64_t* split_ld, const int64_t* ncol, int64_t D, float* const* out,
+                        hipStream_t stream) {
+  BF_REQUIRE(count >= 0 && D >= 0, "bf_beta_coeff_multi: bad arguments");
+  BF_REQUIRE(count == 0 || D == 0 || (beta && beta_ld && split && split_ld && ncol && out),
+             "bf_beta_coeff_multi: null array");
+  for (int base = 0; base < count; base += BF_SEG_MAX) {
+    BetaSegs b;
+    memset(&b, 0, sizeof(b));
+    b.count = count - base < BF_SEG_MAX ? count - base : BF_SEG_MAX;
+    int64_t blocks = 0;
+    for (int t = 0; t < b.count; ++t) {
+      const int k = base + t;
+      BF_REQUIRE(ncol[k] > 0 && beta[k] && split[k] && out[k], "bf_beta_coeff_multi: tensor %d", k);
+      b.beta[t] = beta[k]; b.beta_ld[t] = beta_ld[k]; b.split[t] = split[k]; b.split_ld[t] = split_ld[k];
+      b.ncol[t] = ncol[k]; b.out[t] = out[k];
+      b.bstart[t] = blocks;
+      blocks += ceil_div(D * ncol[k], 256);
+    }
+    b.bstart[b.count] = blocks;
+    if (blocks == 0) continue;
+    BF_REQUIRE(blocks < (1LL << 31), "bf_beta_coeff_multi: too many elements");
+    hipLaunchKernelGGL(beta_coeff_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, b, D);
+    BF_LAUNCH_CHECK("beta_coeff_multi_kernel");
+  }
   return BF_OK;
 }
 

@@ -269,12 +269,22 @@ int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t 
 /* beta split coefficient add = -beta * s * 1(s != 0) (runtime/alpha_beta_crown.py:615-640). */
 int bf_beta_coeff(const float* beta, int64_t beta_ld, const int8_t* split, int64_t split_ld, int64_t D, int64_t N,
                   float* out, hipStream_t stream);
+/* The same for `count` ReLUs in one launch (host arrays of device pointers and sizes; D rows each). */
+int bf_beta_coeff_multi(int count, const float* const* beta, const int64_t* beta_ld, const int8_t* const* split,
+                        const int64_t* split_ld, const int64_t* ncol, int64_t D, float* const* out,
+                        hipStream_t stream);
 
 /* torch.optim.Adam step (no weight decay / amsgrad) then clamp to [lo, hi]
  * (hi only when has_clamp_hi), in place (runtime/alpha_beta_crown.py:747, 918-923). */
 int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, double lr, double beta1,
                        double beta2, float eps, int step, float clamp_lo, float clamp_hi, int has_clamp_hi,
                        hipStream_t stream);
+/* The same step for `count` parameter tensors in one launch (one optimizer over all of them, as the
+ * reference's single torch.optim.Adam over every alpha and beta; host arrays of device pointers, sizes
+ * and per-tensor clamps). */
+int bf_adam_clamp_multi(int count, float* const* p, float* const* m, float* const* v, const float* const* g,
+                        const int64_t* n, const float* clamp_lo, const float* clamp_hi, const int* has_clamp_hi,
+                        double lr, double beta1, double beta2, float eps, int step, hipStream_t stream);
 
 /* Per-domain best-of tracking on mean_s lb (runtime/alpha_beta_crown.py:840-876).  ub and best_ub may
  * both be NULL: the lower bounds alone are tracked (the caller then evaluates the upper bound once, with
@@ -282,6 +292,9 @@ int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, 
 int bf_best_update(const float* lb, const float* ub, int64_t D, int64_t S, float* best_metric, float* best_lb,
                    float* best_ub, int* improved, int first, hipStream_t stream);
 int bf_masked_copy_rows(float* dst, const float* src, int64_t D, int64_t N, const int* mask, hipStream_t stream);
+/* The best-of copy for `count` parameter tensors of D rows in one launch (host arrays). */
+int bf_masked_copy_rows_multi(int count, float* const* dst, const float* const* src, const int64_t* ncol, int64_t D,
+                              const int* mask, hipStream_t stream);
 
 /* out[n] = sum_d x[d, n] (gradient of a parameter shared by all domains). */
 int bf_sum_rows(const float* x, int64_t D, int64_t N, float* out, hipStream_t stream);

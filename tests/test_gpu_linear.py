@@ -385,3 +385,53 @@ def test_adam_clamp_matches_torch():
         torch.cuda.synchronize()
         # torch's CPU kernels mix fused and unfused multiply-adds; agree to a few ulps
         assert torch.allclose(pd.cpu(), p.detach(), rtol=1e-6, atol=1e-7), float((pd.cpu() - p.detach()).abs().max())
+
+
+def test_multi_tensor_steps_equal_single_tensor_steps():
+    """bf_adam_clamp_multi, bf_masked_copy_rows_multi and bf_beta_coeff_multi give, tensor
+    by tensor, bit for bit what the single-tensor entry points give (18 tensors: two
+    launches of the multi kernels; sizes not multiples of the workgroup)."""
+    dev = device()
+    announce("multi-tensor Adam / best-of copy / split term")
+    g = torch.Generator().manual_seed(21)
+    st = _lib.stream_handle()
+    D = 37
+    cols = [3 + 41 * i for i in range(18)]
+    P = [torch.rand(D, c, generator=g).to(dev) for c in cols]
+    G = [torch.randn(D, c, generator=g).to(dev) for c in cols]
+    clamps = [(0.0, 1.0) if i % 2 == 0 else (0.0, None) for i in range(len(cols))]
+    P1 = [t.clone() for t in P]
+    M0 = [torch.zeros_like(t) for t in P]
+    V0 = [torch.zeros_like(t) for t in P]
+    M1 = [torch.zeros_like(t) for t in P]
+    V1 = [torch.zeros_like(t) for t in P]
+    for step in (1, 2, 3):
+        for i, t in enumerate(P):
+            lo, hi = clamps[i]
+            _lib.call("bf_adam_clamp_step", _lib.ptr(t), _lib.ptr(M0[i]), _lib.ptr(V0[i]), _lib.ptr(G[i]), t.numel(),
+                      0.2, 0.9, 0.999, 1e-8, step, lo, hi or 0.0, 0 if hi is None else 1, st)
+        _lib.call("bf_adam_clamp_multi", len(P1), _lib.ptr_array(P1), _lib.ptr_array(M1), _lib.ptr_array(V1),
+                  _lib.ptr_array(G), _lib.i64_array([t.numel() for t in P1]), _lib.f32_array([c[0] for c in clamps]),
+                  _lib.f32_array([c[1] or 0.0 for c in clamps]), _lib.i32_array([0 if c[1] is None else 1 for c in clamps]),
+                  0.2, 0.9, 0.999, 1e-8, step, st)
+    torch.cuda.synchronize()
+    for i in range(len(P)):
+        assert torch.equal(P[i], P1[i]) and torch.equal(M0[i], M1[i]) and torch.equal(V0[i], V1[i]), f"adam tensor {i}"
+    mask = (torch.rand(D, generator=g) > 0.5).to(torch.int32).to(dev)
+    dst0 = [torch.zeros_like(t) for t in P]
+    dst1 = [torch.zeros_like(t) for t in P]
+    for i, t in enumerate(P):
+        _lib.call("bf_masked_copy_rows", _lib.ptr(dst0[i]), _lib.ptr(t), D, cols[i], _lib.ptr(mask), st)
+    _lib.call("bf_masked_copy_rows_multi", len(P), _lib.ptr_array(dst1), _lib.ptr_array(P), _lib.i64_array(cols), D,
+              _lib.ptr(mask), st)
+    splits = [torch.randint(-1, 2, (D, c), generator=g, dtype=torch.int8).to(dev) for c in cols]
+    out0 = [torch.empty_like(t) for t in P]
+    out1 = [torch.empty_like(t) for t in P]
+    for i, t in enumerate(P):
+        _lib.call("bf_beta_coeff", _lib.ptr(t), cols[i], _lib.ptr(splits[i]), cols[i], D, cols[i], _lib.ptr(out0[i]), st)
+    _lib.call("bf_beta_coeff_multi", len(P), _lib.ptr_array(P), _lib.i64_array(cols), _lib.ptr_array(splits),
+              _lib.i64_array(cols), _lib.i64_array(cols), D, _lib.ptr_array(out1), st)
+    torch.cuda.synchronize()
+    for i in range(len(P)):
+        assert torch.equal(dst0[i], dst1[i]), f"masked copy tensor {i}"
+        assert torch.equal(out0[i], out1[i]), f"split term tensor {i}"
