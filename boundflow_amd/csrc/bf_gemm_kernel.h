@@ -360,6 +360,8 @@ gemm_kernel(GemmArgs p) {
     auto mfma_tile = [&](int buf) {
       const float* __restrict__ as = As[buf];
       const float* __restrict__ bs = Bs[buf];
+      // waves with MFMAs to issue go first: the loads and LDS stores of the others fit around them
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int jb = 0; jb < GBK / 2; jb += 4) {
         float av[FM][4];
@@ -385,6 +387,7 @@ gemm_kernel(GemmArgs p) {
               if (FULL || jj < fn_act)
                 acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
       }
+      __builtin_amdgcn_s_setprio(0);
     };
 
     // Prologue: relaxation slices of K tiles 0 and 1, then tile 0 itself.

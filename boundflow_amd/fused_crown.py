@@ -11,6 +11,9 @@ contract unchanged (boundflow/runtime/fused_crown.py):
 * ``fused_crown_graph_fingerprint``                           -- :152-168
 * ``plan_fused_crown_regions`` / ``validate_fused_crown_execution_steps`` -- :178-276
 * ``build_fused_crown_runtime_selection``                     -- :826-847
+* ``HipTaskBackendRegistry``: the typed-registry entry of the HIP backend, the
+  counterpart of ``TVMTaskBackendRegistry.dispatch``
+  (boundflow/runtime/task_backend_dispatch.py:421-495) after its key validation
 
 with one addition: the backend id ``"hip_fused"`` in the step whitelist and the
 runtime selection, mapped to ``HipFusedCrownExecutor``.  That executor accepts
@@ -304,3 +307,66 @@ def build_fused_crown_runtime_selection(ops: Sequence[Any], *, backend: str,
         raise ValueError(f"unsupported fused CROWN runtime backend in the HIP package: {backend}")
     return FusedCrownRuntimeSelection(backend=backend, executor=HipFusedCrownExecutor(),
                                       steps=plan_fused_crown_regions(ops, backend=backend))
+
+
+# The fused Task IR a typed registry hands to this backend: one ReLU relaxation
+# followed by one affine backward op (task_backend_dispatch.py:467-472).
+_FUSED_TASK_KINDS = ("relu_relaxation", ("linear_backward", "conv2d_backward"))
+
+
+@dataclass(frozen=True)
+class _PreparedHipTask:
+    backend: str
+    task_id: str
+    op_ids: Tuple[str, ...]
+    output_value_ids: Tuple[str, ...]
+    capability_id: str
+
+
+class HipTaskBackendRegistry:
+    """Typed-registry entry of the ``"hip_fused"`` backend kind.
+
+    Mirrors what ``TVMTaskBackendRegistry.dispatch`` does once the reference's
+    ``_validate_typed_dispatch`` has checked the dispatch key against the task
+    and plan template (task_backend_dispatch.py:363-402, 435-495): the selected
+    backend candidate must be ``"hip_fused"``, the task must be the fused
+    ReLU -> Linear / Conv2d pair, a prepared task is cached by the key's stable
+    hash (a different task under the same hash is rejected as a collision), and
+    the region runs through the session with ``HipFusedCrownExecutor``.  The
+    duck-typed arguments are the reference's ``TaskIRUnit``,
+    ``BackendDispatchKey``, ``PlainCrownBoundIRSession`` and ``PlanTemplate``."""
+
+    backend = "hip_fused"
+
+    def __init__(self) -> None:
+        self._prepared: dict = {}
+        self.cache_hits = 0
+        self.cache_misses = 0
+        self._executor = HipFusedCrownExecutor()
+
+    def dispatch(self, task: Any, key: Any, *, session: Any, template: Any):
+        candidates = {c.candidate_id: c for c in template.backend_candidates}
+        candidate = candidates.get(key.backend_candidate_id)
+        if candidate is None:
+            raise ValueError("typed registry dispatch references unknown backend")
+        kind = getattr(candidate.backend, "value", candidate.backend)
+        if kind != self.backend:
+            raise ValueError(f"HIP registry rejects backend: {kind}")
+        kinds = tuple(getattr(op.kind, "value", op.kind) for op in task.op_refs)
+        if not (len(kinds) == 2 and kinds[0] == _FUSED_TASK_KINDS[0] and kinds[1] in _FUSED_TASK_KINDS[1]):
+            raise ValueError("HIP CROWN backend requires fused ReLU->Affine Task IR")
+        prepared = _PreparedHipTask(backend=kind, task_id=task.task_id,
+                                    op_ids=tuple(op.op_id for op in task.op_refs),
+                                    output_value_ids=tuple(task.output_value_ids),
+                                    capability_id=candidate.capability_id)
+        digest = key.stable_hash()
+        cached = self._prepared.get(digest)
+        if cached is None:
+            self._prepared[digest] = prepared
+            self.cache_misses += 1
+        elif cached != prepared:
+            raise ValueError("HIP backend cache key collision or stale task")
+        else:
+            self.cache_hits += 1
+        return session.execute_fused_relu_affine_task(prepared.op_ids, output_value_ids=prepared.output_value_ids,
+                                                      executor=self._executor)
