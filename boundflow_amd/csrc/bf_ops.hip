@@ -381,8 +381,10 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
       const float4 cv = cvec ? *reinterpret_cast<const float4*>(cvec + d * K + k) : make_float4(0.f, 0.f, 0.f, 0.f);
       const float kbv[4] = {kb.x, kb.y, kb.z, kb.w};
       const float cvv[4] = {cv.x, cv.y, cv.z, cv.w};
+      // one load serves both bounds when they share the coefficient (the first region of a C = I query)
+      const float4 vu4 = Au ? *reinterpret_cast<const float4*>(Au + a_row + k) : make_float4(0.f, 0.f, 0.f, 0.f);
       if (Au) {
-        const float4 v4 = *reinterpret_cast<const float4*>(Au + a_row + k);
+        const float4 v4 = vu4;
         const float v[4] = {v4.x, v4.y, v4.z, v4.w};
         float o[4];
 #pragma unroll
@@ -396,7 +398,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
         *reinterpret_cast<float4*>(Au_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
       }
       if (Al) {
-        const float4 v4 = *reinterpret_cast<const float4*>(Al + a_row + k);
+        const float4 v4 = Al == Au ? vu4 : *reinterpret_cast<const float4*>(Al + a_row + k);
         const float v[4] = {v4.x, v4.y, v4.z, v4.w};
         const float4 ad =
             add_l ? *reinterpret_cast<const float4*>(add_l + d * add_ld + k) : make_float4(0.f, 0.f, 0.f, 0.f);
