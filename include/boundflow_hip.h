@@ -35,10 +35,10 @@ const char* bf_last_error(void);
  * (0: 128x128x16 4 waves, 3 workgroups/CU; 1: 128x128x32; 2: 256x128x16 8 waves;
  * 3: 128x256x16, store epilogue only; 4: 64x128x16 2 waves; 5: 128x128x16 4 waves,
  * 2 workgroups/CU; 6: 128x128x16 8 waves of 32x64; 7: 128x128x32 16 waves of 32x32).
- * The automatic choice: 0 for the fused relaxation + concretization, 7 for the
- * plain prologue with the relaxation epilogue and for the plain concretization
- * with K >= 384, 6 otherwise.  The relaxation epilogue runs on 0, 6 or 7 (1, 2, 4,
- * 5 fall back to 0 for it).  Process-wide. */
+ * The automatic choice: 6 for every form, 7 when the grid has fewer 128 x 128
+ * tiles (times bounds and split-K chunks) than the device has CUs.  The
+ * relaxation epilogue runs on 0, 6 or 7 (1, 2, 4, 5 fall back to 0 for it).
+ * Process-wide. */
 int bf_tuning_set_gemm_tile(int config);
 
 /* ---- kernel #1: IBP ---------------------------------------------------- */
