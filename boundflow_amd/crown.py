@@ -77,9 +77,15 @@ def _pair(v) -> Tuple[int, int]:
     return (v[0], v[0]) if len(v) == 1 else (v[0], v[1])
 
 
+class NotAChain(NotImplementedError):
+    """The task is a DAG (a value read by several ops, add, concat, a ReLU not right
+    after an affine layer): ``crown_dag`` bounds it with the general backward."""
+
+
 def parse_chain(module: BFTaskModule, spec: InputSpec, output_value: Optional[str] = None) -> Chain:
     """Validate that the entry task is a chain of affine/ReLU/flatten ops and
-    collect per-layer shapes.  Raises NotImplementedError otherwise."""
+    collect per-layer shapes.  Raises NotAChain for DAG structure and
+    NotImplementedError for what neither path supports."""
     module.validate()
     task = module.get_entry_task()
     if task.kind != TaskKind.INTERVAL_IBP:
@@ -100,9 +106,9 @@ def parse_chain(module: BFTaskModule, spec: InputSpec, output_value: Optional[st
         if len(op.outputs) != 1:
             raise NotImplementedError(f"multi-output op {op.name}")
         x = op.inputs[0]
-        if x != current:
-            raise NotImplementedError(f"HIP CROWN supports chain graphs only (op {op.name} reads {x})")
         t = op.op_type
+        if x != current or t in ("add", "concat"):
+            raise NotAChain(f"op {op.name} ({t}) makes the task a DAG")
         if t == "linear":
             W = params[op.inputs[1]]
             b = params[op.inputs[2]] if len(op.inputs) == 3 else None
@@ -135,7 +141,7 @@ def parse_chain(module: BFTaskModule, spec: InputSpec, output_value: Optional[st
                                       input_is_relu_of=relu_of.get(x)))
         elif t == "relu":
             if not layers or layers[-1].out_name != x:
-                raise NotImplementedError("HIP CROWN expects every ReLU to follow an affine layer")
+                raise NotAChain("a ReLU that does not follow an affine layer")
             layers[-1].relu_input_of_consumer = True
             relu_of[op.outputs[0]] = x
             relu_names.append(x)
@@ -160,7 +166,7 @@ def parse_chain(module: BFTaskModule, spec: InputSpec, output_value: Optional[st
     if current != output_value:
         raise ValueError(f"output_value {output_value} not produced by the chain")
     if not layers or layers[-1].out_name != output_value:
-        raise NotImplementedError("the output value must be produced by an affine layer")
+        raise NotAChain("the output value is not produced by an affine layer")
     return Chain(layers=layers, relu_names=[r for r in relu_names if r != output_value], output_value=output_value)
 
 
@@ -203,7 +209,13 @@ def forward_ibp_trace(
 ) -> ForwardTrace:
     spec = normalize_input_spec(input_spec)
     if chain is None:
-        chain = parse_chain(module, spec)
+        try:
+            chain = parse_chain(module, spec)
+        except NotAChain:
+            from .crown_dag import forward_ibp_trace_dag
+            return forward_ibp_trace_dag(module, spec, relu_split_state=relu_split_state,
+                                         relu_pre_constraints=relu_pre_constraints,
+                                         raise_on_infeasible=raise_on_infeasible)
     center = spec.center
     _lib.require_device(center, "input center")
     B = int(center.shape[0])
@@ -593,10 +605,18 @@ def run_crown_ibp_mlp(
     relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
     relu_split_state: Optional[Dict[str, torch.Tensor]] = None,
 ) -> IntervalState:
-    """HIP counterpart of run_crown_ibp_mlp (crown_ibp.py:2054-2133)."""
+    """HIP counterpart of run_crown_ibp_mlp (crown_ibp.py:2054-2133).  Chains run the
+    fused region kernels; DAG tasks (add, concat, fan-out) the general backward of
+    ``crown_dag``."""
     _check_alpha_beta_args(relu_pre_add_coeff_u)
     spec = normalize_input_spec(input_spec)
-    chain_full = parse_chain(module, spec)
+    try:
+        chain_full = parse_chain(module, spec)
+    except NotAChain:
+        from .crown_dag import run_crown_ibp_dag
+        return run_crown_ibp_dag(module, spec, linear_spec_C=linear_spec_C, output_value=output_value,
+                                 relu_alpha=relu_alpha, relu_pre_add_coeff_l=relu_pre_add_coeff_l,
+                                 relu_split_state=relu_split_state)
     trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain_full)
     chain = parse_chain(module, spec, output_value) if output_value is not None else chain_full
     return crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=relu_alpha,
@@ -617,6 +637,10 @@ def run_crown_ibp_mlp_from_forward_trace(
     """HIP counterpart of run_crown_ibp_mlp_from_forward_trace (crown_ibp.py:2136-2199)."""
     _check_alpha_beta_args(relu_pre_add_coeff_u)
     spec = normalize_input_spec(input_spec)
+    from .crown_dag import DagTrace, crown_backward_dag
+    if isinstance(trace, DagTrace):
+        return crown_backward_dag(module, spec, trace, linear_spec_C=linear_spec_C, output_value=output_value,
+                                  relu_alpha=relu_alpha, relu_pre_add_coeff_l=relu_pre_add_coeff_l)
     chain = parse_chain(module, spec, output_value)
     return crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=relu_alpha,
                           relu_pre_add_coeff_l=relu_pre_add_coeff_l)

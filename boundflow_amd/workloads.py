@@ -112,6 +112,92 @@ def build_cnn(*, gen: torch.Generator) -> BFTaskModule:
     return _module(ops, params, values)
 
 
+def _bias(n: int, gen: torch.Generator, std: float) -> torch.Tensor:
+    return (torch.randn(n, generator=gen, dtype=torch.float64) * std).to(torch.float32)
+
+
+DAG_KINDS = ("residual_mlp", "projection_skip_cnn", "feature_concat_mlp", "channel_concat_cnn")
+
+
+def build_dag(kind: str, *, gen: torch.Generator, n_in: int = 16, hidden: int = 24, n_out: int = 10,
+              channels: Tuple[int, int, int] = (2, 6, 6), blocks: int = 1, bias_std: float = 0.1) -> BFTaskModule:
+    """The four DAG shapes of the reference's general-DAG tests
+    (tests/test_phase7a_pr8_general_dag_runtime.py:17-237), with Kaiming weights
+    and small random biases:
+
+    * ``residual_mlp``: input -> linear -> relu -> linear -> add(input, .) -> relu,
+      ``blocks`` times (each block adds its own input), then a linear head;
+    * ``projection_skip_cnn``: conv(input) -> relu, plus a skip conv of the input,
+      add -> relu -> flatten -> linear (C x 8 x 8 input, 3x3 convs, padding 1);
+    * ``feature_concat_mlp``: two linear -> relu branches of the input, concat -> linear;
+    * ``channel_concat_cnn``: two conv -> relu branches of the input, channel concat
+      -> flatten -> linear.
+    """
+    ops: List[TaskOp] = []
+    params: Dict[str, torch.Tensor] = {}
+    values = ["input"]
+
+    def lin(name, x, n_from, n_to, out):
+        params[f"W_{name}"] = _kaiming((n_to, n_from), fan_in=n_from, gen=gen, kind="uniform")
+        params[f"b_{name}"] = _bias(n_to, gen, bias_std)
+        ops.append(TaskOp("linear", name, [x, f"W_{name}", f"b_{name}"], [out]))
+        values.append(out)
+
+    def conv(name, x, c_from, c_to, out):
+        params[f"W_{name}"] = _kaiming((c_to, c_from, 3, 3), fan_in=c_from * 9, gen=gen, kind="uniform")
+        params[f"b_{name}"] = _bias(c_to, gen, bias_std)
+        ops.append(TaskOp("conv2d", name, [x, f"W_{name}", f"b_{name}"], [out],
+                          {"stride": 1, "padding": 1, "dilation": 1, "groups": 1}))
+        values.append(out)
+
+    def op(t, name, ins, out, attrs=None):
+        ops.append(TaskOp(t, name, ins, [out], dict(attrs or {})))
+        values.append(out)
+
+    if kind == "residual_mlp":
+        x = "input"
+        for i in range(blocks):
+            lin(f"lin{i}a", x, n_in, hidden, f"h{i}a")
+            op("relu", f"relu{i}a", [f"h{i}a"], f"r{i}a")
+            lin(f"lin{i}b", f"r{i}a", hidden, n_in, f"h{i}b")
+            op("add", f"add{i}", [x, f"h{i}b"], f"s{i}")
+            op("relu", f"relu{i}", [f"s{i}"], f"r{i}")
+            x = f"r{i}"
+        lin("head", x, n_in, n_out, "out")
+    elif kind == "projection_skip_cnn":
+        c_in, c_mid, _ = channels
+        conv("conv_main", "input", c_in, c_mid, "h_main")
+        op("relu", "relu_main", ["h_main"], "r_main")
+        conv("conv_skip", "input", c_in, c_mid, "h_skip")
+        op("add", "add0", ["r_main", "h_skip"], "sum0")
+        op("relu", "relu_out", ["sum0"], "r_out")
+        op("flatten", "flatten0", ["r_out"], "flat", {"start_dim": 1, "end_dim": -1})
+        lin("head", "flat", c_mid * 64, n_out, "out")
+    elif kind == "feature_concat_mlp":
+        lin("lin1", "input", n_in, hidden, "h1")
+        op("relu", "relu1", ["h1"], "r1")
+        lin("lin2", "input", n_in, hidden // 2, "h2")
+        op("relu", "relu2", ["h2"], "r2")
+        op("concat", "concat0", ["r1", "r2"], "cat0", {"axis": 1})
+        lin("head", "cat0", hidden + hidden // 2, n_out, "out")
+    elif kind == "channel_concat_cnn":
+        c_in, c1, c2 = channels
+        conv("conv1", "input", c_in, c1, "h1")
+        op("relu", "relu1", ["h1"], "r1")
+        conv("conv2", "input", c_in, c2, "h2")
+        op("relu", "relu2", ["h2"], "r2")
+        op("concat", "concat0", ["r1", "r2"], "cat0", {"axis": 1})
+        op("flatten", "flatten0", ["cat0"], "flat", {"start_dim": 1, "end_dim": -1})
+        lin("head", "flat", (c1 + c2) * 64, n_out, "out")
+    else:
+        raise ValueError(f"unknown DAG kind {kind!r}; expected one of {DAG_KINDS}")
+    return _module(ops, params, values)
+
+
+def dag_input_shape(kind: str, *, n_in: int = 16, channels: Tuple[int, int, int] = (2, 6, 6)) -> Tuple[int, ...]:
+    return (channels[0], 8, 8) if kind.endswith("_cnn") else (n_in,)
+
+
 def _module(ops: List[TaskOp], params: Dict[str, torch.Tensor], values: List[str]) -> BFTaskModule:
     task = BoundTask(task_id="t0", kind=TaskKind.INTERVAL_IBP, ops=ops, input_values=["input"],
                      output_values=["out"], params=list(params.keys()))
@@ -189,6 +275,23 @@ def make_c4(seed: int = 0, batch: int = 32) -> Workload:
     w = make_c3(seed=seed, batch=batch, eps=8.0 / 255.0, name="C4")
     w.extra.update({"steps": 20, "lr": 0.1, "alpha_init": "crown"})
     return w
+
+
+def make_dag(kind: str = "residual_mlp", seed: int = 0, batch: int = 8, eps: float = 0.02, box: bool = False,
+             n_in: int = 16, hidden: int = 24, n_out: int = 10, channels: Tuple[int, int, int] = (2, 6, 6),
+             blocks: int = 1) -> Workload:
+    """A DAG network of ``build_dag`` with a margin spec of random labels; the input
+    set is a Linf ball of radius eps, or (box) that ball clamped to [0, 1]."""
+    g = torch.Generator().manual_seed(seed)
+    module = build_dag(kind, gen=g, n_in=n_in, hidden=hidden, n_out=n_out, channels=channels, blocks=blocks)
+    x = torch.rand((batch,) + dag_input_shape(kind, n_in=n_in, channels=channels), generator=g)
+    labels = torch.randint(0, n_out, (batch,), generator=g)
+    if box:
+        spec = InputSpec.box(value_name="input", lower=torch.clamp(x - eps, 0.0, 1.0),
+                             upper=torch.clamp(x + eps, 0.0, 1.0))
+    else:
+        spec = InputSpec.linf(value_name="input", center=x, eps=eps)
+    return Workload(f"dag_{kind}", module, spec, margin_spec(labels, n_out), labels)
 
 
 def _ibp_relu_bounds_f64(module: BFTaskModule, x: torch.Tensor, eps: float) -> List[Tuple[torch.Tensor, torch.Tensor]]:

@@ -13,7 +13,9 @@ Follows, op by op and with the same torch operations and association order:
 * Linear / conv2d / flatten backward -- boundflow/runtime/crown_ibp.py:1073-1173
 * Lazy coefficient operators (Dense, RightMatmul, ReshapeInput, Conv2d) --
   boundflow/runtime/linear_operator.py:299-720, 908-1092, 1378-1477
-* Backward driver -- boundflow/runtime/crown_ibp.py:1669-2051
+* Backward driver -- boundflow/runtime/crown_ibp.py:1669-2051, with the DAG pieces: fan-in
+  accumulation (crown_ibp.py:874-937), add and concat adjoints (crown_ibp.py:1928-2030),
+  AddLinearOperator / SliceInputLinearOperator (linear_operator.py:285-296, 1096-1340)
 * concretize_affine -- boundflow/runtime/perturbation.py:175-222, 327-359
 * Fused region reference -- boundflow/runtime/fused_crown.py:330-400
 """
@@ -147,6 +149,32 @@ def apply_relu_split(pre: IntervalState, split: torch.Tensor, *, name: str) -> I
     return IntervalState(lower=lower.reshape_as(pre.lower), upper=upper.reshape_as(pre.upper))
 
 
+def concat_axis(axis_raw: Any, rank_with_batch: int) -> int:
+    """dag_utils.py:6-20: the feature axis of [B, F] or the channel axis of [B, C, H, W]."""
+    axis = int(axis_raw)
+    if rank_with_batch == 2:
+        if axis in (1, -1):
+            return 1
+        raise NotImplementedError(f"concat: only the feature axis of a rank-2 value, got axis={axis}")
+    if rank_with_batch == 4:
+        if axis in (1, -3):
+            return 1
+        raise NotImplementedError(f"concat: only the channel axis of a rank-4 value, got axis={axis}")
+    raise NotImplementedError(f"concat: only rank-2 or rank-4 values, got rank={rank_with_batch}")
+
+
+def check_concat_shapes(shapes: Sequence[Tuple[int, ...]], axis: int) -> int:
+    """dag_utils.py:23-47: equal rank and equal non-axis dims; returns the concatenated axis size."""
+    ref = tuple(int(d) for d in shapes[0])
+    total = ref[axis]
+    for shp in shapes[1:]:
+        shp = tuple(int(d) for d in shp)
+        if len(shp) != len(ref) or any(a != b for i, (a, b) in enumerate(zip(ref, shp)) if i != axis):
+            raise NotImplementedError(f"concat: shapes {ref} and {shp} differ off the concat axis")
+        total += shp[axis]
+    return total
+
+
 def forward_ibp_trace(
     module: BFTaskModule,
     spec: InputSpec,
@@ -154,7 +182,7 @@ def forward_ibp_trace(
     relu_split_state: Optional[Dict[str, torch.Tensor]] = None,
     relu_pre_constraints: Optional[Mapping[str, IntervalState]] = None,
 ) -> Tuple[Dict[str, IntervalState], Dict[str, IntervalState]]:
-    """crown_ibp.py:101-342 for linear/conv2d/relu/add/flatten/reshape."""
+    """crown_ibp.py:101-342 for linear/conv2d/relu/add/concat/flatten/reshape."""
     task = module.get_entry_task()
     params = module.params
     env: Dict[str, Any] = {spec.value_name: _input_marker(spec)}
@@ -214,7 +242,20 @@ def forward_ibp_trace(
         elif t == "add":
             a = ensure_interval(get_state(op.inputs[0]))
             b2 = ensure_interval(get_state(op.inputs[1]))
+            if tuple(a.lower.shape) != tuple(b2.lower.shape):
+                raise NotImplementedError(
+                    "_forward_ibp_trace_mlp only supports add with exact same-shape inputs; "
+                    f"got {tuple(a.lower.shape)} and {tuple(b2.lower.shape)}")
             y = IntervalState(a.lower + b2.lower, a.upper + b2.upper)
+        elif t == "concat":
+            # crown_ibp.py:235-257 with dag_utils.py:6-47
+            if len(op.inputs) < 2:
+                raise ValueError(f"concat expects at least 2 inputs, got {len(op.inputs)}")
+            parts = [ensure_interval(get_state(name)) for name in op.inputs]
+            axis = concat_axis(op.attrs.get("axis", 1), int(parts[0].lower.dim()))
+            check_concat_shapes([tuple(p.lower.shape) for p in parts], axis)
+            y = IntervalState(torch.cat([p.lower for p in parts], dim=axis),
+                              torch.cat([p.upper for p in parts], dim=axis))
         elif t in ("flatten", "reshape"):
             xs = get_state(op.inputs[0])
             if is_input(xs):
@@ -430,6 +471,88 @@ class Conv2dOp:
         return self._transpose(base_dense).view(self.shape[0], self.spec_dim, -1)
 
 
+class AddOp:
+    """linear_operator.py:1096-1235 (lazy sum of two operators of one input shape)."""
+
+    def __init__(self, lhs, rhs):
+        if tuple(lhs.shape) != tuple(rhs.shape) or tuple(lhs.input_shape) != tuple(rhs.input_shape):
+            raise ValueError(f"add shape mismatch: {lhs.shape}/{lhs.input_shape} vs {rhs.shape}/{rhs.input_shape}")
+        self.lhs = lhs
+        self.rhs = rhs
+        self.input_shape = tuple(lhs.input_shape)
+
+    @property
+    def shape(self):
+        return self.lhs.shape
+
+    @property
+    def spec_dim(self):
+        return self.lhs.spec_dim
+
+    def center_term(self, center):
+        return self.lhs.center_term(center) + self.rhs.center_term(center)
+
+    def contract_input(self, vec):
+        return self.lhs.contract_input(vec) + self.rhs.contract_input(vec)
+
+    def row_abs_sum(self):
+        return self.to_dense().abs().sum(dim=2)
+
+    def to_dense(self):
+        return self.lhs.to_dense() + self.rhs.to_dense()
+
+    def feature_rows(self, shape):
+        return self.to_dense().reshape(self.shape[0] * self.spec_dim, *shape)
+
+
+class SliceOp:
+    """linear_operator.py:1237-1340: the columns [start, stop) of the leading per-sample axis
+    (features of [F], channels of [C, H, W]) of the base operator's input."""
+
+    def __init__(self, base, input_shape, start: int, stop: int):
+        self.base = base
+        self.input_shape = tuple(int(d) for d in input_shape)
+        self.start = int(start)
+        self.stop = int(stop)
+        base_shape = tuple(int(d) for d in base.input_shape)
+        if len(base_shape) != len(self.input_shape) or self.stop - self.start != self.input_shape[0] \
+                or base_shape[1:] != self.input_shape[1:] or not 0 <= self.start <= self.stop <= base_shape[0]:
+            raise ValueError(f"slice_input mismatch: base {base_shape}, slice {self.input_shape} "
+                             f"[{self.start}:{self.stop}]")
+
+    @property
+    def shape(self):
+        return (self.base.shape[0], self.base.shape[1], _prod(self.input_shape))
+
+    @property
+    def spec_dim(self):
+        return self.base.spec_dim
+
+    def _embed(self, flat):
+        """A [B, prod(input_shape)] vector placed, zero-padded, in the base input."""
+        b = int(flat.shape[0])
+        full = torch.zeros((b,) + tuple(self.base.input_shape), dtype=flat.dtype, device=flat.device)
+        full[:, self.start:self.stop] = flat.reshape((b,) + self.input_shape)
+        return full
+
+    def center_term(self, center):
+        return self.base.center_term(self._embed(center.reshape(self.shape[0], -1)))
+
+    def contract_input(self, vec):
+        return self.base.contract_input(self._embed(_flatten_contract_input(vec, self.shape[0], self.input_shape)))
+
+    def row_abs_sum(self):
+        return self.to_dense().abs().sum(dim=2)
+
+    def to_dense(self):
+        b, k = self.shape[0], self.spec_dim
+        dense = self.base.to_dense().reshape((b, k) + tuple(self.base.input_shape))
+        return dense[:, :, self.start:self.stop].reshape(b, k, -1)
+
+    def feature_rows(self, shape):
+        return self.to_dense().reshape(self.shape[0] * self.spec_dim, *shape)
+
+
 def reshape_input(op, shape):
     shape = tuple(int(d) for d in shape)
     if tuple(op.input_shape) == shape:
@@ -588,7 +711,9 @@ def crown_backward_from_trace(
     relu_pre_add_coeff_u: Optional[Dict[str, torch.Tensor]] = None,
     relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
 ) -> IntervalState:
-    """crown_ibp.py:1669-2051 restricted to chain graphs (linear/conv2d/relu/flatten/reshape)."""
+    """crown_ibp.py:1669-2051: ops in reverse order, each popping the backward state of its
+    output; a value read by several ops accumulates their contributions (crown_ibp.py:892-909)
+    before its own op runs."""
     task = module.get_entry_task()
     params = module.params
     if output_value is None:
@@ -612,6 +737,26 @@ def crown_backward_from_trace(
     adjoints: Dict[str, _State] = {
         output_value: _State(DenseOp(A, output_shape), DenseOp(A.clone(), output_shape), b0, b0.clone())
     }
+    # crown_ibp.py:912-919: values that depend on the input; other add operands are constants
+    dynamic = set(interval_env.keys()) | {spec.value_name}
+
+    def operand_box(name) -> IntervalState:
+        if name == spec.value_name:
+            lb, ub = spec.perturbation.bounding_box(spec.center)
+            return IntervalState(lb, ub)
+        if name in interval_env:
+            return interval_env[name]
+        t_ = params[name]
+        return IntervalState(t_, t_)
+
+    def accumulate(name, new: _State) -> None:
+        shape = _value_shape(spec, interval_env, name)
+        new = _State(reshape_input(new.A_u, shape), reshape_input(new.A_l, shape), new.b_u, new.b_l)
+        cur = adjoints.get(name)
+        if cur is not None:
+            cur = _State(reshape_input(cur.A_u, shape), reshape_input(cur.A_l, shape), cur.b_u, cur.b_l)
+            new = _State(AddOp(cur.A_u, new.A_u), AddOp(cur.A_l, new.A_l), cur.b_u + new.b_u, cur.b_l + new.b_l)
+        adjoints[name] = new
 
     for op in reversed(task.ops):
         out_name = op.outputs[0]
@@ -665,12 +810,51 @@ def crown_backward_from_trace(
                 conv2d_right(A_l, w, stride, padding, dilation, groups, in_shape, out_shape),
                 b_u, b_l,
             )
+        elif t == "add":
+            # crown_ibp.py:1928-1970: every dynamic operand receives the same coefficient; a
+            # constant operand's contribution goes into the bias, which the first dynamic
+            # operand carries (the others get zeros, crown_ibp.py:922-937)
+            out_shape = _value_shape(spec, interval_env, out_name)
+            A_u, A_l = reshape_input(st.A_u, out_shape), reshape_input(st.A_l, out_shape)
+            cb_u, cb_l = st.b_u, st.b_l
+            dyn = []
+            for name in op.inputs:
+                val = operand_box(name)
+                if tuple(int(d) for d in val.lower.shape[1:]) != tuple(out_shape):
+                    raise NotImplementedError(
+                        f"add backward: only exact same-shape non-broadcast inputs; got output_shape={out_shape} "
+                        f"input_shape={tuple(int(d) for d in val.lower.shape[1:])}")
+                if name in dynamic:
+                    dyn.append(name)
+                else:
+                    cb_u = cb_u + A_u.contract_input(val.lower)
+                    cb_l = cb_l + A_l.contract_input(val.lower)
+            for idx, name in enumerate(dyn):
+                bu, bl = (cb_u, cb_l) if idx == 0 else (torch.zeros_like(cb_u), torch.zeros_like(cb_l))
+                accumulate(name, _State(A_u, A_l, bu, bl))
+            continue
+        elif t == "concat":
+            # crown_ibp.py:1972-2030: each operand receives its slice of the coefficient's
+            # leading per-sample axis; the bias goes with the first operand
+            out_shape = _value_shape(spec, interval_env, out_name)
+            concat_axis(op.attrs.get("axis", 1), len(out_shape) + 1)
+            A_u, A_l = reshape_input(st.A_u, out_shape), reshape_input(st.A_l, out_shape)
+            shapes = [_value_shape(spec, interval_env, name) for name in op.inputs]
+            total = check_concat_shapes(shapes, 0)
+            start = 0
+            for idx, (name, shp) in enumerate(zip(op.inputs, shapes)):
+                if name not in dynamic:
+                    raise NotImplementedError(f"concat backward: only dynamic tensor values, got {name}")
+                stop = start + int(shp[0])
+                bu, bl = (st.b_u, st.b_l) if idx == 0 else (torch.zeros_like(st.b_u), torch.zeros_like(st.b_l))
+                accumulate(name, _State(SliceOp(A_u, shp, start, stop), SliceOp(A_l, shp, start, stop), bu, bl))
+                start = stop
+            if start != total or total != int(out_shape[0]):
+                raise ValueError(f"concat backward shape mismatch: sliced={start} total={total} out={out_shape}")
+            continue
         else:
             raise NotImplementedError(f"oracle backward: unsupported op_type {t}")
-        if in_name in adjoints:
-            raise NotImplementedError("oracle restates chain graphs only (no fan-in accumulation)")
-        in_shape = _value_shape(spec, interval_env, in_name)
-        adjoints[in_name] = _State(reshape_input(new.A_u, in_shape), reshape_input(new.A_l, in_shape), new.b_u, new.b_l)
+        accumulate(in_name, new)
 
     st = adjoints[spec.value_name]
     center_shape = tuple(int(d) for d in spec.center.shape[1:])
