@@ -13,7 +13,9 @@ dominant kernel (timed with HIP events on the launch stream inside the timed
 region) and a CPU baseline (the PyTorch CPU restatement of the reference path
 timed on a bounded sample on this host).
 
-    python bench.py [--steps K] [--warmup W] [--config C2|C1|C3|C4|C5] [--cpu-seconds S]
+    python bench.py [--steps K] [--warmup W] [--config C2|C1|C3|C4|C5|D1] [--cpu-seconds S]
+
+D1 (not a BASELINE configuration) measures the DAG path: CROWN on a residual MLP.
     python bench.py --calibrate-copy MIB   # one plain device copy of MIB MiB, the
                                            # reference kernel for HBM byte counters
 """
@@ -58,7 +60,7 @@ def hip_runner(name: str):
 
     if name == "C2":
         return lambda wd: hc.run_crown_all_intermediate(wd.module, wd.spec, linear_spec_C=wd.C)[0]
-    if name in ("C1", "C3"):
+    if name in ("C1", "C3", "D1"):
         return lambda wd: hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
     if name == "C4":
         from boundflow_amd import alpha_beta as hab
@@ -91,7 +93,9 @@ def build_case(name: str):
             "C2": "C2: CROWN, all intermediate bounds by CROWN, MLP 784-500x6-10, B=256, Linf 0.015, 9 margin specs",
             "C3": "C3: CROWN, CNN 3x32x32 conv16-conv32-fc100-fc10, B=128, Linf 2/255, 9 margin specs",
             "C4": "C4: alpha-CROWN, CNN of C3, B=32, Linf 8/255, 20 Adam steps lr 0.1, alpha from CROWN",
-            "C5": "C5: beta-CROWN BaB batch, MLP 784-256x4-10, 4096 domains, Linf 0.03, 1-12 splits, 10 steps"}[name]
+            "C5": "C5: beta-CROWN BaB batch, MLP 784-256x4-10, 4096 domains, Linf 0.03, 1-12 splits, 10 steps",
+            "D1": "D1: CROWN on a residual MLP (DAG), 784-256 stem, 4 blocks 256-512-256 with identity skips, "
+                  "head 10, B=256, Linf 0.002, 9 margin specs"}[name]
     return w, step, units, unit, desc
 
 
@@ -120,7 +124,7 @@ def _oracle_run(name: str, sub):
     if name == "C2":
         with torch.inference_mode():
             return cr.run_crown_all_intermediate(sub.module, sub.spec, linear_spec_C=sub.C)
-    if name in ("C1", "C3"):
+    if name in ("C1", "C3", "D1"):
         with torch.inference_mode():
             return cr.run_crown_ibp(sub.module, sub.spec, linear_spec_C=sub.C)
     if name == "C4":
@@ -190,7 +194,7 @@ def cpu_baseline(name: str, w, seconds: float):
     done_units = 0
     elapsed = 0.0
     rounds = 0
-    sample_b = {"C1": 16, "C2": 4, "C3": 16, "C4": 2, "C5": 64}[name]
+    sample_b = {"C1": 16, "C2": 4, "C3": 16, "C4": 2, "C5": 64, "D1": 16}[name]
     first = None
     while elapsed < seconds and rounds < 4096:
         sub = wl.subset(w, sample_b)
@@ -251,7 +255,7 @@ def main() -> int:
     # 20 Adam steps; for C5 the batch's forward trace, 10 alpha-beta steps and the
     # certification).  C1, C3 and C4 are launch-bound at these batch sizes; C5
     # leaves the device idle between launches for about 7 % of an eager batch.
-    use_graph = args.config in ("C1", "C3", "C4", "C5") and not args.no_graph
+    use_graph = args.config in ("C1", "C3", "C4", "C5", "D1") and not args.no_graph
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()

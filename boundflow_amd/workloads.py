@@ -120,13 +120,15 @@ DAG_KINDS = ("residual_mlp", "projection_skip_cnn", "feature_concat_mlp", "chann
 
 
 def build_dag(kind: str, *, gen: torch.Generator, n_in: int = 16, hidden: int = 24, n_out: int = 10,
-              channels: Tuple[int, int, int] = (2, 6, 6), blocks: int = 1, bias_std: float = 0.1) -> BFTaskModule:
+              channels: Tuple[int, int, int] = (2, 6, 6), blocks: int = 1, bias_std: float = 0.1,
+              width: Optional[int] = None) -> BFTaskModule:
     """The four DAG shapes of the reference's general-DAG tests
     (tests/test_phase7a_pr8_general_dag_runtime.py:17-237), with Kaiming weights
     and small random biases:
 
     * ``residual_mlp``: input -> linear -> relu -> linear -> add(input, .) -> relu,
-      ``blocks`` times (each block adds its own input), then a linear head;
+      ``blocks`` times (each block adds its own input), then a linear head; with
+      ``width`` a linear + relu stem maps the input to ``width`` features first;
     * ``projection_skip_cnn``: conv(input) -> relu, plus a skip conv of the input,
       add -> relu -> flatten -> linear (C x 8 x 8 input, 3x3 convs, padding 1);
     * ``feature_concat_mlp``: two linear -> relu branches of the input, concat -> linear;
@@ -156,14 +158,19 @@ def build_dag(kind: str, *, gen: torch.Generator, n_in: int = 16, hidden: int = 
 
     if kind == "residual_mlp":
         x = "input"
+        n = n_in
+        if width is not None:
+            lin("stem", x, n_in, width, "h_stem")
+            op("relu", "relu_stem", ["h_stem"], "r_stem")
+            x, n = "r_stem", width
         for i in range(blocks):
-            lin(f"lin{i}a", x, n_in, hidden, f"h{i}a")
+            lin(f"lin{i}a", x, n, hidden, f"h{i}a")
             op("relu", f"relu{i}a", [f"h{i}a"], f"r{i}a")
-            lin(f"lin{i}b", f"r{i}a", hidden, n_in, f"h{i}b")
+            lin(f"lin{i}b", f"r{i}a", hidden, n, f"h{i}b")
             op("add", f"add{i}", [x, f"h{i}b"], f"s{i}")
             op("relu", f"relu{i}", [f"s{i}"], f"r{i}")
             x = f"r{i}"
-        lin("head", x, n_in, n_out, "out")
+        lin("head", x, n, n_out, "out")
     elif kind == "projection_skip_cnn":
         c_in, c_mid, _ = channels
         conv("conv_main", "input", c_in, c_mid, "h_main")
@@ -279,11 +286,12 @@ def make_c4(seed: int = 0, batch: int = 32) -> Workload:
 
 def make_dag(kind: str = "residual_mlp", seed: int = 0, batch: int = 8, eps: float = 0.02, box: bool = False,
              n_in: int = 16, hidden: int = 24, n_out: int = 10, channels: Tuple[int, int, int] = (2, 6, 6),
-             blocks: int = 1) -> Workload:
+             blocks: int = 1, width: Optional[int] = None) -> Workload:
     """A DAG network of ``build_dag`` with a margin spec of random labels; the input
     set is a Linf ball of radius eps, or (box) that ball clamped to [0, 1]."""
     g = torch.Generator().manual_seed(seed)
-    module = build_dag(kind, gen=g, n_in=n_in, hidden=hidden, n_out=n_out, channels=channels, blocks=blocks)
+    module = build_dag(kind, gen=g, n_in=n_in, hidden=hidden, n_out=n_out, channels=channels, blocks=blocks,
+                       width=width)
     x = torch.rand((batch,) + dag_input_shape(kind, n_in=n_in, channels=channels), generator=g)
     labels = torch.randint(0, n_out, (batch,), generator=g)
     if box:
@@ -455,7 +463,15 @@ def split_ibp_dag(w: Workload) -> BFTaskModule:
                         task_graph=graph)
 
 
-MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5}
+def make_d1(seed: int = 0, batch: int = 256, eps: float = 0.002) -> Workload:
+    """D1: CROWN on a residual MLP, 784 -> 256 stem, 4 blocks 256-512-256 with identity
+    skips, head 10; B=256, Linf eps, 9 margin specs."""
+    w = make_dag("residual_mlp", seed=seed, batch=batch, eps=eps, n_in=784, hidden=512, width=256, blocks=4)
+    w.name = "D1"
+    return w
+
+
+MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5, "D1": make_d1}
 
 
 def make(name: str, **kw) -> Workload:
