@@ -38,6 +38,7 @@ from .crown import (
     _numel,
     crown_backward,
     forward_ibp_trace,
+    NotAChain,
     parse_chain,
 )
 from .profiling import launch as _timed
@@ -196,6 +197,40 @@ def _grad_pass(spec: InputSpec, chain: Chain, trace: ForwardTrace, saved: dict, 
     return g_alpha, g_beta
 
 
+def _evaluator(module, spec: InputSpec, trace, chain: Optional[Chain], linear_spec_C):
+    """(bound, grad, out_dim) of the task: the chain's fused CROWN backward and its
+    reverse pass, or the DAG backward of ``crown_dag`` and its reverse pass.
+    bound(alpha, add, need_upper, need_lower, save) -> IntervalState;
+    grad(saved, B, S, alpha_args, splits, G) -> (dL/dalpha, dL/dbeta)."""
+    if chain is not None:
+        def bound(alpha, add, need_upper, need_lower, save):
+            return crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=alpha,
+                                  relu_pre_add_coeff_l=add, need_upper=need_upper, need_lower=need_lower, save=save)
+
+        def grad(saved, B, S, a_arg, splits, G):
+            return _grad_pass(spec, chain, trace, saved, B, S, a_arg, splits, G)
+
+        return bound, grad, _numel(chain.layers[-1].out_shape)
+    from . import crown_dag
+
+    def bound(alpha, add, need_upper, need_lower, save):
+        return crown_dag.crown_backward_dag(module, spec, trace, linear_spec_C=linear_spec_C, relu_alpha=alpha,
+                                            relu_pre_add_coeff_l=add, need_upper=need_upper, need_lower=need_lower,
+                                            save=save)
+
+    def grad(saved, B, S, a_arg, splits, G):
+        return crown_dag.lower_grad_pass(module, spec, trace, saved, B, a_arg, splits, G)
+
+    return bound, grad, _numel(trace.shapes[module.get_entry_task().output_values[0]])
+
+
+def _chain_or_none(module, spec) -> Optional[Chain]:
+    try:
+        return parse_chain(module, spec)
+    except NotAChain:
+        return None
+
+
 def _bias_map(layer) -> torch.Tensor:
     if layer.kind == "linear":
         return layer.bias.contiguous()
@@ -230,10 +265,11 @@ def run_alpha_beta_crown_mlp(
     if objective != "lower" or spec_reduce != "mean":
         raise NotImplementedError("HIP alpha-beta CROWN implements objective='lower', spec_reduce='mean'")
     spec = normalize_input_spec(input_spec)
-    chain = parse_chain(module, spec)
+    chain = _chain_or_none(module, spec)
     if trace is None:
         trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
                                   raise_on_infeasible=raise_on_infeasible)
+    bound, grad, out_dim = _evaluator(module, spec, trace, chain, linear_spec_C)
     dev = spec.center.device
     B = int(spec.center.shape[0])
     stream = _lib.stream_handle()
@@ -269,7 +305,7 @@ def run_alpha_beta_crown_mlp(
     # the same, and no host synchronization is needed: the batch can be captured as a graph.
     beta_names = list(splits.keys()) if use_beta else []
     b_layer, b_neuron, _gap = branch_tensors(trace, B) if trace.relu_pre else (None, None, None)
-    S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else _numel(chain.layers[-1].out_shape)
+    S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else out_dim
     M = B * S
     # d(-sum_d mean_s lb)/dlb = -1/S ; d(-mean_d mean_s lb)/dlb = (-1/B)/S   (fp32, as autograd divides)
     g_row = np.float32(-1.0) / np.float32(S) if per_batch_params else (np.float32(-1.0) / np.float32(B)) / np.float32(S)
@@ -296,9 +332,7 @@ def run_alpha_beta_crown_mlp(
             _lib.call("bf_beta_coeff_multi", len(beta_names), *beta_args, stream)
         saved = {"grad_rows": G} if step < int(steps) else None
         # lower bound only: the objective and the best-of rule read nothing else
-        bounds = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C,
-                                relu_alpha={n: alpha[n] for n in names},
-                                relu_pre_add_coeff_l={n: add[n] for n in beta_names}, need_upper=False, save=saved)
+        bounds = bound({n: alpha[n] for n in names}, {n: add[n] for n in beta_names}, False, True, saved)
         if per_batch_params:
             _lib.call("bf_best_update", _lib.ptr(bounds.lower), None, B, S, _lib.ptr(best_metric),
                       _lib.ptr(best_lb), None, _lib.ptr(improved), 1 if step == 0 else 0, stream)
@@ -314,7 +348,7 @@ def run_alpha_beta_crown_mlp(
         if step == int(steps):
             break
         a_arg = {n: (alpha[n], p_ld[n]) for n in names}
-        g_alpha, g_beta = _grad_pass(spec, chain, trace, saved, B, S, a_arg, splits, G)
+        g_alpha, g_beta = grad(saved, B, S, a_arg, splits, G)
         if not per_batch_params:
             for d in (g_alpha, g_beta):
                 for n in names:
@@ -326,8 +360,7 @@ def run_alpha_beta_crown_mlp(
     # bound.  The upper bound depends on alpha alone (beta enters the lower bound
     # only) and every domain's rows on that domain's parameters alone, so one upper
     # pass with the best parameters reproduces it.
-    best_ub = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C,
-                             relu_alpha={n: best_alpha[n] for n in names}, need_lower=False).upper
+    best_ub = bound({n: best_alpha[n] for n in names}, None, True, False, None).upper
     out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
     out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
     stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,
@@ -351,8 +384,7 @@ def run_alpha_crown_from_crown_init(module, input_spec, *, linear_spec_C=None, s
     """Config C4: per-domain alpha initialised from the CROWN relaxation
     (alpha_from_crown), then ``steps`` Adam steps on the lower bound."""
     spec = normalize_input_spec(input_spec)
-    chain = parse_chain(module, spec)
-    trace = forward_ibp_trace(module, spec, chain=chain)
+    trace = forward_ibp_trace(module, spec, chain=_chain_or_none(module, spec))
     init = alpha_from_crown(trace)
     return run_alpha_beta_crown_mlp(module, spec, linear_spec_C=linear_spec_C, steps=steps, lr=lr,
                                     warm_start_alpha=init, per_batch_params=True, trace=trace)
@@ -364,8 +396,9 @@ def lower_bound_gradients(module, input_spec, *, linear_spec_C, relu_alpha: Dict
     """One evaluation plus one reverse pass: returns (bounds, dL/dalpha, dL/dbeta)
     for L = -sum_d mean_s lb (per-domain parameters) or -mean lb (shared)."""
     spec = normalize_input_spec(input_spec)
-    chain = parse_chain(module, spec)
+    chain = _chain_or_none(module, spec)
     trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain)
+    bound, grad, _out_dim = _evaluator(module, spec, trace, chain, linear_spec_C)
     dev = spec.center.device
     B = int(spec.center.shape[0])
     names = list(trace.relu_pre.keys())
@@ -389,9 +422,9 @@ def lower_bound_gradients(module, input_spec, *, linear_spec_C, relu_alpha: Dict
                     _lib.call("bf_beta_coeff", _lib.ptr(b), p_ld[n], _lib.ptr(splits[n][0]), splits[n][1], B,
                               numel[n], _lib.ptr(add[n]), stream)
     saved = {"grad_rows": G}
-    bounds = crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=alpha,
-                            relu_pre_add_coeff_l=add, save=saved)
-    g_alpha, g_beta = _grad_pass(spec, chain, trace, saved, B, S, {n: (alpha[n], p_ld[n]) for n in names}, splits, G)
+    # the chain's pass computes both bounds; the DAG pass follows the lower bound alone
+    bounds = bound(alpha, add, chain is not None, True, saved)
+    g_alpha, g_beta = grad(saved, B, S, {n: (alpha[n], p_ld[n]) for n in names}, splits, G)
     if not per_batch_params:
         for d in (g_alpha, g_beta):
             for n in list(d.keys()):

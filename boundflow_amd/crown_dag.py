@@ -95,6 +95,12 @@ def _conv_geometry(op, W, in_shape):
     return stride, padding, (int(W.shape[0]), ho, wo)
 
 
+def _conv_bias_map(bias: torch.Tensor, out_shape) -> torch.Tensor:
+    """The per-channel bias of a conv layer as one value per output element."""
+    Co, Ho, Wo = out_shape
+    return bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(Co * Ho * Wo).contiguous()
+
+
 def _module_task(module: BFTaskModule):
     module.validate()
     task = module.get_entry_task()
@@ -281,8 +287,14 @@ def crown_backward_dag(
     output_value: Optional[str] = None,
     relu_alpha: Optional[Dict[str, torch.Tensor]] = None,
     relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
+    need_upper: bool = True,
+    need_lower: bool = True,
+    save: Optional[dict] = None,
 ) -> IntervalState:
-    """The general backward of crown_ibp.py:1669-2051 on dense coefficient rows."""
+    """The general backward of crown_ibp.py:1669-2051 on dense coefficient rows.  A bound
+    that is not needed is not computed (its side of the result is None).  With ``save``
+    (lower bound only) the coefficient entering every ReLU and the input's coefficient are
+    kept for ``lower_grad_pass``."""
     from .crown import _flat_param, _init_spec
 
     task = _module_task(module)
@@ -296,6 +308,10 @@ def crown_backward_dag(
         output_value = task.output_values[0]
     if output_value not in trace.shapes:
         raise ValueError(f"output_value {output_value} not produced by the task")
+    if not (need_upper or need_lower):
+        raise ValueError("crown_backward_dag: no bound requested")
+    if save is not None and need_upper:
+        raise ValueError("crown_backward_dag: the gradient pass follows the lower bound alone")
     out_dim = _numel(trace.shapes[output_value])
     A0, S, a_dstride = _init_spec(linear_spec_C, B, out_dim, dev)
     M = B * S
@@ -303,41 +319,61 @@ def crown_backward_dag(
         A0 = A0.reshape(1, S, out_dim).expand(B, S, out_dim)
     A0 = A0.reshape(M, out_dim).contiguous()
     zero_b = torch.zeros(M, device=dev, dtype=torch.float32)
-    adjoints: Dict[str, _Rows] = {output_value: _Rows(A0, A0, zero_b, zero_b)}
+    adjoints: Dict[str, _Rows] = {output_value: _Rows(A0 if need_upper else None, A0 if need_lower else None,
+                                                      zero_b if need_upper else None,
+                                                      zero_b if need_lower else None)}
     dynamic = set(trace.shapes.keys())     # every value computed from the input (crown_ibp.py:912-919)
+    if save is not None:
+        save.update({"relu_A": {}, "ran": set(), "S": S, "output_value": output_value})
+
+    def ptr_of(t):
+        return None if t is None else t.data_ptr()
 
     def shared(st: _Rows) -> bool:
         """Both bounds carry the same rows (the spec itself, until the first ReLU splits them)."""
-        return st.A_u.data_ptr() == st.A_l.data_ptr() and st.b_u.data_ptr() == st.b_l.data_ptr()
+        return st.A_u is not None and st.A_l is not None and st.A_u.data_ptr() == st.A_l.data_ptr() \
+            and st.b_u.data_ptr() == st.b_l.data_ptr()
+
+    def like(st: _Rows, cols: int, one: bool):
+        """Fresh (A_u, A_l) of [M, cols] for the bounds st carries (one buffer when shared)."""
+        au = torch.empty(M, cols, device=dev) if st.A_u is not None else None
+        al = (au if one else torch.empty(M, cols, device=dev)) if st.A_l is not None else None
+        return au, al
+
+    def zeros_like_b(st: _Rows):
+        z = torch.zeros(M, device=dev)
+        return (z if st.b_u is not None else None), (z if st.b_l is not None else None)
 
     def rows_pass(st: _Rows, n: int, *, pre=None, alpha=None, alpha_ld=0, add=None, add_ld=0, kbias=None,
                   cvec=None, name="crown_relu_relax"):
-        """bf_crown_relu_relax_lu over both bounds: (A', b + sums, center sums or None).  Without a
+        """bf_crown_relu_relax_lu over the bounds st carries: (A', b + sums, center sums).  Without a
         relaxation, rows shared by both bounds are passed once."""
         one = pre is None and add is None and shared(st)
-        rA_u = torch.empty(M, n, device=dev)
-        rA_l = rA_u if one else torch.empty(M, n, device=dev)
-        nb_u = torch.empty(M, device=dev)
-        nb_l = nb_u if one else torch.empty(M, device=dev)
-        c_u = torch.empty(M, device=dev) if cvec is not None else None
-        c_l = c_u if (one or cvec is None) else torch.empty(M, device=dev)
-        reads = 1 if st.A_u.data_ptr() == st.A_l.data_ptr() else 2
-        with _timed(name, 0.0, 4.0 * (reads + (1 if one else 2)) * M * n):
-            _lib.call("bf_crown_relu_relax_lu", _lib.ptr(st.A_u), None if one else _lib.ptr(st.A_l), S * n, B, S, n,
+        rA_u, rA_l = like(st, n, one)
+        nb_u, nb_l = like(_Rows(st.b_u, st.b_l, None, None), 1, one)
+        nb_u = None if nb_u is None else nb_u.reshape(M)
+        nb_l = None if nb_l is None else nb_l.reshape(M)
+        c_u = torch.empty(M, device=dev) if (cvec is not None and st.A_u is not None) else None
+        c_l = (c_u if one else torch.empty(M, device=dev)) if (cvec is not None and st.A_l is not None) else None
+        A_l_in = None if one else st.A_l
+        nz = int(st.A_u is not None) + int(A_l_in is not None)
+        reads = 1 if (nz == 2 and ptr_of(st.A_u) == ptr_of(st.A_l)) else nz
+        with _timed(name, 0.0, 4.0 * (reads + nz) * M * n):
+            _lib.call("bf_crown_relu_relax_lu", _lib.ptr(st.A_u), _lib.ptr(A_l_in), S * n, B, S, n,
                       _lib.ptr(None if pre is None else pre.lower.reshape(B, n)),
                       _lib.ptr(None if pre is None else pre.upper.reshape(B, n)), _lib.ptr(alpha), alpha_ld,
-                      _lib.ptr(add), add_ld, _lib.ptr(kbias), _lib.ptr(cvec), _lib.ptr(st.b_u),
-                      None if one else _lib.ptr(st.b_l), _lib.ptr(rA_u), None if one else _lib.ptr(rA_l),
-                      _lib.ptr(nb_u), None if one else _lib.ptr(nb_l), _lib.ptr(c_u),
-                      None if one else _lib.ptr(c_l), stream)
+                      _lib.ptr(add if A_l_in is not None else None), add_ld, _lib.ptr(kbias), _lib.ptr(cvec),
+                      _lib.ptr(st.b_u), _lib.ptr(None if one else st.b_l), _lib.ptr(rA_u),
+                      _lib.ptr(None if one else rA_l), _lib.ptr(nb_u), _lib.ptr(None if one else nb_l),
+                      _lib.ptr(c_u), _lib.ptr(None if one else c_l), stream)
         return _Rows(rA_u, rA_l, nb_u, nb_l), (c_u, c_l)
 
-    def pair_add(a_u, a_l, b_u, b_l):
-        o_u = torch.empty_like(a_u)
-        o_l = torch.empty_like(a_l)
-        _lib.call("bf_interval_add", _lib.ptr(a_u), _lib.ptr(a_l), _lib.ptr(b_u), _lib.ptr(b_l), a_u.numel(),
-                  _lib.ptr(o_u), _lib.ptr(o_l), stream)
-        return o_u, o_l
+    def add_rows(a, b, cols):
+        if a is None:
+            return None
+        out = torch.empty(M, cols, device=dev) if cols > 1 else torch.empty(M, device=dev)
+        _lib.call("bf_rows_add", _lib.ptr(a), _lib.ptr(b), M, cols, S, None, None, 0, _lib.ptr(out), stream)
+        return out
 
     def accumulate(name: str, upd: _Rows) -> None:
         """crown_ibp.py:892-909: current + update, coefficients and bias rows."""
@@ -345,16 +381,23 @@ def crown_backward_dag(
         if cur is None:
             adjoints[name] = upd
             return
-        with _timed("dag_accumulate", 0.0, 4.0 * 6 * cur.A_u.numel()):
-            A_u, A_l = pair_add(cur.A_u, cur.A_l, upd.A_u, upd.A_l)
-        b_u, b_l = pair_add(cur.b_u, cur.b_l, upd.b_u, upd.b_l)
+        n = int((upd.A_u if upd.A_u is not None else upd.A_l).shape[1])
+        both = shared(cur) and shared(upd)
+        with _timed("dag_accumulate", 0.0, 4.0 * 3 * M * n * (1 if both else 2)):
+            A_u = add_rows(cur.A_u, upd.A_u, n)
+            A_l = A_u if both else add_rows(cur.A_l, upd.A_l, n)
+        b_u = add_rows(cur.b_u, upd.b_u, 1)
+        b_l = b_u if both else add_rows(cur.b_l, upd.b_l, 1)
         adjoints[name] = _Rows(A_u, A_l, b_u, b_l)
 
-    for op in reversed(task.ops):
+    for op_index in range(len(task.ops) - 1, -1, -1):
+        op = task.ops[op_index]
         out = op.outputs[0]
         st = adjoints.pop(out, None)
         if st is None:
             continue
+        if save is not None:
+            save["ran"].add(op_index)
         t = op.op_type
         x = op.inputs[0]
         if t == "linear":
@@ -363,16 +406,17 @@ def crown_backward_dag(
             N, P = int(W.shape[0]), int(W.shape[1])
             Wt = W.t().contiguous()   # the contraction reads W^T [P, N]: 128-bit operand loads along N
             one = shared(st)
-            nz = 1 if one else 2
-            nA_u = torch.empty(M, P, device=dev)
-            nA_l = nA_u if one else torch.empty(M, P, device=dev)
-            nb_u = torch.empty(M, device=dev)
-            nb_l = nb_u if one else torch.empty(M, device=dev)
+            nA_u, nA_l = like(st, P, one)
+            nb_u, nb_l = like(_Rows(st.b_u, st.b_l, None, None), 1, one)
+            nb_u = None if nb_u is None else nb_u.reshape(M)
+            nb_l = None if nb_l is None else nb_l.reshape(M)
+            A_l_in = None if one else st.A_l
+            nz = int(st.A_u is not None) + int(A_l_in is not None)
             with _timed("crown_linear", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P + M * P)):
-                _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(st.A_u), None if one else _lib.ptr(st.A_l), S * N, B,
-                          S, N, None, None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(st.b_u),
-                          None if one else _lib.ptr(st.b_l), _lib.ptr(nA_u), None if one else _lib.ptr(nA_l),
-                          _lib.ptr(nb_u), None if one else _lib.ptr(nb_l), stream)
+                _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(st.A_u), _lib.ptr(A_l_in), S * N, B, S, N, None,
+                          None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(st.b_u),
+                          _lib.ptr(None if one else st.b_l), _lib.ptr(nA_u), _lib.ptr(None if one else nA_l),
+                          _lib.ptr(nb_u), _lib.ptr(None if one else nb_l), stream)
             accumulate(x, _Rows(nA_u, nA_l, nb_u, nb_l))
         elif t == "conv2d":
             W = params[op.inputs[1]].contiguous()
@@ -382,18 +426,18 @@ def crown_backward_dag(
             Ci, Hi, Wi = in_shape
             n_out = Co * Ho * Wo
             if len(op.inputs) == 3:
-                kbias = params[op.inputs[2]].reshape(Co, 1).expand(Co, Ho * Wo).reshape(n_out).contiguous()
-                st, _ = rows_pass(st, n_out, kbias=kbias, name="conv_bias_rows")
+                st, _ = rows_pass(st, n_out, kbias=_conv_bias_map(params[op.inputs[2]], out_shape),
+                                  name="conv_bias_rows")
             one = shared(st)
-            nz = 1 if one else 2
-            y_u = torch.empty(M, Ci * Hi * Wi, device=dev)
-            y_l = y_u if one else torch.empty(M, Ci * Hi * Wi, device=dev)
+            y_u, y_l = like(st, Ci * Hi * Wi, one)
+            A_l_in = None if one else st.A_l
+            nz = int(st.A_u is not None) + int(A_l_in is not None)
             KH, KW = int(W.shape[2]), int(W.shape[3])
             flops = 2.0 * nz * M * Ci * Hi * Wi * Co * KH * KW / float(sh * sw)
             with _timed("conv_transpose", flops, 4.0 * nz * (M * n_out + M * Ci * Hi * Wi)):
-                _lib.call("bf_conv_transpose_rows", _lib.ptr(st.A_u), None if one else _lib.ptr(st.A_l), M, Co, Ho,
-                          Wo, _lib.ptr(W), Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u),
-                          None if one else _lib.ptr(y_l), S, None, 0, None, None, None, None, stream)
+                _lib.call("bf_conv_transpose_rows", _lib.ptr(st.A_u), _lib.ptr(A_l_in), M, Co, Ho, Wo, _lib.ptr(W),
+                          Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(None if one else y_l), S, None,
+                          0, None, None, None, None, stream)
             accumulate(x, _Rows(y_u, y_l, st.b_u, st.b_l))
         elif t == "relu":
             pre = trace.relu_pre[x]
@@ -404,6 +448,8 @@ def crown_backward_dag(
                 alpha, alpha_ld = _flat_param(relu_alpha[x], B, n, f"relu_alpha[{x}]")
             if relu_pre_add_coeff_l is not None and x in relu_pre_add_coeff_l:
                 add, add_ld = _flat_param(relu_pre_add_coeff_l[x], B, n, f"relu_pre_add_coeff_l[{x}]")
+            if save is not None:
+                save["relu_A"][op_index] = st.A_l      # the coefficient before the relaxation
             new, _ = rows_pass(st, n, pre=pre, alpha=alpha, alpha_ld=alpha_ld, add=add, add_ld=add_ld)
             accumulate(x, new)
         elif t in ("flatten", "reshape"):
@@ -430,16 +476,18 @@ def crown_backward_dag(
                 # a constant operand: its contribution sum_k A[m, k] * val[d, k] joins the bias
                 if int(val.shape[0]) != B:
                     raise NotImplementedError(f"add operand {name}: expected a [B, ...] tensor, got {tuple(val.shape)}")
-                zero = torch.zeros(M, device=dev)
-                _, (c_u, c_l) = rows_pass(_Rows(st.A_u, st.A_l, zero, zero), n,
-                                          cvec=val.reshape(B, n).contiguous(), name="add_constant_rows")
-                cb_u, cb_l = pair_add(cb_u, cb_l, c_u, c_l)
+                zu, zl = zeros_like_b(st)
+                _, (c_u, c_l) = rows_pass(_Rows(st.A_u, st.A_l, zu, zl), n, cvec=val.reshape(B, n).contiguous(),
+                                          name="add_constant_rows")
+                one = shared(st)
+                cb_u = add_rows(cb_u, c_u, 1)
+                cb_l = cb_u if one else add_rows(cb_l, c_l, 1)
             for idx, name in enumerate(dyn):
                 # the bias goes with the first operand that depends on the input (crown_ibp.py:922-937)
                 if idx == 0:
                     bu, bl = cb_u, cb_l
                 else:
-                    bu = bl = torch.zeros(M, device=dev)
+                    bu, bl = zeros_like_b(st)
                 accumulate(name, _Rows(st.A_u, st.A_l, bu, bl))
         elif t == "concat":
             out_shape = trace.shapes[out]
@@ -451,16 +499,17 @@ def crown_backward_dag(
                                               f"got {name}")
             _check_concat_shapes([(0,) + tuple(s) for s in shapes], 1, "run_crown_ibp_mlp")
             inner = _numel(out_shape[1:])
+            one = shared(st)
             start = 0
             for idx, (name, shp) in enumerate(zip(op.inputs, shapes)):
                 stop = start + int(shp[0])
                 cols = slice(start * inner, stop * inner)
-                A_u = st.A_u[:, cols].contiguous()
-                A_l = A_u if st.A_l.data_ptr() == st.A_u.data_ptr() else st.A_l[:, cols].contiguous()
+                A_u = st.A_u[:, cols].contiguous() if st.A_u is not None else None
+                A_l = (A_u if one else st.A_l[:, cols].contiguous()) if st.A_l is not None else None
                 if idx == 0:
                     bu, bl = st.b_u, st.b_l
                 else:
-                    bu = bl = torch.zeros(M, device=dev)
+                    bu, bl = zeros_like_b(st)
                 accumulate(name, _Rows(A_u, A_l, bu, bl))
                 start = stop
             if start != int(out_shape[0]):
@@ -472,33 +521,144 @@ def crown_backward_dag(
     st = adjoints.get(spec.value_name)
     if st is None:
         raise RuntimeError(f"run_crown_ibp_mlp backward did not reach input value {spec.value_name}")
+    if save is not None:
+        save["input_A"] = st.A_l
     return _concretize(spec, st, B, S)
+
+
+def _input_center_radius(spec: InputSpec, B: int, I: int):
+    """(center, rad or None, eps) of the input set: a box's midpoint and radius, or a Linf ball."""
+    pert = spec.perturbation
+    if isinstance(pert, BoxPerturbation):
+        lo = pert.lower.reshape(B, I)
+        hi = pert.upper.reshape(B, I)
+        return ((lo + hi) / 2.0).contiguous(), ((hi - lo) / 2.0).contiguous(), 1.0
+    return spec.center.reshape(B, I).contiguous(), None, float(pert.eps)
 
 
 def _concretize(spec: InputSpec, st: _Rows, B: int, S: int) -> IntervalState:
     """concretize_affine (perturbation.py:175-222, 327-359) on dense rows."""
     stream = _lib.stream_handle()
     dev = spec.center.device
-    I = int(st.A_u.shape[1])
-    pert = spec.perturbation
-    if isinstance(pert, BoxPerturbation):
-        lo = pert.lower.reshape(B, I)
-        hi = pert.upper.reshape(B, I)
-        center = ((lo + hi) / 2.0).contiguous()
-        rad = ((hi - lo) / 2.0).contiguous()
-        eps = 1.0
-    else:
-        center = spec.center.reshape(B, I).contiguous()
-        rad = None
-        eps = float(pert.eps)
-    lb = torch.empty(B, S, device=dev)
-    ub = torch.empty(B, S, device=dev)
-    with _timed("concretize_dense", 2.0 * 2 * B * S * I, 4.0 * 2 * B * S * I):
-        _lib.call("bf_concretize_dense", _lib.ptr(st.A_u), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
-                  _lib.ptr(st.b_u), 0, _lib.ptr(ub), stream)
-        _lib.call("bf_concretize_dense", _lib.ptr(st.A_l), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
-                  _lib.ptr(st.b_l), 1, _lib.ptr(lb), stream)
+    I = int((st.A_u if st.A_u is not None else st.A_l).shape[1])
+    center, rad, eps = _input_center_radius(spec, B, I)
+    lb = torch.empty(B, S, device=dev) if st.A_l is not None else None
+    ub = torch.empty(B, S, device=dev) if st.A_u is not None else None
+    nz = int(lb is not None) + int(ub is not None)
+    with _timed("concretize_dense", 2.0 * nz * B * S * I, 4.0 * nz * B * S * I):
+        if ub is not None:
+            _lib.call("bf_concretize_dense", _lib.ptr(st.A_u), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
+                      _lib.ptr(st.b_u), 0, _lib.ptr(ub), stream)
+        if lb is not None:
+            _lib.call("bf_concretize_dense", _lib.ptr(st.A_l), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
+                      _lib.ptr(st.b_l), 1, _lib.ptr(lb), stream)
     return IntervalState(lower=lb, upper=ub)
+
+
+def lower_grad_pass(module: BFTaskModule, spec: InputSpec, trace: DagTrace, saved: dict, B: int,
+                    alpha: Dict[str, Tuple[torch.Tensor, int]], splits: Dict[str, Tuple[torch.Tensor, int]],
+                    G: torch.Tensor) -> Tuple[Dict[str, torch.Tensor], Dict[str, torch.Tensor]]:
+    """Reverse pass of the lower bound of a DAG task (what autograd computes through
+    crown_ibp.py:1669-2051 for alpha_beta_crown.py:913-923): dL/dalpha and dL/dbeta per
+    ReLU ([B, n]), with G = dL/dlb per coefficient row.
+
+    GA[v] = dL/dA_v for the backward state A_v of value v.  A_v is read once, by the
+    backward of v's producer, so the ops run in forward order and each defines the
+    gradient of its output from those of its inputs: the concretization seeds the input;
+    linear GA[y] = GA[x] W^T + G bias^T; conv2d the forward convolution of GA[x] plus
+    G bias^T; relu through the relaxation (bf_relu_grad, which also reduces dL/dalpha and
+    dL/dbeta); add the sum of its operands' gradients (plus G c^T for a constant c);
+    concat the concatenation of its operands' gradients; flatten/reshape the same rows."""
+    task = _module_task(module)
+    params = module.params
+    dev = spec.center.device
+    stream = _lib.stream_handle()
+    S = int(saved["S"])
+    M = B * S
+    A_in = saved["input_A"]
+    I = int(A_in.shape[1])
+    center, rad, eps = _input_center_radius(spec, B, I)
+    GA: Dict[str, torch.Tensor] = {}
+    g0 = torch.empty(M, I, device=dev)
+    with _timed("concretize_dense_grad", 0.0, 4.0 * 3 * M * I):
+        _lib.call("bf_concretize_dense_grad", _lib.ptr(A_in), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
+                  _lib.ptr(G), _lib.ptr(g0), stream)
+    GA[spec.value_name] = g0
+    g_alpha: Dict[str, torch.Tensor] = {}
+    g_beta: Dict[str, torch.Tensor] = {}
+    ran = saved["ran"]
+    for op_index, op in enumerate(task.ops):
+        if op_index not in ran:
+            continue
+        t = op.op_type
+        y = op.outputs[0]
+        x = op.inputs[0]
+        if t == "linear":
+            W = params[op.inputs[1]].contiguous()
+            bias = params[op.inputs[2]].contiguous() if len(op.inputs) == 3 else None
+            n_out, n_in = int(W.shape[0]), int(W.shape[1])
+            gt = torch.empty(M, n_out, device=dev)
+            wsz = int(_lib.load().bf_gemm_rank1_workspace(M, n_out, n_in))
+            ws = torch.empty(wsz, device=dev) if wsz else None
+            with _timed("grad_gemm", 2.0 * M * n_in * n_out, 4.0 * (M * n_in + M * n_out + n_in * n_out)):
+                _lib.call("bf_gemm_rank1", _lib.ptr(GA[x]), n_in, _lib.ptr(W), n_in, 1, _lib.ptr(gt), n_out, M,
+                          n_out, n_in, S, _lib.ptr(G if bias is not None else None), _lib.ptr(bias), 0, _lib.ptr(ws),
+                          wsz, stream)
+            GA[y] = gt
+        elif t == "conv2d":
+            W = params[op.inputs[1]].contiguous()
+            in_shape = trace.shapes[x]
+            (sh, sw), (ph, pw), out_shape = _conv_geometry(op, W, in_shape)
+            Ci, Hi, Wi = in_shape
+            Co, Ho, Wo = out_shape
+            KH, KW = int(W.shape[2]), int(W.shape[3])
+            vec = _conv_bias_map(params[op.inputs[2]], out_shape) if len(op.inputs) == 3 else None
+            gt = torch.empty(M, Co * Ho * Wo, device=dev)
+            with _timed("grad_conv", 2.0 * M * Co * Ho * Wo * Ci * KH * KW, 4.0 * (M * Ci * Hi * Wi + M * Co * Ho * Wo)):
+                _lib.call("bf_conv2d_rows", _lib.ptr(GA[x]), 1, M, Ci, Hi, Wi, _lib.ptr(W), 0, Co, KH, KW, sh, sw, ph,
+                          pw, Ho, Wo, _lib.ptr(gt), _lib.ptr(G if vec is not None else None), _lib.ptr(vec), 1, 0,
+                          stream)
+            GA[y] = gt
+        elif t == "relu":
+            pre = trace.relu_pre[x]
+            n = _numel(pre.lower.shape[1:])
+            a_t, a_ld = alpha.get(x, (None, 0))
+            sp, sp_ld = splits.get(x, (None, 0))
+            ga = torch.empty(B, n, device=dev)
+            gb = torch.empty(B, n, device=dev)
+            g_in = torch.empty(M, n, device=dev)
+            with _timed("relu_grad", 0.0, 4.0 * (3 * M * n + 4 * B * n)):
+                _lib.call("bf_relu_grad", _lib.ptr(GA[x]), _lib.ptr(saved["relu_A"][op_index]), S * n, B, S, n,
+                          _lib.ptr(pre.lower.reshape(B, n)), _lib.ptr(pre.upper.reshape(B, n)), _lib.ptr(a_t), a_ld,
+                          _lib.ptr(G), _lib.ptr(sp), sp_ld, _lib.ptr(g_in), _lib.ptr(ga), _lib.ptr(gb), stream)
+            g_alpha[x] = ga
+            g_beta[x] = gb
+            GA[y] = g_in
+        elif t in ("flatten", "reshape"):
+            GA[y] = GA[x]
+        elif t == "add":
+            n = _numel(trace.shapes[y])
+            acc = None
+            for name in op.inputs:
+                if name in trace.shapes:
+                    if acc is None:
+                        acc = GA[name]
+                        continue
+                    out = torch.empty(M, n, device=dev)
+                    _lib.call("bf_rows_add", _lib.ptr(acc), _lib.ptr(GA[name]), M, n, S, None, None, 0, _lib.ptr(out),
+                              stream)
+                    acc = out
+                else:
+                    c = params[name].to(device=dev, dtype=torch.float32).reshape(B, n).contiguous()
+                    out = torch.empty(M, n, device=dev)
+                    _lib.call("bf_rows_add", _lib.ptr(acc), None, M, n, S, _lib.ptr(G), _lib.ptr(c), n, _lib.ptr(out),
+                              stream)
+                    acc = out
+            GA[y] = acc
+        elif t == "concat":
+            parts = [GA[name].reshape(M, trace.shapes[name][0], -1) for name in op.inputs]
+            GA[y] = torch.cat(parts, dim=1).reshape(M, -1)
+    return g_alpha, g_beta
 
 
 def run_crown_ibp_dag(

@@ -54,6 +54,38 @@ __global__ void relu_grad_kernel(const float* __restrict__ g_out, const float* _
   }
 }
 
+// dL/dA of the dense concretization of the lower bound (perturbation.py:175-222, 327-359):
+//   lb[m] = A[m, :] . c[d, :] - sum_j w[d, j] |A[m, j]| + b[m],  w = eps (Linf) or the box radius,
+//   g[m, j] = G[m] * c[d, j] + (G[m] * -w[d, j]) * sign(A[m, j])   (sign(0) = 0, as autograd's abs).
+__global__ void concretize_dense_grad_kernel(const float* __restrict__ A, int64_t M, int64_t S, int64_t I,
+                                             const float* __restrict__ cen, const float* __restrict__ rad, float eps,
+                                             const float* __restrict__ G, float* __restrict__ g) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * I) return;
+  const int64_t m = i / I, j = i - (i / I) * I;
+  const int64_t e = (m / S) * I + j;
+  const float a = A[i];
+  const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
+  const float w = rad ? rad[e] : eps;
+  g[i] = G[m] * cen[e] + (G[m] * -w) * sg;
+}
+
+// out[m, n] = (a[m, n] + b[m, n]) + r_row[m] * vec[(m / S) * v_ld + n], each term optional;
+// out may be a or b (elementwise, each element read before it is written).
+__global__ void rows_add_kernel(const float* a, const float* b, int64_t M, int64_t N, int64_t S,
+                                const float* __restrict__ r_row, const float* __restrict__ vec, int64_t v_ld,
+                                float* out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * N) return;
+  float v = a ? a[i] : 0.f;
+  if (b) v = a ? v + b[i] : b[i];
+  if (r_row) {
+    const int64_t m = i / N, n = i - (i / N) * N;
+    v = v + r_row[m] * vec[(m / S) * v_ld + n];
+  }
+  out[i] = v;
+}
+
 // add[d, n] = -beta[d, n] * s[d, n] * 1(s != 0)
 __global__ void beta_coeff_kernel(const float* __restrict__ beta, int64_t beta_ld, const int8_t* __restrict__ split,
                                   int64_t split_ld, int64_t D, int64_t N, float* __restrict__ out) {
@@ -151,6 +183,30 @@ int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t 
   hipLaunchKernelGGL(relu_grad_kernel, dim3((unsigned)ceil_div(D * N, 256)), dim3(256), 0, stream, g_out, A,
                      a_dstride, D, S, N, pre_lo, pre_hi, alpha, alpha_ld, G, split, split_ld, g_in, g_alpha, g_beta);
   BF_LAUNCH_CHECK("relu_grad_kernel");
+  return BF_OK;
+}
+
+int bf_concretize_dense_grad(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
+                             float eps, const float* G, float* g, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && I > 0, "bf_concretize_dense_grad: bad sizes");
+  if (D == 0) return BF_OK;
+  BF_REQUIRE(A && center && G && g, "bf_concretize_dense_grad: null pointer");
+  const int64_t n = D * S * I;
+  hipLaunchKernelGGL(concretize_dense_grad_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, A, D * S,
+                     S, I, center, rad, eps, G, g);
+  BF_LAUNCH_CHECK("concretize_dense_grad_kernel");
+  return BF_OK;
+}
+
+int bf_rows_add(const float* a, const float* b, int64_t M, int64_t N, int64_t S, const float* r_row, const float* vec,
+                int64_t v_ld, float* out, hipStream_t stream) {
+  BF_REQUIRE(M >= 0 && N > 0 && S > 0 && v_ld >= 0, "bf_rows_add: bad sizes");
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(out && (a || b || r_row), "bf_rows_add: null pointer");
+  BF_REQUIRE(r_row == nullptr || vec != nullptr, "bf_rows_add: rank-1 term without its vector");
+  hipLaunchKernelGGL(rows_add_kernel, dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0, stream, a, b, M, N, S,
+                     r_row, vec, v_ld, out);
+  BF_LAUNCH_CHECK("rows_add_kernel");
   return BF_OK;
 }
 

@@ -266,6 +266,20 @@ int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t 
                  const int8_t* split, int64_t split_ld, float* g_in, float* g_alpha, float* g_beta,
                  hipStream_t stream);
 
+/* dL/dA of the dense concretization of the lower bound (bf_concretize_dense, is_lower = 1):
+ * g[m, j] = G[m] * center[d, j] + (G[m] * -w[d, j]) * sign(A[m, j]), w = eps (rad NULL) or rad [D, I];
+ * the autograd backward of concretize_affine (runtime/perturbation.py:175-222, 327-359) at the input of a
+ * DAG task, driven by runtime/alpha_beta_crown.py:913-923. */
+int bf_concretize_dense_grad(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
+                             float eps, const float* G, float* g, hipStream_t stream);
+
+/* out[m, n] = (a[m, n] + b[m, n]) + r_row[m] * vec[(m / S) * v_ld + n], every term optional (NULL), out may
+ * alias a or b: the fan-in accumulation of backward states (runtime/crown_ibp.py:892-909, A_cur.add(A_upd))
+ * and, in the reverse pass of a DAG task, the sum of an add's operand gradients with the rank-1 term of a
+ * constant operand (runtime/crown_ibp.py:1928-1970). */
+int bf_rows_add(const float* a, const float* b, int64_t M, int64_t N, int64_t S, const float* r_row, const float* vec,
+                int64_t v_ld, float* out, hipStream_t stream);
+
 /* beta split coefficient add = -beta * s * 1(s != 0) (runtime/alpha_beta_crown.py:615-640). */
 int bf_beta_coeff(const float* beta, int64_t beta_ld, const int8_t* split, int64_t split_ld, int64_t D, int64_t N,
                   float* out, hipStream_t stream);

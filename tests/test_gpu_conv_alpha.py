@@ -90,6 +90,10 @@ def _abs_op(op):
     if isinstance(op, cr.Conv2dOp):
         return cr.Conv2dOp(_abs_op(op.base), op.weight.abs(), op.stride, op.padding, op.dilation, op.groups,
                            op.input_shape)
+    if isinstance(op, cr.AddOp):
+        return cr.AddOp(_abs_op(op.lhs), _abs_op(op.rhs))
+    if isinstance(op, cr.SliceOp):
+        return cr.SliceOp(_abs_op(op.base), op.input_shape, op.start, op.stop)
     raise TypeError(type(op))
 
 

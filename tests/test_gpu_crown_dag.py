@@ -6,12 +6,15 @@ whose DAG pieces are pinned in tests/test_oracle_dag.py."""
 import pytest
 import torch
 
+from boundflow_amd import alpha_beta as hab
 from boundflow_amd import crown as hc
 from boundflow_amd import crown_dag
 from boundflow_amd import workloads as wl
+from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
 from oracle import parity
 from tests.gpu_util import announce, assert_bounds_close, assert_parity, assert_verdicts, device
+from tests.test_gpu_conv_alpha import _grad_close, _oracle_grads, _sign_tie_allowance
 
 pytestmark = pytest.mark.gpu
 
@@ -141,3 +144,91 @@ def test_dag_crown_rejects_broadcast_add():
     spec = InputSpec.linf(value_name="input", center=torch.rand(2, 3, device=dev), eps=0.1)
     with pytest.raises(NotImplementedError, match="same-shape"):
         hc.run_crown_ibp_mlp(module, spec)
+
+
+def _feasible_splits(w, g):
+    """Random splits on neurons ambiguous given the splits of the ReLUs before them."""
+    _env, pre = cr.forward_ibp_trace(w.module, w.spec)
+    splits = {}
+    for name in pre:
+        _env, cur = cr.forward_ibp_trace(w.module, w.spec, relu_split_state=dict(splits))
+        st = cur[name]
+        amb = (st.lower < 0) & (st.upper > 0)
+        choice = torch.randint(-1, 2, tuple(st.lower.shape), generator=g).to(torch.int8)
+        splits[name] = torch.where(amb, choice, torch.zeros_like(choice))
+    return splits
+
+
+@pytest.mark.parametrize("kind,with_beta", [("residual_mlp", True), ("residual_mlp", False),
+                                            ("projection_skip_cnn", True), ("feature_concat_mlp", False),
+                                            ("channel_concat_cnn", True)])
+def test_dag_lower_bound_gradients_match_autograd(kind, with_beta):
+    """The reverse pass of the DAG backward (crown_dag.lower_grad_pass) against autograd
+    through the oracle's DAG backward: dL/dalpha and dL/dbeta for L = -sum_d mean_s lb."""
+    dev = device()
+    announce(f"DAG alpha/beta gradient pass vs autograd: {kind} beta={with_beta}")
+    g = torch.Generator().manual_seed(31)
+    w = wl.make_dag(kind, seed=8, batch=3, eps=0.03, blocks=2)
+    splits = _feasible_splits(w, g) if with_beta else None
+    _env, pre = cr.forward_ibp_trace(w.module, w.spec, relu_split_state=splits)
+    alpha = {k: torch.rand(v.lower.shape, generator=g) for k, v in pre.items()}
+    beta = {k: torch.rand(v.lower.shape, generator=g) for k, v in pre.items()} if with_beta else None
+    ref32, ga32, gb32 = _oracle_grads(w, alpha, beta, splits)
+    ref64, ga64, gb64 = _oracle_grads(w, alpha, beta, splits, dtype=torch.float64)
+    wd = wl.to_device(w, dev)
+    sd = None if splits is None else {k: v.to(dev) for k, v in splits.items()}
+    bounds, ga, gb = hab.lower_bound_gradients(
+        wd.module, wd.spec, linear_spec_C=wd.C, relu_alpha={k: v.to(dev) for k, v in alpha.items()},
+        relu_beta=None if beta is None else {k: v.to(dev) for k, v in beta.items()}, relu_split_state=sd)
+    torch.cuda.synchronize()
+    assert_parity(bounds.lower, ref32.lower, ref64.lower, f"{kind} lower")
+    allow = None
+    if beta is None:
+        allow, nties = _sign_tie_allowance(parity.to_float64(w), {k: v.double() for k, v in alpha.items()},
+                                           per_batch=True)
+        announce(f"{kind}: {nties} input-layer coefficients within fp32 rounding of zero")
+    assert set(ga.keys()) == set(ga32.keys())
+    for k in ga32:
+        _grad_close(ga[k], ga32[k], ga64[k], f"{kind} dL/dalpha[{k}]", None if allow is None else allow[k])
+    if gb32 is not None:
+        for k in gb32:
+            _grad_close(gb[k], gb32[k], gb64[k], f"{kind} dL/dbeta[{k}]")
+
+
+@pytest.mark.parametrize("kind", ["residual_mlp", "channel_concat_cnn"])
+def test_dag_alpha_crown_matches_oracle(kind):
+    """Per-domain alpha from the CROWN relaxation, 10 Adam steps (the C4 recipe) on a DAG task."""
+    dev = device()
+    announce(f"DAG alpha-CROWN {kind}, 10 steps")
+    w = wl.make_dag(kind, seed=9, batch=4, eps=0.03, blocks=2)
+    wd = wl.to_device(w, dev)
+    bounds, alpha, _beta, _st = hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C,
+                                                                    steps=10, lr=0.1)
+    torch.cuda.synchronize()
+    _env, pre = cr.forward_ibp_trace(w.module, w.spec)
+    init = ab.adaptive_alpha_init(pre)
+    ref = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, steps=10, lr=0.1, warm_start_alpha=init,
+                                  per_batch_params=True)[0]
+    crown = cr.run_crown_ibp(w.module, w.spec, linear_spec_C=w.C)
+    # Adam trajectories of two fp32 runs drift by rounding: 1e-4 relative, as for C4
+    assert_bounds_close(bounds.lower, ref.lower, f"{kind} alpha lower", rtol=1e-4, atol=1e-4)
+    assert_bounds_close(bounds.upper, ref.upper, f"{kind} alpha upper", rtol=1e-4, atol=1e-4)
+    assert bool((bounds.lower.cpu() >= crown.lower - 1e-4 * crown.lower.abs() - 1e-4).all())
+
+
+def test_dag_alpha_beta_crown_with_splits_matches_oracle():
+    """alpha-beta-CROWN (per-domain parameters, split multipliers) on the residual MLP."""
+    dev = device()
+    announce("DAG alpha-beta-CROWN residual_mlp with splits, 8 steps")
+    g = torch.Generator().manual_seed(33)
+    w = wl.make_dag("residual_mlp", seed=10, batch=4, eps=0.03, blocks=2)
+    splits = _feasible_splits(w, g)
+    wd = wl.to_device(w, dev)
+    bounds, _a, _b, _st = hab.run_alpha_beta_crown_mlp(
+        wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state={k: v.to(dev) for k, v in splits.items()},
+        steps=8, lr=0.2, per_batch_params=True)
+    torch.cuda.synchronize()
+    ref = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, relu_split_state=splits, steps=8, lr=0.2,
+                                  per_batch_params=True)[0]
+    assert_bounds_close(bounds.lower, ref.lower, "alpha-beta lower", rtol=1e-4, atol=1e-4)
+    assert_bounds_close(bounds.upper, ref.upper, "alpha-beta upper", rtol=1e-4, atol=1e-4)
