@@ -23,7 +23,7 @@ import torch
 
 from . import _lib
 from .alpha_beta import branch_tensors, run_alpha_beta_crown_mlp, run_alpha_crown_mlp
-from .crown import forward_ibp_trace, parse_chain
+from .crown import NotAChain, forward_ibp_trace, parse_chain
 from .spec import BoxPerturbation, InputSpec, normalize_input_spec
 
 
@@ -37,7 +37,7 @@ def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
     2 infeasible), ``lower``/``upper`` [D, S], ``branch_layer``/``branch_neuron``
     int32 [D] (-1 when no ambiguous neuron is left), ``alpha``/``beta`` per ReLU."""
     spec = normalize_input_spec(input_spec)
-    chain = parse_chain(module, spec)
+    chain, _shapes, _has_conv = _relu_layout(module, spec)
     trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
                               raise_on_infeasible=False)
     D = int(spec.center.shape[0])
@@ -53,6 +53,18 @@ def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
     return {"status": status, "lower": bounds.lower, "upper": bounds.upper, "branch_layer": layer,
             "branch_neuron": neuron, "alpha": alpha, "beta": beta, "infeasible": trace.infeasible,
             "relu_names": list(trace.relu_pre.keys())}
+
+
+def _relu_layout(module, spec):
+    """(chain or None, per-sample shape of every ReLU input in op order, whether a conv2d
+    is present) for a chain or a DAG task."""
+    try:
+        chain = parse_chain(module, spec)
+    except NotAChain:
+        from .crown_dag import relu_input_shapes
+        task = module.get_entry_task()
+        return None, relu_input_shapes(module, spec), any(op.op_type == "conv2d" for op in task.ops)
+    return chain, dict(chain.relu_shapes), any(layer.kind == "conv2d" for layer in chain.layers)
 
 
 # ---------------------------------------------------------------------------
@@ -182,13 +194,12 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
         raise ValueError(f"unknown BaB oracle: {cfg.oracle}")
     spec = normalize_input_spec(input_spec)
     module.validate()
-    chain = parse_chain(module, spec)
-    has_conv = any(layer.kind == "conv2d" for layer in chain.layers)
+    chain, relu_shapes, has_conv = _relu_layout(module, spec)
     if has_conv and cfg.oracle != "alpha_beta":
         raise NotImplementedError("alpha-only BaB does not yet support conv graphs")
     dev = spec.center.device
     E = int(spec.center.shape[0])
-    sizes = {name: int(torch.tensor(chain.relu_shapes[name]).prod()) for name in chain.relu_names}
+    sizes = {name: int(torch.tensor(shape).prod()) for name, shape in relu_shapes.items()}
     names = list(sizes)
     front = _Frontier(sizes, dev)
     threshold, tol = float(cfg.threshold), float(cfg.tol)
@@ -242,7 +253,7 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
         if do_batch:
             batch_rounds += 1
             popped_total += len(items)
-        out = _evaluate_nodes(module, spec, chain, linear_spec_C, items, front, names, cfg)
+        out = _evaluate_nodes(module, spec, chain, relu_shapes, linear_spec_C, items, front, names, cfg)
         expansions: List[Tuple[int, int, int]] = []   # (row in this round, layer, neuron)
         child_meta: List[Tuple[int, float]] = []      # (example, priority) per expansion
         for row, item in enumerate(items):
@@ -311,7 +322,7 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
                      per_example=per)
 
 
-def _evaluate_nodes(module, spec, chain, linear_spec_C, items, front: _Frontier, names, cfg: BabConfig):
+def _evaluate_nodes(module, spec, chain, shapes, linear_spec_C, items, front: _Frontier, names, cfg: BabConfig):
     """One round: gather the popped nodes' inputs, splits and warm starts from
     the frontier, run the oracle on all of them, and return the node
     lower/upper bounds, infeasibility and branch decisions on the host (one
@@ -326,7 +337,6 @@ def _evaluate_nodes(module, spec, chain, linear_spec_C, items, front: _Frontier,
     else:
         sub = InputSpec(value_name=spec.value_name, center=spec.center[ex], perturbation=pert)
     C = None if linear_spec_C is None else linear_spec_C[ex]
-    shapes = chain.relu_shapes
     split = {n: front.split[n][sl] for n in names}
     split_by = {n: split[n].reshape((b,) + tuple(shapes[n])) for n in names}
     warm_a = {n: front.alpha[n][sl].reshape((b,) + tuple(shapes[n])) for n in names}

@@ -116,6 +116,40 @@ def _module_task(module: BFTaskModule):
     return task
 
 
+def relu_input_shapes(module: BFTaskModule, spec: InputSpec) -> Dict[str, Tuple[int, ...]]:
+    """Per-sample shape of every ReLU input, in op order (the order of a trace's relu_pre),
+    from the ops' shape rules alone (no launch)."""
+    task = _module_task(module)
+    params = module.params
+    shapes: Dict[str, Tuple[int, ...]] = {spec.value_name: tuple(int(d) for d in spec.center.shape[1:])}
+
+    def shape_of(name):
+        return shapes[name] if name in shapes else tuple(int(d) for d in params[name].shape[1:])
+
+    out: Dict[str, Tuple[int, ...]] = {}
+    for op in task.ops:
+        t = op.op_type
+        x = op.inputs[0]
+        if t == "linear":
+            y = (int(params[op.inputs[1]].shape[0]),)
+        elif t == "conv2d":
+            y = _conv_geometry(op, params[op.inputs[1]], shape_of(x))[2]
+        elif t == "relu":
+            out[x] = shape_of(x)
+            y = shape_of(x)
+        elif t == "add":
+            y = shape_of(x)
+        elif t == "concat":
+            parts = [shape_of(n) for n in op.inputs]
+            y = (sum(p[0] for p in parts),) + tuple(parts[0][1:])
+        elif t == "flatten":
+            y = (_numel(shape_of(x)),)
+        else:
+            y = tuple(int(d) for d in op.attrs["shape"][1:])
+        shapes[op.outputs[0]] = y
+    return out
+
+
 def forward_ibp_trace_dag(
     module: BFTaskModule,
     input_spec,

@@ -232,3 +232,37 @@ def test_dag_alpha_beta_crown_with_splits_matches_oracle():
                                   per_batch_params=True)[0]
     assert_bounds_close(bounds.lower, ref.lower, "alpha-beta lower", rtol=1e-4, atol=1e-4)
     assert_bounds_close(bounds.upper, ref.upper, "alpha-beta upper", rtol=1e-4, atol=1e-4)
+
+
+DAG_BAB = {
+    "ab_e006_s11": (0.06, 11, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "ab_e006_s12": (0.06, 12, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "alpha_e003_s12": (0.03, 12, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
+}
+
+
+@pytest.mark.parametrize("tag", list(DAG_BAB))
+def test_dag_bab_search_matches_oracle(tag):
+    """solve_bab_mlp on a residual MLP: the whole search (statuses, node counts, rounds,
+    queue) identical to the oracle's, best bounds within rtol 1e-4."""
+    from boundflow_amd import bab as hbab
+    from oracle import bab_ref
+    dev = device()
+    eps, seed, kw = DAG_BAB[tag]
+    announce(f"DAG solve_bab_mlp {tag}")
+    w = wl.make_dag("residual_mlp", seed=seed, batch=4, eps=eps, n_in=8, hidden=12, n_out=4, blocks=1)
+    cfg = dict(use_branch_hint=True, alpha_lr=0.2, alpha_init=0.5, beta_init=0.0, threshold=0.0, tol=1e-6, **kw)
+    ref = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
+    wd = wl.to_device(w, dev)
+    r = hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C, config=hbab.BabConfig(**kw))
+    per = r.per_example
+    announce(f"  statuses {[p.status for p in per]} visited {[p.nodes_visited for p in per]} rounds {r.batch_rounds}")
+    assert r.status == ref["status"]
+    assert [p.status for p in per] == ref["per_status"]
+    assert [p.nodes_visited for p in per] == ref["per_visited"]
+    assert [p.nodes_evaluated for p in per] == ref["per_evaluated"]
+    assert [p.nodes_expanded for p in per] == ref["per_expanded"]
+    assert (r.max_queue, r.batch_rounds) == (ref["max_queue"], ref["batch_rounds"])
+    import numpy as np
+    np.testing.assert_allclose([p.best_lower for p in per], ref["per_best_lower"], rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose([p.best_upper for p in per], ref["per_best_upper"], rtol=1e-4, atol=1e-5)
