@@ -83,8 +83,12 @@ __global__ void row_abs_sum_kernel(const float* __restrict__ W, int64_t O, int64
 
 // lo = (c - dev) + b, hi = (c + dev) + b, then the ReLU split of the consumer
 // (crown_ibp.py:70-98): active -> lo = max(lo, 0); inactive -> hi = min(hi, 0);
-// a domain with lo > hi anywhere is flagged infeasible.
+// a domain with lo > hi anywhere is flagged infeasible.  With `part`, c (and r
+// when two products were taken) are the split-K partial products [z][s][B*N],
+// summed here in chunk order (the order of splitk_reduce_kernel), and c is also
+// written to c_out when given.
 __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __restrict__ r,
+                                    const float* __restrict__ part, int ks, int two, float* __restrict__ c_out,
                                     const float* __restrict__ rownorm, float eps, const float* __restrict__ bias,
                                     int64_t bias_div, const int8_t* __restrict__ split, int64_t split_ld, int64_t B,
                                     int64_t N, float* __restrict__ lo, float* __restrict__ hi,
@@ -92,9 +96,23 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= B * N) return;
   int64_t b = i / N, n = i % N;
-  float dev = rownorm ? eps * rownorm[n] : r[i];
-  float l = c[i] - dev;
-  float u = c[i] + dev;
+  float cv, rv = 0.f;
+  if (part) {
+    const int64_t BN = B * N;
+    cv = part[i];
+    for (int s = 1; s < ks; ++s) cv += part[(int64_t)s * BN + i];
+    if (two) {
+      rv = part[(int64_t)ks * BN + i];
+      for (int s = 1; s < ks; ++s) rv += part[(int64_t)(ks + s) * BN + i];
+    }
+    if (c_out) c_out[i] = cv;
+  } else {
+    cv = c[i];
+    if (r) rv = r[i];
+  }
+  float dev = rownorm ? eps * rownorm[n] : rv;
+  float l = cv - dev;
+  float u = cv + dev;
   if (bias) {
     l = l + bias[n / bias_div];
     u = u + bias[n / bias_div];
@@ -124,14 +142,22 @@ int fill_value(float* p, int64_t n, float v, hipStream_t stream) {
 int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
                       hipStream_t stream);
 
+static int ibp_finalize_parts(const float* c, const float* r, const float* part, int ks, int two, float* c_out,
+                              const float* rownorm, float eps, const float* bias, int64_t bias_div,
+                              const int8_t* split, int64_t split_ld, int64_t B, int64_t N, float* lo, float* hi,
+                              int* infeasible, hipStream_t stream) {
+  if (B * N == 0) return BF_OK;
+  hipLaunchKernelGGL(ibp_finalize_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, c, r, part, ks,
+                     two, c_out, rownorm, eps, bias, bias_div, split, split_ld, B, N, lo, hi, infeasible);
+  BF_LAUNCH_CHECK("ibp_finalize_kernel");
+  return BF_OK;
+}
+
 int ibp_finalize(const float* c, const float* r, const float* rownorm, float eps, const float* bias,
                  int64_t bias_div, const int8_t* split, int64_t split_ld, int64_t B, int64_t N, float* lo, float* hi,
                  int* infeasible, hipStream_t stream) {
-  if (B * N == 0) return BF_OK;
-  hipLaunchKernelGGL(ibp_finalize_kernel, dim3((unsigned)ceil_div(B * N, 256)), dim3(256), 0, stream, c, r, rownorm,
-                     eps, bias, bias_div, split, split_ld, B, N, lo, hi, infeasible);
-  BF_LAUNCH_CHECK("ibp_finalize_kernel");
-  return BF_OK;
+  return ibp_finalize_parts(c, r, nullptr, 1, 0, nullptr, rownorm, eps, bias, bias_div, split, split_ld, B, N, lo,
+                            hi, infeasible, stream);
 }
 
 // Intersect with external constraints (crown_ibp.py:186-209) and apply a split.
@@ -1205,8 +1231,10 @@ int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const f
 // contraction kernel (product z = blockIdx.y).  An output of few tiles (a small
 // batch) is split along K into the partial buffer `part`, whose chunks are added
 // in chunk order.
+// When K is split (*ks > 1), the partial products stay in `part` ([z][s][B*N]) for
+// the finalize kernel to sum; otherwise c (and r) hold the products.
 static int ibp_products(const float* xc, const float* xr, const float* W, int64_t B, int64_t K, int64_t N, float* c,
-                        float* r, float* part, hipStream_t stream) {
+                        float* r, float* part, int* ks_out, hipStream_t stream) {
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   const int nz = xr ? 2 : 1;
@@ -1232,13 +1260,8 @@ static int ibp_products(const float* xc, const float* xr, const float* W, int64_
     a.kchunk = kchunk;
     a.part = part;
   }
-  int rc = gemm_dispatch(a, PRO_PLAIN, EPI_STORE, nz, stream);
-  if (rc || ks == 1) return rc;
-  for (int z = 0; z < nz; ++z) {
-    rc = splitk_reduce(part + (int64_t)z * ks * B * N, ks, B, N, z ? r : c, N, nullptr, nullptr, 0, 1, stream);
-    if (rc) return rc;
-  }
-  return BF_OK;
+  *ks_out = ks;
+  return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, nz, stream);
 }
 
 int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, int input_kind, float eps,
@@ -1258,20 +1281,22 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   float* part = rownorm + N;
   float* cdst = center_out ? center_out : c;
   int rc;
+  int ks = 1;
   if (input_kind == 1) {
-    rc = ibp_products(in_lo, nullptr, W, B, K, N, cdst, nullptr, part, stream);
+    rc = ibp_products(in_lo, nullptr, W, B, K, N, cdst, nullptr, part, &ks, stream);
     if (rc) return rc;
     hipLaunchKernelGGL(row_abs_sum_kernel, dim3((unsigned)N), dim3(256), 0, stream, W, N, K, rownorm);
     BF_LAUNCH_CHECK("row_abs_sum_kernel");
-    return ibp_finalize(cdst, nullptr, rownorm, eps, bias, 1, split, split_ld, B, N, out_lo, out_hi, infeasible,
-                        stream);
+    return ibp_finalize_parts(cdst, nullptr, ks > 1 ? part : nullptr, ks, 0, center_out, rownorm, eps, bias, 1,
+                              split, split_ld, B, N, out_lo, out_hi, infeasible, stream);
   }
   BF_REQUIRE(in_hi, "bf_ibp_linear: interval input needs in_hi");
   rc = ibp_center_radius(in_lo, in_hi, B * K, apply_relu, mid, rad, stream);
   if (rc) return rc;
-  rc = ibp_products(mid, rad, W, B, K, N, cdst, r, part, stream);
+  rc = ibp_products(mid, rad, W, B, K, N, cdst, r, part, &ks, stream);
   if (rc) return rc;
-  return ibp_finalize(cdst, r, nullptr, 0.f, bias, 1, split, split_ld, B, N, out_lo, out_hi, infeasible, stream);
+  return ibp_finalize_parts(cdst, r, ks > 1 ? part : nullptr, ks, 1, center_out, nullptr, 0.f, bias, 1, split,
+                            split_ld, B, N, out_lo, out_hi, infeasible, stream);
 }
 
 int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) {
