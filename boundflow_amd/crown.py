@@ -26,8 +26,9 @@ behaviour.
 
 from __future__ import annotations
 
+from collections import OrderedDict
 from dataclasses import dataclass, field
-from typing import Dict, List, Mapping, Optional, Tuple
+from typing import Callable, Dict, List, Mapping, Optional, Tuple
 
 import torch
 
@@ -36,6 +37,37 @@ from .profiling import launch as _timed
 from .conv import conv_backward_step, ibp_conv2d
 from .ir import BFTaskModule, TaskKind
 from .spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation, normalize_input_spec
+
+
+# ---------------------------------------------------------------------------
+# Derived operands kept across queries
+
+_DERIVED: "OrderedDict[tuple, tuple]" = OrderedDict()
+_DERIVED_MAX = 64
+
+
+def derived(tag: str, sources: Tuple[torch.Tensor, ...], make: Callable[[], torch.Tensor]) -> torch.Tensor:
+    """``make()`` computed once per (tag, source tensors) and reused while every source is the
+    same tensor object at the same version (no in-place change since): a layer weight's
+    transpose or an input box's radius does not change between the queries of a run, so
+    repeated queries (and graph replays) skip the copy.  The entry keeps its sources alive,
+    so their storage cannot be reused under the same key; at most 64 entries are kept."""
+    key = (tag,) + tuple(id(t) for t in sources)
+    hit = _DERIVED.get(key)
+    versions = tuple(t._version for t in sources)
+    if hit is not None and all(a is b for a, b in zip(hit[0], sources)) and hit[1] == versions:
+        _DERIVED.move_to_end(key)
+        return hit[2]
+    out = make()
+    _DERIVED[key] = (tuple(sources), versions, out)
+    if len(_DERIVED) > _DERIVED_MAX:
+        _DERIVED.popitem(last=False)
+    return out
+
+
+def transposed(W: torch.Tensor) -> torch.Tensor:
+    """W^T, contiguous (the contraction's faster operand layout), kept across queries."""
+    return derived("wt", (W,), lambda: W.t().contiguous())
 
 
 # ---------------------------------------------------------------------------
@@ -416,7 +448,7 @@ def crown_backward(
             continue
         W = layer.weight.contiguous()
         # the contraction reads W^T [P, N] row-major: 128-bit operand loads along N
-        Wt = W.t().contiguous()
+        Wt = transposed(W)
         bias = None if layer.bias is None or pre_relaxed else layer.bias.contiguous()
         P = _numel(layer.in_shape)
         if k > 0 and linear_spec_C is None and k == len(layers) - 1:
@@ -479,9 +511,7 @@ def crown_backward(
         if k == 0:
             # input layer: relaxation + contraction fused with the concretization
             if isinstance(pert, BoxPerturbation):
-                lo = pert.lower.reshape(B, P)
-                hi = pert.upper.reshape(B, P)
-                rad = ((hi - lo) / 2.0).contiguous()
+                rad = _input_radius(pert, B, P)[0]
                 cvec = trace.input_center_proj.get(layer.out_name)
                 # center term A' (mid W^T): the trace holds mid W^T when the input is a box
                 eps = 1.0
@@ -585,7 +615,7 @@ def _input_radius(pert, B: int, P: int):
     if isinstance(pert, BoxPerturbation):
         lo = pert.lower.reshape(B, P)
         hi = pert.upper.reshape(B, P)
-        return ((hi - lo) / 2.0).contiguous(), 1.0
+        return derived("box_rad", (pert.lower, pert.upper), lambda: ((hi - lo) / 2.0).contiguous()), 1.0
     return None, float(pert.eps)
 
 

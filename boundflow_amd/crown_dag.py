@@ -329,7 +329,7 @@ def crown_backward_dag(
     that is not needed is not computed (its side of the result is None).  With ``save``
     (lower bound only) the coefficient entering every ReLU and the input's coefficient are
     kept for ``lower_grad_pass``."""
-    from .crown import _flat_param, _init_spec
+    from .crown import _flat_param, _init_spec, transposed
 
     task = _module_task(module)
     params = module.params
@@ -438,7 +438,7 @@ def crown_backward_dag(
             W = params[op.inputs[1]].contiguous()
             bias = params[op.inputs[2]].contiguous() if len(op.inputs) == 3 else None
             N, P = int(W.shape[0]), int(W.shape[1])
-            Wt = W.t().contiguous()   # the contraction reads W^T [P, N]: 128-bit operand loads along N
+            Wt = transposed(W)   # the contraction reads W^T [P, N]: 128-bit operand loads along N
             one = shared(st)
             nA_u, nA_l = like(st, P, one)
             nb_u, nb_l = like(_Rows(st.b_u, st.b_l, None, None), 1, one)
