@@ -37,6 +37,7 @@ from .crown import (
     _broadcast_split,
     _numel,
     crown_backward,
+    derived,
     forward_ibp_trace,
     NotAChain,
     parse_chain,
@@ -155,7 +156,8 @@ def _grad_pass(spec: InputSpec, chain: Chain, trace: ForwardTrace, saved: dict, 
         n_in = _numel(layer.in_shape)
         # rank-1 term: every row's bias contribution b += A~ . bias_k (and the center term on the input layer)
         if k == 0:
-            vec = cvec if layer.bias is None else (cvec + _bias_map(layer))
+            vec = cvec if layer.bias is None else derived("cvec_bias", (cvec, layer.bias),
+                                                          lambda: cvec + _bias_map(layer))
             vec_ld = n_out
         else:
             vec = _bias_map(layer) if layer.bias is not None else None
@@ -235,7 +237,8 @@ def _bias_map(layer) -> torch.Tensor:
     if layer.kind == "linear":
         return layer.bias.contiguous()
     Co, Ho, Wo = layer.out_shape
-    return layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous()
+    return derived("conv_bias_map", (layer.bias,),
+                   lambda: layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous())
 
 
 def run_alpha_beta_crown_mlp(

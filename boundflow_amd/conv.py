@@ -48,6 +48,11 @@ def ibp_conv2d(in_lo, in_hi, relu_in, layer, split, split_ld, lo, hi, infeasible
               _lib.ptr(infeasible), _lib.stream_handle())
 
 
+def derived(tag, sources, make):
+    from .crown import derived as _derived
+    return _derived(tag, sources, make)
+
+
 def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo, pre_hi, alpha, alpha_ld, add,
                        add_ld, spec, trace, save=None):
     """Returns (A_u, A_l, b_u, b_l, stride, done) where ``done`` is the final
@@ -75,7 +80,8 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
     A_l = materialize(A_l)
     kbias = None
     if layer.bias is not None:
-        kbias = layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(n_out).contiguous()
+        kbias = derived("conv_bias_map", (layer.bias,),
+                        lambda: layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(n_out).contiguous())
     cvec = trace.input_center_proj.get(layer.out_name) if is_first else None
     rA_u = torch.empty_like(A_u) if A_u is not None else None
     rA_l = torch.empty_like(A_l) if A_l is not None else None
@@ -115,7 +121,7 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
     norm_l = torch.empty(M, device=dev) if A_l is not None else None
     h_scale = h_out = None
     if save is not None and save.get("grad_rows") is not None:
-        h_scale = (save["grad_rows"] * (-eps)).contiguous()
+        h_scale = derived(f"h_scale:{eps!r}", (save["grad_rows"],), lambda: (save["grad_rows"] * (-eps)).contiguous())
         h_out = torch.empty(M, n_in, device=dev)
         save["h"] = h_out
         save["cvec"] = cvec

@@ -496,7 +496,8 @@ def crown_backward(
             h_scale = h_out = None
             if save is not None and save.get("grad_rows") is not None:
                 # gradient seed of the concretization: h = -eps * G * sign(A W) (* radius for a box)
-                h_scale = (save["grad_rows"] * (-eps)).contiguous()
+                h_scale = derived(f"h_scale:{eps!r}", (save["grad_rows"],),
+                                  lambda: (save["grad_rows"] * (-eps)).contiguous())
                 h_out = torch.empty(M, P, device=dev, dtype=torch.float32)
                 save["h"] = h_out
                 save["cvec"] = trace.input_center_proj.get(layer.out_name)
@@ -528,7 +529,8 @@ def crown_backward(
             h_scale = h_out = None
             if save is not None and save.get("grad_rows") is not None:
                 # gradient seed of the concretization: h = -eps * G * sign(A W) (* radius for a box)
-                h_scale = (save["grad_rows"] * (-eps)).contiguous()
+                h_scale = derived(f"h_scale:{eps!r}", (save["grad_rows"],),
+                                  lambda: (save["grad_rows"] * (-eps)).contiguous())
                 h_out = torch.empty(M, P, device=dev, dtype=torch.float32)
                 save["h"] = h_out
                 save["cvec"] = cvec
