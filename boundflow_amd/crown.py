@@ -51,7 +51,9 @@ def derived(tag: str, sources: Tuple[torch.Tensor, ...], make: Callable[[], torc
     same tensor object at the same version (no in-place change since): a layer weight's
     transpose or an input box's radius does not change between the queries of a run, so
     repeated queries (and graph replays) skip the copy.  The entry keeps its sources alive,
-    so their storage cannot be reused under the same key; at most 64 entries are kept."""
+    so their storage cannot be reused under the same key; at most 64 entries are kept.
+    A change written through ``tensor.data`` does not bump the tensor's version and is not
+    seen: change parameters in place through the tensor itself (or replace the tensor)."""
     key = (tag,) + tuple(id(t) for t in sources)
     hit = _DERIVED.get(key)
     versions = tuple(t._version for t in sources)

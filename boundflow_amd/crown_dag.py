@@ -74,11 +74,12 @@ class DagTrace:
 
 @dataclass
 class _Rows:
-    """Backward state of one value: coefficient rows of both bounds and their bias rows."""
-    A_u: torch.Tensor   # [M, n]
-    A_l: torch.Tensor   # [M, n] (may be the same tensor as A_u)
-    b_u: torch.Tensor   # [M]
-    b_l: torch.Tensor   # [M]
+    """Backward state of one value: coefficient rows of both bounds and their bias rows
+    (None for a bound that is not computed)."""
+    A_u: Optional[torch.Tensor]   # [M, n]
+    A_l: Optional[torch.Tensor]   # [M, n] (may be the same tensor as A_u)
+    b_u: Optional[torch.Tensor]   # [M]
+    b_l: Optional[torch.Tensor]   # [M]
 
 
 def _conv_geometry(op, W, in_shape):
