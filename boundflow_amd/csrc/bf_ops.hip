@@ -637,12 +637,20 @@ struct CopySegs {
   int count;
 };
 
+// QUAD: every segment's row length is a multiple of 4 and its rows 16-byte aligned, and a
+// thread moves one float4; the row index is a 32-bit division when the segment fits.
+template <bool QUAD>
 __global__ void masked_copy_rows_multi_kernel(CopySegs c, int64_t D, const int* __restrict__ mask) {
   const int s = seg_of_block(c.bstart, c.count);
   const int64_t i = ((int64_t)blockIdx.x - c.bstart[s]) * 256 + threadIdx.x;
-  const int64_t N = c.ncol[s];
-  if (i >= D * N) return;
-  if (mask[i / N]) c.dst[s][i] = c.src[s][i];
+  const int64_t N = QUAD ? c.ncol[s] / 4 : c.ncol[s];
+  const int64_t total = D * N;
+  if (i >= total) return;
+  if (!mask[div_rows(i, N, total < (1LL << 31))]) return;
+  if constexpr (QUAD)
+    reinterpret_cast<float4*>(c.dst[s])[i] = reinterpret_cast<const float4*>(c.src[s])[i];
+  else
+    c.dst[s][i] = c.src[s][i];
 }
 
 // out[s][d, j] = -beta[s][d, j] * split[s][d, j] * 1(split != 0) for several ReLUs
@@ -662,7 +670,7 @@ __global__ void beta_coeff_multi_kernel(BetaSegs b, int64_t D) {
   const int64_t i = ((int64_t)blockIdx.x - b.bstart[s]) * 256 + threadIdx.x;
   const int64_t N = b.ncol[s];
   if (i >= D * N) return;
-  const int64_t d = i / N, n = i - d * N;
+  const int64_t d = div_rows(i, N, D * N < (1LL << 31)), n = i - d * N;
   const int8_t sp = b.split[s][d * b.split_ld[s] + n];
   const float sf = (float)sp;
   b.out[s][i] = (-b.beta[s][d * b.beta_ld[s] + n] * sf) * (sp != 0 ? 1.f : 0.f);
@@ -1450,18 +1458,26 @@ int bf_masked_copy_rows_multi(int count, float* const* dst, const float* const* 
     CopySegs c;
     memset(&c, 0, sizeof(c));
     c.count = count - base < BF_SEG_MAX ? count - base : BF_SEG_MAX;
-    int64_t blocks = 0;
+    bool quad = true;
     for (int t = 0; t < c.count; ++t) {
       const int k = base + t;
       BF_REQUIRE(ncol[k] > 0 && dst[k] && src[k], "bf_masked_copy_rows_multi: tensor %d", k);
       c.dst[t] = dst[k]; c.src[t] = src[k]; c.ncol[t] = ncol[k];
+      quad = quad && ncol[k] % 4 == 0 && ((uintptr_t)dst[k] & 15) == 0 && ((uintptr_t)src[k] & 15) == 0;
+    }
+    int64_t blocks = 0;
+    for (int t = 0; t < c.count; ++t) {
       c.bstart[t] = blocks;
-      blocks += ceil_div(D * ncol[k], 256);
+      blocks += ceil_div(D * (quad ? ncol[base + t] / 4 : ncol[base + t]), 256);
     }
     c.bstart[c.count] = blocks;
     if (blocks == 0) continue;
     BF_REQUIRE(blocks < (1LL << 31), "bf_masked_copy_rows_multi: too many elements");
-    hipLaunchKernelGGL(masked_copy_rows_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, c, D, mask);
+    if (quad)
+      hipLaunchKernelGGL(masked_copy_rows_multi_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, c, D, mask);
+    else
+      hipLaunchKernelGGL(masked_copy_rows_multi_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, c, D,
+                         mask);
     BF_LAUNCH_CHECK("masked_copy_rows_multi_kernel");
   }
   return BF_OK;
