@@ -36,7 +36,7 @@ __global__ void relax_table_kernel(const float* __restrict__ lo, const float* __
                                    float4* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= D * K) return;
-  const int64_t d = i / K, k = i - (i / K) * K;
+  const int64_t d = div_rows(i, K, D * K < (1LL << 31)), k = i - d * K;
   const bool has_alpha = alpha != nullptr;
   const float a = has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f;
   const Relax r = relu_relax(lo[i], hi[i], has_alpha, a);
@@ -130,10 +130,10 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int ks, int
                                      const float* __restrict__ v_col, int64_t v_ld, int64_t S) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M * N) return;
-  const int64_t m = i / N, n = i - m * N;
+  const int64_t m = div_rows(i, N, M * N < (1LL << 31)), n = i - m * N;
   float v = part[i];
   for (int s = 1; s < ks; ++s) v += part[(int64_t)s * M * N + i];
-  if (r_row) v = v + r_row[m] * v_col[(m / S) * v_ld + n];
+  if (r_row) v = v + r_row[m] * v_col[div_rows(m, S, M < (1LL << 31)) * v_ld + n];
   C[m * ldc + n] = v;
 }
 

@@ -62,8 +62,8 @@ __global__ void concretize_dense_grad_kernel(const float* __restrict__ A, int64_
                                              const float* __restrict__ G, float* __restrict__ g) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M * I) return;
-  const int64_t m = i / I, j = i - (i / I) * I;
-  const int64_t e = (m / S) * I + j;
+  const int64_t m = div_rows(i, I, M * I < (1LL << 31)), j = i - m * I;
+  const int64_t e = div_rows(m, S, M < (1LL << 31)) * I + j;
   const float a = A[i];
   const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
   const float w = rad ? rad[e] : eps;

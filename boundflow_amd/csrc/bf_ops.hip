@@ -95,7 +95,7 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
                                     int* __restrict__ infeasible) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= B * N) return;
-  int64_t b = i / N, n = i % N;
+  const int64_t b = div_rows(i, N, B * N < (1LL << 31)), n = i - b * N;
   float cv, rv = 0.f;
   if (part) {
     const int64_t BN = B * N;
