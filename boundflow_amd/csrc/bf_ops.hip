@@ -665,15 +665,28 @@ struct BetaSegs {
   int count;
 };
 
+__device__ __forceinline__ float beta_term(float beta, int8_t sp) {
+  return (-beta * (float)sp) * (sp != 0 ? 1.f : 0.f);
+}
+
+// QUAD: every segment's row length and strides are multiples of 4 with aligned rows, and a
+// thread writes four consecutive entries of one row (a float4 of beta, four split bytes).
+template <bool QUAD>
 __global__ void beta_coeff_multi_kernel(BetaSegs b, int64_t D) {
   const int s = seg_of_block(b.bstart, b.count);
   const int64_t i = ((int64_t)blockIdx.x - b.bstart[s]) * 256 + threadIdx.x;
-  const int64_t N = b.ncol[s];
+  const int64_t N = QUAD ? b.ncol[s] / 4 : b.ncol[s];
   if (i >= D * N) return;
-  const int64_t d = div_rows(i, N, D * N < (1LL << 31)), n = i - d * N;
-  const int8_t sp = b.split[s][d * b.split_ld[s] + n];
-  const float sf = (float)sp;
-  b.out[s][i] = (-b.beta[s][d * b.beta_ld[s] + n] * sf) * (sp != 0 ? 1.f : 0.f);
+  const int64_t d = div_rows(i, N, D * N < (1LL << 31)), q = i - d * N;
+  if constexpr (QUAD) {
+    const int64_t n = 4 * q;
+    const float4 bv = *reinterpret_cast<const float4*>(b.beta[s] + d * b.beta_ld[s] + n);
+    const char4 sv = *reinterpret_cast<const char4*>(b.split[s] + d * b.split_ld[s] + n);
+    *reinterpret_cast<float4*>(b.out[s] + 4 * i) =
+        make_float4(beta_term(bv.x, sv.x), beta_term(bv.y, sv.y), beta_term(bv.z, sv.z), beta_term(bv.w, sv.w));
+  } else {
+    b.out[s][i] = beta_term(b.beta[s][d * b.beta_ld[s] + q], b.split[s][d * b.split_ld[s] + q]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1493,19 +1506,27 @@ int bf_beta_coeff_multi(int count, const float* const* beta, const int64_t* beta
     BetaSegs b;
     memset(&b, 0, sizeof(b));
     b.count = count - base < BF_SEG_MAX ? count - base : BF_SEG_MAX;
-    int64_t blocks = 0;
+    bool quad = true;
     for (int t = 0; t < b.count; ++t) {
       const int k = base + t;
       BF_REQUIRE(ncol[k] > 0 && beta[k] && split[k] && out[k], "bf_beta_coeff_multi: tensor %d", k);
       b.beta[t] = beta[k]; b.beta_ld[t] = beta_ld[k]; b.split[t] = split[k]; b.split_ld[t] = split_ld[k];
       b.ncol[t] = ncol[k]; b.out[t] = out[k];
+      quad = quad && ncol[k] % 4 == 0 && beta_ld[k] % 4 == 0 && split_ld[k] % 4 == 0 &&
+             ((uintptr_t)beta[k] & 15) == 0 && ((uintptr_t)out[k] & 15) == 0 && ((uintptr_t)split[k] & 3) == 0;
+    }
+    int64_t blocks = 0;
+    for (int t = 0; t < b.count; ++t) {
       b.bstart[t] = blocks;
-      blocks += ceil_div(D * ncol[k], 256);
+      blocks += ceil_div(D * (quad ? ncol[base + t] / 4 : ncol[base + t]), 256);
     }
     b.bstart[b.count] = blocks;
     if (blocks == 0) continue;
     BF_REQUIRE(blocks < (1LL << 31), "bf_beta_coeff_multi: too many elements");
-    hipLaunchKernelGGL(beta_coeff_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, b, D);
+    if (quad)
+      hipLaunchKernelGGL(beta_coeff_multi_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, b, D);
+    else
+      hipLaunchKernelGGL(beta_coeff_multi_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, b, D);
     BF_LAUNCH_CHECK("beta_coeff_multi_kernel");
   }
   return BF_OK;
