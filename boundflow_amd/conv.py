@@ -53,6 +53,11 @@ def derived(tag, sources, make):
     return _derived(tag, sources, make)
 
 
+def call_memo(save, key, make):
+    from .crown import call_memo as _call_memo
+    return _call_memo(save, key, make)
+
+
 def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo, pre_hi, alpha, alpha_ld, add,
                        add_ld, spec, trace, save=None):
     """Returns (A_u, A_l, b_u, b_l, stride, done) where ``done`` is the final
@@ -80,7 +85,7 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
     A_l = materialize(A_l)
     kbias = None
     if layer.bias is not None:
-        kbias = derived("conv_bias_map", (layer.bias,),
+        kbias = derived(f"conv_bias_map:{Ho}x{Wo}", (layer.bias,),
                         lambda: layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(n_out).contiguous())
     cvec = trace.input_center_proj.get(layer.out_name) if is_first else None
     rA_u = torch.empty_like(A_u) if A_u is not None else None
@@ -121,7 +126,7 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
     norm_l = torch.empty(M, device=dev) if A_l is not None else None
     h_scale = h_out = None
     if save is not None and save.get("grad_rows") is not None:
-        h_scale = derived(f"h_scale:{eps!r}", (save["grad_rows"],), lambda: (save["grad_rows"] * (-eps)).contiguous())
+        h_scale = call_memo(save, f"h_scale:{eps!r}", lambda: (save["grad_rows"] * (-eps)).contiguous())
         h_out = torch.empty(M, n_in, device=dev)
         save["h"] = h_out
         save["cvec"] = cvec

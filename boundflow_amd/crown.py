@@ -26,6 +26,8 @@ behaviour.
 
 from __future__ import annotations
 
+import contextlib
+import threading
 from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Mapping, Optional, Tuple
@@ -44,26 +46,72 @@ from .spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation,
 
 _DERIVED: "OrderedDict[tuple, tuple]" = OrderedDict()
 _DERIVED_MAX = 64
+_SCOPE = threading.local()
 
 
 def derived(tag: str, sources: Tuple[torch.Tensor, ...], make: Callable[[], torch.Tensor]) -> torch.Tensor:
-    """``make()`` computed once per (tag, source tensors) and reused while every source is the
-    same tensor object at the same version (no in-place change since): a layer weight's
-    transpose or an input box's radius does not change between the queries of a run, so
-    repeated queries (and graph replays) skip the copy.  The entry keeps its sources alive,
-    so their storage cannot be reused under the same key; at most 64 entries are kept.
-    A change written through ``tensor.data`` does not bump the tensor's version and is not
-    seen: change parameters in place through the tensor itself (or replace the tensor)."""
+    """``make()`` of a PARAMETER-derived operand (a layer weight's transpose, a conv bias
+    map), computed once per (tag, source tensors) and reused while every source is the
+    same tensor object at the same version (no in-place change since), so repeated
+    queries skip the copy.  Operands that depend on a query's inputs are never kept here.
+
+    * The entry keeps its sources alive, so their storage cannot be reused under the same
+      key; at most 64 entries are kept.  A change written through ``tensor.data`` does not
+      bump the version and is not seen: change parameters through the tensor itself.
+    * A hit on another stream than the one that made the entry waits for the producer
+      (an event recorded after ``make()``), so the consumer never reads it half-written.
+    * Inside ``derived_scope()`` (graph capture) entries live in the scope's own dict:
+      the captured graph then contains the kernels that make them and recomputes them on
+      every replay, so a replay sees in-place parameter updates and never reads an entry
+      the process-wide cache has since evicted."""
+    scope = getattr(_SCOPE, "memo", None)
+    table = _DERIVED if scope is None else scope
     key = (tag,) + tuple(id(t) for t in sources)
-    hit = _DERIVED.get(key)
+    hit = table.get(key)
     versions = tuple(t._version for t in sources)
     if hit is not None and all(a is b for a, b in zip(hit[0], sources)) and hit[1] == versions:
-        _DERIVED.move_to_end(key)
-        return hit[2]
+        if scope is None:
+            _DERIVED.move_to_end(key)
+            out, stream, event = hit[2]
+            if event is not None and torch.cuda.current_stream(out.device) != stream:
+                torch.cuda.current_stream(out.device).wait_event(event)
+            return out
+        return hit[2][0]
     out = make()
-    _DERIVED[key] = (tuple(sources), versions, out)
-    if len(_DERIVED) > _DERIVED_MAX:
+    stream = event = None
+    if scope is None and out.is_cuda:
+        stream = torch.cuda.current_stream(out.device)
+        event = torch.cuda.Event()
+        event.record(stream)
+    table[key] = (tuple(sources), versions, (out, stream, event))
+    if scope is None and len(_DERIVED) > _DERIVED_MAX:
         _DERIVED.popitem(last=False)
+    return out
+
+
+@contextlib.contextmanager
+def derived_scope():
+    """Route ``derived`` to a fresh dict for the duration (used around graph capture);
+    yields that dict, which the caller keeps as long as the captured work may run."""
+    prev = getattr(_SCOPE, "memo", None)
+    memo: dict = {}
+    _SCOPE.memo = memo
+    try:
+        yield memo
+    finally:
+        _SCOPE.memo = prev
+
+
+def call_memo(save: Optional[dict], key: str, make: Callable[[], torch.Tensor]) -> torch.Tensor:
+    """``make()`` once per optimisation call: per-query operands (scaled gradient rows,
+    the first layer's center-plus-bias vector) are kept in the call's own ``save["memo"]``
+    dict, which dies with the call, never in the process-wide cache."""
+    memo = None if save is None else save.get("memo")
+    if memo is None:
+        return make()
+    out = memo.get(key)
+    if out is None:
+        out = memo[key] = make()
     return out
 
 
@@ -498,8 +546,7 @@ def crown_backward(
             h_scale = h_out = None
             if save is not None and save.get("grad_rows") is not None:
                 # gradient seed of the concretization: h = -eps * G * sign(A W) (* radius for a box)
-                h_scale = derived(f"h_scale:{eps!r}", (save["grad_rows"],),
-                                  lambda: (save["grad_rows"] * (-eps)).contiguous())
+                h_scale = call_memo(save, f"h_scale:{eps!r}", lambda: (save["grad_rows"] * (-eps)).contiguous())
                 h_out = torch.empty(M, P, device=dev, dtype=torch.float32)
                 save["h"] = h_out
                 save["cvec"] = trace.input_center_proj.get(layer.out_name)
@@ -531,8 +578,7 @@ def crown_backward(
             h_scale = h_out = None
             if save is not None and save.get("grad_rows") is not None:
                 # gradient seed of the concretization: h = -eps * G * sign(A W) (* radius for a box)
-                h_scale = derived(f"h_scale:{eps!r}", (save["grad_rows"],),
-                                  lambda: (save["grad_rows"] * (-eps)).contiguous())
+                h_scale = call_memo(save, f"h_scale:{eps!r}", lambda: (save["grad_rows"] * (-eps)).contiguous())
                 h_out = torch.empty(M, P, device=dev, dtype=torch.float32)
                 save["h"] = h_out
                 save["cvec"] = cvec
@@ -619,7 +665,8 @@ def _input_radius(pert, B: int, P: int):
     if isinstance(pert, BoxPerturbation):
         lo = pert.lower.reshape(B, P)
         hi = pert.upper.reshape(B, P)
-        return derived("box_rad", (pert.lower, pert.upper), lambda: ((hi - lo) / 2.0).contiguous()), 1.0
+        # depends on the query's input set: computed per query, never kept across queries
+        return ((hi - lo) / 2.0).contiguous(), 1.0
     return None, float(pert.eps)
 
 

@@ -26,6 +26,7 @@ allocator, as the reference executors do (fused_crown.py:704-718).
 
 from __future__ import annotations
 
+import contextlib
 import hashlib
 import json
 from dataclasses import dataclass
@@ -35,6 +36,7 @@ from typing import Any, Literal, Mapping, Optional, Protocol, Sequence, Tuple
 import torch
 
 from . import _lib
+from .crown import derived, transposed
 
 
 class BoundaryRepresentation(Enum):
@@ -256,7 +258,11 @@ class HipFusedCrownExecutor:
 
     def run(self, request: FusedReluAffineRequest, *,
             stream: Optional[torch.cuda.Stream] = None) -> FusedReluAffineResult:
-        st = _lib.stream_handle(stream)
+        # every launch, and the torch ops that prepare operands, go to the caller's stream
+        with (torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()):
+            return self._run(request, _lib.stream_handle(stream))
+
+    def _run(self, request: FusedReluAffineRequest, st) -> FusedReluAffineResult:
         dev = request.A_u.device
         D, S = int(request.A_u.shape[0]), int(request.A_u.shape[1])
         M = D * S
@@ -269,7 +275,7 @@ class HipFusedCrownExecutor:
         dl = torch.empty(D, S, device=dev, dtype=torch.float32)
         if request.kind == "linear":
             P = int(request.weight.shape[1])
-            Wt = request.weight.t().contiguous()   # [P, N]: the kernel's faster operand layout
+            Wt = transposed(request.weight)   # [P, N]: the kernel's faster operand layout, kept across calls
             pu = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             pl = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
@@ -282,7 +288,8 @@ class HipFusedCrownExecutor:
         KH, KW = int(W.shape[2]), int(W.shape[3])
         sh, sw = _pair(request.attrs, "stride", (1, 1))
         ph, pw = _pair(request.attrs, "padding", (0, 0))
-        kbias = None if bias is None else bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous()
+        kbias = None if bias is None else derived(
+            f"conv_bias_map:{Ho}x{Wo}", (bias,), lambda: bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous())
         ru = torch.empty(M, N, device=dev)
         rl = torch.empty(M, N, device=dev)
         _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,

@@ -8,7 +8,10 @@ re-runs every kernel on the same device buffers with one launch.
 Requirements of the captured function: device inputs that stay at the same
 addresses, no host synchronization (the split-infeasibility check of the
 forward trace is one: queries with splits or constraints are not capturable),
-and no memset nodes (the library clears buffers with fill kernels).  The
+and no memset nodes (the library clears buffers with fill kernels).  Inputs may
+be changed in place between replays (``copy_`` into the input box or center):
+everything derived from them, and from the parameters, is recomputed inside
+the graph.  The
 outputs of a replay live in the graph's private memory pool and are
 overwritten by the next replay.
 """
@@ -33,7 +36,11 @@ class CapturedQuery:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        # parameter-derived operands (weight transposes, bias maps) are made inside the
+        # graph, once per replay, instead of read from the process-wide cache: a replay
+        # then sees in-place parameter updates and never reads an evicted entry
+        from .crown import derived_scope
+        with derived_scope() as self._derived, torch.cuda.graph(self.graph):
             self.outputs = fn()
         torch.cuda.synchronize()
 

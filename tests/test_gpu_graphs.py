@@ -88,3 +88,34 @@ def test_captured_domain_batch_replays_match_eager():
         torch.cuda.synchronize()
         for k in keys:
             assert torch.equal(out[k], ref[k]), f"replay {rep} {k}"
+
+
+def test_replay_sees_inputs_and_parameters_changed_in_place():
+    """A captured C1 query (box input) after ``copy_`` of a different box into the
+    perturbation and an in-place change of a layer weight: the replay recomputes
+    the box radius and the weight transposes inside the graph, so it equals an
+    eager query on the new values (and the process-wide operand cache, filled by
+    eager queries before the change, is not read by the graph)."""
+    dev = device()
+    announce("graph replay after in-place input and parameter updates (C1, batch 16)")
+    wd = wl.to_device(wl.subset(wl.make_c1(), 16), dev)
+    hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)   # fills the parameter cache
+    cap = graphs.CapturedQuery(lambda: hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C))
+    pert = wd.spec.perturbation
+    lo0, hi0 = pert.lower.clone(), pert.upper.clone()
+    W1 = wd.module.params["W1"]
+    W1_0 = W1.clone()
+    for rep, (shrink, wscale) in enumerate([(0.5, 1.0), (0.25, 0.9), (1.0, 1.0)]):
+        mid = (lo0 + hi0) / 2
+        rad = (hi0 - lo0) / 2 * shrink
+        pert.lower.copy_(mid - rad)
+        pert.upper.copy_(mid + rad)
+        W1.copy_(W1_0 * wscale)
+        torch.cuda.synchronize()
+        out = cap()
+        torch.cuda.synchronize()
+        got_lo, got_hi = out.lower.clone(), out.upper.clone()
+        eager = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+        torch.cuda.synchronize()
+        assert torch.equal(got_lo, eager.lower), f"replay {rep} lower"
+        assert torch.equal(got_hi, eager.upper), f"replay {rep} upper"

@@ -41,3 +41,45 @@ def test_cache_is_bounded():
     # the newest entries are still there and correct
     last = keep[-1]
     assert torch.equal(crown.derived("bound_test", (last,), lambda: torch.zeros(1)), last * 2.0)
+
+
+def test_scope_keeps_entries_out_of_the_global_cache():
+    """Inside derived_scope (graph capture) entries go to the scope's dict: the
+    process-wide cache is neither read nor filled, so the captured work makes
+    its operands itself."""
+    W = torch.arange(4.0).reshape(2, 2)
+    outside = crown.transposed(W)
+    n_before = len(crown._DERIVED)
+    with crown.derived_scope() as memo:
+        inside = crown.transposed(W)
+        again = crown.transposed(W)
+    assert inside is again and inside is not outside
+    assert len(memo) == 1 and len(crown._DERIVED) == n_before
+    assert torch.equal(inside, W.t())
+    # after the scope the global entry is used again
+    assert crown.transposed(W) is outside
+
+
+def test_call_memo_is_per_call():
+    calls = []
+    save = {"memo": {}}
+    a = crown.call_memo(save, "k", lambda: calls.append(1) or torch.ones(2))
+    b = crown.call_memo(save, "k", lambda: calls.append(1) or torch.ones(2))
+    assert a is b and len(calls) == 1
+    # without a memo (one-off evaluation) the operand is made every time
+    crown.call_memo(None, "k", lambda: calls.append(1) or torch.ones(2))
+    crown.call_memo({}, "k", lambda: calls.append(1) or torch.ones(2))
+    assert len(calls) == 3
+
+
+def test_box_radius_is_not_cached():
+    """The input box radius depends on the query: an in-place change of the box
+    is seen by the next query (and by a graph replay, which recomputes it)."""
+    from boundflow_amd.spec import BoxPerturbation
+    lo = torch.zeros(2, 3)
+    hi = torch.ones(2, 3)
+    pert = BoxPerturbation(lower=lo, upper=hi)
+    r1, e1 = crown._input_radius(pert, 2, 3)
+    pert.upper.copy_(torch.full((2, 3), 3.0))   # the perturbation holds its own copy of the box
+    r2, _ = crown._input_radius(pert, 2, 3)
+    assert e1 == 1.0 and torch.equal(r1, torch.full((2, 3), 0.5)) and torch.equal(r2, torch.full((2, 3), 1.5))
