@@ -36,6 +36,7 @@ from .crown import (
     ForwardTrace,
     _broadcast_split,
     _numel,
+    call_memo,
     crown_backward,
     derived,
     forward_ibp_trace,
@@ -156,8 +157,7 @@ def _grad_pass(spec: InputSpec, chain: Chain, trace: ForwardTrace, saved: dict, 
         n_in = _numel(layer.in_shape)
         # rank-1 term: every row's bias contribution b += A~ . bias_k (and the center term on the input layer)
         if k == 0:
-            vec = cvec if layer.bias is None else derived("cvec_bias", (cvec, layer.bias),
-                                                          lambda: cvec + _bias_map(layer))
+            vec = cvec if layer.bias is None else call_memo(saved, "cvec_bias", lambda: cvec + _bias_map(layer))
             vec_ld = n_out
         else:
             vec = _bias_map(layer) if layer.bias is not None else None
@@ -226,6 +226,14 @@ def _evaluator(module, spec: InputSpec, trace, chain: Optional[Chain], linear_sp
     return bound, grad, _numel(trace.shapes[module.get_entry_task().output_values[0]])
 
 
+def _relu_shapes(module, spec, chain: Optional[Chain]) -> Dict[str, Tuple[int, ...]]:
+    """Per-sample shape of every ReLU input (op order), for a chain or a DAG task."""
+    if chain is not None:
+        return dict(chain.relu_shapes)
+    from .crown_dag import relu_input_shapes
+    return relu_input_shapes(module, spec)
+
+
 def _chain_or_none(module, spec) -> Optional[Chain]:
     try:
         return parse_chain(module, spec)
@@ -237,7 +245,7 @@ def _bias_map(layer) -> torch.Tensor:
     if layer.kind == "linear":
         return layer.bias.contiguous()
     Co, Ho, Wo = layer.out_shape
-    return derived("conv_bias_map", (layer.bias,),
+    return derived(f"conv_bias_map:{Ho}x{Wo}", (layer.bias,),
                    lambda: layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous())
 
 
@@ -259,16 +267,35 @@ def run_alpha_beta_crown_mlp(
     trace: Optional[ForwardTrace] = None,
     raise_on_infeasible: bool = True,
     use_beta: bool = True,
+    first_layer_certificate: bool = True,
 ):
     """HIP counterpart of run_alpha_beta_crown_mlp (alpha_beta_crown.py:643-941).
 
     ``use_beta=False`` drops the split multipliers (alpha-CROWN with splits
     applied only to the pre-activation boxes and relaxations,
-    alpha_crown.py:137-261).  Returns (best_bounds, best_alpha, best_beta, stats)."""
+    alpha_crown.py:137-261).  Returns (best_bounds, best_alpha, best_beta, stats).
+
+    A single domain with a nonzero split is first checked by the first-layer
+    split certificate (alpha_beta_crown.py:694-714); when it proves the splits
+    infeasible the bounds are zeros of shape [1, 1], the parameter dicts are
+    empty and ``stats.feasibility`` is "infeasible", as in the reference.  That
+    check reads its verdict back to the host; callers that decide it
+    themselves (the BaB rounds) pass ``first_layer_certificate=False``."""
     if objective != "lower" or spec_reduce != "mean":
         raise NotImplementedError("HIP alpha-beta CROWN implements objective='lower', spec_reduce='mean'")
     spec = normalize_input_spec(input_spec)
     chain = _chain_or_none(module, spec)
+    if (first_layer_certificate and relu_split_state and int(spec.center.shape[0]) == 1
+            and any(bool((v != 0).any().item()) for v in relu_split_state.values() if v is not None)):
+        from .split_certificate import check_flags, split_certificate
+        shapes0 = _relu_shapes(module, spec, chain)
+        flag = split_certificate(module, spec, relu_split_state, shapes0).cpu().tolist()
+        check_flags(flag)
+        if flag[0] == 1:
+            zeros = torch.zeros((1, 1), device=spec.center.device, dtype=torch.float32)
+            return (IntervalState(lower=zeros, upper=zeros.clone()), {}, {},
+                    AlphaBetaStats(feasibility="infeasible", reason="infeasible: first-layer split certificate",
+                                   steps=int(steps), lr=float(lr)))
     if trace is None:
         trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
                                   raise_on_infeasible=raise_on_infeasible)
@@ -330,10 +357,11 @@ def run_alpha_beta_crown_mlp(
     copy_dst = [best_alpha[n] for n in names] + [best_beta[n] for n in beta_names]
     copy_args = (_lib.ptr_array(copy_dst), _lib.ptr_array([alpha[n] for n in names] + [beta[n] for n in beta_names]),
                  _lib.i64_array([numel[n] for n in names] + [numel[n] for n in beta_names]), B, _lib.ptr(improved))
+    memo: dict = {}   # per-call operands (scaled gradient rows, center-plus-bias), freed with the call
     for step in range(int(steps) + 1):
         if beta_names:
             _lib.call("bf_beta_coeff_multi", len(beta_names), *beta_args, stream)
-        saved = {"grad_rows": G} if step < int(steps) else None
+        saved = {"grad_rows": G, "memo": memo} if step < int(steps) else None
         # lower bound only: the objective and the best-of rule read nothing else
         bounds = bound({n: alpha[n] for n in names}, {n: add[n] for n in beta_names}, False, True, saved)
         if per_batch_params:
@@ -379,7 +407,8 @@ def run_alpha_crown_mlp(module, input_spec, *, linear_spec_C=None, steps: int = 
     ReLU input names to alpha tensors of the ReLU's logical shape."""
     bounds, alpha, _beta, stats = run_alpha_beta_crown_mlp(
         module, input_spec, linear_spec_C=linear_spec_C, relu_split_state=relu_split_state, steps=steps, lr=lr,
-        alpha_init=alpha_init, warm_start_alpha=warm_start, per_batch_params=False, use_beta=False, trace=trace)
+        alpha_init=alpha_init, warm_start_alpha=warm_start, per_batch_params=False, use_beta=False, trace=trace,
+        first_layer_certificate=False)   # alpha_crown.py has no certificate
     return bounds, alpha, stats
 
 

@@ -24,7 +24,7 @@ import torch
 from . import _lib
 from .alpha_beta import branch_tensors, run_alpha_beta_crown_mlp, run_alpha_crown_mlp
 from .crown import NotAChain, forward_ibp_trace, parse_chain
-from .spec import BoxPerturbation, InputSpec, normalize_input_spec
+from .spec import BoxPerturbation, InputSpec, LpBallPerturbation, normalize_input_spec
 
 
 def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
@@ -45,7 +45,7 @@ def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
     bounds, alpha, beta, _stats = run_alpha_beta_crown_mlp(
         module, spec, linear_spec_C=linear_spec_C, relu_split_state=relu_split_state, steps=steps, lr=lr,
         alpha_init=alpha_init, beta_init=beta_init, warm_start_alpha=warm_start_alpha,
-        warm_start_beta=warm_start_beta, per_batch_params=True, trace=trace)
+        warm_start_beta=warm_start_beta, per_batch_params=True, trace=trace, first_layer_certificate=False)
     S = int(bounds.lower.shape[1])
     status = torch.empty(D, dtype=torch.int32, device=spec.center.device)
     _lib.call("bf_domain_status", _lib.ptr(bounds.lower), D, S, _lib.ptr(trace.infeasible), float(threshold),
@@ -176,10 +176,20 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
     is "unsafe" when an open node has no ambiguous neuron left, "unknown" when
     its node budget runs out, "proven" when its tree empties.
 
-    Results do not depend on node evaluations being cached, so the reference's
-    node-evaluation cache has no counterpart.  Supported: objective "lower",
-    spec_reduce "mean", no 1-D input restriction, no first-layer infeasibility
-    pre-pruning.
+    Nodes are closed as infeasible where the reference closes them: an IBP
+    trace that empties a pre-activation box, and the first-layer split
+    certificate (``split_certificate``) wherever the reference evaluates a node
+    alone -- a round of one node, and every node of a batch that holds an
+    IBP-infeasible node (the reference's per-node fallback, bab.py:1399-1456);
+    with ``enable_batch_infeasible_prune`` the certificate also removes nodes
+    from a batch before its evaluation (bab.py:373-425).  With
+    ``use_1d_linf_input_restriction_patch`` a one-input Linf example's node is
+    evaluated on its interval narrowed by the first-layer splits, and closed
+    when they leave nothing (bab.py:524-628).
+
+    A search tree never evaluates the same split set twice, so the reference's
+    node-evaluation cache cannot hit and has no counterpart.  Supported:
+    objective "lower", spec_reduce "mean".
     """
     cfg = config or BabConfig()
     if int(cfg.max_nodes) < 1:
@@ -188,8 +198,6 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
         raise ValueError(f"node_batch_size must be >=1, got {cfg.node_batch_size}")
     if cfg.objective != "lower" or cfg.spec_reduce != "mean":
         raise NotImplementedError("HIP BaB implements objective='lower', spec_reduce='mean'")
-    if cfg.use_1d_linf_input_restriction_patch or cfg.enable_batch_infeasible_prune:
-        raise NotImplementedError("HIP BaB does not implement the 1-D input restriction or batch pre-pruning")
     if cfg.oracle not in ("alpha", "alpha_beta"):
         raise ValueError(f"unknown BaB oracle: {cfg.oracle}")
     spec = normalize_input_spec(input_spec)
@@ -226,7 +234,8 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
     batch_rounds = 0
     popped_total = 0
     max_q = len(heap)
-    do_batch = cfg.oracle == "alpha_beta" and int(cfg.node_batch_size) > 1
+    do_batch = (cfg.oracle == "alpha_beta" and int(cfg.node_batch_size) > 1
+                and not cfg.use_1d_linf_input_restriction_patch)
 
     def finish_if_empty(e: int) -> None:
         if status[e] is None and live[e] == 0:
@@ -258,7 +267,7 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
         child_meta: List[Tuple[int, float]] = []      # (example, priority) per expansion
         for row, item in enumerate(items):
             e = item[2]
-            if out["infeasible"][row]:
+            if out["closed"][row]:
                 live[e] = max(0, live[e] - 1)
                 finish_if_empty(e)
                 continue
@@ -324,9 +333,17 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
 
 def _evaluate_nodes(module, spec, chain, shapes, linear_spec_C, items, front: _Frontier, names, cfg: BabConfig):
     """One round: gather the popped nodes' inputs, splits and warm starts from
-    the frontier, run the oracle on all of them, and return the node
-    lower/upper bounds, infeasibility and branch decisions on the host (one
-    transfer) plus the gathered splits and the best alpha/beta on the device."""
+    the frontier, run the oracle on all of them, and return per node whether it
+    is closed as infeasible, its lower/upper bound and branch decision on the
+    host (one transfer; a second only in a round with an IBP-infeasible node of
+    a batch), plus the gathered splits and the best alpha/beta on the device.
+
+    Closing follows the reference: a node evaluated alone (a round of one node,
+    or every node of a batch that holds an IBP-infeasible one) is closed by the
+    first-layer certificate or its IBP trace; a node of an evaluated batch only
+    by pre-pruning.  Every node is evaluated in the batch regardless: nodes do
+    not interact, so a closed node's evaluation changes nothing for the others."""
+    from .split_certificate import check_flags, split_certificate
     dev = spec.center.device
     ex = torch.tensor([it[2] for it in items], device=dev, dtype=torch.long)
     sl = torch.tensor([it[3] for it in items], device=dev, dtype=torch.long)
@@ -336,18 +353,28 @@ def _evaluate_nodes(module, spec, chain, shapes, linear_spec_C, items, front: _F
         sub = InputSpec.box(value_name=spec.value_name, lower=pert.lower[ex], upper=pert.upper[ex])
     else:
         sub = InputSpec(value_name=spec.value_name, center=spec.center[ex], perturbation=pert)
-    C = None if linear_spec_C is None else linear_spec_C[ex]
     split = {n: front.split[n][sl] for n in names}
     split_by = {n: split[n].reshape((b,) + tuple(shapes[n])) for n in names}
+    if cfg.use_1d_linf_input_restriction_patch and b == 1:
+        sub = _restrict_1d_linf(module, sub, {n: v[0] for n, v in split_by.items()})
+        if sub is None:
+            return {"closed": [True], "node_lower": [0.0], "node_upper": [0.0], "branch_layer": [-1],
+                    "branch_neuron": [0], "split": split, "alpha": {}, "beta": {}}
+    C = None if linear_spec_C is None else linear_spec_C[ex]
     warm_a = {n: front.alpha[n][sl].reshape((b,) + tuple(shapes[n])) for n in names}
     warm_b = {n: front.beta[n][sl].reshape((b,) + tuple(shapes[n])) for n in names}
+    ab = cfg.oracle == "alpha_beta"
+    prune = ab and b > 1 and bool(cfg.enable_batch_infeasible_prune)
+    # the certificate where its verdict is known to be needed (a lone node, or pre-pruning)
+    cert = split_certificate(module, sub, split_by, shapes) if ab and (b == 1 or prune) else None
     trace = forward_ibp_trace(module, sub, relu_split_state=split_by, chain=chain, raise_on_infeasible=False)
     layer, neuron, _gap = branch_tensors(trace, b)
-    if cfg.oracle == "alpha_beta":
+    if ab:
         bounds, alpha, beta, _stats = run_alpha_beta_crown_mlp(
             module, sub, linear_spec_C=C, relu_split_state=split_by, steps=int(cfg.alpha_steps),
             lr=float(cfg.alpha_lr), alpha_init=float(cfg.alpha_init), beta_init=float(cfg.beta_init),
-            warm_start_alpha=warm_a, warm_start_beta=warm_b, per_batch_params=True, trace=trace)
+            warm_start_alpha=warm_a, warm_start_beta=warm_b, per_batch_params=True, trace=trace,
+            first_layer_certificate=False)
     else:
         # alpha oracle: one node per round, shared alpha of that node, no split multipliers
         bounds, alpha, _stats = run_alpha_crown_mlp(
@@ -356,10 +383,86 @@ def _evaluate_nodes(module, spec, chain, shapes, linear_spec_C, items, front: _F
             relu_split_state=split_by, trace=trace)
         alpha = {n: v.reshape((1,) + tuple(v.shape)) for n, v in alpha.items()}
         beta = warm_b
-    summary = torch.stack([bounds.lower.min(dim=1).values.double(), bounds.upper.max(dim=1).values.double(),
-                           trace.infeasible.double(), layer.double(), neuron.double()]).cpu()
-    lo, up, inf, lay, neu = summary.tolist()
-    return {"node_lower": lo, "node_upper": up, "infeasible": [v != 0 for v in inf],
+    rows = [bounds.lower.min(dim=1).values.double(), bounds.upper.max(dim=1).values.double(),
+            trace.infeasible.double(), layer.double(), neuron.double()]
+    if cert is not None:
+        rows.append(cert.double())
+    summary = torch.stack(rows).cpu().tolist()
+    lo, up, inf, lay, neu = summary[:5]
+    ibp_inf = [v != 0 for v in inf]
+    cert_h = None
+    if cert is not None:
+        cert_h = [int(v) for v in summary[5]]
+        check_flags(cert_h)
+    if b == 1:
+        closed = [ibp_inf[0] or (cert_h is not None and cert_h[0] == 1)]
+    else:
+        pruned = [prune and cert_h[i] == 1 for i in range(b)]
+        rest = [i for i in range(b) if not pruned[i]]
+        if any(ibp_inf[i] for i in rest):
+            # the reference's batched call raises; it evaluates every remaining node alone,
+            # each behind the certificate
+            if cert_h is None:
+                cert_h = [int(v) for v in split_certificate(module, sub, split_by, shapes).cpu().tolist()]
+                check_flags(cert_h)
+            closed = [pruned[i] or ibp_inf[i] or cert_h[i] == 1 for i in range(b)]
+        else:
+            closed = pruned
+    return {"closed": closed, "node_lower": lo, "node_upper": up,
             "branch_layer": [int(v) for v in lay], "branch_neuron": [int(v) for v in neu],
             "split": split, "alpha": {n: v.reshape(b, -1) for n, v in alpha.items()},
             "beta": {n: v.reshape(b, -1) for n, v in beta.items()}}
+
+
+def _restrict_1d_linf(module, spec: InputSpec, split: Dict[str, torch.Tensor]) -> Optional[InputSpec]:
+    """The reference's 1-D input restriction (bab.py:524-628): a one-input Linf
+    spec of one node narrowed to the interval where every first-layer split
+    s * (w_i x + b_i) >= 0 of a linear layer reading the input holds; None when
+    the interval is empty.  Any other spec is returned unchanged.  Scalar host
+    arithmetic in Python floats, as the reference's."""
+    if spec.center.dim() != 2 or int(spec.center.shape[1]) != 1 or int(spec.center.shape[0]) != 1:
+        return spec
+    p = spec.perturbation
+    if not isinstance(p, LpBallPerturbation) or p.normalized_p() != "inf":
+        return spec
+    task = module.get_entry_task()
+    params = module.params
+    x0 = float(spec.center[0, 0].item())
+    eps = float(p.eps)
+    lo, hi = x0 - eps, x0 + eps
+    for op in task.ops:
+        if op.op_type != "relu" or op.inputs[0] not in split:
+            continue
+        x = op.inputs[0]
+        prod = next((q for q in task.ops if x in q.outputs), None)
+        if prod is None or prod.op_type != "linear" or not prod.inputs or prod.inputs[0] != spec.value_name:
+            continue
+        W = params.get(prod.inputs[1])
+        if W is None or W.dim() != 2 or int(W.shape[1]) != 1:
+            continue
+        if len(prod.inputs) == 3:
+            bb = params.get(prod.inputs[2])
+            if bb is None or bb.dim() != 1 or int(bb.shape[0]) != int(W.shape[0]):
+                continue
+            b_h = bb.detach().cpu().tolist()
+        else:
+            b_h = [0.0] * int(W.shape[0])
+        w_h = W.detach().cpu().reshape(-1).tolist()
+        s_h = split[x].detach().cpu().reshape(-1).tolist()
+        for i, sg in enumerate(s_h):
+            if sg == 0:
+                continue
+            wi, bi = float(w_h[i]), float(b_h[i])
+            if wi == 0.0:
+                if (sg > 0 and bi < 0.0) or (sg < 0 and bi > 0.0):
+                    return None
+                continue
+            t = -bi / wi
+            if (sg > 0) == (wi > 0):
+                lo = max(lo, t)
+            else:
+                hi = min(hi, t)
+        if lo > hi:
+            return None
+    center = torch.tensor([[0.5 * (lo + hi)]], device=spec.center.device, dtype=spec.center.dtype)
+    return InputSpec.linf(value_name=spec.value_name, center=center, eps=float(0.5 * (hi - lo)))

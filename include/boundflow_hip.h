@@ -323,6 +323,20 @@ int bf_alpha_from_crown(const float* lo, const float* hi, int64_t n, float* out,
 int bf_branch_update(const float* lo, const float* hi, int64_t D, int64_t N, int layer, float* best_gap,
                      int* best_layer, int* best_idx, hipStream_t stream);
 
+/* First-layer split infeasibility certificate, one node per workgroup
+ * (_is_infeasible_split_first_layer_convex_combo, runtime/alpha_beta_crown.py:391-532;
+ * halfspaces as _collect_first_layer_split_halfspaces, :259-389).  Node g's halfspaces
+ * are s * (rows[i] . x + bias[i]) >= 0 for its nonzero split[g * split_ld + i] (in i
+ * order); the input set is the Linf ball (center row g, eps) or, with rad, the box
+ * center +- rad.  Searches a convex combination w = softmax(z) by Adam on z (lr,
+ * betas 0.9/0.999, eps 1e-8, `steps` steps from z = 0) and sets out[g] = 1 at the
+ * first step whose maximum over the set is below -tol, else 0; -1 when a node has
+ * more than 1024 splits.  in_dim <= 16384, steps <= 256. */
+int bf_split_certificate(const float* rows, int64_t row_ld, const float* bias, const int8_t* split, int64_t split_ld,
+                         const float* center, int64_t center_ld, const float* rad, int64_t rad_ld, float eps,
+                         int64_t nodes, int64_t n0, int64_t in_dim, int steps, double lr, double tol, int32_t* out,
+                         hipStream_t stream);
+
 /* Node verdict (runtime/bab.py:870-895): 1 certified (min_s lb >= threshold - tol),
  * 2 infeasible split, 0 open. */
 int bf_domain_status(const float* lb, int64_t D, int64_t S, const int* infeasible, float threshold, float tol,

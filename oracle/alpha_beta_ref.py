@@ -3,9 +3,11 @@ BaB node-batch evaluation (test infrastructure only).
 
 * ``branch_choices`` -- boundflow/runtime/alpha_beta_crown.py:145-182
 * ``beta_to_pre_add`` -- boundflow/runtime/alpha_beta_crown.py:615-640
-* ``run_alpha_beta_crown`` -- boundflow/runtime/alpha_beta_crown.py:643-941 (the
-  B==1 first-layer convex-combination pre-check at :694-714 is a host-side
-  filter that the batched node evaluation never reaches and is not restated)
+* ``run_alpha_beta_crown`` -- boundflow/runtime/alpha_beta_crown.py:643-941, with
+  the B==1 first-layer infeasibility pre-check of :694-714
+* ``first_layer_split_halfspaces`` -- boundflow/runtime/alpha_beta_crown.py:259-389
+* ``split_certificate`` -- ``_is_infeasible_split_first_layer_convex_combo``,
+  boundflow/runtime/alpha_beta_crown.py:391-532
 * ``run_alpha_crown`` -- boundflow/runtime/alpha_crown.py:137-261
 * ``adaptive_alpha_init`` -- boundflow/runtime/native_alpha_beta_optimizer_schedule.py:635-653
 * ``evaluate_domain_batch`` -- the node-batch section of boundflow/runtime/bab.py:1250-1460
@@ -21,7 +23,8 @@ import torch
 from boundflow_amd.ir import BFTaskModule
 from boundflow_amd.spec import InputSpec, IntervalState, normalize_input_spec
 
-from .crown_ref import broadcast_split, crown_backward_from_trace, forward_ibp_trace
+from .crown_ref import (DenseOp, broadcast_split, concretize_affine, conv2d_right, crown_backward_from_trace,
+                        forward_ibp_trace)
 
 
 def branch_choices(relu_pre: Dict[str, IntervalState]) -> List[Optional[Tuple[str, int]]]:
@@ -88,6 +91,111 @@ def beta_to_pre_add(beta: Dict[str, torch.Tensor], relu_pre, relu_split_state) -
     return out
 
 
+def has_nonzero_split(relu_split_state) -> bool:
+    """alpha_beta_crown.py:53-60."""
+    return any(v is not None and v.numel() > 0 and bool((v != 0).any()) for v in (relu_split_state or {}).values())
+
+
+def first_layer_split_halfspaces(module: BFTaskModule, spec: InputSpec, relu_split_state):
+    """alpha_beta_crown.py:259-389: for every ReLU (op order) whose input is made by
+    a linear or conv2d op reading the network input, one halfspace
+    (name, neuron, a = s * row, c = s * bias) per nonzero split entry, in neuron
+    order.  A conv row is the one-hot output neuron pulled back through the conv."""
+    if not has_nonzero_split(relu_split_state):
+        return []
+    task = module.get_entry_task()
+    params = module.params
+    _env, relu_pre = forward_ibp_trace(module, spec)
+    producer = {op.outputs[0]: op for op in task.ops if op.outputs}
+    out = []
+    for op in task.ops:
+        if op.op_type != "relu":
+            continue
+        x = op.inputs[0]
+        split = relu_split_state.get(x)
+        if split is None or x not in relu_pre:
+            continue
+        flat = broadcast_split(split, relu_pre[x].lower)
+        prod = producer.get(x)
+        if prod is None or not prod.inputs or prod.inputs[0] != spec.value_name or int(flat.shape[0]) != 1:
+            continue
+        vec = flat[0]
+        if prod.op_type == "linear":
+            W = params.get(prod.inputs[1])
+            if W is None or W.dim() != 2 or int(W.shape[0]) != int(vec.shape[0]):
+                continue
+            b = params.get(prod.inputs[2]) if len(prod.inputs) == 3 else torch.zeros(int(W.shape[0]), dtype=W.dtype)
+            if b is None or b.dim() != 1 or int(b.shape[0]) != int(W.shape[0]):
+                continue
+            for i in range(int(vec.shape[0])):
+                s = int(vec[i])
+                if s != 0:
+                    out.append((x, i, float(s) * W[i], float(s) * b[i]))
+            continue
+        if prod.op_type != "conv2d":
+            continue
+        W = params.get(prod.inputs[1])
+        if W is None or W.dim() != 4 or spec.center.dim() != 4:
+            continue
+        oshape = tuple(int(d) for d in relu_pre[x].lower.shape[1:])
+        if len(oshape) != 3:
+            continue
+        b = params.get(prod.inputs[2]) if len(prod.inputs) == 3 else None
+        if b is None:
+            b = torch.zeros(int(W.shape[0]), dtype=W.dtype)
+        ishape = tuple(int(d) for d in spec.center.shape[1:])
+        a = prod.attrs
+        for fi in range(int(vec.shape[0])):
+            s = int(vec[fi])
+            if s == 0:
+                continue
+            one_hot = torch.zeros((1, 1) + oshape, dtype=W.dtype)
+            one_hot.view(-1)[fi] = 1.0
+            row = conv2d_right(DenseOp(one_hot, oshape), W, a.get("stride", 1), a.get("padding", 0),
+                               a.get("dilation", 1), int(a.get("groups", 1)), ishape, oshape).to_dense()[0, 0]
+            ch = fi // (oshape[1] * oshape[2])
+            out.append((x, fi, float(s) * row.reshape(-1), float(s) * b[ch]))
+    return out
+
+
+def split_certificate(module: BFTaskModule, input_spec, relu_split_state, *, steps: int = 200, lr: float = 0.1,
+                      tol: float = 1e-6) -> Tuple[bool, str]:
+    """alpha_beta_crown.py:391-532: the first-layer split halfspaces have no common
+    point in the input set when some convex combination of them has a maximum
+    over the set below -tol.  One halfspace is checked directly; several by
+    Adam on the softmax logits of the combination (from 0, ``steps`` steps,
+    stopping at the first maximum below -tol)."""
+    spec = normalize_input_spec(input_spec)
+    hs = first_layer_split_halfspaces(module, spec, relu_split_state)
+    if not hs:
+        return False, "ok (no first-layer split halfspaces)"
+    if int(spec.center.shape[0]) != 1:
+        return False, "skip (batch!=1)"
+    dtype = spec.center.dtype
+    ishape = tuple(int(d) for d in spec.center.shape[1:])
+    a_mat = torch.stack([h[2].to(dtype) for h in hs], dim=0).detach()
+    c_vec = torch.stack([h[3].to(dtype) for h in hs], dim=0).detach()
+
+    def upper(a, c):
+        _lb, ub = concretize_affine(spec, spec.center, DenseOp(a.view(1, 1, -1), ishape), c.view(1, 1))
+        return ub.squeeze()
+
+    if len(hs) == 1:
+        ub0 = float(upper(a_mat[0], c_vec[0]).item())
+        return (True, "infeasible: single halfspace") if ub0 < -float(tol) else (False, "ok")
+    logits = torch.zeros(len(hs), dtype=dtype, requires_grad=True)
+    opt = torch.optim.Adam([logits], lr=float(lr))
+    for _ in range(int(steps)):
+        w = torch.softmax(logits, dim=0)
+        ub0 = upper((w.unsqueeze(1) * a_mat).sum(dim=0), (w * c_vec).sum())
+        if float(ub0.detach().item()) < -float(tol):
+            return True, "infeasible: convex combination"
+        opt.zero_grad(set_to_none=True)
+        ub0.backward()
+        opt.step()
+    return False, "ok"
+
+
 def adaptive_alpha_init(relu_pre: Dict[str, IntervalState]) -> Dict[str, torch.Tensor]:
     """native_alpha_beta_optimizer_schedule.py:635-653 ("from CROWN" slope init)."""
     out = {}
@@ -116,15 +224,33 @@ def run_alpha_beta_crown(
     warm_start_beta: Optional[Dict[str, torch.Tensor]] = None,
     per_batch_params: bool = False,
     forward_trace=None,
+    return_feasibility: bool = False,
+    record: Optional[list] = None,
 ):
     """alpha_beta_crown.py:643-941 with objective="lower", spec_reduce="mean".
 
-    Returns (best_bounds, best_alpha, best_beta, branch_choices).
+    Returns (best_bounds, best_alpha, best_beta, branch_choices), plus the
+    feasibility ("infeasible" or "unknown") with ``return_feasibility``.  A
+    single domain with splits is first checked by ``split_certificate``
+    (:694-714); when it proves the splits infeasible the bounds are zeros of
+    shape [1, 1], the parameter dicts empty and the branch choices None.
+
+    ``record`` (a list) receives one dict per evaluation: the parameters it used
+    (``alpha``, ``beta``), its bounds, and for the steps that update them the
+    gradients, Adam's moments before the update (``exp_avg``, ``exp_avg_sq``;
+    zeros before the first) and the clamped parameters after it (``alpha_next``,
+    ``beta_next``) -- the state the per-step parity tests feed to the device.
     """
     module.validate()
     spec = normalize_input_spec(input_spec)
     dtype = spec.center.dtype
     batch = int(spec.center.shape[0])
+    if batch == 1 and has_nonzero_split(relu_split_state or {}):
+        infeasible, _reason = split_certificate(module, spec, relu_split_state)
+        if infeasible:
+            zeros = torch.zeros((1, 1), dtype=dtype)
+            out = (IntervalState(zeros, zeros.clone()), {}, {}, None)
+            return out + ("infeasible",) if return_feasibility else out
     if forward_trace is None:
         interval_env, relu_pre = forward_ibp_trace(module, spec, relu_split_state=relu_split_state)
     else:
@@ -160,6 +286,10 @@ def run_alpha_beta_crown(
         )
         metric_b = bounds.lower.mean(dim=1)
         metric = metric_b.mean()
+        if record is not None:
+            record.append({"step": step, "alpha": {k: v.detach().clone() for k, v in alpha.items()},
+                           "beta": {k: v.detach().clone() for k, v in beta.items()},
+                           "lower": bounds.lower.detach().clone(), "upper": bounds.upper.detach().clone()})
         if best_metric is None:
             best_metric = metric_b.detach().clone()
             best_metric_scalar = metric.detach().clone()
@@ -195,13 +325,29 @@ def run_alpha_beta_crown(
             break
         opt.zero_grad(set_to_none=True)
         loss.backward()
+        if record is not None:
+            def moments(p, key):
+                st = opt.state.get(p, {})
+                return st[key].detach().clone() if key in st else torch.zeros_like(p)
+            rec = record[-1]
+            rec["grad_alpha"] = {k: (v.grad.detach().clone() if v.grad is not None else None) for k, v in alpha.items()}
+            rec["grad_beta"] = {k: (v.grad.detach().clone() if v.grad is not None else None) for k, v in beta.items()}
+            rec["exp_avg"] = {("alpha", k): moments(v, "exp_avg") for k, v in alpha.items()}
+            rec["exp_avg"].update({("beta", k): moments(v, "exp_avg") for k, v in beta.items()})
+            rec["exp_avg_sq"] = {("alpha", k): moments(v, "exp_avg_sq") for k, v in alpha.items()}
+            rec["exp_avg_sq"].update({("beta", k): moments(v, "exp_avg_sq") for k, v in beta.items()})
+            rec["adam_step"] = step + 1
         opt.step()
         with torch.no_grad():
             for a in alpha.values():
                 a.clamp_(0.0, 1.0)
             for b in beta.values():
                 b.clamp_(0.0)
-    return best_bounds, best_alpha, best_beta, choices
+        if record is not None:
+            record[-1]["alpha_next"] = {k: v.detach().clone() for k, v in alpha.items()}
+            record[-1]["beta_next"] = {k: v.detach().clone() for k, v in beta.items()}
+    out = (best_bounds, best_alpha, best_beta, choices)
+    return out + ("unknown",) if return_feasibility else out
 
 
 def run_alpha_crown(

@@ -4,17 +4,20 @@ Only tests, the smoke check and the bench's CPU baseline use this module, as
 the checker; nothing in ``boundflow_amd`` imports it.
 
 Follows ``solve_bab_mlp`` (boundflow/runtime/bab.py:631-1528) for the paths it
-takes without a query recorder/runtime, node cache hits, the 1-D input
-restriction or first-layer pre-pruning:
+takes without a query recorder/runtime or node cache hits (a search tree never
+evaluates the same split set twice, so the cache cannot hit):
 
 * one search tree per example; heap keyed (priority, node_id), roots at -inf
   (:700-720); pop up to ``node_batch_size`` nodes per round for the alpha-beta
   oracle, one otherwise, skipping decided examples and charging the node
   budget (:957-977);
-* a single popped node is evaluated alone (:995-1110), several together with
-  per-node parameters and warm starts (:1250-1345); when the batched call
-  raises (an infeasible split) every node is evaluated alone and the
-  infeasible ones are rejected (:1399-1456);
+* a single popped node is evaluated alone (:995-1110), where the alpha-beta
+  oracle first runs the first-layer split certificate (alpha_beta_crown.py:694-714)
+  and the 1-D input restriction may narrow or close it (:1000-1012, :524-628);
+  several together with per-node parameters and warm starts (:1250-1345), after
+  the optional first-layer pre-pruning (:373-425); when the batched call raises
+  (an IBP-infeasible split) every node is evaluated alone, certificate included,
+  and the infeasible ones are rejected (:1399-1456);
 * ``_process_evaluated_node`` (:870-955): best bounds, certification at
   min lb >= threshold - tol, branch on the evaluation's hint (alpha-beta) or
   the widest ambiguous IBP neuron (``_pick_branch``, :488-522), "unsafe" when
@@ -58,20 +61,86 @@ def _slice_spec(spec: InputSpec, idx: List[int]) -> InputSpec:
     return InputSpec(value_name=spec.value_name, center=spec.center[idx], perturbation=p)
 
 
+class NodeInfeasible(ValueError):
+    """A node whose splits the first-layer certificate proves infeasible: the
+    reference closes it exactly as it closes one whose IBP trace raises
+    (bab.py:1058-1069, :1421-1431)."""
+
+
 def _eval_single(module, spec, C, item: _Item, cfg):
-    """eval_bab_alpha_beta_node / run_alpha_crown_mlp for one node; raises ValueError when infeasible."""
+    """eval_bab_alpha_beta_node / run_alpha_crown_mlp for one node; raises ValueError when
+    the IBP trace is infeasible and NodeInfeasible when the certificate closes the node."""
     split = {k: v.unsqueeze(0) for k, v in item.split.items()}
     if cfg["oracle"] == "alpha_beta":
-        bounds, alpha, beta, choices = ab.run_alpha_beta_crown(
+        bounds, alpha, beta, choices, feas = ab.run_alpha_beta_crown(
             module, spec, linear_spec_C=C, relu_split_state=split, steps=cfg["alpha_steps"], lr=cfg["alpha_lr"],
             alpha_init=cfg["alpha_init"], beta_init=cfg["beta_init"], warm_start_alpha=item.warm_alpha,
-            warm_start_beta=item.warm_beta)
+            warm_start_beta=item.warm_beta, return_feasibility=True)
+        if feas == "infeasible":
+            raise NodeInfeasible("first-layer split certificate")
         hint = choices[0] if len(choices) == 1 else None
         return bounds, alpha, beta, hint
     bounds, alpha = ab.run_alpha_crown(module, spec, linear_spec_C=C, steps=cfg["alpha_steps"], lr=cfg["alpha_lr"],
                                        alpha_init=cfg["alpha_init"], relu_split_state=split,
                                        warm_start=item.warm_alpha)
     return bounds, alpha, None, None
+
+
+def restrict_1d_linf(module, spec: InputSpec, split: Dict[str, torch.Tensor]) -> Optional[InputSpec]:
+    """bab.py:524-628: a one-input Linf spec narrowed by the first-layer split
+    constraints s * (w_i x + b_i) >= 0 of linear layers reading the input; None
+    when they leave nothing.  Any other spec is returned unchanged."""
+    from boundflow_amd.spec import LpBallPerturbation
+    if spec.center.dim() != 2 or int(spec.center.shape[1]) != 1:
+        return spec
+    p = spec.perturbation
+    if not isinstance(p, LpBallPerturbation) or p.normalized_p() != "inf":
+        return spec
+    if int(spec.center.shape[0]) != 1:
+        return spec
+    task = module.get_entry_task()
+    params = module.params
+    x0 = float(spec.center[0, 0].item())
+    eps = float(p.eps)
+    lo, hi = x0 - eps, x0 + eps
+    for op in task.ops:
+        if op.op_type != "relu":
+            continue
+        x = op.inputs[0]
+        sv = split.get(x)
+        if sv is None:
+            continue
+        prod = next((q for q in task.ops if x in q.outputs), None)
+        if prod is None or prod.op_type != "linear" or not prod.inputs or prod.inputs[0] != spec.value_name:
+            continue
+        W = params.get(prod.inputs[1])
+        if W is None or W.dim() != 2 or int(W.shape[1]) != 1:
+            continue
+        if len(prod.inputs) == 3:
+            b = params.get(prod.inputs[2])
+            if b is None or b.dim() != 1 or int(b.shape[0]) != int(W.shape[0]):
+                continue
+        else:
+            b = torch.zeros(int(W.shape[0]), dtype=W.dtype)
+        for i in range(int(sv.shape[0])):
+            sg = int(sv[i].item())
+            if sg == 0:
+                continue
+            wi = float(W[i, 0].item())
+            bi = float(b[i].item())
+            if wi == 0.0:
+                if (sg > 0 and bi < 0.0) or (sg < 0 and bi > 0.0):
+                    return None
+                continue
+            t = -bi / wi
+            if (sg > 0) == (wi > 0):
+                lo = max(lo, t)
+            else:
+                hi = min(hi, t)
+        if lo > hi:
+            return None
+    center = torch.tensor([[0.5 * (lo + hi)]], dtype=spec.center.dtype)
+    return InputSpec.linf(value_name=spec.value_name, center=center, eps=float(0.5 * (hi - lo)))
 
 
 def _pick_branch(module, spec, split: Dict[str, torch.Tensor]) -> Optional[Tuple[str, int]]:
@@ -102,7 +171,9 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C, config) -> dict:
     batch_rounds = 0
     popped_total = 0
     max_q = len(heap)
-    do_batch = cfg["oracle"] == "alpha_beta" and int(cfg["node_batch_size"]) > 1
+    do_batch = (cfg["oracle"] == "alpha_beta" and int(cfg["node_batch_size"]) > 1
+                and not cfg.get("use_1d_linf_input_restriction_patch", False))
+    prune = bool(cfg.get("enable_batch_infeasible_prune", False)) and cfg["oracle"] == "alpha_beta"
 
     def done_if_empty(e):
         if status[e] is None and live[e] == 0:
@@ -167,41 +238,33 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C, config) -> dict:
             item = items[0]
             e = item.example_idx
             C = None if linear_spec_C is None else linear_spec_C[[e]]
+            node_spec = _slice_spec(spec, [e])
+            if cfg.get("use_1d_linf_input_restriction_patch", False):
+                node_spec = restrict_1d_linf(module, node_spec, item.split)
+                if node_spec is None:
+                    live[e] = max(0, live[e] - 1)
+                    done_if_empty(e)
+                    continue
             try:
-                results[0] = _eval_single(module, _slice_spec(spec, [e]), C, item, cfg)
+                results[0] = _eval_single(module, node_spec, C, item, cfg)
             except ValueError:
                 live[e] = max(0, live[e] - 1)
                 done_if_empty(e)
                 continue
         else:
-            ex = [it.example_idx for it in items]
-            split_b = {k: torch.stack([it.split[k] for it in items]) for k in shapes}
-            warm_a = {k: torch.stack([it.warm_alpha[k].reshape(shapes[k]) if it.warm_alpha is not None
-                                      else torch.full(shapes[k], float(cfg["alpha_init"]), dtype=spec.center.dtype)
-                                      for it in items]) for k in shapes}
-            warm_b = {k: torch.stack([it.warm_beta[k].reshape(shapes[k]) if it.warm_beta is not None
-                                      else torch.full(shapes[k], float(cfg["beta_init"]), dtype=spec.center.dtype)
-                                      for it in items]) for k in shapes}
-            C = None if linear_spec_C is None else linear_spec_C[ex]
-            try:
-                bounds, alpha, beta, choices = ab.run_alpha_beta_crown(
-                    module, _slice_spec(spec, ex), linear_spec_C=C, relu_split_state=split_b,
-                    steps=cfg["alpha_steps"], lr=cfg["alpha_lr"], alpha_init=cfg["alpha_init"],
-                    beta_init=cfg["beta_init"], warm_start_alpha=warm_a, warm_start_beta=warm_b,
-                    per_batch_params=True)
-                for j in range(len(items)):
-                    nb = type(bounds)(bounds.lower[j:j + 1].clone(), bounds.upper[j:j + 1].clone())
-                    results[j] = (nb, {k: v[j].clone() for k, v in alpha.items()},
-                                  {k: v[j].clone() for k, v in beta.items()}, choices[j])
-            except ValueError:
-                for j, item in enumerate(items):
-                    e = item.example_idx
-                    C1 = None if linear_spec_C is None else linear_spec_C[[e]]
-                    try:
-                        results[j] = _eval_single(module, _slice_spec(spec, [e]), C1, item, cfg)
-                    except ValueError:
-                        live[e] = max(0, live[e] - 1)
-                        done_if_empty(e)
+            # per-node first-layer pre-pruning (bab.py:373-425, applied at :1157-1168)
+            keep = []
+            for j, item in enumerate(items):
+                e = item.example_idx
+                if prune and ab.split_certificate(module, _slice_spec(spec, [e]),
+                                                  {k: v.unsqueeze(0) for k, v in item.split.items()})[0]:
+                    live[e] = max(0, live[e] - 1)
+                    done_if_empty(e)
+                else:
+                    keep.append(j)
+            sub_items = [items[j] for j in keep]
+            results.update(_eval_batch(module, spec, linear_spec_C, sub_items, keep, shapes, cfg, live,
+                                       done_if_empty))
         for j, item in enumerate(items):
             if j in results:
                 process(item, *results[j])
@@ -219,3 +282,46 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C, config) -> dict:
         "per_status": status, "per_visited": visited, "per_evaluated": evaluated, "per_expanded": expanded,
         "per_best_lower": best_lower, "per_best_upper": best_upper,
     }
+
+
+def _eval_batch(module, spec, linear_spec_C, items, slots, shapes, cfg, live, done_if_empty) -> Dict[int, tuple]:
+    """bab.py:1250-1456: one per_batch_params call over the nodes; when it raises (an
+    IBP-infeasible split) every node is evaluated alone (with the single-node
+    certificate) and the infeasible ones are closed.  Results keyed by ``slots``."""
+    results: Dict[int, tuple] = {}
+    if not items:
+        return results
+    ex = [it.example_idx for it in items]
+    split_b = {k: torch.stack([it.split[k] for it in items]) for k in shapes}
+    warm_a = {k: torch.stack([it.warm_alpha[k].reshape(shapes[k]) if it.warm_alpha is not None
+                              else torch.full(shapes[k], float(cfg["alpha_init"]), dtype=spec.center.dtype)
+                              for it in items]) for k in shapes}
+    warm_b = {k: torch.stack([it.warm_beta[k].reshape(shapes[k]) if it.warm_beta is not None
+                              else torch.full(shapes[k], float(cfg["beta_init"]), dtype=spec.center.dtype)
+                              for it in items]) for k in shapes}
+    C = None if linear_spec_C is None else linear_spec_C[ex]
+    try:
+        bounds, alpha, beta, choices = ab.run_alpha_beta_crown(
+            module, _slice_spec(spec, ex), linear_spec_C=C, relu_split_state=split_b,
+            steps=cfg["alpha_steps"], lr=cfg["alpha_lr"], alpha_init=cfg["alpha_init"],
+            beta_init=cfg["beta_init"], warm_start_alpha=warm_a, warm_start_beta=warm_b,
+            per_batch_params=True)
+        if len(items) == 1 and choices is None:
+            # one node left after pruning: the batched call's own certificate closed it
+            live[ex[0]] = max(0, live[ex[0]] - 1)
+            done_if_empty(ex[0])
+            return results
+        for j in range(len(items)):
+            nb = type(bounds)(bounds.lower[j:j + 1].clone(), bounds.upper[j:j + 1].clone())
+            results[slots[j]] = (nb, {k: v[j].clone() for k, v in alpha.items()},
+                                 {k: v[j].clone() for k, v in beta.items()}, choices[j])
+    except ValueError:
+        for j, item in enumerate(items):
+            e = item.example_idx
+            C1 = None if linear_spec_C is None else linear_spec_C[[e]]
+            try:
+                results[slots[j]] = _eval_single(module, _slice_spec(spec, [e]), C1, item, cfg)
+            except ValueError:
+                live[e] = max(0, live[e] - 1)
+                done_if_empty(e)
+    return results

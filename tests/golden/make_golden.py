@@ -250,20 +250,36 @@ def golden_task_ibp_scheduled(w, tag):
     save(tag, lower=out.lower, upper=out.upper, checksum=workload_checksum(w))
 
 
-BAB_SOLVE_CASES = {
-    "bab_solve_ab_e003": (0.03, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
-    "bab_solve_ab_e005": (0.05, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
-    "bab_solve_alpha_e005": (0.05, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
-}
+from tests.golden_util import BAB_SOLVE_CASES  # noqa: E402
+
+
+def count_certificates():
+    """Wrap the reference's certificate to count the nodes it closes (for the fixtures' records)."""
+    orig = rabc._is_infeasible_split_first_layer_convex_combo
+    box = {"calls": 0, "closed": 0}
+
+    def wrapped(module, spec, *, relu_split_state, **kw):
+        out = orig(module, spec, relu_split_state=relu_split_state, **kw)
+        box["calls"] += 1
+        box["closed"] += int(bool(out[0]))
+        return out
+
+    rabc._is_infeasible_split_first_layer_convex_combo = wrapped
+    return box, lambda: setattr(rabc, "_is_infeasible_split_first_layer_convex_combo", orig)
 
 
 def golden_bab_solve(tag):
     """solve_bab_mlp (bab.py:631-1528) on the small BaB workload."""
     from boundflow.runtime.bab import BabConfig as RBabConfig
     from boundflow.runtime.bab import solve_bab_mlp as r_solve
-    eps, kw = BAB_SOLVE_CASES[tag]
-    w = wl.make_bab_toy(eps=eps)
-    res = r_solve(to_ref_module(w.module), to_ref_spec(w.spec), linear_spec_C=w.C, config=RBabConfig(**kw))
+    toy, kw = BAB_SOLVE_CASES[tag]
+    w = wl.make_bab_toy(**toy)
+    counts, restore = count_certificates()
+    try:
+        res = r_solve(to_ref_module(w.module), to_ref_spec(w.spec), linear_spec_C=w.C, config=RBabConfig(**kw))
+    finally:
+        restore()
+    print(tag, "certificate calls", counts)
     per = res.per_example
     status_code = {"proven": 0, "unsafe": 1, "unknown": 2}
     save(tag, status=status_code[res.status], nodes_visited=res.nodes_visited, nodes_evaluated=res.nodes_evaluated,
@@ -275,6 +291,7 @@ def golden_bab_solve(tag):
          per_expanded=np.array([r.nodes_expanded for r in per]),
          per_best_lower=np.array([r.best_lower for r in per]),
          per_best_upper=np.array([r.best_upper for r in per]),
+         certificate_calls=counts["calls"], certificate_closed=counts["closed"],
          checksum=workload_checksum(w))
 
 
@@ -315,6 +332,10 @@ GOLDENS = [
     ("bab_solve_ab_e003", golden_bab_solve),
     ("bab_solve_ab_e005", golden_bab_solve),
     ("bab_solve_alpha_e005", golden_bab_solve),
+    ("bab_solve_cert_single", golden_bab_solve),
+    ("bab_solve_cert_fallback", golden_bab_solve),
+    ("bab_solve_cert_prune", golden_bab_solve),
+    ("bab_solve_1d", golden_bab_solve),
 ]
 
 

@@ -41,3 +41,50 @@ def test_library_exports_every_declared_symbol():
     exported = set(re.findall(r"\bT (bf_[a-z0-9_]+)$", out, flags=re.M))
     missing = [s for s in header_symbols() if s not in exported]
     assert not missing, missing
+
+
+def header_declarations():
+    """name -> (return type, [parameter types]) of every declaration in the header,
+    each C type reduced to its ctypes class (pointers and hipStream_t are pointers)."""
+    import ctypes
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    decls = {}
+    for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b(bf_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        ret, name, params = m.group(1).strip(), m.group(2), m.group(3).strip()
+
+        def ctype(decl: str):
+            decl = " ".join(decl.split())
+            if "*" in decl:
+                return ctypes.c_void_p
+            base = decl.replace("const ", "").split()
+            if "hipStream_t" in base:
+                return ctypes.c_void_p
+            for key, ct in (("int64_t", ctypes.c_int64), ("int32_t", ctypes.c_int32), ("int", ctypes.c_int),
+                            ("float", ctypes.c_float), ("double", ctypes.c_double)):
+                if key in base:
+                    return ct
+            raise AssertionError(f"{name}: unknown C type {decl!r}")
+
+        args = [] if params in ("", "void") else [ctype(p) for p in params.split(",")]
+        r = ctypes.c_char_p if ret.replace(" ", "") == "constchar*" else ctype(ret)
+        decls[name] = (r, args)
+    return decls
+
+
+def test_binding_argument_types_match_header():
+    """Every parameter's C type (int / int64_t / float / double / pointer) equals the
+    ctypes type the binding passes: a c_int for an int64_t stack argument would
+    otherwise pass silently."""
+    import ctypes
+    from boundflow_amd import _lib
+    decls = header_declarations()
+    assert sorted(decls) == sorted(_lib.SIGNATURES)
+    norm = {ctypes.c_int32: ctypes.c_int}
+    for name, (res, args) in _lib.SIGNATURES.items():
+        h_res, h_args = decls[name]
+        assert norm.get(h_res, h_res) == norm.get(res, res), f"{name}: return type"
+        assert len(h_args) == len(args), f"{name}: {len(h_args)} parameters in the header, {len(args)} bound"
+        for i, (h, b) in enumerate(zip(h_args, args)):
+            assert norm.get(h, h) == norm.get(b, b), f"{name}: parameter {i} is {h.__name__} in the header, " \
+                                                     f"{b.__name__} in the binding"

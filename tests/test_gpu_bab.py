@@ -1,8 +1,12 @@
 """HIP branch and bound (boundflow_amd.bab.solve_bab_mlp) against whole
-searches of the reference's solve_bab_mlp (tests/golden) on the small BaB
-workload: identical statuses, node counts, rounds and queue size (every
-certification and branching decision matches), best bounds within rtol 1e-4
-(10-step Adam trajectories, as the domain-batch tests)."""
+searches of the reference's solve_bab_mlp (tests/golden) on small BaB
+workloads, including searches where the first-layer split certificate closes
+nodes (node by node, in the per-node fallback of a batch, as pre-pruning) and a
+one-input network under the 1-D input restriction: identical statuses, node
+counts, rounds and queue size (every certification, infeasibility and
+branching decision matches); best bounds within rtol 1e-4 (the count outside
+the 1e-5 / 1e-6 contract is reported: they end 5- and 10-step Adam
+trajectories)."""
 
 import numpy as np
 import pytest
@@ -10,26 +14,22 @@ import torch
 
 from boundflow_amd import bab as hbab
 from boundflow_amd import workloads as wl
-from tests.golden_util import load
+from tests.golden_util import BAB_SOLVE_CASES, load
 from tests.gpu_util import announce, device
 
 pytestmark = pytest.mark.gpu
 
-CASES = {
-    "bab_solve_ab_e003": (0.03, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
-    "bab_solve_ab_e005": (0.05, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
-    "bab_solve_alpha_e005": (0.05, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
-}
+CASES = BAB_SOLVE_CASES
 CODE = {"proven": 0, "unsafe": 1, "unknown": 2}
 
 
 @pytest.mark.parametrize("tag", list(CASES))
 def test_hip_bab_search_matches_reference(tag):
     dev = device()
-    eps, kw = CASES[tag]
+    toy, kw = CASES[tag]
     announce(f"solve_bab_mlp {tag}")
     g = load(tag)
-    wd = wl.to_device(wl.make_bab_toy(eps=eps), dev)
+    wd = wl.to_device(wl.make_bab_toy(**toy), dev)
     r = hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C, config=hbab.BabConfig(**kw))
     per = r.per_example
     announce(f"  statuses {[p.status for p in per]} visited {[p.nodes_visited for p in per]} "
@@ -41,8 +41,14 @@ def test_hip_bab_search_matches_reference(tag):
     assert [p.nodes_expanded for p in per] == g["per_expanded"].tolist()
     assert (r.max_queue, r.batch_rounds) == (int(g["max_queue"]), int(g["batch_rounds"]))
     assert abs(r.avg_batch_fill_rate - float(g["avg_batch_fill_rate"])) < 1e-12
-    np.testing.assert_allclose([p.best_lower for p in per], g["per_best_lower"], rtol=1e-4, atol=1e-5)
-    np.testing.assert_allclose([p.best_upper for p in per], g["per_best_upper"], rtol=1e-4, atol=1e-5)
+    got = np.array([[p.best_lower for p in per], [p.best_upper for p in per]])
+    ref = np.stack([g["per_best_lower"], g["per_best_upper"]])
+    finite = np.isfinite(ref)
+    d = np.abs(got - ref)[finite]
+    out = int((d > 1e-6 + 1e-5 * np.abs(ref[finite])).sum())
+    announce(f"  best bounds: max abs diff {d.max() if d.size else 0.0:.3e}, outside 1e-5/1e-6: {out}/{d.size}")
+    assert np.array_equal(np.isfinite(got), finite)
+    np.testing.assert_allclose(got[finite], ref[finite], rtol=1e-4, atol=1e-5)
 
 
 def test_hip_bab_frontier_growth_and_budget():

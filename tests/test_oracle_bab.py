@@ -14,27 +14,23 @@ import torch
 
 from boundflow_amd import workloads as wl
 from oracle import bab_ref
-from tests.golden_util import load, workload_checksum
+from tests.golden_util import BAB_SOLVE_CASES, load, workload_checksum
 
-CASES = {
-    "bab_solve_ab_e003": (0.03, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
-    "bab_solve_ab_e005": (0.05, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
-    "bab_solve_alpha_e005": (0.05, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
-}
+CASES = BAB_SOLVE_CASES
 DEFAULTS = dict(use_branch_hint=True, alpha_lr=0.2, alpha_init=0.5, beta_init=0.0, threshold=0.0, tol=1e-6)
 CODE = {"proven": 0, "unsafe": 1, "unknown": 2}
 
 
 def config(tag):
-    eps, kw = CASES[tag]
-    return eps, {**DEFAULTS, **kw}
+    toy, kw = CASES[tag]
+    return toy, {**DEFAULTS, **kw}
 
 
 @pytest.mark.parametrize("tag", list(CASES))
 def test_bab_search_matches_reference(tag):
     g = load(tag)
-    eps, cfg = config(tag)
-    w = wl.make_bab_toy(eps=eps)
+    toy, cfg = config(tag)
+    w = wl.make_bab_toy(**toy)
     assert workload_checksum(w) == str(g["checksum"])
     r = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
     assert CODE[r["status"]] == int(g["status"])
@@ -63,8 +59,9 @@ def _margins(w, x):
 
 @pytest.mark.parametrize("tag", ["bab_solve_ab_e003", "bab_solve_ab_e005"])
 def test_bab_verdicts_are_sound(tag):
-    eps, cfg = config(tag)
-    w = wl.make_bab_toy(eps=eps)
+    toy, cfg = config(tag)
+    eps = toy["eps"]
+    w = wl.make_bab_toy(**toy)
     r = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
     x0 = w.spec.center.double()
     g = torch.Generator().manual_seed(9)
