@@ -38,6 +38,8 @@ SIGNATURES = {
     "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, F32, P, P,
                                               P, P, P, P, P, P]),
     "bf_crown_relu_linear_concretize_workspace": (I64, [I64, I64, I64]),
+    "bf_crown_relu_linear_concretize_noalloc": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, F32,
+                                                      P, P, P, P, P, P, P]),
     "bf_crown_relu_linear_relu_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, P, P, P, P, P, I64, P, P,
                                             I64, P, P, P, P, P, P, P, P, P, P]),
     "bf_crown_relu_linear_relu_fwd_workspace": (I64, [I64, I64, I64]),

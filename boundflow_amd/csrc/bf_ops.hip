@@ -8,6 +8,7 @@
 #include "bf_common.h"
 
 #include <cstring>
+#include <mutex>
 
 namespace bf {
 
@@ -809,6 +810,51 @@ small_k_relax_epi_kernel(const float* __restrict__ A0, const float* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------
+// The same concretization without a caller workspace, for callers that cannot
+// allocate (graph capture, serving loops that forbid it).  Its workspace -- the
+// per-column-tile partial norms, the center and bias sums -- lives in a
+// file-scope device array of kConcretizeScratchFloats floats (16 MiB), one copy
+// per GPU for the life of the process.  The kernels write every element they
+// later read (each column tile its partial norm of every row, the first column
+// tile the center and bias sums), so nothing is cleared between calls.  Calls
+// that overlap on one GPU share the array and race: serialise them (one stream,
+// or events) as for any buffer they would share.
+
+constexpr int64_t kConcretizeScratchFloats = (int64_t)4 << 20;
+static __device__ __align__(256) float scratch[kConcretizeScratchFloats];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_dev[kMaxDevices] = {};   // device address of `scratch` on each GPU
+
+// Address of the current device's copy of `scratch`, looked up once per device
+// (the host symbol itself is not a device address).
+static int concretize_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("bf_crown_relu_linear_concretize_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return BF_ELAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("bf_crown_relu_linear_concretize_noalloc: device %d beyond %d", dev, kMaxDevices);
+    return BF_ERANGE;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("bf_crown_relu_linear_concretize_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return BF_ELAUNCH;
+    }
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return BF_OK;
+}
+
 }  // namespace bf
 
 using namespace bf;
@@ -1015,6 +1061,29 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
   const int64_t M = D * S;
   return (2 * (int64_t)gemm_partial_count(I) + 4) * M;
+}
+
+int bf_crown_relu_linear_concretize_noalloc(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D,
+                                            int64_t S, int64_t N, const float* relax, const float* add_l,
+                                            int64_t add_ld, const float* W, int64_t I, int w_trans, const float* bias,
+                                            const float* cvec, const float* rad, float eps, const float* b_u_in,
+                                            const float* b_l_in, const float* h_scale, float* h_out, float* lb,
+                                            float* ub, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize_noalloc: bad sizes");
+  if (D * S == 0) return BF_OK;
+  const int64_t need = bf_crown_relu_linear_concretize_workspace(D, S, I);
+  if (need > kConcretizeScratchFloats) {
+    set_error("bf_crown_relu_linear_concretize_noalloc: %lld rows of %lld columns need %lld workspace floats, the "
+              "fixed scratch holds %lld (at most %lld rows at this width); use bf_crown_relu_linear_concretize",
+              (long long)(D * S), (long long)I, (long long)need, (long long)kConcretizeScratchFloats,
+              (long long)(kConcretizeScratchFloats / (2 * (int64_t)gemm_partial_count(I) + 4)));
+    return BF_ERANGE;
+  }
+  float* ws = nullptr;
+  const int rc = concretize_scratch(&ws);
+  if (rc) return rc;
+  return bf_crown_relu_linear_concretize(A_u, A_l, a_dstride, D, S, N, relax, add_l, add_ld, W, I, w_trans, bias,
+                                         cvec, rad, eps, b_u_in, b_l_in, h_scale, h_out, ws, lb, ub, stream);
 }
 
 int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,

@@ -135,6 +135,21 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
                                     float* workspace, float* lb, float* ub, hipStream_t stream);
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I);
 
+/* bf_crown_relu_linear_concretize without the workspace argument: no counterpart in
+ * the reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops or harnesses that forbid hipMalloc); it allocates
+ * nothing.  Its workspace is a fixed 16 MiB device array per GPU (4M floats, held
+ * until the process ends): returns 3 (size beyond the limit) when
+ * bf_crown_relu_linear_concretize_workspace(D, S, I) exceeds 4194304 floats (e.g.
+ * D * S > 233016 rows at I = 784).  Calls that overlap on one GPU share that array
+ * and race: serialise them.  Same results as bf_crown_relu_linear_concretize. */
+int bf_crown_relu_linear_concretize_noalloc(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D,
+                                            int64_t S, int64_t N, const float* relax, const float* add_l,
+                                            int64_t add_ld, const float* W, int64_t I, int w_trans, const float* bias,
+                                            const float* cvec, const float* rad, float eps, const float* b_u_in,
+                                            const float* b_l_in, const float* h_scale, float* h_out, float* lb,
+                                            float* ub, hipStream_t stream);
+
 /* Two consecutive regions of the CROWN backward of an MLP in one launch: the
  * ReLU -> Linear region of bf_crown_relu_linear_fwd (prologue relaxation with
  * relax / add_l / bias; when all three are NULL, A is taken as already relaxed)
