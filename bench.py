@@ -9,9 +9,13 @@ refinements (C = I, M = 256 x 500 coefficient rows) and the final spec bound.
 The metric is final (lower, upper) bound pairs per second (2304 per step).
 
 Prints ONE JSON line with the throughput, the roofline position of the
-dominant kernel (timed with HIP events on the launch stream inside the timed
-region) and a CPU baseline (the PyTorch CPU restatement of the reference path
-timed on a bounded sample on this host).
+dominant kernel (timed with HIP events on the launch stream) and a CPU baseline
+(the PyTorch CPU restatement of the reference path timed on the whole batch on
+this host, with the parity of the HIP result against it).  With the default C2
+workload the line also carries ``secondary``: the metric's other half, BaB
+domains/s on the C5 domain batch (4096 subdomains of
+the MLP 784-256x4-10, 10 alpha-beta steps each), with its own roofline, CPU
+baseline and parity over all 4096 domains.
 
     python bench.py [--steps K] [--warmup W] [--config C2|C1|C3|C4|C5|D1] [--cpu-seconds S]
 
@@ -117,7 +121,9 @@ def torch_numel(shape) -> int:
 
 
 def _oracle_run(name: str, sub):
-    """The oracle's result for a workload (the computation the CPU baseline times)."""
+    """The oracle's result for a workload: the computation the CPU baseline times.
+    C5 times the reference's node-batch call (one per_batch_params alpha-beta
+    evaluation of every domain, bab.py:1323)."""
     import torch
     from oracle import alpha_beta_ref as ab
     from oracle import crown_ref as cr
@@ -133,87 +139,189 @@ def _oracle_run(name: str, sub):
         init = ab.adaptive_alpha_init(pre)
         return ab.run_alpha_beta_crown(sub.module, sub.spec, linear_spec_C=sub.C, steps=20, lr=0.1,
                                        warm_start_alpha=init, per_batch_params=True)
-    return ab.evaluate_domain_batch(sub.module, sub.spec, linear_spec_C=sub.C,
-                                    relu_split_state=sub.extra["splits"], steps=10, lr=0.2)
+    return ab.run_alpha_beta_crown(sub.module, sub.spec, linear_spec_C=sub.C, relu_split_state=sub.extra["splits"],
+                                   steps=10, lr=0.2, per_batch_params=True)
 
 
 def _bounds(name: str, res):
-    if name == "C5":
+    if isinstance(res, dict):
         return res["lower"], res["upper"]
     r = res[0] if isinstance(res, tuple) else res
     return r.lower, r.upper
 
 
-def parity_summary(name: str, sub, ref) -> dict:
-    """HIP result on the CPU-baseline sample against the oracle's result on it.
-    The contract: rtol 1e-5 / atol 1e-6 on both bounds (C1-C3); rtol 1e-4 /
-    atol 1e-4 on the optimised lower bound (C4, C5: Adam trajectories amplify fp32
-    rounding).  Rows outside it count as explained when the fp64 oracle run is
-    as far from the fp32 oracle as the HIP value is.  Also: verdict mismatches,
-    near ties (|min_s lb| < 1e-4) and, for the BaB batch, statuses and branching."""
+def parity_summary(name: str, w, ref) -> dict:
+    """HIP result on the whole workload against the oracle's result on it.
+    C1-C3, D1: the contract, rtol 1e-5 / atol 1e-6 on both bounds, a row outside
+    it counted as explained when the fp64 oracle is as far from the fp32 oracle
+    as the HIP value is.  C4, C5: whole Adam trajectories, so the counts outside
+    the contract and outside 1e-4 are reported and the verdict is taken at the
+    trajectory band 1e-3 (one step at a time they meet the contract, tested in
+    tests/test_gpu_teacher_forced.py).  Also: verdict mismatches, near ties
+    (|min_s lb| < 1e-4) and, for C5, certified flags and branching decisions of
+    every domain."""
     import torch
     from boundflow_amd import workloads as wl
     from oracle import parity
 
-    got = hip_runner(name)(wl.to_device(sub, torch.device("cuda:0")))
+    got = hip_runner(name)(wl.to_device(w, torch.device("cuda:0")))
     torch.cuda.synchronize()
     g_lo, g_hi = (t.cpu() for t in _bounds(name, got))
     r_lo, r_hi = _bounds(name, ref)
     optimised = name in ("C4", "C5")
-    rtol, atol = (1e-4, 1e-4) if optimised else (1e-5, 1e-6)
-    keep = torch.isfinite(r_lo).all(dim=1)
-    pick = (lambda lo, hi: lo[keep]) if optimised else (lambda lo, hi: torch.cat([lo[keep], hi[keep]]))
-    rep = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None, rtol=rtol, atol=atol)
-    if rep.strict_violations:
-        ref64 = _oracle_run(name, parity.to_float64(sub))
-        e_lo, e_hi = _bounds(name, ref64)
-        rep = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), pick(e_lo, e_hi), rtol=rtol, atol=atol)
-    g_min = g_lo[keep].min(dim=1).values
-    r_min = r_lo[keep].min(dim=1).values
-    out = {"contract": f"rtol {rtol:g} atol {atol:g} on " + ("the optimised lower bound" if optimised else "both bounds"),
-           "values": rep.n, "max_abs_err": rep.max_abs, "max_rel_err": rep.max_rel,
+    pick = (lambda lo, hi: lo) if name == "C5" else (lambda lo, hi: torch.cat([lo, hi]))
+    cache = {}
+
+    def ref64():
+        if "r" not in cache:
+            e_lo, e_hi = _bounds(name, _oracle_run(name, parity.to_float64(w)))
+            cache["r"] = pick(e_lo, e_hi)
+        return cache["r"]
+
+    strict = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None)
+    if optimised:
+        mid = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None, rtol=1e-4, atol=1e-4)
+        band = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None, rtol=1e-3, atol=1e-3)
+        if band.strict_violations:
+            band = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), ref64(), rtol=1e-3, atol=1e-3)
+        rep = band
+        contract = ("trajectory: rtol 1e-3 atol 1e-3 on the optimised " + ("lower bound" if name == "C5"
+                                                                          else "bounds")
+                    + f"; at the contract 1e-5/1e-6 {strict.strict_violations} outside, at 1e-4 "
+                      f"{mid.strict_violations} outside")
+    else:
+        rep = strict if not strict.strict_violations else parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), ref64())
+        contract = "rtol 1e-05 atol 1e-06 on both bounds"
+    g_min = g_lo.min(dim=1).values
+    r_min = r_lo.min(dim=1).values
+    out = {"contract": contract, "values": rep.n, "max_abs_err": rep.max_abs, "max_rel_err": rep.max_rel,
            "outside_contract": rep.strict_violations, "explained_by_fp64": rep.explained_by_fp32,
            "unexplained": rep.unexplained, "verdict_mismatches": int(((g_min >= 0) != (r_min >= 0)).sum()),
-           "near_ties": int((r_min.abs() < 1e-4).sum())}
+           "near_ties": int((r_min.abs() < 1e-4).sum()), "sample": f"the whole batch ({w.batch} inputs)"}
     if name == "C5":
-        out["status_mismatches"] = int(((got["status"].cpu() == 1) != ref["certified"]).sum())
+        ref_cert = r_min >= 0.0 - 1e-6
+        hip_cert = got["status"].cpu() == 1
+        out["certified"] = {"hip": int(hip_cert.sum()), "reference": int(ref_cert.sum()), "of": w.batch}
+        out["status_mismatches"] = int((hip_cert != ref_cert).sum()) + int((got["status"].cpu() == 2).sum())
         names = got["relu_names"]
         layer, neuron = got["branch_layer"].cpu().tolist(), got["branch_neuron"].cpu().tolist()
         hip_branch = [None if l < 0 else (names[l], n) for l, n in zip(layer, neuron)]
-        out["branch_mismatches"] = sum(bool(ref["feasible"][i]) and hip_branch[i] != ref["branch"][i]
-                                       for i in range(len(hip_branch)))
+        out["branch_mismatches"] = sum(hip_branch[i] != ref[3][i] for i in range(len(hip_branch)))
+        out["sample"] = f"all {w.batch} domains"
     return out
 
 
 def cpu_baseline(name: str, w, seconds: float):
-    """Time the CPU oracle (PyTorch CPU restatement of the reference path) on a
-    bounded sample of the same workload; returns throughput in the metric unit."""
+    """Time the CPU oracle (PyTorch CPU restatement of the reference path) on the
+    whole workload, repeated while less than ``seconds`` have elapsed; returns the
+    throughput in the metric unit and the parity of the HIP result against the
+    first run."""
     import torch
-    from boundflow_amd import workloads as wl
 
     threads = torch.get_num_threads()
     done_units = 0
     elapsed = 0.0
     rounds = 0
-    sample_b = {"C1": 16, "C2": 4, "C3": 16, "C4": 2, "C5": 64, "D1": 16}[name]
     first = None
-    while elapsed < seconds and rounds < 4096:
-        sub = wl.subset(w, sample_b)
+    while rounds == 0 or elapsed < seconds:
         t0 = time.perf_counter()
-        res = _oracle_run(name, sub)
-        done_units += sub.batch if name == "C5" else sub.batch * sub.num_specs
+        res = _oracle_run(name, w)
         elapsed += time.perf_counter() - t0
+        done_units += w.batch if name == "C5" else w.batch * w.num_specs
         rounds += 1
         if first is None:
-            first = (sub, res)
+            first = res
+    what = "node-batch alpha-beta evaluations" if name == "C5" else "queries"
     return {
         "value": done_units / elapsed,
         "cores": threads,
         "kind": "port",
-        "sample": f"{rounds} x {sample_b}-input subsets of {name} ({done_units} units, {elapsed:.1f} s), "
-                  f"PyTorch CPU fp32 restatement of the reference path, {threads} threads on {cpu_model()}",
-        "parity": parity_summary(name, *first),
+        "sample": f"{rounds} full-batch {what} of {name} ({done_units} units, {elapsed:.1f} s), PyTorch CPU fp32 "
+                  f"restatement of the reference path, {threads} threads on {cpu_model()}",
+        "parity": parity_summary(name, w, first),
     }
+
+
+def measure(name: str, steps: int, warmup: int, no_graph: bool):
+    """One configuration: throughput of ``steps`` timed steps after ``warmup``, the
+    per-kernel durations of the library's launches and the dominant kernel's
+    roofline position.  Returns (record, workload, unit)."""
+    import torch
+    from boundflow_amd import profiling
+
+    w, step, units, unit, desc = build_case(name)
+    # Every configuration's query is free of host synchronization, so one query is
+    # captured as a HIP graph and every timed step replays it (all kernels rerun on
+    # the same inputs; C2: the IBP trace, five CROWN refinements of 128 000 rows and
+    # the final bound; C4: the forward trace, the alpha initialisation and 20 Adam
+    # steps; C5: the batch's forward trace, 10 alpha-beta steps and the
+    # certification).  Python issue of the eager launches leaves the device idle
+    # between them (C2: about 6 % of a step).
+    use_graph = not no_graph
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = profiling.LaunchTimer()
+    if use_graph:
+        from boundflow_amd import graphs
+        replay = graphs.CapturedQuery(step)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            replay()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        del replay
+        # Per-kernel durations (the same in eager launches) for the roofline, in a
+        # separate pass after one untimed eager query (the first eager query after
+        # the graph replays runs slow), with the garbage collector off: each timed
+        # launch is preceded by a 0.2 ms spin so that its events bracket execution,
+        # not the host's launch latency.
+        step()
+        timer = profiling.LaunchTimer(spin_cycles=profiling.spin_cycles(0.2))
+        gc.disable()
+        try:
+            with profiling.timing(timer):
+                for _ in range(steps):
+                    step()
+            torch.cuda.synchronize()
+        finally:
+            gc.enable()
+    else:
+        with profiling.timing(timer):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+    sec = t1 - t0
+    kernels = timer.summary()
+    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms"]) if kernels else (None, None)
+    roofline = None
+    if dom is not None:
+        traffic, source = MEASURED_TRAFFIC.get((name, dom_name), (None, None))
+        common = {"kernel": dom_name, "traffic": traffic, "traffic_source": source,
+                  "algorithmic_bytes_per_launch": round(dom["bytes"] / max(1, dom["launches"])),
+                  "avg_launch_ms": round(dom["avg_ms"], 4), "launches": int(dom["launches"]),
+                  "share_of_step": round(dom["ms"] / 1e3 / sec, 4),
+                  "timing": "eager launches" if use_graph else "timed steps"}
+        if dom["flops"] > 0:
+            roofline = {"bound": "mfma", "achieved": round(dom["tflops"], 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4), **common}
+        else:
+            roofline = {"bound": "hbm", "achieved": round(dom["gbps"], 1), "peak": PEAK_HBM_GBPS,
+                        "unit": "GB/s", "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), **common}
+    config = {"workload": desc, "units_per_step": units, "parallelism": "single GPU",
+              "launch": "hip_graph replay" if use_graph else "eager"}
+    if name == "C2":
+        config["intermediate_bounds_per_step"] = intermediate_bounds(w)
+    record = {"value": round(units * steps / sec, 2), "unit": unit, "steps": steps,
+              "ms_per_step": round(sec / steps * 1e3, 4), "config": config, "roofline": roofline,
+              "kernels": {k: {"launches": int(v["launches"]), "avg_ms": round(v["avg_ms"], 4),
+                              "tflops": round(v["tflops"], 3), "gbps": round(v["gbps"], 1)}
+                          for k, v in kernels.items()}}
+    return record, w, unit
 
 
 def main() -> int:
@@ -226,6 +334,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     ap.add_argument("--no-graph", action="store_true", help="issue every launch from Python (no HIP graph replay)")
+    ap.add_argument("--no-secondary", action="store_true", help="C2 alone, without the C5 domains/s record")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -249,91 +358,38 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}), flush=True)
         return 0
-    w, step, units, unit, desc = build_case(args.config)
-    # Queries without host synchronization (C1, C3, C4, C5) are captured once as a
-    # HIP graph and every timed step replays the whole query (all kernels rerun on
-    # the same inputs; for C4 the forward trace, the alpha initialisation and all
-    # 20 Adam steps; for C5 the batch's forward trace, 10 alpha-beta steps and the
-    # certification).  C1, C3 and C4 are launch-bound at these batch sizes; C5
-    # leaves the device idle between launches for about 7 % of an eager batch.
-    use_graph = args.config in ("C1", "C3", "C4", "C5", "D1") and not args.no_graph
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    timer = profiling.LaunchTimer()
-    if use_graph:
-        from boundflow_amd import graphs
-        replay = graphs.CapturedQuery(step)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            replay()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        # Per-kernel durations (the same in eager launches) for the roofline, in a
-        # separate pass after one untimed eager query (the first eager query after
-        # the graph replays runs slow), with the garbage collector off: each timed
-        # launch is preceded by a 0.2 ms spin so that its events bracket execution,
-        # not the host's launch latency.
-        step()
-        timer = profiling.LaunchTimer(spin_cycles=profiling.spin_cycles(0.2))
-        # a garbage-collection pause between a start event and its launch would outlast the spin
-        gc.disable()
-        try:
-            with profiling.timing(timer):
-                for _ in range(args.steps):
-                    step()
-            torch.cuda.synchronize()
-        finally:
-            gc.enable()
-    else:
-        with profiling.timing(timer):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                step()
-            torch.cuda.synchronize()
-            t1 = time.perf_counter()
-    sec = t1 - t0
-    kernels = timer.summary()
-    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms"]) if kernels else (None, None)
-    roofline = None
-    if dom is not None:
-        traffic, source = MEASURED_TRAFFIC.get((args.config, dom_name), (None, None))
-        common = {"kernel": dom_name, "traffic": traffic, "traffic_source": source,
-                  "algorithmic_bytes_per_launch": round(dom["bytes"] / max(1, dom["launches"])),
-                  "avg_launch_ms": round(dom["avg_ms"], 4), "launches": int(dom["launches"]),
-                  "share_of_step": round(dom["ms"] / 1e3 / sec, 4),
-                  "timing": "eager launches" if use_graph else "timed steps"}
-        if dom["flops"] > 0:
-            roofline = {"bound": "mfma", "achieved": round(dom["tflops"], 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-                        "unit": "TFLOP/s", "frac": round(dom["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4), **common}
-        else:
-            roofline = {"bound": "hbm", "achieved": round(dom["gbps"], 1), "peak": PEAK_HBM_GBPS,
-                        "unit": "GB/s", "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), **common}
+    head, w, unit = measure(args.config, args.steps, args.warmup, args.no_graph)
     line = {
         "metric": "CROWN bounds/sec & BaB domains/sec on 1 GPU; % of HBM / fp32-MFMA roofline",
-        "value": round(units * args.steps / sec, 2),
+        "value": head["value"],
         "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(sec / args.steps * 1e3, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded Kaiming weights, uniform inputs)",
-        "config": {"workload": desc, "units_per_step": units, "parallelism": "single GPU",
-                   "launch": "hip_graph replay" if use_graph else "eager",
-                   **({"intermediate_bounds_per_step": intermediate_bounds(w)} if args.config == "C2" else {})},
-        "roofline": roofline,
-        "kernels": {k: {"launches": int(v["launches"]), "avg_ms": round(v["avg_ms"], 4),
-                        "tflops": round(v["tflops"], 3), "gbps": round(v["gbps"], 1)} for k, v in kernels.items()},
+        "config": head["config"],
+        "roofline": head["roofline"],
+        "kernels": head["kernels"],
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.config, w, args.cpu_seconds)
         line["cpu_baseline"]["unit"] = unit
+    # the metric's second half: BaB domains/s on the C5 domain batch, measured in the same run
+    if args.config == "C2" and not args.no_secondary:
+        del w
+        gc.collect()
+        torch.cuda.empty_cache()
+        sec_rec, w5, unit5 = measure("C5", args.steps, args.warmup, args.no_graph)
+        sec_rec = {"metric": "BaB domains/sec (beta-CROWN domain batch)", **sec_rec}
+        if not args.no_cpu:
+            sec_rec["cpu_baseline"] = cpu_baseline("C5", w5, args.cpu_seconds)
+            sec_rec["cpu_baseline"]["unit"] = unit5
+        line["secondary"] = [sec_rec]
     print(json.dumps(line), flush=True)
     return 0
 
