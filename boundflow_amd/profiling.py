@@ -162,13 +162,93 @@ def summarize_pmc(csv_path: str, top: int = 12) -> str:
     return "\n".join(out)
 
 
+def _agent_shape(agent_csv: Optional[str]) -> Tuple[int, int]:
+    """(XCDs, SIMDs) of the GPU agent in a rocprofv3 ``*_agent_info.csv``; MI355X's
+    (8, 1024) when no file is given."""
+    import csv
+    import os
+
+    if agent_csv and os.path.isfile(agent_csv):
+        with open(agent_csv, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Agent_Type") == "GPU":
+                    return int(row["Num_Xcc"]), int(row["Simd_Count"])
+    return 8, 1024
+
+
+def summarize_mfma(csv_path: str, agent_csv: Optional[str] = None, top: int = 12, clock_ghz: float = 2.4) -> str:
+    """Per-kernel MFMA and LDS figures from a rocprofv3 ``--pmc`` run, as a Markdown
+    table.  Counters are summed over the device for each dispatch and averaged over
+    dispatches.  GRBM_GUI_ACTIVE counts active cycles on every XCD, so a dispatch
+    lasts GRBM_GUI_ACTIVE / XCDs cycles; the MFMA pipe's busy share is
+    SQ_VALU_MFMA_BUSY_CYCLES / (those cycles x SIMDs); fp32 MFMA flops are
+    SQ_INSTS_VALU_MFMA_MOPS_F32 x 512, their rate uses ``clock_ghz``.  LDS bank
+    conflicts are given as a share of SQ_LDS_IDX_ACTIVE cycles.  Columns whose
+    counters the run did not collect are left empty."""
+    import csv
+    import os
+    from collections import OrderedDict
+
+    if not os.path.isfile(csv_path):
+        raise FileNotFoundError(f"no rocprofv3 counter file at {csv_path}")
+    xcds, simds = _agent_shape(agent_csv)
+    per: "OrderedDict[str, Dict[str, float]]" = OrderedDict()
+    kname: Dict[str, str] = {}
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            d = row["Dispatch_Id"]
+            per.setdefault(d, defaultdict(float))[row["Counter_Name"]] += float(row["Counter_Value"])
+            kname[d] = row["Kernel_Name"]
+    by_kernel: Dict[str, List[Dict[str, float]]] = defaultdict(list)
+    for d, ctrs in per.items():
+        by_kernel[kname[d]].append(ctrs)
+
+    def avg(lst, key):
+        vals = [c[key] for c in lst if key in c]
+        return sum(vals) / len(vals) if vals else None
+
+    rows = []
+    for name, lst in by_kernel.items():
+        gui = avg(lst, "GRBM_GUI_ACTIVE")
+        cyc = gui / xcds if gui else None
+        busy = avg(lst, "SQ_VALU_MFMA_BUSY_CYCLES")
+        mops = avg(lst, "SQ_INSTS_VALU_MFMA_MOPS_F32")
+        mfma = avg(lst, "SQ_INSTS_VALU_MFMA_F32") or avg(lst, "SQ_INSTS_MFMA")
+        valu = avg(lst, "SQ_INSTS_VALU")
+        lds_i = avg(lst, "SQ_INSTS_LDS")
+        bank = avg(lst, "SQ_LDS_BANK_CONFLICT")
+        lds_act = avg(lst, "SQ_LDS_IDX_ACTIVE")
+        rows.append((cyc or 0.0, name, len(lst), cyc,
+                     None if not (busy and cyc) else 100.0 * busy / (cyc * simds),
+                     None if not (mops and cyc) else mops * 512.0 / (cyc / (clock_ghz * 1e9)) / 1e12,
+                     None if not (valu and mfma) else (valu - mfma) / mfma,
+                     None if not (lds_i and mfma) else lds_i / mfma,
+                     None if not (bank and lds_act) else 100.0 * bank / lds_act))
+    rows.sort(key=lambda r: -r[0] * r[2])
+
+    def f(v, fmt):
+        return "" if v is None else format(v, fmt)
+
+    out = ["| kernel | dispatches | cycles per dispatch | MFMA busy | fp32 MFMA TFLOP/s | non-MFMA VALU per MFMA "
+           "| LDS instructions per MFMA | LDS bank-conflict share of LDS-active cycles |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for _w, name, n, cyc, busy, tf, valu_r, lds_r, bank_r in rows[:top]:
+        out.append(f"| `{name[:110]}` | {n} | {f(cyc, '.0f')} | {f(busy, '.1f')}{'%' if busy is not None else ''} | "
+                   f"{f(tf, '.1f')} | {f(valu_r, '.2f')} | {f(lds_r, '.2f')} | "
+                   f"{f(bank_r, '.1f')}{'%' if bank_r is not None else ''} |")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
     import sys
 
     if len(sys.argv) == 3 and sys.argv[1] == "--pmc":
         print(summarize_pmc(sys.argv[2]))
+    elif len(sys.argv) in (3, 4) and sys.argv[1] == "--mfma":
+        print(summarize_mfma(sys.argv[2], sys.argv[3] if len(sys.argv) == 4 else None))
     elif len(sys.argv) == 2 and not sys.argv[1].startswith("-"):
         print(summarize_rocpd(sys.argv[1]))
     else:
         raise SystemExit("usage: python -m boundflow_amd.profiling <rocprofv3 *_results.db>\n"
-                         "       python -m boundflow_amd.profiling --pmc <rocprofv3 *_counter_collection.csv>")
+                         "       python -m boundflow_amd.profiling --pmc <rocprofv3 *_counter_collection.csv>\n"
+                         "       python -m boundflow_amd.profiling --mfma <*_counter_collection.csv> [<*_agent_info.csv>]")
