@@ -312,6 +312,34 @@ def golden_shared_alpha(tag):
     save(tag, **arrays)
 
 
+from tests.frontend_models import VNNLIB_SOURCES, frontend_nets, planned_module_json, vnnlib_c1_property  # noqa: E402,E501
+
+
+def golden_frontend(tag):
+    """import_torch (frontends/pytorch/frontend.py:21-80) + plan_interval_ibp_v0
+    (planner/interval_v0.py:10-76) of the frontend nets: the planned modules' fields."""
+    from boundflow.frontends.pytorch.frontend import import_torch as r_import_torch
+    from boundflow.planner import plan_interval_ibp_v0 as r_plan
+    arrays = {}
+    for name, (net, x) in frontend_nets().items():
+        tm = r_plan(r_import_torch(net, (x,), export_mode="export", normalize=True))
+        arrays[name] = np.array(planned_module_json(tm))
+    save(tag, **arrays)
+
+
+def golden_vnnlib(tag):
+    """parse_vnnlib_box_query (frontends/vnnlib.py) of the VNNLIB sources: the query IR as a dict and its hash."""
+    import json
+    from boundflow.frontends.vnnlib import parse_vnnlib_box_query as r_parse
+    arrays = {}
+    sources = dict(VNNLIB_SOURCES)
+    sources["c1_property0"] = vnnlib_c1_property(0)
+    for name, text in sources.items():
+        q = r_parse(text, query_id=f"{name}:0")
+        arrays[name] = np.array(json.dumps({"dict": q.to_dict(), "stable_hash": q.stable_hash()}, sort_keys=True))
+    save(tag, **arrays)
+
+
 GOLDENS = [
     ("crown_c1", lambda t: golden_crown(wl.make_c1(), t, pre_rows=8)),
     ("crown_c3_b16", lambda t: golden_crown(wl.subset(wl.make_c3(), 16), t, pre_rows=2)),
@@ -336,6 +364,8 @@ GOLDENS = [
     ("bab_solve_cert_fallback", golden_bab_solve),
     ("bab_solve_cert_prune", golden_bab_solve),
     ("bab_solve_1d", golden_bab_solve),
+    ("frontend_planned", golden_frontend),
+    ("vnnlib_queries", golden_vnnlib),
 ]
 
 
