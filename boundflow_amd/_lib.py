@@ -60,6 +60,10 @@ SIGNATURES = {
     "bf_spec_linear": (I32, [P, P, P, I64, I64, I64, P, P, P]),
     "bf_ibp_batched_linear": (I32, [P, P, I64, I64, P, P, I64, P, P, P]),
     "bf_branch_update": (I32, [P, P, I64, I64, I32, P, P, P, P]),
+    "bf_alpha_adaptive": (I32, [P, P, I64, P, P]),
+    "bf_objective_step": (I32, [P, P, I64, I64, I32, I32, F32, F32, F32, F32, P, P, P, P, P, P, P, I32, P]),
+    "bf_scale_rows": (I32, [P, I64, I64, P, P]),
+    "bf_branch_update_native": (I32, [P, P, P, I64, I64, I64, I32, P, P, P, P, P, P]),
     "bf_split_certificate": (I32, [P, I64, P, P, I64, P, I64, P, I64, F32, I64, I64, I64, I32, F64, F64, P, P]),
     "bf_adam_clamp_step": (I32, [P, P, P, P, I64, F64, F64, F64, F32, I32, F32, F32, I32, P]),
     "bf_adam_clamp_multi": (I32, [I32, P, P, P, P, P, P, P, P, F64, F64, F64, F32, I32, P]),

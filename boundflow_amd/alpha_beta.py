@@ -268,6 +268,9 @@ def run_alpha_beta_crown_mlp(
     raise_on_infeasible: bool = True,
     use_beta: bool = True,
     first_layer_certificate: bool = True,
+    soft_tau: float = 1.0,
+    lb_weight: float = 1.0,
+    ub_weight: float = 1.0,
 ):
     """HIP counterpart of run_alpha_beta_crown_mlp (alpha_beta_crown.py:643-941).
 
@@ -281,8 +284,12 @@ def run_alpha_beta_crown_mlp(
     empty and ``stats.feasibility`` is "infeasible", as in the reference.  That
     check reads its verdict back to the host; callers that decide it
     themselves (the BaB rounds) pass ``first_layer_certificate=False``."""
-    if objective != "lower" or spec_reduce != "mean":
-        raise NotImplementedError("HIP alpha-beta CROWN implements objective='lower', spec_reduce='mean'")
+    if objective not in _OBJECTIVES:
+        raise AssertionError(f"unreachable objective: {objective}")
+    if spec_reduce not in _REDUCTIONS:
+        raise AssertionError(f"unreachable spec_reduce: {spec_reduce}")
+    if spec_reduce == "softmin" and float(soft_tau) <= 0.0:
+        raise ValueError(f"soft_tau must be >0, got {soft_tau}")
     spec = normalize_input_spec(input_spec)
     chain = _chain_or_none(module, spec)
     if (first_layer_certificate and relu_split_state and int(spec.center.shape[0]) == 1
@@ -337,6 +344,17 @@ def run_alpha_beta_crown_mlp(
     b_layer, b_neuron, _gap = branch_tensors(trace, B) if trace.relu_pre else (None, None, None)
     S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else out_dim
     M = B * S
+    if objective != "lower" or spec_reduce != "mean":
+        best_lb, best_ub, best_alpha, best_beta = _optimise_general(
+            module, spec, trace, chain, linear_spec_C, bound, grad, out_dim, B=B, S=S, names=names, numel=numel,
+            alpha=alpha, beta=beta, p_ld=p_ld, splits=splits, beta_names=beta_names if objective == "lower" else [],
+            steps=int(steps), lr=float(lr), objective=objective, spec_reduce=spec_reduce, soft_tau=float(soft_tau),
+            lb_weight=float(lb_weight), ub_weight=float(ub_weight), per_batch_params=per_batch_params)
+        out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
+        out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
+        stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,
+                               branch_neuron=b_neuron, relu_names=tuple(trace.relu_pre.keys()))
+        return IntervalState(lower=best_lb, upper=best_ub), out_alpha, out_beta, stats
     # d(-sum_d mean_s lb)/dlb = -1/S ; d(-mean_d mean_s lb)/dlb = (-1/B)/S   (fp32, as autograd divides)
     g_row = np.float32(-1.0) / np.float32(S) if per_batch_params else (np.float32(-1.0) / np.float32(B)) / np.float32(S)
     G = torch.full((M,), float(g_row), device=dev, dtype=torch.float32)
@@ -397,6 +415,118 @@ def run_alpha_beta_crown_mlp(
     stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,
                            branch_neuron=b_neuron, relu_names=tuple(trace.relu_pre.keys()))
     return IntervalState(lower=best_lb, upper=best_ub), out_alpha, out_beta, stats
+
+
+_OBJECTIVES = {"lower": 0, "upper": 1, "gap": 2, "both": 3}
+_REDUCTIONS = {"mean": 0, "min": 1, "softmin": 2}
+
+
+def _optimise_general(module, spec, trace, chain, linear_spec_C, bound, grad, out_dim, *, B, S, names, numel,
+                      alpha, beta, p_ld, splits, beta_names, steps, lr, objective, spec_reduce, soft_tau, lb_weight,
+                      ub_weight, per_batch_params):
+    """The optimisation loop for every objective and spec reduction but ("lower",
+    "mean") (alpha_beta_crown.py:756-815).  The upper bound of C is computed as
+    minus the lower bound of -C, the same arithmetic with every term negated
+    (exactly), so one lower-bound pass and its reverse pass serve both bounds.
+    Per step ``bf_objective_step`` reduces the bounds to each domain's metric,
+    gives the loss's row gradients and updates the best-of state; the
+    concretization seeds are formed with unit row weights and scaled by the row
+    gradients after the pass (the same products, rounded once).  Objectives other
+    than "lower" leave the split multipliers out of the bound (and unchanged).
+    Returns (best lower, best upper, best alpha, best beta)."""
+    dev = spec.center.device
+    stream = _lib.stream_handle()
+    M = B * S
+    obj = _OBJECTIVES[objective]
+    use_l = objective in ("lower", "gap", "both")
+    use_u = objective in ("upper", "gap", "both")
+    C = linear_spec_C
+    if C is None:
+        C = torch.eye(out_dim, device=dev).unsqueeze(0).expand(B, out_dim, out_dim)
+    C_neg = (-C).contiguous()
+    bound_u, grad_u, _ = _evaluator(module, spec, trace, chain, C_neg)
+    ones = torch.ones(M, device=dev)
+    g_scale = float(np.float32(-1.0)) if per_batch_params else float(np.float32(-1.0) / np.float32(B))
+    G_l = torch.empty(M, device=dev) if use_l else None
+    G_nu = torch.empty(M, device=dev) if use_u else None
+    metric = torch.empty(B, device=dev)
+    best_metric = torch.empty(B, device=dev)
+    best_lb = torch.empty(B, S, device=dev)
+    best_ub = torch.empty(B, S, device=dev)
+    improved = torch.empty(B, dtype=torch.int32, device=dev)
+    best_scalar = None
+    adam = _AdamGroup([alpha[n] for n in names] + [beta[n] for n in beta_names],
+                      [(0.0, 1.0)] * len(names) + [(0.0, None)] * len(beta_names))
+    best_alpha = {n: alpha[n].clone() for n in names}
+    best_beta = {n: beta[n].clone() for n in names}
+    add = {n: torch.empty(B, numel[n], device=dev) for n in beta_names}
+    beta_args = (_lib.ptr_array([beta[n] for n in beta_names]), _lib.i64_array([p_ld[n] for n in beta_names]),
+                 _lib.ptr_array([splits[n][0] for n in beta_names]), _lib.i64_array([splits[n][1] for n in beta_names]),
+                 _lib.i64_array([numel[n] for n in beta_names]), B, _lib.ptr_array([add[n] for n in beta_names]))
+    copy_dst = [best_alpha[n] for n in names] + [best_beta[n] for n in beta_names]
+    copy_args = (_lib.ptr_array(copy_dst), _lib.ptr_array([alpha[n] for n in names] + [beta[n] for n in beta_names]),
+                 _lib.i64_array([numel[n] for n in names] + [numel[n] for n in beta_names]), B, _lib.ptr(improved))
+    memo_l: dict = {}
+    memo_u: dict = {}
+    for step in range(steps + 1):
+        last = step == steps
+        if beta_names:
+            _lib.call("bf_beta_coeff_multi", len(beta_names), *beta_args, stream)
+        cur = {n: alpha[n] for n in names}
+        saved_l = {"grad_rows": ones, "memo": memo_l} if (use_l and not last) else None
+        saved_u = {"grad_rows": ones, "memo": memo_u} if (use_u and not last) else None
+        lb = bound(cur, {n: add[n] for n in beta_names}, False, True, saved_l).lower if use_l else None
+        nub = bound_u(cur, None, False, True, saved_u).lower if use_u else None
+        if per_batch_params:
+            _lib.call("bf_objective_step", _lib.ptr(lb), _lib.ptr(nub), B, S, obj, _REDUCTIONS[spec_reduce], soft_tau,
+                      lb_weight, ub_weight, g_scale, _lib.ptr(metric), _lib.ptr(G_l), _lib.ptr(G_nu),
+                      _lib.ptr(best_metric), _lib.ptr(best_lb if use_l else None),
+                      _lib.ptr(best_ub if use_u else None), _lib.ptr(improved), 1 if step == 0 else 0, stream)
+            _lib.call("bf_masked_copy_rows_multi", len(copy_dst), *copy_args, stream)
+        else:
+            _lib.call("bf_objective_step", _lib.ptr(lb), _lib.ptr(nub), B, S, obj, _REDUCTIONS[spec_reduce], soft_tau,
+                      lb_weight, ub_weight, g_scale, _lib.ptr(metric), _lib.ptr(G_l), _lib.ptr(G_nu), None, None,
+                      None, None, 0, stream)
+            value = float(metric.mean().item())   # the reference compares metric_b.mean() as a Python float
+            if best_scalar is None or value > best_scalar:
+                best_scalar = value
+                if use_l:
+                    best_lb.copy_(lb)
+                if use_u:
+                    torch.neg(nub, out=best_ub)
+                for n in names:
+                    best_alpha[n].copy_(alpha[n])
+                    best_beta[n].copy_(beta[n])
+        if last:
+            break
+        a_arg = {n: (alpha[n], p_ld[n]) for n in names}
+        g_alpha: Dict[str, torch.Tensor] = {}
+        g_beta: Dict[str, torch.Tensor] = {}
+        for saved, gfun, Grow in ((saved_l, grad, G_l), (saved_u, grad_u, G_nu)):
+            if saved is None:
+                continue
+            if "h" in saved:
+                h = saved["h"]
+                _lib.call("bf_scale_rows", _lib.ptr(h), M, int(h.numel() // M), _lib.ptr(Grow), stream)
+            ga, gb = gfun(saved, B, S, a_arg, splits, Grow)
+            for n in names:
+                g_alpha[n] = ga[n] if n not in g_alpha else g_alpha[n] + ga[n]
+                if n in beta_names:
+                    g_beta[n] = gb[n] if n not in g_beta else g_beta[n] + gb[n]
+        if not per_batch_params:
+            for d in (g_alpha, g_beta):
+                for n in list(d.keys()):
+                    r = torch.empty(numel[n], device=dev)
+                    _lib.call("bf_sum_rows", _lib.ptr(d[n]), B, numel[n], _lib.ptr(r), stream)
+                    d[n] = r
+        adam.step([g_alpha[n] for n in names] + [g_beta[n] for n in beta_names], lr, stream)
+    # the bound the objective did not follow, at the best parameters (domains are
+    # independent and, outside the "lower" objective, the multipliers do not enter it)
+    if not use_l:
+        best_lb = bound({n: best_alpha[n] for n in names}, None, False, True, None).lower
+    if not use_u:
+        best_ub = bound({n: best_alpha[n] for n in names}, None, True, False, None).upper
+    return best_lb, best_ub, best_alpha, best_beta
 
 
 def run_alpha_crown_mlp(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.2,

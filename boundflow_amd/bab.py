@@ -16,6 +16,7 @@ does not disturb the others.
 from __future__ import annotations
 
 import heapq
+import math
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
@@ -466,3 +467,245 @@ def _restrict_1d_linf(module, spec: InputSpec, split: Dict[str, torch.Tensor]) -
             return None
     center = torch.tensor([[0.5 * (lo + hi)]], device=spec.center.device, dtype=spec.center.dtype)
     return InputSpec.linf(value_name=spec.value_name, center=center, eps=float(0.5 * (hi - lo)))
+
+
+# ---------------------------------------------------------------------------
+# The native ReLU-split queue (boundflow/runtime/native_relu_split_bab_runtime.py:592-789)
+
+
+@dataclass(frozen=True)
+class NativeReluSplitBabConfig:
+    """Queue and node-batching policy, field for field as the reference's
+    (native_relu_split_bab_runtime.py:61-97)."""
+
+    max_nodes: int
+    max_depth: int
+    expansion_batch_size: int
+    max_eval_batch_size: int
+    threshold: float = 0.0
+    available_memory_bytes: int = 1 << 30
+    memory_budget_bytes: int = 1 << 30
+
+    def validate(self) -> None:
+        if (self.max_nodes < 1 or self.max_depth < 0 or self.expansion_batch_size < 1
+                or self.max_eval_batch_size < 1 or self.available_memory_bytes < 1 or self.memory_budget_bytes < 1
+                or self.memory_budget_bytes > self.available_memory_bytes):
+            raise ValueError("native ReLU-split BaB config is invalid")
+        if not torch.isfinite(torch.tensor(self.threshold)):
+            raise ValueError("native ReLU-split BaB threshold must be finite")
+
+
+@dataclass(frozen=True)
+class ReluSplitBranch:
+    relu_input: str
+    neuron_index: int
+    lower: float
+    upper: float
+    width: float
+
+
+@dataclass(frozen=True)
+class NativeReluSplitBabEvaluation:
+    node_id: str
+    parent_node_id: Optional[str]
+    depth: int
+    branch_relu_input: Optional[str]
+    branch_neuron_index: Optional[int]
+    branch_value: int
+    lower: float
+    upper: float
+    priority: float
+    eval_batch_id: str
+    eval_batch_position: int
+    branch_candidate: Optional[ReluSplitBranch]
+
+
+@dataclass(frozen=True)
+class NativeReluSplitBabDecision:
+    decision_index: int
+    node_id: str
+    kind: str                       # "prune" | "expand" | "terminal"
+    reason: str
+    child_node_ids: Tuple[str, ...] = ()
+    branch_candidate: Optional[ReluSplitBranch] = None
+
+
+@dataclass(frozen=True)
+class NativeReluSplitBabTrace:
+    run_id: str
+    status: str                     # "complete" | "budget_exhausted"
+    termination_reason: str
+    config: NativeReluSplitBabConfig
+    evaluations: Tuple[NativeReluSplitBabEvaluation, ...]
+    decisions: Tuple[NativeReluSplitBabDecision, ...]
+    final_frontier_node_ids: Tuple[str, ...]
+    native_stack_count: int
+    max_queue_size: int
+
+
+def native_priority(lower: float) -> float:
+    """The queue key of a node (native_relu_split_bab_runtime.py:1128-1131): its lower
+    bound to 7 significant digits, so near-equal bounds fall back to creation order."""
+    if not math.isfinite(lower):
+        raise ValueError("native ReLU-split queue bound must be finite")
+    return float(f"{lower:.7g}")
+
+
+def run_native_relu_split_bab(module, input_spec, *, linear_spec_C: torch.Tensor, run_id: str,
+                              config: NativeReluSplitBabConfig) -> NativeReluSplitBabTrace:
+    """HIP counterpart of run_native_relu_split_bab (native_relu_split_bab_runtime.py:592-789):
+    a bounded best-first queue over one box input and one scalar objective.
+
+    Node bound: CROWN with the ADAPTIVE lower slope (``bf_alpha_adaptive``) over
+    the node's IBP trace with its splits applied, on the box repeated per node,
+    in batches of at most ``max_eval_batch_size`` nodes (the root, then each
+    round's children).  Branch: the widest unsplit ambiguous neuron, width in
+    double, ties to the first ReLU name in sorted order then the lowest index
+    (``bf_branch_update_native``).  A round pops up to ``expansion_batch_size``
+    queue entries (priority, serial, node id) and prunes (lower >= threshold),
+    stops at the depth limit or without a branch, stops the search when two more
+    nodes would pass ``max_nodes`` (the round's remaining entries return to the
+    queue), or expands into the inactive then active child.  Split vectors stay
+    on the device; each evaluated batch returns its bounds and branches in one
+    transfer.  An infeasible split raises ValueError, as in the reference."""
+    if not run_id:
+        raise ValueError("native ReLU-split BaB run ID must be non-empty")
+    config.validate()
+    module.validate()
+    spec = normalize_input_spec(input_spec)
+    if not isinstance(spec.perturbation, BoxPerturbation):
+        raise NotImplementedError("native ReLU-split BaB v1 requires a box input")
+    lo0, hi0 = spec.perturbation.lower, spec.perturbation.upper
+    if int(lo0.shape[0]) != 1:
+        raise ValueError("native ReLU-split BaB v1 requires one root domain")
+    C = linear_spec_C.detach()
+    if C.dim() == 3:
+        if int(C.shape[0]) != 1:
+            raise ValueError("native ReLU-split objective batch must be one")
+        C = C[0]
+    if C.dim() != 2 or int(C.shape[0]) != 1:
+        raise ValueError("native ReLU-split v1 requires one scalar objective")
+    chain, relu_shapes, _has_conv = _relu_layout(module, spec)
+    names = sorted(relu_shapes)
+    if not names:
+        raise ValueError("native ReLU-split BaB requires at least one ReLU")
+    sizes = {n: int(torch.tensor(relu_shapes[n]).prod()) for n in names}
+    dev = spec.center.device
+    front = _Frontier(sizes, dev, capacity=max(64, 2 * int(config.max_eval_batch_size)))
+    stream = _lib.stream_handle()
+    meta: Dict[str, dict] = {}       # node id -> lineage, slot, results
+    evaluations: List[NativeReluSplitBabEvaluation] = []
+    decisions: List[NativeReluSplitBabDecision] = []
+    counters = {"batches": 0, "next": 1}
+
+    def evaluate(node_ids: List[str]) -> None:
+        for start in range(0, len(node_ids), int(config.max_eval_batch_size)):
+            chunk = node_ids[start:start + int(config.max_eval_batch_size)]
+            k = len(chunk)
+            batch_id = f"{run_id}:eval:{counters['batches']:04d}"
+            counters["batches"] += 1
+            sl = torch.tensor([meta[n]["slot"] for n in chunk], device=dev, dtype=torch.long)
+            split_by = {n: front.split[n][sl].reshape((k,) + tuple(relu_shapes[n])) for n in names}
+            rep = (k,) + (1,) * (lo0.dim() - 1)
+            bspec = InputSpec.box(value_name=spec.value_name, lower=lo0.repeat(rep), upper=hi0.repeat(rep))
+            trace = forward_ibp_trace(module, bspec, relu_split_state=split_by, chain=chain)
+            alpha = {}
+            for n, pre in trace.relu_pre.items():
+                a = torch.empty_like(pre.lower)
+                _lib.call("bf_alpha_adaptive", _lib.ptr(pre.lower), _lib.ptr(pre.upper), pre.lower.numel(),
+                          _lib.ptr(a), stream)
+                alpha[n] = a
+            Ck = C.unsqueeze(0).expand(k, -1, -1).contiguous()
+            if chain is not None:
+                from .crown import crown_backward
+                bounds = crown_backward(module, bspec, trace, chain=chain, linear_spec_C=Ck, relu_alpha=alpha)
+            else:
+                from .crown_dag import crown_backward_dag
+                bounds = crown_backward_dag(module, bspec, trace, linear_spec_C=Ck, relu_alpha=alpha)
+            width = torch.full((k,), -1.0, device=dev, dtype=torch.float64)
+            layer = torch.full((k,), -1, device=dev, dtype=torch.int32)
+            idx = torch.zeros(k, device=dev, dtype=torch.int32)
+            blo = torch.zeros(k, device=dev)
+            bhi = torch.zeros(k, device=dev)
+            for li, n in enumerate(names):
+                pre = trace.relu_pre[n]
+                _lib.call("bf_branch_update_native", _lib.ptr(pre.lower.reshape(k, sizes[n])),
+                          _lib.ptr(pre.upper.reshape(k, sizes[n])), _lib.ptr(split_by[n].reshape(k, sizes[n])),
+                          sizes[n], k, sizes[n], li, _lib.ptr(width), _lib.ptr(layer), _lib.ptr(idx), _lib.ptr(blo),
+                          _lib.ptr(bhi), stream)
+            rows = torch.stack([bounds.lower[:, 0].double(), bounds.upper[:, 0].double(), layer.double(),
+                                idx.double(), blo.double(), bhi.double(), width]).cpu().tolist()
+            for j, nid in enumerate(chunk):
+                m = meta[nid]
+                lay = int(rows[2][j])
+                branch = None if lay < 0 else ReluSplitBranch(names[lay], int(rows[3][j]), rows[4][j], rows[5][j],
+                                                              rows[6][j])
+                m.update(lower=rows[0][j], upper=rows[1][j], branch=branch, priority=native_priority(rows[0][j]))
+                evaluations.append(NativeReluSplitBabEvaluation(
+                    node_id=nid, parent_node_id=m["parent"], depth=m["depth"], branch_relu_input=m["via"][0],
+                    branch_neuron_index=m["via"][1], branch_value=m["via"][2], lower=m["lower"], upper=m["upper"],
+                    priority=m["priority"], eval_batch_id=batch_id, eval_batch_position=j, branch_candidate=branch))
+
+    root_id = f"{run_id}:n000000"
+    root_slot = front.alloc(1)[0]
+    for n in names:
+        front.split[n][root_slot].zero_()
+    meta[root_id] = {"slot": root_slot, "parent": None, "depth": 0, "via": (None, None, 0)}
+    evaluate([root_id])
+    heap: List[Tuple[float, int, str]] = [(meta[root_id]["priority"], 0, root_id)]
+    max_q = 1
+    exhausted = False
+    while heap and not exhausted:
+        selected = [heapq.heappop(heap) for _ in range(min(int(config.expansion_batch_size), len(heap)))]
+        generated: List[str] = []
+        n_dec = len(decisions)
+        for pos, entry in enumerate(selected):
+            nid = entry[2]
+            m = meta[nid]
+            if m["lower"] >= float(config.threshold):
+                decisions.append(NativeReluSplitBabDecision(len(decisions), nid, "prune",
+                                                            "lower_bound_meets_threshold"))
+                continue
+            if m["depth"] >= int(config.max_depth):
+                decisions.append(NativeReluSplitBabDecision(len(decisions), nid, "terminal", "configured_depth_limit"))
+                continue
+            br = m["branch"]
+            if br is None:
+                decisions.append(NativeReluSplitBabDecision(len(decisions), nid, "terminal",
+                                                            "no_unsplit_ambiguous_relu"))
+                continue
+            if len(evaluations) + len(generated) + 2 > int(config.max_nodes):
+                for pending in selected[pos:]:
+                    heapq.heappush(heap, pending)
+                exhausted = True
+                break
+            kids = []
+            slots = front.alloc(2)
+            src = torch.tensor([m["slot"], m["slot"]], device=dev, dtype=torch.long)
+            dst = torch.tensor(slots, device=dev, dtype=torch.long)
+            for n in names:
+                front.split[n][dst] = front.split[n][src]
+            for side, (val, slot) in enumerate(zip((-1, 1), slots)):
+                front.split[br.relu_input][slot, br.neuron_index] = val
+                kid = f"{run_id}:n{counters['next']:06d}"
+                counters["next"] += 1
+                meta[kid] = {"slot": slot, "parent": nid, "depth": m["depth"] + 1,
+                             "via": (br.relu_input, br.neuron_index, val)}
+                kids.append(kid)
+            generated.extend(kids)
+            decisions.append(NativeReluSplitBabDecision(len(decisions), nid, "expand",
+                                                        "widest_unsplit_ambiguous_relu", tuple(kids), br))
+        if generated:
+            evaluate(generated)
+            for kid in generated:
+                heapq.heappush(heap, (meta[kid]["priority"], counters["next"], kid))
+            max_q = max(max_q, len(heap))
+        # nodes decided this round left the queue for good: their split rows are reused
+        # (the children's copies are ordered before any later write on the stream)
+        front.release([meta[d.node_id]["slot"] for d in decisions[n_dec:]])
+    frontier = tuple(e[2] for e in sorted(heap, key=lambda e: (e[0], e[1])))
+    return NativeReluSplitBabTrace(
+        run_id=run_id, status="budget_exhausted" if exhausted else "complete",
+        termination_reason="node_budget_exhausted" if exhausted else "configured_bounded_tree_exhausted",
+        config=config, evaluations=tuple(evaluations), decisions=tuple(decisions), final_frontier_node_ids=frontier,
+        native_stack_count=counters["batches"], max_queue_size=max_q)

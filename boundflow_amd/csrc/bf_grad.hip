@@ -118,6 +118,111 @@ __global__ void best_update_kernel(const float* __restrict__ lb, const float* __
   }
 }
 
+// Spec reductions of the optimisation objective (alpha_beta_crown.py:787-815) over
+// the S specs of one domain: mean; min / max (first index on ties, as torch's
+// min/max over a dimension); softmin -tau log sum exp(-x / tau) / softmax
+// tau log sum exp(x / tau), with the max-shifted log-sum-exp.  ``dir`` -1 is
+// the min direction, +1 the max direction; ``w`` receives dR/dx_s.
+__device__ float spec_reduce(const float* x, int64_t S, int reduce, int dir, float tau, float* w) {
+  if (reduce == 0) {
+    // the 1/S of the mean is applied by the caller, after the upstream factor (torch's
+    // MeanBackward divides the incoming gradient by S)
+    float sum = 0.f;
+    for (int64_t s = 0; s < S; ++s) sum += x[s];
+    for (int64_t s = 0; s < S; ++s) w[s] = 1.f;
+    return sum / (float)S;
+  }
+  if (reduce == 1) {
+    int64_t best = 0;
+    for (int64_t s = 1; s < S; ++s)
+      if (dir < 0 ? x[s] < x[best] : x[s] > x[best]) best = s;
+    for (int64_t s = 0; s < S; ++s) w[s] = (s == best) ? 1.f : 0.f;
+    return x[best];
+  }
+  // softmin / softmax through v = dir * x / tau
+  float m = -INFINITY;
+  for (int64_t s = 0; s < S; ++s) m = fmaxf(m, (dir < 0 ? -x[s] : x[s]) / tau);
+  float se = 0.f;
+  for (int64_t s = 0; s < S; ++s) se += expf((dir < 0 ? -x[s] : x[s]) / tau - m);
+  const float lse = m + logf(se);
+  for (int64_t s = 0; s < S; ++s) w[s] = expf((dir < 0 ? -x[s] : x[s]) / tau - lse);
+  return dir < 0 ? -tau * lse : tau * lse;
+}
+
+constexpr int kObjMaxSpecs = 64;
+
+// One domain per thread: the objective metric of alpha_beta_crown.py:787-815 from the
+// lower bound lb [D, S] of C and nub [D, S], the lower bound of -C (= -ub), the
+// per-row loss gradients G_l = dL/dlb and G_nu = dL/dnub for L = g_scale * sum_d
+// metric_d (g_scale = -1 per domain, -1/D shared), and the per-domain best-of
+// update (first call, or a strictly larger metric) of the metric and both bounds.
+// objective 0 lower: R_min(lb); 1 upper: -R_max(ub); 2 gap: -R_max(ub - lb);
+// 3 both: w_lb R_min(lb) - w_ub R_max(ub).
+__global__ void objective_step_kernel(const float* __restrict__ lb, const float* __restrict__ nub, int64_t D,
+                                      int64_t S, int objective, int reduce, float tau, float w_lb, float w_ub,
+                                      float g_scale, float* __restrict__ metric_out, float* __restrict__ G_l,
+                                      float* __restrict__ G_nu, float* __restrict__ best_metric,
+                                      float* __restrict__ best_lb, float* __restrict__ best_ub,
+                                      int* __restrict__ improved, int first) {
+  const int64_t d = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= D) return;
+  float x[kObjMaxSpecs], w1[kObjMaxSpecs], w2[kObjMaxSpecs];
+  const float* l = lb ? lb + d * S : nullptr;
+  const float* nu = nub ? nub + d * S : nullptr;
+  float metric = 0.f;
+  for (int64_t s = 0; s < S; ++s) {
+    w1[s] = 0.f;
+    w2[s] = 0.f;
+  }
+  if (objective == 0) {
+    metric = spec_reduce(l, S, reduce, -1, tau, w1);                      // dmetric/dlb = w1
+  } else if (objective == 1) {
+    for (int64_t s = 0; s < S; ++s) x[s] = -nu[s];
+    metric = -spec_reduce(x, S, reduce, +1, tau, w2);
+    for (int64_t s = 0; s < S; ++s) w2[s] = -w2[s];                       // dmetric/dub
+  } else if (objective == 2) {
+    for (int64_t s = 0; s < S; ++s) x[s] = -nu[s] - l[s];
+    metric = -spec_reduce(x, S, reduce, +1, tau, w2);
+    for (int64_t s = 0; s < S; ++s) {
+      w1[s] = w2[s];                                                        // dmetric/dlb
+      w2[s] = -w2[s];                                                       // dmetric/dub
+    }
+  } else {
+    const float rl = spec_reduce(l, S, reduce, -1, tau, w1);
+    for (int64_t s = 0; s < S; ++s) x[s] = -nu[s];
+    const float ru = spec_reduce(x, S, reduce, +1, tau, w2);
+    metric = w_lb * rl - w_ub * ru;
+    for (int64_t s = 0; s < S; ++s) {
+      w1[s] = w_lb * w1[s];
+      w2[s] = -(w_ub * w2[s]);
+    }
+  }
+  metric_out[d] = metric;
+  const float div = reduce == 0 ? (float)S : 1.f;
+  for (int64_t s = 0; s < S; ++s) {
+    if (G_l) G_l[d * S + s] = (g_scale * w1[s]) / div;
+    if (G_nu) G_nu[d * S + s] = -((g_scale * w2[s]) / div);                // dL/dnub = -dL/dub
+  }
+  if (best_metric) {
+    const bool take = first || (metric > best_metric[d]);
+    improved[d] = take ? 1 : 0;
+    if (take) {
+      best_metric[d] = metric;
+      if (l && best_lb)
+        for (int64_t s = 0; s < S; ++s) best_lb[d * S + s] = l[s];
+      if (nu && best_ub)
+        for (int64_t s = 0; s < S; ++s) best_ub[d * S + s] = -nu[s];
+    }
+  }
+}
+
+// x[m, :] *= scale[m] (a concretization gradient seed formed with unit row weights)
+__global__ void scale_rows_kernel(float* __restrict__ x, int64_t M, int64_t N, const float* __restrict__ scale) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * N) return;
+  x[i] = scale[div_rows(i, N, M * N < (1LL << 31))] * x[i];
+}
+
 __global__ void masked_copy_rows_kernel(float* __restrict__ dst, const float* __restrict__ src, int64_t D, int64_t N,
                                         const int* __restrict__ mask) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -148,6 +253,67 @@ __global__ void alpha_from_crown_kernel(const float* __restrict__ lo, const floa
   if (pos) a = 1.f;
   if (!pos && !neg) a = (u > -l) ? 1.f : 0.f;
   out[i] = a;
+}
+
+// The ADAPTIVE lower slope of the native plain-CROWN relaxation
+// (boundflow/runtime/bound_ir_interpreter.py:1380-1397): on an ambiguous neuron
+// 1 when the upper chord's slope u / max(u - l, eps) exceeds one half, else 0;
+// 1 on stable-active, 0 on stable-inactive neurons.
+__global__ void alpha_adaptive_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int64_t n,
+                                      float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float l = lo[i], u = hi[i];
+  const bool pos = l >= 0.f;
+  const bool neg = u <= 0.f;
+  float a = 0.f;
+  if (pos) a = 1.f;
+  if (!pos && !neg) a = (u / fmaxf(u - l, kF32Eps) > 0.5f) ? 1.f : 0.f;
+  out[i] = a;
+}
+
+// Branching rule of the native ReLU-split queue for one ReLU layer
+// (native_relu_split_bab_runtime.py:1015-1049): per domain, the widest unsplit
+// ambiguous neuron with the width u - l taken in double (the reference compares
+// Python floats), the first index on ties; the running best is replaced only
+// when strictly wider, so layers processed in sorted-name order win ties in
+// that order.  One wave per domain.
+__global__ void branch_update_native_kernel(const float* __restrict__ lo, const float* __restrict__ hi,
+                                            const int8_t* __restrict__ split, int64_t split_ld, int64_t D, int64_t N,
+                                            int layer, double* __restrict__ best_width, int* __restrict__ best_layer,
+                                            int* __restrict__ best_idx, float* __restrict__ best_lo,
+                                            float* __restrict__ best_hi) {
+  const int lane = threadIdx.x & 63;
+  const int64_t d = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (d >= D) return;
+  double w = -1.0;
+  int idx = -1;
+  for (int64_t n = lane; n < N; n += 64) {
+    const float l = lo[d * N + n], u = hi[d * N + n];
+    const int8_t s = split ? split[d * split_ld + n] : (int8_t)0;
+    if (s == 0 && l < 0.f && u > 0.f) {
+      const double wd = (double)u - (double)l;
+      if (wd > w) {
+        w = wd;
+        idx = (int)n;
+      }
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    const double ow = __shfl_xor(w, off, 64);
+    const int oi = __shfl_xor(idx, off, 64);
+    if (oi >= 0 && (idx < 0 || ow > w || (ow == w && oi < idx))) {
+      w = ow;
+      idx = oi;
+    }
+  }
+  if (lane == 0 && idx >= 0 && w > best_width[d]) {
+    best_width[d] = w;
+    best_layer[d] = layer;
+    best_idx[d] = idx;
+    best_lo[d] = lo[d * N + idx];
+    best_hi[d] = hi[d * N + idx];
+  }
 }
 
 // BaB node verdict (boundflow/runtime/bab.py:870-895): a domain is closed when
@@ -233,6 +399,36 @@ int bf_best_update(const float* lb, const float* ub, int64_t D, int64_t S, float
   return BF_OK;
 }
 
+int bf_objective_step(const float* lb, const float* nub, int64_t D, int64_t S, int objective, int reduce, float tau,
+                      float w_lb, float w_ub, float g_scale, float* metric, float* G_l, float* G_nu,
+                      float* best_metric, float* best_lb, float* best_ub, int* improved, int first,
+                      hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0, "bf_objective_step: bad sizes");
+  if (D == 0) return BF_OK;
+  if (S > kObjMaxSpecs) {
+    set_error("bf_objective_step: %lld specs per domain above %d", (long long)S, kObjMaxSpecs);
+    return BF_ERANGE;
+  }
+  BF_REQUIRE(objective >= 0 && objective <= 3 && reduce >= 0 && reduce <= 2, "bf_objective_step: bad mode");
+  BF_REQUIRE(reduce != 2 || tau > 0.f, "bf_objective_step: soft_tau must be >0");
+  BF_REQUIRE(metric && (objective == 1 || lb) && (objective == 0 || nub), "bf_objective_step: missing bound");
+  BF_REQUIRE(best_metric == nullptr || improved != nullptr, "bf_objective_step: best-of needs the improved flags");
+  hipLaunchKernelGGL(objective_step_kernel, dim3((unsigned)ceil_div(D, 64)), dim3(64), 0, stream, lb, nub, D, S,
+                     objective, reduce, tau, w_lb, w_ub, g_scale, metric, G_l, G_nu, best_metric, best_lb, best_ub,
+                     improved, first);
+  BF_LAUNCH_CHECK("objective_step_kernel");
+  return BF_OK;
+}
+
+int bf_scale_rows(float* x, int64_t M, int64_t N, const float* scale, hipStream_t stream) {
+  BF_REQUIRE(M >= 0 && N >= 0, "bf_scale_rows: bad sizes");
+  if (M * N == 0) return BF_OK;
+  BF_REQUIRE(x && scale, "bf_scale_rows: null pointer");
+  hipLaunchKernelGGL(scale_rows_kernel, dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0, stream, x, M, N, scale);
+  BF_LAUNCH_CHECK("scale_rows_kernel");
+  return BF_OK;
+}
+
 int bf_masked_copy_rows(float* dst, const float* src, int64_t D, int64_t N, const int* mask, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && N >= 0, "bf_masked_copy_rows: bad sizes");
   if (D * N == 0) return BF_OK;
@@ -260,6 +456,28 @@ int bf_domain_status(const float* lb, int64_t D, int64_t S, const int* infeasibl
   hipLaunchKernelGGL(domain_status_kernel, dim3((unsigned)ceil_div(D, 256)), dim3(256), 0, stream, lb, D, S,
                      infeasible, threshold, tol, status);
   BF_LAUNCH_CHECK("domain_status_kernel");
+  return BF_OK;
+}
+
+int bf_alpha_adaptive(const float* lo, const float* hi, int64_t n, float* out, hipStream_t stream) {
+  BF_REQUIRE(n >= 0, "bf_alpha_adaptive: bad size");
+  if (n == 0) return BF_OK;
+  BF_REQUIRE(lo && hi && out, "bf_alpha_adaptive: null pointer");
+  hipLaunchKernelGGL(alpha_adaptive_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, lo, hi, n, out);
+  BF_LAUNCH_CHECK("alpha_adaptive_kernel");
+  return BF_OK;
+}
+
+int bf_branch_update_native(const float* lo, const float* hi, const int8_t* split, int64_t split_ld, int64_t D,
+                            int64_t N, int layer, double* best_width, int* best_layer, int* best_idx, float* best_lo,
+                            float* best_hi, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && N >= 0 && split_ld >= 0, "bf_branch_update_native: bad sizes");
+  if (D == 0 || N == 0) return BF_OK;
+  BF_REQUIRE(lo && hi && best_width && best_layer && best_idx && best_lo && best_hi,
+             "bf_branch_update_native: null pointer");
+  hipLaunchKernelGGL(branch_update_native_kernel, dim3((unsigned)ceil_div(D, 4)), dim3(256), 0, stream, lo, hi,
+                     split, split_ld, D, N, layer, best_width, best_layer, best_idx, best_lo, best_hi);
+  BF_LAUNCH_CHECK("branch_update_native_kernel");
   return BF_OK;
 }
 

@@ -331,12 +331,43 @@ int bf_sum_rows(const float* x, int64_t D, int64_t N, float* out, hipStream_t st
 /* "alpha from CROWN" init (runtime/native_alpha_beta_optimizer_schedule.py:635-653). */
 int bf_alpha_from_crown(const float* lo, const float* hi, int64_t n, float* out, hipStream_t stream);
 
+/* The ADAPTIVE lower slope of the native plain-CROWN relaxation
+ * (runtime/bound_ir_interpreter.py:1380-1397), the node bound of the native
+ * ReLU-split queue: 1 on an ambiguous neuron whose upper chord slope
+ * u / max(u - l, eps) exceeds 0.5, 1 on stable-active, else 0. */
+int bf_alpha_adaptive(const float* lo, const float* hi, int64_t n, float* out, hipStream_t stream);
+
+/* Optimisation objective of one step (runtime/alpha_beta_crown.py:787-815): per domain
+ * the metric of `objective` (0 lower: R_min(lb); 1 upper: -R_max(ub); 2 gap:
+ * -R_max(ub - lb); 3 both: w_lb R_min(lb) - w_ub R_max(ub)) with the spec reduction
+ * `reduce` (0 mean, 1 min/max, 2 softmin/softmax with temperature tau), from lb [D, S]
+ * (lower bound of C) and nub [D, S] (lower bound of -C, i.e. -ub); G_l = dL/dlb and
+ * G_nu = dL/dnub (optional) for L = g_scale * sum_d metric_d; and with best_metric the
+ * per-domain best-of update of the metric, best_lb and best_ub (optional) with the
+ * improved flags.  S <= 64. */
+int bf_objective_step(const float* lb, const float* nub, int64_t D, int64_t S, int objective, int reduce, float tau,
+                      float w_lb, float w_ub, float g_scale, float* metric, float* G_l, float* G_nu,
+                      float* best_metric, float* best_lb, float* best_ub, int* improved, int first,
+                      hipStream_t stream);
+
+/* x[m, :] *= scale[m], in place (row weights applied to a gradient seed). */
+int bf_scale_rows(float* x, int64_t M, int64_t N, const float* scale, hipStream_t stream);
+
 /* ---- BaB decisions ----------------------------------------------------------- */
 
 /* Branching rule update for one ReLU layer (runtime/alpha_beta_crown.py:145-182):
  * widest ambiguous neuron, first index on ties, strictly wider to replace. */
 int bf_branch_update(const float* lo, const float* hi, int64_t D, int64_t N, int layer, float* best_gap,
                      int* best_layer, int* best_idx, hipStream_t stream);
+
+/* Branching rule of the native ReLU-split queue for one layer
+ * (_select_branch, runtime/native_relu_split_bab_runtime.py:1015-1049): per domain the
+ * widest unsplit (split == 0) ambiguous neuron, width u - l in double, first index on
+ * ties; replaces best_* (width, layer, index, its l and u) only when strictly wider.
+ * Call per layer in sorted-name order, best_width starting at -1. */
+int bf_branch_update_native(const float* lo, const float* hi, const int8_t* split, int64_t split_ld, int64_t D,
+                            int64_t N, int layer, double* best_width, int* best_layer, int* best_idx, float* best_lo,
+                            float* best_hi, hipStream_t stream);
 
 /* First-layer split infeasibility certificate, one node per workgroup
  * (_is_infeasible_split_first_layer_convex_combo, runtime/alpha_beta_crown.py:391-532;

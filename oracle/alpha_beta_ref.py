@@ -226,8 +226,18 @@ def run_alpha_beta_crown(
     forward_trace=None,
     return_feasibility: bool = False,
     record: Optional[list] = None,
+    objective: str = "lower",
+    spec_reduce: str = "mean",
+    soft_tau: float = 1.0,
+    lb_weight: float = 1.0,
+    ub_weight: float = 1.0,
 ):
-    """alpha_beta_crown.py:643-941 with objective="lower", spec_reduce="mean".
+    """alpha_beta_crown.py:643-941.  ``objective`` "lower" maximises the reduced lower
+    bound with the split multipliers in the bound; "upper", "gap" and "both" use
+    the bounds without them (alpha_beta_crown.py:756-785) and the metrics
+    -R_max(ub), -R_max(ub - lb) and lb_weight R_min(lb) - ub_weight R_max(ub); the
+    spec reduction R is the mean, min / max, or softmin / softmax with temperature
+    ``soft_tau`` (:787-815).
 
     Returns (best_bounds, best_alpha, best_beta, branch_choices), plus the
     feasibility ("infeasible" or "unknown") with ``return_feasibility``.  A
@@ -278,13 +288,39 @@ def run_alpha_beta_crown(
     best_alpha = None
     best_beta = None
     choices = branch_choices(relu_pre)
+    def reduce_specs(x, direction):
+        if x.dim() != 2:
+            return x.mean().expand(batch)
+        if spec_reduce == "mean":
+            return x.mean(dim=1)
+        if spec_reduce == "min":
+            return x.min(dim=1).values if direction == "min" else x.max(dim=1).values
+        if spec_reduce == "softmin":
+            tau = float(soft_tau)
+            if tau <= 0.0:
+                raise ValueError(f"soft_tau must be >0, got {soft_tau}")
+            if direction == "min":
+                return -tau * torch.logsumexp(-x / tau, dim=1)
+            return tau * torch.logsumexp(x / tau, dim=1)
+        raise AssertionError(f"unreachable spec_reduce: {spec_reduce}")
+
     for step in range(int(steps) + 1):
-        add_l = beta_to_pre_add(beta, relu_pre, relu_split_state)
+        add_l = beta_to_pre_add(beta, relu_pre, relu_split_state) if objective == "lower" else None
         bounds = crown_backward_from_trace(
             module, spec, interval_env=interval_env, relu_pre=relu_pre, linear_spec_C=linear_spec_C,
             relu_alpha=alpha, relu_pre_add_coeff_l=add_l,
         )
-        metric_b = bounds.lower.mean(dim=1)
+        if objective == "lower":
+            metric_b = reduce_specs(bounds.lower, "min")
+        elif objective == "upper":
+            metric_b = -reduce_specs(bounds.upper, "max")
+        elif objective == "gap":
+            metric_b = -reduce_specs(bounds.upper - bounds.lower, "max")
+        elif objective == "both":
+            metric_b = float(lb_weight) * reduce_specs(bounds.lower, "min") - float(ub_weight) * reduce_specs(
+                bounds.upper, "max")
+        else:
+            raise AssertionError(f"unreachable objective: {objective}")
         metric = metric_b.mean()
         if record is not None:
             record.append({"step": step, "alpha": {k: v.detach().clone() for k, v in alpha.items()},

@@ -325,3 +325,146 @@ def _eval_batch(module, spec, linear_spec_C, items, slots, shapes, cfg, live, do
                 live[e] = max(0, live[e] - 1)
                 done_if_empty(e)
     return results
+
+
+# ---------------------------------------------------------------------------
+# The native ReLU-split queue (boundflow/runtime/native_relu_split_bab_runtime.py:592-789)
+
+
+def native_priority(lower: float) -> float:
+    """native_relu_split_bab_runtime.py:1128-1131: the lower bound to 7 significant digits."""
+    if not torch.isfinite(torch.tensor(lower)):
+        raise ValueError("native ReLU-split queue bound must be finite")
+    return float(f"{lower:.7g}")
+
+
+def native_select_branch(relu_pre, split: Dict[str, torch.Tensor]):
+    """native_relu_split_bab_runtime.py:1015-1049: the widest unsplit ambiguous neuron
+    (width upper - lower in Python floats), ties to the first ReLU name in sorted
+    order, then the lowest index; (name, index, lower, upper, width) or None."""
+    best = None
+    for name in sorted(relu_pre):
+        lo = relu_pre[name].lower.reshape(-1).tolist()
+        hi = relu_pre[name].upper.reshape(-1).tolist()
+        sp = split[name].reshape(-1).tolist()
+        for i, (l, u, s) in enumerate(zip(lo, hi, sp)):
+            if int(s) == 0 and l < 0.0 < u:
+                key = (-(u - l), name, i)
+                if best is None or key < best[0]:
+                    best = (key, (name, i, l, u, u - l))
+    return None if best is None else best[1]
+
+
+def native_adaptive_alpha(relu_pre) -> Dict[str, torch.Tensor]:
+    """The ADAPTIVE lower slope of the native plain-CROWN relaxation
+    (boundflow/runtime/bound_ir_interpreter.py:1380-1397): on an ambiguous neuron
+    alpha_l = 1(u / max(u - l, eps) > 0.5), the upper chord's slope above one half."""
+    out = {}
+    for name, pre in relu_pre.items():
+        lo, hi = pre.lower, pre.upper
+        amb = (lo < 0) & (hi > 0)
+        a = torch.zeros_like(lo)
+        a[lo >= 0] = 1.0
+        den = (hi[amb] - lo[amb]).clamp_min(torch.finfo(lo.dtype).eps)
+        a[amb] = (hi[amb] / den > 0.5).to(lo.dtype)
+        out[name] = a
+    return out
+
+
+def run_native_relu_split_bab(module, input_spec, *, linear_spec_C, run_id: str, max_nodes: int, max_depth: int,
+                              expansion_batch_size: int, max_eval_batch_size: int, threshold: float = 0.0) -> dict:
+    """The bounded best-first queue of native_relu_split_bab_runtime.py:592-789.
+
+    Nodes are evaluated in batches of at most ``max_eval_batch_size``: CROWN with the
+    ADAPTIVE lower slope (``native_adaptive_alpha``) on the box input repeated per
+    node, the node's splits applied to its IBP pre-activation boxes; the root
+    first, then every round's children together.
+    A round pops up to ``expansion_batch_size`` entries (priority, serial, node id)
+    and for each: prune when lower >= threshold, terminal at the depth limit or
+    without a branch, stop when two more nodes would exceed ``max_nodes`` (the
+    rest of the round goes back to the heap), else expand into the inactive (-1)
+    then active (+1) child.  Children are pushed with the serial the round ends
+    with.  Returns the evaluations, decisions, final frontier, status and the
+    largest queue."""
+    spec = normalize_input_spec(input_spec)
+    if not isinstance(spec.perturbation, BoxPerturbation):
+        raise NotImplementedError("native ReLU-split BaB v1 requires a box input")
+    lo0, hi0 = spec.perturbation.lower, spec.perturbation.upper
+    C = linear_spec_C if linear_spec_C.dim() == 2 else linear_spec_C[0]
+    _env, root_pre = forward_ibp_trace(module, spec)
+    names = sorted(root_pre)
+    shapes = {n: tuple(int(d) for d in root_pre[n].lower.shape[1:]) for n in names}
+    nodes: Dict[str, dict] = {}
+    evaluations: List[dict] = []
+    decisions: List[dict] = []
+    serial = {"next": 1, "stacks": 0}
+
+    def evaluate(batch: List[dict]) -> None:
+        for start in range(0, len(batch), max_eval_batch_size):
+            chunk = batch[start:start + max_eval_batch_size]
+            k = len(chunk)
+            bspec = InputSpec.box(value_name=spec.value_name, lower=lo0.repeat((k,) + (1,) * (lo0.dim() - 1)),
+                                  upper=hi0.repeat((k,) + (1,) * (hi0.dim() - 1)))
+            split_b = {n: torch.stack([c["split"][n] for c in chunk]) for n in names}
+            _e, pre = forward_ibp_trace(module, bspec, relu_split_state=split_b)
+            from .crown_ref import crown_backward_from_trace
+            b = crown_backward_from_trace(module, bspec, interval_env=_e, relu_pre=pre,
+                                          linear_spec_C=C.unsqueeze(0).expand(k, -1, -1),
+                                          relu_alpha=native_adaptive_alpha(pre))
+            serial["stacks"] += 1
+            for j, c in enumerate(chunk):
+                node_pre = {n: type(pre[n])(pre[n].lower[j:j + 1], pre[n].upper[j:j + 1]) for n in names}
+                c["branch"] = native_select_branch(node_pre, c["split"])
+                c["lower"] = float(b.lower[j, 0].item())
+                c["upper"] = float(b.upper[j, 0].item())
+                c["priority"] = native_priority(c["lower"])
+                evaluations.append({k2: c[k2] for k2 in ("node_id", "parent", "depth", "lower", "upper",
+                                                          "priority", "branch")})
+
+    root = {"node_id": f"{run_id}:n000000", "parent": None, "depth": 0,
+            "split": {n: torch.zeros(shapes[n], dtype=torch.int8) for n in names}}
+    nodes[root["node_id"]] = root
+    evaluate([root])
+    heap = [(root["priority"], 0, root["node_id"])]
+    max_q = 1
+    exhausted = False
+    while heap and not exhausted:
+        selected = [heapq.heappop(heap) for _ in range(min(expansion_batch_size, len(heap)))]
+        generated: List[dict] = []
+        for pos, entry in enumerate(selected):
+            node = nodes[entry[2]]
+            if node["lower"] >= threshold:
+                decisions.append({"node_id": node["node_id"], "kind": "prune", "reason": "lower_bound_meets_threshold"})
+                continue
+            if node["depth"] >= max_depth:
+                decisions.append({"node_id": node["node_id"], "kind": "terminal", "reason": "configured_depth_limit"})
+                continue
+            br = node["branch"]
+            if br is None:
+                decisions.append({"node_id": node["node_id"], "kind": "terminal", "reason": "no_unsplit_ambiguous_relu"})
+                continue
+            if len(evaluations) + len(generated) + 2 > max_nodes:
+                for pending in selected[pos:]:
+                    heapq.heappush(heap, pending)
+                exhausted = True
+                break
+            kids = []
+            for val in (-1, 1):
+                split = {n: v.clone() for n, v in node["split"].items()}
+                split[br[0]].reshape(-1)[br[1]] = val
+                kid = {"node_id": f"{run_id}:n{serial['next']:06d}", "parent": node["node_id"],
+                       "depth": node["depth"] + 1, "split": split}
+                serial["next"] += 1
+                nodes[kid["node_id"]] = kid
+                kids.append(kid)
+            generated.extend(kids)
+            decisions.append({"node_id": node["node_id"], "kind": "expand", "reason": "widest_unsplit_ambiguous_relu",
+                              "children": [k["node_id"] for k in kids], "branch": br})
+        if generated:
+            evaluate(generated)
+            for kid in generated:
+                heapq.heappush(heap, (kid["priority"], serial["next"], kid["node_id"]))
+            max_q = max(max_q, len(heap))
+    frontier = [e[2] for e in sorted(heap, key=lambda e: (e[0], e[1]))]
+    return {"status": "budget_exhausted" if exhausted else "complete", "evaluations": evaluations,
+            "decisions": decisions, "frontier": frontier, "max_queue_size": max_q, "stacks": serial["stacks"]}

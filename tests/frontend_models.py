@@ -160,3 +160,32 @@ def vnnlib_c1_property(index: int = 0) -> str:
     return "\n".join(lines) + "\n"
 
 
+
+
+def native_toy():
+    """The reference's native-queue toy (tests/test_native_relu_split_bab_runtime.py:20-56)."""
+    from boundflow_amd.ir import BFTaskModule, BoundTask, TaskKind, TaskOp
+    from boundflow_amd.spec import InputSpec
+    ops = [TaskOp("linear", "linear1", ["input", "W1", "b1"], ["h1"]), TaskOp("relu", "relu1", ["h1"], ["r1"]),
+           TaskOp("linear", "linear2", ["r1", "W2", "b2"], ["out"])]
+    params = {"W1": torch.tensor([[1.0, -0.5, 0.25], [-0.25, 0.75, 1.0], [0.5, 0.5, -1.0]]),
+              "b1": torch.tensor([0.1, -0.2, 0.05]),
+              "W2": torch.tensor([[0.75, -1.0, 0.5], [-0.5, 0.25, 1.25]]), "b2": torch.tensor([0.15, -0.1])}
+    task = BoundTask(task_id="native-relu-split-toy", kind=TaskKind.INTERVAL_IBP, ops=ops, input_values=["input"],
+                     output_values=["out"])
+    module = BFTaskModule(tasks=[task], entry_task_id=task.task_id, bindings={"params": params})
+    spec = InputSpec.box(value_name="input", lower=torch.tensor([[-0.3, -0.6, -0.1]]),
+                         upper=torch.tensor([[0.7, 0.4, 0.9]]))
+    return module, spec, torch.tensor([[1.0, -1.0]])
+
+
+def native_bab_toy():
+    """A four-layer MLP (make_bab_toy's, seed 1, 6-12-12-3) on a box, objective y_0 - y_1."""
+    from boundflow_amd.spec import InputSpec
+    from boundflow_amd import workloads as wl
+    w = wl.make_bab_toy(seed=1, eps=0.2, dims=(6, 12, 12, 3), batch=1)
+    x = w.spec.center
+    spec = InputSpec.box(value_name="input", lower=x - 0.2, upper=x + 0.2)
+    return w.module, spec, torch.tensor([[1.0, -1.0, 0.0]])
+
+

@@ -340,6 +340,66 @@ def golden_vnnlib(tag):
     save(tag, **arrays)
 
 
+from tests.frontend_models import native_bab_toy, native_toy  # noqa: E402
+from tests.golden_util import OBJECTIVE_CASES, objective_workload  # noqa: E402
+
+
+def golden_objectives(tag):
+    """run_alpha_beta_crown_mlp (runtime/alpha_beta_crown.py:643-941) with the
+    objectives and spec reductions of OBJECTIVE_CASES on a small MLP with splits:
+    the best bounds of each."""
+    w, splits = objective_workload()
+    names = list(splits)
+    rm, rs = to_ref_module(w.module), to_ref_spec(w.spec)
+    arrays = {"checksum": workload_checksum(w)}
+    for case, kw in OBJECTIVE_CASES.items():
+        try:
+            b, _a, _bt, _st = rabc.run_alpha_beta_crown_mlp(rm, rs, linear_spec_C=w.C, relu_split_state=splits,
+                                                            steps=8, lr=0.1, **kw)
+        except ValueError:
+            raise
+        arrays[f"{case}_lower"] = b.lower
+        arrays[f"{case}_upper"] = b.upper
+    for n in names:
+        arrays[f"split_{n}"] = splits[n]
+    save(tag, **arrays)
+
+
+# tag -> (problem, config fields)
+NATIVE_CASES = {
+    "native_toy_b4": ("toy", dict(max_nodes=15, max_depth=3, expansion_batch_size=2, max_eval_batch_size=4,
+                                  threshold=1e6)),
+    "native_toy_budget": ("toy", dict(max_nodes=7, max_depth=3, expansion_batch_size=2, max_eval_batch_size=4,
+                                      threshold=1e6)),
+    "native_mlp": ("mlp", dict(max_nodes=41, max_depth=6, expansion_batch_size=3, max_eval_batch_size=8,
+                               threshold=0.0)),
+}
+
+
+def golden_native(tag):
+    """run_native_relu_split_bab (runtime/native_relu_split_bab_runtime.py:592-789)."""
+    import json
+    from boundflow.runtime.native_relu_split_bab_runtime import NativeReluSplitBabConfig as RCfg
+    from boundflow.runtime.native_relu_split_bab_runtime import run_native_relu_split_bab as r_run
+    prob, cfg = NATIVE_CASES[tag]
+    module, spec, C = native_toy() if prob == "toy" else native_bab_toy()
+    trace = r_run(to_ref_module(module), to_ref_spec(spec), linear_spec_C=C, run_id=tag, config=RCfg(**cfg))
+
+    def br(b):
+        return None if b is None else [b.relu_input, b.neuron_index, b.lower, b.upper, b.width]
+
+    out = {"status": trace.status, "termination_reason": trace.termination_reason,
+           "frontier": list(trace.final_frontier_node_ids), "max_queue_size": trace.max_queue_size,
+           "stacks": trace.native_stack_count,
+           "evaluations": [{"node_id": e.node.node_id, "parent": e.node.parent_node_id, "depth": e.node.depth,
+                            "lower": e.lower, "upper": e.upper, "priority": e.priority,
+                            "branch": br(e.branch_candidate)} for e in trace.evaluations],
+           "decisions": [{"node_id": d.node_id, "kind": d.kind, "reason": d.reason,
+                          "children": list(d.child_node_ids), "branch": br(d.branch_candidate)}
+                         for d in trace.decisions]}
+    save(tag, trace=np.array(json.dumps(out)))
+
+
 GOLDENS = [
     ("crown_c1", lambda t: golden_crown(wl.make_c1(), t, pre_rows=8)),
     ("crown_c3_b16", lambda t: golden_crown(wl.subset(wl.make_c3(), 16), t, pre_rows=2)),
@@ -366,6 +426,10 @@ GOLDENS = [
     ("bab_solve_1d", golden_bab_solve),
     ("frontend_planned", golden_frontend),
     ("vnnlib_queries", golden_vnnlib),
+    ("objectives_mlp", golden_objectives),
+    ("native_toy_b4", golden_native),
+    ("native_toy_budget", golden_native),
+    ("native_mlp", golden_native),
 ]
 
 

@@ -51,3 +51,38 @@ BAB_SOLVE_CASES = {
                      dict(max_nodes=30, oracle="alpha_beta", node_batch_size=4, alpha_steps=5,
                           use_1d_linf_input_restriction_patch=True)),
 }
+
+
+# run_alpha_beta_crown_mlp options of the "objectives_mlp" fixture (objective, spec reduction,
+# temperature, weights, per-domain or shared parameters); alpha_beta_crown.py:756-815
+OBJECTIVE_CASES = {
+    "upper_mean": dict(objective="upper", spec_reduce="mean", per_batch_params=True),
+    "gap_min": dict(objective="gap", spec_reduce="min", per_batch_params=True),
+    "both_softmin": dict(objective="both", spec_reduce="softmin", soft_tau=0.5, lb_weight=1.0, ub_weight=0.5,
+                         per_batch_params=True),
+    "lower_min": dict(objective="lower", spec_reduce="min", per_batch_params=True),
+    "lower_softmin": dict(objective="lower", spec_reduce="softmin", soft_tau=2.0, per_batch_params=True),
+    "gap_mean_shared": dict(objective="gap", spec_reduce="mean", per_batch_params=False),
+}
+
+
+def objective_workload():
+    """The "objectives_mlp" problem: make_bab_toy(seed 4, eps 0.1, 12-16-16-4, 6 inputs) with
+    feasible random splits, chosen layer by layer among the neurons still ambiguous
+    after the splits of the layers before (about one in five, random sign)."""
+    import torch
+
+    from boundflow_amd import workloads as wl
+    from oracle import crown_ref as cr
+
+    w = wl.make_bab_toy(seed=4, eps=0.1, dims=(12, 16, 16, 4), batch=6)
+    g = torch.Generator().manual_seed(6)
+    names = [op.inputs[0] for op in w.module.get_entry_task().ops if op.op_type == "relu"]
+    splits = {n: torch.zeros(6, 16, dtype=torch.int8) for n in names}
+    for n in names:
+        _env, pre = cr.forward_ibp_trace(w.module, w.spec, relu_split_state=splits)
+        amb = (pre[n].lower < 0) & (pre[n].upper > 0)
+        pick = amb & (torch.rand(6, 16, generator=g) < 0.2)
+        sign = (torch.randint(0, 2, (6, 16), generator=g) * 2 - 1).to(torch.int8)
+        splits[n] = torch.where(pick, sign, splits[n])
+    return w, splits

@@ -53,16 +53,18 @@ def test_planned_dag_matches_oracle(name):
     net, _x = frontend_nets()[name]
     g = torch.Generator().manual_seed(5)
     x = torch.rand(6, 1, 2, 2, generator=g)
-    tm = fe.plan_interval_ibp_v0(fe.import_torch(net, (x[:2],)))
+    prog = fe.import_torch(net, (x[:2],))
+    tm = fe.plan_interval_ibp_v0(prog)
+    name_in = prog.graph.inputs[0]
     out_dim = int(net(x[:1]).shape[1])
     labels = torch.randint(0, out_dim, (6,), generator=g)
     C = wl.margin_spec(labels, out_dim)
-    spec = InputSpec.linf(value_name="input", center=x, eps=0.05)
+    spec = InputSpec.linf(value_name=name_in, center=x, eps=0.05)
     ref = cr.run_crown_ibp(tm, spec, linear_spec_C=C)
     w64 = wl.Workload("dag", tm, spec, C, labels)
     w64 = parity.to_float64(w64)
     ref64 = cr.run_crown_ibp(w64.module, w64.spec, linear_spec_C=w64.C)
-    got = hc.run_crown_ibp_mlp(_on(tm, dev), InputSpec.linf(value_name="input", center=x.to(dev), eps=0.05),
+    got = hc.run_crown_ibp_mlp(_on(tm, dev), InputSpec.linf(value_name=name_in, center=x.to(dev), eps=0.05),
                                linear_spec_C=C.to(dev))
     assert_parity(got.lower, ref.lower, ref64.lower, f"{name} lower")
     assert_parity(got.upper, ref.upper, ref64.upper, f"{name} upper")

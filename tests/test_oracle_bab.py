@@ -14,7 +14,7 @@ import torch
 
 from boundflow_amd import workloads as wl
 from oracle import bab_ref
-from tests.golden_util import BAB_SOLVE_CASES, load, workload_checksum
+from tests.golden_util import BAB_SOLVE_CASES, OBJECTIVE_CASES, load, objective_workload, workload_checksum
 
 CASES = BAB_SOLVE_CASES
 DEFAULTS = dict(use_branch_hint=True, alpha_lr=0.2, alpha_init=0.5, beta_init=0.0, threshold=0.0, tol=1e-6)
@@ -86,3 +86,67 @@ def test_bab_verdicts_are_sound(tag):
                     xs -= eps * 0.05 * gx.sign()
                     xs.copy_(torch.maximum(torch.minimum(xs, x0[e] + eps), x0[e] - eps))
             assert float(_margins(ww, xs.detach()).min()) < 0, f"example {e} unsafe but no violating point found"
+
+
+NATIVE = {
+    "native_toy_b4": ("toy", dict(max_nodes=15, max_depth=3, expansion_batch_size=2, max_eval_batch_size=4,
+                                  threshold=1e6)),
+    "native_toy_budget": ("toy", dict(max_nodes=7, max_depth=3, expansion_batch_size=2, max_eval_batch_size=4,
+                                      threshold=1e6)),
+    "native_mlp": ("mlp", dict(max_nodes=41, max_depth=6, expansion_batch_size=3, max_eval_batch_size=8,
+                               threshold=0.0)),
+}
+
+
+def native_problem(kind):
+    from tests.frontend_models import native_bab_toy, native_toy
+    return native_toy() if kind == "toy" else native_bab_toy()
+
+
+def compare_native(got: dict, ref: dict, bound_tol=(1e-5, 1e-6)):
+    """Identical queue: statuses, node ids, lineage, decisions, branch choices, frontier; bounds within tolerance."""
+    rtol, atol = bound_tol
+    assert got["status"] == ref["status"]
+    assert got["frontier"] == ref["frontier"]
+    assert got["max_queue_size"] == ref["max_queue_size"]
+    assert len(got["evaluations"]) == len(ref["evaluations"])
+    for g, r in zip(got["evaluations"], ref["evaluations"]):
+        assert (g["node_id"], g["parent"], g["depth"]) == (r["node_id"], r["parent"], r["depth"])
+        for k in ("lower", "upper"):
+            assert abs(g[k] - r[k]) <= atol + rtol * abs(r[k]), (g["node_id"], k, g[k], r[k])
+        gb, rb = g["branch"], r["branch"]
+        assert (gb is None) == (rb is None) and (gb is None or list(gb[:2]) == list(rb[:2])), g["node_id"]
+    assert len(got["decisions"]) == len(ref["decisions"])
+    for g, r in zip(got["decisions"], ref["decisions"]):
+        assert (g["node_id"], g["kind"], g["reason"]) == (r["node_id"], r["kind"], r["reason"])
+        assert list(g.get("children", [])) == list(r["children"])
+        assert (g.get("branch") is None) == (r["branch"] is None)
+        if r["branch"] is not None:
+            assert list(g["branch"][:2]) == list(r["branch"][:2])
+
+
+@pytest.mark.parametrize("tag", list(NATIVE))
+def test_native_queue_matches_reference(tag):
+    import json
+    kind, cfg = NATIVE[tag]
+    module, spec, C = native_problem(kind)
+    ref = json.loads(str(load(tag)["trace"]))
+    got = bab_ref.run_native_relu_split_bab(module, spec, linear_spec_C=C, run_id=tag, **cfg)
+    compare_native(got, ref)
+    assert got["stacks"] == ref["stacks"]
+
+
+@pytest.mark.parametrize("case", list(OBJECTIVE_CASES))
+def test_objectives_match_reference(case):
+    """The oracle's objectives and spec reductions (alpha_beta_crown.py:756-815) against
+    the reference's run_alpha_beta_crown_mlp on the same problem (fixture objectives_mlp)."""
+    from oracle import alpha_beta_ref as ab
+    g = load("objectives_mlp")
+    w, splits = objective_workload()
+    assert workload_checksum(w) == str(g["checksum"])
+    for n, v in splits.items():
+        assert torch.equal(v, torch.from_numpy(g[f"split_{n}"]))
+    b, _a, _bt, _ch = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, relu_split_state=splits, steps=8,
+                                              lr=0.1, **OBJECTIVE_CASES[case])
+    np.testing.assert_allclose(b.lower.numpy(), g[f"{case}_lower"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(b.upper.numpy(), g[f"{case}_upper"], rtol=1e-5, atol=1e-6)
