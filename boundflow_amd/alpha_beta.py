@@ -530,14 +530,20 @@ def _optimise_general(module, spec, trace, chain, linear_spec_C, bound, grad, ou
 
 
 def run_alpha_crown_mlp(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.2,
-                        alpha_init: float = 0.5, warm_start: Optional[Dict[str, torch.Tensor]] = None,
+                        alpha_init: float = 0.5, objective: str = "lower", spec_reduce: str = "mean",
+                        soft_tau: float = 1.0, lb_weight: float = 1.0, ub_weight: float = 1.0,
+                        warm_start: Optional[Dict[str, torch.Tensor]] = None,
                         relu_split_state=None, trace: Optional[ForwardTrace] = None):
     """HIP counterpart of run_alpha_crown_mlp (alpha_crown.py:137-261): alpha shared
-    by all domains, loss -mean(lb), no split multipliers.  ``warm_start`` maps
-    ReLU input names to alpha tensors of the ReLU's logical shape."""
+    by all domains, no split multipliers, best-of on the batch mean of the
+    objective's metric.  The reference reduces "mean" over every [B, S] element at
+    once and the shared alpha-beta loop over specs and then domains: the same
+    value up to summation order.  ``warm_start`` maps ReLU input names to alpha
+    tensors of the ReLU's logical shape."""
     bounds, alpha, _beta, stats = run_alpha_beta_crown_mlp(
         module, input_spec, linear_spec_C=linear_spec_C, relu_split_state=relu_split_state, steps=steps, lr=lr,
         alpha_init=alpha_init, warm_start_alpha=warm_start, per_batch_params=False, use_beta=False, trace=trace,
+        objective=objective, spec_reduce=spec_reduce, soft_tau=soft_tau, lb_weight=lb_weight, ub_weight=ub_weight,
         first_layer_certificate=False)   # alpha_crown.py has no certificate
     return bounds, alpha, stats
 

@@ -189,16 +189,16 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
     when they leave nothing (bab.py:524-628).
 
     A search tree never evaluates the same split set twice, so the reference's
-    node-evaluation cache cannot hit and has no counterpart.  Supported:
-    objective "lower", spec_reduce "mean".
+    node-evaluation cache cannot hit and has no counterpart.  The objective
+    options (objective, spec_reduce, soft_tau, lb_weight, ub_weight) go to every
+    node evaluation, as the reference forwards them (bab.py:461-466, :1095-1100,
+    :1334-1339); the node's verdict reads its lower bound whatever the objective.
     """
     cfg = config or BabConfig()
     if int(cfg.max_nodes) < 1:
         raise ValueError(f"max_nodes must be >=1, got {cfg.max_nodes}")
     if int(cfg.node_batch_size) < 1:
         raise ValueError(f"node_batch_size must be >=1, got {cfg.node_batch_size}")
-    if cfg.objective != "lower" or cfg.spec_reduce != "mean":
-        raise NotImplementedError("HIP BaB implements objective='lower', spec_reduce='mean'")
     if cfg.oracle not in ("alpha", "alpha_beta"):
         raise ValueError(f"unknown BaB oracle: {cfg.oracle}")
     spec = normalize_input_spec(input_spec)
@@ -332,6 +332,11 @@ def solve_bab_mlp(module, input_spec, *, linear_spec_C: Optional[torch.Tensor] =
                      per_example=per)
 
 
+def _objective_kw(cfg: BabConfig) -> dict:
+    return {"objective": cfg.objective, "spec_reduce": cfg.spec_reduce, "soft_tau": float(cfg.soft_tau),
+            "lb_weight": float(cfg.lb_weight), "ub_weight": float(cfg.ub_weight)}
+
+
 def _evaluate_nodes(module, spec, chain, shapes, linear_spec_C, items, front: _Frontier, names, cfg: BabConfig):
     """One round: gather the popped nodes' inputs, splits and warm starts from
     the frontier, run the oracle on all of them, and return per node whether it
@@ -375,13 +380,13 @@ def _evaluate_nodes(module, spec, chain, shapes, linear_spec_C, items, front: _F
             module, sub, linear_spec_C=C, relu_split_state=split_by, steps=int(cfg.alpha_steps),
             lr=float(cfg.alpha_lr), alpha_init=float(cfg.alpha_init), beta_init=float(cfg.beta_init),
             warm_start_alpha=warm_a, warm_start_beta=warm_b, per_batch_params=True, trace=trace,
-            first_layer_certificate=False)
+            first_layer_certificate=False, **_objective_kw(cfg))
     else:
         # alpha oracle: one node per round, shared alpha of that node, no split multipliers
         bounds, alpha, _stats = run_alpha_crown_mlp(
             module, sub, linear_spec_C=C, steps=int(cfg.alpha_steps), lr=float(cfg.alpha_lr),
             alpha_init=float(cfg.alpha_init), warm_start={n: v[0] for n, v in warm_a.items()},
-            relu_split_state=split_by, trace=trace)
+            relu_split_state=split_by, trace=trace, **_objective_kw(cfg))
         alpha = {n: v.reshape((1,) + tuple(v.shape)) for n, v in alpha.items()}
         beta = warm_b
     rows = [bounds.lower.min(dim=1).values.double(), bounds.upper.max(dim=1).values.double(),

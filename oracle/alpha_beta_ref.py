@@ -396,9 +396,43 @@ def run_alpha_crown(
     alpha_init: float = 0.5,
     relu_split_state=None,
     warm_start: Optional[Dict[str, torch.Tensor]] = None,
+    objective: str = "lower",
+    spec_reduce: str = "mean",
+    soft_tau: float = 1.0,
+    lb_weight: float = 1.0,
+    ub_weight: float = 1.0,
 ):
-    """alpha_crown.py:137-261 (shared alpha per ReLU, objective lower, mean over
-    specs); ``warm_start`` seeds alpha per ReLU input (alpha_crown.py:42-60)."""
+    """alpha_crown.py:137-261 (shared alpha per ReLU); ``warm_start`` seeds alpha
+    per ReLU input (alpha_crown.py:42-60).  The metric and loss of each objective
+    reduce over the whole [B, S] bound (alpha_crown.py:62-135): "mean" is the
+    mean of every element, "min"/"softmin" the batch mean of per-row reductions."""
+
+    def reduce_specs(x, direction):
+        if x.dim() != 2 or spec_reduce == "mean":
+            return x.mean()
+        if spec_reduce == "min":
+            return (x.min(dim=1).values if direction == "min" else x.max(dim=1).values).mean()
+        if spec_reduce == "softmin":
+            tau = float(soft_tau)
+            if tau <= 0.0:
+                raise ValueError(f"soft_tau must be >0, got {soft_tau}")
+            if direction == "min":
+                return (-tau * torch.logsumexp(-x / tau, dim=1)).mean()
+            return (tau * torch.logsumexp(x / tau, dim=1)).mean()
+        raise AssertionError(f"unreachable spec_reduce: {spec_reduce}")
+
+    def metric_of(bounds):
+        if objective == "lower":
+            return reduce_specs(bounds.lower, "min")
+        if objective == "upper":
+            return -reduce_specs(bounds.upper, "max")
+        if objective == "gap":
+            return -reduce_specs(bounds.upper - bounds.lower, "max")
+        if objective == "both":
+            return (float(lb_weight) * reduce_specs(bounds.lower, "min")
+                    - float(ub_weight) * reduce_specs(bounds.upper, "max"))
+        raise AssertionError(f"unreachable objective: {objective}")
+
     spec = normalize_input_spec(input_spec)
     interval_env, relu_pre = forward_ibp_trace(module, spec, relu_split_state=relu_split_state)
     alpha = {}
@@ -416,7 +450,7 @@ def run_alpha_crown(
     for step in range(int(steps) + 1):
         bounds = crown_backward_from_trace(module, spec, interval_env=interval_env, relu_pre=relu_pre,
                                            linear_spec_C=linear_spec_C, relu_alpha=alpha)
-        metric = bounds.lower.mean()
+        metric = metric_of(bounds)
         mv = float(metric.detach().item())
         if best_metric is None or mv > float(best_metric.item()):
             best_metric = metric.detach()
@@ -424,7 +458,7 @@ def run_alpha_crown(
             best_alpha = {k: v.detach().clone() for k, v in alpha.items()}
         if step == int(steps):
             break
-        loss = -bounds.lower.mean()
+        loss = -metric
         if not loss.requires_grad:   # no ambiguous ReLU left (alpha_crown.py:240-241)
             break
         opt.zero_grad(set_to_none=True)

@@ -67,6 +67,14 @@ class NodeInfeasible(ValueError):
     (bab.py:1058-1069, :1421-1431)."""
 
 
+def _objective_kw(cfg) -> dict:
+    """The objective options BabConfig forwards to every oracle call (bab.py:147-151,
+    :461-466, :1095-1100, :1334-1339)."""
+    return {"objective": cfg.get("objective", "lower"), "spec_reduce": cfg.get("spec_reduce", "mean"),
+            "soft_tau": float(cfg.get("soft_tau", 1.0)), "lb_weight": float(cfg.get("lb_weight", 1.0)),
+            "ub_weight": float(cfg.get("ub_weight", 1.0))}
+
+
 def _eval_single(module, spec, C, item: _Item, cfg):
     """eval_bab_alpha_beta_node / run_alpha_crown_mlp for one node; raises ValueError when
     the IBP trace is infeasible and NodeInfeasible when the certificate closes the node."""
@@ -75,14 +83,14 @@ def _eval_single(module, spec, C, item: _Item, cfg):
         bounds, alpha, beta, choices, feas = ab.run_alpha_beta_crown(
             module, spec, linear_spec_C=C, relu_split_state=split, steps=cfg["alpha_steps"], lr=cfg["alpha_lr"],
             alpha_init=cfg["alpha_init"], beta_init=cfg["beta_init"], warm_start_alpha=item.warm_alpha,
-            warm_start_beta=item.warm_beta, return_feasibility=True)
+            warm_start_beta=item.warm_beta, return_feasibility=True, **_objective_kw(cfg))
         if feas == "infeasible":
             raise NodeInfeasible("first-layer split certificate")
         hint = choices[0] if len(choices) == 1 else None
         return bounds, alpha, beta, hint
     bounds, alpha = ab.run_alpha_crown(module, spec, linear_spec_C=C, steps=cfg["alpha_steps"], lr=cfg["alpha_lr"],
                                        alpha_init=cfg["alpha_init"], relu_split_state=split,
-                                       warm_start=item.warm_alpha)
+                                       warm_start=item.warm_alpha, **_objective_kw(cfg))
     return bounds, alpha, None, None
 
 
@@ -305,7 +313,7 @@ def _eval_batch(module, spec, linear_spec_C, items, slots, shapes, cfg, live, do
             module, _slice_spec(spec, ex), linear_spec_C=C, relu_split_state=split_b,
             steps=cfg["alpha_steps"], lr=cfg["alpha_lr"], alpha_init=cfg["alpha_init"],
             beta_init=cfg["beta_init"], warm_start_alpha=warm_a, warm_start_beta=warm_b,
-            per_batch_params=True)
+            per_batch_params=True, **_objective_kw(cfg))
         if len(items) == 1 and choices is None:
             # one node left after pruning: the batched call's own certificate closed it
             live[ex[0]] = max(0, live[ex[0]] - 1)

@@ -341,7 +341,7 @@ def golden_vnnlib(tag):
 
 
 from tests.frontend_models import native_bab_toy, native_toy  # noqa: E402
-from tests.golden_util import OBJECTIVE_CASES, objective_workload  # noqa: E402
+from tests.golden_util import ALPHA_CROWN_OBJECTIVE_CASES, OBJECTIVE_CASES, objective_workload  # noqa: E402
 
 
 def golden_objectives(tag):
@@ -362,6 +362,23 @@ def golden_objectives(tag):
         arrays[f"{case}_upper"] = b.upper
     for n in names:
         arrays[f"split_{n}"] = splits[n]
+    save(tag, **arrays)
+
+
+def golden_alpha_crown_objectives(tag):
+    """run_alpha_crown_mlp (runtime/alpha_crown.py:137-261) with the objectives of
+    ALPHA_CROWN_OBJECTIVE_CASES on the objectives_mlp problem (shared alpha, the
+    same splits): the best bounds and alpha of each."""
+    from boundflow.runtime.alpha_crown import run_alpha_crown_mlp as r_alpha
+    w, splits = objective_workload()
+    rm, rs = to_ref_module(w.module), to_ref_spec(w.spec)
+    arrays = {"checksum": workload_checksum(w)}
+    for case, kw in ALPHA_CROWN_OBJECTIVE_CASES.items():
+        b, st, _stats = r_alpha(rm, rs, linear_spec_C=w.C, relu_split_state=splits, steps=8, lr=0.1, **kw)
+        arrays[f"{case}_lower"] = b.lower
+        arrays[f"{case}_upper"] = b.upper
+        for n, a in st.alpha_by_relu_input.items():
+            arrays[f"{case}_alpha_{n}"] = a
     save(tag, **arrays)
 
 
@@ -424,9 +441,12 @@ GOLDENS = [
     ("bab_solve_cert_fallback", golden_bab_solve),
     ("bab_solve_cert_prune", golden_bab_solve),
     ("bab_solve_1d", golden_bab_solve),
+    ("bab_solve_obj_both", golden_bab_solve),
+    ("bab_solve_obj_alpha_gap", golden_bab_solve),
     ("frontend_planned", golden_frontend),
     ("vnnlib_queries", golden_vnnlib),
     ("objectives_mlp", golden_objectives),
+    ("alpha_crown_objectives", golden_alpha_crown_objectives),
     ("native_toy_b4", golden_native),
     ("native_toy_budget", golden_native),
     ("native_mlp", golden_native),

@@ -50,6 +50,11 @@ BAB_SOLVE_CASES = {
     "bab_solve_1d": (dict(seed=3, eps=0.4, dims=(1, 8, 8, 2), batch=4),
                      dict(max_nodes=30, oracle="alpha_beta", node_batch_size=4, alpha_steps=5,
                           use_1d_linf_input_restriction_patch=True)),
+    "bab_solve_obj_both": (dict(eps=0.05), dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10,
+                                                objective="both", spec_reduce="softmin", soft_tau=0.5,
+                                                ub_weight=0.5)),
+    "bab_solve_obj_alpha_gap": (dict(eps=0.05), dict(max_nodes=20, oracle="alpha", node_batch_size=1,
+                                                     alpha_steps=10, objective="gap", spec_reduce="min")),
 }
 
 
@@ -63,6 +68,16 @@ OBJECTIVE_CASES = {
     "lower_min": dict(objective="lower", spec_reduce="min", per_batch_params=True),
     "lower_softmin": dict(objective="lower", spec_reduce="softmin", soft_tau=2.0, per_batch_params=True),
     "gap_mean_shared": dict(objective="gap", spec_reduce="mean", per_batch_params=False),
+}
+
+
+# run_alpha_crown_mlp options of the "alpha_crown_objectives" fixture (shared alpha);
+# alpha_crown.py:62-135
+ALPHA_CROWN_OBJECTIVE_CASES = {
+    "upper_mean": dict(objective="upper", spec_reduce="mean"),
+    "gap_min": dict(objective="gap", spec_reduce="min"),
+    "both_softmin": dict(objective="both", spec_reduce="softmin", soft_tau=0.5, lb_weight=1.0, ub_weight=0.5),
+    "lower_softmin": dict(objective="lower", spec_reduce="softmin", soft_tau=2.0),
 }
 
 

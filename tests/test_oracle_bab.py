@@ -14,7 +14,8 @@ import torch
 
 from boundflow_amd import workloads as wl
 from oracle import bab_ref
-from tests.golden_util import BAB_SOLVE_CASES, OBJECTIVE_CASES, load, objective_workload, workload_checksum
+from tests.golden_util import (ALPHA_CROWN_OBJECTIVE_CASES, BAB_SOLVE_CASES, OBJECTIVE_CASES, load, objective_workload,
+                               workload_checksum)
 
 CASES = BAB_SOLVE_CASES
 DEFAULTS = dict(use_branch_hint=True, alpha_lr=0.2, alpha_init=0.5, beta_init=0.0, threshold=0.0, tol=1e-6)
@@ -150,3 +151,20 @@ def test_objectives_match_reference(case):
                                               lr=0.1, **OBJECTIVE_CASES[case])
     np.testing.assert_allclose(b.lower.numpy(), g[f"{case}_lower"], rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(b.upper.numpy(), g[f"{case}_upper"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("case", list(ALPHA_CROWN_OBJECTIVE_CASES))
+def test_alpha_crown_objectives_match_reference(case):
+    """The oracle's shared-alpha objectives (alpha_crown.py:62-135, whole-[B, S]
+    "mean") against the reference's run_alpha_crown_mlp (fixture
+    alpha_crown_objectives): best bounds and best alpha after 8 Adam steps."""
+    from oracle import alpha_beta_ref as ab
+    g = load("alpha_crown_objectives")
+    w, splits = objective_workload()
+    assert workload_checksum(w) == str(g["checksum"])
+    b, alpha = ab.run_alpha_crown(w.module, w.spec, linear_spec_C=w.C, relu_split_state=splits, steps=8, lr=0.1,
+                                  **ALPHA_CROWN_OBJECTIVE_CASES[case])
+    np.testing.assert_allclose(b.lower.detach().numpy(), g[f"{case}_lower"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(b.upper.detach().numpy(), g[f"{case}_upper"], rtol=1e-5, atol=1e-6)
+    for n, a in alpha.items():
+        np.testing.assert_allclose(a.numpy(), g[f"{case}_alpha_{n}"], rtol=1e-5, atol=1e-6)
