@@ -2,6 +2,9 @@
 // configurations, and the small kernels around it: the relaxation table, the
 // concretization finalize and the split-K reduction.
 
+#include <cstdlib>
+#include <cstring>
+
 #include "bf_gemm_kernel.h"
 
 namespace bf {
@@ -43,40 +46,32 @@ __global__ void relax_table_kernel(const float* __restrict__ lo, const float* __
   out[i] = make_float4(r.au, r.bu, r.al, r.bl);
 }
 
-static int g_force_config = -1;   // tuning hook: -1 = automatic
+// BOUNDFLOW_GEMM_TILE=G or =H forces one configuration (for measurement); read
+// once when the library is loaded, constant afterwards.
+static int forced_tile_from_env() {
+  const char* v = std::getenv("BOUNDFLOW_GEMM_TILE");
+  if (v == nullptr) return 0;
+  if (std::strcmp(v, "G") == 0) return 'G';
+  if (std::strcmp(v, "H") == 0) return 'H';
+  return 0;
+}
+static const int kForcedTile = forced_tile_from_env();
 
 int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {
   if ((pro != PRO_PLAIN && pro != PRO_RELAX) || (epi != EPI_STORE && epi != EPI_ABSSUM && epi != EPI_RELAX)) {
     set_error("gemm_dispatch: bad mode pro=%d epi=%d", pro, epi);
     return BF_EINVAL;
   }
-  switch (g_force_config) {
-    case 0: return launch_tile<TileA>(a, pro, epi, nz, stream);
-    // the relaxation epilogue exists for the 128 x 128 configurations (TileA, TileG)
-    case 1: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileB>(a, pro, epi, nz, stream);
-    case 2: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileC>(a, pro, epi, nz, stream);
-    case 3:
-      // the |C| epilogues need BN == NORM_BN; TileD is a store-only configuration
-      if (epi == EPI_STORE) return launch_tile<TileD>(a, pro, epi, nz, stream);
-      return launch_tile<TileA>(a, pro, epi, nz, stream);
-    case 4: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileE>(a, pro, epi, nz, stream);
-    case 5: return epi == EPI_RELAX ? launch_tile<TileA>(a, pro, epi, nz, stream) : launch_tile<TileF>(a, pro, epi, nz, stream);
-    case 6: return launch_tile<TileG>(a, pro, epi, nz, stream);
-    case 7: return launch_tile<TileH>(a, pro, epi, nz, stream);
-    default: {
-      // automatic (measured on the five benchmark shapes): the 8-wave TileG at 3
-      // workgroups per CU for every form; a grid with fewer 128 x 128 tiles than the
-      // device has CUs takes the 16-wave TileH instead, which spreads each tile's
-      // contraction over twice the waves.
-      const int64_t ks = (pro == PRO_PLAIN && epi == EPI_STORE && a.ksplit > 1) ? a.ksplit : 1;
-      const int64_t wgs = ceil_div(a.M, 128) * ceil_div(a.N, 128) * nz * ks;
-      if (wgs < 256) return launch_tile<TileH>(a, pro, epi, nz, stream);
-      return launch_tile<TileG>(a, pro, epi, nz, stream);
-    }
-  }
+  if (kForcedTile == 'G') return launch_tile<TileG>(a, pro, epi, nz, stream);
+  if (kForcedTile == 'H') return launch_tile<TileH>(a, pro, epi, nz, stream);
+  // measured on the benchmark shapes: the 8-wave TileG at 3 workgroups per CU for
+  // every form; a grid with fewer 128 x 128 tiles than the device has CUs takes the
+  // 16-wave TileH instead, which spreads each tile's contraction over twice the waves.
+  const int64_t ks = (pro == PRO_PLAIN && epi == EPI_STORE && a.ksplit > 1) ? a.ksplit : 1;
+  const int64_t wgs = ceil_div(a.M, 128) * ceil_div(a.N, 128) * nz * ks;
+  if (wgs < 256) return launch_tile<TileH>(a, pro, epi, nz, stream);
+  return launch_tile<TileG>(a, pro, epi, nz, stream);
 }
-
-void gemm_force_config(int cfg) { g_force_config = cfg; }
 
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
                         const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream) {

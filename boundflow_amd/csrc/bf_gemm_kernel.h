@@ -25,7 +25,7 @@
 // share an A row-block share that XCD's L2.
 //
 // This header holds the kernel template and its launcher; each tile
-// configuration is instantiated in its own translation unit (bf_gemm_tile*.hip)
+// configuration is instantiated in its own translation unit (bf_gemm_tile_*.hip)
 // so that the configurations compile in parallel.
 
 #pragma once
@@ -55,7 +55,9 @@ struct Tile {
   static constexpr int BPT = BK + 4;                 // Bs row pitch (n-major [n][k], for either B layout)
   static constexpr int KQ = BK / 4;                  // float4 per A row per K tile
   static constexpr int A_SLOTS = BM * BK / 4 / NT;
-  static constexpr int B_SLOTS = BN * BK / 4 / NT;
+  static constexpr int B_QUADS = BN * BK / 4;         // float4 of a B tile
+  static constexpr int B_SLOTS = (B_QUADS + NT - 1) / NT;
+  static constexpr bool B_FULL = B_QUADS % NT == 0;   // else the last slot is partly idle
   static constexpr int RPP = NT / KQ;                // A rows covered per slot index
   static constexpr int BS_FLOATS = BN * BPT;
   // Relaxation operands staged in LDS per K tile: one (domain, k) entry per
@@ -64,7 +66,7 @@ struct Tile {
   static constexpr int TAB_ENTRIES = NT < 256 ? NT : 256;
   static constexpr int TAB_DOMS = TAB_ENTRIES / BK;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
-  static_assert((BM * BK) % (4 * NT) == 0 && (BN * BK) % (4 * NT) == 0, "tile/thread mismatch");
+  static_assert((BM * BK) % (4 * NT) == 0 && NT % KQ == 0, "tile/thread mismatch");
   static_assert((BK & (BK - 1)) == 0 && BK >= 8, "BK must be a power of two >= 8");
 };
 
@@ -81,17 +83,56 @@ __device__ __forceinline__ float fsel(const float4& r, bool lower, bool nonneg, 
 // since binding its larger state to the plain kernel's budget spills.
 template <int PRO, class T>
 constexpr int gemm_waves_per_simd() {
-  return (PRO == PRO_PLAIN && T::OCC * T::NT / 256 > T::OCC) ? T::OCC * T::NT / 256 : T::OCC;
+  constexpr int per_simd = (T::OCC * T::NT + 255) / 256;   // OCC workgroups' waves, the busiest SIMD
+  return (PRO == PRO_PLAIN && per_simd > T::OCC) ? per_simd : T::OCC;
 }
 
-template <int PRO, int EPI, bool TRANS_B, class T>
+// LDS-DMA waits and the workgroup barrier of the direct-to-LDS main loop, as
+// inline assembly so that the compiler adds no wait of its own for the copies
+// still in flight (a fence would wait for every one of them).
+// One global_load_lds_dwordx4: lane l's 16 bytes at src land at lds_dst + 16 l
+// (lds_dst wave-uniform).  Issued as inline assembly so that the compiler does
+// not track the copy and adds no wait before the LDS reads of other stages; the
+// loop orders it with wait_vmem and lds_barrier.  M0 holds the LDS address (no
+// other code of the kernel uses M0).
+typedef __attribute__((address_space(3))) float lds_float;
+__device__ __forceinline__ void lds_copy16(const float* src, float* lds_dst) {
+  const uint32_t off = (uint32_t)(uintptr_t)((lds_float*)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(off) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// DL: the direct-to-LDS main loop (plain prologue, transposed B, BK 16, aligned
+// float4 operands): three LDS stages filled by global_load_lds_dwordx4, two K
+// tiles in flight while the third is multiplied, one barrier per K tile.  Each
+// 1 KB stage chunk holds 16 rows x 4 float4 of k, float4 kq of row r at position
+// 4 r + (kq ^ swz(r)), swz(r) = (r >> 1) & 3, so that the MFMA operand reads of
+// 32 rows hit distinct banks.  The reduction order is that of the register-staged
+// loop (lane half h takes k = 8 h + 4 jq + e of each K tile), so both give the
+// same bits.
+template <int PRO, int EPI, bool TRANS_B, class T, bool DL = false>
 __global__ void __launch_bounds__(T::NT, (gemm_waves_per_simd<PRO, T>()))
 gemm_kernel(GemmArgs p) {
   constexpr int GBM = T::BM, GBN = T::BN, GBK = T::BK, GNT = T::NT;
   constexpr int AP = T::AP, BPT = T::BPT, A_SLOTS = T::A_SLOTS, B_SLOTS = T::B_SLOTS;
   constexpr int KQ = T::KQ, RPP = T::RPP, FM = T::FM, FN = T::FN;
-  __shared__ __attribute__((aligned(16))) float As[2][GBM * AP];
-  __shared__ __attribute__((aligned(16))) float Bs[2][T::BS_FLOATS];
+  static_assert(!DL || (PRO == PRO_PLAIN && TRANS_B && GBK == 16 && GBM % 16 == 0 && GBN % 16 == 0 &&
+                        T::WTM % 8 == 0 && T::WTN % 8 == 0),
+                "direct-to-LDS loop: plain prologue, transposed B, BK 16");
+  constexpr int NSTAGE = DL ? 3 : 2;
+  constexpr int A_STAGE = DL ? GBM * GBK : GBM * AP;
+  constexpr int B_STAGE = DL ? GBN * GBK : T::BS_FLOATS;
+  // the A and B stages, one array: the relaxation epilogue stages its operands over all of it
+  __shared__ __attribute__((aligned(16))) float smem_ab[NSTAGE * (A_STAGE + B_STAGE)];
+  float (*As)[A_STAGE] = reinterpret_cast<float (*)[A_STAGE]>(smem_ab);
+  float (*Bs)[B_STAGE] = reinterpret_cast<float (*)[B_STAGE]>(smem_ab + NSTAGE * A_STAGE);
   __shared__ float red[T::NWN][GBM];
   constexpr int TE = (PRO == PRO_RELAX) ? T::TAB_ENTRIES : 1;
   constexpr int TK = (PRO == PRO_RELAX) ? GBK : 1;
@@ -153,7 +194,39 @@ gemm_kernel(GemmArgs p) {
   float4 a_reg[A_SLOTS];
   float4 b_reg[B_SLOTS];
 
-  auto load_tiles = [&](int64_t k0) {
+  // B-tile ownership (transposed B): float4 slot q = t + GNT*j -> column n0 + q / KQ,
+  // k quad q % KQ.  On the unchecked path a column past N reads column N - 1 and a
+  // row past M reads row 0: their products land in rows / columns no epilogue keeps.
+  uint32_t b_off[B_SLOTS];
+#pragma unroll
+  for (int j = 0; j < B_SLOTS; ++j) {
+    const int q = t + GNT * j;
+    const int64_t gn = n0 + q / KQ;
+    b_off[j] = (uint32_t)((gn < N ? gn : N - 1) * p.ldb + 4 * (q % KQ));
+  }
+  const bool unchecked = PRO == PRO_PLAIN && TRANS_B && vec_a && vec_b && ((K - kbase) % GBK == 0);
+
+  // unchk: every K tile of this workgroup is whole and every operand row is
+  // float4-aligned (uniform), so the loads need no bounds checks
+  auto load_tiles = [&](int64_t k0, auto unchk_c) {
+    if constexpr (TRANS_B && decltype(unchk_c)::value) {
+#pragma unroll
+      for (int j = 0; j < A_SLOTS; ++j)
+        a_reg[j] = *reinterpret_cast<const float4*>(A + a_base[j] + k0 + 4 * a_kq);
+#pragma unroll
+      for (int j = 0; j < B_SLOTS; ++j) {
+        if (!T::B_FULL && t + GNT * j >= T::B_QUADS) {
+          b_reg[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+          continue;
+        }
+        float4 v = *reinterpret_cast<const float4*>(p.B + b_off[j] + (uint32_t)k0);
+        if (abs_b) {
+          v.x = fabsf(v.x); v.y = fabsf(v.y); v.z = fabsf(v.z); v.w = fabsf(v.w);
+        }
+        b_reg[j] = v;
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < A_SLOTS; ++j) {
       const int64_t m = m0 + a_r0 + RPP * j;
@@ -176,6 +249,10 @@ gemm_kernel(GemmArgs p) {
     for (int j = 0; j < B_SLOTS; ++j) {
       const int q = t + GNT * j;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!T::B_FULL && q >= T::B_QUADS) {
+        b_reg[j] = v;
+        continue;
+      }
       if (TRANS_B) {
         const int n = q / KQ, kq = q % KQ;
         const int64_t gn = n0 + n, gk = k0 + 4 * kq;
@@ -256,7 +333,7 @@ gemm_kernel(GemmArgs p) {
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int64_t wcol0 = n0 + (int64_t)(wave_u % T::NWN) * T::WTN;
   const int fn_act = wcol0 >= N ? 0 : (int)(ceil_div(N - wcol0, 32) < FN ? ceil_div(N - wcol0, 32) : FN);
-  auto main_loop = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c, auto full_c) {
+  auto main_loop = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c, auto full_c, auto unchk_c) {
     constexpr bool FAST = decltype(fast_c)::value;
     constexpr bool ADD = decltype(add_c)::value;
     constexpr bool KB = decltype(kb_c)::value;
@@ -350,6 +427,7 @@ gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < B_SLOTS; ++j) {
         const int q = t + GNT * j;
+        if (!T::B_FULL && q >= T::B_QUADS) continue;
         const int n = TRANS_B ? q / KQ : q % GBN;
         const int kq = TRANS_B ? q % KQ : q / GBN;
         *reinterpret_cast<float4*>(&Bs[buf][n * BPT + 4 * kq]) = b_reg[j];
@@ -397,7 +475,7 @@ gemm_kernel(GemmArgs p) {
       load_tab(GBK);
       store_tab(1);
     }
-    load_tiles(kbase);
+    load_tiles(kbase, unchk_c);
     __syncthreads();
     store_tiles(0, kbase, 0);
     __syncthreads();
@@ -405,7 +483,7 @@ gemm_kernel(GemmArgs p) {
     for (int64_t kt = 0; kt < nk; ++kt) {
       const bool more = kt + 1 < nk;
       const bool more2 = kt + 2 < nk;
-      if (more) load_tiles(kbase + (kt + 1) * GBK);
+      if (more) load_tiles(kbase + (kt + 1) * GBK, unchk_c);
       if (more2) load_tab((kt + 2) * GBK);
       mfma_tile(buf);
       if (more) store_tiles(buf ^ 1, kbase + (kt + 1) * GBK, kt + 1);
@@ -420,10 +498,135 @@ gemm_kernel(GemmArgs p) {
   using FF = std::false_type;
   const bool full = fn_act == FN;   // wave-uniform
   auto run = [&](auto fast_c, auto add_c, auto kb_c, auto rr_c) {
-    if (full) main_loop(fast_c, add_c, kb_c, rr_c, TT{});
-    else main_loop(fast_c, add_c, kb_c, rr_c, FF{});
+    if constexpr (PRO != PRO_PLAIN || !TRANS_B) {
+      if (full) main_loop(fast_c, add_c, kb_c, rr_c, TT{}, FF{});
+      else main_loop(fast_c, add_c, kb_c, rr_c, FF{}, FF{});
+    } else if (unchecked) {
+      if (full) main_loop(fast_c, add_c, kb_c, rr_c, TT{}, TT{});
+      else main_loop(fast_c, add_c, kb_c, rr_c, FF{}, TT{});
+    } else {
+      if (full) main_loop(fast_c, add_c, kb_c, rr_c, TT{}, FF{});
+      else main_loop(fast_c, add_c, kb_c, rr_c, FF{}, FF{});
+    }
   };
-  if constexpr (PRO == PRO_PLAIN) {
+  if constexpr (DL) {
+    // ---- direct-to-LDS main loop ----
+    constexpr int A_CHUNKS = GBM / 16, B_CHUNKS = GBN / 16, NW = GNT / 64;
+    constexpr int A_PW = (A_CHUNKS + NW - 1) / NW, B_PW = (B_CHUNKS + NW - 1) / NW;
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    // this lane's copy slots: chunk c = wave + NW j, row 16 c + lane / 4, stored float4
+    // lane % 4 holding k quad (lane % 4) ^ swz(row); rows past M / N read row M-1 / N-1
+    const int sl_q = lane & 3;
+    int64_t a_row[A_PW];
+    int a_kq[A_PW];
+#pragma unroll
+    for (int j = 0; j < A_PW; ++j) {
+      const int r = 16 * (wave_s + NW * j) + (lane >> 2);
+      const int64_t m = m0 + r < M ? m0 + r : M - 1;
+      const int64_t d = m / p.S;
+      a_row[j] = d * p.lda_d + (m - d * p.S) * p.lda;
+      a_kq[j] = sl_q ^ ((r >> 1) & 3);
+    }
+    uint32_t b_row[B_PW];
+    int b_kq[B_PW];
+#pragma unroll
+    for (int j = 0; j < B_PW; ++j) {
+      const int r = 16 * (wave_s + NW * j) + (lane >> 2);
+      const int64_t n = n0 + r < N ? n0 + r : N - 1;
+      b_row[j] = (uint32_t)(n * p.ldb);
+      b_kq[j] = sl_q ^ ((r >> 1) & 3);
+    }
+    constexpr int PER_STAGE_A = A_CHUNKS % NW == 0 ? A_PW : -1;
+    constexpr int PER_STAGE_B = B_CHUNKS % NW == 0 ? B_PW : -1;
+    static_assert(PER_STAGE_A > 0 && PER_STAGE_B > 0, "every wave issues the same copies per stage");
+    constexpr int COPIES = PER_STAGE_A + PER_STAGE_B;   // vmem operations per stage and wave
+    // copy K tile [k0, k0 + 16) into a stage; quads at or past K read the row start
+    // and are zeroed by fix_tail once they have landed
+    auto issue = [&](int st, int64_t k0) {
+#pragma unroll
+      for (int j = 0; j < A_PW; ++j) {
+        const int64_t k = k0 + 4 * a_kq[j];
+        const float* src = A + a_row[j] + (k < K ? k : 0);
+        lds_copy16(src, &As[st][(wave_s + NW * j) * 256]);
+      }
+#pragma unroll
+      for (int j = 0; j < B_PW; ++j) {
+        const int64_t k = k0 + 4 * b_kq[j];
+        const float* src = p.B + b_row[j] + (uint32_t)(k < K ? k : 0);
+        lds_copy16(src, &Bs[st][(wave_s + NW * j) * 256]);
+      }
+    };
+    auto fix_tail = [&](int st, int64_t k0) {
+#pragma unroll
+      for (int j = 0; j < A_PW; ++j)
+        if (k0 + 4 * a_kq[j] >= K)
+          *reinterpret_cast<float4*>(&As[st][(wave_s + NW * j) * 256 + 4 * lane]) = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < B_PW; ++j)
+        if (k0 + 4 * b_kq[j] >= K)
+          *reinterpret_cast<float4*>(&Bs[st][(wave_s + NW * j) * 256 + 4 * lane]) = make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    // operand positions (floats) of this lane: row wm WTM + 32 i + lrow (n: wn WTN + 32 jj + lrow),
+    // k quad 2 h + jq; swz of the row is (lrow >> 1) & 3 since the block offsets are multiples of 8
+    const int swz = (lrow >> 1) & 3;
+    int a_pos[FM][2], b_pos[FN][2];
+#pragma unroll
+    for (int jq = 0; jq < 2; ++jq) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a_pos[i][jq] = 4 * (4 * (wm * T::WTM + 32 * i + lrow) + ((2 * h + jq) ^ swz));
+#pragma unroll
+      for (int jj = 0; jj < FN; ++jj) b_pos[jj][jq] = 4 * (4 * (wn * T::WTN + 32 * jj + lrow) + ((2 * h + jq) ^ swz));
+    }
+    auto dl_loop = [&](auto full_c) {
+      constexpr bool FULL = decltype(full_c)::value;
+      const bool tail = (K - kbase) % GBK != 0;
+      const int nki = (int)nk;   // K tiles of this workgroup (K < 2^31)
+      issue(0, kbase);
+      if (nki > 1) issue(1, kbase + GBK);
+      int st = 0, st2 = 2;   // stage of tile kt, stage refilled with tile kt + 2
+      for (int kt = 0; kt < nki; ++kt) {
+        if (kt + 1 < nki) wait_vmem<COPIES>(); else wait_vmem<0>();
+        if (tail && kt + 1 == nki) fix_tail(st, kbase + (int64_t)kt * GBK);
+        lds_barrier();   // tile kt visible; every wave is done with the stage refilled next
+        if (kt + 2 < nki) issue(st2, kbase + (int64_t)(kt + 2) * GBK);
+        const float* __restrict__ as = As[st];
+        const float* __restrict__ bs = Bs[st];
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int jq = 0; jq < 2; ++jq) {
+          float av[FM][4];
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            const float4 a4 = *reinterpret_cast<const float4*>(&as[a_pos[i][jq]]);
+            av[i][0] = a4.x; av[i][1] = a4.y; av[i][2] = a4.z; av[i][3] = a4.w;
+          }
+          float bv[FN][4];
+#pragma unroll
+          for (int jj = 0; jj < FN; ++jj) {
+            float4 b4 = *reinterpret_cast<const float4*>(&bs[b_pos[jj][jq]]);
+            if (abs_b) {
+              b4.x = fabsf(b4.x); b4.y = fabsf(b4.y); b4.z = fabsf(b4.z); b4.w = fabsf(b4.w);
+            }
+            bv[jj][0] = b4.x; bv[jj][1] = b4.y; bv[jj][2] = b4.z; bv[jj][3] = b4.w;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+              for (int jj = 0; jj < FN; ++jj)
+                if (FULL || jj < fn_act)
+                  acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        st = st == 2 ? 0 : st + 1;
+        st2 = st2 == 2 ? 0 : st2 + 1;
+      }
+      lds_barrier();   // every wave is done with the stages before an epilogue reuses them
+    };
+    if (full) dl_loop(TT{});
+    else dl_loop(FF{});
+  } else if constexpr (PRO == PRO_PLAIN) {
     run(FF{}, FF{}, FF{}, FF{});
   } else {
     const bool kb = p.kbias != nullptr;
@@ -462,17 +665,26 @@ gemm_kernel(GemmArgs p) {
     float* __restrict__ C = split ? p.part + (int64_t)blockIdx.y * M * N : p.C[z];   // partial (z, kc)
     const int64_t ldc = split ? N : p.ldc;
     const bool r1 = !split && p.r1_row;
+    const bool fits32 = M < (1LL << 31);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row >= M) continue;
+        // the row's rank-1 factor and vector, once per row (no division when the vector is shared)
+        float rf = 0.f;
+        const float* __restrict__ vrow = p.r1_col;
+        if (r1) {
+          rf = p.r1_row[row];
+          if (p.r1_ld) vrow += div_rows(row, p.S, fits32) * p.r1_ld;
+        }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (row < M && col < N) {
+        for (int j = 0; j < FN; ++j) {
+          const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
+          if (col < N) {
             float v = acc[i][j][r];
-            if (r1) v = v + p.r1_row[row] * p.r1_col[(row / p.S) * p.r1_ld + col];
+            if (r1) v = v + rf * vrow[col];
             C[row * ldc + col] = v;
           }
         }
@@ -481,18 +693,19 @@ gemm_kernel(GemmArgs p) {
     static_assert(GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
     // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order.
     float rs[FM][16];
+    const bool fits32 = M < (1LL << 31);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int64_t d = (row < M) ? row / p.S : 0;
+        const int64_t d = (p.wvec && row < M) ? div_rows(row, p.S, fits32) : 0;
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
           const float a = acc[i][j][r];
-          float v = fabsf(a);
+          float v = col < N ? fabsf(a) : 0.f;   // columns past N hold products no one keeps
           float wgt = 1.f;
           if (p.wvec) {
             wgt = (row < M && col < N) ? p.wvec[d * p.w_ld + col] : 0.f;
@@ -543,14 +756,14 @@ gemm_kernel(GemmArgs p) {
     // As / Bs are free once every wave has left the main loop: As holds the
     // relaxation entries of the tile's domains x columns, Bs the split term,
     // the center vector, the bias and the domain of each row.
-    constexpr int E_DOMS = (2 * GBM * AP) / (4 * GBN);
-    static_assert(2 * E_DOMS * GBN + GBN + GBM <= 2 * T::BS_FLOATS, "epilogue slices exceed the B stage");
+    // per (domain, column) entry: the float4 relaxation, the split term and the center
+    constexpr int E_DOMS = (NSTAGE * (A_STAGE + B_STAGE)) / (6 * GBN);
+    __shared__ float Ke[GBN];
+    __shared__ int Re[GBM];
     __syncthreads();
-    float4* Te = reinterpret_cast<float4*>(&As[0][0]);
-    float* Ae = &Bs[0][0];
+    float4* Te = reinterpret_cast<float4*>(smem_ab);
+    float* Ae = smem_ab + 4 * E_DOMS * GBN;
     float* Ce = Ae + E_DOMS * GBN;
-    float* Ke = Ce + E_DOMS * GBN;
-    int* Re = reinterpret_cast<int*>(Ke + GBN);
     const int64_t m_last = (m0 + GBM < M ? m0 + GBM : M) - 1;
     const int e_first = (int)(m0 / p.S);
     const int endom = (int)(m_last / p.S) - e_first + 1;
@@ -577,6 +790,7 @@ gemm_kernel(GemmArgs p) {
     float* __restrict__ C = p.C[z];
     float* __restrict__ Cpre = p.C_pre[z];
     float pb[FM][16], pc[FM][16];
+    const bool fits32 = M < (1LL << 31);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -584,6 +798,19 @@ gemm_kernel(GemmArgs p) {
         const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         const int64_t row = m0 + rloc;
         float sb = 0.f, sc = 0.f;
+        // the row's domain, once per row: its LDS entry block, or its rows of the global operands
+        int eq = 0;
+        const float4* __restrict__ erow = p.e_relax;
+        const float* __restrict__ arow = p.e_add;
+        const float* __restrict__ crow = p.e_cvec;
+        if (staged) {
+          eq = Re[rloc] * GBN;
+        } else if (row < M) {
+          const int64_t d = div_rows(row, p.S, fits32);
+          erow += d * N;
+          if (add_e) arow += d * p.e_add_ld;
+          if (cv_e) crow += d * p.e_cvec_ld;
+        }
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const int cloc = wn * T::WTN + j * 32 + lrow;
@@ -593,16 +820,15 @@ gemm_kernel(GemmArgs p) {
             float4 e;
             float add = 0.f, cv = 0.f, kb = 0.f;
             if (staged) {
-              const int q = Re[rloc] * GBN + cloc;
+              const int q = eq + cloc;
               e = Te[q];
               if (add_e) add = Ae[q];
               if (cv_e) cv = Ce[q];
               kb = Ke[cloc];
             } else {
-              const int64_t d = row / p.S;
-              e = p.e_relax[d * N + col];
-              if (add_e) add = p.e_add[d * p.e_add_ld + col];
-              if (cv_e) cv = p.e_cvec[d * p.e_cvec_ld + col];
+              e = erow[col];
+              if (add_e) add = arow[col];
+              if (cv_e) cv = crow[col];
               if (kb_e) kb = p.e_kbias[col];
             }
             if (Cpre) Cpre[row * p.ldc + col] = a;
@@ -656,14 +882,7 @@ gemm_kernel(GemmArgs p) {
   }
 }
 
-// Tile configurations (selected at run time by launch_gemm; a fixed one can be
-// forced through bf_tuning_set_gemm_tile).
-using TileA = Tile<128, 128, 16, 2, 2, 3>;   // 4 waves of 64x64, 3 workgroups per CU
-using TileB = Tile<128, 128, 32, 2, 2, 2>;   // deeper K tile, 2 workgroups per CU
-using TileC = Tile<256, 128, 16, 4, 2, 1>;   // 8 waves of 64x64
-using TileD = Tile<128, 256, 16, 2, 2, 2>;   // 4 waves of 64x128 (store epilogue only)
-using TileE = Tile<64, 128, 16, 1, 2, 4>;    // 2 waves of 64x64: more workgroups for short M
-using TileF = Tile<128, 128, 16, 2, 2, 2>;   // TileA at 2 workgroups per CU
+// Tile configurations (selected per call by gemm_dispatch).
 using TileG = Tile<128, 128, 16, 4, 2, 3>;   // 8 waves of 32x64: twice the waves per CU of TileA
 using TileH = Tile<128, 128, 32, 4, 4, 2>;   // 16 waves of 32x32, BK 32, 2 workgroups per CU (64 VGPRs)
 
@@ -676,6 +895,17 @@ static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
   BF_REQUIRE(ntiles + 8 < (1LL << 31), "gemm grid too large (M=%lld N=%lld)", (long long)a.M, (long long)a.N);
   const unsigned gy = (PRO == PRO_PLAIN && EPI == EPI_STORE && a.ksplit > 1) ? (unsigned)(a.ksplit * nz) : (unsigned)nz;
   dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), gy);
+  if constexpr (PRO == PRO_PLAIN && T::BK == 16) {
+    // the direct-to-LDS loop copies whole aligned float4s
+    bool dl = a.trans_b && (a.K & 3) == 0 && (a.lda & 3) == 0 && (a.lda_d & 3) == 0 && (a.ldb & 3) == 0 &&
+              ((uintptr_t)a.B & 15) == 0;
+    for (int z = 0; z < nz; ++z) dl = dl && ((uintptr_t)a.A[z] & 15) == 0;
+    if (dl) {
+      hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T, true>), grid, dim3(T::NT), 0, stream, a);
+      BF_LAUNCH_CHECK("gemm_kernel");
+      return BF_OK;
+    }
+  }
   if (a.trans_b) {
     hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T>), grid, dim3(T::NT), 0, stream, a);
   } else {
@@ -700,11 +930,11 @@ int launch_tile(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream)
   int launch_tile<T>(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {      \
     if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_gemm_t<PRO_PLAIN, EPI_STORE, T>(a, nz, stream);   \
     if (pro == PRO_RELAX && epi == EPI_STORE) return launch_gemm_t<PRO_RELAX, EPI_STORE, T>(a, nz, stream);   \
-    if constexpr (T::BN == NORM_BN) {                                                        \
+    if constexpr (T::BN == NORM_BN && T::BM <= 128) {                                        \
       if (pro == PRO_PLAIN && epi == EPI_ABSSUM) return launch_gemm_t<PRO_PLAIN, EPI_ABSSUM, T>(a, nz, stream); \
       if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_gemm_t<PRO_RELAX, EPI_ABSSUM, T>(a, nz, stream); \
     }                                                                                        \
-    if constexpr (T::BN == NORM_BN && T::BM == 128) {                                        \
+    if constexpr (T::BN == NORM_BN && T::BM <= 128) {                                        \
       if (pro == PRO_PLAIN && epi == EPI_RELAX) return launch_gemm_t<PRO_PLAIN, EPI_RELAX, T>(a, nz, stream);   \
       if (pro == PRO_RELAX && epi == EPI_RELAX) return launch_gemm_t<PRO_RELAX, EPI_RELAX, T>(a, nz, stream);   \
     }                                                                                        \
@@ -712,12 +942,6 @@ int launch_tile(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream)
     return BF_EINVAL;                                                                        \
   }
 
-template <> int launch_tile<TileA>(const GemmArgs&, int, int, int, hipStream_t);
-template <> int launch_tile<TileB>(const GemmArgs&, int, int, int, hipStream_t);
-template <> int launch_tile<TileC>(const GemmArgs&, int, int, int, hipStream_t);
-template <> int launch_tile<TileD>(const GemmArgs&, int, int, int, hipStream_t);
-template <> int launch_tile<TileE>(const GemmArgs&, int, int, int, hipStream_t);
-template <> int launch_tile<TileF>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileG>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileH>(const GemmArgs&, int, int, int, hipStream_t);
 

@@ -36,7 +36,6 @@ int rows_finalize(const float* b_src, const float* pb, const float* pc, int npar
 int gemm_ksplit(int64_t M, int64_t N, int64_t K, int64_t* kchunk);
 int splitk_reduce(const float* part, int ks, int64_t M, int64_t N, float* C, int64_t ldc, const float* r_row,
                   const float* v_col, int64_t v_ld, int64_t S, hipStream_t stream);
-void gemm_force_config(int cfg);
 int relax_table(const float* lo, const float* hi, const float* alpha, int64_t alpha_ld, int64_t D, int64_t K,
                 float4* out, hipStream_t stream);
 
@@ -862,12 +861,6 @@ using namespace bf;
 extern "C" {
 
 int bf_abi_version(void) { return 1; }
-
-int bf_tuning_set_gemm_tile(int config) {
-  BF_REQUIRE(config >= -1 && config <= 7, "bf_tuning_set_gemm_tile: config must be -1 (automatic) or 0..7");
-  gemm_force_config(config);
-  return BF_OK;
-}
 
 const char* bf_last_error(void) { return g_err; }
 

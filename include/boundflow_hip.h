@@ -30,16 +30,12 @@ typedef struct ihipStream_t* hipStream_t;
 int bf_abi_version(void);
 const char* bf_last_error(void);
 
-/* Tuning knob (no reference counterpart): force the contraction tile
- * configuration, -1 = automatic choice, 0..7 = fixed configuration
- * (0: 128x128x16 4 waves, 3 workgroups/CU; 1: 128x128x32; 2: 256x128x16 8 waves;
- * 3: 128x256x16, store epilogue only; 4: 64x128x16 2 waves; 5: 128x128x16 4 waves,
- * 2 workgroups/CU; 6: 128x128x16 8 waves of 32x64; 7: 128x128x32 16 waves of 32x32).
- * The automatic choice: 6 for every form, 7 when the grid has fewer 128 x 128
- * tiles (times bounds and split-K chunks) than the device has CUs.  The
- * relaxation epilogue runs on 0, 6 or 7 (1, 2, 4, 5 fall back to 0 for it).
- * Process-wide. */
-int bf_tuning_set_gemm_tile(int config);
+/* The contraction's tile configuration is chosen per call: 128 x 128 x 16 with
+ * 8 waves of 32 x 64 (3 workgroups per CU) for every form, 128 x 128 x 32 with
+ * 16 waves of 32 x 32 when the grid has fewer 128 x 128 tiles (times bounds and
+ * split-K chunks) than the device has CUs.  The environment variable
+ * BOUNDFLOW_GEMM_TILE=G or =H, read once when the library is loaded, forces one
+ * of the two for measurement. */
 
 /* ---- kernel #1: IBP ---------------------------------------------------- */
 

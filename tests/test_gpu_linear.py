@@ -387,24 +387,42 @@ def test_adam_clamp_matches_torch():
         assert torch.allclose(pd.cpu(), p.detach(), rtol=1e-6, atol=1e-7), float((pd.cpu() - p.detach()).abs().max())
 
 
-def test_multi_tensor_steps_equal_single_tensor_steps():
+def _placed(t: torch.Tensor, offset: int) -> torch.Tensor:
+    """A contiguous copy of ``t`` whose storage starts ``offset`` floats into a fresh buffer."""
+    buf = torch.empty(t.numel() + offset, device=t.device, dtype=t.dtype)
+    out = buf[offset:].view(t.shape)
+    out.copy_(t)
+    return out
+
+
+@pytest.mark.parametrize("layout", ["ragged", "quad", "quad_misaligned"])
+def test_multi_tensor_steps_equal_single_tensor_steps(layout):
     """bf_adam_clamp_multi, bf_masked_copy_rows_multi and bf_beta_coeff_multi give, tensor
     by tensor, bit for bit what the single-tensor entry points give (18 tensors: two
-    launches of the multi kernels; sizes not multiples of the workgroup)."""
+    launches of the multi kernels; sizes not multiples of the workgroup).  "ragged":
+    widths 3 + 41 i (the scalar path); "quad": widths that are multiples of 4 on
+    16-byte-aligned storage (the float4 path of the best-of copy and the split term);
+    "quad_misaligned": the same widths on storage one float off alignment (the scalar
+    fallback)."""
     dev = device()
-    announce("multi-tensor Adam / best-of copy / split term")
+    announce(f"multi-tensor Adam / best-of copy / split term ({layout})")
     g = torch.Generator().manual_seed(21)
     st = _lib.stream_handle()
     D = 37
-    cols = [3 + 41 * i for i in range(18)]
-    P = [torch.rand(D, c, generator=g).to(dev) for c in cols]
-    G = [torch.randn(D, c, generator=g).to(dev) for c in cols]
+    cols = [3 + 41 * i for i in range(18)] if layout == "ragged" else [4 * (1 + 13 * i) for i in range(18)]
+    off = 1 if layout == "quad_misaligned" else 0
+    P = [_placed(torch.rand(D, c, generator=g).to(dev), off) for c in cols]
+    G = [_placed(torch.randn(D, c, generator=g).to(dev), off) for c in cols]
+    if layout == "quad":
+        assert all(t.data_ptr() % 16 == 0 for t in P + G)
+    if layout == "quad_misaligned":
+        assert all(t.data_ptr() % 16 != 0 for t in P + G)
     clamps = [(0.0, 1.0) if i % 2 == 0 else (0.0, None) for i in range(len(cols))]
-    P1 = [t.clone() for t in P]
-    M0 = [torch.zeros_like(t) for t in P]
-    V0 = [torch.zeros_like(t) for t in P]
-    M1 = [torch.zeros_like(t) for t in P]
-    V1 = [torch.zeros_like(t) for t in P]
+    P1 = [_placed(t, off) for t in P]
+    M0 = [_placed(torch.zeros_like(t), off) for t in P]
+    V0 = [_placed(torch.zeros_like(t), off) for t in P]
+    M1 = [_placed(torch.zeros_like(t), off) for t in P]
+    V1 = [_placed(torch.zeros_like(t), off) for t in P]
     for step in (1, 2, 3):
         for i, t in enumerate(P):
             lo, hi = clamps[i]
@@ -418,15 +436,15 @@ def test_multi_tensor_steps_equal_single_tensor_steps():
     for i in range(len(P)):
         assert torch.equal(P[i], P1[i]) and torch.equal(M0[i], M1[i]) and torch.equal(V0[i], V1[i]), f"adam tensor {i}"
     mask = (torch.rand(D, generator=g) > 0.5).to(torch.int32).to(dev)
-    dst0 = [torch.zeros_like(t) for t in P]
-    dst1 = [torch.zeros_like(t) for t in P]
+    dst0 = [_placed(torch.zeros_like(t), off) for t in P]
+    dst1 = [_placed(torch.zeros_like(t), off) for t in P]
     for i, t in enumerate(P):
         _lib.call("bf_masked_copy_rows", _lib.ptr(dst0[i]), _lib.ptr(t), D, cols[i], _lib.ptr(mask), st)
     _lib.call("bf_masked_copy_rows_multi", len(P), _lib.ptr_array(dst1), _lib.ptr_array(P), _lib.i64_array(cols), D,
               _lib.ptr(mask), st)
-    splits = [torch.randint(-1, 2, (D, c), generator=g, dtype=torch.int8).to(dev) for c in cols]
-    out0 = [torch.empty_like(t) for t in P]
-    out1 = [torch.empty_like(t) for t in P]
+    splits = [_placed(torch.randint(-1, 2, (D, c), generator=g, dtype=torch.int8).to(dev), 4 * off) for c in cols]
+    out0 = [_placed(torch.empty_like(t), off) for t in P]
+    out1 = [_placed(torch.empty_like(t), off) for t in P]
     for i, t in enumerate(P):
         _lib.call("bf_beta_coeff", _lib.ptr(t), cols[i], _lib.ptr(splits[i]), cols[i], D, cols[i], _lib.ptr(out0[i]), st)
     _lib.call("bf_beta_coeff_multi", len(P), _lib.ptr_array(P), _lib.i64_array(cols), _lib.ptr_array(splits),
