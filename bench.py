@@ -78,11 +78,71 @@ def hip_runner(name: str):
     raise SystemExit(f"unknown config {name}")
 
 
+def executor_regions(name: str, dev):
+    """The fused ReLU -> affine regions of the C1 (X1) or C3 (X3) network as the
+    drop-in executor receives them (FusedReluAffineRequest, fused_crown.py:97-123):
+    for every Linear / Conv2d layer whose output feeds a ReLU, the coefficient of
+    the batch's 9 margin specs at that ReLU, the layer's weights, and synthetic
+    relaxations (upper slope in [0.1, 1] with intercept in [0, 0.5], lower slope
+    0 or 1, lower intercept 0)."""
+    import torch
+    from boundflow_amd import fused_crown as fc
+    from boundflow_amd import workloads as wl
+
+    w = wl.make("C1" if name == "X1" else "C3")
+    ops = w.module.get_entry_task().ops
+    params = w.module.params
+    g = torch.Generator().manual_seed(17)
+    B, S = w.batch, w.num_specs
+    x = w.spec.center
+    reqs = []
+    for i, op in enumerate(ops):
+        x_in = x
+        if op.op_type == "linear":
+            x = torch.nn.functional.linear(x, params[op.inputs[1]], params[op.inputs[2]])
+        elif op.op_type == "conv2d":
+            x = torch.nn.functional.conv2d(x, params[op.inputs[1]], params[op.inputs[2]], stride=op.attrs["stride"],
+                                           padding=op.attrs["padding"])
+        elif op.op_type == "relu":
+            x = torch.relu(x)
+        elif op.op_type == "flatten":
+            x = x.flatten(1)
+        feeds_relu = i + 1 < len(ops) and ops[i + 1].op_type == "relu" and ops[i + 1].inputs[0] == op.outputs[0]
+        if op.op_type not in ("linear", "conv2d") or not feeds_relu:
+            continue
+        n = int(x[0].numel())
+        au = torch.rand(B, n, generator=g) * 0.9 + 0.1
+        bu = torch.rand(B, n, generator=g) * 0.5
+        al = (torch.rand(B, n, generator=g) > 0.5).float()
+        reqs.append(fc.FusedReluAffineRequest(
+            kind=op.op_type, A_u=torch.randn(B, S, n, generator=g).to(dev), A_l=torch.randn(B, S, n, generator=g).to(dev),
+            alpha_u=au.to(dev), alpha_l=al.to(dev), beta_u=bu.to(dev), beta_l=torch.zeros(B, n, device=dev),
+            weight=params[op.inputs[1]].to(dev), bias=params[op.inputs[2]].to(dev),
+            input_shape=tuple(int(d) for d in x_in.shape[1:]), output_shape=tuple(int(d) for d in x.shape[1:]),
+            attrs=dict(op.attrs) if op.op_type == "conv2d" else {}))
+    return w, reqs
+
+
 def build_case(name: str):
     import torch
     from boundflow_amd import workloads as wl
 
     dev = torch.device("cuda:0")
+    if name in ("X1", "X3"):
+        from boundflow_amd import fused_crown as fc
+        w, reqs = executor_regions(name, dev)
+        ex = fc.HipFusedCrownExecutor()
+        ctx = fc.FusedCrownExecutionContext()
+        assert all(ex.supports(r, ctx) for r in reqs)
+
+        def step():
+            return [ex.run(r) for r in reqs]
+
+        rows = sum(int(r.A_u.shape[0] * r.A_u.shape[1]) for r in reqs)
+        desc = (f"{name}: HipFusedCrownExecutor.run on every ReLU -> affine region of the "
+                f"{'C1 MLP' if name == 'X1' else 'C3 CNN'} ({len(reqs)} regions, B={w.batch}, 9 margin specs, "
+                "upper and lower coefficients, synthetic relaxations)")
+        return w, step, rows, "region rows/s", desc
     w = wl.make(name)
     wd = wl.to_device(w, dev)
     run = hip_runner(name)
@@ -376,7 +436,7 @@ def main() -> int:
         "roofline": head["roofline"],
         "kernels": head["kernels"],
     }
-    if not args.no_cpu:
+    if not args.no_cpu and not args.config.startswith("X"):   # X1 / X3: executor profile entries, no CPU leg
         line["cpu_baseline"] = cpu_baseline(args.config, w, args.cpu_seconds)
         line["cpu_baseline"]["unit"] = unit
     # the metric's second half: BaB domains/s on the C5 domain batch, measured in the same run

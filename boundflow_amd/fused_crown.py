@@ -37,6 +37,7 @@ import torch
 
 from . import _lib
 from .crown import derived, transposed
+from .profiling import launch as _timed
 
 
 class BoundaryRepresentation(Enum):
@@ -278,9 +279,10 @@ class HipFusedCrownExecutor:
             Wt = transposed(request.weight)   # [P, N]: the kernel's faster operand layout, kept across calls
             pu = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             pl = torch.empty(D, S, P, device=dev, dtype=torch.float32)
-            _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
-                      _lib.ptr(table), None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None, _lib.ptr(pu),
-                      _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
+            with _timed("executor_relu_linear", 4.0 * M * N * P, 4.0 * (2 * M * N + 4 * D * N + N * P + 2 * M * P)):
+                _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
+                          _lib.ptr(table), None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None, _lib.ptr(pu),
+                          _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
             return FusedReluAffineResult(pu, pl, du, dl)
         Co, Ho, Wo = (int(d) for d in request.output_shape)
         Ci, Hi, Wi = (int(d) for d in request.input_shape)
@@ -292,13 +294,16 @@ class HipFusedCrownExecutor:
             f"conv_bias_map:{Ho}x{Wo}", (bias,), lambda: bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous())
         ru = torch.empty(M, N, device=dev)
         rl = torch.empty(M, N, device=dev)
-        _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
-                  _lib.ptr(table), None, 0, _lib.ptr(kbias), None, None, None, _lib.ptr(ru), _lib.ptr(rl), _lib.ptr(du),
-                  _lib.ptr(dl), None, None, st)
+        with _timed("executor_relu_relax", 0.0, 4.0 * (4 * M * N + 4 * D * N)):
+            _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
+                      _lib.ptr(table), None, 0, _lib.ptr(kbias), None, None, None, _lib.ptr(ru), _lib.ptr(rl),
+                      _lib.ptr(du), _lib.ptr(dl), None, None, st)
         pu = torch.empty(D, S, Ci, Hi, Wi, device=dev)
         pl = torch.empty(D, S, Ci, Hi, Wi, device=dev)
-        _lib.call("bf_conv_transpose_rows", _lib.ptr(ru), _lib.ptr(rl), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW, sh, sw,
-                  ph, pw, Hi, Wi, _lib.ptr(pu), _lib.ptr(pl), S, None, 0, None, None, None, None, st)
+        with _timed("executor_conv_transpose", 4.0 * M * Co * Ho * Wo * Ci * KH * KW,
+                    4.0 * (2 * M * N + 2 * M * Ci * Hi * Wi)):
+            _lib.call("bf_conv_transpose_rows", _lib.ptr(ru), _lib.ptr(rl), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW,
+                      sh, sw, ph, pw, Hi, Wi, _lib.ptr(pu), _lib.ptr(pl), S, None, 0, None, None, None, None, st)
         return FusedReluAffineResult(pu, pl, du, dl)
 
 

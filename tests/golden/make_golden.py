@@ -341,7 +341,8 @@ def golden_vnnlib(tag):
 
 
 from tests.frontend_models import native_bab_toy, native_toy  # noqa: E402
-from tests.golden_util import ALPHA_CROWN_OBJECTIVE_CASES, OBJECTIVE_CASES, objective_workload  # noqa: E402
+from tests.golden_util import (ALPHA_CROWN_OBJECTIVE_CASES, OBJECTIVE_CASES, c3_box, dag_case,  # noqa: E402
+                               objective_workload)
 
 
 def golden_objectives(tag):
@@ -446,6 +447,11 @@ GOLDENS = [
     ("frontend_planned", golden_frontend),
     ("vnnlib_queries", golden_vnnlib),
     ("objectives_mlp", golden_objectives),
+    ("crown_c3_box", lambda t: golden_crown(c3_box(), t, pre_rows=6)),
+] + [
+    (f"crown_dag_{k}{'_box' if b else ''}", (lambda k, b: lambda t: golden_crown(dag_case(k, b), t))(k, b))
+    for k in wl.DAG_KINDS for b in (False, True)
+] + [
     ("alpha_crown_objectives", golden_alpha_crown_objectives),
     ("native_toy_b4", golden_native),
     ("native_toy_budget", golden_native),

@@ -101,3 +101,20 @@ def objective_workload():
         sign = (torch.randint(0, 2, (6, 16), generator=g) * 2 - 1).to(torch.int8)
         splits[n] = torch.where(pick, sign, splits[n])
     return w, splits
+
+
+def c3_box(batch: int = 6):
+    """The C3 CNN on a box input: the first ``batch`` C3 inputs widened by 0.01 and
+    clipped to [0, 1] (fixture crown_c3_box)."""
+    from boundflow_amd import workloads as wl
+    from boundflow_amd.spec import InputSpec
+    w = wl.subset(wl.make_c3(), batch)
+    lo = (w.spec.center - 0.01).clamp(0, 1)
+    hi = (w.spec.center + 0.01).clamp(0, 1)
+    return wl.Workload("C3box", w.module, InputSpec.box(value_name="input", lower=lo, upper=hi), w.C, w.labels)
+
+
+def dag_case(kind: str, box: bool):
+    """The DAG workload of fixture crown_dag_<kind>[_box]."""
+    from boundflow_amd import workloads as wl
+    return wl.make_dag(kind, seed=3, batch=6, eps=0.03, box=box, blocks=2)

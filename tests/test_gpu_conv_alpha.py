@@ -14,7 +14,7 @@ from boundflow_amd.spec import InputSpec
 from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
 from oracle import parity
-from tests.golden_util import load, t
+from tests.golden_util import c3_box, load, t, workload_checksum
 from tests.gpu_util import announce, assert_bounds_close, assert_parity, assert_verdicts, device
 
 pytestmark = pytest.mark.gpu
@@ -42,10 +42,7 @@ def test_crown_cnn_matches_reference():
 def test_crown_cnn_box_input_matches_oracle():
     dev = device()
     announce("CNN with a box input (bounding box + radius-weighted concretization)")
-    w = wl.subset(wl.make_c3(), 6)
-    lo = (w.spec.center - 0.01).clamp(0, 1)
-    hi = (w.spec.center + 0.01).clamp(0, 1)
-    w = wl.Workload("C3box", w.module, InputSpec.box(value_name="input", lower=lo, upper=hi), w.C, w.labels)
+    w = c3_box(6)
     ref = cr.run_crown_ibp(w.module, w.spec, linear_spec_C=w.C)
     w64 = parity.to_float64(w)
     ref64 = cr.run_crown_ibp(w64.module, w64.spec, linear_spec_C=w64.C)
@@ -53,6 +50,12 @@ def test_crown_cnn_box_input_matches_oracle():
     b = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
     assert_parity(b.lower, ref.lower, ref64.lower, "C3 box lower")
     assert_parity(b.upper, ref.upper, ref64.upper, "C3 box upper")
+    # the same network and box through the reference's run_crown_ibp_mlp (fixture crown_c3_box)
+    g = load("crown_c3_box")
+    assert workload_checksum(w) == str(g["checksum"])
+    assert_parity(b.lower, t(g["lower"]), ref64.lower, "C3 box lower vs reference")
+    assert_parity(b.upper, t(g["upper"]), ref64.upper, "C3 box upper vs reference")
+    assert_verdicts(b.lower, t(g["lower"]), ref64.lower, "C3 box")
 
 
 def _oracle_grads(w, alpha, beta=None, splits=None, per_batch=True, dtype=torch.float32):

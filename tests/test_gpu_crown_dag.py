@@ -13,6 +13,7 @@ from boundflow_amd import workloads as wl
 from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
 from oracle import parity
+from tests.golden_util import dag_case, load, t, workload_checksum
 from tests.gpu_util import announce, assert_bounds_close, assert_parity, assert_verdicts, device
 from tests.test_gpu_conv_alpha import _grad_close, _oracle_grads, _sign_tie_allowance
 
@@ -43,6 +44,27 @@ def test_dag_crown_matches_oracle(kind, box):
     announce(f"DAG CROWN {kind} box={box}")
     w = wl.make_dag(kind, seed=3, batch=6, eps=0.03, box=box, blocks=2)
     _check(w, dev, f"{kind} box={box}")
+
+
+@pytest.mark.parametrize("kind", wl.DAG_KINDS)
+@pytest.mark.parametrize("box", [False, True])
+def test_dag_crown_matches_reference_fixture(kind, box):
+    """HIP DAG CROWN against the reference's run_crown_ibp_mlp on the same network
+    (fixture crown_dag_<kind>[_box]), fp64-explained at the contract, same verdicts."""
+    dev = device()
+    tag = f"crown_dag_{kind}{'_box' if box else ''}"
+    announce(f"DAG CROWN {tag} vs reference fixture")
+    g = load(tag)
+    w = dag_case(kind, box)
+    assert workload_checksum(w) == str(g["checksum"])
+    wd = wl.to_device(w, dev)
+    got = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+    torch.cuda.synchronize()
+    w64 = parity.to_float64(w)
+    ref64 = cr.run_crown_ibp(w64.module, w64.spec, linear_spec_C=w64.C)
+    assert_parity(got.lower, t(g["lower"]), ref64.lower, f"{tag} lower")
+    assert_parity(got.upper, t(g["upper"]), ref64.upper, f"{tag} upper")
+    assert_verdicts(got.lower, t(g["lower"]), ref64.lower, tag)
 
 
 @pytest.mark.parametrize("kind", wl.DAG_KINDS)

@@ -15,7 +15,7 @@ import torch
 from boundflow_amd import workloads as wl
 from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
-from tests.golden_util import load, t, workload_checksum
+from tests.golden_util import c3_box, dag_case, load, t, workload_checksum
 
 
 def _close(a, b, rtol=1e-6, atol=1e-6):
@@ -29,6 +29,10 @@ def _close(a, b, rtol=1e-6, atol=1e-6):
     ("crown_c1", lambda: wl.make_c1()),
     ("crown_c1_mixed", lambda: wl.make_c1(eps=0.001, label_mode="predicted")),
     ("crown_c3_b16", lambda: wl.subset(wl.make_c3(), 16)),
+    ("crown_c3_box", c3_box),
+] + [
+    (f"crown_dag_{k}{'_box' if b else ''}", (lambda k, b: lambda: dag_case(k, b))(k, b))
+    for k in wl.DAG_KINDS for b in (False, True)
 ])
 def test_crown_matches_reference(tag, maker):
     g = load(tag)
