@@ -4,12 +4,16 @@
   the counterpart of the reference's W+/W- conv transformer
   (boundflow/domains/interval.py:57-74) after ``bounding_box`` for the input
   layer (boundflow/runtime/crown_ibp.py:167-181).
-* ``conv_backward_step`` -- one ReLU -> Conv2d region of the CROWN backward:
-  the relaxation pass (``bf_crown_relu_relax_lu``, with the conv bias map and, on
-  the input layer, the center projection reduced in the same pass), then the
-  transposed convolution (``bf_conv_transpose_rows``,
-  boundflow/runtime/linear_operator.py:1067-1092), fused with the Linf / box
-  concretization on the input layer.
+* ``conv_backward_step`` -- one ReLU -> Conv2d region of the CROWN backward.
+  Inner layers: one pass (``bf_crown_relu_conv_transpose``) that relaxes each
+  coefficient row while the transposed convolution stages it (the sign split of
+  runtime/linear_operator.py:722-905 taken into the conv operator of
+  :1067-1092), with the bias terms reduced in the same pass.  The input layer,
+  and shapes that pass does not take: the relaxation pass
+  (``bf_crown_relu_relax_lu``, with the conv bias map and, on the input layer, the
+  center projection reduced in the same pass), then the transposed convolution
+  (``bf_conv_transpose_rows``), fused with the Linf / box concretization on the
+  input layer.
 """
 
 from __future__ import annotations
@@ -88,20 +92,44 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
         kbias = derived(f"conv_bias_map:{Ho}x{Wo}", (layer.bias,),
                         lambda: layer.bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(n_out).contiguous())
     cvec = trace.input_center_proj.get(layer.out_name) if is_first else None
+    nz = int(A_u is not None) + int(A_l is not None)
+    taps = KH * KW / float(sh * sw)
+    flops = 2.0 * nz * M * n_in * Co * taps
+    if not is_first and _lib.load().bf_conv_transpose_hwc_supported(Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi):
+        # the relaxation applied while the transposed convolution stages each row: the relaxed
+        # rows reach HBM only when the gradient pass needs them
+        y_u = torch.empty(M, n_in, device=dev) if A_u is not None else None
+        y_l = torch.empty(M, n_in, device=dev) if A_l is not None else None
+        nb_u = torch.empty(M, device=dev) if A_u is not None else None
+        nb_l = torch.empty(M, device=dev) if A_l is not None else None
+        keep_l = torch.empty_like(A_l) if (save is not None and A_l is not None) else None
+        geo = (Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi)
+
+        def pack():
+            out = torch.empty(int(_lib.load().bf_conv_transpose_packed_floats(*geo)), device=dev)
+            _lib.call("bf_conv_transpose_pack_weights", _lib.ptr(W), *geo, _lib.ptr(out), stream)
+            return out
+        packed = derived("conv_t_pack:" + "x".join(str(v) for v in geo), (layer.weight,), pack)
+        with _timed("crown_relu_conv_transpose", flops,
+                    4.0 * nz * (M * n_out + M * n_in) + (4.0 * M * n_out if keep_l is not None else 0.0)):
+            _lib.call("bf_crown_relu_conv_transpose", _lib.ptr(A_u), _lib.ptr(A_l), B, S, Co, Ho, Wo, _lib.ptr(pre_lo),
+                      _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld, _lib.ptr(kbias),
+                      _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(W), _lib.ptr(packed), Ci, KH, KW, sh, sw, ph, pw, Hi, Wi,
+                      _lib.ptr(y_u), _lib.ptr(y_l), _lib.ptr(nb_u), _lib.ptr(nb_l), None, _lib.ptr(keep_l), stream)
+        if save is not None:
+            save.setdefault("relaxed", {})[layer.op_index] = keep_l
+        return y_u, y_l, nb_u, nb_l, S * n_in, None
     rA_u = torch.empty_like(A_u) if A_u is not None else None
     rA_l = torch.empty_like(A_l) if A_l is not None else None
     nb_u = torch.empty(M, device=dev) if A_u is not None else None
     nb_l = torch.empty(M, device=dev) if A_l is not None else None
     c_u = torch.empty(M, device=dev) if (A_u is not None and cvec is not None) else None
     c_l = torch.empty(M, device=dev) if (A_l is not None and cvec is not None) else None
-    nz = int(A_u is not None) + int(A_l is not None)
     with _timed("crown_relu_relax", 0.0, 4.0 * nz * 2 * M * n_out):
         _lib.call("bf_crown_relu_relax_lu", _lib.ptr(A_u), _lib.ptr(A_l), S * n_out, B, S, n_out, _lib.ptr(pre_lo),
                   _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld, _lib.ptr(kbias), _lib.ptr(cvec),
                   _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u), _lib.ptr(rA_l), _lib.ptr(nb_u), _lib.ptr(nb_l),
                   _lib.ptr(c_u), _lib.ptr(c_l), stream)
-    taps = KH * KW / float(sh * sw)
-    flops = 2.0 * nz * M * n_in * Co * taps
     if not is_first:
         y_u = torch.empty(M, n_in, device=dev) if A_u is not None else None
         y_l = torch.empty(M, n_in, device=dev) if A_l is not None else None

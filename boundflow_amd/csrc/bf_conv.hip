@@ -195,6 +195,8 @@ struct GatherArgs {
   int nA, nB, T;                          // MODE_T taps per class
   int Kc, Kc4, npad, nblk, nclasses, ntasks;
   FastDiv f_kstride, f_npad, f_T, f_nB, f_sw, f_KHKW, f_KW, f_HpWp, f_Wp;   // staging index divisions
+  FastDiv f_HWm, f_Wm;                    // channel-last staging: divisions by Hm*Wm and Wm
+  const float* wpack;                     // channel-last: weights already in LDS order (or null)
   GatherClass cls[GMAX_CLASSES];
 };
 
@@ -387,6 +389,285 @@ conv_mfma_kernel(GatherArgs g) {
       }
     }
   }
+}
+
+// conv_transpose2d of coefficient rows with the map channel-last in LDS (Co % 16 == 0).
+//
+// The row's map is staged as [Hp][Wp][CP] (channel pitch CP = Co + 4, zero halo
+// written once per workgroup), so in parity class c the operand of output pixel
+// (u, v) for tap (a, b) and channels co .. co + 3 is ONE float4 at
+//   ((u + pad_h - a) Wp + (v + pad_w - b)) CP + co
+// -- a lane-constant base plus a per-step uniform offset, with no offset table
+// read in front of it.  The reduction index of a step quad q (T taps x Co / 16
+// halves) is k = 16 q + 4 e + j for MFMA step e and lane group j, mapped to
+// (tap ab = q / (Co / 16), channel co = 16 (q % (Co / 16)) + 4 j + e); the weights
+// are staged in the same order (ws_index), one float4 per lane per quad.
+//
+// RELAX: the ReLU relaxation of the region is applied while the map is staged
+// (the sign-split A+ pos + A- neg of runtime/linear_operator.py:722-905 and the
+// dense ReLU backward of runtime/crown_ibp.py:1211-1298, slopes computed from the
+// pre-activation box as bf_crown_relu_relax_lu does), with the row sums
+//   b_out = (b_in + sum A * beta_sel) + sum A' * kbias
+// reduced in the same pass; the relaxed rows are written out only when asked.
+struct ConvRelax {
+  const float* lo;       // pre-activation box [D, nin] of the ReLU (nin = Co*Ho*Wo)
+  const float* hi;
+  const float* alpha;    // lower-slope override, [D, nin] (alpha_ld nin) or shared (0); null = CROWN slopes
+  int64_t alpha_ld;
+  const float* add;      // lower bound: split term [D, nin] (add_ld)
+  int64_t add_ld;
+  const float* kbias;    // [nin] bias map of the conv whose output the ReLU reads
+  const float* b_in[2];
+  float* b_out[2];
+  float* relaxed[2];     // optional A' rows [R, nin]
+};
+
+template <bool RELAX>
+__global__ void __launch_bounds__(GTM)
+conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* Ws = smem;                                                  // [nclasses][Kc4][npad] (ws_index order)
+  float* Mp = Ws + (size_t)g.nclasses * g.Kc4 * g.npad;              // [Hp][Wp][CP]
+  __shared__ float red[GTM / 64][2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int z = blockIdx.y;
+  const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
+  const float* __restrict__ X = g.X[z];
+  float* __restrict__ y = g.y[z];
+  float* __restrict__ nrm = g.nrm[z];
+  const int CP = g.Cm + 4;
+  const int hq = g.Cm >> 4;                 // 16-channel halves per tap
+  const int kstride = g.Kc4 * g.npad;
+
+  // weights of every class in the quad order above, zero-padded in k and channels:
+  // a float4 copy of the packed layout when the caller keeps one (conv_t_hwc_pack_kernel)
+  const int wtotal = g.nclasses * kstride;
+  if (g.wpack) {
+    for (int i4 = tid; i4 < wtotal / 4; i4 += GTM)
+      reinterpret_cast<float4*>(Ws)[i4] = reinterpret_cast<const float4*>(g.wpack)[i4];
+  }
+  for (int base = 0; base < wtotal && !g.wpack; base += 8 * GTM) {
+    float wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * GTM + tid;
+      const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
+      const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
+      const bool ok = idx < wtotal && k < g.Kc && n < g.nch;
+      const int j = k & 3, q = k >> 4, e = (k >> 2) & 3;
+      const int ab = q / hq, half = q - ab * hq;
+      const int co = 16 * half + 4 * j + e;
+      const int a = fdivq(ab, g.f_nB), b = ab - a * g.nB;
+      const int cr = fdivq(c, g.f_sw);
+      const int kh = cr + g.sh * a, kw = (c - cr * g.sw) + g.sw * b;
+      const int64_t src = (((int64_t)co * g.Cin + n) * g.KH + kh) * g.KW + kw;
+      const float w = g.W[ok ? src : 0];
+      wv[u] = ok ? w : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * GTM + tid;
+      if (idx < wtotal) {
+        const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
+        const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
+        Ws[ws_index(g, c, n, k)] = wv[u];
+      }
+    }
+  }
+  // zero halo (and channel padding): interior positions are rewritten per row, the rest stays zero
+  const int mtotal = g.Hp * g.Wp * CP;
+  for (int i = tid; i < mtotal; i += GTM) Mp[i] = 0.f;
+
+  const int HWm = g.Hm * g.Wm;
+  const int nin = g.Cm * HWm;
+  const int64_t nout = (int64_t)g.nch * g.HWout;
+  const int j = lane >> 4;     // k lane group of the MFMA operands; output row group
+  const int col = lane & 15;   // pixel column (B operand / D column); channel row (A operand)
+  const FastDiv f_hw = g.f_HWm;
+  const FastDiv f_w = g.f_Wm;
+
+  // One element of a row: relax it (RELAX) into the channel-last map.
+  auto stage = [&](int64_t r, int64_t d, int e, float v, float lo, float hi, float al, float ad, float& sb,
+                   float& sk) {
+    const int co = fdivq(e, f_hw), rem = e - co * HWm;
+    const int yy = fdivq(rem, f_w), xx = rem - yy * g.Wm;
+    if constexpr (RELAX) {
+      float4 t = make_float4(1.f, 0.f, 1.f, 0.f);
+      if (rx.lo) {
+        const bool has_alpha = rx.alpha != nullptr;
+        const Relax rr = relu_relax(lo, hi, has_alpha, has_alpha ? clamp01(al) : 0.f);
+        t = make_float4(rr.au, rr.bu, rr.al, rr.bl);
+      }
+      const bool nn = v >= 0.f;
+      float o;
+      if (lower) {
+        o = v * (nn ? t.z : t.x);
+        sb += v * (nn ? t.w : t.y);
+        if (rx.add) o = o + ad;
+      } else {
+        o = v * (nn ? t.x : t.z);
+        sb += v * (nn ? t.y : t.w);
+      }
+      if (rx.kbias) sk += o * rx.kbias[e];
+      if (rx.relaxed[z]) rx.relaxed[z][r * nin + e] = o;
+      v = o;
+    }
+    Mp[((yy + g.pad_h) * g.Wp + xx + g.pad_w) * CP + co] = v;
+  };
+  // The coefficients of rows of at most PF * GTM elements are fetched one row ahead,
+  // into registers, so that their loads overlap the MFMAs of the row before (the
+  // relaxation operands are per domain: the rows of a domain find them in cache).
+  constexpr int PF = 4;
+  const bool pf = nin <= PF * GTM;   // uniform
+  float pa[PF];
+  auto fetch = [&](int64_t r) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int e = tid + u * GTM;
+      pa[u] = e < nin ? X[r * nin + e] : 0.f;
+    }
+  };
+  auto relax_operands = [&](int64_t d, int e, float& lo, float& hi, float& al, float& ad) {
+    lo = hi = al = ad = 0.f;
+    if constexpr (RELAX) {
+      if (rx.lo) {
+        lo = rx.lo[d * nin + e];
+        hi = rx.hi[d * nin + e];
+      }
+      if (rx.alpha) al = rx.alpha[d * rx.alpha_ld + e];
+      if (rx.add && lower) ad = rx.add[d * rx.add_ld + e];
+    }
+  };
+  const int64_t r_first = (int64_t)blockIdx.x * g.rows_per_wg;
+  if (pf && r_first < g.R) fetch(r_first);
+
+  for (int i = 0; i < g.rows_per_wg; ++i) {
+    const int64_t r = (int64_t)blockIdx.x * g.rows_per_wg + i;
+    if (r >= g.R) break;   // uniform
+    __syncthreads();       // weights / halo staged; previous row's map and partial sums consumed
+    const int64_t d = r / g.S;
+    float sb = 0.f, sk = 0.f;
+    if (pf) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int e = tid + u * GTM;
+        if (e < nin) {
+          float lo, hi, al, ad;
+          relax_operands(d, e, lo, hi, al, ad);
+          stage(r, d, e, pa[u], lo, hi, al, ad, sb, sk);
+        }
+      }
+    } else {
+      for (int e = tid; e < nin; e += GTM) {
+        float lo, hi, al, ad;
+        relax_operands(d, e, lo, hi, al, ad);
+        stage(r, d, e, X[r * nin + e], lo, hi, al, ad, sb, sk);
+      }
+    }
+    if constexpr (RELAX) {
+      sb = wave_sum(sb);
+      sk = wave_sum(sk);
+      if (lane == 0) {
+        red[wave][0] = sb;
+        red[wave][1] = sk;
+      }
+    }
+    __syncthreads();
+    if constexpr (RELAX) {
+      if (tid == 0 && rx.b_out[z]) {
+        float tb = 0.f, tk = 0.f;
+        for (int q = 0; q < GTM / 64; ++q) {
+          tb += red[q][0];
+          tk += red[q][1];
+        }
+        rx.b_out[z][r] = ((rx.b_in[z] ? rx.b_in[z][r] : 0.f) + tb) + tk;
+      }
+    }
+    if (pf && i + 1 < g.rows_per_wg && r + 1 < g.R) fetch(r + 1);   // lands during this row's MFMAs
+    const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
+    float s = 0.f;
+    for (int task = wave; task < g.ntasks; task += GTM / 64) {
+      int c = 0;
+      while (c + 1 < g.nclasses && task >= g.cls[c + 1].tbase) ++c;
+      const GatherClass& C = g.cls[c];
+      const int tl = task - C.tbase;
+      const int pt = tl / g.nblk, cb = tl - pt * g.nblk;
+      const int p = pt * 16 + col;
+      const bool pok = p < C.np;
+      const int pc = pok ? p : C.np - 1;
+      const int q1 = pc / C.n2, q2 = pc - q1 * C.n2;
+      const float* __restrict__ mp = Mp + (C.poff0 + q1 * C.s1 + q2 * C.s2) * CP + 4 * j;
+      const float* __restrict__ wl = Ws + ws_index(g, c, cb * 16 + col, j);
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      int q = 0;
+      for (int a = 0; a < g.nA; ++a) {
+        for (int b = 0; b < g.nB; ++b) {
+          const float* __restrict__ tp = mp - (a * g.Wp + b) * CP;
+          for (int half = 0; half < hq; ++half, ++q) {
+            const float4 w4 = *reinterpret_cast<const float4*>(wl + q * 64);
+            const float4 x4 = *reinterpret_cast<const float4*>(tp + 16 * half);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.x, x4.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.y, x4.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.z, x4.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.w, x4.w, acc, 0, 0, 0);
+          }
+        }
+      }
+      const int opix = C.out0 + q1 * C.o1 + q2 * C.o2;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int n = cb * 16 + 4 * j + rr;
+        if (n < g.nch && pok) {
+          const float v = acc[rr];
+          const int64_t oidx = (int64_t)n * g.HWout + opix;
+          if (y) y[r * nout + oidx] = v;
+          if (nrm) {
+            const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
+            s += g.wv ? fabsf(v) * wgt : fabsf(v);
+            if (lower && g.h_out) {
+              const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
+              g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
+            }
+          }
+        }
+      }
+    }
+    if (nrm) {
+      s = wave_sum(s);
+      __syncthreads();   // red of the row sums above is read; reuse it
+      if (lane == 0) red[wave][0] = s;
+      __syncthreads();
+      if (tid == 0) {
+        float t = 0.f;
+        for (int q2 = 0; q2 < GTM / 64; ++q2) t += red[q2][0];
+        nrm[r] = t;
+      }
+    }
+  }
+}
+
+// The weights of conv_t_hwc_kernel in its LDS order (ws_index over classes, output
+// channels and the quad-ordered reduction index), zero-padded: what each workgroup
+// would otherwise gather from the OIHW tensor, computed once per weight.
+__global__ void conv_t_hwc_pack_kernel(GatherArgs g, float* __restrict__ out) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int kstride = g.Kc4 * g.npad;
+  if (idx >= g.nclasses * kstride) return;
+  const int hq = g.Cm >> 4;
+  const int c = idx / kstride, rem = idx - c * kstride;
+  const int k = rem / g.npad, n = rem - k * g.npad;
+  float w = 0.f;
+  if (k < g.Kc && n < g.nch) {
+    const int j = k & 3, q = k >> 4, e = (k >> 2) & 3;
+    const int ab = q / hq, half = q - ab * hq;
+    const int co = 16 * half + 4 * j + e;
+    const int a = ab / g.nB, b = ab - a * g.nB;
+    const int cr = c / g.sw;
+    const int kh = cr + g.sh * a, kw = (c - cr * g.sw) + g.sw * b;
+    w = g.W[(((int64_t)co * g.Cin + n) * g.KH + kh) * g.KW + kw];
+  }
+  out[ws_index(g, c, n, k)] = w;
 }
 
 // conv_transpose2d of rows with few output channels (Ci <= 4, KH * KW <= 16),
@@ -594,6 +875,22 @@ static bool conv_t_mfma_plan(GatherArgs& g, int64_t R, int Co, int Ho, int Wo, i
   return true;
 }
 
+// The channel-last variant of the transposed-conv gather-GEMM (conv_t_hwc_kernel):
+// the parity classes of conv_t_mfma_plan, Co a multiple of 16, map indices below
+// 2^16 (exact FastDiv) and the stage within 64 KB.
+static bool conv_t_hwc_plan(GatherArgs& g, int64_t R, int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw,
+                            int ph, int pw, int Hi, int Wi, size_t* lds_bytes) {
+  if (Co % 16 != 0 || (int64_t)Co * Ho * Wo >= (1 << 16)) return false;
+  size_t base_lds = 0;
+  if (!conv_t_mfma_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &base_lds)) return false;
+  const size_t lds = sizeof(float) * ((size_t)g.nclasses * g.Kc4 * g.npad + (size_t)g.Hp * g.Wp * (Co + 4));
+  if (lds > 64 * 1024) return false;
+  *lds_bytes = lds;
+  g.f_HWm = make_fdiv(Ho * Wo);
+  g.f_Wm = make_fdiv(Wo);
+  return true;
+}
+
 // conv2d as one gather class; returns false when the LDS stage does not fit.
 static bool conv_f_mfma_plan(GatherArgs& g, int64_t R, int Ci, int Hi, int Wi, int Co, int KH, int KW, int sh,
                              int sw, int ph, int pw, int Ho, int Wo, size_t* lds_bytes) {
@@ -739,6 +1036,32 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
     GatherArgs g;
     memset(&g, 0, sizeof(g));
     size_t glds = 0;
+    if (conv_t_hwc_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
+      int nzi = 0;
+      if (A_u) { g.X[nzi] = A_u; g.y[nzi] = y_u; g.nrm[nzi] = norm_u; ++nzi; }
+      if (A_l) { g.X[nzi] = A_l; g.y[nzi] = y_l; g.nrm[nzi] = norm_l; ++nzi; }
+      g.z_lower_first = A_u ? 0 : 1;
+      g.W = W;
+      g.wv = wvec;
+      g.w_ld = w_ld;
+      g.h_scale = h_scale;
+      g.h_out = h_out;
+      g.S = S;
+      const int rpw = gather_rows_per_wg(R * nz);
+      g.rows_per_wg = rpw;
+      BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
+      ConvRelax rx;
+      memset(&rx, 0, sizeof(rx));
+      hipLaunchKernelGGL(conv_t_hwc_kernel<false>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds,
+                         stream, g, rx);
+      BF_LAUNCH_CHECK("conv_t_hwc_kernel");
+      return BF_OK;
+    }
+  }
+  {
+    GatherArgs g;
+    memset(&g, 0, sizeof(g));
+    size_t glds = 0;
     if (conv_t_mfma_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
       int nzi = 0;
       if (A_u) { g.X[nzi] = A_u; g.y[nzi] = y_u; g.nrm[nzi] = norm_u; ++nzi; }
@@ -764,6 +1087,97 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
   hipLaunchKernelGGL(conv_transpose_rows_kernel, dim3((unsigned)R, nz), dim3(CT), lds, stream, A_u, A_l, Co, Ho, Wo,
                      W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S, wvec, w_ld, norm_u, norm_l, h_scale, h_out);
   BF_LAUNCH_CHECK("conv_transpose_rows_kernel");
+  return BF_OK;
+}
+
+int bf_conv_transpose_hwc_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
+                                    int Hi, int Wi) {
+  if (Co <= 0 || Ci <= 0 || KH <= 0 || KW <= 0 || sh <= 0 || sw <= 0 || Hi <= 0 || Wi <= 0 || Ho <= 0 || Wo <= 0)
+    return 0;
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t lds = 0;
+  return conv_t_hwc_plan(g, 1, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &lds) ? 1 : 0;
+}
+
+int64_t bf_conv_transpose_packed_floats(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph,
+                                        int pw, int Hi, int Wi) {
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t lds = 0;
+  if (!conv_t_hwc_plan(g, 1, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &lds)) return 0;
+  return (int64_t)g.nclasses * g.Kc4 * g.npad;
+}
+
+int bf_conv_transpose_pack_weights(const float* W, int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw,
+                                   int ph, int pw, int Hi, int Wi, float* out, hipStream_t stream) {
+  BF_REQUIRE(W && out, "bf_conv_transpose_pack_weights: null pointer");
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t lds = 0;
+  if (!conv_t_hwc_plan(g, 1, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &lds)) {
+    set_error("bf_conv_transpose_pack_weights: shape not supported (bf_conv_transpose_hwc_supported)");
+    return BF_EINVAL;
+  }
+  g.W = W;
+  const int total = g.nclasses * g.Kc4 * g.npad;
+  hipLaunchKernelGGL(conv_t_hwc_pack_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, stream, g, out);
+  BF_LAUNCH_CHECK("conv_t_hwc_pack_kernel");
+  return BF_OK;
+}
+
+int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho, int Wo,
+                                 const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
+                                 const float* add_l, int64_t add_ld, const float* kbias, const float* b_u_in,
+                                 const float* b_l_in, const float* W, const float* w_packed, int Ci, int KH, int KW,
+                                 int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u, float* y_l,
+                                 float* b_u_out, float* b_l_out, float* relaxed_u, float* relaxed_l,
+                                 hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && Co > 0 && Ci > 0, "bf_crown_relu_conv_transpose: bad sizes");
+  const int64_t R = D * S;
+  if (R == 0) return BF_OK;
+  BF_REQUIRE(W && (A_u || A_l), "bf_crown_relu_conv_transpose: null pointer");
+  BF_REQUIRE((A_u == nullptr) == (y_u == nullptr) && (A_l == nullptr) == (y_l == nullptr),
+             "bf_crown_relu_conv_transpose: each given coefficient needs an output");
+  BF_REQUIRE((pre_lo == nullptr) == (pre_hi == nullptr), "bf_crown_relu_conv_transpose: pre_lo and pre_hi go together");
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t glds = 0;
+  if (!conv_t_hwc_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
+    set_error("bf_crown_relu_conv_transpose: shape not supported (bf_conv_transpose_hwc_supported)");
+    return BF_EINVAL;
+  }
+  const unsigned nz = (A_u && A_l) ? 2u : 1u;
+  ConvRelax rx;
+  memset(&rx, 0, sizeof(rx));
+  rx.lo = pre_lo;
+  rx.hi = pre_hi;
+  rx.alpha = alpha;
+  rx.alpha_ld = alpha_ld;
+  rx.add = add_l;
+  rx.add_ld = add_ld;
+  rx.kbias = kbias;
+  int nzi = 0;
+  if (A_u) {
+    g.X[nzi] = A_u; g.y[nzi] = y_u;
+    rx.b_in[nzi] = b_u_in; rx.b_out[nzi] = b_u_out; rx.relaxed[nzi] = relaxed_u;
+    ++nzi;
+  }
+  if (A_l) {
+    g.X[nzi] = A_l; g.y[nzi] = y_l;
+    rx.b_in[nzi] = b_l_in; rx.b_out[nzi] = b_l_out; rx.relaxed[nzi] = relaxed_l;
+    ++nzi;
+  }
+  g.z_lower_first = A_u ? 0 : 1;
+  g.W = W;
+  g.wpack = ((uintptr_t)w_packed & 15) == 0 ? w_packed : nullptr;
+  g.S = S;
+  const int rpw = gather_rows_per_wg(R * nz);
+  g.rows_per_wg = rpw;
+  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_crown_relu_conv_transpose: too many rows");
+  hipLaunchKernelGGL(conv_t_hwc_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g,
+                     rx);
+  BF_LAUNCH_CHECK("conv_t_hwc_kernel<relax>");
   return BF_OK;
 }
 

@@ -227,6 +227,43 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
                            float* y_l, int64_t S, const float* wvec, int64_t w_ld, float* norm_u, float* norm_l,
                            const float* h_scale, float* h_out, hipStream_t stream);
 
+/* 1 when bf_crown_relu_conv_transpose (and the channel-last path of
+ * bf_conv_transpose_rows) takes this conv shape: KH % sh == KW % sw == 0, Co a
+ * multiple of 16, the staged map and weights within 64 KB of LDS; else 0. */
+int bf_conv_transpose_hwc_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
+                                    int Hi, int Wi);
+
+/* One ReLU -> Conv2d region of the CROWN backward in one pass: the ReLU
+ * relaxation of the coefficient rows A [D*S, Co*Ho*Wo] (slopes from the
+ * pre-activation box pre_lo/pre_hi [D, Co*Ho*Wo] and the optional lower-slope
+ * override alpha, as bf_crown_relu_relax_lu; the split term add_l on the lower
+ * bound) applied while each row's map is staged, never written unless
+ * relaxed_u/relaxed_l are given, then the transposed convolution to
+ * y [D*S, Ci*Hi*Wi], with b_out = (b_in + sum A * beta_sel) + sum A' * kbias.
+ * Replaces bf_crown_relu_relax_lu followed by bf_conv_transpose_rows: the
+ * sign-split transform of SignSplitLinearOperator (runtime/linear_operator.py:722-905)
+ * taken lazily into the conv operator (Conv2dLinearOperator.to_dense,
+ * linear_operator.py:1067-1092), with the dense ReLU backward's bias terms
+ * (runtime/crown_ibp.py:1211-1298).  Returns 1 for a shape that
+ * bf_conv_transpose_hwc_supported rejects.  w_packed (optional): the weights
+ * packed by bf_conv_transpose_pack_weights. */
+int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho, int Wo,
+                                 const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld,
+                                 const float* add_l, int64_t add_ld, const float* kbias, const float* b_u_in,
+                                 const float* b_l_in, const float* W, const float* w_packed, int Ci, int KH, int KW,
+                                 int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u, float* y_l,
+                                 float* b_u_out, float* b_l_out, float* relaxed_u, float* relaxed_l,
+                                 hipStream_t stream);
+
+/* The weights of that pass in the order its workgroups stage them
+ * (bf_conv_transpose_packed_floats floats, 16-byte aligned; 0 = shape not
+ * taken), so that a caller who keeps them per weight tensor passes them as
+ * w_packed and each workgroup copies them instead of gathering from W. */
+int64_t bf_conv_transpose_packed_floats(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph,
+                                        int pw, int Hi, int Wi);
+int bf_conv_transpose_pack_weights(const float* W, int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw,
+                                   int ph, int pw, int Hi, int Wi, float* out, hipStream_t stream);
+
 /* Convolution of rows (IBP center/radius, center projection x0 conv W, and the
  * gradient of a transposed convolution), plus optional rank-1 term
  * y[r] += row_scale[r] * vec[(r / vec_div) * vec_ld + e]. */

@@ -6,7 +6,10 @@ coefficient row, optionally fused with the concretization norm
 sum |y| * w and the gradient seed h = h_scale * sign(y) * w.  Shapes with at
 most 4 output channels and 16 taps run the tap-product MFMA kernel, other
 shapes with KH % sh == 0 and KW % sw == 0 the parity-class MFMA kernel, the
-rest the row kernel; all three are covered.  bf_conv2d_rows (conv2d of rows with W or |W| and
+rest the row kernel; all three are covered, the parity-class kernel in both of its
+map layouts (channel-last when Co is a multiple of 16).  bf_crown_relu_conv_transpose
+(the ReLU relaxation applied while that kernel stages each row) is checked against
+the relaxation pass followed by the transposed convolution.  bf_conv2d_rows (conv2d of rows with W or |W| and
 a rank-1 term: the IBP conv step, the input-center projection and the gradient
 of a transposed convolution) runs the same gather-GEMM kernel in its forward
 mode.  Tolerance: the fp32 accumulation bound K * 2^-23 * sum |terms| of each
@@ -24,7 +27,9 @@ pytestmark = pytest.mark.gpu
 
 # (R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, S)
 SHAPES = [
-    (37, 32, 8, 8, 16, 4, 4, 2, 2, 1, 1, 9),     # C3 conv1 backward (parity-class MFMA kernel)
+    (37, 32, 8, 8, 16, 4, 4, 2, 2, 1, 1, 9),     # C3 conv1 backward (channel-last parity-class MFMA kernel)
+    (13, 16, 6, 6, 24, 2, 2, 2, 2, 0, 0, 3),     # one tap per class, 24 channels in two blocks (channel-last)
+    (8, 48, 4, 4, 8, 3, 3, 1, 1, 1, 1, 4),       # stride 1, 9 taps, three 16-channel halves (channel-last)
     (20, 16, 16, 16, 3, 4, 4, 2, 2, 1, 1, 4),    # C3 conv0 backward (tap-product kernel, float4 map copy)
     (9, 8, 7, 5, 20, 3, 3, 1, 1, 1, 1, 3),       # stride 1, 3x3, Ci > 16 (parity-class kernel, 9 taps)
     (6, 5, 6, 6, 4, 2, 2, 2, 2, 0, 0, 2),        # 2x2 stride 2, no padding, 36 pixels (tap-product kernel)
@@ -145,3 +150,86 @@ def test_conv2d_rows_matches_fp64(shape):
     tol = (Ci * KH * KW + 2) * 2.0 ** -23 * bound + 1e-30
     err = (y.cpu().double() - ref).abs()
     assert bool((err <= tol).all()), f"{float((err / tol).max()):.3g} x tolerance"
+
+
+FUSED_SHAPES = [
+    (37, 32, 8, 8, 16, 4, 4, 2, 2, 1, 1, 9),     # C3 / C4 conv1 region
+    (8, 48, 4, 4, 8, 3, 3, 1, 1, 1, 1, 4),
+]
+
+
+@pytest.mark.parametrize("shape", FUSED_SHAPES, ids=[f"R{s[0]}_Co{s[1]}_Ci{s[4]}" for s in FUSED_SHAPES])
+@pytest.mark.parametrize("variant", ["crown", "alpha_split"])
+def test_relu_conv_transpose_matches_pass_then_conv(shape, variant):
+    """bf_crown_relu_conv_transpose against bf_crown_relu_relax_lu + a float64 conv_transpose2d:
+    the relaxed rows it writes are bit-identical to the pass's, the bias rows agree to the
+    fp32 bound of their two summation orders, and y to the accumulation bound of the
+    transposed convolution of those rows."""
+    dev = device()
+    R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, S = shape
+    Hi, Wi = _out_hw(Ho, Wo, KH, KW, sh, sw, ph, pw)
+    announce(f"bf_crown_relu_conv_transpose {shape} {variant}")
+    assert _lib.load().bf_conv_transpose_hwc_supported(Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi) == 1
+    g = torch.Generator().manual_seed(R * 7 + Co)
+    D = (R + S - 1) // S
+    R = D * S
+    nin = Co * Ho * Wo
+    A_u = torch.randn(R, nin, generator=g)
+    A_l = torch.randn(R, nin, generator=g)
+    c = torch.randn(D, nin, generator=g)
+    w = torch.rand(D, nin, generator=g)
+    lo, hi = c - w, c + 0.5 * w          # mixes inactive, active and ambiguous neurons
+    W = torch.randn(Co, Ci, KH, KW, generator=g)
+    kb = torch.randn(nin, generator=g)
+    b_in = torch.randn(2, R, generator=g)
+    alpha = torch.rand(D, nin, generator=g) if variant == "alpha_split" else None
+    add = torch.randn(D, nin, generator=g) if variant == "alpha_split" else None
+    T = lambda x: None if x is None else x.to(dev).contiguous()   # noqa: E731
+    st = _lib.stream_handle()
+    args = dict(A_u=T(A_u), A_l=T(A_l), lo=T(lo), hi=T(hi), alpha=T(alpha), add=T(add), kb=T(kb), bu=T(b_in[0]),
+                bl=T(b_in[1]), W=T(W))
+    # the pass, then the transposed convolution of its output in float64
+    rp_u = torch.empty(R, nin, device=dev)
+    rp_l = torch.empty(R, nin, device=dev)
+    bp_u = torch.empty(R, device=dev)
+    bp_l = torch.empty(R, device=dev)
+    _lib.call("bf_crown_relu_relax_lu", _lib.ptr(args["A_u"]), _lib.ptr(args["A_l"]), S * nin, D, S, nin,
+              _lib.ptr(args["lo"]), _lib.ptr(args["hi"]), _lib.ptr(args["alpha"]), nin if alpha is not None else 0,
+              _lib.ptr(args["add"]), nin, _lib.ptr(args["kb"]), None, _lib.ptr(args["bu"]), _lib.ptr(args["bl"]),
+              _lib.ptr(rp_u), _lib.ptr(rp_l), _lib.ptr(bp_u), _lib.ptr(bp_l), None, None, st)
+    # the fused pass
+    geo = (Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi)
+    packed = torch.empty(int(_lib.load().bf_conv_transpose_packed_floats(*geo)), device=dev)
+    _lib.call("bf_conv_transpose_pack_weights", _lib.ptr(args["W"]), *geo, _lib.ptr(packed), st)
+    outs = []
+    for wp in (None, packed):   # weights gathered by each workgroup, then the packed copy
+        y_u = torch.empty(R, Ci * Hi * Wi, device=dev)
+        y_l = torch.empty(R, Ci * Hi * Wi, device=dev)
+        b_u = torch.empty(R, device=dev)
+        b_l = torch.empty(R, device=dev)
+        rf_l = torch.empty(R, nin, device=dev)
+        _lib.call("bf_crown_relu_conv_transpose", _lib.ptr(args["A_u"]), _lib.ptr(args["A_l"]), D, S, Co, Ho, Wo,
+                  _lib.ptr(args["lo"]), _lib.ptr(args["hi"]), _lib.ptr(args["alpha"]), nin if alpha is not None else 0,
+                  _lib.ptr(args["add"]), nin, _lib.ptr(args["kb"]), _lib.ptr(args["bu"]), _lib.ptr(args["bl"]),
+                  _lib.ptr(args["W"]), _lib.ptr(wp), Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(y_l),
+                  _lib.ptr(b_u), _lib.ptr(b_l), None, _lib.ptr(rf_l), st)
+        outs.append((y_u, y_l, b_u, b_l, rf_l))
+    torch.cuda.synchronize()
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b), "packed weights change the result"
+    y_u, y_l, b_u, b_l, rf_l = outs[1]
+    assert torch.equal(rf_l, rp_l), "relaxed rows differ from the relaxation pass"
+    for k, rp, y, bf, bp, A in (("u", rp_u, y_u, b_u, bp_u, A_u), ("l", rp_l, y_l, b_l, bp_l, A_l)):
+        ref = F.conv_transpose2d(rp.double().cpu().reshape(R, Co, Ho, Wo), W.double(), stride=(sh, sw),
+                                 padding=(ph, pw)).reshape(R, -1)
+        bound = F.conv_transpose2d(rp.double().cpu().abs().reshape(R, Co, Ho, Wo), W.double().abs(),
+                                   stride=(sh, sw), padding=(ph, pw)).reshape(R, -1)
+        taps = Co * ((KH + sh - 1) // sh) * ((KW + sw - 1) // sw)
+        err = (y.double().cpu() - ref).abs()
+        assert bool((err <= taps * 2.0 ** -23 * bound + 1e-30).all()), f"y_{k}: max err {float(err.max()):.3e}"
+        # bias rows: the same terms summed in two orders; bound 2 * nin * u * sum |terms|
+        beta_max = float(lo.abs().max())   # every intercept -l u / (u - l) of an ambiguous neuron is at most |l|
+        terms = (A.abs().sum(1).double() * beta_max + rp.double().cpu().abs().mul(kb.double().abs()).sum(1)
+                 + float(b_in.abs().max()))
+        berr = (bf.double().cpu() - bp.double().cpu()).abs()
+        assert bool((berr <= 2 * nin * 2.0 ** -24 * terms + 1e-30).all()), f"b_{k}: max err {float(berr.max()):.3e}"
