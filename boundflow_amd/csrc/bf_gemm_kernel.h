@@ -65,6 +65,8 @@ struct Tile {
   // domains reads them there (16 domains: every tile when S >= 9).
   static constexpr int TAB_ENTRIES = NT < 256 ? NT : 256;
   static constexpr int TAB_DOMS = TAB_ENTRIES / BK;
+  // LDS stages of the direct-to-LDS loop: three, or two when four workgroups share a CU
+  static constexpr int DL_STAGES = OCC >= 4 ? 2 : 3;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert((BM * BK) % (4 * NT) == 0 && NT % KQ == 0, "tile/thread mismatch");
   static_assert((BK & (BK - 1)) == 0 && BK >= 8, "BK must be a power of two >= 8");
@@ -126,7 +128,7 @@ gemm_kernel(GemmArgs p) {
   static_assert(!DL || (PRO == PRO_PLAIN && TRANS_B && GBK == 16 && GBM % 16 == 0 && GBN % 16 == 0 &&
                         T::WTM % 8 == 0 && T::WTN % 8 == 0),
                 "direct-to-LDS loop: plain prologue, transposed B, BK 16");
-  constexpr int NSTAGE = DL ? 3 : 2;
+  constexpr int NSTAGE = DL ? T::DL_STAGES : 2;
   constexpr int A_STAGE = DL ? GBM * GBK : GBM * AP;
   constexpr int B_STAGE = DL ? GBN * GBK : T::BS_FLOATS;
   // the A and B stages, one array: the relaxation epilogue stages its operands over all of it
@@ -581,14 +583,15 @@ gemm_kernel(GemmArgs p) {
       constexpr bool FULL = decltype(full_c)::value;
       const bool tail = (K - kbase) % GBK != 0;
       const int nki = (int)nk;   // K tiles of this workgroup (K < 2^31)
+      constexpr int AHEAD = NSTAGE - 1;   // K tiles in flight beyond the one being multiplied
       issue(0, kbase);
-      if (nki > 1) issue(1, kbase + GBK);
-      int st = 0, st2 = 2;   // stage of tile kt, stage refilled with tile kt + 2
+      if (AHEAD > 1 && nki > 1) issue(1, kbase + GBK);
+      int st = 0, st2 = AHEAD;   // stage of tile kt, stage refilled with tile kt + AHEAD
       for (int kt = 0; kt < nki; ++kt) {
-        if (kt + 1 < nki) wait_vmem<COPIES>(); else wait_vmem<0>();
+        if (AHEAD > 1 && kt + 1 < nki) wait_vmem<(AHEAD - 1) * COPIES>(); else wait_vmem<0>();
         if (tail && kt + 1 == nki) fix_tail(st, kbase + (int64_t)kt * GBK);
         lds_barrier();   // tile kt visible; every wave is done with the stage refilled next
-        if (kt + 2 < nki) issue(st2, kbase + (int64_t)(kt + 2) * GBK);
+        if (kt + AHEAD < nki) issue(st2, kbase + (int64_t)(kt + AHEAD) * GBK);
         const float* __restrict__ as = As[st];
         const float* __restrict__ bs = Bs[st];
         __builtin_amdgcn_s_setprio(1);
@@ -619,8 +622,8 @@ gemm_kernel(GemmArgs p) {
                   acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[jj][e], acc[i][jj], 0, 0, 0);
         }
         __builtin_amdgcn_s_setprio(0);
-        st = st == 2 ? 0 : st + 1;
-        st2 = st2 == 2 ? 0 : st2 + 1;
+        st = st == NSTAGE - 1 ? 0 : st + 1;
+        st2 = st2 == NSTAGE - 1 ? 0 : st2 + 1;
       }
       lds_barrier();   // every wave is done with the stages before an epilogue reuses them
     };

@@ -789,11 +789,9 @@ small_k_relax_epi_kernel(const float* __restrict__ A0, const float* __restrict__
       if (Ap) *reinterpret_cast<float4*>(Ap + m * P + p0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
       *reinterpret_cast<float4*>(An + m * P + p0) = make_float4(out[0], out[1], out[2], out[3]);
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      sb += __shfl_xor(sb, off, 64);
-      if (cvec_next) sc += __shfl_xor(sc, off, 64);
-    }
+    // fixed-order DPP wave sums (VALU only, no LDS round trips)
+    sb = wave_sum(sb);
+    if (cvec_next) sc = wave_sum(sc);
     if (lane == 0) {
       pb[(int64_t)chunk * M + m] = sb;
       if (cvec_next) pc[(int64_t)chunk * M + m] = sc;
