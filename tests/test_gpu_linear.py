@@ -453,3 +453,56 @@ def test_multi_tensor_steps_equal_single_tensor_steps(layout):
     for i in range(len(P)):
         assert torch.equal(dst0[i], dst1[i]), f"masked copy tensor {i}"
         assert torch.equal(out0[i], out1[i]), f"split term tensor {i}"
+
+
+@pytest.mark.parametrize("with_alpha", [True, False])
+def test_relu_grad_matches_formula(with_alpha):
+    """bf_relu_grad (the reverse pass through one ReLU relaxation), on aligned storage and on
+    storage one float off alignment (the same bits), against the gradient of the relaxed
+    coefficient in float64: g_in = g * slope_sel + G * bias_sel, dL/dalpha = sum_s g * A over
+    A >= 0 on passed ambiguous neurons, dL/dbeta = -split * sum_s g."""
+    dev = device()
+    announce(f"bf_relu_grad against its formula (alpha={with_alpha})")
+    g = torch.Generator().manual_seed(33)
+    D, S, N = 37, 9, 132
+    c = torch.randn(D, N, generator=g)
+    w = torch.rand(D, N, generator=g)
+    lo, hi = c - w, c + 0.5 * w
+    A = torch.randn(D * S, N, generator=g)
+    go = torch.randn(D * S, N, generator=g)
+    Gr = torch.randn(D * S, generator=g)
+    alpha = (torch.rand(D, N, generator=g) * 1.2 - 0.1) if with_alpha else None
+    split = torch.randint(-1, 2, (D, N), generator=g, dtype=torch.int8)
+    st = _lib.stream_handle()
+    outs = []
+    for off in (0, 1):
+        P = lambda x: None if x is None else _placed(x.to(dev), off if x.dtype != torch.int8 else 4 * off)  # noqa: E731
+        t = {k: P(v) for k, v in dict(lo=lo, hi=hi, A=A, go=go, alpha=alpha, split=split).items()}
+        Gd = Gr.to(dev)
+        gin = _placed(torch.empty(D * S, N, device=dev), off)
+        ga = _placed(torch.empty(D, N, device=dev), off)
+        gb = _placed(torch.empty(D, N, device=dev), off)
+        _lib.call("bf_relu_grad", _lib.ptr(t["go"]), _lib.ptr(t["A"]), S * N, D, S, N, _lib.ptr(t["lo"]),
+                  _lib.ptr(t["hi"]), _lib.ptr(t["alpha"]), N if with_alpha else 0, _lib.ptr(Gd), _lib.ptr(t["split"]),
+                  N, _lib.ptr(gin), _lib.ptr(ga), _lib.ptr(gb), st)
+        outs.append((gin.cpu(), ga.cpu(), gb.cpu()))
+    torch.cuda.synchronize()
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+    gin, ga, gb = outs[0]
+    # the formulas in float64
+    l64, u64 = lo.double(), hi.double()
+    amb = (l64 < 0) & (u64 > 0)
+    au = torch.where(u64 <= 0, 0.0, torch.where(l64 >= 0, 1.0, u64 / (u64 - l64).clamp_min(1.1920928955078125e-07)))
+    bu = torch.where(amb, -l64 * au, 0.0)
+    al = torch.where(u64 <= 0, 0.0, torch.where(l64 >= 0, 1.0, alpha.double().clamp(0, 1) if with_alpha else 0.0))
+    A3, g3 = A.double().view(D, S, N), go.double().view(D, S, N)
+    nn = A3 >= 0
+    ref_in = torch.where(nn, g3 * al[:, None], g3 * au[:, None]) + Gr.double().view(D, S, 1) * torch.where(
+        nn, 0.0, bu[:, None])
+    assert torch.allclose(gin.double().view(D, S, N), ref_in, rtol=1e-5, atol=1e-6)
+    passed = amb & ((alpha >= 0) & (alpha <= 1) if with_alpha else torch.zeros_like(amb))
+    ref_ga = torch.where(passed, (torch.where(nn, g3 * A3, 0.0)).sum(1), 0.0)
+    ref_gb = -split.double() * g3.sum(1)
+    assert torch.allclose(ga.double(), ref_ga, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(gb.double(), ref_gb, rtol=1e-5, atol=1e-5)
