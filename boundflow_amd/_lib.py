@@ -29,6 +29,7 @@ F64 = ctypes.c_double
 SIGNATURES = {
     "bf_abi_version": (I32, []),
     "bf_last_error": (ctypes.c_char_p, []),
+    "bf_gemm_tile_config": (I32, [I64, I64, I32, I32, I32, I32]),
     "bf_gemm": (I32, [P, I64, P, I64, I32, I32, P, I64, I64, I64, I64, P]),
     "bf_gemm_rank1": (I32, [P, I64, P, I64, I32, P, I64, I64, I64, I64, I64, P, P, I64, P, I64, P]),
     "bf_gemm_rank1_workspace": (I64, [I64, I64, I64]),

@@ -46,31 +46,55 @@ __global__ void relax_table_kernel(const float* __restrict__ lo, const float* __
   out[i] = make_float4(r.au, r.bu, r.al, r.bl);
 }
 
-// BOUNDFLOW_GEMM_TILE=G or =H forces one configuration (for measurement); read
+// BOUNDFLOW_GEMM_TILE=G, =H or =Q forces one configuration (for measurement); read
 // once when the library is loaded, constant afterwards.
 static int forced_tile_from_env() {
   const char* v = std::getenv("BOUNDFLOW_GEMM_TILE");
   if (v == nullptr) return 0;
   if (std::strcmp(v, "G") == 0) return 'G';
   if (std::strcmp(v, "H") == 0) return 'H';
+  if (std::strcmp(v, "Q") == 0) return 'Q';
   return 0;
 }
+
+// Share of the busiest CU's work that is useful when `tiles` equal tiles are dealt
+// over the device's 256 CUs (tiles / 256 per CU on average, the ceiling on the
+// busiest one).
+static double quantization_efficiency(int64_t tiles) {
+  const int64_t per_cu = ceil_div(tiles, (int64_t)256);
+  return (double)tiles / (double)(256 * per_cu);
+}
 static const int kForcedTile = forced_tile_from_env();
+
+// Tile configuration of a contraction: 'G', 'H' or 'Q'.  ks: K chunks of a split
+// contraction (1 when unsplit); dl: the operands suit the direct-to-LDS loop.
+int gemm_tile_choice(int64_t M, int64_t N, int nz, int64_t ks, int pro, bool dl) {
+  if (kForcedTile) return kForcedTile;
+  // measured on the benchmark shapes: the 8-wave TileG at 3 workgroups per CU for
+  // every form; a grid with fewer 128 x 128 tiles than the device has CUs takes the
+  // 16-wave TileH instead, which spreads each tile's contraction over twice the waves.
+  const int64_t wgs = ceil_div(M, 128) * ceil_div(N, 128) * nz * ks;
+  if (wgs < 256) return 'H';
+  // A grid whose 128 x 128 tiles leave the CUs unevenly loaded (C5's 576 tiles: 2.25
+  // per CU run at the cost of 3) takes the 64 x 128 TileQ, whose twice as many tiles
+  // at 6 workgroups per CU even it out (4.5 per CU at the cost of 5); TileQ is a few
+  // per cent slower per flop, so only a clear gain in balance picks it.
+  const int64_t wgs_q = ceil_div(M, 64) * ceil_div(N, 128) * nz * ks;
+  if (pro == PRO_PLAIN && dl && quantization_efficiency(wgs_q) > quantization_efficiency(wgs) + 0.1) return 'Q';
+  return 'G';
+}
 
 int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {
   if ((pro != PRO_PLAIN && pro != PRO_RELAX) || (epi != EPI_STORE && epi != EPI_ABSSUM && epi != EPI_RELAX)) {
     set_error("gemm_dispatch: bad mode pro=%d epi=%d", pro, epi);
     return BF_EINVAL;
   }
-  if (kForcedTile == 'G') return launch_tile<TileG>(a, pro, epi, nz, stream);
-  if (kForcedTile == 'H') return launch_tile<TileH>(a, pro, epi, nz, stream);
-  // measured on the benchmark shapes: the 8-wave TileG at 3 workgroups per CU for
-  // every form; a grid with fewer 128 x 128 tiles than the device has CUs takes the
-  // 16-wave TileH instead, which spreads each tile's contraction over twice the waves.
   const int64_t ks = (pro == PRO_PLAIN && epi == EPI_STORE && a.ksplit > 1) ? a.ksplit : 1;
-  const int64_t wgs = ceil_div(a.M, 128) * ceil_div(a.N, 128) * nz * ks;
-  if (wgs < 256) return launch_tile<TileH>(a, pro, epi, nz, stream);
-  return launch_tile<TileG>(a, pro, epi, nz, stream);
+  switch (gemm_tile_choice(a.M, a.N, nz, ks, pro, gemm_dl_operands(a, nz))) {
+    case 'H': return launch_tile<TileH>(a, pro, epi, nz, stream);
+    case 'Q': return launch_tile<TileQ>(a, pro, epi, nz, stream);
+    default: return launch_tile<TileG>(a, pro, epi, nz, stream);
+  }
 }
 
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,

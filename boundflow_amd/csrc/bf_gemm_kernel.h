@@ -43,9 +43,12 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // tile configuration used with EPI_ABSSUM has BN == NORM_BN.
 constexpr int NORM_BN = 128;
 
-template <int BM_, int BN_, int BK_, int NWM_, int NWN_, int OCC_>
+// DL_ONLY_: the configuration is built for the direct-to-LDS loop alone (its
+// occupancy needs that loop's LDS footprint); other operands are refused.
+template <int BM_, int BN_, int BK_, int NWM_, int NWN_, int OCC_, bool DL_ONLY_ = false>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, NWM = NWM_, NWN = NWN_, OCC = OCC_;
+  static constexpr bool DL_ONLY = DL_ONLY_;
   static constexpr int NT = 64 * NWM * NWN;          // threads (OCC: workgroups per CU, see gemm_waves_per_simd)
   static constexpr int WTM = BM / NWM;               // wave tile rows
   static constexpr int WTN = BN / NWN;               // wave tile cols
@@ -886,8 +889,20 @@ gemm_kernel(GemmArgs p) {
 }
 
 // Tile configurations (selected per call by gemm_dispatch).
-using TileG = Tile<128, 128, 16, 4, 2, 3>;   // 8 waves of 32x64: twice the waves per CU of TileA
+using TileG = Tile<128, 128, 16, 4, 2, 3>;   // 8 waves of 32x64, 3 workgroups per CU
 using TileH = Tile<128, 128, 32, 4, 4, 2>;   // 16 waves of 32x32, BK 32, 2 workgroups per CU (64 VGPRs)
+using TileQ = Tile<64, 128, 16, 2, 2, 6, true>;   // 4 waves of 32x64, 6 workgroups per CU (two LDS stages)
+
+// Operands the direct-to-LDS loop takes: transposed B and whole aligned float4 rows.
+inline bool gemm_dl_operands(const GemmArgs& a, int nz) {
+  bool dl = a.trans_b && (a.K & 3) == 0 && (a.lda & 3) == 0 && (a.lda_d & 3) == 0 && (a.ldb & 3) == 0 &&
+            ((uintptr_t)a.B & 15) == 0;
+  for (int z = 0; z < nz; ++z) dl = dl && ((uintptr_t)a.A[z] & 15) == 0;
+  return dl;
+}
+
+template <int PRO, int EPI, class T>
+static int launch_gemm_staged(const GemmArgs& a, dim3 grid, hipStream_t stream);
 
 template <int PRO, int EPI, class T>
 static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
@@ -899,16 +914,23 @@ static int launch_gemm_t(const GemmArgs& a, int nz, hipStream_t stream) {
   const unsigned gy = (PRO == PRO_PLAIN && EPI == EPI_STORE && a.ksplit > 1) ? (unsigned)(a.ksplit * nz) : (unsigned)nz;
   dim3 grid((unsigned)(ceil_div(ntiles, 8) * 8), gy);
   if constexpr (PRO == PRO_PLAIN && T::BK == 16) {
-    // the direct-to-LDS loop copies whole aligned float4s
-    bool dl = a.trans_b && (a.K & 3) == 0 && (a.lda & 3) == 0 && (a.lda_d & 3) == 0 && (a.ldb & 3) == 0 &&
-              ((uintptr_t)a.B & 15) == 0;
-    for (int z = 0; z < nz; ++z) dl = dl && ((uintptr_t)a.A[z] & 15) == 0;
-    if (dl) {
+    if (gemm_dl_operands(a, nz)) {
       hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T, true>), grid, dim3(T::NT), 0, stream, a);
       BF_LAUNCH_CHECK("gemm_kernel");
       return BF_OK;
     }
   }
+  if constexpr (T::DL_ONLY) {
+    set_error("gemm: this tile configuration takes only the direct-to-LDS operands (plain prologue, "
+              "transposed B, 16-byte aligned float4 rows)");
+    return BF_EINVAL;
+  } else {
+    return launch_gemm_staged<PRO, EPI, T>(a, grid, stream);
+  }
+}
+
+template <int PRO, int EPI, class T>
+static int launch_gemm_staged(const GemmArgs& a, dim3 grid, hipStream_t stream) {
   if (a.trans_b) {
     hipLaunchKernelGGL((gemm_kernel<PRO, EPI, true, T>), grid, dim3(T::NT), 0, stream, a);
   } else {
@@ -947,5 +969,6 @@ int launch_tile(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream)
 
 template <> int launch_tile<TileG>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileH>(const GemmArgs&, int, int, int, hipStream_t);
+template <> int launch_tile<TileQ>(const GemmArgs&, int, int, int, hipStream_t);
 
 }  // namespace bf

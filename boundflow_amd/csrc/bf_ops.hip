@@ -28,6 +28,7 @@ void set_error(const char* fmt, ...) {
 namespace bf {
 
 int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream);
+int gemm_tile_choice(int64_t M, int64_t N, int nz, int64_t ks, int pro, bool dl);
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
                         const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream);
 int gemm_partial_count(int64_t N);
@@ -861,6 +862,11 @@ extern "C" {
 int bf_abi_version(void) { return 1; }
 
 const char* bf_last_error(void) { return g_err; }
+
+int bf_gemm_tile_config(int64_t M, int64_t N, int nz, int ksplit, int relax_prologue, int dl_operands) {
+  if (M <= 0 || N <= 0 || nz < 1 || nz > 2 || ksplit < 1) return 0;
+  return gemm_tile_choice(M, N, nz, ksplit, relax_prologue ? PRO_RELAX : PRO_PLAIN, dl_operands != 0);
+}
 
 int bf_gemm(const float* A, int64_t lda, const float* B, int64_t ldb, int trans_b, int abs_b, float* C, int64_t ldc,
             int64_t M, int64_t N, int64_t K, hipStream_t stream) {

@@ -88,3 +88,24 @@ def test_binding_argument_types_match_header():
         for i, (h, b) in enumerate(zip(h_args, args)):
             assert norm.get(h, h) == norm.get(b, b), f"{name}: parameter {i} is {h.__name__} in the header, " \
                                                      f"{b.__name__} in the binding"
+
+
+def test_tile_configuration_rule():
+    """The contraction's tile choice (a host-side rule, no device call): 128 x 128
+    TileG for evenly loaded grids (C2), TileH for grids of fewer 128 x 128 tiles than
+    CUs (C1, C4, D1), the 64 x 128 TileQ for C5's unevenly loaded 36 864-row grids
+    on direct-to-LDS operands with the plain prologue, and 0 for bad sizes."""
+    from boundflow_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built (run python -m boundflow_amd.build)")
+    if os.environ.get("BOUNDFLOW_GEMM_TILE"):
+        pytest.skip("tile forced by the environment")
+    cfg = lambda *a: chr(_lib.load().bf_gemm_tile_config(*a)) if _lib.load().bf_gemm_tile_config(*a) else ""
+    assert cfg(36864, 256, 1, 1, 0, 1) == "Q"      # C5 gradient / relaxation-epilogue contractions
+    assert cfg(36864, 784, 1, 1, 0, 1) == "G"      # C5 concretization: 2016 tiles, even enough
+    assert cfg(36864, 256, 2, 1, 0, 1) == "G"      # both bounds: 1152 tiles, 4.5 per CU either way
+    assert cfg(128000, 500, 2, 1, 0, 1) == "G"     # C2 refinements
+    assert cfg(2304, 500, 2, 1, 0, 1) == "H"       # C2's final spec query
+    assert cfg(36864, 256, 1, 1, 1, 1) == "G"      # relaxation prologue: TileQ takes the plain one only
+    assert cfg(36864, 256, 1, 1, 0, 0) == "G"      # operands the direct-to-LDS loop does not take
+    assert cfg(0, 256, 1, 1, 0, 1) == "" and cfg(10, 10, 3, 1, 0, 1) == ""

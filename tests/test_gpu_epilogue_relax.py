@@ -45,21 +45,26 @@ def _table(lo, hi, alpha, dev):
 # S = 9: up to 16 domains per tile (entries read from global memory).  N <= 16 with no
 # prologue relaxation: the short-contraction kernel (a wave per domain and 256 columns;
 # P = 300 gives two column chunks, the second partial), with or without the region's bias.
-@pytest.mark.parametrize("S,prologue,alpha,add,cvec,N,bias_only", [
-    (20, True, True, True, True, 150, False),
-    (20, False, False, False, False, 150, False),
-    (9, True, False, True, True, 150, False),
-    (40, False, True, True, False, 150, False),
-    (9, False, True, True, True, 10, True),
-    (20, False, False, False, False, 16, False),
-    (3, False, True, False, True, 7, True),
+# D = 2048 with the plain prologue: 18 432 rows, a grid that takes the 64 x 128 tile
+# configuration (its 128 x 128 tiles would load the CUs unevenly).
+@pytest.mark.parametrize("S,prologue,alpha,add,cvec,N,bias_only,D", [
+    (20, True, True, True, True, 150, False, 13),
+    (20, False, False, False, False, 150, False, 13),
+    (9, True, False, True, True, 150, False, 13),
+    (40, False, True, True, False, 150, False, 13),
+    (9, False, True, True, True, 10, True, 13),
+    (20, False, False, False, False, 16, False, 13),
+    (3, False, True, False, True, 7, True, 13),
+    (9, False, True, True, True, 150, False, 2048),
 ])
-def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec, N, bias_only):
+def test_two_region_step_matches_oracle(S, prologue, alpha, add, cvec, N, bias_only, D):
     dev = device()
-    announce(f"relax epilogue step S={S} N={N} prologue={prologue} bias_only={bias_only} alpha={alpha} add={add} "
-             f"cvec={cvec}")
+    announce(f"relax epilogue step D={D} S={S} N={N} prologue={prologue} bias_only={bias_only} alpha={alpha} "
+             f"add={add} cvec={cvec}")
     g = torch.Generator().manual_seed(S * 3 + prologue + N)
-    D, P = 13, 300
+    P = 300
+    if D > 13:
+        assert chr(_lib.load().bf_gemm_tile_config(D * S, P, 2, 1, 0, 1)) == "Q"
     A_u = torch.randn(D, S, N, generator=g)
     A_l = torch.randn(D, S, N, generator=g)
     l1, u1 = _pre(D, N, g)
