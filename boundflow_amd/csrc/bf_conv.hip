@@ -238,7 +238,8 @@ conv_mfma_kernel(GatherArgs g) {
   float* As = reinterpret_cast<float*>(koff + g.Kc4);            // [Cm][Hp][Wp]
   __shared__ float red[GTM / 64];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: task indices stay scalar
   const int z = blockIdx.y;
   const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
   const float* __restrict__ X = g.X[z];
@@ -430,7 +431,8 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
   float* Mp = Ws + (size_t)g.nclasses * g.Kc4 * g.npad;              // [Hp][Wp][CP]
   __shared__ float red[GTM / 64][2];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: task indices stay scalar
   const int z = blockIdx.y;
   const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
   const float* __restrict__ X = g.X[z];
@@ -702,7 +704,8 @@ conv_t_small_kernel(SmallTArgs g) {
   float* Xs = Wsm + (size_t)g.Ci * g.Co4 * 16;          // [Co4][nblk * 16]
   float* Zs = Xs + (size_t)g.Co4 * g.nblk * 16;         // [16][nblk * 16]
   __shared__ float red[GTM / 64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: task indices stay scalar
   const int z = blockIdx.y;
   const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
   const float* __restrict__ X = g.X[z];
