@@ -180,7 +180,7 @@ struct GatherArgs {
   float* y[2];
   float* nrm[2];
   const float* W;
-  int abs_w;
+  int abs_w;           // MODE_F: bit z set -> operand pair z multiplies by |W|
   const float* wv;     // MODE_T norm weights [D, nout] (w_ld)
   const float* h_scale;
   float* h_out;
@@ -269,7 +269,7 @@ conv_mfma_kernel(GatherArgs g) {
         src = (int64_t)n * g.Kc + k;   // k = (ci * KH + kh) * KW + kw
       }
       float w = g.W[ok ? src : 0];
-      if (MODE == MODE_F && g.abs_w) w = fabsf(w);
+      if (MODE == MODE_F && ((g.abs_w >> z) & 1)) w = fabsf(w);
       wv[u] = ok ? w : 0.f;
     }
 #pragma unroll
@@ -942,9 +942,13 @@ int ibp_finalize(const float* c, const float* r, const float* rownorm, float eps
                  int* infeasible, hipStream_t stream);
 int fill_value(float* p, int64_t n, float v, hipStream_t stream);
 
+// conv2d of rows; with x2/y2 a second operand pair (abs_w2 for its weights) runs in
+// the same launch (blockIdx.y = 1), e.g. the center and the radius of an IBP layer.
 static int conv2d_launch(const float* x, int64_t in_div, int64_t R, int Ci, int Hi, int Wi, const float* W, int abs_w,
                          int Co, int KH, int KW, int sh, int sw, int ph, int pw, int Ho, int Wo, float* y,
-                         const float* rs, const float* v, int64_t v_div, int64_t v_ld, hipStream_t stream) {
+                         const float* rs, const float* v, int64_t v_div, int64_t v_ld, hipStream_t stream,
+                         const float* x2 = nullptr, float* y2 = nullptr, int abs_w2 = 0) {
+  const int nz = x2 ? 2 : 1;
   {
     GatherArgs g;
     memset(&g, 0, sizeof(g));
@@ -952,22 +956,31 @@ static int conv2d_launch(const float* x, int64_t in_div, int64_t R, int Ci, int 
     if (conv_f_mfma_plan(g, R, Ci, Hi, Wi, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, &glds)) {
       g.X[0] = x;
       g.y[0] = y;
+      g.X[1] = x2;
+      g.y[1] = y2;
       g.W = W;
-      g.abs_w = abs_w;
+      g.abs_w = (abs_w ? 1 : 0) | (abs_w2 ? 2 : 0);   // bit z: operand pair z uses |W|
       g.in_div = in_div;
       g.rs = rs;
       g.v = v;
       g.v_div = v_div;
       g.v_ld = v_ld;
       g.S = 1;
-      g.rows_per_wg = gather_rows_per_wg(R);
+      g.rows_per_wg = gather_rows_per_wg(R * nz);
       const int rpw = g.rows_per_wg;
       BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "conv2d: too many rows");
-      hipLaunchKernelGGL(conv_mfma_kernel<MODE_F>, dim3((unsigned)((R + rpw - 1) / rpw), 1), dim3(GTM), glds, stream,
+      hipLaunchKernelGGL(conv_mfma_kernel<MODE_F>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream,
                          g);
       BF_LAUNCH_CHECK("conv_mfma_kernel<conv2d>");
       return BF_OK;
     }
+  }
+  if (x2) {
+    const int rc = conv2d_launch(x, in_div, R, Ci, Hi, Wi, W, abs_w, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, y, rs, v,
+                                 v_div, v_ld, stream);
+    if (rc) return rc;
+    return conv2d_launch(x2, in_div, R, Ci, Hi, Wi, W, abs_w2, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, y2, rs, v, v_div,
+                         v_ld, stream);
   }
   const size_t lds = sizeof(float) * (size_t)Ci * Hi * Wi;
   BF_REQUIRE(lds <= 64 * 1024, "conv2d: input map of %d x %d x %d exceeds the 64 KB LDS row stage", Ci, Hi, Wi);
@@ -1201,23 +1214,20 @@ int bf_ibp_conv2d(const float* in_lo, const float* in_hi, int64_t B, int Ci, int
   float* r = c + B * nout;
   float* cdst = center_out ? center_out : c;
   int rc;
+  // the center (W) and the radius (|W|) products in one launch
   if (input_kind == 1) {
     // center x0 conv W; the radius map is eps everywhere inside the image (padding has none)
-    rc = conv2d_launch(in_lo, 1, B, Ci, Hi, Wi, W, 0, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, cdst, nullptr, nullptr, 1, 0,
-                       stream);
-    if (rc) return rc;
     rc = fill_value(rad, B * nin, eps, stream);
     if (rc) return rc;
+    rc = conv2d_launch(in_lo, 1, B, Ci, Hi, Wi, W, 0, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, cdst, nullptr, nullptr, 1, 0,
+                       stream, rad, r, 1);
   } else {
     BF_REQUIRE(in_hi, "bf_ibp_conv2d: interval input needs in_hi");
     rc = ibp_center_radius(in_lo, in_hi, B * nin, apply_relu, mid, rad, stream);
     if (rc) return rc;
     rc = conv2d_launch(mid, 1, B, Ci, Hi, Wi, W, 0, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, cdst, nullptr, nullptr, 1, 0,
-                       stream);
-    if (rc) return rc;
+                       stream, rad, r, 1);
   }
-  rc = conv2d_launch(rad, 1, B, Ci, Hi, Wi, W, 1, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, r, nullptr, nullptr, 1, 0,
-                     stream);
   if (rc) return rc;
   return ibp_finalize(cdst, r, nullptr, 0.f, bias, (int64_t)Ho * Wo, split, split_ld, B, nout, out_lo, out_hi,
                       infeasible, stream);

@@ -307,7 +307,7 @@ __global__ void branch_update_native_kernel(const float* __restrict__ lo, const 
                                             int* __restrict__ best_idx, float* __restrict__ best_lo,
                                             float* __restrict__ best_hi) {
   const int lane = threadIdx.x & 63;
-  const int64_t d = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t d = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (d >= D) return;
   double w = -1.0;
   int idx = -1;

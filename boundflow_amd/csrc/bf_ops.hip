@@ -99,12 +99,29 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
   const int64_t b = div_rows(i, N, B * N < (1LL << 31)), n = i - b * N;
   float cv, rv = 0.f;
   if (part) {
+    // the K chunks summed in order, their loads issued eight at a time
     const int64_t BN = B * N;
-    cv = part[i];
-    for (int s = 1; s < ks; ++s) cv += part[(int64_t)s * BN + i];
-    if (two) {
-      rv = part[(int64_t)ks * BN + i];
-      for (int s = 1; s < ks; ++s) rv += part[(int64_t)(ks + s) * BN + i];
+    const float* __restrict__ pc = part + i;
+    const float* __restrict__ pr = part + (int64_t)ks * BN + i;
+    cv = pc[0];
+    if (two) rv = pr[0];
+    int s = 1;
+    for (; s + 8 <= ks; s += 8) {
+      float tc[8], tr[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        tc[q] = pc[(int64_t)(s + q) * BN];
+        tr[q] = two ? pr[(int64_t)(s + q) * BN] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        cv += tc[q];
+        rv += tr[q];
+      }
+    }
+    for (; s < ks; ++s) {
+      cv += pc[(int64_t)s * BN];
+      if (two) rv += pr[(int64_t)s * BN];
     }
     if (c_out) c_out[i] = cv;
   } else {
@@ -249,7 +266,7 @@ ibp_batched_linear_kernel(const float* __restrict__ lo, const float* __restrict_
                           const float* __restrict__ W, const float* __restrict__ bias, int64_t O,
                           float* __restrict__ olo, float* __restrict__ ohi) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (r >= B * O) return;
   const int64_t b = r / O;
   float c = 0.f, d = 0.f;
@@ -332,7 +349,7 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
                        float* __restrict__ Al_out, float* __restrict__ bu_out, float* __restrict__ bl_out,
                        float* __restrict__ cu_out, float* __restrict__ cl_out) {
   const int lane = threadIdx.x & 63;
-  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (m >= M) return;
   const int64_t d = m / S;
   const int64_t a_row = d * a_dstride + (m - d * S) * K;   // input row (shared by all domains when a_dstride = 0)
@@ -395,8 +412,9 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
   constexpr int WPR = TPR / 64;    // waves per row
   __shared__ float red[6][256 / 64];
   const int t = threadIdx.x % TPR;
-  const int64_t m = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
-  const bool live = m < M;   // uniform per wave (TPR >= 64)
+  // the row is uniform per wave (TPR >= 64): its index and address arithmetic stay scalar
+  const int64_t m = (int64_t)blockIdx.x * RPB + __builtin_amdgcn_readfirstlane(threadIdx.x / TPR);
+  const bool live = m < M;
   float s[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // su, sl, ku, kl, cu, cl
   if (live) {
     const int64_t d = div_rows(m, S, M < (1LL << 31));
@@ -480,7 +498,7 @@ concretize_rows_kernel(const float* __restrict__ A, int64_t M, int64_t S, int64_
                        const float* __restrict__ rad, float eps, const float* __restrict__ b, int is_lower,
                        float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (m >= M) return;
   const int64_t d = m / S;
   float c = 0.f, nrm = 0.f;
@@ -526,7 +544,7 @@ __global__ void branch_update_kernel(const float* __restrict__ lo, const float* 
                                      int64_t N, int layer, float* __restrict__ best_gap, int* __restrict__ best_layer,
                                      int* __restrict__ best_idx) {
   const int lane = threadIdx.x & 63;
-  const int64_t d = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t d = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (d >= D) return;
   float g = -INFINITY;
   int idx = 0;
