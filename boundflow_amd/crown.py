@@ -60,10 +60,10 @@ def derived(tag: str, sources: Tuple[torch.Tensor, ...], make: Callable[[], torc
       bump the version and is not seen: change parameters through the tensor itself.
     * A hit on another stream than the one that made the entry waits for the producer
       (an event recorded after ``make()``), so the consumer never reads it half-written.
-    * Inside ``derived_scope()`` (graph capture) entries live in the scope's own dict:
-      the captured graph then contains the kernels that make them and recomputes them on
-      every replay, so a replay sees in-place parameter updates and never reads an entry
-      the process-wide cache has since evicted."""
+    * Inside ``derived_scope()`` (graph capture) entries live in the scope's own dict,
+      which the captured query keeps: a replay never reads an entry the process-wide
+      cache has since evicted, and ``refresh_scope`` remakes (in place, before a replay)
+      every entry whose source changed in place since it was made."""
     scope = getattr(_SCOPE, "memo", None)
     table = _DERIVED if scope is None else scope
     key = (tag,) + tuple(id(t) for t in sources)
@@ -83,23 +83,41 @@ def derived(tag: str, sources: Tuple[torch.Tensor, ...], make: Callable[[], torc
         stream = torch.cuda.current_stream(out.device)
         event = torch.cuda.Event()
         event.record(stream)
-    table[key] = (tuple(sources), versions, (out, stream, event))
+    table[key] = (tuple(sources), versions, (out, stream, event), make if scope is not None else None)
     if scope is None and len(_DERIVED) > _DERIVED_MAX:
         _DERIVED.popitem(last=False)
     return out
 
 
 @contextlib.contextmanager
-def derived_scope():
-    """Route ``derived`` to a fresh dict for the duration (used around graph capture);
-    yields that dict, which the caller keeps as long as the captured work may run."""
+def derived_scope(memo: Optional[dict] = None):
+    """Route ``derived`` to ``memo`` (a fresh dict when None) for the duration (used
+    around graph capture); yields that dict, which the caller keeps as long as the
+    captured work may run."""
     prev = getattr(_SCOPE, "memo", None)
-    memo: dict = {}
+    memo = {} if memo is None else memo
     _SCOPE.memo = memo
     try:
         yield memo
     finally:
         _SCOPE.memo = prev
+
+
+def refresh_scope(memo: dict) -> int:
+    """Remake, into the same storage, every entry of a ``derived_scope`` dict whose
+    sources changed in place since it was made (in the order the entries were made,
+    so an entry derived from another sees the remade one); returns the number remade.
+    Runs on the current stream, ahead of whatever is queued after it."""
+    n = 0
+    with derived_scope(memo):
+        for key, (sources, versions, (out, stream, event), make) in list(memo.items()):
+            now = tuple(t._version for t in sources)
+            if now == versions:
+                continue
+            out.copy_(make())
+            memo[key] = (sources, now, (out, stream, event), make)
+            n += 1
+    return n
 
 
 def call_memo(save: Optional[dict], key: str, make: Callable[[], torch.Tensor]) -> torch.Tensor:

@@ -10,10 +10,12 @@ addresses, no host synchronization (the split-infeasibility check of the
 forward trace is one: queries with splits or constraints are not capturable),
 and no memset nodes (the library clears buffers with fill kernels).  Inputs may
 be changed in place between replays (``copy_`` into the input box or center):
-everything derived from them, and from the parameters, is recomputed inside
-the graph.  The
-outputs of a replay live in the graph's private memory pool and are
-overwritten by the next replay.
+everything derived from them is recomputed inside the graph.  Operands derived
+from the parameters (weight transposes, bias maps, packed conv weights) are
+made once, before the capture, into storage the captured query keeps; a
+parameter changed in place between replays has its operands remade into that
+storage before the next replay.  The outputs of a replay live in the graph's
+private memory pool and are overwritten by the next replay.
 """
 
 from __future__ import annotations
@@ -28,22 +30,24 @@ class CapturedQuery:
     returns the (graph-owned) outputs of that replay."""
 
     def __init__(self, fn: Callable[[], Any], *, warmup: int = 2):
+        from .crown import derived_scope
+        # parameter-derived operands are made by the warm-up calls into a dict this
+        # object keeps (never evicted, unlike the process-wide cache), so the graph
+        # reads them instead of recomputing them on every replay
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(warmup):
+        with derived_scope() as self._derived, torch.cuda.stream(side):
+            for _ in range(max(1, warmup)):
                 fn()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
-        # parameter-derived operands (weight transposes, bias maps) are made inside the
-        # graph, once per replay, instead of read from the process-wide cache: a replay
-        # then sees in-place parameter updates and never reads an evicted entry
-        from .crown import derived_scope
-        with derived_scope() as self._derived, torch.cuda.graph(self.graph):
+        with derived_scope(self._derived), torch.cuda.graph(self.graph):
             self.outputs = fn()
         torch.cuda.synchronize()
 
     def __call__(self) -> Any:
+        from .crown import refresh_scope
+        refresh_scope(self._derived)   # parameters changed in place since the last replay
         self.graph.replay()
         return self.outputs

@@ -93,9 +93,9 @@ def test_captured_domain_batch_replays_match_eager():
 def test_replay_sees_inputs_and_parameters_changed_in_place():
     """A captured C1 query (box input) after ``copy_`` of a different box into the
     perturbation and an in-place change of a layer weight: the replay recomputes
-    the box radius and the weight transposes inside the graph, so it equals an
-    eager query on the new values (and the process-wide operand cache, filled by
-    eager queries before the change, is not read by the graph)."""
+    the box radius inside the graph, and the weight transposes the graph reads
+    (kept by the captured query, not by the process-wide cache) are remade in
+    place before the replay, so it equals an eager query on the new values."""
     dev = device()
     announce("graph replay after in-place input and parameter updates (C1, batch 16)")
     wd = wl.to_device(wl.subset(wl.make_c1(), 16), dev)
