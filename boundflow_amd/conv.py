@@ -119,12 +119,18 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
         if save is not None:
             save.setdefault("relaxed", {})[layer.op_index] = keep_l
         return y_u, y_l, nb_u, nb_l, S * n_in, None
-    rA_u = torch.empty_like(A_u) if A_u is not None else None
-    rA_l = torch.empty_like(A_l) if A_l is not None else None
     nb_u = torch.empty(M, device=dev) if A_u is not None else None
     nb_l = torch.empty(M, device=dev) if A_l is not None else None
     c_u = torch.empty(M, device=dev) if (A_u is not None and cvec is not None) else None
     c_l = torch.empty(M, device=dev) if (A_l is not None and cvec is not None) else None
+    if is_first and cvec is not None and _lib.load().bf_conv_transpose_small_supported(
+            Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi):
+        # input layer: relaxation, transposed conv and concretization norm in one pass
+        return _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, alpha, alpha_ld, add,
+                                  add_ld, kbias, cvec, W, geo=(Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi),
+                                  nb=(nb_u, nb_l), c=(c_u, c_l), flops=flops, nz=nz, layer=layer)
+    rA_u = torch.empty_like(A_u) if A_u is not None else None
+    rA_l = torch.empty_like(A_l) if A_l is not None else None
     with _timed("crown_relu_relax", 0.0, 4.0 * nz * 2 * M * n_out):
         _lib.call("bf_crown_relu_relax_lu", _lib.ptr(A_u), _lib.ptr(A_l), S * n_out, B, S, n_out, _lib.ptr(pre_lo),
                   _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld, _lib.ptr(kbias), _lib.ptr(cvec),
@@ -164,6 +170,51 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
                   _lib.ptr(h_scale), _lib.ptr(h_out), stream)
     if save is not None:
         save.setdefault("relaxed", {})[layer.op_index] = rA_l
+    lb = torch.empty(B, S, device=dev) if A_l is not None else None
+    ub = torch.empty(B, S, device=dev) if A_u is not None else None
+    _lib.call("bf_concretize_finalize", _lib.ptr(norm_u), _lib.ptr(norm_l), 1, M, _lib.ptr(c_u), _lib.ptr(c_l),
+              _lib.ptr(nb_u), _lib.ptr(nb_l), eps, _lib.ptr(lb), _lib.ptr(ub), stream)
+    return None, None, None, None, 0, IntervalState(lower=lb, upper=ub)
+
+
+def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, alpha, alpha_ld, add, add_ld, kbias,
+                       cvec, W, geo, nb, c, flops, nz, layer):
+    """The input conv layer through bf_crown_relu_conv_transpose_concretize: the ReLU
+    relaxation applied while each row is staged, the transposed conv reduced to the
+    concretization norm (and the gradient seed), the relaxed rows written only for a
+    gradient pass; then the bounds from the norms, centers and biases."""
+    dev = spec.center.device
+    stream = _lib.stream_handle()
+    Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi = geo
+    n_out, n_in = Co * Ho * Wo, Ci * Hi * Wi
+    nb_u, nb_l = nb
+    c_u, c_l = c
+    pert = spec.perturbation
+    if isinstance(pert, BoxPerturbation):
+        rad = ((pert.upper - pert.lower) / 2.0).reshape(B, n_in).contiguous()
+        eps = 1.0
+    else:
+        rad = None
+        eps = float(pert.eps)
+    norm_u = torch.empty(M, device=dev) if A_u is not None else None
+    norm_l = torch.empty(M, device=dev) if A_l is not None else None
+    h_scale = h_out = None
+    if save is not None and save.get("grad_rows") is not None:
+        h_scale = call_memo(save, f"h_scale:{eps!r}", lambda: (save["grad_rows"] * (-eps)).contiguous())
+        h_out = torch.empty(M, n_in, device=dev)
+        save["h"] = h_out
+        save["cvec"] = cvec
+    rel_l = torch.empty(M, n_out, device=dev) if (save is not None and A_l is not None) else None
+    with _timed("crown_relu_conv_transpose_concretize", flops,
+                4.0 * nz * (M * n_out + 2 * B * n_out) + (4.0 * M * n_out if rel_l is not None else 0.0)):
+        _lib.call("bf_crown_relu_conv_transpose_concretize", _lib.ptr(A_u), _lib.ptr(A_l), B, S, Co, Ho, Wo,
+                  _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld,
+                  _lib.ptr(kbias), _lib.ptr(cvec), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(W), Ci, KH, KW, sh, sw, ph,
+                  pw, Hi, Wi, _lib.ptr(rad), n_in, _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(norm_u),
+                  _lib.ptr(norm_l), _lib.ptr(nb_u), _lib.ptr(nb_l), _lib.ptr(c_u), _lib.ptr(c_l), None,
+                  _lib.ptr(rel_l), stream)
+    if save is not None:
+        save.setdefault("relaxed", {})[layer.op_index] = rel_l
     lb = torch.empty(B, S, device=dev) if A_l is not None else None
     ub = torch.empty(B, S, device=dev) if A_u is not None else None
     _lib.call("bf_concretize_finalize", _lib.ptr(norm_u), _lib.ptr(norm_l), 1, M, _lib.ptr(c_u), _lib.ptr(c_l),

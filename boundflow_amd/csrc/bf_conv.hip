@@ -421,7 +421,33 @@ struct ConvRelax {
   const float* b_in[2];
   float* b_out[2];
   float* relaxed[2];     // optional A' rows [R, nin]
+  const float* cvec;     // input layer only (conv_t_small_kernel): center projection [D, nin]
+  float* c_out[2];       //   and its row sums sum A' * cvec
 };
+
+// One element of a coefficient row through the ReLU relaxation (the sign-split
+// transform and the dense backward's bias term; slopes from the pre-activation box
+// as bf_crown_relu_relax_lu computes them): returns A', adds A * beta_sel to sb.
+__device__ __forceinline__ float relax_element(const ConvRelax& rx, bool lower, float v, float lo, float hi, float al,
+                                               float ad, float& sb) {
+  float4 t = make_float4(1.f, 0.f, 1.f, 0.f);
+  if (rx.lo) {
+    const bool has_alpha = rx.alpha != nullptr;
+    const Relax rr = relu_relax(lo, hi, has_alpha, has_alpha ? clamp01(al) : 0.f);
+    t = make_float4(rr.au, rr.bu, rr.al, rr.bl);
+  }
+  const bool nn = v >= 0.f;
+  float o;
+  if (lower) {
+    o = v * (nn ? t.z : t.x);
+    sb += v * (nn ? t.w : t.y);
+    if (rx.add) o = o + ad;
+  } else {
+    o = v * (nn ? t.x : t.z);
+    sb += v * (nn ? t.y : t.w);
+  }
+  return o;
+}
 
 template <bool RELAX>
 __global__ void __launch_bounds__(GTM)
@@ -697,13 +723,19 @@ struct SmallTArgs {
   FastDiv f_Wi, f_sh, f_sw, f_pitch;   // index divisions of the col2im and the map copy
 };
 
-__global__ void __launch_bounds__(GTM)
-conv_t_small_kernel(SmallTArgs g) {
+// RELAX: the input layer's ReLU relaxation applied while each row is staged, with
+// the row sums b_out = (b_in + sum A * beta_sel) + sum A' * kbias and
+// c_out = sum A' * cvec[d] reduced in the same pass (a wave sum per wave, then the
+// waves in order) and the relaxed rows written only when asked.
+template <bool RELAX>
+__global__ void __launch_bounds__(GTM, 6)   // 6 waves per SIMD: three workgroups per CU
+conv_t_small_kernel(SmallTArgs g, ConvRelax rx) {
   extern __shared__ float smem[];
   float* Wsm = smem;                                   // [Ci][Co4][16]: tap-fastest MFMA A operand
   float* Xs = Wsm + (size_t)g.Ci * g.Co4 * 16;          // [Co4][nblk * 16]
   float* Zs = Xs + (size_t)g.Co4 * g.nblk * 16;         // [16][nblk * 16]
   __shared__ float red[GTM / 64];
+  __shared__ float rred[GTM / 64][3];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: task indices stay scalar
   const int z = blockIdx.y;
@@ -731,19 +763,92 @@ conv_t_small_kernel(SmallTArgs g) {
     if (r >= g.R) break;   // uniform
     __syncthreads();       // weights staged / the previous row's maps consumed
     const float* __restrict__ xr = X + r * nin;
+    const int64_t d = r / g.S;
+    float sb = 0.f, sk = 0.f, sc = 0.f;
+    // the row's (uniform) bases of the relaxation operands
+    const float* __restrict__ lo_d = RELAX && rx.lo ? rx.lo + d * nin : nullptr;
+    const float* __restrict__ hi_d = RELAX && rx.lo ? rx.hi + d * nin : nullptr;
+    const float* __restrict__ al_d = RELAX && rx.alpha ? rx.alpha + d * rx.alpha_ld : nullptr;
+    const float* __restrict__ ad_d = RELAX && rx.add ? rx.add + d * rx.add_ld : nullptr;
+    const float* __restrict__ cv_d = RELAX && rx.cvec ? rx.cvec + d * nin : nullptr;
+    float* __restrict__ rel_r = RELAX && rx.relaxed[z] ? rx.relaxed[z] + r * nin : nullptr;
+    // element e of the row through the relaxation (RELAX), summed in each thread's order
+    auto relax_at = [&](int e, float v) -> float {
+      if constexpr (RELAX) {
+        const float lo = rx.lo ? rx.lo[d * nin + e] : 0.f, hi = rx.lo ? rx.hi[d * nin + e] : 0.f;
+        const float al = rx.alpha ? rx.alpha[d * rx.alpha_ld + e] : 0.f;
+        const float ad = (rx.add && lower) ? rx.add[d * rx.add_ld + e] : 0.f;
+        const float o = relax_element(rx, lower, v, lo, hi, al, ad, sb);
+        if (rx.kbias) sk += o * rx.kbias[e];
+        if (rx.cvec) sc += o * rx.cvec[d * nin + e];
+        if (rx.relaxed[z]) rx.relaxed[z][r * nin + e] = o;
+        return o;
+      } else {
+        return v;
+      }
+    };
     if (g.vec) {
       // unpadded map (npix % 16 == 0, 16-byte aligned rows): a float4 copy, then the zero channels
       const float4* __restrict__ x4 = reinterpret_cast<const float4*>(xr);
       float4* xs4 = reinterpret_cast<float4*>(Xs);
-      for (int q = tid; q < nin / 4; q += GTM) xs4[q] = x4[q];
+#pragma unroll 1
+      for (int q = tid; q < nin / 4; q += GTM) {
+        float4 v = x4[q];
+        if constexpr (RELAX) {
+          // the four elements' operands as float4 loads (16-byte aligned, checked by the host)
+          const int e = 4 * q;
+          const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+          auto ld4 = [](const float* p) { return *reinterpret_cast<const float4*>(p); };
+          const float4 lo4 = rx.lo ? ld4(lo_d + e) : zero;
+          const float4 hi4 = rx.lo ? ld4(hi_d + e) : zero;
+          const float4 al4 = rx.alpha ? ld4(al_d + e) : zero;
+          const float4 ad4 = (rx.add && lower) ? ld4(ad_d + e) : zero;
+          const float4 kb4 = rx.kbias ? ld4(rx.kbias + e) : zero;
+          const float4 cv4 = rx.cvec ? ld4(cv_d + e) : zero;
+          const float vv[4] = {v.x, v.y, v.z, v.w}, lo[4] = {lo4.x, lo4.y, lo4.z, lo4.w},
+                      hi[4] = {hi4.x, hi4.y, hi4.z, hi4.w}, al[4] = {al4.x, al4.y, al4.z, al4.w},
+                      ad[4] = {ad4.x, ad4.y, ad4.z, ad4.w}, kb[4] = {kb4.x, kb4.y, kb4.z, kb4.w},
+                      cv[4] = {cv4.x, cv4.y, cv4.z, cv4.w};
+          float o[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            o[u] = relax_element(rx, lower, vv[u], lo[u], hi[u], al[u], ad[u], sb);
+            if (rx.kbias) sk += o[u] * kb[u];
+            if (rx.cvec) sc += o[u] * cv[u];
+          }
+          v = make_float4(o[0], o[1], o[2], o[3]);
+          if (rx.relaxed[z]) *reinterpret_cast<float4*>(rel_r + e) = v;
+        }
+        xs4[q] = v;
+      }
       for (int idx = nin + tid; idx < g.Co4 * pitch; idx += GTM) Xs[idx] = 0.f;
     } else {
       for (int idx = tid; idx < g.Co4 * pitch; idx += GTM) {
         const int co = fdivq(idx, g.f_pitch), p = idx - co * pitch;
-        Xs[idx] = (co < g.Co && p < g.npix) ? xr[co * g.npix + p] : 0.f;
+        Xs[idx] = (co < g.Co && p < g.npix) ? relax_at(co * g.npix + p, xr[co * g.npix + p]) : 0.f;
       }
     }
-    const int64_t d = r / g.S;
+    if constexpr (RELAX) {
+      sb = wave_sum(sb);
+      sk = wave_sum(sk);
+      sc = wave_sum(sc);
+      if (lane == 0) {
+        rred[wave][0] = sb;
+        rred[wave][1] = sk;
+        rred[wave][2] = sc;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        float tb = 0.f, tk = 0.f, tc = 0.f;
+        for (int q = 0; q < GTM / 64; ++q) {
+          tb += rred[q][0];
+          tk += rred[q][1];
+          tc += rred[q][2];
+        }
+        if (rx.b_out[z]) rx.b_out[z][r] = ((rx.b_in[z] ? rx.b_in[z][r] : 0.f) + tb) + tk;
+        if (rx.c_out[z]) rx.c_out[z][r] = tc;
+      }
+    }
     const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
     float s = 0.f;
     for (int n = 0; n < g.Ci; ++n) {
@@ -1043,7 +1148,10 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
       const int rpw = gather_rows_per_wg(R * nz);
       g.rows_per_wg = rpw;
       BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
-      hipLaunchKernelGGL(conv_t_small_kernel, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g);
+      ConvRelax rx;
+      memset(&rx, 0, sizeof(rx));
+      hipLaunchKernelGGL(conv_t_small_kernel<false>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds,
+                         stream, g, rx);
       BF_LAUNCH_CHECK("conv_t_small_kernel");
       return BF_OK;
     }
@@ -1194,6 +1302,84 @@ int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, 
   hipLaunchKernelGGL(conv_t_hwc_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g,
                      rx);
   BF_LAUNCH_CHECK("conv_t_hwc_kernel<relax>");
+  return BF_OK;
+}
+
+int bf_conv_transpose_small_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph,
+                                      int pw, int Hi, int Wi) {
+  if (Co <= 0 || Ci <= 0 || KH <= 0 || KW <= 0 || sh <= 0 || sw <= 0 || Hi <= 0 || Wi <= 0 || Ho <= 0 || Wo <= 0)
+    return 0;
+  SmallTArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t lds = 0;
+  return conv_t_small_plan(g, 1, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &lds) ? 1 : 0;
+}
+
+int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
+                                            int Wo, const float* pre_lo, const float* pre_hi, const float* alpha,
+                                            int64_t alpha_ld, const float* add_l, int64_t add_ld, const float* kbias,
+                                            const float* cvec, const float* b_u_in, const float* b_l_in,
+                                            const float* W, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
+                                            int Hi, int Wi, const float* wvec, int64_t w_ld, const float* h_scale,
+                                            float* h_out, float* norm_u, float* norm_l, float* b_u_out,
+                                            float* b_l_out, float* c_u_out, float* c_l_out, float* relaxed_u,
+                                            float* relaxed_l, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && Co > 0 && Ci > 0, "bf_crown_relu_conv_transpose_concretize: bad sizes");
+  const int64_t R = D * S;
+  if (R == 0) return BF_OK;
+  BF_REQUIRE(W && (A_u || A_l), "bf_crown_relu_conv_transpose_concretize: null pointer");
+  BF_REQUIRE((A_u == nullptr) == (norm_u == nullptr) && (A_l == nullptr) == (norm_l == nullptr),
+             "bf_crown_relu_conv_transpose_concretize: each given coefficient needs its norm output");
+  BF_REQUIRE((pre_lo == nullptr) == (pre_hi == nullptr),
+             "bf_crown_relu_conv_transpose_concretize: pre_lo and pre_hi go together");
+  BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || norm_l != nullptr),
+             "bf_crown_relu_conv_transpose_concretize: h_out needs h_scale and the lower norm");
+  SmallTArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t glds = 0;
+  if (!conv_t_small_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
+    set_error("bf_crown_relu_conv_transpose_concretize: shape not supported (bf_conv_transpose_small_supported)");
+    return BF_EINVAL;
+  }
+  const unsigned nz = (A_u && A_l) ? 2u : 1u;
+  ConvRelax rx;
+  memset(&rx, 0, sizeof(rx));
+  rx.lo = pre_lo;
+  rx.hi = pre_hi;
+  rx.alpha = alpha;
+  rx.alpha_ld = alpha_ld;
+  rx.add = add_l;
+  rx.add_ld = add_ld;
+  rx.kbias = kbias;
+  rx.cvec = cvec;
+  int nzi = 0;
+  if (A_u) {
+    g.X[nzi] = A_u; g.nrm[nzi] = norm_u;
+    rx.b_in[nzi] = b_u_in; rx.b_out[nzi] = b_u_out; rx.c_out[nzi] = c_u_out; rx.relaxed[nzi] = relaxed_u;
+    ++nzi;
+  }
+  if (A_l) {
+    g.X[nzi] = A_l; g.nrm[nzi] = norm_l;
+    rx.b_in[nzi] = b_l_in; rx.b_out[nzi] = b_l_out; rx.c_out[nzi] = c_l_out; rx.relaxed[nzi] = relaxed_l;
+    ++nzi;
+  }
+  g.z_lower_first = A_u ? 0 : 1;
+  g.W = W;
+  g.wv = wvec;
+  g.w_ld = w_ld;
+  g.h_scale = h_scale;
+  g.h_out = h_out;
+  g.S = S;
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  g.vec = (g.npix % 16 == 0) && al16(A_u) && al16(A_l) && al16(pre_lo) && al16(pre_hi) && al16(alpha) &&
+          al16(add_l) && al16(kbias) && al16(cvec) && al16(relaxed_u) && al16(relaxed_l) &&
+          (alpha == nullptr || alpha_ld % 4 == 0) && (add_l == nullptr || add_ld % 4 == 0) ? 1 : 0;
+  const int rpw = gather_rows_per_wg(R * nz);
+  g.rows_per_wg = rpw;
+  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_crown_relu_conv_transpose_concretize: too many rows");
+  hipLaunchKernelGGL(conv_t_small_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream,
+                     g, rx);
+  BF_LAUNCH_CHECK("conv_t_small_kernel<relax>");
   return BF_OK;
 }
 

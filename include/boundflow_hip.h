@@ -263,6 +263,30 @@ int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, 
                                  float* b_u_out, float* b_l_out, float* relaxed_u, float* relaxed_l,
                                  hipStream_t stream);
 
+/* The input layer of a conv network in one pass: the ReLU relaxation of
+ * bf_crown_relu_relax_lu applied to each coefficient row as it is staged (with
+ * b_out = (b_in + sum A * beta_sel) + sum A' * kbias and c_out = sum A' * cvec[d]),
+ * then the transposed convolution reduced to the concretization norm
+ * norm[r] = sum |y| (* wvec[d, e]) and, with h_scale, the lower bound's gradient
+ * seed h_out = h_scale[r] * sign(y) (* wvec) -- bf_conv_transpose_rows with norm
+ * outputs on the relaxed rows, never writing them unless relaxed_u/relaxed_l are
+ * given.  Replaces bf_crown_relu_relax_lu followed by bf_conv_transpose_rows for
+ * the input region (runtime/crown_ibp.py:1211-1298 then the input-layer
+ * concretization of Conv2dLinearOperator, runtime/linear_operator.py:1378-1452
+ * and runtime/perturbation.py:175-222).  Shapes: those
+ * bf_conv_transpose_small_supported accepts (<= 4 input channels, <= 16 taps). */
+int bf_conv_transpose_small_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph,
+                                      int pw, int Hi, int Wi);
+int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
+                                            int Wo, const float* pre_lo, const float* pre_hi, const float* alpha,
+                                            int64_t alpha_ld, const float* add_l, int64_t add_ld, const float* kbias,
+                                            const float* cvec, const float* b_u_in, const float* b_l_in,
+                                            const float* W, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
+                                            int Hi, int Wi, const float* wvec, int64_t w_ld, const float* h_scale,
+                                            float* h_out, float* norm_u, float* norm_l, float* b_u_out,
+                                            float* b_l_out, float* c_u_out, float* c_l_out, float* relaxed_u,
+                                            float* relaxed_l, hipStream_t stream);
+
 /* The weights of that pass in the order its workgroups stage them
  * (bf_conv_transpose_packed_floats floats, 16-byte aligned; 0 = shape not
  * taken), so that a caller who keeps them per weight tensor passes them as

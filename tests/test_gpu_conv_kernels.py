@@ -233,3 +233,95 @@ def test_relu_conv_transpose_matches_pass_then_conv(shape, variant):
                  + float(b_in.abs().max()))
         berr = (bf.double().cpu() - bp.double().cpu()).abs()
         assert bool((berr <= 2 * nin * 2.0 ** -24 * terms + 1e-30).all()), f"b_{k}: max err {float(berr.max()):.3e}"
+
+
+INPUT_SHAPES = [
+    (37, 16, 16, 16, 3, 4, 4, 2, 2, 1, 1, 9),    # C3 / C4 input region (3 channels, 4 x 4 taps, stride 2)
+    (10, 8, 6, 6, 2, 3, 3, 1, 1, 1, 1, 5),       # npix % 16 != 0: the scalar staging path
+]
+
+
+@pytest.mark.parametrize("shape", INPUT_SHAPES, ids=[f"R{s[0]}_Co{s[1]}_Ci{s[4]}" for s in INPUT_SHAPES])
+@pytest.mark.parametrize("variant", ["linf", "box_alpha_split"])
+def test_relu_conv_transpose_concretize_matches_pass_then_conv(shape, variant):
+    """bf_crown_relu_conv_transpose_concretize (the input layer in one pass) against
+    bf_crown_relu_relax_lu + bf_conv_transpose_rows with norm outputs: the relaxed rows
+    bit-identical to the pass's, the bias and center sums within the fp32 bound of their
+    two summation orders, the norms within the accumulation bound of the transposed
+    convolution, and the gradient seed equal where the sign of y is certain."""
+    dev = device()
+    R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, S = shape
+    Hi, Wi = _out_hw(Ho, Wo, KH, KW, sh, sw, ph, pw)
+    announce(f"bf_crown_relu_conv_transpose_concretize {shape} {variant}")
+    assert _lib.load().bf_conv_transpose_small_supported(Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi) == 1
+    g = torch.Generator().manual_seed(R * 5 + Co)
+    D = (R + S - 1) // S
+    R = D * S
+    nin, nout = Co * Ho * Wo, Ci * Hi * Wi
+    A_u = torch.randn(R, nin, generator=g)
+    A_l = torch.randn(R, nin, generator=g)
+    c = torch.randn(D, nin, generator=g)
+    w = torch.rand(D, nin, generator=g)
+    lo, hi = c - w, c + 0.5 * w
+    W = torch.randn(Co, Ci, KH, KW, generator=g)
+    kb = torch.randn(nin, generator=g)
+    cv = torch.randn(D, nin, generator=g)
+    b_in = torch.randn(2, R, generator=g)
+    box = variant.startswith("box")
+    alpha = torch.rand(D, nin, generator=g) if box else None
+    add = torch.randn(D, nin, generator=g) if box else None
+    wv = torch.rand(D, nout, generator=g) if box else None
+    h_scale = torch.randn(R, generator=g)
+    T = lambda x: None if x is None else x.to(dev).contiguous()   # noqa: E731
+    a = {k: T(v) for k, v in dict(A_u=A_u, A_l=A_l, lo=lo, hi=hi, alpha=alpha, add=add, kb=kb, cv=cv, bu=b_in[0],
+                                  bl=b_in[1], W=W, wv=wv, hs=h_scale).items()}
+    P = lambda k: _lib.ptr(a[k])   # noqa: E731
+    st = _lib.stream_handle()
+    ald = nin if alpha is not None else 0
+    # the pass, then the transposed conv with norm outputs
+    rp = [torch.empty(R, nin, device=dev) for _ in range(2)]
+    bp = [torch.empty(R, device=dev) for _ in range(2)]
+    cp = [torch.empty(R, device=dev) for _ in range(2)]
+    _lib.call("bf_crown_relu_relax_lu", P("A_u"), P("A_l"), S * nin, D, S, nin, P("lo"), P("hi"), P("alpha"), ald,
+              P("add"), nin, P("kb"), P("cv"), P("bu"), P("bl"), _lib.ptr(rp[0]), _lib.ptr(rp[1]), _lib.ptr(bp[0]),
+              _lib.ptr(bp[1]), _lib.ptr(cp[0]), _lib.ptr(cp[1]), st)
+    np_ = [torch.empty(R, device=dev) for _ in range(2)]
+    hp = torch.empty(R, nout, device=dev)
+    _lib.call("bf_conv_transpose_rows", _lib.ptr(rp[0]), _lib.ptr(rp[1]), R, Co, Ho, Wo, P("W"), Ci, KH, KW, sh, sw,
+              ph, pw, Hi, Wi, None, None, S, P("wv"), nout, _lib.ptr(np_[0]), _lib.ptr(np_[1]), P("hs"),
+              _lib.ptr(hp), st)
+    # the fused kernel
+    nf = [torch.empty(R, device=dev) for _ in range(2)]
+    bf = [torch.empty(R, device=dev) for _ in range(2)]
+    cf = [torch.empty(R, device=dev) for _ in range(2)]
+    hf = torch.empty(R, nout, device=dev)
+    rf_l = torch.empty(R, nin, device=dev)
+    _lib.call("bf_crown_relu_conv_transpose_concretize", P("A_u"), P("A_l"), D, S, Co, Ho, Wo, P("lo"), P("hi"),
+              P("alpha"), ald, P("add"), nin, P("kb"), P("cv"), P("bu"), P("bl"), P("W"), Ci, KH, KW, sh, sw, ph, pw,
+              Hi, Wi, P("wv"), nout, P("hs"), _lib.ptr(hf), _lib.ptr(nf[0]), _lib.ptr(nf[1]), _lib.ptr(bf[0]),
+              _lib.ptr(bf[1]), _lib.ptr(cf[0]), _lib.ptr(cf[1]), None, _lib.ptr(rf_l), st)
+    torch.cuda.synchronize()
+    assert torch.equal(rf_l, rp[1]), "relaxed rows differ from the relaxation pass"
+    beta_max = float(lo.abs().max())
+    for z, A in ((0, A_u), (1, A_l)):
+        rel = rp[z].double().cpu()
+        y = F.conv_transpose2d(rel.reshape(R, Co, Ho, Wo), W.double(), stride=(sh, sw), padding=(ph, pw)).reshape(R, -1)
+        ybound = F.conv_transpose2d(rel.abs().reshape(R, Co, Ho, Wo), W.double().abs(), stride=(sh, sw),
+                                    padding=(ph, pw)).reshape(R, -1)
+        taps = Co * ((KH + sh - 1) // sh) * ((KW + sw - 1) // sw)
+        wgt = wv.double()[torch.arange(R) // S] if box else torch.ones(R, nout, dtype=torch.float64)
+        ytol = taps * 2.0 ** -23 * ybound
+        nref = (y.abs() * wgt).sum(1)
+        ntol = (ytol * wgt).sum(1) + nout * 2.0 ** -23 * nref + 1e-30
+        nerr = (nf[z].double().cpu() - nref).abs()
+        assert bool((nerr <= ntol).all()), f"norm {z}: {float((nerr / ntol).max()):.3g} x tolerance"
+        terms = (A.abs().sum(1).double() * beta_max + rel.abs().mul(kb.double().abs()).sum(1)
+                 + float(b_in.abs().max()))
+        berr = (bf[z].double().cpu() - bp[z].double().cpu()).abs()
+        assert bool((berr <= 2 * nin * 2.0 ** -24 * terms + 1e-30).all()), f"b {z}: max err {float(berr.max()):.3e}"
+        cterms = (rel.abs() * cv.double().abs()[torch.arange(R) // S]).sum(1)
+        cerr = (cf[z].double().cpu() - cp[z].double().cpu()).abs()
+        assert bool((cerr <= 2 * nin * 2.0 ** -24 * cterms + 1e-30).all()), f"c {z}: max err {float(cerr.max()):.3e}"
+        if z == 1:
+            sure = y.abs() > ytol
+            assert torch.equal(hf.cpu()[sure], hp.cpu()[sure]), "gradient seed differs where sign(y) is certain"
