@@ -803,16 +803,19 @@ conv_t_small_kernel(SmallTArgs g, ConvRelax rx) {
           const float4 hi4 = rx.lo ? ld4(hi_d + e) : zero;
           const float4 al4 = rx.alpha ? ld4(al_d + e) : zero;
           const float4 ad4 = (rx.add && lower) ? ld4(ad_d + e) : zero;
-          const float4 kb4 = rx.kbias ? ld4(rx.kbias + e) : zero;
-          const float4 cv4 = rx.cvec ? ld4(cv_d + e) : zero;
           const float vv[4] = {v.x, v.y, v.z, v.w}, lo[4] = {lo4.x, lo4.y, lo4.z, lo4.w},
                       hi[4] = {hi4.x, hi4.y, hi4.z, hi4.w}, al[4] = {al4.x, al4.y, al4.z, al4.w},
-                      ad[4] = {ad4.x, ad4.y, ad4.z, ad4.w}, kb[4] = {kb4.x, kb4.y, kb4.z, kb4.w},
-                      cv[4] = {cv4.x, cv4.y, cv4.z, cv4.w};
+                      ad[4] = {ad4.x, ad4.y, ad4.z, ad4.w};
           float o[4];
 #pragma unroll
+          for (int u = 0; u < 4; ++u) o[u] = relax_element(rx, lower, vv[u], lo[u], hi[u], al[u], ad[u], sb);
+          // the bias and center operands after the relaxation (fewer registers live at once)
+          __builtin_amdgcn_sched_barrier(0);
+          const float4 kb4 = rx.kbias ? ld4(rx.kbias + e) : zero;
+          const float4 cv4 = rx.cvec ? ld4(cv_d + e) : zero;
+          const float kb[4] = {kb4.x, kb4.y, kb4.z, kb4.w}, cv[4] = {cv4.x, cv4.y, cv4.z, cv4.w};
+#pragma unroll
           for (int u = 0; u < 4; ++u) {
-            o[u] = relax_element(rx, lower, vv[u], lo[u], hi[u], al[u], ad[u], sb);
             if (rx.kbias) sk += o[u] * kb[u];
             if (rx.cvec) sc += o[u] * cv[u];
           }
