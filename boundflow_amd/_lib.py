@@ -35,20 +35,21 @@ SIGNATURES = {
     "bf_gemm_rank1_workspace": (I64, [I64, I64, I64]),
     "bf_relu_relax_table": (I32, [P, P, P, I64, I64, I64, P, P]),
     "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, P, P, P, P, P]),
-    "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, F32, P, P,
-                                              P, P, P, P, P, P]),
+    "bf_crown_relu_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, F32, I32, P,
+                                              P, P, P, P, P, P, P]),
     "bf_crown_relu_linear_concretize_workspace": (I64, [I64, I64, I64]),
     "bf_crown_relu_linear_concretize_noalloc": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, F32,
-                                                      P, P, P, P, P, P, P]),
+                                                      I32, P, P, P, P, P, P, P]),
     "bf_crown_relu_linear_relu_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, P, P, P, P, P, I64, P, P,
                                             I64, P, P, P, P, P, P, P, P, P, P]),
     "bf_crown_relu_linear_relu_fwd_workspace": (I64, [I64, I64, I64]),
-    "bf_crown_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, I64, P, F32, P, P, P, P, P, P, P, P, P, P]),
+    "bf_crown_linear_concretize": (I32, [P, P, I64, I64, I64, I64, P, I64, P, F32, I32, P, P, P, P, P, P, P, P, P,
+                                         P]),
     "bf_crown_linear_concretize_workspace": (I64, [I64, I64, I64]),
     "bf_crown_relu_relax": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, P, P, P, P, P, P, P, P, P, P]),
     "bf_crown_relu_relax_lu": (I32, [P, P, I64, I64, I64, I64, P, P, P, I64, P, I64, P, P, P, P, P, P, P, P, P, P,
                                      P]),
-    "bf_concretize_dense": (I32, [P, I64, I64, I64, P, P, F32, P, I32, P, P]),
+    "bf_concretize_dense": (I32, [P, I64, I64, I64, P, P, F32, I32, P, I32, P, P]),
     "bf_concretize_dense_grad": (I32, [P, I64, I64, I64, P, P, F32, P, P, P]),
     "bf_rows_add": (I32, [P, P, I64, I64, I64, P, P, I64, P, P]),
     "bf_ibp_linear": (I32, [P, P, I64, I64, I32, F32, I32, P, P, I64, P, I64, P, P, P, P, P, P]),
@@ -70,13 +71,13 @@ SIGNATURES = {
     "bf_conv2d_rows": (I32, [P, I64, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P, P,
                              I64, I64, P]),
     "bf_conv_transpose_rows": (I32, [P, P, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P,
-                                     I64, P, I64, P, P, P, P, P]),
+                                     I64, P, I64, I32, P, P, P, P, P]),
     "bf_conv_transpose_hwc_supported": (I32, [I32] * 12),
     "bf_crown_relu_conv_transpose": (I32, [P, P, I64, I64, I32, I32, I32, P, P, P, I64, P, I64, P, P, P, P, P, I32, I32,
                                            I32, I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P]),
     "bf_conv_transpose_small_supported": (I32, [I32] * 12),
     "bf_crown_relu_conv_transpose_concretize": (I32, [P, P, I64, I64, I32, I32, I32, P, P, P, I64, P, I64, P, P, P, P, P]
-                                                + [I32] * 9 + [P, I64, P, P, P, P, P, P, P, P, P, P, P]),
+                                                + [I32] * 9 + [P, I64, I32, P, P, P, P, P, P, P, P, P, P, P]),
     "bf_conv_transpose_packed_floats": (I64, [I32] * 12),
     "bf_conv_transpose_pack_weights": (I32, [P] + [I32] * 12 + [P, P]),
     "bf_ibp_conv2d": (I32, [P, P, I64, I32, I32, I32, I32, F32, I32, P, P, I32, I32, I32, I32, I32, I32, I32, I32, I32,
@@ -89,7 +90,7 @@ SIGNATURES = {
     "bf_masked_copy_rows": (I32, [P, P, I64, I64, P, P]),
     "bf_masked_copy_rows_multi": (I32, [I32, P, P, P, I64, P, P]),
     "bf_sum_rows": (I32, [P, I64, I64, P, P]),
-    "bf_concretize_finalize": (I32, [P, P, I32, I64, P, P, P, P, F32, P, P, P]),
+    "bf_concretize_finalize": (I32, [P, P, I32, I64, P, P, P, P, F32, I32, P, P, P]),
     "bf_alpha_from_crown": (I32, [P, P, I64, P, P]),
     "bf_domain_status": (I32, [P, I64, I64, P, F32, F32, P, P]),
 }

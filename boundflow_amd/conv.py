@@ -24,7 +24,7 @@ import torch
 
 from . import _lib
 from .profiling import launch as _timed
-from .spec import BoxPerturbation, IntervalState
+from .spec import BoxPerturbation, IntervalState, input_norm_p
 
 
 def _numel(shape) -> int:
@@ -141,13 +141,14 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
         y_l = torch.empty(M, n_in, device=dev) if A_l is not None else None
         with _timed("conv_transpose", flops, 4.0 * nz * (M * n_out + M * n_in)):
             _lib.call("bf_conv_transpose_rows", _lib.ptr(rA_u), _lib.ptr(rA_l), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH,
-                      KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(y_l), S, None, 0, None, None, None, None,
-                      stream)
+                      KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(y_l), S, None, 0, 0, None, None, None,
+                      None, stream)
         if save is not None:
             save.setdefault("relaxed", {})[layer.op_index] = rA_l
         return y_u, y_l, nb_u, nb_l, S * n_in, None
     # input layer: transposed conv fused with the concretization
     pert = spec.perturbation
+    norm_p = _input_norm(pert, save)
     if cvec is None:
         raise RuntimeError("forward trace lacks the input-layer projection")
     if isinstance(pert, BoxPerturbation):
@@ -166,14 +167,14 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
         save["cvec"] = cvec
     with _timed("conv_transpose_concretize", flops, 4.0 * nz * M * n_out):
         _lib.call("bf_conv_transpose_rows", _lib.ptr(rA_u), _lib.ptr(rA_l), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW,
-                  sh, sw, ph, pw, Hi, Wi, None, None, S, _lib.ptr(rad), n_in, _lib.ptr(norm_u), _lib.ptr(norm_l),
-                  _lib.ptr(h_scale), _lib.ptr(h_out), stream)
+                  sh, sw, ph, pw, Hi, Wi, None, None, S, _lib.ptr(rad), n_in, norm_p, _lib.ptr(norm_u),
+                  _lib.ptr(norm_l), _lib.ptr(h_scale), _lib.ptr(h_out), stream)
     if save is not None:
         save.setdefault("relaxed", {})[layer.op_index] = rA_l
     lb = torch.empty(B, S, device=dev) if A_l is not None else None
     ub = torch.empty(B, S, device=dev) if A_u is not None else None
     _lib.call("bf_concretize_finalize", _lib.ptr(norm_u), _lib.ptr(norm_l), 1, M, _lib.ptr(c_u), _lib.ptr(c_l),
-              _lib.ptr(nb_u), _lib.ptr(nb_l), eps, _lib.ptr(lb), _lib.ptr(ub), stream)
+              _lib.ptr(nb_u), _lib.ptr(nb_l), eps, norm_p, _lib.ptr(lb), _lib.ptr(ub), stream)
     return None, None, None, None, 0, IntervalState(lower=lb, upper=ub)
 
 
@@ -185,6 +186,7 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
     gradient pass; then the bounds from the norms, centers and biases."""
     dev = spec.center.device
     stream = _lib.stream_handle()
+    norm_p = _input_norm(spec.perturbation, save)
     Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi = geo
     n_out, n_in = Co * Ho * Wo, Ci * Hi * Wi
     nb_u, nb_l = nb
@@ -210,7 +212,7 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
         _lib.call("bf_crown_relu_conv_transpose_concretize", _lib.ptr(A_u), _lib.ptr(A_l), B, S, Co, Ho, Wo,
                   _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld,
                   _lib.ptr(kbias), _lib.ptr(cvec), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(W), Ci, KH, KW, sh, sw, ph,
-                  pw, Hi, Wi, _lib.ptr(rad), n_in, _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(norm_u),
+                  pw, Hi, Wi, _lib.ptr(rad), n_in, norm_p, _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(norm_u),
                   _lib.ptr(norm_l), _lib.ptr(nb_u), _lib.ptr(nb_l), _lib.ptr(c_u), _lib.ptr(c_l), None,
                   _lib.ptr(rel_l), stream)
     if save is not None:
@@ -218,5 +220,17 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
     lb = torch.empty(B, S, device=dev) if A_l is not None else None
     ub = torch.empty(B, S, device=dev) if A_u is not None else None
     _lib.call("bf_concretize_finalize", _lib.ptr(norm_u), _lib.ptr(norm_l), 1, M, _lib.ptr(c_u), _lib.ptr(c_l),
-              _lib.ptr(nb_u), _lib.ptr(nb_l), eps, _lib.ptr(lb), _lib.ptr(ub), stream)
+              _lib.ptr(nb_u), _lib.ptr(nb_l), eps, norm_p, _lib.ptr(lb), _lib.ptr(ub), stream)
     return None, None, None, None, 0, IntervalState(lower=lb, upper=ub)
+
+
+def _input_norm(pert, save):
+    """Norm code of the input conv layer's concretization: sum |y| for a Linf ball or a
+    box, the row's L2 norm for an L2 ball, max |y| for an L1 ball
+    (Conv2dLinearOperator.row_abs_sum / row_l2_norm / row_abs_max,
+    runtime/linear_operator.py:991-997).  The gradient seed of the alpha/beta pass is
+    built for sum |y| only."""
+    norm_p = input_norm_p(pert)
+    if norm_p != 0 and save is not None and save.get("grad_rows") is not None:
+        raise NotImplementedError("the alpha/beta reverse pass takes Linf balls and boxes")
+    return norm_p

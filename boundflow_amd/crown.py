@@ -38,7 +38,7 @@ from . import _lib
 from .profiling import launch as _timed
 from .conv import conv_backward_step, ibp_conv2d
 from .ir import BFTaskModule, TaskKind
-from .spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation, normalize_input_spec
+from .spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation, input_norm_p, normalize_input_spec
 
 
 # ---------------------------------------------------------------------------
@@ -327,8 +327,7 @@ def forward_ibp_trace(
     relu_pre: Dict[str, IntervalState] = {}
     proj: Dict[str, torch.Tensor] = {}
     pert = spec.perturbation
-    if isinstance(pert, LpBallPerturbation) and pert.normalized_p() != "inf":
-        raise NotImplementedError("HIP backend supports Linf balls and boxes")
+    norm_p = input_norm_p(pert)
     prev_lo = prev_hi = None
     for li, layer in enumerate(chain.layers):
         split = None
@@ -354,7 +353,9 @@ def forward_ibp_trace(
                     in_lo, in_hi, kind, eps, relu_in = (pert.lower.reshape(B, K).contiguous(),
                                                         pert.upper.reshape(B, K).contiguous(), 0, 0.0, 0)
                 else:
-                    in_lo, in_hi, kind, eps, relu_in = center.reshape(B, K).contiguous(), None, 1, float(pert.eps), 0
+                    # Lp ball: x0 W^T -/+ eps * row norm of W (sum |W|, ||W||_2, max |W| for p = inf, 2, 1)
+                    kind = {0: 1, 2: 2, 1: 3}[norm_p]
+                    in_lo, in_hi, eps, relu_in = center.reshape(B, K).contiguous(), None, float(pert.eps), 0
             else:
                 in_lo, in_hi, kind, eps = prev_lo.reshape(B, K), prev_hi.reshape(B, K), 0, 0.0
                 relu_in = 1 if layer.input_is_relu_of is not None else 0
@@ -571,7 +572,8 @@ def crown_backward(
             nz = int(A_u is not None) + int(A_l is not None)
             with _timed("crown_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
                 _lib.call("bf_crown_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N, _lib.ptr(Wt),
-                          P, _lib.ptr(rad), eps, _lib.ptr(c_u), _lib.ptr(c_l), _lib.ptr(b_u), _lib.ptr(b_l),
+                          P, _lib.ptr(rad), eps, input_norm_p(pert), _lib.ptr(c_u), _lib.ptr(c_l), _lib.ptr(b_u),
+                          _lib.ptr(b_l),
                           _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(ws), _lib.ptr(lb), _lib.ptr(ub), stream)
             if save is not None:
                 save["final_ws"] = ws
@@ -604,7 +606,7 @@ def crown_backward(
             with _timed("crown_relu_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
                 _lib.call("bf_crown_relu_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
                           _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(cvec),
-                          _lib.ptr(rad), eps, _lib.ptr(b_u),
+                          _lib.ptr(rad), eps, input_norm_p(pert), _lib.ptr(b_u),
                           _lib.ptr(b_l), _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(ws), _lib.ptr(lb),
                           _lib.ptr(ub), stream)
             if save is not None:

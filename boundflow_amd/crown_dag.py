@@ -41,7 +41,7 @@ from . import _lib
 from .conv import ibp_conv2d
 from .ir import BFTaskModule, TaskKind
 from .profiling import launch as _timed
-from .spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation, normalize_input_spec
+from .spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation, input_norm_p, normalize_input_spec
 from .task_executor import _check_concat_shapes, _concat_axis
 
 DAG_OPS = ("linear", "conv2d", "relu", "add", "concat", "flatten", "reshape")
@@ -171,9 +171,10 @@ def forward_ibp_trace_dag(
     dev = center.device
     stream = _lib.stream_handle()
     pert = spec.perturbation
-    if isinstance(pert, LpBallPerturbation) and pert.normalized_p() != "inf":
-        raise NotImplementedError("HIP backend supports Linf balls and boxes")
     box = isinstance(pert, BoxPerturbation)
+    # a linear layer on the input takes the ball's dual row norm of W; every other consumer of
+    # the input reads its bounding box (center -/+ eps for p = 1, 2, inf), as crown_ibp.py:125-178
+    ibp_kind = 0 if box else {0: 1, 2: 2, 1: 3}[input_norm_p(pert)]
     infeasible = torch.zeros(B, dtype=torch.int32, device=dev)
     env: Dict[str, IntervalState] = {}
     relu_pre: Dict[str, IntervalState] = {}
@@ -215,7 +216,7 @@ def forward_ibp_trace_dag(
                 if box:
                     args = (blo.reshape(B, K).contiguous(), bhi.reshape(B, K).contiguous(), 0, 0.0)
                 else:
-                    args = (c.reshape(B, K).contiguous(), None, 1, float(pert.eps))
+                    args = (c.reshape(B, K).contiguous(), None, ibp_kind, float(pert.eps))
             else:
                 xi = box_of(x)
                 args = (xi.lower.reshape(B, K), xi.upper.reshape(B, K), 0, 0.0)
@@ -472,7 +473,7 @@ def crown_backward_dag(
             with _timed("conv_transpose", flops, 4.0 * nz * (M * n_out + M * Ci * Hi * Wi)):
                 _lib.call("bf_conv_transpose_rows", _lib.ptr(st.A_u), _lib.ptr(A_l_in), M, Co, Ho, Wo, _lib.ptr(W),
                           Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(None if one else y_l), S, None,
-                          0, None, None, None, None, stream)
+                          0, 0, None, None, None, None, stream)
             accumulate(x, _Rows(y_u, y_l, st.b_u, st.b_l))
         elif t == "relu":
             pre = trace.relu_pre[x]
@@ -583,10 +584,10 @@ def _concretize(spec: InputSpec, st: _Rows, B: int, S: int) -> IntervalState:
     with _timed("concretize_dense", 2.0 * nz * B * S * I, 4.0 * nz * B * S * I):
         if ub is not None:
             _lib.call("bf_concretize_dense", _lib.ptr(st.A_u), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
-                      _lib.ptr(st.b_u), 0, _lib.ptr(ub), stream)
+                      input_norm_p(spec.perturbation), _lib.ptr(st.b_u), 0, _lib.ptr(ub), stream)
         if lb is not None:
             _lib.call("bf_concretize_dense", _lib.ptr(st.A_l), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
-                      _lib.ptr(st.b_l), 1, _lib.ptr(lb), stream)
+                      input_norm_p(spec.perturbation), _lib.ptr(st.b_l), 1, _lib.ptr(lb), stream)
     return IntervalState(lower=lb, upper=ub)
 
 
@@ -612,6 +613,8 @@ def lower_grad_pass(module: BFTaskModule, spec: InputSpec, trace: DagTrace, save
     M = B * S
     A_in = saved["input_A"]
     I = int(A_in.shape[1])
+    if input_norm_p(spec.perturbation) != 0:
+        raise NotImplementedError("the alpha/beta reverse pass takes Linf balls and boxes")
     center, rad, eps = _input_center_radius(spec, B, I)
     GA: Dict[str, torch.Tensor] = {}
     g0 = torch.empty(M, I, device=dev)

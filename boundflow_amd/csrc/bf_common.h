@@ -85,6 +85,19 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Max over the 64 lanes of a wave of values >= 0, by the DPP steps of wave_sum with
+// max in place of the sum (a lane a step leaves unwritten reads 0, the identity of
+// the max of non-negative values), returned to every lane.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.f, v, 0xb1, 0xf, 0xf, false));
+  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.f, v, 0x4e, 0xf, 0xf, false));
+  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.f, v, 0x141, 0xf, 0xf, false));
+  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.f, v, 0x140, 0xf, 0xf, false));
+  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.f, v, 0x142, 0xa, 0xf, false));
+  v = fmaxf(v, __builtin_amdgcn_update_dpp(0.f, v, 0x143, 0xc, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // m / d for 0 <= m, d > 0, in 32-bit arithmetic when both fit (uniform over a launch)
 __device__ __forceinline__ int64_t div_rows(int64_t m, int64_t d, bool fits32) {
   return fits32 ? (int64_t)((uint32_t)m / (uint32_t)d) : m / d;

@@ -22,6 +22,25 @@ namespace bf {
 
 constexpr int CT = 256;
 
+// One output v's share of its row's concretization norm, by the input set:
+// nk 0 sums |v| (Linf ball), or |v| * wgt when weighted (box radius wgt);
+// nk 2 sums v * v (L2 ball: the root is taken by the finalize); nk 1 keeps
+// max |v| (L1 ball).  The partial norms of a row combine with norm_join.
+__device__ __forceinline__ float norm_step(float s, float v, float wgt, bool weighted, int nk) {
+  const float a = fabsf(v);
+  if (nk == 1) return fmaxf(s, a);
+  if (nk == 2) return s + v * v;
+  return s + (weighted ? a * wgt : a);
+}
+
+__device__ __forceinline__ float norm_join(float a, float b, int nk) { return nk == 1 ? fmaxf(a, b) : a + b; }
+
+// norm_join over the 64 lanes of a wave by an xor butterfly, the total in every lane
+__device__ __forceinline__ float norm_wave_xor(float s, int nk) {
+  for (int off = 32; off >= 1; off >>= 1) s = norm_join(s, __shfl_xor(s, off, 64), nk);
+  return s;
+}
+
 __global__ void __launch_bounds__(CT)
 conv2d_rows_kernel(const float* __restrict__ x, int64_t in_div, int Ci, int Hi, int Wi,
                    const float* __restrict__ W, int abs_w, int Co, int KH, int KW, int sh, int sw, int ph, int pw,
@@ -67,7 +86,7 @@ __global__ void __launch_bounds__(CT)
 conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restrict__ A_l, int Co, int Ho, int Wo,
                            const float* __restrict__ W, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
                            int Hi, int Wi, float* __restrict__ y_u, float* __restrict__ y_l, int64_t S,
-                           const float* __restrict__ wv, int64_t w_ld, float* __restrict__ norm_u,
+                           const float* __restrict__ wv, int64_t w_ld, int nk, float* __restrict__ norm_u,
                            float* __restrict__ norm_l, const float* __restrict__ h_scale, float* __restrict__ h_out) {
   extern __shared__ float as[];
   __shared__ float red[CT / 64];
@@ -108,7 +127,7 @@ conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restric
     if (y) y[r * (int64_t)nout + e] = acc;
     if (nrm) {
       const float wgt = wv ? wv[d * w_ld + e] : 1.f;
-      s += wv ? fabsf(acc) * wgt : fabsf(acc);
+      s = norm_step(s, acc, wgt, wv != nullptr, nk);
       if (lower && h_out) {
         const float sg = (acc > 0.f) ? 1.f : ((acc < 0.f) ? -1.f : 0.f);
         h_out[r * (int64_t)nout + e] = wv ? hs * sg * wgt : hs * sg;
@@ -116,12 +135,12 @@ conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restric
     }
   }
   if (nrm) {
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    s = norm_wave_xor(s, nk);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
     if (threadIdx.x == 0) {
       float t = 0.f;
-      for (int q = 0; q < CT / 64; ++q) t += red[q];
+      for (int q = 0; q < CT / 64; ++q) t = norm_join(t, red[q], nk);
       nrm[r] = t;
     }
   }
@@ -182,6 +201,7 @@ struct GatherArgs {
   const float* W;
   int abs_w;           // MODE_F: bit z set -> operand pair z multiplies by |W|
   const float* wv;     // MODE_T norm weights [D, nout] (w_ld)
+  int nkind;           // MODE_T norm: 0 sum |y| (weighted by wv), 2 sum y^2, 1 max |y|
   const float* h_scale;
   float* h_out;
   const float* rs;     // MODE_F rank-1 term
@@ -370,7 +390,7 @@ conv_mfma_kernel(GatherArgs g) {
           if (y) y[r * nout + oidx] = v;
           if (MODE == MODE_T && nrm) {
             const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
-            s += g.wv ? fabsf(v) * wgt : fabsf(v);
+            s = norm_step(s, v, wgt, g.wv != nullptr, g.nkind);
             if (lower && g.h_out) {
               const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
               g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
@@ -380,12 +400,12 @@ conv_mfma_kernel(GatherArgs g) {
       }
     }
     if (MODE == MODE_T && nrm) {
-      for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+      s = norm_wave_xor(s, g.nkind);
       if (lane == 0) red[wave] = s;
       __syncthreads();
       if (tid == 0) {
         float t = 0.f;
-        for (int q = 0; q < GTM / 64; ++q) t += red[q];
+        for (int q = 0; q < GTM / 64; ++q) t = norm_join(t, red[q], g.nkind);
         nrm[r] = t;
       }
     }
@@ -652,7 +672,7 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
           if (y) y[r * nout + oidx] = v;
           if (nrm) {
             const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
-            s += g.wv ? fabsf(v) * wgt : fabsf(v);
+            s = norm_step(s, v, wgt, g.wv != nullptr, g.nkind);
             if (lower && g.h_out) {
               const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
               g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
@@ -662,13 +682,13 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
       }
     }
     if (nrm) {
-      s = wave_sum(s);
+      s = g.nkind == 1 ? wave_max_nonneg(s) : wave_sum(s);
       __syncthreads();   // red of the row sums above is read; reuse it
       if (lane == 0) red[wave][0] = s;
       __syncthreads();
       if (tid == 0) {
         float t = 0.f;
-        for (int q2 = 0; q2 < GTM / 64; ++q2) t += red[q2][0];
+        for (int q2 = 0; q2 < GTM / 64; ++q2) t = norm_join(t, red[q2][0], g.nkind);
         nrm[r] = t;
       }
     }
@@ -713,6 +733,7 @@ struct SmallTArgs {
   float* nrm[2];
   const float* W;          // [Co, Ci, KH, KW]
   const float* wv;         // norm weights [D, Ci*Hi*Wi] (w_ld) or NULL
+  int nkind;               // norm: 0 sum |y| (weighted by wv), 2 sum y^2, 1 max |y|
   const float* h_scale;
   float* h_out;
   int64_t R, S, w_ld;
@@ -882,7 +903,7 @@ conv_t_small_kernel(SmallTArgs g, ConvRelax rx) {
         if (y) y[r * nout + oidx] = v;
         if (nrm) {
           const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
-          s += g.wv ? fabsf(v) * wgt : fabsf(v);
+          s = norm_step(s, v, wgt, g.wv != nullptr, g.nkind);
           if (lower && g.h_out) {
             const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
             g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
@@ -891,12 +912,12 @@ conv_t_small_kernel(SmallTArgs g, ConvRelax rx) {
       }
     }
     if (nrm) {
-      for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+      s = norm_wave_xor(s, g.nkind);
       if (lane == 0) red[wave] = s;
       __syncthreads();
       if (tid == 0) {
         float tsum = 0.f;
-        for (int q = 0; q < GTM / 64; ++q) tsum += red[q];
+        for (int q = 0; q < GTM / 64; ++q) tsum = norm_join(tsum, red[q], g.nkind);
         nrm[r] = tsum;
       }
     }
@@ -1120,10 +1141,12 @@ int bf_conv2d_rows(const float* x, int64_t in_div, int64_t R, int Ci, int Hi, in
 
 int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co, int Ho, int Wo, const float* W,
                            int Ci, int KH, int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
-                           float* y_l, int64_t S, const float* wvec, int64_t w_ld, float* norm_u, float* norm_l,
-                           const float* h_scale, float* h_out, hipStream_t stream) {
+                           float* y_l, int64_t S, const float* wvec, int64_t w_ld, int norm_p, float* norm_u,
+                           float* norm_l, const float* h_scale, float* h_out, hipStream_t stream) {
   BF_REQUIRE(R >= 0 && Co > 0 && Ci > 0 && KH > 0 && KW > 0 && sh > 0 && sw > 0 && Hi > 0 && Wi > 0 && S > 0,
              "bf_conv_transpose_rows: bad sizes");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (wvec == nullptr && h_out == nullptr)),
+             "bf_conv_transpose_rows: norm_p is 0, 1 or 2; 1 and 2 take no weights and no h_out");
   if (R == 0) return BF_OK;
   BF_REQUIRE(W && (A_u || A_l), "bf_conv_transpose_rows: null pointer");
   BF_REQUIRE((A_u == nullptr) == (y_u == nullptr && norm_u == nullptr) && (A_l == nullptr) == (y_l == nullptr && norm_l == nullptr),
@@ -1143,6 +1166,7 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
       g.W = W;
       g.wv = wvec;
       g.w_ld = w_ld;
+      g.nkind = norm_p;
       g.h_scale = h_scale;
       g.h_out = h_out;
       g.S = S;
@@ -1171,6 +1195,7 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
       g.W = W;
       g.wv = wvec;
       g.w_ld = w_ld;
+      g.nkind = norm_p;
       g.h_scale = h_scale;
       g.h_out = h_out;
       g.S = S;
@@ -1197,6 +1222,7 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
       g.W = W;
       g.wv = wvec;
       g.w_ld = w_ld;
+      g.nkind = norm_p;
       g.h_scale = h_scale;
       g.h_out = h_out;
       g.S = S;
@@ -1212,7 +1238,8 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
   const size_t lds = sizeof(float) * (size_t)Co * Ho * Wo;
   BF_REQUIRE(lds <= 64 * 1024, "bf_conv_transpose_rows: coefficient map exceeds the 64 KB LDS row stage");
   hipLaunchKernelGGL(conv_transpose_rows_kernel, dim3((unsigned)R, nz), dim3(CT), lds, stream, A_u, A_l, Co, Ho, Wo,
-                     W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S, wvec, w_ld, norm_u, norm_l, h_scale, h_out);
+                     W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S, wvec, w_ld, norm_p, norm_u, norm_l, h_scale,
+                     h_out);
   BF_LAUNCH_CHECK("conv_transpose_rows_kernel");
   return BF_OK;
 }
@@ -1323,8 +1350,9 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
                                             int64_t alpha_ld, const float* add_l, int64_t add_ld, const float* kbias,
                                             const float* cvec, const float* b_u_in, const float* b_l_in,
                                             const float* W, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
-                                            int Hi, int Wi, const float* wvec, int64_t w_ld, const float* h_scale,
-                                            float* h_out, float* norm_u, float* norm_l, float* b_u_out,
+                                            int Hi, int Wi, const float* wvec, int64_t w_ld, int norm_p,
+                                            const float* h_scale, float* h_out, float* norm_u, float* norm_l,
+                                            float* b_u_out,
                                             float* b_l_out, float* c_u_out, float* c_l_out, float* relaxed_u,
                                             float* relaxed_l, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0 && Co > 0 && Ci > 0, "bf_crown_relu_conv_transpose_concretize: bad sizes");
@@ -1335,6 +1363,8 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
              "bf_crown_relu_conv_transpose_concretize: each given coefficient needs its norm output");
   BF_REQUIRE((pre_lo == nullptr) == (pre_hi == nullptr),
              "bf_crown_relu_conv_transpose_concretize: pre_lo and pre_hi go together");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (wvec == nullptr && h_out == nullptr)),
+             "bf_crown_relu_conv_transpose_concretize: norm_p is 0, 1 or 2; 1 and 2 take no weights and no h_out");
   BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || norm_l != nullptr),
              "bf_crown_relu_conv_transpose_concretize: h_out needs h_scale and the lower norm");
   SmallTArgs g;
@@ -1370,6 +1400,7 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
   g.W = W;
   g.wv = wvec;
   g.w_ld = w_ld;
+  g.nkind = norm_p;
   g.h_scale = h_scale;
   g.h_out = h_out;
   g.S = S;

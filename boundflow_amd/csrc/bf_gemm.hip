@@ -9,26 +9,30 @@
 
 namespace bf {
 
-// Fixed-order sum of the per-column-block partial norms, then
+// The per-column-block partial norms combined in a fixed order -- summed (norm_p 0:
+// Linf ball, box), their maximum (1: L1 ball, the dual norm max |A|), the square root
+// of their sum (2: L2 ball) -- then
 //   lb = (center - eps * norm) + b,   ub = (center + eps * norm) + b
 // (perturbation.py:175-222; box: eps = 1 and the norm is already radius-weighted).
+__device__ __forceinline__ float combine_parts(const float* __restrict__ part, int nparts, int64_t M, int64_t m,
+                                               int norm_p) {
+  float s = 0.f;
+  for (int q = 0; q < nparts; ++q) {
+    const float v = part[(int64_t)q * M + m];
+    s = norm_p == 1 ? fmaxf(s, v) : s + v;
+  }
+  return norm_p == 2 ? sqrtf(s) : s;
+}
+
 __global__ void concretize_finalize_kernel(const float* __restrict__ partial_u, const float* __restrict__ partial_l,
                                            int nparts, int64_t M, const float* __restrict__ cen_u,
                                            const float* __restrict__ cen_l, const float* __restrict__ b_u,
-                                           const float* __restrict__ b_l, float eps, float* __restrict__ lb,
-                                           float* __restrict__ ub) {
+                                           const float* __restrict__ b_l, float eps, int norm_p,
+                                           float* __restrict__ lb, float* __restrict__ ub) {
   int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (m >= M) return;
-  if (ub) {
-    float nu = 0.f;
-    for (int q = 0; q < nparts; ++q) nu += partial_u[(int64_t)q * M + m];
-    ub[m] = (cen_u[m] + eps * nu) + b_u[m];
-  }
-  if (lb) {
-    float nl = 0.f;
-    for (int q = 0; q < nparts; ++q) nl += partial_l[(int64_t)q * M + m];
-    lb[m] = (cen_l[m] - eps * nl) + b_l[m];
-  }
+  if (ub) ub[m] = (cen_u[m] + eps * combine_parts(partial_u, nparts, M, m, norm_p)) + b_u[m];
+  if (lb) lb[m] = (cen_l[m] - eps * combine_parts(partial_l, nparts, M, m, norm_p)) + b_l[m];
 }
 
 // Slopes/intercepts of the ReLU relaxation per (domain, neuron)
@@ -98,10 +102,12 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
 }
 
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
-                        const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream) {
+                        const float* bu, const float* bl, float eps, int norm_p, float* lb, float* ub,
+                        hipStream_t stream) {
   if (M == 0) return BF_OK;
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2, "concretize: norm_p %d (0 Linf/box, 1 L1, 2 L2)", norm_p);
   hipLaunchKernelGGL(concretize_finalize_kernel, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, stream, pu, pl,
-                     nparts, M, cu, cl, bu, bl, eps, lb, ub);
+                     nparts, M, cu, cl, bu, bl, eps, norm_p, lb, ub);
   BF_LAUNCH_CHECK("concretize_finalize_kernel");
   return BF_OK;
 }

@@ -40,6 +40,8 @@ struct GemmArgs {
   float* partial[2];         // [gridDim.y, M] partial row sums
   const float* h_scale;      // optional [M]: lower pass also writes h = h_scale[m] * sign(C) * w  (gradient seed)
   float* h_out;              // [M, N] row-major (ldh = N)
+  int norm_kind;             // the row norm of C: 0 sum |C| (* w) (Linf ball, box); 1 max |C| (L1 ball);
+                             // 2 sum C^2, the square root taken by the finalize (L2 ball)
 
   // --- relaxation epilogue (EPI_RELAX): the ReLU relaxation of the NEXT layer,
   // indexed by the output columns, applied to C before it is stored:

@@ -697,9 +697,11 @@ gemm_kernel(GemmArgs p) {
       }
   } else if constexpr (EPI == EPI_ABSSUM) {
     static_assert(GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
-    // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order.
+    // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order (norm_kind 0);
+    // max_n |C[m, n]| (1) or sum_n C[m, n]^2 (2) for the L1 and L2 balls.
     float rs[FM][16];
     const bool fits32 = M < (1LL << 31);
+    const int nk = p.norm_kind;   // uniform
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -711,13 +713,13 @@ gemm_kernel(GemmArgs p) {
         for (int j = 0; j < FN; ++j) {
           const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
           const float a = acc[i][j][r];
-          float v = col < N ? fabsf(a) : 0.f;   // columns past N hold products no one keeps
+          float v = col < N ? (nk == 2 ? a * a : fabsf(a)) : 0.f;   // columns past N hold products no one keeps
           float wgt = 1.f;
           if (p.wvec) {
             wgt = (row < M && col < N) ? p.wvec[d * p.w_ld + col] : 0.f;
             v = v * wgt;
           }
-          s += v;
+          s = nk == 1 ? fmaxf(s, v) : s + v;
           if (lower && p.h_out && row < M && col < N) {
             const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
             const float hs = p.h_scale[row];
@@ -732,7 +734,10 @@ gemm_kernel(GemmArgs p) {
       for (int r = 0; r < 16; ++r) {
         float s = rs[i][r];
 #pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+        for (int off = 16; off >= 1; off >>= 1) {
+          const float o = __shfl_xor(s, off, 64);
+          s = nk == 1 ? fmaxf(s, o) : s + o;
+        }
         rs[i][r] = s;
       }
     if (lrow == 0) {
@@ -750,7 +755,7 @@ gemm_kernel(GemmArgs p) {
       if (row < M) {
         float s = 0.f;
 #pragma unroll
-        for (int q = 0; q < T::NWN; ++q) s += red[q][rr];
+        for (int q = 0; q < T::NWN; ++q) s = nk == 1 ? fmaxf(s, red[q][rr]) : s + red[q][rr];
         p.partial[z][tile_n * M + row] = s;
       }
     }

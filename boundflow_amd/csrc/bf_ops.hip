@@ -30,7 +30,8 @@ namespace bf {
 int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream);
 int gemm_tile_choice(int64_t M, int64_t N, int nz, int64_t ks, int pro, bool dl);
 int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
-                        const float* bu, const float* bl, float eps, float* lb, float* ub, hipStream_t stream);
+                        const float* bu, const float* bl, float eps, int norm_p, float* lb, float* ub,
+                        hipStream_t stream);
 int gemm_partial_count(int64_t N);
 int rows_finalize(const float* b_src, const float* pb, const float* pc, int nparts, int64_t M, float* b_out,
                   float* c_out, hipStream_t stream);
@@ -66,20 +67,26 @@ int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_rel
   return BF_OK;
 }
 
-// row_norm[o] = sum_i |W[o, i]|   (Linf input layer, perturbation.py:133)
-__global__ void row_abs_sum_kernel(const float* __restrict__ W, int64_t O, int64_t I, float* __restrict__ out) {
+// Row norm of the input layer's weight under the input ball (perturbation.py:127-136):
+// kind 0 sum_i |W[o, i]| (Linf ball), 1 max_i |W[o, i]| (L1 ball), 2 sqrt(sum_i W[o, i]^2) (L2 ball);
+// the per-thread partials combined by a fixed tree.
+__global__ void row_norm_kernel(const float* __restrict__ W, int64_t O, int64_t I, int kind, float* __restrict__ out) {
   int64_t o = (int64_t)blockIdx.x;
   if (o >= O) return;
   float s = 0.f;
-  for (int64_t i = threadIdx.x; i < I; i += blockDim.x) s += fabsf(W[o * I + i]);
+  for (int64_t i = threadIdx.x; i < I; i += blockDim.x) {
+    const float w = W[o * I + i];
+    s = kind == 1 ? fmaxf(s, fabsf(w)) : (kind == 2 ? s + w * w : s + fabsf(w));
+  }
   __shared__ float sh[256];
   sh[threadIdx.x] = s;
   __syncthreads();
   for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+    if ((int)threadIdx.x < w)
+      sh[threadIdx.x] = kind == 1 ? fmaxf(sh[threadIdx.x], sh[threadIdx.x + w]) : sh[threadIdx.x] + sh[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) out[o] = sh[0];
+  if (threadIdx.x == 0) out[o] = kind == 2 ? sqrtf(sh[0]) : sh[0];
 }
 
 // lo = (c - dev) + b, hi = (c + dev) + b, then the ReLU split of the consumer
@@ -491,12 +498,13 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // Dense concretization (north-star kernel #4): one wave64 per row
-//   center = sum_i A[m,i] * c[d,i];  norm = sum_i |A[m,i]| (* rad[d,i])
-//   Linf: lb = (center - eps*norm) + b ; box: eps = 1 with radius weights.
+//   center = sum_i A[m,i] * c[d,i];  norm = sum_i |A[m,i]| (* rad[d,i])  (norm_p 0: Linf ball, box),
+//   max_i |A[m,i]| (1: L1 ball), sqrt(sum_i A[m,i]^2) (2: L2 ball);
+//   lb = (center - eps*norm) + b ; box: eps = 1 with radius weights.
 __global__ void __launch_bounds__(256)
 concretize_rows_kernel(const float* __restrict__ A, int64_t M, int64_t S, int64_t I, const float* __restrict__ cen,
-                       const float* __restrict__ rad, float eps, const float* __restrict__ b, int is_lower,
-                       float* __restrict__ out) {
+                       const float* __restrict__ rad, float eps, int norm_p, const float* __restrict__ b,
+                       int is_lower, float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (m >= M) return;
@@ -514,6 +522,10 @@ concretize_rows_kernel(const float* __restrict__ A, int64_t M, int64_t S, int64_
       if (r4) {
         float4 w = r4[q];
         nrm += fabsf(a.x) * w.x + fabsf(a.y) * w.y + fabsf(a.z) * w.z + fabsf(a.w) * w.w;
+      } else if (norm_p == 1) {
+        nrm = fmaxf(nrm, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+      } else if (norm_p == 2) {
+        nrm += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
       } else {
         nrm += fabsf(a.x) + fabsf(a.y) + fabsf(a.z) + fabsf(a.w);
       }
@@ -522,15 +534,19 @@ concretize_rows_kernel(const float* __restrict__ A, int64_t M, int64_t S, int64_
     for (int64_t i = lane; i < I; i += 64) {
       float a = row[i];
       c += a * cr[i];
-      nrm += rad ? fabsf(a) * rad[d * I + i] : fabsf(a);
+      if (rad) nrm += fabsf(a) * rad[d * I + i];
+      else if (norm_p == 1) nrm = fmaxf(nrm, fabsf(a));
+      else if (norm_p == 2) nrm += a * a;
+      else nrm += fabsf(a);
     }
   }
   for (int off = 32; off >= 1; off >>= 1) {
     c += __shfl_xor(c, off, 64);
-    nrm += __shfl_xor(nrm, off, 64);
+    const float o = __shfl_xor(nrm, off, 64);
+    nrm = norm_p == 1 ? fmaxf(nrm, o) : nrm + o;
   }
   if (lane == 0) {
-    float dev = eps * nrm;
+    float dev = eps * (norm_p == 2 ? sqrtf(nrm) : nrm);
     float v = is_lower ? c - dev : c + dev;
     out[m] = b ? v + b[m] : v;
   }
@@ -952,11 +968,11 @@ int bf_gemm_rank1(const float* A, int64_t lda, const float* B, int64_t ldb, int 
 
 int bf_concretize_finalize(const float* partial_u, const float* partial_l, int nparts, int64_t M,
                            const float* cen_u, const float* cen_l, const float* b_u, const float* b_l, float eps,
-                           float* lb, float* ub, hipStream_t stream) {
+                           int norm_p, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(M >= 0 && nparts >= 1, "bf_concretize_finalize: bad sizes");
   BF_REQUIRE((lb == nullptr || (partial_l && cen_l && b_l)) && (ub == nullptr || (partial_u && cen_u && b_u)),
              "bf_concretize_finalize: null pointer");
-  return concretize_finalize(partial_u, partial_l, nparts, M, cen_u, cen_l, b_u, b_l, eps, lb, ub, stream);
+  return concretize_finalize(partial_u, partial_l, nparts, M, cen_u, cen_l, b_u, b_l, eps, norm_p, lb, ub, stream);
 }
 
 int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, int64_t D,
@@ -1020,9 +1036,12 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
                                     const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t I,
                                     int w_trans, const float* bias, const float* cvec, const float* rad, float eps,
-                                    const float* b_u_in, const float* b_l_in, const float* h_scale,
+                                    int norm_p, const float* b_u_in, const float* b_l_in, const float* h_scale,
                                     float* h_out, float* workspace, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize: bad sizes");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (rad == nullptr && h_out == nullptr)),
+             "bf_crown_relu_linear_concretize: norm_p %d (0 Linf/box, 1 L1, 2 L2; the box radius and the "
+             "gradient seed go with 0 only)", norm_p);
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
   BF_REQUIRE(W && cvec && workspace, "bf_crown_relu_linear_concretize: null pointer");
@@ -1068,9 +1087,10 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
              "bf_crown_relu_linear_concretize: h_out needs h_scale and the lower coefficient");
   a.h_scale = h_scale;
   a.h_out = h_out;
+  a.norm_kind = norm_p;
   int rc = gemm_dispatch(a, PRO_RELAX, EPI_ABSSUM, nz, stream);
   if (rc) return rc;
-  return concretize_finalize(pu, pl, nparts, M, cu, cl, bu, bl, rad ? 1.0f : eps, lb, ub, stream);
+  return concretize_finalize(pu, pl, nparts, M, cu, cl, bu, bl, rad ? 1.0f : eps, norm_p, lb, ub, stream);
 }
 
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
@@ -1081,9 +1101,9 @@ int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t 
 int bf_crown_relu_linear_concretize_noalloc(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D,
                                             int64_t S, int64_t N, const float* relax, const float* add_l,
                                             int64_t add_ld, const float* W, int64_t I, int w_trans, const float* bias,
-                                            const float* cvec, const float* rad, float eps, const float* b_u_in,
-                                            const float* b_l_in, const float* h_scale, float* h_out, float* lb,
-                                            float* ub, hipStream_t stream) {
+                                            const float* cvec, const float* rad, float eps, int norm_p,
+                                            const float* b_u_in, const float* b_l_in, const float* h_scale,
+                                            float* h_out, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize_noalloc: bad sizes");
   if (D * S == 0) return BF_OK;
   const int64_t need = bf_crown_relu_linear_concretize_workspace(D, S, I);
@@ -1098,7 +1118,7 @@ int bf_crown_relu_linear_concretize_noalloc(const float* A_u, const float* A_l, 
   const int rc = concretize_scratch(&ws);
   if (rc) return rc;
   return bf_crown_relu_linear_concretize(A_u, A_l, a_dstride, D, S, N, relax, add_l, add_ld, W, I, w_trans, bias,
-                                         cvec, rad, eps, b_u_in, b_l_in, h_scale, h_out, ws, lb, ub, stream);
+                                         cvec, rad, eps, norm_p, b_u_in, b_l_in, h_scale, h_out, ws, lb, ub, stream);
 }
 
 int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
@@ -1215,11 +1235,14 @@ int64_t bf_crown_relu_linear_relu_fwd_workspace(int64_t D, int64_t S, int64_t P)
 }
 
 int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
-                               int64_t N, const float* W_t, int64_t I, const float* rad, float eps,
+                               int64_t N, const float* W_t, int64_t I, const float* rad, float eps, int norm_p,
                                const float* cen_u, const float* cen_l, const float* b_u, const float* b_l,
                                const float* h_scale, float* h_out, float* workspace, float* lb, float* ub,
                                hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0 && N > 0 && I > 0, "bf_crown_linear_concretize: bad sizes");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (rad == nullptr && h_out == nullptr)),
+             "bf_crown_linear_concretize: norm_p %d (0 Linf/box, 1 L1, 2 L2; the box radius and the gradient seed "
+             "go with 0 only)", norm_p);
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
   BF_REQUIRE(W_t && workspace, "bf_crown_linear_concretize: null weight or workspace");
@@ -1253,10 +1276,11 @@ int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dst
              "bf_crown_linear_concretize: h_out needs h_scale and the lower coefficient");
   a.h_scale = h_scale;
   a.h_out = h_out;
+  a.norm_kind = norm_p;
   int rc = gemm_dispatch(a, PRO_PLAIN, EPI_ABSSUM, nz, stream);
   if (rc) return rc;
   return concretize_finalize(A_u ? pu : nullptr, A_l ? pl : nullptr, nparts, M, cen_u, cen_l, b_u, b_l,
-                             rad ? 1.0f : eps, A_l ? lb : nullptr, A_u ? ub : nullptr, stream);
+                             rad ? 1.0f : eps, norm_p, A_l ? lb : nullptr, A_u ? ub : nullptr, stream);
 }
 
 int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
@@ -1320,14 +1344,16 @@ int bf_crown_relu_relax_lu(const float* A_u, const float* A_l, int64_t a_dstride
 }
 
 int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
-                        float eps, const float* b, int is_lower, float* out, hipStream_t stream) {
+                        float eps, int norm_p, const float* b, int is_lower, float* out, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && I > 0, "bf_concretize_dense: bad sizes");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || rad == nullptr),
+             "bf_concretize_dense: norm_p %d (0 Linf/box, 1 L1, 2 L2; the box radius goes with 0 only)", norm_p);
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
   BF_REQUIRE(A && center && out, "bf_concretize_dense: null pointer");
   BF_REQUIRE(((uintptr_t)A % 16) == 0 && ((uintptr_t)center % 16) == 0, "bf_concretize_dense: unaligned");
   hipLaunchKernelGGL(concretize_rows_kernel, dim3((unsigned)ceil_div(M, 4)), dim3(256), 0, stream, A, M, S, I,
-                     center, rad, rad ? 1.0f : eps, b, is_lower, out);
+                     center, rad, rad ? 1.0f : eps, norm_p, b, is_lower, out);
   BF_LAUNCH_CHECK("concretize_rows_kernel");
   return BF_OK;
 }
@@ -1373,8 +1399,9 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
                   int apply_relu, const float* W, const float* bias, int64_t N, const int8_t* split, int64_t split_ld,
                   float* workspace, float* out_lo, float* out_hi, float* center_out, int* infeasible,
                   hipStream_t stream) {
-  // input_kind 0: interval [in_lo, in_hi] (optionally through ReLU) or box; 1: Linf ball around in_lo
-  BF_REQUIRE(B >= 0 && K > 0 && N > 0, "bf_ibp_linear: bad sizes");
+  // input_kind 0: interval [in_lo, in_hi] (optionally through ReLU) or box; 1: Linf ball around in_lo;
+  // 2: L2 ball; 3: L1 ball (the row norm of W is the ball's dual norm, perturbation.py:127-136)
+  BF_REQUIRE(B >= 0 && K > 0 && N > 0 && input_kind >= 0 && input_kind <= 3, "bf_ibp_linear: bad sizes or input kind");
   if (B == 0) return BF_OK;
   BF_REQUIRE(in_lo && W && out_lo && out_hi && workspace, "bf_ibp_linear: null pointer");
   // workspace: mid [B*K], rad [B*K], c [B*N], r [B*N], rownorm [N], split-K partials
@@ -1387,11 +1414,12 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   float* cdst = center_out ? center_out : c;
   int rc;
   int ks = 1;
-  if (input_kind == 1) {
+  if (input_kind >= 1) {
     rc = ibp_products(in_lo, nullptr, W, B, K, N, cdst, nullptr, part, &ks, stream);
     if (rc) return rc;
-    hipLaunchKernelGGL(row_abs_sum_kernel, dim3((unsigned)N), dim3(256), 0, stream, W, N, K, rownorm);
-    BF_LAUNCH_CHECK("row_abs_sum_kernel");
+    const int kind = input_kind == 1 ? 0 : (input_kind == 2 ? 2 : 1);
+    hipLaunchKernelGGL(row_norm_kernel, dim3((unsigned)N), dim3(256), 0, stream, W, N, K, kind, rownorm);
+    BF_LAUNCH_CHECK("row_norm_kernel");
     return ibp_finalize_parts(cdst, nullptr, ks > 1 ? part : nullptr, ks, 0, center_out, rownorm, eps, bias, 1,
                               split, split_ld, B, N, out_lo, out_hi, infeasible, stream);
   }

@@ -303,7 +303,7 @@ class HipFusedCrownExecutor:
         with _timed("executor_conv_transpose", 4.0 * M * Co * Ho * Wo * Ci * KH * KW,
                     4.0 * (2 * M * N + 2 * M * Ci * Hi * Wi)):
             _lib.call("bf_conv_transpose_rows", _lib.ptr(ru), _lib.ptr(rl), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW,
-                      sh, sw, ph, pw, Hi, Wi, _lib.ptr(pu), _lib.ptr(pl), S, None, 0, None, None, None, None, st)
+                      sh, sw, ph, pw, Hi, Wi, _lib.ptr(pu), _lib.ptr(pl), S, None, 0, 0, None, None, None, None, st)
         return FusedReluAffineResult(pu, pl, du, dl)
 
 

@@ -96,6 +96,15 @@ class LinfInputSpec:
     eps: float
 
 
+def input_norm_p(pert) -> int:
+    """Norm code of the input concretization (perturbation.py:175-222): 0 for a Linf ball
+    or a box (sum |A|, radius-weighted for a box), 1 for an L1 ball (its dual norm
+    max |A|), 2 for an L2 ball (the row's L2 norm)."""
+    if isinstance(pert, BoxPerturbation):
+        return 0
+    return {"inf": 0, "1": 1, "2": 2}[pert.normalized_p()]
+
+
 @dataclass(frozen=True)
 class InputSpec:
     value_name: str
@@ -105,6 +114,14 @@ class InputSpec:
     @staticmethod
     def linf(*, value_name: str, center: torch.Tensor, eps: float) -> "InputSpec":
         return InputSpec(value_name=value_name, center=center, perturbation=LpBallPerturbation(p="inf", eps=eps))
+
+    @staticmethod
+    def l2(*, value_name: str, center: torch.Tensor, eps: float) -> "InputSpec":
+        return InputSpec(value_name=value_name, center=center, perturbation=LpBallPerturbation(p=2, eps=eps))
+
+    @staticmethod
+    def l1(*, value_name: str, center: torch.Tensor, eps: float) -> "InputSpec":
+        return InputSpec(value_name=value_name, center=center, perturbation=LpBallPerturbation(p=1, eps=eps))
 
     @staticmethod
     def box(*, value_name: str, lower: torch.Tensor, upper: torch.Tensor) -> "InputSpec":

@@ -48,7 +48,7 @@ def _conv_jacobian(W: torch.Tensor, attrs, in_shape, out_shape) -> torch.Tensor:
     eye = torch.eye(n_out, device=W.device, dtype=torch.float32)
     rows = torch.empty(n_out, Ci * Hi * Wi, device=W.device, dtype=torch.float32)
     _lib.call("bf_conv_transpose_rows", _lib.ptr(eye), None, n_out, Co, Ho, Wo, _lib.ptr(W.contiguous()), Ci, KH, KW,
-              sh, sw, ph, pw, Hi, Wi, _lib.ptr(rows), None, 1, None, 0, None, None, None, None,
+              sh, sw, ph, pw, Hi, Wi, _lib.ptr(rows), None, 1, None, 0, 0, None, None, None, None,
               _lib.stream_handle())
     return rows
 

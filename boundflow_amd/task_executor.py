@@ -26,7 +26,8 @@ import torch
 
 from . import _lib
 from .ir import BFTaskModule, BoundTask, StoragePlan, TaskKind
-from .spec import BoxPerturbation, InputSpec, IntervalState, LinfInputSpec, LpBallPerturbation, normalize_input_spec
+from .spec import (BoxPerturbation, InputSpec, IntervalState, LinfInputSpec, LpBallPerturbation, input_norm_p,
+                   normalize_input_spec)
 
 
 def _pair(v):
@@ -92,6 +93,9 @@ class HipTaskExecutor:
             raise ValueError(f"concretize_matmul expects center rank-2 [B,I], got {tuple(center.shape)}")
         B, K = (int(d) for d in center.shape)
         if w.dim() == 3:
+            if input_norm_p(p) != 0:
+                raise NotImplementedError("per-sample weights take Linf balls and boxes (L1/L2 need rank-2 weights)")
+            # Linf ball: eps * sum |W| over the rows equals the bounding box's radius term
             lo, hi = p.bounding_box(center)
             return self._batched_linear(IntervalState(lo, hi), w, b)
         if int(w.shape[1]) != K:
@@ -99,9 +103,9 @@ class HipTaskExecutor:
         if isinstance(p, BoxPerturbation):
             in_lo, in_hi, kind, eps = p.lower.reshape(B, K).contiguous(), p.upper.reshape(B, K).contiguous(), 0, 0.0
         else:
-            if p.normalized_p() != "inf":
-                raise NotImplementedError("HIP IBP supports Linf balls and boxes")
-            in_lo, in_hi, kind, eps = center.contiguous(), None, 1, float(p.eps)
+            # input kinds 1, 2, 3: Linf, L2, L1 ball (eps times the dual norm of each W row)
+            kind = {0: 1, 2: 2, 1: 3}[input_norm_p(p)]
+            in_lo, in_hi, eps = center.contiguous(), None, float(p.eps)
         return self._dense_linear(in_lo, in_hi, kind, eps, w, b)
 
     def _dense_linear(self, in_lo, in_hi, kind: int, eps: float, w: torch.Tensor,

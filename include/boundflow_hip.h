@@ -54,7 +54,8 @@ int bf_gemm_tile_config(int64_t M, int64_t N, int nz, int ksplit, int relax_prol
  * IntervalDomain.affine_transformer (domains/interval.py:79-86) for hidden
  * layers, and _apply_relu_split (runtime/crown_ibp.py:70-98).
  * input_kind 0: [in_lo, in_hi] box (ReLU applied first when apply_relu);
- * input_kind 1: Linf ball of radius eps around in_lo.
+ * input_kind 1: Linf ball of radius eps around in_lo; 2: L2 ball; 3: L1 ball
+ * (eps times the dual norm of each W row: sum |w|, the L2 norm, max |w|).
  * workspace: bf_ibp_linear_workspace(B, K, N) floats.  center_out (optional,
  * [B, N]) receives mid @ W^T without bias. */
 int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, int input_kind, float eps,
@@ -124,7 +125,10 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
 
 /* The input-layer region fused with the concretization (kernel #4):
  * lb = (A' . cvec - eps * sum_i |(A' W)_i| * rad_i) + b, ub mirrored;
- * rad NULL = Linf (weights 1, eps used), else box radius [D, I] (eps ignored).
+ * rad NULL = Lp ball (weights 1, eps used), else box radius [D, I] (eps ignored).
+ * norm_p selects the dual norm of the ball's row term: 0 sum |.| (Linf ball or
+ * box), 2 the L2 norm (L2 ball), 1 max |.| (L1 ball); 1 and 2 take no rad and
+ * no h_out.
  * cvec = center @ W^T per domain [D, N].  Replaces concretize_affine
  * (runtime/perturbation.py:175-222, 327-359) on RightMatmulLinearOperator
  * (runtime/linear_operator.py:503-586) as called at runtime/crown_ibp.py:2044-2051.
@@ -134,7 +138,7 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
                                     int64_t N, const float* relax, const float* add_l, int64_t add_ld, const float* W,
                                     int64_t I, int w_trans,
-                                    const float* bias, const float* cvec, const float* rad, float eps,
+                                    const float* bias, const float* cvec, const float* rad, float eps, int norm_p,
                                     const float* b_u_in, const float* b_l_in, const float* h_scale, float* h_out,
                                     float* workspace, float* lb, float* ub, hipStream_t stream);
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I);
@@ -145,12 +149,12 @@ int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t 
  * nothing.  Its workspace is a fixed 16 MiB device array per GPU (4M floats, held
  * until the process ends): returns 3 (size beyond the limit) when
  * bf_crown_relu_linear_concretize_workspace(D, S, I) exceeds 4194304 floats (e.g.
- * D * S > 233016 rows at I = 784).  Calls that overlap on one GPU share that array
+ * D * S > 233016 rows at I = 784).  norm_p as for bf_crown_relu_linear_concretize.  Calls that overlap on one GPU share that array
  * and race: serialise them.  Same results as bf_crown_relu_linear_concretize. */
 int bf_crown_relu_linear_concretize_noalloc(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D,
                                             int64_t S, int64_t N, const float* relax, const float* add_l,
                                             int64_t add_ld, const float* W, int64_t I, int w_trans, const float* bias,
-                                            const float* cvec, const float* rad, float eps, const float* b_u_in,
+                                            const float* cvec, const float* rad, float eps, int norm_p, const float* b_u_in,
                                             const float* b_l_in, const float* h_scale, float* h_out, float* lb,
                                             float* ub, hipStream_t stream);
 
@@ -186,16 +190,17 @@ int bf_crown_relu_linear_relu_fwd(const float* A_u, const float* A_l, int64_t a_
                                   float* c_l_out, hipStream_t stream);
 int64_t bf_crown_relu_linear_relu_fwd_workspace(int64_t D, int64_t S, int64_t P);
 
-/* Linf / box concretization of an input layer whose coefficient is already
+/* Lp-ball / box concretization of an input layer whose coefficient is already
  * relaxed (the output of bf_crown_relu_linear_relu_fwd):
  *   lb = (cen_l - eps * sum_i |(A_l W^T)_i| * rad_i) + b_l, ub mirrored,
- * with the center and bias sums given per row.  concretize_affine
+ * with the center and bias sums given per row; norm_p (0, 1, 2) swaps the
+ * row sum for the ball's dual norm as in bf_crown_relu_linear_concretize.  concretize_affine
  * (runtime/perturbation.py:175-222, 327-359) as called at crown_ibp.py:2044-2051.
  * h_scale/h_out (optional, lower bound only): the gradient seed
  * h = h_scale[m] * sign(A_l W^T) * rad, as in bf_crown_relu_linear_concretize.
  * workspace: bf_crown_linear_concretize_workspace(D, S, I) floats. */
 int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
-                               int64_t N, const float* W_t, int64_t I, const float* rad, float eps,
+                               int64_t N, const float* W_t, int64_t I, const float* rad, float eps, int norm_p,
                                const float* cen_u, const float* cen_l, const float* b_u, const float* b_l,
                                const float* h_scale, float* h_out, float* workspace, float* lb, float* ub,
                                hipStream_t stream);
@@ -229,11 +234,14 @@ int bf_crown_relu_relax_lu(const float* A_u, const float* A_l, int64_t a_dstride
  * runtime/linear_operator.py:1067-1092; FusedCrownExecutor "fused_relu_conv2d"
  * after bf_crown_relu_relax).  With norm_u/norm_l instead of y_u/y_l the
  * output rows are reduced to sum |y| (* wvec[d, e]) -- the concretization norm
- * of the input layer (linear_operator.py:1378-1452 + perturbation.py:175-222). */
+ * of the input layer (linear_operator.py:1378-1452 + perturbation.py:175-222).
+ * norm_p 2 reduces to sum y^2 (L2 ball), 1 to max |y| (L1 ball; Conv2dLinearOperator
+ * row_l2_norm / row_abs_max, linear_operator.py:991-997), both without wvec and h_out;
+ * bf_concretize_finalize with the same norm_p turns them into bounds. */
 int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co, int Ho, int Wo, const float* W,
                            int Ci, int KH, int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
-                           float* y_l, int64_t S, const float* wvec, int64_t w_ld, float* norm_u, float* norm_l,
-                           const float* h_scale, float* h_out, hipStream_t stream);
+                           float* y_l, int64_t S, const float* wvec, int64_t w_ld, int norm_p, float* norm_u,
+                           float* norm_l, const float* h_scale, float* h_out, hipStream_t stream);
 
 /* 1 when bf_crown_relu_conv_transpose (and the channel-last path of
  * bf_conv_transpose_rows) takes this conv shape: KH % sh == KW % sw == 0, Co a
@@ -273,8 +281,9 @@ int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, 
  * given.  Replaces bf_crown_relu_relax_lu followed by bf_conv_transpose_rows for
  * the input region (runtime/crown_ibp.py:1211-1298 then the input-layer
  * concretization of Conv2dLinearOperator, runtime/linear_operator.py:1378-1452
- * and runtime/perturbation.py:175-222).  Shapes: those
- * bf_conv_transpose_small_supported accepts (<= 4 input channels, <= 16 taps). */
+ * and runtime/perturbation.py:175-222).  norm_p as for bf_conv_transpose_rows.
+ * Shapes: those bf_conv_transpose_small_supported accepts (<= 4 input channels,
+ * <= 16 taps). */
 int bf_conv_transpose_small_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph,
                                       int pw, int Hi, int Wi);
 int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
@@ -282,10 +291,10 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
                                             int64_t alpha_ld, const float* add_l, int64_t add_ld, const float* kbias,
                                             const float* cvec, const float* b_u_in, const float* b_l_in,
                                             const float* W, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
-                                            int Hi, int Wi, const float* wvec, int64_t w_ld, const float* h_scale,
-                                            float* h_out, float* norm_u, float* norm_l, float* b_u_out,
-                                            float* b_l_out, float* c_u_out, float* c_l_out, float* relaxed_u,
-                                            float* relaxed_l, hipStream_t stream);
+                                            int Hi, int Wi, const float* wvec, int64_t w_ld, int norm_p,
+                                            const float* h_scale, float* h_out, float* norm_u, float* norm_l,
+                                            float* b_u_out, float* b_l_out, float* c_u_out, float* c_l_out,
+                                            float* relaxed_u, float* relaxed_l, hipStream_t stream);
 
 /* The weights of that pass in the order its workgroups stage them
  * (bf_conv_transpose_packed_floats floats, 16-byte aligned; 0 = shape not
@@ -323,16 +332,19 @@ int64_t bf_gemm_rank1_workspace(int64_t M, int64_t N, int64_t K);
 /* ---- kernel #4: concretization -------------------------------------------- */
 
 /* Dense coefficient rows A [M, I] against the input set:
- * out = A . center[d] -/+ eps * sum |A| (Linf, rad NULL) or -/+ sum |A| * rad[d] (box), + b.
+ * out = A . center[d] -/+ eps * sum |A| (Linf, rad NULL) or -/+ sum |A| * rad[d] (box), + b;
+ * norm_p 2 / 1 (rad NULL): eps times the row's L2 norm / max |A| (L2 / L1 ball).
  * Replaces LpBallPerturbation/BoxPerturbation.concretize_affine on a
  * DenseLinearOperator (runtime/perturbation.py:175-222, 327-359;
  * runtime/linear_operator.py:354-372).  is_lower selects the sign. */
 int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
-                        float eps, const float* b, int is_lower, float* out, hipStream_t stream);
+                        float eps, int norm_p, const float* b, int is_lower, float* out, hipStream_t stream);
 
-/* lb = (cen_l - eps * sum_q partial_l[q]) + b_l (ub mirrored), fixed-order sum over nparts. */
+/* lb = (cen_l - eps * sum_q partial_l[q]) + b_l (ub mirrored), fixed-order sum over nparts;
+ * norm_p 1: max over the parts (partials of max |.|), 2: sqrt of their sum
+ * (partials of sum of squares), 0: their sum. */
 int bf_concretize_finalize(const float* partial_u, const float* partial_l, int nparts, int64_t M,
-                           const float* cen_u, const float* cen_l, const float* b_u, const float* b_l, float eps,
+                           const float* cen_u, const float* cen_l, const float* b_u, const float* b_l, float eps, int norm_p,
                            float* lb, float* ub, hipStream_t stream);
 
 /* ---- kernel #5: alpha / beta gradients and the optimiser ------------------ */

@@ -62,15 +62,25 @@ def _input_marker(spec: InputSpec):
     return ("__input__", spec)
 
 
+def _dual_row_norm(weight: torch.Tensor, p: str, dim: int) -> torch.Tensor:
+    """Dual norm of each row over the Lp ball (perturbation.py:126-133): sum |w| for
+    Linf, the L2 norm for L2, max |w| for L1."""
+    if p == "inf":
+        return weight.abs().sum(dim=dim)
+    if p == "2":
+        return torch.linalg.vector_norm(weight, ord=2, dim=dim)
+    if p == "1":
+        return weight.abs().amax(dim=dim)
+    raise ValueError(f"unsupported p: {p!r}")
+
+
 def concretize_matmul(spec: InputSpec, center: torch.Tensor, weight: torch.Tensor, bias):
-    """perturbation.py:102-173 (Linf) and :282-325 (box), rank-2 weights."""
+    """perturbation.py:102-173 (Lp ball, p in {inf, 2, 1}) and :282-325 (box), rank-2 weights."""
     p = spec.perturbation
     if isinstance(p, LpBallPerturbation):
-        if p.normalized_p() != "inf":
-            raise NotImplementedError("oracle restates the Linf ball only")
         eps = float(p.eps)
         out_center = center.matmul(weight.t())
-        row_norm = weight.abs().sum(dim=1)
+        row_norm = _dual_row_norm(weight, p.normalized_p(), dim=1)
         deviation = eps * row_norm.unsqueeze(0)
         lb = out_center - deviation
         ub = out_center + deviation
@@ -684,12 +694,16 @@ def _value_shape(spec: InputSpec, interval_env, name) -> Tuple[int, ...]:
 
 
 def concretize_affine(spec: InputSpec, center: torch.Tensor, op, b):
-    """perturbation.py:175-222 (Linf) and :327-359 (box)."""
+    """perturbation.py:175-222 (Lp ball, p in {inf, 2, 1}) and :327-359 (box)."""
     p = spec.perturbation
     if isinstance(p, LpBallPerturbation):
         eps = float(p.eps)
         out_center = op.center_term(center)
-        deviation = eps * op.row_abs_sum()
+        q = p.normalized_p()
+        # row_l2_norm / row_abs_max of every reference operator reduce its dense
+        # materialization (linear_operator.py:368-372, 518-522, 813-821, 991-997)
+        row_norm = op.row_abs_sum() if q == "inf" else _dual_row_norm(op.to_dense(), q, dim=2)
+        deviation = eps * row_norm
         return out_center - deviation + b, out_center + deviation + b
     midpoint = (p.lower + p.upper) / 2.0
     radius = (p.upper - p.lower) / 2.0

@@ -29,7 +29,7 @@ import torch
 from boundflow_amd.ir import BFTaskModule, StoragePlan
 from boundflow_amd.spec import BoxPerturbation, InputSpec, IntervalState, LpBallPerturbation, normalize_input_spec
 
-from .crown_ref import interval_affine
+from .crown_ref import _dual_row_norm, interval_affine
 
 
 class _Ball:
@@ -51,15 +51,14 @@ def _concretize_matmul(spec: InputSpec, w: torch.Tensor, b) -> IntervalState:
         raise ValueError(f"concretize_matmul expects center rank-2 [B,I], got {tuple(c.shape)}")
     p = spec.perturbation
     if isinstance(p, LpBallPerturbation):
-        if p.normalized_p() != "inf":
-            raise NotImplementedError("oracle restates the Linf ball only")
         eps = float(p.eps)
+        q = p.normalized_p()
         if w.dim() == 2:
             out = c.matmul(w.t())
-            dev = eps * w.abs().sum(dim=1).unsqueeze(0)
+            dev = eps * _dual_row_norm(w, q, dim=1).unsqueeze(0)
         else:
             out = torch.bmm(c.unsqueeze(1), w.transpose(1, 2)).squeeze(1)
-            dev = eps * w.abs().sum(dim=2)
+            dev = eps * _dual_row_norm(w, q, dim=2)
         lb, ub = out - dev, out + dev
     else:
         mid = (p.lower + p.upper) / 2.0

@@ -71,17 +71,17 @@ def test_conv_transpose_rows_matches_fp64(shape):
     y_u = torch.empty(R, Ci, Hi, Wi, device=dev)
     y_l = torch.empty(R, Ci, Hi, Wi, device=dev)
     _lib.call("bf_conv_transpose_rows", _lib.ptr(Ad["u"]), _lib.ptr(Ad["l"]), R, Co, Ho, Wo, _lib.ptr(Wd), Ci, KH,
-              KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(y_l), S, None, 0, None, None, None, None, st)
+              KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(y_u), _lib.ptr(y_l), S, None, 0, 0, None, None, None, None, st)
     # norm epilogue (Linf weights and box weights) with the gradient seed on the lower bound
     n_u = torch.empty(R, device=dev)
     n_l = torch.empty(R, device=dev)
     h = torch.empty(R, nout, device=dev)
     _lib.call("bf_conv_transpose_rows", _lib.ptr(Ad["u"]), _lib.ptr(Ad["l"]), R, Co, Ho, Wo, _lib.ptr(Wd), Ci, KH,
-              KW, sh, sw, ph, pw, Hi, Wi, None, None, S, _lib.ptr(wvd), nout, _lib.ptr(n_u), _lib.ptr(n_l),
+              KW, sh, sw, ph, pw, Hi, Wi, None, None, S, _lib.ptr(wvd), nout, 0, _lib.ptr(n_u), _lib.ptr(n_l),
               _lib.ptr(hsd), _lib.ptr(h), st)
     n1 = torch.empty(R, device=dev)
     _lib.call("bf_conv_transpose_rows", None, _lib.ptr(Ad["l"]), R, Co, Ho, Wo, _lib.ptr(Wd), Ci, KH, KW, sh, sw, ph,
-              pw, Hi, Wi, None, None, S, None, 0, None, _lib.ptr(n1), None, None, st)
+              pw, Hi, Wi, None, None, S, None, 0, 0, None, _lib.ptr(n1), None, None, st)
     torch.cuda.synchronize()
 
     for k, y in (("u", y_u), ("l", y_l)):
@@ -104,6 +104,47 @@ def test_conv_transpose_rows_matches_fp64(shape):
     got = h.cpu().double()
     assert torch.allclose(got[sure], expect[sure], rtol=1e-6, atol=0), "gradient seed"
 
+
+
+@pytest.mark.parametrize("norm_p", [2, 1])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"R{s[0]}_Co{s[1]}_{s[2]}x{s[3]}_Ci{s[4]}_k{s[5]}s{s[7]}p{s[9]}"
+                                                for s in SHAPES])
+def test_conv_transpose_rows_lp_norms(shape, norm_p):
+    """The L2 / L1 ball norms of each transposed-conv row in every kernel's epilogue:
+    norm_p 2 gives sum y^2 (the root is the finalize's), norm_p 1 max |y|, for both
+    bounds.  Tolerance: each y carries at most taps * 2^-23 * (|A| conv |W|); the sum
+    of squares adds nout roundings, the max moves by at most the largest y error."""
+    dev = device()
+    R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, S = shape
+    Hi, Wi = _out_hw(Ho, Wo, KH, KW, sh, sw, ph, pw)
+    announce(f"bf_conv_transpose_rows Lp norm {norm_p} {shape}")
+    g = torch.Generator().manual_seed(R * 17 + Co + norm_p)
+    A = {k: torch.randn(R, Co, Ho, Wo, generator=g) for k in ("u", "l")}
+    W = torch.randn(Co, Ci, KH, KW, generator=g)
+    taps = Co * ((KH + sh - 1) // sh) * ((KW + sw - 1) // sw)
+    nout = Ci * Hi * Wi
+    n = {k: torch.full((R,), float("nan"), device=dev) for k in ("u", "l")}
+    Ad, Wd = {k: v.to(dev) for k, v in A.items()}, W.to(dev)
+    _lib.call("bf_conv_transpose_rows", _lib.ptr(Ad["u"]), _lib.ptr(Ad["l"]), R, Co, Ho, Wo,
+              _lib.ptr(Wd), Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, None, None, S, None, 0, norm_p,
+              _lib.ptr(n["u"]), _lib.ptr(n["l"]), None, None, _lib.stream_handle())
+    torch.cuda.synchronize()
+    for k in ("u", "l"):
+        y = F.conv_transpose2d(A[k].double(), W.double(), stride=(sh, sw), padding=(ph, pw)).flatten(1)
+        yb = F.conv_transpose2d(A[k].double().abs(), W.double().abs(), stride=(sh, sw), padding=(ph, pw)).flatten(1)
+        if norm_p == 2:
+            exact = y.pow(2).sum(1)
+            tol = (2 * taps + nout) * 2.0 ** -23 * yb.pow(2).sum(1)
+        else:
+            exact = y.abs().amax(1)
+            tol = taps * 2.0 ** -23 * yb.amax(1)
+        err = (n[k].cpu().double() - exact).abs()
+        assert bool((err <= tol + 1e-30).all()), f"norm_{k}: {float((err / tol).max()):.3g} x tolerance"
+    # weights and gradient seeds belong to sum |y| only
+    rc = _lib.load().bf_conv_transpose_rows(_lib.ptr(Ad["u"]), None, R, Co, Ho, Wo, _lib.ptr(Wd), Ci, KH, KW, sh, sw,
+                                            ph, pw, Hi, Wi, None, None, S, _lib.ptr(Wd), 1, norm_p, _lib.ptr(n["u"]),
+                                            None, None, None, _lib.stream_handle())
+    assert rc != 0 and b"norm_p" in _lib.load().bf_last_error()
 
 # (R, in_div, Ci, Hi, Wi, Co, KH, KW, sh, sw, ph, pw, abs_w, rank1)
 CONV_SHAPES = [
@@ -242,13 +283,14 @@ INPUT_SHAPES = [
 
 
 @pytest.mark.parametrize("shape", INPUT_SHAPES, ids=[f"R{s[0]}_Co{s[1]}_Ci{s[4]}" for s in INPUT_SHAPES])
-@pytest.mark.parametrize("variant", ["linf", "box_alpha_split"])
+@pytest.mark.parametrize("variant", ["linf", "box_alpha_split", "l2", "l1"])
 def test_relu_conv_transpose_concretize_matches_pass_then_conv(shape, variant):
     """bf_crown_relu_conv_transpose_concretize (the input layer in one pass) against
     bf_crown_relu_relax_lu + bf_conv_transpose_rows with norm outputs: the relaxed rows
     bit-identical to the pass's, the bias and center sums within the fp32 bound of their
     two summation orders, the norms within the accumulation bound of the transposed
-    convolution, and the gradient seed equal where the sign of y is certain."""
+    convolution, and the gradient seed equal where the sign of y is certain.  l2 / l1:
+    the norms of the L2 / L1 ball (sum y^2, max |y|), without the gradient seed."""
     dev = device()
     R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, S = shape
     Hi, Wi = _out_hw(Ho, Wo, KH, KW, sh, sw, ph, pw)
@@ -271,7 +313,8 @@ def test_relu_conv_transpose_concretize_matches_pass_then_conv(shape, variant):
     alpha = torch.rand(D, nin, generator=g) if box else None
     add = torch.randn(D, nin, generator=g) if box else None
     wv = torch.rand(D, nout, generator=g) if box else None
-    h_scale = torch.randn(R, generator=g)
+    norm_p = {"l2": 2, "l1": 1}.get(variant, 0)
+    h_scale = torch.randn(R, generator=g) if norm_p == 0 else None
     T = lambda x: None if x is None else x.to(dev).contiguous()   # noqa: E731
     a = {k: T(v) for k, v in dict(A_u=A_u, A_l=A_l, lo=lo, hi=hi, alpha=alpha, add=add, kb=kb, cv=cv, bu=b_in[0],
                                   bl=b_in[1], W=W, wv=wv, hs=h_scale).items()}
@@ -286,19 +329,19 @@ def test_relu_conv_transpose_concretize_matches_pass_then_conv(shape, variant):
               P("add"), nin, P("kb"), P("cv"), P("bu"), P("bl"), _lib.ptr(rp[0]), _lib.ptr(rp[1]), _lib.ptr(bp[0]),
               _lib.ptr(bp[1]), _lib.ptr(cp[0]), _lib.ptr(cp[1]), st)
     np_ = [torch.empty(R, device=dev) for _ in range(2)]
-    hp = torch.empty(R, nout, device=dev)
+    hp = torch.empty(R, nout, device=dev) if norm_p == 0 else None
     _lib.call("bf_conv_transpose_rows", _lib.ptr(rp[0]), _lib.ptr(rp[1]), R, Co, Ho, Wo, P("W"), Ci, KH, KW, sh, sw,
-              ph, pw, Hi, Wi, None, None, S, P("wv"), nout, _lib.ptr(np_[0]), _lib.ptr(np_[1]), P("hs"),
+              ph, pw, Hi, Wi, None, None, S, P("wv"), nout, norm_p, _lib.ptr(np_[0]), _lib.ptr(np_[1]), P("hs"),
               _lib.ptr(hp), st)
     # the fused kernel
     nf = [torch.empty(R, device=dev) for _ in range(2)]
     bf = [torch.empty(R, device=dev) for _ in range(2)]
     cf = [torch.empty(R, device=dev) for _ in range(2)]
-    hf = torch.empty(R, nout, device=dev)
+    hf = torch.empty(R, nout, device=dev) if norm_p == 0 else None
     rf_l = torch.empty(R, nin, device=dev)
     _lib.call("bf_crown_relu_conv_transpose_concretize", P("A_u"), P("A_l"), D, S, Co, Ho, Wo, P("lo"), P("hi"),
               P("alpha"), ald, P("add"), nin, P("kb"), P("cv"), P("bu"), P("bl"), P("W"), Ci, KH, KW, sh, sw, ph, pw,
-              Hi, Wi, P("wv"), nout, P("hs"), _lib.ptr(hf), _lib.ptr(nf[0]), _lib.ptr(nf[1]), _lib.ptr(bf[0]),
+              Hi, Wi, P("wv"), nout, norm_p, P("hs"), _lib.ptr(hf), _lib.ptr(nf[0]), _lib.ptr(nf[1]), _lib.ptr(bf[0]),
               _lib.ptr(bf[1]), _lib.ptr(cf[0]), _lib.ptr(cf[1]), None, _lib.ptr(rf_l), st)
     torch.cuda.synchronize()
     assert torch.equal(rf_l, rp[1]), "relaxed rows differ from the relaxation pass"
@@ -311,8 +354,15 @@ def test_relu_conv_transpose_concretize_matches_pass_then_conv(shape, variant):
         taps = Co * ((KH + sh - 1) // sh) * ((KW + sw - 1) // sw)
         wgt = wv.double()[torch.arange(R) // S] if box else torch.ones(R, nout, dtype=torch.float64)
         ytol = taps * 2.0 ** -23 * ybound
-        nref = (y.abs() * wgt).sum(1)
-        ntol = (ytol * wgt).sum(1) + nout * 2.0 ** -23 * nref + 1e-30
+        if norm_p == 2:
+            nref = y.pow(2).sum(1)
+            ntol = (2 * taps + nout) * 2.0 ** -23 * ybound.pow(2).sum(1) + 1e-30
+        elif norm_p == 1:
+            nref = y.abs().amax(1)
+            ntol = ytol.amax(1) + 1e-30
+        else:
+            nref = (y.abs() * wgt).sum(1)
+            ntol = (ytol * wgt).sum(1) + nout * 2.0 ** -23 * nref + 1e-30
         nerr = (nf[z].double().cpu() - nref).abs()
         assert bool((nerr <= ntol).all()), f"norm {z}: {float((nerr / ntol).max()):.3g} x tolerance"
         terms = (A.abs().sum(1).double() * beta_max + rel.abs().mul(kb.double().abs()).sum(1)
@@ -322,6 +372,6 @@ def test_relu_conv_transpose_concretize_matches_pass_then_conv(shape, variant):
         cterms = (rel.abs() * cv.double().abs()[torch.arange(R) // S]).sum(1)
         cerr = (cf[z].double().cpu() - cp[z].double().cpu()).abs()
         assert bool((cerr <= 2 * nin * 2.0 ** -24 * cterms + 1e-30).all()), f"c {z}: max err {float(cerr.max()):.3e}"
-        if z == 1:
+        if z == 1 and norm_p == 0:
             sure = y.abs() > ytol
             assert torch.equal(hf.cpu()[sure], hp.cpu()[sure]), "gradient seed differs where sign(y) is certain"

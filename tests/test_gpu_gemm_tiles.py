@@ -95,7 +95,7 @@ def test_concretize_on_tile_q_matches_fp64(box):
     h_out = torch.empty(M, I, device=dev)
     A_ud, A_ld, Wtd, radd = d(A_u), d(A_l), d(Wt), d(rad)
     _lib.call("bf_crown_linear_concretize", _lib.ptr(A_ud), _lib.ptr(A_ld), S * N, D, S, N, _lib.ptr(Wtd), I,
-              _lib.ptr(radd), eps, _lib.ptr(d(cen_u)), _lib.ptr(d(cen_l)), _lib.ptr(d(b_u)), _lib.ptr(d(b_l)),
+              _lib.ptr(radd), eps, 0, _lib.ptr(d(cen_u)), _lib.ptr(d(cen_l)), _lib.ptr(d(b_u)), _lib.ptr(d(b_l)),
               _lib.ptr(d(h_scale)), _lib.ptr(h_out), _lib.ptr(ws), _lib.ptr(lb), _lib.ptr(ub), _lib.stream_handle())
     torch.cuda.synchronize()
     for side, got in (("u", ub), ("l", lb)):

@@ -275,7 +275,7 @@ def test_relax_pass_and_dense_concretize_match_oracle(K, S):
     xd = x0.to(dev).contiguous()
     Al = ref[1].to(dev).contiguous()
     bld = ref[3].to(dev).contiguous()
-    _lib.call("bf_concretize_dense", _lib.ptr(Al), D, S, K, _lib.ptr(xd), None, 0.05, _lib.ptr(bld), 1,
+    _lib.call("bf_concretize_dense", _lib.ptr(Al), D, S, K, _lib.ptr(xd), None, 0.05, 0, _lib.ptr(bld), 1,
               _lib.ptr(lb), _lib.stream_handle())
     torch.cuda.synchronize()
     # fp32 cancellation in center - eps * norm + b: judged against the fp64 oracle where the fp32 one differs

@@ -1,0 +1,164 @@
+"""Pin the oracle's L1 / L2 ball concretization (perturbation.py:102-222).
+
+Over the ball ||x - x0||_p <= eps the minimum of w . x is w . x0 - eps * ||w||_q
+with q the dual exponent (q = 1 for Linf, 2 for L2, inf for L1), and the
+minimum is attained at a point the mathematics names: x0 - eps * sign(w) (Linf),
+x0 - eps * w / ||w||_2 (L2), x0 - eps * sign(w_j) e_j at j = argmax |w_j| (L1).
+Each check below evaluates the network at that point: a bound that is sound
+(no sample below it) and attained is the exact minimum, which a wrong dual norm
+(the L1 norm for an L2 ball, a missing square root, a sum for a max) fails.
+Samplers are restatements of tests/test_phase6b_crown_ibp_mlp.py:29-56.
+"""
+
+import pytest
+import torch
+
+from boundflow_amd.ir import BFTaskModule, BoundTask, TaskKind, TaskOp
+from boundflow_amd.spec import InputSpec, LpBallPerturbation
+from oracle import crown_ref as cr
+from oracle import task_ibp_ref as tr
+
+
+def _spec(p, x0, eps):
+    return InputSpec(value_name="input", center=x0, perturbation=LpBallPerturbation(p=p, eps=eps))
+
+
+def _argmin_point(p, x0, w, eps):
+    """The point of the ball around x0 [I] that minimizes w . x (w [I])."""
+    if p == "inf":
+        return x0 - eps * torch.sign(w)
+    if p == 2:
+        return x0 - eps * w / torch.linalg.vector_norm(w)
+    j = int(w.abs().argmax())
+    x = x0.clone()
+    x[j] -= eps * torch.sign(w[j])
+    return x
+
+
+def _in_ball(p, x, x0, eps, tol=1e-12):
+    ord_ = float("inf") if p == "inf" else p
+    return float(torch.linalg.vector_norm(x - x0, ord=ord_)) <= eps + tol
+
+
+def _sample(p, x0, eps, n, gen):
+    """n points of the ball around each row of x0 [B, I] -> [n, B, I]."""
+    b, d = (int(s) for s in x0.shape)
+    if p == "inf":
+        return x0.unsqueeze(0) + eps * (torch.rand(n, b, d, generator=gen, dtype=x0.dtype) * 2 - 1)
+    g = torch.randn(n, b, d, generator=gen, dtype=x0.dtype)
+    r = torch.rand(n, b, 1, generator=gen, dtype=x0.dtype).pow(1.0 / d) * eps
+    if p == 2:
+        u = g / torch.linalg.vector_norm(g, ord=2, dim=-1, keepdim=True).clamp_min(1e-12)
+        return x0.unsqueeze(0) + u * r
+    s = torch.sign(g)
+    s[s == 0] = 1.0
+    u = g.abs() / g.abs().sum(dim=-1, keepdim=True).clamp_min(1e-12)
+    return x0.unsqueeze(0) + s * u * r
+
+
+def _mlp(w1, b1, w2, b2):
+    task = BoundTask(task_id="t0", kind=TaskKind.INTERVAL_IBP, ops=[
+        TaskOp("linear", "linear1", ["input", "W1", "b1"], ["h1"]),
+        TaskOp("relu", "relu1", ["h1"], ["r1"]),
+        TaskOp("linear", "linear2", ["r1", "W2", "b2"], ["out"]),
+    ], input_values=["input"], output_values=["out"])
+    return BFTaskModule(tasks=[task], entry_task_id="t0", bindings={"params": {"W1": w1, "b1": b1, "W2": w2, "b2": b2}})
+
+
+@pytest.mark.parametrize("p", ["inf", 2, 1])
+def test_concretize_matmul_is_the_attained_minimum(p):
+    gen = torch.Generator().manual_seed(5)
+    B, I, O, eps = 3, 11, 7, 0.3
+    x0 = torch.randn(B, I, generator=gen, dtype=torch.float64)
+    W = torch.randn(O, I, generator=gen, dtype=torch.float64)
+    bias = torch.randn(O, generator=gen, dtype=torch.float64)
+    lb, ub = cr.concretize_matmul(_spec(p, x0, eps), x0, W, bias)
+    for b in range(B):
+        for o in range(O):
+            xl = _argmin_point(p, x0[b], W[o], eps)
+            xu = _argmin_point(p, x0[b], -W[o], eps)
+            assert _in_ball(p, xl, x0[b], eps) and _in_ball(p, xu, x0[b], eps)
+            assert abs(float(W[o] @ xl + bias[o] - lb[b, o])) < 1e-12
+            assert abs(float(W[o] @ xu + bias[o] - ub[b, o])) < 1e-12
+    ys = _sample(p, x0, eps, 512, gen).matmul(W.t()) + bias
+    assert (ys >= lb - 1e-12).all() and (ys <= ub + 1e-12).all()
+    # the task-executor restatement of the same input layer agrees (rank-2 weights)
+    st = tr._concretize_matmul(_spec(p, x0, eps), W, bias)
+    assert torch.allclose(st.lower, lb, rtol=0, atol=1e-12)
+    assert torch.allclose(st.upper, ub, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("p", ["inf", 2, 1])
+def test_concretize_affine_dense_and_lazy_operators(p):
+    """concretize_affine on a dense coefficient and on the lazy A @ W operator: the same
+    closed form, attained, as the rank-2 case."""
+    gen = torch.Generator().manual_seed(9)
+    B, K, O, I, eps = 2, 4, 6, 9, 0.2
+    x0 = torch.randn(B, I, generator=gen, dtype=torch.float64)
+    A = torch.randn(B, K, O, generator=gen, dtype=torch.float64)
+    W = torch.randn(O, I, generator=gen, dtype=torch.float64)
+    bb = torch.randn(B, K, generator=gen, dtype=torch.float64)
+    dense = A.matmul(W)
+    lazy = cr.RightMatmulOp(cr.DenseOp(A, (O,)), W)
+    for op in (cr.DenseOp(dense, (I,)), lazy):
+        lb, ub = cr.concretize_affine(_spec(p, x0, eps), x0, op, bb)
+        for b in range(B):
+            for k in range(K):
+                xl = _argmin_point(p, x0[b], dense[b, k], eps)
+                xu = _argmin_point(p, x0[b], -dense[b, k], eps)
+                assert abs(float(dense[b, k] @ xl + bb[b, k] - lb[b, k])) < 1e-12
+                assert abs(float(dense[b, k] @ xu + bb[b, k] - ub[b, k])) < 1e-12
+
+
+@pytest.mark.parametrize("p,B,I,H,O,eps", [
+    ("inf", 3, 16, 32, 8, 0.2),   # tests/test_phase6b_crown_ibp_mlp.py:68-95 shapes
+    (2, 2, 24, 16, 6, 0.5),       # :98-122
+    (1, 2, 20, 12, 4, 0.6),       # :125-150
+])
+def test_crown_mlp_sound_on_sampled_ball(p, B, I, H, O, eps):
+    torch.manual_seed(0)
+    x0 = torch.randn(B, I)
+    w1, b1 = torch.randn(H, I), torch.randn(H)
+    w2, b2 = torch.randn(O, H), torch.randn(O)
+    out = cr.run_crown_ibp(_mlp(w1, b1, w2, b2), _spec(p, x0, eps))
+    xs = _sample(p, x0, eps, 256, torch.Generator().manual_seed(1))
+    ys = torch.relu(xs.matmul(w1.t()) + b1).matmul(w2.t()) + b2
+    assert (ys >= out.lower.unsqueeze(0) - 1e-5).all()
+    assert (ys <= out.upper.unsqueeze(0) + 1e-5).all()
+    # CROWN is no looser than IBP on the upper bound (test_phase6b_crown_ibp_mlp.py:85-88)
+    ibp = tr.run_ibp(_mlp(w1, b1, w2, b2), _spec(p, x0, eps))
+    assert (out.upper <= ibp.upper + 1e-5).all()
+
+
+@pytest.mark.parametrize("p", ["inf", 2, 1])
+def test_crown_exact_when_every_relu_is_active(p):
+    """A first-layer bias far above every pre-activation's range keeps every ReLU active:
+    the network is the affine map W2 W1 x + (W2 b1 + b2), and CROWN's bounds are its
+    attained minimum and maximum over the ball."""
+    gen = torch.Generator().manual_seed(2)
+    B, I, H, O, eps = 2, 10, 8, 5, 0.25
+    x0 = torch.randn(B, I, generator=gen, dtype=torch.float64)
+    w1 = torch.randn(H, I, generator=gen, dtype=torch.float64)
+    b1 = torch.full((H,), 100.0, dtype=torch.float64)
+    w2 = torch.randn(O, H, generator=gen, dtype=torch.float64)
+    b2 = torch.randn(O, generator=gen, dtype=torch.float64)
+    out = cr.run_crown_ibp(_mlp(w1, b1, w2, b2), _spec(p, x0, eps))
+    M = w2 @ w1
+    for b in range(B):
+        for o in range(O):
+            xl = _argmin_point(p, x0[b], M[o], eps)
+            xu = _argmin_point(p, x0[b], -M[o], eps)
+            f = lambda x: float(w2[o] @ torch.relu(w1 @ x + b1) + b2[o])
+            assert abs(f(xl) - float(out.lower[b, o])) < 1e-9
+            assert abs(f(xu) - float(out.upper[b, o])) < 1e-9
+
+
+def test_dual_norms_are_ordered():
+    """For every row, max |w| <= ||w||_2 <= sum |w| (balls of the same eps nest the
+    other way), so the L1 ball's bounds lie inside the L2 ball's, inside the Linf ball's."""
+    gen = torch.Generator().manual_seed(4)
+    x0 = torch.randn(4, 13, generator=gen, dtype=torch.float64)
+    W = torch.randn(9, 13, generator=gen, dtype=torch.float64)
+    lo = {p: cr.concretize_matmul(_spec(p, x0, 0.1), x0, W, None)[0] for p in ("inf", 2, 1)}
+    assert (lo[1] >= lo[2] - 1e-15).all() and (lo[2] >= lo["inf"] - 1e-15).all()
+    assert not torch.equal(lo[1], lo[2]) and not torch.equal(lo[2], lo["inf"])

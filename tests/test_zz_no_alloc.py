@@ -43,7 +43,7 @@ def _run(c, noalloc):
     ub = torch.full((D, S), float("nan"), device=dev)
     h = torch.full((D * S, I), float("nan"), device=dev)
     args = [_lib.ptr(c["A_u"]), _lib.ptr(c["A_l"]), S * N, D, S, N, _lib.ptr(c["table"]), _lib.ptr(c["add"]), N,
-            _lib.ptr(c["Wt"]), I, 1, _lib.ptr(c["bias"]), _lib.ptr(c["cvec"]), _lib.ptr(c["rad"]), c["eps"],
+            _lib.ptr(c["Wt"]), I, 1, _lib.ptr(c["bias"]), _lib.ptr(c["cvec"]), _lib.ptr(c["rad"]), c["eps"], 0,
             _lib.ptr(c["b_u"]), _lib.ptr(c["b_l"]), _lib.ptr(c["h_scale"]), _lib.ptr(h)]
     if noalloc:
         _lib.call("bf_crown_relu_linear_concretize_noalloc", *args, _lib.ptr(lb), _lib.ptr(ub), _lib.stream_handle())
@@ -75,6 +75,6 @@ def test_noalloc_refuses_sizes_beyond_its_array():
     dummy = torch.zeros(4, device=dev)
     rc = _lib.load().bf_crown_relu_linear_concretize_noalloc(
         _lib.ptr(dummy), None, S * N, D, S, N, None, None, 0, _lib.ptr(dummy), I, 1, None, _lib.ptr(dummy), None,
-        0.01, None, None, None, None, None, _lib.ptr(dummy), _lib.stream_handle())
+        0.01, 0, None, None, None, None, None, _lib.ptr(dummy), _lib.stream_handle())
     assert rc == 3
     assert b"fixed scratch" in _lib.load().bf_last_error()
