@@ -44,7 +44,7 @@ from .crown import (
     parse_chain,
 )
 from .profiling import launch as _timed
-from .spec import InputSpec, IntervalState, normalize_input_spec, input_norm_p
+from .spec import InputSpec, IntervalState, normalize_input_spec
 
 
 @dataclass
@@ -291,9 +291,6 @@ def run_alpha_beta_crown_mlp(
     if spec_reduce == "softmin" and float(soft_tau) <= 0.0:
         raise ValueError(f"soft_tau must be >0, got {soft_tau}")
     spec = normalize_input_spec(input_spec)
-    if input_norm_p(spec.perturbation) != 0:
-        # the reverse pass seeds the concretization's gradient for sum |A| (Linf ball, box) only
-        raise NotImplementedError("alpha/alpha-beta CROWN takes Linf balls and boxes; L1/L2 balls run with CROWN")
     chain = _chain_or_none(module, spec)
     if (first_layer_certificate and relu_split_state and int(spec.center.shape[0]) == 1
             and any(bool((v != 0).any().item()) for v in relu_split_state.values() if v is not None)):

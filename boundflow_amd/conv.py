@@ -148,7 +148,7 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
         return y_u, y_l, nb_u, nb_l, S * n_in, None
     # input layer: transposed conv fused with the concretization
     pert = spec.perturbation
-    norm_p = _input_norm(pert, save)
+    norm_p = input_norm_p(pert)
     if cvec is None:
         raise RuntimeError("forward trace lacks the input-layer projection")
     if isinstance(pert, BoxPerturbation):
@@ -186,7 +186,7 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
     gradient pass; then the bounds from the norms, centers and biases."""
     dev = spec.center.device
     stream = _lib.stream_handle()
-    norm_p = _input_norm(spec.perturbation, save)
+    norm_p = input_norm_p(spec.perturbation)
     Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi = geo
     n_out, n_in = Co * Ho * Wo, Ci * Hi * Wi
     nb_u, nb_l = nb
@@ -223,14 +223,3 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
               _lib.ptr(nb_u), _lib.ptr(nb_l), eps, norm_p, _lib.ptr(lb), _lib.ptr(ub), stream)
     return None, None, None, None, 0, IntervalState(lower=lb, upper=ub)
 
-
-def _input_norm(pert, save):
-    """Norm code of the input conv layer's concretization: sum |y| for a Linf ball or a
-    box, the row's L2 norm for an L2 ball, max |y| for an L1 ball
-    (Conv2dLinearOperator.row_abs_sum / row_l2_norm / row_abs_max,
-    runtime/linear_operator.py:991-997).  The gradient seed of the alpha/beta pass is
-    built for sum |y| only."""
-    norm_p = input_norm_p(pert)
-    if norm_p != 0 and save is not None and save.get("grad_rows") is not None:
-        raise NotImplementedError("the alpha/beta reverse pass takes Linf balls and boxes")
-    return norm_p

@@ -613,14 +613,12 @@ def lower_grad_pass(module: BFTaskModule, spec: InputSpec, trace: DagTrace, save
     M = B * S
     A_in = saved["input_A"]
     I = int(A_in.shape[1])
-    if input_norm_p(spec.perturbation) != 0:
-        raise NotImplementedError("the alpha/beta reverse pass takes Linf balls and boxes")
     center, rad, eps = _input_center_radius(spec, B, I)
     GA: Dict[str, torch.Tensor] = {}
     g0 = torch.empty(M, I, device=dev)
     with _timed("concretize_dense_grad", 0.0, 4.0 * 3 * M * I):
         _lib.call("bf_concretize_dense_grad", _lib.ptr(A_in), B, S, I, _lib.ptr(center), _lib.ptr(rad), eps,
-                  _lib.ptr(G), _lib.ptr(g0), stream)
+                  input_norm_p(spec.perturbation), _lib.ptr(G), _lib.ptr(g0), stream)
     GA[spec.value_name] = g0
     g_alpha: Dict[str, torch.Tensor] = {}
     g_beta: Dict[str, torch.Tensor] = {}

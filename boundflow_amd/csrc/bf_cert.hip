@@ -10,14 +10,15 @@
 // from z = 0, Adam (lr 0.1, betas 0.9 / 0.999, eps 1e-8) on the maximum,
 // 200 steps, stopping at the first step whose maximum is below -tol
 // (boundflow/runtime/alpha_beta_crown.py:391-532, halfspaces collected in
-// op order then neuron order at :259-389).  The maximum over an Linf ball is
-// a . x0 + eps * |a|_1 + c, over a box a . mid + |a| . rad + c
+// op order then neuron order at :259-389).  The maximum over an Lp ball is
+// a . x0 + eps * |a|_q + c with q the dual exponent (|a|_1 for Linf, |a|_2 for
+// L2, max |a| for L1), over a box a . mid + |a| . rad + c
 // (boundflow/runtime/perturbation.py:175-222, :327-359).
 //
 // One workgroup per node runs the whole search: the node's nonzero splits are
 // compacted into LDS in neuron order, each step forms a = sum_i w_i a_i in LDS
 // (every column summed over i in order), reduces the maximum, and takes the
-// gradient dmax/dw_i = a_i . (x0 + eps * sign(a)) + c_i (one wave per row),
+// gradient dmax/dw_i = a_i . (x0 + eps * d|a|_q/da) + c_i (one wave per row),
 // the softmax's backward and the Adam step on z.  Rows are read from the
 // weight itself (L2-resident across steps); nothing is materialised per node.
 
@@ -61,8 +62,8 @@ template <bool BOX>
 __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
     const float* __restrict__ rows, int64_t row_ld, const float* __restrict__ bias,
     const int8_t* __restrict__ split, int64_t split_ld, const float* __restrict__ center, int64_t center_ld,
-    const float* __restrict__ rad, int64_t rad_ld, float eps, int n0, int in_dim, int steps, double tol, float w1,
-    float b2, float w2, float adam_eps, CertAdamTable tab, int32_t* __restrict__ out) {
+    const float* __restrict__ rad, int64_t rad_ld, float eps, int nk, int n0, int in_dim, int steps, double tol,
+    float w1, float b2, float w2, float adam_eps, CertAdamTable tab, int32_t* __restrict__ out) {
   extern __shared__ float a_vec[];                       // [in_dim]: the combined normal a
   __shared__ int h_idx[kCertMaxHalfspaces];              // neuron of each halfspace, in order
   __shared__ float h_sgn[kCertMaxHalfspaces];            // its split sign s_i
@@ -135,16 +136,25 @@ __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
     for (int i = tid; i < m; i += kCertThreads) w[i] = w[i] / esum;
     __syncthreads();
     // 3. a = sum_i w_i s_i r_i (each column summed over i in order) and the maximum
+    // nk (Lp ball): 0 sum |a| (Linf), 2 the L2 norm, 1 max |a| (L1)
     float ct = 0.f, nrm = 0.f;
     for (int j = tid; j < in_dim; j += kCertThreads) {
       float acc = 0.f;
       for (int i = 0; i < m; ++i) acc += w[i] * (h_sgn[i] * rows[(int64_t)h_idx[i] * row_ld + j]);
       a_vec[j] = acc;
       ct += acc * x0[j];
-      nrm += BOX ? fabsf(acc) * rr[j] : fabsf(acc);
+      if (BOX) nrm += fabsf(acc) * rr[j];
+      else nrm = nk == 1 ? fmaxf(nrm, fabsf(acc)) : nrm + (nk == 2 ? acc * acc : fabsf(acc));
     }
     ct = block_sum_cert(ct, red);
-    nrm = block_sum_cert(nrm, red);
+    nrm = (!BOX && nk == 1) ? block_max_cert(nrm, red) : block_sum_cert(nrm, red);
+    if (!BOX && nk == 2) nrm = sqrtf(nrm);
+    float ties = 1.f;   // L1: entries at max |a| share amax's gradient
+    if (!BOX && nk == 1) {
+      float cnt = 0.f;
+      for (int j = tid; j < in_dim; j += kCertThreads) cnt += fabsf(a_vec[j]) == nrm ? 1.f : 0.f;
+      ties = block_sum_cert(cnt, red);
+    }
     float c = 0.f;
     if (bias != nullptr)
       for (int i = 0; i < m; ++i) c += w[i] * (h_sgn[i] * bias[h_idx[i]]);
@@ -155,12 +165,20 @@ __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
       break;
     }
     if (t + 1 == n_steps) break;
-    // 4. dub/dw_i = a_i . (x0 + eps * sign(a)) + c_i, one wave per halfspace
+    // 4. dub/dw_i = a_i . (x0 + eps * d|a|_q/da) + c_i, one wave per halfspace; d|a|_q/da is
+    //    sign(a) (Linf), a / |a|_2 (L2, 0 at a = 0), sign(a) / ties on the maxima of |a| (L1)
+    const float l2s = nrm > 0.f ? eps / nrm : 0.f;
+    const float l1s = eps / ties;
     for (int i = wave; i < m; i += kCertThreads / 64) {
       const float* r = rows + (int64_t)h_idx[i] * row_ld;
       float acc = 0.f;
       for (int j = lane; j < in_dim; j += 64) {
-        const float ga = BOX ? x0[j] + sign_f(a_vec[j]) * rr[j] : x0[j] + eps * sign_f(a_vec[j]);
+        const float aj = a_vec[j];
+        float ga;
+        if (BOX) ga = x0[j] + sign_f(aj) * rr[j];
+        else if (nk == 2) ga = x0[j] + aj * l2s;
+        else if (nk == 1) ga = x0[j] + (fabsf(aj) == nrm ? sign_f(aj) * l1s : 0.f);
+        else ga = x0[j] + eps * sign_f(aj);
         acc += (h_sgn[i] * r[j]) * ga;
       }
       acc = wave_sum(acc);
@@ -195,9 +213,11 @@ using namespace bf;
 
 extern "C" int bf_split_certificate(const float* rows, int64_t row_ld, const float* bias, const int8_t* split,
                                     int64_t split_ld, const float* center, int64_t center_ld, const float* rad,
-                                    int64_t rad_ld, float eps, int64_t nodes, int64_t n0, int64_t in_dim, int steps,
-                                    double lr, double tol, int32_t* out, hipStream_t stream) {
+                                    int64_t rad_ld, float eps, int norm_p, int64_t nodes, int64_t n0, int64_t in_dim,
+                                    int steps, double lr, double tol, int32_t* out, hipStream_t stream) {
   BF_REQUIRE(nodes >= 0 && n0 >= 0 && in_dim >= 1, "bf_split_certificate: bad sizes");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || rad == nullptr),
+             "bf_split_certificate: norm_p is 0, 1 or 2; the box radius goes with 0");
   if (nodes == 0) return BF_OK;
   BF_REQUIRE(rows && split && center && out, "bf_split_certificate: null pointer");
   BF_REQUIRE(steps >= 1 && steps <= kCertMaxSteps, "bf_split_certificate: steps must be in [1, %d]", kCertMaxSteps);
@@ -222,12 +242,12 @@ extern "C" int bf_split_certificate(const float* rows, int64_t row_ld, const flo
   const size_t lds = (size_t)in_dim * sizeof(float);
   if (rad != nullptr)
     hipLaunchKernelGGL(split_certificate_kernel<true>, dim3((unsigned)nodes), dim3(kCertThreads), lds, stream, rows,
-                       row_ld, bias, split, split_ld, center, center_ld, rad, rad_ld, 0.f, (int)n0, (int)in_dim,
+                       row_ld, bias, split, split_ld, center, center_ld, rad, rad_ld, 0.f, 0, (int)n0, (int)in_dim,
                        steps, tol, w1, (float)beta2, w2, 1e-8f, tab, out);
   else
     hipLaunchKernelGGL(split_certificate_kernel<false>, dim3((unsigned)nodes), dim3(kCertThreads), lds, stream, rows,
-                       row_ld, bias, split, split_ld, center, center_ld, rad, rad_ld, eps, (int)n0, (int)in_dim,
-                       steps, tol, w1, (float)beta2, w2, 1e-8f, tab, out);
+                       row_ld, bias, split, split_ld, center, center_ld, rad, rad_ld, eps, norm_p, (int)n0,
+                       (int)in_dim, steps, tol, w1, (float)beta2, w2, 1e-8f, tab, out);
   BF_LAUNCH_CHECK("split_certificate_kernel");
   return BF_OK;
 }

@@ -1070,6 +1070,7 @@ int ibp_finalize(const float* c, const float* r, const float* rownorm, float eps
                  int64_t bias_div, const int8_t* split, int64_t split_ld, int64_t B, int64_t N, float* lo, float* hi,
                  int* infeasible, hipStream_t stream);
 int fill_value(float* p, int64_t n, float v, hipStream_t stream);
+int lp_seed_rows(float* h, int64_t M, int64_t I, const float* h_scale, int norm_p, hipStream_t stream);
 
 // conv2d of rows; with x2/y2 a second operand pair (abs_w2 for its weights) runs in
 // the same launch (blockIdx.y = 1), e.g. the center and the radius of an IBP layer.
@@ -1139,20 +1140,11 @@ int bf_conv2d_rows(const float* x, int64_t in_div, int64_t R, int Ci, int Hi, in
                        vec ? vec_div : 1, vec_ld, stream);
 }
 
-int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co, int Ho, int Wo, const float* W,
-                           int Ci, int KH, int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
-                           float* y_l, int64_t S, const float* wvec, int64_t w_ld, int norm_p, float* norm_u,
-                           float* norm_l, const float* h_scale, float* h_out, hipStream_t stream) {
-  BF_REQUIRE(R >= 0 && Co > 0 && Ci > 0 && KH > 0 && KW > 0 && sh > 0 && sw > 0 && Hi > 0 && Wi > 0 && S > 0,
-             "bf_conv_transpose_rows: bad sizes");
-  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (wvec == nullptr && h_out == nullptr)),
-             "bf_conv_transpose_rows: norm_p is 0, 1 or 2; 1 and 2 take no weights and no h_out");
-  if (R == 0) return BF_OK;
-  BF_REQUIRE(W && (A_u || A_l), "bf_conv_transpose_rows: null pointer");
-  BF_REQUIRE((A_u == nullptr) == (y_u == nullptr && norm_u == nullptr) && (A_l == nullptr) == (y_l == nullptr && norm_l == nullptr),
-             "bf_conv_transpose_rows: each given coefficient needs an output or a norm");
-  BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || norm_l != nullptr),
-             "bf_conv_transpose_rows: h_out needs h_scale and the lower norm");
+static int conv_transpose_rows_launch(const float* A_u, const float* A_l, int64_t R, int Co, int Ho, int Wo,
+                                      const float* W, int Ci, int KH, int KW, int sh, int sw, int ph, int pw, int Hi,
+                                      int Wi, float* y_u, float* y_l, int64_t S, const float* wvec, int64_t w_ld,
+                                      int norm_p, float* norm_u, float* norm_l, const float* h_scale, float* h_out,
+                                      hipStream_t stream) {
   const unsigned nz = (A_u && A_l) ? 2u : 1u;
   {
     SmallTArgs g;
@@ -1242,6 +1234,31 @@ int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co
                      h_out);
   BF_LAUNCH_CHECK("conv_transpose_rows_kernel");
   return BF_OK;
+}
+
+int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co, int Ho, int Wo, const float* W,
+                           int Ci, int KH, int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
+                           float* y_l, int64_t S, const float* wvec, int64_t w_ld, int norm_p, float* norm_u,
+                           float* norm_l, const float* h_scale, float* h_out, hipStream_t stream) {
+  BF_REQUIRE(R >= 0 && Co > 0 && Ci > 0 && KH > 0 && KW > 0 && sh > 0 && sw > 0 && Hi > 0 && Wi > 0 && S > 0,
+             "bf_conv_transpose_rows: bad sizes");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || wvec == nullptr),
+             "bf_conv_transpose_rows: norm_p is 0, 1 or 2; 1 and 2 take no weights");
+  if (R == 0) return BF_OK;
+  BF_REQUIRE(W && (A_u || A_l), "bf_conv_transpose_rows: null pointer");
+  BF_REQUIRE((A_u == nullptr) == (y_u == nullptr && norm_u == nullptr) && (A_l == nullptr) == (y_l == nullptr && norm_l == nullptr),
+             "bf_conv_transpose_rows: each given coefficient needs an output or a norm");
+  BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || norm_l != nullptr),
+             "bf_conv_transpose_rows: h_out needs h_scale and the lower norm");
+  if (norm_p == 0 || h_out == nullptr)
+    return conv_transpose_rows_launch(A_u, A_l, R, Co, Ho, Wo, W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S,
+                                      wvec, w_ld, norm_p, norm_u, norm_l, h_scale, h_out, stream);
+  // L1/L2 seeds need each row's whole norm: the lower rows are stored into h_out, then made into the seed
+  BF_REQUIRE(y_l == nullptr, "bf_conv_transpose_rows: with norm_p 1 or 2, h_out takes the place of y_l");
+  const int rc = conv_transpose_rows_launch(A_u, A_l, R, Co, Ho, Wo, W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u,
+                                            h_out, S, nullptr, 0, norm_p, norm_u, norm_l, nullptr, nullptr, stream);
+  if (rc) return rc;
+  return lp_seed_rows(h_out, R, (int64_t)Ci * Hi * Wi, h_scale, norm_p, stream);
 }
 
 int bf_conv_transpose_hwc_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
@@ -1363,8 +1380,8 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
              "bf_crown_relu_conv_transpose_concretize: each given coefficient needs its norm output");
   BF_REQUIRE((pre_lo == nullptr) == (pre_hi == nullptr),
              "bf_crown_relu_conv_transpose_concretize: pre_lo and pre_hi go together");
-  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (wvec == nullptr && h_out == nullptr)),
-             "bf_crown_relu_conv_transpose_concretize: norm_p is 0, 1 or 2; 1 and 2 take no weights and no h_out");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || wvec == nullptr),
+             "bf_crown_relu_conv_transpose_concretize: norm_p is 0, 1 or 2; 1 and 2 take no weights");
   BF_REQUIRE((h_out == nullptr) == (h_scale == nullptr) && (h_out == nullptr || norm_l != nullptr),
              "bf_crown_relu_conv_transpose_concretize: h_out needs h_scale and the lower norm");
   SmallTArgs g;
@@ -1401,8 +1418,11 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
   g.wv = wvec;
   g.w_ld = w_ld;
   g.nkind = norm_p;
-  g.h_scale = h_scale;
-  g.h_out = h_out;
+  // L1/L2 seeds need each row's whole norm: the lower rows go to h_out, made into the seed after the launch
+  const bool lp_seed = norm_p != 0 && h_out != nullptr;
+  if (lp_seed) g.y[A_u ? 1 : 0] = h_out;
+  g.h_scale = lp_seed ? nullptr : h_scale;
+  g.h_out = lp_seed ? nullptr : h_out;
   g.S = S;
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   g.vec = (g.npix % 16 == 0) && al16(A_u) && al16(A_l) && al16(pre_lo) && al16(pre_hi) && al16(alpha) &&
@@ -1414,6 +1434,7 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
   hipLaunchKernelGGL(conv_t_small_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream,
                      g, rx);
   BF_LAUNCH_CHECK("conv_t_small_kernel<relax>");
+  if (lp_seed) return lp_seed_rows(h_out, R, (int64_t)Ci * Hi * Wi, h_scale, norm_p, stream);
   return BF_OK;
 }
 

@@ -38,7 +38,8 @@ struct GemmArgs {
   const float* wvec;         // optional [D, N] weights (box radius), row stride w_ld
   int64_t w_ld;
   float* partial[2];         // [gridDim.y, M] partial row sums
-  const float* h_scale;      // optional [M]: lower pass also writes h = h_scale[m] * sign(C) * w  (gradient seed)
+  const float* h_scale;      // optional [M]: lower pass also writes h = h_scale[m] * sign(C) * w  (gradient seed;
+                             // with norm_kind 1 or 2 it writes C itself, turned into the seed afterwards)
   float* h_out;              // [M, N] row-major (ldh = N)
   int norm_kind;             // the row norm of C: 0 sum |C| (* w) (Linf ball, box); 1 max |C| (L1 ball);
                              // 2 sum C^2, the square root taken by the finalize (L2 ball)

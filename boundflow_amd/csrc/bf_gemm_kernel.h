@@ -721,9 +721,13 @@ gemm_kernel(GemmArgs p) {
           }
           s = nk == 1 ? fmaxf(s, v) : s + v;
           if (lower && p.h_out && row < M && col < N) {
-            const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
-            const float hs = p.h_scale[row];
-            p.h_out[row * N + col] = p.wvec ? hs * sg * wgt : hs * sg;
+            if (nk != 0) {
+              p.h_out[row * N + col] = a;   // the L1/L2 seeds need the whole row's norm: made from C afterwards
+            } else {
+              const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
+              const float hs = p.h_scale[row];
+              p.h_out[row * N + col] = p.wvec ? hs * sg * wgt : hs * sg;
+            }
           }
         }
         rs[i][r] = s;

@@ -93,6 +93,83 @@ __global__ void concretize_dense_grad_kernel(const float* __restrict__ A, int64_
   g[i] = G[m] * cen[e] + (G[m] * -w) * sg;
 }
 
+// The gradient of a row's L2 norm or of its max |.| (the dual norms of the L2 and
+// L1 balls, perturbation.py:126-133 and 209-214) as autograd forms it, scaled by
+// hs: hs * y / ||y||_2 (0 for a zero row, torch's norm backward), or
+// hs * sign(y_j) / count on the entries with |y_j| == max |y| (amax's backward
+// shares the gradient among ties).  One workgroup of 256 per row; the row is read
+// twice (reduce, then write).
+constexpr int kSeedThreads = 256;
+
+__device__ __forceinline__ float lp_row_reduce(const float* __restrict__ y, int64_t I, int nk, float* cnt_out) {
+  __shared__ float red[kSeedThreads / 64];
+  __shared__ float redc[kSeedThreads / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float s = 0.f;
+  for (int64_t j = threadIdx.x; j < I; j += kSeedThreads) {
+    const float v = y[j];
+    s = nk == 1 ? fmaxf(s, fabsf(v)) : s + v * v;
+  }
+  s = nk == 1 ? wave_max_nonneg(s) : wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  float t = red[0];
+  for (int q = 1; q < kSeedThreads / 64; ++q) t = nk == 1 ? fmaxf(t, red[q]) : t + red[q];
+  float c = 0.f;
+  if (nk == 1) {
+    for (int64_t j = threadIdx.x; j < I; j += kSeedThreads) c += fabsf(y[j]) == t ? 1.f : 0.f;
+    c = wave_sum(c);
+    if (lane == 0) redc[wave] = c;
+    __syncthreads();
+    c = redc[0];
+    for (int q = 1; q < kSeedThreads / 64; ++q) c += redc[q];
+  }
+  *cnt_out = c;
+  return nk == 1 ? t : sqrtf(t);
+}
+
+__device__ __forceinline__ float lp_seed_value(float v, float nrm, float cnt, float hs, int nk) {
+  if (nk == 2) return nrm > 0.f ? v * (hs / nrm) : 0.f;
+  const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
+  return fabsf(v) == nrm ? sg * (hs / cnt) : 0.f;
+}
+
+// h[m, :] holds y = the input layer's coefficient row; replaced in place by the
+// seed hs[m] * d norm(y) / dy.
+__global__ void __launch_bounds__(kSeedThreads)
+lp_seed_rows_kernel(float* __restrict__ h, int64_t I, const float* __restrict__ h_scale, int nk) {
+  const int64_t m = blockIdx.x;
+  float* y = h + m * I;
+  float cnt;
+  const float nrm = lp_row_reduce(y, I, nk, &cnt);
+  const float hs = h_scale[m];
+  for (int64_t j = threadIdx.x; j < I; j += kSeedThreads) y[j] = lp_seed_value(y[j], nrm, cnt, hs, nk);
+}
+
+// dL/dA of the dense concretization of the lower bound over an L2 or L1 ball:
+//   g[m, j] = G[m] * c[d, j] + seed with hs = G[m] * -eps.
+__global__ void __launch_bounds__(kSeedThreads)
+concretize_dense_grad_lp_kernel(const float* __restrict__ A, int64_t S, int64_t I, const float* __restrict__ cen,
+                                float eps, const float* __restrict__ G, float* __restrict__ g, int nk) {
+  const int64_t m = blockIdx.x;
+  const float* a = A + m * I;
+  const float* c = cen + (m / S) * I;
+  float cnt;
+  const float nrm = lp_row_reduce(a, I, nk, &cnt);
+  const float gm = G[m];
+  const float hs = gm * -eps;
+  for (int64_t j = threadIdx.x; j < I; j += kSeedThreads)
+    g[m * I + j] = gm * c[j] + lp_seed_value(a[j], nrm, cnt, hs, nk);
+}
+
+int lp_seed_rows(float* h, int64_t M, int64_t I, const float* h_scale, int norm_p, hipStream_t stream) {
+  if (M == 0) return BF_OK;
+  BF_REQUIRE(M < (1LL << 31), "lp_seed_rows: too many rows");
+  hipLaunchKernelGGL(lp_seed_rows_kernel, dim3((unsigned)M), dim3(kSeedThreads), 0, stream, h, I, h_scale, norm_p);
+  BF_LAUNCH_CHECK("lp_seed_rows_kernel");
+  return BF_OK;
+}
+
 // out[m, n] = (a[m, n] + b[m, n]) + r_row[m] * vec[(m / S) * v_ld + n], each term optional;
 // out may be a or b (elementwise, each element read before it is written).
 __global__ void rows_add_kernel(const float* a, const float* b, int64_t M, int64_t N, int64_t S,
@@ -376,10 +453,19 @@ int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t 
 }
 
 int bf_concretize_dense_grad(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
-                             float eps, const float* G, float* g, hipStream_t stream) {
+                             float eps, int norm_p, const float* G, float* g, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0 && I > 0, "bf_concretize_dense_grad: bad sizes");
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || rad == nullptr),
+             "bf_concretize_dense_grad: norm_p is 0, 1 or 2; the box radius goes with 0");
   if (D == 0) return BF_OK;
   BF_REQUIRE(A && center && G && g, "bf_concretize_dense_grad: null pointer");
+  if (norm_p != 0) {
+    BF_REQUIRE(D * S < (1LL << 31), "bf_concretize_dense_grad: too many rows");
+    hipLaunchKernelGGL(concretize_dense_grad_lp_kernel, dim3((unsigned)(D * S)), dim3(kSeedThreads), 0, stream, A, S,
+                       I, center, eps, G, g, norm_p);
+    BF_LAUNCH_CHECK("concretize_dense_grad_lp_kernel");
+    return BF_OK;
+  }
   const int64_t n = D * S * I;
   hipLaunchKernelGGL(concretize_dense_grad_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, A, D * S,
                      S, I, center, rad, eps, G, g);

@@ -40,6 +40,7 @@ int splitk_reduce(const float* part, int ks, int64_t M, int64_t N, float* C, int
                   const float* v_col, int64_t v_ld, int64_t S, hipStream_t stream);
 int relax_table(const float* lo, const float* hi, const float* alpha, int64_t alpha_ld, int64_t D, int64_t K,
                 float4* out, hipStream_t stream);
+int lp_seed_rows(float* h, int64_t M, int64_t I, const float* h_scale, int norm_p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // IBP helpers (center/radius form)
@@ -1039,9 +1040,9 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
                                     int norm_p, const float* b_u_in, const float* b_l_in, const float* h_scale,
                                     float* h_out, float* workspace, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && I > 0, "bf_crown_relu_linear_concretize: bad sizes");
-  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (rad == nullptr && h_out == nullptr)),
-             "bf_crown_relu_linear_concretize: norm_p %d (0 Linf/box, 1 L1, 2 L2; the box radius and the "
-             "gradient seed go with 0 only)", norm_p);
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || rad == nullptr),
+             "bf_crown_relu_linear_concretize: norm_p %d (0 Linf/box, 1 L1, 2 L2; the box radius goes with 0 only)",
+             norm_p);
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
   BF_REQUIRE(W && cvec && workspace, "bf_crown_relu_linear_concretize: null pointer");
@@ -1090,6 +1091,10 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
   a.norm_kind = norm_p;
   int rc = gemm_dispatch(a, PRO_RELAX, EPI_ABSSUM, nz, stream);
   if (rc) return rc;
+  if (h_out && norm_p != 0) {
+    rc = lp_seed_rows(h_out, M, I, h_scale, norm_p, stream);   // h_out holds the lower coefficient A'W
+    if (rc) return rc;
+  }
   return concretize_finalize(pu, pl, nparts, M, cu, cl, bu, bl, rad ? 1.0f : eps, norm_p, lb, ub, stream);
 }
 
@@ -1240,9 +1245,9 @@ int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dst
                                const float* h_scale, float* h_out, float* workspace, float* lb, float* ub,
                                hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0 && N > 0 && I > 0, "bf_crown_linear_concretize: bad sizes");
-  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || (rad == nullptr && h_out == nullptr)),
-             "bf_crown_linear_concretize: norm_p %d (0 Linf/box, 1 L1, 2 L2; the box radius and the gradient seed "
-             "go with 0 only)", norm_p);
+  BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || rad == nullptr),
+             "bf_crown_linear_concretize: norm_p %d (0 Linf/box, 1 L1, 2 L2; the box radius goes with 0 only)",
+             norm_p);
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
   BF_REQUIRE(W_t && workspace, "bf_crown_linear_concretize: null weight or workspace");
@@ -1279,6 +1284,10 @@ int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dst
   a.norm_kind = norm_p;
   int rc = gemm_dispatch(a, PRO_PLAIN, EPI_ABSSUM, nz, stream);
   if (rc) return rc;
+  if (h_out && norm_p != 0) {
+    rc = lp_seed_rows(h_out, M, I, h_scale, norm_p, stream);   // h_out holds the lower coefficient A W
+    if (rc) return rc;
+  }
   return concretize_finalize(A_u ? pu : nullptr, A_l ? pl : nullptr, nparts, M, cen_u, cen_l, b_u, b_l,
                              rad ? 1.0f : eps, norm_p, A_l ? lb : nullptr, A_u ? ub : nullptr, stream);
 }

@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from .crown import derived
-from .spec import BoxPerturbation, InputSpec, LpBallPerturbation, normalize_input_spec
+from .spec import BoxPerturbation, InputSpec, input_norm_p, normalize_input_spec
 
 
 def _pair(v) -> Tuple[int, int]:
@@ -120,12 +120,11 @@ def split_certificate(module, input_spec, relu_split_state: Dict[str, torch.Tens
         center = ((lo + hi) / 2.0).contiguous()
         rad = ((hi - lo) / 2.0).contiguous()
         eps = 0.0
-    elif isinstance(pert, LpBallPerturbation) and pert.normalized_p() == "inf":
+    else:
         center = spec.center.reshape(B, I).contiguous()
         rad = None
         eps = float(pert.eps)
-    else:
-        raise NotImplementedError("first-layer split certificate: Linf balls and boxes only")
+    norm_p = input_norm_p(pert)
 
     def split_rows(name: str, n: int) -> torch.Tensor:
         s = relu_split_state[name].to(device=dev, dtype=torch.int8)
@@ -151,7 +150,7 @@ def split_certificate(module, input_spec, relu_split_state: Dict[str, torch.Tens
         split = torch.cat([split_rows(nm, int(r.shape[0])) for nm, r, _b in sources], dim=1).contiguous()
         ld = n
     _lib.call("bf_split_certificate", _lib.ptr(rows), int(rows.stride(0)), _lib.ptr(bias), _lib.ptr(split), ld,
-              _lib.ptr(center), I, _lib.ptr(rad), I if rad is not None else 0, float(eps), B, n, I, int(steps),
+              _lib.ptr(center), I, _lib.ptr(rad), I if rad is not None else 0, float(eps), norm_p, B, n, I, int(steps),
               float(lr), float(tol), _lib.ptr(flags), _lib.stream_handle())
     return flags
 

@@ -127,8 +127,9 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
  * lb = (A' . cvec - eps * sum_i |(A' W)_i| * rad_i) + b, ub mirrored;
  * rad NULL = Lp ball (weights 1, eps used), else box radius [D, I] (eps ignored).
  * norm_p selects the dual norm of the ball's row term: 0 sum |.| (Linf ball or
- * box), 2 the L2 norm (L2 ball), 1 max |.| (L1 ball); 1 and 2 take no rad and
- * no h_out.
+ * box), 2 the L2 norm (L2 ball), 1 max |.| (L1 ball); 1 and 2 take no rad, and
+ * their gradient seed is h = h_scale[m] * d norm / d(A'W) (A'W / |A'W|_2, or
+ * sign / ties on the maxima of |A'W|), made after the row's norm is known.
  * cvec = center @ W^T per domain [D, N].  Replaces concretize_affine
  * (runtime/perturbation.py:175-222, 327-359) on RightMatmulLinearOperator
  * (runtime/linear_operator.py:503-586) as called at runtime/crown_ibp.py:2044-2051.
@@ -236,8 +237,10 @@ int bf_crown_relu_relax_lu(const float* A_u, const float* A_l, int64_t a_dstride
  * output rows are reduced to sum |y| (* wvec[d, e]) -- the concretization norm
  * of the input layer (linear_operator.py:1378-1452 + perturbation.py:175-222).
  * norm_p 2 reduces to sum y^2 (L2 ball), 1 to max |y| (L1 ball; Conv2dLinearOperator
- * row_l2_norm / row_abs_max, linear_operator.py:991-997), both without wvec and h_out;
- * bf_concretize_finalize with the same norm_p turns them into bounds. */
+ * row_l2_norm / row_abs_max, linear_operator.py:991-997), both without wvec;
+ * bf_concretize_finalize with the same norm_p turns them into bounds.  Their
+ * gradient seed h_out (y_l NULL) is h_scale[r] * d norm / dy, as for
+ * bf_crown_relu_linear_concretize. */
 int bf_conv_transpose_rows(const float* A_u, const float* A_l, int64_t R, int Co, int Ho, int Wo, const float* W,
                            int Ci, int KH, int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
                            float* y_l, int64_t S, const float* wvec, int64_t w_ld, int norm_p, float* norm_u,
@@ -360,10 +363,12 @@ int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t 
 
 /* dL/dA of the dense concretization of the lower bound (bf_concretize_dense, is_lower = 1):
  * g[m, j] = G[m] * center[d, j] + (G[m] * -w[d, j]) * sign(A[m, j]), w = eps (rad NULL) or rad [D, I];
+ * norm_p 2 / 1 (rad NULL): G[m] * center[d, j] - eps * G[m] * d|A[m]|_q / dA[m, j] with the L2 norm's
+ * A / |A|_2 (0 for a zero row) or max |A|'s sign(A) / ties on the maxima, as autograd forms them;
  * the autograd backward of concretize_affine (runtime/perturbation.py:175-222, 327-359) at the input of a
  * DAG task, driven by runtime/alpha_beta_crown.py:913-923. */
 int bf_concretize_dense_grad(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,
-                             float eps, const float* G, float* g, hipStream_t stream);
+                             float eps, int norm_p, const float* G, float* g, hipStream_t stream);
 
 /* out[m, n] = (a[m, n] + b[m, n]) + r_row[m] * vec[(m / S) * v_ld + n], every term optional (NULL), out may
  * alias a or b: the fan-in accumulation of backward states (runtime/crown_ibp.py:892-909, A_cur.add(A_upd))
@@ -450,15 +455,15 @@ int bf_branch_update_native(const float* lo, const float* hi, const int8_t* spli
  * (_is_infeasible_split_first_layer_convex_combo, runtime/alpha_beta_crown.py:391-532;
  * halfspaces as _collect_first_layer_split_halfspaces, :259-389).  Node g's halfspaces
  * are s * (rows[i] . x + bias[i]) >= 0 for its nonzero split[g * split_ld + i] (in i
- * order); the input set is the Linf ball (center row g, eps) or, with rad, the box
- * center +- rad.  Searches a convex combination w = softmax(z) by Adam on z (lr,
+ * order); the input set is the Lp ball (center row g, eps; norm_p 0 Linf, 2 L2,
+ * 1 L1) or, with rad, the box center +- rad (norm_p 0).  Searches a convex combination w = softmax(z) by Adam on z (lr,
  * betas 0.9/0.999, eps 1e-8, `steps` steps from z = 0) and sets out[g] = 1 at the
  * first step whose maximum over the set is below -tol, else 0; -1 when a node has
  * more than 1024 splits.  in_dim <= 16384, steps <= 256. */
 int bf_split_certificate(const float* rows, int64_t row_ld, const float* bias, const int8_t* split, int64_t split_ld,
                          const float* center, int64_t center_ld, const float* rad, int64_t rad_ld, float eps,
-                         int64_t nodes, int64_t n0, int64_t in_dim, int steps, double lr, double tol, int32_t* out,
-                         hipStream_t stream);
+                         int norm_p, int64_t nodes, int64_t n0, int64_t in_dim, int steps, double lr, double tol,
+                         int32_t* out, hipStream_t stream);
 
 /* Node verdict (runtime/bab.py:870-895): 1 certified (min_s lb >= threshold - tol),
  * 2 infeasible split, 0 open. */

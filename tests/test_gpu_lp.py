@@ -8,26 +8,37 @@ coefficient row); a first conv layer takes the ball's bounding box in the
 forward pass (crown_ibp.py:125-178).  Each path that concretizes is covered:
 the fused input region of an MLP, the relaxation-epilogue contraction, every
 intermediate bound, a CNN's fused input conv, the DAG backward, and the IBP
-task executor.  The oracle's L1/L2 arithmetic is pinned in
-tests/test_oracle_lp.py.
+task executor.  The alpha/beta reverse pass seeds the concretization's gradient with
+the dual norm's derivative (y / ||y||_2, or sign(y) on the maxima of |y|), checked
+against autograd through the oracle; alpha-CROWN, alpha-beta-CROWN with splits,
+the first-layer certificate and whole BaB searches run over the balls too.  The
+oracle's L1/L2 arithmetic is pinned in tests/test_oracle_lp.py and
+tests/test_oracle_certificate.py.
 """
 
 import pytest
 import torch
 
+from boundflow_amd import alpha_beta as hab
+from boundflow_amd import bab as hbab
 from boundflow_amd import crown as hc
 from boundflow_amd import task_executor as te
 from boundflow_amd import workloads as wl
 from boundflow_amd.spec import InputSpec, LpBallPerturbation
+from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
 from oracle import parity
 from oracle import task_ibp_ref as ti
 from tests.gpu_util import announce, assert_bounds_close, assert_parity, assert_verdicts, device
+from tests.test_gpu_conv_alpha import _grad_close, _oracle_grads
+from tests.test_gpu_crown_dag import _feasible_splits
+from tests.test_oracle_certificate import LP_KATS, first_layer_module, lp_spec
 
 pytestmark = pytest.mark.gpu
 
 # radii that leave a mix of stable and unstable ReLUs on the test networks
-EPS = {"mlp": {2: 0.5, 1: 1.5}, "cnn": {2: 0.02, 1: 0.03}, "dag": {2: 0.08, 1: 0.2}}
+EPS = {"mlp": {2: 0.3, 1: 1.0}, "cnn": {2: 0.02, 1: 0.03}, "dag": {2: 0.08, 1: 0.2}, "c5": {2: 0.1, 1: 0.5},
+       "c4": {2: 0.01, 1: 0.01}}
 
 
 def _lp(w, p, eps, C=None):
@@ -121,3 +132,164 @@ def test_task_executor_ibp_lp_matches_oracle(p):
     ref = ti.run_ibp(w.module, w.spec)
     assert_parity(out.lower, ref.lower, ref64.lower, f"IBP L{p} lower")
     assert_parity(out.upper, ref.upper, ref64.upper, f"IBP L{p} upper")
+
+
+def _grad_case(case, p):
+    g = torch.Generator().manual_seed(41 + p)
+    if case.startswith("mlp"):
+        w = _lp(wl.subset(wl.make_c5(depth=2, label_mode="predicted"), 12), p, EPS["c5"][p])
+    elif case == "cnn":
+        w = _lp(wl.subset(wl.make_c4(), 3), p, EPS["c4"][p])
+    else:
+        kind = {"dag": "residual_mlp", "dag_cnn": "channel_concat_cnn"}[case]
+        w = _lp(wl.make_dag(kind, seed=8, batch=3, eps=0.03, blocks=2), p, EPS["dag"][p])
+    beta_on = case in ("mlp", "mlp_epilogue", "dag")
+    splits = _feasible_splits(w, g) if beta_on else None
+    _env, pre = cr.forward_ibp_trace(w.module, w.spec, relu_split_state=splits)
+    alpha = {k: torch.rand(v.lower.shape, generator=g) for k, v in pre.items()}
+    beta = {k: torch.rand(v.lower.shape, generator=g) for k, v in pre.items()} if beta_on else None
+    return w, splits, alpha, beta
+
+
+@pytest.mark.parametrize("case", ["mlp", "mlp_epilogue", "cnn", "dag", "dag_cnn"])
+@pytest.mark.parametrize("p", [2, 1])
+def test_lp_lower_bound_gradients_match_autograd(case, p, monkeypatch):
+    """dL/dalpha and dL/dbeta for L = -sum_d mean_s lb over an L2 / L1 ball: the
+    chain's fused input region (and, with mlp_epilogue, the relaxation-epilogue path's
+    plain concretization), the CNN's fused input conv, and the DAG reverse pass."""
+    dev = device()
+    announce(f"L{p} alpha/beta gradient pass vs autograd: {case}")
+    if case == "mlp_epilogue":
+        monkeypatch.setattr(hc, "EPILOGUE_MIN_M", 0)
+    w, splits, alpha, beta = _grad_case(case, p)
+    ref32, ga32, gb32 = _oracle_grads(w, alpha, beta, splits)
+    ref64, ga64, gb64 = _oracle_grads(w, alpha, beta, splits, dtype=torch.float64)
+    wd = wl.to_device(w, dev)
+    sd = None if splits is None else {k: v.to(dev) for k, v in splits.items()}
+    bounds, ga, gb = hab.lower_bound_gradients(
+        wd.module, wd.spec, linear_spec_C=wd.C, relu_alpha={k: v.to(dev) for k, v in alpha.items()},
+        relu_beta=None if beta is None else {k: v.to(dev) for k, v in beta.items()}, relu_split_state=sd)
+    torch.cuda.synchronize()
+    assert_parity(bounds.lower, ref32.lower, ref64.lower, f"L{p} {case} lower")
+    assert set(ga.keys()) == set(ga32.keys())
+    for k in ga32:
+        _grad_close(ga[k], ga32[k], ga64[k], f"L{p} {case} dL/dalpha[{k}]")
+    if gb32 is not None:
+        for k in gb32:
+            _grad_close(gb[k], gb32[k], gb64[k], f"L{p} {case} dL/dbeta[{k}]")
+
+
+@pytest.mark.parametrize("net", ["c1", "dag"])
+@pytest.mark.parametrize("p", [2, 1])
+def test_lp_alpha_crown_matches_oracle(net, p):
+    """alpha-CROWN from the CROWN slopes, 10 Adam steps (the C4 recipe), over an L2 / L1
+    ball: bounds within 1e-4 of the oracle's trajectory, never looser than CROWN."""
+    dev = device()
+    announce(f"L{p} alpha-CROWN {net}, 10 steps")
+    if net == "c1":
+        w = _lp(wl.make_c1(batch=8), p, EPS["mlp"][p])
+    else:
+        w = _lp(wl.make_dag("residual_mlp", seed=9, batch=4, eps=0.03, blocks=2), p, EPS["dag"][p])
+    wd = wl.to_device(w, dev)
+    bounds, _alpha, _beta, _st = hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C,
+                                                                     steps=10, lr=0.1)
+    torch.cuda.synchronize()
+    _env, pre = cr.forward_ibp_trace(w.module, w.spec)
+    ref = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, steps=10, lr=0.1,
+                                  warm_start_alpha=ab.adaptive_alpha_init(pre), per_batch_params=True)[0]
+    crown = cr.run_crown_ibp(w.module, w.spec, linear_spec_C=w.C)
+    assert_bounds_close(bounds.lower, ref.lower, f"L{p} {net} alpha lower", rtol=1e-4, atol=1e-4)
+    assert_bounds_close(bounds.upper, ref.upper, f"L{p} {net} alpha upper", rtol=1e-4, atol=1e-4)
+    assert bool((bounds.lower.cpu() >= crown.lower - 1e-4 * crown.lower.abs() - 1e-4).all())
+
+
+@pytest.mark.parametrize("p", [2, 1])
+def test_lp_alpha_beta_crown_with_splits_matches_oracle(p):
+    dev = device()
+    announce(f"L{p} alpha-beta-CROWN residual_mlp with splits, 8 steps")
+    g = torch.Generator().manual_seed(33)
+    w = _lp(wl.make_dag("residual_mlp", seed=10, batch=4, eps=0.03, blocks=2), p, EPS["dag"][p])
+    splits = _feasible_splits(w, g)
+    wd = wl.to_device(w, dev)
+    bounds, _a, _b, _st = hab.run_alpha_beta_crown_mlp(
+        wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state={k: v.to(dev) for k, v in splits.items()},
+        steps=8, lr=0.2, per_batch_params=True)
+    torch.cuda.synchronize()
+    ref = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, relu_split_state=splits, steps=8, lr=0.2,
+                                  per_batch_params=True)[0]
+    assert_bounds_close(bounds.lower, ref.lower, f"L{p} alpha-beta lower", rtol=1e-4, atol=1e-4)
+    assert_bounds_close(bounds.upper, ref.upper, f"L{p} alpha-beta upper", rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("p", ["inf", 2, 1])
+@pytest.mark.parametrize("name", list(LP_KATS))
+def test_lp_certificate_known_answers(name, p):
+    """The first-layer certificate (bf_split_certificate) over Linf, L2 and L1 balls on the
+    geometric known answers, and run_alpha_beta_crown_mlp's infeasible result."""
+    from boundflow_amd.ir import BFTaskModule
+    from boundflow_amd.split_certificate import split_certificate
+    dev = device()
+    announce(f"split certificate L{p} KAT {name}")
+    W, b, s, expect = LP_KATS[name]
+    m = first_layer_module(torch.tensor(W), torch.tensor(b))
+    md = BFTaskModule(tasks=m.tasks, entry_task_id=m.entry_task_id,
+                      bindings={"params": {k: v.to(dev) for k, v in m.params.items()}})
+    spec = lp_spec(p, torch.zeros(1, 2, device=dev))
+    split = {"h1": torch.tensor([s], dtype=torch.int8, device=dev)}
+    flags = split_certificate(md, spec, split, {"h1": (len(b),)}).cpu().tolist()
+    ibp_closes = False
+    try:
+        cr.forward_ibp_trace(m, lp_spec(p, torch.zeros(1, 2)), relu_split_state={"h1": split["h1"].cpu()})
+    except ValueError:
+        ibp_closes = True
+    assert flags == [1 if expect[p] else 0] or ibp_closes
+    _bounds, _alpha, _beta, stats = hab.run_alpha_beta_crown_mlp(md, spec, relu_split_state=split, steps=0)
+    assert stats.feasibility == ("infeasible" if expect[p] else "unknown")
+
+
+@pytest.mark.parametrize("p", [2, 1])
+def test_lp_certificate_matches_oracle_on_c5_first_layer(p):
+    from tests.test_gpu_certificate import _random_nodes, _row_spec
+    from boundflow_amd.split_certificate import split_certificate
+    dev = device()
+    announce(f"split certificate vs oracle, C5 first layer, 48 nodes, L{p}")
+    g = torch.Generator().manual_seed(4 + p)
+    w = _lp(wl.make_c5(domains=48), p, {2: 0.5, 1: 2.0}[p])
+    name, rows = _random_nodes(w, g, 48, 12)
+    shapes = {n: (256,) for n in wl.relu_input_names(w.module)}
+    wd = wl.to_device(w, dev)
+    got = split_certificate(wd.module, wd.spec, {name: rows.to(dev)}, shapes).cpu().tolist()
+    ref = [int(ab.split_certificate(w.module, _row_spec(w.spec, r), {name: rows[r:r + 1]})[0]) for r in range(48)]
+    announce(f"  infeasible nodes: hip {sum(got)}, oracle {sum(ref)}")
+    assert got == ref
+
+
+BAB_LP = {
+    "alpha_beta_l2": (2, 0.1, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+    "alpha_l1": (1, 0.25, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10)),
+}
+
+
+@pytest.mark.parametrize("tag", list(BAB_LP))
+def test_lp_bab_search_matches_oracle(tag):
+    """solve_bab_mlp over an L2 / L1 ball: the whole search identical to the oracle's."""
+    from oracle import bab_ref
+    dev = device()
+    p, eps, kw = BAB_LP[tag]
+    announce(f"solve_bab_mlp {tag}")
+    base = wl.make_dag("residual_mlp", seed=12, batch=4, eps=0.03, n_in=8, hidden=12, n_out=4, blocks=1)
+    w = _lp(base, p, eps)
+    cfg = dict(use_branch_hint=True, alpha_lr=0.2, alpha_init=0.5, beta_init=0.0, threshold=0.0, tol=1e-6, **kw)
+    ref = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
+    wd = wl.to_device(w, dev)
+    r = hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C, config=hbab.BabConfig(**kw))
+    per = r.per_example
+    announce(f"  statuses {[q.status for q in per]} visited {[q.nodes_visited for q in per]} "
+             f"rounds {r.batch_rounds}; oracle {ref['per_status']} {ref['per_visited']}")
+    assert [q.status for q in per] == ref["per_status"]
+    assert [q.nodes_visited for q in per] == ref["per_visited"]
+    assert [q.nodes_evaluated for q in per] == ref["per_evaluated"]
+    assert [q.nodes_expanded for q in per] == ref["per_expanded"]
+    assert (r.max_queue, r.batch_rounds) == (ref["max_queue"], ref["batch_rounds"])
+    import numpy as np
+    np.testing.assert_allclose([q.best_lower for q in per], ref["per_best_lower"], rtol=1e-4, atol=1e-5)

@@ -120,3 +120,70 @@ def test_infeasible_verdicts_are_sound_against_an_lp():
             found += 1
             assert not feas, f"trial {trial}: certificate on a feasible set"
     assert found >= 1
+
+
+# Known answers over L2 and L1 balls of radius 1 at the origin, fixed by geometry:
+# x1 >= 0.6 and x2 >= 0.6 meet inside the Linf and L2 balls ((0.6, 0.6) has L2 norm
+# 0.85) but not inside the L1 ball (|x1| + |x2| >= 1.2); at 0.75 they miss the L2 ball
+# too (0.75 * sqrt(2) > 1).  Three unit normals at 0/120/240 degrees sum to zero, so
+# a_i . x >= 0.49 for all three has no point in any set (the reference's L2 case,
+# tests/test_phase6f_alpha_beta_crown_pr1.py:96-118); at -0.1 the origin satisfies all.
+_DIRS = [[1.0, 0.0], [-0.5, 0.8660254], [-0.5, -0.8660254]]
+LP_KATS = {
+    # name: (W, b, split, {p: infeasible})
+    "pair_0.6": ([[1.0, 0.0], [0.0, 1.0]], [-0.6, -0.6], [1, 1], {"inf": False, 2: False, 1: True}),
+    "pair_0.75": ([[1.0, 0.0], [0.0, 1.0]], [-0.75, -0.75], [1, 1], {"inf": False, 2: True, 1: True}),
+    "three_directions": (_DIRS, [-0.49] * 3, [1, 1, 1], {"inf": True, 2: True, 1: True}),
+    "three_directions_feasible": (_DIRS, [0.1] * 3, [1, 1, 1], {"inf": False, 2: False, 1: False}),
+    "single_1.2": ([[1.0, 1.0]], [-1.2], [1], {"inf": False, 2: False, 1: True}),
+    "single_1.5": ([[1.0, 1.0]], [-1.5], [1], {"inf": False, 2: True, 1: True}),
+}
+
+
+def lp_spec(p, center, eps=1.0):
+    from boundflow_amd.spec import LpBallPerturbation
+    return InputSpec(value_name="input", center=center, perturbation=LpBallPerturbation(p=p, eps=eps))
+
+
+@pytest.mark.parametrize("p", ["inf", 2, 1])
+@pytest.mark.parametrize("name", list(LP_KATS))
+def test_lp_ball_known_answers(name, p):
+    W, b, s, expect = LP_KATS[name]
+    m = first_layer_module(torch.tensor(W), torch.tensor(b))
+    spec = lp_spec(p, torch.zeros(1, 2))
+    split = {"h1": torch.tensor([s], dtype=torch.int8)}
+    assert ab.split_certificate(m, spec, split)[0] == expect[p]
+    out = ab.run_alpha_beta_crown(m, spec, linear_spec_C=None, relu_split_state=split, steps=0,
+                                  return_feasibility=True)
+    assert out[4] == ("infeasible" if expect[p] else "unknown")
+
+
+@pytest.mark.parametrize("p", [2, 1])
+def test_lp_ball_infeasible_verdicts_are_sound(p):
+    """No point of a dense sample of the ball satisfies every halfspace of a set the
+    certificate closes (the L1 ball's vertices and edges are in the sample)."""
+    g = torch.Generator().manual_seed(17 + p)
+    r = torch.linspace(0, 1, 81, dtype=torch.float64)
+    th = torch.linspace(0, 2 * torch.pi, 721, dtype=torch.float64)[:-1]
+    rr, tt = torch.meshgrid(r, th, indexing="ij")
+    u = torch.stack([torch.cos(tt), torch.sin(tt)], -1).reshape(-1, 2)
+    if p == 1:
+        u = u / u.abs().sum(-1, keepdim=True)
+    pts = rr.reshape(-1, 1) * u
+    found = 0
+    for trial in range(60):
+        k = int(torch.randint(2, 5, (1,), generator=g))
+        w = torch.randn(k, 2, generator=g)
+        b = torch.randn(k, generator=g) * 0.5 - 0.4
+        m = first_layer_module(w, b)
+        spec = lp_spec(p, torch.zeros(1, 2))
+        s = torch.ones(1, k, dtype=torch.int8)
+        try:
+            cr.forward_ibp_trace(m, spec, relu_split_state={"h1": s})
+        except ValueError:
+            continue
+        if ab.split_certificate(m, spec, {"h1": s})[0]:
+            found += 1
+            inside = ((pts @ w.double().t() + b.double()) >= 0).all(dim=1)
+            assert not bool(inside.any()), f"trial {trial}: certificate on a set with a point in the ball"
+    assert found >= 1

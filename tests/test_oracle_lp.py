@@ -10,6 +10,8 @@ Each check below evaluates the network at that point: a bound that is sound
 Samplers are restatements of tests/test_phase6b_crown_ibp_mlp.py:29-56.
 """
 
+import itertools
+
 import pytest
 import torch
 
@@ -162,3 +164,56 @@ def test_dual_norms_are_ordered():
     lo = {p: cr.concretize_matmul(_spec(p, x0, 0.1), x0, W, None)[0] for p in ("inf", 2, 1)}
     assert (lo[1] >= lo[2] - 1e-15).all() and (lo[2] >= lo["inf"] - 1e-15).all()
     assert not torch.equal(lo[1], lo[2]) and not torch.equal(lo[2], lo["inf"])
+
+
+@pytest.mark.parametrize("p", [2, 1])
+def test_concretize_gradient_matches_finite_differences(p):
+    """The gradient of the lower bound with respect to the coefficient (what the alpha/beta
+    reverse pass seeds): c - eps * A / ||A||_2 for L2, c - eps * sign(A_j) e_j at the
+    max |A_j| for L1, checked by central differences in fp64 away from ties."""
+    gen = torch.Generator().manual_seed(12)
+    B, K, I, eps = 2, 3, 7, 0.4
+    x0 = torch.randn(B, I, generator=gen, dtype=torch.float64)
+    A = torch.randn(B, K, I, generator=gen, dtype=torch.float64, requires_grad=True)
+    lb, _ub = cr.concretize_affine(_spec(p, x0, eps), x0, cr.DenseOp(A, (I,)), torch.zeros(B, K, dtype=torch.float64))
+    (g,) = torch.autograd.grad(lb.sum(), A)
+    h = 1e-6
+    fd = torch.zeros_like(A)
+    with torch.no_grad():
+        for idx in itertools.product(range(B), range(K), range(I)):
+            Ap, Am = A.detach().clone(), A.detach().clone()
+            Ap[idx] += h
+            Am[idx] -= h
+            lp = cr.concretize_affine(_spec(p, x0, eps), x0, cr.DenseOp(Ap, (I,)), 0.0)[0][idx[0], idx[1]]
+            lm = cr.concretize_affine(_spec(p, x0, eps), x0, cr.DenseOp(Am, (I,)), 0.0)[0][idx[0], idx[1]]
+            fd[idx] = (lp - lm) / (2 * h)
+    assert torch.allclose(g, fd, rtol=0, atol=1e-6)
+    a = A.detach()
+    if p == 2:
+        expect = x0.unsqueeze(1) - eps * a / torch.linalg.vector_norm(a, dim=2, keepdim=True)
+    else:
+        onehot = (a.abs() == a.abs().amax(dim=2, keepdim=True)).to(a.dtype)
+        expect = x0.unsqueeze(1) - eps * torch.sign(a) * onehot
+    assert torch.allclose(g, expect, rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("p", [2, 1])
+def test_alpha_crown_sound_and_not_looser_than_crown(p):
+    """alpha-CROWN (20 Adam steps from the CROWN slopes) over an L2 / L1 ball: no sampled
+    output falls below its lower bound, which is at least CROWN's."""
+    from oracle import alpha_beta_ref as ab
+    torch.manual_seed(0)
+    B, I, H, O, eps = 2, 24, 16, 6, 0.5 if p == 2 else 0.6
+    x0 = torch.randn(B, I)
+    w1, b1 = torch.randn(H, I), torch.randn(H)
+    w2, b2 = torch.randn(O, H), torch.randn(O)
+    mod, spec = _mlp(w1, b1, w2, b2), _spec(p, x0, eps)
+    crown = cr.run_crown_ibp(mod, spec)
+    _env, pre = cr.forward_ibp_trace(mod, spec)
+    out = ab.run_alpha_beta_crown(mod, spec, linear_spec_C=None, steps=20, lr=0.1,
+                                  warm_start_alpha=ab.adaptive_alpha_init(pre), per_batch_params=True)[0]
+    xs = _sample(p, x0, eps, 256, torch.Generator().manual_seed(3))
+    ys = torch.relu(xs.matmul(w1.t()) + b1).matmul(w2.t()) + b2
+    assert (ys >= out.lower.unsqueeze(0) - 1e-5).all()
+    assert (out.lower >= crown.lower - 1e-5).all()
+    assert (out.lower > crown.lower + 1e-4).any()
