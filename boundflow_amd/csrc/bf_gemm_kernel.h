@@ -697,72 +697,76 @@ gemm_kernel(GemmArgs p) {
       }
   } else if constexpr (EPI == EPI_ABSSUM) {
     static_assert(GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
-    // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order (norm_kind 0);
-    // max_n |C[m, n]| (1) or sum_n C[m, n]^2 (2) for the L1 and L2 balls.
-    float rs[FM][16];
+    // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order (norm kind 0);
+    // max_n |C[m, n]| (1) or sum_n C[m, n]^2 (2) for the L1 and L2 balls.  The kind
+    // is uniform over the launch: one specialisation of the epilogue per kind.
     const bool fits32 = M < (1LL << 31);
-    const int nk = p.norm_kind;   // uniform
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int64_t d = (p.wvec && row < M) ? div_rows(row, p.S, fits32) : 0;
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
-          const float a = acc[i][j][r];
-          float v = col < N ? (nk == 2 ? a * a : fabsf(a)) : 0.f;   // columns past N hold products no one keeps
-          float wgt = 1.f;
-          if (p.wvec) {
-            wgt = (row < M && col < N) ? p.wvec[d * p.w_ld + col] : 0.f;
-            v = v * wgt;
-          }
-          s = nk == 1 ? fmaxf(s, v) : s + v;
-          if (lower && p.h_out && row < M && col < N) {
-            if (nk != 0) {
-              p.h_out[row * N + col] = a;   // the L1/L2 seeds need the whole row's norm: made from C afterwards
-            } else {
-              const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
-              const float hs = p.h_scale[row];
-              p.h_out[row * N + col] = p.wvec ? hs * sg * wgt : hs * sg;
-            }
-          }
-        }
-        rs[i][r] = s;
-      }
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float s = rs[i][r];
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) {
-          const float o = __shfl_xor(s, off, 64);
-          s = nk == 1 ? fmaxf(s, o) : s + o;
-        }
-        rs[i][r] = s;
-      }
-    if (lrow == 0) {
+    auto norm_epilogue = [&](auto kind) {
+      constexpr int NK = decltype(kind)::value;
+      auto join = [](float a, float b) { return NK == 1 ? fmaxf(a, b) : a + b; };
+      float rs[FM][16];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          red[wn][rloc] = rs[i][r];
-        }
-    }
-    __syncthreads();
-    for (int rr = t; rr < GBM; rr += GNT) {
-      const int64_t row = m0 + rr;
-      if (row < M) {
-        float s = 0.f;
+          const int64_t row = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int64_t d = (p.wvec && row < M) ? div_rows(row, p.S, fits32) : 0;
+          float s = 0.f;
 #pragma unroll
-        for (int q = 0; q < T::NWN; ++q) s = nk == 1 ? fmaxf(s, red[q][rr]) : s + red[q][rr];
-        p.partial[z][tile_n * M + row] = s;
+          for (int j = 0; j < FN; ++j) {
+            const int64_t col = n0 + wn * T::WTN + j * 32 + lrow;
+            const float a = acc[i][j][r];
+            float v = col < N ? (NK == 2 ? a * a : fabsf(a)) : 0.f;   // columns past N hold products no one keeps
+            float wgt = 1.f;
+            if (NK == 0 && p.wvec) {
+              wgt = (row < M && col < N) ? p.wvec[d * p.w_ld + col] : 0.f;
+              v = v * wgt;
+            }
+            s = join(s, v);
+            if (lower && p.h_out && row < M && col < N) {
+              if (NK != 0) {
+                p.h_out[row * N + col] = a;   // the L1/L2 seeds need the whole row's norm: made from C afterwards
+              } else {
+                const float sg = (a > 0.f) ? 1.f : ((a < 0.f) ? -1.f : 0.f);
+                const float hs = p.h_scale[row];
+                p.h_out[row * N + col] = p.wvec ? hs * sg * wgt : hs * sg;
+              }
+            }
+          }
+          rs[i][r] = s;
+        }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float s = rs[i][r];
+#pragma unroll
+          for (int off = 16; off >= 1; off >>= 1) s = join(s, __shfl_xor(s, off, 64));
+          rs[i][r] = s;
+        }
+      if (lrow == 0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            red[wn][rloc] = rs[i][r];
+          }
       }
-    }
+      __syncthreads();
+      for (int rr = t; rr < GBM; rr += GNT) {
+        const int64_t row = m0 + rr;
+        if (row < M) {
+          float s = 0.f;
+#pragma unroll
+          for (int q = 0; q < T::NWN; ++q) s = join(s, red[q][rr]);
+          p.partial[z][tile_n * M + row] = s;
+        }
+      }
+    };
+    if (p.norm_kind == 0) norm_epilogue(std::integral_constant<int, 0>{});
+    else if (p.norm_kind == 1) norm_epilogue(std::integral_constant<int, 1>{});
+    else norm_epilogue(std::integral_constant<int, 2>{});
   } else {
     // Relaxation of the next ReLU (crown_ibp.py:1261-1296) applied to C before
     // it is stored, so the next contraction reads A' directly; every coefficient
