@@ -747,6 +747,88 @@ def run_crown_ibp_mlp_from_forward_trace(
                           relu_pre_add_coeff_l=relu_pre_add_coeff_l)
 
 
+def run_crown_ibp_mlp_with_relu_influence_from_forward_trace(
+    module: BFTaskModule,
+    input_spec,
+    *,
+    interval_env: Dict[str, IntervalState],
+    relu_pre: Dict[str, IntervalState],
+    linear_spec_C: torch.Tensor,
+    output_value: Optional[str] = None,
+) -> Tuple[IntervalState, Dict[str, torch.Tensor]]:
+    """Bounds of the objective C and each ReLU's objective influence (crown_ibp.py:2201-2241):
+    for every ReLU input x, max over the spec rows of max(|A_u|, |A_l|) of the backward
+    coefficient of the ReLU's output, [B, *shape of x].  The backward runs on dense rows
+    (``crown_dag``) from the given boxes; one INTERVAL_IBP task, as in the reference."""
+    from .crown_dag import DagTrace, crown_backward_dag, value_shapes
+    module.validate()
+    task = module.get_entry_task()
+    if task.kind != TaskKind.INTERVAL_IBP:
+        raise NotImplementedError("ReLU influence extraction only supports INTERVAL_IBP tasks")
+    if module.task_graph is not None or len(module.tasks) != 1:
+        raise NotImplementedError("ReLU influence extraction currently supports one task only")
+    spec = normalize_input_spec(input_spec)
+    shapes, _relu_shapes = value_shapes(module, spec)
+    trace = DagTrace(interval_env=dict(interval_env), relu_pre=dict(relu_pre), shapes=shapes)
+    influence: Dict[str, torch.Tensor] = {}
+    bounds = crown_backward_dag(module, spec, trace, linear_spec_C=linear_spec_C, output_value=output_value,
+                                relu_influence=influence)
+    if set(influence) != set(relu_pre):
+        raise ValueError("ReLU objective influence coverage differs")
+    return bounds, {name: influence[name] for name in relu_pre}
+
+
+@dataclass
+class CrownIbpStats:
+    """Whether ``run_crown_ibp_mlp`` takes a module (crown_ibp.py:63-67)."""
+    supported: bool
+    reason: str = ""
+    ops_seen: Tuple[str, ...] = ()
+
+
+def get_crown_ibp_mlp_stats(module: BFTaskModule) -> CrownIbpStats:
+    """The support check of crown_ibp.py:2279-2350 for this path: one INTERVAL_IBP task of
+    linear / relu / conv2d / flatten / reshape / add / concat ops (chains and DAGs), with
+    single outputs, flatten over (1, -1), two-operand adds, concats of two or more
+    operands on the feature or channel axis, and conv2d with groups 1 and dilation 1.
+    Never raises: what fails validation is reported as unsupported with the reason."""
+    from .crown_dag import DAG_OPS
+    try:
+        module.validate()
+        task = module.get_entry_task()
+        if task.kind != TaskKind.INTERVAL_IBP:
+            return CrownIbpStats(False, f"TaskKind={task.kind}")
+        if module.task_graph is not None or len(module.tasks) != 1:
+            return CrownIbpStats(False, "multi-task module not supported")
+        ops = tuple(op.op_type for op in task.ops)
+        if not ops:
+            return CrownIbpStats(False, "empty task", ops)
+        bad = [t for t in ops if t not in DAG_OPS]
+        if bad:
+            return CrownIbpStats(False, f"unsupported ops: {bad}", ops)
+        for i, op in enumerate(task.ops):
+            t = op.op_type
+            if len(op.outputs) != 1:
+                return CrownIbpStats(False, f"multi-output op not supported at op {i}: outputs={op.outputs}", ops)
+            if t == "flatten" and (int(op.attrs.get("start_dim", 1)), int(op.attrs.get("end_dim", -1))) != (1, -1):
+                return CrownIbpStats(False, f"unsupported flatten attrs at op {i}: {op.attrs}", ops)
+            if t == "add" and len(op.inputs) != 2:
+                return CrownIbpStats(False, f"add expects 2 inputs at op {i}, got {len(op.inputs)}", ops)
+            if t == "concat":
+                if len(op.inputs) < 2:
+                    return CrownIbpStats(False, f"concat expects at least 2 inputs at op {i}, got {len(op.inputs)}",
+                                         ops)
+                if int(op.attrs.get("axis", 1)) not in (1, -1):
+                    return CrownIbpStats(False, f"unsupported concat axis at op {i}: {op.attrs.get('axis', 1)}", ops)
+            if t == "conv2d":
+                dilation = _pair(op.attrs.get("dilation", 1))
+                if int(op.attrs.get("groups", 1)) != 1 or dilation != (1, 1):
+                    return CrownIbpStats(False, f"conv2d with groups or dilation != 1 at op {i}", ops)
+        return CrownIbpStats(True, "", ops)
+    except Exception as e:   # validation errors are the answer, not a failure of the check
+        return CrownIbpStats(False, str(e))
+
+
 def run_crown_all_intermediate(module: BFTaskModule, input_spec, *, linear_spec_C: torch.Tensor):
     """Every intermediate pre-activation bound by CROWN (C = I per layer),
     intersected with the IBP bound, then the final spec bound; the composition of

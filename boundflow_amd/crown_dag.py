@@ -120,6 +120,12 @@ def _module_task(module: BFTaskModule):
 def relu_input_shapes(module: BFTaskModule, spec: InputSpec) -> Dict[str, Tuple[int, ...]]:
     """Per-sample shape of every ReLU input, in op order (the order of a trace's relu_pre),
     from the ops' shape rules alone (no launch)."""
+    return value_shapes(module, spec)[1]
+
+
+def value_shapes(module: BFTaskModule, spec: InputSpec):
+    """Per-sample shapes of every value the ops compute (and the input), and of every
+    ReLU input in op order, from the ops' shape rules alone (no launch)."""
     task = _module_task(module)
     params = module.params
     shapes: Dict[str, Tuple[int, ...]] = {spec.value_name: tuple(int(d) for d in spec.center.shape[1:])}
@@ -148,7 +154,7 @@ def relu_input_shapes(module: BFTaskModule, spec: InputSpec) -> Dict[str, Tuple[
         else:
             y = tuple(int(d) for d in op.attrs["shape"][1:])
         shapes[op.outputs[0]] = y
-    return out
+    return shapes, out
 
 
 def forward_ibp_trace_dag(
@@ -326,11 +332,14 @@ def crown_backward_dag(
     need_upper: bool = True,
     need_lower: bool = True,
     save: Optional[dict] = None,
+    relu_influence: Optional[Dict[str, torch.Tensor]] = None,
 ) -> IntervalState:
     """The general backward of crown_ibp.py:1669-2051 on dense coefficient rows.  A bound
     that is not needed is not computed (its side of the result is None).  With ``save``
     (lower bound only) the coefficient entering every ReLU and the input's coefficient are
-    kept for ``lower_grad_pass``."""
+    kept for ``lower_grad_pass``.  With ``relu_influence`` each ReLU input x reached by the
+    backward gets max over specs of max(|A_u|, |A_l|) of the coefficient of the ReLU's
+    output, [B, *shape of x] (crown_ibp.py:1810-1833)."""
     from .crown import _flat_param, _init_spec, transposed
 
     task = _module_task(module)
@@ -484,6 +493,12 @@ def crown_backward_dag(
                 alpha, alpha_ld = _flat_param(relu_alpha[x], B, n, f"relu_alpha[{x}]")
             if relu_pre_add_coeff_l is not None and x in relu_pre_add_coeff_l:
                 add, add_ld = _flat_param(relu_pre_add_coeff_l[x], B, n, f"relu_pre_add_coeff_l[{x}]")
+            if relu_influence is not None:
+                if x in relu_influence:
+                    raise ValueError(f"duplicate ReLU objective influence identity: {x}")
+                infl = torch.empty((B,) + tuple(pre.lower.shape[1:]), device=dev, dtype=torch.float32)
+                _lib.call("bf_rows_abs_max", _lib.ptr(st.A_u), _lib.ptr(st.A_l), B, S, n, _lib.ptr(infl), stream)
+                relu_influence[x] = infl
             if save is not None:
                 save["relu_A"][op_index] = st.A_l      # the coefficient before the relaxation
             new, _ = rows_pass(st, n, pre=pre, alpha=alpha, alpha_ld=alpha_ld, add=add, add_ld=add_ld)

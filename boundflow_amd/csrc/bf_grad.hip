@@ -170,6 +170,22 @@ int lp_seed_rows(float* h, int64_t M, int64_t I, const float* h_scale, int norm_
   return BF_OK;
 }
 
+// out[d, n] = max over the S rows of domain d of max(|A_u[m, n]|, |A_l[m, n]|) (either
+// may be NULL): the objective influence of a ReLU, crown_ibp.py:1810-1833.
+__global__ void rows_abs_max_kernel(const float* __restrict__ A_u, const float* __restrict__ A_l, int64_t D,
+                                    int64_t S, int64_t N, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D * N) return;
+  const int64_t d = i / N, n = i - d * N;
+  float v = 0.f;
+  for (int64_t s = 0; s < S; ++s) {
+    const int64_t e = (d * S + s) * N + n;
+    if (A_u) v = fmaxf(v, fabsf(A_u[e]));
+    if (A_l) v = fmaxf(v, fabsf(A_l[e]));
+  }
+  out[i] = v;
+}
+
 // out[m, n] = (a[m, n] + b[m, n]) + r_row[m] * vec[(m / S) * v_ld + n], each term optional;
 // out may be a or b (elementwise, each element read before it is written).
 __global__ void rows_add_kernel(const float* a, const float* b, int64_t M, int64_t N, int64_t S,
@@ -449,6 +465,17 @@ int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t 
   hipLaunchKernelGGL(relu_grad_kernel, dim3((unsigned)ceil_div(D * N, 256)), dim3(256), 0, stream, g_out, A,
                      a_dstride, D, S, N, pre_lo, pre_hi, alpha, alpha_ld, G, split, split_ld, g_in, g_alpha, g_beta);
   BF_LAUNCH_CHECK("relu_grad_kernel");
+  return BF_OK;
+}
+
+int bf_rows_abs_max(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t N, float* out,
+                    hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && N > 0, "bf_rows_abs_max: bad sizes");
+  if (D == 0) return BF_OK;
+  BF_REQUIRE((A_u || A_l) && out, "bf_rows_abs_max: null pointer");
+  hipLaunchKernelGGL(rows_abs_max_kernel, dim3((unsigned)ceil_div(D * N, 256)), dim3(256), 0, stream, A_u, A_l, D, S,
+                     N, out);
+  BF_LAUNCH_CHECK("rows_abs_max_kernel");
   return BF_OK;
 }
 

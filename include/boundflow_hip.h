@@ -361,6 +361,14 @@ int bf_relu_grad(const float* g_out, const float* A, int64_t a_dstride, int64_t 
                  const int8_t* split, int64_t split_ld, float* g_in, float* g_alpha, float* g_beta,
                  hipStream_t stream);
 
+/* out[d, n] = max over the S rows of domain d of max(|A_u[d*S+s, n]|, |A_l[d*S+s, n]|)
+ * for the dense coefficient rows [D*S, N] of the two bounds (either may be NULL):
+ * the per-ReLU objective influence of
+ * run_crown_ibp_mlp_with_relu_influence_from_forward_trace (runtime/crown_ibp.py:1810-1833,
+ * 2201-2241). */
+int bf_rows_abs_max(const float* A_u, const float* A_l, int64_t D, int64_t S, int64_t N, float* out,
+                    hipStream_t stream);
+
 /* dL/dA of the dense concretization of the lower bound (bf_concretize_dense, is_lower = 1):
  * g[m, j] = G[m] * center[d, j] + (G[m] * -w[d, j]) * sign(A[m, j]), w = eps (rad NULL) or rad [D, I];
  * norm_p 2 / 1 (rad NULL): G[m] * center[d, j] - eps * G[m] * d|A[m]|_q / dA[m, j] with the L2 norm's

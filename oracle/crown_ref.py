@@ -724,6 +724,7 @@ def crown_backward_from_trace(
     relu_alpha: Optional[Dict[str, torch.Tensor]] = None,
     relu_pre_add_coeff_u: Optional[Dict[str, torch.Tensor]] = None,
     relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
+    relu_influence_out: Optional[Dict[str, torch.Tensor]] = None,
 ) -> IntervalState:
     """crown_ibp.py:1669-2051: ops in reverse order, each popping the backward state of its
     output; a value read by several ops accumulates their contributions (crown_ibp.py:892-909)
@@ -796,6 +797,13 @@ def crown_backward_from_trace(
             name = op.inputs[0]
             pre = relu_pre[name]
             in_shape = tuple(int(d) for d in pre.lower.shape[1:])
+            if relu_influence_out is not None:
+                # crown_ibp.py:1810-1833: max over specs of the coefficient magnitudes at the ReLU
+                if name in relu_influence_out:
+                    raise ValueError(f"duplicate ReLU objective influence identity: {name}")
+                cu = st.A_u.to_dense().reshape(batch, -1, *in_shape)
+                cl = st.A_l.to_dense().reshape(batch, -1, *in_shape)
+                relu_influence_out[name] = torch.maximum(cu.abs().amax(dim=1), cl.abs().amax(dim=1)).detach()
             dA_u, dA_l, b_u, b_l = relu_backward_dense(
                 st.A_u.to_dense(), st.A_l.to_dense(), st.b_u, st.b_l, pre=pre, name=name,
                 relu_alpha=relu_alpha, add_u=relu_pre_add_coeff_u, add_l=relu_pre_add_coeff_l,

@@ -288,3 +288,37 @@ def test_dag_bab_search_matches_oracle(tag):
     import numpy as np
     np.testing.assert_allclose([p.best_lower for p in per], ref["per_best_lower"], rtol=1e-4, atol=1e-5)
     np.testing.assert_allclose([p.best_upper for p in per], ref["per_best_upper"], rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("net", ["c1", "c3", "residual_mlp", "channel_concat_cnn"])
+def test_relu_influence_matches_oracle(net):
+    """run_crown_ibp_mlp_with_relu_influence_from_forward_trace (crown_ibp.py:2201-2241): the
+    objective bounds at the contract and each ReLU's influence (max over specs of the
+    coefficient magnitudes, bf_rows_abs_max) within the rounding of the coefficients."""
+    dev = device()
+    announce(f"ReLU objective influence {net}")
+    if net == "c1":
+        w = wl.make_c1(batch=8)
+    elif net == "c3":
+        w = wl.make_c3(batch=4)
+    else:
+        w = wl.make_dag(net, seed=5, batch=3, eps=0.03, blocks=2)
+    wd = wl.to_device(w, dev)
+    tr = hc.forward_ibp_trace(wd.module, wd.spec)
+    got, infl = hc.run_crown_ibp_mlp_with_relu_influence_from_forward_trace(
+        wd.module, wd.spec, interval_env=tr.interval_env, relu_pre=tr.relu_pre, linear_spec_C=wd.C)
+    torch.cuda.synchronize()
+    env, pre = cr.forward_ibp_trace(w.module, w.spec)
+    ref_infl = {}
+    ref = cr.crown_backward_from_trace(w.module, w.spec, interval_env=env, relu_pre=pre, linear_spec_C=w.C,
+                                       relu_influence_out=ref_infl)
+    w64 = parity.to_float64(w)
+    env64, pre64 = cr.forward_ibp_trace(w64.module, w64.spec)
+    ref64 = cr.crown_backward_from_trace(w64.module, w64.spec, interval_env=env64, relu_pre=pre64,
+                                         linear_spec_C=w64.C)
+    assert_parity(got.lower, ref.lower, ref64.lower, f"{net} lower")
+    assert_parity(got.upper, ref.upper, ref64.upper, f"{net} upper")
+    assert list(infl) == list(pre) and set(ref_infl) == set(pre)   # in relu_pre order, as the reference returns it
+    for k in ref_infl:
+        scale = float(ref_infl[k].abs().max())
+        assert_bounds_close(infl[k], ref_infl[k], f"{net} influence[{k}]", rtol=1e-5, atol=1e-6 * scale)

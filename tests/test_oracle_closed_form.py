@@ -164,3 +164,25 @@ def test_split_application_and_infeasibility():
         pass
     else:
         raise AssertionError("active split on a stably inactive neuron must be infeasible")
+
+
+def test_relu_influence_closed_form():
+    """crown_ibp.py:1810-1833: the influence of the last ReLU is max over specs of |C W2| (both
+    bounds carry C W2 there); every ReLU is covered once, with its input's shape."""
+    g = torch.Generator().manual_seed(8)
+    w1, b1 = torch.randn(6, 4, generator=g, dtype=torch.float64), torch.randn(6, generator=g, dtype=torch.float64)
+    w2, b2 = torch.randn(3, 6, generator=g, dtype=torch.float64), torch.randn(3, generator=g, dtype=torch.float64)
+    m = _mlp(w1, b1, w2, b2)
+    x0 = torch.randn(2, 4, generator=g, dtype=torch.float64)
+    spec = InputSpec.linf(value_name="input", center=x0, eps=0.3)
+    C = torch.randn(2, 5, 3, generator=g, dtype=torch.float64)
+    env, pre = cr.forward_ibp_trace(m, spec)
+    infl = {}
+    out = cr.crown_backward_from_trace(m, spec, interval_env=env, relu_pre=pre, linear_spec_C=C,
+                                       relu_influence_out=infl)
+    assert set(infl) == {"h1"} and tuple(infl["h1"].shape) == (2, 6)
+    expect = (C @ w2).abs().amax(dim=1)
+    assert torch.allclose(infl["h1"], expect, rtol=0, atol=1e-12)
+    # the bounds are those of the plain backward
+    ref = cr.crown_backward_from_trace(m, spec, interval_env=env, relu_pre=pre, linear_spec_C=C)
+    assert torch.equal(out.lower, ref.lower) and torch.equal(out.upper, ref.upper)
