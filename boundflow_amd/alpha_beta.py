@@ -25,7 +25,7 @@ the gradient of every lower bound row is -1/S or -1/(D*S).
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Dict, List, Optional, Tuple
+from typing import Any, Dict, List, Optional, Tuple
 
 import numpy as np
 import torch
@@ -47,6 +47,41 @@ from .profiling import launch as _timed
 from .spec import InputSpec, IntervalState, normalize_input_spec
 
 
+class AlphaState(dict):
+    """Alpha per ReLU input (alpha_crown.py:25-30): a dict of ReLU input name to the
+    slopes, which ``alpha_by_relu_input`` also returns, so the reference's and this
+    package's callers read it alike."""
+
+    @property
+    def alpha_by_relu_input(self) -> Dict[str, torch.Tensor]:
+        return self
+
+    def detach_clone(self) -> "AlphaState":
+        return AlphaState({k: v.detach().clone() for k, v in self.items()})
+
+
+class BetaState(dict):
+    """Beta per ReLU input (alpha_beta_crown.py:29-42), as AlphaState."""
+
+    @property
+    def beta_by_relu_input(self) -> Dict[str, torch.Tensor]:
+        return self
+
+    def detach_clone(self) -> "BetaState":
+        return BetaState({k: v.detach().clone() for k, v in self.items()})
+
+
+def _as_param_dict(warm, attr: str) -> Optional[Dict[str, torch.Tensor]]:
+    """A warm start given as the reference's state object or as a plain dict."""
+    if warm is None:
+        return None
+    return getattr(warm, attr, warm)
+
+
+def _certificate_record(value: torch.Tensor) -> Dict[str, Any]:
+    return {"type": "convex_combo_max_negative", "max_value": float(value[0].item())}
+
+
 @dataclass
 class AlphaBetaStats:
     """Run statistics.  The branching decision stays on the device
@@ -58,6 +93,9 @@ class AlphaBetaStats:
     feasibility: str = "unknown"
     reason: str = "ok"
     infeasible: Optional[torch.Tensor] = None
+    # set when the first-layer certificate closed the query: {"type", "max_value"} as the
+    # reference reports (alpha_beta_crown.py:484-531; its weights and halfspaces stay on the device)
+    infeasible_certificate: Optional[Dict[str, Any]] = None
     steps: int = 0
     lr: float = 0.0
     branch_layer: Optional[torch.Tensor] = None
@@ -296,13 +334,15 @@ def run_alpha_beta_crown_mlp(
             and any(bool((v != 0).any().item()) for v in relu_split_state.values() if v is not None)):
         from .split_certificate import check_flags, split_certificate
         shapes0 = _relu_shapes(module, spec, chain)
-        flag = split_certificate(module, spec, relu_split_state, shapes0).cpu().tolist()
+        value = torch.empty(1, device=spec.center.device, dtype=torch.float32)
+        flag = split_certificate(module, spec, relu_split_state, shapes0, max_out=value).cpu().tolist()
         check_flags(flag)
         if flag[0] == 1:
             zeros = torch.zeros((1, 1), device=spec.center.device, dtype=torch.float32)
-            return (IntervalState(lower=zeros, upper=zeros.clone()), {}, {},
+            return (IntervalState(lower=zeros, upper=zeros.clone()), AlphaState(), BetaState(),
                     AlphaBetaStats(feasibility="infeasible", reason="infeasible: first-layer split certificate",
-                                   steps=int(steps), lr=float(lr)))
+                                   steps=int(steps), lr=float(lr),
+                                   infeasible_certificate=_certificate_record(value)))
     if trace is None:
         trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
                                   raise_on_infeasible=raise_on_infeasible)
@@ -327,8 +367,8 @@ def run_alpha_beta_crown_mlp(
                 out[n] = torch.full(target, float(value), device=dev, dtype=torch.float32)
         return out
 
-    alpha = init_param(warm_start_alpha, alpha_init)
-    beta = init_param(warm_start_beta, beta_init)
+    alpha = init_param(_as_param_dict(warm_start_alpha, "alpha_by_relu_input"), alpha_init)
+    beta = init_param(_as_param_dict(warm_start_beta, "beta_by_relu_input"), beta_init)
     p_ld = {n: (numel[n] if per_batch_params else 0) for n in names}
     splits: Dict[str, Tuple[torch.Tensor, int]] = {}
     if relu_split_state:
@@ -350,8 +390,9 @@ def run_alpha_beta_crown_mlp(
             alpha=alpha, beta=beta, p_ld=p_ld, splits=splits, beta_names=beta_names if objective == "lower" else [],
             steps=int(steps), lr=float(lr), objective=objective, spec_reduce=spec_reduce, soft_tau=float(soft_tau),
             lb_weight=float(lb_weight), ub_weight=float(ub_weight), per_batch_params=per_batch_params)
-        out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
-        out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
+        out_alpha = AlphaState({n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n])
+                                for n in names})
+        out_beta = BetaState({n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names})
         stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,
                                branch_neuron=b_neuron, relu_names=tuple(trace.relu_pre.keys()))
         return IntervalState(lower=best_lb, upper=best_ub), out_alpha, out_beta, stats
@@ -410,8 +451,8 @@ def run_alpha_beta_crown_mlp(
     # only) and every domain's rows on that domain's parameters alone, so one upper
     # pass with the best parameters reproduces it.
     best_ub = bound({n: best_alpha[n] for n in names}, None, True, False, None).upper
-    out_alpha = {n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
-    out_beta = {n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names}
+    out_alpha = AlphaState({n: best_alpha[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names})
+    out_beta = BetaState({n: best_beta[n].reshape(((B,) if per_batch_params else ()) + shapes[n]) for n in names})
     stats = AlphaBetaStats(infeasible=trace.infeasible, steps=int(steps), lr=float(lr), branch_layer=b_layer,
                            branch_neuron=b_neuron, relu_names=tuple(trace.relu_pre.keys()))
     return IntervalState(lower=best_lb, upper=best_ub), out_alpha, out_beta, stats
@@ -527,6 +568,31 @@ def _optimise_general(module, spec, trace, chain, linear_spec_C, bound, grad, ou
     if not use_u:
         best_ub = bound({n: best_alpha[n] for n in names}, None, True, False, None).upper
     return best_lb, best_ub, best_alpha, best_beta
+
+
+def check_first_layer_infeasible_split(module, input_spec, *,
+                                       relu_split_state: Dict[str, torch.Tensor]) -> AlphaBetaStats:
+    """alpha_beta_crown.py:109-142: feasibility "infeasible" when the first-layer split
+    certificate (``bf_split_certificate``: a convex combination of the split halfspaces
+    whose maximum over the input set is below -1e-6) closes the one-input query, else
+    "unknown" (also for batches of more than one input, which the reference skips)."""
+    from .split_certificate import check_flags, split_certificate
+    module.validate()
+    spec = normalize_input_spec(input_spec)
+    if int(spec.center.shape[0]) != 1:
+        return AlphaBetaStats(feasibility="unknown", reason="skip (batch!=1)")
+    if not relu_split_state or not any(bool((v != 0).any().item()) for v in relu_split_state.values()
+                                       if v is not None):
+        return AlphaBetaStats(feasibility="unknown", reason="ok (no first-layer split halfspaces)")
+    value = torch.empty(1, device=spec.center.device, dtype=torch.float32)
+    flag = split_certificate(module, spec, relu_split_state, _relu_shapes(module, spec, _chain_or_none(module, spec)),
+                             max_out=value)
+    flag = flag.cpu().tolist()
+    check_flags(flag)
+    if flag[0] == 1:
+        return AlphaBetaStats(feasibility="infeasible", reason="infeasible: first-layer split certificate",
+                              infeasible_certificate=_certificate_record(value))
+    return AlphaBetaStats(feasibility="unknown", reason="ok")
 
 
 def run_alpha_crown_mlp(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.2,

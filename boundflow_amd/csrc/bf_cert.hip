@@ -63,7 +63,8 @@ __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
     const float* __restrict__ rows, int64_t row_ld, const float* __restrict__ bias,
     const int8_t* __restrict__ split, int64_t split_ld, const float* __restrict__ center, int64_t center_ld,
     const float* __restrict__ rad, int64_t rad_ld, float eps, int nk, int n0, int in_dim, int steps, double tol,
-    float w1, float b2, float w2, float adam_eps, CertAdamTable tab, int32_t* __restrict__ out) {
+    float w1, float b2, float w2, float adam_eps, CertAdamTable tab, int32_t* __restrict__ out,
+    float* __restrict__ max_out) {
   extern __shared__ float a_vec[];                       // [in_dim]: the combined normal a
   __shared__ int h_idx[kCertMaxHalfspaces];              // neuron of each halfspace, in order
   __shared__ float h_sgn[kCertMaxHalfspaces];            // its split sign s_i
@@ -104,11 +105,17 @@ __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
   }
   const int m = count_s;
   if (m == 0) {                // no first-layer halfspace: nothing to certify
-    if (tid == 0) out[node] = 0;
+    if (tid == 0) {
+      out[node] = 0;
+      if (max_out) max_out[node] = 0.f;
+    }
     return;
   }
   if (m > kCertMaxHalfspaces) {  // beyond the LDS stage: reported, the host raises
-    if (tid == 0) out[node] = -1;
+    if (tid == 0) {
+      out[node] = -1;
+      if (max_out) max_out[node] = 0.f;
+    }
     return;
   }
   for (int i = tid; i < m; i += kCertThreads) {
@@ -121,6 +128,7 @@ __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
   // softmax is 0, so the first step decides (the reference's m == 1 case)
   const int n_steps = (m == 1) ? 1 : steps;
   int verdict = 0;
+  float best = INFINITY;   // the smallest maximum seen (the certificate's value when it closes the node)
   for (int t = 0; t < n_steps; ++t) {
     // 2. w = softmax(z)
     float zmax = -INFINITY;
@@ -159,6 +167,7 @@ __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
     if (bias != nullptr)
       for (int i = 0; i < m; ++i) c += w[i] * (h_sgn[i] * bias[h_idx[i]]);
     const float ub = BOX ? (ct + nrm) + c : (ct + eps * nrm) + c;
+    best = fminf(best, ub);
     // compared in double, as the reference compares the Python float of the fp32 maximum
     if ((double)ub < -tol) {   // uniform over the workgroup
       verdict = 1;
@@ -204,7 +213,10 @@ __global__ __launch_bounds__(kCertThreads) void split_certificate_kernel(
     }
     __syncthreads();
   }
-  if (tid == 0) out[node] = verdict;
+  if (tid == 0) {
+    out[node] = verdict;
+    if (max_out) max_out[node] = best;
+  }
 }
 
 }  // namespace bf
@@ -214,7 +226,8 @@ using namespace bf;
 extern "C" int bf_split_certificate(const float* rows, int64_t row_ld, const float* bias, const int8_t* split,
                                     int64_t split_ld, const float* center, int64_t center_ld, const float* rad,
                                     int64_t rad_ld, float eps, int norm_p, int64_t nodes, int64_t n0, int64_t in_dim,
-                                    int steps, double lr, double tol, int32_t* out, hipStream_t stream) {
+                                    int steps, double lr, double tol, int32_t* out, float* max_out,
+                                    hipStream_t stream) {
   BF_REQUIRE(nodes >= 0 && n0 >= 0 && in_dim >= 1, "bf_split_certificate: bad sizes");
   BF_REQUIRE(norm_p >= 0 && norm_p <= 2 && (norm_p == 0 || rad == nullptr),
              "bf_split_certificate: norm_p is 0, 1 or 2; the box radius goes with 0");
@@ -243,11 +256,11 @@ extern "C" int bf_split_certificate(const float* rows, int64_t row_ld, const flo
   if (rad != nullptr)
     hipLaunchKernelGGL(split_certificate_kernel<true>, dim3((unsigned)nodes), dim3(kCertThreads), lds, stream, rows,
                        row_ld, bias, split, split_ld, center, center_ld, rad, rad_ld, 0.f, 0, (int)n0, (int)in_dim,
-                       steps, tol, w1, (float)beta2, w2, 1e-8f, tab, out);
+                       steps, tol, w1, (float)beta2, w2, 1e-8f, tab, out, max_out);
   else
     hipLaunchKernelGGL(split_certificate_kernel<false>, dim3((unsigned)nodes), dim3(kCertThreads), lds, stream, rows,
                        row_ld, bias, split, split_ld, center, center_ld, rad, rad_ld, eps, norm_p, (int)n0,
-                       (int)in_dim, steps, tol, w1, (float)beta2, w2, 1e-8f, tab, out);
+                       (int)in_dim, steps, tol, w1, (float)beta2, w2, 1e-8f, tab, out, max_out);
   BF_LAUNCH_CHECK("split_certificate_kernel");
   return BF_OK;
 }

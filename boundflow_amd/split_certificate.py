@@ -100,16 +100,20 @@ def first_layer_sources(module, spec: InputSpec, relu_shapes: Dict[str, Tuple[in
 
 def split_certificate(module, input_spec, relu_split_state: Dict[str, torch.Tensor],
                       relu_shapes: Dict[str, Tuple[int, ...]], *, steps: int = 200, lr: float = 0.1,
-                      tol: float = 1e-6) -> torch.Tensor:
+                      tol: float = 1e-6, max_out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """int32 [B] on the device: 1 where the first-layer splits of domain b (row b
     of each split tensor, or a shared row) are proven infeasible over domain b's
     input set, 0 otherwise (also when the domain has no first-layer split).
+    ``max_out`` (optional, float32 [B] on the device) receives the smallest maximum of
+    each domain's search (the certificate's value where the flag is 1).
     No host synchronization."""
     spec = normalize_input_spec(input_spec)
     B = int(spec.center.shape[0])
     dev = spec.center.device
     flags = torch.zeros(B, dtype=torch.int32, device=dev)
     sources = [s for s in first_layer_sources(module, spec, relu_shapes) if s[0] in (relu_split_state or {})]
+    if max_out is not None:
+        max_out.zero_()
     if not sources or B == 0:
         return flags
     I = int(spec.center[0].numel())
@@ -151,7 +155,7 @@ def split_certificate(module, input_spec, relu_split_state: Dict[str, torch.Tens
         ld = n
     _lib.call("bf_split_certificate", _lib.ptr(rows), int(rows.stride(0)), _lib.ptr(bias), _lib.ptr(split), ld,
               _lib.ptr(center), I, _lib.ptr(rad), I if rad is not None else 0, float(eps), norm_p, B, n, I, int(steps),
-              float(lr), float(tol), _lib.ptr(flags), _lib.stream_handle())
+              float(lr), float(tol), _lib.ptr(flags), _lib.ptr(max_out), _lib.stream_handle())
     return flags
 
 

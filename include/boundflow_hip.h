@@ -467,11 +467,13 @@ int bf_branch_update_native(const float* lo, const float* hi, const int8_t* spli
  * 1 L1) or, with rad, the box center +- rad (norm_p 0).  Searches a convex combination w = softmax(z) by Adam on z (lr,
  * betas 0.9/0.999, eps 1e-8, `steps` steps from z = 0) and sets out[g] = 1 at the
  * first step whose maximum over the set is below -tol, else 0; -1 when a node has
- * more than 1024 splits.  in_dim <= 16384, steps <= 256. */
+ * more than 1024 splits.  max_out (optional, [nodes]) receives the smallest maximum
+ * the search saw (the certificate's value when out is 1; 0 for a node with no split
+ * or too many).  in_dim <= 16384, steps <= 256. */
 int bf_split_certificate(const float* rows, int64_t row_ld, const float* bias, const int8_t* split, int64_t split_ld,
                          const float* center, int64_t center_ld, const float* rad, int64_t rad_ld, float eps,
                          int norm_p, int64_t nodes, int64_t n0, int64_t in_dim, int steps, double lr, double tol,
-                         int32_t* out, hipStream_t stream);
+                         int32_t* out, float* max_out, hipStream_t stream);
 
 /* Node verdict (runtime/bab.py:870-895): 1 certified (min_s lb >= threshold - tol),
  * 2 infeasible split, 0 open. */

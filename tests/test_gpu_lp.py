@@ -245,6 +245,9 @@ def test_lp_certificate_known_answers(name, p):
     assert flags == [1 if expect[p] else 0] or ibp_closes
     _bounds, _alpha, _beta, stats = hab.run_alpha_beta_crown_mlp(md, spec, relu_split_state=split, steps=0)
     assert stats.feasibility == ("infeasible" if expect[p] else "unknown")
+    # the reference's stand-alone check (alpha_beta_crown.py:109-142) sees the certificate alone
+    chk = hab.check_first_layer_infeasible_split(md, spec, relu_split_state=split)
+    assert chk.feasibility == ("infeasible" if flags == [1] else "unknown")
 
 
 @pytest.mark.parametrize("p", [2, 1])
@@ -293,3 +296,34 @@ def test_lp_bab_search_matches_oracle(tag):
     assert (r.max_queue, r.batch_rounds) == (ref["max_queue"], ref["batch_rounds"])
     import numpy as np
     np.testing.assert_allclose([q.best_lower for q in per], ref["per_best_lower"], rtol=1e-4, atol=1e-5)
+
+
+def test_certificate_record_and_state_objects():
+    """The reference's result types: the L2 three-directions query closes with a
+    certificate whose max_value is negative (tests/test_phase6f_alpha_beta_crown_pr1.py:96-118);
+    alpha/beta come back as AlphaState / BetaState (dicts with alpha_by_relu_input /
+    beta_by_relu_input) and are taken back as warm starts in either form."""
+    from types import SimpleNamespace
+    dev = device()
+    announce("certificate record and AlphaState/BetaState round trip")
+    W, b, s, _expect = LP_KATS["three_directions"]
+    m = first_layer_module(torch.tensor(W), torch.tensor(b))
+    from boundflow_amd.ir import BFTaskModule
+    md = BFTaskModule(tasks=m.tasks, entry_task_id=m.entry_task_id,
+                      bindings={"params": {k: v.to(dev) for k, v in m.params.items()}})
+    spec = lp_spec(2, torch.zeros(1, 2, device=dev))
+    split = {"h1": torch.tensor([s], dtype=torch.int8, device=dev)}
+    _b, alpha, beta, stats = hab.run_alpha_beta_crown_mlp(md, spec, relu_split_state=split, steps=0, lr=0.2)
+    assert stats.feasibility == "infeasible" and stats.infeasible_certificate is not None
+    assert float(stats.infeasible_certificate["max_value"]) < 0.0
+    chk = hab.check_first_layer_infeasible_split(md, spec, relu_split_state=split)
+    assert chk.feasibility == "infeasible" and float(chk.infeasible_certificate["max_value"]) < 0.0
+    assert isinstance(alpha, hab.AlphaState) and isinstance(beta, hab.BetaState)
+    w = wl.to_device(_lp(wl.make_c1(batch=4), 2, EPS["mlp"][2]), dev)
+    b1, a1, st1 = hab.run_alpha_crown_mlp(w.module, w.spec, linear_spec_C=w.C, steps=3, lr=0.1)
+    assert isinstance(a1, hab.AlphaState) and a1.alpha_by_relu_input is a1
+    clone = a1.detach_clone()
+    for warm in (clone, SimpleNamespace(alpha_by_relu_input=dict(clone)), dict(clone)):
+        b2, _a2, _s2 = hab.run_alpha_crown_mlp(w.module, w.spec, linear_spec_C=w.C, steps=0, lr=0.1, warm_start=warm)
+        # zero steps from the best alpha of the first run: its bound again
+        assert torch.allclose(b2.lower, b1.lower, rtol=1e-6, atol=1e-6)
