@@ -93,11 +93,12 @@ class HipTaskExecutor:
             raise ValueError(f"concretize_matmul expects center rank-2 [B,I], got {tuple(center.shape)}")
         B, K = (int(d) for d in center.shape)
         if w.dim() == 3:
-            if input_norm_p(p) != 0:
-                raise NotImplementedError("per-sample weights take Linf balls and boxes (L1/L2 need rank-2 weights)")
-            # Linf ball: eps * sum |W| over the rows equals the bounding box's radius term
-            lo, hi = p.bounding_box(center)
-            return self._batched_linear(IntervalState(lo, hi), w, b)
+            norm_p = input_norm_p(p)
+            if norm_p == 0:
+                # Linf ball or box: eps * sum |W| over the rows equals the bounding box's radius term
+                lo, hi = p.bounding_box(center)
+                return self._batched_linear(IntervalState(lo, hi), w, b)
+            return self._batched_linear_ball(center, float(p.eps), norm_p, w, b)
         if int(w.shape[1]) != K:
             raise ValueError(f"matmul shape mismatch: center={tuple(center.shape)} weight={tuple(w.shape)}")
         if isinstance(p, BoxPerturbation):
@@ -107,6 +108,26 @@ class HipTaskExecutor:
             kind = {0: 1, 2: 2, 1: 3}[input_norm_p(p)]
             in_lo, in_hi, eps = center.contiguous(), None, float(p.eps)
         return self._dense_linear(in_lo, in_hi, kind, eps, w, b)
+
+    def _batched_linear_ball(self, center: torch.Tensor, eps: float, norm_p: int, w: torch.Tensor,
+                             b: Optional[torch.Tensor]) -> IntervalState:
+        """Per-sample weights W [B, O, I] over an L2 / L1 ball (perturbation.py:146-173): the
+        rows of W[b] concretized against center[b] with the ball's dual norm
+        (bf_concretize_dense: W[b, o] . c[b] -/+ eps * ||W[b, o]||_q + bias)."""
+        B, O, I = (int(d) for d in w.shape)
+        if tuple(center.shape) != (B, I):
+            raise ValueError(f"batched matmul mismatch: center={tuple(center.shape)} weight={tuple(w.shape)}")
+        dev = center.device
+        rows = w.to(torch.float32).contiguous()
+        bias = None if b is None else b.to(device=dev, dtype=torch.float32).expand(B, O).contiguous()
+        lo = torch.empty(B, O, device=dev)
+        hi = torch.empty_like(lo)
+        c = center.to(torch.float32).contiguous()
+        stream = _lib.stream_handle()
+        for out, is_lower in ((lo, 1), (hi, 0)):
+            _lib.call("bf_concretize_dense", _lib.ptr(rows), B, O, I, _lib.ptr(c), None, eps, norm_p, _lib.ptr(bias),
+                      is_lower, _lib.ptr(out), stream)
+        return IntervalState(lo, hi)
 
     def _dense_linear(self, in_lo, in_hi, kind: int, eps: float, w: torch.Tensor,
                       b: Optional[torch.Tensor]) -> IntervalState:

@@ -327,3 +327,32 @@ def test_certificate_record_and_state_objects():
         b2, _a2, _s2 = hab.run_alpha_crown_mlp(w.module, w.spec, linear_spec_C=w.C, steps=0, lr=0.1, warm_start=warm)
         # zero steps from the best alpha of the first run: its bound again
         assert torch.allclose(b2.lower, b1.lower, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("p", ["inf", 2, 1])
+def test_task_executor_per_sample_weights_over_balls(p):
+    """HipTaskExecutor.run_ibp with a rank-3 linear weight W [B, O, I] applied to the input
+    ball (perturbation.py:146-173): the ball's dual norm of each W[b] row."""
+    from boundflow_amd.ir import BFTaskModule, BoundTask, TaskKind, TaskOp
+    dev = device()
+    announce(f"HipTaskExecutor per-sample weights, L{p} ball")
+    g = torch.Generator().manual_seed(61)
+    B, O, I = 5, 7, 33
+    W = torch.randn(B, O, I, generator=g)
+    bias = torch.randn(O, generator=g)
+    x0 = torch.randn(B, I, generator=g)
+    task = BoundTask(task_id="t0", kind=TaskKind.INTERVAL_IBP,
+                     ops=[TaskOp("linear", "l", ["input", "W", "b"], ["out"])], input_values=["input"],
+                     output_values=["out"])
+
+    def mod(dev_):
+        return BFTaskModule(tasks=[task], entry_task_id="t0", bindings={"params": {"W": W.to(dev_), "b": bias.to(dev_)}})
+
+    got = te.HipTaskExecutor().run_ibp(mod(dev), lp_spec(p, x0.to(dev), 0.2))
+    torch.cuda.synchronize()
+    ref = ti.run_ibp(mod("cpu"), lp_spec(p, x0, 0.2))
+    ref64 = ti.run_ibp(BFTaskModule(tasks=[task], entry_task_id="t0",
+                                    bindings={"params": {"W": W.double(), "b": bias.double()}}),
+                       lp_spec(p, x0.double(), 0.2))
+    assert_parity(got.lower, ref.lower, ref64.lower, f"per-sample L{p} lower")
+    assert_parity(got.upper, ref.upper, ref64.upper, f"per-sample L{p} upper")
