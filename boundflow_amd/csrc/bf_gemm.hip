@@ -58,6 +58,7 @@ static int forced_tile_from_env() {
   if (std::strcmp(v, "G") == 0) return 'G';
   if (std::strcmp(v, "H") == 0) return 'H';
   if (std::strcmp(v, "Q") == 0) return 'Q';
+  if (std::strcmp(v, "S") == 0) return 'S';
   return 0;
 }
 
@@ -78,7 +79,12 @@ int gemm_tile_choice(int64_t M, int64_t N, int nz, int64_t ks, int pro, bool dl)
   // every form; a grid with fewer 128 x 128 tiles than the device has CUs takes the
   // 16-wave TileH instead, which spreads each tile's contraction over twice the waves.
   const int64_t wgs = ceil_div(M, 128) * ceil_div(N, 128) * nz * ks;
-  if (wgs < 256) return 'H';
+  // A grid of fewer 128 x 128 tiles than the device has CUs takes, with the plain
+  // prologue, the 4-wave 64 x 64 TileS, which deals four times as many tiles over
+  // the CUs (C1 0.174 -> 0.164 ms, C3 0.257 -> 0.246, D1 0.771 -> 0.737); with the
+  // relaxation prologue (more registers per wave) and for the |A W| and relaxation
+  // epilogues (128 columns per tile) the 16-wave TileH.
+  if (wgs < 256) return pro == PRO_PLAIN ? 'S' : 'H';
   // A grid whose 128 x 128 tiles leave the CUs unevenly loaded (C5's 576 tiles: 2.25
   // per CU run at the cost of 3) takes the 64 x 128 TileQ, whose twice as many tiles
   // at 6 workgroups per CU even it out (4.5 per CU at the cost of 5); TileQ is a few
@@ -94,7 +100,10 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
     return BF_EINVAL;
   }
   const int64_t ks = (pro == PRO_PLAIN && epi == EPI_STORE && a.ksplit > 1) ? a.ksplit : 1;
-  switch (gemm_tile_choice(a.M, a.N, nz, ks, pro, gemm_dl_operands(a, nz))) {
+  int t = gemm_tile_choice(a.M, a.N, nz, ks, pro, gemm_dl_operands(a, nz));
+  if (t == 'S' && epi != EPI_STORE) t = 'H';
+  switch (t) {
+    case 'S': return launch_tile<TileS>(a, pro, epi, nz, stream);
     case 'H': return launch_tile<TileH>(a, pro, epi, nz, stream);
     case 'Q': return launch_tile<TileQ>(a, pro, epi, nz, stream);
     default: return launch_tile<TileG>(a, pro, epi, nz, stream);

@@ -905,6 +905,7 @@ gemm_kernel(GemmArgs p) {
 using TileG = Tile<128, 128, 16, 4, 2, 3>;   // 8 waves of 32x64, 3 workgroups per CU
 using TileH = Tile<128, 128, 32, 4, 4, 2>;   // 16 waves of 32x32, BK 32, 2 workgroups per CU (64 VGPRs)
 using TileQ = Tile<64, 128, 16, 2, 2, 6, true>;   // 4 waves of 32x64, 6 workgroups per CU (two LDS stages)
+using TileS = Tile<64, 64, 32, 2, 2, 4>;          // 4 waves of 32x32, 4 workgroups per CU, store epilogues only
 
 // Operands the direct-to-LDS loop takes: transposed B and whole aligned float4 rows.
 inline bool gemm_dl_operands(const GemmArgs& a, int nz) {
@@ -983,5 +984,6 @@ int launch_tile(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream)
 template <> int launch_tile<TileG>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileH>(const GemmArgs&, int, int, int, hipStream_t);
 template <> int launch_tile<TileQ>(const GemmArgs&, int, int, int, hipStream_t);
+template <> int launch_tile<TileS>(const GemmArgs&, int, int, int, hipStream_t);
 
 }  // namespace bf

@@ -33,15 +33,19 @@ const char* bf_last_error(void);
 /* The contraction's tile configuration is chosen per call: 'G', 128 x 128 x 16
  * with 8 waves of 32 x 64 (3 workgroups per CU), for every form; 'H', 128 x 128 x
  * 32 with 16 waves of 32 x 32, when the grid has fewer 128 x 128 tiles (times
- * bounds and split-K chunks) than the device has CUs; 'Q', 64 x 128 x 16 with 4
+ * bounds and split-K chunks) than the device has CUs and the contraction has the
+ * relaxation prologue or the |A W| or relaxation epilogue; 'S', 64 x 64 x 32 with
+ * 4 waves (4 workgroups per CU), for such a grid with the plain prologue and the
+ * store epilogue; 'Q', 64 x 128 x 16 with 4
  * waves (6 workgroups per CU), for a plain-prologue contraction on direct-to-LDS
  * operands (transposed B, 16-byte aligned float4 rows) whose 128 x 128 tiles
  * load the 256 CUs unevenly and whose 64 x 128 tiles load them at least 10
- * points more evenly.  The environment variable BOUNDFLOW_GEMM_TILE=G, =H or =Q,
- * read once when the library is loaded, forces one for measurement ('Q' then
- * refuses other operands).
- * bf_gemm_tile_config returns the configuration ('G', 'H' or 'Q') a contraction
- * of M x N outputs, nz bounds and ksplit K chunks would take (0 for bad sizes).
+ * points more evenly.  The environment variable BOUNDFLOW_GEMM_TILE=G, =H, =Q or
+ * =S, read once when the library is loaded, forces one for measurement ('Q' then
+ * refuses other operands; 'S' takes the store epilogue alone, others fall back to 'H').
+ * bf_gemm_tile_config returns the configuration ('G', 'H', 'Q' or 'S') a
+ * store-epilogue contraction of M x N outputs, nz bounds and ksplit K chunks would
+ * take (0 for bad sizes); the other epilogues take 'H' where it says 'S'.
  * No counterpart in the reference: introspection of this build's dispatch. */
 int bf_gemm_tile_config(int64_t M, int64_t N, int nz, int ksplit, int relax_prologue, int dl_operands);
 

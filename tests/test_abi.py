@@ -92,8 +92,9 @@ def test_binding_argument_types_match_header():
 
 def test_tile_configuration_rule():
     """The contraction's tile choice (a host-side rule, no device call): 128 x 128
-    TileG for evenly loaded grids (C2), TileH for grids of fewer 128 x 128 tiles than
-    CUs (C1, C4, D1), the 64 x 128 TileQ for C5's unevenly loaded 36 864-row grids
+    TileG for evenly loaded grids (C2), for grids of fewer 128 x 128 tiles than CUs the
+    64 x 64 TileS with the plain prologue and TileH with the relaxation prologue (C1,
+    C3, C4, D1), the 64 x 128 TileQ for C5's unevenly loaded 36 864-row grids
     on direct-to-LDS operands with the plain prologue, and 0 for bad sizes."""
     from boundflow_amd import _lib
     if not _lib.LIB_PATH.exists():
@@ -105,7 +106,8 @@ def test_tile_configuration_rule():
     assert cfg(36864, 784, 1, 1, 0, 1) == "G"      # C5 concretization: 2016 tiles, even enough
     assert cfg(36864, 256, 2, 1, 0, 1) == "G"      # both bounds: 1152 tiles, 4.5 per CU either way
     assert cfg(128000, 500, 2, 1, 0, 1) == "G"     # C2 refinements
-    assert cfg(2304, 500, 2, 1, 0, 1) == "H"       # C2's final spec query
+    assert cfg(2304, 500, 2, 1, 0, 1) == "S"       # a small grid, plain prologue
+    assert cfg(2304, 500, 2, 1, 1, 1) == "H"       # C2's final spec query (relaxation prologue)
     assert cfg(36864, 256, 1, 1, 1, 1) == "G"      # relaxation prologue: TileQ takes the plain one only
     assert cfg(36864, 256, 1, 1, 0, 0) == "G"      # operands the direct-to-LDS loop does not take
     assert cfg(0, 256, 1, 1, 0, 1) == "" and cfg(10, 10, 3, 1, 0, 1) == ""

@@ -109,3 +109,26 @@ def test_concretize_on_tile_q_matches_fp64(box):
     h_ref = h_scale.double()[:, None] * torch.sign(C_l) * w64
     got = h_out.cpu().double()
     assert torch.equal(got[sure], h_ref[sure].float().double())
+
+
+@pytest.mark.parametrize("M,N,K,trans_b", [(288, 2048, 100, 1), (300, 250, 77, 1), (130, 70, 33, 0)])
+def test_store_on_tile_s_matches_fp64(M, N, K, trans_b):
+    """Grids of fewer 128 x 128 tiles than CUs with the plain prologue (the CNN
+    configurations' fully connected layers) run on the 64 x 64 TileS: row, column and
+    K tails, either B layout."""
+    dev = device()
+    announce(f"gemm on TileS M={M} N={N} K={K} trans_b={trans_b}")
+    assert tile(M, N, 1) == "S"
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(N, K, generator=g) if trans_b else torch.randn(K, N, generator=g)
+    Bm = B.t() if trans_b else B
+    ref = A.double() @ Bm.double()
+    C = torch.empty(M, N, device=dev)
+    Ad, Bd = A.to(dev), B.contiguous().to(dev)
+    ldb = K if trans_b else N
+    _lib.call("bf_gemm", _lib.ptr(Ad), K, _lib.ptr(Bd), ldb, trans_b, 0, _lib.ptr(C), N, M, N, K, _lib.stream_handle())
+    torch.cuda.synchronize()
+    tol = contraction_tol(A, Bm, K) + 1e-30
+    err = (C.cpu().double() - ref).abs()
+    assert bool((err <= tol).all()), float((err / tol).max())
