@@ -14,8 +14,9 @@ dominant kernel (timed with HIP events on the launch stream) and a CPU baseline
 this host, with the parity of the HIP result against it).  With the default C2
 workload the line also carries ``secondary``: the metric's other half, BaB
 domains/s on the C5 domain batch (4096 subdomains of
-the MLP 784-256x4-10, 10 alpha-beta steps each), with its own roofline, CPU
-baseline and parity over all 4096 domains.
+the MLP 784-256x4-10, 10 alpha-beta steps each), and the bounds/s of the other
+BASELINE configurations C1, C3 and C4, each with its own roofline, CPU
+baseline and parity over its whole batch.
 
     python bench.py [--steps K] [--warmup W] [--config C2|C1|C3|C4|C5|D1] [--cpu-seconds S]
 
@@ -211,64 +212,118 @@ def _bounds(name: str, res):
 
 
 def parity_summary(name: str, w, ref) -> dict:
-    """HIP result on the whole workload against the oracle's result on it.
-    C1-C3, D1: the contract, rtol 1e-5 / atol 1e-6 on both bounds, a row outside
-    it counted as explained when the fp64 oracle is as far from the fp32 oracle
-    as the HIP value is.  C4, C5: whole Adam trajectories, so the counts outside
-    the contract and outside 1e-4 are reported and the verdict is taken at the
-    trajectory band 1e-3 (one step at a time they meet the contract, tested in
-    tests/test_gpu_teacher_forced.py).  Also: verdict mismatches, near ties
-    (|min_s lb| < 1e-4) and, for C5, certified flags and branching decisions of
-    every domain."""
+    """HIP result on the whole workload against the oracle's result on it, at the
+    contract rtol 1e-5 / atol 1e-6 on both bounds: a value outside it counts as
+    explained when the fp64 oracle is as far from the fp32 oracle as the HIP
+    value is.  C4, C5 (optimised bounds): ``optimised_parity``.  Also: verdict
+    mismatches and near ties (|min_s lb| < 1e-4)."""
     import torch
     from boundflow_amd import workloads as wl
     from oracle import parity
 
+    if name in ("C4", "C5"):
+        return optimised_parity(name, w)
     got = hip_runner(name)(wl.to_device(w, torch.device("cuda:0")))
     torch.cuda.synchronize()
     g_lo, g_hi = (t.cpu() for t in _bounds(name, got))
     r_lo, r_hi = _bounds(name, ref)
-    optimised = name in ("C4", "C5")
-    pick = (lambda lo, hi: lo) if name == "C5" else (lambda lo, hi: torch.cat([lo, hi]))
-    cache = {}
-
-    def ref64():
-        if "r" not in cache:
-            e_lo, e_hi = _bounds(name, _oracle_run(name, parity.to_float64(w)))
-            cache["r"] = pick(e_lo, e_hi)
-        return cache["r"]
-
+    pick = lambda lo, hi: torch.cat([lo, hi])   # noqa: E731
     strict = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None)
-    if optimised:
-        mid = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None, rtol=1e-4, atol=1e-4)
-        band = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), None, rtol=1e-3, atol=1e-3)
-        if band.strict_violations:
-            band = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), ref64(), rtol=1e-3, atol=1e-3)
-        rep = band
-        contract = ("trajectory: rtol 1e-3 atol 1e-3 on the optimised " + ("lower bound" if name == "C5"
-                                                                          else "bounds")
-                    + f"; at the contract 1e-5/1e-6 {strict.strict_violations} outside, at 1e-4 "
-                      f"{mid.strict_violations} outside")
-    else:
-        rep = strict if not strict.strict_violations else parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), ref64())
-        contract = "rtol 1e-05 atol 1e-06 on both bounds"
+    rep = strict
+    if strict.strict_violations:
+        e_lo, e_hi = _bounds(name, _oracle_run(name, parity.to_float64(w)))
+        rep = parity.compare(pick(g_lo, g_hi), pick(r_lo, r_hi), pick(e_lo, e_hi))
     g_min = g_lo.min(dim=1).values
     r_min = r_lo.min(dim=1).values
-    out = {"contract": contract, "values": rep.n, "max_abs_err": rep.max_abs, "max_rel_err": rep.max_rel,
-           "outside_contract": rep.strict_violations, "explained_by_fp64": rep.explained_by_fp32,
-           "unexplained": rep.unexplained, "verdict_mismatches": int(((g_min >= 0) != (r_min >= 0)).sum()),
-           "near_ties": int((r_min.abs() < 1e-4).sum()), "sample": f"the whole batch ({w.batch} inputs)"}
-    if name == "C5":
-        ref_cert = r_min >= 0.0 - 1e-6
-        hip_cert = got["status"].cpu() == 1
-        out["certified"] = {"hip": int(hip_cert.sum()), "reference": int(ref_cert.sum()), "of": w.batch}
-        out["status_mismatches"] = int((hip_cert != ref_cert).sum()) + int((got["status"].cpu() == 2).sum())
+    return {"contract": "rtol 1e-05 atol 1e-06 on both bounds", "values": rep.n, "max_abs_err": rep.max_abs,
+            "max_rel_err": rep.max_rel, "outside_contract": rep.strict_violations,
+            "explained_by_fp64": rep.explained_by_fp32, "unexplained": rep.unexplained,
+            "verdict_mismatches": int(((g_min >= 0) != (r_min >= 0)).sum()),
+            "near_ties": int((r_min.abs() < 1e-4).sum()), "sample": f"the whole batch ({w.batch} inputs)"}
+
+
+def optimised_parity(name: str, w) -> dict:
+    """C4 / C5: the HIP optimisation and the oracle's, both recorded step by step,
+    over the whole batch.  ``outside_contract`` counts the final bounds outside
+    rtol 1e-5 / atol 1e-6 (C4: both bounds; C5: the lower bound of the feasible
+    domains); ``outside_band_1e-3`` the same at 1e-3.  Every domain outside the
+    contract is traced (oracle/trajectory.py: the HIP trajectory checked step by
+    step against the oracle at the HIP states, and the step at which the two
+    trajectories part shown to be reachable by Adam within the gradients' fp32
+    uncertainty); ``unexplained`` is 0 when the trace holds.  C5 also: certified
+    counts, status and branching mismatches over the feasible domains, and the
+    infeasible domains on each side."""
+    import torch
+    from boundflow_amd import alpha_beta as hab
+    from boundflow_amd import bab as hbab
+    from boundflow_amd import workloads as wl
+    from oracle import alpha_beta_ref as ab
+    from oracle import crown_ref as cr
+    from oracle import parity
+    from oracle import trajectory as tt
+
+    wd = wl.to_device(w, torch.device("cuda:0"))
+    hrec, srec = [], []
+    if name == "C4":
+        got, best_alpha, _b, _st = hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C,
+                                                                       steps=20, lr=0.1, record=hrec)
+        torch.cuda.synchronize()
+        _e, pre = cr.forward_ibp_trace(w.module, w.spec)
+        ref = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, steps=20, lr=0.1,
+                                      warm_start_alpha=ab.adaptive_alpha_init(pre), per_batch_params=True,
+                                      record=srec)[0]
+        wf, g_lo, g_hi, r_lo, r_hi, lr = w, got.lower.cpu(), got.upper.cpu(), ref.lower, ref.upper, 0.1
+        best = {n: v.cpu() for n, v in best_alpha.items()}
+        sample = range(w.batch)
+        out = {}
+    else:
+        got = hbab.evaluate_domain_batch(wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state=wd.extra["splits"],
+                                         steps=10, lr=0.2, record=hrec)
+        torch.cuda.synchronize()
+        ref = ab.evaluate_domain_batch(w.module, w.spec, linear_spec_C=w.C, relu_split_state=w.extra["splits"],
+                                       steps=10, lr=0.2, record=srec)
+        status = got["status"].cpu()
+        feas = ref["feasible"]
+        idx = feas.nonzero().flatten()
+        hrec = tt.slice_record(hrec, idx)
+        wf = tt.sub_workload(w, idx)
+        g_lo, g_hi, r_lo, r_hi, lr = got["lower"].cpu()[idx], got["upper"].cpu()[idx], ref["lower"][idx], None, 0.2
+        best = {n: v.cpu()[idx] for n, v in got["alpha"].items()}
+        sample = range(0, len(idx), 64)
+        hip_cert = status == 1
         names = got["relu_names"]
         layer, neuron = got["branch_layer"].cpu().tolist(), got["branch_neuron"].cpu().tolist()
         hip_branch = [None if l < 0 else (names[l], n) for l, n in zip(layer, neuron)]
-        out["branch_mismatches"] = sum(hip_branch[i] != ref[3][i] for i in range(len(hip_branch)))
-        out["sample"] = f"all {w.batch} domains"
-    return out
+        out = {"certified": {"hip": int(hip_cert.sum()), "reference": int(ref["certified"].sum()), "of": w.batch},
+               "infeasible": {"hip": int((status == 2).sum()), "reference": int((~feas).sum())},
+               "status_mismatches": int((hip_cert != ref["certified"]).sum()) + int(((status == 2) != ~feas).sum()),
+               "branch_mismatches": sum(hip_branch[i] != ref["branch"][i] for i in idx.tolist())}
+    both_g = g_lo if r_hi is None else torch.cat([g_lo, g_hi])
+    both_r = r_lo if r_hi is None else torch.cat([r_lo, r_hi])
+    strict = parity.compare(both_g, both_r, None)
+    band = parity.compare(both_g, both_r, None, rtol=1e-3, atol=1e-3)
+    logs = []
+    try:
+        trace = tt.trace_run(wf, hrec, srec, g_lo, r_lo, lr, what=name, sample=sample, got_upper=g_hi,
+                             ref_upper=r_hi, best_alpha=best, fp64_lower=lambda rows: _oracle_run(
+                                 name, parity.to_float64(tt.sub_workload(wf, rows)))[0].lower, log=logs.append)
+        unexplained, failure = 0, None
+    except AssertionError as exc:
+        trace, unexplained, failure = None, strict.strict_violations, str(exc)[:300]
+    g_min, r_min = g_lo.min(dim=1).values, r_lo.min(dim=1).values
+    res = {"contract": "rtol 1e-05 atol 1e-06 on the optimised " + ("lower bound of the feasible domains"
+                                                                     if name == "C5" else "bounds"),
+           "values": strict.n, "max_abs_err": strict.max_abs, "max_rel_err": strict.max_rel,
+           "outside_contract": strict.strict_violations, "outside_band_1e-3": band.strict_violations,
+           "traced_to_trajectory_divergence": strict.strict_violations if trace is not None else 0,
+           "unexplained": unexplained, "trajectory_trace": trace,
+           "verdict_mismatches": int(((g_min >= 0) != (r_min >= 0)).sum()),
+           "near_ties": int((r_min.abs() < 1e-4).sum()),
+           "sample": f"all {w.batch} domains" if name == "C5" else f"the whole batch ({w.batch} inputs)"}
+    if failure is not None:
+        res["trace_failure"] = failure
+    res.update(out)
+    return res
 
 
 def cpu_baseline(name: str, w, seconds: float):
@@ -391,10 +446,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="C2")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--secondary-cpu-seconds", type=float, default=8.0,
+                    help="CPU baseline time of each secondary configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     ap.add_argument("--no-graph", action="store_true", help="issue every launch from Python (no HIP graph replay)")
-    ap.add_argument("--no-secondary", action="store_true", help="C2 alone, without the C5 domains/s record")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="C2 alone, without the C5 domains/s and C1 / C3 / C4 bounds/s records")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -439,17 +497,24 @@ def main() -> int:
     if not args.no_cpu and not args.config.startswith("X"):   # X1 / X3: executor profile entries, no CPU leg
         line["cpu_baseline"] = cpu_baseline(args.config, w, args.cpu_seconds)
         line["cpu_baseline"]["unit"] = unit
-    # the metric's second half: BaB domains/s on the C5 domain batch, measured in the same run
+    # the metric's second half (BaB domains/s on the C5 domain batch) and the other BASELINE
+    # configurations' bounds/s (C1, C3, C4), each measured in the same run with its own
+    # roofline, CPU baseline and whole-batch parity
     if args.config == "C2" and not args.no_secondary:
         del w
-        gc.collect()
-        torch.cuda.empty_cache()
-        sec_rec, w5, unit5 = measure("C5", args.steps, args.warmup, args.no_graph)
-        sec_rec = {"metric": "BaB domains/sec (beta-CROWN domain batch)", **sec_rec}
-        if not args.no_cpu:
-            sec_rec["cpu_baseline"] = cpu_baseline("C5", w5, args.cpu_seconds)
-            sec_rec["cpu_baseline"]["unit"] = unit5
-        line["secondary"] = [sec_rec]
+        line["secondary"] = []
+        for name, metric in (("C5", "BaB domains/sec (beta-CROWN domain batch)"),
+                             ("C1", "CROWN bounds/sec (IBP + CROWN, MLP)"), ("C3", "CROWN bounds/sec (CNN)"),
+                             ("C4", "CROWN bounds/sec (alpha-CROWN, CNN)")):
+            gc.collect()
+            torch.cuda.empty_cache()
+            sec_rec, ws, unit_s = measure(name, args.steps, args.warmup, args.no_graph)
+            sec_rec = {"metric": metric, "config_id": name, **sec_rec}
+            if not args.no_cpu:
+                sec_rec["cpu_baseline"] = cpu_baseline(name, ws, args.secondary_cpu_seconds)
+                sec_rec["cpu_baseline"]["unit"] = unit_s
+            line["secondary"].append(sec_rec)
+            del ws
     print(json.dumps(line), flush=True)
     return 0
 

@@ -309,6 +309,7 @@ def run_alpha_beta_crown_mlp(
     soft_tau: float = 1.0,
     lb_weight: float = 1.0,
     ub_weight: float = 1.0,
+    record: Optional[list] = None,
 ):
     """HIP counterpart of run_alpha_beta_crown_mlp (alpha_beta_crown.py:643-941).
 
@@ -385,6 +386,8 @@ def run_alpha_beta_crown_mlp(
     S = int(linear_spec_C.shape[-2]) if linear_spec_C is not None else out_dim
     M = B * S
     if objective != "lower" or spec_reduce != "mean":
+        if record is not None:
+            raise NotImplementedError("record is kept for the lower-bound objective with the mean reduction")
         best_lb, best_ub, best_alpha, best_beta = _optimise_general(
             module, spec, trace, chain, linear_spec_C, bound, grad, out_dim, B=B, S=S, names=names, numel=numel,
             alpha=alpha, beta=beta, p_ld=p_ld, splits=splits, beta_names=beta_names if objective == "lower" else [],
@@ -435,6 +438,11 @@ def run_alpha_beta_crown_mlp(
                 for n in names:
                     best_alpha[n].copy_(alpha[n])
                     best_beta[n].copy_(beta[n])
+        if record is not None:
+            pshape = {n: ((B,) if per_batch_params else ()) + shapes[n] for n in names}
+            record.append({"step": step, "alpha": {n: alpha[n].reshape(pshape[n]).cpu() for n in names},
+                           "beta": {n: beta[n].reshape(pshape[n]).cpu() for n in names},
+                           "lower": bounds.lower.cpu()})
         if step == int(steps):
             break
         a_arg = {n: (alpha[n], p_ld[n]) for n in names}
@@ -446,6 +454,12 @@ def run_alpha_beta_crown_mlp(
                     _lib.call("bf_sum_rows", _lib.ptr(d[n]), B, numel[n], _lib.ptr(r), stream)
                     d[n] = r
         adam.step([g_alpha[n] for n in names] + [g_beta[n] for n in beta_names], lr, stream)
+        if record is not None:
+            rec = record[-1]
+            rec["grad_alpha"] = {n: g_alpha[n].reshape(pshape[n]).cpu() for n in names}
+            rec["grad_beta"] = {n: (g_beta[n].reshape(pshape[n]).cpu() if n in beta_names else None) for n in names}
+            rec["alpha_next"] = {n: alpha[n].reshape(pshape[n]).cpu() for n in names}
+            rec["beta_next"] = {n: beta[n].reshape(pshape[n]).cpu() for n in names}
     # The reference keeps the upper bound of the evaluation that gave the best lower
     # bound.  The upper bound depends on alpha alone (beta enters the lower bound
     # only) and every domain's rows on that domain's parameters alone, so one upper
@@ -614,14 +628,15 @@ def run_alpha_crown_mlp(module, input_spec, *, linear_spec_C=None, steps: int = 
     return bounds, alpha, stats
 
 
-def run_alpha_crown_from_crown_init(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.1):
+def run_alpha_crown_from_crown_init(module, input_spec, *, linear_spec_C=None, steps: int = 20, lr: float = 0.1,
+                                    record: Optional[list] = None):
     """Config C4: per-domain alpha initialised from the CROWN relaxation
     (alpha_from_crown), then ``steps`` Adam steps on the lower bound."""
     spec = normalize_input_spec(input_spec)
     trace = forward_ibp_trace(module, spec, chain=_chain_or_none(module, spec))
     init = alpha_from_crown(trace)
     return run_alpha_beta_crown_mlp(module, spec, linear_spec_C=linear_spec_C, steps=steps, lr=lr,
-                                    warm_start_alpha=init, per_batch_params=True, trace=trace)
+                                    warm_start_alpha=init, per_batch_params=True, trace=trace, record=record)
 
 
 def lower_bound_gradients(module, input_spec, *, linear_spec_C, relu_alpha: Dict[str, torch.Tensor],

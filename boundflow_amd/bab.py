@@ -33,10 +33,11 @@ def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
                           alpha_init: float = 0.5, beta_init: float = 0.0,
                           warm_start_alpha: Optional[Dict[str, torch.Tensor]] = None,
                           warm_start_beta: Optional[Dict[str, torch.Tensor]] = None,
-                          threshold: float = 0.0, tol: float = 1e-6):
+                          threshold: float = 0.0, tol: float = 1e-6, record: Optional[list] = None):
     """Returns a dict of device tensors: ``status`` int32 [D] (0 open, 1 certified,
     2 infeasible), ``lower``/``upper`` [D, S], ``branch_layer``/``branch_neuron``
-    int32 [D] (-1 when no ambiguous neuron is left), ``alpha``/``beta`` per ReLU."""
+    int32 [D] (-1 when no ambiguous neuron is left), ``alpha``/``beta`` per ReLU.
+    ``record`` is passed to the optimiser (per-step parity diagnostics)."""
     spec = normalize_input_spec(input_spec)
     chain, _shapes, _has_conv = _relu_layout(module, spec)
     trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
@@ -46,7 +47,8 @@ def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
     bounds, alpha, beta, _stats = run_alpha_beta_crown_mlp(
         module, spec, linear_spec_C=linear_spec_C, relu_split_state=relu_split_state, steps=steps, lr=lr,
         alpha_init=alpha_init, beta_init=beta_init, warm_start_alpha=warm_start_alpha,
-        warm_start_beta=warm_start_beta, per_batch_params=True, trace=trace, first_layer_certificate=False)
+        warm_start_beta=warm_start_beta, per_batch_params=True, trace=trace, first_layer_certificate=False,
+        record=record)
     S = int(bounds.lower.shape[1])
     status = torch.empty(D, dtype=torch.int32, device=spec.center.device)
     _lib.call("bf_domain_status", _lib.ptr(bounds.lower), D, S, _lib.ptr(trace.infeasible), float(threshold),

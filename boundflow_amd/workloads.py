@@ -419,6 +419,50 @@ def make_bab_toy(seed: int = 0, batch: int = 6, eps: float = 0.08, dims: Sequenc
     return Workload("bab_toy", module, spec, margin_spec(labels, dims[-1]), labels)
 
 
+def build_small_cnn(*, gen: torch.Generator, in_shape: Sequence[int] = (2, 6, 6), channels: int = 4,
+                    kernel: int = 3, stride: int = 1, padding: int = 0, hidden: int = 10, n_out: int = 3,
+                    bias_std: float = 0.1, conv_bias_std: float = 0.1) -> BFTaskModule:
+    """in_shape -> conv(channels, kernel, stride, padding) -> relu -> flatten -> fc hidden -> relu -> fc n_out."""
+    ci, hi, wi = (int(d) for d in in_shape)
+    ho = (hi + 2 * padding - kernel) // stride + 1
+    wo = (wi + 2 * padding - kernel) // stride + 1
+    n_flat = channels * ho * wo
+    params: Dict[str, torch.Tensor] = {
+        "W0": _kaiming((channels, ci, kernel, kernel), fan_in=ci * kernel * kernel, gen=gen, kind="uniform"),
+        "b0": _bias(channels, gen, conv_bias_std),
+        "W1": _kaiming((hidden, n_flat), fan_in=n_flat, gen=gen, kind="uniform"),
+        "b1": _bias(hidden, gen, bias_std),
+        "W2": _kaiming((n_out, hidden), fan_in=hidden, gen=gen, kind="uniform"),
+        "b2": _bias(n_out, gen, bias_std),
+    }
+    conv = {"stride": stride, "padding": padding, "dilation": 1, "groups": 1}
+    ops = [TaskOp("conv2d", "conv0", ["input", "W0", "b0"], ["h0"], conv),
+           TaskOp("relu", "relu0", ["h0"], ["r0"]),
+           TaskOp("flatten", "flatten", ["r0"], ["f0"], {"start_dim": 1, "end_dim": -1}),
+           TaskOp("linear", "linear1", ["f0", "W1", "b1"], ["h1"]),
+           TaskOp("relu", "relu1", ["h1"], ["r1"]),
+           TaskOp("linear", "linear2", ["r1", "W2", "b2"], ["out"])]
+    return _module(ops, params, ["input", "h0", "r0", "f0", "h1", "r1", "out"])
+
+
+def make_bab_cnn_toy(seed: int = 0, batch: int = 4, eps: float = 0.02, in_shape: Sequence[int] = (2, 6, 6),
+                     channels: int = 4, hidden: int = 10, n_out: int = 3, conv_bias_std: float = 0.1) -> Workload:
+    """Small CNN for whole branch-and-bound searches on conv graphs: inputs in
+    [0, 1]^in_shape, Linf eps, margin specs of the network's own prediction."""
+    g = torch.Generator().manual_seed(3000 + seed)
+    module = build_small_cnn(gen=g, in_shape=in_shape, channels=channels, hidden=hidden, n_out=n_out,
+                             conv_bias_std=conv_bias_std)
+    x = torch.rand((batch,) + tuple(int(d) for d in in_shape), generator=g)
+    labels = predicted_labels(module, x)
+    spec = InputSpec.linf(value_name="input", center=x, eps=eps)
+    return Workload("bab_cnn_toy", module, spec, margin_spec(labels, n_out), labels)
+
+
+def make_bab_case(kind: str = "mlp", **kw) -> Workload:
+    """The whole-search workloads: ``make_bab_toy`` (kind "mlp") or ``make_bab_cnn_toy`` (kind "cnn")."""
+    return make_bab_cnn_toy(**kw) if kind == "cnn" else make_bab_toy(**kw)
+
+
 def split_ibp_dag(w: Workload) -> BFTaskModule:
     """The ``make_ibp_dag`` program as three tasks joined by a TaskGraph, with a
     storage plan that reuses physical buffers (``h0``/``a`` and ``c``/``rr``

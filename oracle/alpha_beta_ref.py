@@ -23,7 +23,7 @@ import torch
 from boundflow_amd.ir import BFTaskModule
 from boundflow_amd.spec import InputSpec, IntervalState, normalize_input_spec
 
-from .crown_ref import (DenseOp, broadcast_split, concretize_affine, conv2d_right, crown_backward_from_trace,
+from .crown_ref import (DenseOp, _pair, broadcast_split, concretize_affine, conv2d_right, crown_backward_from_trace,
                         forward_ibp_trace)
 
 
@@ -151,8 +151,9 @@ def first_layer_split_halfspaces(module: BFTaskModule, spec: InputSpec, relu_spl
                 continue
             one_hot = torch.zeros((1, 1) + oshape, dtype=W.dtype)
             one_hot.view(-1)[fi] = 1.0
-            row = conv2d_right(DenseOp(one_hot, oshape), W, a.get("stride", 1), a.get("padding", 0),
-                               a.get("dilation", 1), int(a.get("groups", 1)), ishape, oshape).to_dense()[0, 0]
+            # the reference's conv2d_right pairs scalar attributes (linear_operator.py:434-436)
+            row = conv2d_right(DenseOp(one_hot, oshape), W, _pair(a.get("stride", 1)), _pair(a.get("padding", 0)),
+                               _pair(a.get("dilation", 1)), int(a.get("groups", 1)), ishape, oshape).to_dense()[0, 0]
             ch = fi // (oshape[1] * oshape[2])
             out.append((x, fi, float(s) * row.reshape(-1), float(s) * b[ch]))
     return out
@@ -497,6 +498,7 @@ def evaluate_domain_batch(
     beta_init: float = 0.0,
     threshold: float = 0.0,
     tol: float = 1e-6,
+    record: Optional[list] = None,
 ):
     """Node-batch evaluation of a BaB frontier (bab.py:1250-1460 + :870-895).
 
@@ -504,6 +506,8 @@ def evaluate_domain_batch(
     reference's per-node fallback does; the rest are evaluated in one
     ``per_batch_params=True`` alpha-beta call.  Returns a dict with per-domain
     ``feasible``, ``lower`` [D,S], ``upper``, ``certified`` and ``branch``.
+    ``record`` receives the optimisation's per-step record over the feasible
+    domains (``run_alpha_beta_crown``).
     """
     feasible = domain_feasible(module, spec, relu_split_state)
     idx = feasible.nonzero(as_tuple=False).flatten()
@@ -517,7 +521,7 @@ def evaluate_domain_batch(
         sub_split = {k: v[idx] for k, v in relu_split_state.items()}
         bounds, _a, _b, choices = run_alpha_beta_crown(
             module, sub_spec, linear_spec_C=linear_spec_C[idx], relu_split_state=sub_split,
-            steps=steps, lr=lr, alpha_init=alpha_init, beta_init=beta_init, per_batch_params=True,
+            steps=steps, lr=lr, alpha_init=alpha_init, beta_init=beta_init, per_batch_params=True, record=record,
         )
         lower[idx] = bounds.lower
         upper[idx] = bounds.upper

@@ -1,0 +1,250 @@
+"""Gradients of a CROWN lower bound with respect to the alpha / beta
+parameters, and the kink allowances of those gradients (CPU, float32 or float64;
+test infrastructure: only tests/, __graft_entry__.smoke() and bench.py's parity
+leg use it).
+
+``oracle_grads`` is autograd through the oracle's restatement of the backward
+pass (crown_ref.crown_backward_from_trace, the reference's
+crown_ibp.py:1669-2051), i.e. the gradient the reference's own optimiser steps
+on (alpha_beta_crown.py:756-925).
+
+Kink allowances.  The lower bound is piecewise smooth in alpha and beta: it has
+kinks where a coefficient changes sign.  Two correct fp32 computations that sum
+in different orders can land on different sides of a kink when the coefficient
+there is within rounding of zero, and their gradients then differ by a jump (a
+valid subgradient each).  Two kinds:
+
+* an input-layer coefficient y (the Linf concretization's eps * |y| term): the
+  gradient dL/dy jumps by 2 * eps * |G|;
+* a coefficient A entering a ReLU relaxation (the slope select A >= 0 picks the
+  lower or the upper line): dL/dA jumps by |go (alpha_l - alpha_u) + G (beta_l - beta_u)|
+  with go the gradient of the relaxed coefficient.
+
+A jump dJ at an element e moves dL/dtheta by at most dJ * |de/dtheta|, so the
+allowance of theta sums that over the elements that are within ``slack`` times
+their fp32 rounding error of zero, the first-order effect of each tie decided
+the other way.  ``tie_allowances`` (chain MLPs) estimates the rounding error of
+each coefficient as a chain of contractions does (Higham and Mary, 2019): a
+length-n sum rounds by about sqrt(n) u sum |a_i w_i| (u = 2^-24), errors
+already in A add in quadrature through W, and a relaxation scales them by its
+slope.  ``sign_tie_allowances`` (any network, input-layer ties only) counts the
+coefficients with |y| <= tau * sum |terms|.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional
+
+import torch
+
+from oracle import alpha_beta_ref as ab
+from oracle import crown_ref as cr
+from oracle import parity
+
+
+def _accumulate_ties(ties, plist, per_domain: bool = True):
+    """sum over ties (domain, element, jump) of jump * |d element / d param|, per
+    parameter.  Domains share no parameter (per-domain alpha / beta rows), so one
+    reverse pass takes one tie of every domain at once: the gradient of
+    sum_d jump_d * e_d has domain d's row from e_d alone.  ``per_domain=False``
+    (parameters shared by the batch) takes one tie per pass."""
+    allow = {k: torch.zeros_like(v) for k, v in plist}
+    if per_domain:
+        by_dom: Dict[int, list] = {}
+        for d, e, jump in ties:
+            by_dom.setdefault(d, []).append((e, jump))
+        rounds = [[lst[r] for lst in by_dom.values() if r < len(lst)]
+                  for r in range(max((len(v) for v in by_dom.values()), default=0))]
+    else:
+        rounds = [[(e, jump)] for _d, e, jump in ties]
+    for terms in rounds:
+        total = torch.stack([e * jump for e, jump in terms]).sum()
+        grads = torch.autograd.grad(total, [v for _k, v in plist], retain_graph=True, allow_unused=True)
+        for (k, _v), g in zip(plist, grads):
+            if g is not None:
+                allow[k] += g.abs()
+    return allow
+
+
+def oracle_grads(w, alpha, beta=None, splits=None, per_batch=True, dtype=torch.float32):
+    """Autograd gradient of L = -sum_d mean_s lb (or -mean lb) in the oracle."""
+    mod = w.module
+    spec = w.spec
+    C = w.C
+    if dtype == torch.float64:
+        w = parity.to_float64(w)
+        mod, spec, C = w.module, w.spec, w.C
+    a = {k: v.to(dtype).clone().requires_grad_(True) for k, v in alpha.items()}
+    bt = None
+    if beta is not None:
+        bt = {k: v.to(dtype).clone().requires_grad_(True) for k, v in beta.items()}
+    env, pre = cr.forward_ibp_trace(mod, spec, relu_split_state=splits)
+    add = ab.beta_to_pre_add(bt, pre, splits) if bt is not None else None
+    b = cr.crown_backward_from_trace(mod, spec, interval_env=env, relu_pre=pre, linear_spec_C=C, relu_alpha=a,
+                                     relu_pre_add_coeff_l=add)
+    loss = -b.lower.mean(dim=1).sum() if per_batch else -b.lower.mean(dim=1).mean()
+    loss.backward()
+    # a slope that enters no bound (no ambiguous neuron of that ReLU on these domains) has gradient 0
+    ga = {k: (v.grad.detach() if v.grad is not None else torch.zeros_like(v.detach())) for k, v in a.items()}
+    # a split multiplier that enters no bound (its split is zero on every domain) has gradient 0
+    gb = None if bt is None else {k: (v.grad.detach() if v.grad is not None else torch.zeros_like(v.detach()))
+                                  for k, v in bt.items()}
+    return b, ga, gb
+
+
+def abs_op(op):
+    """The same lazy input-layer operator over |coefficients| and |weights|: its
+    dense form is sum_k |A_k| |W_k,i|, the magnitude bound of each coefficient's sum."""
+    if isinstance(op, cr.DenseOp):
+        return cr.DenseOp(op.coeffs.abs(), op.input_shape)
+    if isinstance(op, cr.RightMatmulOp):
+        return cr.RightMatmulOp(abs_op(op.base), op.rhs.abs())
+    if isinstance(op, cr.ReshapeOp):
+        return cr.ReshapeOp(abs_op(op.base), op.input_shape)
+    if isinstance(op, cr.Conv2dOp):
+        return cr.Conv2dOp(abs_op(op.base), op.weight.abs(), op.stride, op.padding, op.dilation, op.groups,
+                           op.input_shape)
+    if isinstance(op, cr.AddOp):
+        return cr.AddOp(abs_op(op.lhs), abs_op(op.rhs))
+    if isinstance(op, cr.SliceOp):
+        return cr.SliceOp(abs_op(op.base), op.input_shape, op.start, op.stop)
+    raise TypeError(type(op))
+
+
+def sign_tie_allowances(w64, alpha64, per_batch, tau=1e-5, beta64=None, splits=None):
+    """Float64 bound of how far dL/dalpha (and dL/dbeta) may move when the sign of an
+    input-layer coefficient y_i (the concretization's |y_i| term, whose derivative is
+    sign(y_i)) is decided the other way.  Only coefficients with
+    |y_i| <= tau * sum_k |terms| -- inside fp32 rounding of their sum -- count;
+    flipping one changes the lower bound's gradient by 2 * eps * dy_i/dparam,
+    scaled by the loss's mean over specs (and batch when shared).  Returns
+    (alpha allowances, beta allowances, number of tied coefficients)."""
+    captured = {}
+    orig = cr.concretize_affine
+
+    def capture(spec, center, op, b):
+        captured["dense"] = op.to_dense()
+        captured["bound"] = abs_op(op).to_dense().detach()
+        return orig(spec, center, op, b)
+
+    a = {k: v.clone().requires_grad_(True) for k, v in alpha64.items()}
+    bt = None if beta64 is None else {k: v.clone().requires_grad_(True) for k, v in beta64.items()}
+    cr.concretize_affine = capture
+    try:
+        env, pre = cr.forward_ibp_trace(w64.module, w64.spec, relu_split_state=splits)
+        add = ab.beta_to_pre_add(bt, pre, splits) if bt is not None else None
+        cr.crown_backward_from_trace(w64.module, w64.spec, interval_env=env, relu_pre=pre, linear_spec_C=w64.C,
+                                     relu_alpha=a, relu_pre_add_coeff_l=add)
+    finally:
+        cr.concretize_affine = orig
+    dense, bound = captured["dense"], captured["bound"]
+    B, S = int(dense.shape[0]), int(dense.shape[1])
+    eps = float(w64.spec.perturbation.eps)
+    scale = 1.0 / S if per_batch else 1.0 / (S * B)
+    flat = dense.reshape(-1)
+    tie = (flat.detach().abs() <= tau * bound.reshape(-1)).nonzero().flatten().tolist()
+    params = list(a.items()) + ([] if bt is None else [(("beta", k), v) for k, v in bt.items()])
+    per_row = S * (flat.numel() // (B * S))
+    allow = _accumulate_ties([(i // per_row, flat[i], 2.0 * eps * scale) for i in tie], params,
+                             per_domain=per_batch)
+    allow_a = {k: allow[k] for k in a}
+    allow_b = {} if bt is None else {k: allow[("beta", k)] for k in bt}
+    return allow_a, allow_b, len(tie)
+
+
+def tie_allowances(w64, alpha64: Dict[str, torch.Tensor], beta64: Optional[Dict[str, torch.Tensor]], splits,
+                   *, slack: float = 4.0):
+    """(alpha allowances, beta allowances, number of ties) of L = -sum_d mean_s lb."""
+    module, spec = w64.module, w64.spec
+    params = module.params
+    ops = module.get_entry_task().ops
+    lin = [op for op in ops if op.op_type == "linear"]
+    relus = [op for op in ops if op.op_type == "relu"]
+    if len(lin) != len(relus) + 1 or any(op.op_type not in ("linear", "relu") for op in ops):
+        raise NotImplementedError("tie allowances are restated for chain MLPs")
+    _env, pre = cr.forward_ibp_trace(module, spec, relu_split_state=splits)
+    B = int(spec.center.shape[0])
+    C = w64.C.double()
+    S = int(C.shape[1])
+    u32 = 2.0 ** -24
+    a = {k: v.clone().requires_grad_(True) for k, v in alpha64.items()}
+    bt = None if beta64 is None else {k: v.clone().requires_grad_(True) for k, v in beta64.items()}
+    add = ab.beta_to_pre_add(bt, pre, splits) if bt is not None else {}
+    A = C
+    err = torch.zeros_like(C)
+    b = torch.zeros(B, S, dtype=torch.float64)
+    kinks = []
+    for i in reversed(range(len(lin))):
+        W = params[lin[i].inputs[1]].double()
+        if len(lin[i].inputs) == 3:
+            b = b + (A * params[lin[i].inputs[2]].double()).sum(-1)
+        n = int(W.shape[0])
+        err = (n ** 0.5) * u32 * (A.detach().abs() @ W.abs()) + ((err * err) @ (W * W)).sqrt()
+        A = A @ W
+        if i == 0:
+            break
+        name = relus[i - 1].inputs[0]
+        _pf, au, bu, al, bl = cr.relu_backward_relaxation(pre[name], name, a)
+        nn = A >= 0
+        sel_a = torch.where(nn, al.unsqueeze(1), au.unsqueeze(1))
+        sel_b = torch.where(nn, bl.unsqueeze(1), bu.unsqueeze(1))
+        b = b + (A * sel_b).sum(-1)
+        Ap = A * sel_a
+        if name in add:
+            Ap = Ap + cr.broadcast_pre_add(add[name], B, int(A.shape[2])).unsqueeze(1)
+        Ap.retain_grad()
+        kinks.append((A, err, Ap, (al - au).detach(), (bl - bu).detach()))
+        err = err * torch.maximum(al.abs(), au.abs()).detach().unsqueeze(1) + u32 * Ap.detach().abs()
+        A = Ap
+    eps = float(spec.perturbation.eps)
+    x0 = spec.center.double().reshape(B, 1, -1)
+    lb = (A * x0).sum(-1) - eps * A.abs().sum(-1) + b
+    loss = -lb.mean(dim=1).sum()
+    loss.backward(retain_graph=True)
+    G = torch.full((B, S), -1.0 / S, dtype=torch.float64)
+    plist = list(a.items()) + ([] if bt is None else [(("beta", k), v) for k, v in bt.items()])
+    ties = []    # (domain, element, jump)
+    # input-layer coefficients within rounding of zero
+    for d, s, j in (A.detach().abs() <= slack * err).nonzero().tolist():
+        ties.append((d, A[d, s, j], 2.0 * eps * abs(float(G[d, s]))))
+    # relaxation selects within rounding of zero
+    for Ak, ek, Apk, dal, dbl in kinks:
+        go = Apk.grad
+        for d, s, n in (Ak.detach().abs() <= slack * ek).nonzero().tolist():
+            jump = abs(float(go[d, s, n] * dal[d, n] + G[d, s] * dbl[d, n]))
+            if jump > 0.0:
+                ties.append((d, Ak[d, s, n], jump))
+    allow = _accumulate_ties(ties, plist)
+    count = len(ties)
+    allow_a = {k: allow[k].detach() for k in a}
+    allow_b = {} if bt is None else {k: allow[("beta", k)].detach() for k in bt}
+    return allow_a, allow_b, count
+
+
+def tie_allowances_for_domains(w, rec, splits, doms, with_beta):
+    """{"alpha": {name: [len(doms), ...]}, "beta": {...}}: the kink allowances of the
+    lower bound's gradient at the parameters rec["alpha"], rec["beta"] (tensors over
+    the domains of ``w``), for the listed domains (float64; chain MLPs take both
+    kinds of kink, other networks the input-layer ties); domains do not interact."""
+    from boundflow_amd import workloads as wl
+    idx = torch.tensor(doms)
+    sub = wl.Workload(w.name, w.module, spec_rows(w.spec, idx), w.C[idx], w.labels[idx],
+                      {} if splits is None else {"splits": {q: v[idx] for q, v in splits.items()}})
+    w64 = parity.to_float64(sub)
+    a64 = {q: v[idx].double() for q, v in rec["alpha"].items()}
+    b64 = {q: v[idx].double() for q, v in rec["beta"].items()} if with_beta else None
+    s64 = None if splits is None else sub.extra["splits"]
+    if all(op.op_type in ("linear", "relu") for op in w.module.get_entry_task().ops):
+        aa, bb, nt = tie_allowances(w64, a64, b64, s64)
+    else:
+        aa, bb, nt = sign_tie_allowances(w64, a64, True, beta64=b64, splits=s64)
+    return {"alpha": aa, "beta": bb}, nt
+
+
+def spec_rows(spec, idx):
+    """The rows ``idx`` of an input specification (Linf / Lp ball or box)."""
+    from boundflow_amd.spec import BoxPerturbation, InputSpec
+    p = spec.perturbation
+    if isinstance(p, BoxPerturbation):
+        return InputSpec.box(value_name=spec.value_name, lower=p.lower[idx], upper=p.upper[idx])
+    return InputSpec(value_name=spec.value_name, center=spec.center[idx], perturbation=p)

@@ -14,6 +14,7 @@ from boundflow_amd.spec import InputSpec
 from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
 from oracle import parity
+from oracle.gradients import oracle_grads, sign_tie_allowances
 from tests.golden_util import c3_box, load, t, workload_checksum
 from tests.gpu_util import announce, assert_bounds_close, assert_parity, assert_verdicts, device
 
@@ -58,95 +59,12 @@ def test_crown_cnn_box_input_matches_oracle():
     assert_verdicts(b.lower, t(g["lower"]), ref64.lower, "C3 box")
 
 
-def _oracle_grads(w, alpha, beta=None, splits=None, per_batch=True, dtype=torch.float32):
-    """Autograd gradient of L = -sum_d mean_s lb (or -mean lb) in the oracle."""
-    mod = w.module
-    spec = w.spec
-    C = w.C
-    if dtype == torch.float64:
-        w = parity.to_float64(w)
-        mod, spec, C = w.module, w.spec, w.C
-    a = {k: v.to(dtype).clone().requires_grad_(True) for k, v in alpha.items()}
-    bt = None
-    if beta is not None:
-        bt = {k: v.to(dtype).clone().requires_grad_(True) for k, v in beta.items()}
-    env, pre = cr.forward_ibp_trace(mod, spec, relu_split_state=splits)
-    add = ab.beta_to_pre_add(bt, pre, splits) if bt is not None else None
-    b = cr.crown_backward_from_trace(mod, spec, interval_env=env, relu_pre=pre, linear_spec_C=C, relu_alpha=a,
-                                     relu_pre_add_coeff_l=add)
-    loss = -b.lower.mean(dim=1).sum() if per_batch else -b.lower.mean(dim=1).mean()
-    loss.backward()
-    ga = {k: v.grad.detach() for k, v in a.items()}
-    gb = {k: v.grad.detach() for k, v in bt.items()} if bt is not None else None
-    return b, ga, gb
-
-
-def _abs_op(op):
-    """The same lazy input-layer operator over |coefficients| and |weights|: its
-    dense form is sum_k |A_k| |W_k,i|, the magnitude bound of each coefficient's sum."""
-    if isinstance(op, cr.DenseOp):
-        return cr.DenseOp(op.coeffs.abs(), op.input_shape)
-    if isinstance(op, cr.RightMatmulOp):
-        return cr.RightMatmulOp(_abs_op(op.base), op.rhs.abs())
-    if isinstance(op, cr.ReshapeOp):
-        return cr.ReshapeOp(_abs_op(op.base), op.input_shape)
-    if isinstance(op, cr.Conv2dOp):
-        return cr.Conv2dOp(_abs_op(op.base), op.weight.abs(), op.stride, op.padding, op.dilation, op.groups,
-                           op.input_shape)
-    if isinstance(op, cr.AddOp):
-        return cr.AddOp(_abs_op(op.lhs), _abs_op(op.rhs))
-    if isinstance(op, cr.SliceOp):
-        return cr.SliceOp(_abs_op(op.base), op.input_shape, op.start, op.stop)
-    raise TypeError(type(op))
+_oracle_grads = oracle_grads
 
 
 def _sign_tie_allowance(w64, alpha64, per_batch, tau=1e-5):
     allow_a, _allow_b, n = sign_tie_allowances(w64, alpha64, per_batch, tau=tau)
     return allow_a, n
-
-
-def sign_tie_allowances(w64, alpha64, per_batch, tau=1e-5, beta64=None, splits=None):
-    """Float64 bound of how far dL/dalpha (and dL/dbeta) may move when the sign of an
-    input-layer coefficient y_i (the concretization's |y_i| term, whose derivative is
-    sign(y_i)) is decided the other way.  Only coefficients with
-    |y_i| <= tau * sum_k |terms| -- inside fp32 rounding of their sum -- count;
-    flipping one changes the lower bound's gradient by 2 * eps * dy_i/dparam,
-    scaled by the loss's mean over specs (and batch when shared).  Returns
-    (alpha allowances, beta allowances, number of tied coefficients)."""
-    captured = {}
-    orig = cr.concretize_affine
-
-    def capture(spec, center, op, b):
-        captured["dense"] = op.to_dense()
-        captured["bound"] = _abs_op(op).to_dense().detach()
-        return orig(spec, center, op, b)
-
-    a = {k: v.clone().requires_grad_(True) for k, v in alpha64.items()}
-    bt = None if beta64 is None else {k: v.clone().requires_grad_(True) for k, v in beta64.items()}
-    cr.concretize_affine = capture
-    try:
-        env, pre = cr.forward_ibp_trace(w64.module, w64.spec, relu_split_state=splits)
-        add = ab.beta_to_pre_add(bt, pre, splits) if bt is not None else None
-        cr.crown_backward_from_trace(w64.module, w64.spec, interval_env=env, relu_pre=pre, linear_spec_C=w64.C,
-                                     relu_alpha=a, relu_pre_add_coeff_l=add)
-    finally:
-        cr.concretize_affine = orig
-    dense, bound = captured["dense"], captured["bound"]
-    B, S = int(dense.shape[0]), int(dense.shape[1])
-    eps = float(w64.spec.perturbation.eps)
-    scale = 1.0 / S if per_batch else 1.0 / (S * B)
-    flat = dense.reshape(-1)
-    tie = (flat.detach().abs() <= tau * bound.reshape(-1)).nonzero().flatten().tolist()
-    params = list(a.items()) + ([] if bt is None else [(("beta", k), v) for k, v in bt.items()])
-    allow = {k: torch.zeros_like(v) for k, v in params}
-    for i in tie:
-        grads = torch.autograd.grad(flat[i], [v for _k, v in params], retain_graph=True, allow_unused=True)
-        for (k, _), gr in zip(params, grads):
-            if gr is not None:
-                allow[k] += 2.0 * eps * scale * gr.abs()
-    allow_a = {k: allow[k] for k in a}
-    allow_b = {} if bt is None else {k: allow[("beta", k)] for k in bt}
-    return allow_a, allow_b, len(tie)
 
 
 def _grad_close(got, ref32, ref64, what, allowance=None):

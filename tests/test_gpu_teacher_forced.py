@@ -14,7 +14,7 @@ device, and one step is compared:
   or inside the jump allowance of a kink: where an input-layer coefficient (its
   |.| in the concretization) or a coefficient entering a ReLU relaxation (its
   sign selects the slope) is within fp32 rounding of zero, the two fp32
-  computations may take different one-sided derivatives (tests/tie_allowance.py);
+  computations may take different one-sided derivatives (oracle/gradients.py);
 * the Adam update: the device's clamped alpha_{k+1}, beta_{k+1} equal torch's
   fp32 Adam applied to the device's own gradient and the same moments, at the
   contract -- the optimiser step itself adds no error.  Against the oracle's
@@ -36,8 +36,8 @@ from oracle import alpha_beta_ref as ab
 from oracle import crown_ref as cr
 from oracle import parity
 from tests.gpu_util import announce, device
-from tests.test_gpu_conv_alpha import _oracle_grads, sign_tie_allowances
-from tests.tie_allowance import tie_allowances
+from oracle.gradients import oracle_grads as _oracle_grads
+from oracle.gradients import tie_allowances_for_domains
 
 pytestmark = pytest.mark.gpu
 
@@ -74,27 +74,9 @@ def _grad_report(got, ref32, ref64, what, allowance=None):
 def _tie_allowance(w, rec, splits, doms, with_beta):
     """{"alpha": {name: [len(doms), ...]}, "beta": {...}}: the kink allowances of the
     lower bound's gradient at this step's parameters, for the listed domains."""
-    idx = torch.tensor(doms)
-    sub = wl.Workload(w.name, w.module, _spec_rows(w.spec, idx), w.C[idx], w.labels[idx],
-                      {} if splits is None else {"splits": {q: v[idx] for q, v in splits.items()}})
-    w64 = parity.to_float64(sub)
-    a64 = {q: v[idx].double() for q, v in rec["alpha"].items()}
-    b64 = {q: v[idx].double() for q, v in rec["beta"].items()} if with_beta else None
-    s64 = None if splits is None else sub.extra["splits"]
-    if all(op.op_type in ("linear", "relu") for op in w.module.get_entry_task().ops):
-        aa, bb, nt = tie_allowances(w64, a64, b64, s64)
-    else:
-        aa, bb, nt = sign_tie_allowances(w64, a64, True, beta64=b64, splits=s64)
+    allow, nt = tie_allowances_for_domains(w, rec, splits, doms, with_beta)
     announce(f"  {nt} coefficients within fp32 rounding of zero on domains {doms[:8]}")
-    return {"alpha": aa, "beta": bb}
-
-
-def _spec_rows(spec, idx):
-    from boundflow_amd.spec import BoxPerturbation, InputSpec
-    p = spec.perturbation
-    if isinstance(p, BoxPerturbation):
-        return InputSpec.box(value_name=spec.value_name, lower=p.lower[idx], upper=p.upper[idx])
-    return InputSpec(value_name=spec.value_name, center=spec.center[idx], perturbation=p)
+    return allow
 
 
 def _adam_ref(p, g, m, v, t, lr, lo, hi):
