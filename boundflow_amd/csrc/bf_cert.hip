@@ -237,9 +237,17 @@ extern "C" int bf_split_certificate(const float* rows, int64_t row_ld, const flo
   BF_REQUIRE(row_ld >= in_dim && (split_ld >= n0 || split_ld == 0) && (center_ld >= in_dim || center_ld == 0),
              "bf_split_certificate: bad leading dimensions");
   BF_REQUIRE(rad == nullptr || rad_ld >= in_dim || rad_ld == 0, "bf_split_certificate: bad radius stride");
-  if (in_dim > 16384 || nodes > (1LL << 31) - 1 || n0 > (1LL << 30)) {
+  if (in_dim > 16384) {
     set_error("bf_split_certificate: input dimension %lld above 16384 (the LDS stage of the combined normal)",
               (long long)in_dim);
+    return BF_ERANGE;
+  }
+  if (nodes > (1LL << 31) - 1) {
+    set_error("bf_split_certificate: %lld nodes, above 2^31 - 1 (one workgroup per node)", (long long)nodes);
+    return BF_ERANGE;
+  }
+  if (n0 > (1LL << 30)) {
+    set_error("bf_split_certificate: %lld first-layer neurons, above 2^30 (32-bit split offsets)", (long long)n0);
     return BF_ERANGE;
   }
   CertAdamTable tab;

@@ -36,20 +36,32 @@ def _pair(v) -> Tuple[int, int]:
     return (v[0], v[0]) if len(v) == 1 else (v[0], v[1])
 
 
+# identity rows pulled back per launch when a conv's Jacobian is built (a 1024 x n_out block)
+JACOBIAN_CHUNK = 1024
+
+
 def _conv_jacobian(W: torch.Tensor, attrs, in_shape, out_shape) -> torch.Tensor:
-    """Rows of the conv's Jacobian, [Co*Ho*Wo, Ci*Hi*Wi]: the identity rows pulled
-    back through the transposed convolution of the library."""
+    """Rows of the conv's Jacobian, [Co*Ho*Wo, Ci*Hi*Wi]: identity rows pulled back
+    through the transposed convolution of the library, JACOBIAN_CHUNK rows at a
+    time (the identity block of a chunk is the only temporary)."""
     Co, Ho, Wo = out_shape
     Ci, Hi, Wi = in_shape
     KH, KW = int(W.shape[2]), int(W.shape[3])
     sh, sw = _pair(attrs.get("stride", 1))
     ph, pw = _pair(attrs.get("padding", 0))
     n_out = Co * Ho * Wo
-    eye = torch.eye(n_out, device=W.device, dtype=torch.float32)
     rows = torch.empty(n_out, Ci * Hi * Wi, device=W.device, dtype=torch.float32)
-    _lib.call("bf_conv_transpose_rows", _lib.ptr(eye), None, n_out, Co, Ho, Wo, _lib.ptr(W.contiguous()), Ci, KH, KW,
-              sh, sw, ph, pw, Hi, Wi, _lib.ptr(rows), None, 1, None, 0, 0, None, None, None, None,
-              _lib.stream_handle())
+    Wc = W.contiguous()
+    stream = _lib.stream_handle()
+    block = torch.empty(min(JACOBIAN_CHUNK, n_out), n_out, device=W.device, dtype=torch.float32)
+    for r0 in range(0, n_out, JACOBIAN_CHUNK):
+        m = min(JACOBIAN_CHUNK, n_out - r0)
+        eye = block[:m]
+        eye.zero_()
+        eye.diagonal(offset=r0).fill_(1.0)
+        _lib.call("bf_conv_transpose_rows", _lib.ptr(eye), None, m, Co, Ho, Wo, _lib.ptr(Wc), Ci, KH, KW,
+                  sh, sw, ph, pw, Hi, Wi, _lib.ptr(rows[r0:r0 + m]), None, 1, None, 0, 0, None, None, None, None,
+                  stream)
     return rows
 
 
@@ -71,6 +83,8 @@ def first_layer_sources(module, spec: InputSpec, relu_shapes: Dict[str, Tuple[in
             continue
         W = params.get(prod.inputs[1])
         b = params.get(prod.inputs[2]) if len(prod.inputs) == 3 else None
+        if prod.op_type == "linear" and len(prod.inputs) == 3 and b is None:
+            continue   # a named bias missing from the parameters: the reference skips the layer (:306-308)
         n = 1
         for d in relu_shapes[x]:
             n *= int(d)

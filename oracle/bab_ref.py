@@ -159,6 +159,9 @@ def _pick_branch(module, spec, split: Dict[str, torch.Tensor]) -> Optional[Tuple
 def solve_bab_mlp(module, input_spec, *, linear_spec_C, config) -> dict:
     cfg = dict(config)
     spec = normalize_input_spec(input_spec)
+    # bab.py:656-659: the alpha oracle does not take conv graphs
+    if any(op.op_type in ("conv2d", "flatten") for op in module.get_entry_task().ops) and cfg["oracle"] != "alpha_beta":
+        raise NotImplementedError("alpha-only BaB does not yet support conv graphs")
     E = int(spec.center.shape[0])
     _env, pre0 = forward_ibp_trace(module, _slice_spec(spec, [0]))
     shapes = {k: tuple(int(d) for d in v.lower.shape[1:]) for k, v in pre0.items()}

@@ -248,3 +248,89 @@ def spec_rows(spec, idx):
     if isinstance(p, BoxPerturbation):
         return InputSpec.box(value_name=spec.value_name, lower=p.lower[idx], upper=p.upper[idx])
     return InputSpec(value_name=spec.value_name, center=spec.center[idx], perturbation=p)
+
+
+def permuted_oracle_grads(w, alpha, beta, splits, seed: int):
+    """fp32 gradients of L = -sum_d mean_s lb (``oracle_grads``) computed on the same
+    network with its hidden units, conv channels and input features permuted by a
+    seeded permutation, returned in the original order ({(kind, name): [B, n]}), or
+    None for networks other than chains of linear / conv2d / relu / flatten; key
+    "lower" holds the lower bound [B, S] (unchanged by the permutation).  The
+    function is unchanged, but every contraction of the forward trace, the backward
+    pass and the concretization sums in another order, so the spread of these
+    gradients around the fp64 one measures the fp32 rounding of the computation."""
+    from boundflow_amd import workloads as wl
+    from boundflow_amd.ir import BFTaskModule
+    from boundflow_amd.spec import BoxPerturbation, InputSpec
+
+    task = w.module.get_entry_task()
+    if any(op.op_type not in ("linear", "conv2d", "relu", "flatten") for op in task.ops):
+        return None
+    spec = w.spec
+    x = spec.center
+    if x.dim() not in (2, 4):
+        return None
+    g = torch.Generator().manual_seed(int(seed))
+    env, _pre = cr.forward_ibp_trace(w.module, spec, relu_split_state=splits)
+    relu_inputs = {op.inputs[0] for op in task.ops if op.op_type == "relu"}
+    B = int(x.shape[0])
+
+    def shape_of(name):
+        return tuple(int(d) for d in (x if name == spec.value_name else env[name].lower).shape[1:])
+
+    def flat_of(name):
+        """Permutation of the flattened features of a value."""
+        kind, pv = perm[name]
+        if kind == "flat":
+            return pv
+        sh = shape_of(name)
+        hw = sh[1] * sh[2]
+        return (pv.reshape(-1, 1) * hw + torch.arange(hw).reshape(1, -1)).reshape(-1)
+
+    # ("flat", perm of features) or ("chan", perm of channels) per value
+    perm = {spec.value_name: ("flat", torch.randperm(int(x.shape[1]), generator=g)) if x.dim() == 2
+            else ("chan", torch.randperm(int(x.shape[1]), generator=g))}
+    params = dict(w.module.params)
+    for op in task.ops:
+        src, out = op.inputs[0], op.outputs[0]
+        hidden = out in relu_inputs
+        if op.op_type in ("linear", "conv2d"):
+            W = w.module.params[op.inputs[1]]
+            n = int(W.shape[0])
+            po = torch.randperm(n, generator=g) if hidden else torch.arange(n)
+            if op.op_type == "linear":
+                params[op.inputs[1]] = W[po][:, flat_of(src)].contiguous()
+                perm[out] = ("flat", po)
+            else:
+                if perm[src][0] != "chan":
+                    return None
+                params[op.inputs[1]] = W[po][:, perm[src][1]].contiguous()
+                perm[out] = ("chan", po)
+            if len(op.inputs) == 3:
+                params[op.inputs[2]] = w.module.params[op.inputs[2]][po].contiguous()
+        elif op.op_type == "relu":
+            perm[out] = perm[src]
+        else:   # flatten
+            perm[out] = ("flat", flat_of(src))
+
+    def fwd(t, name):
+        return t.reshape(B, -1)[:, flat_of(name)].reshape(t.shape).contiguous()
+
+    p = spec.perturbation
+    if isinstance(p, BoxPerturbation):
+        pspec = InputSpec.box(value_name=spec.value_name, lower=fwd(p.lower, spec.value_name),
+                              upper=fwd(p.upper, spec.value_name))
+    else:
+        pspec = InputSpec(value_name=spec.value_name, center=fwd(x, spec.value_name), perturbation=p)
+    mod = BFTaskModule(tasks=w.module.tasks, entry_task_id=w.module.entry_task_id, bindings={"params": params})
+    pw = wl.Workload(w.name, mod, pspec, w.C, w.labels, {})
+    pa = {k: fwd(v, k) for k, v in alpha.items()}
+    pb = None if beta is None else {k: fwd(v, k) for k, v in beta.items()}
+    ps = None if splits is None else {k: fwd(v, k) for k, v in splits.items()}
+    bounds, ga, gb = oracle_grads(pw, pa, pb, ps, dtype=torch.float32)
+    out = {"lower": bounds.lower.detach().double()}
+    for kind, gd in (("alpha", ga), ("beta", gb or {})):
+        for k, v in gd.items():
+            inv = torch.argsort(flat_of(k))
+            out[(kind, k)] = v.reshape(B, -1)[:, inv].double()
+    return out

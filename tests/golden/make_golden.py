@@ -254,9 +254,11 @@ from tests.golden_util import BAB_SOLVE_CASES  # noqa: E402
 
 
 def count_certificates():
-    """Wrap the reference's certificate to count the nodes it closes (for the fixtures' records)."""
+    """Wrap the reference's certificate to count the nodes it closes and the calls that
+    evaluate at least one first-layer halfspace (for the fixtures' records)."""
     orig = rabc._is_infeasible_split_first_layer_convex_combo
-    box = {"calls": 0, "closed": 0}
+    orig_collect = rabc._collect_first_layer_split_halfspaces
+    box = {"calls": 0, "closed": 0, "halfspace_calls": 0}
 
     def wrapped(module, spec, *, relu_split_state, **kw):
         out = orig(module, spec, relu_split_state=relu_split_state, **kw)
@@ -264,8 +266,18 @@ def count_certificates():
         box["closed"] += int(bool(out[0]))
         return out
 
+    def collect(*a, **kw):
+        hs = orig_collect(*a, **kw)
+        box["halfspace_calls"] += int(len(hs) > 0)
+        return hs
+
     rabc._is_infeasible_split_first_layer_convex_combo = wrapped
-    return box, lambda: setattr(rabc, "_is_infeasible_split_first_layer_convex_combo", orig)
+    rabc._collect_first_layer_split_halfspaces = collect
+
+    def restore():
+        rabc._is_infeasible_split_first_layer_convex_combo = orig
+        rabc._collect_first_layer_split_halfspaces = orig_collect
+    return box, restore
 
 
 def golden_bab_solve(tag):
@@ -273,7 +285,7 @@ def golden_bab_solve(tag):
     from boundflow.runtime.bab import BabConfig as RBabConfig
     from boundflow.runtime.bab import solve_bab_mlp as r_solve
     toy, kw = BAB_SOLVE_CASES[tag]
-    w = wl.make_bab_toy(**toy)
+    w = wl.make_bab_case(**toy)
     counts, restore = count_certificates()
     try:
         res = r_solve(to_ref_module(w.module), to_ref_spec(w.spec), linear_spec_C=w.C, config=RBabConfig(**kw))
@@ -292,6 +304,43 @@ def golden_bab_solve(tag):
          per_best_lower=np.array([r.best_lower for r in per]),
          per_best_upper=np.array([r.best_upper for r in per]),
          certificate_calls=counts["calls"], certificate_closed=counts["closed"],
+         certificate_halfspace_calls=counts["halfspace_calls"], checksum=workload_checksum(w))
+
+
+def golden_cert_conv(tag):
+    """The reference's first-layer certificate (_is_infeasible_split_first_layer_convex_combo,
+    alpha_beta_crown.py:391-532) on C3's first conv layer (3x32x32 input, 16x16x16
+    neurons), one node per call with one split neuron: a split against a stable neuron's
+    sign is infeasible by itself ("single_halfspace_max_negative", with its max_value), one
+    with the sign or on an ambiguous neuron is not.  24 nodes over the first 8 inputs."""
+    w = wl.subset(wl.make_c3(), 8)
+    rm = to_ref_module(w.module)
+    with torch.inference_mode():
+        _env, pre = rci._forward_ibp_trace_mlp(rm, to_ref_spec(w.spec))
+    lo = pre["h0"].lower.reshape(8, -1)
+    hi = pre["h0"].upper.reshape(8, -1)
+    g = torch.Generator().manual_seed(41)
+    rows = []
+    for e in range(8):
+        pos = (lo[e] > 0).nonzero().flatten()
+        neg = (hi[e] < 0).nonzero().flatten()
+        amb = ((lo[e] < 0) & (hi[e] > 0)).nonzero().flatten()
+        pick = lambda t: int(t[int(torch.randint(0, int(t.numel()), (1,), generator=g))])  # noqa: E731
+        rows.append((e, pick(pos), -1))                      # against the sign: infeasible
+        rows.append((e, pick(neg), 1 if e % 2 == 0 else -1))   # +1 infeasible, -1 with the sign
+        rows.append((e, pick(amb) if amb.numel() else pick(pos), 1 if e % 2 else -1))
+    flags, values = [], []
+    for e, n, sg in rows:
+        split = torch.zeros(1, 16 * 16 * 16, dtype=torch.int8)
+        split[0, n] = sg
+        spec = RSpec.linf(value_name="input", center=w.spec.center[e:e + 1], eps=float(w.spec.perturbation.eps))
+        ok, _reason, cert = rabc._is_infeasible_split_first_layer_convex_combo(
+            rm, spec, relu_split_state={"h0": split.reshape(1, 16, 16, 16)})
+        flags.append(int(bool(ok)))
+        values.append(float(cert["max_value"]) if cert is not None else float("nan"))
+    print(tag, "infeasible", sum(flags), "of", len(rows))
+    save(tag, example=np.array([r[0] for r in rows]), neuron=np.array([r[1] for r in rows]),
+         sign=np.array([r[2] for r in rows]), flag=np.array(flags), max_value=np.array(values),
          checksum=workload_checksum(w))
 
 
@@ -444,6 +493,9 @@ GOLDENS = [
     ("bab_solve_1d", golden_bab_solve),
     ("bab_solve_obj_both", golden_bab_solve),
     ("bab_solve_obj_alpha_gap", golden_bab_solve),
+    ("bab_solve_cnn_b1", golden_bab_solve),
+    ("bab_solve_cnn_b4", golden_bab_solve),
+    ("cert_c3_conv", golden_cert_conv),
     ("frontend_planned", golden_frontend),
     ("vnnlib_queries", golden_vnnlib),
     ("objectives_mlp", golden_objectives),

@@ -55,6 +55,14 @@ BAB_SOLVE_CASES = {
                                                 ub_weight=0.5)),
     "bab_solve_obj_alpha_gap": (dict(eps=0.05), dict(max_nodes=20, oracle="alpha", node_batch_size=1,
                                                      alpha_steps=10, objective="gap", spec_reduce="min")),
+    # conv graphs (make_bab_cnn_toy: conv 2x6x6 -> 2x4x4, fc 16, fc 3).  Each example has at most
+    # one ambiguous first-layer (conv) neuron, so a node carries at most one first-layer split:
+    # the reference's certificate evaluates the conv row's halfspace (alpha_beta_crown.py:345-389)
+    # and does not reach its multi-halfspace stack, which cannot broadcast conv rows.
+    "bab_solve_cnn_b1": (dict(kind="cnn", seed=2, eps=0.01, channels=2, hidden=16, conv_bias_std=1.0),
+                         dict(max_nodes=30, oracle="alpha_beta", node_batch_size=1, alpha_steps=5)),
+    "bab_solve_cnn_b4": (dict(kind="cnn", seed=4, eps=0.02, channels=2, hidden=16, conv_bias_std=1.0),
+                         dict(max_nodes=30, oracle="alpha_beta", node_batch_size=4, alpha_steps=5)),
 }
 
 

@@ -29,7 +29,7 @@ def test_hip_bab_search_matches_reference(tag):
     toy, kw = CASES[tag]
     announce(f"solve_bab_mlp {tag}")
     g = load(tag)
-    wd = wl.to_device(wl.make_bab_toy(**toy), dev)
+    wd = wl.to_device(wl.make_bab_case(**toy), dev)
     r = hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C, config=hbab.BabConfig(**kw))
     per = r.per_example
     announce(f"  statuses {[p.status for p in per]} visited {[p.nodes_visited for p in per]} "
@@ -63,3 +63,12 @@ def test_hip_bab_frontier_growth_and_budget():
     assert all(p.status in ("proven", "unsafe", "unknown") for p in r.per_example)
     assert all(p.nodes_visited <= 60 for p in r.per_example)
     assert r.max_queue >= 1 and r.batch_rounds >= 1
+
+
+def test_alpha_oracle_refuses_conv_graphs():
+    """The reference's alpha-only BaB does not take conv graphs (bab.py:656-659)."""
+    dev = device()
+    announce("solve_bab_mlp alpha oracle on a conv graph")
+    wd = wl.to_device(wl.make_bab_cnn_toy(seed=2, eps=0.01, channels=2, hidden=16, conv_bias_std=1.0), dev)
+    with pytest.raises(NotImplementedError, match="alpha-only BaB does not yet support conv graphs"):
+        hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C, config=hbab.BabConfig(oracle="alpha"))

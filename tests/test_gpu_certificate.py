@@ -107,3 +107,68 @@ def test_matches_oracle_on_random_2d_sets():
     announce(f"  infeasible: hip {sum(got)}, oracle {sum(ref)}")
     assert sum(ref) >= 4
     assert got == ref
+
+
+def test_conv_first_layer_matches_the_reference_fixture():
+    """C3's first conv layer (3x32x32 input: a 12 KB LDS stage; 16x16x16 neurons, the
+    Jacobian rows made by the transposed convolution in chunks): 24 nodes with one split
+    neuron each, in one launch, against the reference's certificate
+    (_is_infeasible_split_first_layer_convex_combo, fixture cert_c3_conv): identical
+    flags, the reference's max_value where it closes a node, and the single halfspace's
+    maximum (fp64, from the conv's Jacobian row) on every node."""
+    from tests.golden_util import load, workload_checksum
+    dev = device()
+    announce("split certificate, C3 first conv layer, 24 nodes, vs reference fixture")
+    g = load("cert_c3_conv")
+    w = wl.subset(wl.make_c3(), 8)
+    assert workload_checksum(w) == str(g["checksum"])
+    ex = torch.as_tensor(g["example"]).long()
+    N = int(ex.numel())
+    split = torch.zeros(N, 16 * 16 * 16, dtype=torch.int8)
+    split[torch.arange(N), torch.as_tensor(g["neuron"]).long()] = torch.as_tensor(g["sign"]).to(torch.int8)
+    eps = float(w.spec.perturbation.eps)
+    spec = InputSpec.linf(value_name="input", center=w.spec.center[ex].to(dev), eps=eps)
+    wd = wl.to_device(w, dev)
+    value = torch.empty(N, device=dev)
+    flags = split_certificate(wd.module, spec, {"h0": split.reshape(N, 16, 16, 16).to(dev)}, {"h0": (16, 16, 16)},
+                              max_out=value).cpu()
+    value = value.cpu().double()
+    assert flags.tolist() == [int(f) for f in g["flag"]], (flags.tolist(), g["flag"].tolist())
+    W, b = w.module.params["W0"].double(), w.module.params["b0"].double()
+    worst = 0.0
+    for k in range(N):
+        n, s = int(g["neuron"][k]), int(g["sign"][k])
+        one = torch.zeros(1, 16, 16, 16, dtype=torch.float64)
+        one.view(-1)[n] = 1.0
+        row = torch.nn.functional.conv_transpose2d(one, W, stride=2, padding=1).reshape(-1)
+        vmax = s * (float(row @ w.spec.center[int(ex[k])].double().reshape(-1)) + float(b[n // 256])) \
+            + eps * float(row.abs().sum())
+        worst = max(worst, abs(float(value[k]) - vmax))
+        assert abs(float(value[k]) - vmax) <= 1e-5 * abs(vmax) + 1e-5, (k, float(value[k]), vmax)
+        if int(g["flag"][k]):
+            ref = float(g["max_value"][k])
+            assert abs(float(value[k]) - ref) <= 1e-5 * abs(ref) + 1e-5, (k, float(value[k]), ref)
+    announce(f"  closed {int(flags.sum())}/{N} (reference {int(g['flag'].sum())}), max |value - fp64| {worst:.2e}")
+
+
+def test_conv_first_layer_two_or_more_splits_match_oracle_and_lp():
+    """Two to four split neurons on a conv first layer (where the reference's stacking
+    of conv rows cannot broadcast): the device verdicts equal the oracle's, and every
+    node the device closes has no point in the box (exact LP on the conv's Jacobian)."""
+    from tests.test_oracle_certificate import _conv_lp_trials, _lp_feasible, conv_jacobian
+    dev = device()
+    announce("split certificate, conv first layer, 2-4 splits per node, vs oracle and LP")
+    got, ref = [], []
+    for trial, W, b, m, spec, sp, split in _conv_lp_trials(31, 80):
+        ref.append(int(ab.split_certificate(m, spec, sp)[0]))
+        sd = InputSpec.linf(value_name="input", center=spec.center.to(dev), eps=1.0)
+        oshape = tuple(sp["h1"].shape[1:])
+        flag = int(split_certificate(_to(m, dev), sd, {"h1": sp["h1"].to(dev)}, {"h1": oshape}).cpu()[0])
+        got.append(flag)
+        if flag:
+            J, off = conv_jacobian(W, b, (1, 3, 3))
+            rows = split[0].nonzero().flatten()
+            assert not _lp_feasible(J[rows].numpy(), off[rows].numpy(), [-1.0] * 9, [1.0] * 9), trial
+    announce(f"  infeasible: hip {sum(got)}, oracle {sum(ref)} of {len(got)}")
+    assert sum(ref) >= 3
+    assert got == ref

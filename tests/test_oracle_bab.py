@@ -31,7 +31,7 @@ def config(tag):
 def test_bab_search_matches_reference(tag):
     g = load(tag)
     toy, cfg = config(tag)
-    w = wl.make_bab_toy(**toy)
+    w = wl.make_bab_case(**toy)
     assert workload_checksum(w) == str(g["checksum"])
     r = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
     assert CODE[r["status"]] == int(g["status"])
@@ -62,7 +62,7 @@ def _margins(w, x):
 def test_bab_verdicts_are_sound(tag):
     toy, cfg = config(tag)
     eps = toy["eps"]
-    w = wl.make_bab_toy(**toy)
+    w = wl.make_bab_case(**toy)
     r = bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config=cfg)
     x0 = w.spec.center.double()
     g = torch.Generator().manual_seed(9)
@@ -168,3 +168,10 @@ def test_alpha_crown_objectives_match_reference(case):
     np.testing.assert_allclose(b.upper.detach().numpy(), g[f"{case}_upper"], rtol=1e-5, atol=1e-6)
     for n, a in alpha.items():
         np.testing.assert_allclose(a.numpy(), g[f"{case}_alpha_{n}"], rtol=1e-5, atol=1e-6)
+
+
+def test_alpha_oracle_refuses_conv_graphs():
+    """bab.py:656-659: the alpha-only search does not take conv graphs."""
+    w = wl.make_bab_cnn_toy(seed=2, eps=0.01, channels=2, hidden=16, conv_bias_std=1.0)
+    with pytest.raises(NotImplementedError, match="alpha-only BaB does not yet support conv graphs"):
+        bab_ref.solve_bab_mlp(w.module, w.spec, linear_spec_C=w.C, config={**DEFAULTS, "oracle": "alpha"})

@@ -187,3 +187,131 @@ def test_lp_ball_infeasible_verdicts_are_sound(p):
             inside = ((pts @ w.double().t() + b.double()) >= 0).all(dim=1)
             assert not bool(inside.any()), f"trial {trial}: certificate on a set with a point in the ball"
     assert found >= 1
+
+
+# ---------------------------------------------------------------------------
+# conv first layers (alpha_beta_crown.py:345-389: a conv row is the one-hot output
+# neuron pulled back through the conv)
+
+
+def conv_first_layer_module(W, b):
+    """input -> conv2d(W, b, stride 1, no padding) -> relu -> flatten -> identity linear."""
+    Co, Ci, KH, KW = (int(d) for d in W.shape)
+    task = BoundTask(task_id="t0", kind=TaskKind.INTERVAL_IBP, ops=[
+        TaskOp("conv2d", "conv1", ["input", "W1", "b1"], ["h1"], {"stride": 1, "padding": 0, "dilation": 1,
+                                                                   "groups": 1}),
+        TaskOp("relu", "relu1", ["h1"], ["r1"]),
+        TaskOp("flatten", "flatten", ["r1"], ["f1"], {"start_dim": 1, "end_dim": -1}),
+        TaskOp("linear", "linear2", ["f1", "W2", "b2"], ["out"]),
+    ], input_values=["input"], output_values=["out"])
+    return task, Co
+
+
+def _conv_module(W, b, in_shape):
+    task, Co = conv_first_layer_module(W, b)
+    ho = in_shape[1] - int(W.shape[2]) + 1
+    wo = in_shape[2] - int(W.shape[3]) + 1
+    n = Co * ho * wo
+    return BFTaskModule(tasks=[task], entry_task_id="t0",
+                        bindings={"params": {"W1": W, "b1": b, "W2": torch.eye(n), "b2": torch.zeros(n)}}), (Co, ho, wo)
+
+
+def conv_jacobian(W, b, in_shape):
+    """[n_out, I] rows and [n_out] offsets of conv2d (stride 1, no padding), by autograd in fp64."""
+    x = torch.zeros((1,) + tuple(in_shape), dtype=torch.float64)
+    f = lambda z: torch.nn.functional.conv2d(z, W.double(), b.double()).reshape(-1)  # noqa: E731
+    J = torch.autograd.functional.jacobian(f, x).reshape(-1, x.numel())
+    return J, f(x).detach()
+
+
+def test_conv_halfspaces_are_the_conv_jacobian_rows():
+    g = torch.Generator().manual_seed(6)
+    in_shape = (2, 5, 4)
+    W = torch.randn(3, 2, 3, 2, generator=g)
+    b = torch.randn(3, generator=g)
+    m, oshape = _conv_module(W, b, in_shape)
+    n = oshape[0] * oshape[1] * oshape[2]
+    spec = InputSpec.linf(value_name="input", center=torch.rand((1,) + in_shape, generator=g), eps=0.1)
+    split = torch.zeros((1,) + oshape, dtype=torch.int8)
+    picks = [0, 5, n - 1, 7]
+    for i, p in enumerate(picks):
+        split.view(-1)[p] = 1 if i % 2 == 0 else -1
+    hs = ab.first_layer_split_halfspaces(m, spec, {"h1": split})
+    J, off = conv_jacobian(W, b, in_shape)
+    assert [h[1] for h in hs] == sorted(picks)
+    for name, idx, a, c in hs:
+        s = float(split.view(-1)[idx])
+        assert name == "h1"
+        assert torch.allclose(a.double(), s * J[idx], atol=1e-6)
+        assert abs(float(c) - s * float(off[idx])) < 1e-6
+
+
+def test_conv_certificate_matches_the_reference_fixture():
+    """C3's first conv layer, one split neuron per node: the reference's flags, and its
+    single-halfspace max_value where it closes the node (against the same maximum in
+    fp64 from the conv's Jacobian row: s (r . x0 + b) + eps ||r||_1)."""
+    from boundflow_amd import workloads as wl
+    from tests.golden_util import load, workload_checksum
+    g = load("cert_c3_conv")
+    w = wl.subset(wl.make_c3(), 8)
+    assert workload_checksum(w) == str(g["checksum"])
+    eps = float(w.spec.perturbation.eps)
+    W, b = w.module.params["W0"], w.module.params["b0"]
+    for k in range(len(g["flag"])):
+        e, n, s = int(g["example"][k]), int(g["neuron"][k]), int(g["sign"][k])
+        split = torch.zeros(1, 16, 16, 16, dtype=torch.int8)
+        split.view(-1)[n] = s
+        spec = InputSpec.linf(value_name="input", center=w.spec.center[e:e + 1], eps=eps)
+        got = ab.split_certificate(w.module, spec, {"h0": split})[0]
+        assert int(got) == int(g["flag"][k]), k
+        # the single halfspace's maximum over the ball, in fp64
+        one = torch.zeros(1, 16, 16, 16, dtype=torch.float64)
+        one.view(-1)[n] = 1.0
+        row = torch.nn.functional.conv_transpose2d(one, W.double(), stride=2, padding=1).reshape(-1)
+        ch = n // 256
+        vmax = s * (float(row @ w.spec.center[e].double().reshape(-1)) + float(b[ch])) + eps * float(row.abs().sum())
+        if int(g["flag"][k]):
+            assert abs(float(g["max_value"][k]) - vmax) <= 1e-5 * abs(vmax) + 1e-5, (k, float(g["max_value"][k]), vmax)
+        assert (vmax < -1e-6) == bool(g["flag"][k])
+
+
+def _conv_lp_trials(seed, trials):
+    """Random conv first layers on a 1x3x3 input in the box [-1, 1]^9 with 2-4 split
+    neurons each (each halfspace feasible alone: the IBP trace passes)."""
+    g = torch.Generator().manual_seed(seed)
+    in_shape = (1, 3, 3)
+    for trial in range(trials):
+        W = torch.randn(3, 1, 2, 2, generator=g)
+        b = torch.randn(3, generator=g) * 0.6 - 0.9
+        m, oshape = _conv_module(W, b, in_shape)
+        n = oshape[0] * oshape[1] * oshape[2]
+        k = int(torch.randint(2, 5, (1,), generator=g))
+        split = torch.zeros(1, n, dtype=torch.int8)
+        split[0, torch.randperm(n, generator=g)[:k]] = 1
+        spec = InputSpec.linf(value_name="input", center=torch.zeros((1,) + in_shape), eps=1.0)
+        sp = {"h1": split.reshape((1,) + oshape)}
+        try:
+            cr.forward_ibp_trace(m, spec, relu_split_state=sp)
+        except ValueError:
+            continue
+        yield trial, W, b, m, spec, sp, split
+
+
+def test_conv_certificate_verdicts_are_sound_against_an_lp():
+    """Two or more split neurons on a conv first layer (where the reference's stacking of
+    conv rows cannot broadcast): every set the oracle closes has no point in the box
+    (exact LP on the conv's Jacobian rows), and the verdicts equal those of the same
+    halfspaces written as a linear first layer (the path the reference's known answers pin)."""
+    found = 0
+    for trial, W, b, m, spec, sp, split in _conv_lp_trials(31, 80):
+        got = ab.split_certificate(m, spec, sp)[0]
+        J, off = conv_jacobian(W, b, (1, 3, 3))
+        rows = split[0].nonzero().flatten()
+        lin = first_layer_module(J.float(), off.float())
+        lin_spec = InputSpec.linf(value_name="input", center=torch.zeros(1, 9), eps=1.0)
+        assert got == ab.split_certificate(lin, lin_spec, {"h1": split})[0], trial
+        if got:
+            found += 1
+            feas = _lp_feasible(J[rows].numpy(), off[rows].numpy(), [-1.0] * 9, [1.0] * 9)
+            assert not feas, f"trial {trial}: certificate on a feasible conv halfspace set"
+    assert found >= 3, found
