@@ -27,6 +27,20 @@ from .profiling import launch as _timed
 from .spec import BoxPerturbation, IntervalState, input_norm_p
 
 
+
+def packed_conv_transpose_weights(W: torch.Tensor, Co: int, Ho: int, Wo: int, Ci: int, KH: int, KW: int, sh: int,
+                                  sw: int, ph: int, pw: int, Hi: int, Wi: int, source=None) -> torch.Tensor:
+    """The weights of the channel-last transposed convolution in its LDS order
+    (bf_conv_transpose_pack_weights), made once per weight tensor and geometry and kept
+    across queries (``source``: the tensor they derive from, default W)."""
+    geo = (Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi)
+
+    def pack():
+        out = torch.empty(int(_lib.load().bf_conv_transpose_packed_floats(*geo)), device=W.device)
+        _lib.call("bf_conv_transpose_pack_weights", _lib.ptr(W), *geo, _lib.ptr(out), _lib.stream_handle())
+        return out
+    return derived("conv_t_pack:" + "x".join(str(v) for v in geo), (W if source is None else source,), pack)
+
 def _numel(shape) -> int:
     n = 1
     for d in shape:
@@ -103,13 +117,8 @@ def conv_backward_step(layer, is_first, A_u, A_l, stride, b_u, b_l, B, S, pre_lo
         nb_u = torch.empty(M, device=dev) if A_u is not None else None
         nb_l = torch.empty(M, device=dev) if A_l is not None else None
         keep_l = torch.empty_like(A_l) if (save is not None and A_l is not None) else None
-        geo = (Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi)
-
-        def pack():
-            out = torch.empty(int(_lib.load().bf_conv_transpose_packed_floats(*geo)), device=dev)
-            _lib.call("bf_conv_transpose_pack_weights", _lib.ptr(W), *geo, _lib.ptr(out), stream)
-            return out
-        packed = derived("conv_t_pack:" + "x".join(str(v) for v in geo), (layer.weight,), pack)
+        packed = packed_conv_transpose_weights(W, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi,
+                                               source=layer.weight)
         with _timed("crown_relu_conv_transpose", flops,
                     4.0 * nz * (M * n_out + M * n_in) + (4.0 * M * n_out if keep_l is not None else 0.0)):
             _lib.call("bf_crown_relu_conv_transpose", _lib.ptr(A_u), _lib.ptr(A_l), B, S, Co, Ho, Wo, _lib.ptr(pre_lo),

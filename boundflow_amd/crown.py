@@ -690,9 +690,28 @@ def _input_radius(pert, B: int, P: int):
     return None, float(pert.eps)
 
 
-def _check_alpha_beta_args(relu_pre_add_coeff_u):
-    if relu_pre_add_coeff_u:
-        raise NotImplementedError("relu_pre_add_coeff_u is not used by the alpha-beta objective and unsupported")
+def _with_upper_add(backward, relu_pre, C, add_l, add_u, B: int, out_dim: int) -> IntervalState:
+    """Both bounds with the split terms of the lower (``add_l``) and upper (``add_u``)
+    coefficients.  With ``add_u`` (crown_ibp.py:1270-1278: added to A_u after its
+    relaxation, rank-2 pre-activations only, :1256-1260) the upper bound is minus the
+    lower bound of -C with the term -add_u: every step of that pass is the upper pass's
+    arithmetic with each value negated (the relaxation select A >= 0 differs only where
+    A = 0, whose products are zero), so its results are the upper pass's, negated."""
+    if not add_u:
+        return backward(C, add_l, True, True)
+    for name, v in add_u.items():
+        pre = relu_pre.get(name)
+        if pre is not None and pre.lower.dim() != 2:
+            raise NotImplementedError(
+                f"run_crown_ibp_mlp only supports relu_pre_add_coeff_u on rank-2 pre-activations; got "
+                f"{tuple(pre.lower.shape)} for {name}")
+    if C is None:
+        dev = next(iter(relu_pre.values())).lower.device if relu_pre else None
+        C = torch.eye(out_dim, device=dev).unsqueeze(0).expand(B, out_dim, out_dim).contiguous()
+    lower = backward(C, add_l, False, True).lower
+    neg_add = {k: -v for k, v in add_u.items()}
+    upper = -backward(-C, neg_add, False, True).lower
+    return IntervalState(lower=lower, upper=upper)
 
 
 def run_crown_ibp_mlp(
@@ -709,19 +728,25 @@ def run_crown_ibp_mlp(
     """HIP counterpart of run_crown_ibp_mlp (crown_ibp.py:2054-2133).  Chains run the
     fused region kernels; DAG tasks (add, concat, fan-out) the general backward of
     ``crown_dag``."""
-    _check_alpha_beta_args(relu_pre_add_coeff_u)
     spec = normalize_input_spec(input_spec)
     try:
         chain_full = parse_chain(module, spec)
     except NotAChain:
-        from .crown_dag import run_crown_ibp_dag
-        return run_crown_ibp_dag(module, spec, linear_spec_C=linear_spec_C, output_value=output_value,
-                                 relu_alpha=relu_alpha, relu_pre_add_coeff_l=relu_pre_add_coeff_l,
-                                 relu_split_state=relu_split_state)
+        from .crown_dag import forward_ibp_trace_dag
+        trace = forward_ibp_trace_dag(module, spec, relu_split_state=relu_split_state)
+        return run_crown_ibp_mlp_from_forward_trace(module, spec, trace=trace, linear_spec_C=linear_spec_C,
+                                                    output_value=output_value, relu_alpha=relu_alpha,
+                                                    relu_pre_add_coeff_u=relu_pre_add_coeff_u,
+                                                    relu_pre_add_coeff_l=relu_pre_add_coeff_l)
     trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain_full)
     chain = parse_chain(module, spec, output_value) if output_value is not None else chain_full
-    return crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=relu_alpha,
-                          relu_pre_add_coeff_l=relu_pre_add_coeff_l)
+
+    def backward(C, add_l, need_upper, need_lower):
+        return crown_backward(module, spec, trace, chain=chain, linear_spec_C=C, relu_alpha=relu_alpha,
+                              relu_pre_add_coeff_l=add_l, need_upper=need_upper, need_lower=need_lower)
+
+    return _with_upper_add(backward, trace.relu_pre, linear_spec_C, relu_pre_add_coeff_l, relu_pre_add_coeff_u,
+                           int(spec.center.shape[0]), _numel(chain.layers[-1].out_shape))
 
 
 def run_crown_ibp_mlp_from_forward_trace(
@@ -736,15 +761,27 @@ def run_crown_ibp_mlp_from_forward_trace(
     relu_pre_add_coeff_l: Optional[Dict[str, torch.Tensor]] = None,
 ) -> IntervalState:
     """HIP counterpart of run_crown_ibp_mlp_from_forward_trace (crown_ibp.py:2136-2199)."""
-    _check_alpha_beta_args(relu_pre_add_coeff_u)
     spec = normalize_input_spec(input_spec)
     from .crown_dag import DagTrace, crown_backward_dag
+    B = int(spec.center.shape[0])
     if isinstance(trace, DagTrace):
-        return crown_backward_dag(module, spec, trace, linear_spec_C=linear_spec_C, output_value=output_value,
-                                  relu_alpha=relu_alpha, relu_pre_add_coeff_l=relu_pre_add_coeff_l)
+        out = output_value or module.get_entry_task().output_values[0]
+
+        def backward(C, add_l, need_upper, need_lower):
+            return crown_backward_dag(module, spec, trace, linear_spec_C=C, output_value=output_value,
+                                      relu_alpha=relu_alpha, relu_pre_add_coeff_l=add_l, need_upper=need_upper,
+                                      need_lower=need_lower)
+
+        return _with_upper_add(backward, trace.relu_pre, linear_spec_C, relu_pre_add_coeff_l, relu_pre_add_coeff_u,
+                               B, _numel(trace.shapes[out]))
     chain = parse_chain(module, spec, output_value)
-    return crown_backward(module, spec, trace, chain=chain, linear_spec_C=linear_spec_C, relu_alpha=relu_alpha,
-                          relu_pre_add_coeff_l=relu_pre_add_coeff_l)
+
+    def backward(C, add_l, need_upper, need_lower):
+        return crown_backward(module, spec, trace, chain=chain, linear_spec_C=C, relu_alpha=relu_alpha,
+                              relu_pre_add_coeff_l=add_l, need_upper=need_upper, need_lower=need_lower)
+
+    return _with_upper_add(backward, trace.relu_pre, linear_spec_C, relu_pre_add_coeff_l, relu_pre_add_coeff_u, B,
+                           _numel(chain.layers[-1].out_shape))
 
 
 def run_crown_ibp_mlp_with_relu_influence_from_forward_trace(

@@ -41,17 +41,24 @@ __device__ __forceinline__ float norm_wave_xor(float s, int nk) {
   return s;
 }
 
+// STAGED: the row's input map is copied to LDS first (maps of at most 64 KB); otherwise
+// the taps read it from global memory through the caches, for maps of any size.
+template <bool STAGED>
 __global__ void __launch_bounds__(CT)
 conv2d_rows_kernel(const float* __restrict__ x, int64_t in_div, int Ci, int Hi, int Wi,
                    const float* __restrict__ W, int abs_w, int Co, int KH, int KW, int sh, int sw, int ph, int pw,
                    int Ho, int Wo, float* __restrict__ y, const float* __restrict__ rs, const float* __restrict__ v,
                    int64_t v_div, int64_t v_ld) {
-  extern __shared__ float xs[];
+  extern __shared__ float xs_lds[];
   const int64_t r = blockIdx.x;
   const int nin = Ci * Hi * Wi;
   const float* __restrict__ xr = x + (r / in_div) * (int64_t)nin;
-  for (int i = threadIdx.x; i < nin; i += CT) xs[i] = xr[i];
-  __syncthreads();
+  const float* xs = xr;
+  if constexpr (STAGED) {
+    for (int i = threadIdx.x; i < nin; i += CT) xs_lds[i] = xr[i];
+    __syncthreads();
+    xs = xs_lds;
+  }
   const int nout = Co * Ho * Wo;
   float* __restrict__ yr = y + r * (int64_t)nout;
   const float scale = rs ? rs[r] : 0.f;
@@ -82,13 +89,15 @@ conv2d_rows_kernel(const float* __restrict__ x, int64_t in_div, int Ci, int Hi, 
   }
 }
 
+// STAGED as for conv2d_rows_kernel: the coefficient map in LDS, or read from global memory.
+template <bool STAGED>
 __global__ void __launch_bounds__(CT)
 conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restrict__ A_l, int Co, int Ho, int Wo,
                            const float* __restrict__ W, int Ci, int KH, int KW, int sh, int sw, int ph, int pw,
                            int Hi, int Wi, float* __restrict__ y_u, float* __restrict__ y_l, int64_t S,
                            const float* __restrict__ wv, int64_t w_ld, int nk, float* __restrict__ norm_u,
                            float* __restrict__ norm_l, const float* __restrict__ h_scale, float* __restrict__ h_out) {
-  extern __shared__ float as[];
+  extern __shared__ float as_lds[];
   __shared__ float red[CT / 64];
   const int z = blockIdx.y;
   const bool lower = (A_u == nullptr) || (z == 1);
@@ -98,8 +107,12 @@ conv_transpose_rows_kernel(const float* __restrict__ A_u, const float* __restric
   const int64_t r = blockIdx.x;
   const int nin = Co * Ho * Wo;
   const float* __restrict__ ar = A + r * (int64_t)nin;
-  for (int i = threadIdx.x; i < nin; i += CT) as[i] = ar[i];
-  __syncthreads();
+  const float* as = ar;
+  if constexpr (STAGED) {
+    for (int i = threadIdx.x; i < nin; i += CT) as_lds[i] = ar[i];
+    __syncthreads();
+    as = as_lds;
+  }
   const int nout = Ci * Hi * Wi;
   const int64_t d = r / S;
   float s = 0.f;
@@ -443,6 +456,8 @@ struct ConvRelax {
   float* relaxed[2];     // optional A' rows [R, nin]
   const float* cvec;     // input layer only (conv_t_small_kernel): center projection [D, nin]
   float* c_out[2];       //   and its row sums sum A' * cvec
+  const float* pl[4];    // conv_t_hwc_kernel: the relaxation as four planes [D, nin] {alpha_u, beta_u, alpha_l,
+                         //   beta_l} (the executor's request), in place of the box; pl[0] null = from the box
 };
 
 // One element of a coefficient row through the ReLU relaxation (the sign-split
@@ -535,18 +550,11 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
   const FastDiv f_hw = g.f_HWm;
   const FastDiv f_w = g.f_Wm;
 
-  // One element of a row: relax it (RELAX) into the channel-last map.
-  auto stage = [&](int64_t r, int64_t d, int e, float v, float lo, float hi, float al, float ad, float& sb,
-                   float& sk) {
+  // One element of a row: relax it (RELAX; t = {alpha_u, beta_u, alpha_l, beta_l}) into the channel-last map.
+  auto stage = [&](int64_t r, int64_t d, int e, float v, float4 t, float ad, float& sb, float& sk) {
     const int co = fdivq(e, f_hw), rem = e - co * HWm;
     const int yy = fdivq(rem, f_w), xx = rem - yy * g.Wm;
     if constexpr (RELAX) {
-      float4 t = make_float4(1.f, 0.f, 1.f, 0.f);
-      if (rx.lo) {
-        const bool has_alpha = rx.alpha != nullptr;
-        const Relax rr = relu_relax(lo, hi, has_alpha, has_alpha ? clamp01(al) : 0.f);
-        t = make_float4(rr.au, rr.bu, rr.al, rr.bl);
-      }
       const bool nn = v >= 0.f;
       float o;
       if (lower) {
@@ -576,14 +584,22 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
       pa[u] = e < nin ? X[r * nin + e] : 0.f;
     }
   };
-  auto relax_operands = [&](int64_t d, int e, float& lo, float& hi, float& al, float& ad) {
-    lo = hi = al = ad = 0.f;
+  // The relaxation entry of element e of domain d: the four planes, or the slopes from
+  // the pre-activation box (and lower-slope override) as bf_crown_relu_relax_lu computes them.
+  auto relax_operands = [&](int64_t d, int e, float4& t, float& ad) {
+    t = make_float4(1.f, 0.f, 1.f, 0.f);
+    ad = 0.f;
     if constexpr (RELAX) {
-      if (rx.lo) {
-        lo = rx.lo[d * nin + e];
-        hi = rx.hi[d * nin + e];
+      if (rx.pl[0]) {
+        const int64_t i = d * nin + e;
+        t = make_float4(rx.pl[0][i], rx.pl[1][i], rx.pl[2][i], rx.pl[3][i]);
+      } else if (rx.lo) {
+        const float lo = rx.lo[d * nin + e], hi = rx.hi[d * nin + e];
+        const bool has_alpha = rx.alpha != nullptr;
+        const float al = has_alpha ? rx.alpha[d * rx.alpha_ld + e] : 0.f;
+        const Relax rr = relu_relax(lo, hi, has_alpha, has_alpha ? clamp01(al) : 0.f);
+        t = make_float4(rr.au, rr.bu, rr.al, rr.bl);
       }
-      if (rx.alpha) al = rx.alpha[d * rx.alpha_ld + e];
       if (rx.add && lower) ad = rx.add[d * rx.add_ld + e];
     }
   };
@@ -601,16 +617,18 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
       for (int u = 0; u < PF; ++u) {
         const int e = tid + u * GTM;
         if (e < nin) {
-          float lo, hi, al, ad;
-          relax_operands(d, e, lo, hi, al, ad);
-          stage(r, d, e, pa[u], lo, hi, al, ad, sb, sk);
+          float4 t;
+          float ad;
+          relax_operands(d, e, t, ad);
+          stage(r, d, e, pa[u], t, ad, sb, sk);
         }
       }
     } else {
       for (int e = tid; e < nin; e += GTM) {
-        float lo, hi, al, ad;
-        relax_operands(d, e, lo, hi, al, ad);
-        stage(r, d, e, X[r * nin + e], lo, hi, al, ad, sb, sk);
+        float4 t;
+        float ad;
+        relax_operands(d, e, t, ad);
+        stage(r, d, e, X[r * nin + e], t, ad, sb, sk);
       }
     }
     if constexpr (RELAX) {
@@ -1113,10 +1131,14 @@ static int conv2d_launch(const float* x, int64_t in_div, int64_t R, int Ci, int 
                          v_ld, stream);
   }
   const size_t lds = sizeof(float) * (size_t)Ci * Hi * Wi;
-  BF_REQUIRE(lds <= 64 * 1024, "conv2d: input map of %d x %d x %d exceeds the 64 KB LDS row stage", Ci, Hi, Wi);
   BF_REQUIRE(R < (1LL << 31), "conv2d: too many rows");
-  hipLaunchKernelGGL(conv2d_rows_kernel, dim3((unsigned)R), dim3(CT), lds, stream, x, in_div, Ci, Hi, Wi, W, abs_w,
-                     Co, KH, KW, sh, sw, ph, pw, Ho, Wo, y, rs, v, v_div, v_ld);
+  BF_REQUIRE((int64_t)Ci * Hi * Wi < (1LL << 31) && (int64_t)Co * Ho * Wo < (1LL << 31), "conv2d: map too large");
+  if (lds <= 64 * 1024)
+    hipLaunchKernelGGL(conv2d_rows_kernel<true>, dim3((unsigned)R), dim3(CT), lds, stream, x, in_div, Ci, Hi, Wi, W,
+                       abs_w, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, y, rs, v, v_div, v_ld);
+  else   // a map beyond the LDS row stage: the taps read it from global memory
+    hipLaunchKernelGGL(conv2d_rows_kernel<false>, dim3((unsigned)R), dim3(CT), 0, stream, x, in_div, Ci, Hi, Wi, W,
+                       abs_w, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, y, rs, v, v_div, v_ld);
   BF_LAUNCH_CHECK("conv2d_rows_kernel");
   return BF_OK;
 }
@@ -1228,10 +1250,17 @@ static int conv_transpose_rows_launch(const float* A_u, const float* A_l, int64_
     }
   }
   const size_t lds = sizeof(float) * (size_t)Co * Ho * Wo;
-  BF_REQUIRE(lds <= 64 * 1024, "bf_conv_transpose_rows: coefficient map exceeds the 64 KB LDS row stage");
-  hipLaunchKernelGGL(conv_transpose_rows_kernel, dim3((unsigned)R, nz), dim3(CT), lds, stream, A_u, A_l, Co, Ho, Wo,
-                     W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S, wvec, w_ld, norm_p, norm_u, norm_l, h_scale,
-                     h_out);
+  BF_REQUIRE(R < (1LL << 31), "bf_conv_transpose_rows: too many rows");
+  BF_REQUIRE((int64_t)Co * Ho * Wo < (1LL << 31) && (int64_t)Ci * Hi * Wi < (1LL << 31),
+             "bf_conv_transpose_rows: map too large");
+  if (lds <= 64 * 1024)
+    hipLaunchKernelGGL(conv_transpose_rows_kernel<true>, dim3((unsigned)R, nz), dim3(CT), lds, stream, A_u, A_l, Co,
+                       Ho, Wo, W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S, wvec, w_ld, norm_p, norm_u, norm_l,
+                       h_scale, h_out);
+  else   // a map beyond the LDS row stage: the taps read it from global memory
+    hipLaunchKernelGGL(conv_transpose_rows_kernel<false>, dim3((unsigned)R, nz), dim3(CT), 0, stream, A_u, A_l, Co,
+                       Ho, Wo, W, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, y_u, y_l, S, wvec, w_ld, norm_p, norm_u, norm_l,
+                       h_scale, h_out);
   BF_LAUNCH_CHECK("conv_transpose_rows_kernel");
   return BF_OK;
 }
@@ -1346,6 +1375,58 @@ int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, 
   const int rpw = gather_rows_per_wg(R * nz);
   g.rows_per_wg = rpw;
   BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_crown_relu_conv_transpose: too many rows");
+  hipLaunchKernelGGL(conv_t_hwc_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g,
+                     rx);
+  BF_LAUNCH_CHECK("conv_t_hwc_kernel<relax>");
+  return BF_OK;
+}
+
+int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
+                                        int Wo, const float* alpha_u, const float* beta_u, const float* alpha_l,
+                                        const float* beta_l, const float* kbias, const float* b_u_in,
+                                        const float* b_l_in, const float* W, const float* w_packed, int Ci, int KH,
+                                        int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
+                                        float* y_l, float* b_u_out, float* b_l_out, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S > 0 && Co > 0 && Ci > 0, "bf_crown_relu_planes_conv_transpose: bad sizes");
+  const int64_t R = D * S;
+  if (R == 0) return BF_OK;
+  BF_REQUIRE(W && (A_u || A_l), "bf_crown_relu_planes_conv_transpose: null pointer");
+  BF_REQUIRE(alpha_u && beta_u && alpha_l && beta_l, "bf_crown_relu_planes_conv_transpose: null relaxation plane");
+  BF_REQUIRE((A_u == nullptr) == (y_u == nullptr) && (A_l == nullptr) == (y_l == nullptr),
+             "bf_crown_relu_planes_conv_transpose: each given coefficient needs an output");
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t glds = 0;
+  if (!conv_t_hwc_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
+    set_error("bf_crown_relu_planes_conv_transpose: shape not supported (bf_conv_transpose_hwc_supported)");
+    return BF_EINVAL;
+  }
+  const unsigned nz = (A_u && A_l) ? 2u : 1u;
+  ConvRelax rx;
+  memset(&rx, 0, sizeof(rx));
+  rx.pl[0] = alpha_u;
+  rx.pl[1] = beta_u;
+  rx.pl[2] = alpha_l;
+  rx.pl[3] = beta_l;
+  rx.kbias = kbias;
+  int nzi = 0;
+  if (A_u) {
+    g.X[nzi] = A_u; g.y[nzi] = y_u;
+    rx.b_in[nzi] = b_u_in; rx.b_out[nzi] = b_u_out;
+    ++nzi;
+  }
+  if (A_l) {
+    g.X[nzi] = A_l; g.y[nzi] = y_l;
+    rx.b_in[nzi] = b_l_in; rx.b_out[nzi] = b_l_out;
+    ++nzi;
+  }
+  g.z_lower_first = A_u ? 0 : 1;
+  g.W = W;
+  g.wpack = ((uintptr_t)w_packed & 15) == 0 ? w_packed : nullptr;
+  g.S = S;
+  const int rpw = gather_rows_per_wg(R * nz);
+  g.rows_per_wg = rpw;
+  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_crown_relu_planes_conv_transpose: too many rows");
   hipLaunchKernelGGL(conv_t_hwc_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g,
                      rx);
   BF_LAUNCH_CHECK("conv_t_hwc_kernel<relax>");

@@ -36,6 +36,7 @@ from typing import Any, Literal, Mapping, Optional, Protocol, Sequence, Tuple
 import torch
 
 from . import _lib
+from .conv import packed_conv_transpose_weights
 from .crown import derived, transposed
 from .profiling import launch as _timed
 
@@ -243,9 +244,7 @@ class HipFusedCrownExecutor:
             a = descriptor.attrs
             if int(a.get("groups", 1)) != 1 or _pair(a, "dilation", (1, 1)) != (1, 1):
                 return False
-            Co, Ho, Wo = (int(d) for d in descriptor.output_shape)
-            Ci, Hi, Wi = (int(d) for d in descriptor.input_shape)
-            return Co * Ho * Wo * 4 <= 64 * 1024 and descriptor.weight.dim() == 4
+            return descriptor.weight.dim() == 4
         return False
 
     def supports(self, request: FusedReluAffineRequest, context: FusedCrownExecutionContext) -> bool:
@@ -264,13 +263,16 @@ class HipFusedCrownExecutor:
             return self._run(request, _lib.stream_handle(stream))
 
     def _run(self, request: FusedReluAffineRequest, st) -> FusedReluAffineResult:
+        """One launch per region: the contraction (linear) or the transposed convolution
+        (conv2d, channel-last gather) reads the request's four relaxation tensors in its
+        prologue / while staging each row, and reduces the bias rows in the same pass.
+        Conv shapes the channel-last kernel does not take run the relaxation pass and then
+        the transposed convolution."""
         dev = request.A_u.device
         D, S = int(request.A_u.shape[0]), int(request.A_u.shape[1])
         M = D * S
         N = int(request.alpha_u.reshape(D, -1).shape[1])
-        # the four relaxation tensors, interleaved as the kernels' table
-        table = torch.stack([request.alpha_u.reshape(D, N), request.beta_u.reshape(D, N),
-                             request.alpha_l.reshape(D, N), request.beta_l.reshape(D, N)], dim=-1).contiguous()
+        planes = [request.alpha_u, request.beta_u, request.alpha_l, request.beta_l]
         bias = None if request.bias is None else request.bias.contiguous()
         du = torch.empty(D, S, device=dev, dtype=torch.float32)
         dl = torch.empty(D, S, device=dev, dtype=torch.float32)
@@ -280,9 +282,9 @@ class HipFusedCrownExecutor:
             pu = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             pl = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             with _timed("executor_relu_linear", 4.0 * M * N * P, 4.0 * (2 * M * N + 4 * D * N + N * P + 2 * M * P)):
-                _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
-                          _lib.ptr(table), None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None, _lib.ptr(pu),
-                          _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
+                _lib.call("bf_crown_relu_planes_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S,
+                          N, *[_lib.ptr(t) for t in planes], _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None,
+                          _lib.ptr(pu), _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
             return FusedReluAffineResult(pu, pl, du, dl)
         Co, Ho, Wo = (int(d) for d in request.output_shape)
         Ci, Hi, Wi = (int(d) for d in request.input_shape)
@@ -292,16 +294,26 @@ class HipFusedCrownExecutor:
         ph, pw = _pair(request.attrs, "padding", (0, 0))
         kbias = None if bias is None else derived(
             f"conv_bias_map:{Ho}x{Wo}", (bias,), lambda: bias.reshape(Co, 1).expand(Co, Ho * Wo).reshape(-1).contiguous())
+        pu = torch.empty(D, S, Ci, Hi, Wi, device=dev)
+        pl = torch.empty(D, S, Ci, Hi, Wi, device=dev)
+        flops = 4.0 * M * Co * Ho * Wo * Ci * KH * KW / (sh * sw)
+        if _lib.load().bf_conv_transpose_hwc_supported(Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi):
+            wpk = packed_conv_transpose_weights(W, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi)
+            with _timed("executor_relu_conv_transpose", flops, 4.0 * (2 * M * N + 4 * D * N + 2 * M * Ci * Hi * Wi)):
+                _lib.call("bf_crown_relu_planes_conv_transpose", _lib.ptr(request.A_u), _lib.ptr(request.A_l), D, S,
+                          Co, Ho, Wo, *[_lib.ptr(t) for t in planes], _lib.ptr(kbias), None, None, _lib.ptr(W),
+                          _lib.ptr(wpk), Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, _lib.ptr(pu), _lib.ptr(pl),
+                          _lib.ptr(du), _lib.ptr(dl), st)
+            return FusedReluAffineResult(pu, pl, du, dl)
+        # other conv shapes: the relaxation pass (from the interleaved table), then the transposed convolution
+        table = torch.stack([t.reshape(D, N) for t in planes], dim=-1).contiguous()
         ru = torch.empty(M, N, device=dev)
         rl = torch.empty(M, N, device=dev)
         with _timed("executor_relu_relax", 0.0, 4.0 * (4 * M * N + 4 * D * N)):
             _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
                       _lib.ptr(table), None, 0, _lib.ptr(kbias), None, None, None, _lib.ptr(ru), _lib.ptr(rl),
                       _lib.ptr(du), _lib.ptr(dl), None, None, st)
-        pu = torch.empty(D, S, Ci, Hi, Wi, device=dev)
-        pl = torch.empty(D, S, Ci, Hi, Wi, device=dev)
-        with _timed("executor_conv_transpose", 4.0 * M * Co * Ho * Wo * Ci * KH * KW,
-                    4.0 * (2 * M * N + 2 * M * Ci * Hi * Wi)):
+        with _timed("executor_conv_transpose", flops, 4.0 * (2 * M * N + 2 * M * Ci * Hi * Wi)):
             _lib.call("bf_conv_transpose_rows", _lib.ptr(ru), _lib.ptr(rl), M, Co, Ho, Wo, _lib.ptr(W), Ci, KH, KW,
                       sh, sw, ph, pw, Hi, Wi, _lib.ptr(pu), _lib.ptr(pl), S, None, 0, 0, None, None, None, None, st)
         return FusedReluAffineResult(pu, pl, du, dl)

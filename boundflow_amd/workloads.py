@@ -458,6 +458,32 @@ def make_bab_cnn_toy(seed: int = 0, batch: int = 4, eps: float = 0.02, in_shape:
     return Workload("bab_cnn_toy", module, spec, margin_spec(labels, n_out), labels)
 
 
+def make_wide_cnn(seed: int = 0, batch: int = 4, eps: float = 2.0 / 255.0) -> Workload:
+    """A CNN whose first conv writes a 32x32x32 map (128 KB per row, beyond a 64 KB LDS
+    row stage): 3x32x32 -> conv(32, 3x3, s1, p1) -> relu -> conv(16, 4x4, s2, p1)
+    16x16x16 -> relu -> flatten -> fc 4096 -> 10; Kaiming-uniform weights, small
+    biases, inputs uniform in [0, 1], Linf eps, 9 margin specs of random labels."""
+    g = torch.Generator().manual_seed(4000 + seed)
+    params: Dict[str, torch.Tensor] = {
+        "W0": _kaiming((32, 3, 3, 3), fan_in=27, gen=g, kind="uniform"), "b0": _bias(32, g, 0.05),
+        "W1": _kaiming((16, 32, 4, 4), fan_in=512, gen=g, kind="uniform"), "b1": _bias(16, g, 0.05),
+        "W2": _kaiming((10, 4096), fan_in=4096, gen=g, kind="uniform"), "b2": _bias(10, g, 0.05),
+    }
+    ops = [TaskOp("conv2d", "conv0", ["input", "W0", "b0"], ["h0"], {"stride": 1, "padding": 1, "dilation": 1,
+                                                                     "groups": 1}),
+           TaskOp("relu", "relu0", ["h0"], ["r0"]),
+           TaskOp("conv2d", "conv1", ["r0", "W1", "b1"], ["h1"], {"stride": 2, "padding": 1, "dilation": 1,
+                                                                  "groups": 1}),
+           TaskOp("relu", "relu1", ["h1"], ["r1"]),
+           TaskOp("flatten", "flatten", ["r1"], ["f1"], {"start_dim": 1, "end_dim": -1}),
+           TaskOp("linear", "linear2", ["f1", "W2", "b2"], ["out"])]
+    module = _module(ops, params, ["input", "h0", "r0", "h1", "r1", "f1", "out"])
+    x = torch.rand(batch, 3, 32, 32, generator=g)
+    labels = torch.randint(0, 10, (batch,), generator=g)
+    spec = InputSpec.linf(value_name="input", center=x, eps=eps)
+    return Workload("wide_cnn", module, spec, margin_spec(labels), labels)
+
+
 def make_bab_case(kind: str = "mlp", **kw) -> Workload:
     """The whole-search workloads: ``make_bab_toy`` (kind "mlp") or ``make_bab_cnn_toy`` (kind "cnn")."""
     return make_bab_cnn_toy(**kw) if kind == "cnn" else make_bab_toy(**kw)

@@ -127,6 +127,17 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
                              int w_trans, const float* bias, const float* b_u_in, const float* b_l_in,
                              float* A_prev_u, float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream);
 
+/* bf_crown_relu_linear_fwd with the relaxation as the four tensors of a
+ * "fused_relu_linear" FusedReluAffineRequest (runtime/fused_crown.py:33-48,
+ * run at :97-123) -- alpha_u, beta_u, alpha_l, beta_l, each [D, N] -- read by
+ * the contraction's prologue directly instead of an interleaved table; no
+ * split term. */
+int bf_crown_relu_planes_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
+                                    int64_t N, const float* alpha_u, const float* beta_u, const float* alpha_l,
+                                    const float* beta_l, const float* W, int64_t P, int w_trans, const float* bias,
+                                    const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
+                                    float* b_u_out, float* b_l_out, hipStream_t stream);
+
 /* The input-layer region fused with the concretization (kernel #4):
  * lb = (A' . cvec - eps * sum_i |(A' W)_i| * rad_i) + b, ub mirrored;
  * rad NULL = Lp ball (weights 1, eps used), else box radius [D, I] (eps ignored).
@@ -277,6 +288,21 @@ int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, 
                                  int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u, float* y_l,
                                  float* b_u_out, float* b_l_out, float* relaxed_u, float* relaxed_l,
                                  hipStream_t stream);
+
+/* One "fused_relu_conv2d" region of FusedCrownExecutor.run
+ * (runtime/fused_crown.py:97-123; the reference's fused TVM kernel,
+ * backends/tvm/fused_crown_conv2d.py:161-350) in one pass: the relaxation is
+ * the request's four tensors alpha_u, beta_u, alpha_l, beta_l [D, Co*Ho*Wo]
+ * read directly (no box, no split term), applied while each row's map is
+ * staged as in bf_crown_relu_conv_transpose, then the transposed convolution
+ * and b_out = (b_in + sum A * beta_sel) + sum A' * kbias.  Shapes: those of
+ * bf_conv_transpose_hwc_supported (else returns 1). */
+int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
+                                        int Wo, const float* alpha_u, const float* beta_u, const float* alpha_l,
+                                        const float* beta_l, const float* kbias, const float* b_u_in,
+                                        const float* b_l_in, const float* W, const float* w_packed, int Ci, int KH,
+                                        int KW, int sh, int sw, int ph, int pw, int Hi, int Wi, float* y_u,
+                                        float* y_l, float* b_u_out, float* b_l_out, hipStream_t stream);
 
 /* The input layer of a conv network in one pass: the ReLU relaxation of
  * bf_crown_relu_relax_lu applied to each coefficient row as it is staged (with

@@ -804,6 +804,11 @@ def crown_backward_from_trace(
                 cu = st.A_u.to_dense().reshape(batch, -1, *in_shape)
                 cl = st.A_l.to_dense().reshape(batch, -1, *in_shape)
                 relu_influence_out[name] = torch.maximum(cu.abs().amax(dim=1), cl.abs().amax(dim=1)).detach()
+            if pre.lower.dim() != 2 and relu_pre_add_coeff_u is not None and name in relu_pre_add_coeff_u:
+                # crown_ibp.py:1256-1260
+                raise NotImplementedError(
+                    f"run_crown_ibp_mlp only supports relu_pre_add_coeff_u on rank-2 pre-activations; got "
+                    f"{tuple(pre.lower.shape)} for {name}")
             dA_u, dA_l, b_u, b_l = relu_backward_dense(
                 st.A_u.to_dense(), st.A_l.to_dense(), st.b_u, st.b_l, pre=pre, name=name,
                 relu_alpha=relu_alpha, add_u=relu_pre_add_coeff_u, add_l=relu_pre_add_coeff_l,

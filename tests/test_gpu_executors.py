@@ -155,3 +155,44 @@ def test_registry_dispatch_runs_the_hip_kernels(tag, kind, affine):
             assert_bounds_close(getattr(res, k), t(g[k]), f"{tag} dispatch {round_} {k}", rtol=1e-5, atol=1e-5)
     assert sess.ran == [(("relu0", "aff0"), ("v_out",))] * 2
     assert (reg.cache_misses, reg.cache_hits) == (1, 1)
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_hip_fused_crown_executor_on_c3_conv_regions(layer):
+    """The ReLU -> conv regions of the C3 network (16 channels 16x16 over 3x32x32, and
+    32 channels 8x8 over 16x16x16), which the executor runs in one launch (the
+    relaxation's four tensors read while the channel-last transposed convolution stages
+    each row), against the oracle's fused region (fused_crown.py:330-400), B=4, S=9,
+    with synthetic relaxations (both slopes and intercepts nonzero)."""
+    from boundflow_amd import workloads as wl
+    from oracle import crown_ref as cr
+    dev = device()
+    announce(f"HipFusedCrownExecutor.run on C3 conv region {layer}")
+    w = wl.make_c3()
+    W, b = w.module.params[f"W{layer}"], w.module.params[f"b{layer}"]
+    in_shape, out_shape = ((3, 32, 32), (16, 16, 16)) if layer == 0 else ((16, 16, 16), (32, 8, 8))
+    g = torch.Generator().manual_seed(40 + layer)
+    B, S = 4, 9
+    n = out_shape[0] * out_shape[1] * out_shape[2]
+    A_u, A_l = torch.randn(B, S, n, generator=g), torch.randn(B, S, n, generator=g)
+    au = torch.rand(B, n, generator=g) * 0.9 + 0.1
+    bu = torch.rand(B, n, generator=g) * 0.5
+    al = torch.rand(B, n, generator=g)
+    bl = -torch.rand(B, n, generator=g) * 0.1
+    b = b + torch.randn(b.shape, generator=g) * 0.1
+    attrs = {"stride": 2, "padding": 1, "dilation": 1, "groups": 1}
+    req = fc.FusedReluAffineRequest(kind="conv2d", A_u=A_u.to(dev), A_l=A_l.to(dev), alpha_u=au.to(dev),
+                                    alpha_l=al.to(dev), beta_u=bu.to(dev), beta_l=bl.to(dev), weight=W.to(dev),
+                                    bias=b.to(dev), input_shape=in_shape, output_shape=out_shape, attrs=attrs)
+    ex = fc.HipFusedCrownExecutor()
+    assert ex.supports(req, fc.FusedCrownExecutionContext())
+    res = ex.run(req)
+    torch.cuda.synchronize()
+    ref = cr.fused_relu_affine_reference(A_u.double(), A_l.double(), au.double(), al.double(), bu.double(),
+                                         bl.double(), W.double(), b.double(), "conv2d", in_shape, out_shape, attrs)
+    for k, r in zip(("A_prev_u", "A_prev_l", "bias_delta_u", "bias_delta_l"), ref):
+        got = getattr(res, k).detach().cpu().double()
+        tol = 1e-5 * float(r.abs().max()) + 1e-6
+        d = float((got - r).abs().max())
+        announce(f"  {k}: max |hip - fp64| {d:.3e} (tol {tol:.3e})")
+        assert d <= tol, k
