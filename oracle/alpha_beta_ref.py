@@ -160,18 +160,21 @@ def first_layer_split_halfspaces(module: BFTaskModule, spec: InputSpec, relu_spl
 
 
 def split_certificate(module: BFTaskModule, input_spec, relu_split_state, *, steps: int = 200, lr: float = 0.1,
-                      tol: float = 1e-6) -> Tuple[bool, str]:
+                      tol: float = 1e-6, return_value: bool = False):
     """alpha_beta_crown.py:391-532: the first-layer split halfspaces have no common
     point in the input set when some convex combination of them has a maximum
     over the set below -tol.  One halfspace is checked directly; several by
     Adam on the softmax logits of the combination (from 0, ``steps`` steps,
-    stopping at the first maximum below -tol)."""
+    stopping at the first maximum below -tol).  ``return_value`` appends the
+    certificate's max_value (the maximum that closed the node, as the reference's
+    certificate record holds it), or None when the node is not closed."""
     spec = normalize_input_spec(input_spec)
     hs = first_layer_split_halfspaces(module, spec, relu_split_state)
     if not hs:
-        return False, "ok (no first-layer split halfspaces)"
+        return (False, "ok (no first-layer split halfspaces)", None) if return_value else (
+            False, "ok (no first-layer split halfspaces)")
     if int(spec.center.shape[0]) != 1:
-        return False, "skip (batch!=1)"
+        return (False, "skip (batch!=1)", None) if return_value else (False, "skip (batch!=1)")
     dtype = spec.center.dtype
     ishape = tuple(int(d) for d in spec.center.shape[1:])
     a_mat = torch.stack([h[2].to(dtype) for h in hs], dim=0).detach()
@@ -181,20 +184,24 @@ def split_certificate(module: BFTaskModule, input_spec, relu_split_state, *, ste
         _lb, ub = concretize_affine(spec, spec.center, DenseOp(a.view(1, 1, -1), ishape), c.view(1, 1))
         return ub.squeeze()
 
+    def out(flag, reason, value=None):
+        return (flag, reason, value) if return_value else (flag, reason)
+
     if len(hs) == 1:
         ub0 = float(upper(a_mat[0], c_vec[0]).item())
-        return (True, "infeasible: single halfspace") if ub0 < -float(tol) else (False, "ok")
+        return out(True, "infeasible: single halfspace", ub0) if ub0 < -float(tol) else out(False, "ok")
     logits = torch.zeros(len(hs), dtype=dtype, requires_grad=True)
     opt = torch.optim.Adam([logits], lr=float(lr))
     for _ in range(int(steps)):
         w = torch.softmax(logits, dim=0)
         ub0 = upper((w.unsqueeze(1) * a_mat).sum(dim=0), (w * c_vec).sum())
-        if float(ub0.detach().item()) < -float(tol):
-            return True, "infeasible: convex combination"
+        val = float(ub0.detach().item())
+        if val < -float(tol):
+            return out(True, "infeasible: convex combination", val)
         opt.zero_grad(set_to_none=True)
         ub0.backward()
         opt.step()
-    return False, "ok"
+    return out(False, "ok")
 
 
 def adaptive_alpha_init(relu_pre: Dict[str, IntervalState]) -> Dict[str, torch.Tensor]:

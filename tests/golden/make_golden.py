@@ -87,6 +87,9 @@ def to_ref_spec(spec):
     p = spec.perturbation
     if isinstance(p, BoxPerturbation):
         return RSpec(value_name=spec.value_name, center=spec.center, perturbation=RBox(lower=p.lower, upper=p.upper))
+    if str(getattr(p, "p", "inf")) not in ("inf", "Linf"):
+        from boundflow.runtime.perturbation import LpBallPerturbation as RLp
+        return RSpec(value_name=spec.value_name, center=spec.center, perturbation=RLp(p=int(p.p), eps=float(p.eps)))
     return RSpec.linf(value_name=spec.value_name, center=spec.center, eps=float(p.eps))
 
 
@@ -307,6 +310,74 @@ def golden_bab_solve(tag):
          certificate_halfspace_calls=counts["halfspace_calls"], checksum=workload_checksum(w))
 
 
+def golden_lp(tag):
+    """Every reference path over an L2 (tag lp_reference_p2) or L1 (lp_reference_p1) ball,
+    on the networks of tests/golden_util.lp_case: run_crown_ibp_mlp on an MLP and a CNN,
+    alpha-CROWN from the CROWN slopes (10 steps), the first-layer certificate on the
+    geometric known answers and on 48 C5 first-layer nodes (flags and max_value), and a
+    whole solve_bab_mlp search."""
+    from boundflow.runtime.bab import BabConfig as RBabConfig
+    from boundflow.runtime.bab import solve_bab_mlp as r_solve
+    from boundflow.runtime.perturbation import LpBallPerturbation as RLp
+    from tests.golden_util import LP_BAB, lp_case, lp_cert_nodes
+    from tests.test_oracle_certificate import LP_KATS, first_layer_module
+    p = int(tag[-1])
+    arrays = {}
+    for kind in ("mlp", "cnn"):
+        w = lp_case(kind, p)
+        with torch.inference_mode():
+            b = rci.run_crown_ibp_mlp(to_ref_module(w.module), to_ref_spec(w.spec), linear_spec_C=w.C)
+        arrays[f"crown_{kind}_lower"], arrays[f"crown_{kind}_upper"] = b.lower, b.upper
+        arrays[f"crown_{kind}_checksum"] = workload_checksum(w)
+    # alpha-CROWN: adaptive init (native_alpha_beta_optimizer_schedule.py:635-653), 10 steps, lr 0.1
+    w = lp_case("alpha", p)
+    rm, rs = to_ref_module(w.module), to_ref_spec(w.spec)
+    _env, pre = rci._forward_ibp_trace_mlp(rm, rs)
+    from boundflow.runtime.native_alpha_beta_optimizer_schedule import _initial_alpha_state
+    from boundflow.runtime.native_alpha_beta_optimization_state import NativeAlphaBetaOptimizerPolicy
+    init = _initial_alpha_state(pre, policy=NativeAlphaBetaOptimizerPolicy(steps=10, lr=0.1,
+                                                                          alpha_initialization_mode="adaptive"))
+    bounds, _alpha, _beta, _stats = rabc.run_alpha_beta_crown_mlp(
+        rm, rs, linear_spec_C=w.C, steps=10, lr=0.1, warm_start_alpha=rac.AlphaState(init), per_batch_params=True)
+    arrays["alpha_lower"], arrays["alpha_upper"] = bounds.lower, bounds.upper
+    arrays["alpha_checksum"] = workload_checksum(w)
+    # the certificate: known answers and C5 first-layer nodes
+    for name, (Wk, bk, sk, _expect) in LP_KATS.items():
+        m = first_layer_module(torch.tensor(Wk), torch.tensor(bk))
+        spec = RSpec(value_name="input", center=torch.zeros(1, 2), perturbation=RLp(p=p, eps=1.0))
+        ok, _r, cert = rabc._is_infeasible_split_first_layer_convex_combo(
+            to_ref_module(m), spec, relu_split_state={"h1": torch.tensor([sk], dtype=torch.int8)})
+        arrays[f"kat_{name}_flag"] = int(bool(ok))
+        arrays[f"kat_{name}_value"] = float(cert["max_value"]) if cert is not None else float("nan")
+    w = lp_case("cert_c5", p)
+    name, rows = lp_cert_nodes(w, p)
+    rm = to_ref_module(w.module)
+    flags, values = [], []
+    for r in range(int(rows.shape[0])):
+        spec = to_ref_spec(wl.subset(w, r + 1).spec)
+        spec = RSpec(value_name=spec.value_name, center=spec.center[r:r + 1], perturbation=spec.perturbation)
+        ok, _r, cert = rabc._is_infeasible_split_first_layer_convex_combo(rm, spec,
+                                                                          relu_split_state={name: rows[r:r + 1]})
+        flags.append(int(bool(ok)))
+        values.append(float(cert["max_value"]) if cert is not None else float("nan"))
+    arrays["cert_c5_flag"], arrays["cert_c5_value"] = np.array(flags), np.array(values)
+    arrays["cert_c5_checksum"] = workload_checksum(w)
+    # a whole search
+    w = lp_case("bab", p)
+    res = r_solve(to_ref_module(w.module), to_ref_spec(w.spec), linear_spec_C=w.C, config=RBabConfig(**LP_BAB[p][1]))
+    per = res.per_example
+    code = {"proven": 0, "unsafe": 1, "unknown": 2}
+    arrays.update(bab_per_status=np.array([code[q.status] for q in per]),
+                  bab_per_visited=np.array([q.nodes_visited for q in per]),
+                  bab_per_evaluated=np.array([q.nodes_evaluated for q in per]),
+                  bab_per_expanded=np.array([q.nodes_expanded for q in per]),
+                  bab_per_best_lower=np.array([q.best_lower for q in per]),
+                  bab_per_best_upper=np.array([q.best_upper for q in per]),
+                  bab_max_queue=res.max_queue, bab_batch_rounds=res.batch_rounds, bab_checksum=workload_checksum(w))
+    print(tag, "certificate C5 closed", sum(flags), "of", len(flags), "bab", [q.status for q in per])
+    save(tag, **arrays)
+
+
 def golden_cert_conv(tag):
     """The reference's first-layer certificate (_is_infeasible_split_first_layer_convex_combo,
     alpha_beta_crown.py:391-532) on C3's first conv layer (3x32x32 input, 16x16x16
@@ -496,6 +567,8 @@ GOLDENS = [
     ("bab_solve_cnn_b1", golden_bab_solve),
     ("bab_solve_cnn_b4", golden_bab_solve),
     ("cert_c3_conv", golden_cert_conv),
+    ("lp_reference_p2", golden_lp),
+    ("lp_reference_p1", golden_lp),
     ("frontend_planned", golden_frontend),
     ("vnnlib_queries", golden_vnnlib),
     ("objectives_mlp", golden_objectives),

@@ -126,3 +126,60 @@ def dag_case(kind: str, box: bool):
     """The DAG workload of fixture crown_dag_<kind>[_box]."""
     from boundflow_amd import workloads as wl
     return wl.make_dag(kind, seed=3, batch=6, eps=0.03, box=box, blocks=2)
+
+
+# L2 / L1 input balls (LpBallPerturbation p=2, p=1): radii that leave a mix of stable and
+# unstable ReLUs on each network, shared by the reference fixtures (lp_reference_p{p}) and
+# the tests that read them
+LP_EPS = {"mlp": {2: 0.3, 1: 1.0}, "cnn": {2: 0.02, 1: 0.03}, "dag": {2: 0.08, 1: 0.2}, "c5": {2: 0.1, 1: 0.5},
+          "c4": {2: 0.01, 1: 0.01}, "cert_c5": {2: 0.5, 1: 2.0}}
+# whole searches over the balls: (eps, BabConfig options) per p
+LP_BAB = {2: (0.1, dict(max_nodes=40, oracle="alpha_beta", node_batch_size=8, alpha_steps=10)),
+          1: (0.25, dict(max_nodes=20, oracle="alpha", node_batch_size=1, alpha_steps=10))}
+
+
+def lp_workload(w, p, eps, C=None):
+    """The workload ``w`` with its input set replaced by the Lp ball of radius eps at its centers."""
+    from boundflow_amd import workloads as wl
+    from boundflow_amd.spec import InputSpec, LpBallPerturbation
+    spec = InputSpec(value_name=w.spec.value_name, center=w.spec.center,
+                     perturbation=LpBallPerturbation(p=p, eps=eps))
+    return wl.Workload(w.name, w.module, spec, w.C if C is None else C, w.labels, {})
+
+
+def lp_case(kind: str, p: int):
+    """The networks of the Lp reference fixtures: "mlp" (C1, 16 inputs), "cnn" (C3, 8
+    inputs), "alpha" (C1, 8 inputs: alpha-CROWN from CROWN slopes, 10 steps, lr 0.1),
+    "cert_c5" (the C5 network, 48 domains, first-layer certificate) and "bab" (a residual
+    MLP of 4 inputs for whole searches)."""
+    from boundflow_amd import workloads as wl
+    if kind == "mlp":
+        return lp_workload(wl.make_c1(batch=16), p, LP_EPS["mlp"][p])
+    if kind == "cnn":
+        return lp_workload(wl.make_c3(batch=8), p, LP_EPS["cnn"][p])
+    if kind == "alpha":
+        return lp_workload(wl.make_c1(batch=8), p, LP_EPS["mlp"][p])
+    if kind == "cert_c5":
+        return lp_workload(wl.make_c5(domains=48), p, LP_EPS["cert_c5"][p])
+    if kind == "bab":
+        base = wl.make_dag("residual_mlp", seed=12, batch=4, eps=0.03, n_in=8, hidden=12, n_out=4, blocks=1)
+        return lp_workload(base, p, LP_BAB[p][0])
+    raise ValueError(kind)
+
+
+def lp_cert_nodes(w, p):
+    """48 first-layer split rows on the C5 network's ambiguous neurons (2-12 per node)."""
+    from oracle import crown_ref as cr
+    from boundflow_amd import workloads as wl
+    g = torch.Generator().manual_seed(4 + p)
+    _env, pre = cr.forward_ibp_trace(w.module, wl.subset(w, 1).spec)
+    name = next(iter(pre))
+    l, u = pre[name].lower[0], pre[name].upper[0]
+    amb = ((l < 0) & (u > 0)).nonzero().flatten()
+    rows = torch.zeros(48, int(l.numel()), dtype=torch.int8)
+    for r in range(48):
+        k = int(torch.randint(2, 13, (1,), generator=g))
+        pick = amb[torch.randperm(int(amb.numel()), generator=g)[:k]]
+        rows[r, pick] = (torch.randint(0, 2, (int(pick.numel()),), generator=g) * 2 - 1).to(torch.int8)
+    return name, rows
+

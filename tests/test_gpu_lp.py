@@ -183,42 +183,143 @@ def test_lp_lower_bound_gradients_match_autograd(case, p, monkeypatch):
 @pytest.mark.parametrize("p", [2, 1])
 def test_lp_alpha_crown_matches_oracle(net, p):
     """alpha-CROWN from the CROWN slopes, 10 Adam steps (the C4 recipe), over an L2 / L1
-    ball: bounds within 1e-4 of the oracle's trajectory, never looser than CROWN."""
+    ball: the final bounds at the contract, a domain outside it traced step by step
+    (oracle/trajectory.py); never looser than CROWN.  On the C1 network the oracle's
+    trajectory is the reference's own (fixture lp_reference_p{p}, pinned in
+    tests/test_oracle_lp.py), and the HIP bounds are compared with the fixture too."""
+    from oracle import trajectory as tt
+    from tests.golden_util import load, lp_case, t
     dev = device()
     announce(f"L{p} alpha-CROWN {net}, 10 steps")
     if net == "c1":
-        w = _lp(wl.make_c1(batch=8), p, EPS["mlp"][p])
+        w = lp_case("alpha", p)
     else:
         w = _lp(wl.make_dag("residual_mlp", seed=9, batch=4, eps=0.03, blocks=2), p, EPS["dag"][p])
     wd = wl.to_device(w, dev)
-    bounds, _alpha, _beta, _st = hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C,
-                                                                     steps=10, lr=0.1)
+    hrec = []
+    bounds, best_alpha, _beta, _st = hab.run_alpha_crown_from_crown_init(wd.module, wd.spec, linear_spec_C=wd.C,
+                                                                         steps=10, lr=0.1, record=hrec)
     torch.cuda.synchronize()
     _env, pre = cr.forward_ibp_trace(w.module, w.spec)
+    srec = []
     ref = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, steps=10, lr=0.1,
-                                  warm_start_alpha=ab.adaptive_alpha_init(pre), per_batch_params=True)[0]
+                                  warm_start_alpha=ab.adaptive_alpha_init(pre), per_batch_params=True,
+                                  record=srec)[0]
     crown = cr.run_crown_ibp(w.module, w.spec, linear_spec_C=w.C)
-    assert_bounds_close(bounds.lower, ref.lower, f"L{p} {net} alpha lower", rtol=1e-4, atol=1e-4)
-    assert_bounds_close(bounds.upper, ref.upper, f"L{p} {net} alpha upper", rtol=1e-4, atol=1e-4)
+
+    def fp64_lower(rows):
+        w64 = parity.to_float64(tt.sub_workload(w, rows))
+        _e64, pre64 = cr.forward_ibp_trace(w64.module, w64.spec)
+        return ab.run_alpha_beta_crown(w64.module, w64.spec, linear_spec_C=w64.C, steps=10, lr=0.1,
+                                       warm_start_alpha=ab.adaptive_alpha_init(pre64), per_batch_params=True)[0].lower
+
+    summary = tt.trace_run(w, hrec, srec, bounds.lower.cpu(), ref.lower, 0.1, what=f"L{p} {net} alpha",
+                           sample=range(w.batch), got_upper=bounds.upper.cpu(), ref_upper=ref.upper,
+                           best_alpha={n: v.cpu() for n, v in best_alpha.items()}, fp64_lower=fp64_lower,
+                           log=announce)
+    announce(f"  trace: {summary}")
     assert bool((bounds.lower.cpu() >= crown.lower - 1e-4 * crown.lower.abs() - 1e-4).all())
+    if net == "c1":
+        g = load(f"lp_reference_p{p}")
+        assert torch.allclose(ref.lower, t(g["alpha_lower"]), rtol=1e-5, atol=1e-6)
+        assert torch.allclose(ref.upper, t(g["alpha_upper"]), rtol=1e-5, atol=1e-6)
+        out = tt.domains_outside(torch.cat([bounds.lower.cpu(), bounds.upper.cpu()], 1),
+                                 torch.cat([t(g["alpha_lower"]), t(g["alpha_upper"])], 1))
+        announce(f"  vs the reference fixture: domains outside the contract {out} (traced above against the "
+                 f"oracle, whose trajectory is the reference's)")
 
 
 @pytest.mark.parametrize("p", [2, 1])
 def test_lp_alpha_beta_crown_with_splits_matches_oracle(p):
+    """alpha-beta-CROWN with splits over an L2 / L1 ball: final bounds at the contract, a
+    domain outside it traced step by step (oracle/trajectory.py)."""
+    from oracle import trajectory as tt
     dev = device()
     announce(f"L{p} alpha-beta-CROWN residual_mlp with splits, 8 steps")
     g = torch.Generator().manual_seed(33)
     w = _lp(wl.make_dag("residual_mlp", seed=10, batch=4, eps=0.03, blocks=2), p, EPS["dag"][p])
     splits = _feasible_splits(w, g)
+    w = wl.Workload(w.name, w.module, w.spec, w.C, w.labels, {"splits": splits})
     wd = wl.to_device(w, dev)
-    bounds, _a, _b, _st = hab.run_alpha_beta_crown_mlp(
+    hrec = []
+    bounds, best_alpha, _b, _st = hab.run_alpha_beta_crown_mlp(
         wd.module, wd.spec, linear_spec_C=wd.C, relu_split_state={k: v.to(dev) for k, v in splits.items()},
-        steps=8, lr=0.2, per_batch_params=True)
+        steps=8, lr=0.2, per_batch_params=True, record=hrec)
     torch.cuda.synchronize()
+    srec = []
     ref = ab.run_alpha_beta_crown(w.module, w.spec, linear_spec_C=w.C, relu_split_state=splits, steps=8, lr=0.2,
-                                  per_batch_params=True)[0]
-    assert_bounds_close(bounds.lower, ref.lower, f"L{p} alpha-beta lower", rtol=1e-4, atol=1e-4)
-    assert_bounds_close(bounds.upper, ref.upper, f"L{p} alpha-beta upper", rtol=1e-4, atol=1e-4)
+                                  per_batch_params=True, record=srec)[0]
+
+    def fp64_lower(rows):
+        w64 = parity.to_float64(tt.sub_workload(w, rows))
+        return ab.run_alpha_beta_crown(w64.module, w64.spec, linear_spec_C=w64.C,
+                                       relu_split_state=w64.extra["splits"], steps=8, lr=0.2,
+                                       per_batch_params=True)[0].lower
+
+    summary = tt.trace_run(w, hrec, srec, bounds.lower.cpu(), ref.lower, 0.2, what=f"L{p} alpha-beta",
+                           sample=range(w.batch), got_upper=bounds.upper.cpu(), ref_upper=ref.upper,
+                           best_alpha={n: v.cpu() for n, v in best_alpha.items()}, fp64_lower=fp64_lower,
+                           log=announce)
+    announce(f"  trace: {summary}")
+
+
+@pytest.mark.parametrize("p", [2, 1])
+def test_hip_matches_lp_reference_fixtures(p):
+    """The HIP path against the reference's own runs over an L2 / L1 ball (fixture
+    lp_reference_p{p}): CROWN on the C1 MLP and the C3 CNN at the contract
+    (fp64-explained), the first-layer certificate's flags and max_value on the
+    geometric known answers and on 48 C5 first-layer nodes, and a whole BaB search."""
+    import numpy as np
+    from boundflow_amd.ir import BFTaskModule
+    from boundflow_amd.split_certificate import split_certificate
+    from tests.golden_util import LP_BAB, load, lp_case, lp_cert_nodes, t, workload_checksum
+    dev = device()
+    announce(f"HIP vs the reference's L{p} runs")
+    g = load(f"lp_reference_p{p}")
+    for kind in ("mlp", "cnn"):
+        w = lp_case(kind, p)
+        assert workload_checksum(w) == str(g[f"crown_{kind}_checksum"])
+        wd = wl.to_device(w, dev)
+        got = hc.run_crown_ibp_mlp(wd.module, wd.spec, linear_spec_C=wd.C)
+        w64 = parity.to_float64(w)
+        ref64 = cr.run_crown_ibp(w64.module, w64.spec, linear_spec_C=w64.C)
+        assert_parity(got.lower, t(g[f"crown_{kind}_lower"]), ref64.lower, f"L{p} {kind} lower vs reference")
+        assert_parity(got.upper, t(g[f"crown_{kind}_upper"]), ref64.upper, f"L{p} {kind} upper vs reference")
+    for name, (Wk, bk, sk, _e) in LP_KATS.items():
+        m = first_layer_module(torch.tensor(Wk), torch.tensor(bk))
+        md = BFTaskModule(tasks=m.tasks, entry_task_id=m.entry_task_id,
+                          bindings={"params": {k: v.to(dev) for k, v in m.params.items()}})
+        val = torch.empty(1, device=dev)
+        flag = split_certificate(md, lp_spec(p, torch.zeros(1, 2, device=dev)),
+                                 {"h1": torch.tensor([sk], dtype=torch.int8, device=dev)}, {"h1": (len(bk),)},
+                                 max_out=val).cpu().tolist()[0]
+        assert flag == int(g[f"kat_{name}_flag"]), name
+        if flag:
+            ref = float(g[f"kat_{name}_value"])
+            assert abs(float(val.cpu()[0]) - ref) <= 1e-5 * abs(ref) + 1e-5, (name, float(val.cpu()[0]), ref)
+    w = lp_case("cert_c5", p)
+    name, rows = lp_cert_nodes(w, p)
+    wd = wl.to_device(w, dev)
+    vals = torch.empty(int(rows.shape[0]), device=dev)
+    flags = split_certificate(wd.module, wd.spec, {name: rows.to(dev)}, {n: (256,) for n in wl.relu_input_names(
+        w.module)}, max_out=vals).cpu()
+    announce(f"  C5 first-layer nodes closed: hip {int(flags.sum())}, reference {int(g['cert_c5_flag'].sum())}")
+    assert flags.tolist() == g["cert_c5_flag"].tolist()
+    closed = flags.bool().numpy()
+    if closed.any():
+        ref = g["cert_c5_value"][closed]
+        np.testing.assert_allclose(vals.cpu().numpy()[closed], ref, rtol=1e-4, atol=1e-5)
+    w = lp_case("bab", p)
+    wd = wl.to_device(w, dev)
+    r = hbab.solve_bab_mlp(wd.module, wd.spec, linear_spec_C=wd.C, config=hbab.BabConfig(**LP_BAB[p][1]))
+    per = r.per_example
+    code = {"proven": 0, "unsafe": 1, "unknown": 2}
+    announce(f"  BaB statuses {[q.status for q in per]} visited {[q.nodes_visited for q in per]}")
+    assert [code[q.status] for q in per] == g["bab_per_status"].tolist()
+    assert [q.nodes_visited for q in per] == g["bab_per_visited"].tolist()
+    assert [q.nodes_evaluated for q in per] == g["bab_per_evaluated"].tolist()
+    assert [q.nodes_expanded for q in per] == g["bab_per_expanded"].tolist()
+    assert (r.max_queue, r.batch_rounds) == (int(g["bab_max_queue"]), int(g["bab_batch_rounds"]))
 
 
 @pytest.mark.parametrize("p", ["inf", 2, 1])
