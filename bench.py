@@ -357,6 +357,22 @@ def cpu_baseline(name: str, w, seconds: float):
     }
 
 
+def _settle(run, warmup: int, seconds: float = 0.2) -> None:
+    """Untimed runs right before the timed ones: at least ``warmup`` of them and at least
+    ``seconds`` of sustained work.  A timed region of a few milliseconds (C1 and C3 take
+    well under 0.3 ms per step) started on a device that has just been idle can catch its
+    clocks still ramping up, which multiplies the measured step time by up to ten."""
+    import torch
+    t0 = time.perf_counter()
+    n = 0
+    while n < max(1, warmup) or time.perf_counter() - t0 < seconds:
+        run()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def measure(name: str, steps: int, warmup: int, no_graph: bool):
     """One configuration: throughput of ``steps`` timed steps after ``warmup``, the
     per-kernel durations of the library's launches and the dominant kernel's
@@ -381,6 +397,7 @@ def measure(name: str, steps: int, warmup: int, no_graph: bool):
         from boundflow_amd import graphs
         replay = graphs.CapturedQuery(step)
         torch.cuda.synchronize()
+        _settle(replay, warmup)
         t0 = time.perf_counter()
         for _ in range(steps):
             replay()
@@ -403,6 +420,7 @@ def measure(name: str, steps: int, warmup: int, no_graph: bool):
         finally:
             gc.enable()
     else:
+        _settle(step, warmup)
         with profiling.timing(timer):
             torch.cuda.synchronize()
             t0 = time.perf_counter()

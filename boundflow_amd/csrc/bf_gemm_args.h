@@ -25,7 +25,6 @@ struct GemmArgs {
   // --- ReLU relaxation prologue (PRO_RELAX) ---
   int64_t S;                 // rows per domain
   const float4* relax;       // [D, K] {alpha_u, beta_u, alpha_l, beta_l}; null = identity (row sums only)
-  const float* relax_pl[4];  // or the same four as separate planes [D, K] (relax_pl[0] non-null takes precedence)
   const float* add_l;        // optional coefficient added to the lower A' (beta split term), row stride add_ld
   int64_t add_ld;
   const float* kbias;        // optional [K] bias of the affine layer: sum_k A'[m,k] * kbias[k]

@@ -75,16 +75,6 @@ struct Tile {
   static_assert((BK & (BK - 1)) == 0 && BK >= 8, "BK must be a power of two >= 8");
 };
 
-// One relaxation entry {alpha_u, beta_u, alpha_l, beta_l}: from the four planes when
-// given (pl0 non-null), else from the interleaved table.  Pointers by value: a
-// reference to the kernel's argument struct would make the compiler copy it to
-// private memory.
-__device__ __forceinline__ float4 relax_entry(const float4* tab, const float* pl0, const float* pl1,
-                                              const float* pl2, const float* pl3, int64_t i) {
-  if (pl0 != nullptr) return make_float4(pl0[i], pl1[i], pl2[i], pl3[i]);
-  return tab[i];
-}
-
 __device__ __forceinline__ float fsel(const float4& r, bool lower, bool nonneg, float* beta) {
   // upper: A >= 0 -> (alpha_u, beta_u) else (alpha_l, beta_l); lower: mirrored
   const bool use_u = lower ? !nonneg : nonneg;
@@ -304,12 +294,6 @@ gemm_kernel(GemmArgs p) {
   };
 
   const bool use_add = (PRO == PRO_RELAX) && lower && (p.add_l != nullptr);
-  // the relaxation source, read once: the table, or its four planes (rpl0 non-null)
-  const float4* const rtab = p.relax;
-  const float* const rpl0 = p.relax_pl[0];
-  const float* const rpl1 = p.relax_pl[1];
-  const float* const rpl2 = p.relax_pl[2];
-  const float* const rpl3 = p.relax_pl[3];
 
   // The rows of this tile span domains d_first .. d_first + ndom - 1.  When that
   // fits TAB_DOMS, the relaxation operands of a K tile are loaded once per
@@ -318,7 +302,7 @@ gemm_kernel(GemmArgs p) {
   int d_first = 0;
   int ndom = 0;
   bool tab_lds = false;
-  if (PRO == PRO_RELAX && (rtab || rpl0) && (EPI != EPI_ABSSUM || p.cvec)) {
+  if (PRO == PRO_RELAX && p.relax && (EPI != EPI_ABSSUM || p.cvec)) {
     const int64_t m_last = (m0 + GBM < M ? m0 + GBM : M) - 1;
     d_first = (int)(m0 / p.S);
     const int64_t nd = m_last / p.S - d_first + 1;
@@ -369,7 +353,7 @@ gemm_kernel(GemmArgs p) {
         const int64_t k = k0 + e_k;
         const bool ok = e_dom < ndom && k < K;
         const int64_t d = (int64_t)d_first + e_dom;
-        tab_reg = ok ? relax_entry(rtab, rpl0, rpl1, rpl2, rpl3, d * K + k) : make_float4(1.f, 0.f, 1.f, 0.f);
+        tab_reg = ok ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
         if constexpr (ADD) add_reg = ok ? p.add_l[d * p.add_ld + k] : 0.f;
         if constexpr (CV && RR) cv_reg = ok ? p.cvec[d * p.cvec_ld + k] : 0.f;
         if constexpr (KB && RR)
@@ -402,7 +386,7 @@ gemm_kernel(GemmArgs p) {
       } else {
         if (k >= K) return a;
         const int64_t d = a_dom[j];
-        r = (rtab || rpl0) ? relax_entry(rtab, rpl0, rpl1, rpl2, rpl3, d * K + k) : make_float4(1.f, 0.f, 1.f, 0.f);
+        r = p.relax ? p.relax[d * K + k] : make_float4(1.f, 0.f, 1.f, 0.f);
         if (use_add) add = p.add_l[d * p.add_ld + k];
         if (p.kbias) kb = p.kbias[k];
         if (p.cvec) cv = p.cvec[d * p.cvec_ld + k];

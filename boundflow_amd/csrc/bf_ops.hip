@@ -153,6 +153,15 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
   hi[i] = u;
 }
 
+// The relaxation table {alpha_u, beta_u, alpha_l, beta_l} from the four separate tensors
+// of a FusedReluAffineRequest: one 16-byte store per entry.
+__global__ void planes_table_kernel(const float* __restrict__ au, const float* __restrict__ bu,
+                                    const float* __restrict__ al, const float* __restrict__ bl, int64_t n,
+                                    float4* __restrict__ table) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) table[i] = make_float4(au[i], bu[i], al[i], bl[i]);
+}
+
 __global__ void fill_kernel(float* __restrict__ p, int64_t n, float v) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -976,6 +985,20 @@ int bf_concretize_finalize(const float* partial_u, const float* partial_l, int n
   return concretize_finalize(partial_u, partial_l, nparts, M, cen_u, cen_l, b_u, b_l, eps, norm_p, lb, ub, stream);
 }
 
+int bf_relu_relax_table_from_planes(const float* alpha_u, const float* beta_u, const float* alpha_l,
+                                    const float* beta_l, int64_t n, float* table, hipStream_t stream) {
+  BF_REQUIRE(n >= 0, "bf_relu_relax_table_from_planes: bad size");
+  if (n == 0) return BF_OK;
+  BF_REQUIRE(alpha_u && beta_u && alpha_l && beta_l && table, "bf_relu_relax_table_from_planes: null pointer");
+  BF_REQUIRE(((uintptr_t)table & 15) == 0, "bf_relu_relax_table_from_planes: table must be 16-byte aligned");
+  const int64_t blocks = (n + 255) / 256;
+  BF_REQUIRE(blocks < (1LL << 31), "bf_relu_relax_table_from_planes: too many entries");
+  hipLaunchKernelGGL(planes_table_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, alpha_u, beta_u, alpha_l,
+                     beta_l, n, reinterpret_cast<float4*>(table));
+  BF_LAUNCH_CHECK("planes_table_kernel");
+  return BF_OK;
+}
+
 int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, int64_t D,
                         int64_t K, float* table, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && K >= 0, "bf_relu_relax_table: bad sizes");
@@ -985,20 +1008,18 @@ int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* a
   return relax_table(pre_lo, pre_hi, alpha, alpha_ld, D, K, reinterpret_cast<float4*>(table), stream);
 }
 
-// bf_crown_relu_linear_fwd with the relaxation as a table (relax) or as four planes (planes).
-static int relu_linear_fwd(const char* who, const float* A_u, const float* A_l, int64_t a_dstride, int64_t D,
-                           int64_t S, int64_t N, const float* relax, const float* const* planes, const float* add_l,
-                           int64_t add_ld, const float* W, int64_t P, int w_trans, const float* bias,
-                           const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
-                           float* b_u_out, float* b_l_out, hipStream_t stream) {
-  BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && P > 0, "%s: bad sizes", who);
+int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
+                             const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
+                             int w_trans, const float* bias, const float* b_u_in, const float* b_l_in,
+                             float* A_prev_u, float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream) {
+  BF_REQUIRE(D >= 0 && S >= 0 && N > 0 && P > 0, "bf_crown_relu_linear_fwd: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
-  BF_REQUIRE(W != nullptr, "%s: null weight", who);
-  BF_REQUIRE(((uintptr_t)relax & 15) == 0, "%s: relax table must be 16-byte aligned", who);
+  BF_REQUIRE(W != nullptr, "bf_crown_relu_linear_fwd: null weight");
+  BF_REQUIRE(((uintptr_t)relax & 15) == 0, "bf_crown_relu_linear_fwd: relax table must be 16-byte aligned");
   BF_REQUIRE((A_u != nullptr) == (A_prev_u != nullptr) && (A_l != nullptr) == (A_prev_l != nullptr),
-             "%s: input/output pointer mismatch", who);
-  BF_REQUIRE(A_u || A_l, "%s: no coefficient", who);
+             "bf_crown_relu_linear_fwd: input/output pointer mismatch");
+  BF_REQUIRE(A_u || A_l, "bf_crown_relu_linear_fwd: no coefficient");
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   int nz = 0;
@@ -1021,12 +1042,10 @@ static int relu_linear_fwd(const char* who, const float* A_u, const float* A_l, 
   a.K = N;
   a.S = S;
   a.relax = reinterpret_cast<const float4*>(relax);
-  if (planes)
-    for (int i = 0; i < 4; ++i) a.relax_pl[i] = planes[i];
   a.add_l = add_l;
   a.add_ld = add_ld;
   a.kbias = bias;
-  if (relax || planes || add_l || bias) return gemm_dispatch(a, PRO_RELAX, EPI_STORE, nz, stream);
+  if (relax || add_l || bias) return gemm_dispatch(a, PRO_RELAX, EPI_STORE, nz, stream);
   // nothing to relax (A already relaxed): the plain contraction, b_out = b_in
   const int rc = gemm_dispatch(a, PRO_PLAIN, EPI_STORE, nz, stream);
   for (int z = 0; z < nz && rc == 0; ++z) {
@@ -1036,25 +1055,6 @@ static int relu_linear_fwd(const char* who, const float* A_u, const float* A_l, 
     }
   }
   return rc;
-}
-
-int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
-                             const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
-                             int w_trans, const float* bias, const float* b_u_in, const float* b_l_in,
-                             float* A_prev_u, float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream) {
-  return relu_linear_fwd("bf_crown_relu_linear_fwd", A_u, A_l, a_dstride, D, S, N, relax, nullptr, add_l, add_ld, W,
-                         P, w_trans, bias, b_u_in, b_l_in, A_prev_u, A_prev_l, b_u_out, b_l_out, stream);
-}
-
-int bf_crown_relu_planes_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
-                                    int64_t N, const float* alpha_u, const float* beta_u, const float* alpha_l,
-                                    const float* beta_l, const float* W, int64_t P, int w_trans, const float* bias,
-                                    const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
-                                    float* b_u_out, float* b_l_out, hipStream_t stream) {
-  BF_REQUIRE(alpha_u && beta_u && alpha_l && beta_l, "bf_crown_relu_planes_linear_fwd: null relaxation plane");
-  const float* planes[4] = {alpha_u, beta_u, alpha_l, beta_l};
-  return relu_linear_fwd("bf_crown_relu_planes_linear_fwd", A_u, A_l, a_dstride, D, S, N, nullptr, planes, nullptr,
-                         0, W, P, w_trans, bias, b_u_in, b_l_in, A_prev_u, A_prev_l, b_u_out, b_l_out, stream);
 }
 
 int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,

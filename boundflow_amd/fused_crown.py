@@ -263,11 +263,11 @@ class HipFusedCrownExecutor:
             return self._run(request, _lib.stream_handle(stream))
 
     def _run(self, request: FusedReluAffineRequest, st) -> FusedReluAffineResult:
-        """One launch per region: the contraction (linear) or the transposed convolution
-        (conv2d, channel-last gather) reads the request's four relaxation tensors in its
-        prologue / while staging each row, and reduces the bias rows in the same pass.
-        Conv shapes the channel-last kernel does not take run the relaxation pass and then
-        the transposed convolution."""
+        """A linear region: the four relaxation tensors interleaved into the kernels' table
+        (one small launch), then the fused relaxation + contraction.  A conv region: one
+        launch, the channel-last transposed convolution reading the four tensors while it
+        stages each row; conv shapes that kernel does not take run the relaxation pass and
+        then the transposed convolution."""
         dev = request.A_u.device
         D, S = int(request.A_u.shape[0]), int(request.A_u.shape[1])
         M = D * S
@@ -281,10 +281,13 @@ class HipFusedCrownExecutor:
             Wt = transposed(request.weight)   # [P, N]: the kernel's faster operand layout, kept across calls
             pu = torch.empty(D, S, P, device=dev, dtype=torch.float32)
             pl = torch.empty(D, S, P, device=dev, dtype=torch.float32)
+            table = torch.empty(D * N * 4, device=dev, dtype=torch.float32)
+            with _timed("executor_relax_table", 0.0, 4.0 * 8 * D * N):
+                _lib.call("bf_relu_relax_table_from_planes", *[_lib.ptr(t) for t in planes], D * N, _lib.ptr(table), st)
             with _timed("executor_relu_linear", 4.0 * M * N * P, 4.0 * (2 * M * N + 4 * D * N + N * P + 2 * M * P)):
-                _lib.call("bf_crown_relu_planes_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S,
-                          N, *[_lib.ptr(t) for t in planes], _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None,
-                          _lib.ptr(pu), _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
+                _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
+                          _lib.ptr(table), None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None, _lib.ptr(pu),
+                          _lib.ptr(pl), _lib.ptr(du), _lib.ptr(dl), st)
             return FusedReluAffineResult(pu, pl, du, dl)
         Co, Ho, Wo = (int(d) for d in request.output_shape)
         Ci, Hi, Wi = (int(d) for d in request.input_shape)
@@ -306,7 +309,8 @@ class HipFusedCrownExecutor:
                           _lib.ptr(du), _lib.ptr(dl), st)
             return FusedReluAffineResult(pu, pl, du, dl)
         # other conv shapes: the relaxation pass (from the interleaved table), then the transposed convolution
-        table = torch.stack([t.reshape(D, N) for t in planes], dim=-1).contiguous()
+        table = torch.empty(D * N * 4, device=dev, dtype=torch.float32)
+        _lib.call("bf_relu_relax_table_from_planes", *[_lib.ptr(t) for t in planes], D * N, _lib.ptr(table), st)
         ru = torch.empty(M, N, device=dev)
         rl = torch.empty(M, N, device=dev)
         with _timed("executor_relu_relax", 0.0, 4.0 * (4 * M * N + 4 * D * N)):

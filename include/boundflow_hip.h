@@ -109,6 +109,13 @@ int bf_ibp_batched_linear(const float* lo, const float* hi, int64_t B, int64_t I
 int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, int64_t D,
                         int64_t K, float* table, hipStream_t stream);
 
+/* The same table from the four separate tensors of a FusedReluAffineRequest
+ * (runtime/fused_crown.py:33-48: alpha_u, beta_u, alpha_l, beta_l, each n =
+ * D*K floats), interleaved in one pass: what HipFusedCrownExecutor hands the
+ * contraction of a "fused_relu_linear" region (run, :97-123). */
+int bf_relu_relax_table_from_planes(const float* alpha_u, const float* beta_u, const float* alpha_l,
+                                    const float* beta_l, int64_t n, float* table, hipStream_t stream);
+
 /* One ReLU -> Linear region: A' = relax(A) (upper: sel(A>=0, alpha_u, alpha_l),
  * lower mirrored, plus the optional beta split coefficient add_l on the lower
  * bound), A_prev = A' @ W on fp32 MFMA, and
@@ -126,17 +133,6 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
                              const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
                              int w_trans, const float* bias, const float* b_u_in, const float* b_l_in,
                              float* A_prev_u, float* A_prev_l, float* b_u_out, float* b_l_out, hipStream_t stream);
-
-/* bf_crown_relu_linear_fwd with the relaxation as the four tensors of a
- * "fused_relu_linear" FusedReluAffineRequest (runtime/fused_crown.py:33-48,
- * run at :97-123) -- alpha_u, beta_u, alpha_l, beta_l, each [D, N] -- read by
- * the contraction's prologue directly instead of an interleaved table; no
- * split term. */
-int bf_crown_relu_planes_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S,
-                                    int64_t N, const float* alpha_u, const float* beta_u, const float* alpha_l,
-                                    const float* beta_l, const float* W, int64_t P, int w_trans, const float* bias,
-                                    const float* b_u_in, const float* b_l_in, float* A_prev_u, float* A_prev_l,
-                                    float* b_u_out, float* b_l_out, hipStream_t stream);
 
 /* The input-layer region fused with the concretization (kernel #4):
  * lb = (A' . cvec - eps * sum_i |(A' W)_i| * rad_i) + b, ub mirrored;
