@@ -23,6 +23,8 @@ baseline and parity over its whole batch.
 D1 (not a BASELINE configuration) measures the DAG path: CROWN on a residual MLP.
     python bench.py --calibrate-copy MIB   # one plain device copy of MIB MiB, the
                                            # reference kernel for HBM byte counters
+    python bench.py --hbm-ceiling MIB      # attainable HBM rates on MIB MiB buffers:
+                                           # fill, copy, read-only sum, two-stream fill
 """
 
 from __future__ import annotations
@@ -373,6 +375,50 @@ def _settle(run, warmup: int, seconds: float = 0.2) -> None:
     torch.cuda.synchronize()
 
 
+def hbm_ceiling(mib: int, reps: int) -> dict:
+    """Attainable HBM rates of plain streams over ``mib`` MiB buffers, each launch
+    timed with HIP events on the current stream and averaged over ``reps``:
+    fill (write only), copy (read + write, the runtime's blit), sum (read only) and
+    a broadcast product out[d, r, k] = w[r, k] * s[d, k] whose small operands stay
+    in L2 (the write-bound shape of the strided relaxation pass: 500 x 500 rows per
+    domain, two outputs)."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.rand(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    R = K = 500
+    D = max(1, n // (2 * R * K))
+    wm = torch.rand(R, K, device="cuda:0")
+    s = torch.rand(D, 1, K, device="cuda:0")
+    out_u = torch.empty(D, R, K, device="cuda:0")
+    out_l = torch.empty(D, R, K, device="cuda:0")
+
+    def bcast():
+        torch.mul(wm, s, out=out_u)
+        torch.mul(wm, s, out=out_l)
+
+    cases = {
+        "fill": (lambda: dst.fill_(1.0), 4 * n),
+        "copy": (lambda: dst.copy_(src), 8 * n),
+        "sum": (lambda: src.sum(), 4 * n),
+        "broadcast_product_two_outputs": (bcast, 2 * 4 * D * R * K),
+    }
+    res = {"mib": mib, "reps": reps}
+    for name, (fn, nbytes) in cases.items():
+        _settle(fn, 3, seconds=0.3)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            fn()
+        s1.record()
+        s1.synchronize()
+        ms = s0.elapsed_time(s1) / reps
+        res[name] = {"bytes": nbytes, "avg_ms": round(ms, 4), "gbps": round(nbytes / ms / 1e6, 1),
+                     "frac_of_peak": round(nbytes / ms / 1e6 / PEAK_HBM_GBPS, 4)}
+    return res
+
+
 def measure(name: str, steps: int, warmup: int, no_graph: bool):
     """One configuration: throughput of ``steps`` timed steps after ``warmup``, the
     per-kernel durations of the library's launches and the dominant kernel's
@@ -468,6 +514,8 @@ def main() -> int:
                     help="CPU baseline time of each secondary configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
+    ap.add_argument("--hbm-ceiling", type=int, default=0, metavar="MIB",
+                    help="time plain fill / copy / read streams of MIB MiB (the attainable HBM ceiling)")
     ap.add_argument("--no-graph", action="store_true", help="issue every launch from Python (no HIP graph replay)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="C2 alone, without the C5 domains/s and C1 / C3 / C4 bounds/s records")
@@ -493,6 +541,9 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}), flush=True)
+        return 0
+    if args.hbm_ceiling:
+        print(json.dumps(hbm_ceiling(args.hbm_ceiling, max(args.steps, 5))), flush=True)
         return 0
     head, w, unit = measure(args.config, args.steps, args.warmup, args.no_graph)
     line = {

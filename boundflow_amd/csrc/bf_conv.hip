@@ -14,6 +14,7 @@
 //   an optional fused concretization epilogue: the weighted |y| row sum (the
 //   Linf / box norm) and, for the gradient pass, h = h_scale[r] * sign(y) * w.
 
+#include <cstdlib>
 #include <cstring>
 
 #include "bf_common.h"
@@ -760,6 +761,7 @@ struct SmallTArgs {
   int Co4, npix, nblk;     // channels padded to 4, pixels Ho*Wo, 16-pixel blocks
   int vec;                 // rows copied as float4 (npix % 16 == 0 and 16-byte aligned row starts)
   FastDiv f_Wi, f_sh, f_sw, f_pitch;   // index divisions of the col2im and the map copy
+  int pitchz, zsz;         // conv_t_small_fast_kernel: tap-row pitch of Z, floats per channel block
 };
 
 // RELAX: the input layer's ReLU relaxation applied while each row is staged, with
@@ -940,6 +942,329 @@ conv_t_small_kernel(SmallTArgs g, ConvRelax rx) {
       }
     }
   }
+}
+
+// Register form of conv_t_small_kernel for the usual input layers: at most 16 map
+// channels, at most 256 map pixels, at most 3 output channels of at most 2 GTM pixels,
+// at most 2 x 2 taps per output pixel (the 1 -> 16 and 3 -> 16, 4 x 4 stride-2
+// convolutions of 28 x 28 and 32 x 32 images, say).
+//   * Workgroups of 16 waves, one per CU.  Wave jb owns the 16-pixel block jb of the
+//     map: lane (k4, col) loads the row's elements (co = k4 + 4 kk, pixel 16 jb + col)
+//     straight into registers -- exactly its B operands of MFMA step kk -- and applies the
+//     relaxation there, so the map never passes through LDS.  The relaxation's slopes
+//     and intercepts, the split term and the center projection stay in registers while
+//     consecutive rows share a domain, the bias map for the whole launch, the weights
+//     (A operands) in LDS.
+//   * A lane slot past the map's channels or pixels reads element 0 of the row and
+//     carries zero slopes, zero weights and zero operands, so it adds exact zeros
+//     (the coefficient rows are finite).
+//   * Z of every output channel is written to LDS at a fixed layout; the col2im reads
+//     each output pixel's taps at offsets computed once per workgroup (an absent tap
+//     reads a zero cell: adding +0 to a sum that starts at +0 leaves it unchanged).
+//   * Two barriers per row; the next row's elements load during the gather.
+// The tap products, the col2im order and the norm order are those of
+// conv_t_small_kernel, so y, the norms and the gradient seeds are identical; the row
+// sums b_out and c_out add the same terms in another order.
+// SRC: 0 the rows as given (no relaxation); 1 the relaxation from the pre-activation
+// box (lo, hi, optional alpha); 2 from the four planes {alpha_u, beta_u, alpha_l, beta_l}.
+constexpr int SF_NT = 1024;   // threads per workgroup
+constexpr int SF_NW = SF_NT / 64;
+constexpr int SF_UB = 1;      // 16-pixel blocks per wave: map pixels <= 16 * SF_NW * SF_UB
+constexpr int SF_KS = 4;      // MFMA k steps: map channels <= 4 * SF_KS
+constexpr int SF_CI = 3;      // output channels
+constexpr int SF_PPT = 1;     // output pixels per thread: Hi * Wi <= SF_PPT * SF_NT
+constexpr int SF_PITCHZ = 16 * SF_NW * SF_UB + 4;   // tap-row pitch of Z: 4 banks between tap rows
+constexpr int SF_ZSZ = 16 * SF_PITCHZ + 4;               // floats per output channel: Z, then the zero cell
+constexpr int SF_WS = SF_CI * SF_KS * 64;                // the A operands
+
+template <int SRC>
+__global__ void __launch_bounds__(SF_NT, 4)   // 4 waves per SIMD: one workgroup per CU
+conv_t_small_fast_kernel(SmallTArgs g, ConvRelax rx) {
+  constexpr bool RELAX = SRC != 0;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* Ws = smem;           // [SF_CI][SF_KS][64 lanes]
+  float* Zs = smem + SF_WS;   // [SF_CI][SF_ZSZ]
+  __shared__ float red[SF_NW];
+  __shared__ float rred[SF_NW][3];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: block indices stay scalar
+  const int z = blockIdx.y;
+  const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
+  const float* __restrict__ X = g.X[z];
+  float* __restrict__ y = g.y[z];
+  float* __restrict__ nrm = g.nrm[z];
+  float* __restrict__ relaxed = RELAX ? rx.relaxed[z] : nullptr;
+  const int taps = g.KH * g.KW;
+  const int npix = g.npix, HW = g.Hi * g.Wi;
+  const uint32_t nin = (uint32_t)(g.Co * npix);
+  const int64_t nout = (int64_t)g.Ci * HW;
+  const int k4 = lane >> 4, col = lane & 15;
+  constexpr int zero_cell = 16 * SF_PITCHZ;
+  const int ksteps = g.Co4 >> 2;   // uniform
+
+  if (tid < SF_CI) Zs[tid * SF_ZSZ + zero_cell] = 0.f;
+  // A operands: Ws[n][kk][lane (k4, col)] = W[co = k4 + 4 kk, n, tap = col]
+  for (int i = tid; i < SF_WS; i += SF_NT) {
+    const int l = i & 63, nk = i >> 6, n = nk / SF_KS, kk = nk - n * SF_KS;
+    const int co = (l >> 4) + 4 * kk, t = l & 15;
+    Ws[i] = (n < g.Ci && co < g.Co && t < taps) ? g.W[((int64_t)co * g.Ci + n) * taps + t] : 0.f;
+  }
+  // this lane's row element of block u, step kk: xo[u][kk] (0 for a slot past the map)
+  uint32_t xo[SF_UB][SF_KS];
+  uint32_t pmask = 0;   // bit u SF_KS + kk: the slot holds an element of the map
+#pragma unroll
+  for (int u = 0; u < SF_UB; ++u)
+#pragma unroll
+    for (int kk = 0; kk < SF_KS; ++kk) {
+      const int co = k4 + 4 * kk, p = 16 * (wave + SF_NW * u) + col;
+      const bool present = co < g.Co && p < npix;
+      xo[u][kk] = present ? (uint32_t)(co * npix + p) : 0u;
+      if (present) pmask |= 1u << (u * SF_KS + kk);
+    }
+  auto present_at = [&](int u, int kk) { return ((pmask >> (u * SF_KS + kk)) & 1u) != 0; };
+  // the taps of output pixel o_j = tid + SF_NT j, in the order (kh, kw) of conv_t_small_kernel
+  int off[SF_PPT][4];
+#pragma unroll
+  for (int j = 0; j < SF_PPT; ++j) {
+    const int o = tid + SF_NT * j;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) off[j][t] = zero_cell;
+    if (o < HW) {
+      const int oh = o / g.Wi, ow = o - oh * g.Wi;
+      const int qh = (oh + g.ph) / g.sh, qw = (ow + g.pw) / g.sw;
+      const int kh0 = oh + g.ph - qh * g.sh, kw0 = ow + g.pw - qw * g.sw;
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int kh = kh0 + g.sh * a, kw = kw0 + g.sw * b, ih = qh - a, iw = qw - b;
+          if (kh < g.KH && kw < g.KW && ih >= 0 && ih < g.Ho && iw >= 0 && iw < g.Wo)
+            off[j][2 * a + b] = (kh * g.KW + kw) * SF_PITCHZ + ih * g.Wo + iw;
+        }
+    }
+  }
+
+  const int64_t r0 = (int64_t)blockIdx.x * g.rows_per_wg;
+  const int64_t r_end = r0 + g.rows_per_wg < g.R ? r0 + g.rows_per_wg : g.R;
+  float xv[SF_UB][SF_KS];
+  auto load_row = [&](int64_t r) {
+    const float* __restrict__ xr = X + r * (int64_t)nin;
+#pragma unroll
+    for (int u = 0; u < SF_UB; ++u)
+#pragma unroll
+      for (int kk = 0; kk < SF_KS; ++kk) xv[u][kk] = xr[xo[u][kk]];
+  };
+  // per element of the cached domain: the slopes for v >= 0 and v < 0 on this side, the
+  // intercepts for v >= 0 and v < 0 (ip, in), the split term, the center projection; the bias map
+  float sp[SF_UB][SF_KS], sn[SF_UB][SF_KS], ip[SF_UB][SF_KS], in_[SF_UB][SF_KS];
+  float adc[SF_UB][SF_KS], cvc[SF_UB][SF_KS], kbc[SF_UB][SF_KS];
+  if constexpr (RELAX) {
+#pragma unroll
+    for (int u = 0; u < SF_UB; ++u)
+#pragma unroll
+      for (int kk = 0; kk < SF_KS; ++kk) kbc[u][kk] = (rx.kbias && present_at(u, kk)) ? rx.kbias[xo[u][kk]] : 0.f;
+  }
+  // domain of the current row, and the row's index inside it
+  int64_t d = r0 / g.S;
+  int64_t s_in = r0 - d * g.S;
+  int64_t d_cached = -1;
+  if (r0 < r_end) load_row(r0);
+  for (int64_t r = r0; r < r_end; ++r) {
+    float bop[SF_UB][SF_KS];
+    if constexpr (RELAX) {
+      if (d != d_cached) {   // uniform
+        d_cached = d;
+        const int64_t dn = d * (int64_t)nin;
+#pragma unroll
+        for (int u = 0; u < SF_UB; ++u)
+#pragma unroll
+          for (int kk = 0; kk < SF_KS; ++kk) {
+            // opaque to the optimizer: the element addresses are formed here, once per domain,
+            // rather than hoisted out of the row loop as live 64-bit registers
+            uint32_t e = xo[u][kk];
+            asm volatile("" : "+v"(e));
+            const bool pr = present_at(u, kk);
+            float4 t = make_float4(1.f, 0.f, 1.f, 0.f);
+            if (SRC == 2) {
+              t = make_float4(rx.pl[0][dn + e], rx.pl[1][dn + e], rx.pl[2][dn + e], rx.pl[3][dn + e]);
+            } else if (rx.lo) {
+              const bool has_alpha = rx.alpha != nullptr;
+              const Relax rr = relu_relax(rx.lo[dn + e], rx.hi[dn + e], has_alpha,
+                                          has_alpha ? clamp01(rx.alpha[d * rx.alpha_ld + e]) : 0.f);
+              t = make_float4(rr.au, rr.bu, rr.al, rr.bl);
+            }
+            // lower: A' = A (al | au), A * (bl | bu); upper: A' = A (au | al), A * (bu | bl)  (v >= 0 | v < 0)
+            sp[u][kk] = pr ? (lower ? t.z : t.x) : 0.f;
+            sn[u][kk] = pr ? (lower ? t.x : t.z) : 0.f;
+            ip[u][kk] = pr ? (lower ? t.w : t.y) : 0.f;
+            in_[u][kk] = pr ? (lower ? t.y : t.w) : 0.f;
+            adc[u][kk] = (pr && lower && rx.add) ? rx.add[d * rx.add_ld + e] : 0.f;
+            cvc[u][kk] = (pr && rx.cvec) ? rx.cvec[dn + e] : 0.f;
+          }
+      }
+      float sb = 0.f, sk = 0.f, sc = 0.f;
+#pragma unroll
+      for (int u = 0; u < SF_UB; ++u)
+#pragma unroll
+        for (int kk = 0; kk < SF_KS; ++kk) {
+          // relax_element's arithmetic: a slot past the map has zero slopes and terms
+          const float v = xv[u][kk];
+          const bool nn = v >= 0.f;
+          float o = v * (nn ? sp[u][kk] : sn[u][kk]);
+          sb += v * (nn ? ip[u][kk] : in_[u][kk]);
+          if (lower && rx.add) o = o + adc[u][kk];
+          if (rx.kbias) sk += o * kbc[u][kk];
+          if (rx.cvec) sc += o * cvc[u][kk];
+          if (relaxed && present_at(u, kk)) relaxed[r * (int64_t)nin + xo[u][kk]] = o;
+          bop[u][kk] = o;
+        }
+      sb = wave_sum(sb);
+      sk = wave_sum(sk);
+      sc = wave_sum(sc);
+      if (lane == 0) {
+        rred[wave][0] = sb;
+        rred[wave][1] = sk;
+        rred[wave][2] = sc;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < SF_UB; ++u)
+#pragma unroll
+        for (int kk = 0; kk < SF_KS; ++kk) bop[u][kk] = present_at(u, kk) ? xv[u][kk] : 0.f;
+    }
+    // tap products of every output channel: Z_n[tap 4 k4 + q][pixel 16 jb + col] = acc[q]
+#pragma unroll
+    for (int n = 0; n < SF_CI; ++n) {
+      if (n >= g.Ci) break;   // uniform
+      float wr[SF_KS];
+#pragma unroll
+      for (int kk = 0; kk < SF_KS; ++kk) wr[kk] = Ws[(n * SF_KS + kk) * 64 + lane];
+#pragma unroll
+      for (int u = 0; u < SF_UB; ++u) {
+        const int jb = wave + SF_NW * u;
+        if (jb >= g.nblk) break;   // uniform
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < SF_KS; ++kk)
+          if (kk < ksteps) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wr[kk], bop[u][kk], acc, 0, 0, 0);
+        float* zr = Zs + n * SF_ZSZ + (4 * k4) * SF_PITCHZ + 16 * jb + col;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) zr[q * SF_PITCHZ] = acc[q];
+      }
+    }
+    if (r + 1 < r_end) load_row(r + 1);
+    __syncthreads();   // Z of every channel written; the row sums of every wave posted
+    if constexpr (RELAX) {
+      if (tid == 0) {
+        float tb = 0.f, tk = 0.f, tcs = 0.f;
+        for (int q = 0; q < SF_NW; ++q) {
+          tb += rred[q][0];
+          tk += rred[q][1];
+          tcs += rred[q][2];
+        }
+        if (rx.b_out[z]) rx.b_out[z][r] = ((rx.b_in[z] ? rx.b_in[z][r] : 0.f) + tb) + tk;
+        if (rx.c_out[z]) rx.c_out[z][r] = tcs;
+      }
+    }
+    const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
+    float s = 0.f;
+#pragma unroll
+    for (int n = 0; n < SF_CI; ++n) {
+      if (n >= g.Ci) break;   // uniform
+      const float* __restrict__ zn = Zs + n * SF_ZSZ;
+#pragma unroll
+      for (int j = 0; j < SF_PPT; ++j) {
+        const int o = tid + SF_NT * j;
+        if (o >= HW) break;
+        float v = 0.f;
+        v += zn[off[j][0]];
+        v += zn[off[j][1]];
+        v += zn[off[j][2]];
+        v += zn[off[j][3]];
+        const int64_t oidx = (int64_t)n * HW + o;
+        if (y) y[r * nout + oidx] = v;
+        if (nrm) {
+          const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
+          s = norm_step(s, v, wgt, g.wv != nullptr, g.nkind);
+          if (lower && g.h_out) {
+            const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
+            g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
+          }
+        }
+      }
+    }
+    if (nrm) {
+      s = norm_wave_xor(s, g.nkind);
+      if (lane == 0) red[wave] = s;
+    }
+    __syncthreads();   // every wave's taps gathered (Z free for the next row); the norms posted
+    if (nrm && tid == 0) {
+      float tsum = 0.f;
+      for (int q = 0; q < SF_NW; ++q) tsum = norm_join(tsum, red[q], g.nkind);
+      nrm[r] = tsum;
+    }
+    if (++s_in == g.S) {
+      s_in = 0;
+      ++d;
+    }
+  }
+}
+
+// Plan of conv_t_small_fast_kernel over a conv_t_small_kernel plan; false when it does not apply.
+static bool conv_t_small_fast_plan(SmallTArgs& g, size_t* lds_bytes) {
+  if (g.Co > 4 * SF_KS || g.nblk > SF_NW * SF_UB || g.Ci > SF_CI || g.Hi * g.Wi > SF_PPT * SF_NT) return false;
+  if ((g.KH + g.sh - 1) / g.sh > 2 || (g.KW + g.sw - 1) / g.sw > 2) return false;
+  *lds_bytes = sizeof(float) * (size_t)(SF_WS + SF_CI * SF_ZSZ);
+  return true;
+}
+
+// Rows per workgroup of conv_t_small_fast_kernel: one round of one workgroup per CU.
+static int small_fast_rows_per_wg(int64_t work) {
+  const int64_t rpw = (work + 255) / 256;
+  return rpw < 1 ? 1 : (rpw > 64 ? 64 : (int)rpw);
+}
+
+// BOUNDFLOW_CONV_T_SMALL=generic keeps every shape on conv_t_small_kernel (for
+// measurement); read once when the library is loaded.
+static bool small_fast_disabled_from_env() {
+  const char* v = std::getenv("BOUNDFLOW_CONV_T_SMALL");
+  return v != nullptr && std::strcmp(v, "generic") == 0;
+}
+static const bool kSmallFastDisabled = small_fast_disabled_from_env();
+
+static int gather_rows_per_wg(int64_t work);
+
+// Launch of the tap-product transposed conv over a conv_t_small_kernel plan: the
+// register form where it applies, else the generic kernel (which takes the
+// relaxation from the pre-activation box only).
+template <bool RELAX>
+static int small_t_launch(SmallTArgs& g, const ConvRelax& rx, unsigned nz, size_t glds, const char* who,
+                          hipStream_t stream) {
+  size_t flds = 0;
+  if (!kSmallFastDisabled && conv_t_small_fast_plan(g, &flds)) {
+    BF_REQUIRE(g.R * (int64_t)g.Co * g.npix < (1LL << 62) && (int64_t)g.Co * g.npix < (1LL << 31),
+               "%s: rows too large", who);
+    const int rpw = small_fast_rows_per_wg(g.R * nz);
+    g.rows_per_wg = rpw;
+    BF_REQUIRE((g.R + rpw - 1) / rpw < (1LL << 31), "%s: too many rows", who);
+    const dim3 grid((unsigned)((g.R + rpw - 1) / rpw), nz);
+    if (!RELAX)
+      hipLaunchKernelGGL(conv_t_small_fast_kernel<0>, grid, dim3(SF_NT), flds, stream, g, rx);
+    else if (rx.pl[0])
+      hipLaunchKernelGGL(conv_t_small_fast_kernel<2>, grid, dim3(SF_NT), flds, stream, g, rx);
+    else
+      hipLaunchKernelGGL(conv_t_small_fast_kernel<1>, grid, dim3(SF_NT), flds, stream, g, rx);
+    BF_LAUNCH_CHECK(who);
+    return BF_OK;
+  }
+  BF_REQUIRE(!RELAX || rx.pl[0] == nullptr, "%s: relaxation planes need the register form of the kernel", who);
+  const int rpw = gather_rows_per_wg(g.R * nz);
+  g.rows_per_wg = rpw;
+  BF_REQUIRE((g.R + rpw - 1) / rpw < (1LL << 31), "%s: too many rows", who);
+  hipLaunchKernelGGL(conv_t_small_kernel<RELAX>, dim3((unsigned)((g.R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream,
+                     g, rx);
+  BF_LAUNCH_CHECK(who);
+  return BF_OK;
 }
 
 // Plan of conv_t_small_kernel; false when it does not apply.
@@ -1186,15 +1511,9 @@ static int conv_transpose_rows_launch(const float* A_u, const float* A_l, int64_
       g.S = S;
       g.vec = (g.npix % 16 == 0) && (((uintptr_t)(A_u ? A_u : A_l) & 15) == 0) &&
               (A_u == nullptr || A_l == nullptr || ((uintptr_t)A_l & 15) == 0) ? 1 : 0;
-      const int rpw = gather_rows_per_wg(R * nz);
-      g.rows_per_wg = rpw;
-      BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
       ConvRelax rx;
       memset(&rx, 0, sizeof(rx));
-      hipLaunchKernelGGL(conv_t_small_kernel<false>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds,
-                         stream, g, rx);
-      BF_LAUNCH_CHECK("conv_t_small_kernel");
-      return BF_OK;
+      return small_t_launch<false>(g, rx, nz, glds, "bf_conv_transpose_rows (tap products)", stream);
     }
   }
   {
@@ -1394,13 +1713,6 @@ int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int6
   BF_REQUIRE(alpha_u && beta_u && alpha_l && beta_l, "bf_crown_relu_planes_conv_transpose: null relaxation plane");
   BF_REQUIRE((A_u == nullptr) == (y_u == nullptr) && (A_l == nullptr) == (y_l == nullptr),
              "bf_crown_relu_planes_conv_transpose: each given coefficient needs an output");
-  GatherArgs g;
-  memset(&g, 0, sizeof(g));
-  size_t glds = 0;
-  if (!conv_t_hwc_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
-    set_error("bf_crown_relu_planes_conv_transpose: shape not supported (bf_conv_transpose_hwc_supported)");
-    return BF_EINVAL;
-  }
   const unsigned nz = (A_u && A_l) ? 2u : 1u;
   ConvRelax rx;
   memset(&rx, 0, sizeof(rx));
@@ -1409,6 +1721,37 @@ int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int6
   rx.pl[2] = alpha_l;
   rx.pl[3] = beta_l;
   rx.kbias = kbias;
+  {
+    // few output channels (an input layer): the tap-product kernel in its register form
+    SmallTArgs sg;
+    memset(&sg, 0, sizeof(sg));
+    size_t slds = 0, flds = 0;
+    if (!kSmallFastDisabled && conv_t_small_plan(sg, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &slds) &&
+        conv_t_small_fast_plan(sg, &flds)) {
+      int nzi = 0;
+      if (A_u) {
+        sg.X[nzi] = A_u; sg.y[nzi] = y_u;
+        rx.b_in[nzi] = b_u_in; rx.b_out[nzi] = b_u_out;
+        ++nzi;
+      }
+      if (A_l) {
+        sg.X[nzi] = A_l; sg.y[nzi] = y_l;
+        rx.b_in[nzi] = b_l_in; rx.b_out[nzi] = b_l_out;
+        ++nzi;
+      }
+      sg.z_lower_first = A_u ? 0 : 1;
+      sg.W = W;
+      sg.S = S;
+      return small_t_launch<true>(sg, rx, nz, slds, "bf_crown_relu_planes_conv_transpose", stream);
+    }
+  }
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t glds = 0;
+  if (!conv_t_hwc_plan(g, R, Co, Ho, Wo, Ci, KH, KW, sh, sw, ph, pw, Hi, Wi, &glds)) {
+    set_error("bf_crown_relu_planes_conv_transpose: shape not supported (bf_conv_transpose_hwc_supported)");
+    return BF_EINVAL;
+  }
   int nzi = 0;
   if (A_u) {
     g.X[nzi] = A_u; g.y[nzi] = y_u;
@@ -1509,12 +1852,8 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
   g.vec = (g.npix % 16 == 0) && al16(A_u) && al16(A_l) && al16(pre_lo) && al16(pre_hi) && al16(alpha) &&
           al16(add_l) && al16(kbias) && al16(cvec) && al16(relaxed_u) && al16(relaxed_l) &&
           (alpha == nullptr || alpha_ld % 4 == 0) && (add_l == nullptr || add_ld % 4 == 0) ? 1 : 0;
-  const int rpw = gather_rows_per_wg(R * nz);
-  g.rows_per_wg = rpw;
-  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_crown_relu_conv_transpose_concretize: too many rows");
-  hipLaunchKernelGGL(conv_t_small_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream,
-                     g, rx);
-  BF_LAUNCH_CHECK("conv_t_small_kernel<relax>");
+  const int rc = small_t_launch<true>(g, rx, nz, glds, "bf_crown_relu_conv_transpose_concretize", stream);
+  if (rc) return rc;
   if (lp_seed) return lp_seed_rows(h_out, R, (int64_t)Ci * Hi * Wi, h_scale, norm_p, stream);
   return BF_OK;
 }

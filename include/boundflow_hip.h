@@ -292,7 +292,10 @@ int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, 
  * read directly (no box, no split term), applied while each row's map is
  * staged as in bf_crown_relu_conv_transpose, then the transposed convolution
  * and b_out = (b_in + sum A * beta_sel) + sum A' * kbias.  Shapes: those of
- * bf_conv_transpose_hwc_supported (else returns 1). */
+ * bf_conv_transpose_hwc_supported (else returns 1); an input-layer shape (at
+ * most 16 map channels of at most 256 pixels, at most 3 output channels of at
+ * most 1024 pixels, at most 2 x 2 taps per output pixel) runs the tap-product
+ * kernel in its register form instead. */
 int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
                                         int Wo, const float* alpha_u, const float* beta_u, const float* alpha_l,
                                         const float* beta_l, const float* kbias, const float* b_u_in,

@@ -4,7 +4,9 @@ bf_conv_transpose_rows replaces Conv2dLinearOperator.to_dense
 (boundflow/runtime/linear_operator.py:1067-1092), i.e. conv_transpose2d of every
 coefficient row, optionally fused with the concretization norm
 sum |y| * w and the gradient seed h = h_scale * sign(y) * w.  Shapes with at
-most 4 output channels and 16 taps run the tap-product MFMA kernel, other
+most 4 output channels and 16 taps run the tap-product MFMA kernel (in its register
+form when the map has at most 16 channels and 256 pixels and each output pixel at
+most 2 x 2 taps, else in its generic form), other
 shapes with KH % sh == 0 and KW % sw == 0 the parity-class MFMA kernel, the
 rest the row kernel; all three are covered, the parity-class kernel in both of its
 map layouts (channel-last when Co is a multiple of 16).  bf_crown_relu_conv_transpose
@@ -34,7 +36,8 @@ SHAPES = [
     (9, 8, 7, 5, 20, 3, 3, 1, 1, 1, 1, 3),       # stride 1, 3x3, Ci > 16 (parity-class kernel, 9 taps)
     (6, 5, 6, 6, 4, 2, 2, 2, 2, 0, 0, 2),        # 2x2 stride 2, no padding, 36 pixels (tap-product kernel)
     (7, 6, 5, 5, 3, 3, 3, 2, 2, 1, 1, 7),        # KH % sh != 0, 3 channels (tap-product kernel)
-    (11, 7, 9, 9, 1, 3, 3, 1, 1, 0, 0, 4),       # one channel, stride 1, no padding (tap-product kernel)
+    (11, 7, 9, 9, 1, 3, 3, 1, 1, 0, 0, 4),       # one channel, stride 1, no padding (tap-product kernel, generic form)
+    (600, 16, 16, 16, 3, 4, 4, 2, 2, 1, 1, 7),   # several rows per workgroup (tap-product kernel, register form)
     (5, 6, 5, 5, 8, 3, 3, 2, 2, 1, 1, 5),        # KH % sh != 0, 8 channels (row kernel)
 ]
 
@@ -278,7 +281,10 @@ def test_relu_conv_transpose_matches_pass_then_conv(shape, variant):
 
 INPUT_SHAPES = [
     (37, 16, 16, 16, 3, 4, 4, 2, 2, 1, 1, 9),    # C3 / C4 input region (3 channels, 4 x 4 taps, stride 2)
-    (10, 8, 6, 6, 2, 3, 3, 1, 1, 1, 1, 5),       # npix % 16 != 0: the scalar staging path
+    (10, 8, 6, 6, 2, 3, 3, 1, 1, 1, 1, 5),       # npix % 16 != 0: the scalar staging path (generic form)
+    (603, 16, 16, 16, 3, 4, 4, 2, 2, 1, 1, 7),   # several rows per workgroup, domains changing inside one
+    (40, 8, 14, 14, 1, 4, 4, 2, 2, 1, 1, 5),     # one output channel of 28 x 28, 196 map pixels (partial blocks)
+    (20, 12, 8, 8, 4, 3, 3, 2, 2, 1, 1, 4),      # four output channels, 3 x 3 taps at stride 2 (absent taps)
 ]
 
 
