@@ -23,8 +23,9 @@ baseline and parity over its whole batch.
 D1 (not a BASELINE configuration) measures the DAG path: CROWN on a residual MLP.
     python bench.py --calibrate-copy MIB   # one plain device copy of MIB MiB, the
                                            # reference kernel for HBM byte counters
-    python bench.py --hbm-ceiling MIB      # attainable HBM rates on MIB MiB buffers:
-                                           # fill, copy, read-only sum, two-stream fill
+    python bench.py --hbm-ceiling MIB      # attainable rates: fill, copy, read-only sum and a
+                                           # write-bound product on MIB MiB buffers, and the
+                                           # library's fp32 GEMM on the C2 / C5 contraction shapes
 """
 
 from __future__ import annotations
@@ -381,7 +382,8 @@ def hbm_ceiling(mib: int, reps: int) -> dict:
     fill (write only), copy (read + write, the runtime's blit), sum (read only) and
     a broadcast product out[d, r, k] = w[r, k] * s[d, k] whose small operands stay
     in L2 (the write-bound shape of the strided relaxation pass: 500 x 500 rows per
-    domain, two outputs)."""
+    domain, two outputs); and the vendor library's fp32 product (torch.mm, TF32 off)
+    on the shapes of the C2 and C5 contractions."""
     import torch
 
     n = mib * (1 << 20) // 4
@@ -405,6 +407,42 @@ def hbm_ceiling(mib: int, reps: int) -> dict:
         "broadcast_product_two_outputs": (bcast, 2 * 4 * D * R * K),
     }
     res = {"mib": mib, "reps": reps}
+    # the vendor library's plain fp32 products on the shapes of the dominant contractions
+    # (C2: 128000 x 500 rows against a 500 x 500 weight; C5: 36864 x 256 against 256 x 256),
+    # full fp32: no TF32, no reduced precision
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for M, N, K in ((128000, 500, 500), (36864, 256, 256)):
+        a_m = torch.rand(M, K, device="cuda:0")
+        w_m = torch.rand(N, K, device="cuda:0")
+        c_m = torch.empty(M, N, device="cuda:0")
+        mm = lambda: torch.mm(a_m, w_m.t(), out=c_m)   # noqa: E731
+        _settle(mm, 3, seconds=0.3)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            mm()
+        s1.record()
+        s1.synchronize()
+        ms = s0.elapsed_time(s1) / reps
+        flops = 2.0 * M * N * K
+        res[f"library_sgemm_{M}x{N}x{K}"] = {"flops": flops, "avg_ms": round(ms, 4),
+                                             "tflops": round(flops / ms / 1e9, 2),
+                                             "frac_of_fp32_mfma_peak": round(flops / ms / 1e9 / PEAK_FP32_MFMA_TFLOPS, 4)}
+        # this library's plain contraction (bf_gemm, store epilogue) on the same operands
+        from boundflow_amd import _lib
+        st = _lib.stream_handle()
+        ours = lambda: _lib.call("bf_gemm", _lib.ptr(a_m), K, _lib.ptr(w_m), K, 1, 0, _lib.ptr(c_m), N,  # noqa: E731
+                                 M, N, K, st)
+        _settle(ours, 3, seconds=0.3)
+        s0.record()
+        for _ in range(reps):
+            ours()
+        s1.record()
+        s1.synchronize()
+        ms = s0.elapsed_time(s1) / reps
+        res[f"bf_gemm_{M}x{N}x{K}"] = {"flops": flops, "avg_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 2),
+                                       "frac_of_fp32_mfma_peak": round(flops / ms / 1e9 / PEAK_FP32_MFMA_TFLOPS, 4)}
+        del a_m, w_m, c_m
     for name, (fn, nbytes) in cases.items():
         _settle(fn, 3, seconds=0.3)
         s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
