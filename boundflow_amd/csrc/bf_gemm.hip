@@ -50,8 +50,8 @@ __global__ void relax_table_kernel(const float* __restrict__ lo, const float* __
   out[i] = make_float4(r.au, r.bu, r.al, r.bl);
 }
 
-// BOUNDFLOW_GEMM_TILE=G, =H or =Q forces one configuration (for measurement); read
-// once when the library is loaded, constant afterwards.
+// BOUNDFLOW_GEMM_TILE=G, =H, =Q or =S forces one configuration (for measurement);
+// read once when the library is loaded, constant afterwards.
 static int forced_tile_from_env() {
   const char* v = std::getenv("BOUNDFLOW_GEMM_TILE");
   if (v == nullptr) return 0;
@@ -71,7 +71,7 @@ static double quantization_efficiency(int64_t tiles) {
 }
 static const int kForcedTile = forced_tile_from_env();
 
-// Tile configuration of a contraction: 'G', 'H' or 'Q'.  ks: K chunks of a split
+// Tile configuration of a contraction: 'G', 'H', 'Q' or 'S'.  ks: K chunks of a split
 // contraction (1 when unsplit); dl: the operands suit the direct-to-LDS loop.
 int gemm_tile_choice(int64_t M, int64_t N, int nz, int64_t ks, int pro, bool dl) {
   if (kForcedTile) return kForcedTile;

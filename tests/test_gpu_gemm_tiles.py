@@ -3,7 +3,9 @@ by plain-prologue contractions whose 128 x 128 tiles would load the 256 CUs
 unevenly (C5's 36 864-row grids): the store, rank-1 store and |A W|
 concretization epilogues against float64 on shapes that select it, with row,
 column and K tails.  The relaxation epilogue on such a shape is covered by
-test_gpu_epilogue_relax.test_two_region_step_matches_oracle (D = 2048)."""
+test_gpu_epilogue_relax.test_two_region_step_matches_oracle (D = 2048).  The 64 x 64
+TileS (plain-prologue store contractions on grids of fewer 128 x 128 tiles than
+CUs): plain, two-sided, rank-1 and split-K forms against float64."""
 
 import pytest
 import torch
@@ -130,5 +132,64 @@ def test_store_on_tile_s_matches_fp64(M, N, K, trans_b):
     _lib.call("bf_gemm", _lib.ptr(Ad), K, _lib.ptr(Bd), ldb, trans_b, 0, _lib.ptr(C), N, M, N, K, _lib.stream_handle())
     torch.cuda.synchronize()
     tol = contraction_tol(A, Bm, K) + 1e-30
+    err = (C.cpu().double() - ref).abs()
+    assert bool((err <= tol).all()), float((err / tol).max())
+
+
+@pytest.mark.parametrize("form", ["nz2_store", "rank1_S9", "rank1_split_k"])
+def test_other_store_forms_on_tile_s_match_fp64(form):
+    """The other plain-prologue store forms that take TileS on small grids: both
+    coefficient sides in one launch (bf_crown_relu_linear_fwd with nothing to relax,
+    nz = 2), the rank-1 epilogue with 9 rows per domain (bf_gemm_rank1, S = 9), and
+    the rank-1 epilogue with K split into chunks summed by splitk_reduce."""
+    dev = device()
+    g = torch.Generator().manual_seed({"nz2_store": 3, "rank1_S9": 4, "rank1_split_k": 5}[form])
+    st = _lib.stream_handle()
+    if form == "nz2_store":
+        D, S, N, P = 32, 9, 256, 100
+        M = D * S
+        announce(f"crown_relu_linear_fwd (plain, nz=2) on TileS M={M} N={P} K={N}")
+        assert tile(M, P, 2) == "S"
+        A_u, A_l = torch.randn(M, N, generator=g), torch.randn(M, N, generator=g)
+        W = torch.randn(P, N, generator=g)
+        b_u, b_l = torch.randn(M, generator=g), torch.randn(M, generator=g)
+        d = {k: v.to(dev) for k, v in dict(A_u=A_u, A_l=A_l, W=W, b_u=b_u, b_l=b_l).items()}
+        out_u, out_l = torch.empty(M, P, device=dev), torch.empty(M, P, device=dev)
+        bo_u, bo_l = torch.empty(M, device=dev), torch.empty(M, device=dev)
+        _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(d["A_u"]), _lib.ptr(d["A_l"]), S * N, D, S, N, None, None, 0,
+                  _lib.ptr(d["W"]), P, 1, None, _lib.ptr(d["b_u"]), _lib.ptr(d["b_l"]), _lib.ptr(out_u),
+                  _lib.ptr(out_l), _lib.ptr(bo_u), _lib.ptr(bo_l), st)
+        torch.cuda.synchronize()
+        for A, out, b_in, b_out in ((A_u, out_u, b_u, bo_u), (A_l, out_l, b_l, bo_l)):
+            ref = A.double() @ W.double().t()
+            tol = contraction_tol(A, W.t(), N) + 1e-30
+            err = (out.cpu().double() - ref).abs()
+            assert bool((err <= tol).all()), float((err / tol).max())
+            assert torch.equal(b_out.cpu(), b_in), "b_out is b_in when nothing is relaxed"
+        return
+    M, N, K, S = (288, 100, 256, 9) if form == "rank1_S9" else (288, 100, 1024, 9)
+    ws_floats = int(_lib.load().bf_gemm_rank1_workspace(M, N, K))
+    if form == "rank1_split_k":
+        assert ws_floats > 0, "this shape splits K"
+        ks = ws_floats // (M * N)
+        assert chr(_lib.load().bf_gemm_tile_config(M, N, 1, ks, 0, 1)) == "S"
+    else:
+        # no workspace given: the contraction runs unsplit
+        ws_floats = 0
+        assert tile(M, N) == "S"
+    announce(f"gemm_rank1 {form} M={M} N={N} K={K} S={S} workspace={ws_floats}")
+    A = torch.randn(M, K, generator=g)
+    W = torch.randn(N, K, generator=g)
+    r = torch.randn(M, generator=g)
+    v = torch.randn(M // S, N, generator=g)
+    rv = r.double()[:, None] * v.double()[torch.arange(M) // S]
+    ref = A.double() @ W.double().t() + rv
+    tol = contraction_tol(A, W.t(), K) + rv.abs() * 2.0 ** -22 + 1e-30
+    C = torch.empty(M, N, device=dev)
+    ws = torch.empty(max(ws_floats, 1), device=dev)
+    Ad, Wd, rd, vd = A.to(dev), W.to(dev), r.to(dev), v.to(dev)
+    _lib.call("bf_gemm_rank1", _lib.ptr(Ad), K, _lib.ptr(Wd), K, 1, _lib.ptr(C), N, M, N, K, S, _lib.ptr(rd),
+              _lib.ptr(vd), N, _lib.ptr(ws) if ws_floats else None, ws_floats, st)
+    torch.cuda.synchronize()
     err = (C.cpu().double() - ref).abs()
     assert bool((err <= tol).all()), float((err / tol).max())
