@@ -570,7 +570,10 @@ def crown_backward(
                 save["h"] = h_out
                 save["cvec"] = trace.input_center_proj.get(layer.out_name)
             nz = int(A_u is not None) + int(A_l is not None)
-            with _timed("crown_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
+            # bytes: the coefficient rows and the weight read, the row partial norms written, the
+            # gradient seed [M, P] written when asked
+            with _timed("crown_linear_concretize", 2.0 * nz * M * N * P,
+                        4.0 * nz * (M * N + N * P + M * -(-P // 128)) + (4.0 * M * P if h_out is not None else 0.0)):
                 _lib.call("bf_crown_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N, _lib.ptr(Wt),
                           P, _lib.ptr(rad), eps, input_norm_p(pert), _lib.ptr(c_u), _lib.ptr(c_l), _lib.ptr(b_u),
                           _lib.ptr(b_l),
@@ -603,7 +606,8 @@ def crown_backward(
                 save["h"] = h_out
                 save["cvec"] = cvec
             nz = int(A_u is not None) + int(A_l is not None)
-            with _timed("crown_relu_linear_concretize", 2.0 * nz * M * N * P, 4.0 * nz * (M * N + N * P)):
+            with _timed("crown_relu_linear_concretize", 2.0 * nz * M * N * P,
+                        4.0 * nz * (M * N + N * P) + 16.0 * B * N + (4.0 * M * P if h_out is not None else 0.0)):
                 _lib.call("bf_crown_relu_linear_concretize", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
                           _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(cvec),
                           _lib.ptr(rad), eps, input_norm_p(pert), _lib.ptr(b_u),
@@ -638,8 +642,14 @@ def crown_backward(
             nc_l = torch.empty(M, device=dev, dtype=torch.float32) if (cvec is not None and A_l is not None) else None
             # the gradient pass reads the lower coefficient before the next relaxation
             pre_l = torch.empty(M, P, device=dev, dtype=torch.float32) if (save is not None and A_l is not None) else None
-            # bytes: the unrelaxed lower coefficient kept for the gradient is a second output
-            with _timed("crown_relu_linear_relu_fwd", flops, nbytes + (4.0 * M * P if pre_l is not None else 0.0)):
+            # bytes: the next relaxation's operands per (domain, column) -- the float4 table, the split
+            # term of the lower bound, the center projection -- and the row partial sums are read or
+            # written once; the unrelaxed lower coefficient kept for the gradient is a second output
+            e_bytes = (16.0 * B * P + (4.0 * B * P if (n_add is not None and A_l is not None) else 0.0)
+                       + (4.0 * B * P if cvec is not None else 0.0)
+                       + 4.0 * nz * M * -(-P // 128) * (2 if cvec is not None else 1))
+            with _timed("crown_relu_linear_relu_fwd", flops,
+                        nbytes + e_bytes + (4.0 * M * P if pre_l is not None else 0.0)):
                 _lib.call("bf_crown_relu_linear_relu_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
                           _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, _lib.ptr(bias), _lib.ptr(b_u),
                           _lib.ptr(b_l), _lib.ptr(n_table), _lib.ptr(n_add), n_add_ld, _lib.ptr(n_bias),
