@@ -485,27 +485,12 @@ __device__ __forceinline__ float relax_element(const ConvRelax& rx, bool lower, 
   return o;
 }
 
-template <bool RELAX>
-__global__ void __launch_bounds__(GTM)
-conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
-  extern __shared__ __attribute__((aligned(16))) float smem[];
-  float* Ws = smem;                                                  // [nclasses][Kc4][npad] (ws_index order)
-  float* Mp = Ws + (size_t)g.nclasses * g.Kc4 * g.npad;              // [Hp][Wp][CP]
-  __shared__ float red[GTM / 64][2];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: task indices stay scalar
-  const int z = blockIdx.y;
-  const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
-  const float* __restrict__ X = g.X[z];
-  float* __restrict__ y = g.y[z];
-  float* __restrict__ nrm = g.nrm[z];
-  const int CP = g.Cm + 4;
-  const int hq = g.Cm >> 4;                 // 16-channel halves per tap
+// Weights of every class of conv_t_hwc_kernel in the quad order of ws_index, zero-padded in
+// k and channels: a float4 copy of the packed layout when the caller keeps one
+// (conv_t_hwc_pack_kernel), else gathered from the OIHW tensor.
+__device__ __forceinline__ void hwc_stage_weights(const GatherArgs& g, float* Ws, int tid) {
+  const int hq = g.Cm >> 4;
   const int kstride = g.Kc4 * g.npad;
-
-  // weights of every class in the quad order above, zero-padded in k and channels:
-  // a float4 copy of the packed layout when the caller keeps one (conv_t_hwc_pack_kernel)
   const int wtotal = g.nclasses * kstride;
   if (g.wpack) {
     for (int i4 = tid; i4 < wtotal / 4; i4 += GTM)
@@ -539,15 +524,91 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
       }
     }
   }
+}
+
+// The MFMA tasks of one coefficient row against its staged channel-last map Mp (every
+// output pixel class, pixel block and output-channel block the wave owns), with the
+// store / weighted-norm / gradient-seed epilogue; the norm terms accumulate in s.
+__device__ __forceinline__ void hwc_row_tasks(const GatherArgs& g, const float* Ws, const float* Mp, int wave, int lane,
+                                              int64_t r, int64_t d, bool lower, float* __restrict__ y,
+                                              float* __restrict__ nrm, float hs, float& s) {
+  const int CP = g.Cm + 4;
+  const int hq = g.Cm >> 4;
+  const int64_t nout = (int64_t)g.nch * g.HWout;
+  const int j = lane >> 4;     // k lane group of the MFMA operands; output row group
+  const int col = lane & 15;   // pixel column (B operand / D column); channel row (A operand)
+  for (int task = wave; task < g.ntasks; task += GTM / 64) {
+    int c = 0;
+    while (c + 1 < g.nclasses && task >= g.cls[c + 1].tbase) ++c;
+    const GatherClass& C = g.cls[c];
+    const int tl = task - C.tbase;
+    const int pt = tl / g.nblk, cb = tl - pt * g.nblk;
+    const int p = pt * 16 + col;
+    const bool pok = p < C.np;
+    const int pc = pok ? p : C.np - 1;
+    const int q1 = pc / C.n2, q2 = pc - q1 * C.n2;
+    const float* __restrict__ mp = Mp + (C.poff0 + q1 * C.s1 + q2 * C.s2) * CP + 4 * j;
+    const float* __restrict__ wl = Ws + ws_index(g, c, cb * 16 + col, j);
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    int q = 0;
+    for (int a = 0; a < g.nA; ++a) {
+      for (int b = 0; b < g.nB; ++b) {
+        const float* __restrict__ tp = mp - (a * g.Wp + b) * CP;
+        for (int half = 0; half < hq; ++half, ++q) {
+          const float4 w4 = *reinterpret_cast<const float4*>(wl + q * 64);
+          const float4 x4 = *reinterpret_cast<const float4*>(tp + 16 * half);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.x, x4.x, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.y, x4.y, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.z, x4.z, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.w, x4.w, acc, 0, 0, 0);
+        }
+      }
+    }
+    const int opix = C.out0 + q1 * C.o1 + q2 * C.o2;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int n = cb * 16 + 4 * j + rr;
+      if (n < g.nch && pok) {
+        const float v = acc[rr];
+        const int64_t oidx = (int64_t)n * g.HWout + opix;
+        if (y) y[r * nout + oidx] = v;
+        if (nrm) {
+          const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
+          s = norm_step(s, v, wgt, g.wv != nullptr, g.nkind);
+          if (lower && g.h_out) {
+            const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
+            g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <bool RELAX>
+__global__ void __launch_bounds__(GTM)
+conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* Ws = smem;                                                  // [nclasses][Kc4][npad] (ws_index order)
+  float* Mp = Ws + (size_t)g.nclasses * g.Kc4 * g.npad;              // [Hp][Wp][CP]
+  __shared__ float red[GTM / 64][2];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: task indices stay scalar
+  const int z = blockIdx.y;
+  const bool lower = g.z_lower_first ? (z == 0) : (z == 1);
+  const float* __restrict__ X = g.X[z];
+  float* __restrict__ y = g.y[z];
+  float* __restrict__ nrm = g.nrm[z];
+  const int CP = g.Cm + 4;
+
+  hwc_stage_weights(g, Ws, tid);
   // zero halo (and channel padding): interior positions are rewritten per row, the rest stays zero
   const int mtotal = g.Hp * g.Wp * CP;
   for (int i = tid; i < mtotal; i += GTM) Mp[i] = 0.f;
 
   const int HWm = g.Hm * g.Wm;
   const int nin = g.Cm * HWm;
-  const int64_t nout = (int64_t)g.nch * g.HWout;
-  const int j = lane >> 4;     // k lane group of the MFMA operands; output row group
-  const int col = lane & 15;   // pixel column (B operand / D column); channel row (A operand)
   const FastDiv f_hw = g.f_HWm;
   const FastDiv f_w = g.f_Wm;
 
@@ -654,52 +715,7 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
     if (pf && i + 1 < g.rows_per_wg && r + 1 < g.R) fetch(r + 1);   // lands during this row's MFMAs
     const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
     float s = 0.f;
-    for (int task = wave; task < g.ntasks; task += GTM / 64) {
-      int c = 0;
-      while (c + 1 < g.nclasses && task >= g.cls[c + 1].tbase) ++c;
-      const GatherClass& C = g.cls[c];
-      const int tl = task - C.tbase;
-      const int pt = tl / g.nblk, cb = tl - pt * g.nblk;
-      const int p = pt * 16 + col;
-      const bool pok = p < C.np;
-      const int pc = pok ? p : C.np - 1;
-      const int q1 = pc / C.n2, q2 = pc - q1 * C.n2;
-      const float* __restrict__ mp = Mp + (C.poff0 + q1 * C.s1 + q2 * C.s2) * CP + 4 * j;
-      const float* __restrict__ wl = Ws + ws_index(g, c, cb * 16 + col, j);
-      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-      int q = 0;
-      for (int a = 0; a < g.nA; ++a) {
-        for (int b = 0; b < g.nB; ++b) {
-          const float* __restrict__ tp = mp - (a * g.Wp + b) * CP;
-          for (int half = 0; half < hq; ++half, ++q) {
-            const float4 w4 = *reinterpret_cast<const float4*>(wl + q * 64);
-            const float4 x4 = *reinterpret_cast<const float4*>(tp + 16 * half);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.x, x4.x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.y, x4.y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.z, x4.z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.w, x4.w, acc, 0, 0, 0);
-          }
-        }
-      }
-      const int opix = C.out0 + q1 * C.o1 + q2 * C.o2;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int n = cb * 16 + 4 * j + rr;
-        if (n < g.nch && pok) {
-          const float v = acc[rr];
-          const int64_t oidx = (int64_t)n * g.HWout + opix;
-          if (y) y[r * nout + oidx] = v;
-          if (nrm) {
-            const float wgt = g.wv ? g.wv[d * g.w_ld + oidx] : 1.f;
-            s = norm_step(s, v, wgt, g.wv != nullptr, g.nkind);
-            if (lower && g.h_out) {
-              const float sg = (v > 0.f) ? 1.f : ((v < 0.f) ? -1.f : 0.f);
-              g.h_out[r * nout + oidx] = g.wv ? hs * sg * wgt : hs * sg;
-            }
-          }
-        }
-      }
-    }
+    hwc_row_tasks(g, Ws, Mp, wave, lane, r, d, lower, y, nrm, hs, s);
     if (nrm) {
       s = g.nkind == 1 ? wave_max_nonneg(s) : wave_sum(s);
       __syncthreads();   // red of the row sums above is read; reuse it
@@ -1407,6 +1423,20 @@ static int gather_rows_per_wg(int64_t work) {
   return rpw < 1 ? 1 : (rpw > 8 ? 8 : (int)rpw);
 }
 
+
+// Launch of the channel-last gather-GEMM over a conv_t_hwc plan (lds: its LDS footprint).
+template <bool RELAX>
+static int hwc_launch(GatherArgs& g, const ConvRelax& rx, unsigned nz, size_t lds, const char* who,
+                      hipStream_t stream) {
+  const int rpw = gather_rows_per_wg(g.R * nz);
+  g.rows_per_wg = rpw;
+  BF_REQUIRE((g.R + rpw - 1) / rpw < (1LL << 31), "%s: too many rows", who);
+  hipLaunchKernelGGL(conv_t_hwc_kernel<RELAX>, dim3((unsigned)((g.R + rpw - 1) / rpw), nz), dim3(GTM), lds, stream, g,
+                     rx);
+  BF_LAUNCH_CHECK(who);
+  return BF_OK;
+}
+
 int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
                       hipStream_t stream);
 int ibp_finalize(const float* c, const float* r, const float* rownorm, float eps, const float* bias,
@@ -1532,15 +1562,9 @@ static int conv_transpose_rows_launch(const float* A_u, const float* A_l, int64_
       g.h_scale = h_scale;
       g.h_out = h_out;
       g.S = S;
-      const int rpw = gather_rows_per_wg(R * nz);
-      g.rows_per_wg = rpw;
-      BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_conv_transpose_rows: too many rows");
       ConvRelax rx;
       memset(&rx, 0, sizeof(rx));
-      hipLaunchKernelGGL(conv_t_hwc_kernel<false>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds,
-                         stream, g, rx);
-      BF_LAUNCH_CHECK("conv_t_hwc_kernel");
-      return BF_OK;
+      return hwc_launch<false>(g, rx, nz, glds, "bf_conv_transpose_rows (channel-last gather-GEMM)", stream);
     }
   }
   {
@@ -1691,13 +1715,7 @@ int bf_crown_relu_conv_transpose(const float* A_u, const float* A_l, int64_t D, 
   g.W = W;
   g.wpack = ((uintptr_t)w_packed & 15) == 0 ? w_packed : nullptr;
   g.S = S;
-  const int rpw = gather_rows_per_wg(R * nz);
-  g.rows_per_wg = rpw;
-  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_crown_relu_conv_transpose: too many rows");
-  hipLaunchKernelGGL(conv_t_hwc_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g,
-                     rx);
-  BF_LAUNCH_CHECK("conv_t_hwc_kernel<relax>");
-  return BF_OK;
+  return hwc_launch<true>(g, rx, nz, glds, "bf_crown_relu_conv_transpose", stream);
 }
 
 int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
@@ -1767,13 +1785,7 @@ int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int6
   g.W = W;
   g.wpack = ((uintptr_t)w_packed & 15) == 0 ? w_packed : nullptr;
   g.S = S;
-  const int rpw = gather_rows_per_wg(R * nz);
-  g.rows_per_wg = rpw;
-  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "bf_crown_relu_planes_conv_transpose: too many rows");
-  hipLaunchKernelGGL(conv_t_hwc_kernel<true>, dim3((unsigned)((R + rpw - 1) / rpw), nz), dim3(GTM), glds, stream, g,
-                     rx);
-  BF_LAUNCH_CHECK("conv_t_hwc_kernel<relax>");
-  return BF_OK;
+  return hwc_launch<true>(g, rx, nz, glds, "bf_crown_relu_planes_conv_transpose", stream);
 }
 
 int bf_conv_transpose_small_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph,
