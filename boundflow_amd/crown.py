@@ -529,13 +529,21 @@ def crown_backward(
             b_l = brow if A_l is not None else None
             stride = 0
             continue
-        if (stride == 0 and relaxes and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M
-                and (k == 0 or layers[k - 1].kind == "linear")):
+        shared_first = (stride == 0 and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M
+                        and (k == 0 or layers[k - 1].kind == "linear"))
+        small_grid = M < EPILOGUE_MIN_M and N >= RELAX_PASS_MIN_K
+        if relaxes and (shared_first or small_grid):
             # A coefficient shared by every domain (the first region of a C = I query):
             # its relaxation differs per domain, so one bandwidth-bound pass writes it
             # per domain (with the bias terms and, at the input layer, the center sums)
-            # and the contraction below runs with the plain prologue.
+            # and the contraction below runs with the plain prologue.  A query of few
+            # rows takes the same two steps: its contraction is a grid of few tiles whose
+            # K loop runs serially on a few CUs, and the plain prologue deals it as
+            # 64 x 64 tiles over four times as many CUs as the relaxation prologue's
+            # 128 x 128 ones.
             cvec0 = trace.input_center_proj.get(layer.out_name) if k == 0 else None
+            if k == 0 and cvec0 is None:
+                raise RuntimeError("forward trace lacks the input-layer projection")
             rA_u = torch.empty(M, N, device=dev, dtype=torch.float32) if A_u is not None else None
             rA_l = torch.empty(M, N, device=dev, dtype=torch.float32) if A_l is not None else None
             rb_u = torch.empty(M, device=dev, dtype=torch.float32) if A_u is not None else None
@@ -543,8 +551,8 @@ def crown_backward(
             c_u = torch.empty(M, device=dev, dtype=torch.float32) if (cvec0 is not None and A_u is not None) else None
             c_l = torch.empty(M, device=dev, dtype=torch.float32) if (cvec0 is not None and A_l is not None) else None
             nz = int(A_u is not None) + int(A_l is not None)
-            with _timed("crown_relu_relax", 0.0, 4.0 * nz * (S * N + M * N)):
-                _lib.call("bf_crown_relu_relax_lu", _lib.ptr(A_u), _lib.ptr(A_l), 0, B, S, N, _lib.ptr(pre_lo),
+            with _timed("crown_relu_relax", 0.0, 4.0 * nz * ((M if stride else S) * N + M * N)):
+                _lib.call("bf_crown_relu_relax_lu", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N, _lib.ptr(pre_lo),
                           _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, _lib.ptr(add), add_ld, _lib.ptr(bias),
                           _lib.ptr(cvec0), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(rA_u), _lib.ptr(rA_l),
                           _lib.ptr(rb_u), _lib.ptr(rb_l), _lib.ptr(c_u), _lib.ptr(c_l), stream)
@@ -661,11 +669,18 @@ def crown_backward(
             c_u, c_l = nc_u, nc_l
             pre_relaxed = True
         else:
+            # with nothing to relax and no bias the contraction leaves the bias rows as they
+            # are: they pass through instead of being copied
+            keep_b = (relax is None and add is None and bias is None and (A_u is None or b_u is not None)
+                      and (A_l is None or b_l is not None))
+            if keep_b:
+                nb_u, nb_l = b_u, b_l
             with _timed("crown_relu_linear_fwd", flops, nbytes):
                 _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
-                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias), _lib.ptr(b_u),
-                          _lib.ptr(b_l), _lib.ptr(nA_u),
-                          _lib.ptr(nA_l), _lib.ptr(nb_u), _lib.ptr(nb_l), stream)
+                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias),
+                          None if keep_b else _lib.ptr(b_u), None if keep_b else _lib.ptr(b_l), _lib.ptr(nA_u),
+                          _lib.ptr(nA_l), None if keep_b else _lib.ptr(nb_u), None if keep_b else _lib.ptr(nb_l),
+                          stream)
             pre_relaxed = False
         A_u, A_l, b_u, b_l = nA_u, nA_l, nb_u, nb_l
         stride = S * P
@@ -680,6 +695,11 @@ def crown_backward(
 # prologue).
 EPILOGUE_MIN_ROWS = 8
 EPILOGUE_MIN_M = 8192
+
+# A query below EPILOGUE_MIN_M rows relaxes a coefficient of at least this many
+# columns in a pass of its own before the contraction (plain prologue); narrower
+# coefficients keep the fused prologue, whose K loop is then one or two tiles long.
+RELAX_PASS_MIN_K = 32
 
 
 def _identity_table(B: int, n: int, dev) -> torch.Tensor:
