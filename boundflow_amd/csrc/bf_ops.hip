@@ -381,7 +381,7 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
       su += v * (nn ? r.y : r.w);
       if (kbias) ku += o * kbias[k];
       if (cvec) cu += o * cvec[d * K + k];
-      Au_out[m * K + k] = o;
+      if (Au_out) Au_out[m * K + k] = o;
     }
     if (Al) {
       float v = Al[a_row + k];
@@ -391,7 +391,7 @@ relu_relax_rows_kernel(const float* __restrict__ Au, const float* __restrict__ A
       if (add_l) o = o + add_l[d * add_ld + k];
       if (kbias) kl += o * kbias[k];
       if (cvec) cl += o * cvec[d * K + k];
-      Al_out[m * K + k] = o;
+      if (Al_out) Al_out[m * K + k] = o;
     }
   }
   for (int off = 32; off >= 1; off >>= 1) {
@@ -457,7 +457,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
           if (kbias) s[2] += o[e] * kbv[e];
           if (cvec) s[4] += o[e] * cvv[e];
         }
-        *reinterpret_cast<float4*>(Au_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
+        if (Au_out) *reinterpret_cast<float4*>(Au_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
       }
       if (Al) {
         const float4 v4 = Al == Au ? vu4 : *reinterpret_cast<const float4*>(Al + a_row + k);
@@ -475,7 +475,7 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
           if (kbias) s[3] += o[e] * kbv[e];
           if (cvec) s[5] += o[e] * cvv[e];
         }
-        *reinterpret_cast<float4*>(Al_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
+        if (Al_out) *reinterpret_cast<float4*>(Al_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
       }
     }
   }
@@ -1008,6 +1008,11 @@ int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* a
   return relax_table(pre_lo, pre_hi, alpha, alpha_ld, D, K, reinterpret_cast<float4*>(table), stream);
 }
 
+static int relax_pass(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
+                      const RelaxSrc& src, const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
+                      const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
+                      float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream, bool sums_only);
+
 int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t N,
                              const float* relax, const float* add_l, int64_t add_ld, const float* W, int64_t P,
                              int w_trans, const float* bias, const float* b_u_in, const float* b_l_in,
@@ -1045,6 +1050,20 @@ int bf_crown_relu_linear_fwd(const float* A_u, const float* A_l, int64_t a_dstri
   a.add_l = add_l;
   a.add_ld = add_ld;
   a.kbias = bias;
+  // Bias rows alone (nothing to relax) on a grid of fewer 128 x 128 tiles than the device
+  // has CUs: the row sums in a pass of their own (A read once, no coefficient written),
+  // then the plain contraction, whose 64 x 64 tiles spread the short grid over four times
+  // as many CUs as the relaxation prologue's tiles (a K loop of a few tiles keeps the
+  // one-launch form).
+  if (!relax && !add_l && bias && N >= 32 && ceil_div(M, 128) * ceil_div(P, 128) * nz < 256) {
+    if (b_u_out || b_l_out) {
+      const RelaxSrc none{nullptr, nullptr, nullptr, nullptr, 0};
+      const int rc = relax_pass(A_u, A_l, a_dstride, D, S, N, none, nullptr, 0, bias, nullptr, b_u_in, b_l_in, nullptr,
+                                nullptr, b_u_out, b_l_out, nullptr, nullptr, stream, true);
+      if (rc) return rc;
+    }
+    return gemm_dispatch(a, PRO_PLAIN, EPI_STORE, nz, stream);
+  }
   if (relax || add_l || bias) return gemm_dispatch(a, PRO_RELAX, EPI_STORE, nz, stream);
   // nothing to relax (A already relaxed): the plain contraction, b_out = b_in
   const int rc = gemm_dispatch(a, PRO_PLAIN, EPI_STORE, nz, stream);
@@ -1319,16 +1338,18 @@ int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
   return 2 * (int64_t)gemm_partial_count(I) * D * S;
 }
 
+// sums_only: the row sums alone, no coefficient written (A_u_out / A_l_out NULL).
 static int relax_pass(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
                       const RelaxSrc& src, const float* add_l, int64_t add_ld, const float* kbias, const float* cvec,
                       const float* b_u_in, const float* b_l_in, float* A_u_out, float* A_l_out, float* b_u_out,
-                      float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
+                      float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream, bool sums_only) {
   BF_REQUIRE(D >= 0 && S >= 0 && K > 0, "bf_crown_relu_relax: bad sizes");
   const int64_t M = D * S;
   if (M == 0) return BF_OK;
   BF_REQUIRE(((uintptr_t)src.table & 15) == 0, "bf_crown_relu_relax: relax table must be 16-byte aligned");
   BF_REQUIRE((src.lo == nullptr) == (src.hi == nullptr), "bf_crown_relu_relax: give both pre_lo and pre_hi");
-  BF_REQUIRE((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr),
+  BF_REQUIRE(sums_only ? (A_u_out == nullptr && A_l_out == nullptr)
+                       : ((A_u == nullptr) == (A_u_out == nullptr) && (A_l == nullptr) == (A_l_out == nullptr)),
              "bf_crown_relu_relax: input/output mismatch");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   const bool vec = (K % 4 == 0) && (a_dstride % 4 == 0) && al16(A_u) && al16(A_l) && al16(A_u_out) &&
@@ -1361,7 +1382,7 @@ int bf_crown_relu_relax(const float* A_u, const float* A_l, int64_t a_dstride, i
                         float* b_l_out, float* c_u_out, float* c_l_out, hipStream_t stream) {
   const RelaxSrc src{reinterpret_cast<const float4*>(relax), nullptr, nullptr, nullptr, 0};
   return relax_pass(A_u, A_l, a_dstride, D, S, K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out,
-                    b_u_out, b_l_out, c_u_out, c_l_out, stream);
+                    b_u_out, b_l_out, c_u_out, c_l_out, stream, false);
 }
 
 int bf_crown_relu_relax_lu(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,
@@ -1372,7 +1393,7 @@ int bf_crown_relu_relax_lu(const float* A_u, const float* A_l, int64_t a_dstride
   BF_REQUIRE(alpha == nullptr || alpha_ld == 0 || alpha_ld >= K, "bf_crown_relu_relax_lu: bad alpha_ld");
   const RelaxSrc src{nullptr, pre_lo, pre_hi, alpha, alpha_ld};
   return relax_pass(A_u, A_l, a_dstride, D, S, K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out,
-                    b_u_out, b_l_out, c_u_out, c_l_out, stream);
+                    b_u_out, b_l_out, c_u_out, c_l_out, stream, false);
 }
 
 int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const float* center, const float* rad,

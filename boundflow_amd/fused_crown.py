@@ -37,7 +37,7 @@ import torch
 
 from . import _lib
 from .conv import packed_conv_transpose_weights
-from .crown import derived, transposed
+from .crown import EPILOGUE_MIN_M, RELAX_PASS_MIN_K, derived, transposed
 from .profiling import launch as _timed
 
 
@@ -264,7 +264,8 @@ class HipFusedCrownExecutor:
 
     def _run(self, request: FusedReluAffineRequest, st) -> FusedReluAffineResult:
         """A linear region: the four relaxation tensors interleaved into the kernels' table
-        (one small launch), then the fused relaxation + contraction.  A conv region: one
+        (one small launch), then the fused relaxation + contraction (a region of few rows:
+        the relaxation pass, then the plain contraction).  A conv region: one
         launch, the channel-last transposed convolution reading the four tensors while it
         stages each row; conv shapes that kernel does not take run the relaxation pass and
         then the transposed convolution."""
@@ -284,6 +285,19 @@ class HipFusedCrownExecutor:
             table = torch.empty(D * N * 4, device=dev, dtype=torch.float32)
             with _timed("executor_relax_table", 0.0, 4.0 * 8 * D * N):
                 _lib.call("bf_relu_relax_table_from_planes", *[_lib.ptr(t) for t in planes], D * N, _lib.ptr(table), st)
+            if M < EPILOGUE_MIN_M and N >= RELAX_PASS_MIN_K:
+                # a region of few rows: the relaxation pass, then the plain-prologue contraction,
+                # whose 64 x 64 tiles spread the short grid over more CUs (as crown_backward does)
+                ru = torch.empty(M, N, device=dev, dtype=torch.float32)
+                rl = torch.empty(M, N, device=dev, dtype=torch.float32)
+                with _timed("executor_relu_relax", 0.0, 4.0 * (4 * M * N + 4 * D * N)):
+                    _lib.call("bf_crown_relu_relax", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
+                              _lib.ptr(table), None, 0, _lib.ptr(bias), None, None, None, _lib.ptr(ru), _lib.ptr(rl),
+                              _lib.ptr(du), _lib.ptr(dl), None, None, st)
+                with _timed("executor_linear", 4.0 * M * N * P, 4.0 * (2 * M * N + N * P + 2 * M * P)):
+                    _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(ru), _lib.ptr(rl), S * N, D, S, N, None, None, 0,
+                              _lib.ptr(Wt), P, 1, None, None, None, _lib.ptr(pu), _lib.ptr(pl), None, None, st)
+                return FusedReluAffineResult(pu, pl, du, dl)
             with _timed("executor_relu_linear", 4.0 * M * N * P, 4.0 * (2 * M * N + 4 * D * N + N * P + 2 * M * P)):
                 _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(request.A_u), _lib.ptr(request.A_l), S * N, D, S, N,
                           _lib.ptr(table), None, 0, _lib.ptr(Wt), P, 1, _lib.ptr(bias), None, None, _lib.ptr(pu),
