@@ -100,8 +100,12 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
     return BF_EINVAL;
   }
   const int64_t ks = (pro == PRO_PLAIN && epi == EPI_STORE && a.ksplit > 1) ? a.ksplit : 1;
-  int t = gemm_tile_choice(a.M, a.N, nz, ks, pro, gemm_dl_operands(a, nz));
-  if (t == 'S' && epi != EPI_STORE) t = 'H';
+  const bool dl = gemm_dl_operands(a, nz);
+  int t = gemm_tile_choice(a.M, a.N, nz, ks, pro, dl);
+  // the norm and relaxation epilogues take 128 columns per tile: a short grid of them runs
+  // as the 4-wave 64 x 128 TileQ when the operands suit its direct-to-LDS loop (twice the
+  // tiles of TileH over as many CUs, each tile's K loop on one wave per SIMD), else TileH
+  if (t == 'S' && epi != EPI_STORE) t = dl ? 'Q' : 'H';
   switch (t) {
     case 'S': return launch_tile<TileS>(a, pro, epi, nz, stream);
     case 'H': return launch_tile<TileH>(a, pro, epi, nz, stream);

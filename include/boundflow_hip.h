@@ -42,10 +42,12 @@ const char* bf_last_error(void);
  * load the 256 CUs unevenly and whose 64 x 128 tiles load them at least 10
  * points more evenly.  The environment variable BOUNDFLOW_GEMM_TILE=G, =H, =Q or
  * =S, read once when the library is loaded, forces one for measurement ('Q' then
- * refuses other operands; 'S' takes the store epilogue alone, others fall back to 'H').
+ * refuses other operands; 'S' takes the store epilogue alone, others fall back to 'Q'
+ * on direct-to-LDS operands, else 'H').
  * bf_gemm_tile_config returns the configuration ('G', 'H', 'Q' or 'S') a
  * store-epilogue contraction of M x N outputs, nz bounds and ksplit K chunks would
- * take (0 for bad sizes); the other epilogues take 'H' where it says 'S'.
+ * take (0 for bad sizes); the other epilogues take 'Q' where it says 'S' when the
+ * operands suit the direct-to-LDS loop, else 'H'.
  * No counterpart in the reference: introspection of this build's dispatch. */
 int bf_gemm_tile_config(int64_t M, int64_t N, int nz, int ksplit, int relax_prologue, int dl_operands);
 
