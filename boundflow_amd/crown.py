@@ -675,12 +675,26 @@ def crown_backward(
                       and (A_l is None or b_l is not None))
             if keep_b:
                 nb_u, nb_l = b_u, b_l
-            with _timed("crown_relu_linear_fwd", flops, nbytes):
-                _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
-                          _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias),
-                          None if keep_b else _lib.ptr(b_u), None if keep_b else _lib.ptr(b_l), _lib.ptr(nA_u),
-                          _lib.ptr(nA_l), None if keep_b else _lib.ptr(nb_u), None if keep_b else _lib.ptr(nb_l),
-                          stream)
+            # The head region (the spec C through the last layer, nothing to relax) depends on C
+            # and the layer's parameters alone: an optimisation call makes it once and its later
+            # passes reuse it (kept in the call's own memo, keyed by C's storage and version).
+            head_key = None
+            if (k == len(layers) - 1 and relax is None and add is None and save is not None
+                    and save.get("memo") is not None and torch.is_tensor(linear_spec_C)):
+                head_key = (f"head:{k}:{linear_spec_C.data_ptr()}:{linear_spec_C._version}:"
+                            f"{A_u is not None}:{A_l is not None}")
+            hit = save["memo"].get(head_key) if head_key is not None else None
+            if hit is not None:
+                nA_u, nA_l, nb_u, nb_l = hit
+            else:
+                with _timed("crown_relu_linear_fwd", flops, nbytes):
+                    _lib.call("bf_crown_relu_linear_fwd", _lib.ptr(A_u), _lib.ptr(A_l), stride, B, S, N,
+                              _lib.ptr(relax), _lib.ptr(add), add_ld, _lib.ptr(Wt), P, 1, _lib.ptr(bias),
+                              None if keep_b else _lib.ptr(b_u), None if keep_b else _lib.ptr(b_l), _lib.ptr(nA_u),
+                              _lib.ptr(nA_l), None if keep_b else _lib.ptr(nb_u), None if keep_b else _lib.ptr(nb_l),
+                              stream)
+                if head_key is not None:
+                    save["memo"][head_key] = (nA_u, nA_l, nb_u, nb_l)
             pre_relaxed = False
         A_u, A_l, b_u, b_l = nA_u, nA_l, nb_u, nb_l
         stride = S * P
