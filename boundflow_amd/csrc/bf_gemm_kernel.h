@@ -114,6 +114,30 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Reduction of the 16 row values a lane holds in a 32 x 32 MFMA block (row index r of
+// acc[..][r]) over the 32 lanes of its half-wave (the block's columns), by recursive
+// halving: at the step across lane bit b (16, 8, 4, 2, 1) a lane keeps the half of its
+// values whose row bit matches its own lane bit and joins the partner's copy of them.
+// The pairs are those of the butterfly over lanes ^16, ^8, ^4, ^2, ^1, whose lanes all
+// end with the same bits (join is commutative), so the result is the butterfly's bit for
+// bit, with 16 exchanges per lane instead of 80.  Lane lrow ends with row index lrow >> 1.
+struct AddJoin {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+template <class J>
+__device__ __forceinline__ float halve_rows16(const float (&v)[16], int lrow, J join) {
+  const bool b4 = (lrow >> 4) & 1, b3 = (lrow >> 3) & 1, b2 = (lrow >> 2) & 1, b1 = (lrow >> 1) & 1;
+  float w8[8], w4[4], w2[2];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) w8[q] = join(b4 ? v[q + 8] : v[q], __shfl_xor(b4 ? v[q] : v[q + 8], 16, 64));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) w4[q] = join(b3 ? w8[q + 4] : w8[q], __shfl_xor(b3 ? w8[q] : w8[q + 4], 8, 64));
+#pragma unroll
+  for (int q = 0; q < 2; ++q) w2[q] = join(b2 ? w4[q + 2] : w4[q], __shfl_xor(b2 ? w4[q] : w4[q + 2], 4, 64));
+  const float w1 = join(b1 ? w2[1] : w2[0], __shfl_xor(b1 ? w2[0] : w2[1], 2, 64));
+  return join(w1, __shfl_xor(w1, 1, 64));
+}
+
 // DL: the direct-to-LDS main loop (plain prologue, transposed B, BK 16, aligned
 // float4 operands): three LDS stages filled by global_load_lds_dwordx4, two K
 // tiles in flight while the third is multiplied, one barrier per K tile.  Each
@@ -735,23 +759,16 @@ gemm_kernel(GemmArgs p) {
           }
           rs[i][r] = s;
         }
+      float rsum[FM];
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i) rsum[i] = halve_rows16(rs[i], lrow, join);
+      if ((lrow & 1) == 0) {
+        const int r = lrow >> 1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float s = rs[i][r];
-#pragma unroll
-          for (int off = 16; off >= 1; off >>= 1) s = join(s, __shfl_xor(s, off, 64));
-          rs[i][r] = s;
+        for (int i = 0; i < FM; ++i) {
+          const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          red[wn][rloc] = rsum[i];
         }
-      if (lrow == 0) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            red[wn][rloc] = rs[i][r];
-          }
       }
       __syncthreads();
       for (int rr = t; rr < GBM; rr += GNT) {
@@ -863,27 +880,24 @@ gemm_kernel(GemmArgs p) {
         pb[i][r] = sb;
         pc[i][r] = sc;
       }
-    // fixed-order reduction over the tile's columns: 32 lanes, then the NWN waves
+    // fixed-order reduction over the tile's columns: 32 lanes (halve_rows16), then the NWN waves
+    const AddJoin add_f;
+    float rb[FM], rc[FM];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) {
-          pb[i][r] += __shfl_xor(pb[i][r], off, 64);
-          if (cv_e) pc[i][r] += __shfl_xor(pc[i][r], off, 64);
-        }
+    for (int i = 0; i < FM; ++i) {
+      rb[i] = halve_rows16(pb[i], lrow, add_f);
+      rc[i] = cv_e ? halve_rows16(pc[i], lrow, add_f) : 0.f;
+    }
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       if (pass == 1 && !cv_e) break;   // uniform
-      if (lrow == 0) {
+      if ((lrow & 1) == 0) {
+        const int r = lrow >> 1;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            red[wn][rloc] = pass == 0 ? pb[i][r] : pc[i][r];
-          }
+        for (int i = 0; i < FM; ++i) {
+          const int rloc = wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          red[wn][rloc] = pass == 0 ? rb[i] : rc[i];
+        }
       }
       __syncthreads();
       float* __restrict__ dst = pass == 0 ? p.partial[z] : p.partial_c[z];
