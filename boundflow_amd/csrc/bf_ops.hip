@@ -506,6 +506,105 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
   }
 }
 
+// The same pass over a coefficient shared by every domain (a_dstride 0: the first region
+// of a C = I query, rows of K <= 256 NQ): a workgroup takes rows_per_wg rows of one
+// domain, and each lane keeps that domain's operands of its NQ quads of k (k = 4 lane +
+// 256 q: the relaxation entries, split term, center and bias) in registers across all of
+// them, so a row costs one read of the shared (L2-resident) row and the writes of its
+// relaxed rows.  Per-lane partials in k order and the wave sum: the sums of
+// relu_relax_rows4_kernel<64>, bit for bit.
+template <int NQ>
+__global__ void __launch_bounds__(256)
+relu_relax_shared_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t S, int64_t K,
+                         int64_t chunks, int rows_per_wg, RelaxSrc relax, const float* __restrict__ add_l,
+                         int64_t add_ld, const float* __restrict__ kbias, const float* __restrict__ cvec,
+                         const float* __restrict__ bu_in, const float* __restrict__ bl_in,
+                         float* __restrict__ Au_out, float* __restrict__ Al_out, float* __restrict__ bu_out,
+                         float* __restrict__ bl_out, float* __restrict__ cu_out, float* __restrict__ cl_out) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t d = (int64_t)blockIdx.x / chunks;
+  const int64_t s0 = ((int64_t)blockIdx.x - d * chunks) * rows_per_wg;
+  const int64_t s_end = s0 + rows_per_wg < S ? s0 + rows_per_wg : S;
+  float4 e[NQ][4];
+  float kbv[NQ][4], cvv[NQ][4], adv[NQ][4];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int64_t k = 4 * ((int64_t)lane + 64 * q);
+    const bool ok = k < K;
+    if (ok) {
+      relax.quad(d, K, k, e[q]);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) e[q][u] = make_float4(1.f, 0.f, 1.f, 0.f);
+    }
+    const float4 kb = (ok && kbias) ? *reinterpret_cast<const float4*>(kbias + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 cv = (ok && cvec) ? *reinterpret_cast<const float4*>(cvec + d * K + k)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 ad = (ok && add_l) ? *reinterpret_cast<const float4*>(add_l + d * add_ld + k)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    kbv[q][0] = kb.x; kbv[q][1] = kb.y; kbv[q][2] = kb.z; kbv[q][3] = kb.w;
+    cvv[q][0] = cv.x; cvv[q][1] = cv.y; cvv[q][2] = cv.z; cvv[q][3] = cv.w;
+    adv[q][0] = ad.x; adv[q][1] = ad.y; adv[q][2] = ad.z; adv[q][3] = ad.w;
+  }
+  const bool need[6] = {Au != nullptr, Al != nullptr, Au && kbias, Al && kbias, Au && cvec, Al && cvec};
+  for (int64_t srow = s0 + wave; srow < s_end; srow += 4) {
+    const int64_t m = d * S + srow;
+    const float* __restrict__ au = Au + srow * K;
+    const float* __restrict__ al = Al + srow * K;
+    float4 vu4[NQ], vl4[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t k = 4 * ((int64_t)lane + 64 * q);
+      const bool ok = k < K;
+      vu4[q] = (ok && Au) ? *reinterpret_cast<const float4*>(au + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      vl4[q] = (ok && Al && Al != Au) ? *reinterpret_cast<const float4*>(al + k) : vu4[q];
+    }
+    float s[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // su, sl, ku, kl, cu, cl
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t k = 4 * ((int64_t)lane + 64 * q);
+      if (k >= K) continue;
+      if (Au) {
+        const float v[4] = {vu4[q].x, vu4[q].y, vu4[q].z, vu4[q].w};
+        float o[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool nn = v[u] >= 0.f;
+          o[u] = v[u] * (nn ? e[q][u].x : e[q][u].z);
+          s[0] += v[u] * (nn ? e[q][u].y : e[q][u].w);
+          if (kbias) s[2] += o[u] * kbv[q][u];
+          if (cvec) s[4] += o[u] * cvv[q][u];
+        }
+        if (Au_out) *reinterpret_cast<float4*>(Au_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+      if (Al) {
+        const float v[4] = {vl4[q].x, vl4[q].y, vl4[q].z, vl4[q].w};
+        float o[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool nn = v[u] >= 0.f;
+          o[u] = v[u] * (nn ? e[q][u].z : e[q][u].x);
+          s[1] += v[u] * (nn ? e[q][u].w : e[q][u].y);
+          if (add_l) o[u] = o[u] + adv[q][u];
+          if (kbias) s[3] += o[u] * kbv[q][u];
+          if (cvec) s[5] += o[u] * cvv[q][u];
+        }
+        if (Al_out) *reinterpret_cast<float4*>(Al_out + m * K + k) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 6; ++q)
+      if (need[q]) s[q] = wave_sum(s[q]);
+    if (lane == 0) {   // wave_sum returns the total to every lane
+      if (bu_out) bu_out[m] = ((bu_in ? bu_in[m] : 0.f) + s[0]) + s[2];
+      if (bl_out) bl_out[m] = ((bl_in ? bl_in[m] : 0.f) + s[1]) + s[3];
+      if (cu_out) cu_out[m] = s[4];
+      if (cl_out) cl_out[m] = s[5];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Dense concretization (north-star kernel #4): one wave64 per row
 //   center = sum_i A[m,i] * c[d,i];  norm = sum_i |A[m,i]| (* rad[d,i])  (norm_p 0: Linf ball, box),
@@ -1356,7 +1455,23 @@ static int relax_pass(const float* A_u, const float* A_l, int64_t a_dstride, int
                    al16(A_l_out) && al16(kbias) &&
                    al16(cvec) && al16(add_l) && (add_l == nullptr || add_ld % 4 == 0) && al16(src.lo) &&
                    al16(src.hi) && al16(src.alpha) && (src.alpha_ld % 4 == 0);
-  if (vec && K >= 1024) {
+  if (vec && a_dstride == 0 && K <= 512 && S >= 16) {
+    // a shared coefficient: 16 rows of one domain per workgroup (4 per wave), the
+    // domain's operands held in registers across them (C2's 500 x 500 shape: 8, 16 and
+    // 64 rows per workgroup measured 150, 129 and 141 us, the per-row kernel 156 us)
+    const int rpw = S < 16 ? (int)S : 16;
+    const int64_t chunks = ceil_div(S, rpw);
+    BF_REQUIRE(D * chunks < (1LL << 31), "bf_crown_relu_relax: too many rows");
+    if (K <= 256)
+      hipLaunchKernelGGL(relu_relax_shared_kernel<1>, dim3((unsigned)(D * chunks)), dim3(256), 0, stream, A_u, A_l, S,
+                         K, chunks, rpw, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out,
+                         b_l_out, c_u_out, c_l_out);
+    else
+      hipLaunchKernelGGL(relu_relax_shared_kernel<2>, dim3((unsigned)(D * chunks)), dim3(256), 0, stream, A_u, A_l, S,
+                         K, chunks, rpw, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out,
+                         b_l_out, c_u_out, c_l_out);
+    BF_LAUNCH_CHECK("relu_relax_shared_kernel");
+  } else if (vec && K >= 1024) {
     hipLaunchKernelGGL(relu_relax_rows4_kernel<256>, dim3((unsigned)M), dim3(256), 0, stream, A_u, A_l, a_dstride, M, S,
                        K, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out, b_l_out, c_u_out,
                        c_l_out);

@@ -231,6 +231,46 @@ def test_relax_pass_of_shared_coefficient(K):
         assert bool((err <= tol).all()), f"{what}: {float((err / tol).max()):.3f} x tolerance"
 
 
+@pytest.mark.parametrize("K,S,same", [(256, 150, True), (500, 150, False), (512, 64, True), (132, 20, False)])
+def test_shared_coefficient_pass_equals_per_domain_pass(K, S, same):
+    """The shared-coefficient pass (operands of a domain held in registers over 16-row
+    chunks; S = 150: ten chunks, the last partial) against the per-row pass over the
+    same coefficient written out per domain: every output bit-identical, with the split
+    term, the next layer's bias and the center sums all present."""
+    dev = device()
+    announce(f"shared-coefficient relax pass vs per-domain pass K={K} S={S} same={same}")
+    g = torch.Generator().manual_seed(K * 7 + S)
+    D = 5
+    A_u = torch.randn(S, K, generator=g)
+    A_l = A_u if same else torch.randn(S, K, generator=g)
+    A_u[0, :3] = torch.tensor([0.0, -0.0, 1.0])
+    l = torch.randn(D, K, generator=g)
+    u = l + torch.rand(D, K, generator=g)
+    alpha = torch.rand(D, K, generator=g)
+    add = torch.randn(D, K, generator=g)
+    kb = torch.randn(K, generator=g)
+    cv = torch.randn(D, K, generator=g)
+    bu, bl = torch.randn(D, S, generator=g), torch.randn(D, S, generator=g)
+    d = {k: v.to(dev).contiguous() for k, v in dict(A_u=A_u, A_l=A_l, l=l, u=u, alpha=alpha, add=add, kb=kb, cv=cv,
+                                                     bu=bu, bl=bl).items()}
+    if same:
+        d["A_l"] = d["A_u"]
+    full_u = d["A_u"].expand(D, S, K).contiguous()
+    full_l = full_u if same else d["A_l"].expand(D, S, K).contiguous()
+    outs = []
+    for Au, Al, stride in ((d["A_u"], d["A_l"], 0), (full_u, full_l, S * K)):
+        o = [torch.empty(D * S, K, device=dev), torch.empty(D * S, K, device=dev)] + \
+            [torch.empty(D * S, device=dev) for _ in range(4)]
+        _lib.call("bf_crown_relu_relax_lu", _lib.ptr(Au), _lib.ptr(Al), stride, D, S, K, _lib.ptr(d["l"]),
+                  _lib.ptr(d["u"]), _lib.ptr(d["alpha"]), K, _lib.ptr(d["add"]), K, _lib.ptr(d["kb"]),
+                  _lib.ptr(d["cv"]), _lib.ptr(d["bu"]), _lib.ptr(d["bl"]), *[_lib.ptr(x) for x in o],
+                  _lib.stream_handle())
+        outs.append(o)
+    torch.cuda.synchronize()
+    for i, what in enumerate(("A_u'", "A_l'", "b_u", "b_l", "c_u", "c_l")):
+        assert torch.equal(outs[0][i], outs[1][i]), what
+
+
 # K = 133: scalar kernel (K % 4 != 0); 132, 256, 500: float4 kernel, a wave per row (500:
 # two quad steps, the second partial); 2048, 4100: float4, a workgroup per row (4100: a
 # partial last step); S = 19, 9, 3 vary the rows per domain
