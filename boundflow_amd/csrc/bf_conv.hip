@@ -231,8 +231,15 @@ struct GatherArgs {
   FastDiv f_kstride, f_npad, f_T, f_nB, f_sw, f_KHKW, f_KW, f_HpWp, f_Wp;   // staging index divisions
   FastDiv f_HWm, f_Wm;                    // channel-last staging: divisions by Hm*Wm and Wm
   const float* wpack;                     // channel-last: weights already in LDS order (or null)
+  // MODE_F interval input (IBP): 0 X[z] as given; IVL_BOX X[0] = lo, ivl_hi = hi, operand z = 0
+  // the center (l + u) / 2, z = 1 the radius (u - l) / 2 (IVL_RELU: of max(., 0)); IVL_BALL
+  // z = 0 X[0], z = 1 ivl_eps inside the map (the padding stays zero)
+  int ivl;
+  const float* ivl_hi;
+  float ivl_eps;
   GatherClass cls[GMAX_CLASSES];
 };
+constexpr int IVL_BOX = 1, IVL_RELU = 2, IVL_BALL = 4;
 
 static void gather_fdivs(GatherArgs& g) {
   g.f_kstride = make_fdiv(g.Kc4 * g.npad);
@@ -343,6 +350,10 @@ conv_mfma_kernel(GatherArgs g) {
     if (r >= g.R) break;   // uniform
     __syncthreads();       // weights staged / previous row's map and partial sums consumed
     const float* __restrict__ xr = X + (r / g.in_div) * nin;
+    // interval input: the operand is made from the bounds as the map is staged (the
+    // arithmetic of ibp_center_radius_kernel), uniform over the launch
+    const int ivl = MODE == MODE_F ? g.ivl : 0;
+    const float* __restrict__ hr_row = (ivl & IVL_BOX) ? g.ivl_hi + (r / g.in_div) * nin : nullptr;
     for (int base = 0; base < map; base += 8 * GTM) {
       float xv[8];
 #pragma unroll
@@ -352,7 +363,20 @@ conv_mfma_kernel(GatherArgs g) {
         const int hr = fdivq(rem, g.f_Wp);
         const int hm = hr - g.pad_h, wm = (rem - hr * g.Wp) - g.pad_w;
         const bool ok = idx < map && hm >= 0 && hm < g.Hm && wm >= 0 && wm < g.Wm;
-        const float x = xr[ok ? (c * g.Hm + hm) * g.Wm + wm : 0];
+        const int src = ok ? (c * g.Hm + hm) * g.Wm + wm : 0;
+        float x;
+        if (ivl & IVL_BOX) {
+          float l = xr[src], h = hr_row[src];
+          if (ivl & IVL_RELU) {
+            l = fmaxf(l, 0.f);
+            h = fmaxf(h, 0.f);
+          }
+          x = z == 0 ? (l + h) / 2.0f : (h - l) / 2.0f;
+        } else if ((ivl & IVL_BALL) && z == 1) {
+          x = g.ivl_eps;
+        } else {
+          x = xr[src];
+        }
         xv[u] = ok ? x : 0.f;
       }
 #pragma unroll
@@ -1870,6 +1894,37 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
   return BF_OK;
 }
 
+// The center and radius products of an IBP conv layer in one launch of the forward
+// gather-GEMM, the operands made from the input set while each row's map is staged
+// (ivl: IVL_BOX [| IVL_RELU] from lo / hi, or IVL_BALL from the center and eps).  Returns
+// BF_OK with *planned false, launching nothing, for shapes the gather-GEMM does not take.
+static int conv2d_ivl_launch(const float* lo, const float* hi, int ivl, float eps, int64_t R, int Ci, int Hi, int Wi,
+                             const float* W, int Co, int KH, int KW, int sh, int sw, int ph, int pw, int Ho, int Wo,
+                             float* yc, float* yr, bool* planned, hipStream_t stream) {
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t glds = 0;
+  *planned = conv_f_mfma_plan(g, R, Ci, Hi, Wi, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, &glds);
+  if (!*planned) return BF_OK;
+  g.X[0] = lo;
+  g.X[1] = lo;
+  g.y[0] = yc;
+  g.y[1] = yr;
+  g.W = W;
+  g.abs_w = 2;   // the radius product takes |W|
+  g.in_div = 1;
+  g.S = 1;
+  g.ivl = ivl;
+  g.ivl_hi = hi;
+  g.ivl_eps = eps;
+  g.rows_per_wg = gather_rows_per_wg(R * 2);
+  const int rpw = g.rows_per_wg;
+  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "conv2d: too many rows");
+  hipLaunchKernelGGL(conv_mfma_kernel<MODE_F>, dim3((unsigned)((R + rpw - 1) / rpw), 2), dim3(GTM), glds, stream, g);
+  BF_LAUNCH_CHECK("conv_mfma_kernel<conv2d, interval>");
+  return BF_OK;
+}
+
 int bf_ibp_conv2d(const float* in_lo, const float* in_hi, int64_t B, int Ci, int Hi, int Wi, int input_kind,
                   float eps, int apply_relu, const float* W, const float* bias, int Co, int KH, int KW, int sh,
                   int sw, int ph, int pw, int Ho, int Wo, const int8_t* split, int64_t split_ld, float* workspace,
@@ -1887,8 +1942,17 @@ int bf_ibp_conv2d(const float* in_lo, const float* in_hi, int64_t B, int Ci, int
   float* r = c + B * nout;
   float* cdst = center_out ? center_out : c;
   int rc;
-  // the center (W) and the radius (|W|) products in one launch
-  if (input_kind == 1) {
+  // the center (W) and the radius (|W|) products in one launch, the center and radius made
+  // from the input set while the gather-GEMM stages each row
+  bool planned = false;
+  if (input_kind == 1 || in_hi) {
+    rc = conv2d_ivl_launch(in_lo, in_hi, input_kind == 1 ? IVL_BALL : (IVL_BOX | (apply_relu ? IVL_RELU : 0)), eps, B,
+                           Ci, Hi, Wi, W, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, cdst, r, &planned, stream);
+    if (rc) return rc;
+  }
+  if (planned) {
+    rc = BF_OK;
+  } else if (input_kind == 1) {
     // center x0 conv W; the radius map is eps everywhere inside the image (padding has none)
     rc = fill_value(rad, B * nin, eps, stream);
     if (rc) return rc;

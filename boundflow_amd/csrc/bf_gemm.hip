@@ -169,8 +169,18 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int ks, int
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= M * N) return;
   const int64_t m = div_rows(i, N, M * N < (1LL << 31)), n = i - m * N;
+  const int64_t MN = M * N;
   float v = part[i];
-  for (int s = 1; s < ks; ++s) v += part[(int64_t)s * M * N + i];
+  // the chunks' loads issued eight at a time, their sums still in chunk order
+  int s = 1;
+  for (; s + 8 <= ks; s += 8) {
+    float t[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) t[q] = part[(int64_t)(s + q) * MN + i];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v += t[q];
+  }
+  for (; s < ks; ++s) v += part[(int64_t)s * MN + i];
   if (r_row) v = v + r_row[m] * v_col[div_rows(m, S, M < (1LL << 31)) * v_ld + n];
   C[m * ldc + n] = v;
 }

@@ -172,3 +172,50 @@ def test_conv_first_layer_two_or_more_splits_match_oracle_and_lp():
     announce(f"  infeasible: hip {sum(got)}, oracle {sum(ref)} of {len(got)}")
     assert sum(ref) >= 3
     assert got == ref
+
+
+def test_cifar_sized_input_matches_oracle():
+    """A 3072-input first layer (3x32x32 flattened: a 12 KB LDS stage of the combined
+    normal plus the per-node state): 16 nodes, each splitting a pair of neurons that share
+    a weight row and differ in bias by delta in [0.05, 0.15] (both ambiguous: the box's
+    radius term is about 0.44), plus two random neurons.  Active on the lower-bias neuron
+    and inactive on the other is empty (w.x + b >= 0 and w.x + b + delta <= 0), which the
+    Adam search closes with a maximum near -delta / 2 scaled by the pair's weight; the
+    reverse is a feasible band.  The device's verdicts and closing maxima equal the
+    oracle's, and both verdicts occur."""
+    dev = device()
+    announce("split certificate vs oracle, 3072 inputs, 16 nodes")
+    g = torch.Generator().manual_seed(30)
+    I, H = 3072, 64
+    x0 = torch.rand(1, I, generator=g)
+    eps = 0.01
+    W = torch.randn(H // 2, I, generator=g) / I ** 0.5
+    W = torch.cat([W, W])
+    b0 = -(W[: H // 2] @ x0[0]) + 0.002 * torch.randn(H // 2, generator=g)
+    delta = 0.05 + 0.1 * torch.rand(H // 2, generator=g)
+    b = torch.cat([b0, b0 + delta])
+    m = first_layer_module(W, b)
+    nodes = 16
+    rows = torch.zeros(nodes, H, dtype=torch.int8)
+    for r in range(nodes):
+        j = int(torch.randint(0, H // 2, (1,), generator=g))
+        rows[r, j], rows[r, j + H // 2] = (1, -1) if r % 2 == 0 else (-1, 1)
+        others = [k for k in torch.randperm(H, generator=g).tolist() if k % (H // 2) != j][:2]
+        for k in others:
+            rows[r, k] = 1 if int(torch.randint(0, 2, (1,), generator=g)) else -1
+    ref_flags, ref_vals = [], []
+    spec1 = InputSpec.linf(value_name="input", center=x0, eps=eps)
+    for r in range(nodes):
+        flag, _reason, val = ab.split_certificate(m, spec1, {"h1": rows[r:r + 1]}, return_value=True)
+        ref_flags.append(int(flag))
+        ref_vals.append(val)
+    sd = InputSpec.linf(value_name="input", center=x0.expand(nodes, I).contiguous().to(dev), eps=eps)
+    value = torch.empty(nodes, device=dev)
+    got = split_certificate(_to(m, dev), sd, {"h1": rows.to(dev)}, {"h1": (H,)}, max_out=value).cpu().tolist()
+    announce(f"  infeasible: hip {sum(got)}, oracle {sum(ref_flags)} of {nodes}")
+    assert got == ref_flags
+    assert 0 < sum(ref_flags) < nodes
+    for r in range(nodes):
+        if ref_flags[r]:
+            v, ref = float(value[r]), float(ref_vals[r])
+            assert abs(v - ref) <= 1e-4 * abs(ref) + 1e-6, (r, v, ref)
