@@ -19,6 +19,11 @@ struct GemmArgs {
   int64_t ldb;
   int trans_b;
   int abs_b;        // bit z set: product z uses |B| (interval radius products)
+  // Interval operand of the IBP products (plain prologue, register-staged loop): A[0] = A[1]
+  // hold the lower bounds and ivl_hi the upper ones (same layout); product z = 0 reads the
+  // center (l + u) / 2, z = 1 the radius (u - l) / 2, of max(l, 0) and max(u, 0) when ivl_relu.
+  const float* ivl_hi;
+  int ivl_relu;
   int64_t M, N, K;
   int z_lower_first;  // when 1, blockIdx.z = 0 uses lower semantics (single lower pass)
 

@@ -138,6 +138,20 @@ __device__ __forceinline__ float halve_rows16(const float (&v)[16], int lrow, J 
   return join(w1, __shfl_xor(w1, 1, 64));
 }
 
+// Center (z = 0) or radius (z = 1) of an interval operand, of its ReLU when relu (the
+// arithmetic of ibp_center_radius_kernel, so either way gives the same bits).
+__device__ __forceinline__ float ivl_pick(float l, float u, bool center, bool relu) {
+  if (relu) {
+    l = fmaxf(l, 0.f);
+    u = fmaxf(u, 0.f);
+  }
+  return center ? (l + u) / 2.0f : (u - l) / 2.0f;
+}
+__device__ __forceinline__ float4 ivl_pick4(float4 l, float4 u, bool center, bool relu) {
+  return make_float4(ivl_pick(l.x, u.x, center, relu), ivl_pick(l.y, u.y, center, relu),
+                     ivl_pick(l.z, u.z, center, relu), ivl_pick(l.w, u.w, center, relu));
+}
+
 // DL: the direct-to-LDS main loop (plain prologue, transposed B, BK 16, aligned
 // float4 operands): three LDS stages filled by global_load_lds_dwordx4, two K
 // tiles in flight while the third is multiplied, one barrier per K tile.  Each
@@ -198,7 +212,9 @@ gemm_kernel(GemmArgs p) {
   const int64_t m0 = (tile / ntn) * GBM;
   const int64_t n0 = tile_n * GBN;
   const bool row_reduce = (PRO == PRO_RELAX) && (tile_n == 0);
-  const bool vec_a = ((K & 3) == 0) && ((p.lda & 3) == 0) && ((p.lda_d & 3) == 0) && (((uintptr_t)A & 15) == 0);
+  const bool vec_a = ((K & 3) == 0) && ((p.lda & 3) == 0) && ((p.lda_d & 3) == 0) && (((uintptr_t)A & 15) == 0) &&
+                     (((uintptr_t)p.ivl_hi & 15) == 0);
+  const bool ivl = PRO == PRO_PLAIN && !DL && p.ivl_hi != nullptr;   // uniform
   const bool vec_b = TRANS_B ? (((K & 3) == 0) && ((p.ldb & 3) == 0) && (((uintptr_t)p.B & 15) == 0))
                              : (((N & 3) == 0) && ((p.ldb & 3) == 0) && (((uintptr_t)p.B & 15) == 0));
 
@@ -242,6 +258,12 @@ gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < A_SLOTS; ++j)
         a_reg[j] = *reinterpret_cast<const float4*>(A + a_base[j] + k0 + 4 * a_kq);
+      if (PRO == PRO_PLAIN && ivl) {
+#pragma unroll
+        for (int j = 0; j < A_SLOTS; ++j)
+          a_reg[j] = ivl_pick4(a_reg[j], *reinterpret_cast<const float4*>(p.ivl_hi + a_base[j] + k0 + 4 * a_kq),
+                               z == 0, p.ivl_relu != 0);
+      }
 #pragma unroll
       for (int j = 0; j < B_SLOTS; ++j) {
         if (!T::B_FULL && t + GNT * j >= T::B_QUADS) {
@@ -260,18 +282,24 @@ gemm_kernel(GemmArgs p) {
     for (int j = 0; j < A_SLOTS; ++j) {
       const int64_t m = m0 + a_r0 + RPP * j;
       const int64_t k = k0 + 4 * a_kq;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (m < M) {
-        const float* src = A + a_base[j] + k;
-        if (vec_a) {
-          if (k < K) v = *reinterpret_cast<const float4*>(src);
-        } else {
-          if (k + 0 < K) v.x = src[0];
-          if (k + 1 < K) v.y = src[1];
-          if (k + 2 < K) v.z = src[2];
-          if (k + 3 < K) v.w = src[3];
+      auto load_a = [&](const float* base) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m < M) {
+          const float* src = base + a_base[j] + k;
+          if (vec_a) {
+            if (k < K) v = *reinterpret_cast<const float4*>(src);
+          } else {
+            if (k + 0 < K) v.x = src[0];
+            if (k + 1 < K) v.y = src[1];
+            if (k + 2 < K) v.z = src[2];
+            if (k + 3 < K) v.w = src[3];
+          }
         }
-      }
+        return v;
+      };
+      float4 v = load_a(A);
+      // padding (zero bounds) gives a zero center and radius
+      if (PRO == PRO_PLAIN && ivl) v = ivl_pick4(v, load_a(p.ivl_hi), z == 0, p.ivl_relu != 0);
       a_reg[j] = v;
     }
 #pragma unroll
@@ -924,7 +952,7 @@ using TileS = Tile<64, 64, 32, 2, 2, 4>;          // 4 waves of 32x32, 4 workgro
 // Operands the direct-to-LDS loop takes: transposed B and whole aligned float4 rows.
 inline bool gemm_dl_operands(const GemmArgs& a, int nz) {
   bool dl = a.trans_b && (a.K & 3) == 0 && (a.lda & 3) == 0 && (a.lda_d & 3) == 0 && (a.ldb & 3) == 0 &&
-            ((uintptr_t)a.B & 15) == 0;
+            ((uintptr_t)a.B & 15) == 0 && a.ivl_hi == nullptr;
   for (int z = 0; z < nz; ++z) dl = dl && ((uintptr_t)a.A[z] & 15) == 0;
   return dl;
 }

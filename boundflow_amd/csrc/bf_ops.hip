@@ -1532,8 +1532,11 @@ int bf_concretize_dense(const float* A, int64_t D, int64_t S, int64_t I, const f
 // in chunk order.
 // When K is split (*ks > 1), the partial products stay in `part` ([z][s][B*N]) for
 // the finalize kernel to sum; otherwise c (and r) hold the products.
+// ivl_hi: xc = xr hold an interval's lower bounds and ivl_hi its upper ones; the products
+// read their center and radius (of the ReLU when relu) as the operand tiles are loaded.
 static int ibp_products(const float* xc, const float* xr, const float* W, int64_t B, int64_t K, int64_t N, float* c,
-                        float* r, float* part, int* ks_out, hipStream_t stream) {
+                        float* r, float* part, int* ks_out, hipStream_t stream, const float* ivl_hi = nullptr,
+                        int relu = 0) {
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   const int nz = xr ? 2 : 1;
@@ -1541,6 +1544,8 @@ static int ibp_products(const float* xc, const float* xr, const float* W, int64_
   a.C[0] = c;
   a.A[1] = xr;
   a.C[1] = r;
+  a.ivl_hi = ivl_hi;
+  a.ivl_relu = relu;
   a.lda = K;
   a.lda_d = K;
   a.ldc = N;
@@ -1592,9 +1597,10 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
                               split, split_ld, B, N, out_lo, out_hi, infeasible, stream);
   }
   BF_REQUIRE(in_hi, "bf_ibp_linear: interval input needs in_hi");
-  rc = ibp_center_radius(in_lo, in_hi, B * K, apply_relu, mid, rad, stream);
-  if (rc) return rc;
-  rc = ibp_products(mid, rad, W, B, K, N, cdst, r, part, &ks, stream);
+  // the center and radius (of the ReLU when apply_relu) made as the products load their tiles
+  (void)mid;
+  (void)rad;
+  rc = ibp_products(in_lo, in_lo, W, B, K, N, cdst, r, part, &ks, stream, in_hi, apply_relu);
   if (rc) return rc;
   return ibp_finalize_parts(cdst, r, ks > 1 ? part : nullptr, ks, 1, center_out, nullptr, 0.f, bias, 1, split,
                             split_ld, B, N, out_lo, out_hi, infeasible, stream);
