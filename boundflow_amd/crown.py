@@ -496,6 +496,7 @@ def crown_backward(
     # A coefficient produced by bf_crown_relu_linear_relu_fwd already carries the
     # relaxation (and bias) of the ReLU it enters: the next region skips its prologue.
     pre_relaxed = False
+    relax_pass_next = False   # the coefficient is a kept head product: relax it in a pass of its own
     for k in range(len(layers) - 1, -1, -1):
         layer = layers[k]
         alpha, alpha_ld, add, add_ld, pre_lo, pre_hi, N = relax_params(k)
@@ -509,6 +510,7 @@ def crown_backward(
             save.setdefault("A_in", {})[k] = (A_l, stride)
             save.setdefault("b_in", {})[k] = b_l
         if layer.kind == "conv2d":
+            relax_pass_next = False   # a conv region relaxes its coefficient itself
             A_u, A_l, b_u, b_l, stride, done = conv_backward_step(
                 layer, k == 0, A_u, A_l, stride, b_u, b_l, B, S, pre_lo, pre_hi, alpha, alpha_ld, add, add_ld,
                 spec, trace, save=save)
@@ -532,7 +534,7 @@ def crown_backward(
         shared_first = (stride == 0 and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M
                         and (k == 0 or layers[k - 1].kind == "linear"))
         small_grid = M < EPILOGUE_MIN_M and N >= RELAX_PASS_MIN_K
-        if relaxes and (shared_first or small_grid):
+        if relaxes and (shared_first or small_grid or relax_pass_next):
             # A coefficient shared by every domain (the first region of a C = I query):
             # its relaxation differs per domain, so one bandwidth-bound pass writes it
             # per domain (with the bias terms and, at the input layer, the center sums)
@@ -562,6 +564,7 @@ def crown_backward(
             add_ld = 0
             relaxes = False
             pre_relaxed = True
+        relax_pass_next = False
         relax = relax_table(k) if relaxes else None
         if k == 0 and pre_relaxed:
             # input layer of an already relaxed coefficient: contraction fused with the concretization
@@ -631,7 +634,13 @@ def crown_backward(
         nz = int(A_u is not None) + int(A_l is not None)
         a_rows = M if stride != 0 else S
         flops, nbytes = 2.0 * nz * M * N * P, 4.0 * nz * (a_rows * N + N * P + M * P)
-        if layers[k - 1].kind == "linear" and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M:
+        # The head region (the spec C through the last layer, nothing to relax) depends on C
+        # and the layer's parameters alone: an optimisation call makes it once and its later
+        # passes reuse it (kept in the call's own memo, keyed by C's storage and version); the
+        # next region then relaxes the kept product in a pass of its own.
+        head_memo = (k == len(layers) - 1 and relax is None and add is None and save is not None
+                     and save.get("memo") is not None and torch.is_tensor(linear_spec_C))
+        if not head_memo and layers[k - 1].kind == "linear" and S >= EPILOGUE_MIN_ROWS and M >= EPILOGUE_MIN_M:
             # the next region's relaxation in this contraction's epilogue
             n_alpha, n_alpha_ld, n_add, n_add_ld, _, _, _ = relax_params(k - 1)
             n_table = relax_table(k - 1)
@@ -675,14 +684,11 @@ def crown_backward(
                       and (A_l is None or b_l is not None))
             if keep_b:
                 nb_u, nb_l = b_u, b_l
-            # The head region (the spec C through the last layer, nothing to relax) depends on C
-            # and the layer's parameters alone: an optimisation call makes it once and its later
-            # passes reuse it (kept in the call's own memo, keyed by C's storage and version).
             head_key = None
-            if (k == len(layers) - 1 and relax is None and add is None and save is not None
-                    and save.get("memo") is not None and torch.is_tensor(linear_spec_C)):
+            if head_memo:
                 head_key = (f"head:{k}:{linear_spec_C.data_ptr()}:{linear_spec_C._version}:"
                             f"{A_u is not None}:{A_l is not None}")
+                relax_pass_next = True
             hit = save["memo"].get(head_key) if head_key is not None else None
             if hit is not None:
                 nA_u, nA_l, nb_u, nb_l = hit
