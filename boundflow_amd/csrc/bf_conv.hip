@@ -230,6 +230,7 @@ struct GatherArgs {
   int Kc, Kc4, npad, nblk, nclasses, ntasks;
   FastDiv f_kstride, f_npad, f_T, f_nB, f_sw, f_KHKW, f_KW, f_HpWp, f_Wp;   // staging index divisions
   FastDiv f_HWm, f_Wm;                    // channel-last staging: divisions by Hm*Wm and Wm
+  FastDiv f_Kc4;                          // MODE_F weight staging in source order: division by Kc4
   const float* wpack;                     // channel-last: weights already in LDS order (or null)
   // MODE_F interval input (IBP): 0 X[z] as given; IVL_BOX X[0] = lo, ivl_hi = hi, operand z = 0
   // the center (l + u) / 2, z = 1 the radius (u - l) / 2 (IVL_RELU: of max(., 0)); IVL_BALL
@@ -251,6 +252,7 @@ static void gather_fdivs(GatherArgs& g) {
   g.f_KW = make_fdiv(g.KW);
   g.f_HpWp = make_fdiv(g.Hp * g.Wp);
   g.f_Wp = make_fdiv(g.Wp);
+  g.f_Kc4 = make_fdiv(g.Kc4 > 0 ? g.Kc4 : 1);
 }
 
 // LDS layout of the gather-GEMM operands.  The weights of class c, output channel n
@@ -289,15 +291,30 @@ conv_mfma_kernel(GatherArgs g) {
   const int kstride = g.Kc4 * g.npad;
 
   // weights of every class, zero-padded in k (to Kc4) and in channels (to npad);
-  // eight loads per thread in flight, from clamped addresses, before the stores
+  // eight loads per thread in flight, from clamped addresses, before the stores.
+  // MODE_F (one class) walks them in the source order, k fastest, so a wave's loads
+  // are consecutive floats of one output channel's row (W[n * Kc + k]), and scatters
+  // them into the LDS order.
   const int wtotal = g.nclasses * kstride;
+  auto w_coords = [&](int idx, int& c, int& k, int& n) {
+    if (MODE == MODE_F) {
+      c = 0;
+      n = fdivq(idx, g.f_Kc4);
+      k = idx - n * g.Kc4;
+    } else {
+      c = fdivq(idx, g.f_kstride);
+      const int rem = idx - c * kstride;
+      k = fdivq(rem, g.f_npad);
+      n = rem - k * g.npad;
+    }
+  };
   for (int base = 0; base < wtotal; base += 8 * GTM) {
     float wv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int idx = base + u * GTM + tid;
-      const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
-      const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
+      int c, k, n;
+      w_coords(idx, c, k, n);
       const bool ok = idx < wtotal && k < g.Kc && n < g.nch;
       int64_t src;
       if (MODE == MODE_T) {
@@ -317,8 +334,8 @@ conv_mfma_kernel(GatherArgs g) {
     for (int u = 0; u < 8; ++u) {
       const int idx = base + u * GTM + tid;
       if (idx < wtotal) {
-        const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
-        const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
+        int c, k, n;
+        w_coords(idx, c, k, n);
         Ws[ws_index(g, c, n, k)] = wv[u];
       }
     }
