@@ -46,9 +46,9 @@ PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E
 # reads for a 1 GiB device copy: x2.0 and x1.0), averaged over the launch mix
 # of that query.  Keyed by (config, kernel family); other pairs report null.
 MEASURED_TRAFFIC = {
-    ("C2", "crown_relu_linear_relu_fwd"): (1.2383e9, "profiles/hbm_traffic_dominant_kernels.md"),
-    ("C5", "crown_relu_linear_relu_fwd"): (1.3490e8, "profiles/hbm_traffic_dominant_kernels.md"),
-    ("C5", "grad_gemm"): (1.0042e8, "profiles/hbm_traffic_dominant_kernels.md"),
+    ("C2", "crown_relu_linear_relu_fwd"): (1.2301e9, "profiles/hbm_traffic_dominant_kernels.md"),
+    ("C5", "crown_relu_linear_relu_fwd"): (1.3250e8, "profiles/hbm_traffic_dominant_kernels.md"),
+    ("C5", "grad_gemm"): (1.0040e8, "profiles/hbm_traffic_dominant_kernels.md"),
 }
 
 
