@@ -285,8 +285,18 @@ def _numel(shape) -> int:
 class ForwardTrace:
     interval_env: Dict[str, IntervalState]
     relu_pre: Dict[str, IntervalState]
-    infeasible: Optional[torch.Tensor]       # int32 [B] (1 = the split/constraint emptied a box)
+    # int32 [B] (1 = the split/constraint emptied a box); None while no split or constraint
+    # was applied (no box can be emptied then): ``infeasible`` makes the zeros on first read
+    infeasible_flags: Optional[torch.Tensor]
     input_center_proj: Dict[str, torch.Tensor] = field(default_factory=dict)  # first-layer x0 W^T (no bias)
+    batch: int = 0
+    device: Optional[torch.device] = None
+
+    @property
+    def infeasible(self) -> torch.Tensor:
+        if self.infeasible_flags is None:
+            self.infeasible_flags = torch.zeros(self.batch, dtype=torch.int32, device=self.device)
+        return self.infeasible_flags
 
 
 def _broadcast_split(split: torch.Tensor, batch: int, numel: int) -> Tuple[torch.Tensor, int]:
@@ -322,7 +332,9 @@ def forward_ibp_trace(
     dev = center.device
     stream = _lib.stream_handle()
     relu_set = set(chain.relu_names)
-    infeasible = torch.zeros(B, dtype=torch.int32, device=dev)
+    # flags only where a split or a constraint can empty a box (the kernels take NULL)
+    may_empty = bool(relu_split_state) or relu_pre_constraints is not None
+    infeasible = torch.zeros(B, dtype=torch.int32, device=dev) if may_empty else None
     interval_env: Dict[str, IntervalState] = {}
     relu_pre: Dict[str, IntervalState] = {}
     proj: Dict[str, torch.Tensor] = {}
@@ -393,7 +405,7 @@ def forward_ibp_trace(
     if raise_on_infeasible and (relu_split_state or relu_pre_constraints):
         if bool(infeasible.any().item()):
             raise ValueError("infeasible relu split or constraint: lower>upper after applying split")
-    return ForwardTrace(interval_env=interval_env, relu_pre=relu_pre, infeasible=infeasible,
+    return ForwardTrace(interval_env=interval_env, relu_pre=relu_pre, infeasible_flags=infeasible, batch=B, device=dev,
                         input_center_proj=proj)
 
 
