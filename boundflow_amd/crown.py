@@ -868,7 +868,8 @@ def run_crown_ibp_mlp_with_relu_influence_from_forward_trace(
         raise NotImplementedError("ReLU influence extraction currently supports one task only")
     spec = normalize_input_spec(input_spec)
     shapes, _relu_shapes = value_shapes(module, spec)
-    trace = DagTrace(interval_env=dict(interval_env), relu_pre=dict(relu_pre), shapes=shapes)
+    trace = DagTrace(interval_env=dict(interval_env), relu_pre=dict(relu_pre), shapes=shapes,
+                     batch=int(spec.center.shape[0]), device=spec.center.device)
     influence: Dict[str, torch.Tensor] = {}
     bounds = crown_backward_dag(module, spec, trace, linear_spec_C=linear_spec_C, output_value=output_value,
                                 relu_influence=influence)

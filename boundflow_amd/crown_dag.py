@@ -68,8 +68,18 @@ class DagTrace:
     interval_env: Dict[str, IntervalState]
     relu_pre: Dict[str, IntervalState]
     shapes: Dict[str, Tuple[int, ...]]
-    infeasible: Optional[torch.Tensor] = None
+    # int32 [B]; None while no split or constraint was applied (no box can be emptied then):
+    # ``infeasible`` makes the zeros on first read
+    infeasible_flags: Optional[torch.Tensor] = None
     input_views: Dict[str, str] = field(default_factory=dict)   # value -> "input" for the input and its reshapes
+    batch: int = 0
+    device: Optional[torch.device] = None
+
+    @property
+    def infeasible(self) -> torch.Tensor:
+        if self.infeasible_flags is None:
+            self.infeasible_flags = torch.zeros(self.batch, dtype=torch.int32, device=self.device)
+        return self.infeasible_flags
 
 
 @dataclass
@@ -181,7 +191,9 @@ def forward_ibp_trace_dag(
     # a linear layer on the input takes the ball's dual row norm of W; every other consumer of
     # the input reads its bounding box (center -/+ eps for p = 1, 2, inf), as crown_ibp.py:125-178
     ibp_kind = 0 if box else {0: 1, 2: 2, 1: 3}[input_norm_p(pert)]
-    infeasible = torch.zeros(B, dtype=torch.int32, device=dev)
+    # flags only where a split or a constraint can empty a box (the kernels take NULL)
+    may_empty = bool(relu_split_state) or relu_pre_constraints is not None
+    infeasible = torch.zeros(B, dtype=torch.int32, device=dev) if may_empty else None
     env: Dict[str, IntervalState] = {}
     relu_pre: Dict[str, IntervalState] = {}
     shapes: Dict[str, Tuple[int, ...]] = {spec.value_name: tuple(int(d) for d in center.shape[1:])}
@@ -316,7 +328,7 @@ def forward_ibp_trace_dag(
     if raise_on_infeasible and (relu_split_state or relu_pre_constraints):
         if bool(infeasible.any().item()):
             raise ValueError("infeasible relu split or constraint: lower>upper after applying split")
-    return DagTrace(interval_env=env, relu_pre=relu_pre, shapes=shapes, infeasible=infeasible,
+    return DagTrace(interval_env=env, relu_pre=relu_pre, shapes=shapes, infeasible_flags=infeasible, batch=B, device=dev,
                     input_views={name: spec.value_name for name in views})
 
 
@@ -386,8 +398,8 @@ def crown_backward_dag(
         return au, al
 
     def zeros_like_b(st: _Rows):
-        z = torch.zeros(M, device=dev)
-        return (z if st.b_u is not None else None), (z if st.b_l is not None else None)
+        # bias rows are values (every step writes fresh ones): one zero row serves them all
+        return (zero_b if st.b_u is not None else None), (zero_b if st.b_l is not None else None)
 
     def rows_pass(st: _Rows, n: int, *, pre=None, alpha=None, alpha_ld=0, add=None, add_ld=0, kbias=None,
                   cvec=None, name="crown_relu_relax"):
