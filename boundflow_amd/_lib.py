@@ -60,6 +60,7 @@ SIGNATURES = {
     "bf_ibp_linear_workspace": (I64, [I64, I64, I64]),
     "bf_interval_clip": (I32, [P, P, P, P, P, I64, I64, I64, P, P]),
     "bf_interval_relu": (I32, [P, P, I64, P, P, P]),
+    "bf_interval_center_radius": (I32, [P, P, I64, I32, P, P, P]),
     "bf_interval_add": (I32, [P, P, P, P, I64, P, P, P]),
     "bf_interval_mul": (I32, [P, P, P, P, I64, P, P, P]),
     "bf_spec_linear": (I32, [P, P, P, I64, I64, I64, P, P, P]),

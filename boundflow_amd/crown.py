@@ -745,10 +745,13 @@ def _identity_table(B: int, n: int, dev) -> torch.Tensor:
 def _input_radius(pert, B: int, P: int):
     """(rad, eps) of the input concretization: box radius with eps 1, or Linf eps without weights."""
     if isinstance(pert, BoxPerturbation):
-        lo = pert.lower.reshape(B, P)
-        hi = pert.upper.reshape(B, P)
-        # depends on the query's input set: computed per query, never kept across queries
-        return ((hi - lo) / 2.0).contiguous(), 1.0
+        lo = pert.lower.reshape(B, P).contiguous()
+        hi = pert.upper.reshape(B, P).contiguous()
+        # depends on the query's input set: computed per query (one launch), never kept across queries
+        rad = torch.empty(B, P, device=lo.device, dtype=torch.float32)
+        _lib.call("bf_interval_center_radius", _lib.ptr(lo), _lib.ptr(hi), B * P, 0, None, _lib.ptr(rad),
+                  _lib.stream_handle())
+        return rad, 1.0
     return None, float(pert.eps)
 
 

@@ -55,8 +55,8 @@ __global__ void ibp_center_radius_kernel(const float* __restrict__ lo, const flo
     l = fmaxf(l, 0.f);
     u = fmaxf(u, 0.f);
   }
-  mid[i] = (l + u) / 2.0f;
-  rad[i] = (u - l) / 2.0f;
+  if (mid) mid[i] = (l + u) / 2.0f;
+  if (rad) rad[i] = (u - l) / 2.0f;
 }
 
 int ibp_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
@@ -1610,6 +1610,14 @@ int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) {
   int64_t kchunk;
   const int ks = gemm_ksplit(B, N, K, &kchunk);
   return 2 * B * K + 2 * B * N + N + (ks > 1 ? 2 * (int64_t)ks * B * N : 0);
+}
+
+int bf_interval_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
+                              hipStream_t stream) {
+  BF_REQUIRE(n >= 0, "bf_interval_center_radius: bad size");
+  if (n == 0 || (mid == nullptr && rad == nullptr)) return BF_OK;
+  BF_REQUIRE(lo && hi, "bf_interval_center_radius: null pointer");
+  return ibp_center_radius(lo, hi, n, apply_relu, mid, rad, stream);
 }
 
 int bf_interval_relu(const float* lo, const float* hi, int64_t n, float* out_lo, float* out_hi, hipStream_t stream) {

@@ -90,6 +90,11 @@ int bf_interval_clip(float* lo, float* hi, const float* clo, const float* chi, c
  * spec_linear (C+ l + C- u, :423-439) and the batched per-sample linear W [B, O, I] in
  * center/radius form (:445-458).  mul expects both operands already broadcast to n elements. */
 int bf_interval_relu(const float* lo, const float* hi, int64_t n, float* out_lo, float* out_hi, hipStream_t stream);
+/* Center (l + u) / 2 and radius (u - l) / 2 of an interval (of max(., 0) when apply_relu),
+ * either output NULL to skip it: the center/radius form of IBP (domains/interval.py:57-86)
+ * and the box radius of a concretization (runtime/perturbation.py:327-359, (upper - lower) / 2). */
+int bf_interval_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,
+                              hipStream_t stream);
 int bf_interval_add(const float* a_lo, const float* a_hi, const float* b_lo, const float* b_hi, int64_t n,
                     float* out_lo, float* out_hi, hipStream_t stream);
 int bf_interval_mul(const float* a_lo, const float* a_hi, const float* b_lo, const float* b_hi, int64_t n,
