@@ -546,3 +546,47 @@ def test_relu_grad_matches_formula(with_alpha):
     ref_gb = -split.double() * g3.sum(1)
     assert torch.allclose(ga.double(), ref_ga, rtol=1e-5, atol=1e-5)
     assert torch.allclose(gb.double(), ref_gb, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("relu", [0, 1])
+def test_interval_center_radius_matches_torch(relu):
+    """bf_interval_center_radius: (l + u) / 2 and (u - l) / 2 of the interval (of its ReLU
+    when asked), bit for bit torch's fp32 arithmetic, either output alone when the other is
+    NULL (the input concretization's box radius asks for the radius only)."""
+    dev = device()
+    announce(f"interval center/radius relu={relu}")
+    g = torch.Generator().manual_seed(7 + relu)
+    n = 100003
+    lo = torch.randn(n, generator=g)
+    hi = lo + torch.rand(n, generator=g)
+    lo[:4] = torch.tensor([0.0, -0.0, -1.0, 2.0])
+    hi[:4] = torch.tensor([0.0, 0.0, -0.5, 3.0])
+    l, u = (lo.clamp_min(0), hi.clamp_min(0)) if relu else (lo, hi)
+    d = [x.to(dev) for x in (lo, hi)]
+    mid = torch.empty(n, device=dev)
+    rad = torch.empty(n, device=dev)
+    _lib.call("bf_interval_center_radius", _lib.ptr(d[0]), _lib.ptr(d[1]), n, relu, _lib.ptr(mid), _lib.ptr(rad),
+              _lib.stream_handle())
+    rad_only = torch.full((n,), 7.0, device=dev)
+    _lib.call("bf_interval_center_radius", _lib.ptr(d[0]), _lib.ptr(d[1]), n, relu, None, _lib.ptr(rad_only),
+              _lib.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(mid.cpu(), (l + u) / 2.0)
+    assert torch.equal(rad.cpu(), (u - l) / 2.0)
+    assert torch.equal(rad_only.cpu(), (u - l) / 2.0)
+
+
+def test_flags_without_splits_are_zeros_made_on_read():
+    """A forward trace with no split or constraint launches no flag fill (no box can be
+    emptied); its ``infeasible`` reads as int32 zeros on the device, as the flags of a trace
+    whose splits empty nothing."""
+    dev = device()
+    announce("forward trace flags without splits")
+    w = wl.make_c1()
+    wd = wl.to_device(w, dev)
+    trace = hc.forward_ibp_trace(wd.module, wd.spec)
+    assert trace.infeasible_flags is None
+    flags = trace.infeasible
+    assert flags.dtype == torch.int32 and flags.device.type == dev.type and tuple(flags.shape) == (w.batch,)
+    assert int(flags.abs().sum()) == 0
+    assert trace.infeasible is flags
