@@ -529,19 +529,20 @@ __device__ __forceinline__ float relax_element(const ConvRelax& rx, bool lower, 
 // Weights of every class of conv_t_hwc_kernel in the quad order of ws_index, zero-padded in
 // k and channels: a float4 copy of the packed layout when the caller keeps one
 // (conv_t_hwc_pack_kernel), else gathered from the OIHW tensor.
+template <int NT>
 __device__ __forceinline__ void hwc_stage_weights(const GatherArgs& g, float* Ws, int tid) {
   const int hq = g.Cm >> 4;
   const int kstride = g.Kc4 * g.npad;
   const int wtotal = g.nclasses * kstride;
   if (g.wpack) {
-    for (int i4 = tid; i4 < wtotal / 4; i4 += GTM)
+    for (int i4 = tid; i4 < wtotal / 4; i4 += NT)
       reinterpret_cast<float4*>(Ws)[i4] = reinterpret_cast<const float4*>(g.wpack)[i4];
   }
-  for (int base = 0; base < wtotal && !g.wpack; base += 8 * GTM) {
+  for (int base = 0; base < wtotal && !g.wpack; base += 8 * NT) {
     float wv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int idx = base + u * GTM + tid;
+      const int idx = base + u * NT + tid;
       const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
       const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
       const bool ok = idx < wtotal && k < g.Kc && n < g.nch;
@@ -557,7 +558,7 @@ __device__ __forceinline__ void hwc_stage_weights(const GatherArgs& g, float* Ws
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int idx = base + u * GTM + tid;
+      const int idx = base + u * NT + tid;
       if (idx < wtotal) {
         const int c = fdivq(idx, g.f_kstride), rem = idx - c * kstride;
         const int k = fdivq(rem, g.f_npad), n = rem - k * g.npad;
@@ -626,6 +627,56 @@ __device__ __forceinline__ void hwc_row_tasks(const GatherArgs& g, const float* 
   }
 }
 
+// The relaxation entry of element e of domain d for the channel-last staging: the four
+// planes, or the slopes from the pre-activation box (and lower-slope override) as
+// bf_crown_relu_relax_lu computes them; ad the lower bound's split term.
+template <bool RELAX>
+__device__ __forceinline__ void hwc_relax_operands(const ConvRelax& rx, bool lower, int nin, int64_t d, int e,
+                                                   float4& t, float& ad) {
+  t = make_float4(1.f, 0.f, 1.f, 0.f);
+  ad = 0.f;
+  if constexpr (RELAX) {
+    if (rx.pl[0]) {
+      const int64_t i = d * nin + e;
+      t = make_float4(rx.pl[0][i], rx.pl[1][i], rx.pl[2][i], rx.pl[3][i]);
+    } else if (rx.lo) {
+      const float lo = rx.lo[d * nin + e], hi = rx.hi[d * nin + e];
+      const bool has_alpha = rx.alpha != nullptr;
+      const float al = has_alpha ? rx.alpha[d * rx.alpha_ld + e] : 0.f;
+      const Relax rr = relu_relax(lo, hi, has_alpha, has_alpha ? clamp01(al) : 0.f);
+      t = make_float4(rr.au, rr.bu, rr.al, rr.bl);
+    }
+    if (rx.add && lower) ad = rx.add[d * rx.add_ld + e];
+  }
+}
+
+// One element e (CHW order) of coefficient row r relaxed (RELAX; t = {alpha_u, beta_u,
+// alpha_l, beta_l}) into the channel-last map Mp, its bias terms added to sb and sk.
+template <bool RELAX>
+__device__ __forceinline__ void hwc_stage_element(const GatherArgs& g, const ConvRelax& rx, bool lower, int z,
+                                                  float* Mp, int CP, int HWm, FastDiv f_hw, FastDiv f_w, int nin,
+                                                  int64_t r, int e, float v, float4 t, float ad, float& sb,
+                                                  float& sk) {
+  const int co = fdivq(e, f_hw), rem = e - co * HWm;
+  const int yy = fdivq(rem, f_w), xx = rem - yy * g.Wm;
+  if constexpr (RELAX) {
+    const bool nn = v >= 0.f;
+    float o;
+    if (lower) {
+      o = v * (nn ? t.z : t.x);
+      sb += v * (nn ? t.w : t.y);
+      if (rx.add) o = o + ad;
+    } else {
+      o = v * (nn ? t.x : t.z);
+      sb += v * (nn ? t.y : t.w);
+    }
+    if (rx.kbias) sk += o * rx.kbias[e];
+    if (rx.relaxed[z]) rx.relaxed[z][r * nin + e] = o;
+    v = o;
+  }
+  Mp[((yy + g.pad_h) * g.Wp + xx + g.pad_w) * CP + co] = v;
+}
+
 template <bool RELAX>
 __global__ void __launch_bounds__(GTM)
 conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
@@ -643,7 +694,7 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
   float* __restrict__ nrm = g.nrm[z];
   const int CP = g.Cm + 4;
 
-  hwc_stage_weights(g, Ws, tid);
+  hwc_stage_weights<GTM>(g, Ws, tid);
   // zero halo (and channel padding): interior positions are rewritten per row, the rest stays zero
   const int mtotal = g.Hp * g.Wp * CP;
   for (int i = tid; i < mtotal; i += GTM) Mp[i] = 0.f;
@@ -653,26 +704,8 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
   const FastDiv f_hw = g.f_HWm;
   const FastDiv f_w = g.f_Wm;
 
-  // One element of a row: relax it (RELAX; t = {alpha_u, beta_u, alpha_l, beta_l}) into the channel-last map.
   auto stage = [&](int64_t r, int64_t d, int e, float v, float4 t, float ad, float& sb, float& sk) {
-    const int co = fdivq(e, f_hw), rem = e - co * HWm;
-    const int yy = fdivq(rem, f_w), xx = rem - yy * g.Wm;
-    if constexpr (RELAX) {
-      const bool nn = v >= 0.f;
-      float o;
-      if (lower) {
-        o = v * (nn ? t.z : t.x);
-        sb += v * (nn ? t.w : t.y);
-        if (rx.add) o = o + ad;
-      } else {
-        o = v * (nn ? t.x : t.z);
-        sb += v * (nn ? t.y : t.w);
-      }
-      if (rx.kbias) sk += o * rx.kbias[e];
-      if (rx.relaxed[z]) rx.relaxed[z][r * nin + e] = o;
-      v = o;
-    }
-    Mp[((yy + g.pad_h) * g.Wp + xx + g.pad_w) * CP + co] = v;
+    hwc_stage_element<RELAX>(g, rx, lower, z, Mp, CP, HWm, f_hw, f_w, nin, r, e, v, t, ad, sb, sk);
   };
   // The coefficients of rows of at most PF * GTM elements are fetched one row ahead,
   // into registers, so that their loads overlap the MFMAs of the row before (the
@@ -687,24 +720,8 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
       pa[u] = e < nin ? X[r * nin + e] : 0.f;
     }
   };
-  // The relaxation entry of element e of domain d: the four planes, or the slopes from
-  // the pre-activation box (and lower-slope override) as bf_crown_relu_relax_lu computes them.
   auto relax_operands = [&](int64_t d, int e, float4& t, float& ad) {
-    t = make_float4(1.f, 0.f, 1.f, 0.f);
-    ad = 0.f;
-    if constexpr (RELAX) {
-      if (rx.pl[0]) {
-        const int64_t i = d * nin + e;
-        t = make_float4(rx.pl[0][i], rx.pl[1][i], rx.pl[2][i], rx.pl[3][i]);
-      } else if (rx.lo) {
-        const float lo = rx.lo[d * nin + e], hi = rx.hi[d * nin + e];
-        const bool has_alpha = rx.alpha != nullptr;
-        const float al = has_alpha ? rx.alpha[d * rx.alpha_ld + e] : 0.f;
-        const Relax rr = relu_relax(lo, hi, has_alpha, has_alpha ? clamp01(al) : 0.f);
-        t = make_float4(rr.au, rr.bu, rr.al, rr.bl);
-      }
-      if (rx.add && lower) ad = rx.add[d * rx.add_ld + e];
-    }
+    hwc_relax_operands<RELAX>(rx, lower, nin, d, e, t, ad);
   };
   const int64_t r_first = (int64_t)blockIdx.x * g.rows_per_wg;
   if (pf && r_first < g.R) fetch(r_first);
@@ -770,6 +787,7 @@ conv_t_hwc_kernel(GatherArgs g, ConvRelax rx) {
     }
   }
 }
+
 
 // The weights of conv_t_hwc_kernel in its LDS order (ws_index over classes, output
 // channels and the quad-ordered reduction index), zero-padded: what each workgroup
@@ -1288,6 +1306,7 @@ static bool small_fast_disabled_from_env() {
   return v != nullptr && std::strcmp(v, "generic") == 0;
 }
 static const bool kSmallFastDisabled = small_fast_disabled_from_env();
+
 
 static int gather_rows_per_wg(int64_t work);
 
