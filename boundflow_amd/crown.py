@@ -17,7 +17,10 @@ but every numeric step runs in the HIP library on the caller's stream:
 * the CROWN backward as one fused kernel per Affine->ReLU region
   (``bf_crown_relu_linear_fwd``: ReLU relaxation in the A-tile prologue, fp32
   MFMA contraction, bias reductions), and the input layer fused with the
-  Linf/box concretization (``bf_crown_relu_linear_concretize``).
+  Linf/box concretization (``bf_crown_relu_linear_concretize``); large queries
+  relax each coefficient in the epilogue of the contraction that makes it
+  (``bf_crown_relu_linear_relu_fwd``), and queries of few rows relax it in a pass
+  of its own (``bf_crown_relu_relax_lu``) ahead of a plain contraction.
 
 Tensors live on the HIP device; nothing is copied to the host except the
 feasibility flags when the caller asked for the reference's raise-on-infeasible

@@ -1577,10 +1577,8 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   BF_REQUIRE(B >= 0 && K > 0 && N > 0 && input_kind >= 0 && input_kind <= 3, "bf_ibp_linear: bad sizes or input kind");
   if (B == 0) return BF_OK;
   BF_REQUIRE(in_lo && W && out_lo && out_hi && workspace, "bf_ibp_linear: null pointer");
-  // workspace: mid [B*K], rad [B*K], c [B*N], r [B*N], rownorm [N], split-K partials
-  float* mid = workspace;
-  float* rad = mid + B * K;
-  float* c = rad + B * K;
+  // workspace: c [B*N], r [B*N], rownorm [N], split-K partials
+  float* c = workspace;
   float* r = c + B * N;
   float* rownorm = r + B * N;
   float* part = rownorm + N;
@@ -1598,8 +1596,6 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   }
   BF_REQUIRE(in_hi, "bf_ibp_linear: interval input needs in_hi");
   // the center and radius (of the ReLU when apply_relu) made as the products load their tiles
-  (void)mid;
-  (void)rad;
   rc = ibp_products(in_lo, in_lo, W, B, K, N, cdst, r, part, &ks, stream, in_hi, apply_relu);
   if (rc) return rc;
   return ibp_finalize_parts(cdst, r, ks > 1 ? part : nullptr, ks, 1, center_out, nullptr, 0.f, bias, 1, split,
@@ -1609,7 +1605,7 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
 int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N) {
   int64_t kchunk;
   const int ks = gemm_ksplit(B, N, K, &kchunk);
-  return 2 * B * K + 2 * B * N + N + (ks > 1 ? 2 * (int64_t)ks * B * N : 0);
+  return 2 * B * N + N + (ks > 1 ? 2 * (int64_t)ks * B * N : 0);
 }
 
 int bf_interval_center_radius(const float* lo, const float* hi, int64_t n, int apply_relu, float* mid, float* rad,

@@ -2,6 +2,7 @@
 maps and gradient seeds kept across queries): a hit needs the same source tensor
 objects at the same versions; an in-place change or a new tensor recomputes."""
 
+import pytest
 import torch
 
 from boundflow_amd import crown
@@ -72,14 +73,20 @@ def test_call_memo_is_per_call():
     assert len(calls) == 3
 
 
+@pytest.mark.gpu
 def test_box_radius_is_not_cached():
     """The input box radius depends on the query: an in-place change of the box
-    is seen by the next query (and by a graph replay, which recomputes it)."""
+    is seen by the next query (and by a graph replay, which recomputes it).  The
+    radius is one library launch, so this runs on the HIP device."""
     from boundflow_amd.spec import BoxPerturbation
-    lo = torch.zeros(2, 3)
-    hi = torch.ones(2, 3)
+    from tests.gpu_util import device
+    dev = device()
+    lo = torch.zeros(2, 3, device=dev)
+    hi = torch.ones(2, 3, device=dev)
     pert = BoxPerturbation(lower=lo, upper=hi)
     r1, e1 = crown._input_radius(pert, 2, 3)
-    pert.upper.copy_(torch.full((2, 3), 3.0))   # the perturbation holds its own copy of the box
+    r1 = r1.clone()
+    pert.upper.copy_(torch.full((2, 3), 3.0, device=dev))   # the perturbation holds its own copy of the box
     r2, _ = crown._input_radius(pert, 2, 3)
-    assert e1 == 1.0 and torch.equal(r1, torch.full((2, 3), 0.5)) and torch.equal(r2, torch.full((2, 3), 1.5))
+    assert e1 == 1.0
+    assert torch.equal(r1.cpu(), torch.full((2, 3), 0.5)) and torch.equal(r2.cpu(), torch.full((2, 3), 1.5))
