@@ -346,7 +346,7 @@ def run_alpha_beta_crown_mlp(
                                    infeasible_certificate=_certificate_record(value)))
     if trace is None:
         trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
-                                  raise_on_infeasible=raise_on_infeasible)
+                                  raise_on_infeasible=raise_on_infeasible, relu_inputs_only=True)
     bound, grad, out_dim = _evaluator(module, spec, trace, chain, linear_spec_C)
     dev = spec.center.device
     B = int(spec.center.shape[0])
@@ -633,7 +633,7 @@ def run_alpha_crown_from_crown_init(module, input_spec, *, linear_spec_C=None, s
     """Config C4: per-domain alpha initialised from the CROWN relaxation
     (alpha_from_crown), then ``steps`` Adam steps on the lower bound."""
     spec = normalize_input_spec(input_spec)
-    trace = forward_ibp_trace(module, spec, chain=_chain_or_none(module, spec))
+    trace = forward_ibp_trace(module, spec, chain=_chain_or_none(module, spec), relu_inputs_only=True)
     init = alpha_from_crown(trace)
     return run_alpha_beta_crown_mlp(module, spec, linear_spec_C=linear_spec_C, steps=steps, lr=lr,
                                     warm_start_alpha=init, per_batch_params=True, trace=trace, record=record)
@@ -646,7 +646,7 @@ def lower_bound_gradients(module, input_spec, *, linear_spec_C, relu_alpha: Dict
     for L = -sum_d mean_s lb (per-domain parameters) or -mean lb (shared)."""
     spec = normalize_input_spec(input_spec)
     chain = _chain_or_none(module, spec)
-    trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain)
+    trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain, relu_inputs_only=True)
     bound, grad, _out_dim = _evaluator(module, spec, trace, chain, linear_spec_C)
     dev = spec.center.device
     B = int(spec.center.shape[0])

@@ -41,7 +41,7 @@ def evaluate_domain_batch(module, input_spec, *, linear_spec_C: torch.Tensor,
     spec = normalize_input_spec(input_spec)
     chain, _shapes, _has_conv = _relu_layout(module, spec)
     trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain,
-                              raise_on_infeasible=False)
+                              raise_on_infeasible=False, relu_inputs_only=True)
     D = int(spec.center.shape[0])
     layer, neuron, _gap = branch_tensors(trace, D)
     bounds, alpha, beta, _stats = run_alpha_beta_crown_mlp(
@@ -375,7 +375,8 @@ def _evaluate_nodes(module, spec, chain, shapes, linear_spec_C, items, front: _F
     prune = ab and b > 1 and bool(cfg.enable_batch_infeasible_prune)
     # the certificate where its verdict is known to be needed (a lone node, or pre-pruning)
     cert = split_certificate(module, sub, split_by, shapes) if ab and (b == 1 or prune) else None
-    trace = forward_ibp_trace(module, sub, relu_split_state=split_by, chain=chain, raise_on_infeasible=False)
+    trace = forward_ibp_trace(module, sub, relu_split_state=split_by, chain=chain, raise_on_infeasible=False,
+                              relu_inputs_only=True)
     layer, neuron, _gap = branch_tensors(trace, b)
     if ab:
         bounds, alpha, beta, _stats = run_alpha_beta_crown_mlp(
@@ -615,7 +616,7 @@ def run_native_relu_split_bab(module, input_spec, *, linear_spec_C: torch.Tensor
             split_by = {n: front.split[n][sl].reshape((k,) + tuple(relu_shapes[n])) for n in names}
             rep = (k,) + (1,) * (lo0.dim() - 1)
             bspec = InputSpec.box(value_name=spec.value_name, lower=lo0.repeat(rep), upper=hi0.repeat(rep))
-            trace = forward_ibp_trace(module, bspec, relu_split_state=split_by, chain=chain)
+            trace = forward_ibp_trace(module, bspec, relu_split_state=split_by, chain=chain, relu_inputs_only=True)
             alpha = {}
             for n, pre in trace.relu_pre.items():
                 a = torch.empty_like(pre.lower)

@@ -319,7 +319,13 @@ def forward_ibp_trace(
     relu_pre_constraints: Optional[Mapping[str, IntervalState]] = None,
     raise_on_infeasible: bool = True,
     chain: Optional[Chain] = None,
+    relu_inputs_only: bool = False,
 ) -> ForwardTrace:
+    """IBP through the chain (crown_ibp.py:101-342).  relu_inputs_only: stop at the
+    last layer whose output feeds a ReLU (at least the first layer, whose center
+    projection the input region reads); the layers after it get no interval.  A CROWN
+    query reads nothing else of the trace: of the output's interval the reference's
+    backward reads only its shape (crown_ibp.py:650-669)."""
     spec = normalize_input_spec(input_spec)
     if chain is None:
         try:
@@ -344,7 +350,11 @@ def forward_ibp_trace(
     pert = spec.perturbation
     norm_p = input_norm_p(pert)
     prev_lo = prev_hi = None
-    for li, layer in enumerate(chain.layers):
+    n_layers = len(chain.layers)
+    if relu_inputs_only:
+        feeding = [i for i, layer in enumerate(chain.layers) if layer.out_name in relu_set]
+        n_layers = (feeding[-1] if feeding else 0) + 1
+    for li, layer in enumerate(chain.layers[:n_layers]):
         split = None
         split_ld = 0
         out_numel = _numel(layer.out_shape)
@@ -806,7 +816,8 @@ def run_crown_ibp_mlp(
                                                     output_value=output_value, relu_alpha=relu_alpha,
                                                     relu_pre_add_coeff_u=relu_pre_add_coeff_u,
                                                     relu_pre_add_coeff_l=relu_pre_add_coeff_l)
-    trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain_full)
+    trace = forward_ibp_trace(module, spec, relu_split_state=relu_split_state, chain=chain_full,
+                              relu_inputs_only=True)
     chain = parse_chain(module, spec, output_value) if output_value is not None else chain_full
 
     def backward(C, add_l, need_upper, need_lower):
@@ -941,7 +952,7 @@ def run_crown_all_intermediate(module: BFTaskModule, input_spec, *, linear_spec_
     native_intermediate_refinement.py:923-988 applied to every ReLU after the first."""
     spec = normalize_input_spec(input_spec)
     chain_full = parse_chain(module, spec)
-    trace = forward_ibp_trace(module, spec, chain=chain_full)
+    trace = forward_ibp_trace(module, spec, chain=chain_full, relu_inputs_only=True)
     names = list(trace.relu_pre.keys())
     stream = _lib.stream_handle()
     B = int(spec.center.shape[0])
