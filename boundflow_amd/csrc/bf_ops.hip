@@ -153,6 +153,177 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
   hi[i] = u;
 }
 
+// IBP of a linear layer whose output has few 16 x 16 tiles (a small batch), in one
+// launch: workgroup t owns output tile t (16 rows of the batch x 16 output neurons) and
+// takes the whole reduction for both products -- the center Xc . W^T and the radius
+// Xr . |W|^T of an interval input (center and radius made from [lo, hi] as they are
+// loaded, of the ReLU when relu, with the arithmetic of ibp_center_radius_kernel), or the
+// center and eps times the row norm of W (norm code nk as row_norm_kernel) of a ball --
+// its 16 waves taking the 16-wide steps of k in turn (wave w: steps w, w + 16, ...; the
+// loads of four steps issued together).  The waves' partial tiles are added in LDS in
+// wave order and the workgroup applies ibp_finalize_kernel's arithmetic, so no partial
+// buffer and no second launch is needed.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int ISM_WAVES = 16;
+constexpr int ISM_GROUP = 4;
+constexpr int64_t ISM_MAX_TILES = 1024;
+
+__device__ __forceinline__ float4 ism_load4(const float* __restrict__ p, int64_t k, int64_t K, bool ok, bool vec) {
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!ok) return v;
+  if (vec) {
+    if (k < K) v = *reinterpret_cast<const float4*>(p + k);   // K % 4 == 0: a quad is whole or past K
+  } else {
+    if (k + 0 < K) v.x = p[k + 0];
+    if (k + 1 < K) v.y = p[k + 1];
+    if (k + 2 < K) v.z = p[k + 2];
+    if (k + 3 < K) v.w = p[k + 3];
+  }
+  return v;
+}
+
+__device__ __forceinline__ float ism_center(float l, float u, bool relu) {
+  if (relu) {
+    l = fmaxf(l, 0.f);
+    u = fmaxf(u, 0.f);
+  }
+  return (l + u) / 2.0f;
+}
+__device__ __forceinline__ float ism_radius(float l, float u, bool relu) {
+  if (relu) {
+    l = fmaxf(l, 0.f);
+    u = fmaxf(u, 0.f);
+  }
+  return (u - l) / 2.0f;
+}
+__device__ __forceinline__ float ism_norm_step(float s, float w, int nk) {
+  return nk == 1 ? fmaxf(s, fabsf(w)) : (nk == 2 ? s + w * w : s + fabsf(w));
+}
+
+template <bool BALL>
+__global__ void __launch_bounds__(64 * ISM_WAVES)
+ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int relu, int nk, float eps,
+                        const float* __restrict__ W, const float* __restrict__ bias, int64_t B, int64_t K, int64_t N,
+                        int vec, const int8_t* __restrict__ split, int64_t split_ld, float* __restrict__ out_lo,
+                        float* __restrict__ out_hi, float* __restrict__ c_out, int* __restrict__ infeasible) {
+  __shared__ float red_c[ISM_WAVES][256];
+  __shared__ float red_r[BALL ? 1 : ISM_WAVES][256];
+  __shared__ float red_n[BALL ? ISM_WAVES : 1][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t ntn = (N + 15) / 16;
+  const int64_t b0 = (int64_t)(blockIdx.x / ntn) * 16, n0 = (int64_t)(blockIdx.x % ntn) * 16;
+  // MFMA lanes: i = lane & 15 is the batch row of the A operand and the neuron of the B
+  // operand, g = lane >> 4 the k slot; a lane's float4 at k = 16 s + 4 g holds the four
+  // k of its slot for the four MFMAs of step s
+  const int i = lane & 15, g = lane >> 4;
+  const bool bok = b0 + i < B, nok = n0 + i < N;
+  const bool rl = relu != 0, vc = vec != 0;
+  const float* __restrict__ xl = lo + (bok ? b0 + i : 0) * K;
+  const float* __restrict__ xh = BALL ? lo : hi + (bok ? b0 + i : 0) * K;
+  const float* __restrict__ wr = W + (nok ? n0 + i : 0) * K;
+  floatx4 acc_c = {0.f, 0.f, 0.f, 0.f};
+  floatx4 acc_r = {0.f, 0.f, 0.f, 0.f};
+  float nrm = 0.f;
+  const int64_t nsteps = (K + 15) / 16;
+  for (int64_t s0 = wave; s0 < nsteps; s0 += (int64_t)ISM_WAVES * ISM_GROUP) {
+    float4 al[ISM_GROUP], ah[ISM_GROUP], w4[ISM_GROUP];
+#pragma unroll
+    for (int q = 0; q < ISM_GROUP; ++q) {
+      const int64_t s = s0 + (int64_t)q * ISM_WAVES;
+      const int64_t k = s * 16 + 4 * g;
+      const bool sok = s < nsteps;
+      al[q] = ism_load4(xl, k, K, bok && sok, vc);
+      if (!BALL) ah[q] = ism_load4(xh, k, K, bok && sok, vc);
+      w4[q] = ism_load4(wr, k, K, nok && sok, vc);
+    }
+#pragma unroll
+    for (int q = 0; q < ISM_GROUP; ++q) {
+      if constexpr (BALL) {
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].x, w4[q].x, acc_c, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].y, w4[q].y, acc_c, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].z, w4[q].z, acc_c, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].w, w4[q].w, acc_c, 0, 0, 0);
+        nrm = ism_norm_step(nrm, w4[q].x, nk);
+        nrm = ism_norm_step(nrm, w4[q].y, nk);
+        nrm = ism_norm_step(nrm, w4[q].z, nk);
+        nrm = ism_norm_step(nrm, w4[q].w, nk);
+      } else {
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_center(al[q].x, ah[q].x, rl), w4[q].x, acc_c, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_center(al[q].y, ah[q].y, rl), w4[q].y, acc_c, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_center(al[q].z, ah[q].z, rl), w4[q].z, acc_c, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_center(al[q].w, ah[q].w, rl), w4[q].w, acc_c, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_radius(al[q].x, ah[q].x, rl), fabsf(w4[q].x), acc_r, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_radius(al[q].y, ah[q].y, rl), fabsf(w4[q].y), acc_r, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_radius(al[q].z, ah[q].z, rl), fabsf(w4[q].z), acc_r, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_radius(al[q].w, ah[q].w, rl), fabsf(w4[q].w), acc_r, 0, 0, 0);
+      }
+    }
+  }
+  // lane's acc[r] is tile element (row 4 g + r, neuron i)
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    red_c[wave][(4 * g + r) * 16 + i] = acc_c[r];
+    if constexpr (!BALL) red_r[wave][(4 * g + r) * 16 + i] = acc_r[r];
+  }
+  if constexpr (BALL) red_n[wave][lane] = nrm;
+  __syncthreads();
+  if (tid >= 256) return;
+  const int mr = tid >> 4, nc = tid & 15;
+  const int64_t b = b0 + mr, n = n0 + nc;
+  float cv = red_c[0][tid], dev;
+  for (int w = 1; w < ISM_WAVES; ++w) cv += red_c[w][tid];
+  if constexpr (BALL) {
+    float s = 0.f;
+    for (int w = 0; w < ISM_WAVES; ++w)
+      for (int q = 0; q < 4; ++q) {
+        const float v = red_n[w][16 * q + nc];
+        s = nk == 1 ? fmaxf(s, v) : s + v;
+      }
+    dev = eps * (nk == 2 ? sqrtf(s) : s);
+  } else {
+    dev = red_r[0][tid];
+    for (int w = 1; w < ISM_WAVES; ++w) dev += red_r[w][tid];
+  }
+  if (b >= B || n >= N) return;
+  float l = cv - dev;
+  float u = cv + dev;
+  if (bias) {
+    l = l + bias[n];
+    u = u + bias[n];
+  }
+  if (split) {
+    const int8_t sp = split[b * split_ld + n];
+    if (sp > 0) l = fmaxf(l, 0.f);
+    if (sp < 0) u = fminf(u, 0.f);
+    if (l > u && infeasible) infeasible[b] = 1;
+  }
+  const int64_t o = b * N + n;
+  out_lo[o] = l;
+  out_hi[o] = u;
+  if (c_out) c_out[o] = cv;
+}
+
+// True when ibp_linear_small_kernel takes a B x N output.
+bool ibp_linear_small_route(int64_t B, int64_t N) { return ceil_div(B, 16) * ceil_div(N, 16) <= ISM_MAX_TILES; }
+
+int ibp_linear_small(const float* lo, const float* hi, int relu, int nk, float eps, const float* W, const float* bias,
+                     int64_t B, int64_t K, int64_t N, const int8_t* split, int64_t split_ld, float* out_lo,
+                     float* out_hi, float* c_out, int* infeasible, hipStream_t stream) {
+  const unsigned tiles = (unsigned)(ceil_div(B, 16) * ceil_div(N, 16));
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const int vec = (K % 4 == 0) && al16(lo) && al16(hi) && al16(W) ? 1 : 0;
+  if (hi) {
+    hipLaunchKernelGGL(ibp_linear_small_kernel<false>, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, lo, hi, relu, nk,
+                       eps, W, bias, B, K, N, vec, split, split_ld, out_lo, out_hi, c_out, infeasible);
+  } else {
+    hipLaunchKernelGGL(ibp_linear_small_kernel<true>, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, lo, hi, relu, nk,
+                       eps, W, bias, B, K, N, vec, split, split_ld, out_lo, out_hi, c_out, infeasible);
+  }
+  BF_LAUNCH_CHECK("ibp_linear_small_kernel");
+  return BF_OK;
+}
+
 // The relaxation table {alpha_u, beta_u, alpha_l, beta_l} from the four separate tensors
 // of a FusedReluAffineRequest: one 16-byte store per entry.
 __global__ void planes_table_kernel(const float* __restrict__ au, const float* __restrict__ bu,
@@ -1585,6 +1756,13 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   float* cdst = center_out ? center_out : c;
   int rc;
   int ks = 1;
+  BF_REQUIRE(input_kind >= 1 || in_hi, "bf_ibp_linear: interval input needs in_hi");
+  if (ibp_linear_small_route(B, N)) {
+    // a small output: products and finalize in one launch (row norm code as row_norm_kernel)
+    const int nk = input_kind == 1 ? 0 : (input_kind == 2 ? 2 : 1);
+    return ibp_linear_small(in_lo, input_kind >= 1 ? nullptr : in_hi, apply_relu, nk, eps, W, bias, B, K, N, split,
+                            split_ld, out_lo, out_hi, center_out, infeasible, stream);
+  }
   if (input_kind >= 1) {
     rc = ibp_products(in_lo, nullptr, W, B, K, N, cdst, nullptr, part, &ks, stream);
     if (rc) return rc;
