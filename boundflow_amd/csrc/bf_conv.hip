@@ -467,6 +467,195 @@ conv_mfma_kernel(GatherArgs g) {
   }
 }
 
+// IBP of a conv layer in one launch: the forward gather-GEMM above with both products of
+// the center/radius form taken together -- the row's center map and radius map staged
+// side by side from the input set (IVL_BOX [| IVL_RELU] from lo / hi, or IVL_BALL from the
+// center and eps, the arithmetic of conv_mfma_kernel<MODE_F>'s staging), each task running
+// a center accumulator with W and a radius accumulator with |W| -- and the finalize of
+// ibp_finalize_kernel applied to the two accumulators in registers:
+//   lo = (c - r) + bias[ch],  hi = (c + r) + bias[ch],  then the consumer's split and the
+//   infeasibility flag (crown_ibp.py:70-98); c to c_out when asked (the center projection).
+// blockIdx.y halves a row's tasks: with an even number of 16-channel blocks, half y takes
+// blocks [y nblk / 2, (y + 1) nblk / 2) and stages only their weights (CB_SPLIT); otherwise
+// it takes the pixel tiles of parity y.
+struct IbpConvOut {
+  const float* bias;    // [nch] or null
+  const int8_t* split;  // [R, nout] (split_ld) or null
+  int64_t split_ld;
+  float* lo;            // [R, nout]
+  float* hi;
+  float* c_out;         // [R, nout] or null
+  int* infeasible;      // [R] or null
+};
+
+template <bool CB_SPLIT>
+__global__ void __launch_bounds__(GTM)
+conv_ibp_kernel(GatherArgs g, IbpConvOut o) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int half = blockIdx.y;
+  const int nbl = CB_SPLIT ? g.nblk / 2 : g.nblk;   // channel blocks staged here
+  const int cb0 = CB_SPLIT ? half * nbl : 0;
+  const int nloc = nbl * 16;
+  float* Ws = smem;                                                    // [Kc4][nloc] in ws order (nblk = nbl)
+  int* koff = reinterpret_cast<int*>(Ws + (size_t)g.Kc4 * nloc);      // [Kc4]
+  const int map = g.Cm * g.Hp * g.Wp;
+  float* Mc = reinterpret_cast<float*>(koff + g.Kc4);                 // center map [Cm][Hp][Wp]
+  float* Mr = Mc + map;                                                // radius map
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kq = g.Kc4 >> 4;
+  auto ws_at = [&](int n, int k) {   // ws_index with nbl blocks
+    const int cb = n >> 4, col = n & 15, j = k & 3, s = k >> 2, sq = s >> 2, e = s & 3;
+    return (((cb * 4 + j) * kq + sq) * 16 + col) * 4 + e;
+  };
+  // weights of this half's channels in the source order (k fastest: consecutive floats of
+  // one output channel's row), eight loads per thread in flight, scattered into the LDS order
+  const int wtotal = g.Kc4 * nloc;
+  for (int base = 0; base < wtotal; base += 8 * GTM) {
+    float wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * GTM + tid;
+      const int n = fdivq(idx, g.f_Kc4), k = idx - n * g.Kc4;
+      const int ch = 16 * cb0 + n;
+      const bool ok = idx < wtotal && k < g.Kc && ch < g.nch;
+      const float w = g.W[ok ? (int64_t)ch * g.Kc + k : 0];
+      wv[u] = ok ? w : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * GTM + tid;
+      if (idx < wtotal) {
+        const int n = fdivq(idx, g.f_Kc4), k = idx - n * g.Kc4;
+        Ws[ws_at(n, k)] = wv[u];
+      }
+    }
+  }
+  for (int k = tid; k < g.Kc4; k += GTM) {
+    int off = 0;
+    if (k < g.Kc) {
+      const int ci = fdivq(k, g.f_KHKW), t = k - ci * g.KH * g.KW;
+      const int kh = fdivq(t, g.f_KW), kw = t - kh * g.KW;
+      off = (ci * g.Hp + kh) * g.Wp + kw;
+    }
+    koff[koff_index(g, k)] = off;
+  }
+
+  const int nin = g.Cm * g.Hm * g.Wm;
+  const int64_t nout = (int64_t)g.nch * g.HWout;
+  const int j = lane >> 4;
+  const int col = lane & 15;
+  const GatherClass& C = g.cls[0];
+  const int npt = (C.np + 15) / 16;
+  // tasks of this half: (pixel tile, local channel block)
+  const int ntl = CB_SPLIT ? npt * nbl : ((npt - half + 1) / 2) * g.nblk;
+  const bool box = (g.ivl & IVL_BOX) != 0, relu = (g.ivl & IVL_RELU) != 0;
+
+  for (int i = 0; i < g.rows_per_wg; ++i) {
+    const int64_t r = (int64_t)blockIdx.x * g.rows_per_wg + i;
+    if (r >= g.R) break;   // uniform
+    __syncthreads();       // weights staged / the previous row's maps consumed
+    const float* __restrict__ xr = g.X[0] + r * nin;
+    const float* __restrict__ hr_row = box ? g.ivl_hi + r * nin : nullptr;
+    for (int base = 0; base < map; base += 8 * GTM) {
+      float cv[8], rv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int idx = base + u * GTM + tid;
+        const int c = fdivq(idx, g.f_HpWp), rem = idx - c * g.Hp * g.Wp;
+        const int hr = fdivq(rem, g.f_Wp);
+        const int hm = hr - g.pad_h, wm = (rem - hr * g.Wp) - g.pad_w;
+        const bool ok = idx < map && hm >= 0 && hm < g.Hm && wm >= 0 && wm < g.Wm;
+        const int src = ok ? (c * g.Hm + hm) * g.Wm + wm : 0;
+        float cx, rx;
+        if (box) {
+          float l = xr[src], h = hr_row[src];
+          if (relu) {
+            l = fmaxf(l, 0.f);
+            h = fmaxf(h, 0.f);
+          }
+          cx = (l + h) / 2.0f;
+          rx = (h - l) / 2.0f;
+        } else {
+          cx = xr[src];
+          rx = g.ivl_eps;
+        }
+        cv[u] = ok ? cx : 0.f;
+        rv[u] = ok ? rx : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int idx = base + u * GTM + tid;
+        if (idx < map) {
+          Mc[idx] = cv[u];
+          Mr[idx] = rv[u];
+        }
+      }
+    }
+    __syncthreads();
+    for (int tl = wave; tl < ntl; tl += GTM / 64) {
+      int pt, cbl;
+      if (CB_SPLIT) {
+        pt = tl / nbl;
+        cbl = tl - pt * nbl;
+      } else {
+        const int q = tl / g.nblk;
+        cbl = tl - q * g.nblk;
+        pt = 2 * q + half;
+      }
+      const int p = pt * 16 + col;
+      const bool pok = p < C.np;
+      const int pc = pok ? p : C.np - 1;
+      const int q1 = pc / C.n2, q2 = pc - q1 * C.n2;
+      const int moff = C.poff0 + q1 * C.s1 + q2 * C.s2;
+      const float* __restrict__ mc = Mc + moff;
+      const float* __restrict__ mr = Mr + moff;
+      const float* __restrict__ wl = Ws + ws_at(cbl * 16 + col, j);
+      const int* __restrict__ kl = koff + koff_index(g, j);
+      floatx4 acc_c = {0.f, 0.f, 0.f, 0.f};
+      floatx4 acc_r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+      for (int sq = 0; sq < kq; ++sq) {
+        const float4 w4 = *reinterpret_cast<const float4*>(wl + sq * 64);
+        const int4 o4 = *reinterpret_cast<const int4*>(kl + sq * 4);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.x, mc[o4.x], acc_c, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(fabsf(w4.x), mr[o4.x], acc_r, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.y, mc[o4.y], acc_c, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(fabsf(w4.y), mr[o4.y], acc_r, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.z, mc[o4.z], acc_c, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(fabsf(w4.z), mr[o4.z], acc_r, 0, 0, 0);
+        acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(w4.w, mc[o4.w], acc_c, 0, 0, 0);
+        acc_r = __builtin_amdgcn_mfma_f32_16x16x4f32(fabsf(w4.w), mr[o4.w], acc_r, 0, 0, 0);
+      }
+      const int opix = C.out0 + q1 * C.o1 + q2 * C.o2;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int n = 16 * (cb0 + cbl) + 4 * j + rr;
+        if (n < g.nch && pok) {
+          const float cvv = acc_c[rr], dev = acc_r[rr];
+          const int64_t oidx = (int64_t)n * g.HWout + opix;
+          float l = cvv - dev;
+          float u = cvv + dev;
+          if (o.bias) {
+            l = l + o.bias[n];
+            u = u + o.bias[n];
+          }
+          if (o.split) {
+            const int8_t sp = o.split[r * o.split_ld + oidx];
+            if (sp > 0) l = fmaxf(l, 0.f);
+            if (sp < 0) u = fminf(u, 0.f);
+            if (l > u && o.infeasible) o.infeasible[r] = 1;
+          }
+          o.lo[r * nout + oidx] = l;
+          o.hi[r * nout + oidx] = u;
+          if (o.c_out) o.c_out[r * nout + oidx] = cvv;
+        }
+      }
+    }
+  }
+}
+
 // conv_transpose2d of coefficient rows with the map channel-last in LDS (Co % 16 == 0).
 //
 // The row's map is staged as [Hp][Wp][CP] (channel pitch CP = Co + 4, zero halo
@@ -1961,6 +2150,39 @@ static int conv2d_ivl_launch(const float* lo, const float* hi, int ivl, float ep
   return BF_OK;
 }
 
+// IBP of a conv layer in one launch of conv_ibp_kernel; BF_OK with *planned false, launching
+// nothing, for shapes it does not take (the two maps and this half's weights above 64 KB).
+static int conv_ibp_fused_launch(const float* lo, const float* hi, int ivl, float eps, int64_t R, int Ci, int Hi,
+                                 int Wi, const float* W, int Co, int KH, int KW, int sh, int sw, int ph, int pw,
+                                 int Ho, int Wo, const IbpConvOut& o, bool* planned, hipStream_t stream) {
+  GatherArgs g;
+  memset(&g, 0, sizeof(g));
+  size_t one_map_lds = 0;
+  *planned = false;
+  if (!conv_f_mfma_plan(g, R, Ci, Hi, Wi, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, &one_map_lds)) return BF_OK;
+  const bool cb_split = g.nblk % 2 == 0;
+  const int nloc = (cb_split ? g.nblk / 2 : g.nblk) * 16;
+  const size_t map = (size_t)Ci * g.Hp * g.Wp;
+  const size_t lds = sizeof(float) * ((size_t)g.Kc4 * nloc + g.Kc4 + 2 * map);
+  if (lds > 64 * 1024) return BF_OK;
+  *planned = true;
+  g.X[0] = lo;
+  g.W = W;
+  g.ivl = ivl;
+  g.ivl_hi = hi;
+  g.ivl_eps = eps;
+  g.rows_per_wg = gather_rows_per_wg(R * 2);
+  const int rpw = g.rows_per_wg;
+  BF_REQUIRE((R + rpw - 1) / rpw < (1LL << 31), "conv2d: too many rows");
+  const dim3 grid((unsigned)((R + rpw - 1) / rpw), 2);
+  if (cb_split)
+    hipLaunchKernelGGL(conv_ibp_kernel<true>, grid, dim3(GTM), lds, stream, g, o);
+  else
+    hipLaunchKernelGGL(conv_ibp_kernel<false>, grid, dim3(GTM), lds, stream, g, o);
+  BF_LAUNCH_CHECK("conv_ibp_kernel");
+  return BF_OK;
+}
+
 int bf_ibp_conv2d(const float* in_lo, const float* in_hi, int64_t B, int Ci, int Hi, int Wi, int input_kind,
                   float eps, int apply_relu, const float* W, const float* bias, int Co, int KH, int KW, int sh,
                   int sw, int ph, int pw, int Ho, int Wo, const int8_t* split, int64_t split_ld, float* workspace,
@@ -1978,9 +2200,23 @@ int bf_ibp_conv2d(const float* in_lo, const float* in_hi, int64_t B, int Ci, int
   float* r = c + B * nout;
   float* cdst = center_out ? center_out : c;
   int rc;
+  bool planned = false;
+  if (input_kind == 1 || in_hi) {
+    // both products and the finalize in one launch
+    IbpConvOut o;
+    o.bias = bias;
+    o.split = split;
+    o.split_ld = split_ld;
+    o.lo = out_lo;
+    o.hi = out_hi;
+    o.c_out = center_out;
+    o.infeasible = infeasible;
+    rc = conv_ibp_fused_launch(in_lo, in_hi, input_kind == 1 ? IVL_BALL : (IVL_BOX | (apply_relu ? IVL_RELU : 0)),
+                               eps, B, Ci, Hi, Wi, W, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, o, &planned, stream);
+    if (rc || planned) return rc;
+  }
   // the center (W) and the radius (|W|) products in one launch, the center and radius made
   // from the input set while the gather-GEMM stages each row
-  bool planned = false;
   if (input_kind == 1 || in_hi) {
     rc = conv2d_ivl_launch(in_lo, in_hi, input_kind == 1 ? IVL_BALL : (IVL_BOX | (apply_relu ? IVL_RELU : 0)), eps, B,
                            Ci, Hi, Wi, W, Co, KH, KW, sh, sw, ph, pw, Ho, Wo, cdst, r, &planned, stream);
