@@ -168,18 +168,20 @@ constexpr int ISM_WAVES = 16;
 constexpr int ISM_GROUP = 4;
 constexpr int64_t ISM_MAX_TILES = 1024;
 
-__device__ __forceinline__ float4 ism_load4(const float* __restrict__ p, int64_t k, int64_t K, bool ok, bool vec) {
-  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (!ok) return v;
-  if (vec) {
-    if (k < K) v = *reinterpret_cast<const float4*>(p + k);   // K % 4 == 0: a quad is whole or past K
+// Four k of one row, zero where ok is false or k runs past K.  Branch-free: every load is
+// issued (from a clamped address inside the row) and masked afterwards, so the loads of a
+// group stay in flight together.  VEC: K % 4 == 0 and 16-byte rows (a quad is whole or past K).
+template <bool VEC>
+__device__ __forceinline__ float4 ism_load4(const float* __restrict__ p, int64_t k, int64_t K, bool ok) {
+  if constexpr (VEC) {
+    const bool in = ok && k < K;
+    const float4 v = *reinterpret_cast<const float4*>(p + (in ? k : 0));
+    return in ? v : make_float4(0.f, 0.f, 0.f, 0.f);
   } else {
-    if (k + 0 < K) v.x = p[k + 0];
-    if (k + 1 < K) v.y = p[k + 1];
-    if (k + 2 < K) v.z = p[k + 2];
-    if (k + 3 < K) v.w = p[k + 3];
+    const bool i0 = ok && k < K, i1 = ok && k + 1 < K, i2 = ok && k + 2 < K, i3 = ok && k + 3 < K;
+    const float x0 = p[i0 ? k : 0], x1 = p[i1 ? k + 1 : 0], x2 = p[i2 ? k + 2 : 0], x3 = p[i3 ? k + 3 : 0];
+    return make_float4(i0 ? x0 : 0.f, i1 ? x1 : 0.f, i2 ? x2 : 0.f, i3 ? x3 : 0.f);
   }
-  return v;
 }
 
 __device__ __forceinline__ float ism_center(float l, float u, bool relu) {
@@ -200,11 +202,11 @@ __device__ __forceinline__ float ism_norm_step(float s, float w, int nk) {
   return nk == 1 ? fmaxf(s, fabsf(w)) : (nk == 2 ? s + w * w : s + fabsf(w));
 }
 
-template <bool BALL>
+template <bool BALL, bool VEC>
 __global__ void __launch_bounds__(64 * ISM_WAVES)
 ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int relu, int nk, float eps,
                         const float* __restrict__ W, const float* __restrict__ bias, int64_t B, int64_t K, int64_t N,
-                        int vec, const int8_t* __restrict__ split, int64_t split_ld, float* __restrict__ out_lo,
+                        const int8_t* __restrict__ split, int64_t split_ld, float* __restrict__ out_lo,
                         float* __restrict__ out_hi, float* __restrict__ c_out, int* __restrict__ infeasible) {
   __shared__ float red_c[ISM_WAVES][256];
   __shared__ float red_r[BALL ? 1 : ISM_WAVES][256];
@@ -218,7 +220,7 @@ ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ 
   // k of its slot for the four MFMAs of step s
   const int i = lane & 15, g = lane >> 4;
   const bool bok = b0 + i < B, nok = n0 + i < N;
-  const bool rl = relu != 0, vc = vec != 0;
+  const bool rl = relu != 0;
   const float* __restrict__ xl = lo + (bok ? b0 + i : 0) * K;
   const float* __restrict__ xh = BALL ? lo : hi + (bok ? b0 + i : 0) * K;
   const float* __restrict__ wr = W + (nok ? n0 + i : 0) * K;
@@ -233,9 +235,9 @@ ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ 
       const int64_t s = s0 + (int64_t)q * ISM_WAVES;
       const int64_t k = s * 16 + 4 * g;
       const bool sok = s < nsteps;
-      al[q] = ism_load4(xl, k, K, bok && sok, vc);
-      if (!BALL) ah[q] = ism_load4(xh, k, K, bok && sok, vc);
-      w4[q] = ism_load4(wr, k, K, nok && sok, vc);
+      al[q] = ism_load4<VEC>(xl, k, K, bok && sok);
+      if (!BALL) ah[q] = ism_load4<VEC>(xh, k, K, bok && sok);
+      w4[q] = ism_load4<VEC>(wr, k, K, nok && sok);
     }
 #pragma unroll
     for (int q = 0; q < ISM_GROUP; ++q) {
@@ -312,13 +314,17 @@ int ibp_linear_small(const float* lo, const float* hi, int relu, int nk, float e
                      float* out_hi, float* c_out, int* infeasible, hipStream_t stream) {
   const unsigned tiles = (unsigned)(ceil_div(B, 16) * ceil_div(N, 16));
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  const int vec = (K % 4 == 0) && al16(lo) && al16(hi) && al16(W) ? 1 : 0;
+  const bool vec = (K % 4 == 0) && al16(lo) && al16(hi) && al16(W);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, lo, hi, relu, nk, eps, W, bias, B, K, N,
+                       split, split_ld, out_lo, out_hi, c_out, infeasible);
+  };
   if (hi) {
-    hipLaunchKernelGGL(ibp_linear_small_kernel<false>, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, lo, hi, relu, nk,
-                       eps, W, bias, B, K, N, vec, split, split_ld, out_lo, out_hi, c_out, infeasible);
+    if (vec) launch(ibp_linear_small_kernel<false, true>);
+    else launch(ibp_linear_small_kernel<false, false>);
   } else {
-    hipLaunchKernelGGL(ibp_linear_small_kernel<true>, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, lo, hi, relu, nk,
-                       eps, W, bias, B, K, N, vec, split, split_ld, out_lo, out_hi, c_out, infeasible);
+    if (vec) launch(ibp_linear_small_kernel<true, true>);
+    else launch(ibp_linear_small_kernel<true, false>);
   }
   BF_LAUNCH_CHECK("ibp_linear_small_kernel");
   return BF_OK;
