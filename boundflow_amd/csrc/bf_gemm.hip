@@ -94,6 +94,8 @@ int gemm_tile_choice(int64_t M, int64_t N, int nz, int64_t ks, int pro, bool dl)
   return 'G';
 }
 
+int gemm_norm_cols(int64_t M, int64_t N, int pro);
+
 int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream) {
   if ((pro != PRO_PLAIN && pro != PRO_RELAX) || (epi != EPI_STORE && epi != EPI_ABSSUM && epi != EPI_RELAX)) {
     set_error("gemm_dispatch: bad mode pro=%d epi=%d", pro, epi);
@@ -106,6 +108,8 @@ int gemm_dispatch(const GemmArgs& a, int pro, int epi, int nz, hipStream_t strea
   // as the 4-wave 64 x 128 TileQ when the operands suit its direct-to-LDS loop (twice the
   // tiles of TileH over as many CUs, each tile's K loop on one wave per SIMD), else TileH
   if (t == 'S' && epi != EPI_STORE) t = dl ? 'Q' : 'H';
+  // the |A W| epilogue's partial norms are per gemm_norm_cols columns: 64 is TileS's width
+  if (epi == EPI_ABSSUM && gemm_norm_cols(a.M, a.N, pro) == NORM_BN / 2) t = 'S';
   switch (t) {
     case 'S': return launch_tile<TileS>(a, pro, epi, nz, stream);
     case 'H': return launch_tile<TileH>(a, pro, epi, nz, stream);
@@ -135,6 +139,17 @@ int relax_table(const float* lo, const float* hi, const float* alpha, int64_t al
 }
 
 int gemm_partial_count(int64_t N) { return (int)ceil_div(N, NORM_BN); }
+
+// Columns per partial norm of the |A W| epilogue: 64 (the 64 x 64 TileS, plain prologue)
+// when the 64 x 128 tiles of one bound would leave more than half of the device's 256
+// CUs idle -- a small batch, where a tile's whole K loop on one wave per SIMD is the
+// launch's critical path -- else NORM_BN.
+int gemm_norm_cols(int64_t M, int64_t N, int pro) {
+  if (pro != PRO_PLAIN || N <= NORM_BN / 2) return NORM_BN;
+  return ceil_div(M, (int64_t)64) * ceil_div(N, (int64_t)NORM_BN) < 128 ? NORM_BN / 2 : NORM_BN;
+}
+
+int gemm_norm_partial_count(int64_t M, int64_t N, int pro) { return (int)ceil_div(N, (int64_t)gemm_norm_cols(M, N, pro)); }
 
 // Sums of the relaxation epilogue over the column tiles, in tile order:
 //   b_out[m] = b_src[m] + sum_t pb[t][m]   (b_src NULL = 0; b_src may alias b_out)

@@ -748,7 +748,7 @@ gemm_kernel(GemmArgs p) {
         }
       }
   } else if constexpr (EPI == EPI_ABSSUM) {
-    static_assert(GBN == NORM_BN, "the |C| epilogue needs BN == NORM_BN");
+    static_assert(GBN == NORM_BN || GBN == NORM_BN / 2, "the |C| epilogue takes 128- or 64-column tiles");
     // sum_n |C[m, n]| * w[d, n] over this block's columns, fixed order (norm kind 0);
     // max_n |C[m, n]| (1) or sum_n C[m, n]^2 (2) for the L1 and L2 balls.  The kind
     // is uniform over the launch: one specialisation of the epilogue per kind.
@@ -1014,6 +1014,9 @@ int launch_tile(const GemmArgs& a, int pro, int epi, int nz, hipStream_t stream)
     if constexpr (T::BN == NORM_BN && T::BM <= 128) {                                        \
       if (pro == PRO_PLAIN && epi == EPI_ABSSUM) return launch_gemm_t<PRO_PLAIN, EPI_ABSSUM, T>(a, nz, stream); \
       if (pro == PRO_RELAX && epi == EPI_ABSSUM) return launch_gemm_t<PRO_RELAX, EPI_ABSSUM, T>(a, nz, stream); \
+    }                                                                                        \
+    if constexpr (T::BN == NORM_BN / 2 && T::BM <= 128) {                                    \
+      if (pro == PRO_PLAIN && epi == EPI_ABSSUM) return launch_gemm_t<PRO_PLAIN, EPI_ABSSUM, T>(a, nz, stream); \
     }                                                                                        \
     if constexpr (T::BN == NORM_BN && T::BM <= 128) {                                        \
       if (pro == PRO_PLAIN && epi == EPI_RELAX) return launch_gemm_t<PRO_PLAIN, EPI_RELAX, T>(a, nz, stream);   \

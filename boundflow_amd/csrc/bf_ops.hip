@@ -33,6 +33,7 @@ int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M,
                         const float* bu, const float* bl, float eps, int norm_p, float* lb, float* ub,
                         hipStream_t stream);
 int gemm_partial_count(int64_t N);
+int gemm_norm_partial_count(int64_t M, int64_t N, int pro);
 int rows_finalize(const float* b_src, const float* pb, const float* pc, int nparts, int64_t M, float* b_out,
                   float* c_out, hipStream_t stream);
 int gemm_ksplit(int64_t M, int64_t N, int64_t K, int64_t* kchunk);
@@ -1367,7 +1368,7 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
   BF_REQUIRE(((uintptr_t)relax & 15) == 0, "bf_crown_relu_linear_concretize: relax table must be 16-byte aligned");
   BF_REQUIRE((A_u != nullptr) == (ub != nullptr) && (A_l != nullptr) == (lb != nullptr),
              "bf_crown_relu_linear_concretize: input/output pointer mismatch");
-  const int nparts = gemm_partial_count(I);
+  const int nparts = gemm_norm_partial_count(M, I, PRO_RELAX);
   // workspace layout: partial_u [nparts*M], partial_l [nparts*M], cen_u [M], cen_l [M], bout_u [M], bout_l [M]
   float* pu = workspace;
   float* pl = pu + (int64_t)nparts * M;
@@ -1418,7 +1419,7 @@ int bf_crown_relu_linear_concretize(const float* A_u, const float* A_l, int64_t 
 
 int64_t bf_crown_relu_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
   const int64_t M = D * S;
-  return (2 * (int64_t)gemm_partial_count(I) + 4) * M;
+  return (2 * (int64_t)gemm_norm_partial_count(M, I, PRO_RELAX) + 4) * M;
 }
 
 int bf_crown_relu_linear_concretize_noalloc(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D,
@@ -1434,7 +1435,7 @@ int bf_crown_relu_linear_concretize_noalloc(const float* A_u, const float* A_l, 
     set_error("bf_crown_relu_linear_concretize_noalloc: %lld rows of %lld columns need %lld workspace floats, the "
               "fixed scratch holds %lld (at most %lld rows at this width); use bf_crown_relu_linear_concretize",
               (long long)(D * S), (long long)I, (long long)need, (long long)kConcretizeScratchFloats,
-              (long long)(kConcretizeScratchFloats / (2 * (int64_t)gemm_partial_count(I) + 4)));
+              (long long)(kConcretizeScratchFloats / (2 * (int64_t)gemm_norm_partial_count(D * S, I, PRO_RELAX) + 4)));
     return BF_ERANGE;
   }
   float* ws = nullptr;
@@ -1571,7 +1572,7 @@ int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dst
   BF_REQUIRE(W_t && workspace, "bf_crown_linear_concretize: null weight or workspace");
   BF_REQUIRE((A_u == nullptr || (ub && cen_u && b_u)) && (A_l == nullptr || (lb && cen_l && b_l)) && (A_u || A_l),
              "bf_crown_linear_concretize: missing coefficient, center, bias or output");
-  const int nparts = gemm_partial_count(I);
+  const int nparts = gemm_norm_partial_count(M, I, PRO_PLAIN);
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   int nz = 0;
@@ -1611,7 +1612,7 @@ int bf_crown_linear_concretize(const float* A_u, const float* A_l, int64_t a_dst
 }
 
 int64_t bf_crown_linear_concretize_workspace(int64_t D, int64_t S, int64_t I) {
-  return 2 * (int64_t)gemm_partial_count(I) * D * S;
+  return 2 * (int64_t)gemm_norm_partial_count(D * S, I, PRO_PLAIN) * D * S;
 }
 
 // sums_only: the row sums alone, no coefficient written (A_u_out / A_l_out NULL).
