@@ -56,7 +56,7 @@ SIGNATURES = {
     "bf_concretize_dense_grad": (I32, [P, I64, I64, I64, P, P, F32, I32, P, P, P]),
     "bf_rows_abs_max": (I32, [P, P, I64, I64, I64, P, P]),
     "bf_rows_add": (I32, [P, P, I64, I64, I64, P, P, I64, P, P]),
-    "bf_ibp_linear": (I32, [P, P, I64, I64, I32, F32, I32, P, P, I64, P, I64, P, P, P, P, P, P]),
+    "bf_ibp_linear": (I32, [P, P, I64, I64, I32, F32, I32, P, P, I64, P, I64, P, P, P, P, P, P, P]),
     "bf_ibp_linear_workspace": (I64, [I64, I64, I64]),
     "bf_interval_clip": (I32, [P, P, P, P, P, I64, I64, I64, P, P]),
     "bf_interval_relu": (I32, [P, P, I64, P, P, P]),

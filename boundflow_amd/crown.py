@@ -294,6 +294,10 @@ class ForwardTrace:
     input_center_proj: Dict[str, torch.Tensor] = field(default_factory=dict)  # first-layer x0 W^T (no bias)
     batch: int = 0
     device: Optional[torch.device] = None
+    # [B, P] radius of a box input, written by the first layer's IBP launch (None: not made there),
+    # and the box it was made from: (lower, upper, their versions)
+    input_radius: Optional[torch.Tensor] = None
+    input_box: Optional[tuple] = None
 
     @property
     def infeasible(self) -> torch.Tensor:
@@ -350,6 +354,7 @@ def forward_ibp_trace(
     pert = spec.perturbation
     norm_p = input_norm_p(pert)
     prev_lo = prev_hi = None
+    input_radius = input_box = None
     n_layers = len(chain.layers)
     if relu_inputs_only:
         feeding = [i for i, layer in enumerate(chain.layers) if layer.out_name in relu_set]
@@ -377,6 +382,9 @@ def forward_ibp_trace(
                 if isinstance(pert, BoxPerturbation):
                     in_lo, in_hi, kind, eps, relu_in = (pert.lower.reshape(B, K).contiguous(),
                                                         pert.upper.reshape(B, K).contiguous(), 0, 0.0, 0)
+                    # the box radius the input concretization weighs by, written by this launch
+                    input_radius = torch.empty(B, K, device=dev, dtype=torch.float32)
+                    input_box = (pert.lower, pert.upper, pert.lower._version, pert.upper._version)
                 else:
                     # Lp ball: x0 W^T -/+ eps * row norm of W (sum |W|, ||W||_2, max |W| for p = inf, 2, 1)
                     kind = {0: 1, 2: 2, 1: 3}[norm_p]
@@ -386,7 +394,8 @@ def forward_ibp_trace(
                 relu_in = 1 if layer.input_is_relu_of is not None else 0
             _lib.call("bf_ibp_linear", _lib.ptr(in_lo), _lib.ptr(in_hi), B, K, kind, eps, relu_in, _lib.ptr(W),
                       _lib.ptr(b), N, _lib.ptr(None if has_constraint else split), split_ld, _lib.ptr(ws),
-                      _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(cproj), _lib.ptr(infeasible), stream)
+                      _lib.ptr(lo), _lib.ptr(hi), _lib.ptr(cproj), _lib.ptr(infeasible),
+                      _lib.ptr(input_radius if first else None), stream)
             if cproj is not None:
                 proj[layer.out_name] = cproj
         else:
@@ -419,7 +428,7 @@ def forward_ibp_trace(
         if bool(infeasible.any().item()):
             raise ValueError("infeasible relu split or constraint: lower>upper after applying split")
     return ForwardTrace(interval_env=interval_env, relu_pre=relu_pre, infeasible_flags=infeasible, batch=B, device=dev,
-                        input_center_proj=proj)
+                        input_center_proj=proj, input_radius=input_radius, input_box=input_box)
 
 
 # ---------------------------------------------------------------------------
@@ -593,7 +602,7 @@ def crown_backward(
         relax = relax_table(k) if relaxes else None
         if k == 0 and pre_relaxed:
             # input layer of an already relaxed coefficient: contraction fused with the concretization
-            rad, eps = _input_radius(pert, B, P)
+            rad, eps = _input_radius(pert, B, P, trace)
             ws = torch.empty(int(_lib.load().bf_crown_linear_concretize_workspace(B, S, P)), device=dev,
                              dtype=torch.float32)
             lb = torch.empty(B, S, device=dev, dtype=torch.float32) if A_l is not None else None
@@ -620,7 +629,7 @@ def crown_backward(
         if k == 0:
             # input layer: relaxation + contraction fused with the concretization
             if isinstance(pert, BoxPerturbation):
-                rad = _input_radius(pert, B, P)[0]
+                rad = _input_radius(pert, B, P, trace)[0]
                 cvec = trace.input_center_proj.get(layer.out_name)
                 # center term A' (mid W^T): the trace holds mid W^T when the input is a box
                 eps = 1.0
@@ -755,9 +764,15 @@ def _identity_table(B: int, n: int, dev) -> torch.Tensor:
     return t
 
 
-def _input_radius(pert, B: int, P: int):
-    """(rad, eps) of the input concretization: box radius with eps 1, or Linf eps without weights."""
+def _input_radius(pert, B: int, P: int, trace=None):
+    """(rad, eps) of the input concretization: box radius with eps 1, or Linf eps without weights.
+    The radius the trace's first IBP launch wrote when it was made from this very box (same
+    tensors, unchanged since), else one launch here."""
     if isinstance(pert, BoxPerturbation):
+        box = getattr(trace, "input_box", None)
+        if (box is not None and box[0] is pert.lower and box[1] is pert.upper
+                and box[2] == pert.lower._version and box[3] == pert.upper._version):
+            return trace.input_radius, 1.0
         lo = pert.lower.reshape(B, P).contiguous()
         hi = pert.upper.reshape(B, P).contiguous()
         # depends on the query's input set: computed per query (one launch), never kept across queries

@@ -240,7 +240,7 @@ def forward_ibp_trace_dag(
                 args = (xi.lower.reshape(B, K), xi.upper.reshape(B, K), 0, 0.0)
             _lib.call("bf_ibp_linear", _lib.ptr(args[0]), _lib.ptr(args[1]), B, K, args[2], args[3], 0, _lib.ptr(W),
                       _lib.ptr(b), N, None, 0, _lib.ptr(ws), _lib.ptr(lo), _lib.ptr(hi), None,
-                      _lib.ptr(infeasible), stream)
+                      _lib.ptr(infeasible), None, stream)
             y = IntervalState(lo, hi)
             shapes[out] = (N,)
         elif t == "conv2d":

@@ -208,7 +208,8 @@ __global__ void __launch_bounds__(64 * ISM_WAVES)
 ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int relu, int nk, float eps,
                         const float* __restrict__ W, const float* __restrict__ bias, int64_t B, int64_t K, int64_t N,
                         const int8_t* __restrict__ split, int64_t split_ld, float* __restrict__ out_lo,
-                        float* __restrict__ out_hi, float* __restrict__ c_out, int* __restrict__ infeasible) {
+                        float* __restrict__ out_hi, float* __restrict__ c_out, int* __restrict__ infeasible,
+                        float* __restrict__ rad_out) {
   __shared__ float red_c[ISM_WAVES][256];
   __shared__ float red_r[BALL ? 1 : ISM_WAVES][256];
   __shared__ float red_n[BALL ? ISM_WAVES : 1][64];
@@ -229,6 +230,10 @@ ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ 
   floatx4 acc_r = {0.f, 0.f, 0.f, 0.f};
   float nrm = 0.f;
   const int64_t nsteps = (K + 15) / 16;
+  // rad_out (interval input without ReLU): the first column of tiles writes the box radius
+  // (u - l) / 2 of its rows from the loaded bounds (the arithmetic of ibp_center_radius_kernel)
+  const bool put_rad = !BALL && rad_out != nullptr && n0 == 0 && bok;
+  float* __restrict__ rrow = put_rad ? rad_out + (b0 + i) * K : nullptr;
   for (int64_t s0 = wave; s0 < nsteps; s0 += (int64_t)ISM_WAVES * ISM_GROUP) {
     float4 al[ISM_GROUP], ah[ISM_GROUP], w4[ISM_GROUP];
 #pragma unroll
@@ -252,6 +257,19 @@ ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ 
         nrm = ism_norm_step(nrm, w4[q].z, nk);
         nrm = ism_norm_step(nrm, w4[q].w, nk);
       } else {
+        if (put_rad) {
+          const int64_t k = (s0 + (int64_t)q * ISM_WAVES) * 16 + 4 * g;
+          const float4 rv = make_float4(ism_radius(al[q].x, ah[q].x, false), ism_radius(al[q].y, ah[q].y, false),
+                                        ism_radius(al[q].z, ah[q].z, false), ism_radius(al[q].w, ah[q].w, false));
+          if constexpr (VEC) {
+            if (k < K) *reinterpret_cast<float4*>(rrow + k) = rv;
+          } else {
+            if (k + 0 < K) rrow[k + 0] = rv.x;
+            if (k + 1 < K) rrow[k + 1] = rv.y;
+            if (k + 2 < K) rrow[k + 2] = rv.z;
+            if (k + 3 < K) rrow[k + 3] = rv.w;
+          }
+        }
         acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_center(al[q].x, ah[q].x, rl), w4[q].x, acc_c, 0, 0, 0);
         acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_center(al[q].y, ah[q].y, rl), w4[q].y, acc_c, 0, 0, 0);
         acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(ism_center(al[q].z, ah[q].z, rl), w4[q].z, acc_c, 0, 0, 0);
@@ -312,13 +330,13 @@ bool ibp_linear_small_route(int64_t B, int64_t N) { return ceil_div(B, 16) * cei
 
 int ibp_linear_small(const float* lo, const float* hi, int relu, int nk, float eps, const float* W, const float* bias,
                      int64_t B, int64_t K, int64_t N, const int8_t* split, int64_t split_ld, float* out_lo,
-                     float* out_hi, float* c_out, int* infeasible, hipStream_t stream) {
+                     float* out_hi, float* c_out, int* infeasible, float* rad_out, hipStream_t stream) {
   const unsigned tiles = (unsigned)(ceil_div(B, 16) * ceil_div(N, 16));
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  const bool vec = (K % 4 == 0) && al16(lo) && al16(hi) && al16(W);
+  const bool vec = (K % 4 == 0) && al16(lo) && al16(hi) && al16(W) && al16(rad_out);
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, lo, hi, relu, nk, eps, W, bias, B, K, N,
-                       split, split_ld, out_lo, out_hi, c_out, infeasible);
+                       split, split_ld, out_lo, out_hi, c_out, infeasible, rad_out);
   };
   if (hi) {
     if (vec) launch(ibp_linear_small_kernel<false, true>);
@@ -1749,7 +1767,7 @@ static int ibp_products(const float* xc, const float* xr, const float* W, int64_
 int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, int input_kind, float eps,
                   int apply_relu, const float* W, const float* bias, int64_t N, const int8_t* split, int64_t split_ld,
                   float* workspace, float* out_lo, float* out_hi, float* center_out, int* infeasible,
-                  hipStream_t stream) {
+                  float* box_radius_out, hipStream_t stream) {
   // input_kind 0: interval [in_lo, in_hi] (optionally through ReLU) or box; 1: Linf ball around in_lo;
   // 2: L2 ball; 3: L1 ball (the row norm of W is the ball's dual norm, perturbation.py:127-136)
   BF_REQUIRE(B >= 0 && K > 0 && N > 0 && input_kind >= 0 && input_kind <= 3, "bf_ibp_linear: bad sizes or input kind");
@@ -1764,11 +1782,18 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   int rc;
   int ks = 1;
   BF_REQUIRE(input_kind >= 1 || in_hi, "bf_ibp_linear: interval input needs in_hi");
+  BF_REQUIRE(box_radius_out == nullptr || (input_kind == 0 && apply_relu == 0),
+             "bf_ibp_linear: box_radius_out is for a box input without ReLU");
   if (ibp_linear_small_route(B, N)) {
-    // a small output: products and finalize in one launch (row norm code as row_norm_kernel)
+    // a small output: products and finalize in one launch (row norm code as row_norm_kernel),
+    // the box radius written from the loaded bounds
     const int nk = input_kind == 1 ? 0 : (input_kind == 2 ? 2 : 1);
     return ibp_linear_small(in_lo, input_kind >= 1 ? nullptr : in_hi, apply_relu, nk, eps, W, bias, B, K, N, split,
-                            split_ld, out_lo, out_hi, center_out, infeasible, stream);
+                            split_ld, out_lo, out_hi, center_out, infeasible, box_radius_out, stream);
+  }
+  if (box_radius_out) {
+    rc = ibp_center_radius(in_lo, in_hi, B * K, 0, nullptr, box_radius_out, stream);
+    if (rc) return rc;
   }
   if (input_kind >= 1) {
     rc = ibp_products(in_lo, nullptr, W, B, K, N, cdst, nullptr, part, &ks, stream);

@@ -141,7 +141,7 @@ class HipTaskExecutor:
         ws = torch.empty(int(_lib.load().bf_ibp_linear_workspace(B, K, N)), device=dev)
         _lib.call("bf_ibp_linear", _lib.ptr(in_lo), _lib.ptr(in_hi), B, K, kind, eps, 0, _lib.ptr(w.contiguous()),
                   _lib.ptr(None if b is None else b.contiguous()), N, None, 0, _lib.ptr(ws), _lib.ptr(lo),
-                  _lib.ptr(hi), None, None, _lib.stream_handle())
+                  _lib.ptr(hi), None, None, None, _lib.stream_handle())
         return IntervalState(lo, hi)
 
     def _batched_linear(self, iv: IntervalState, w: torch.Tensor, b: Optional[torch.Tensor]) -> IntervalState:

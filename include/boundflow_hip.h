@@ -63,11 +63,14 @@ int bf_gemm_tile_config(int64_t M, int64_t N, int nz, int ksplit, int relax_prol
  * input_kind 1: Linf ball of radius eps around in_lo; 2: L2 ball; 3: L1 ball
  * (eps times the dual norm of each W row: sum |w|, the L2 norm, max |w|).
  * workspace: bf_ibp_linear_workspace(B, K, N) floats.  center_out (optional,
- * [B, N]) receives mid @ W^T without bias. */
+ * [B, N]) receives mid @ W^T without bias.  box_radius_out (optional, [B, K],
+ * box input without ReLU only) receives the input box radius (in_hi - in_lo) / 2,
+ * the weights of the box concretization (perturbation.py:282-325), written from
+ * the bounds the products load when the output is small. */
 int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, int input_kind, float eps,
                   int apply_relu, const float* W, const float* bias, int64_t N, const int8_t* split,
                   int64_t split_ld, float* workspace, float* out_lo, float* out_hi, float* center_out,
-                  int* infeasible, hipStream_t stream);
+                  int* infeasible, float* box_radius_out, hipStream_t stream);
 int64_t bf_ibp_linear_workspace(int64_t B, int64_t K, int64_t N);
 
 /* Interval conv2d (NCHW, groups 1, dilation 1) in center/radius form.

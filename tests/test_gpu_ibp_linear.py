@@ -49,7 +49,7 @@ def _run(lo, hi, W, b, kind, eps, relu, split, want_center):
     flags = torch.zeros(B, dtype=torch.int32, device=dev)
     _lib.call("bf_ibp_linear", _lib.ptr(lo), _lib.ptr(hi), B, K, kind, eps, relu, _lib.ptr(W), _lib.ptr(b), N,
               _lib.ptr(split), N if split is not None else 0, _lib.ptr(ws), _lib.ptr(out_l), _lib.ptr(out_u),
-              _lib.ptr(cen), _lib.ptr(flags), _lib.stream_handle())
+              _lib.ptr(cen), _lib.ptr(flags), None, _lib.stream_handle())
     torch.cuda.synchronize()
     return out_l, out_u, cen, flags
 
@@ -127,3 +127,46 @@ def test_ibp_linear_without_center_output_or_bias():
     tol = 2 * K * 2.0 ** -23 * mag + 1e-6
     assert bool(((a_l.double().cpu() - ref_l).abs() <= tol).all())
     assert bool(((a_u.double().cpu() - ref_u).abs() <= tol).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,K,N", [(64, 784, 256), (37, 301, 45), (512, 96, 600)])
+def test_ibp_linear_box_radius_output(B, K, N):
+    """box_radius_out receives (hi - lo) / 2 of the input box, bit for bit as torch's fp32
+    arithmetic makes it, on the one-launch route (written from the loaded bounds, including
+    K % 4 != 0) and on the split-K contraction route (its own launch); the bounds are the
+    same as without it."""
+    dev = device()
+    g = torch.Generator().manual_seed(B + K + N)
+    x = torch.randn(B, K, generator=g)
+    w = torch.rand(B, K, generator=g)
+    lo = (x - w).to(dev)
+    hi = (x + w).to(dev)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(dev)
+    ws = torch.empty(max(1, int(_lib.load().bf_ibp_linear_workspace(B, K, N))), device=dev)
+    outs = []
+    for with_rad in (False, True):
+        out_l = torch.empty(B, N, device=dev)
+        out_u = torch.empty(B, N, device=dev)
+        rad = torch.full((B, K), float("nan"), device=dev) if with_rad else None
+        _lib.call("bf_ibp_linear", _lib.ptr(lo), _lib.ptr(hi), B, K, 0, 0.0, 0, _lib.ptr(W), None, N, None, 0,
+                  _lib.ptr(ws), _lib.ptr(out_l), _lib.ptr(out_u), None, None, _lib.ptr(rad), _lib.stream_handle())
+        outs.append((out_l, out_u, rad))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[1][2], (hi - lo) / 2)
+
+
+@pytest.mark.gpu
+def test_ibp_linear_box_radius_refuses_relu_or_ball():
+    dev = device()
+    lo = torch.zeros(2, 8, device=dev)
+    W = torch.ones(3, 8, device=dev)
+    ws = torch.empty(int(_lib.load().bf_ibp_linear_workspace(2, 8, 3)), device=dev)
+    out = torch.empty(2, 3, device=dev)
+    rad = torch.empty(2, 8, device=dev)
+    for kind, relu in ((0, 1), (1, 0)):
+        with pytest.raises(_lib.HipError, match="box_radius_out"):
+            _lib.call("bf_ibp_linear", _lib.ptr(lo), _lib.ptr(lo), 2, 8, kind, 0.1, relu, _lib.ptr(W), None, 3, None,
+                      0, _lib.ptr(ws), _lib.ptr(out), _lib.ptr(out), None, None, _lib.ptr(rad),
+                      _lib.stream_handle())
