@@ -16,8 +16,17 @@ namespace bf {
 // (perturbation.py:175-222; box: eps = 1 and the norm is already radius-weighted).
 __device__ __forceinline__ float combine_parts(const float* __restrict__ part, int nparts, int64_t M, int64_t m,
                                                int norm_p) {
+  // the partials' loads issued eight at a time, combined in block order
   float s = 0.f;
-  for (int q = 0; q < nparts; ++q) {
+  int q = 0;
+  for (; q + 8 <= nparts; q += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(q + u) * M + m];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s = norm_p == 1 ? fmaxf(s, v[u]) : s + v[u];
+  }
+  for (; q < nparts; ++q) {
     const float v = part[(int64_t)q * M + m];
     s = norm_p == 1 ? fmaxf(s, v) : s + v;
   }
