@@ -154,20 +154,49 @@ __global__ void ibp_finalize_kernel(const float* __restrict__ c, const float* __
   hi[i] = u;
 }
 
-// IBP of a linear layer whose output has few 16 x 16 tiles (a small batch), in one
-// launch: workgroup t owns output tile t (16 rows of the batch x 16 output neurons) and
-// takes the whole reduction for both products -- the center Xc . W^T and the radius
-// Xr . |W|^T of an interval input (center and radius made from [lo, hi] as they are
-// loaded, of the ReLU when relu, with the arithmetic of ibp_center_radius_kernel), or the
-// center and eps times the row norm of W (norm code nk as row_norm_kernel) of a ball --
-// its 16 waves taking the 16-wide steps of k in turn (wave w: steps w, w + 16, ...; the
-// loads of four steps issued together).  The waves' partial tiles are added in LDS in
-// wave order and the workgroup applies ibp_finalize_kernel's arithmetic, so no partial
-// buffer and no second launch is needed.
+// Products of a small output (few 16 x 16 tiles: a small batch) in one launch, with no
+// split of the reduction: workgroup t owns output tile t (16 rows x 16 columns) and takes
+// the whole reduction, its 16 waves taking the 16-wide steps of k in turn (wave w: steps
+// w, w + 16, ...; the loads of four steps issued together).  The waves' partial tiles are
+// added in LDS in wave order and the workgroup applies the epilogue, so no partial buffer
+// and no second launch is needed.  Modes:
+//  * SM_INTERVAL / SM_BALL -- IBP of a linear layer: the center Xc . W^T and the radius
+//    Xr . |W|^T of an interval input (center and radius made from [lo, hi] as they are
+//    loaded, of the ReLU when relu, with the arithmetic of ibp_center_radius_kernel), or
+//    the center and eps times the row norm of W (norm code nk as row_norm_kernel) of a
+//    ball; the epilogue is ibp_finalize_kernel's arithmetic.  With rad_out (interval
+//    input without ReLU) the first column of tiles also writes the box radius.
+//  * SM_GEMM -- C = A . W^T (+ r_row[m] v_col[(m / S) v_ld + n]), the rank-1 term added
+//    as splitk_reduce_kernel adds it.
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int ISM_WAVES = 16;
 constexpr int ISM_GROUP = 4;
 constexpr int64_t ISM_MAX_TILES = 1024;
+enum : int { SM_INTERVAL = 0, SM_BALL = 1, SM_GEMM = 2 };
+
+struct SmallOutArgs {
+  const float* lo;        // left operand rows (the interval's lower bounds, the ball's center, or A)
+  const float* hi;        // the interval's upper bounds (SM_INTERVAL)
+  int64_t lda;            // row stride of lo / hi
+  const float* W;         // [N, ldw] rows
+  int64_t ldw;
+  int64_t B, K, N;        // output rows, reduction, output columns
+  int relu, nk;
+  float eps;
+  const float* bias;      // IBP outputs
+  const int8_t* split;
+  int64_t split_ld;
+  float* out_lo;
+  float* out_hi;
+  float* c_out;
+  int* infeasible;
+  float* rad_out;
+  float* C;               // SM_GEMM output
+  int64_t ldc;
+  const float* r_row;
+  const float* v_col;
+  int64_t v_ld, S;
+};
 
 // Four k of one row, zero where ok is false or k runs past K.  Branch-free: every load is
 // issued (from a clamped address inside the row) and masked afterwards, so the loads of a
@@ -203,37 +232,35 @@ __device__ __forceinline__ float ism_norm_step(float s, float w, int nk) {
   return nk == 1 ? fmaxf(s, fabsf(w)) : (nk == 2 ? s + w * w : s + fabsf(w));
 }
 
-template <bool BALL, bool VEC>
+template <int MODE, bool VEC>
 __global__ void __launch_bounds__(64 * ISM_WAVES)
-ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ hi, int relu, int nk, float eps,
-                        const float* __restrict__ W, const float* __restrict__ bias, int64_t B, int64_t K, int64_t N,
-                        const int8_t* __restrict__ split, int64_t split_ld, float* __restrict__ out_lo,
-                        float* __restrict__ out_hi, float* __restrict__ c_out, int* __restrict__ infeasible,
-                        float* __restrict__ rad_out) {
+small_out_kernel(SmallOutArgs a) {
+  constexpr bool BALL = MODE == SM_BALL, IVL = MODE == SM_INTERVAL;
   __shared__ float red_c[ISM_WAVES][256];
-  __shared__ float red_r[BALL ? 1 : ISM_WAVES][256];
+  __shared__ float red_r[IVL ? ISM_WAVES : 1][256];
   __shared__ float red_n[BALL ? ISM_WAVES : 1][64];
+  const int64_t B = a.B, K = a.K, N = a.N;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t ntn = (N + 15) / 16;
   const int64_t b0 = (int64_t)(blockIdx.x / ntn) * 16, n0 = (int64_t)(blockIdx.x % ntn) * 16;
-  // MFMA lanes: i = lane & 15 is the batch row of the A operand and the neuron of the B
+  // MFMA lanes: i = lane & 15 is the row of the A operand and the column of the B
   // operand, g = lane >> 4 the k slot; a lane's float4 at k = 16 s + 4 g holds the four
   // k of its slot for the four MFMAs of step s
   const int i = lane & 15, g = lane >> 4;
   const bool bok = b0 + i < B, nok = n0 + i < N;
-  const bool rl = relu != 0;
-  const float* __restrict__ xl = lo + (bok ? b0 + i : 0) * K;
-  const float* __restrict__ xh = BALL ? lo : hi + (bok ? b0 + i : 0) * K;
-  const float* __restrict__ wr = W + (nok ? n0 + i : 0) * K;
+  const bool rl = a.relu != 0;
+  const float* __restrict__ xl = a.lo + (bok ? b0 + i : 0) * a.lda;
+  const float* __restrict__ xh = IVL ? a.hi + (bok ? b0 + i : 0) * a.lda : a.lo;
+  const float* __restrict__ wr = a.W + (nok ? n0 + i : 0) * a.ldw;
   floatx4 acc_c = {0.f, 0.f, 0.f, 0.f};
   floatx4 acc_r = {0.f, 0.f, 0.f, 0.f};
   float nrm = 0.f;
   const int64_t nsteps = (K + 15) / 16;
   // rad_out (interval input without ReLU): the first column of tiles writes the box radius
   // (u - l) / 2 of its rows from the loaded bounds (the arithmetic of ibp_center_radius_kernel)
-  const bool put_rad = !BALL && rad_out != nullptr && n0 == 0 && bok;
-  float* __restrict__ rrow = put_rad ? rad_out + (b0 + i) * K : nullptr;
+  const bool put_rad = IVL && a.rad_out != nullptr && n0 == 0 && bok;
+  float* __restrict__ rrow = put_rad ? a.rad_out + (b0 + i) * K : nullptr;
   for (int64_t s0 = wave; s0 < nsteps; s0 += (int64_t)ISM_WAVES * ISM_GROUP) {
     float4 al[ISM_GROUP], ah[ISM_GROUP], w4[ISM_GROUP];
 #pragma unroll
@@ -242,20 +269,22 @@ ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ 
       const int64_t k = s * 16 + 4 * g;
       const bool sok = s < nsteps;
       al[q] = ism_load4<VEC>(xl, k, K, bok && sok);
-      if (!BALL) ah[q] = ism_load4<VEC>(xh, k, K, bok && sok);
+      if (IVL) ah[q] = ism_load4<VEC>(xh, k, K, bok && sok);
       w4[q] = ism_load4<VEC>(wr, k, K, nok && sok);
     }
 #pragma unroll
     for (int q = 0; q < ISM_GROUP; ++q) {
-      if constexpr (BALL) {
+      if constexpr (!IVL) {
         acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].x, w4[q].x, acc_c, 0, 0, 0);
         acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].y, w4[q].y, acc_c, 0, 0, 0);
         acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].z, w4[q].z, acc_c, 0, 0, 0);
         acc_c = __builtin_amdgcn_mfma_f32_16x16x4f32(al[q].w, w4[q].w, acc_c, 0, 0, 0);
-        nrm = ism_norm_step(nrm, w4[q].x, nk);
-        nrm = ism_norm_step(nrm, w4[q].y, nk);
-        nrm = ism_norm_step(nrm, w4[q].z, nk);
-        nrm = ism_norm_step(nrm, w4[q].w, nk);
+        if constexpr (BALL) {
+          nrm = ism_norm_step(nrm, w4[q].x, a.nk);
+          nrm = ism_norm_step(nrm, w4[q].y, a.nk);
+          nrm = ism_norm_step(nrm, w4[q].z, a.nk);
+          nrm = ism_norm_step(nrm, w4[q].w, a.nk);
+        }
       } else {
         if (put_rad) {
           const int64_t k = (s0 + (int64_t)q * ISM_WAVES) * 16 + 4 * g;
@@ -281,72 +310,106 @@ ibp_linear_small_kernel(const float* __restrict__ lo, const float* __restrict__ 
       }
     }
   }
-  // lane's acc[r] is tile element (row 4 g + r, neuron i)
+  // lane's acc[r] is tile element (row 4 g + r, column i)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     red_c[wave][(4 * g + r) * 16 + i] = acc_c[r];
-    if constexpr (!BALL) red_r[wave][(4 * g + r) * 16 + i] = acc_r[r];
+    if constexpr (IVL) red_r[wave][(4 * g + r) * 16 + i] = acc_r[r];
   }
   if constexpr (BALL) red_n[wave][lane] = nrm;
   __syncthreads();
   if (tid >= 256) return;
   const int mr = tid >> 4, nc = tid & 15;
   const int64_t b = b0 + mr, n = n0 + nc;
-  float cv = red_c[0][tid], dev;
+  float cv = red_c[0][tid];
   for (int w = 1; w < ISM_WAVES; ++w) cv += red_c[w][tid];
-  if constexpr (BALL) {
-    float s = 0.f;
-    for (int w = 0; w < ISM_WAVES; ++w)
-      for (int q = 0; q < 4; ++q) {
-        const float v = red_n[w][16 * q + nc];
-        s = nk == 1 ? fmaxf(s, v) : s + v;
-      }
-    dev = eps * (nk == 2 ? sqrtf(s) : s);
+  if constexpr (MODE == SM_GEMM) {
+    if (b >= B || n >= N) return;
+    float v = cv;
+    if (a.r_row) v = v + a.r_row[b] * a.v_col[(b / a.S) * a.v_ld + n];
+    a.C[b * a.ldc + n] = v;
   } else {
-    dev = red_r[0][tid];
-    for (int w = 1; w < ISM_WAVES; ++w) dev += red_r[w][tid];
+    float dev;
+    if constexpr (BALL) {
+      float sn = 0.f;
+      for (int w = 0; w < ISM_WAVES; ++w)
+        for (int q = 0; q < 4; ++q) {
+          const float v = red_n[w][16 * q + nc];
+          sn = a.nk == 1 ? fmaxf(sn, v) : sn + v;
+        }
+      dev = a.eps * (a.nk == 2 ? sqrtf(sn) : sn);
+    } else {
+      dev = red_r[0][tid];
+      for (int w = 1; w < ISM_WAVES; ++w) dev += red_r[w][tid];
+    }
+    if (b >= B || n >= N) return;
+    float l = cv - dev;
+    float u = cv + dev;
+    if (a.bias) {
+      l = l + a.bias[n];
+      u = u + a.bias[n];
+    }
+    if (a.split) {
+      const int8_t sp = a.split[b * a.split_ld + n];
+      if (sp > 0) l = fmaxf(l, 0.f);
+      if (sp < 0) u = fminf(u, 0.f);
+      if (l > u && a.infeasible) a.infeasible[b] = 1;
+    }
+    const int64_t o = b * N + n;
+    a.out_lo[o] = l;
+    a.out_hi[o] = u;
+    if (a.c_out) a.c_out[o] = cv;
   }
-  if (b >= B || n >= N) return;
-  float l = cv - dev;
-  float u = cv + dev;
-  if (bias) {
-    l = l + bias[n];
-    u = u + bias[n];
-  }
-  if (split) {
-    const int8_t sp = split[b * split_ld + n];
-    if (sp > 0) l = fmaxf(l, 0.f);
-    if (sp < 0) u = fminf(u, 0.f);
-    if (l > u && infeasible) infeasible[b] = 1;
-  }
-  const int64_t o = b * N + n;
-  out_lo[o] = l;
-  out_hi[o] = u;
-  if (c_out) c_out[o] = cv;
 }
 
-// True when ibp_linear_small_kernel takes a B x N output.
-bool ibp_linear_small_route(int64_t B, int64_t N) { return ceil_div(B, 16) * ceil_div(N, 16) <= ISM_MAX_TILES; }
+// True when small_out_kernel takes a B x N output.
+bool small_out_route(int64_t B, int64_t N) { return ceil_div(B, 16) * ceil_div(N, 16) <= ISM_MAX_TILES; }
+
+static int small_out_launch(int mode, const SmallOutArgs& a, hipStream_t stream) {
+  const unsigned tiles = (unsigned)(ceil_div(a.B, 16) * ceil_div(a.N, 16));
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool vec = (a.K % 4 == 0) && (a.lda % 4 == 0) && (a.ldw % 4 == 0) && al16(a.lo) && al16(a.hi) && al16(a.W) &&
+                   al16(a.rad_out);
+  auto launch = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, a); };
+  if (mode == SM_INTERVAL) {
+    if (vec) launch(small_out_kernel<SM_INTERVAL, true>);
+    else launch(small_out_kernel<SM_INTERVAL, false>);
+  } else if (mode == SM_BALL) {
+    if (vec) launch(small_out_kernel<SM_BALL, true>);
+    else launch(small_out_kernel<SM_BALL, false>);
+  } else {
+    if (vec) launch(small_out_kernel<SM_GEMM, true>);
+    else launch(small_out_kernel<SM_GEMM, false>);
+  }
+  BF_LAUNCH_CHECK("small_out_kernel");
+  return BF_OK;
+}
 
 int ibp_linear_small(const float* lo, const float* hi, int relu, int nk, float eps, const float* W, const float* bias,
                      int64_t B, int64_t K, int64_t N, const int8_t* split, int64_t split_ld, float* out_lo,
                      float* out_hi, float* c_out, int* infeasible, float* rad_out, hipStream_t stream) {
-  const unsigned tiles = (unsigned)(ceil_div(B, 16) * ceil_div(N, 16));
-  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  const bool vec = (K % 4 == 0) && al16(lo) && al16(hi) && al16(W) && al16(rad_out);
-  auto launch = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * ISM_WAVES), 0, stream, lo, hi, relu, nk, eps, W, bias, B, K, N,
-                       split, split_ld, out_lo, out_hi, c_out, infeasible, rad_out);
-  };
-  if (hi) {
-    if (vec) launch(ibp_linear_small_kernel<false, true>);
-    else launch(ibp_linear_small_kernel<false, false>);
-  } else {
-    if (vec) launch(ibp_linear_small_kernel<true, true>);
-    else launch(ibp_linear_small_kernel<true, false>);
-  }
-  BF_LAUNCH_CHECK("ibp_linear_small_kernel");
-  return BF_OK;
+  SmallOutArgs a;
+  memset(&a, 0, sizeof(a));
+  a.lo = lo;
+  a.hi = hi;
+  a.lda = K;
+  a.W = W;
+  a.ldw = K;
+  a.B = B;
+  a.K = K;
+  a.N = N;
+  a.relu = relu;
+  a.nk = nk;
+  a.eps = eps;
+  a.bias = bias;
+  a.split = split;
+  a.split_ld = split_ld;
+  a.out_lo = out_lo;
+  a.out_hi = out_hi;
+  a.c_out = c_out;
+  a.infeasible = infeasible;
+  a.rad_out = rad_out;
+  return small_out_launch(hi ? SM_INTERVAL : SM_BALL, a, stream);
 }
 
 // The relaxation table {alpha_u, beta_u, alpha_l, beta_l} from the four separate tensors
@@ -1244,6 +1307,26 @@ int bf_gemm_rank1(const float* A, int64_t lda, const float* B, int64_t ldb, int 
   BF_REQUIRE(A && B && C && ((r_row == nullptr) == (v_col == nullptr)), "bf_gemm_rank1: null pointer");
   int64_t kchunk = K;
   int ks = gemm_ksplit(M, N, K, &kchunk);
+  if (ks > 1 && trans_b && small_out_route(M, N)) {
+    // a small output whose contraction would be split: the whole reduction per 16 x 16 tile
+    // in one launch, the rank-1 term in its epilogue
+    SmallOutArgs s;
+    memset(&s, 0, sizeof(s));
+    s.lo = A;
+    s.lda = lda;
+    s.W = B;
+    s.ldw = ldb;
+    s.B = M;
+    s.K = K;
+    s.N = N;
+    s.C = C;
+    s.ldc = ldc;
+    s.r_row = r_row;
+    s.v_col = v_col;
+    s.v_ld = v_ld;
+    s.S = S;
+    return small_out_launch(SM_GEMM, s, stream);
+  }
   if (ks > 1 && (workspace == nullptr || workspace_floats < (int64_t)ks * M * N)) ks = 1;   // no split without room
   GemmArgs a;
   memset(&a, 0, sizeof(a));
@@ -1784,7 +1867,7 @@ int bf_ibp_linear(const float* in_lo, const float* in_hi, int64_t B, int64_t K, 
   BF_REQUIRE(input_kind >= 1 || in_hi, "bf_ibp_linear: interval input needs in_hi");
   BF_REQUIRE(box_radius_out == nullptr || (input_kind == 0 && apply_relu == 0),
              "bf_ibp_linear: box_radius_out is for a box input without ReLU");
-  if (ibp_linear_small_route(B, N)) {
+  if (small_out_route(B, N)) {
     // a small output: products and finalize in one launch (row norm code as row_norm_kernel),
     // the box radius written from the loaded bounds
     const int nk = input_kind == 1 ? 0 : (input_kind == 2 ? 2 : 1);

@@ -136,14 +136,15 @@ def test_store_on_tile_s_matches_fp64(M, N, K, trans_b):
     assert bool((err <= tol).all()), float((err / tol).max())
 
 
-@pytest.mark.parametrize("form", ["nz2_store", "rank1_S9", "rank1_split_k"])
+@pytest.mark.parametrize("form", ["nz2_store", "rank1_S9", "rank1_split_k", "rank1_small_out"])
 def test_other_store_forms_on_tile_s_match_fp64(form):
     """The other plain-prologue store forms that take TileS on small grids: both
     coefficient sides in one launch (bf_crown_relu_linear_fwd with nothing to relax,
-    nz = 2), the rank-1 epilogue with 9 rows per domain (bf_gemm_rank1, S = 9), and
-    the rank-1 epilogue with K split into chunks summed by splitk_reduce."""
+    nz = 2), the rank-1 epilogue with 9 rows per domain (bf_gemm_rank1, S = 9), the
+    rank-1 epilogue with K split into chunks summed by splitk_reduce, and a small output
+    whose split K takes the one-launch small-output kernel (rank-1 term in its epilogue)."""
     dev = device()
-    g = torch.Generator().manual_seed({"nz2_store": 3, "rank1_S9": 4, "rank1_split_k": 5}[form])
+    g = torch.Generator().manual_seed({"nz2_store": 3, "rank1_S9": 4, "rank1_split_k": 5, "rank1_small_out": 6}[form])
     st = _lib.stream_handle()
     if form == "nz2_store":
         D, S, N, P = 32, 9, 256, 100
@@ -167,15 +168,18 @@ def test_other_store_forms_on_tile_s_match_fp64(form):
             assert bool((err <= tol).all()), float((err / tol).max())
             assert torch.equal(b_out.cpu(), b_in), "b_out is b_in when nothing is relaxed"
         return
-    M, N, K, S = (288, 100, 256, 9) if form == "rank1_S9" else (288, 100, 1024, 9)
+    # rank1_S9: an unsplit TileS contraction (K = 200 below the split threshold); rank1_split_k: an output of
+    # more than 1024 tiles of 16 x 16 whose K is split over TileS chunks and reduced in chunk order;
+    # rank1_small_out: a small output whose split K takes the one-launch small-output kernel instead
+    M, N, K, S = {"rank1_S9": (288, 100, 200, 9), "rank1_split_k": (1152, 400, 1024, 9),
+                  "rank1_small_out": (288, 100, 1024, 9)}[form]
     ws_floats = int(_lib.load().bf_gemm_rank1_workspace(M, N, K))
-    if form == "rank1_split_k":
+    if form in ("rank1_split_k", "rank1_small_out"):
         assert ws_floats > 0, "this shape splits K"
-        ks = ws_floats // (M * N)
-        assert chr(_lib.load().bf_gemm_tile_config(M, N, 1, ks, 0, 1)) == "S"
+        assert (-(-M // 16) * -(-N // 16) > 1024) == (form == "rank1_split_k")
     else:
-        # no workspace given: the contraction runs unsplit
-        ws_floats = 0
+        # K below the split threshold: the contraction runs unsplit on TileS
+        assert ws_floats == 0
         assert tile(M, N) == "S"
     announce(f"gemm_rank1 {form} M={M} N={N} K={K} S={S} workspace={ws_floats}")
     A = torch.randn(M, K, generator=g)
