@@ -73,7 +73,7 @@ SIGNATURES = {
     "bf_split_certificate": (I32, [P, I64, P, P, I64, P, I64, P, I64, F32, I32, I64, I64, I64, I32, F64, F64, P, P,
                                    P]),
     "bf_adam_clamp_step": (I32, [P, P, P, P, I64, F64, F64, F64, F32, I32, F32, F32, I32, P]),
-    "bf_adam_clamp_multi": (I32, [I32, P, P, P, P, P, P, P, P, F64, F64, F64, F32, I32, P]),
+    "bf_adam_clamp_multi": (I32, [I32, P, P, P, P, P, P, P, P, F64, F64, F64, F32, I32, P, P, I64, P]),
     "bf_conv2d_rows": (I32, [P, I64, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P, P,
                              I64, I64, P]),
     "bf_conv_transpose_rows": (I32, [P, P, I64, I32, I32, I32, P, I32, I32, I32, I32, I32, I32, I32, I32, I32, P, P,

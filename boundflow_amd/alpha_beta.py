@@ -111,6 +111,13 @@ class AlphaBetaStats:
         return [None if lay[i] < 0 else (self.relu_names[lay[i]], int(ids[i])) for i in range(len(lay))]
 
 
+# Parameters of at most this many elements in all take the best-of copy inside the Adam step's
+# launch (C4: 0.2 M elements, one launch fewer per step); larger ones keep the float4 copy kernel,
+# which moves them faster than the step's per-element copy (C5's 8.4 M: 45.8 + 14.8 us apart,
+# 67.8 us fused).
+FUSED_COPY_MAX_ELEMS = 1 << 20
+
+
 class _AdamGroup:
     """Device-resident Adam state of several parameter tensors, stepped together in
     one launch (the reference runs one torch.optim.Adam over every alpha and beta,
@@ -127,10 +134,13 @@ class _AdamGroup:
         self.hi = _lib.f32_array([0.0 if hi is None else hi for _lo, hi in clamps])
         self.has_hi = _lib.i32_array([0 if hi is None else 1 for _lo, hi in clamps])
 
-    def step(self, grads: List[torch.Tensor], lr: float, stream) -> None:
+    def step(self, grads: List[torch.Tensor], lr: float, stream, best=None, improved=None, rows: int = 0) -> None:
+        """One step; with ``best`` (one tensor per parameter) the rows flagged in ``improved``
+        are first copied to it from the values the step updates (the best-of copy)."""
         self.t += 1
         _lib.call("bf_adam_clamp_multi", len(self.p), *self.args, _lib.ptr_array(grads), self.n, self.lo, self.hi,
-                  self.has_hi, float(lr), 0.9, 0.999, 1e-8, self.t, stream)
+                  self.has_hi, float(lr), 0.9, 0.999, 1e-8, self.t,
+                  None if best is None else _lib.ptr_array(best), _lib.ptr(improved), int(rows), stream)
 
 
 def branch_choices(trace: ForwardTrace, batch: int) -> List[Optional[Tuple[str, int]]]:
@@ -420,6 +430,7 @@ def run_alpha_beta_crown_mlp(
     copy_args = (_lib.ptr_array(copy_dst), _lib.ptr_array([alpha[n] for n in names] + [beta[n] for n in beta_names]),
                  _lib.i64_array([numel[n] for n in names] + [numel[n] for n in beta_names]), B, _lib.ptr(improved))
     memo: dict = {}   # per-call operands (scaled gradient rows, center-plus-bias), freed with the call
+    fuse_copy = per_batch_params and sum(int(t.numel()) for t in adam.p) <= FUSED_COPY_MAX_ELEMS
     for step in range(int(steps) + 1):
         if beta_names:
             _lib.call("bf_beta_coeff_multi", len(beta_names), *beta_args, stream)
@@ -429,7 +440,10 @@ def run_alpha_beta_crown_mlp(
         if per_batch_params:
             _lib.call("bf_best_update", _lib.ptr(bounds.lower), None, B, S, _lib.ptr(best_metric),
                       _lib.ptr(best_lb), None, _lib.ptr(improved), 1 if step == 0 else 0, stream)
-            _lib.call("bf_masked_copy_rows_multi", len(copy_dst), *copy_args, stream)
+            if not fuse_copy or step == int(steps):
+                # a launch of its own: large parameters (the float4 copy kernel moves them faster than
+                # the step's per-element copy), or the last evaluation (no step follows)
+                _lib.call("bf_masked_copy_rows_multi", len(copy_dst), *copy_args, stream)
         else:
             metric = float(bounds.lower.mean().item())
             if best_scalar is None or metric > best_scalar:
@@ -453,7 +467,10 @@ def run_alpha_beta_crown_mlp(
                     r = torch.empty(numel[n], device=dev)
                     _lib.call("bf_sum_rows", _lib.ptr(d[n]), B, numel[n], _lib.ptr(r), stream)
                     d[n] = r
-        adam.step([g_alpha[n] for n in names] + [g_beta[n] for n in beta_names], lr, stream)
+        # small parameters: the step takes the best-of copy of this evaluation's parameters with it
+        # (rows = domains), one launch fewer per step
+        adam.step([g_alpha[n] for n in names] + [g_beta[n] for n in beta_names], lr, stream,
+                  best=copy_dst if fuse_copy else None, improved=improved, rows=B)
         if record is not None:
             rec = record[-1]
             rec["grad_alpha"] = {n: g_alpha[n].reshape(pshape[n]).cpu() for n in names}

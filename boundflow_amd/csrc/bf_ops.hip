@@ -1009,6 +1009,8 @@ struct AdamSegs {
   float* m[BF_SEG_MAX];
   float* v[BF_SEG_MAX];
   const float* g[BF_SEG_MAX];
+  float* best[BF_SEG_MAX];   // best-of copy before the step (null: none)
+  int64_t ncol[BF_SEG_MAX];  // row length of the copy's mask rows
   int64_t n[BF_SEG_MAX];
   float lo[BF_SEG_MAX], hi[BF_SEG_MAX];
   int clamp_hi[BF_SEG_MAX];
@@ -1022,11 +1024,15 @@ __device__ __forceinline__ int seg_of_block(const int64_t* bstart, int count) {
   return s;
 }
 
+// improved (with best): row i / ncol of every tensor improved at the evaluation the step
+// follows, so the parameter is first copied to its best-of tensor (the copy of
+// masked_copy_rows_multi_kernel, taken from the same values before they are stepped).
 __global__ void adam_clamp_multi_kernel(AdamSegs a, float w1, float b2, float w2, float eps, float neg_step,
-                                        float bc2_sqrt) {
+                                        float bc2_sqrt, const int* __restrict__ improved) {
   const int s = seg_of_block(a.bstart, a.count);
   const int64_t i = ((int64_t)blockIdx.x - a.bstart[s]) * 256 + threadIdx.x;
   if (i >= a.n[s]) return;
+  if (a.best[s] && improved[div_rows(i, a.ncol[s], a.n[s] < (1LL << 31))]) a.best[s][i] = a.p[s][i];
   adam_clamp_one(a.p[s], a.m[s], a.v[s], a.g[s], i, w1, b2, w2, eps, neg_step, bc2_sqrt, a.lo[s], a.hi[s],
                  a.clamp_hi[s]);
 }
@@ -2017,10 +2023,12 @@ static void adam_consts(double lr, double beta1, double beta2, int step, float* 
 
 int bf_adam_clamp_multi(int count, float* const* p, float* const* m, float* const* v, const float* const* g,
                         const int64_t* n, const float* clamp_lo, const float* clamp_hi, const int* has_clamp_hi,
-                        double lr, double beta1, double beta2, float eps, int step, hipStream_t stream) {
+                        double lr, double beta1, double beta2, float eps, int step, float* const* best,
+                        const int* improved, int64_t rows, hipStream_t stream) {
   BF_REQUIRE(count >= 0 && step >= 1, "bf_adam_clamp_multi: bad arguments");
   BF_REQUIRE(count == 0 || (p && m && v && g && n && clamp_lo && clamp_hi && has_clamp_hi),
              "bf_adam_clamp_multi: null array");
+  BF_REQUIRE(best == nullptr || (improved && rows > 0), "bf_adam_clamp_multi: the best-of copy needs improved and rows");
   float w1, w2, neg_step, bc2_sqrt;
   adam_consts(lr, beta1, beta2, step, &w1, &w2, &neg_step, &bc2_sqrt);
   for (int base = 0; base < count; base += BF_SEG_MAX) {
@@ -2032,6 +2040,12 @@ int bf_adam_clamp_multi(int count, float* const* p, float* const* m, float* cons
       const int k = base + t;
       BF_REQUIRE(n[k] >= 0 && (n[k] == 0 || (p[k] && m[k] && v[k] && g[k])), "bf_adam_clamp_multi: tensor %d", k);
       a.p[t] = p[k]; a.m[t] = m[k]; a.v[t] = v[k]; a.g[t] = g[k]; a.n[t] = n[k];
+      if (best) {
+        BF_REQUIRE(best[k] && n[k] % rows == 0, "bf_adam_clamp_multi: best-of tensor %d (%lld elements, %lld rows)", k,
+                   (long long)n[k], (long long)rows);
+        a.best[t] = best[k];
+        a.ncol[t] = n[k] / rows;
+      }
       a.lo[t] = clamp_lo[k]; a.hi[t] = clamp_hi[k]; a.clamp_hi[t] = has_clamp_hi[k];
       a.bstart[t] = blocks;
       blocks += ceil_div(n[k], 256);
@@ -2040,7 +2054,7 @@ int bf_adam_clamp_multi(int count, float* const* p, float* const* m, float* cons
     if (blocks == 0) continue;
     BF_REQUIRE(blocks < (1LL << 31), "bf_adam_clamp_multi: too many elements");
     hipLaunchKernelGGL(adam_clamp_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a, w1, (float)beta2,
-                       w2, eps, neg_step, bc2_sqrt);
+                       w2, eps, neg_step, bc2_sqrt, improved);
     BF_LAUNCH_CHECK("adam_clamp_multi_kernel");
   }
   return BF_OK;

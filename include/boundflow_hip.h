@@ -439,10 +439,13 @@ int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, 
                        hipStream_t stream);
 /* The same step for `count` parameter tensors in one launch (one optimizer over all of them, as the
  * reference's single torch.optim.Adam over every alpha and beta; host arrays of device pointers, sizes
- * and per-tensor clamps). */
+ * and per-tensor clamps).  best (optional host array of device pointers): each tensor, taken as `rows`
+ * rows, is first copied to best[k] on the rows where improved[row] != 0 -- the best-of copy of
+ * bf_masked_copy_rows_multi (alpha_beta_crown.py:840-876) taken from the values the step then updates. */
 int bf_adam_clamp_multi(int count, float* const* p, float* const* m, float* const* v, const float* const* g,
                         const int64_t* n, const float* clamp_lo, const float* clamp_hi, const int* has_clamp_hi,
-                        double lr, double beta1, double beta2, float eps, int step, hipStream_t stream);
+                        double lr, double beta1, double beta2, float eps, int step, float* const* best,
+                        const int* improved, int64_t rows, hipStream_t stream);
 
 /* Per-domain best-of tracking on mean_s lb (runtime/alpha_beta_crown.py:840-876).  ub and best_ub may
  * both be NULL: the lower bounds alone are tracked (the caller then evaluates the upper bound once, with

@@ -437,8 +437,9 @@ def _placed(t: torch.Tensor, offset: int) -> torch.Tensor:
 
 @pytest.mark.parametrize("layout", ["ragged", "quad", "quad_misaligned"])
 def test_multi_tensor_steps_equal_single_tensor_steps(layout):
-    """bf_adam_clamp_multi, bf_masked_copy_rows_multi and bf_beta_coeff_multi give, tensor
-    by tensor, bit for bit what the single-tensor entry points give (18 tensors: two
+    """bf_adam_clamp_multi (also with its fused best-of copy), bf_masked_copy_rows_multi and
+    bf_beta_coeff_multi give, tensor by tensor, bit for bit what the single-tensor entry
+    points give (18 tensors: two
     launches of the multi kernels; sizes not multiples of the workgroup).  "ragged":
     widths 3 + 41 i (the scalar path); "quad": widths that are multiples of 4 on
     16-byte-aligned storage (the float4 path of the best-of copy and the split term);
@@ -471,7 +472,7 @@ def test_multi_tensor_steps_equal_single_tensor_steps(layout):
         _lib.call("bf_adam_clamp_multi", len(P1), _lib.ptr_array(P1), _lib.ptr_array(M1), _lib.ptr_array(V1),
                   _lib.ptr_array(G), _lib.i64_array([t.numel() for t in P1]), _lib.f32_array([c[0] for c in clamps]),
                   _lib.f32_array([c[1] or 0.0 for c in clamps]), _lib.i32_array([0 if c[1] is None else 1 for c in clamps]),
-                  0.2, 0.9, 0.999, 1e-8, step, st)
+                  0.2, 0.9, 0.999, 1e-8, step, None, None, 0, st)
     torch.cuda.synchronize()
     for i in range(len(P)):
         assert torch.equal(P[i], P1[i]) and torch.equal(M0[i], M1[i]) and torch.equal(V0[i], V1[i]), f"adam tensor {i}"
@@ -493,6 +494,23 @@ def test_multi_tensor_steps_equal_single_tensor_steps(layout):
     for i in range(len(P)):
         assert torch.equal(dst0[i], dst1[i]), f"masked copy tensor {i}"
         assert torch.equal(out0[i], out1[i]), f"split term tensor {i}"
+    # the best-of copy fused into the multi-tensor step: the masked rows get the values before the
+    # step, and the step itself is the single-tensor one
+    before = [t.clone() for t in P1]
+    best = [_placed(torch.zeros_like(t), off) for t in P]
+    for i, t in enumerate(P):
+        lo, hi = clamps[i]
+        _lib.call("bf_adam_clamp_step", _lib.ptr(t), _lib.ptr(M0[i]), _lib.ptr(V0[i]), _lib.ptr(G[i]), t.numel(),
+                  0.2, 0.9, 0.999, 1e-8, 4, lo, hi or 0.0, 0 if hi is None else 1, st)
+    _lib.call("bf_adam_clamp_multi", len(P1), _lib.ptr_array(P1), _lib.ptr_array(M1), _lib.ptr_array(V1),
+              _lib.ptr_array(G), _lib.i64_array([t.numel() for t in P1]), _lib.f32_array([c[0] for c in clamps]),
+              _lib.f32_array([c[1] or 0.0 for c in clamps]), _lib.i32_array([0 if c[1] is None else 1 for c in clamps]),
+              0.2, 0.9, 0.999, 1e-8, 4, _lib.ptr_array(best), _lib.ptr(mask), D, st)
+    torch.cuda.synchronize()
+    keep = mask.bool()[:, None]
+    for i in range(len(P)):
+        assert torch.equal(P[i], P1[i]) and torch.equal(M0[i], M1[i]) and torch.equal(V0[i], V1[i]), f"adam tensor {i}"
+        assert torch.equal(best[i], torch.where(keep, before[i], torch.zeros_like(before[i]))), f"best-of tensor {i}"
 
 
 @pytest.mark.parametrize("with_alpha", [True, False])
