@@ -83,7 +83,8 @@ SIGNATURES = {
                                            I32, I32, I32, I32, I32, I32, I32, P, P, P, P, P, P, P]),
     "bf_conv_transpose_small_supported": (I32, [I32] * 12),
     "bf_crown_relu_conv_transpose_concretize": (I32, [P, P, I64, I64, I32, I32, I32, P, P, P, I64, P, I64, P, P, P, P, P]
-                                                + [I32] * 9 + [P, I64, I32, P, P, P, P, P, P, P, P, P, P, P]),
+                                                + [I32] * 9 + [P, I64, I32, P, P, P, P, P, P, P, P, P, P, F32, P, P,
+                                                               P]),
     "bf_conv_transpose_packed_floats": (I64, [I32] * 12),
     "bf_conv_transpose_pack_weights": (I32, [P] + [I32] * 12 + [P, P]),
     "bf_ibp_conv2d": (I32, [P, P, I64, I32, I32, I32, I32, F32, I32, P, P, I32, I32, I32, I32, I32, I32, I32, I32, I32,

@@ -192,7 +192,7 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
     """The input conv layer through bf_crown_relu_conv_transpose_concretize: the ReLU
     relaxation applied while each row is staged, the transposed conv reduced to the
     concretization norm (and the gradient seed), the relaxed rows written only for a
-    gradient pass; then the bounds from the norms, centers and biases."""
+    gradient pass; the bounds from the norms, centers and biases in the same launch."""
     dev = spec.center.device
     stream = _lib.stream_handle()
     norm_p = input_norm_p(spec.perturbation)
@@ -216,6 +216,8 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
         save["h"] = h_out
         save["cvec"] = cvec
     rel_l = torch.empty(M, n_out, device=dev) if (save is not None and A_l is not None) else None
+    lb = torch.empty(B, S, device=dev) if A_l is not None else None
+    ub = torch.empty(B, S, device=dev) if A_u is not None else None
     with _timed("crown_relu_conv_transpose_concretize", flops,
                 4.0 * nz * (M * n_out + 2 * B * n_out) + (4.0 * M * n_out if rel_l is not None else 0.0)):
         _lib.call("bf_crown_relu_conv_transpose_concretize", _lib.ptr(A_u), _lib.ptr(A_l), B, S, Co, Ho, Wo,
@@ -223,12 +225,9 @@ def _input_layer_fused(spec, save, A_u, A_l, b_u, b_l, B, S, M, pre_lo, pre_hi, 
                   _lib.ptr(kbias), _lib.ptr(cvec), _lib.ptr(b_u), _lib.ptr(b_l), _lib.ptr(W), Ci, KH, KW, sh, sw, ph,
                   pw, Hi, Wi, _lib.ptr(rad), n_in, norm_p, _lib.ptr(h_scale), _lib.ptr(h_out), _lib.ptr(norm_u),
                   _lib.ptr(norm_l), _lib.ptr(nb_u), _lib.ptr(nb_l), _lib.ptr(c_u), _lib.ptr(c_l), None,
-                  _lib.ptr(rel_l), stream)
+                  _lib.ptr(rel_l), eps, _lib.ptr(lb), _lib.ptr(ub), stream)
     if save is not None:
         save.setdefault("relaxed", {})[layer.op_index] = rel_l
-    lb = torch.empty(B, S, device=dev) if A_l is not None else None
-    ub = torch.empty(B, S, device=dev) if A_u is not None else None
-    _lib.call("bf_concretize_finalize", _lib.ptr(norm_u), _lib.ptr(norm_l), 1, M, _lib.ptr(c_u), _lib.ptr(c_l),
-              _lib.ptr(nb_u), _lib.ptr(nb_l), eps, norm_p, _lib.ptr(lb), _lib.ptr(ub), stream)
+    # the launch wrote the bounds (c -/+ eps * norm) + b of every row
     return None, None, None, None, 0, IntervalState(lower=lb, upper=ub)
 

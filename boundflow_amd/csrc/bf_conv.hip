@@ -1026,6 +1026,8 @@ struct SmallTArgs {
   int vec;                 // rows copied as float4 (npix % 16 == 0 and 16-byte aligned row starts)
   FastDiv f_Wi, f_sh, f_sw, f_pitch;   // index divisions of the col2im and the map copy
   int pitchz, zsz;         // conv_t_small_fast_kernel: tap-row pitch of Z, floats per channel block
+  float* bnd[2];           // conv_t_small_fast_kernel<relaxation>: the row's bound (c -/+ eps * norm) + b, or null
+  float eps;
 };
 
 // RELAX: the input layer's ReLU relaxation applied while each row is staged, with
@@ -1418,6 +1420,7 @@ conv_t_small_fast_kernel(SmallTArgs g, ConvRelax rx) {
     }
     if (r + 1 < r_end) load_row(r + 1);
     __syncthreads();   // Z of every channel written; the row sums of every wave posted
+    float row_b = 0.f, row_c = 0.f;   // the row's bias and center sums (thread 0)
     if constexpr (RELAX) {
       if (tid == 0) {
         float tb = 0.f, tk = 0.f, tcs = 0.f;
@@ -1426,8 +1429,10 @@ conv_t_small_fast_kernel(SmallTArgs g, ConvRelax rx) {
           tk += rred[q][1];
           tcs += rred[q][2];
         }
-        if (rx.b_out[z]) rx.b_out[z][r] = ((rx.b_in[z] ? rx.b_in[z][r] : 0.f) + tb) + tk;
-        if (rx.c_out[z]) rx.c_out[z][r] = tcs;
+        row_b = ((rx.b_in[z] ? rx.b_in[z][r] : 0.f) + tb) + tk;
+        row_c = tcs;
+        if (rx.b_out[z]) rx.b_out[z][r] = row_b;
+        if (rx.c_out[z]) rx.c_out[z][r] = row_c;
       }
     }
     const float hs = (lower && g.h_out) ? g.h_scale[r] : 0.f;
@@ -1466,6 +1471,13 @@ conv_t_small_fast_kernel(SmallTArgs g, ConvRelax rx) {
       float tsum = 0.f;
       for (int q = 0; q < SF_NW; ++q) tsum = norm_join(tsum, red[q], g.nkind);
       nrm[r] = tsum;
+      if constexpr (RELAX) {
+        // the bound of the row, as concretize_finalize_kernel forms it from this one partial norm
+        if (g.bnd[z]) {
+          const float fin = g.nkind == 2 ? sqrtf(tsum) : tsum;
+          g.bnd[z][r] = lower ? (row_c - g.eps * fin) + row_b : (row_c + g.eps * fin) + row_b;
+        }
+      }
     }
     if (++s_in == g.S) {
       s_in = 0;
@@ -1504,9 +1516,11 @@ static int gather_rows_per_wg(int64_t work);
 // relaxation from the pre-activation box only).
 template <bool RELAX>
 static int small_t_launch(SmallTArgs& g, const ConvRelax& rx, unsigned nz, size_t glds, const char* who,
-                          hipStream_t stream) {
+                          hipStream_t stream, bool* fast = nullptr) {
   size_t flds = 0;
+  if (fast) *fast = false;
   if (!kSmallFastDisabled && conv_t_small_fast_plan(g, &flds)) {
+    if (fast) *fast = true;
     BF_REQUIRE(g.R * (int64_t)g.Co * g.npix < (1LL << 62) && (int64_t)g.Co * g.npix < (1LL << 31),
                "%s: rows too large", who);
     const int rpw = small_fast_rows_per_wg(g.R * nz);
@@ -1693,6 +1707,9 @@ int ibp_finalize(const float* c, const float* r, const float* rownorm, float eps
                  int* infeasible, hipStream_t stream);
 int fill_value(float* p, int64_t n, float v, hipStream_t stream);
 int lp_seed_rows(float* h, int64_t M, int64_t I, const float* h_scale, int norm_p, hipStream_t stream);
+int concretize_finalize(const float* pu, const float* pl, int nparts, int64_t M, const float* cu, const float* cl,
+                        const float* bu, const float* bl, float eps, int norm_p, float* lb, float* ub,
+                        hipStream_t stream);
 
 // conv2d of rows; with x2/y2 a second operand pair (abs_w2 for its weights) runs in
 // the same launch (blockIdx.y = 1), e.g. the center and the radius of an IBP layer.
@@ -2056,8 +2073,11 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
                                             const float* h_scale, float* h_out, float* norm_u, float* norm_l,
                                             float* b_u_out,
                                             float* b_l_out, float* c_u_out, float* c_l_out, float* relaxed_u,
-                                            float* relaxed_l, hipStream_t stream) {
+                                            float* relaxed_l, float eps, float* lb, float* ub, hipStream_t stream) {
   BF_REQUIRE(D >= 0 && S > 0 && Co > 0 && Ci > 0, "bf_crown_relu_conv_transpose_concretize: bad sizes");
+  BF_REQUIRE((lb == nullptr || (A_l && norm_l && b_l_out && c_l_out)) &&
+                 (ub == nullptr || (A_u && norm_u && b_u_out && c_u_out)),
+             "bf_crown_relu_conv_transpose_concretize: a bound needs its coefficient, norm, bias and center outputs");
   const int64_t R = D * S;
   if (R == 0) return BF_OK;
   BF_REQUIRE(W && (A_u || A_l), "bf_crown_relu_conv_transpose_concretize: null pointer");
@@ -2113,8 +2133,21 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
   g.vec = (g.npix % 16 == 0) && al16(A_u) && al16(A_l) && al16(pre_lo) && al16(pre_hi) && al16(alpha) &&
           al16(add_l) && al16(kbias) && al16(cvec) && al16(relaxed_u) && al16(relaxed_l) &&
           (alpha == nullptr || alpha_ld % 4 == 0) && (add_l == nullptr || add_ld % 4 == 0) ? 1 : 0;
-  const int rc = small_t_launch<true>(g, rx, nz, glds, "bf_crown_relu_conv_transpose_concretize", stream);
+  {
+    int zi = 0;
+    if (A_u) g.bnd[zi++] = ub;
+    if (A_l) g.bnd[zi++] = lb;
+  }
+  g.eps = eps;
+  bool fast = false;
+  const int rc = small_t_launch<true>(g, rx, nz, glds, "bf_crown_relu_conv_transpose_concretize", stream, &fast);
   if (rc) return rc;
+  if (!fast && (lb || ub)) {
+    // the generic kernel writes the norms, centers and biases: the bounds from them
+    const int rcf = concretize_finalize(norm_u, norm_l, 1, R, c_u_out, c_l_out, b_u_out, b_l_out, eps, norm_p,
+                                        lb, ub, stream);
+    if (rcf) return rcf;
+  }
   if (lp_seed) return lp_seed_rows(h_out, R, (int64_t)Ci * Hi * Wi, h_scale, norm_p, stream);
   return BF_OK;
 }

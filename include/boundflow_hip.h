@@ -325,7 +325,10 @@ int bf_crown_relu_planes_conv_transpose(const float* A_u, const float* A_l, int6
  * concretization of Conv2dLinearOperator, runtime/linear_operator.py:1378-1452
  * and runtime/perturbation.py:175-222).  norm_p as for bf_conv_transpose_rows.
  * Shapes: those bf_conv_transpose_small_supported accepts (<= 4 input channels,
- * <= 16 taps). */
+ * <= 16 taps).  lb / ub (optional, [D*S]; each needs its coefficient and its
+ * norm, bias and center outputs): the bounds (c -/+ eps * norm) + b of
+ * bf_concretize_finalize with one partial norm, written by the launch itself
+ * where the register form runs (else by one finalize launch). */
 int bf_conv_transpose_small_supported(int Co, int Ho, int Wo, int Ci, int KH, int KW, int sh, int sw, int ph,
                                       int pw, int Hi, int Wi);
 int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, int64_t D, int64_t S, int Co, int Ho,
@@ -336,7 +339,8 @@ int bf_crown_relu_conv_transpose_concretize(const float* A_u, const float* A_l, 
                                             int Hi, int Wi, const float* wvec, int64_t w_ld, int norm_p,
                                             const float* h_scale, float* h_out, float* norm_u, float* norm_l,
                                             float* b_u_out, float* b_l_out, float* c_u_out, float* c_l_out,
-                                            float* relaxed_u, float* relaxed_l, hipStream_t stream);
+                                            float* relaxed_u, float* relaxed_l, float eps, float* lb, float* ub,
+                                            hipStream_t stream);
 
 /* The weights of that pass in the order its workgroups stage them
  * (bf_conv_transpose_packed_floats floats, 16-byte aligned; 0 = shape not

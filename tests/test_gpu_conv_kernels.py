@@ -345,11 +345,19 @@ def test_relu_conv_transpose_concretize_matches_pass_then_conv(shape, variant):
     cf = [torch.empty(R, device=dev) for _ in range(2)]
     hf = torch.empty(R, nout, device=dev) if norm_p == 0 else None
     rf_l = torch.empty(R, nin, device=dev)
+    eps = 1.0 if box else 0.7
+    lbf, ubf = torch.empty(R, device=dev), torch.empty(R, device=dev)
     _lib.call("bf_crown_relu_conv_transpose_concretize", P("A_u"), P("A_l"), D, S, Co, Ho, Wo, P("lo"), P("hi"),
               P("alpha"), ald, P("add"), nin, P("kb"), P("cv"), P("bu"), P("bl"), P("W"), Ci, KH, KW, sh, sw, ph, pw,
               Hi, Wi, P("wv"), nout, norm_p, P("hs"), _lib.ptr(hf), _lib.ptr(nf[0]), _lib.ptr(nf[1]), _lib.ptr(bf[0]),
-              _lib.ptr(bf[1]), _lib.ptr(cf[0]), _lib.ptr(cf[1]), None, _lib.ptr(rf_l), st)
+              _lib.ptr(bf[1]), _lib.ptr(cf[0]), _lib.ptr(cf[1]), None, _lib.ptr(rf_l), eps, _lib.ptr(lbf),
+              _lib.ptr(ubf), st)
+    # the bounds the launch wrote are the finalize's of its own norms, centers and biases, bit for bit
+    lb_ref, ub_ref = torch.empty(R, device=dev), torch.empty(R, device=dev)
+    _lib.call("bf_concretize_finalize", _lib.ptr(nf[0]), _lib.ptr(nf[1]), 1, R, _lib.ptr(cf[0]), _lib.ptr(cf[1]),
+              _lib.ptr(bf[0]), _lib.ptr(bf[1]), eps, norm_p, _lib.ptr(lb_ref), _lib.ptr(ub_ref), st)
     torch.cuda.synchronize()
+    assert torch.equal(lbf, lb_ref) and torch.equal(ubf, ub_ref), "bounds differ from the finalize of the norms"
     assert torch.equal(rf_l, rp[1]), "relaxed rows differ from the relaxation pass"
     beta_max = float(lo.abs().max())
     for z, A in ((0, A_u), (1, A_l)):
