@@ -34,6 +34,7 @@ SIGNATURES = {
     "bf_gemm_rank1": (I32, [P, I64, P, I64, I32, P, I64, I64, I64, I64, I64, P, P, I64, P, I64, P]),
     "bf_gemm_rank1_workspace": (I64, [I64, I64, I64]),
     "bf_relu_relax_table": (I32, [P, P, P, I64, I64, I64, P, P]),
+    "bf_relu_relax_table_multi": (I32, [I32, P, P, P, P, I64, P, P, P]),
     "bf_crown_relu_linear_fwd": (I32, [P, P, I64, I64, I64, I64, P, P, I64, P, I64, I32, P, P, P, P, P, P, P, P]),
     "bf_relu_relax_table_from_planes": (I32, [P, P, P, P, I64, P, P]),
     "bf_crown_relu_planes_conv_transpose": (I32, [P, P, I64, I64, I32, I32, I32, P, P, P, P, P, P, P, P, P, I32, I32,

@@ -518,14 +518,27 @@ def crown_backward(
         """Slopes/intercepts of the ReLU after linear layer k, once per (domain, neuron), shared by both bounds."""
         if k in tables:
             return tables[k]
-        alpha, alpha_ld, _, _, pre_lo, pre_hi, n = relax_params(k)
-        table = None
-        if pre_lo is not None and layers[k].kind == "linear":
-            table = torch.empty(B, n, 4, device=dev, dtype=torch.float32)
+        # A query of many rows reads the tables of every linear layer below this one in
+        # turn: they are built together, in one launch.
+        todo = [j for j in range(k, -1, -1) if j not in tables] if M >= EPILOGUE_MIN_M else [k]
+        built = []
+        for j in todo:
+            alpha, alpha_ld, _, _, pre_lo, pre_hi, n = relax_params(j)
+            table = None
+            if pre_lo is not None and layers[j].kind == "linear":
+                table = torch.empty(B, n, 4, device=dev, dtype=torch.float32)
+                built.append((pre_lo, pre_hi, alpha, alpha_ld, n, table))
+            tables[j] = table
+        if len(built) == 1:
+            pre_lo, pre_hi, alpha, alpha_ld, n, table = built[0]
             _lib.call("bf_relu_relax_table", _lib.ptr(pre_lo), _lib.ptr(pre_hi), _lib.ptr(alpha), alpha_ld, B, n,
                       _lib.ptr(table), stream)
-        tables[k] = table
-        return table
+        elif built:
+            col = lambda i: [t[i] for t in built]
+            _lib.call("bf_relu_relax_table_multi", len(built), _lib.ptr_array(col(0)), _lib.ptr_array(col(1)),
+                      _lib.ptr_array(col(2)), _lib.i64_array(col(3)), B, _lib.i64_array(col(4)),
+                      _lib.ptr_array(col(5)), stream)
+        return tables[k]
 
     # A coefficient produced by bf_crown_relu_linear_relu_fwd already carries the
     # relaxation (and bias) of the ReLU it enters: the next region skips its prologue.

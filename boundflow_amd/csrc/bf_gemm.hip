@@ -9,6 +9,8 @@
 
 namespace bf {
 
+constexpr int RELAX_SEG_MAX = 16;  // tables per relax_table_multi_kernel launch
+
 // The per-column-block partial norms combined in a fixed order -- summed (norm_p 0:
 // Linf ball, box), their maximum (1: L1 ball, the dual norm max |A|), the square root
 // of their sum (2: L2 ball) -- then
@@ -47,16 +49,40 @@ __global__ void concretize_finalize_kernel(const float* __restrict__ partial_u, 
 // Slopes/intercepts of the ReLU relaxation per (domain, neuron)
 // (crown_ibp.py:722-758, 1176-1208): {alpha_u, beta_u, alpha_l, beta_l}, with the
 // optional lower-slope override clamp(alpha, 0, 1) on ambiguous neurons.
-__global__ void relax_table_kernel(const float* __restrict__ lo, const float* __restrict__ hi,
-                                   const float* __restrict__ alpha, int64_t alpha_ld, int64_t D, int64_t K,
-                                   float4* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void relax_table_elem(const float* __restrict__ lo, const float* __restrict__ hi,
+                                                 const float* __restrict__ alpha, int64_t alpha_ld, int64_t D,
+                                                 int64_t K, float4* __restrict__ out, int64_t i) {
   if (i >= D * K) return;
   const int64_t d = div_rows(i, K, D * K < (1LL << 31)), k = i - d * K;
   const bool has_alpha = alpha != nullptr;
   const float a = has_alpha ? clamp01(alpha[d * alpha_ld + k]) : 0.f;
   const Relax r = relu_relax(lo[i], hi[i], has_alpha, a);
   out[i] = make_float4(r.au, r.bu, r.al, r.bl);
+}
+
+__global__ void relax_table_kernel(const float* __restrict__ lo, const float* __restrict__ hi,
+                                   const float* __restrict__ alpha, int64_t alpha_ld, int64_t D, int64_t K,
+                                   float4* __restrict__ out) {
+  relax_table_elem(lo, hi, alpha, alpha_ld, D, K, out, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+}
+
+// Several ReLUs' tables in one launch: table s owns blocks [bstart[s], bstart[s+1]).
+struct TableSegs {
+  const float* lo[RELAX_SEG_MAX];
+  const float* hi[RELAX_SEG_MAX];
+  const float* alpha[RELAX_SEG_MAX];
+  int64_t alpha_ld[RELAX_SEG_MAX];
+  int64_t K[RELAX_SEG_MAX];
+  float4* out[RELAX_SEG_MAX];
+  int64_t bstart[RELAX_SEG_MAX + 1];
+  int count;
+};
+
+__global__ void relax_table_multi_kernel(TableSegs t, int64_t D) {
+  int s = 0;
+  while (s + 1 < t.count && (int64_t)blockIdx.x >= t.bstart[s + 1]) ++s;
+  relax_table_elem(t.lo[s], t.hi[s], t.alpha[s], t.alpha_ld[s], D, t.K[s], t.out[s],
+                   ((int64_t)blockIdx.x - t.bstart[s]) * blockDim.x + threadIdx.x);
 }
 
 // BOUNDFLOW_GEMM_TILE=G, =H, =Q or =S forces one configuration (for measurement);
@@ -144,6 +170,33 @@ int relax_table(const float* lo, const float* hi, const float* alpha, int64_t al
   hipLaunchKernelGGL(relax_table_kernel, dim3((unsigned)ceil_div(D * K, 256)), dim3(256), 0, stream, lo, hi, alpha,
                      alpha_ld, D, K, out);
   BF_LAUNCH_CHECK("relax_table_kernel");
+  return BF_OK;
+}
+
+int relax_table_multi(int count, const float* const* lo, const float* const* hi, const float* const* alpha,
+                      const int64_t* alpha_ld, int64_t D, const int64_t* K, float* const* out, hipStream_t stream) {
+  for (int base = 0; base < count; base += RELAX_SEG_MAX) {
+    TableSegs t;
+    memset(&t, 0, sizeof(t));
+    t.count = count - base < RELAX_SEG_MAX ? count - base : RELAX_SEG_MAX;
+    int64_t blocks = 0;
+    for (int q = 0; q < t.count; ++q) {
+      const int j = base + q;
+      t.lo[q] = lo[j];
+      t.hi[q] = hi[j];
+      t.alpha[q] = alpha[j];
+      t.alpha_ld[q] = alpha_ld[j];
+      t.K[q] = K[j];
+      t.out[q] = reinterpret_cast<float4*>(out[j]);
+      t.bstart[q] = blocks;
+      blocks += ceil_div(D * K[j], 256);
+    }
+    t.bstart[t.count] = blocks;
+    if (blocks == 0) continue;
+    BF_REQUIRE(blocks < (1LL << 31), "relax_table_multi: too many entries");
+    hipLaunchKernelGGL(relax_table_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, t, D);
+    BF_LAUNCH_CHECK("relax_table_multi_kernel");
+  }
   return BF_OK;
 }
 

@@ -41,6 +41,8 @@ int splitk_reduce(const float* part, int ks, int64_t M, int64_t N, float* C, int
                   const float* v_col, int64_t v_ld, int64_t S, hipStream_t stream);
 int relax_table(const float* lo, const float* hi, const float* alpha, int64_t alpha_ld, int64_t D, int64_t K,
                 float4* out, hipStream_t stream);
+int relax_table_multi(int count, const float* const* lo, const float* const* hi, const float* const* alpha,
+                      const int64_t* alpha_ld, int64_t D, const int64_t* K, float* const* out, hipStream_t stream);
 int lp_seed_rows(float* h, int64_t M, int64_t I, const float* h_scale, int norm_p, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
@@ -1390,6 +1392,21 @@ int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* a
   BF_REQUIRE(pre_lo && pre_hi && table, "bf_relu_relax_table: null pointer");
   BF_REQUIRE(((uintptr_t)table & 15) == 0, "bf_relu_relax_table: table must be 16-byte aligned");
   return relax_table(pre_lo, pre_hi, alpha, alpha_ld, D, K, reinterpret_cast<float4*>(table), stream);
+}
+
+int bf_relu_relax_table_multi(int count, const float* const* pre_lo, const float* const* pre_hi,
+                              const float* const* alpha, const int64_t* alpha_ld, int64_t D, const int64_t* K,
+                              float* const* table, hipStream_t stream) {
+  BF_REQUIRE(count >= 0 && D >= 0, "bf_relu_relax_table_multi: bad sizes");
+  if (count == 0 || D == 0) return BF_OK;
+  BF_REQUIRE(pre_lo && pre_hi && alpha && alpha_ld && K && table, "bf_relu_relax_table_multi: null array");
+  for (int j = 0; j < count; ++j) {
+    BF_REQUIRE(K[j] >= 0, "bf_relu_relax_table_multi: bad size of table %d", j);
+    if (K[j] == 0) continue;
+    BF_REQUIRE(pre_lo[j] && pre_hi[j] && table[j], "bf_relu_relax_table_multi: null pointer in table %d", j);
+    BF_REQUIRE(((uintptr_t)table[j] & 15) == 0, "bf_relu_relax_table_multi: table %d must be 16-byte aligned", j);
+  }
+  return relax_table_multi(count, pre_lo, pre_hi, alpha, alpha_ld, D, K, table, stream);
 }
 
 static int relax_pass(const float* A_u, const float* A_l, int64_t a_dstride, int64_t D, int64_t S, int64_t K,

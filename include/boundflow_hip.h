@@ -119,6 +119,15 @@ int bf_ibp_batched_linear(const float* lo, const float* hi, int64_t B, int64_t I
 int bf_relu_relax_table(const float* pre_lo, const float* pre_hi, const float* alpha, int64_t alpha_ld, int64_t D,
                         int64_t K, float* table, hipStream_t stream);
 
+/* The tables of count ReLUs in one launch (host arrays of device pointers, alpha rows and
+ * widths; one domain count D): table j is bf_relu_relax_table(pre_lo[j], pre_hi[j],
+ * alpha[j], alpha_ld[j], D, K[j], table[j]) element for element.  Same boundary as
+ * bf_relu_relax_table (crown_ibp.py:722-758, 1176-1208), for a backward pass that reads
+ * several layers' tables. */
+int bf_relu_relax_table_multi(int count, const float* const* pre_lo, const float* const* pre_hi,
+                              const float* const* alpha, const int64_t* alpha_ld, int64_t D, const int64_t* K,
+                              float* const* table, hipStream_t stream);
+
 /* The same table from the four separate tensors of a FusedReluAffineRequest
  * (runtime/fused_crown.py:33-48: alpha_u, beta_u, alpha_l, beta_l, each n =
  * D*K floats), interleaved in one pass: what HipFusedCrownExecutor hands the

@@ -212,3 +212,33 @@ def test_crown_query_on_epilogue_path_matches_oracle(box, shared, monkeypatch):
     assert_parity(b.lower, ref.lower, ref64.lower, "epilogue path lower")
     assert_parity(b.upper, ref.upper, ref64.upper, "epilogue path upper")
     assert_verdicts(b.lower, ref.lower, ref64.lower, "epilogue path")
+
+
+def test_multi_table_launch_equals_single_tables():
+    """bf_relu_relax_table_multi: each table bit-equal to bf_relu_relax_table's, with and
+    without alpha (per-domain and shared rows), an empty table among them, and more
+    tables than one launch takes (17, two launches)."""
+    dev = device()
+    announce("bf_relu_relax_table_multi: 17 tables, D=7")
+    g = torch.Generator().manual_seed(41)
+    D = 7
+    widths = [5, 300, 0, 64, 1] + [33 + 7 * i for i in range(12)]
+    lo, hi, al, ld, want, got = [], [], [], [], [], []
+    for i, n in enumerate(widths):
+        l, h = _pre(D, n, g) if n >= 4 else (torch.randn(D, n, generator=g), torch.randn(D, n, generator=g).abs())
+        h = torch.maximum(h, l)
+        a = None if i % 3 == 0 else torch.rand(D if i % 3 == 1 else 1, n, generator=g) * 1.4 - 0.2
+        lo.append(l.to(dev).contiguous())
+        hi.append(h.to(dev).contiguous())
+        al.append(None if a is None else a.to(dev).contiguous())
+        ld.append(n if i % 3 == 1 else 0)
+        w = torch.empty(D, n, 4, device=dev)
+        _lib.call("bf_relu_relax_table", _lib.ptr(lo[-1]), _lib.ptr(hi[-1]), _lib.ptr(al[-1]), ld[-1], D, n,
+                  _lib.ptr(w), _lib.stream_handle())
+        want.append(w)
+        got.append(torch.full((D, n, 4), float("nan"), device=dev))
+    _lib.call("bf_relu_relax_table_multi", len(widths), _lib.ptr_array(lo), _lib.ptr_array(hi), _lib.ptr_array(al),
+              _lib.i64_array(ld), D, _lib.i64_array(widths), _lib.ptr_array(got), _lib.stream_handle())
+    torch.cuda.synchronize()
+    for i, (w, t) in enumerate(zip(want, got)):
+        assert torch.equal(w.cpu(), t.cpu()), f"table {i} (K={widths[i]})"
