@@ -768,16 +768,16 @@ relu_relax_rows4_kernel(const float* __restrict__ Au, const float* __restrict__ 
 }
 
 // The same pass over a coefficient shared by every domain (a_dstride 0: the first region
-// of a C = I query, rows of K <= 256 NQ): a workgroup takes rows_per_wg rows of one
-// domain, and each lane keeps that domain's operands of its NQ quads of k (k = 4 lane +
-// 256 q: the relaxation entries, split term, center and bias) in registers across all of
-// them, so a row costs one read of the shared (L2-resident) row and the writes of its
-// relaxed rows.  Per-lane partials in k order and the wave sum: the sums of
+// of a C = I query, rows of K <= 256 NQ), or over a per-domain one of many rows: a
+// workgroup takes rows_per_wg rows of one domain, and each lane keeps that domain's
+// operands of its NQ quads of k (k = 4 lane + 256 q: the relaxation entries, split term,
+// center and bias) in registers across all of them, so a row costs one read of its
+// coefficient row (for a shared one, L2-resident) and the writes of its relaxed rows.  Per-lane partials in k order and the wave sum: the sums of
 // relu_relax_rows4_kernel<64>, bit for bit.
 template <int NQ>
 __global__ void __launch_bounds__(256)
-relu_relax_shared_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t S, int64_t K,
-                         int64_t chunks, int rows_per_wg, RelaxSrc relax, const float* __restrict__ add_l,
+relu_relax_shared_kernel(const float* __restrict__ Au, const float* __restrict__ Al, int64_t a_dstride, int64_t S,
+                         int64_t K, int64_t chunks, int rows_per_wg, RelaxSrc relax, const float* __restrict__ add_l,
                          int64_t add_ld, const float* __restrict__ kbias, const float* __restrict__ cvec,
                          const float* __restrict__ bu_in, const float* __restrict__ bl_in,
                          float* __restrict__ Au_out, float* __restrict__ Al_out, float* __restrict__ bu_out,
@@ -811,8 +811,8 @@ relu_relax_shared_kernel(const float* __restrict__ Au, const float* __restrict__
   const bool need[6] = {Au != nullptr, Al != nullptr, Au && kbias, Al && kbias, Au && cvec, Al && cvec};
   for (int64_t srow = s0 + wave; srow < s_end; srow += 4) {
     const int64_t m = d * S + srow;
-    const float* __restrict__ au = Au + srow * K;
-    const float* __restrict__ al = Al + srow * K;
+    const float* __restrict__ au = Au + d * a_dstride + srow * K;
+    const float* __restrict__ al = Al + d * a_dstride + srow * K;
     float4 vu4[NQ], vl4[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -1757,19 +1757,23 @@ static int relax_pass(const float* A_u, const float* A_l, int64_t a_dstride, int
                    al16(A_l_out) && al16(kbias) &&
                    al16(cvec) && al16(add_l) && (add_l == nullptr || add_ld % 4 == 0) && al16(src.lo) &&
                    al16(src.hi) && al16(src.alpha) && (src.alpha_ld % 4 == 0);
-  if (vec && a_dstride == 0 && K <= 512 && S >= 16) {
+  if (vec && K <= 512 && (a_dstride == 0 ? S >= 16 : (S >= 8 && M >= 8192))) {
     // a shared coefficient: 16 rows of one domain per workgroup (4 per wave), the
     // domain's operands held in registers across them (C2's 500 x 500 shape: 8, 16 and
-    // 64 rows per workgroup measured 150, 129 and 141 us, the per-row kernel 156 us)
+    // 64 rows per workgroup measured 150, 129 and 141 us, the per-row kernel 156 us).
+    // A per-domain coefficient of many rows takes the same kernel: its rows are read
+    // once either way, and the domain's operands are loaded once per wave, not per row.
     const int rpw = S < 16 ? (int)S : 16;
     const int64_t chunks = ceil_div(S, rpw);
     BF_REQUIRE(D * chunks < (1LL << 31), "bf_crown_relu_relax: too many rows");
     if (K <= 256)
-      hipLaunchKernelGGL(relu_relax_shared_kernel<1>, dim3((unsigned)(D * chunks)), dim3(256), 0, stream, A_u, A_l, S,
+      hipLaunchKernelGGL(relu_relax_shared_kernel<1>, dim3((unsigned)(D * chunks)), dim3(256), 0, stream, A_u, A_l,
+                         a_dstride, S,
                          K, chunks, rpw, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out,
                          b_l_out, c_u_out, c_l_out);
     else
-      hipLaunchKernelGGL(relu_relax_shared_kernel<2>, dim3((unsigned)(D * chunks)), dim3(256), 0, stream, A_u, A_l, S,
+      hipLaunchKernelGGL(relu_relax_shared_kernel<2>, dim3((unsigned)(D * chunks)), dim3(256), 0, stream, A_u, A_l,
+                         a_dstride, S,
                          K, chunks, rpw, src, add_l, add_ld, kbias, cvec, b_u_in, b_l_in, A_u_out, A_l_out, b_u_out,
                          b_l_out, c_u_out, c_l_out);
     BF_LAUNCH_CHECK("relu_relax_shared_kernel");

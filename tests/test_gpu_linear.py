@@ -271,6 +271,49 @@ def test_shared_coefficient_pass_equals_per_domain_pass(K, S, same):
         assert torch.equal(outs[0][i], outs[1][i]), what
 
 
+@pytest.mark.parametrize("K,S,same", [(256, 9, False), (500, 9, True), (256, 20, False)])
+def test_large_per_domain_pass_equals_per_row_pass(K, S, same):
+    """A per-domain coefficient of at least 8192 rows (the domain's operands held in
+    registers over its rows; S = 9: one workgroup of unequal waves per domain, S = 20: two
+    chunks, the last partial) against the same rows relaxed in calls of fewer rows (the
+    per-row pass): every output bit-identical, with the split term, the next layer's bias
+    and the center sums present."""
+    dev = device()
+    announce(f"large per-domain relax pass vs per-row pass K={K} S={S} same={same}")
+    g = torch.Generator().manual_seed(K * 5 + S)
+    D = -(-8192 // S) + 3
+    A_u = torch.randn(D, S, K, generator=g)
+    A_l = A_u if same else torch.randn(D, S, K, generator=g)
+    A_u[0, 0, :3] = torch.tensor([0.0, -0.0, 1.0])
+    l = torch.randn(D, K, generator=g)
+    u = l + torch.rand(D, K, generator=g)
+    d = {k: v.to(dev).contiguous() for k, v in dict(A_u=A_u, A_l=A_l, l=l, u=u, alpha=torch.rand(D, K, generator=g),
+                                                     add=torch.randn(D, K, generator=g), kb=torch.randn(K, generator=g),
+                                                     cv=torch.randn(D, K, generator=g),
+                                                     bu=torch.randn(D, S, generator=g),
+                                                     bl=torch.randn(D, S, generator=g)).items()}
+    if same:
+        d["A_l"] = d["A_u"]
+
+    def run(d0, d1):
+        n = d1 - d0
+        o = [torch.empty(n * S, K, device=dev), torch.empty(n * S, K, device=dev)] + \
+            [torch.empty(n * S, device=dev) for _ in range(4)]
+        Al = d["A_u"][d0:d1] if same else d["A_l"][d0:d1]
+        _lib.call("bf_crown_relu_relax_lu", _lib.ptr(d["A_u"][d0:d1]), _lib.ptr(Al), S * K, n, S, K,
+                  _lib.ptr(d["l"][d0:d1]), _lib.ptr(d["u"][d0:d1]), _lib.ptr(d["alpha"][d0:d1]), K,
+                  _lib.ptr(d["add"][d0:d1]), K, _lib.ptr(d["kb"]), _lib.ptr(d["cv"][d0:d1]),
+                  _lib.ptr(d["bu"][d0:d1]), _lib.ptr(d["bl"][d0:d1]), *[_lib.ptr(x) for x in o], _lib.stream_handle())
+        return o
+
+    whole = run(0, D)
+    step = 8192 // S // 2
+    parts = [run(a, min(a + step, D)) for a in range(0, D, step)]
+    torch.cuda.synchronize()
+    for i, what in enumerate(("A_u'", "A_l'", "b_u", "b_l", "c_u", "c_l")):
+        assert torch.equal(whole[i], torch.cat([p[i] for p in parts])), what
+
+
 # K = 133: scalar kernel (K % 4 != 0); 132, 256, 500: float4 kernel, a wave per row (500:
 # two quad steps, the second partial); 2048, 4100: float4, a workgroup per row (4100: a
 # partial last step); S = 19, 9, 3 vary the rows per domain
