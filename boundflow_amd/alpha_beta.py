@@ -125,8 +125,9 @@ class _AdamGroup:
 
     def __init__(self, params: List[torch.Tensor], clamps: List[Tuple[float, Optional[float]]]):
         self.p = params
-        self.m = [torch.zeros_like(t) for t in params]
-        self.v = [torch.zeros_like(t) for t in params]
+        # the first step starts the moments at zero without reading them
+        self.m = [torch.empty_like(t) for t in params]
+        self.v = [torch.empty_like(t) for t in params]
         self.t = 0
         self.args = (_lib.ptr_array(self.p), _lib.ptr_array(self.m), _lib.ptr_array(self.v))
         self.n = _lib.i64_array([t.numel() for t in params])

@@ -977,12 +977,13 @@ __global__ void branch_update_kernel(const float* __restrict__ lo, const float* 
 __device__ __forceinline__ void adam_clamp_one(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
                                                const float* __restrict__ g, int64_t i, float w1, float b2, float w2,
                                                float eps, float neg_step, float bc2_sqrt, float lo, float hi,
-                                               int clamp_hi) {
+                                               int clamp_hi, bool fresh) {
+  // fresh (step 1): torch.optim.Adam's state starts at zero, so the moments are not read
   const float gi = g[i];
-  float mi = m[i];
+  float mi = fresh ? 0.f : m[i];
   // exp_avg.lerp_(grad, 1 - beta1): torch's vectorized CPU lerp is fma(w, g - m, m) for w < 0.5
   mi = (w1 < 0.5f) ? fmaf(w1, gi - mi, mi) : fmaf(w1 - 1.0f, gi - mi, gi);
-  float vi = v[i] * b2;                                                       // exp_avg_sq.mul_(beta2)
+  float vi = (fresh ? 0.f : v[i]) * b2;                                       // exp_avg_sq.mul_(beta2)
   vi = vi + w2 * gi * gi;                                                     //   .addcmul_(g, g, 1 - beta2)
   m[i] = mi;
   v[i] = vi;
@@ -995,10 +996,10 @@ __device__ __forceinline__ void adam_clamp_one(float* __restrict__ p, float* __r
 
 __global__ void adam_clamp_kernel(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
                                   const float* __restrict__ g, int64_t n, float w1, float b2, float w2, float eps,
-                                  float neg_step, float bc2_sqrt, float lo, float hi, int clamp_hi) {
+                                  float neg_step, float bc2_sqrt, float lo, float hi, int clamp_hi, int fresh) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  adam_clamp_one(p, m, v, g, i, w1, b2, w2, eps, neg_step, bc2_sqrt, lo, hi, clamp_hi);
+  adam_clamp_one(p, m, v, g, i, w1, b2, w2, eps, neg_step, bc2_sqrt, lo, hi, clamp_hi, fresh != 0);
 }
 
 // Several tensors in one launch.  Workgroups are dealt to the tensors in order
@@ -1030,13 +1031,13 @@ __device__ __forceinline__ int seg_of_block(const int64_t* bstart, int count) {
 // follows, so the parameter is first copied to its best-of tensor (the copy of
 // masked_copy_rows_multi_kernel, taken from the same values before they are stepped).
 __global__ void adam_clamp_multi_kernel(AdamSegs a, float w1, float b2, float w2, float eps, float neg_step,
-                                        float bc2_sqrt, const int* __restrict__ improved) {
+                                        float bc2_sqrt, const int* __restrict__ improved, int fresh) {
   const int s = seg_of_block(a.bstart, a.count);
   const int64_t i = ((int64_t)blockIdx.x - a.bstart[s]) * 256 + threadIdx.x;
   if (i >= a.n[s]) return;
   if (a.best[s] && improved[div_rows(i, a.ncol[s], a.n[s] < (1LL << 31))]) a.best[s][i] = a.p[s][i];
   adam_clamp_one(a.p[s], a.m[s], a.v[s], a.g[s], i, w1, b2, w2, eps, neg_step, bc2_sqrt, a.lo[s], a.hi[s],
-                 a.clamp_hi[s]);
+                 a.clamp_hi[s], fresh != 0);
 }
 
 // dst[s][d, j] = src[s][d, j] where mask[d] (the best-of copy of several parameters)
@@ -2026,7 +2027,7 @@ int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, 
   const float w1 = (float)(1.0 - (double)beta1);
   const float w2 = (float)(1.0 - (double)beta2);
   hipLaunchKernelGGL(adam_clamp_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, p, m, v, g, n, w1,
-                     beta2, w2, eps, neg_step, bc2_sqrt, clamp_lo, clamp_hi, has_clamp_hi);
+                     beta2, w2, eps, neg_step, bc2_sqrt, clamp_lo, clamp_hi, has_clamp_hi, (int)(step == 1));
   BF_LAUNCH_CHECK("adam_clamp_kernel");
   return BF_OK;
 }
@@ -2075,7 +2076,7 @@ int bf_adam_clamp_multi(int count, float* const* p, float* const* m, float* cons
     if (blocks == 0) continue;
     BF_REQUIRE(blocks < (1LL << 31), "bf_adam_clamp_multi: too many elements");
     hipLaunchKernelGGL(adam_clamp_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a, w1, (float)beta2,
-                       w2, eps, neg_step, bc2_sqrt, improved);
+                       w2, eps, neg_step, bc2_sqrt, improved, (int)(step == 1));
     BF_LAUNCH_CHECK("adam_clamp_multi_kernel");
   }
   return BF_OK;

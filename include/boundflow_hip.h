@@ -446,7 +446,9 @@ int bf_beta_coeff_multi(int count, const float* const* beta, const int64_t* beta
                         hipStream_t stream);
 
 /* torch.optim.Adam step (no weight decay / amsgrad) then clamp to [lo, hi]
- * (hi only when has_clamp_hi), in place (runtime/alpha_beta_crown.py:747, 918-923). */
+ * (hi only when has_clamp_hi), in place (runtime/alpha_beta_crown.py:747, 918-923).
+ * At step 1 the moments start at zero, as torch.optim.Adam's fresh state does: m and v
+ * are written, not read (they need no clearing before the first step). */
 int bf_adam_clamp_step(float* p, float* m, float* v, const float* g, int64_t n, double lr, double beta1,
                        double beta2, float eps, int step, float clamp_lo, float clamp_hi, int has_clamp_hi,
                        hipStream_t stream);

@@ -651,3 +651,30 @@ def test_flags_without_splits_are_zeros_made_on_read():
     assert flags.dtype == torch.int32 and flags.device.type == dev.type and tuple(flags.shape) == (w.batch,)
     assert int(flags.abs().sum()) == 0
     assert trace.infeasible is flags
+
+
+def test_adam_first_step_does_not_read_the_moments():
+    """At step 1 bf_adam_clamp_step and bf_adam_clamp_multi start the moments at zero
+    (torch.optim.Adam's fresh state): NaN-filled m and v give the bits of zero-filled ones,
+    and step 2 then reads the moments step 1 wrote."""
+    dev = device()
+    announce("Adam first step with unread moments")
+    g = torch.Generator().manual_seed(3)
+    p0 = torch.rand(3, 700, generator=g).to(dev)
+    gr = [torch.randn(3, 700, generator=g).to(dev) for _ in range(2)]
+    out = []
+    for fill in (0.0, float("nan")):
+        p, m, v = p0.clone(), torch.full_like(p0, fill), torch.full_like(p0, fill)
+        q, mq, vq = p0.clone(), torch.full_like(p0, fill), torch.full_like(p0, fill)
+        for step in (1, 2):
+            _lib.call("bf_adam_clamp_step", _lib.ptr(p), _lib.ptr(m), _lib.ptr(v), _lib.ptr(gr[step - 1]), p.numel(),
+                      0.1, 0.9, 0.999, 1e-8, step, 0.0, 1.0, 1, _lib.stream_handle())
+            _lib.call("bf_adam_clamp_multi", 1, _lib.ptr_array([q]), _lib.ptr_array([mq]), _lib.ptr_array([vq]),
+                      _lib.ptr_array([gr[step - 1]]), _lib.i64_array([q.numel()]), _lib.f32_array([0.0]),
+                      _lib.f32_array([1.0]), _lib.i32_array([1]), 0.1, 0.9, 0.999, 1e-8, step, None, None, 0,
+                      _lib.stream_handle())
+        torch.cuda.synchronize()
+        out.append((p, m, v, q, mq, vq))
+    for a, b in zip(out[0], out[1]):
+        assert torch.equal(a, b)
+    assert torch.equal(out[0][0], out[0][3])
